@@ -1,0 +1,52 @@
+"""Loads libameva_hip.so (the HIP kernels behind the C ABI of include/ameva_hip.h) and declares its signatures.
+
+There is no fallback: if the library is missing or fails to load, every operator raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libameva_hip.so")
+
+P, I32, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+
+# name -> (restype, argtypes); every symbol include/ameva_hip.h declares
+SIGNATURES = {
+    "amv_last_error": (ctypes.c_char_p, []),
+    "amv_version": (I32, []),
+    "amv_weight_bytes": (I64, [I32, I64, I64]),
+    "amv_repack": (I32, [I32, P, P, I64, I64, P]),
+    "amv_unrepack": (I32, [I32, P, P, I64, I64, P]),
+    "amv_act_bytes": (I64, [I32, I64, I64]),
+    "amv_quantize_act": (I32, [I32, P, I64, I64, I32, P, P, P]),
+    "amv_quantize_q4_0": (I32, [P, I64, I64, P, P]),
+    "amv_mul_mat_vec": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
+    "amv_mul_mat_block_sums": (I32, [I32, P, I64, I64, P, I64, P, P]),
+}
+
+_lib = None
+
+
+class AmevaError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise AmevaError(f"{LIB_PATH} is not built: run __graft_entry__.build() (no CPU fallback exists)")
+        _lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().amv_last_error().decode(errors="replace")
+        raise AmevaError(f"{what} failed ({rc}): {msg} (FAIL-FAST)")

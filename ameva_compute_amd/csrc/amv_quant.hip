@@ -1,0 +1,359 @@
+// Quantizers (activations to Q8_0 / Q8_K, rows to Q4_0) and the weight repack between ggml blocks and the MI355X
+// structure-of-arrays layout. Quantization reproduces the CPU's f32 arithmetic exactly: this file is built with
+// -ffp-contract=off and correctly rounded division, so x * id, 1 / d and 127 / amax round as on the CPU.
+#include "amv_common.h"
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q8_0 activations: one lane per element, 32 lanes per block (a wave holds two blocks).
+// ggml quantize_row_q8_0 (x86: id = 127/amax, round half even; ARM: id = 1/d, round half even; ref: id = 1/d,
+// roundf) -- the rules of ameva_act_fq.comp:5,38-41 and ameva_quant_a8.comp:46-54; d = amax/127 stored fp16.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x, int64_t n_elem, int rule,
+                                                   uint8_t* __restrict__ y_ggml, int8_t* __restrict__ aq,
+                                                   int2* __restrict__ ads) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = i < n_elem;
+    const float v = live ? x[i] : 0.0f;
+    // max |x| over the 32 lanes of the block (xor offsets < 32 stay inside the half-wave)
+    float amax = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, AMV_WAVE));
+    const float d = amax / 127.0f;
+    float id;
+    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float t = v * id;
+    float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+    qf = fminf(127.0f, fmaxf(-127.0f, qf));
+    const int q = (int)qf;
+    int s = q;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, AMV_WAVE);
+    if (!live) return;
+    const int64_t b = i >> 5;
+    const int j = (int)(i & 31);
+    const uint16_t d16 = amv_f2h(d);
+    if (y_ggml) {
+        uint8_t* yb = y_ggml + b * 34;
+        yb[2 + j] = (uint8_t)(int8_t)q;
+        if (j == 0) *(uint16_t*)yb = d16;
+    }
+    if (aq) {
+        aq[i] = (int8_t)q;
+        if (j == 0) ads[b] = make_int2(__float_as_int(amv_h2f(d16)), s);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q8_K activations (ggml quantize_row_q8_K_ref): one wave per 256-element block, 4 elements per lane.
+// max = the element of largest magnitude (the first on ties), iscale = -127/max, q = min(127, round-half-even(
+// iscale * x)), d = 1/iscale, bsums = sums of q over 16 elements.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x, int64_t n_blk,
+                                                   uint8_t* __restrict__ y_ggml, int8_t* __restrict__ aq,
+                                                   float* __restrict__ ad, int32_t* __restrict__ abs16) {
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= n_blk) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const float4 v4 = reinterpret_cast<const float4*>(x + b * 256)[lane];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    // (amax, index) with the smallest index on ties, then the signed value at that index
+    float am = 0.0f;
+    int ai = 0x7FFFFFFF;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float a = fabsf(v[e]);
+        if (a > am) { am = a; ai = 4 * lane + e; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float om = __shfl_xor(am, o, AMV_WAVE);
+        const int oi = __shfl_xor(ai, o, AMV_WAVE);
+        if (om > am || (om == am && oi < ai)) { am = om; ai = oi; }
+    }
+    uint8_t* yb = y_ggml ? y_ggml + b * 292 : nullptr;
+    if (am == 0.0f) {
+        int* yq = yb ? reinterpret_cast<int*>(yb) : nullptr;
+        if (yq) {
+            for (int w = lane; w < 73; w += 64) yq[w] = 0;
+        }
+        if (aq) {
+            reinterpret_cast<int*>(aq + b * 256)[lane] = 0;
+            if (lane < 16) abs16[b * 16 + lane] = 0;
+            if (lane == 0) ad[b] = 0.0f;
+        }
+        return;
+    }
+    const float mx = __shfl(v[ai & 3], ai >> 2, AMV_WAVE);
+    const float iscale = -127.0f / mx;
+    int q[4];
+    int s = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int t = (int)rintf(iscale * v[e]);
+        q[e] = t < 127 ? t : 127;
+        s += q[e];
+    }
+    // sums over 16 elements = 4 lanes
+    s += __shfl_xor(s, 1, AMV_WAVE);
+    s += __shfl_xor(s, 2, AMV_WAVE);
+    const float d = 1.0f / iscale;
+    const int packed = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | ((q[3] & 0xFF) << 24);
+    if (yb) {
+        reinterpret_cast<int*>(yb + 4)[lane] = packed;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(yb + 260)[lane >> 2] = (int16_t)s;
+        if (lane == 0) *reinterpret_cast<float*>(yb) = d;
+    }
+    if (aq) {
+        reinterpret_cast<int*>(aq + b * 256)[lane] = packed;
+        if ((lane & 3) == 0) abs16[b * 16 + (lane >> 2)] = s;
+        if (lane == 0) ad[b] = d;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q4_0 rows (ggml quantize_row_q4_0_ref; ameva_set_rows_q.comp:95-115): one lane per 32-element block.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quant_q4_0(const float* __restrict__ x, int64_t n_blk,
+                                                   uint8_t* __restrict__ y) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blk) return;
+    const float4* xp = reinterpret_cast<const float4*>(x + b * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = xp[i];
+        v[4 * i] = t.x;
+        v[4 * i + 1] = t.y;
+        v[4 * i + 2] = t.z;
+        v[4 * i + 3] = t.w;
+    }
+    float amax = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        if (amax < fabsf(v[j])) { amax = fabsf(v[j]); mx = v[j]; }
+    }
+    const float d = mx / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t h[9];
+    h[0] = amv_f2h(d);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int j = 2 * k + e;
+            const float x0 = v[j] * id, x1 = v[j + 16] * id;
+            int q0 = (int)(x0 + 8.5f), q1 = (int)(x1 + 8.5f);
+            q0 = q0 < 15 ? q0 : 15;
+            q1 = q1 < 15 ? q1 : 15;
+            pair |= (uint32_t)(q0 | (q1 << 4)) << (8 * e);
+        }
+        h[1 + k] = (uint16_t)pair;
+    }
+    uint16_t* yb = reinterpret_cast<uint16_t*>(y + b * 18);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) yb[k] = h[k];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Repack ggml blocks <-> structure of arrays. One lane per block; block b = row * nb + j in both layouts.
+// ---------------------------------------------------------------------------------------------------------------
+template <bool FWD>
+__global__ __launch_bounds__(256) void k_repack_q4_0(uint8_t* __restrict__ g, uint4* __restrict__ qs,
+                                                    uint16_t* __restrict__ dd, int64_t n_blk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blk) return;
+    uint16_t* gb = reinterpret_cast<uint16_t*>(g + b * 18);
+    if (FWD) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (uint32_t)gb[1 + 2 * i] | ((uint32_t)gb[2 + 2 * i] << 16);
+        qs[b] = make_uint4(w[0], w[1], w[2], w[3]);
+        dd[b] = gb[0];
+    } else {
+        const uint4 q = qs[b];
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        gb[0] = dd[b];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            gb[1 + 2 * i] = (uint16_t)(w[i] & 0xFFFFu);
+            gb[2 + 2 * i] = (uint16_t)(w[i] >> 16);
+        }
+    }
+}
+
+template <bool FWD>
+__global__ __launch_bounds__(256) void k_repack_q8_0(uint8_t* __restrict__ g, uint4* __restrict__ qs,
+                                                    uint16_t* __restrict__ dd, int64_t n_blk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blk) return;
+    uint16_t* gb = reinterpret_cast<uint16_t*>(g + b * 34);
+    if (FWD) {
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = (uint32_t)gb[1 + 2 * i] | ((uint32_t)gb[2 + 2 * i] << 16);
+        qs[2 * b] = make_uint4(w[0], w[1], w[2], w[3]);
+        qs[2 * b + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+        dd[b] = gb[0];
+    } else {
+        const uint4 q0 = qs[2 * b], q1 = qs[2 * b + 1];
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        gb[0] = dd[b];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            gb[1 + 2 * i] = (uint16_t)(w[i] & 0xFFFFu);
+            gb[2 + 2 * i] = (uint16_t)(w[i] >> 16);
+        }
+    }
+}
+
+// Q4_K: 144-byte blocks (16-byte aligned when the tensor is): head 16 B | qs 128 B
+template <bool FWD>
+__global__ __launch_bounds__(256) void k_repack_q4_K(uint8_t* __restrict__ g, uint4* __restrict__ qs,
+                                                    uint4* __restrict__ head, int64_t n_blk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blk) return;
+    uint4* gb = reinterpret_cast<uint4*>(g + b * 144);
+    if (FWD) {
+        head[b] = gb[0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qs[8 * b + i] = gb[1 + i];
+    } else {
+        gb[0] = head[b];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) gb[1 + i] = qs[8 * b + i];
+    }
+}
+
+// Q6_K: 210-byte blocks (2-byte aligned): ql 128 | qh 64 | scales 16 | d 2
+template <bool FWD>
+__global__ __launch_bounds__(256) void k_repack_q6_K(uint8_t* __restrict__ g, uint32_t* __restrict__ ql,
+                                                    uint32_t* __restrict__ qh, uint32_t* __restrict__ sc,
+                                                    uint16_t* __restrict__ dd, int64_t n_blk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blk) return;
+    uint16_t* gb = reinterpret_cast<uint16_t*>(g + b * 210);
+    if (FWD) {
+        for (int i = 0; i < 32; ++i) ql[32 * b + i] = (uint32_t)gb[2 * i] | ((uint32_t)gb[2 * i + 1] << 16);
+        for (int i = 0; i < 16; ++i) qh[16 * b + i] = (uint32_t)gb[64 + 2 * i] | ((uint32_t)gb[65 + 2 * i] << 16);
+        for (int i = 0; i < 4; ++i) sc[4 * b + i] = (uint32_t)gb[96 + 2 * i] | ((uint32_t)gb[97 + 2 * i] << 16);
+        dd[b] = gb[104];
+    } else {
+        for (int i = 0; i < 32; ++i) {
+            gb[2 * i] = (uint16_t)(ql[32 * b + i] & 0xFFFFu);
+            gb[2 * i + 1] = (uint16_t)(ql[32 * b + i] >> 16);
+        }
+        for (int i = 0; i < 16; ++i) {
+            gb[64 + 2 * i] = (uint16_t)(qh[16 * b + i] & 0xFFFFu);
+            gb[65 + 2 * i] = (uint16_t)(qh[16 * b + i] >> 16);
+        }
+        for (int i = 0; i < 4; ++i) {
+            gb[96 + 2 * i] = (uint16_t)(sc[4 * b + i] & 0xFFFFu);
+            gb[97 + 2 * i] = (uint16_t)(sc[4 * b + i] >> 16);
+        }
+        gb[104] = dd[b];
+    }
+}
+
+static inline unsigned grid_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+static int repack_impl(int type, uint8_t* g, uint8_t* r, int64_t n_rows, int64_t k, bool fwd, hipStream_t st) {
+    AMV_REQUIRE(g && r, "amv_repack: null pointer");
+    AMV_REQUIRE(n_rows > 0 && k > 0, "amv_repack: empty tensor (%lld x %lld)", (long long)n_rows, (long long)k);
+    AMV_REQUIRE(((uintptr_t)r & 15) == 0, "amv_repack: repacked buffer must be 16-byte aligned");
+    switch (type) {
+    case AMV_T_Q4_0: {
+        AMV_REQUIRE(k % 32 == 0, "amv_repack: Q4_0 k %% 32 != 0");
+        AMV_REQUIRE(((uintptr_t)g & 1) == 0, "amv_repack: ggml buffer must be 2-byte aligned");
+        const int64_t nb = n_rows * (k / 32);
+        uint4* qs = reinterpret_cast<uint4*>(r);
+        uint16_t* dd = reinterpret_cast<uint16_t*>(r + nb * 16);
+        if (fwd) hipLaunchKernelGGL(k_repack_q4_0<true>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb);
+        else hipLaunchKernelGGL(k_repack_q4_0<false>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb);
+        break;
+    }
+    case AMV_T_Q8_0: {
+        AMV_REQUIRE(k % 32 == 0, "amv_repack: Q8_0 k %% 32 != 0");
+        AMV_REQUIRE(((uintptr_t)g & 1) == 0, "amv_repack: ggml buffer must be 2-byte aligned");
+        const int64_t nb = n_rows * (k / 32);
+        uint4* qs = reinterpret_cast<uint4*>(r);
+        uint16_t* dd = reinterpret_cast<uint16_t*>(r + nb * 32);
+        if (fwd) hipLaunchKernelGGL(k_repack_q8_0<true>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb);
+        else hipLaunchKernelGGL(k_repack_q8_0<false>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb);
+        break;
+    }
+    case AMV_T_Q4_K: {
+        AMV_REQUIRE(k % 256 == 0, "amv_repack: Q4_K k %% 256 != 0");
+        AMV_REQUIRE(((uintptr_t)g & 15) == 0, "amv_repack: Q4_K ggml buffer must be 16-byte aligned");
+        const int64_t nb = n_rows * (k / 256);
+        uint4* qs = reinterpret_cast<uint4*>(r);
+        uint4* head = reinterpret_cast<uint4*>(r + nb * 128);
+        if (fwd) hipLaunchKernelGGL(k_repack_q4_K<true>, grid_for(nb, 256), 256, 0, st, g, qs, head, nb);
+        else hipLaunchKernelGGL(k_repack_q4_K<false>, grid_for(nb, 256), 256, 0, st, g, qs, head, nb);
+        break;
+    }
+    case AMV_T_Q6_K: {
+        AMV_REQUIRE(k % 256 == 0, "amv_repack: Q6_K k %% 256 != 0");
+        AMV_REQUIRE(((uintptr_t)g & 1) == 0, "amv_repack: ggml buffer must be 2-byte aligned");
+        const int64_t nb = n_rows * (k / 256);
+        uint32_t* ql = reinterpret_cast<uint32_t*>(r);
+        uint32_t* qh = reinterpret_cast<uint32_t*>(r + nb * 128);
+        uint32_t* sc = reinterpret_cast<uint32_t*>(r + nb * 192);
+        uint16_t* dd = reinterpret_cast<uint16_t*>(r + nb * 208);
+        if (fwd) hipLaunchKernelGGL(k_repack_q6_K<true>, grid_for(nb, 256), 256, 0, st, g, ql, qh, sc, dd, nb);
+        else hipLaunchKernelGGL(k_repack_q6_K<false>, grid_for(nb, 256), 256, 0, st, g, ql, qh, sc, dd, nb);
+        break;
+    }
+    default: amv_set_error("amv_repack: unsupported type %d", type); return AMV_ERR_UNSUPPORTED;
+    }
+    return amv_check_launch("amv_repack");
+}
+
+extern "C" int amv_repack(int type, const void* src_ggml, void* dst, int64_t n_rows, int64_t k, void* stream) {
+    return repack_impl(type, (uint8_t*)src_ggml, (uint8_t*)dst, n_rows, k, true, amv_stream(stream));
+}
+
+extern "C" int amv_unrepack(int type, const void* src, void* dst_ggml, int64_t n_rows, int64_t k, void* stream) {
+    return repack_impl(type, (uint8_t*)dst_ggml, (uint8_t*)src, n_rows, k, false, amv_stream(stream));
+}
+
+extern "C" int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, int rule, void* y_ggml, void* y_act,
+                                void* stream) {
+    AMV_REQUIRE(x, "amv_quantize_act: null input");
+    AMV_REQUIRE(m > 0 && k > 0, "amv_quantize_act: empty input (%lld x %lld)", (long long)m, (long long)k);
+    AMV_REQUIRE(((uintptr_t)x & 15) == 0, "amv_quantize_act: input must be 16-byte aligned");
+    AMV_REQUIRE(y_act == nullptr || ((uintptr_t)y_act & 15) == 0, "amv_quantize_act: y_act must be 16-byte aligned");
+    hipStream_t st = amv_stream(stream);
+    if (type == AMV_T_Q8_0) {
+        AMV_REQUIRE(k % 32 == 0, "amv_quantize_act: Q8_0 needs k %% 32 == 0 (k = %lld)", (long long)k);
+        AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_quantize_act: bad rule %d", rule);
+        AMV_REQUIRE(y_ggml == nullptr || ((uintptr_t)y_ggml & 1) == 0, "amv_quantize_act: y_ggml misaligned");
+        const int64_t n = m * k;
+        int8_t* aq = y_act ? (int8_t*)y_act : nullptr;
+        int2* ads = y_act ? (int2*)((uint8_t*)y_act + n) : nullptr;
+        hipLaunchKernelGGL(k_quant_q8_0, grid_for(n, 256), 256, 0, st, x, n, rule, (uint8_t*)y_ggml, aq, ads);
+    } else if (type == AMV_T_Q8_K) {
+        AMV_REQUIRE(k % 256 == 0, "amv_quantize_act: Q8_K needs k %% 256 == 0 (k = %lld)", (long long)k);
+        AMV_REQUIRE(y_ggml == nullptr || ((uintptr_t)y_ggml & 3) == 0, "amv_quantize_act: y_ggml misaligned");
+        const int64_t n = m * k, nb = n / 256;
+        int8_t* aq = y_act ? (int8_t*)y_act : nullptr;
+        float* ad = y_act ? (float*)((uint8_t*)y_act + n) : nullptr;
+        int32_t* abs16 = y_act ? (int32_t*)((uint8_t*)y_act + n + nb * 4) : nullptr;
+        hipLaunchKernelGGL(k_quant_q8_K, grid_for(nb, 4), 256, 0, st, x, nb, (uint8_t*)y_ggml, aq, ad, abs16);
+    } else {
+        amv_set_error("amv_quantize_act: unsupported activation type %d", type);
+        return AMV_ERR_UNSUPPORTED;
+    }
+    return amv_check_launch("amv_quantize_act");
+}
+
+extern "C" int amv_quantize_q4_0(const float* x, int64_t n_rows, int64_t k, void* y_ggml, void* stream) {
+    AMV_REQUIRE(x && y_ggml, "amv_quantize_q4_0: null pointer");
+    AMV_REQUIRE(n_rows > 0 && k > 0 && k % 32 == 0, "amv_quantize_q4_0: bad shape %lld x %lld", (long long)n_rows,
+                (long long)k);
+    AMV_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)y_ggml & 1) == 0, "amv_quantize_q4_0: misaligned buffer");
+    const int64_t nb = n_rows * (k / 32);
+    hipLaunchKernelGGL(k_quant_q4_0, grid_for(nb, 256), 256, 0, amv_stream(stream), x, nb, (uint8_t*)y_ggml);
+    return amv_check_launch("amv_quantize_q4_0");
+}

@@ -1,0 +1,207 @@
+"""Benchmark of the quantized ggml hot path on one MI355X.
+
+Headline (BASELINE.json metric "Q4_0 GEMV GB/s (% HBM peak) + bs1 decode tok/s, Llama-8B-shape layer"):
+  one step = one Q4_0 x Q8_0 decode GEMV (MUL_MAT, M = 1) at the Llama-3-8B FFN gate/up shape 14336 x 4096, weights
+  N(0, 0.02) quantized on the GPU with ggml's Q4_0 rule, activation N(0, 1) quantized to Q8_0 (x86 rule) once.
+  The weights rotate over COPIES distinct copies (> 512 MiB in total, twice the 256 MiB Infinity Cache), so every
+  step streams its weight from HBM ("cold"); a "hot" figure (one copy, cache-resident) is reported beside it.
+  value = algorithmic bytes per GEMV (weights + Q8_0 activation + f32 output) / time per step.
+Timing: W untimed warm-up steps, then K steps bracketed by torch.cuda.synchronize() and HIP events on the stream the
+kernels run on. The CPU baseline times the oracle's multithreaded C restatement of ggml's vec_dot_q4_0_q8_0 on the
+host cores over a bounded sample of the same GEMV.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+N_ROWS, K = 14336, 4096
+COPIES = 16
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(n: int, k: int, wtype_bytes_per_block: int = 18) -> int:
+    # weights + Q8_0 activation (34 B per 32) + f32 output
+    return n * (k // 32) * wtype_bytes_per_block + (k // 32) * 34 + n * 4
+
+
+def make_weights(ops, torch, n, k, copies, seed, dev, wtype):
+    g = torch.Generator(device=dev)
+    ws = []
+    for c in range(copies):
+        g.manual_seed(seed + c)
+        wf = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32) * 0.02
+        if wtype == ops.Q4_0:
+            wg = ops.quantize_q4_0(wf)
+        else:
+            act, wg = ops.quantize_act(wf, ops.Q8_0, ops.Q8_REF, ggml=True)
+            del act
+        ws.append(ops.QWeight.from_ggml(wtype, wg, n, k))
+        del wf, wg
+    torch.cuda.synchronize()
+    return ws
+
+
+def time_steps(torch, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per step
+
+
+def cpu_baseline(seconds: float = 10.0):
+    import numpy as np
+    import oracle
+    rng = np.random.default_rng(1234)
+    w = (rng.standard_normal((N_ROWS, K)) * 0.02).astype(np.float32)
+    wq = oracle.quantize_q4_0(w)
+    del w
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    aq = oracle.quantize_q8_0(x, oracle.Q8_X86)
+    oracle.mul_mat(oracle.Q4_0, wq, N_ROWS, K, aq, 1)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.mul_mat(oracle.Q4_0, wq, N_ROWS, K, aq, 1)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 3:
+            break
+    per = el / n
+    return {
+        "value": round(gemv_bytes(N_ROWS, K) / per / 1e9, 3),
+        "unit": "GB/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"{n} Q4_0 GEMVs 14336x4096 (M=1) in {el:.1f} s, oracle vec_dot_q4_0_q8_0 (C, OpenMP), "
+                  f"{per * 1e3:.2f} ms each; host CPU: {cpu_model()}",
+    }
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def load_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 --pmc summary (profiles/)."""
+    path = os.path.join(ROOT, "profiles", "q4_0_gemv_14336x4096_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-headline", action="store_true", help="skip the secondary figures (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from ameva_compute_amd import ops
+    assert torch.cuda.is_available(), "no GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")
+    ws = make_weights(ops, torch, N_ROWS, K, COPIES, 42, dev, ops.Q4_0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    x = torch.randn((1, K), generator=g, device=dev, dtype=torch.float32)
+    act, _ = ops.quantize_act(x, ops.Q8_0, ops.Q8_X86)
+    out = torch.empty((1, N_ROWS), dtype=torch.float32, device=dev)
+
+    def step_cold(i):
+        ops.mul_mat_q(ws[i % COPIES], act, 1, out)
+
+    def step_hot(i):
+        ops.mul_mat_q(ws[0], act, 1, out)
+
+    ms_cold = time_steps(torch, step_cold, args.steps, args.warmup)
+    nbytes = gemv_bytes(N_ROWS, K)
+    gbs = nbytes / (ms_cold * 1e-3) / 1e9
+    log(f"bench: cold {ms_cold * 1e3:.2f} us/GEMV = {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
+    extra = {}
+    if not args.only_headline:
+        ms_hot = time_steps(torch, step_hot, args.steps, args.warmup)
+        extra["hot_gbs"] = round(nbytes / (ms_hot * 1e-3) / 1e9, 1)
+        extra["hot_us"] = round(ms_hot * 1e3, 3)
+
+        def step_quant(i):
+            ops.quantize_act(x, ops.Q8_0, ops.Q8_X86)
+        extra["q8_0_quantize_4096_us"] = round(time_steps(torch, step_quant, 500, 50) * 1e3, 3)
+        del ws
+        torch.cuda.empty_cache()
+        # Q4_0 4096 x 4096 (BASELINE config 1 shape), cold over 32 copies (302 MB)
+        ws1 = make_weights(ops, torch, 4096, K, 32, 99, dev, ops.Q4_0)
+        out1 = torch.empty((1, 4096), dtype=torch.float32, device=dev)
+        ms1 = time_steps(torch, lambda i: ops.mul_mat_q(ws1[i % 32], act, 1, out1), 2000, 200)
+        extra["q4_0_4096x4096_cold_gbs"] = round(gemv_bytes(4096, K) / (ms1 * 1e-3) / 1e9, 1)
+        del ws1
+        torch.cuda.empty_cache()
+        # Q8_0 14336 x 4096, cold over 10 copies (624 MB)
+        ws8 = make_weights(ops, torch, N_ROWS, K, 10, 77, dev, ops.Q8_0)
+        ms8 = time_steps(torch, lambda i: ops.mul_mat_q(ws8[i % 10], act, 1, out), 1000, 100)
+        extra["q8_0_14336x4096_cold_gbs"] = round(gemv_bytes(N_ROWS, K, 34) / (ms8 * 1e-3) / 1e9, 1)
+        del ws8
+        torch.cuda.empty_cache()
+
+    result = {
+        "metric": "Q4_0 GEMV GB/s (% HBM peak) + bs1 decode tok/s, Llama-8B-shape layer",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_cold, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 x q8_0 (int8 dot, f32 accumulate)",
+        "data": "synthetic: seeded N(0,0.02) weights quantized on the GPU (ggml Q4_0 rule), N(0,1) activation",
+        "config": {"workload": "Q4_0 GEMV 14336x4096 M=1 (Llama-3-8B FFN gate/up), Q8_0 activation, cold: "
+                               f"{COPIES} rotating weight copies ({COPIES * N_ROWS * K * 18 // 32 / 2**20:.0f} MiB)",
+                   "n_rows": N_ROWS, "k": K, "m": 1, "weight_copies": COPIES},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic()},
+        "extra": extra,
+    }
+    if not args.no_cpu:
+        log("bench: CPU baseline ...")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
