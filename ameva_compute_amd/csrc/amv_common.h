@@ -32,10 +32,33 @@ int amv_check_launch(const char* what);
 static inline hipStream_t amv_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // ---------------------------------------------------------------------------------------------------------------
-// device: fp16 <-> f32 (v_cvt_f16_f32 rounds to nearest even; the conversion back is exact)
+// device: fp16 <-> f32
+// f32 -> fp16 for stored quantization scales: IEEE round to nearest even done in integers, with ggml's NaN (0x7E00)
+// and the sign of zero kept. The hardware conversion is not used here because the compiler folds a preceding
+// multiplication into v_fma_mix (an fma with a +0 addend), which turns ggml's d = 0 / -8 = -0.0 into +0.0.
 __device__ __forceinline__ uint16_t amv_f2h(float f) {
-    _Float16 h = (_Float16)f;
-    return __builtin_bit_cast(uint16_t, h);
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u);
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // rounds to infinity
+    const int e = (int)(ax >> 23) - 127;
+    uint32_t h, rest, half;
+    if (e >= -14) {  // normal half: drop 13 mantissa bits
+        h = ((uint32_t)(e + 15) << 10) | ((ax & 0x7FFFFFu) >> 13);
+        rest = ax & 0x1FFFu;
+        half = 0x1000u;
+    } else if (e >= -25) {  // subnormal half: the 24-bit significand shifted right by -(e + 1) = 14..24 bits
+        const uint32_t mf = (ax & 0x7FFFFFu) | 0x800000u;
+        const int d = -(e + 1);
+        h = mf >> d;
+        rest = mf & ((1u << d) - 1u);
+        half = 1u << (d - 1);
+    } else {
+        return (uint16_t)sign;
+    }
+    if (rest > half || (rest == half && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
 }
 __device__ __forceinline__ float amv_h2f(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));

@@ -40,7 +40,7 @@ def q8_edge_rows(k, rng):
     x[1, :32] = 0.0                                  # all-zero block: d = 0, q = 0
     x[2, :32] = np.arange(32, dtype=np.float32) - 15.5  # ties of x * 127/amax
     x[3, :] *= 1e-3
-    x[4, 32:64] = 127.0 * (np.arange(32) % 3 - 1)    # exact +-127
+    x[4, k - 32:] = 127.0 * (np.arange(32) % 3 - 1)   # exact +-127
     x[5, :32] = np.float32(2.0) ** -20 * (np.arange(32) - 16)  # tiny block (fp16 subnormal d)
     return x
 
