@@ -10,7 +10,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libameva_hip.so")
 
-P, I32, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+P, I32, I64, F32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 # name -> (restype, argtypes); every symbol include/ameva_hip.h declares
 SIGNATURES = {
@@ -24,6 +24,16 @@ SIGNATURES = {
     "amv_quantize_q4_0": (I32, [P, I64, I64, P, P]),
     "amv_mul_mat_vec": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
     "amv_mul_mat_block_sums": (I32, [I32, P, I64, I64, P, I64, P, P]),
+    "amv_quantize_k": (I32, [I32, P, I64, I64, P, P]),
+    "amv_i2s_act_bytes": (I64, [I64, I64]),
+    "amv_i2s_quantize_act": (I32, [P, I64, I64, P, P]),
+    "amv_i2s_gemv": (I32, [P, I64, I64, P, I64, F32, P, I64, P]),
+    "amv_i2s_gemv_sums": (I32, [P, I64, I64, P, I64, P, P]),
+    "amv_rms_norm": (I32, [P, I64, I64, F32, P, P, P, P, I32, P]),
+    "amv_rope": (I32, [P, P, P, I64, I64, I64, I32, I32, F32, F32, F32, P]),
+    "amv_swiglu": (I32, [P, P, P, I64, P]),
+    "amv_flash_attn_workspace_bytes": (I64, [I64, I64, I64, I64]),
+    "amv_flash_attn_decode": (I32, [P, P, P, P, P, I64, I64, I64, I64, I64, F32, P, I64, P]),
 }
 
 _lib = None

@@ -140,6 +140,168 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
     }
 }
 
+// ------------------------------------------------------------------------------------------------ K-quants
+// Q4_K and Q6_K rows are cut into 16-byte slices of their 4-bit data (k / 32 slices per row, 8 per 256-weight
+// super-block), lane l taking slice l + 64 i. A Q4_K slice t of a super-block holds the low nibbles of weights
+// 64c + 16h + (0..15) and the high nibbles of 64c + 32 + 16h + (0..15) (c = t / 2, h = t % 2), i.e. halves of
+// units 2c and 2c + 1. A Q6_K slice holds ql bytes 16t .. 16t + 15 (weights 128hh + 32s + lq + (0..15) for
+// s = s_lo and s_lo + 2), its two high bits come from 16 bytes of qh. Activations are Q8_K (one f32 scale per 256,
+// int32 sums per 16, which also supply the constant offsets -32 (Q6_K) and the minima (Q4_K)).
+// Per super-block ggml's vec_dot_q4_K_q8_K computes d*da*sum_u sc_u dot_u - dmin*da*sum_u m_u bsum_u and
+// vec_dot_q6_K_q8_K d*da*sum_g sc_g dot(q6 - 32, qa)_g; the lanes form the same integers per slice.
+
+// byte i (0..11) of the packed 6-bit scales held in three words
+__device__ __forceinline__ uint32_t k4_byte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xFFu;
+}
+// get_scale_min_k4 (reference ameva_qdecode.glsl:229-236)
+__device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc, int& m) {
+    if (j < 4) {
+        sc = (int)(k4_byte(s0, s1, s2, j) & 63u);
+        m = (int)(k4_byte(s0, s1, s2, j + 4) & 63u);
+    } else {
+        sc = (int)((k4_byte(s0, s1, s2, j + 4) & 0xFu) | ((k4_byte(s0, s1, s2, j - 4) >> 6) << 4));
+        m = (int)((k4_byte(s0, s1, s2, j + 4) >> 4) | ((k4_byte(s0, s1, s2, j) >> 6) << 4));
+    }
+}
+
+__device__ __forceinline__ int dot16(uint4 w, int4 a, int acc) {
+    acc = amv_dot4((int)w.x, a.x, acc);
+    acc = amv_dot4((int)w.y, a.y, acc);
+    acc = amv_dot4((int)w.z, a.z, acc);
+    return amv_dot4((int)w.w, a.w, acc);
+}
+
+template <int R, bool BLOCK_SUMS>
+__global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, const uint4* __restrict__ wh,
+                                                 int n_rows, int nsl, const int8_t* __restrict__ aq,
+                                                 const float* __restrict__ ad, const int* __restrict__ abs16,
+                                                 float* __restrict__ dst, int32_t* __restrict__ sums) {
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+    if (row0 >= n_rows) return;
+    const int nsb = nsl >> 3;
+    const int4* a4 = reinterpret_cast<const int4*>(aq);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int j0 = 0; j0 < nsl; j0 += 64) {
+        const int j = min(j0 + lane, nsl - 1);  // nsl is a multiple of 8: clamped lanes fill whole groups of 8
+        const int sb = j >> 3, t = j & 7, c = t >> 1, h = t & 1;
+        uint4 q[R], hd[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t row = (size_t)min(row0 + r, n_rows - 1);
+            q[r] = wq[row * nsl + j];
+            hd[r] = wh[row * nsb + sb];
+        }
+        const int4 alo = a4[sb * 16 + 4 * c + h], ahi = a4[sb * 16 + 4 * c + 2 + h];
+        const float da = ad[sb];
+        const int bslo = abs16[sb * 16 + 4 * c + h], bshi = abs16[sb * 16 + 4 * c + 2 + h];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int sl, ml, sh, mh;
+            k4_scale_min(2 * c, hd[r].y, hd[r].z, hd[r].w, sl, ml);
+            k4_scale_min(2 * c + 1, hd[r].y, hd[r].z, hd[r].w, sh, mh);
+            const uint4 lo = make_uint4(q[r].x & M4, q[r].y & M4, q[r].z & M4, q[r].w & M4);
+            const uint4 hi = make_uint4((q[r].x >> 4) & M4, (q[r].y >> 4) & M4, (q[r].z >> 4) & M4, (q[r].w >> 4) & M4);
+            int isum = sl * dot16(lo, alo, 0) + sh * dot16(hi, ahi, 0);
+            int msum = ml * bslo + mh * bshi;
+            if (BLOCK_SUMS) {
+#pragma unroll
+                for (int o = 1; o < 8; o <<= 1) {
+                    isum += __shfl_xor(isum, o, AMV_WAVE);
+                    msum += __shfl_xor(msum, o, AMV_WAVE);
+                }
+                if (t == 0 && j0 + lane < nsl && row0 + r < n_rows) {
+                    sums[((size_t)(row0 + r) * nsb + sb) * 2] = isum;
+                    sums[((size_t)(row0 + r) * nsb + sb) * 2 + 1] = msum;
+                }
+            } else if (j0 + lane < nsl) {
+                const float d = amv_h2f(hd[r].x) * da, dmin = amv_h2f(hd[r].x >> 16) * da;
+                acc[r] = fmaf(d, (float)isum, acc[r]);
+                acc[r] = fmaf(-dmin, (float)msum, acc[r]);
+            }
+        }
+    }
+    if (!BLOCK_SUMS) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float tt = amv_wave_sum(acc[r]);
+            if (lane == 0 && row0 + r < n_rows) dst[row0 + r] = tt;
+        }
+    }
+}
+
+template <int R, bool BLOCK_SUMS>
+__global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, const uint4* __restrict__ wqh,
+                                                 const uint4* __restrict__ wsc, const uint16_t* __restrict__ wd,
+                                                 int n_rows, int nsl, const int8_t* __restrict__ aq,
+                                                 const float* __restrict__ ad, const int* __restrict__ abs16,
+                                                 float* __restrict__ dst, int32_t* __restrict__ sums) {
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+    if (row0 >= n_rows) return;
+    const int nsb = nsl >> 3;
+    const int4* a4 = reinterpret_cast<const int4*>(aq);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int j0 = 0; j0 < nsl; j0 += 64) {
+        const int j = min(j0 + lane, nsl - 1);
+        const int sb = j >> 3, t = j & 7;
+        const int hh = t >> 2, l0 = 16 * (t & 3);  // ql byte offset 64 hh + l0
+        const int slo = l0 >> 5, lq = l0 & 31;      // weights 128 hh + 32 s + lq + i, s in {slo, slo + 2}
+        uint4 ql[R], qh[R], sc[R];
+        uint16_t dd[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t rb = (size_t)min(row0 + r, n_rows - 1) * nsb + sb;
+            ql[r] = wl[(size_t)min(row0 + r, n_rows - 1) * nsl + j];
+            qh[r] = wqh[rb * 4 + 2 * hh + (lq >> 4)];
+            sc[r] = wsc[rb];
+            dd[r] = wd[rb];
+        }
+        const int elo = 128 * hh + 32 * slo + lq;  // element offset in the super-block
+        const int4 alo = a4[(sb * 256 + elo) >> 4], ahi = a4[(sb * 256 + elo + 64) >> 4];
+        const float da = ad[sb];
+        const int glo = elo >> 4, ghi = glo + 4;
+        const int blo = abs16[sb * 16 + glo], bhi = abs16[sb * 16 + ghi];
+        const int shlo = 2 * slo, shhi = 2 * slo + 4;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint4 L = ql[r], H = qh[r];
+            const uint4 vlo = make_uint4((L.x & M4) | (((H.x >> shlo) & 0x03030303u) << 4),
+                                         (L.y & M4) | (((H.y >> shlo) & 0x03030303u) << 4),
+                                         (L.z & M4) | (((H.z >> shlo) & 0x03030303u) << 4),
+                                         (L.w & M4) | (((H.w >> shlo) & 0x03030303u) << 4));
+            const uint4 vhi = make_uint4(((L.x >> 4) & M4) | (((H.x >> shhi) & 0x03030303u) << 4),
+                                         ((L.y >> 4) & M4) | (((H.y >> shhi) & 0x03030303u) << 4),
+                                         ((L.z >> 4) & M4) | (((H.z >> shhi) & 0x03030303u) << 4),
+                                         ((L.w >> 4) & M4) | (((H.w >> shhi) & 0x03030303u) << 4));
+            const uint32_t scw[4] = {sc[r].x, sc[r].y, sc[r].z, sc[r].w};
+            const int sclo = (int)(int8_t)((scw[glo >> 2] >> (8 * (glo & 3))) & 0xFFu);
+            const int schi = (int)(int8_t)((scw[ghi >> 2] >> (8 * (ghi & 3))) & 0xFFu);
+            int isum = sclo * (dot16(vlo, alo, 0) - 32 * blo) + schi * (dot16(vhi, ahi, 0) - 32 * bhi);
+            if (BLOCK_SUMS) {
+#pragma unroll
+                for (int o = 1; o < 8; o <<= 1) isum += __shfl_xor(isum, o, AMV_WAVE);
+                if (t == 0 && j0 + lane < nsl && row0 + r < n_rows) sums[(size_t)(row0 + r) * nsb + sb] = isum;
+            } else if (j0 + lane < nsl) {
+                acc[r] = fmaf(amv_h2f(dd[r]) * da, (float)isum, acc[r]);
+            }
+        }
+    }
+    if (!BLOCK_SUMS) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float tt = amv_wave_sum(acc[r]);
+            if (lane == 0 && row0 + r < n_rows) dst[row0 + r] = tt;
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ dispatch
 struct MmvArgs {
     int wtype;
@@ -178,6 +340,30 @@ static void launch_q8_0(const MmvArgs& a, hipStream_t st) {
                        a.dst, a.sums);
 }
 
+template <int R, bool S>
+static void launch_q4_K(const MmvArgs& a, hipStream_t st) {
+    const int nsl = a.k / 32, nsb = a.k / 256;
+    const int64_t nblk = (int64_t)a.n_rows * nsb;
+    const uint4* wq = reinterpret_cast<const uint4*>(a.w);
+    const uint4* wh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
+    const int waves = (a.n_rows + R - 1) / R;
+    hipLaunchKernelGGL((k_mmv_q4_K<R, S>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
+                       (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums);
+}
+
+template <int R, bool S>
+static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
+    const int nsl = a.k / 32, nsb = a.k / 256;
+    const int64_t nblk = (int64_t)a.n_rows * nsb;
+    const uint4* wl = reinterpret_cast<const uint4*>(a.w);
+    const uint4* wqh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
+    const uint4* wsc = reinterpret_cast<const uint4*>(a.w + nblk * 192);
+    const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 208);
+    const int waves = (a.n_rows + R - 1) / R;
+    hipLaunchKernelGGL((k_mmv_q6_K<R, S>), dim3((waves + 3) / 4), dim3(256), 0, st, wl, wqh, wsc, wd, a.n_rows, nsl,
+                       a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums);
+}
+
 // Kernel variant (rows per wave R, blocks-per-lane unroll U) chosen from the block count of a row; the table is the
 // result of the launch-shape sweep on MI355X (see the bench and profiles of this repository).
 template <bool S>
@@ -185,15 +371,17 @@ static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
     switch (a.wtype) {
     case AMV_T_Q4_0:
-        if (nb <= 64) launch_q4_0<4, 1, S>(a, st);
-        else if (nb <= 128) launch_q4_0<4, 2, S>(a, st);
-        else launch_q4_0<2, 4, S>(a, st);
+        // R = 2 rows per wave, one 64-block step at a time: the fastest shape of the MI355X sweep at K = 4096
+        // (7.44 us cold for 14336 x 4096 against 8.5 us for R = 4, 11.2 us for R = 8)
+        launch_q4_0<2, 1, S>(a, st);
         return AMV_OK;
     case AMV_T_Q8_0:
         if (nb <= 64) launch_q8_0<4, 1, S>(a, st);
         else if (nb <= 128) launch_q8_0<2, 2, S>(a, st);
         else launch_q8_0<2, 2, S>(a, st);
         return AMV_OK;
+    case AMV_T_Q4_K: launch_q4_K<2, S>(a, st); return AMV_OK;
+    case AMV_T_Q6_K: launch_q6_K<2, S>(a, st); return AMV_OK;
     default: amv_set_error("amv_mul_mat_vec: weight type %d not supported", a.wtype); return AMV_ERR_UNSUPPORTED;
     }
 }

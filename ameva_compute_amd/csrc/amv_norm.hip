@@ -1,0 +1,191 @@
+// RMS_NORM (with the fused MUL by the norm weight and the fused Q8_0 quantization of the next GEMV's input), ROPE
+// and SWIGLU for the decode/prefill path.
+//
+// RMS_NORM follows ggml_compute_forward_rms_norm_f32 (reference ameva_rms_norm.comp:3-7): squares as f32 products
+// summed in double, mean = (float)(sum / n), scale = 1 / sqrtf(mean + eps), y = x * scale, o = y * w. Division and
+// sqrt are correctly rounded (build flags), so y and o match the CPU bit for bit whenever the two double sums round
+// to the same f32 mean. ROPE follows ggml's rope f32 (ggml-ameva.cpp:3982-3984, ameva_rope.comp:64-92): the angle of
+// pair j is freq_scale * (p * theta_scale^j) built by the same repeated f32 multiplication as the CPU.
+#include "amv_common.h"
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q8_0 quantization of one 32-element block held by one lane (the rules of amv_quantize_act)
+__device__ __forceinline__ void q8_block(const float (&v)[32], int rule, int8_t* __restrict__ qs, int2* __restrict__ meta) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.0f;
+    float id;
+    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t wq[8];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float t = v[4 * i + e] * id;
+            float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+            qf = fminf(127.0f, fmaxf(-127.0f, qf));
+            const int q = (int)qf;
+            s += q;
+            wv |= (uint32_t)(q & 0xFF) << (8 * e);
+        }
+        wq[i] = wv;
+    }
+    reinterpret_cast<uint4*>(qs)[0] = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+    reinterpret_cast<uint4*>(qs)[1] = make_uint4(wq[4], wq[5], wq[6], wq[7]);
+    *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
+}
+
+// one workgroup of 256 per row
+__global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, int n, float eps,
+                                                 const float* __restrict__ w, float* __restrict__ y,
+                                                 float* __restrict__ o, int8_t* __restrict__ aq,
+                                                 int2* __restrict__ ameta, int rule) {
+    __shared__ double sred[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* xr = x + (size_t)row * n;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    double s = 0.0;
+    for (int i = tid; i < n / 4; i += 256) {
+        const float4 v = x4[i];
+        s += (double)(v.x * v.x);
+        s += (double)(v.y * v.y);
+        s += (double)(v.z * v.z);
+        s += (double)(v.w * v.w);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, AMV_WAVE);
+    if ((tid & 63) == 0) sred[tid >> 6] = s;
+    __syncthreads();
+    const double tot = (sred[0] + sred[1]) + (sred[2] + sred[3]);
+    const float mean = (float)(tot / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    const bool to_o = (w != nullptr && o != nullptr);
+    if (aq == nullptr) {
+        for (int i = tid; i < n / 4; i += 256) {
+            const float4 v = x4[i];
+            const float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
+            if (y) reinterpret_cast<float4*>(y + (size_t)row * n)[i] = yv;
+            if (to_o) {
+                const float4 wv = reinterpret_cast<const float4*>(w)[i];
+                reinterpret_cast<float4*>(o + (size_t)row * n)[i] =
+                    make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
+            }
+        }
+        return;
+    }
+    // with the fused quantization a lane owns whole 32-element blocks
+    const int nb = n / 32;
+    for (int b = tid; b < nb; b += 256) {
+        float q[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = x4[8 * b + i];
+            float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
+            if (y) reinterpret_cast<float4*>(y + (size_t)row * n)[8 * b + i] = yv;
+            if (to_o) {
+                const float4 wv = reinterpret_cast<const float4*>(w)[8 * b + i];
+                yv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
+                reinterpret_cast<float4*>(o + (size_t)row * n)[8 * b + i] = yv;
+            }
+            q[4 * i] = yv.x;
+            q[4 * i + 1] = yv.y;
+            q[4 * i + 2] = yv.z;
+            q[4 * i + 3] = yv.w;
+        }
+        q8_block(q, rule, aq + (size_t)row * n + 32 * b, ameta + (size_t)row * nb + b);
+    }
+}
+
+extern "C" int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y, float* o,
+                            void* act, int rule, void* stream) {
+    AMV_REQUIRE(x, "amv_rms_norm: null input");
+    AMV_REQUIRE(n_rows > 0 && n > 0 && n_rows <= INT32_MAX && n <= INT32_MAX, "amv_rms_norm: bad shape");
+    AMV_REQUIRE(n % 4 == 0, "amv_rms_norm: n %% 4 != 0");
+    AMV_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)o & 15) == 0 &&
+                    ((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0,
+                "amv_rms_norm: buffers must be 16-byte aligned");
+    AMV_REQUIRE(!o || w, "amv_rms_norm: o needs the weight w");
+    AMV_REQUIRE(y || o || act, "amv_rms_norm: no output requested");
+    AMV_REQUIRE(!act || n % 32 == 0, "amv_rms_norm: the fused Q8_0 output needs n %% 32 == 0");
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_rms_norm: bad rule");
+    int8_t* aq = act ? (int8_t*)act : nullptr;
+    int2* ameta = act ? (int2*)((uint8_t*)act + n_rows * n) : nullptr;
+    // the quantized output is of o when the weight is given, of y otherwise
+    const float* wq = w;
+    float* oo = o;
+    if (act && w && !o) {
+        amv_set_error("amv_rms_norm: the fused quantization of y * w needs o");
+        return AMV_ERR_INVALID_ARG;
+    }
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(256), 0, amv_stream(stream), x, (int)n, eps, wq, y, oo,
+                       aq, ameta, rule);
+    return amv_check_launch("amv_rms_norm");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// ROPE: x, y [n_tok][n_head][ne0] contiguous f32 (in place allowed), pos int32 [n_tok]; mode 0 NORMAL (pairs 2j, 2j+1)
+// or 2 NEOX (pairs j, j + n_dims/2); elements past n_dims copied. One lane per pair.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rope(const float* x, float* y,  // may alias (in place)
+                                             const int32_t* __restrict__ pos, int64_t n_pairs, int n_head, int ne0,
+                                             int n_dims, int neox, float theta_scale, float freq_scale,
+                                             float attn_factor) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_pairs) return;
+    const int half = ne0 / 2;
+    const int j = (int)(i % half);
+    const int64_t th = i / half;  // token * n_head + head
+    const int t = (int)(th / n_head);
+    const float* xr = x + th * ne0;
+    float* yr = y + th * ne0;
+    if (2 * j >= n_dims) {
+        const float a = xr[2 * j], b = xr[2 * j + 1];
+        yr[2 * j] = a;
+        yr[2 * j + 1] = b;
+        return;
+    }
+    float theta = (float)pos[t];
+    for (int k = 0; k < j; ++k) theta *= theta_scale;
+    const float ang = freq_scale * theta;
+    const float c = cosf(ang) * attn_factor, s = sinf(ang) * attn_factor;
+    const int e0 = neox ? j : 2 * j;
+    const int e1 = neox ? j + n_dims / 2 : 2 * j + 1;
+    const float x0 = xr[e0], x1 = xr[e1];
+    yr[e0] = x0 * c - x1 * s;
+    yr[e1] = x0 * s + x1 * c;
+}
+
+extern "C" int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_tok, int64_t n_head, int64_t ne0,
+                        int n_dims, int mode, float freq_base, float freq_scale, float attn_factor, void* stream) {
+    AMV_REQUIRE(x && y && pos, "amv_rope: null pointer");
+    AMV_REQUIRE(n_tok > 0 && n_head > 0 && ne0 > 0 && ne0 % 2 == 0, "amv_rope: bad shape");
+    AMV_REQUIRE(n_dims > 0 && n_dims <= ne0 && n_dims % 2 == 0, "amv_rope: bad n_dims %d", n_dims);
+    AMV_REQUIRE(mode == 0 || mode == 2, "amv_rope: mode %d not supported (NORMAL 0 and NEOX 2 are)", mode);
+    // the same expression as the CPU (ggml-ameva.cpp:3984)
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    const int64_t n_pairs = n_tok * n_head * (ne0 / 2);
+    hipLaunchKernelGGL(k_rope, dim3((unsigned)((n_pairs + 255) / 256)), dim3(256), 0, amv_stream(stream), x, y, pos,
+                       n_pairs, (int)n_head, (int)ne0, n_dims, mode == 2 ? 1 : 0, theta_scale, freq_scale, attn_factor);
+    return amv_check_launch("amv_rope");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// SWIGLU (ggml_vec_swiglu_f32; ameva_glu.comp:45-46): y = g / (1 + expf(-g)) * u
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ g, const float* __restrict__ u,
+                                               float* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float a = g[i];
+    y[i] = (a / (1.0f + expf(-a))) * u[i];
+}
+
+extern "C" int amv_swiglu(const float* g, const float* u, float* y, int64_t n, void* stream) {
+    AMV_REQUIRE(g && u && y && n > 0, "amv_swiglu: bad arguments");
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, amv_stream(stream), g, u, y, n);
+    return amv_check_launch("amv_swiglu");
+}

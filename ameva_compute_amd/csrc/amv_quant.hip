@@ -357,3 +357,123 @@ extern "C" int amv_quantize_q4_0(const float* x, int64_t n_rows, int64_t k, void
     hipLaunchKernelGGL(k_quant_q4_0, grid_for(nb, 256), 256, 0, amv_stream(stream), x, nb, (uint8_t*)y_ggml);
     return amv_check_launch("amv_quantize_q4_0");
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q4_K / Q6_K weight quantization with this library's own deterministic rule (ggml's make_qkx2_quants search is not
+// reproduced: the weight bytes of these types are not a parity target, the dot products on given bytes are).
+// One lane per 256-weight super-block; output in ggml's block layout.
+//   Q4_K: per 32-weight unit u: lo = min(0, min x), hi = max(lo, max x), scale_u = (hi - lo) / 15, min_u = -lo;
+//         d = max scale_u / 63, dmin = max min_u / 63 (fp16); sc_u = rint(scale_u / d), m_u = rint(min_u / dmin)
+//         (<= 63); q = clamp(rint((x + dmin m_u) / (d sc_u)), 0, 15).
+//   Q6_K: per 16-weight group g: scale_g = max|x| / 31; d = max scale_g / 127 (fp16); sc_g = rint(scale_g / d)
+//         (<= 127); q = clamp(rint(x / (d sc_g)), -32, 31).
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(128) void k_quant_q4_K(const float* __restrict__ x, int64_t n_sb, uint8_t* __restrict__ y) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_sb) return;
+    const float* xb = x + b * 256;
+    float scl[8], mns[8];
+    float maxs = 0.0f, maxm = 0.0f;
+    for (int u = 0; u < 8; ++u) {
+        float lo = 0.0f, hi = -INFINITY;
+        for (int i = 0; i < 32; ++i) {
+            lo = fminf(lo, xb[32 * u + i]);
+            hi = fmaxf(hi, xb[32 * u + i]);
+        }
+        hi = fmaxf(hi, lo);
+        scl[u] = (hi - lo) / 15.0f;
+        mns[u] = -lo;
+        maxs = fmaxf(maxs, scl[u]);
+        maxm = fmaxf(maxm, mns[u]);
+    }
+    const uint16_t d16 = amv_f2h(maxs / 63.0f), m16 = amv_f2h(maxm / 63.0f);
+    const float df = amv_h2f(d16), mf = amv_h2f(m16);
+    int sc[8], mq[8];
+    for (int u = 0; u < 8; ++u) {
+        sc[u] = df > 0.0f ? min(63, (int)rintf(scl[u] / df)) : 0;
+        mq[u] = mf > 0.0f ? min(63, (int)rintf(mns[u] / mf)) : 0;
+    }
+    uint8_t blk[144];
+    blk[0] = (uint8_t)(d16 & 0xFF);
+    blk[1] = (uint8_t)(d16 >> 8);
+    blk[2] = (uint8_t)(m16 & 0xFF);
+    blk[3] = (uint8_t)(m16 >> 8);
+    for (int j = 0; j < 4; ++j) {
+        blk[4 + j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+        blk[8 + j] = (uint8_t)((mq[j] & 63) | ((mq[j + 4] >> 4) << 6));
+        blk[12 + j] = (uint8_t)((sc[j + 4] & 15) | ((mq[j + 4] & 15) << 4));
+    }
+    for (int c = 0; c < 4; ++c) {
+        for (int l = 0; l < 32; ++l) {
+            int qq[2];
+            for (int h = 0; h < 2; ++h) {
+                const int u = 2 * c + h;
+                const float dl = df * (float)sc[u], ml = mf * (float)mq[u];
+                int q = 0;
+                if (dl > 0.0f) q = (int)rintf((xb[64 * c + 32 * h + l] + ml) / dl);
+                qq[h] = min(15, max(0, q));
+            }
+            blk[16 + 32 * c + l] = (uint8_t)(qq[0] | (qq[1] << 4));
+        }
+    }
+    uint4* yb = reinterpret_cast<uint4*>(y + b * 144);
+    const uint4* src = reinterpret_cast<const uint4*>(blk);
+    for (int i = 0; i < 9; ++i) yb[i] = src[i];
+}
+
+__global__ __launch_bounds__(128) void k_quant_q6_K(const float* __restrict__ x, int64_t n_sb, uint8_t* __restrict__ y) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_sb) return;
+    const float* xb = x + b * 256;
+    float scl[16], maxs = 0.0f;
+    for (int g = 0; g < 16; ++g) {
+        float a = 0.0f;
+        for (int i = 0; i < 16; ++i) a = fmaxf(a, fabsf(xb[16 * g + i]));
+        scl[g] = a / 31.0f;
+        maxs = fmaxf(maxs, scl[g]);
+    }
+    const uint16_t d16 = amv_f2h(maxs / 127.0f);
+    const float df = amv_h2f(d16);
+    int sc[16];
+    for (int g = 0; g < 16; ++g) sc[g] = df > 0.0f ? min(127, (int)rintf(scl[g] / df)) : 0;
+    uint8_t blk[210];
+    for (int i = 0; i < 192; ++i) blk[i] = 0;
+    for (int h = 0; h < 2; ++h) {
+        for (int l = 0; l < 32; ++l) {
+            int q[4];
+            for (int s = 0; s < 4; ++s) {
+                const int e = 128 * h + 32 * s + l;
+                const float dl = df * (float)sc[e >> 4];
+                int t = 0;
+                if (dl > 0.0f) t = (int)rintf(xb[e] / dl);
+                q[s] = min(31, max(-32, t)) + 32;
+            }
+            blk[64 * h + l] = (uint8_t)((q[0] & 15) | ((q[2] & 15) << 4));
+            blk[64 * h + 32 + l] = (uint8_t)((q[1] & 15) | ((q[3] & 15) << 4));
+            blk[128 + 32 * h + l] = (uint8_t)((q[0] >> 4) | ((q[1] >> 4) << 2) | ((q[2] >> 4) << 4) | ((q[3] >> 4) << 6));
+        }
+    }
+    for (int g = 0; g < 16; ++g) blk[192 + g] = (uint8_t)(int8_t)sc[g];
+    blk[208] = (uint8_t)(d16 & 0xFF);
+    blk[209] = (uint8_t)(d16 >> 8);
+    uint16_t* yb = reinterpret_cast<uint16_t*>(y + b * 210);
+    for (int i = 0; i < 105; ++i) yb[i] = (uint16_t)(blk[2 * i] | (blk[2 * i + 1] << 8));
+}
+
+extern "C" int amv_quantize_k(int type, const float* x, int64_t n_rows, int64_t k, void* y_ggml, void* stream) {
+    AMV_REQUIRE(x && y_ggml, "amv_quantize_k: null pointer");
+    AMV_REQUIRE(n_rows > 0 && k > 0 && k % 256 == 0, "amv_quantize_k: bad shape %lld x %lld", (long long)n_rows,
+                (long long)k);
+    const int64_t nsb = n_rows * (k / 256);
+    if (type == AMV_T_Q4_K) {
+        AMV_REQUIRE(((uintptr_t)y_ggml & 15) == 0, "amv_quantize_k: Q4_K output must be 16-byte aligned");
+        hipLaunchKernelGGL(k_quant_q4_K, grid_for(nsb, 128), 128, 0, amv_stream(stream), x, nsb, (uint8_t*)y_ggml);
+    } else if (type == AMV_T_Q6_K) {
+        AMV_REQUIRE(((uintptr_t)y_ggml & 1) == 0, "amv_quantize_k: Q6_K output must be 2-byte aligned");
+        hipLaunchKernelGGL(k_quant_q6_K, grid_for(nsb, 128), 128, 0, amv_stream(stream), x, nsb, (uint8_t*)y_ggml);
+    } else {
+        amv_set_error("amv_quantize_k: type %d is not a K-quant this library quantizes (12 Q4_K, 14 Q6_K)", type);
+        return AMV_ERR_UNSUPPORTED;
+    }
+    return amv_check_launch("amv_quantize_k");
+}

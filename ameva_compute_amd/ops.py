@@ -130,3 +130,103 @@ def block_sums(w: QWeight, act: torch.Tensor, m: int) -> torch.Tensor:
     check(lib().amv_mul_mat_block_sums(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(),
                                        _stream()), "amv_mul_mat_block_sums")
     return out
+
+
+def quantize_k(x: torch.Tensor, wtype: int) -> torch.Tensor:
+    """f32 rows [n, k] -> ggml Q4_K / Q6_K blocks with this library's own rule (see include/ameva_hip.h)."""
+    _need_gpu(x, "quantize_k")
+    x2 = x.reshape(-1, x.shape[-1])
+    n, k = x2.shape
+    y = torch.empty((n, ggml_row_bytes(wtype, k)), dtype=torch.uint8, device=x.device)
+    check(lib().amv_quantize_k(wtype, x2.data_ptr(), n, k, y.data_ptr(), _stream()), "amv_quantize_k")
+    return y
+
+
+# ------------------------------------------------------------------------------------------------ BitNet I2_S
+def i2s_quantize_act(x: torch.Tensor) -> torch.Tensor:
+    """quantize_activation_int8 per row of x f32 [m, k] -> activation buffer (int8 q | {dequant, sum q} per row)."""
+    _need_gpu(x, "i2s_quantize_act")
+    x2 = x.reshape(-1, x.shape[-1])
+    m, k = x2.shape
+    act = torch.empty(lib().amv_i2s_act_bytes(m, k), dtype=torch.uint8, device=x.device)
+    check(lib().amv_i2s_quantize_act(x2.data_ptr(), m, k, act.data_ptr(), _stream()), "amv_i2s_quantize_act")
+    return act
+
+
+def i2s_gemv(w: torch.Tensor, n_rows: int, k: int, act: torch.Tensor, m: int, weight_scale: float) -> torch.Tensor:
+    """bitnet_gemv: [m, n_rows] f32 from the I2_S tensor bytes w (payload first) and i2s_quantize_act output."""
+    _need_gpu(w, "i2s_gemv")
+    out = torch.empty((m, n_rows), dtype=torch.float32, device=w.device)
+    check(lib().amv_i2s_gemv(w.data_ptr(), n_rows, k, act.data_ptr(), m, weight_scale, out.data_ptr(), n_rows,
+                             _stream()), "amv_i2s_gemv")
+    return out
+
+
+def i2s_gemv_sums(w: torch.Tensor, n_rows: int, k: int, act: torch.Tensor, m: int) -> torch.Tensor:
+    out = torch.empty((m, n_rows), dtype=torch.int32, device=w.device)
+    check(lib().amv_i2s_gemv_sums(w.data_ptr(), n_rows, k, act.data_ptr(), m, out.data_ptr(), _stream()),
+          "amv_i2s_gemv_sums")
+    return out
+
+
+def i2s_tensor_scale(tensor_bytes: torch.Tensor, n_rows: int, k: int) -> float:
+    """The f32 scale trailer right after the n_rows * k/4 byte payload (amuda_gguf.c:659-681); read on the host."""
+    off = n_rows * k // 4
+    return float(tensor_bytes[off:off + 4].cpu().view(torch.float32)[0])
+
+
+# ------------------------------------------------------------------------------------ RMS_NORM, ROPE, SWIGLU
+def rms_norm(x: torch.Tensor, eps: float, w: torch.Tensor | None = None, quantize: bool = False,
+             rule: int = Q8_X86):
+    """ggml_rms_norm (+ the fused MUL by w, + the fused Q8_0 quantization of the result).
+    Returns y, or (y, o) with w, plus the activation buffer last when quantize=True."""
+    _need_gpu(x, "rms_norm")
+    x2 = x.reshape(-1, x.shape[-1])
+    m, n = x2.shape
+    y = torch.empty_like(x2)
+    o = torch.empty_like(x2) if w is not None else None
+    act = torch.empty(lib().amv_act_bytes(Q8_0, m, n), dtype=torch.uint8, device=x.device) if quantize else None
+    check(lib().amv_rms_norm(x2.data_ptr(), m, n, eps, _ptr(w), y.data_ptr(), _ptr(o), _ptr(act), rule, _stream()),
+          "amv_rms_norm")
+    res = (y,) if o is None else (y, o)
+    if quantize:
+        res = res + (act,)
+    return res[0] if len(res) == 1 else res
+
+
+def rope(x: torch.Tensor, pos: torch.Tensor, n_dims: int, mode: int = 0, freq_base: float = 10000.0,
+         freq_scale: float = 1.0, attn_factor: float = 1.0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_rope_ext (ext_factor 0): x f32 [n_tok, n_head, ne0], pos int32 [n_tok]."""
+    _need_gpu(x, "rope")
+    n_tok, n_head, ne0 = x.shape
+    y = torch.empty_like(x) if out is None else out
+    check(lib().amv_rope(x.data_ptr(), y.data_ptr(), pos.data_ptr(), n_tok, n_head, ne0, n_dims, mode, freq_base,
+                         freq_scale, attn_factor, _stream()), "amv_rope")
+    return y
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    _need_gpu(g, "swiglu")
+    y = torch.empty_like(g)
+    check(lib().amv_swiglu(g.data_ptr(), u.data_ptr(), y.data_ptr(), g.numel(), _stream()), "amv_swiglu")
+    return y
+
+
+# ------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
+def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, n_kv: int | None = None,
+                      mask: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """q f32 [n_head, D]; k, v f16 [n_head_kv, kv_stride, D] (the first n_kv rows used); mask f16 [n_kv] or None."""
+    _need_gpu(q, "flash_attn_decode")
+    n_head, D = q.shape
+    n_head_kv, kv_stride, _ = k.shape
+    n_kv = kv_stride if n_kv is None else n_kv
+    need = lib().amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv, D)
+    if need < 0:
+        raise ValueError("flash_attn_decode: unsupported shape")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    out = torch.empty_like(q)
+    check(lib().amv_flash_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(mask), out.data_ptr(), n_head,
+                                      n_head_kv, n_kv, kv_stride, D, scale, workspace.data_ptr(), need, _stream()),
+          "amv_flash_attn_decode")
+    return out

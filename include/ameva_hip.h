@@ -86,6 +86,57 @@ int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t k, const v
 int amv_mul_mat_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m,
                            int32_t* sums, void* stream);
 
+/* Q4_K / Q6_K weights from f32 rows (ggml blocks), with this library's own deterministic rule: ggml's
+ * make_qkx2_quants search (quantize_row_q4_K_ref / q6_K_ref) is not reproduced, so these weight bytes are not a
+ * parity target (parity is on the dot products of given bytes). Used for synthetic K-quant weights. */
+int amv_quantize_k(int type, const float* x, int64_t n_rows, int64_t k, void* y_ggml, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * BitNet I2_S. Replaces quantize_activation_int8 + bitnet_gemv / ggml_vec_dot_i2_i8_s
+ * (adapters/bitnet/src/cpu/llama_bitnet_core.cpp:914-941, ggml_bitnet_mad.cpp:191-231) and the GPU engine's
+ * bitnet_norm_q8.comp / bitnet_gemv_i2_s.comp (ac_bitnet_engine.cpp RecordNormQ8 268, RecordGemv 280).
+ * Activations: per row absmax int8, layout q int8 [m][k] | {f32 dequant, i32 sum q}[m] (amv_i2s_act_bytes).
+ * Weights: the BitNet I2_S tensor as stored (row r at r * k/4 bytes, 128-weight blocks of 32 bytes), k % 128 == 0;
+ * the per-tensor scale is the f32 that follows the n_rows * k/4 payload (amuda_gguf.c:659-681) and is passed in.
+ * dst[c * ldd + r] = float(sum_j (code_rj - 1) q_cj) * (dequant_c * weight_scale).
+ * ---------------------------------------------------------------------------------------------------------- */
+int64_t amv_i2s_act_bytes(int64_t m, int64_t k);
+int amv_i2s_quantize_act(const float* x, int64_t m, int64_t k, void* act, void* stream);
+int amv_i2s_gemv(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float weight_scale, float* dst,
+                 int64_t ldd, void* stream);
+/* the exact integers sum_j (code_rj - 1) q_cj, int32 [m][n_rows] (bit-exact contract) */
+int amv_i2s_gemv_sums(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, int32_t* sums,
+                      void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * RMS_NORM (ggml_compute_forward_rms_norm_f32; enc_rms_norm ggml-ameva.cpp:3941 with the fused MUL of
+ * ameva_find_fusion 4348-4357, ameva_rms_norm.comp): x f32 [n_rows][n]; y = x / sqrt(mean(x^2) + eps) (may be NULL),
+ * o = y * w (w f32 [n]; NULL for none), act (may be NULL): the Q8_0 activation layout of amv_quantize_act, of o when
+ * w is given and of y otherwise, quantized with `rule` -- the input of the next MUL_MAT in one pass.
+ * ---------------------------------------------------------------------------------------------------------- */
+int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y, float* o, void* act,
+                 int rule, void* stream);
+
+/* ROPE (ggml_rope_ext f32, enc_rope ggml-ameva.cpp:3965, ameva_rope.comp): x, y [n_tok][n_head][ne0] contiguous
+ * (in place allowed), pos int32 [n_tok]; mode 0 NORMAL or 2 NEOX; ext_factor 0, no frequency factors. */
+int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_tok, int64_t n_head, int64_t ne0, int n_dims,
+             int mode, float freq_base, float freq_scale, float attn_factor, void* stream);
+
+/* GLU SWIGLU (ggml_vec_swiglu_f32; enc_glu, ameva_glu.comp:45-46): y = silu(g) * u. */
+int amv_swiglu(const float* g, const float* u, float* y, int64_t n, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * FLASH_ATTN_EXT, decode (one query position), f16 K/V cache (enc_flash_attn ggml-ameva.cpp:4204-4284 with the key
+ * splits of ameva_fa_split_keys 4170-4195, ameva_flash_attn.comp + ameva_fa_combine.comp).
+ *   q f32 [n_head][D]; k, v f16 [n_head_kv][kv_stride][D] (ggml's cache view: rows of D halves, kv_stride rows per
+ *   head, the first n_kv used); mask f16 [n_kv] or NULL (added to the scaled scores); out f32 [n_head][D].
+ *   D = 128; n_head / n_head_kv in {1, 2, 4, 8}. workspace: amv_flash_attn_workspace_bytes() bytes of device memory.
+ * ---------------------------------------------------------------------------------------------------------- */
+int64_t amv_flash_attn_workspace_bytes(int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D);
+int amv_flash_attn_decode(const float* q, const void* k, const void* v, const void* mask, float* out, int64_t n_head,
+                          int64_t n_head_kv, int64_t n_kv, int64_t kv_stride, int64_t D, float scale, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,219 @@
+"""GPU parity of the K-quant GEMVs, BitNet I2_S, RMS_NORM (+MUL +Q8_0), ROPE, SWIGLU and FLASH_ATTN_EXT decode
+against the CPU oracle, through the C ABI.
+
+Bars: integer block sums and I2_S integer outputs bit-exact; Q8_0 bytes of the fused quantization bit-exact; f32
+outputs within 1e-3 relative L2 of the oracle; attention with the f16 KV cache within 2e-3.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_FA = 2e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from ameva_compute_amd import ops
+    return ops
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def gpu(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def random_kquant(rng, t, n, k):
+    """Random bytes are valid Q4_K / Q6_K blocks once the fp16 scales are small finite values."""
+    bb = 144 if t == 12 else 210
+    y = rng.integers(0, 256, (n, k // 256, bb), dtype=np.uint8)
+    def put(off):
+        v = rng.uniform(0.0, 0.002, (n, k // 256)).astype(np.float16)
+        y[:, :, off:off + 2] = v.view(np.uint8).reshape(n, k // 256, 2)
+    if t == 12:
+        put(0)
+        put(2)
+    else:
+        put(208)
+    return y.reshape(n, -1)
+
+
+KSHAPES = [(1, 256), (37, 512), (300, 2048), (4096, 4096), (14336, 4096), (4096, 14336)]
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("n,k", KSHAPES)
+def test_kquant_gemv_parity(dev, ops, orc, wtype, n, k):
+    rng = np.random.default_rng(n + k + wtype)
+    wg = random_kquant(rng, wtype, n, k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    a_ref = orc.quantize_q8_K(x)
+    y_ref, s_ref = orc.mul_mat(wtype, wg, n, k, a_ref, 1, with_blocks=True)
+    w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, k)
+    act, ag = ops.quantize_act(gpu(x, dev), ops.Q8_K, ggml=True)
+    assert np.array_equal(ag.cpu().numpy(), a_ref)
+    y = ops.mul_mat_q(w, act, 1).cpu().numpy()
+    sums = ops.block_sums(w, act, 1).cpu().numpy()
+    assert np.array_equal(sums, s_ref)
+    assert rel_l2(y, y_ref) < TOL_F32
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+def test_kquant_quantizer_valid_and_gemv(dev, ops, orc, wtype):
+    """The library's own K-quant rule yields valid blocks: the oracle's dequantization (pinned by known answers)
+    reproduces the input within the 4- / 6-bit error, and the GEMV on those bytes matches the oracle."""
+    rng = np.random.default_rng(3)
+    n, k = 512, 4096
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wg = ops.quantize_k(gpu(wf, dev), wtype).cpu().numpy()
+    deq = orc.dequantize(wtype, wg, k)
+    err = rel_l2(deq, wf)
+    assert err < (0.12 if wtype == 12 else 0.03), err
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    y_ref = orc.mul_mat(wtype, wg, n, k, orc.quantize_q8_K(x), 1)
+    y = ops.mul_mat(ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, k), gpu(x, dev)).cpu().numpy()
+    assert rel_l2(y, y_ref) < TOL_F32
+
+
+# ----------------------------------------------------------------------------------------------------- I2_S
+def pack_i2s(codes):
+    n, k = codes.shape
+    w = np.zeros((n, k // 4), np.uint8)
+    for b in range(k // 128):
+        for g in range(4):
+            w[:, 32 * b:32 * b + 32] |= (codes[:, 128 * b + 32 * g:128 * b + 32 * g + 32] << (6 - 2 * g)).astype(np.uint8)
+    return w
+
+
+@pytest.mark.parametrize("n,k,m", [(6912, 2560, 1), (2560, 6912, 1), (6912, 2560, 128), (3, 128, 2), (129, 256, 5)])
+def test_i2s_parity(dev, ops, orc, n, k, m):
+    rng = np.random.default_rng(n * 3 + k + m)
+    codes = rng.integers(0, 3, (n, k))
+    w = pack_i2s(codes)
+    scale = np.float32(1.37)
+    tensor = np.concatenate([w.reshape(-1), np.frombuffer(scale.tobytes(), np.uint8), np.zeros(28, np.uint8)])
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0, :7] = 0.0
+    q_ref, deq_ref = orc.i2s_quantize_act(x)
+    out_ref, sums_ref = orc.i2s_gemv(w, n, k, q_ref, deq_ref, float(scale))
+    tg = gpu(tensor, dev)
+    assert ops.i2s_tensor_scale(tg, n, k) == scale
+    act = ops.i2s_quantize_act(gpu(x, dev))
+    a = act.cpu().numpy()
+    assert np.array_equal(a[: m * k].view(np.int8).reshape(m, k), q_ref)
+    meta = a[m * k:].view(np.int32).reshape(m, 2)
+    assert np.array_equal(meta[:, 0].view(np.float32), deq_ref)
+    assert np.array_equal(meta[:, 1], q_ref.astype(np.int32).sum(axis=1))
+    sums = ops.i2s_gemv_sums(tg, n, k, act, m).cpu().numpy()
+    assert np.array_equal(sums, sums_ref.astype(np.int32))
+    out = ops.i2s_gemv(tg, n, k, act, m, float(scale)).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), out_ref.view(np.uint32))  # same f32 operations: bit-exact
+
+
+def test_i2s_on_reference_fixture(dev, ops, orc):
+    """The reference's upstream I2_S fixture (2 rows x 128, scale trailer 1.625) through the GPU GEMV: the integer
+    sums equal the dot of the fixture's independent expected f32 weights (divided by the scale) with q."""
+    import os
+    gold = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    data = np.fromfile(os.path.join(gold, "fixture_i2s_upstream.bin"), np.uint8)
+    expected = np.fromfile(os.path.join(gold, "expected_i2s_upstream_f32.bin"), np.float32).reshape(2, 128)
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((1, 128)).astype(np.float32)
+    tg = gpu(data, dev)
+    scale = ops.i2s_tensor_scale(tg, 2, 128)
+    assert scale == 1.625
+    act = ops.i2s_quantize_act(gpu(x, dev))
+    q = act.cpu().numpy()[:128].view(np.int8).astype(np.int64)
+    want = (expected.astype(np.float64) / scale) @ q
+    sums = ops.i2s_gemv_sums(tg, 2, 128, act, 1).cpu().numpy()[0]
+    assert np.array_equal(sums, want.astype(np.int64))
+
+
+# ---------------------------------------------------------------------------------------------- RMS_NORM
+@pytest.mark.parametrize("m,n", [(1, 4096), (7, 4096), (3, 14336), (2, 2560)])
+def test_rms_norm_fused(dev, ops, orc, m, n):
+    rng = np.random.default_rng(m * n)
+    x = (rng.standard_normal((m, n)) * 2).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    y_ref, o_ref = orc.rms_norm(x, 1e-5, w)
+    y, o, act = ops.rms_norm(gpu(x, dev), 1e-5, gpu(w, dev), quantize=True)
+    y, o, a = y.cpu().numpy(), o.cpu().numpy(), act.cpu().numpy()
+    assert rel_l2(y, y_ref) < 1e-6 and rel_l2(o, o_ref) < 1e-6
+    # the fused quantization equals ggml's quantize_row_q8_0 (x86 rule) of the GPU's own o, byte for byte
+    ref_blocks = orc.quantize_q8_0(o, orc.Q8_X86).reshape(m, n // 32, 34)
+    qs = a[: m * n].view(np.int8).reshape(m, n // 32, 32)
+    assert np.array_equal(qs, ref_blocks[:, :, 2:].view(np.int8))
+    meta = a[m * n:].view(np.int32).reshape(m, n // 32, 2)
+    d16 = orc.fp16_to_fp32(ref_blocks[:, :, 0].astype(np.uint16) | (ref_blocks[:, :, 1].astype(np.uint16) << 8))
+    assert np.array_equal(meta[:, :, 0].view(np.float32), d16)
+    y2 = ops.rms_norm(gpu(x, dev), 1e-5).cpu().numpy()
+    assert np.array_equal(y2, y)
+
+
+# ---------------------------------------------------------------------------------------------- ROPE
+@pytest.mark.parametrize("mode", [0, 2])
+@pytest.mark.parametrize("n_head,ne0,n_dims", [(32, 128, 128), (8, 128, 128), (4, 64, 32)])
+def test_rope(dev, ops, orc, mode, n_head, ne0, n_dims):
+    rng = np.random.default_rng(n_head + ne0 + mode)
+    pos = np.array([0, 1, 5, 511, 4095, 70000], np.int32)
+    x = rng.standard_normal((len(pos), n_head, ne0)).astype(np.float32)
+    y_ref = orc.rope(x, pos, n_dims, mode, 500000.0)
+    xg = gpu(x, dev)
+    y = ops.rope(xg, gpu(pos, dev), n_dims, mode, 500000.0).cpu().numpy()
+    assert rel_l2(y, y_ref) < 1e-5
+    assert np.array_equal(y[0], x[0])
+    ops.rope(xg, gpu(pos, dev), n_dims, mode, 500000.0, out=xg)  # in place
+    assert np.array_equal(xg.cpu().numpy(), y)
+
+
+def test_swiglu(dev, ops, orc):
+    rng = np.random.default_rng(12)
+    g = (rng.standard_normal(14336) * 5).astype(np.float32)
+    u = rng.standard_normal(14336).astype(np.float32)
+    y = ops.swiglu(gpu(g, dev), gpu(u, dev)).cpu().numpy()
+    assert rel_l2(y, orc.swiglu(g, u)) < 1e-6
+
+
+# ---------------------------------------------------------------------------------------------- FA decode
+@pytest.mark.parametrize("n_head,n_head_kv,n_kv,stride", [(32, 8, 4096, 4096), (32, 8, 1000, 4096), (8, 8, 17, 64),
+                                                          (16, 8, 300, 300), (8, 1, 1, 8), (32, 4, 2049, 2100)])
+def test_flash_attn_decode(dev, ops, orc, n_head, n_head_kv, n_kv, stride):
+    rng = np.random.default_rng(n_head * 31 + n_kv)
+    D = 128
+    q = rng.standard_normal((n_head, D)).astype(np.float32)
+    k = rng.standard_normal((n_head_kv, stride, D)).astype(np.float16)
+    v = rng.standard_normal((n_head_kv, stride, D)).astype(np.float16)
+    scale = 1.0 / np.sqrt(D)
+    ref = orc.flash_attn_decode(q, k[:, :n_kv].view(np.uint16), v[:, :n_kv].view(np.uint16), scale)
+    out = ops.flash_attn_decode(gpu(q, dev), gpu(k.view(np.uint16), dev).view(torch.float16),
+                                gpu(v.view(np.uint16), dev).view(torch.float16), scale, n_kv=n_kv).cpu().numpy()
+    assert rel_l2(out, ref) < TOL_FA
+
+
+def test_flash_attn_decode_mask(dev, ops, orc):
+    rng = np.random.default_rng(99)
+    n_head, n_head_kv, n_kv, D = 32, 8, 1024, 128
+    q = rng.standard_normal((n_head, D)).astype(np.float32)
+    k = rng.standard_normal((n_head_kv, n_kv, D)).astype(np.float16)
+    v = rng.standard_normal((n_head_kv, n_kv, D)).astype(np.float16)
+    mask = np.zeros(n_kv, np.float16)
+    mask[700:] = -np.inf          # padding of the cache: whole splits masked out
+    mask[::7] = -1.5
+    scale = 1.0 / np.sqrt(D)
+    ref = orc.flash_attn_decode(q, k.view(np.uint16), v.view(np.uint16), scale, mask.view(np.uint16))
+    out = ops.flash_attn_decode(gpu(q, dev), gpu(k, dev), gpu(v, dev), scale, mask=gpu(mask, dev)).cpu().numpy()
+    assert rel_l2(out, ref) < TOL_FA
