@@ -25,6 +25,8 @@ SIGNATURES = {
     "amv_mul_mat_vec": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
     "amv_mul_mat_block_sums": (I32, [I32, P, I64, I64, P, I64, P, P]),
     "amv_quantize_k": (I32, [I32, P, I64, I64, P, P]),
+    "amv_mul_mat_q": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
+    "amv_mul_mat_q_block_sums": (I32, [I32, P, I64, I64, P, I64, P, P]),
     "amv_i2s_act_bytes": (I64, [I64, I64]),
     "amv_i2s_quantize_act": (I32, [P, I64, I64, P, P]),
     "amv_i2s_gemv": (I32, [P, I64, I64, P, I64, F32, P, I64, P]),

@@ -103,13 +103,22 @@ def quantize_q4_0(x: torch.Tensor) -> torch.Tensor:
     return y
 
 
-def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    """dst [m, n_rows] f32 from already quantized activations (amv_quantize_act layout of m rows)."""
+# batch size from which MUL_MAT runs the int8-MFMA kernel (AMEVA_QGEMM_MIN_M of the reference, ggml-ameva.cpp:2486)
+MMQ_MIN_M = 8
+MMQ_TYPES = (Q4_0, Q8_0)
+
+
+def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = None,
+              kernel: str = "auto") -> torch.Tensor:
+    """dst [m, n_rows] f32 from already quantized activations (amv_quantize_act layout of m rows).
+    kernel: "auto" (the reference's routing: MFMA GEMM for m >= MMQ_MIN_M where the type has one), "mmv", "mmq"."""
     _need_gpu(act, "mul_mat_q")
     if out is None:
         out = torch.empty((m, w.n_rows), dtype=torch.float32, device=act.device)
-    check(lib().amv_mul_mat_vec(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(),
-                                w.n_rows, _stream()), "amv_mul_mat_vec")
+    use_mmq = kernel == "mmq" or (kernel == "auto" and m >= MMQ_MIN_M and w.type in MMQ_TYPES)
+    fn = lib().amv_mul_mat_q if use_mmq else lib().amv_mul_mat_vec
+    check(fn(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(), w.n_rows, _stream()),
+          "amv_mul_mat_q" if use_mmq else "amv_mul_mat_vec")
     return out
 
 
@@ -122,13 +131,14 @@ def mul_mat(w: QWeight, x: torch.Tensor, rule: int = Q8_X86) -> torch.Tensor:
     return mul_mat_q(w, act, x2.shape[0])
 
 
-def block_sums(w: QWeight, act: torch.Tensor, m: int) -> torch.Tensor:
-    """The exact per-block int32 sums of the GEMV kernels, [m, n_rows, nblk(*2 for Q4_K)]."""
+def block_sums(w: QWeight, act: torch.Tensor, m: int, kernel: str = "mmv") -> torch.Tensor:
+    """The exact per-block int32 sums of the GEMV ("mmv") or MFMA GEMM ("mmq") kernels, [m, n_rows, nblk(*2 Q4_K)]."""
     be = BLOCK[w.type][0]
     per = 2 if w.type == Q4_K else 1
     out = torch.empty((m, w.n_rows, w.k // be * per), dtype=torch.int32, device=act.device)
-    check(lib().amv_mul_mat_block_sums(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(),
-                                       _stream()), "amv_mul_mat_block_sums")
+    fn = lib().amv_mul_mat_q_block_sums if kernel == "mmq" else lib().amv_mul_mat_block_sums
+    check(fn(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(), _stream()),
+          "amv_mul_mat_block_sums")
     return out
 
 
