@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libameva_hip.so")
-SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_mmq.hip"]
+SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_mmq.hip", "amv_elem.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -50,7 +50,32 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     for o in objs:
         os.remove(o)
+    build_plugin()
     return LIB
+
+
+PLUGIN = os.path.join(HERE, "libggml-ameva.so")
+
+
+def build_plugin() -> str:
+    """libggml-ameva.so: the ggml backend plugin over libameva_hip.so. ggml_backend_buffer_init stays undefined and
+    binds to the host's libggml-base at load time."""
+    src = os.path.join(CSRC, "ggml_ameva.cpp")
+    tmp = PLUGIN + ".tmp"
+    commit = "unknown"
+    try:
+        commit = subprocess.run(["git", "-C", HERE, "rev-parse", "--short", "HEAD"], capture_output=True,
+                                text=True).stdout.strip() or "unknown"
+    except OSError:
+        pass
+    cmd = [HIPCC, *FLAGS, "-shared", f'-DAMEVA_BUILD_COMMIT="{commit}"', "-o", tmp, src, "-L" + HERE,
+           "-lameva_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed on ggml_ameva.cpp")
+    os.replace(tmp, PLUGIN)
+    return PLUGIN
 
 
 if __name__ == "__main__":

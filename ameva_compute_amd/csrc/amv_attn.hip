@@ -18,8 +18,9 @@
 template <int G>
 __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, const uint16_t* __restrict__ k,
                                                  const uint16_t* __restrict__ v, const uint16_t* __restrict__ mask,
-                                                 float* __restrict__ part, int n_kv, int64_t kv_stride,
-                                                 int split_len, int n_split, float scale) {
+                                                 float* __restrict__ part, int n_kv, int64_t k_row, int64_t k_head,
+                                                 int64_t v_row, int64_t v_head, int split_len, int n_split,
+                                                 float scale) {
     __shared__ float sS[G][FA_MAX_SPLIT];
     __shared__ float sRed[4][G][FA_D];
     __shared__ float sM[G], sL[G];
@@ -28,8 +29,8 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
     const int kb = split * split_len;
     const int ke = min(n_kv, kb + split_len);
     const int nk = ke - kb;  // >= 1
-    const uint16_t* kh = k + (size_t)hk * kv_stride * FA_D;
-    const uint16_t* vh = v + (size_t)hk * kv_stride * FA_D;
+    const uint16_t* kh = k + (size_t)hk * k_head;
+    const uint16_t* vh = v + (size_t)hk * v_head;
 
     // q of the G heads, 8 dims per lane (dims 8 * (lane & 15) + e), rounded to f16 as ggml does
     const int d8 = 8 * (lane & 15);
@@ -46,7 +47,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
     for (int base = 0; base < nk; base += 16) {
         const int kk = base + 4 * wv + (lane >> 4);
         const int kc = min(kk, nk - 1);
-        const uint4 kr = *reinterpret_cast<const uint4*>(kh + (size_t)(kb + kc) * FA_D + d8);
+        const uint4 kr = *reinterpret_cast<const uint4*>(kh + (size_t)(kb + kc) * k_row + d8);
         const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
         float kf[8];
 #pragma unroll
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.0f;
     for (int i = wv; i < nk; i += 4) {
-        const uint32_t vv = *reinterpret_cast<const uint32_t*>(vh + (size_t)(kb + i) * FA_D + 2 * lane);
+        const uint32_t vv = *reinterpret_cast<const uint32_t*>(vh + (size_t)(kb + i) * v_row + 2 * lane);
         const float v0 = amv_h2f(vv & 0xFFFFu), v1 = amv_h2f(vv >> 16);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -155,15 +156,19 @@ extern "C" int64_t amv_flash_attn_workspace_bytes(int64_t n_head, int64_t n_head
 }
 
 extern "C" int amv_flash_attn_decode(const float* q, const void* k, const void* v, const void* mask, float* out,
-                                     int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t kv_stride, int64_t D,
-                                     float scale, void* workspace, int64_t workspace_bytes, void* stream) {
+                                     int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row,
+                                     int64_t k_head, int64_t v_row, int64_t v_head, float scale, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
     AMV_REQUIRE(q && k && v && out && workspace, "amv_flash_attn_decode: null pointer");
     AMV_REQUIRE(D == FA_D, "amv_flash_attn_decode: head size %lld not supported (128 is)", (long long)D);
     AMV_REQUIRE(n_head > 0 && n_head_kv > 0 && n_head % n_head_kv == 0, "amv_flash_attn_decode: bad head counts");
     const int64_t G = n_head / n_head_kv;
     AMV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "amv_flash_attn_decode: GQA group %lld not supported", (long long)G);
-    AMV_REQUIRE(n_kv > 0 && kv_stride >= n_kv && n_kv <= INT32_MAX, "amv_flash_attn_decode: bad n_kv/kv_stride");
+    AMV_REQUIRE(n_kv > 0 && n_kv <= INT32_MAX, "amv_flash_attn_decode: bad n_kv");
     AMV_REQUIRE(n_head_kv <= 65535, "amv_flash_attn_decode: too many KV heads");
+    AMV_REQUIRE(k_row >= D && v_row >= D && k_row % 8 == 0 && v_row % 8 == 0 && k_head % 8 == 0 && v_head % 8 == 0 &&
+                    k_head >= 0 && v_head >= 0,
+                "amv_flash_attn_decode: K/V strides must be >= D and multiples of 8 elements");
     AMV_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 &&
                     ((uintptr_t)workspace & 15) == 0,
                 "amv_flash_attn_decode: buffers must be 16-byte aligned");
@@ -178,12 +183,16 @@ extern "C" int amv_flash_attn_decode(const float* q, const void* k, const void* 
     const uint16_t* kk = (const uint16_t*)k;
     const uint16_t* vv = (const uint16_t*)v;
     const uint16_t* mm = (const uint16_t*)mask;
+#define FA_LAUNCH(GG)                                                                                                   \
+    hipLaunchKernelGGL(k_fa_split<GG>, grid, dim3(256), 0, st, q, kk, vv, mm, part, (int)n_kv, k_row, k_head, v_row,  \
+                       v_head, sl, n_split, scale)
     switch (G) {
-    case 1: hipLaunchKernelGGL(k_fa_split<1>, grid, dim3(256), 0, st, q, kk, vv, mm, part, (int)n_kv, kv_stride, sl, n_split, scale); break;
-    case 2: hipLaunchKernelGGL(k_fa_split<2>, grid, dim3(256), 0, st, q, kk, vv, mm, part, (int)n_kv, kv_stride, sl, n_split, scale); break;
-    case 4: hipLaunchKernelGGL(k_fa_split<4>, grid, dim3(256), 0, st, q, kk, vv, mm, part, (int)n_kv, kv_stride, sl, n_split, scale); break;
-    default: hipLaunchKernelGGL(k_fa_split<8>, grid, dim3(256), 0, st, q, kk, vv, mm, part, (int)n_kv, kv_stride, sl, n_split, scale); break;
+    case 1: FA_LAUNCH(1); break;
+    case 2: FA_LAUNCH(2); break;
+    case 4: FA_LAUNCH(4); break;
+    default: FA_LAUNCH(8); break;
     }
+#undef FA_LAUNCH
     hipLaunchKernelGGL(k_fa_combine, dim3((unsigned)n_head), dim3(FA_D), 0, st, part, out, n_split);
     return amv_check_launch("amv_flash_attn_decode");
 }

@@ -1,0 +1,876 @@
+// ggml backend plugin "AMEVA" on MI355X: registry, device AMEVA0, buffer type and buffers (with the MI355X weight
+// layout), and the graph engine that runs a ggml graph on one in-order HIP stream through the kernel ABI of
+// include/ameva_hip.h.
+//
+// Behaviour follows the reference plugin (adapters/llama/ggml-ameva/):
+//   * one process-wide device; graph_compute is serialised by a mutex and returns after completion (synchronize NULL);
+//   * contract first: every node of the graph goes through op_unsupported_reason before anything runs, and one
+//     unsupported node fails the whole graph with a "(FAIL-FAST)" line (ggml-ameva.cpp:5330-5343); supports_op uses
+//     the same function, so the scheduler never hands the backend a node it would reject; no CPU fallback;
+//   * quantized weights live in the MI355X layout (amv_repack), converted when a MUL_MAT first reads them (the lazy
+//     repack of ggml-ameva.cpp:5352-5373) and converted back by get_tensor, so other backends see ggml bytes;
+//   * MUL_MAT routes like enc_mul_mat (3607): int8-MFMA GEMM from 8 columns for Q4_0 / Q8_0, GEMV otherwise; the
+//     quantized activations of one src1 are reused by every MUL_MAT that reads it (the a8_src cache, 2738-2749);
+//   * RMS_NORM followed by a MUL by the norm weight runs as one kernel (ameva_find_fusion, 4345);
+//   * counters and failure injection as ggml-ameva.h:30-98.
+// On MI355X the Vulkan hazard tracking of the reference (ameva_record, 2174) is the in-order stream itself: each
+// kernel starts after the previous one has finished, so no barrier bookkeeping is needed.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/ameva_hip.h"
+#include "../../include/ggml-ameva.h"
+#include "ggml_abi.h"
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------ counters
+struct Counters {
+    std::atomic<int64_t> supports_query{0}, supported_op{0}, gpu_op{0}, mul_mat{0}, qmv{0}, mmq{0};
+    std::atomic<int64_t> ctx_create{0}, ctx_destroy{0}, buf_create{0}, buf_destroy{0};
+    std::atomic<int64_t> repacked_tensors{0}, repacked_bytes{0}, fused{0}, act_reuse{0};
+};
+Counters g_cnt;
+std::atomic<int> g_fail{AMEVA_FAIL_NONE};
+
+void log_line(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::fprintf(stderr, "ggml-ameva: ");
+    std::vfprintf(stderr, fmt, ap);
+    std::fprintf(stderr, "\n");
+    va_end(ap);
+}
+
+// ------------------------------------------------------------------------------------------------ ggml sizes
+int64_t blck_size(int t) {
+    switch (t) {
+    case GGML_TYPE_Q4_0:
+    case GGML_TYPE_Q8_0: return 32;
+    case GGML_TYPE_Q4_K:
+    case GGML_TYPE_Q6_K:
+    case GGML_TYPE_Q8_K: return 256;
+    default: return 1;
+    }
+}
+int64_t type_size(int t) {
+    switch (t) {
+    case GGML_TYPE_F32: return 4;
+    case GGML_TYPE_F16: return 2;
+    case GGML_TYPE_BF16: return 2;
+    case GGML_TYPE_Q4_0: return 18;
+    case GGML_TYPE_Q8_0: return 34;
+    case GGML_TYPE_Q4_K: return 144;
+    case GGML_TYPE_Q6_K: return 210;
+    case GGML_TYPE_Q8_K: return 292;
+    case GGML_TYPE_I8: return 1;
+    case GGML_TYPE_I16: return 2;
+    case GGML_TYPE_I32: return 4;
+    case GGML_TYPE_I64: return 8;
+    default: return 0;
+    }
+}
+// ggml_nbytes
+size_t nbytes(const ggml_tensor* t) {
+    const int64_t bs = blck_size(t->type);
+    size_t n;
+    if (bs == 1) {
+        n = (size_t)type_size(t->type);
+        for (int i = 0; i < GGML_MAX_DIMS; ++i) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    } else {
+        n = (size_t)(t->ne[0] * (int64_t)t->nb[0] / bs);
+        for (int i = 1; i < GGML_MAX_DIMS; ++i) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    }
+    return n;
+}
+int64_t nelements(const ggml_tensor* t) { return t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]; }
+int64_t nrows(const ggml_tensor* t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
+bool is_contiguous(const ggml_tensor* t) {
+    const int64_t ts = type_size(t->type), bs = blck_size(t->type);
+    if (ts == 0) return false;
+    size_t next = (size_t)ts;
+    if ((int64_t)t->nb[0] != ts) return false;
+    next = (size_t)(ts * (t->ne[0] / bs));
+    for (int i = 1; i < GGML_MAX_DIMS; ++i) {
+        if (t->ne[i] != 1 && t->nb[i] != next) return false;
+        next *= (size_t)t->ne[i];
+    }
+    return true;
+}
+float op_f32(const ggml_tensor* t, int i) {
+    float f;
+    std::memcpy(&f, &t->op_params[i], 4);
+    return f;
+}
+bool quant_weight_type(int t) {
+    return t == GGML_TYPE_Q4_0 || t == GGML_TYPE_Q8_0 || t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K;
+}
+bool noop(int op) {
+    return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
+           op == GGML_OP_TRANSPOSE;
+}
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// ------------------------------------------------------------------------------------------------ device state
+struct Device;
+Device* device();
+
+// per buffer: device memory and the layout state of the quantized weights it holds
+struct BufCtx {
+    void* dev = nullptr;
+    size_t size = 0;
+    std::mutex mu;
+    std::unordered_map<const void*, int> repacked;  // tensor data -> ggml type, for tensors in the MI355X layout
+};
+
+const char* buft_get_name(ggml_backend_buffer_type_t) { return GGML_AMEVA_DEVICE_NAME; }
+ggml_backend_buffer_t buft_alloc_buffer(ggml_backend_buffer_type_t buft, size_t size);
+size_t buft_get_alignment(ggml_backend_buffer_type_t) { return 256; }
+size_t buft_get_max_size(ggml_backend_buffer_type_t) { return (size_t)64 << 30; }
+size_t buft_get_alloc_size(ggml_backend_buffer_type_t, const ggml_tensor* t) { return nbytes(t); }
+bool buft_is_host(ggml_backend_buffer_type_t) { return false; }
+
+struct ggml_backend_buffer_type g_buft = {
+    {buft_get_name, buft_alloc_buffer, buft_get_alignment, buft_get_max_size, buft_get_alloc_size, buft_is_host},
+    nullptr,
+    nullptr};
+
+bool is_ours(const ggml_tensor* t) { return t && t->buffer && t->buffer->buft == &g_buft; }
+
+// device-side scratch of a graph (activation quantization, attention partials, status word); grows, never shrinks
+struct Arena {
+    uint8_t* base = nullptr;
+    size_t cap = 0, used = 0;
+    bool reserve(size_t need) {
+        if (need <= cap) return true;
+        if (base) (void)hipFree(base);
+        base = nullptr;
+        cap = 0;
+        size_t c = need + need / 2 + (1 << 20);
+        if (hipMalloc(&base, c) != hipSuccess) return false;
+        cap = c;
+        return true;
+    }
+    void* take(size_t n) {
+        const size_t off = (used + 255) & ~(size_t)255;
+        if (off + n > cap) return nullptr;
+        used = off + n;
+        return base + off;
+    }
+};
+
+struct Device {
+    std::mutex compute_mu;
+    hipStream_t stream = nullptr;
+    Arena arena;
+    unsigned int* status = nullptr;  // bad-index counter of SET_ROWS / GET_ROWS
+    bool inited = false;
+    bool init() {
+        if (inited) return true;
+        if (hipSetDevice(0) != hipSuccess) return false;
+        if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess) return false;
+        if (hipMalloc(&status, 256) != hipSuccess) return false;
+        inited = true;
+        g_cnt.ctx_create++;
+        return true;
+    }
+};
+
+Device* device() {
+    static Device d;
+    return &d;
+}
+
+// ------------------------------------------------------------------------------------------------ buffers
+void buf_free(ggml_backend_buffer_t b) {
+    BufCtx* c = (BufCtx*)b->context;
+    if (c) {
+        std::lock_guard<std::mutex> lk(c->mu);
+        for (auto& kv : c->repacked) {
+            (void)kv;
+            g_cnt.repacked_tensors--;
+        }
+        (void)hipFree(c->dev);
+        delete c;
+    }
+    g_cnt.buf_destroy++;
+}
+void* buf_get_base(ggml_backend_buffer_t b) { return ((BufCtx*)b->context)->dev; }
+void buf_memset(ggml_backend_buffer_t, ggml_tensor* t, uint8_t v, size_t off, size_t size) {
+    (void)hipMemset((uint8_t*)t->data + off, v, size);
+}
+
+// converts a quantized tensor between ggml blocks and the MI355X layout in place (through a temporary copy)
+bool convert_in_place(ggml_tensor* t, bool to_repacked) {
+    const size_t n = nbytes(t);
+    void* tmp = nullptr;
+    if (hipMalloc(&tmp, n) != hipSuccess) return false;
+    bool ok = hipMemcpy(tmp, t->data, n, hipMemcpyDeviceToDevice) == hipSuccess;
+    if (ok) {
+        const int rc = to_repacked ? amv_repack(t->type, tmp, t->data, t->ne[1], t->ne[0], nullptr)
+                                   : amv_unrepack(t->type, tmp, t->data, t->ne[1], t->ne[0], nullptr);
+        ok = rc == AMV_OK && hipDeviceSynchronize() == hipSuccess;
+        if (rc != AMV_OK) log_line("repack of %s failed: %s", t->name, amv_last_error());
+    }
+    (void)hipFree(tmp);
+    return ok;
+}
+
+bool repackable(const ggml_tensor* t) {
+    return quant_weight_type(t->type) && t->ne[2] == 1 && t->ne[3] == 1 && is_contiguous(t) && t->view_src == nullptr &&
+           t->ne[0] % blck_size(t->type) == 0 && aligned16(t->data);
+}
+
+// returns the tensor to ggml layout if it is held repacked (before a partial write or a raw read)
+bool ensure_raw(BufCtx* c, ggml_tensor* t) {
+    auto it = c->repacked.find(t->data);
+    if (it == c->repacked.end()) return true;
+    if (!convert_in_place(t, false)) return false;
+    c->repacked.erase(it);
+    g_cnt.repacked_tensors--;
+    g_cnt.repacked_bytes -= (int64_t)nbytes(t);
+    return true;
+}
+
+void buf_set_tensor(ggml_backend_buffer_t b, ggml_tensor* t, const void* data, size_t off, size_t size) {
+    BufCtx* c = (BufCtx*)b->context;
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (!ensure_raw(c, t)) log_line("set_tensor %s: could not restore the ggml layout (FAIL-FAST)", t->name);
+    if (hipMemcpy((uint8_t*)t->data + off, data, size, hipMemcpyHostToDevice) != hipSuccess)
+        log_line("set_tensor %s: copy failed", t->name);
+}
+
+void buf_get_tensor(ggml_backend_buffer_t b, const ggml_tensor* t, void* data, size_t off, size_t size) {
+    BufCtx* c = (BufCtx*)b->context;
+    std::lock_guard<std::mutex> lk(c->mu);
+    auto it = c->repacked.find(t->data);
+    if (it == c->repacked.end()) {
+        (void)hipMemcpy(data, (const uint8_t*)t->data + off, size, hipMemcpyDeviceToHost);
+        return;
+    }
+    // a repacked weight is read in ggml layout: convert a copy
+    const size_t n = nbytes(t);
+    void* tmp = nullptr;
+    if (hipMalloc(&tmp, n) != hipSuccess) {
+        log_line("get_tensor %s: no memory for the layout conversion", t->name);
+        return;
+    }
+    if (amv_unrepack(t->type, t->data, tmp, t->ne[1], t->ne[0], nullptr) == AMV_OK)
+        (void)hipMemcpy(data, (const uint8_t*)tmp + off, size, hipMemcpyDeviceToHost);
+    (void)hipFree(tmp);
+}
+
+bool buf_cpy_tensor(ggml_backend_buffer_t b, const ggml_tensor* src, ggml_tensor* dst) {
+    if (!is_ours(src)) return false;
+    BufCtx* c = (BufCtx*)b->context;
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (!ensure_raw(c, dst)) return false;
+    BufCtx* cs = (BufCtx*)src->buffer->context;
+    if (cs != c) {
+        std::lock_guard<std::mutex> lk2(cs->mu);
+        if (!ensure_raw(cs, const_cast<ggml_tensor*>(src))) return false;
+    } else if (!ensure_raw(c, const_cast<ggml_tensor*>(src))) {
+        return false;
+    }
+    return hipMemcpy(dst->data, src->data, nbytes(src), hipMemcpyDeviceToDevice) == hipSuccess;
+}
+
+void buf_clear(ggml_backend_buffer_t b, uint8_t v) {
+    BufCtx* c = (BufCtx*)b->context;
+    std::lock_guard<std::mutex> lk(c->mu);
+    g_cnt.repacked_tensors -= (int64_t)c->repacked.size();
+    c->repacked.clear();
+    (void)hipMemset(c->dev, v, c->size);
+}
+
+const ggml_backend_buffer_i g_buf_iface = {
+    buf_free, buf_get_base, nullptr, buf_memset, buf_set_tensor, buf_get_tensor, nullptr, nullptr, buf_cpy_tensor,
+    buf_clear, nullptr};
+
+ggml_backend_buffer_t buft_alloc_buffer(ggml_backend_buffer_type_t buft, size_t size) {
+    if (!device()->init()) {
+        log_line("no HIP device (FAIL-FAST)");
+        return nullptr;
+    }
+    BufCtx* c = new BufCtx;
+    c->size = size;
+    if (hipMalloc(&c->dev, size ? size : 256) != hipSuccess) {
+        log_line("alloc_buffer: hipMalloc of %zu bytes failed", size);
+        delete c;
+        return nullptr;
+    }
+    g_cnt.buf_create++;
+    return ggml_backend_buffer_init(buft, g_buf_iface, c, size);
+}
+
+// ------------------------------------------------------------------------------------------------ the contract
+const char* unsupported_reason(const ggml_tensor* n) {
+    if (g_fail.load() == AMEVA_FAIL_TENSOR_RANGE_OOB) return "failure injection: tensor range out of bounds";
+    if (noop(n->op)) return nullptr;
+    if (!is_ours(n)) return "destination is not in an AMEVA buffer";
+    for (int i = 0; i < GGML_MAX_SRC && n->src[i]; ++i)
+        if (!is_ours(n->src[i])) return "a source is not in an AMEVA buffer";
+    const ggml_tensor* s0 = n->src[0];
+    const ggml_tensor* s1 = n->src[1];
+    switch (n->op) {
+    case GGML_OP_MUL_MAT: {
+        if (!quant_weight_type(s0->type)) return "MUL_MAT src0 type is not Q4_0, Q8_0, Q4_K or Q6_K";
+        if (s0->ne[2] != 1 || s0->ne[3] != 1) return "MUL_MAT src0 must be a 2-D weight";
+        if (!is_contiguous(s0) || s0->view_src) return "MUL_MAT src0 must be a whole contiguous tensor";
+        if (!aligned16(s0->data)) return "MUL_MAT src0 must be 16-byte aligned";
+        if (s1->type != GGML_TYPE_F32 || !is_contiguous(s1)) return "MUL_MAT src1 must be contiguous F32";
+        if (s1->ne[0] != s0->ne[0]) return "MUL_MAT inner dimensions differ";
+        if (n->type != GGML_TYPE_F32 || !is_contiguous(n)) return "MUL_MAT dst must be contiguous F32";
+        if (s0->ne[0] % blck_size(s0->type) != 0) return "MUL_MAT row is not whole blocks";
+        return nullptr;
+    }
+    case GGML_OP_RMS_NORM:
+        if (s0->type != GGML_TYPE_F32 || n->type != GGML_TYPE_F32) return "RMS_NORM is F32 only";
+        if (!is_contiguous(s0) || !is_contiguous(n)) return "RMS_NORM needs contiguous rows";
+        if (s0->ne[0] % 4 != 0 || !aligned16(s0->data) || !aligned16(n->data)) return "RMS_NORM rows must be 16-byte units";
+        return nullptr;
+    case GGML_OP_ADD:
+    case GGML_OP_MUL: {
+        if (s0->type != GGML_TYPE_F32 || s1->type != GGML_TYPE_F32 || n->type != GGML_TYPE_F32) return "binary op is F32 only";
+        if (!is_contiguous(s0) || !is_contiguous(s1) || !is_contiguous(n)) return "binary op needs contiguous tensors";
+        if (s1->ne[0] != s0->ne[0]) return "binary op broadcast along dim 0 is not supported";
+        const bool same = s1->ne[1] == s0->ne[1] && s1->ne[2] == s0->ne[2] && s1->ne[3] == s0->ne[3];
+        const bool one_row = nrows(s1) == 1;
+        const bool rows_only = s1->ne[1] == s0->ne[1] && s1->ne[2] == 1 && s1->ne[3] == 1;
+        if (!same && !one_row && !rows_only) return "binary op broadcast pattern not supported";
+        return nullptr;
+    }
+    case GGML_OP_ROPE: {
+        const int mode = n->op_params[2];
+        if (s0->type != GGML_TYPE_F32 || n->type != GGML_TYPE_F32) return "ROPE is F32 only";
+        if (!is_contiguous(s0) || !is_contiguous(n)) return "ROPE needs contiguous tensors";
+        if (mode != 0 && mode != 2) return "ROPE mode must be NORMAL or NEOX";
+        if (n->src[2]) return "ROPE frequency factors not supported";
+        if (op_f32(n, 7) != 0.0f) return "ROPE YaRN ext_factor != 0 not supported";
+        if (s1->type != GGML_TYPE_I32 || s1->ne[0] != s0->ne[2]) return "ROPE positions must be I32 per token";
+        if (s0->ne[3] != 1) return "ROPE ne[3] must be 1";
+        if (n->op_params[1] <= 0 || n->op_params[1] > s0->ne[0] || n->op_params[1] % 2) return "ROPE n_dims invalid";
+        return nullptr;
+    }
+    case GGML_OP_FLASH_ATTN_EXT: {
+        const ggml_tensor *q = s0, *k = s1, *v = n->src[2], *m = n->src[3];
+        if (n->src[4]) return "FLASH_ATTN_EXT sinks not supported";
+        if (q->type != GGML_TYPE_F32 || k->type != GGML_TYPE_F16 || v->type != GGML_TYPE_F16)
+            return "FLASH_ATTN_EXT needs F32 q and an F16 K/V cache";
+        if (q->ne[0] != 128 || v->ne[0] != 128) return "FLASH_ATTN_EXT head size must be 128";
+        if (q->ne[1] != 1 || q->ne[3] != 1 || k->ne[3] != 1) return "FLASH_ATTN_EXT decode (one query) only";
+        if (q->nb[0] != 4 || q->nb[2] != 128 * 4 || !aligned16(q->data)) return "FLASH_ATTN_EXT q heads must be contiguous";
+        if (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 || v->nb[2] % 16)
+            return "FLASH_ATTN_EXT K/V rows must be 16-byte aligned";
+        if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2]) return "FLASH_ATTN_EXT K/V shapes differ";
+        const int64_t G = q->ne[2] / k->ne[2];
+        if (q->ne[2] % k->ne[2] || (G != 1 && G != 2 && G != 4 && G != 8)) return "FLASH_ATTN_EXT GQA group not 1/2/4/8";
+        if (op_f32(n, 1) != 0.0f || op_f32(n, 2) != 0.0f) return "FLASH_ATTN_EXT ALiBi / softcap not supported";
+        if (m && (m->type != GGML_TYPE_F16 || m->ne[0] < k->ne[1] || m->nb[0] != 2 || m->ne[2] != 1))
+            return "FLASH_ATTN_EXT mask must be F16 [n_kv, ...] shared by all heads";
+        if (n->type != GGML_TYPE_F32 || !is_contiguous(n)) return "FLASH_ATTN_EXT dst must be contiguous F32";
+        return nullptr;
+    }
+    case GGML_OP_GLU: {
+        if (n->op_params[0] != GGML_GLU_OP_SWIGLU) return "GLU op other than SWIGLU";
+        if (!s1) {
+            if (nrows(s0) != 1) return "GLU single-tensor form only for one row";
+        } else if (s1->type != GGML_TYPE_F32 || !is_contiguous(s1) || nelements(s1) != nelements(s0)) {
+            return "GLU src1 must match src0";
+        }
+        if (s0->type != GGML_TYPE_F32 || !is_contiguous(s0) || n->type != GGML_TYPE_F32 || !is_contiguous(n))
+            return "GLU is contiguous F32 only";
+        return nullptr;
+    }
+    case GGML_OP_SET_ROWS:
+        if (s0->type != GGML_TYPE_F32 || n->type != GGML_TYPE_F16) return "SET_ROWS F32 -> F16 only";
+        if (s1->type != GGML_TYPE_I64 && s1->type != GGML_TYPE_I32) return "SET_ROWS index must be I32 or I64";
+        if (s0->ne[2] != 1 || s0->ne[3] != 1 || n->ne[2] != 1 || n->ne[3] != 1) return "SET_ROWS 2-D only";
+        if (s0->nb[0] != 4 || n->nb[0] != 2 || s1->nb[0] != (size_t)type_size(s1->type)) return "SET_ROWS rows must be dense";
+        if (s0->ne[0] != n->ne[0] || s1->ne[0] != s0->ne[1]) return "SET_ROWS shapes differ";
+        return nullptr;
+    case GGML_OP_CPY:
+    case GGML_OP_CONT:
+        if (s0->type != GGML_TYPE_F32 || (n->type != GGML_TYPE_F32 && n->type != GGML_TYPE_F16)) return "CPY F32 -> F32/F16 only";
+        if (!is_contiguous(s0) || !is_contiguous(n) || nelements(s0) != nelements(n)) return "CPY needs contiguous tensors";
+        return nullptr;
+    case GGML_OP_GET_ROWS:
+        if (s0->type != GGML_TYPE_F32 && s0->type != GGML_TYPE_F16 && s0->type != GGML_TYPE_Q4_0 &&
+            s0->type != GGML_TYPE_Q8_0)
+            return "GET_ROWS source type not supported";
+        if (s1->type != GGML_TYPE_I32 || s0->ne[2] != 1 || s0->ne[3] != 1 || !is_contiguous(s0) || !is_contiguous(s1))
+            return "GET_ROWS needs a 2-D source and I32 indices";
+        if (n->type != GGML_TYPE_F32 || !is_contiguous(n)) return "GET_ROWS dst must be F32";
+        return nullptr;
+    default: return "op not implemented on AMEVA";
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ graph engine
+struct ActEntry {
+    const void* data;
+    size_t bytes;
+    int atype;
+    void* act;
+};
+
+struct Engine {
+    Device* dev;
+    hipStream_t st;
+    std::vector<ActEntry> acts;  // quantized activations valid at this point of the graph
+    bool failed = false;
+    std::string why;
+
+    bool fail(const ggml_tensor* n, const char* what) {
+        failed = true;
+        char buf[512];
+        std::snprintf(buf, sizeof(buf), "node %s (op %d): %s", n ? n->name : "?", n ? (int)n->op : -1, what);
+        why = buf;
+        return false;
+    }
+    bool rc(const ggml_tensor* n, int r) { return r == AMV_OK ? true : fail(n, amv_last_error()); }
+
+    // a node's output overwrites memory that cached activations were quantized from
+    void invalidate(const ggml_tensor* n) {
+        const uint8_t* lo = (const uint8_t*)n->data;
+        const uint8_t* hi = lo + nbytes(n);
+        for (size_t i = 0; i < acts.size();) {
+            const uint8_t* a = (const uint8_t*)acts[i].data;
+            if (a < hi && lo < a + acts[i].bytes) acts.erase(acts.begin() + i);
+            else ++i;
+        }
+    }
+
+    void* act_for(const ggml_tensor* n, const ggml_tensor* x, int atype, int64_t m, int64_t k) {
+        for (auto& e : acts)
+            if (e.data == x->data && e.atype == atype && e.bytes == nbytes(x)) {
+                g_cnt.act_reuse++;
+                return e.act;
+            }
+        void* act = dev->arena.take((size_t)amv_act_bytes(atype, m, k));
+        if (!act) {
+            fail(n, "scratch exhausted");
+            return nullptr;
+        }
+        if (amv_quantize_act(atype, (const float*)x->data, m, k, AMV_Q8_X86, nullptr, act, st) != AMV_OK) {
+            fail(n, amv_last_error());
+            return nullptr;
+        }
+        acts.push_back({x->data, nbytes(x), atype, act});
+        return act;
+    }
+
+    bool mul_mat(const ggml_tensor* n) {
+        const ggml_tensor *w = n->src[0], *x = n->src[1];
+        const int64_t N = w->ne[1], K = w->ne[0], M = nrows(x);
+        const int atype = (w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K) ? GGML_TYPE_Q8_K : GGML_TYPE_Q8_0;
+        // src0 in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized tensor of any
+        // other buffer is repacked into scratch for this use
+        const void* wp = w->data;
+        BufCtx* bc = (BufCtx*)w->buffer->context;
+        {
+            std::lock_guard<std::mutex> lk(bc->mu);
+            if (!bc->repacked.count(w->data)) {
+                if (w->buffer->usage == GGML_BACKEND_BUFFER_USAGE_WEIGHTS && repackable(w)) {
+                    if (!convert_in_place(const_cast<ggml_tensor*>(w), true)) return fail(n, "weight repack failed");
+                    bc->repacked[w->data] = w->type;
+                    g_cnt.repacked_tensors++;
+                    g_cnt.repacked_bytes += (int64_t)nbytes(w);
+                } else {
+                    void* tmp = dev->arena.take(nbytes(w));
+                    if (!tmp) return fail(n, "scratch exhausted");
+                    if (!rc(n, amv_repack(w->type, w->data, tmp, N, K, st))) return false;
+                    wp = tmp;
+                }
+            }
+        }
+        if (g_fail.load() == AMEVA_FAIL_MAP_SRC1) return fail(n, "failure injection: src1");
+        void* act = act_for(n, x, atype, M, K);
+        if (!act) return false;
+        if (g_fail.load() == AMEVA_FAIL_DISPATCH) return fail(n, "failure injection: dispatch");
+        const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0);
+        const int r = mmq ? amv_mul_mat_q(w->type, wp, N, K, act, M, (float*)n->data, N, st)
+                          : amv_mul_mat_vec(w->type, wp, N, K, act, M, (float*)n->data, N, st);
+        if (!rc(n, r)) return false;
+        g_cnt.mul_mat++;
+        g_cnt.qmv++;
+        if (mmq) g_cnt.mmq++;
+        return true;
+    }
+
+    bool binary(const ggml_tensor* n, int op) {
+        const ggml_tensor *a = n->src[0], *b = n->src[1];
+        return rc(n, amv_binary(op, (const float*)a->data, (const float*)b->data, (float*)n->data, nrows(a), a->ne[0],
+                                nrows(b), st));
+    }
+
+    bool rms_norm(const ggml_tensor* n, const ggml_tensor* mul) {
+        const ggml_tensor* x = n->src[0];
+        const float eps = op_f32(n, 0);
+        if (!mul) return rc(n, amv_rms_norm((const float*)x->data, nrows(x), x->ne[0], eps, nullptr, (float*)n->data,
+                                            nullptr, nullptr, AMV_Q8_X86, st));
+        const ggml_tensor* w = mul->src[0] == n ? mul->src[1] : mul->src[0];
+        return rc(n, amv_rms_norm((const float*)x->data, nrows(x), x->ne[0], eps, (const float*)w->data,
+                                  (float*)n->data, (float*)mul->data, nullptr, AMV_Q8_X86, st));
+    }
+
+    bool rope(const ggml_tensor* n) {
+        const ggml_tensor *x = n->src[0], *pos = n->src[1];
+        return rc(n, amv_rope((const float*)x->data, (float*)n->data, (const int32_t*)pos->data, x->ne[2], x->ne[1],
+                              x->ne[0], n->op_params[1], n->op_params[2], op_f32(n, 5), op_f32(n, 6), op_f32(n, 8), st));
+    }
+
+    bool flash_attn(const ggml_tensor* n) {
+        const ggml_tensor *q = n->src[0], *k = n->src[1], *v = n->src[2], *m = n->src[3];
+        const int64_t n_head = q->ne[2], n_head_kv = k->ne[2], n_kv = k->ne[1], D = q->ne[0];
+        const int64_t ws = amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv, D);
+        void* work = dev->arena.take((size_t)ws);
+        if (!work) return fail(n, "scratch exhausted");
+        return rc(n, amv_flash_attn_decode((const float*)q->data, k->data, v->data, m ? m->data : nullptr,
+                                           (float*)n->data, n_head, n_head_kv, n_kv, D, (int64_t)k->nb[1] / 2,
+                                           (int64_t)k->nb[2] / 2, (int64_t)v->nb[1] / 2, (int64_t)v->nb[2] / 2,
+                                           op_f32(n, 0), work, ws, st));
+    }
+
+    bool glu(const ggml_tensor* n) {
+        const ggml_tensor *a = n->src[0], *b = n->src[1];
+        const bool swapped = n->op_params[1] != 0;
+        if (b) {
+            const ggml_tensor* g = swapped ? b : a;
+            const ggml_tensor* u = swapped ? a : b;
+            return rc(n, amv_swiglu((const float*)g->data, (const float*)u->data, (float*)n->data, nelements(n), st));
+        }
+        const int64_t h = a->ne[0] / 2;
+        const float* g = (const float*)a->data + (swapped ? h : 0);
+        const float* u = (const float*)a->data + (swapped ? 0 : h);
+        return rc(n, amv_swiglu(g, u, (float*)n->data, h, st));
+    }
+
+    bool set_rows(const ggml_tensor* n) {
+        const ggml_tensor *src = n->src[0], *idx = n->src[1];
+        return rc(n, amv_set_rows_f16((const float*)src->data, (int64_t)src->nb[1] / 4, n->data, (int64_t)n->nb[1] / 2,
+                                      src->ne[1], src->ne[0], idx->data, idx->type == GGML_TYPE_I64 ? 64 : 32, n->ne[1],
+                                      dev->status, st));
+    }
+
+    bool cpy(const ggml_tensor* n) {
+        const ggml_tensor* src = n->src[0];
+        if (n->type == GGML_TYPE_F32)
+            return hipMemcpyAsync(n->data, src->data, nbytes(src), hipMemcpyDeviceToDevice, st) == hipSuccess
+                       ? true
+                       : fail(n, "copy failed");
+        return rc(n, amv_set_rows_f16((const float*)src->data, nelements(src), n->data, nelements(src), 1,
+                                      nelements(src), nullptr, 0, 1, nullptr, st));
+    }
+
+    bool get_rows(const ggml_tensor* n) {
+        const ggml_tensor *src = n->src[0], *idx = n->src[1];
+        const void* sp = src->data;
+        BufCtx* bc = (BufCtx*)src->buffer->context;
+        {
+            std::lock_guard<std::mutex> lk(bc->mu);
+            if (bc->repacked.count(src->data)) {  // a weight also used by MUL_MAT: read a ggml-layout copy
+                void* tmp = dev->arena.take(nbytes(src));
+                if (!tmp) return fail(n, "scratch exhausted");
+                if (!rc(n, amv_unrepack(src->type, src->data, tmp, src->ne[1], src->ne[0], st))) return false;
+                sp = tmp;
+            }
+        }
+        return rc(n, amv_get_rows(src->type, sp, src->ne[1], src->ne[0], (const int32_t*)idx->data, nelements(idx),
+                                  (float*)n->data, dev->status, st));
+    }
+
+    // scratch a graph can need at most (activation buffers, attention partials, layout copies)
+    static size_t scratch_bound(const ggml_cgraph* g) {
+        size_t s = 1 << 20;
+        for (int i = 0; i < g->n_nodes; ++i) {
+            const ggml_tensor* n = g->nodes[i];
+            if (n->op == GGML_OP_MUL_MAT) {
+                s += (size_t)amv_act_bytes(GGML_TYPE_Q8_0, nrows(n->src[1]), n->src[1]->ne[0]) + 4096;
+                s += (size_t)amv_act_bytes(GGML_TYPE_Q8_K, nrows(n->src[1]), (n->src[1]->ne[0] + 255) / 256 * 256) + 4096;
+                if (n->src[0]->buffer->usage != GGML_BACKEND_BUFFER_USAGE_WEIGHTS) s += nbytes(n->src[0]) + 256;
+            } else if (n->op == GGML_OP_FLASH_ATTN_EXT) {
+                const int64_t ws = amv_flash_attn_workspace_bytes(n->src[0]->ne[2], n->src[1]->ne[2], n->src[1]->ne[1], 128);
+                s += (size_t)(ws > 0 ? ws : 0) + 256;
+            } else if (n->op == GGML_OP_GET_ROWS) {
+                s += nbytes(n->src[0]) + 256;
+            }
+        }
+        return s;
+    }
+
+    // MUL by a one-row weight that consumes this RMS_NORM output and nothing else reads that output later
+    static const ggml_tensor* fusable_mul(const ggml_cgraph* g, int i) {
+        const ggml_tensor* n = g->nodes[i];
+        if (i + 1 >= g->n_nodes) return nullptr;
+        const ggml_tensor* m = g->nodes[i + 1];
+        if (m->op != GGML_OP_MUL) return nullptr;
+        const ggml_tensor* w = m->src[0] == n ? m->src[1] : (m->src[1] == n ? m->src[0] : nullptr);
+        if (!w || w->type != GGML_TYPE_F32 || nrows(w) != 1 || w->ne[0] != n->ne[0] || !aligned16(w->data)) return nullptr;
+        if (m->type != GGML_TYPE_F32 || !is_contiguous(m) || !aligned16(m->data)) return nullptr;
+        return m;
+    }
+
+    bool run(ggml_cgraph* g) {
+        for (int i = 0; i < g->n_nodes; ++i) {
+            const ggml_tensor* n = g->nodes[i];
+            if (noop(n->op)) continue;
+            bool ok = true;
+            switch (n->op) {
+            case GGML_OP_MUL_MAT: ok = mul_mat(n); break;
+            case GGML_OP_RMS_NORM: {
+                const ggml_tensor* m = fusable_mul(g, i);
+                ok = rms_norm(n, m);
+                if (ok && m) {
+                    invalidate(n);
+                    invalidate(m);
+                    g_cnt.gpu_op++;
+                    g_cnt.fused++;
+                    ++i;
+                    n = m;
+                }
+                break;
+            }
+            case GGML_OP_ADD: ok = binary(n, 0); break;
+            case GGML_OP_MUL: ok = binary(n, 1); break;
+            case GGML_OP_ROPE: ok = rope(n); break;
+            case GGML_OP_FLASH_ATTN_EXT: ok = flash_attn(n); break;
+            case GGML_OP_GLU: ok = glu(n); break;
+            case GGML_OP_SET_ROWS: ok = set_rows(n); break;
+            case GGML_OP_CPY:
+            case GGML_OP_CONT: ok = cpy(n); break;
+            case GGML_OP_GET_ROWS: ok = get_rows(n); break;
+            default: ok = fail(n, "no encoder");
+            }
+            if (!ok) return false;
+            invalidate(n);
+            g_cnt.gpu_op++;
+        }
+        return true;
+    }
+};
+
+enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
+    Device* d = device();
+    std::lock_guard<std::mutex> lk(d->compute_mu);
+    if (!d->init()) {
+        log_line("no HIP device (FAIL-FAST)");
+        return GGML_STATUS_FAILED;
+    }
+    // contract pass over the whole graph before anything runs
+    for (int i = 0; i < g->n_nodes; ++i) {
+        const char* why = unsupported_reason(g->nodes[i]);
+        if (why) {
+            log_line("graph rejected at node %d %s: %s (FAIL-FAST)", i, g->nodes[i]->name, why);
+            return GGML_STATUS_FAILED;
+        }
+    }
+    if (!d->arena.reserve(Engine::scratch_bound(g))) {
+        log_line("scratch allocation failed (FAIL-FAST)");
+        return GGML_STATUS_FAILED;
+    }
+    d->arena.used = 0;
+    if (hipMemsetAsync(d->status, 0, 256, d->stream) != hipSuccess) return GGML_STATUS_FAILED;
+    Engine e{d, d->stream, {}, false, {}};
+    const bool ok = e.run(g);
+    const hipError_t se = hipStreamSynchronize(d->stream);
+    if (!ok) {
+        log_line("%s (FAIL-FAST)", e.why.c_str());
+        return GGML_STATUS_FAILED;
+    }
+    if (g_fail.load() == AMEVA_FAIL_WAIT_TIMEOUT) {
+        log_line("failure injection: wait timeout (FAIL-FAST)");
+        return GGML_STATUS_FAILED;
+    }
+    if (se != hipSuccess) {
+        log_line("graph execution failed: %s (FAIL-FAST)", hipGetErrorString(se));
+        return GGML_STATUS_FAILED;
+    }
+    unsigned int bad = 0;
+    (void)hipMemcpy(&bad, d->status, sizeof(bad), hipMemcpyDeviceToHost);
+    if (bad != 0 || g_fail.load() == AMEVA_FAIL_INVALIDATE_DST) {
+        log_line("%u row indices out of range (FAIL-FAST)", bad);
+        return GGML_STATUS_FAILED;
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
+// ------------------------------------------------------------------------------------------------ backend / device
+ggml_guid g_guid = {0x61, 0x6d, 0x65, 0x76, 0x61, 0x2d, 0x6d, 0x69, 0x33, 0x35, 0x35, 0x78, 0x2d, 0x68, 0x69, 0x70};
+
+const char* be_get_name(ggml_backend_t) { return GGML_AMEVA_NAME; }
+void be_free(ggml_backend_t b) {
+    g_cnt.ctx_destroy++;
+    delete b;
+}
+
+const ggml_backend_i g_backend_iface = {be_get_name, be_free, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                        nullptr,     nullptr, nullptr, nullptr, graph_compute, nullptr, nullptr, nullptr};
+
+const char* dev_get_name(ggml_backend_dev_t) { return GGML_AMEVA_DEVICE_NAME; }
+const char* dev_get_description(ggml_backend_dev_t) { return GGML_AMEVA_DEVICE_DESCRIPTION; }
+void dev_get_memory(ggml_backend_dev_t, size_t* fr, size_t* total) {
+    *fr = 0;
+    *total = 0;
+    if (device()->init()) (void)hipMemGetInfo(fr, total);
+}
+enum ggml_backend_dev_type dev_get_type(ggml_backend_dev_t) { return GGML_BACKEND_DEVICE_TYPE_GPU; }
+void dev_get_props(ggml_backend_dev_t d, ggml_backend_dev_props* p) {
+    p->name = dev_get_name(d);
+    p->description = dev_get_description(d);
+    dev_get_memory(d, &p->memory_free, &p->memory_total);
+    p->type = GGML_BACKEND_DEVICE_TYPE_GPU;
+    p->device_id = nullptr;
+    p->caps = {false, false, false, false};
+}
+ggml_backend_t dev_init_backend(ggml_backend_dev_t, const char*) { return ggml_backend_ameva_init(0); }
+ggml_backend_buffer_type_t dev_get_buffer_type(ggml_backend_dev_t) { return &g_buft; }
+bool dev_supports_op(ggml_backend_dev_t, const ggml_tensor* op) {
+    g_cnt.supports_query++;
+    const bool ok = unsupported_reason(op) == nullptr;
+    if (ok) g_cnt.supported_op++;
+    return ok;
+}
+bool dev_supports_buft(ggml_backend_dev_t, ggml_backend_buffer_type_t b) { return b == &g_buft; }
+bool dev_offload_op(ggml_backend_dev_t, const ggml_tensor* op) {
+    // a weight held by the host is worth copying for batches of prompt size
+    return op->op == GGML_OP_MUL_MAT && op->ne[1] >= 32;
+}
+
+struct ggml_backend_device g_device;
+struct ggml_backend_reg g_reg;
+
+const char* reg_get_name(ggml_backend_reg_t) { return GGML_AMEVA_NAME; }
+size_t reg_get_device_count(ggml_backend_reg_t) { return 1; }
+ggml_backend_dev_t reg_get_device(ggml_backend_reg_t, size_t i) { return i == 0 ? &g_device : nullptr; }
+void* reg_get_proc_address(ggml_backend_reg_t, const char* name) {
+    if (std::strcmp(name, "ggml_backend_ameva_profile_report") == 0) return (void*)ggml_backend_ameva_profile_report;
+    if (std::strcmp(name, "ggml_backend_ameva_reset_counters") == 0) return (void*)ggml_backend_ameva_reset_counters;
+    return nullptr;
+}
+
+void setup_registry() {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        g_device.iface = {dev_get_name,        dev_get_description, dev_get_memory,  dev_get_type,    dev_get_props,
+                          dev_init_backend,    dev_get_buffer_type, nullptr,         nullptr,         dev_supports_op,
+                          dev_supports_buft,   dev_offload_op,      nullptr,         nullptr,         nullptr};
+        g_device.reg = &g_reg;
+        g_device.context = nullptr;
+        g_reg.api_version = GGML_BACKEND_API_VERSION;
+        g_reg.iface = {reg_get_name, reg_get_device_count, reg_get_device, reg_get_proc_address};
+        g_reg.context = nullptr;
+        g_buft.device = &g_device;
+    });
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------ exports
+extern "C" {
+
+ggml_backend_reg_t ggml_backend_ameva_reg(void) {
+    setup_registry();
+    return &g_reg;
+}
+void ggml_backend_ameva_register(void) { setup_registry(); }
+void ggml_backend_ameva_teardown(void) {
+    Device* d = device();
+    std::lock_guard<std::mutex> lk(d->compute_mu);
+    if (d->inited) {
+        (void)hipStreamSynchronize(d->stream);
+        if (d->arena.base) (void)hipFree(d->arena.base);
+        d->arena = Arena{};
+        (void)hipFree(d->status);
+        (void)hipStreamDestroy(d->stream);
+        d->inited = false;
+    }
+}
+ggml_backend_reg_t ggml_backend_init(void) { return ggml_backend_ameva_reg(); }
+int ggml_backend_score(void) { return 100; }
+
+ggml_backend_t ggml_backend_ameva_init(size_t dev_num) {
+    if (dev_num != 0) {
+        log_line("device %zu does not exist (AMEVA0 only)", dev_num);
+        return nullptr;
+    }
+    setup_registry();
+    if (!device()->init()) {
+        log_line("no HIP device (FAIL-FAST)");
+        return nullptr;
+    }
+    ggml_backend* b = new ggml_backend;
+    b->guid = &g_guid;
+    b->iface = g_backend_iface;
+    b->device = &g_device;
+    b->context = nullptr;
+    return b;
+}
+bool ggml_backend_is_ameva(ggml_backend_t b) { return b && b->guid == &g_guid; }
+ggml_backend_buffer_type_t ggml_backend_ameva_buffer_type(size_t dev_num) {
+    setup_registry();
+    return dev_num == 0 ? &g_buft : nullptr;
+}
+
+int64_t ggml_backend_ameva_get_supports_query_count(void) { return g_cnt.supports_query; }
+int64_t ggml_backend_ameva_get_supported_op_count(void) { return g_cnt.supported_op; }
+int64_t ggml_backend_ameva_get_gpu_op_count(void) { return g_cnt.gpu_op; }
+int64_t ggml_backend_ameva_get_q5_0_cpu_dequant_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_f32_gpu_sgemm_dispatch_count(void) { return g_cnt.mul_mat; }
+int64_t ggml_backend_ameva_get_context_create_count(void) { return g_cnt.ctx_create; }
+int64_t ggml_backend_ameva_get_context_destroy_count(void) { return g_cnt.ctx_destroy; }
+int64_t ggml_backend_ameva_get_kernel_create_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_kernel_destroy_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_buffer_create_count(void) { return g_cnt.buf_create; }
+int64_t ggml_backend_ameva_get_buffer_destroy_count(void) { return g_cnt.buf_destroy; }
+int64_t ggml_backend_ameva_get_event_create_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_event_destroy_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_q5_0_staging_alloc_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_q5_0_staging_free_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_repacked_tensor_count(void) { return g_cnt.repacked_tensors; }
+int64_t ggml_backend_ameva_get_repacked_bytes(void) { return g_cnt.repacked_bytes; }
+int64_t ggml_backend_ameva_get_qmv_mul_mat_count(void) { return g_cnt.qmv; }
+int64_t ggml_backend_ameva_get_mmq_mul_mat_count(void) { return g_cnt.mmq; }
+int64_t ggml_backend_ameva_get_mmqb_mul_mat_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_fused_pair_count(void) { return g_cnt.fused; }
+int64_t ggml_backend_ameva_get_act_quant_reuse_count(void) { return g_cnt.act_reuse; }
+const char* ggml_backend_ameva_get_build_commit(void) {
+#ifdef AMEVA_BUILD_COMMIT
+    return AMEVA_BUILD_COMMIT;
+#else
+    return "unknown";
+#endif
+}
+void ggml_backend_ameva_reset_counters(void) {
+    // stored state (repacked tensors and bytes) is not cleared, as in the reference
+    g_cnt.supports_query = 0;
+    g_cnt.supported_op = 0;
+    g_cnt.gpu_op = 0;
+    g_cnt.mul_mat = 0;
+    g_cnt.qmv = 0;
+    g_cnt.mmq = 0;
+    g_cnt.fused = 0;
+    g_cnt.act_reuse = 0;
+}
+void ggml_backend_ameva_profile_report(void) {
+    log_line("counters: gpu_op %lld mul_mat %lld mmq %lld fused %lld act_reuse %lld repacked %lld (%lld bytes)",
+             (long long)g_cnt.gpu_op.load(), (long long)g_cnt.mul_mat.load(), (long long)g_cnt.mmq.load(),
+             (long long)g_cnt.fused.load(), (long long)g_cnt.act_reuse.load(), (long long)g_cnt.repacked_tensors.load(),
+             (long long)g_cnt.repacked_bytes.load());
+}
+void ggml_backend_ameva_set_failure_injection(AmevaFailureInjectionPoint p) { g_fail = (int)p; }
+AmevaFailureInjectionPoint ggml_backend_ameva_get_failure_injection(void) { return (AmevaFailureInjectionPoint)g_fail.load(); }
+const char* ggml_backend_ameva_op_unsupported_reason(const void* node) {
+    return unsupported_reason((const ggml_tensor*)node);
+}
+
+}  // extern "C"

@@ -225,11 +225,14 @@ def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
 # ------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
 def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, n_kv: int | None = None,
                       mask: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """q f32 [n_head, D]; k, v f16 [n_head_kv, kv_stride, D] (the first n_kv rows used); mask f16 [n_kv] or None."""
+    """q f32 [n_head, D]; k, v f16 views [n_head_kv, n_keys, D] with any strides (a head-major cache, or llama.cpp's
+    token-major one as k_cache[:, :n_kv].permute(1, 0, 2)); the first n_kv keys are used; mask f16 [n_kv] or None."""
     _need_gpu(q, "flash_attn_decode")
     n_head, D = q.shape
-    n_head_kv, kv_stride, _ = k.shape
-    n_kv = kv_stride if n_kv is None else n_kv
+    n_head_kv, n_keys, _ = k.shape
+    n_kv = n_keys if n_kv is None else n_kv
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("flash_attn_decode: K/V rows must be contiguous")
     need = lib().amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv, D)
     if need < 0:
         raise ValueError("flash_attn_decode: unsupported shape")
@@ -237,6 +240,52 @@ def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     out = torch.empty_like(q)
     check(lib().amv_flash_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(mask), out.data_ptr(), n_head,
-                                      n_head_kv, n_kv, kv_stride, D, scale, workspace.data_ptr(), need, _stream()),
-          "amv_flash_attn_decode")
+                                      n_head_kv, n_kv, D, k.stride(1), k.stride(0), v.stride(1), v.stride(0), scale,
+                                      workspace.data_ptr(), need, _stream()), "amv_flash_attn_decode")
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ glue ops
+def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """ggml_add with b broadcast over rows (b rows divide a rows)."""
+    return _binary(0, a, b)
+
+
+def mul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return _binary(1, a, b)
+
+
+def _binary(op: int, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    _need_gpu(a, "binary")
+    _need_gpu(b, "binary")
+    n = a.shape[-1]
+    out = torch.empty_like(a)
+    check(lib().amv_binary(op, a.data_ptr(), b.data_ptr(), out.data_ptr(), a.numel() // n, n, b.numel() // n,
+                           _stream()), "amv_binary")
+    return out
+
+
+def set_rows_f16(dst: torch.Tensor, src: torch.Tensor, idx: torch.Tensor | None = None) -> None:
+    """Rows of src f32 [r, n] into rows idx (int32/int64 [r]) of dst f16 [rows, n]; raises on out-of-range indices."""
+    _need_gpu(src, "set_rows_f16")
+    bad = torch.zeros(1, dtype=torch.int32, device=src.device)
+    r, n = src.shape
+    bits = 0 if idx is None else (64 if idx.dtype == torch.int64 else 32)
+    check(lib().amv_set_rows_f16(src.data_ptr(), src.stride(0), dst.data_ptr(), dst.stride(0), r, n, _ptr(idx), bits,
+                                 dst.shape[0], bad.data_ptr(), _stream()), "amv_set_rows_f16")
+    if int(bad.item()) != 0:
+        raise IndexError(f"set_rows_f16: {int(bad.item())} row indices out of range (FAIL-FAST)")
+
+
+def get_rows(src: torch.Tensor, src_type: int, n: int, idx: torch.Tensor) -> torch.Tensor:
+    """ggml_get_rows: f32 [len(idx), n] from rows of src (F32 = 0, F16 = 1, Q4_0, Q8_0 in ggml layout)."""
+    _need_gpu(idx, "get_rows")
+    rb = {0: n * 4, 1: n * 2, Q4_0: n // 32 * 18, Q8_0: n // 32 * 34}[src_type]
+    rows = src.numel() * src.element_size() // rb
+    out = torch.empty((idx.numel(), n), dtype=torch.float32, device=idx.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=idx.device)
+    check(lib().amv_get_rows(src_type, src.data_ptr(), rows, n, idx.data_ptr(), idx.numel(), out.data_ptr(),
+                             bad.data_ptr(), _stream()), "amv_get_rows")
+    if int(bad.item()) != 0:
+        raise IndexError("get_rows: row index out of range (FAIL-FAST)")
     return out

@@ -137,14 +137,30 @@ int amv_swiglu(const float* g, const float* u, float* y, int64_t n, void* stream
 /* ------------------------------------------------------------------------------------------------------------
  * FLASH_ATTN_EXT, decode (one query position), f16 K/V cache (enc_flash_attn ggml-ameva.cpp:4204-4284 with the key
  * splits of ameva_fa_split_keys 4170-4195, ameva_flash_attn.comp + ameva_fa_combine.comp).
- *   q f32 [n_head][D]; k, v f16 [n_head_kv][kv_stride][D] (ggml's cache view: rows of D halves, kv_stride rows per
- *   head, the first n_kv used); mask f16 [n_kv] or NULL (added to the scaled scores); out f32 [n_head][D].
- *   D = 128; n_head / n_head_kv in {1, 2, 4, 8}. workspace: amv_flash_attn_workspace_bytes() bytes of device memory.
+ *   q f32 [n_head][D] contiguous; out f32 [n_head][D]; D = 128; n_head / n_head_kv in {1, 2, 4, 8}.
+ *   k, v f16: element d of key j of KV head h at k[j * k_row + h * k_head + d] (strides in elements, ggml's nb[1] / 2
+ *   and nb[2] / 2: llama.cpp's cache view has k_row = n_head_kv * D, k_head = D); the first n_kv keys are used.
+ *   mask f16 [n_kv] or NULL (added to the scaled scores; -inf masks a key).
+ *   workspace: amv_flash_attn_workspace_bytes() bytes of device memory for the split partials.
  * ---------------------------------------------------------------------------------------------------------- */
 int64_t amv_flash_attn_workspace_bytes(int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D);
 int amv_flash_attn_decode(const float* q, const void* k, const void* v, const void* mask, float* out, int64_t n_head,
-                          int64_t n_head_kv, int64_t n_kv, int64_t kv_stride, int64_t D, float scale, void* workspace,
-                          int64_t workspace_bytes, void* stream);
+                          int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row, int64_t k_head, int64_t v_row,
+                          int64_t v_head, float scale, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Glue ops of the decoder graph (ameva_binary.comp, ameva_cpy.comp, ameva_set_rows.comp, ameva_get_rows(_q).comp).
+ * ---------------------------------------------------------------------------------------------------------- */
+/* ADD (op 0) / MUL (op 1), f32: dst[r][i] = a[r][i] op b[r % b_rows][i] for n_rows rows of n elements. */
+int amv_binary(int op, const float* a, const float* b, float* dst, int64_t n_rows, int64_t n, int64_t b_rows,
+               void* stream);
+/* SET_ROWS / CPY f32 -> f16: row r of src (stride src_stride elements) to row idx[r] of dst (stride dst_stride), or row
+ * r when idx is NULL; idx_bits 32 or 64. Out-of-range indices are skipped and counted in *bad (device, may be NULL). */
+int amv_set_rows_f16(const float* src, int64_t src_stride, void* dst, int64_t dst_stride, int64_t n_rows, int64_t n,
+                     const void* idx, int idx_bits, int64_t dst_rows, unsigned int* bad, void* stream);
+/* GET_ROWS: dst f32 [n_idx][n] = row idx[i] of src (type F32, F16, Q4_0 or Q8_0 in ggml layout, src_rows rows). */
+int amv_get_rows(int type, const void* src, int64_t src_rows, int64_t n, const int32_t* idx, int64_t n_idx, float* dst,
+                 unsigned int* bad, void* stream);
 
 #ifdef __cplusplus
 }

@@ -202,6 +202,11 @@ def test_flash_attn_decode(dev, ops, orc, n_head, n_head_kv, n_kv, stride):
     out = ops.flash_attn_decode(gpu(q, dev), gpu(k.view(np.uint16), dev).view(torch.float16),
                                 gpu(v.view(np.uint16), dev).view(torch.float16), scale, n_kv=n_kv).cpu().numpy()
     assert rel_l2(out, ref) < TOL_FA
+    # llama.cpp's token-major cache [kv_size][n_head_kv][D] viewed per head: same result
+    kt = gpu(np.ascontiguousarray(k.transpose(1, 0, 2)), dev)
+    vt = gpu(np.ascontiguousarray(v.transpose(1, 0, 2)), dev)
+    out_t = ops.flash_attn_decode(gpu(q, dev), kt.permute(1, 0, 2), vt.permute(1, 0, 2), scale, n_kv=n_kv).cpu().numpy()
+    assert np.array_equal(out_t, out)
 
 
 def test_flash_attn_decode_mask(dev, ops, orc):
@@ -217,3 +222,25 @@ def test_flash_attn_decode_mask(dev, ops, orc):
     ref = orc.flash_attn_decode(q, k.view(np.uint16), v.view(np.uint16), scale, mask.view(np.uint16))
     out = ops.flash_attn_decode(gpu(q, dev), gpu(k, dev), gpu(v, dev), scale, mask=gpu(mask, dev)).cpu().numpy()
     assert rel_l2(out, ref) < TOL_FA
+
+
+def test_glue_ops(dev, ops, orc):
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((7, 4096)).astype(np.float32)
+    b = rng.standard_normal((1, 4096)).astype(np.float32)
+    assert np.array_equal(ops.add(gpu(a, dev), gpu(b, dev)).cpu().numpy(), a + b)
+    assert np.array_equal(ops.mul(gpu(a, dev), gpu(b, dev)).cpu().numpy(), a * b)
+    cache = torch.zeros((16, 1024), dtype=torch.float16, device=dev)
+    src = rng.standard_normal((3, 1024)).astype(np.float32)
+    idx = torch.tensor([5, 0, 15], dtype=torch.int64, device=dev)
+    ops.set_rows_f16(cache, gpu(src, dev), idx)
+    c = cache.cpu().numpy()
+    assert np.array_equal(c[[5, 0, 15]].view(np.uint16), orc.fp32_to_fp16(src))
+    assert not c[1:5].any()
+    with pytest.raises(IndexError):
+        ops.set_rows_f16(cache, gpu(src, dev), torch.tensor([5, 16, 0], dtype=torch.int64, device=dev))
+    emb = (rng.standard_normal((50, 256)) * 0.02).astype(np.float32)
+    embq = orc.quantize_q4_0(emb)
+    ids = np.array([3, 49, 0, 3], np.int32)
+    got = ops.get_rows(gpu(embq, dev), ops.Q4_0, 256, gpu(ids, dev)).cpu().numpy()
+    assert np.array_equal(got, orc.dequantize(ops.Q4_0, embq, 256)[ids])

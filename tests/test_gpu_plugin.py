@@ -1,0 +1,260 @@
+"""GPU tests through the ggml backend plugin (libggml-ameva.so): single-node graphs for every op of the hot path,
+the counters the reference's own tests use as ground truth that a GPU kernel ran, lossless get_tensor of repacked
+weights, the FAIL-FAST paths forced by failure injection, and one Llama-3-8B-shaped decoder layer (BASELINE config
+4: hidden 4096, 32 / 8 heads of 128, RoPE theta 500000, FA decode over an f16 KV cache of 4096, SwiGLU 14336, Q4_0
+weights) against the oracle's chain of the same ops."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import ggml_plugin as gp  # noqa: E402
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def plugin():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return gp.load()[1]
+
+
+def quantize(orc, t, w):
+    if t == gp.Q4_0:
+        return orc.quantize_q4_0(w)
+    if t == gp.Q8_0:
+        return orc.quantize_q8_0(w, orc.Q8_REF)
+    raise ValueError(t)
+
+
+def random_kquant(rng, t, n, k):
+    bb = 144 if t == gp.Q4_K else 210
+    y = rng.integers(0, 256, (n, k // 256, bb), dtype=np.uint8)
+    offs = (0, 2) if t == gp.Q4_K else (208,)
+    for off in offs:
+        v = rng.uniform(0.0, 0.002, (n, k // 256)).astype(np.float16)
+        y[:, :, off:off + 2] = v.view(np.uint8).reshape(n, k // 256, 2)
+    return y.reshape(n, -1)
+
+
+@pytest.mark.parametrize("wt", [gp.Q4_0, gp.Q8_0, gp.Q4_K, gp.Q6_K])
+@pytest.mark.parametrize("m", [1, 16])
+def test_mul_mat_node(plugin, orc, wt, m):
+    rng = np.random.default_rng(wt * 10 + m)
+    n, k = 512, 4096
+    if wt in (gp.Q4_0, gp.Q8_0):
+        wg = quantize(orc, wt, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        aq = lambda x: orc.quantize_q8_0(x, orc.Q8_X86)  # noqa: E731
+    else:
+        wg = random_kquant(rng, wt, n, k)
+        aq = orc.quantize_q8_K
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    g = gp.Graph(wg.nbytes + 4096, 64 << 20)
+    try:
+        plugin.ggml_backend_ameva_reset_counters()
+        W = g.tensor(wt, [k, n], "w", "w")
+        X = g.tensor(gp.F32, [k, m], "c", "x")
+        g.set(W, wg)
+        g.set(X, x)
+        Y = g.mul_mat(W, X)
+        rep0 = gp.counter(plugin, "repacked_tensor_count")
+        assert g.compute() == gp.STATUS_SUCCESS
+        y = g.get(Y, np.float32, (m, n))
+        assert rel_l2(y, orc.mul_mat(wt, wg, n, k, aq(x), m)) < 1e-3
+        assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 1
+        assert gp.counter(plugin, "mmq_mul_mat_count") == (1 if m >= 8 and wt in (gp.Q4_0, gp.Q8_0) else 0)
+        assert gp.counter(plugin, "repacked_tensor_count") == rep0 + 1
+        # the weight reads back in ggml layout, byte for byte
+        assert np.array_equal(g.get(W, np.uint8), wg.reshape(-1))
+        # a second run reuses the repacked weight
+        assert g.compute() == gp.STATUS_SUCCESS
+        assert np.array_equal(g.get(Y, np.float32, (m, n)), y)
+    finally:
+        g.free()
+
+
+def test_activation_reuse_and_norm_fusion(plugin, orc):
+    rng = np.random.default_rng(3)
+    k, n = 4096, 256
+    wa = quantize(orc, gp.Q4_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    wb = quantize(orc, gp.Q4_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((1, k)).astype(np.float32) * 3
+    nw = rng.standard_normal(k).astype(np.float32)
+    g = gp.Graph(2 * wa.nbytes + 8192, 32 << 20)
+    try:
+        plugin.ggml_backend_ameva_reset_counters()
+        WA, WB = g.tensor(gp.Q4_0, [k, n], "w", "wa"), g.tensor(gp.Q4_0, [k, n], "w", "wb")
+        X, NW = g.tensor(gp.F32, [k, 1], "c", "x"), g.tensor(gp.F32, [k], "c", "nw")
+        for t, a in ((WA, wa), (WB, wb), (X, x), (NW, nw)):
+            g.set(t, a)
+        N = g.rms_norm(X, 1e-5)
+        M = g.mul(N, NW)
+        YA, YB = g.mul_mat(WA, M), g.mul_mat(WB, M)
+        assert g.compute() == gp.STATUS_SUCCESS
+        y_ref, o_ref = orc.rms_norm(x, 1e-5, nw)
+        o = g.get(M, np.float32, (1, k))
+        assert rel_l2(g.get(N, np.float32, (1, k)), y_ref) < 1e-6 and rel_l2(o, o_ref) < 1e-6
+        a = orc.quantize_q8_0(o, orc.Q8_X86)
+        assert rel_l2(g.get(YA, np.float32), orc.mul_mat(gp.Q4_0, wa, n, k, a, 1)) < 1e-3
+        assert rel_l2(g.get(YB, np.float32), orc.mul_mat(gp.Q4_0, wb, n, k, a, 1)) < 1e-3
+        assert gp.counter(plugin, "fused_pair_count") == 1
+        assert gp.counter(plugin, "act_quant_reuse_count") == 1
+        assert gp.counter(plugin, "gpu_op_count") == 4
+    finally:
+        g.free()
+
+
+def test_rope_swiglu_get_rows_nodes(plugin, orc):
+    rng = np.random.default_rng(4)
+    g = gp.Graph(1 << 20, 16 << 20)
+    try:
+        x = rng.standard_normal((3, 32, 128)).astype(np.float32)
+        pos = np.array([0, 17, 4095], np.int32)
+        X, POS = g.tensor(gp.F32, [128, 32, 3]), g.tensor(gp.I32, [3])
+        g.set(X, x)
+        g.set(POS, pos)
+        R = g.rope(X, POS, 128, 0, 500000.0)
+        gt, up = rng.standard_normal(14336).astype(np.float32), rng.standard_normal(14336).astype(np.float32)
+        G_, U_ = g.tensor(gp.F32, [14336, 1]), g.tensor(gp.F32, [14336, 1])
+        g.set(G_, gt)
+        g.set(U_, up)
+        S = g.swiglu(G_, U_)
+        emb = (rng.standard_normal((64, 4096)) * 0.02).astype(np.float32)
+        embq = orc.quantize_q4_0(emb)
+        E = g.tensor(gp.Q4_0, [4096, 64], "w", "tok_embd")
+        g.set(E, embq)
+        ids = np.array([5, 63, 0], np.int32)
+        IDS = g.tensor(gp.I32, [3])
+        g.set(IDS, ids)
+        GR = g.get_rows(E, IDS)
+        assert g.compute() == gp.STATUS_SUCCESS
+        assert rel_l2(g.get(R, np.float32, (3, 32, 128)), orc.rope(x, pos, 128, 0, 500000.0)) < 1e-5
+        assert rel_l2(g.get(S, np.float32), orc.swiglu(gt, up)) < 1e-6
+        assert np.array_equal(g.get(GR, np.float32, (3, 4096)), orc.dequantize(gp.Q4_0, embq, 4096)[ids])
+    finally:
+        g.free()
+
+
+def test_failure_injection_and_contract_fail_fast(plugin):
+    rng = np.random.default_rng(5)
+    g = gp.Graph(1 << 20, 8 << 20)
+    try:
+        X = g.tensor(gp.F32, [4096, 1])
+        g.set(X, rng.standard_normal(4096).astype(np.float32))
+        W = g.tensor(gp.Q4_0, [4096, 64], "w", "w")
+        g.set(W, rng.integers(0, 256, 64 * 128 * 18, dtype=np.uint8).reshape(64, -1) & 0x0F)
+        Y = g.mul_mat(W, X)
+        plugin.ggml_backend_ameva_reset_counters()
+        plugin.ggml_backend_ameva_set_failure_injection(6)  # AMEVA_FAIL_DISPATCH
+        try:
+            assert g.compute() == gp.STATUS_FAILED
+            assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 0
+        finally:
+            plugin.ggml_backend_ameva_set_failure_injection(0)
+        plugin.ggml_backend_ameva_set_failure_injection(7)  # AMEVA_FAIL_WAIT_TIMEOUT
+        try:
+            assert g.compute() == gp.STATUS_FAILED
+        finally:
+            plugin.ggml_backend_ameva_set_failure_injection(0)
+        assert g.compute() == gp.STATUS_SUCCESS
+        # one unsupported node fails the whole graph before anything runs
+        plugin.ggml_backend_ameva_reset_counters()
+        bad = g._node(gp.OP_SOFT_MAX, gp.F32, [4096, 1], [X], "softmax")
+        assert g.compute([Y, bad]) == gp.STATUS_FAILED
+        assert gp.counter(plugin, "gpu_op_count") == 0
+    finally:
+        g.free()
+
+
+def test_llama3_8b_decode_layer(plugin, orc):
+    """One decoder layer of Llama-3-8B shape, bs1 decode at position 4095 with 4095 cached tokens."""
+    rng = np.random.default_rng(2024)
+    H, NH, NKV, D, FF, CTX = 4096, 32, 8, 128, 14336, 4096
+    pos_t = CTX - 1
+    eps, base = 1e-5, 500000.0
+    def wq4(n, k):
+        return orc.quantize_q4_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    w = {"q": wq4(NH * D, H), "k": wq4(NKV * D, H), "v": wq4(NKV * D, H), "o": wq4(H, NH * D),
+         "gate": wq4(FF, H), "up": wq4(FF, H), "down": wq4(H, FF)}
+    attn_norm = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    ffn_norm = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    kc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)  # llama.cpp cache rows [token][head * D]
+    vc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    wbytes = sum(a.nbytes for a in w.values()) + 16 * 4096
+    g = gp.Graph(wbytes, 96 << 20)
+    try:
+        plugin.ggml_backend_ameva_reset_counters()
+        T = {k_: g.tensor(gp.Q4_0, [a.shape[1] * 32 // 18, a.shape[0]], "w", k_) for k_, a in w.items()}
+        for k_, a in w.items():
+            g.set(T[k_], a)
+        AN, FN = g.tensor(gp.F32, [H], "w", "attn_norm"), g.tensor(gp.F32, [H], "w", "ffn_norm")
+        g.set(AN, attn_norm)
+        g.set(FN, ffn_norm)
+        KC, VC = g.tensor(gp.F16, [NKV * D, CTX], "c", "k_cache"), g.tensor(gp.F16, [NKV * D, CTX], "c", "v_cache")
+        g.set(KC, kc)
+        g.set(VC, vc)
+        X = g.tensor(gp.F32, [H, 1], "c", "inp")
+        g.set(X, x)
+        POS = g.tensor(gp.I32, [1], "c", "pos")
+        g.set(POS, np.array([pos_t], np.int32))
+        IDX = g.tensor(gp.I64, [1], "c", "kv_idx")
+        g.set(IDX, np.array([pos_t], np.int64))
+        MASK = g.tensor(gp.F16, [CTX, 1], "c", "mask")
+        g.set(MASK, np.zeros(CTX, np.float16))
+
+        cur = g.mul(g.rms_norm(X, eps), AN)
+        q = g.reshape_3d(g.mul_mat(T["q"], cur), D, NH, 1)
+        k = g.reshape_3d(g.mul_mat(T["k"], cur), D, NKV, 1)
+        v = g.mul_mat(T["v"], cur)
+        q = g.rope(q, POS, D, 0, base)
+        k = g.rope(k, POS, D, 0, base)
+        k2 = g.view_nd(k, gp.OP_RESHAPE, [NKV * D, 1], [4, NKV * D * 4, NKV * D * 4, NKV * D * 4])
+        g.set_rows(KC, k2, IDX)
+        g.set_rows(VC, v, IDX)
+        kv_nb = [2, NKV * D * 2, D * 2, NKV * D * 2 * CTX]
+        kview = g.view_nd(KC, gp.OP_VIEW, [D, CTX, NKV], kv_nb)
+        vview = g.view_nd(VC, gp.OP_VIEW, [D, CTX, NKV], kv_nb)
+        qp = g.view_nd(q, gp.OP_PERMUTE, [D, 1, NH], [4, D * NH * 4, D * 4, D * NH * 4])
+        att = g.flash_attn_ext(qp, kview, vview, MASK, 1.0 / np.sqrt(D))
+        att2 = g.view_nd(att, gp.OP_RESHAPE, [H, 1], [4, H * 4, H * 4, H * 4])
+        ffn_inp = g.add(g.mul_mat(T["o"], att2), X)
+        cur = g.mul(g.rms_norm(ffn_inp, eps), FN)
+        ff = g.swiglu(g.mul_mat(T["gate"], cur), g.mul_mat(T["up"], cur))
+        out = g.add(g.mul_mat(T["down"], ff), ffn_inp)
+        assert g.compute() == gp.STATUS_SUCCESS
+        y = g.get(out, np.float32, (1, H))
+        assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 7
+        assert gp.counter(plugin, "fused_pair_count") == 2
+        assert gp.counter(plugin, "act_quant_reuse_count") == 3  # k, v share q's; up shares gate's
+
+        # the oracle's chain of the same ops
+        q8 = lambda a: orc.quantize_q8_0(a, orc.Q8_X86)  # noqa: E731
+        def mm(name, a):
+            n_, kk_ = w[name].shape[0], w[name].shape[1] * 32 // 18
+            return orc.mul_mat(gp.Q4_0, w[name], n_, kk_, q8(a), 1)
+        _, c = orc.rms_norm(x, eps, attn_norm)
+        qr = orc.rope(mm("q", c).reshape(1, NH, D), np.array([pos_t], np.int32), D, 0, base)
+        kr = orc.rope(mm("k", c).reshape(1, NKV, D), np.array([pos_t], np.int32), D, 0, base)
+        kc2, vc2 = kc.copy(), vc.copy()
+        kc2[pos_t] = kr.reshape(-1).astype(np.float16)
+        vc2[pos_t] = mm("v", c).reshape(-1).astype(np.float16)
+        kh = np.ascontiguousarray(kc2.reshape(CTX, NKV, D).transpose(1, 0, 2))
+        vh = np.ascontiguousarray(vc2.reshape(CTX, NKV, D).transpose(1, 0, 2))
+        a_ = orc.flash_attn_decode(qr.reshape(NH, D), kh.view(np.uint16), vh.view(np.uint16), 1.0 / np.sqrt(D))
+        f_in = mm("o", a_.reshape(1, H)) + x
+        _, c2 = orc.rms_norm(f_in, eps, ffn_norm)
+        y_ref = mm("down", orc.swiglu(mm("gate", c2), mm("up", c2))) + f_in
+        # the KV cache row written by SET_ROWS is the f16 of the roped K / V
+        assert np.array_equal(g.get(KC, np.uint16, (CTX, NKV * D))[:pos_t], kc[:pos_t].view(np.uint16))
+        assert rel_l2(g.get(KC, np.float16, (CTX, NKV * D))[pos_t], kc2[pos_t]) < 1e-3
+        err = rel_l2(y, y_ref)
+        assert err < 2e-3, err
+    finally:
+        g.free()
