@@ -1,0 +1,135 @@
+"""One Llama-3-architecture decoder layer on quantized weights, as the sequence of hot-path kernels a ggml decode
+graph of that layer runs (the reference's graph engine records the same nodes:
+RMS_NORM+MUL, MUL_MAT q/k/v, ROPE, SET_ROWS into the KV cache, FLASH_ATTN_EXT, MUL_MAT o, ADD, RMS_NORM+MUL,
+MUL_MAT gate/up, SWIGLU, MUL_MAT down, ADD).
+
+MI355X-specific choices: q/k/v and gate/up are each one weight of stacked rows (one GEMV launch instead of three /
+two; the rows are independent, so the outputs equal the separate MUL_MATs), the Q8_0 quantization of each GEMV input
+is fused into the RMS_NORM kernel, and RoPE of q and k is one launch over the 40 contiguous heads. Every buffer is
+allocated up front, so a decode step launches kernels only and can be captured in a HIP graph.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from ._lib import check, lib
+
+
+class LlamaLayer:
+    def __init__(self, wq: ops.QWeight, wo: ops.QWeight, wgu: ops.QWeight, wdown: ops.QWeight,
+                 attn_norm: torch.Tensor, ffn_norm: torch.Tensor, n_head: int = 32, n_head_kv: int = 8,
+                 head_dim: int = 128, ctx: int = 4096, eps: float = 1e-5, rope_base: float = 500000.0):
+        dev = attn_norm.device
+        self.wqkv, self.wo, self.wgu, self.wdown = wq, wo, wgu, wdown
+        self.attn_norm, self.ffn_norm = attn_norm, ffn_norm
+        self.n_head, self.n_head_kv, self.D, self.ctx = n_head, n_head_kv, head_dim, ctx
+        self.eps, self.base = eps, rope_base
+        self.H = n_head * head_dim
+        self.kv = n_head_kv * head_dim
+        self.FF = wgu.n_rows // 2
+        assert wq.n_rows == self.H + 2 * self.kv and wq.k == self.H
+        assert wdown.k == self.FF and wdown.n_rows == self.H and wo.n_rows == self.H
+        # llama.cpp's cache layout: rows [token][n_head_kv * head_dim]
+        self.k_cache = torch.zeros((ctx, self.kv), dtype=torch.float16, device=dev)
+        self.v_cache = torch.zeros((ctx, self.kv), dtype=torch.float16, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.t_norm = torch.empty(self.H, **f32)
+        self.t_o = torch.empty(self.H, **f32)      # attention-norm output (y * w)
+        self.t_o2 = torch.empty(self.H, **f32)     # FFN-norm output
+        self.qkv = torch.empty(wq.n_rows, **f32)
+        self.att = torch.empty(self.H, **f32)
+        self.proj = torch.empty(self.H, **f32)
+        self.x1 = torch.empty(self.H, **f32)
+        self.gu = torch.empty(wgu.n_rows, **f32)
+        self.h = torch.empty(self.FF, **f32)
+        self.down = torch.empty(self.H, **f32)
+        u8 = dict(dtype=torch.uint8, device=dev)
+        self.act_h = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.H), **u8)
+        self.act_att = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.H), **u8)
+        self.act_h2 = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.H), **u8)
+        self.act_ff = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.FF), **u8)
+        self.fa_ws = torch.empty(lib().amv_flash_attn_workspace_bytes(n_head, n_head_kv, ctx, head_dim), **u8)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.kv_idx = torch.zeros(1, dtype=torch.int64, device=dev)
+
+    @staticmethod
+    def stack_rows(*blocks: torch.Tensor) -> torch.Tensor:
+        """Rows of several ggml-layout weights with the same k, stacked (ggml blocks are whole rows)."""
+        return torch.cat([b.reshape(b.shape[0], -1) for b in blocks], dim=0).contiguous()
+
+    def set_position(self, pos: int) -> None:
+        """Position of the next decode step (written into device memory, so a captured graph picks it up)."""
+        self.pos.fill_(pos)
+        self.kv_idx.fill_(pos)
+        self.n_kv = pos + 1
+
+    def decode(self, x: torch.Tensor, out: torch.Tensor) -> None:
+        """x f32 [H] -> out f32 [H] for the token at the position of set_position(); writes K/V into the cache.
+        The number of cached keys is fixed at n_kv for the launch (graph replays reuse it)."""
+        L, st = lib(), torch.cuda.current_stream().cuda_stream
+        H, kv, D = self.H, self.kv, self.D
+        n_kv = self.n_kv
+        # attention block
+        check(L.amv_rms_norm(x.data_ptr(), 1, H, self.eps, self.attn_norm.data_ptr(), self.t_norm.data_ptr(),
+                             self.t_o.data_ptr(), self.act_h.data_ptr(), ops.Q8_X86, st), "rms_norm")
+        check(L.amv_mul_mat_vec(self.wqkv.type, self.wqkv.data.data_ptr(),
+                                self.wqkv.n_rows, H, self.act_h.data_ptr(), 1, self.qkv.data_ptr(), self.wqkv.n_rows,
+                                st), "qkv")
+        # RoPE of q and k: 40 contiguous heads of the qkv output, in place
+        check(L.amv_rope(self.qkv.data_ptr(), self.qkv.data_ptr(), self.pos.data_ptr(), 1,
+                         self.n_head + self.n_head_kv, D, D, 0, self.base, 1.0, 1.0, st), "rope")
+        kp = self.qkv.data_ptr() + H * 4
+        vp = kp + kv * 4
+        check(L.amv_set_rows_f16(kp, kv, self.k_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64, self.ctx,
+                                 None, st), "set_rows k")
+        check(L.amv_set_rows_f16(vp, kv, self.v_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64, self.ctx,
+                                 None, st), "set_rows v")
+        ws = self.fa_ws.numel()
+        check(L.amv_flash_attn_decode(self.qkv.data_ptr(), self.k_cache.data_ptr(), self.v_cache.data_ptr(), None,
+                                      self.att.data_ptr(), self.n_head, self.n_head_kv, n_kv, D, kv, D, kv, D,
+                                      1.0 / (D ** 0.5), self.fa_ws.data_ptr(), ws, st), "flash_attn")
+        check(L.amv_quantize_act(ops.Q8_0, self.att.data_ptr(), 1, H, ops.Q8_X86, None, self.act_att.data_ptr(), st),
+              "quant att")
+        check(L.amv_mul_mat_vec(self.wo.type, self.wo.data.data_ptr(), H, H, self.act_att.data_ptr(), 1,
+                                self.proj.data_ptr(), H, st), "wo")
+        check(L.amv_binary(0, self.proj.data_ptr(), x.data_ptr(), self.x1.data_ptr(), 1, H, 1, st), "residual 1")
+        # FFN block
+        check(L.amv_rms_norm(self.x1.data_ptr(), 1, H, self.eps, self.ffn_norm.data_ptr(), self.t_norm.data_ptr(),
+                             self.t_o2.data_ptr(), self.act_h2.data_ptr(), ops.Q8_X86, st), "ffn norm")
+        check(L.amv_mul_mat_vec(self.wgu.type, self.wgu.data.data_ptr(), self.wgu.n_rows, H, self.act_h2.data_ptr(), 1,
+                                self.gu.data_ptr(), self.wgu.n_rows, st), "gate_up")
+        check(L.amv_swiglu(self.gu.data_ptr(), self.gu.data_ptr() + self.FF * 4, self.h.data_ptr(), self.FF, st),
+              "swiglu")
+        check(L.amv_quantize_act(ops.Q8_0, self.h.data_ptr(), 1, self.FF, ops.Q8_X86, None, self.act_ff.data_ptr(),
+                                 st), "quant ffn")
+        check(L.amv_mul_mat_vec(self.wdown.type, self.wdown.data.data_ptr(), H, self.FF, self.act_ff.data_ptr(), 1,
+                                self.down.data_ptr(), H, st), "down")
+        check(L.amv_binary(0, self.down.data_ptr(), self.x1.data_ptr(), out.data_ptr(), 1, H, 1, st), "residual 2")
+
+    # algorithmic HBM bytes of one decode step at n_kv cached keys (weights + KV read + norms)
+    def step_bytes(self, n_kv: int) -> int:
+        w = sum(q.nbytes for q in (self.wqkv, self.wo, self.wgu, self.wdown))
+        return w + 2 * n_kv * self.kv * 2 + 2 * self.H * 4
+
+
+def random_layer(dev, seed: int = 0, H: int = 4096, n_head: int = 32, n_head_kv: int = 8, D: int = 128,
+                 FF: int = 14336, ctx: int = 4096, wtype: int = ops.Q4_0) -> LlamaLayer:
+    """A layer with seeded N(0, 0.02) weights quantized on the GPU (Q4_0 rule), norm weights 1 + N(0, 0.1)^."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def q(n, k):
+        wf = torch.randn((n, k), generator=g, device=dev) * 0.02
+        b = ops.quantize_q4_0(wf) if wtype == ops.Q4_0 else ops.quantize_k(wf, wtype)
+        del wf
+        return b
+
+    kv = n_head_kv * D
+    wqkv = ops.QWeight.from_ggml(wtype, LlamaLayer.stack_rows(q(H, H), q(kv, H), q(kv, H)), H + 2 * kv, H)
+    wo = ops.QWeight.from_ggml(wtype, q(H, H), H, H)
+    wgu = ops.QWeight.from_ggml(wtype, LlamaLayer.stack_rows(q(FF, H), q(FF, H)), 2 * FF, H)
+    wdown = ops.QWeight.from_ggml(wtype, q(H, FF), H, FF)
+    an = 1 + 0.1 * torch.randn(H, generator=g, device=dev)
+    fn = 1 + 0.1 * torch.randn(H, generator=g, device=dev)
+    return LlamaLayer(wqkv, wo, wgu, wdown, an, fn, n_head, n_head_kv, D, ctx)

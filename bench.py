@@ -23,7 +23,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 N_ROWS, K = 14336, 4096
-COPIES = 16
+COPIES = 20          # 20 x 33 MB = 661 MB of distinct weights, > 2 x the 256 MiB Infinity Cache
+GRAPH_STEPS = 100    # steps captured in one HIP graph
 
 
 def log(*a):
@@ -66,6 +67,27 @@ def time_steps(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps  # ms per step
 
 
+def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS):
+    """fn(i) for i in 0..per_graph-1 captured once in a HIP graph; the graph is replayed so that K >= steps steps
+    run back to back with no host launch cost between kernels. Returns ms per step."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(per_graph):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(per_graph):
+            fn(i)
+    reps = max(1, (steps + per_graph - 1) // per_graph)
+    wreps = max(1, warmup // per_graph)
+    ms = time_steps(torch, lambda i: graph.replay(), reps, wreps)
+    del graph
+    return ms / per_graph
+
+
 def cpu_baseline(seconds: float = 10.0):
     import numpy as np
     import oracle
@@ -92,6 +114,48 @@ def cpu_baseline(seconds: float = 10.0):
         "sample": f"{n} Q4_0 GEMVs 14336x4096 (M=1) in {el:.1f} s, oracle vec_dot_q4_0_q8_0 (C, OpenMP), "
                   f"{per * 1e3:.2f} ms each; host CPU: {cpu_model()}",
     }
+
+
+def bench_layer(torch, dev, args):
+    """bs1 decode of a Llama-3-8B-shape layer at position 4095 (4096 cached keys): LAYERS
+    different random layers chained (cold weights: 4 x 140 MB), the chain captured once in a HIP graph and replayed.
+    Reported per layer; tok/s = 1 / (time of one layer)."""
+    from ameva_compute_amd.llama import random_layer
+    layers_n = 4
+    layers = [random_layer(dev, seed=100 + i) for i in range(layers_n)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    for lay in layers:
+        lay.k_cache.copy_(torch.randn(lay.k_cache.shape, generator=g, device=dev).half())
+        lay.v_cache.copy_(torch.randn(lay.v_cache.shape, generator=g, device=dev).half())
+        lay.set_position(lay.ctx - 1)
+    xs = [torch.randn(4096, generator=g, device=dev)] + [torch.empty(4096, device=dev) for _ in range(layers_n)]
+
+    def chain():
+        for i, lay in enumerate(layers):
+            lay.decode(xs[i], xs[i + 1])
+
+    ms_eager = time_steps(torch, lambda i: chain(), 50, 5) / layers_n
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        chain()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain()
+    ms = time_steps(torch, lambda i: graph.replay(), 200, 20) / layers_n
+    nbytes = layers[0].step_bytes(layers[0].ctx)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"bench: layer decode {ms * 1e3:.2f} us/layer (graph), {ms_eager * 1e3:.2f} us eager; "
+        f"{nbytes / 1e6:.1f} MB -> {gbs:.0f} GB/s")
+    del layers, graph
+    torch.cuda.empty_cache()
+    return {"layer_decode_us": round(ms * 1e3, 3), "layer_decode_tok_s": round(1e3 / ms, 1),
+            "layer_decode_gbs": round(gbs, 1), "layer_decode_eager_us": round(ms_eager * 1e3, 3),
+            "layer_decode_bytes": nbytes,
+            "layer_decode_note": "Llama-3-8B layer, Q4_0, bs1, 4096 cached keys, 4 chained cold layers in one HIP graph"}
 
 
 def cpu_model() -> str:
@@ -148,34 +212,45 @@ def main():
     def step_hot(i):
         ops.mul_mat_q(ws[0], act, 1, out)
 
-    ms_cold = time_steps(torch, step_cold, args.steps, args.warmup)
+    ms_cold = time_steps_graph(torch, step_cold, args.steps, args.warmup)
     nbytes = gemv_bytes(N_ROWS, K)
     gbs = nbytes / (ms_cold * 1e-3) / 1e9
     log(f"bench: cold {ms_cold * 1e3:.2f} us/GEMV = {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
     extra = {}
     if not args.only_headline:
-        ms_hot = time_steps(torch, step_hot, args.steps, args.warmup)
+        ms_hot = time_steps_graph(torch, step_hot, args.steps, args.warmup)
         extra["hot_gbs"] = round(nbytes / (ms_hot * 1e-3) / 1e9, 1)
         extra["hot_us"] = round(ms_hot * 1e3, 3)
+        ms_eager = time_steps(torch, step_cold, 500, 50)
+        extra["cold_eager_launch_us"] = round(ms_eager * 1e3, 3)
+
+        act2 = torch.empty_like(act)
+        from ameva_compute_amd._lib import lib as _lib
 
         def step_quant(i):
-            ops.quantize_act(x, ops.Q8_0, ops.Q8_X86)
-        extra["q8_0_quantize_4096_us"] = round(time_steps(torch, step_quant, 500, 50) * 1e3, 3)
+            _lib().amv_quantize_act(ops.Q8_0, x.data_ptr(), 1, K, ops.Q8_X86, None, act2.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream)
+        extra["q8_0_quantize_4096_us"] = round(time_steps_graph(torch, step_quant, 500, 100) * 1e3, 3)
         del ws
         torch.cuda.empty_cache()
         # Q4_0 4096 x 4096 (BASELINE config 1 shape), cold over 32 copies (302 MB)
         ws1 = make_weights(ops, torch, 4096, K, 32, 99, dev, ops.Q4_0)
         out1 = torch.empty((1, 4096), dtype=torch.float32, device=dev)
-        ms1 = time_steps(torch, lambda i: ops.mul_mat_q(ws1[i % 32], act, 1, out1), 2000, 200)
+        ms1 = time_steps_graph(torch, lambda i: ops.mul_mat_q(ws1[i % 32], act, 1, out1), 2000, 200)
         extra["q4_0_4096x4096_cold_gbs"] = round(gemv_bytes(4096, K) / (ms1 * 1e-3) / 1e9, 1)
         del ws1
         torch.cuda.empty_cache()
         # Q8_0 14336 x 4096, cold over 10 copies (624 MB)
         ws8 = make_weights(ops, torch, N_ROWS, K, 10, 77, dev, ops.Q8_0)
-        ms8 = time_steps(torch, lambda i: ops.mul_mat_q(ws8[i % 10], act, 1, out), 1000, 100)
+        ms8 = time_steps_graph(torch, lambda i: ops.mul_mat_q(ws8[i % 10], act, 1, out), 1000, 100)
         extra["q8_0_14336x4096_cold_gbs"] = round(gemv_bytes(N_ROWS, K, 34) / (ms8 * 1e-3) / 1e9, 1)
         del ws8
         torch.cuda.empty_cache()
+
+    layer_info = None
+    if not args.only_headline:
+        layer_info = bench_layer(torch, dev, args)
+        extra.update(layer_info)
 
     result = {
         "metric": "Q4_0 GEMV GB/s (% HBM peak) + bs1 decode tok/s, Llama-8B-shape layer",
@@ -192,7 +267,7 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights quantized on the GPU (ggml Q4_0 rule), N(0,1) activation",
         "config": {"workload": "Q4_0 GEMV 14336x4096 M=1 (Llama-3-8B FFN gate/up), Q8_0 activation, cold: "
                                f"{COPIES} rotating weight copies ({COPIES * N_ROWS * K * 18 // 32 / 2**20:.0f} MiB)",
-                   "n_rows": N_ROWS, "k": K, "m": 1, "weight_copies": COPIES},
+                   "n_rows": N_ROWS, "k": K, "m": 1, "weight_copies": COPIES, "timing": f"HIP graph of {GRAPH_STEPS} GEMV launches, replayed"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic()},
         "extra": extra,
