@@ -23,6 +23,7 @@ SIGNATURES = {
     "amv_quantize_act": (I32, [I32, P, I64, I64, I32, P, P, P]),
     "amv_quantize_q4_0": (I32, [P, I64, I64, P, P]),
     "amv_mul_mat_vec": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
+    "amv_mul_mat_vec_ep": (I32, [I32, P, I64, I64, P, P, I32, P, P, P]),
     "amv_mul_mat_block_sums": (I32, [I32, P, I64, I64, P, I64, P, P]),
     "amv_quantize_k": (I32, [I32, P, I64, I64, P, P]),
     "amv_mul_mat_q": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
@@ -33,9 +34,10 @@ SIGNATURES = {
     "amv_i2s_gemv_sums": (I32, [P, I64, I64, P, I64, P, P]),
     "amv_rms_norm": (I32, [P, I64, I64, F32, P, P, P, P, I32, P]),
     "amv_rope": (I32, [P, P, P, I64, I64, I64, I32, I32, F32, F32, F32, P]),
+    "amv_rope_kv_store": (I32, [P, P, I64, I64, I64, I64, I32, I32, F32, F32, F32, P, P, I64, P, I64, P, P]),
     "amv_swiglu": (I32, [P, P, P, I64, P]),
     "amv_flash_attn_workspace_bytes": (I64, [I64, I64, I64, I64]),
-    "amv_flash_attn_decode": (I32, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I64, F32, P, I64, P]),
+    "amv_flash_attn_decode": (I32, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I64, F32, P, I64, P, I32, P]),
     "amv_binary": (I32, [I32, P, P, P, I64, I64, I64, P]),
     "amv_set_rows_f16": (I32, [P, I64, P, I64, I64, I64, P, I32, I64, P, P]),
     "amv_get_rows": (I32, [I32, P, I64, I64, P, I64, P, P, P]),

@@ -60,6 +60,9 @@ __device__ __forceinline__ uint16_t amv_f2h(float f) {
     if (rest > half || (rest == half && (h & 1u))) h += 1u;
     return (uint16_t)(sign | h);
 }
+// f32 -> fp16 -> f32 rounding of a value loaded from memory (v_cvt_f16_f32, round to nearest even): one instruction,
+// for rounding points of a computation (ggml's f16 q in flash attention); the stored scales above use amv_f2h.
+__device__ __forceinline__ float amv_round_f16(float x) { return (float)(_Float16)x; }
 __device__ __forceinline__ float amv_h2f(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
 }
@@ -67,10 +70,24 @@ __device__ __forceinline__ float amv_h2f(uint32_t h) {
 // signed 4x8-bit dot product with 32-bit accumulate (v_dot4_i32_i8)
 __device__ __forceinline__ int amv_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// wave64 butterfly sum: every lane ends with the total
+// Sum over the 16 lanes of each DPP row (lanes 16 r .. 16 r + 15), result in every lane of the row, with DPP row
+// permutations (VALU only, no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1] sum each quad, row_half_mirror
+// (lane i <-> 7 - i) pairs the two quads of each 8, row_mirror (i <-> 15 - i) the two halves of the row.
+#define AMV_DPP_ADD(v, ctrl) \
+    ((v) + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), 0xF, 0xF, false)))
+__device__ __forceinline__ float amv_row16_sum(float v) {
+    v = AMV_DPP_ADD(v, 0xB1);   // quad_perm [1,0,3,2]
+    v = AMV_DPP_ADD(v, 0x4E);   // quad_perm [2,3,0,1]
+    v = AMV_DPP_ADD(v, 0x141);  // row_half_mirror
+    v = AMV_DPP_ADD(v, 0x140);  // row_mirror
+    return v;
+}
+
+// wave64 sum: every lane ends with the total (DPP within rows, then two cross-row exchanges)
 __device__ __forceinline__ float amv_wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, AMV_WAVE);
+    v = amv_row16_sum(v);
+    v += __shfl_xor(v, 16, AMV_WAVE);
+    v += __shfl_xor(v, 32, AMV_WAVE);
     return v;
 }
 __device__ __forceinline__ int amv_wave_sum_i(int v) {
@@ -82,4 +99,27 @@ __device__ __forceinline__ float amv_wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, AMV_WAVE));
     return v;
+}
+
+// Q8_0 quantization of one 32-element block held one element per lane by 32 consecutive lanes of a wave (lane j of
+// the block holds element j): the rules of amv_quantize_act (ggml quantize_row_q8_0 x86 / ARM / ref). Every lane of
+// the 32 must call it. Writes the int8 of its element to qs[j]; lane j == 0 writes {fp16-rounded d, sum q} to *meta.
+__device__ __forceinline__ void amv_q8_0_lanes32(float v, int rule, int j, int8_t* __restrict__ qs,
+                                                 int2* __restrict__ meta) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, AMV_WAVE));
+    const float d = amax / 127.0f;
+    float id;
+    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float t = v * id;
+    float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+    qf = fminf(127.0f, fmaxf(-127.0f, qf));
+    const int q = (int)qf;
+    int s = q;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, AMV_WAVE);
+    qs[j] = (int8_t)q;
+    if (j == 0) *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
 }

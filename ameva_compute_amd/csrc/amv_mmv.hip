@@ -13,15 +13,62 @@
 
 #define M4 0x0F0F0F0Fu
 
-// ------------------------------------------------------------------------------------------------ Q4_0 x Q8_0
-template <int R, int U, bool BLOCK_SUMS>
+// Epilogues of the one-column GEMV, the reference's ameva_qmv / ameva_mmvq ep_mode (ameva_qmv.comp:233-246,
+// fusion pairs ggml-ameva.cpp:4280-4285). v_n is the row's dot product, e the epilogue operand, eout its output;
+// dst[n] = v_n is written too when dst is not NULL (the reference's write-through of the MUL_MAT node):
+//   EP 1 (MUL_MAT -> ADD):                   eout[n] = v_n + e[n]
+//   EP 2 (MUL_MAT -> SWIGLU, gate operand):  eout[n] = v_n / (1 + exp(-v_n)) * e[n]
+//   EP 3 (MUL_MAT -> SWIGLU, up operand):    eout[n] = e[n] / (1 + exp(-e[n])) * v_n
+//   EP 4 (MI355X, one weight of stacked gate rows 0..F-1 and up rows F..2F-1): wave w computes rows w and F + w and
+//        eout[w] = v_w / (1 + exp(-v_w)) * v_{F+w}; the gate and up MUL_MATs read the same activations, so one
+//        launch streams both weights.
+template <int EP>
+__device__ __forceinline__ int mmv_row(int wave, int r, int R, int n_rows) {
+    return EP == AMV_EP_SWIGLU_STACKED ? wave + r * (n_rows >> 1) : wave * R + r;
+}
+template <int EP>
+__device__ __forceinline__ bool mmv_wave_live(int wave, int R, int n_rows) {
+    return EP == AMV_EP_SWIGLU_STACKED ? wave < (n_rows >> 1) : wave * R < n_rows;
+}
+__device__ __forceinline__ float mmv_silu(float x) { return x / (1.0f + expf(-x)); }
+
+template <int R, int EP>
+__device__ __forceinline__ void mmv_epilogue(const float (&acc)[R], int lane, int wave, int n_rows,
+                                             float* __restrict__ dst, const float* __restrict__ epi,
+                                             float* __restrict__ eout) {
+    static_assert(EP != AMV_EP_SWIGLU_STACKED || R == 2, "the stacked SWIGLU pairs two rows per wave");
+    float t[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) t[r] = amv_wave_sum(acc[r]);
+    if (lane != 0) return;
+    if constexpr (EP == AMV_EP_SWIGLU_STACKED) {
+        if (dst) {
+            dst[wave] = t[0];
+            dst[wave + (n_rows >> 1)] = t[1];
+        }
+        eout[wave] = mmv_silu(t[0]) * t[1];
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = wave * R + r;
+        if (row >= n_rows) continue;
+        if (EP == AMV_EP_NONE || dst) dst[row] = t[r];
+        if (EP == AMV_EP_ADD) eout[row] = t[r] + epi[row];
+        if (EP == AMV_EP_SILU_MUL) eout[row] = mmv_silu(t[r]) * epi[row];
+        if (EP == AMV_EP_MUL_SILU) eout[row] = mmv_silu(epi[row]) * t[r];
+    }
+}
+
+template <int R, int U, bool BLOCK_SUMS, int EP>
 __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                  int n_rows, int nb, const int8_t* __restrict__ aq,
                                                  const int2* __restrict__ ads, float* __restrict__ dst,
-                                                 int32_t* __restrict__ sums) {
+                                                 int32_t* __restrict__ sums, const float* __restrict__ epi,
+                                                 float* __restrict__ eout) {
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
-    if (row0 >= n_rows) return;  // uniform per wave
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;  // uniform per wave
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
 #pragma unroll
@@ -35,7 +82,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
             const int j = min(j0 + 64 * u + lane, nb - 1);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const size_t bi = (size_t)min(row0 + r, n_rows - 1) * nb + j;
+                const size_t bi = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1) * nb + j;
                 w[u][r] = wq[bi];
                 dw[u][r] = wd[bi];
             }
@@ -60,7 +107,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
                     s = amv_dot4((int)((q.w >> 4) & M4), a1.w, s);
                     s -= 8 * ds.y;
                     if (BLOCK_SUMS) {
-                        if (row0 + r < n_rows) sums[(size_t)(row0 + r) * nb + j] = s;
+                        if (mmv_row<EP>(wave, r, R, n_rows) < n_rows) sums[(size_t)mmv_row<EP>(wave, r, R, n_rows) * nb + j] = s;
                     } else {
                         acc[r] = fmaf((float)s, amv_h2f(dw[u][r]) * da, acc[r]);
                     }
@@ -68,24 +115,19 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
             }
         }
     }
-    if (!BLOCK_SUMS) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float t = amv_wave_sum(acc[r]);
-            if (lane == 0 && row0 + r < n_rows) dst[row0 + r] = t;
-        }
-    }
+    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
 }
 
 // ------------------------------------------------------------------------------------------------ Q8_0 x Q8_0
-template <int R, int U, bool BLOCK_SUMS>
+template <int R, int U, bool BLOCK_SUMS, int EP>
 __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                  int n_rows, int nb, const int8_t* __restrict__ aq,
                                                  const int2* __restrict__ ads, float* __restrict__ dst,
-                                                 int32_t* __restrict__ sums) {
+                                                 int32_t* __restrict__ sums, const float* __restrict__ epi,
+                                                 float* __restrict__ eout) {
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
-    if (row0 >= n_rows) return;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;  // uniform per wave
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
 #pragma unroll
@@ -99,7 +141,7 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
             const int j = min(j0 + 64 * u + lane, nb - 1);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const size_t bi = (size_t)min(row0 + r, n_rows - 1) * nb + j;
+                const size_t bi = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1) * nb + j;
                 w0[u][r] = wq[2 * bi];
                 w1[u][r] = wq[2 * bi + 1];
                 dw[u][r] = wd[bi];
@@ -123,7 +165,7 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
                     s = amv_dot4((int)q.z, a1.z, s);
                     s = amv_dot4((int)q.w, a1.w, s);
                     if (BLOCK_SUMS) {
-                        if (row0 + r < n_rows) sums[(size_t)(row0 + r) * nb + j] = s;
+                        if (mmv_row<EP>(wave, r, R, n_rows) < n_rows) sums[(size_t)mmv_row<EP>(wave, r, R, n_rows) * nb + j] = s;
                     } else {
                         acc[r] = fmaf((float)s, amv_h2f(dw[u][r]) * da, acc[r]);
                     }
@@ -131,13 +173,7 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
             }
         }
     }
-    if (!BLOCK_SUMS) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float t = amv_wave_sum(acc[r]);
-            if (lane == 0 && row0 + r < n_rows) dst[row0 + r] = t;
-        }
-    }
+    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
 }
 
 // ------------------------------------------------------------------------------------------------ K-quants
@@ -173,14 +209,15 @@ __device__ __forceinline__ int dot16(uint4 w, int4 a, int acc) {
     return amv_dot4((int)w.w, a.w, acc);
 }
 
-template <int R, bool BLOCK_SUMS>
+template <int R, bool BLOCK_SUMS, int EP>
 __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, const uint4* __restrict__ wh,
                                                  int n_rows, int nsl, const int8_t* __restrict__ aq,
                                                  const float* __restrict__ ad, const int* __restrict__ abs16,
-                                                 float* __restrict__ dst, int32_t* __restrict__ sums) {
+                                                 float* __restrict__ dst, int32_t* __restrict__ sums, const float* __restrict__ epi,
+                                                 float* __restrict__ eout) {
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
-    if (row0 >= n_rows) return;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;
     const int nsb = nsl >> 3;
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
@@ -192,7 +229,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
         uint4 q[R], hd[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const size_t row = (size_t)min(row0 + r, n_rows - 1);
+            const size_t row = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
             q[r] = wq[row * nsl + j];
             hd[r] = wh[row * nsb + sb];
         }
@@ -214,9 +251,10 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
                     isum += __shfl_xor(isum, o, AMV_WAVE);
                     msum += __shfl_xor(msum, o, AMV_WAVE);
                 }
-                if (t == 0 && j0 + lane < nsl && row0 + r < n_rows) {
-                    sums[((size_t)(row0 + r) * nsb + sb) * 2] = isum;
-                    sums[((size_t)(row0 + r) * nsb + sb) * 2 + 1] = msum;
+                const int rr = mmv_row<EP>(wave, r, R, n_rows);
+                if (t == 0 && j0 + lane < nsl && rr < n_rows) {
+                    sums[((size_t)rr * nsb + sb) * 2] = isum;
+                    sums[((size_t)rr * nsb + sb) * 2 + 1] = msum;
                 }
             } else if (j0 + lane < nsl) {
                 const float d = amv_h2f(hd[r].x) * da, dmin = amv_h2f(hd[r].x >> 16) * da;
@@ -225,24 +263,19 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
             }
         }
     }
-    if (!BLOCK_SUMS) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float tt = amv_wave_sum(acc[r]);
-            if (lane == 0 && row0 + r < n_rows) dst[row0 + r] = tt;
-        }
-    }
+    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
 }
 
-template <int R, bool BLOCK_SUMS>
+template <int R, bool BLOCK_SUMS, int EP>
 __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, const uint4* __restrict__ wqh,
                                                  const uint4* __restrict__ wsc, const uint16_t* __restrict__ wd,
                                                  int n_rows, int nsl, const int8_t* __restrict__ aq,
                                                  const float* __restrict__ ad, const int* __restrict__ abs16,
-                                                 float* __restrict__ dst, int32_t* __restrict__ sums) {
+                                                 float* __restrict__ dst, int32_t* __restrict__ sums, const float* __restrict__ epi,
+                                                 float* __restrict__ eout) {
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
-    if (row0 >= n_rows) return;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;
     const int nsb = nsl >> 3;
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
@@ -257,8 +290,9 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
         uint16_t dd[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const size_t rb = (size_t)min(row0 + r, n_rows - 1) * nsb + sb;
-            ql[r] = wl[(size_t)min(row0 + r, n_rows - 1) * nsl + j];
+            const size_t rw = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
+            const size_t rb = rw * nsb + sb;
+            ql[r] = wl[rw * nsl + j];
             qh[r] = wqh[rb * 4 + 2 * hh + (lq >> 4)];
             sc[r] = wsc[rb];
             dd[r] = wd[rb];
@@ -287,19 +321,13 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
             if (BLOCK_SUMS) {
 #pragma unroll
                 for (int o = 1; o < 8; o <<= 1) isum += __shfl_xor(isum, o, AMV_WAVE);
-                if (t == 0 && j0 + lane < nsl && row0 + r < n_rows) sums[(size_t)(row0 + r) * nsb + sb] = isum;
+                if (t == 0 && j0 + lane < nsl && mmv_row<EP>(wave, r, R, n_rows) < n_rows) sums[(size_t)mmv_row<EP>(wave, r, R, n_rows) * nsb + sb] = isum;
             } else if (j0 + lane < nsl) {
                 acc[r] = fmaf(amv_h2f(dd[r]) * da, (float)isum, acc[r]);
             }
         }
     }
-    if (!BLOCK_SUMS) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float tt = amv_wave_sum(acc[r]);
-            if (lane == 0 && row0 + r < n_rows) dst[row0 + r] = tt;
-        }
-    }
+    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
@@ -312,9 +340,11 @@ struct MmvArgs {
     const void* ameta1;    // Q8_K: sums per 16
     float* dst;
     int32_t* sums;
+    const float* epi;      // epilogue operand
+    float* eout;           // epilogue output
 };
 
-template <int R, int U, bool S>
+template <int R, int U, bool S, int EP>
 static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
     const int64_t nblk = (int64_t)a.n_rows * nb;
@@ -322,12 +352,12 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 16);
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
-    const int waves = (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q4_0<R, U, S>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
-                       a.dst, a.sums);
+    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    hipLaunchKernelGGL((k_mmv_q4_0<R, U, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
+                       a.dst, a.sums, a.epi, a.eout);
 }
 
-template <int R, int U, bool S>
+template <int R, int U, bool S, int EP>
 static void launch_q8_0(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
     const int64_t nblk = (int64_t)a.n_rows * nb;
@@ -335,23 +365,23 @@ static void launch_q8_0(const MmvArgs& a, hipStream_t st) {
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 32);
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
-    const int waves = (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q8_0<R, U, S>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
-                       a.dst, a.sums);
+    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    hipLaunchKernelGGL((k_mmv_q8_0<R, U, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
+                       a.dst, a.sums, a.epi, a.eout);
 }
 
-template <int R, bool S>
+template <int R, bool S, int EP>
 static void launch_q4_K(const MmvArgs& a, hipStream_t st) {
     const int nsl = a.k / 32, nsb = a.k / 256;
     const int64_t nblk = (int64_t)a.n_rows * nsb;
     const uint4* wq = reinterpret_cast<const uint4*>(a.w);
     const uint4* wh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
-    const int waves = (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q4_K<R, S>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
-                       (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums);
+    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    hipLaunchKernelGGL((k_mmv_q4_K<R, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
+                       (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout);
 }
 
-template <int R, bool S>
+template <int R, bool S, int EP>
 static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
     const int nsl = a.k / 32, nsb = a.k / 256;
     const int64_t nblk = (int64_t)a.n_rows * nsb;
@@ -359,29 +389,33 @@ static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
     const uint4* wqh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
     const uint4* wsc = reinterpret_cast<const uint4*>(a.w + nblk * 192);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 208);
-    const int waves = (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q6_K<R, S>), dim3((waves + 3) / 4), dim3(256), 0, st, wl, wqh, wsc, wd, a.n_rows, nsl,
-                       a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums);
+    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    hipLaunchKernelGGL((k_mmv_q6_K<R, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wl, wqh, wsc, wd, a.n_rows, nsl,
+                       a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout);
 }
 
 // Kernel variant (rows per wave R, blocks-per-lane unroll U) chosen from the block count of a row; the table is the
-// result of the launch-shape sweep on MI355X (see the bench and profiles of this repository).
-template <bool S>
+// result of the launch-shape sweep on MI355X. The stacked SWIGLU epilogue pairs rows w and F + w, so it runs R = 2.
+template <bool S, int EP>
 static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
     switch (a.wtype) {
     case AMV_T_Q4_0:
         // R = 2 rows per wave, one 64-block step at a time: the fastest shape of the MI355X sweep at K = 4096
         // (7.44 us cold for 14336 x 4096 against 8.5 us for R = 4, 11.2 us for R = 8)
-        launch_q4_0<2, 1, S>(a, st);
+        launch_q4_0<2, 1, S, EP>(a, st);
         return AMV_OK;
     case AMV_T_Q8_0:
-        if (nb <= 64) launch_q8_0<4, 1, S>(a, st);
-        else if (nb <= 128) launch_q8_0<2, 2, S>(a, st);
-        else launch_q8_0<2, 2, S>(a, st);
+        if constexpr (EP != AMV_EP_SWIGLU_STACKED) {
+            if (nb <= 64) {
+                launch_q8_0<4, 1, S, EP>(a, st);
+                return AMV_OK;
+            }
+        }
+        launch_q8_0<2, 2, S, EP>(a, st);
         return AMV_OK;
-    case AMV_T_Q4_K: launch_q4_K<2, S>(a, st); return AMV_OK;
-    case AMV_T_Q6_K: launch_q6_K<2, S>(a, st); return AMV_OK;
+    case AMV_T_Q4_K: launch_q4_K<2, S, EP>(a, st); return AMV_OK;
+    case AMV_T_Q6_K: launch_q6_K<2, S, EP>(a, st); return AMV_OK;
     default: amv_set_error("amv_mul_mat_vec: weight type %d not supported", a.wtype); return AMV_ERR_UNSUPPORTED;
     }
 }
@@ -419,6 +453,32 @@ static void column_view(MmvArgs& a, const uint8_t* act, int64_t m, int64_t c) {
     }
 }
 
+extern "C" int amv_mul_mat_vec_ep(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst,
+                                  int ep_mode, const float* e, float* eout, void* stream) {
+    int rc = check_common("amv_mul_mat_vec_ep", wtype, w, n_rows, k, act, 1);
+    if (rc) return rc;
+    AMV_REQUIRE(ep_mode >= AMV_EP_NONE && ep_mode <= AMV_EP_SWIGLU_STACKED, "amv_mul_mat_vec_ep: ep_mode %d unknown",
+                ep_mode);
+    AMV_REQUIRE(ep_mode != AMV_EP_NONE || dst, "amv_mul_mat_vec_ep: null dst");
+    AMV_REQUIRE(ep_mode == AMV_EP_NONE || eout, "amv_mul_mat_vec_ep: null eout");
+    AMV_REQUIRE(ep_mode == AMV_EP_NONE || ep_mode == AMV_EP_SWIGLU_STACKED || e,
+                "amv_mul_mat_vec_ep: ep_mode %d needs its operand e", ep_mode);
+    AMV_REQUIRE(ep_mode != AMV_EP_SWIGLU_STACKED || n_rows % 2 == 0,
+                "amv_mul_mat_vec_ep: the stacked SWIGLU needs an even number of rows (gate rows, then up rows)");
+    MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, dst, nullptr, e, eout};
+    column_view(a, (const uint8_t*)act, 1, 0);
+    hipStream_t st = amv_stream(stream);
+    switch (ep_mode) {
+    case AMV_EP_ADD: rc = mmv_one_column<false, AMV_EP_ADD>(a, st); break;
+    case AMV_EP_SILU_MUL: rc = mmv_one_column<false, AMV_EP_SILU_MUL>(a, st); break;
+    case AMV_EP_MUL_SILU: rc = mmv_one_column<false, AMV_EP_MUL_SILU>(a, st); break;
+    case AMV_EP_SWIGLU_STACKED: rc = mmv_one_column<false, AMV_EP_SWIGLU_STACKED>(a, st); break;
+    default: rc = mmv_one_column<false, AMV_EP_NONE>(a, st); break;
+    }
+    if (rc) return rc;
+    return amv_check_launch("amv_mul_mat_vec_ep");
+}
+
 extern "C" int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m,
                                float* dst, int64_t ldd, void* stream) {
     int rc = check_common("amv_mul_mat_vec", wtype, w, n_rows, k, act, m);
@@ -427,9 +487,10 @@ extern "C" int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t
     AMV_REQUIRE(ldd >= n_rows, "amv_mul_mat_vec: ldd %lld < n_rows %lld", (long long)ldd, (long long)n_rows);
     hipStream_t st = amv_stream(stream);
     for (int64_t c = 0; c < m; ++c) {
-        MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, dst + c * ldd, nullptr};
+        MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, dst + c * ldd, nullptr,
+                  nullptr, nullptr};
         column_view(a, (const uint8_t*)act, m, c);
-        rc = mmv_one_column<false>(a, st);
+        rc = mmv_one_column<false, AMV_EP_NONE>(a, st);
         if (rc) return rc;
     }
     return amv_check_launch("amv_mul_mat_vec");
@@ -445,9 +506,9 @@ extern "C" int amv_mul_mat_block_sums(int wtype, const void* w, int64_t n_rows, 
     const int64_t nblk = (act_type_of(wtype) == AMV_T_Q8_0 ? k / 32 : k / 256) * per;
     for (int64_t c = 0; c < m; ++c) {
         MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, nullptr,
-                  sums + c * n_rows * nblk};
+                  sums + c * n_rows * nblk, nullptr, nullptr};
         column_view(a, (const uint8_t*)act, m, c);
-        rc = mmv_one_column<true>(a, st);
+        rc = mmv_one_column<true, AMV_EP_NONE>(a, st);
         if (rc) return rc;
     }
     return amv_check_launch("amv_mul_mat_block_sums");

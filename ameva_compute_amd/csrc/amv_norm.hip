@@ -39,17 +39,55 @@ __device__ __forceinline__ void q8_block(const float (&v)[32], int rule, int8_t*
     *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
 }
 
-// one workgroup of 256 per row
-__global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, int n, float eps,
-                                                 const float* __restrict__ w, float* __restrict__ y,
-                                                 float* __restrict__ o, int8_t* __restrict__ aq,
-                                                 int2* __restrict__ ameta, int rule) {
-    __shared__ double sred[4];
+// Q8_0 quantization of one 32-element block spread over 8 consecutive lanes (4 elements each, lane j of the 8 holds
+// elements 4j .. 4j + 3): the rules of amv_quantize_act. All 8 lanes must call it; stores 4 int8 per lane.
+__device__ __forceinline__ void q8_block_lanes8(const float (&v)[4], int rule, int j, int8_t* __restrict__ qs,
+                                                int2* __restrict__ meta) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, AMV_WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, AMV_WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, AMV_WAVE));
+    const float d = amax / 127.0f;
+    float id;
+    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t packed = 0;
+    int s = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float t = v[e] * id;
+        float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+        qf = fminf(127.0f, fmaxf(-127.0f, qf));
+        const int q = (int)qf;
+        s += q;
+        packed |= (uint32_t)(q & 0xFF) << (8 * e);
+    }
+    s += __shfl_xor(s, 1, AMV_WAVE);
+    s += __shfl_xor(s, 2, AMV_WAVE);
+    s += __shfl_xor(s, 4, AMV_WAVE);
+    reinterpret_cast<uint32_t*>(qs)[j] = packed;
+    if (j == 0) *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
+}
+
+// One workgroup of 1024 per row; thread t owns the float4 chunks t, t + 1024, ... (its first chunk stays in registers
+// between the two passes). With the fused quantization the 8 lanes of a 32-element block quantize it together.
+#define RMS_THREADS 1024
+__global__ __launch_bounds__(RMS_THREADS) void k_rms_norm(const float* __restrict__ x, int n, float eps,
+                                                         const float* __restrict__ w, float* __restrict__ y,
+                                                         float* __restrict__ o, int8_t* __restrict__ aq,
+                                                         int2* __restrict__ ameta, int rule) {
+    __shared__ double sred[RMS_THREADS / 64];
     const int row = blockIdx.x, tid = threadIdx.x;
-    const float* xr = x + (size_t)row * n;
-    const float4* x4 = reinterpret_cast<const float4*>(xr);
-    double s = 0.0;
-    for (int i = tid; i < n / 4; i += 256) {
+    const int n4 = n / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)row * n);
+    const bool to_o = (w != nullptr && o != nullptr);
+    const float4 v0 = tid < n4 ? x4[tid] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 w0 = (to_o && tid < n4) ? reinterpret_cast<const float4*>(w)[tid] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    double s = (double)(v0.x * v0.x);
+    s += (double)(v0.y * v0.y);
+    s += (double)(v0.z * v0.z);
+    s += (double)(v0.w * v0.w);
+    for (int i = tid + RMS_THREADS; i < n4; i += RMS_THREADS) {
         const float4 v = x4[i];
         s += (double)(v.x * v.x);
         s += (double)(v.y * v.y);
@@ -60,43 +98,27 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, i
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, AMV_WAVE);
     if ((tid & 63) == 0) sred[tid >> 6] = s;
     __syncthreads();
-    const double tot = (sred[0] + sred[1]) + (sred[2] + sred[3]);
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < RMS_THREADS / 64; ++i) tot += sred[i];
     const float mean = (float)(tot / (double)n);
     const float scale = 1.0f / sqrtf(mean + eps);
-    const bool to_o = (w != nullptr && o != nullptr);
-    if (aq == nullptr) {
-        for (int i = tid; i < n / 4; i += 256) {
-            const float4 v = x4[i];
-            const float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
-            if (y) reinterpret_cast<float4*>(y + (size_t)row * n)[i] = yv;
-            if (to_o) {
-                const float4 wv = reinterpret_cast<const float4*>(w)[i];
-                reinterpret_cast<float4*>(o + (size_t)row * n)[i] =
-                    make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
-            }
+    for (int i = tid; i < n4; i += RMS_THREADS) {
+        const float4 v = i == tid ? v0 : x4[i];
+        const float4 wv = !to_o ? make_float4(1.0f, 1.0f, 1.0f, 1.0f) : (i == tid ? w0 : reinterpret_cast<const float4*>(w)[i]);
+        const float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
+        if (y) reinterpret_cast<float4*>(y + (size_t)row * n)[i] = yv;
+        float4 qv = yv;
+        if (to_o) {
+            qv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
+            reinterpret_cast<float4*>(o + (size_t)row * n)[i] = qv;
         }
-        return;
-    }
-    // with the fused quantization a lane owns whole 32-element blocks
-    const int nb = n / 32;
-    for (int b = tid; b < nb; b += 256) {
-        float q[32];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 v = x4[8 * b + i];
-            float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
-            if (y) reinterpret_cast<float4*>(y + (size_t)row * n)[8 * b + i] = yv;
-            if (to_o) {
-                const float4 wv = reinterpret_cast<const float4*>(w)[8 * b + i];
-                yv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
-                reinterpret_cast<float4*>(o + (size_t)row * n)[8 * b + i] = yv;
-            }
-            q[4 * i] = yv.x;
-            q[4 * i + 1] = yv.y;
-            q[4 * i + 2] = yv.z;
-            q[4 * i + 3] = yv.w;
+        if (aq) {
+            // n % 32 == 0 and the 8 chunks of a block are lanes 8 b .. 8 b + 7 of one wave (1024 is a multiple of 8)
+            const float vals[4] = {qv.x, qv.y, qv.z, qv.w};
+            q8_block_lanes8(vals, rule, i & 7, aq + (size_t)row * n + 32 * (i >> 3),
+                            ameta + (size_t)row * (n / 32) + (i >> 3));
         }
-        q8_block(q, rule, aq + (size_t)row * n + 32 * b, ameta + (size_t)row * nb + b);
     }
 }
 
@@ -121,8 +143,8 @@ extern "C" int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps
         amv_set_error("amv_rms_norm: the fused quantization of y * w needs o");
         return AMV_ERR_INVALID_ARG;
     }
-    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(256), 0, amv_stream(stream), x, (int)n, eps, wq, y, oo,
-                       aq, ameta, rule);
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0, amv_stream(stream), x, (int)n, eps, wq,
+                       y, oo, aq, ameta, rule);
     return amv_check_launch("amv_rms_norm");
 }
 
@@ -171,6 +193,75 @@ extern "C" int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_
     hipLaunchKernelGGL(k_rope, dim3((unsigned)((n_pairs + 255) / 256)), dim3(256), 0, amv_stream(stream), x, y, pos,
                        n_pairs, (int)n_head, (int)ne0, n_dims, mode == 2 ? 1 : 0, theta_scale, freq_scale, attn_factor);
     return amv_check_launch("amv_rope");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// ROPE of q and k + SET_ROWS of k and v into the f16 cache, one launch per decode step. Token t's row of qkv holds
+// n_head q heads, n_head_kv k heads and n_head_kv v heads of D floats. Block (head, t), one wave: q and k heads are
+// rotated in place (k_rope's arithmetic, so the values equal ROPE's), k and v heads are also stored as f16 (amv_f2h,
+// round to nearest even as the CPU's fp32 -> fp16) at row kv_idx[t] of the caches; rows outside [0, cache_rows) are
+// skipped and counted in *bad.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_rope_kv(float* __restrict__ qkv, const int32_t* __restrict__ pos, int n_head,
+                                                int n_head_kv, int D, int n_dims, int neox, float theta_scale,
+                                                float freq_scale, float attn_factor, uint16_t* __restrict__ kc,
+                                                uint16_t* __restrict__ vc, int64_t cache_row,
+                                                const int64_t* __restrict__ kv_idx, int64_t cache_rows,
+                                                unsigned int* __restrict__ bad) {
+    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int n_all = n_head + 2 * n_head_kv;
+    float* xr = qkv + ((int64_t)t * n_all + h) * D;
+    const bool is_q = h < n_head, is_v = h >= n_head + n_head_kv;
+    const int64_t dr = is_q ? 0 : kv_idx[t];
+    const bool store = !is_q && dr >= 0 && dr < cache_rows;
+    if (!is_q && !store && lane == 0 && bad) atomicAdd(bad, 1u);
+    uint16_t* cr = nullptr;
+    if (store) cr = (is_v ? vc + (int64_t)(h - n_head - n_head_kv) * D : kc + (int64_t)(h - n_head) * D) + dr * cache_row;
+    if (is_v) {
+        if (store)
+            for (int e = lane; e < D; e += 64) cr[e] = amv_f2h(xr[e]);
+        return;
+    }
+    const float p = (float)pos[t];
+    for (int j = lane; j < D / 2; j += 64) {
+        const int e0 = 2 * j >= n_dims ? 2 * j : (neox ? j : 2 * j);
+        const int e1 = 2 * j >= n_dims ? 2 * j + 1 : (neox ? j + n_dims / 2 : 2 * j + 1);
+        const float x0 = xr[e0], x1 = xr[e1];
+        float y0 = x0, y1 = x1;
+        if (2 * j < n_dims) {
+            float theta = p;
+            for (int k = 0; k < j; ++k) theta *= theta_scale;
+            const float ang = freq_scale * theta;
+            const float c = cosf(ang) * attn_factor, s = sinf(ang) * attn_factor;
+            y0 = x0 * c - x1 * s;
+            y1 = x0 * s + x1 * c;
+        }
+        xr[e0] = y0;
+        xr[e1] = y1;
+        if (store) {
+            cr[e0] = amv_f2h(y0);
+            cr[e1] = amv_f2h(y1);
+        }
+    }
+}
+
+extern "C" int amv_rope_kv_store(float* qkv, const int32_t* pos, int64_t n_tok, int64_t n_head, int64_t n_head_kv,
+                                 int64_t D, int n_dims, int mode, float freq_base, float freq_scale, float attn_factor,
+                                 void* k_cache, void* v_cache, int64_t cache_row, const int64_t* kv_idx,
+                                 int64_t cache_rows, unsigned int* bad, void* stream) {
+    AMV_REQUIRE(qkv && pos && k_cache && v_cache && kv_idx, "amv_rope_kv_store: null pointer");
+    AMV_REQUIRE(n_tok > 0 && n_tok <= 65535 && n_head > 0 && n_head_kv > 0 && D > 0 && D % 2 == 0,
+                "amv_rope_kv_store: bad shape");
+    AMV_REQUIRE(n_dims > 0 && n_dims <= D && n_dims % 2 == 0, "amv_rope_kv_store: bad n_dims %d", n_dims);
+    AMV_REQUIRE(mode == 0 || mode == 2, "amv_rope_kv_store: mode %d not supported (NORMAL 0 and NEOX 2 are)", mode);
+    AMV_REQUIRE(cache_row >= n_head_kv * D && cache_rows > 0, "amv_rope_kv_store: cache row %lld < %lld",
+                (long long)cache_row, (long long)(n_head_kv * D));
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)(n_head + 2 * n_head_kv), (unsigned)n_tok), dim3(64), 0,
+                       amv_stream(stream), qkv, pos, (int)n_head, (int)n_head_kv, (int)D, n_dims, mode == 2 ? 1 : 0,
+                       theta_scale, freq_scale, attn_factor, (uint16_t*)k_cache, (uint16_t*)v_cache, cache_row,
+                       kv_idx, cache_rows, bad);
+    return amv_check_launch("amv_rope_kv_store");
 }
 
 // ---------------------------------------------------------------------------------------------------------------

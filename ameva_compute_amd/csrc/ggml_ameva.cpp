@@ -538,7 +538,7 @@ struct Engine {
         return rc(n, amv_flash_attn_decode((const float*)q->data, k->data, v->data, m ? m->data : nullptr,
                                            (float*)n->data, n_head, n_head_kv, n_kv, D, (int64_t)k->nb[1] / 2,
                                            (int64_t)k->nb[2] / 2, (int64_t)v->nb[1] / 2, (int64_t)v->nb[2] / 2,
-                                           op_f32(n, 0), work, ws, st));
+                                           op_f32(n, 0), work, ws, nullptr, AMV_Q8_X86, st));
     }
 
     bool glu(const ggml_tensor* n) {

@@ -5,8 +5,9 @@ MUL_MAT gate/up, SWIGLU, MUL_MAT down, ADD).
 
 MI355X-specific choices: q/k/v and gate/up are each one weight of stacked rows (one GEMV launch instead of three /
 two; the rows are independent, so the outputs equal the separate MUL_MATs), the Q8_0 quantization of each GEMV input
-is fused into the RMS_NORM kernel, and RoPE of q and k is one launch over the 40 contiguous heads. Every buffer is
-allocated up front, so a decode step launches kernels only and can be captured in a HIP graph.
+is fused into the kernel that produces it (RMS_NORM, the attention combine), the residual ADDs and the SWIGLU are
+GEMV epilogues, and RoPE of q and k is one launch with the KV-cache stores. Every buffer is allocated up front, so a
+decode step launches kernels only and can be captured in a HIP graph.
 """
 from __future__ import annotations
 
@@ -64,9 +65,13 @@ class LlamaLayer:
         self.kv_idx.fill_(pos)
         self.n_kv = pos + 1
 
-    def decode(self, x: torch.Tensor, out: torch.Tensor) -> None:
+    def decode(self, x: torch.Tensor, out: torch.Tensor, fused: bool = True) -> None:
         """x f32 [H] -> out f32 [H] for the token at the position of set_position(); writes K/V into the cache.
-        The number of cached keys is fixed at n_kv for the launch (graph replays reuse it)."""
+        The number of cached keys is fixed at n_kv for the launch (graph replays reuse it).
+
+        fused=True runs 10 launches: RMS_NORM+MUL+Q8_0, q/k/v GEMV, ROPE+SET_ROWS, FA split, FA combine+Q8_0,
+        o GEMV+ADD, RMS_NORM+MUL+Q8_0, gate/up GEMV+SWIGLU, Q8_0, down GEMV+ADD. fused=False runs the same
+        arithmetic as one launch per graph node (16 launches); the results are identical."""
         L, st = lib(), torch.cuda.current_stream().cuda_stream
         H, kv, D = self.H, self.kv, self.D
         n_kv = self.n_kv
@@ -76,36 +81,56 @@ class LlamaLayer:
         check(L.amv_mul_mat_vec(self.wqkv.type, self.wqkv.data.data_ptr(),
                                 self.wqkv.n_rows, H, self.act_h.data_ptr(), 1, self.qkv.data_ptr(), self.wqkv.n_rows,
                                 st), "qkv")
-        # RoPE of q and k: 40 contiguous heads of the qkv output, in place
-        check(L.amv_rope(self.qkv.data_ptr(), self.qkv.data_ptr(), self.pos.data_ptr(), 1,
-                         self.n_head + self.n_head_kv, D, D, 0, self.base, 1.0, 1.0, st), "rope")
-        kp = self.qkv.data_ptr() + H * 4
-        vp = kp + kv * 4
-        check(L.amv_set_rows_f16(kp, kv, self.k_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64, self.ctx,
-                                 None, st), "set_rows k")
-        check(L.amv_set_rows_f16(vp, kv, self.v_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64, self.ctx,
-                                 None, st), "set_rows v")
+        if fused:
+            check(L.amv_rope_kv_store(self.qkv.data_ptr(), self.pos.data_ptr(), 1, self.n_head, self.n_head_kv, D, D,
+                                      0, self.base, 1.0, 1.0, self.k_cache.data_ptr(), self.v_cache.data_ptr(), kv,
+                                      self.kv_idx.data_ptr(), self.ctx, None, st), "rope + kv store")
+        else:
+            # RoPE of q and k: 40 contiguous heads of the qkv output, in place
+            check(L.amv_rope(self.qkv.data_ptr(), self.qkv.data_ptr(), self.pos.data_ptr(), 1,
+                             self.n_head + self.n_head_kv, D, D, 0, self.base, 1.0, 1.0, st), "rope")
+            kp = self.qkv.data_ptr() + H * 4
+            vp = kp + kv * 4
+            check(L.amv_set_rows_f16(kp, kv, self.k_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64,
+                                     self.ctx, None, st), "set_rows k")
+            check(L.amv_set_rows_f16(vp, kv, self.v_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64,
+                                     self.ctx, None, st), "set_rows v")
         ws = self.fa_ws.numel()
         check(L.amv_flash_attn_decode(self.qkv.data_ptr(), self.k_cache.data_ptr(), self.v_cache.data_ptr(), None,
                                       self.att.data_ptr(), self.n_head, self.n_head_kv, n_kv, D, kv, D, kv, D,
-                                      1.0 / (D ** 0.5), self.fa_ws.data_ptr(), ws, st), "flash_attn")
-        check(L.amv_quantize_act(ops.Q8_0, self.att.data_ptr(), 1, H, ops.Q8_X86, None, self.act_att.data_ptr(), st),
-              "quant att")
-        check(L.amv_mul_mat_vec(self.wo.type, self.wo.data.data_ptr(), H, H, self.act_att.data_ptr(), 1,
-                                self.proj.data_ptr(), H, st), "wo")
-        check(L.amv_binary(0, self.proj.data_ptr(), x.data_ptr(), self.x1.data_ptr(), 1, H, 1, st), "residual 1")
+                                      1.0 / (D ** 0.5), self.fa_ws.data_ptr(), ws, self.act_att.data_ptr(), ops.Q8_X86,
+                                      st), "flash_attn (+ Q8_0 of its output)")
+        if fused:
+            check(L.amv_mul_mat_vec_ep(self.wo.type, self.wo.data.data_ptr(), H, H, self.act_att.data_ptr(),
+                                       self.proj.data_ptr(), ops.EP_ADD, x.data_ptr(), self.x1.data_ptr(), st),
+                  "wo + residual")
+        else:
+            check(L.amv_mul_mat_vec(self.wo.type, self.wo.data.data_ptr(), H, H, self.act_att.data_ptr(), 1,
+                                    self.proj.data_ptr(), H, st), "wo")
+            check(L.amv_binary(0, self.proj.data_ptr(), x.data_ptr(), self.x1.data_ptr(), 1, H, 1, st), "residual 1")
         # FFN block
         check(L.amv_rms_norm(self.x1.data_ptr(), 1, H, self.eps, self.ffn_norm.data_ptr(), self.t_norm.data_ptr(),
                              self.t_o2.data_ptr(), self.act_h2.data_ptr(), ops.Q8_X86, st), "ffn norm")
-        check(L.amv_mul_mat_vec(self.wgu.type, self.wgu.data.data_ptr(), self.wgu.n_rows, H, self.act_h2.data_ptr(), 1,
-                                self.gu.data_ptr(), self.wgu.n_rows, st), "gate_up")
-        check(L.amv_swiglu(self.gu.data_ptr(), self.gu.data_ptr() + self.FF * 4, self.h.data_ptr(), self.FF, st),
-              "swiglu")
+        if fused:
+            check(L.amv_mul_mat_vec_ep(self.wgu.type, self.wgu.data.data_ptr(), self.wgu.n_rows, H,
+                                       self.act_h2.data_ptr(), self.gu.data_ptr(), ops.EP_SWIGLU_STACKED, None,
+                                       self.h.data_ptr(), st), "gate_up + swiglu")
+        else:
+            check(L.amv_mul_mat_vec(self.wgu.type, self.wgu.data.data_ptr(), self.wgu.n_rows, H,
+                                    self.act_h2.data_ptr(), 1, self.gu.data_ptr(), self.wgu.n_rows, st), "gate_up")
+            check(L.amv_swiglu(self.gu.data_ptr(), self.gu.data_ptr() + self.FF * 4, self.h.data_ptr(), self.FF, st),
+                  "swiglu")
         check(L.amv_quantize_act(ops.Q8_0, self.h.data_ptr(), 1, self.FF, ops.Q8_X86, None, self.act_ff.data_ptr(),
                                  st), "quant ffn")
-        check(L.amv_mul_mat_vec(self.wdown.type, self.wdown.data.data_ptr(), H, self.FF, self.act_ff.data_ptr(), 1,
-                                self.down.data_ptr(), H, st), "down")
-        check(L.amv_binary(0, self.down.data_ptr(), self.x1.data_ptr(), out.data_ptr(), 1, H, 1, st), "residual 2")
+        if fused:
+            check(L.amv_mul_mat_vec_ep(self.wdown.type, self.wdown.data.data_ptr(), H, self.FF,
+                                       self.act_ff.data_ptr(), self.down.data_ptr(), ops.EP_ADD, self.x1.data_ptr(),
+                                       out.data_ptr(), st), "down + residual")
+        else:
+            check(L.amv_mul_mat_vec(self.wdown.type, self.wdown.data.data_ptr(), H, self.FF, self.act_ff.data_ptr(),
+                                    1, self.down.data_ptr(), H, st), "down")
+            check(L.amv_binary(0, self.down.data_ptr(), self.x1.data_ptr(), out.data_ptr(), 1, H, 1, st),
+                  "residual 2")
 
     # algorithmic HBM bytes of one decode step at n_kv cached keys (weights + KV read + norms)
     def step_bytes(self, n_kv: int) -> int:

@@ -122,6 +122,28 @@ def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = 
     return out
 
 
+# GEMV epilogue modes (amv_mul_mat_vec_ep)
+EP_NONE, EP_ADD, EP_SILU_MUL, EP_MUL_SILU, EP_SWIGLU_STACKED = 0, 1, 2, 3, 4
+
+
+def mul_mat_vec_ep(w: QWeight, act: torch.Tensor, ep_mode: int, e: torch.Tensor | None = None,
+                   write_dst: bool = True) -> tuple[torch.Tensor | None, torch.Tensor]:
+    """One activation column through the GEMV with a fused epilogue: returns (dst, eout); dst (the MUL_MAT value,
+    n_rows floats) is None when write_dst is False. eout has n_rows floats, n_rows / 2 for EP_SWIGLU_STACKED; with
+    EP_NONE it is dst."""
+    _need_gpu(act, "mul_mat_vec_ep")
+    if e is not None and (e.dtype != torch.float32 or not e.is_contiguous() or e.numel() != w.n_rows):
+        raise ValueError("mul_mat_vec_ep: e must be contiguous f32 with n_rows elements")
+    f32 = dict(dtype=torch.float32, device=act.device)
+    dst = torch.empty(w.n_rows, **f32) if write_dst or ep_mode == EP_NONE else None
+    eout = None
+    if ep_mode != EP_NONE:
+        eout = torch.empty(w.n_rows // 2 if ep_mode == EP_SWIGLU_STACKED else w.n_rows, **f32)
+    check(lib().amv_mul_mat_vec_ep(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), _ptr(dst), ep_mode,
+                                   _ptr(e), _ptr(eout), _stream()), "amv_mul_mat_vec_ep")
+    return dst, (dst if eout is None else eout)
+
+
 def mul_mat(w: QWeight, x: torch.Tensor, rule: int = Q8_X86) -> torch.Tensor:
     """ggml_mul_mat(src0 = w, src1 = x): x f32 [m, k] -> [m, n_rows]; activations quantized to vec_dot_type."""
     x2 = x.reshape(-1, x.shape[-1])
@@ -215,6 +237,24 @@ def rope(x: torch.Tensor, pos: torch.Tensor, n_dims: int, mode: int = 0, freq_ba
     return y
 
 
+def rope_kv_store(qkv: torch.Tensor, pos: torch.Tensor, n_head: int, n_head_kv: int, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, kv_idx: torch.Tensor, n_dims: int | None = None, mode: int = 0,
+                  freq_base: float = 10000.0, freq_scale: float = 1.0, attn_factor: float = 1.0,
+                  bad: torch.Tensor | None = None) -> None:
+    """ROPE of the q and k heads of qkv f32 [n_tok, n_head + 2 n_head_kv, D] in place, and the rotated k / the v heads
+    stored as f16 at rows kv_idx (int64 [n_tok]) of k_cache / v_cache ([rows, n_head_kv * D] f16)."""
+    _need_gpu(qkv, "rope_kv_store")
+    n_tok, n_all, D = qkv.shape
+    if n_all != n_head + 2 * n_head_kv or kv_idx.dtype != torch.int64 or pos.dtype != torch.int32:
+        raise ValueError("rope_kv_store: bad operands")
+    if k_cache.dtype != torch.float16 or v_cache.dtype != torch.float16 or k_cache.stride(0) != v_cache.stride(0):
+        raise ValueError("rope_kv_store: caches must be f16 with the same row stride")
+    check(lib().amv_rope_kv_store(qkv.data_ptr(), pos.data_ptr(), n_tok, n_head, n_head_kv, D,
+                                  D if n_dims is None else n_dims, mode, freq_base, freq_scale, attn_factor,
+                                  k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), kv_idx.data_ptr(),
+                                  k_cache.shape[0], _ptr(bad), _stream()), "amv_rope_kv_store")
+
+
 def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     _need_gpu(g, "swiglu")
     y = torch.empty_like(g)
@@ -224,9 +264,11 @@ def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
 
 # ------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
 def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, n_kv: int | None = None,
-                      mask: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                      mask: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                      act: torch.Tensor | None = None, rule: int = Q8_X86) -> torch.Tensor:
     """q f32 [n_head, D]; k, v f16 views [n_head_kv, n_keys, D] with any strides (a head-major cache, or llama.cpp's
-    token-major one as k_cache[:, :n_kv].permute(1, 0, 2)); the first n_kv keys are used; mask f16 [n_kv] or None."""
+    token-major one as k_cache[:, :n_kv].permute(1, 0, 2)); the first n_kv keys are used; mask f16 [n_kv] or None.
+    act: optional buffer (amv_act_bytes(Q8_0, 1, n_head * D)) that also receives the output quantized to Q8_0."""
     _need_gpu(q, "flash_attn_decode")
     n_head, D = q.shape
     n_head_kv, n_keys, _ = k.shape
@@ -241,7 +283,7 @@ def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
     out = torch.empty_like(q)
     check(lib().amv_flash_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(mask), out.data_ptr(), n_head,
                                       n_head_kv, n_kv, D, k.stride(1), k.stride(0), v.stride(1), v.stride(0), scale,
-                                      workspace.data_ptr(), need, _stream()), "amv_flash_attn_decode")
+                                      workspace.data_ptr(), need, _ptr(act), rule, _stream()), "amv_flash_attn_decode")
     return out
 
 

@@ -131,29 +131,36 @@ def bench_layer(torch, dev, args):
         lay.set_position(lay.ctx - 1)
     xs = [torch.randn(4096, generator=g, device=dev)] + [torch.empty(4096, device=dev) for _ in range(layers_n)]
 
-    def chain():
+    def chain(fused=True):
         for i, lay in enumerate(layers):
-            lay.decode(xs[i], xs[i + 1])
+            lay.decode(xs[i], xs[i + 1], fused=fused)
+
+    def graph_ms(fused):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            chain(fused)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            chain(fused)
+        t = time_steps(torch, lambda i: graph.replay(), 200, 20) / layers_n
+        del graph
+        return t
 
     ms_eager = time_steps(torch, lambda i: chain(), 50, 5) / layers_n
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        chain()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        chain()
-    ms = time_steps(torch, lambda i: graph.replay(), 200, 20) / layers_n
+    ms_unfused = graph_ms(False)
+    ms = graph_ms(True)
     nbytes = layers[0].step_bytes(layers[0].ctx)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"bench: layer decode {ms * 1e3:.2f} us/layer (graph), {ms_eager * 1e3:.2f} us eager; "
-        f"{nbytes / 1e6:.1f} MB -> {gbs:.0f} GB/s")
-    del layers, graph
+    log(f"bench: layer decode {ms * 1e3:.2f} us/layer (graph, 10 launches), {ms_unfused * 1e3:.2f} us unfused "
+        f"(16 launches), {ms_eager * 1e3:.2f} us eager; {nbytes / 1e6:.1f} MB -> {gbs:.0f} GB/s")
+    del layers
     torch.cuda.empty_cache()
     return {"layer_decode_us": round(ms * 1e3, 3), "layer_decode_tok_s": round(1e3 / ms, 1),
             "layer_decode_gbs": round(gbs, 1), "layer_decode_eager_us": round(ms_eager * 1e3, 3),
+            "layer_decode_unfused_us": round(ms_unfused * 1e3, 3),
             "layer_decode_bytes": nbytes,
             "layer_decode_note": "Llama-3-8B layer, Q4_0, bs1, 4096 cached keys, 4 chained cold layers in one HIP graph"}
 

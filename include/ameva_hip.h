@@ -80,6 +80,25 @@ int amv_quantize_q4_0(const float* x, int64_t n_rows, int64_t k, void* y_ggml, v
 int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                     int64_t ldd, void* stream);
 
+/* One-column GEMV with the fused epilogue of the next graph node: the reference's ameva_qmv / ameva_mmvq ep_mode
+ * (ameva_qmv.comp:233-246) chosen by ameva_find_fusion (ggml-ameva.cpp:4280-4285, 4355-4375). v[n] is the dot
+ * product of row n, e the epilogue operand (f32 [n_rows]), eout the epilogue output; dst[n] = v[n] is written as
+ * well when dst is not NULL (the MUL_MAT node's own value, the reference's write-through).
+ *   AMV_EP_NONE:     dst[n] = v[n]                                     (dst required)
+ *   AMV_EP_ADD:      eout[n] = v[n] + e[n]                             (MUL_MAT -> ADD: bias, residual)
+ *   AMV_EP_SILU_MUL: eout[n] = v[n] / (1 + exp(-v[n])) * e[n]          (MUL_MAT -> SWIGLU, as its gate operand)
+ *   AMV_EP_MUL_SILU: eout[n] = e[n] / (1 + exp(-e[n])) * v[n]          (MUL_MAT -> SWIGLU, as its up operand)
+ *   AMV_EP_SWIGLU_STACKED (no counterpart in the reference): w holds the F gate rows then the F up rows
+ *     (n_rows = 2 F) and eout[i] = silu(v[i]) * v[F + i] for i < F, e unused; dst, when given, gets all 2 F values.
+ * eout must not overlap act, w or e. */
+#define AMV_EP_NONE 0
+#define AMV_EP_ADD 1
+#define AMV_EP_SILU_MUL 2
+#define AMV_EP_MUL_SILU 3
+#define AMV_EP_SWIGLU_STACKED 4
+int amv_mul_mat_vec_ep(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst, int ep_mode,
+                       const float* e, float* eout, void* stream);
+
 /* Parity instrumentation of the same kernels: the exact integer sums per weight block, int32
  * [m][n_rows][nblk * per] with nblk = k / block size, per = 2 for Q4_K (sum sc*dot, sum m*bsum) and 1 otherwise.
  * These are the per-block int32 sums of ggml's vec_dot (bit-exact contract). */
@@ -131,6 +150,17 @@ int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps, const flo
 int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_tok, int64_t n_head, int64_t ne0, int n_dims,
              int mode, float freq_base, float freq_scale, float attn_factor, void* stream);
 
+/* ROPE of q and k followed by the two SET_ROWS of the KV cache, in one launch (no counterpart in the reference, which
+ * records ROPE enc_rope ggml-ameva.cpp:3965 and SET_ROWS ameva_set_rows.comp as separate nodes; values are those of
+ * amv_rope then amv_set_rows_f16). qkv f32 [n_tok][n_head + 2 n_head_kv][D]: q heads, k heads, v heads of each token.
+ * q and k heads are rotated in place (pos int32 [n_tok]); the rotated k heads and the v heads are stored as f16 at row
+ * kv_idx[t] (int64) of k_cache / v_cache (row stride cache_row elements, head h at h * D, cache_rows rows). Rows
+ * outside the cache are skipped and counted in *bad (device, may be NULL). */
+int amv_rope_kv_store(float* qkv, const int32_t* pos, int64_t n_tok, int64_t n_head, int64_t n_head_kv, int64_t D,
+                      int n_dims, int mode, float freq_base, float freq_scale, float attn_factor, void* k_cache,
+                      void* v_cache, int64_t cache_row, const int64_t* kv_idx, int64_t cache_rows, unsigned int* bad,
+                      void* stream);
+
 /* GLU SWIGLU (ggml_vec_swiglu_f32; enc_glu, ameva_glu.comp:45-46): y = silu(g) * u. */
 int amv_swiglu(const float* g, const float* u, float* y, int64_t n, void* stream);
 
@@ -142,11 +172,14 @@ int amv_swiglu(const float* g, const float* u, float* y, int64_t n, void* stream
  *   and nb[2] / 2: llama.cpp's cache view has k_row = n_head_kv * D, k_head = D); the first n_kv keys are used.
  *   mask f16 [n_kv] or NULL (added to the scaled scores; -inf masks a key).
  *   workspace: amv_flash_attn_workspace_bytes() bytes of device memory for the split partials.
+ *   act (may be NULL): the output also quantized to the Q8_0 activation layout of amv_quantize_act (one row of
+ *   n_head * D) with `rule` -- the input of the attention output projection, without a separate pass.
  * ---------------------------------------------------------------------------------------------------------- */
 int64_t amv_flash_attn_workspace_bytes(int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D);
 int amv_flash_attn_decode(const float* q, const void* k, const void* v, const void* mask, float* out, int64_t n_head,
                           int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row, int64_t k_head, int64_t v_row,
-                          int64_t v_head, float scale, void* workspace, int64_t workspace_bytes, void* stream);
+                          int64_t v_head, float scale, void* workspace, int64_t workspace_bytes, void* act, int rule,
+                          void* stream);
 
 /* ------------------------------------------------------------------------------------------------------------
  * Glue ops of the decoder graph (ameva_binary.comp, ameva_cpy.comp, ameva_set_rows.comp, ameva_get_rows(_q).comp).

@@ -48,6 +48,11 @@ def test_layer_decode_vs_oracle_and_graph_replay(dev, orc):
     layer.decode(xg, out)
     torch.cuda.synchronize()
     y = out.cpu().numpy()
+    # the fused launches (RoPE + KV store, GEMV epilogues) compute exactly what one launch per graph node computes
+    out_u = torch.empty_like(out)
+    layer.decode(xg, out_u, fused=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_u, out)
 
     q8 = lambda a: orc.quantize_q8_0(a.reshape(1, -1), orc.Q8_X86)  # noqa: E731
     def mm(name, a):

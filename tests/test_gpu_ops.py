@@ -209,6 +209,22 @@ def test_flash_attn_decode(dev, ops, orc, n_head, n_head_kv, n_kv, stride):
     assert np.array_equal(out_t, out)
 
 
+def test_flash_attn_decode_fused_quant(dev, ops, orc):
+    """The Q8_0 output of the combine equals ggml's quantize_row_q8_0 of the attention output, byte for byte."""
+    rng = np.random.default_rng(8)
+    n_head, n_head_kv, n_kv, D = 32, 8, 777, 128
+    q = rng.standard_normal((n_head, D)).astype(np.float32)
+    k = rng.standard_normal((n_head_kv, n_kv, D)).astype(np.float16)
+    v = rng.standard_normal((n_head_kv, n_kv, D)).astype(np.float16)
+    act = torch.empty(ops.lib().amv_act_bytes(ops.Q8_0, 1, n_head * D), dtype=torch.uint8, device=dev)
+    out = ops.flash_attn_decode(gpu(q, dev), gpu(k, dev), gpu(v, dev), 0.0884, act=act).cpu().numpy()
+    ref = orc.quantize_q8_0(out.reshape(1, -1), orc.Q8_X86).reshape(-1, 34)
+    a = act.cpu().numpy()
+    assert np.array_equal(a[: n_head * D].view(np.int8).reshape(-1, 32), ref[:, 2:].view(np.int8))
+    d16 = orc.fp16_to_fp32(ref[:, 0].astype(np.uint16) | (ref[:, 1].astype(np.uint16) << 8))
+    assert np.array_equal(a[n_head * D:].view(np.int32).reshape(-1, 2)[:, 0].view(np.float32), d16)
+
+
 def test_flash_attn_decode_mask(dev, ops, orc):
     rng = np.random.default_rng(99)
     n_head, n_head_kv, n_kv, D = 32, 8, 1024, 128
@@ -244,3 +260,103 @@ def test_glue_ops(dev, ops, orc):
     ids = np.array([3, 49, 0, 3], np.int32)
     got = ops.get_rows(gpu(embq, dev), ops.Q4_0, 256, gpu(ids, dev)).cpu().numpy()
     assert np.array_equal(got, orc.dequantize(ops.Q4_0, embq, 256)[ids])
+
+
+# ---------------------------------------------------------------------------------------------- GEMV epilogues
+def _weight(rng, orc, t, n, k):
+    if t in (12, 14):
+        return random_kquant(rng, t, n, k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    return orc.quantize_q4_0(w) if t == 2 else orc.quantize_q8_0(w, orc.Q8_REF)
+
+
+@pytest.mark.parametrize("wtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("n,k", [(37, 512), (4096, 4096), (2 * 14336, 4096)])
+def test_gemv_epilogues(dev, ops, orc, wtype, n, k):
+    """Each epilogue's output equals the separate node applied to the plain GEMV's value: ADD bit for bit (the same
+    f32 addition), the SWIGLU forms within 1e-6 of the oracle's silu (expf of the GPU against the CPU's); the
+    write-through dst equals the plain GEMV bit for bit."""
+    rng = np.random.default_rng(n + k + wtype)
+    wg = _weight(rng, orc, wtype, n, k)
+    w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    act, _ = ops.quantize_act(gpu(x, dev), ops.act_type(wtype), ops.Q8_X86)
+    v = ops.mul_mat_q(w, act, 1, kernel="mmv").reshape(-1)
+    vn = v.cpu().numpy()
+    e = (rng.standard_normal(n) * 3).astype(np.float32)
+    eg = gpu(e, dev)
+    d, o = ops.mul_mat_vec_ep(w, act, ops.EP_ADD, eg)
+    assert torch.equal(d, v) and np.array_equal(o.cpu().numpy(), vn + e)
+    d, o = ops.mul_mat_vec_ep(w, act, ops.EP_SILU_MUL, eg, write_dst=False)
+    assert d is None and rel_l2(o.cpu().numpy(), orc.swiglu(vn, e)) < 1e-6
+    d, o = ops.mul_mat_vec_ep(w, act, ops.EP_MUL_SILU, eg)
+    assert torch.equal(d, v) and rel_l2(o.cpu().numpy(), orc.swiglu(e, vn)) < 1e-6
+    F = n // 2
+    if n % 2 == 0:
+        d, o = ops.mul_mat_vec_ep(w, act, ops.EP_SWIGLU_STACKED)
+        assert torch.equal(d, v) and o.numel() == F
+        assert rel_l2(o.cpu().numpy(), orc.swiglu(vn[:F], vn[F:])) < 1e-6
+        # the stacked form against the graph's two MUL_MATs + SWIGLU, and the epilogue against amv_swiglu
+        assert torch.equal(o, ops.swiglu(v[:F].contiguous(), v[F:].contiguous()))
+    d, o0 = ops.mul_mat_vec_ep(w, act, ops.EP_NONE)
+    assert torch.equal(d, v) and o0 is d
+
+
+def test_gemv_epilogue_errors(dev, ops, orc):
+    from ameva_compute_amd._lib import AmevaError
+    rng = np.random.default_rng(3)
+    w = ops.QWeight.from_ggml(2, gpu(_weight(rng, orc, 2, 33, 64), dev), 33, 64)
+    act, _ = ops.quantize_act(gpu(rng.standard_normal((1, 64)).astype(np.float32), dev), ops.Q8_0, ops.Q8_X86)
+    with pytest.raises(AmevaError, match="even number of rows"):
+        ops.mul_mat_vec_ep(w, act, ops.EP_SWIGLU_STACKED)
+    with pytest.raises(AmevaError, match="needs its operand"):
+        ops.mul_mat_vec_ep(w, act, ops.EP_ADD)
+    with pytest.raises(AmevaError, match="unknown"):
+        ops.mul_mat_vec_ep(w, act, 9)
+
+
+# ---------------------------------------------------------------------------------------------- ROPE + KV store
+@pytest.mark.parametrize("mode", [0, 2])
+@pytest.mark.parametrize("n_head,n_head_kv,D,n_tok", [(32, 8, 128, 1), (32, 8, 128, 5), (8, 2, 64, 3)])
+def test_rope_kv_store(dev, ops, orc, mode, n_head, n_head_kv, D, n_tok):
+    """Equals amv_rope followed by the two SET_ROWS bit for bit, and the oracle's rope within 1e-5."""
+    rng = np.random.default_rng(n_head + D + n_tok + mode)
+    CTX = 64
+    n_all = n_head + 2 * n_head_kv
+    kvw = n_head_kv * D
+    pos = rng.integers(0, 100000, n_tok).astype(np.int32)
+    idx = rng.permutation(CTX)[:n_tok].astype(np.int64)
+    x = rng.standard_normal((n_tok, n_all, D)).astype(np.float32)
+    kc0 = rng.standard_normal((CTX, kvw)).astype(np.float16)
+    vc0 = rng.standard_normal((CTX, kvw)).astype(np.float16)
+    base = 500000.0
+    # fused
+    qkv = gpu(x, dev)
+    kc, vc = gpu(kc0, dev), gpu(vc0, dev)
+    ops.rope_kv_store(qkv, gpu(pos, dev), n_head, n_head_kv, kc, vc, gpu(idx, dev), D, mode, base)
+    # unfused: ROPE of the q and k heads, then SET_ROWS of k and v
+    qk = gpu(x[:, :n_head + n_head_kv], dev)
+    qk_r = ops.rope(qk, gpu(pos, dev), D, mode, base)
+    kc2, vc2 = gpu(kc0, dev), gpu(vc0, dev)
+    ops.set_rows_f16(kc2, qk_r[:, n_head:].reshape(n_tok, kvw).contiguous(), gpu(idx, dev))
+    ops.set_rows_f16(vc2, gpu(x[:, n_head + n_head_kv:].reshape(n_tok, kvw), dev), gpu(idx, dev))
+    assert torch.equal(qkv[:, :n_head + n_head_kv], qk_r)
+    assert torch.equal(qkv[:, n_head + n_head_kv:], gpu(x[:, n_head + n_head_kv:], dev))
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    ref = orc.rope(x[:, :n_head + n_head_kv], pos, D, mode, base)
+    assert rel_l2(qkv[:, :n_head + n_head_kv].cpu().numpy(), ref) < 1e-5
+    untouched = np.setdiff1d(np.arange(CTX), idx)
+    assert np.array_equal(kc.cpu().numpy()[untouched].view(np.uint16), kc0[untouched].view(np.uint16))
+
+
+def test_rope_kv_store_bad_index(dev, ops):
+    n_head, n_head_kv, D = 4, 2, 64
+    qkv = torch.randn((1, n_head + 2 * n_head_kv, D), device=dev)
+    kc = torch.zeros((8, n_head_kv * D), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.rope_kv_store(qkv, torch.tensor([3], dtype=torch.int32, device=dev), n_head, n_head_kv, kc, vc,
+                      torch.tensor([8], dtype=torch.int64, device=dev), bad=bad)
+    # one k head and one v head of each of the n_head_kv heads count the skipped row
+    assert int(bad.item()) == 2 * n_head_kv
+    assert not kc.any() and not vc.any()
