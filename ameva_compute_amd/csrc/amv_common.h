@@ -67,6 +67,14 @@ __device__ __forceinline__ float amv_h2f(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
 }
 
+// Index (in fp16 units) of the scale of Q4_0 block j of row `row` in the repacked scale array: rows are paired,
+// d[p][j][0..1] holding rows 2p and 2p + 1, so a wave owning both rows fetches the two scales with one dword; an
+// odd last row follows as a plain run of nb scales. Same size as the ggml tensor.
+__device__ __forceinline__ size_t amv_q4_0_didx(int row, int j, int nb, int n_rows) {
+    const int ne = n_rows & ~1;
+    return row < ne ? ((size_t)(row >> 1) * nb + j) * 2 + (row & 1) : (size_t)ne * nb + j;
+}
+
 // signed 4x8-bit dot product with 32-bit accumulate (v_dot4_i32_i8)
 __device__ __forceinline__ int amv_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

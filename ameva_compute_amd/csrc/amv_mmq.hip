@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ wq, con
                 q = *reinterpret_cast<const uint2*>(wq + bi * 32 + 8 * g);
             }
             A[i] = (long)(((uint64_t)q.y << 32) | q.x);
-            dwl[i] = amv_h2f(wd[bi]);
+            dwl[i] = amv_h2f(wd[WT == AMV_T_Q4_0 ? amv_q4_0_didx(nrow[i], b, nb, N) : bi]);
         }
         long B[MMQ_TJ];
         float da[MMQ_TJ];

@@ -32,14 +32,32 @@ __device__ __forceinline__ bool mmv_wave_live(int wave, int R, int n_rows) {
 }
 __device__ __forceinline__ float mmv_silu(float x) { return x / (1.0f + expf(-x)); }
 
-template <int R, int EP>
-__device__ __forceinline__ void mmv_epilogue(const float (&acc)[R], int lane, int wave, int n_rows,
-                                             float* __restrict__ dst, const float* __restrict__ epi,
-                                             float* __restrict__ eout) {
+// End of a row group: wave sums of the R accumulators; with a split of K (S > 1 waves per row group) the S partial
+// sums meet in LDS and are added in the fixed order ks = 0 .. S-1 by the group's first wave; then the epilogue.
+template <int R, int EP, int S>
+__device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int wi, int ks, bool live, int wave,
+                                           int n_rows, float* __restrict__ dst, const float* __restrict__ epi,
+                                           float* __restrict__ eout) {
     static_assert(EP != AMV_EP_SWIGLU_STACKED || R == 2, "the stacked SWIGLU pairs two rows per wave");
     float t[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) t[r] = amv_wave_sum(acc[r]);
+    if constexpr (S > 1) {
+        __shared__ float part[4][R];
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) part[wi][r] = t[r];
+        }
+        __syncthreads();
+        if (ks != 0 || !live) return;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float v = part[wi][r];
+#pragma unroll
+            for (int k = 1; k < S; ++k) v += part[wi + k][r];
+            t[r] = v;
+        }
+    }
     if (lane != 0) return;
     if constexpr (EP == AMV_EP_SWIGLU_STACKED) {
         if (dst) {
@@ -60,37 +78,63 @@ __device__ __forceinline__ void mmv_epilogue(const float (&acc)[R], int lane, in
     }
 }
 
-template <int R, int U, bool BLOCK_SUMS, int EP>
+// FULL: every 64 U-block step is whole (nb % (64 U) == 0) and every row of a live wave exists, so the loads need no
+// clamps and the blocks no guard (all Llama shapes); otherwise indices are clamped and tail blocks skipped. Block
+// indices are 32-bit (the launcher checks n_rows * nb < 2^31). PAIRS: n_rows is even, every scale sits in a pair.
+template <int R, int U, bool BLOCK_SUMS, int EP, int S, bool PAIRS, bool FULL>
 __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                  int n_rows, int nb, const int8_t* __restrict__ aq,
                                                  const int2* __restrict__ ads, float* __restrict__ dst,
                                                  int32_t* __restrict__ sums, const float* __restrict__ epi,
                                                  float* __restrict__ eout) {
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;  // uniform per wave
+    static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
+    const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
+    const bool live = mmv_wave_live<EP>(wave, R, n_rows);
+    if (S == 1 && !live) return;  // uniform per wave
     const int4* a4 = reinterpret_cast<const int4*>(aq);
+    const uint32_t* wd2 = reinterpret_cast<const uint32_t*>(wd);
+    uint32_t rb[R], db[R];  // block index of (row, 0); scale index of (row, 0) minus the block offset factor
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = FULL ? mmv_row<EP>(wave, r, R, n_rows) : min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
+        rb[r] = (uint32_t)row * (uint32_t)nb;
+        db[r] = (uint32_t)(row >> 1) * (uint32_t)nb * 2u + (uint32_t)(row & 1);  // PAIRS: + 2 j
+    }
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    for (int j0 = 0; j0 < nb; j0 += 64 * U) {
+    for (int j0 = live ? 64 * U * ks : nb; j0 < nb; j0 += 64 * U * S) {
         uint4 w[U][R];
-        uint16_t dw[U][R];
+        uint32_t dw[U][R];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = min(j0 + 64 * u + lane, nb - 1);
+            const int j = FULL ? j0 + 64 * u + lane : min(j0 + 64 * u + lane, nb - 1);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const size_t bi = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1) * nb + j;
-                w[u][r] = wq[bi];
-                dw[u][r] = wd[bi];
+            for (int r = 0; r < R; ++r) w[u][r] = wq[rb[r] + j];
+            if (BLOCK_SUMS) continue;
+            if constexpr (PAIRS && EP != AMV_EP_SWIGLU_STACKED && R % 2 == 0) {
+                // the wave's rows 2p, 2p + 1 read both scales with one dword
+#pragma unroll
+                for (int r = 0; r < R; r += 2) {
+                    const uint32_t d2 = wd2[(db[r] >> 1) + j];
+                    dw[u][r] = d2 & 0xFFFFu;
+                    dw[u][r + 1] = d2 >> 16;
+                }
+            } else if constexpr (PAIRS) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) dw[u][r] = wd[db[r] + 2 * j];
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    dw[u][r] = wd[amv_q4_0_didx(min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1), j, nb, n_rows)];
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = j0 + 64 * u + lane;
-            if (j < nb) {
+            if (FULL || j < nb) {
                 const int4 a0 = a4[2 * j], a1 = a4[2 * j + 1];
                 const int2 ds = ads[j];
                 const float da = __int_as_float(ds.x);
@@ -115,25 +159,27 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
             }
         }
     }
-    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
 }
 
 // ------------------------------------------------------------------------------------------------ Q8_0 x Q8_0
-template <int R, int U, bool BLOCK_SUMS, int EP>
+template <int R, int U, bool BLOCK_SUMS, int EP, int S>
 __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                  int n_rows, int nb, const int8_t* __restrict__ aq,
                                                  const int2* __restrict__ ads, float* __restrict__ dst,
                                                  int32_t* __restrict__ sums, const float* __restrict__ epi,
                                                  float* __restrict__ eout) {
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;  // uniform per wave
+    static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
+    const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
+    const bool live = mmv_wave_live<EP>(wave, R, n_rows);
+    if (S == 1 && !live) return;  // uniform per wave
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    for (int j0 = 0; j0 < nb; j0 += 64 * U) {
+    for (int j0 = live ? 64 * U * ks : nb; j0 < nb; j0 += 64 * U * S) {
         uint4 w0[U][R], w1[U][R];
         uint16_t dw[U][R];
 #pragma unroll
@@ -173,7 +219,7 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
             }
         }
     }
-    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
 }
 
 // ------------------------------------------------------------------------------------------------ K-quants
@@ -209,21 +255,23 @@ __device__ __forceinline__ int dot16(uint4 w, int4 a, int acc) {
     return amv_dot4((int)w.w, a.w, acc);
 }
 
-template <int R, bool BLOCK_SUMS, int EP>
+template <int R, bool BLOCK_SUMS, int EP, int S>
 __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, const uint4* __restrict__ wh,
                                                  int n_rows, int nsl, const int8_t* __restrict__ aq,
                                                  const float* __restrict__ ad, const int* __restrict__ abs16,
                                                  float* __restrict__ dst, int32_t* __restrict__ sums, const float* __restrict__ epi,
                                                  float* __restrict__ eout) {
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;
+    static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
+    const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
+    const bool live = mmv_wave_live<EP>(wave, R, n_rows);
+    if (S == 1 && !live) return;  // uniform per wave
     const int nsb = nsl >> 3;
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int j0 = 0; j0 < nsl; j0 += 64) {
+    for (int j0 = live ? 64 * ks : nsl; j0 < nsl; j0 += 64 * S) {
         const int j = min(j0 + lane, nsl - 1);  // nsl is a multiple of 8: clamped lanes fill whole groups of 8
         const int sb = j >> 3, t = j & 7, c = t >> 1, h = t & 1;
         uint4 q[R], hd[R];
@@ -263,25 +311,27 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
             }
         }
     }
-    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
 }
 
-template <int R, bool BLOCK_SUMS, int EP>
+template <int R, bool BLOCK_SUMS, int EP, int S>
 __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, const uint4* __restrict__ wqh,
                                                  const uint4* __restrict__ wsc, const uint16_t* __restrict__ wd,
                                                  int n_rows, int nsl, const int8_t* __restrict__ aq,
                                                  const float* __restrict__ ad, const int* __restrict__ abs16,
                                                  float* __restrict__ dst, int32_t* __restrict__ sums, const float* __restrict__ epi,
                                                  float* __restrict__ eout) {
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (!mmv_wave_live<EP>(wave, R, n_rows)) return;
+    static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
+    const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
+    const bool live = mmv_wave_live<EP>(wave, R, n_rows);
+    if (S == 1 && !live) return;  // uniform per wave
     const int nsb = nsl >> 3;
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int j0 = 0; j0 < nsl; j0 += 64) {
+    for (int j0 = live ? 64 * ks : nsl; j0 < nsl; j0 += 64 * S) {
         const int j = min(j0 + lane, nsl - 1);
         const int sb = j >> 3, t = j & 7;
         const int hh = t >> 2, l0 = 16 * (t & 3);  // ql byte offset 64 hh + l0
@@ -327,7 +377,7 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
             }
         }
     }
-    if (!BLOCK_SUMS) mmv_epilogue<R, EP>(acc, lane, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
@@ -344,7 +394,7 @@ struct MmvArgs {
     float* eout;           // epilogue output
 };
 
-template <int R, int U, bool S, int EP>
+template <int R, int U, bool BS, int EP, int S>
 static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
     const int64_t nblk = (int64_t)a.n_rows * nb;
@@ -353,11 +403,20 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
     const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q4_0<R, U, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
-                       a.dst, a.sums, a.epi, a.eout);
+    const bool full = nb % (64 * U) == 0 && (EP == AMV_EP_SWIGLU_STACKED || a.n_rows % R == 0);
+    const dim3 grid((waves * S + 3) / 4);
+    if (a.n_rows % 2 == 0 && full)
+        hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, true, true>), grid, dim3(256), 0, st, wq, wd, a.n_rows, nb, aq,
+                           ads, a.dst, a.sums, a.epi, a.eout);
+    else if (a.n_rows % 2 == 0)
+        hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, true, false>), grid, dim3(256), 0, st, wq, wd, a.n_rows, nb,
+                           aq, ads, a.dst, a.sums, a.epi, a.eout);
+    else
+        hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, false, false>), grid, dim3(256), 0, st, wq, wd, a.n_rows, nb,
+                           aq, ads, a.dst, a.sums, a.epi, a.eout);
 }
 
-template <int R, int U, bool S, int EP>
+template <int R, int U, bool BS, int EP, int S>
 static void launch_q8_0(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
     const int64_t nblk = (int64_t)a.n_rows * nb;
@@ -366,22 +425,22 @@ static void launch_q8_0(const MmvArgs& a, hipStream_t st) {
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
     const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q8_0<R, U, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
+    hipLaunchKernelGGL((k_mmv_q8_0<R, U, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
                        a.dst, a.sums, a.epi, a.eout);
 }
 
-template <int R, bool S, int EP>
+template <int R, bool BS, int EP, int S>
 static void launch_q4_K(const MmvArgs& a, hipStream_t st) {
     const int nsl = a.k / 32, nsb = a.k / 256;
     const int64_t nblk = (int64_t)a.n_rows * nsb;
     const uint4* wq = reinterpret_cast<const uint4*>(a.w);
     const uint4* wh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
     const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q4_K<R, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
+    hipLaunchKernelGGL((k_mmv_q4_K<R, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
                        (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout);
 }
 
-template <int R, bool S, int EP>
+template <int R, bool BS, int EP, int S>
 static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
     const int nsl = a.k / 32, nsb = a.k / 256;
     const int64_t nblk = (int64_t)a.n_rows * nsb;
@@ -390,32 +449,78 @@ static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
     const uint4* wsc = reinterpret_cast<const uint4*>(a.w + nblk * 192);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 208);
     const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
-    hipLaunchKernelGGL((k_mmv_q6_K<R, S, EP>), dim3((waves + 3) / 4), dim3(256), 0, st, wl, wqh, wsc, wd, a.n_rows, nsl,
+    hipLaunchKernelGGL((k_mmv_q6_K<R, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wl, wqh, wsc, wd, a.n_rows, nsl,
                        a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout);
+}
+
+// Split of K over the S waves of a row group (S = 1, 2, 4) for launches of few row groups. Measured on MI355X
+// (cold, one launch): from 2048 row groups up (the 4096-row projections) the split does not pay (4096 x 14336:
+// 8.0 us with S = 4 against 7.9 us without), so only matrices of at most 2048 rows are split, S doubling while the
+// launch stays within 4096 waves and each wave keeps a whole 64-unit step.
+static int mmv_split(int64_t groups, int64_t steps) {
+    int S = 1;
+    while (S < 4 && groups * S * 2 <= 2048 && S * 2 <= steps) S *= 2;
+    return S;
+}
+
+template <int R, int U, bool BS, int EP>
+static void launch_q4_0_s(const MmvArgs& a, hipStream_t st, int S) {
+    if constexpr (!BS) {
+        if (S == 4) return launch_q4_0<R, U, BS, EP, 4>(a, st);
+        if (S == 2) return launch_q4_0<R, U, BS, EP, 2>(a, st);
+    }
+    launch_q4_0<R, U, BS, EP, 1>(a, st);
+}
+template <int R, int U, bool BS, int EP>
+static void launch_q8_0_s(const MmvArgs& a, hipStream_t st, int S) {
+    if constexpr (!BS) {
+        if (S == 4) return launch_q8_0<R, U, BS, EP, 4>(a, st);
+        if (S == 2) return launch_q8_0<R, U, BS, EP, 2>(a, st);
+    }
+    launch_q8_0<R, U, BS, EP, 1>(a, st);
+}
+template <int R, bool BS, int EP>
+static void launch_q4_K_s(const MmvArgs& a, hipStream_t st, int S) {
+    if constexpr (!BS) {
+        if (S == 4) return launch_q4_K<R, BS, EP, 4>(a, st);
+        if (S == 2) return launch_q4_K<R, BS, EP, 2>(a, st);
+    }
+    launch_q4_K<R, BS, EP, 1>(a, st);
+}
+template <int R, bool BS, int EP>
+static void launch_q6_K_s(const MmvArgs& a, hipStream_t st, int S) {
+    if constexpr (!BS) {
+        if (S == 4) return launch_q6_K<R, BS, EP, 4>(a, st);
+        if (S == 2) return launch_q6_K<R, BS, EP, 2>(a, st);
+    }
+    launch_q6_K<R, BS, EP, 1>(a, st);
 }
 
 // Kernel variant (rows per wave R, blocks-per-lane unroll U) chosen from the block count of a row; the table is the
 // result of the launch-shape sweep on MI355X. The stacked SWIGLU epilogue pairs rows w and F + w, so it runs R = 2.
-template <bool S, int EP>
+// The block-sum instrumentation runs without a split (S = 1).
+template <bool BS, int EP>
 static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
+    const int64_t groups2 = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + 1) / 2;  // R = 2 row groups
+    const auto split = [&](int64_t groups, int64_t steps) { return BS ? 1 : mmv_split(groups, steps); };
     switch (a.wtype) {
     case AMV_T_Q4_0:
         // R = 2 rows per wave, one 64-block step at a time: the fastest shape of the MI355X sweep at K = 4096
         // (7.44 us cold for 14336 x 4096 against 8.5 us for R = 4, 11.2 us for R = 8)
-        launch_q4_0<2, 1, S, EP>(a, st);
+        launch_q4_0_s<2, 1, BS, EP>(a, st, split(groups2, (nb + 63) / 64));
         return AMV_OK;
     case AMV_T_Q8_0:
         if constexpr (EP != AMV_EP_SWIGLU_STACKED) {
             if (nb <= 64) {
-                launch_q8_0<4, 1, S, EP>(a, st);
+                launch_q8_0_s<4, 1, BS, EP>(a, st, 1);
                 return AMV_OK;
             }
         }
-        launch_q8_0<2, 2, S, EP>(a, st);
+        launch_q8_0_s<2, 2, BS, EP>(a, st, split(groups2, (nb + 127) / 128));
         return AMV_OK;
-    case AMV_T_Q4_K: launch_q4_K<2, S, EP>(a, st); return AMV_OK;
-    case AMV_T_Q6_K: launch_q6_K<2, S, EP>(a, st); return AMV_OK;
+    case AMV_T_Q4_K: launch_q4_K_s<2, BS, EP>(a, st, split(groups2, (nb + 63) / 64)); return AMV_OK;
+    case AMV_T_Q6_K: launch_q6_K_s<2, BS, EP>(a, st, split(groups2, (nb + 63) / 64)); return AMV_OK;
     default: amv_set_error("amv_mul_mat_vec: weight type %d not supported", a.wtype); return AMV_ERR_UNSUPPORTED;
     }
 }
@@ -424,7 +529,8 @@ static int check_common(const char* fn, int wtype, const void* w, int64_t n_rows
                         int64_t m) {
     AMV_REQUIRE(w && act, "%s: null pointer", fn);
     AMV_REQUIRE(n_rows > 0 && k > 0 && m > 0, "%s: empty shape", fn);
-    AMV_REQUIRE(n_rows <= INT32_MAX && k <= INT32_MAX, "%s: shape too large", fn);
+    AMV_REQUIRE(n_rows <= INT32_MAX && k <= INT32_MAX && n_rows * (k / 32) < ((int64_t)1 << 31),
+                "%s: shape too large (n_rows * k / 32 must stay below 2^31)", fn);
     AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "%s: w and act must be 16-byte aligned", fn);
     if (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0) {
         AMV_REQUIRE(k % 32 == 0, "%s: k %% 32 != 0", fn);

@@ -161,20 +161,21 @@ __global__ __launch_bounds__(256) void k_quant_q4_0(const float* __restrict__ x,
 // ---------------------------------------------------------------------------------------------------------------
 template <bool FWD>
 __global__ __launch_bounds__(256) void k_repack_q4_0(uint8_t* __restrict__ g, uint4* __restrict__ qs,
-                                                    uint16_t* __restrict__ dd, int64_t n_blk) {
+                                                    uint16_t* __restrict__ dd, int64_t n_blk, int nb, int n_rows) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= n_blk) return;
     uint16_t* gb = reinterpret_cast<uint16_t*>(g + b * 18);
+    const size_t di = amv_q4_0_didx((int)(b / nb), (int)(b % nb), nb, n_rows);
     if (FWD) {
         uint32_t w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[i] = (uint32_t)gb[1 + 2 * i] | ((uint32_t)gb[2 + 2 * i] << 16);
         qs[b] = make_uint4(w[0], w[1], w[2], w[3]);
-        dd[b] = gb[0];
+        dd[di] = gb[0];
     } else {
         const uint4 q = qs[b];
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-        gb[0] = dd[b];
+        gb[0] = dd[di];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             gb[1 + 2 * i] = (uint16_t)(w[i] & 0xFFFFu);
@@ -269,8 +270,9 @@ static int repack_impl(int type, uint8_t* g, uint8_t* r, int64_t n_rows, int64_t
         const int64_t nb = n_rows * (k / 32);
         uint4* qs = reinterpret_cast<uint4*>(r);
         uint16_t* dd = reinterpret_cast<uint16_t*>(r + nb * 16);
-        if (fwd) hipLaunchKernelGGL(k_repack_q4_0<true>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb);
-        else hipLaunchKernelGGL(k_repack_q4_0<false>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb);
+        const int nbr = (int)(k / 32);
+        if (fwd) hipLaunchKernelGGL(k_repack_q4_0<true>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb, nbr, (int)n_rows);
+        else hipLaunchKernelGGL(k_repack_q4_0<false>, grid_for(nb, 256), 256, 0, st, g, qs, dd, nb, nbr, (int)n_rows);
         break;
     }
     case AMV_T_Q8_0: {

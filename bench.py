@@ -44,6 +44,8 @@ def make_weights(ops, torch, n, k, copies, seed, dev, wtype):
         wf = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32) * 0.02
         if wtype == ops.Q4_0:
             wg = ops.quantize_q4_0(wf)
+        elif wtype in (ops.Q4_K, ops.Q6_K):
+            wg = ops.quantize_k(wf, wtype)
         else:
             act, wg = ops.quantize_act(wf, ops.Q8_0, ops.Q8_REF, ggml=True)
             del act
@@ -165,6 +167,83 @@ def bench_layer(torch, dev, args):
             "layer_decode_note": "Llama-3-8B layer, Q4_0, bs1, 4096 cached keys, 4 chained cold layers in one HIP graph"}
 
 
+BLOCK_BYTES = {2: 18, 8: 34, 12: 144 * 32 // 256, 14: 210 * 32 // 256}  # bytes per 32 weights
+
+
+def cold_gemv_us(ops, torch, dev, wtype, n, k, seed, steps=1000):
+    """Time of one cold GEMV of wtype n x k (M = 1): enough distinct copies to exceed 512 MiB, rotated."""
+    per = n * k // 32 * BLOCK_BYTES[wtype]
+    copies = max(4, -(-(600 << 20) // per))
+    ws = make_weights(ops, torch, n, k, copies, seed, dev, wtype)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn((1, k), generator=g, device=dev, dtype=torch.float32)
+    act, _ = ops.quantize_act(x, ops.act_type(wtype), ops.Q8_X86)
+    out = torch.empty((1, n), dtype=torch.float32, device=dev)
+    ms = time_steps_graph(torch, lambda i: ops.mul_mat_q(ws[i % copies], act, 1, out), steps, steps // 10)
+    del ws
+    torch.cuda.empty_cache()
+    return ms * 1e3, per + (k // 32) * 34 + n * 4
+
+
+def secondary_gemvs(ops, torch, dev):
+    """Cold M = 1 GEMVs of BASELINE configs 1 and 2 (Q4_0 4096 x 4096, the down shape, Q8_0 / Q4_K FFN shapes)."""
+    res = {}
+    for name, wtype, n, k in (("q4_0_4096x4096", ops.Q4_0, 4096, 4096), ("q4_0_4096x14336", ops.Q4_0, 4096, 14336),
+                              ("q8_0_14336x4096", ops.Q8_0, 14336, 4096), ("q4_K_14336x4096", ops.Q4_K, 14336, 4096),
+                              ("q4_K_4096x14336", ops.Q4_K, 4096, 14336)):
+        us, nb = cold_gemv_us(ops, torch, dev, wtype, n, k, 99 + n + k)
+        res[name + "_cold_gbs"] = round(nb / us / 1e3, 1)
+        res[name + "_cold_us"] = round(us, 3)
+        log(f"bench: {name} cold {us:.2f} us = {nb / us / 1e3:.0f} GB/s")
+    return res
+
+
+def bench_i2s(ops, torch, dev):
+    """BitNet I2_S GEMV, batch 1, cold over 120 copies of each 4.4 MB weight."""
+    res = {}
+    g = torch.Generator(device=dev)
+    for n, k in ((2560, 6912), (6912, 2560)):
+        copies = 120
+        ws = []
+        for c in range(copies):
+            g.manual_seed(500 + c)
+            codes = torch.randint(0, 3, (n, k), generator=g, device=dev, dtype=torch.int32)
+            # 128-weight blocks of 32 bytes: byte i holds the codes of weights i, 32 + i, 64 + i, 96 + i
+            cb = codes.reshape(n, k // 128, 4, 32)
+            packed = (cb[:, :, 0] << 6) | (cb[:, :, 1] << 4) | (cb[:, :, 2] << 2) | cb[:, :, 3]
+            ws.append(packed.to(torch.uint8).reshape(n, k // 4).contiguous())
+            del codes, cb, packed
+        x = torch.randn((1, k), generator=g, device=dev)
+        act = ops.i2s_quantize_act(x)
+        out = torch.empty((1, n), dtype=torch.float32, device=dev)
+        from ameva_compute_amd._lib import lib as _lib
+
+        def step(i):
+            _lib().amv_i2s_gemv(ws[i % copies].data_ptr(), n, k, act.data_ptr(), 1, 1.5, out.data_ptr(), n,
+                                torch.cuda.current_stream().cuda_stream)
+        ms = time_steps_graph(torch, step, 2000, 200)
+        nbytes = n * k // 4 + k + n * 4
+        res[f"i2s_{n}x{k}_b1_cold_gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        res[f"i2s_{n}x{k}_b1_cold_us"] = round(ms * 1e3, 3)
+        log(f"bench: I2_S {n}x{k} b1 cold {ms * 1e3:.2f} us = {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+        del ws
+        torch.cuda.empty_cache()
+    return res
+
+
+def copy_ceiling(torch, dev, nbytes):
+    """Device-to-device copy of the headline's byte count (torch copy kernel), cold over 20 buffers: the HBM rate a
+    single launch of a plain streaming kernel of that size reaches on this box, read + write bytes counted."""
+    n = nbytes // 4
+    srcs = [torch.randn(n, device=dev) for _ in range(20)]
+    dsts = [torch.empty(n, device=dev) for _ in range(20)]
+    ms = time_steps_graph(torch, lambda i: dsts[i % 20].copy_(srcs[i % 20]), 1000, 100)
+    del srcs, dsts
+    torch.cuda.empty_cache()
+    return {"d2d_copy_33MB_gbs": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1), "d2d_copy_33MB_us": round(ms * 1e3, 3)}
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -240,19 +319,9 @@ def main():
         extra["q8_0_quantize_4096_us"] = round(time_steps_graph(torch, step_quant, 500, 100) * 1e3, 3)
         del ws
         torch.cuda.empty_cache()
-        # Q4_0 4096 x 4096 (BASELINE config 1 shape), cold over 32 copies (302 MB)
-        ws1 = make_weights(ops, torch, 4096, K, 32, 99, dev, ops.Q4_0)
-        out1 = torch.empty((1, 4096), dtype=torch.float32, device=dev)
-        ms1 = time_steps_graph(torch, lambda i: ops.mul_mat_q(ws1[i % 32], act, 1, out1), 2000, 200)
-        extra["q4_0_4096x4096_cold_gbs"] = round(gemv_bytes(4096, K) / (ms1 * 1e-3) / 1e9, 1)
-        del ws1
-        torch.cuda.empty_cache()
-        # Q8_0 14336 x 4096, cold over 10 copies (624 MB)
-        ws8 = make_weights(ops, torch, N_ROWS, K, 10, 77, dev, ops.Q8_0)
-        ms8 = time_steps_graph(torch, lambda i: ops.mul_mat_q(ws8[i % 10], act, 1, out), 1000, 100)
-        extra["q8_0_14336x4096_cold_gbs"] = round(gemv_bytes(N_ROWS, K, 34) / (ms8 * 1e-3) / 1e9, 1)
-        del ws8
-        torch.cuda.empty_cache()
+        extra.update(secondary_gemvs(ops, torch, dev))
+        extra.update(bench_i2s(ops, torch, dev))
+        extra.update(copy_ceiling(torch, dev, nbytes))
 
     layer_info = None
     if not args.only_headline:

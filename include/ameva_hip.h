@@ -41,7 +41,8 @@ int amv_version(void);
  * (adapters/llama/ggml-ameva/ggml-ameva-repack.h:1-69, ggml-ameva-repack.cpp:21-351, set_tensor/get_tensor at
  * ggml-ameva-buffer.cpp:509-561). The MI355X layout is structure-of-arrays per tensor of n_rows x k weights, row
  * major within each region, every region but the last starting 16-byte aligned:
- *   Q4_0: qs[n_rows][k/32][16] | d f16[n_rows][k/32]
+ *   Q4_0: qs[n_rows][k/32][16] | d f16[n_rows/2][k/32][2] (the scales of rows 2p and 2p + 1 side by side, one dword
+ *         per block pair; an odd last row follows as d f16[k/32])
  *   Q8_0: qs[n_rows][k/32][32] | d f16[n_rows][k/32]
  *   Q4_K: qs[n_rows][k/256][128] | head[n_rows][k/256][16] (d, dmin, scales[12])
  *   Q6_K: ql[n_rows][k/256][128] | qh[..][64] | scales[..][16] | d f16[..]

@@ -100,6 +100,25 @@ def test_repack_round_trip(dev, ops, wtype):
         assert np.array_equal(w.to_ggml().cpu().numpy(), raw)
 
 
+@pytest.mark.parametrize("n", [1, 6, 37])
+def test_q4_0_repacked_layout(dev, ops, n):
+    """The documented Q4_0 layout: qs[n][k/32][16] | scales of rows 2p, 2p+1 side by side per block, odd last row
+    as a plain run."""
+    rng = np.random.default_rng(n)
+    k = 96
+    nb = k // 32
+    raw = rng.integers(0, 256, (n, nb, 18), dtype=np.uint8)
+    w = ops.QWeight.from_ggml(2, gpu(raw.reshape(n, -1), dev), n, k)
+    r = w.data.cpu().numpy().reshape(-1)
+    assert np.array_equal(r[: n * nb * 16].reshape(n, nb, 16), raw[:, :, 2:])
+    d = r[n * nb * 16:].view(np.uint16)
+    dg = raw[:, :, :2].copy().view(np.uint16).reshape(n, nb)
+    ne = n & ~1
+    assert np.array_equal(d[: ne * nb].reshape(ne // 2, nb, 2), dg[:ne].reshape(ne // 2, 2, nb).transpose(0, 2, 1))
+    if n % 2:
+        assert np.array_equal(d[ne * nb:], dg[ne])
+
+
 def _q4_0_case(orc, rng, n, k):
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     return orc.quantize_q4_0(w)
