@@ -244,6 +244,32 @@ def copy_ceiling(torch, dev, nbytes):
     return {"d2d_copy_33MB_gbs": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1), "d2d_copy_33MB_us": round(ms * 1e3, 3)}
 
 
+def pmc_probe(ops, torch, dev):
+    """Dispatches for the HBM-traffic counters: the headline GEMV, eager (one dispatch each) over the rotating cold
+    weights, and torch's copy kernel moving a float32 tensor of the GEMV's weight byte count, whose FETCH_SIZE and
+    WRITE_SIZE must read that byte count (the scale of the counters)."""
+    ws = make_weights(ops, torch, N_ROWS, K, COPIES, 42, dev, ops.Q4_0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    x = torch.randn((1, K), generator=g, device=dev, dtype=torch.float32)
+    act, _ = ops.quantize_act(x, ops.Q8_0, ops.Q8_X86)
+    out = torch.empty((1, N_ROWS), dtype=torch.float32, device=dev)
+    for i in range(50):
+        ops.mul_mat_q(ws[i % COPIES], act, 1, out)
+    torch.cuda.synchronize()
+    wbytes = ws[0].nbytes
+    del ws
+    n = wbytes // 4
+    srcs = [torch.randn(n, device=dev) for _ in range(COPIES)]
+    dst = torch.empty(n, device=dev)
+    torch.cuda.synchronize()
+    for i in range(50):
+        dst.copy_(srcs[i % COPIES])
+    torch.cuda.synchronize()
+    print(json.dumps({"gemv_dispatches": 50, "gemv_algorithmic_bytes": gemv_bytes(N_ROWS, K),
+                      "copy_dispatches": 50, "copy_bytes_each_way": n * 4}), flush=True)
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -272,6 +298,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true", help="skip the secondary figures (for profiling)")
+    ap.add_argument("--only-layer", action="store_true", help="only the layer decode figure (for profiling)")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
+                         "count (the counter scale reference); prints a JSON line of what ran")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -283,6 +313,13 @@ def main():
     assert torch.cuda.is_available(), "no GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.pmc_probe:
+        pmc_probe(ops, torch, dev)
+        return
+    if args.only_layer:
+        print(json.dumps(bench_layer(torch, dev, args)), flush=True)
+        return
 
     log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")
     ws = make_weights(ops, torch, N_ROWS, K, COPIES, 42, dev, ops.Q4_0)
