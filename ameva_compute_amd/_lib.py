@@ -38,6 +38,8 @@ SIGNATURES = {
     "amv_swiglu": (I32, [P, P, P, I64, P]),
     "amv_flash_attn_workspace_bytes": (I64, [I64, I64, I64, I64]),
     "amv_flash_attn_decode": (I32, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I64, F32, P, I64, P, I32, P]),
+    "amv_flash_attn_prefill": (I32, [P, I64, I64, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64, F32,
+                                     I64, P]),
     "amv_binary": (I32, [I32, P, P, P, I64, I64, I64, P]),
     "amv_set_rows_f16": (I32, [P, I64, P, I64, I64, I64, P, I32, I64, P, P]),
     "amv_get_rows": (I32, [I32, P, I64, I64, P, I64, P, P, P]),

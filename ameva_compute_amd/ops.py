@@ -28,10 +28,10 @@ def _ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
-def _need_gpu(t: torch.Tensor, what: str) -> None:
+def _need_gpu(t: torch.Tensor, what: str, contiguous: bool = True) -> None:
     if not t.is_cuda:
         raise ValueError(f"{what}: tensor must be on the GPU (no CPU path)")
-    if not t.is_contiguous():
+    if contiguous and not t.is_contiguous():
         raise ValueError(f"{what}: tensor must be contiguous")
 
 
@@ -284,6 +284,27 @@ def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
     check(lib().amv_flash_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(mask), out.data_ptr(), n_head,
                                       n_head_kv, n_kv, D, k.stride(1), k.stride(0), v.stride(1), v.stride(0), scale,
                                       workspace.data_ptr(), need, _ptr(act), rule, _stream()), "amv_flash_attn_decode")
+    return out
+
+
+def flash_attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, n_kv: int | None = None,
+                       mask: torch.Tensor | None = None, causal_pos0: int = -1) -> torch.Tensor:
+    """q f32 [n_tok, n_head, D] (any strides with contiguous rows); k, v f16 views [n_head_kv, n_keys, D] as in
+    flash_attn_decode; mask f16 [n_tok, >= n_kv] or None; causal_pos0 >= 0: token t sees keys <= causal_pos0 + t.
+    Returns f32 [n_tok, n_head, D]."""
+    _need_gpu(q, "flash_attn_prefill", contiguous=False)
+    n_tok, n_head, D = q.shape
+    n_head_kv, n_keys, _ = k.shape
+    n_kv = n_keys if n_kv is None else n_kv
+    if q.stride(2) != 1 or k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("flash_attn_prefill: q, K and V rows must be contiguous")
+    if mask is not None and (mask.dtype != torch.float16 or mask.stride(1) != 1 or mask.shape[0] < n_tok):
+        raise ValueError("flash_attn_prefill: mask must be f16 [n_tok, n_kv] with contiguous rows")
+    out = torch.empty((n_tok, n_head, D), dtype=torch.float32, device=q.device)
+    check(lib().amv_flash_attn_prefill(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), _ptr(mask),
+                                       0 if mask is None else mask.stride(0), out.data_ptr(), n_tok, n_head,
+                                       n_head_kv, n_kv, D, k.stride(1), k.stride(0), v.stride(1), v.stride(0), scale,
+                                       causal_pos0, _stream()), "amv_flash_attn_prefill")
     return out
 
 

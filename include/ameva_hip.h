@@ -182,6 +182,20 @@ int amv_flash_attn_decode(const float* q, const void* k, const void* v, const vo
                           int64_t v_head, float scale, void* workspace, int64_t workspace_bytes, void* act, int rule,
                           void* stream);
 
+/* FLASH_ATTN_EXT over n_tok query positions (prompt prefill; enc_flash_attn ggml-ameva.cpp:4204-4284 with
+ * q->ne[1] > 1, ameva_flash_attn.comp), on the f16 matrix cores. D = 128, n_head / n_head_kv integral.
+ *   q f32: element d of head h of token t at q[t * q_tok_stride + h * q_head_stride + d] (strides in floats, multiples
+ *   of 4: the q heads of a fused q/k/v row can be passed in place); out f32 [n_tok][n_head][D] contiguous.
+ *   k, v f16 as in amv_flash_attn_decode (strides in elements, multiples of 8); keys 0 .. n_kv - 1.
+ *   mask f16 [n_tok][mask_stride] or NULL, added to the scaled scores (ggml's KQ mask; -inf hides a key).
+ *   causal_pos0 >= 0: token t is at position causal_pos0 + t and sees keys 0 .. causal_pos0 + t only (the causal
+ *   mask built in); < 0: no position limit.
+ * Queries that see no key get a zero row. */
+int amv_flash_attn_prefill(const float* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k, const void* v,
+                           const void* mask, int64_t mask_stride, float* out, int64_t n_tok, int64_t n_head,
+                           int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row, int64_t k_head, int64_t v_row,
+                           int64_t v_head, float scale, int64_t causal_pos0, void* stream);
+
 /* ------------------------------------------------------------------------------------------------------------
  * Glue ops of the decoder graph (ameva_binary.comp, ameva_cpy.comp, ameva_set_rows.comp, ameva_get_rows(_q).comp).
  * ---------------------------------------------------------------------------------------------------------- */

@@ -196,6 +196,25 @@ def flash_attn_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
     return out
 
 
+def flash_attn_prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal_pos0: int = -1,
+                       mask: np.ndarray | None = None):
+    """q f32 [n_tok, n_head, D]; k, v f16 bits [n_head_kv, n_kv, D]; mask f16 bits [n_tok, n_kv] or None.
+    Query t is the decode of flash_attn_decode over the keys it may see: all n_kv, or with causal_pos0 >= 0 the
+    first causal_pos0 + t + 1 (ggml's causal KQ mask hides the later ones), plus its mask row."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_tok, n_head, D = q.shape
+    n_kv = k.shape[1]
+    out = np.zeros((n_tok, n_head, D), dtype=np.float32)
+    for t in range(n_tok):
+        nk = n_kv if causal_pos0 < 0 else min(n_kv, causal_pos0 + t + 1)
+        if nk <= 0:
+            continue
+        mrow = None if mask is None else np.ascontiguousarray(mask[t, :nk])
+        out[t] = flash_attn_decode(q[t], np.ascontiguousarray(k[:, :nk]), np.ascontiguousarray(v[:, :nk]), scale,
+                                   mrow)
+    return out
+
+
 def i2s_quantize_act(x: np.ndarray):
     """Per-row absmax int8 quantization; returns (q int8 [rows, n], dequant f32 [rows])."""
     x = np.ascontiguousarray(x, dtype=np.float32)

@@ -360,3 +360,47 @@ def test_rope_kv_store_bad_index(dev, ops):
     # one k head and one v head of each of the n_head_kv heads count the skipped row
     assert int(bad.item()) == 2 * n_head_kv
     assert not kc.any() and not vc.any()
+
+
+# ---------------------------------------------------------------------------------------------- FA prefill
+@pytest.mark.parametrize("n_tok,n_head,n_head_kv,n_kv,pos0,layout", [
+    (512, 32, 8, 512, 0, "token"),      # config 4 prompt: 512 tokens from position 0
+    (100, 8, 2, 300, 200, "token"),     # chunk of a longer prompt (tail tile, keys before the chunk)
+    (64, 8, 1, 1000, -1, "head"),       # no causal limit, GQA 8, head-major cache
+    (1, 4, 4, 1, 0, "head"),            # one token
+])
+def test_flash_attn_prefill(dev, ops, orc, n_tok, n_head, n_head_kv, n_kv, pos0, layout):
+    rng = np.random.default_rng(n_tok + n_kv)
+    D = 128
+    q = rng.standard_normal((n_tok, n_head, D)).astype(np.float32)
+    kh = orc.fp32_to_fp16(rng.standard_normal((n_head_kv, n_kv, D)))
+    vh = orc.fp32_to_fp16(rng.standard_normal((n_head_kv, n_kv, D)))
+    scale = 1.0 / np.sqrt(D)
+    ref = orc.flash_attn_prefill(q, kh, vh, scale, causal_pos0=pos0)
+    if layout == "token":  # llama.cpp cache [kv_size][n_head_kv * D], viewed head-major
+        kt = gpu(np.ascontiguousarray(kh.transpose(1, 0, 2)), dev).view(torch.float16)
+        vt = gpu(np.ascontiguousarray(vh.transpose(1, 0, 2)), dev).view(torch.float16)
+        kg, vg = kt.permute(1, 0, 2), vt.permute(1, 0, 2)
+    else:
+        kg, vg = gpu(kh, dev).view(torch.float16), gpu(vh, dev).view(torch.float16)
+    out = ops.flash_attn_prefill(gpu(q, dev), kg, vg, scale, causal_pos0=pos0).cpu().numpy()
+    assert rel_l2(out, ref) < TOL_FA
+
+
+def test_flash_attn_prefill_mask_and_fused_qkv_rows(dev, ops, orc):
+    """ggml's KQ mask path (f16, -inf above the diagonal plus finite biases) and q read in place from fused q/k/v rows
+    (token stride (n_head + 2 n_head_kv) * D)."""
+    rng = np.random.default_rng(4)
+    n_tok, n_head, n_head_kv, D = 70, 8, 2, 128
+    n_kv = n_tok
+    qkv = rng.standard_normal((n_tok, n_head + 2 * n_head_kv, D)).astype(np.float32)
+    kh = orc.fp32_to_fp16(rng.standard_normal((n_head_kv, n_kv, D)))
+    vh = orc.fp32_to_fp16(rng.standard_normal((n_head_kv, n_kv, D)))
+    mf = (rng.standard_normal((n_tok, 80)) * 0.5).astype(np.float32)
+    mf[np.triu_indices(n_tok, 1, 80)] = -np.inf
+    mask = orc.fp32_to_fp16(mf)
+    ref = orc.flash_attn_prefill(qkv[:, :n_head], kh, vh, 0.1, mask=mask[:, :n_kv])
+    qg = gpu(qkv, dev)[:, :n_head]
+    out = ops.flash_attn_prefill(qg, gpu(kh, dev).view(torch.float16), gpu(vh, dev).view(torch.float16), 0.1,
+                                 mask=gpu(mask, dev).view(torch.float16)).cpu().numpy()
+    assert rel_l2(out, ref) < TOL_FA

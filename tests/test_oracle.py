@@ -388,3 +388,29 @@ def test_i2s_gemv_vs_reference_kernel_and_brute_force(orc):
             assert np.array_equal(s, sums[c].astype(np.float32))
     else:
         pytest.skip("oracle/_ref not built (reference source absent)")
+
+
+def test_flash_attn_prefill_oracle_is_masked_decode(orc):
+    """The prefill restatement: query t equals the decode over the keys it sees; the built-in causal limit and an
+    explicit ggml KQ mask (-inf above the diagonal, f16) give the same rows; the first query sees key 0 only, so its
+    output is V row 0 of its KV head (softmax of one score)."""
+    rng = np.random.default_rng(21)
+    n_tok, n_head, n_head_kv, D, pos0 = 9, 4, 2, 128, 3
+    n_kv = pos0 + n_tok
+    q = rng.standard_normal((n_tok, n_head, D)).astype(np.float32)
+    k = orc.fp32_to_fp16(rng.standard_normal((n_head_kv, n_kv, D)))
+    v = orc.fp32_to_fp16(rng.standard_normal((n_head_kv, n_kv, D)))
+    a = orc.flash_attn_prefill(q, k, v, 0.0884, causal_pos0=pos0)
+    neg = np.uint16(0xFC00)  # f16 -inf
+    mask = np.zeros((n_tok, n_kv), np.uint16)
+    for t in range(n_tok):
+        mask[t, pos0 + t + 1:] = neg
+    b = orc.flash_attn_prefill(q, k, v, 0.0884, mask=mask)
+    np.testing.assert_allclose(a, b, rtol=0, atol=0)
+    for t in (0, 5):
+        d = orc.flash_attn_decode(q[t], np.ascontiguousarray(k[:, :pos0 + t + 1]), np.ascontiguousarray(v[:, :pos0 + t + 1]),
+                                  0.0884)
+        np.testing.assert_array_equal(a[t], d)
+    one = orc.flash_attn_prefill(q[:1], k[:, :1], v[:, :1], 0.0884, causal_pos0=0)
+    vf = orc.fp16_to_fp32(v[:, 0])
+    np.testing.assert_allclose(one[0], vf[np.arange(n_head) // (n_head // n_head_kv)], rtol=1e-6)
