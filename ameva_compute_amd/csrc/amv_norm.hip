@@ -280,3 +280,32 @@ extern "C" int amv_swiglu(const float* g, const float* u, float* y, int64_t n, v
     hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, amv_stream(stream), g, u, y, n);
     return amv_check_launch("amv_swiglu");
 }
+
+// SWIGLU of n_rows rows (row strides in floats) with the Q8_0 quantization of each output row fused: thread i is
+// element i % n of row i / n, a 32-lane half-wave one Q8_0 block (n % 32 == 0).
+__global__ __launch_bounds__(256) void k_swiglu_q8(const float* __restrict__ g, int64_t gs, const float* __restrict__ u,
+                                                  int64_t us, float* __restrict__ y, int64_t ys, int64_t n_rows,
+                                                  int64_t n, int rule, int8_t* __restrict__ aq, int2* __restrict__ am) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // n_rows * n is a multiple of 32
+    if (i >= n_rows * n) return;                                       // whole 32-lane blocks leave together
+    const int64_t r = i / n, c = i - r * n;
+    const float a = g[r * gs + c];
+    const float h = (a / (1.0f + expf(-a))) * u[r * us + c];
+    if (y) y[r * ys + c] = h;
+    if (aq) amv_q8_0_lanes32(h, rule, (int)(c & 31), aq + r * n + (c & ~(int64_t)31), am + r * (n / 32) + c / 32);
+}
+
+extern "C" int amv_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* y,
+                               int64_t y_stride, int64_t n_rows, int64_t n, void* act, int rule, void* stream) {
+    AMV_REQUIRE(g && u && (y || act) && n_rows > 0 && n > 0, "amv_swiglu_rows: bad arguments");
+    AMV_REQUIRE(g_stride >= n && u_stride >= n && (!y || y_stride >= n), "amv_swiglu_rows: row stride < n");
+    AMV_REQUIRE(!act || n % 32 == 0, "amv_swiglu_rows: the Q8_0 output needs n %% 32 == 0");
+    AMV_REQUIRE(!act || ((uintptr_t)act & 7) == 0, "amv_swiglu_rows: act must be 8-byte aligned");
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_swiglu_rows: unknown rule %d", rule);
+    int8_t* aq = (int8_t*)act;
+    int2* am = act ? reinterpret_cast<int2*>(aq + n_rows * n) : nullptr;
+    const int64_t total = n_rows * n;
+    hipLaunchKernelGGL(k_swiglu_q8, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, amv_stream(stream), g,
+                       g_stride, u, u_stride, y, y_stride, n_rows, n, rule, aq, am);
+    return amv_check_launch("amv_swiglu_rows");
+}

@@ -132,6 +132,77 @@ class LlamaLayer:
             check(L.amv_binary(0, self.down.data_ptr(), self.x1.data_ptr(), out.data_ptr(), 1, H, 1, st),
                   "residual 2")
 
+    def _prefill_buffers(self, n_tok: int) -> dict:
+        """Per-token-count buffers of prefill (allocated on first use; a captured graph must see them allocated)."""
+        bufs = getattr(self, "_pf", None)
+        if bufs is not None and bufs["n"] >= n_tok:
+            return bufs
+        dev = self.attn_norm.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        u8 = dict(dtype=torch.uint8, device=dev)
+        L = lib()
+        H, FF = self.H, self.FF
+        bufs = {"n": n_tok,
+                "t_o": torch.empty((n_tok, H), **f32), "qkv": torch.empty((n_tok, self.wqkv.n_rows), **f32),
+                "att": torch.empty((n_tok, H), **f32), "proj": torch.empty((n_tok, H), **f32),
+                "x1": torch.empty((n_tok, H), **f32), "t_o2": torch.empty((n_tok, H), **f32),
+                "gu": torch.empty((n_tok, self.wgu.n_rows), **f32), "down": torch.empty((n_tok, H), **f32),
+                "act_h": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, H), **u8),
+                "act_att": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, H), **u8),
+                "act_h2": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, H), **u8),
+                "act_ff": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, FF), **u8),
+                "pos": torch.zeros(n_tok, dtype=torch.int32, device=dev),
+                "idx": torch.zeros(n_tok, dtype=torch.int64, device=dev)}
+        self._pf = bufs
+        return bufs
+
+    def set_prefill_position(self, pos0: int, n_tok: int) -> None:
+        """Positions pos0 .. pos0 + n_tok - 1 for the next prefill (device memory, so a captured graph picks them up)."""
+        b = self._prefill_buffers(n_tok)
+        r = torch.arange(pos0, pos0 + n_tok, device=self.attn_norm.device)
+        b["pos"][:n_tok].copy_(r.to(torch.int32))
+        b["idx"][:n_tok].copy_(r)
+        self.pf_pos0, self.pf_n = pos0, n_tok
+
+    def prefill(self, x: torch.Tensor, out: torch.Tensor) -> None:
+        """A prompt chunk through the layer: x f32 [n_tok, H] at positions set_prefill_position(pos0, n_tok) ->
+        out f32 [n_tok, H]; writes the chunk's K/V rows into the cache and attends causally over keys
+        0 .. pos0 + t. The MUL_MATs run on the int8 MFMA kernel (n_tok >= 8, the reference's crossover) and the
+        attention on the f16 MFMA prefill kernel; 12 launches."""
+        L, st = lib(), torch.cuda.current_stream().cuda_stream
+        n, pos0 = self.pf_n, self.pf_pos0
+        b = self._prefill_buffers(n)
+        H, kv, D, FF = self.H, self.kv, self.D, self.FF
+        mm = L.amv_mul_mat_q if n >= ops.MMQ_MIN_M else L.amv_mul_mat_vec
+        P = lambda t: t.data_ptr()  # noqa: E731
+        check(L.amv_rms_norm(P(x), n, H, self.eps, P(self.attn_norm), None, P(b["t_o"]), P(b["act_h"]), ops.Q8_X86,
+                             st), "rms_norm")
+        nq = self.wqkv.n_rows
+        check(mm(self.wqkv.type, P(self.wqkv.data), nq, H, P(b["act_h"]), n, P(b["qkv"]), nq, st), "qkv")
+        check(L.amv_rope_kv_store(P(b["qkv"]), P(b["pos"]), n, self.n_head, self.n_head_kv, D, D, 0, self.base, 1.0,
+                                  1.0, P(self.k_cache), P(self.v_cache), kv, P(b["idx"]), self.ctx, None, st),
+              "rope + kv store")
+        check(L.amv_flash_attn_prefill(P(b["qkv"]), nq, D, P(self.k_cache), P(self.v_cache), None, 0, P(b["att"]), n,
+                                       self.n_head, self.n_head_kv, pos0 + n, D, kv, D, kv, D, 1.0 / (D ** 0.5), pos0,
+                                       st), "flash_attn prefill")
+        check(L.amv_quantize_act(ops.Q8_0, P(b["att"]), n, H, ops.Q8_X86, None, P(b["act_att"]), st), "quant att")
+        check(mm(self.wo.type, P(self.wo.data), H, H, P(b["act_att"]), n, P(b["proj"]), H, st), "wo")
+        check(L.amv_binary(0, P(b["proj"]), P(x), P(b["x1"]), n, H, n, st), "residual 1")
+        check(L.amv_rms_norm(P(b["x1"]), n, H, self.eps, P(self.ffn_norm), None, P(b["t_o2"]), P(b["act_h2"]),
+                             ops.Q8_X86, st), "ffn norm")
+        ng = self.wgu.n_rows
+        check(mm(self.wgu.type, P(self.wgu.data), ng, H, P(b["act_h2"]), n, P(b["gu"]), ng, st), "gate_up")
+        check(L.amv_swiglu_rows(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, None, FF, n, FF, P(b["act_ff"]), ops.Q8_X86,
+                                st), "swiglu + quant")
+        check(mm(self.wdown.type, P(self.wdown.data), H, FF, P(b["act_ff"]), n, P(b["down"]), H, st), "down")
+        check(L.amv_binary(0, P(b["down"]), P(b["x1"]), P(out), n, H, n, st), "residual 2")
+
+    def prefill_ops(self, n_tok: int, n_kv: int) -> int:
+        """Multiply-adds x 2 of one prefill chunk: the four weight products and the attention (causal half)."""
+        w = sum(q.n_rows * q.k for q in (self.wqkv, self.wo, self.wgu, self.wdown))
+        att = 4 * self.n_head * self.D * (n_tok * n_kv - n_tok * (n_tok - 1) // 2)
+        return 2 * n_tok * w + att
+
     # algorithmic HBM bytes of one decode step at n_kv cached keys (weights + KV read + norms)
     def step_bytes(self, n_kv: int) -> int:
         w = sum(q.nbytes for q in (self.wqkv, self.wo, self.wgu, self.wdown))

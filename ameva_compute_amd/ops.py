@@ -262,6 +262,22 @@ def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def swiglu_rows(g: torch.Tensor, u: torch.Tensor, quantize: bool = False, rule: int = Q8_X86):
+    """SWIGLU of row views g, u [n_rows, n] (contiguous rows, any row stride). Returns y, or (y, act) with the Q8_0
+    activation buffer of y (amv_quantize_act layout) when quantize."""
+    _need_gpu(g, "swiglu_rows", contiguous=False)
+    n_rows, n = g.shape
+    if g.stride(1) != 1 or u.stride(1) != 1 or u.shape != g.shape:
+        raise ValueError("swiglu_rows: g and u must be [n_rows, n] views with contiguous rows")
+    y = torch.empty((n_rows, n), dtype=torch.float32, device=g.device)
+    act = None
+    if quantize:
+        act = torch.empty(lib().amv_act_bytes(Q8_0, n_rows, n), dtype=torch.uint8, device=g.device)
+    check(lib().amv_swiglu_rows(g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), y.data_ptr(), n, n_rows, n,
+                                _ptr(act), rule, _stream()), "amv_swiglu_rows")
+    return (y, act) if quantize else y
+
+
 # ------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
 def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, n_kv: int | None = None,
                       mask: torch.Tensor | None = None, workspace: torch.Tensor | None = None,

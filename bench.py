@@ -156,13 +156,14 @@ def bench_layer(torch, dev, args):
     ms = graph_ms(True)
     nbytes = layers[0].step_bytes(layers[0].ctx)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    pf = bench_prefill(torch, dev, layers[0], 512)
     log(f"bench: layer decode {ms * 1e3:.2f} us/layer (graph, 10 launches), {ms_unfused * 1e3:.2f} us unfused "
         f"(16 launches), {ms_eager * 1e3:.2f} us eager; {nbytes / 1e6:.1f} MB -> {gbs:.0f} GB/s")
     del layers
     torch.cuda.empty_cache()
     return {"layer_decode_us": round(ms * 1e3, 3), "layer_decode_tok_s": round(1e3 / ms, 1),
             "layer_decode_gbs": round(gbs, 1), "layer_decode_eager_us": round(ms_eager * 1e3, 3),
-            "layer_decode_unfused_us": round(ms_unfused * 1e3, 3),
+            "layer_decode_unfused_us": round(ms_unfused * 1e3, 3), **pf,
             "layer_decode_bytes": nbytes,
             "layer_decode_note": "Llama-3-8B layer, Q4_0, bs1, 4096 cached keys, 4 chained cold layers in one HIP graph"}
 
@@ -268,6 +269,29 @@ def pmc_probe(ops, torch, dev):
     torch.cuda.synchronize()
     print(json.dumps({"gemv_dispatches": 50, "gemv_algorithmic_bytes": gemv_bytes(N_ROWS, K),
                       "copy_dispatches": 50, "copy_bytes_each_way": n * 4}), flush=True)
+
+
+INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix peak (5.0 POPS)
+
+
+def bench_prefill(torch, dev, layer, n_tok):
+    """BASELINE config 4 prefill: a prompt of n_tok tokens from position 0 through one layer (int8-MFMA MUL_MATs,
+    f16-MFMA causal attention), captured in a HIP graph and replayed; tok/s = n_tok / time of the layer."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    x = torch.randn((n_tok, layer.H), generator=g, device=dev)
+    out = torch.empty_like(x)
+    layer.set_prefill_position(0, n_tok)
+    layer.prefill(x, out)  # allocates the chunk buffers before the capture
+    ms = time_steps_graph(torch, lambda i: layer.prefill(x, out), 50, 5, per_graph=5)
+    ops_ = layer.prefill_ops(n_tok, n_tok)
+    tops = ops_ / (ms * 1e-3) / 1e12
+    log(f"bench: layer prefill {n_tok} tokens {ms * 1e3:.1f} us = {n_tok / (ms * 1e-3):.0f} tok/s, "
+        f"{tops:.1f} TOPS ({tops / INT8_MFMA_PEAK_TOPS * 100:.1f}% of int8 MFMA peak)")
+    return {"layer_prefill_512_us": round(ms * 1e3, 2), "layer_prefill_512_tok_s": round(n_tok / (ms * 1e-3), 1),
+            "layer_prefill_512_tops": round(tops, 2),
+            "layer_prefill_512_frac_int8_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+            "layer_prefill_note": "one Llama-3-8B layer, Q4_0, 512-token prompt from position 0, HIP graph"}
 
 
 def cpu_model() -> str:

@@ -164,6 +164,11 @@ int amv_rope_kv_store(float* qkv, const int32_t* pos, int64_t n_tok, int64_t n_h
 
 /* GLU SWIGLU (ggml_vec_swiglu_f32; enc_glu, ameva_glu.comp:45-46): y = silu(g) * u. */
 int amv_swiglu(const float* g, const float* u, float* y, int64_t n, void* stream);
+/* SWIGLU of n_rows rows (g, u, y row strides in floats; ggml's split GLU over views of one gate/up row) with the
+ * Q8_0 quantization of every output row fused (act: amv_quantize_act's Q8_0 layout of n_rows x n, or NULL; y may be
+ * NULL when act is given). The act bytes equal amv_quantize_act of y. */
+int amv_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* y, int64_t y_stride,
+                    int64_t n_rows, int64_t n, void* act, int rule, void* stream);
 
 /* ------------------------------------------------------------------------------------------------------------
  * FLASH_ATTN_EXT, decode (one query position), f16 K/V cache (enc_flash_attn ggml-ameva.cpp:4204-4284 with the key
