@@ -93,6 +93,120 @@ __global__ __launch_bounds__(256) void k_i2s_gemv(const uint4* __restrict__ w, i
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Batched (m >= 8 tokens) I2_S MUL_MAT on int8 MFMA. The activation scale is per token over the whole row, so the
+// ternary dot stays integer across all of k: v_mfma_i32_32x32x32_i8 (the full-rate int8 shape of gfx950) accumulates
+// sum_k code * q in its int32 accumulator from the first block to the last (codes 0..3 are valid signed bytes), and
+// sum q is subtracted once.
+// MFMA k slots may be assigned to weights in any order A and B share: in block b, step t (0..3), lane half h
+// (lanes 32 h .. 32 h + 31) supplies the 16 weights 32 t + 16 h + s (s = 0..15), i.e. the 2-bit field t (shift
+// 6 - 2 t) of block bytes 16 h .. 16 h + 15, and the activations q[128 b + 32 t + 16 h + s]: one 16-byte load each.
+// Workgroup: 64 weight rows x 64 tokens (2 x 2 MFMA tiles of 32 x 32 per wave); its NW waves split the k blocks
+// (wave w takes blocks w, w + NW, ...) and the integer partials meet in LDS through integer atomics (exact). Lane l of
+// a 32 x 32 tile holds token column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
+// ---------------------------------------------------------------------------------------------------------------
+typedef int i2s_v4i __attribute__((ext_vector_type(4)));
+typedef int i2s_v16i __attribute__((ext_vector_type(16)));
+
+template <bool OUT_SUMS, int NW>
+__global__ __launch_bounds__(64 * NW) void k_i2s_mmq(const uint8_t* __restrict__ w, int n_rows, int kb,
+                                                    const int8_t* __restrict__ q, const int2* __restrict__ meta, int m,
+                                                    float wscale, float* __restrict__ dst, int64_t ldd,
+                                                    int32_t* __restrict__ isums) {
+    __shared__ int part[2][2][16][64];  // integer sum of the wave partials: [row tile][token tile][r][lane]
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 31, h = lane >> 5;
+    const int row0 = blockIdx.x * 64, tok0 = blockIdx.y * 64;
+    const int k = kb * 128;
+    for (int i = threadIdx.x; i < 2 * 2 * 16 * 64; i += 64 * NW) (&part[0][0][0][0])[i] = 0;
+    const uint4* wr[2];
+    const int4* qa[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        wr[i] = reinterpret_cast<const uint4*>(w + (size_t)min(row0 + 32 * i + c, n_rows - 1) * kb * 32) + h;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        qa[j] = reinterpret_cast<const int4*>(q + (size_t)min(tok0 + 32 * j + c, m - 1) * k + 16 * h);
+    i2s_v16i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    uint4 wb[2];
+    int4 ab[2][4];
+    int b = wv;
+    if (b < kb) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) wb[i] = wr[i][2 * b];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) ab[j][t] = qa[j][8 * b + 2 * t];
+    }
+    for (; b < kb; b += NW) {
+        const int bn = b + NW < kb ? b + NW : b;  // next block of this wave (reloads b at the end: harmless)
+        uint4 nwb[2];
+        int4 nab[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) nwb[i] = wr[i][2 * bn];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) nab[j][t] = qa[j][8 * bn + 2 * t];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int sh = 6 - 2 * t;
+            i2s_v4i A[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                A[i] = i2s_v4i{(int)((wb[i].x >> sh) & 0x03030303u), (int)((wb[i].y >> sh) & 0x03030303u),
+                               (int)((wb[i].z >> sh) & 0x03030303u), (int)((wb[i].w >> sh) & 0x03030303u)};
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int4 v = ab[j][t];
+                    const i2s_v4i B = {v.x, v.y, v.z, v.w};
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B, acc[i][j], 0, 0, 0);
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) wb[i] = nwb[i];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) ab[j][t] = nab[j][t];
+    }
+    __syncthreads();  // part zeroed
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) atomicAdd(&part[i][j][r][lane], acc[i][j][r]);
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int tok = tok0 + 32 * j + c;
+        if (tok >= m) continue;
+        const int2 mt = meta[tok];
+        const float ts = __int_as_float(mt.x) * wscale;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = row0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row >= n_rows) continue;
+                const int t = part[i][j][r][lane] - mt.y;
+                if (OUT_SUMS) isums[(size_t)tok * n_rows + row] = t;
+                else dst[(size_t)tok * ldd + row] = (float)t * ts;
+            }
+        }
+    }
+}
+
 extern "C" int64_t amv_i2s_act_bytes(int64_t m, int64_t k) { return (m < 0 || k < 0) ? -1 : m * k + m * 8; }
 
 extern "C" int amv_i2s_quantize_act(const float* x, int64_t m, int64_t k, void* act, void* stream) {
@@ -106,14 +220,43 @@ extern "C" int amv_i2s_quantize_act(const float* x, int64_t m, int64_t k, void* 
     return amv_check_launch("amv_i2s_quantize_act");
 }
 
+// batch from which the MFMA kernel runs (as the Q4_0 / Q8_0 MUL_MAT, AMEVA_QGEMM_MIN_M = 8)
+#define I2S_MMQ_MIN_M 8
+#ifndef I2S_MMQ_WAVES
+#define I2S_MMQ_WAVES 4
+#endif
+
 static int i2s_gemv_impl(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float wscale,
                          float* dst, int64_t ldd, int32_t* sums, void* stream) {
     AMV_REQUIRE(w && act && (dst || sums), "amv_i2s_gemv: null pointer");
-    AMV_REQUIRE(n_rows > 0 && k > 0 && m > 0 && n_rows <= INT32_MAX, "amv_i2s_gemv: bad shape");
+    AMV_REQUIRE(n_rows > 0 && k > 0 && m > 0 && n_rows <= INT32_MAX && m <= 65535LL * 64 && n_rows * k / 4 < (1LL << 40),
+                "amv_i2s_gemv: bad shape");
     AMV_REQUIRE(k % 128 == 0, "amv_i2s_gemv: k %% 128 != 0 (k = %lld)", (long long)k);
     AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "amv_i2s_gemv: buffers must be 16-byte aligned");
     AMV_REQUIRE(!dst || ldd >= n_rows, "amv_i2s_gemv: ldd < n_rows");
     hipStream_t st = amv_stream(stream);
+    if (m >= I2S_MMQ_MIN_M) {
+        const int kb = (int)(k / 128);
+        const int8_t* q = (const int8_t*)act;
+        const int2* meta = (const int2*)((const uint8_t*)act + m * k);
+        const int64_t tok_tiles = (m + 63) / 64;
+        const dim3 grid((unsigned)((n_rows + 63) / 64), (unsigned)tok_tiles);
+        const uint8_t* wp = (const uint8_t*)w;
+        const int nw = I2S_MMQ_WAVES;
+#define I2S_MMQ(S, NWV, D, L, IS) hipLaunchKernelGGL((k_i2s_mmq<S, NWV>), grid, dim3(64 * NWV), 0, st, wp, \
+                                                     (int)n_rows, kb, q, meta, (int)m, wscale, D, L, IS)
+        if (sums) {
+            if (nw == 16) I2S_MMQ(true, 16, nullptr, (int64_t)0, sums);
+            else if (nw == 8) I2S_MMQ(true, 8, nullptr, (int64_t)0, sums);
+            else I2S_MMQ(true, 4, nullptr, (int64_t)0, sums);
+        } else {
+            if (nw == 16) I2S_MMQ(false, 16, dst, ldd, nullptr);
+            else if (nw == 8) I2S_MMQ(false, 8, dst, ldd, nullptr);
+            else I2S_MMQ(false, 4, dst, ldd, nullptr);
+        }
+#undef I2S_MMQ
+        return amv_check_launch("amv_i2s_gemv");
+    }
     const int nsl = (int)(k / 64);
     const int R = 2;
     const int waves = (int)((n_rows + R - 1) / R);

@@ -228,6 +228,21 @@ def bench_i2s(ops, torch, dev):
         res[f"i2s_{n}x{k}_b1_cold_gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         res[f"i2s_{n}x{k}_b1_cold_us"] = round(ms * 1e3, 3)
         log(f"bench: I2_S {n}x{k} b1 cold {ms * 1e3:.2f} us = {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+        # batch 128 (int8 MFMA): 2 n k 128 integer ops
+        x128 = torch.randn((128, k), generator=g, device=dev)
+        act128 = ops.i2s_quantize_act(x128)
+        out128 = torch.empty((128, n), dtype=torch.float32, device=dev)
+
+        def step128(i):
+            _lib().amv_i2s_gemv(ws[i % copies].data_ptr(), n, k, act128.data_ptr(), 128, 1.5, out128.data_ptr(), n,
+                                torch.cuda.current_stream().cuda_stream)
+        ms128 = time_steps_graph(torch, step128, 1000, 100)
+        tops = 2.0 * n * k * 128 / (ms128 * 1e-3) / 1e12
+        res[f"i2s_{n}x{k}_b128_us"] = round(ms128 * 1e3, 3)
+        res[f"i2s_{n}x{k}_b128_tops"] = round(tops, 1)
+        res[f"i2s_{n}x{k}_b128_frac_int8_peak"] = round(tops / INT8_MFMA_PEAK_TOPS, 4)
+        log(f"bench: I2_S {n}x{k} b128 {ms128 * 1e3:.2f} us = {tops:.0f} TOPS ({tops / INT8_MFMA_PEAK_TOPS * 100:.1f}% "
+            f"of int8 MFMA peak)")
         del ws
         torch.cuda.empty_cache()
     return res
@@ -323,6 +338,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true", help="skip the secondary figures (for profiling)")
     ap.add_argument("--only-layer", action="store_true", help="only the layer decode figure (for profiling)")
+    ap.add_argument("--only-i2s", action="store_true", help="only the BitNet I2_S figures (for profiling)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
@@ -343,6 +359,9 @@ def main():
         return
     if args.only_layer:
         print(json.dumps(bench_layer(torch, dev, args)), flush=True)
+        return
+    if args.only_i2s:
+        print(json.dumps(bench_i2s(ops, torch, dev)), flush=True)
         return
 
     log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")

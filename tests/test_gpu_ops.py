@@ -99,8 +99,11 @@ def pack_i2s(codes):
     return w
 
 
-@pytest.mark.parametrize("n,k,m", [(6912, 2560, 1), (2560, 6912, 1), (6912, 2560, 128), (3, 128, 2), (129, 256, 5)])
+@pytest.mark.parametrize("n,k,m", [(6912, 2560, 1), (2560, 6912, 1), (6912, 2560, 128), (2560, 6912, 128), (3, 128, 2),
+                                   (129, 256, 5), (100, 384, 70), (64, 128, 8)])
 def test_i2s_parity(dev, ops, orc, n, k, m):
+    """m < 8: the GEMV; m >= 8: the int8-MFMA kernel (BASELINE config 3 batch 128). Integer outputs bit-exact and the
+    f32 outputs bit-exact too (the same f32 operations as the CPU on the same integer)."""
     rng = np.random.default_rng(n * 3 + k + m)
     codes = rng.integers(0, 3, (n, k))
     w = pack_i2s(codes)
