@@ -16,6 +16,22 @@ enum {
 
 #define AMV_WAVE 64
 
+// Offsets (bytes) of the matrix-core extension of the AMV_ACT_Q8_K_MMA activation layout: after the Q8_K layout
+// (rounded up to 16 bytes) come the int8 values as f16 [m][k], the sums per 16 as f16 [m][k/16] and the super-block
+// scales transposed, f32 [k/256][m]; all exact copies (|sum of 16 int8| <= 2032 is exact in f16).
+struct AmvQ8kMma {
+    int64_t a16, bs16, dt, total;
+};
+static inline AmvQ8kMma amv_q8k_mma_layout(int64_t m, int64_t k) {
+    AmvQ8kMma L;
+    const int64_t q8k = m * k + m * (k / 256) * 4 + m * (k / 16) * 4;
+    L.a16 = (q8k + 15) & ~(int64_t)15;
+    L.bs16 = L.a16 + 2 * m * k;
+    L.dt = (L.bs16 + 2 * m * (k / 16) + 15) & ~(int64_t)15;
+    L.total = L.dt + 4 * m * (k / 256);
+    return L;
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // host: error state (first message of the failing call, per thread)
 void amv_set_error(const char* fmt, ...);
@@ -73,6 +89,22 @@ __device__ __forceinline__ float amv_h2f(uint32_t h) {
 __device__ __forceinline__ size_t amv_q4_0_didx(int row, int j, int nb, int n_rows) {
     const int ne = n_rows & ~1;
     return row < ne ? ((size_t)(row >> 1) * nb + j) * 2 + (row & 1) : (size_t)ne * nb + j;
+}
+
+// byte i (0..11) of the packed 6-bit scales held in three words
+__device__ __forceinline__ uint32_t k4_byte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xFFu;
+}
+// get_scale_min_k4 of a Q4_K super-block (reference ameva_qdecode.glsl:229-236)
+__device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc, int& m) {
+    if (j < 4) {
+        sc = (int)(k4_byte(s0, s1, s2, j) & 63u);
+        m = (int)(k4_byte(s0, s1, s2, j + 4) & 63u);
+    } else {
+        sc = (int)((k4_byte(s0, s1, s2, j + 4) & 0xFu) | ((k4_byte(s0, s1, s2, j - 4) >> 6) << 4));
+        m = (int)((k4_byte(s0, s1, s2, j + 4) >> 4) | ((k4_byte(s0, s1, s2, j) >> 6) << 4));
+    }
 }
 
 // signed 4x8-bit dot product with 32-bit accumulate (v_dot4_i32_i8)

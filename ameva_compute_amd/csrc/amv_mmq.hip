@@ -117,14 +117,19 @@ __device__ __forceinline__ void mmq_compute(const MmqFrag<TI, TJ, U>& f, int b0,
 }
 
 // FULLK: nb % U == 0 (every step is whole: block indices need no clamp and fold into load offsets).
-template <int WT, bool SUMS, int TI, int TJ, int U, bool FULL, bool FULLK>
+// KS = 4: the 4 waves share one tile (16 TI rows x 16 TJ tokens per workgroup) and split its pipeline steps
+// (wave w takes steps w, w + 4, ...); their f32 partials are added in LDS in wave order (small batches: many
+// workgroups instead of few long ones).
+template <int WT, bool SUMS, int TI, int TJ, int U, bool FULL, bool FULLK, int WR, int KS>
 __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int N,
                                             int nb, const int8_t* __restrict__ aq, const int2* __restrict__ ameta,
                                             int M, float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ sums) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int n_wave = blockIdx.x * (2 * 16 * TI) + (w & 1) * (16 * TI);
-    const int m_wave = blockIdx.y * (2 * 16 * TJ) + (w >> 1) * (16 * TJ);
+    // WR waves along the weight rows, 4 / WR along the tokens (KS = 1); with KS = 4 one tile per workgroup
+    const int n_wave = KS == 4 ? blockIdx.x * (16 * TI) : blockIdx.x * (WR * 16 * TI) + (w % WR) * (16 * TI);
+    const int m_wave = KS == 4 ? blockIdx.y * (16 * TJ) : blockIdx.y * ((4 / WR) * 16 * TJ) + (w / WR) * (16 * TJ);
+    const int ks = KS == 4 ? w : 0;
     const int K = nb * 32;
     float acc[TI][TJ][4];
 #pragma unroll
@@ -144,16 +149,39 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ wq, con
     // (steps of U blocks; the last step may be partial when nb % U != 0)
     const int steps = (nb + U - 1) / U;
     MmqFrag<TI, TJ, U> f0, f1;
-    mmq_load<WT, TI, TJ, U, FULL, FULLK>(f0, 0, wq, wd, N, nb, aq, ameta, K, nrow, mrow, n_wave, g);
-    int s = 0;
-    for (; s + 2 <= steps; s += 2) {
-        mmq_load<WT, TI, TJ, U, FULL, FULLK>(f1, (s + 1) * U, wq, wd, N, nb, aq, ameta, K, nrow, mrow, n_wave, g);
+    int s = ks;
+    if (s < steps) mmq_load<WT, TI, TJ, U, FULL, FULLK>(f0, s * U, wq, wd, N, nb, aq, ameta, K, nrow, mrow, n_wave, g);
+    for (; s + KS < steps; s += 2 * KS) {
+        mmq_load<WT, TI, TJ, U, FULL, FULLK>(f1, (s + KS) * U, wq, wd, N, nb, aq, ameta, K, nrow, mrow, n_wave, g);
         mmq_compute<WT, SUMS, TI, TJ, U, FULLK>(f0, s * U, nb, sh, acc, N, M, n_wave, m_wave, g, r16, sums);
-        if (s + 2 < steps)
-            mmq_load<WT, TI, TJ, U, FULL, FULLK>(f0, (s + 2) * U, wq, wd, N, nb, aq, ameta, K, nrow, mrow, n_wave, g);
-        mmq_compute<WT, SUMS, TI, TJ, U, FULLK>(f1, (s + 1) * U, nb, sh, acc, N, M, n_wave, m_wave, g, r16, sums);
+        if (s + 2 * KS < steps)
+            mmq_load<WT, TI, TJ, U, FULL, FULLK>(f0, (s + 2 * KS) * U, wq, wd, N, nb, aq, ameta, K, nrow, mrow, n_wave,
+                                                 g);
+        mmq_compute<WT, SUMS, TI, TJ, U, FULLK>(f1, (s + KS) * U, nb, sh, acc, N, M, n_wave, m_wave, g, r16, sums);
     }
     if (s < steps) mmq_compute<WT, SUMS, TI, TJ, U, FULLK>(f0, s * U, nb, sh, acc, N, M, n_wave, m_wave, g, r16, sums);
+    if constexpr (KS == 4 && !SUMS) {
+        __shared__ float red[3][TI * TJ * 4][64];
+        if (w > 0) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) red[w - 1][(i * TJ + j) * 4 + r][lane] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (w > 0) return;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int q = (i * TJ + j) * 4 + r;
+                    acc[i][j][r] = ((acc[i][j][r] + red[0][q][lane]) + red[1][q][lane]) + red[2][q][lane];
+                }
+    }
     if (!SUMS) {
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
@@ -175,17 +203,18 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ wq, con
     }
 }
 
-template <int WT, bool SUMS, int TI, int TJ, int U>
+template <int WT, bool SUMS, int TI, int TJ, int U, int WR = 2, int KS = 1>
 static void mmq_launch(const uint8_t* wq, const uint16_t* wd, int N, int nb, const int8_t* aq, const int2* ameta,
                        int M, float* dst, int64_t ldd, int32_t* sums, hipStream_t st) {
-    const dim3 grid((unsigned)((N + 32 * TI - 1) / (32 * TI)), (unsigned)((M + 32 * TJ - 1) / (32 * TJ)));
-    const bool full = N % (32 * TI) == 0 && (!dst || ((uintptr_t)dst & 15) == 0);
+    constexpr int RT = KS == 4 ? 16 * TI : WR * 16 * TI, MT = KS == 4 ? 16 * TJ : (4 / WR) * 16 * TJ;
+    const dim3 grid((unsigned)((N + RT - 1) / RT), (unsigned)((M + MT - 1) / MT));
+    const bool full = N % RT == 0 && (!dst || ((uintptr_t)dst & 15) == 0);
     if (full && nb % U == 0)
-        hipLaunchKernelGGL((k_mmq<WT, SUMS, TI, TJ, U, true, true>), grid, dim3(256), 0, st, wq, wd, N, nb, aq, ameta, M,
-                           dst, ldd, sums);
+        hipLaunchKernelGGL((k_mmq<WT, SUMS, TI, TJ, U, true, true, WR, KS>), grid, dim3(256), 0, st, wq, wd, N, nb, aq,
+                           ameta, M, dst, ldd, sums);
     else
-        hipLaunchKernelGGL((k_mmq<WT, SUMS, TI, TJ, U, false, false>), grid, dim3(256), 0, st, wq, wd, N, nb, aq, ameta,
-                           M, dst, ldd, sums);
+        hipLaunchKernelGGL((k_mmq<WT, SUMS, TI, TJ, U, false, false, WR, KS>), grid, dim3(256), 0, st, wq, wd, N, nb,
+                           aq, ameta, M, dst, ldd, sums);
 }
 
 // Token tile by batch and grid fill (MI355X sweep, 512 tokens): 128-token workgroups (TJ = 4, one block per step)
@@ -195,21 +224,230 @@ template <int WT, bool SUMS>
 static void mmq_dispatch(const uint8_t* wq, const uint16_t* wd, int N, int nb, const int8_t* aq, const int2* ameta,
                          int M, float* dst, int64_t ldd, int32_t* sums, hipStream_t st) {
     const int64_t row_tiles = (N + 127) / 128;
-    if (M <= 32) mmq_launch<WT, SUMS, 4, 1, 2>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
-    else if (M <= 64 || row_tiles * ((M + 127) / 128) < 192)
+    if (M <= 32) {
+        // small batches: one 16 TI x 16 TJ tile per workgroup, its 4 waves splitting k; the largest row tile that
+        // still gives >= 224 workgroups (M = 16: 14336 x 4096 28 us with TI = 4, 4096 x 14336 41 us with TI = 1)
+        const int ti = N / 64 >= 224 ? 4 : (N / 32 >= 224 ? 2 : 1);
+        if (M <= 16) {
+            if (ti == 4) mmq_launch<WT, SUMS, 4, 1, 2, 1, 4>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
+            else if (ti == 2) mmq_launch<WT, SUMS, 2, 1, 4, 1, 4>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
+            else mmq_launch<WT, SUMS, 1, 1, 4, 1, 4>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
+        } else {
+            if (ti == 4) mmq_launch<WT, SUMS, 4, 2, 2, 1, 4>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
+            else if (ti == 2) mmq_launch<WT, SUMS, 2, 2, 2, 1, 4>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
+            else mmq_launch<WT, SUMS, 1, 2, 4, 1, 4>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
+        }
+    } else if (M <= 64 || row_tiles * ((M + 127) / 128) < 192)
         mmq_launch<WT, SUMS, 4, 2, 2>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
     else mmq_launch<WT, SUMS, 4, 4, 1>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q4_K x Q8_K for many tokens on the f16 matrix cores (v_mfma_f32_32x32x16_f16), with ggml's integer structure kept
+// exactly: per 256-weight super-block ggml forms I1 = sum_u sc_u * dot_u (dot_u the int dot of 32-weight unit u) and
+// I2 = sum_u m_u * bsum_u, then adds d_a * (d * I1 - dmin * I2). Here the weight operand carries sc_u * q (<= 945)
+// and the activation operand q_a (<= 127), both exact in f16, so the MFMA's f32 sums are exact integers while they
+// stay below 2^24: each super-block is summed in two accumulators of 128 products (<= 15.4 M each), whose f32 sum
+// rounds exactly as ggml's conversion of the int32 I1. I2 is one more exact MFMA per super-block (m_u against the
+// f16 sums per 16 of the activations). The f32 epilogue thus runs once per 256 weights instead of per 32.
+// Roles: A = activations (32 tokens x 16 k), B = weights (16 k x 32 rows), so lane l's output column is weight row
+// l % 32 (its own scales) and its 16 outputs are tokens 8 (r / 4) + 4 (l / 32) + r % 4. k slots: lane half h owns
+// the weights 128 h .. 128 h + 127 of a super-block (bytes 64 h .. 64 h + 63 of its 128 qs bytes); step s (0..15)
+// takes weights 128 h + 8 s .. + 7 (chunk 2 h + s / 8, nibble (s / 4) % 2, bytes 32 (s / 8) + 8 (s % 4) .. + 7).
+// ---------------------------------------------------------------------------------------------------------------
+typedef _Float16 k4_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 k4_h2 __attribute__((ext_vector_type(2)));
+typedef float k4_f16v __attribute__((ext_vector_type(16)));
+
+// 8 nibbles (bytes of x0, x1 after the nibble select) -> 8 f16 values nib * sc (exact)
+__device__ __forceinline__ k4_h8 k4_nib_f16(uint32_t x0, uint32_t x1, k4_h2 sc2) {
+    const k4_h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t m64 = 0x64646464u;
+    const k4_h2 p0 = __builtin_bit_cast(k4_h2, __builtin_amdgcn_perm(x0, m64, 0x00050004u));  // 1024 + n0, 1024 + n1
+    const k4_h2 p1 = __builtin_bit_cast(k4_h2, __builtin_amdgcn_perm(x0, m64, 0x00070006u));
+    const k4_h2 p2 = __builtin_bit_cast(k4_h2, __builtin_amdgcn_perm(x1, m64, 0x00050004u));
+    const k4_h2 p3 = __builtin_bit_cast(k4_h2, __builtin_amdgcn_perm(x1, m64, 0x00070006u));
+    const k4_h2 v0 = (p0 - off) * sc2, v1 = (p1 - off) * sc2, v2 = (p2 - off) * sc2, v3 = (p3 - off) * sc2;
+    return k4_h8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+}
+
+// KS = 4 (small batches): the 4 waves share one 32 x 32 TT tile and split the super-blocks (wave w takes j = w,
+// w + 4, ...); their f32 partials are added in LDS in wave order.
+template <bool SUMS, int TT, int KS>
+__global__ __launch_bounds__(256) void k_mmq_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
+                                                int nsb, const uint16_t* __restrict__ a16,
+                                                const uint16_t* __restrict__ bs16, const float* __restrict__ dt, int M,
+                                                float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ sums) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = lane & 31, h = lane >> 5;
+    const int row0 = KS == 4 ? blockIdx.x * 32 : blockIdx.x * 64 + 32 * (w & 1);
+    const int tok0 = KS == 4 ? blockIdx.y * (32 * TT) : blockIdx.y * (64 * TT) + 32 * TT * (w >> 1);
+    const int K = nsb * 256;
+    const int row = min(row0 + c, N - 1);
+    const uint4* qrow = wq + (size_t)row * nsb * 8 + 4 * h;  // 8 uint4 of qs per super-block; this half's 4
+    const uint4* hrow = wh + (size_t)row * nsb;
+    const uint16_t* arow[TT];
+    const uint16_t* brow[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int tok = min(tok0 + 32 * t + c, M - 1);
+        arow[t] = a16 + (size_t)tok * K + 128 * h;
+        brow[t] = bs16 + (size_t)tok * (K / 16) + 8 * h;
+    }
+    k4_f16v acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+
+    for (int j = KS == 4 ? w : 0; j < nsb; j += KS) {
+        uint4 q4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q4[i] = qrow[(size_t)j * 8 + i];
+        const uint4 hd = hrow[j];
+        // scales and mins of units 4 h .. 4 h + 3 (get_scale_min_k4 on the 12 packed bytes)
+        int scv[4], mv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) k4_scale_min(4 * h + e, hd.y, hd.z, hd.w, scv[e], mv[e]);
+        k4_f16v C0[TT], C1[TT], I2[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) C0[t][r] = C1[t][r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+            const int jj = st >> 3, nib = (st >> 2) & 1, seg = st & 3;
+            const uint4 v = q4[2 * jj + (seg >> 1)];
+            uint32_t x0 = (seg & 1) ? v.z : v.x, x1 = (seg & 1) ? v.w : v.y;
+            x0 = (x0 >> (4 * nib)) & 0x0F0F0F0Fu;
+            x1 = (x1 >> (4 * nib)) & 0x0F0F0F0Fu;
+            const _Float16 scf = (_Float16)(float)scv[2 * jj + nib];
+            const k4_h8 B = k4_nib_f16(x0, x1, k4_h2{scf, scf});
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const k4_h8 A = *reinterpret_cast<const k4_h8*>(arow[t] + (size_t)j * 256 + 8 * st);
+                if (st < 8) C0[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, C0[t], 0, 0, 0);
+                else C1[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, C1[t], 0, 0, 0);
+            }
+        }
+        // I2: m of the lane's units against the activation sums per 16 (slot e <-> sum 8 h + e <-> unit 4 h + e / 2)
+        {
+            k4_h8 Bm;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) Bm[e] = (_Float16)(float)mv[e >> 1];
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const k4_h8 A = *reinterpret_cast<const k4_h8*>(brow[t] + (size_t)j * 16);
+                k4_f16v z;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) z[r] = 0.0f;
+                I2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bm, z, 0, 0, 0);
+            }
+        }
+        const float d = amv_h2f(hd.x), dmin = amv_h2f(hd.x >> 16);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int tk = tok0 + 32 * t + 8 * r4 + 4 * h;  // tokens tk .. tk + 3 of outputs 4 r4 .. 4 r4 + 3
+                float da[4];
+                if (!SUMS) {
+                    if (tk + 3 < M && (M & 3) == 0) {
+                        const float4 d4 = *reinterpret_cast<const float4*>(dt + (size_t)j * M + tk);
+                        da[0] = d4.x; da[1] = d4.y; da[2] = d4.z; da[3] = d4.w;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) da[e] = dt[(size_t)j * M + min(tk + e, M - 1)];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * r4 + e;
+                    if (SUMS) {
+                        const int tok = tk + e, n = row0 + c;
+                        if (tok < M && n < N) {
+                            int32_t* o = sums + (((size_t)tok * N + n) * nsb + j) * 2;
+                            o[0] = (int)C0[t][r] + (int)C1[t][r];
+                            o[1] = (int)I2[t][r];
+                        }
+                    } else {
+                        const float i1 = C0[t][r] + C1[t][r];
+                        acc[t][r] = fmaf(da[e], fmaf(d, i1, -dmin * I2[t][r]), acc[t][r]);
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (KS == 4 && !SUMS) {
+        __shared__ float red[3][TT * 16][64];
+        if (w > 0) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[w - 1][t * 16 + r][lane] = acc[t][r];
+        }
+        __syncthreads();
+        if (w > 0) return;
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                acc[t][r] = ((acc[t][r] + red[0][t * 16 + r][lane]) + red[1][t * 16 + r][lane]) + red[2][t * 16 + r][lane];
+    }
+    if (!SUMS) {
+        const int n = row0 + c;
+        if (n < N) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int tok = tok0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (tok < M) dst[(size_t)tok * ldd + n] = acc[t][r];
+                }
+        }
+    }
+}
+
+static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
+                   int32_t* sums, hipStream_t st) {
+    AMV_REQUIRE(k % 256 == 0, "amv_mul_mat_q: Q4_K needs k %% 256 == 0");
+    const int nsb = (int)(k / 256);
+    const int64_t nblk = n_rows * nsb;
+    const uint4* wq = (const uint4*)w;
+    const uint4* wh = (const uint4*)((const uint8_t*)w + nblk * 128);
+    const AmvQ8kMma L = amv_q8k_mma_layout(m, k);
+    const uint16_t* a16 = (const uint16_t*)((const uint8_t*)act + L.a16);
+    const uint16_t* bs16 = (const uint16_t*)((const uint8_t*)act + L.bs16);
+    const float* dt = (const float*)((const uint8_t*)act + L.dt);
+    const unsigned gx = (unsigned)((n_rows + 63) / 64);
+#define Q4K_LAUNCH(TT, KS, G) \
+    do { \
+        if (sums) hipLaunchKernelGGL((k_mmq_q4k<true, TT, KS>), G, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, \
+                                     bs16, dt, (int)m, dst, ldd, sums); \
+        else hipLaunchKernelGGL((k_mmq_q4k<false, TT, KS>), G, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, \
+                                dt, (int)m, dst, ldd, sums); \
+    } while (0)
+    if (m <= 32) {
+        // small batches: one 32-row x 32-token tile per workgroup, the 4 waves splitting the super-blocks
+        Q4K_LAUNCH(1, 4, dim3((unsigned)((n_rows + 31) / 32), (unsigned)((m + 31) / 32)));
+    } else if (m <= 64) {
+        Q4K_LAUNCH(1, 1, dim3(gx, (unsigned)((m + 63) / 64)));
+    } else {
+        Q4K_LAUNCH(2, 1, dim3(gx, (unsigned)((m + 127) / 128)));
+    }
+#undef Q4K_LAUNCH
+    return amv_check_launch("amv_mul_mat_q");
 }
 
 static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                     int64_t ldd, int32_t* sums, void* stream) {
     AMV_REQUIRE(w && act && (dst || sums), "amv_mul_mat_q: null pointer");
-    AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0, "amv_mul_mat_q: weight type %d not supported (Q4_0, Q8_0)",
-                wtype);
+    AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0 || wtype == AMV_T_Q4_K,
+                "amv_mul_mat_q: weight type %d not supported (Q4_0, Q8_0, Q4_K)", wtype);
     AMV_REQUIRE(n_rows > 0 && m > 0 && k > 0 && k % 32 == 0, "amv_mul_mat_q: bad shape");
     AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 32 && n_rows * (k / 32) <= INT32_MAX, "amv_mul_mat_q: too large");
     AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "amv_mul_mat_q: buffers must be 16-byte aligned");
     AMV_REQUIRE(!dst || ldd >= n_rows, "amv_mul_mat_q: ldd < n_rows");
+    if (wtype == AMV_T_Q4_K) return mmq_q4k(w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
     const int nb = (int)(k / 32);
     const int64_t nblk = n_rows * nb;
     const uint8_t* wq = (const uint8_t*)w;

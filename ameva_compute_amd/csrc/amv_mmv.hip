@@ -232,22 +232,6 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
 // Per super-block ggml's vec_dot_q4_K_q8_K computes d*da*sum_u sc_u dot_u - dmin*da*sum_u m_u bsum_u and
 // vec_dot_q6_K_q8_K d*da*sum_g sc_g dot(q6 - 32, qa)_g; the lanes form the same integers per slice.
 
-// byte i (0..11) of the packed 6-bit scales held in three words
-__device__ __forceinline__ uint32_t k4_byte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
-    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-    return (w >> (8 * (i & 3))) & 0xFFu;
-}
-// get_scale_min_k4 (reference ameva_qdecode.glsl:229-236)
-__device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc, int& m) {
-    if (j < 4) {
-        sc = (int)(k4_byte(s0, s1, s2, j) & 63u);
-        m = (int)(k4_byte(s0, s1, s2, j + 4) & 63u);
-    } else {
-        sc = (int)((k4_byte(s0, s1, s2, j + 4) & 0xFu) | ((k4_byte(s0, s1, s2, j - 4) >> 6) << 4));
-        m = (int)((k4_byte(s0, s1, s2, j + 4) >> 4) | ((k4_byte(s0, s1, s2, j) >> 6) << 4));
-    }
-}
-
 __device__ __forceinline__ int dot16(uint4 w, int4 a, int acc) {
     acc = amv_dot4((int)w.x, a.x, acc);
     acc = amv_dot4((int)w.y, a.y, acc);

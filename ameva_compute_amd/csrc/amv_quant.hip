@@ -49,9 +49,13 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x,
 // max = the element of largest magnitude (the first on ties), iscale = -127/max, q = min(127, round-half-even(
 // iscale * x)), d = 1/iscale, bsums = sums of q over 16 elements.
 // ---------------------------------------------------------------------------------------------------------------
+// With a16 (AMV_ACT_Q8_K_MMA) the block's values also go out as f16, its sums per 16 as f16 and its scale transposed
+// (token t = b / nsb, super-block j = b % nsb at dt[j * m + t]).
 __global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x, int64_t n_blk,
                                                    uint8_t* __restrict__ y_ggml, int8_t* __restrict__ aq,
-                                                   float* __restrict__ ad, int32_t* __restrict__ abs16) {
+                                                   float* __restrict__ ad, int32_t* __restrict__ abs16,
+                                                   uint16_t* __restrict__ a16, uint16_t* __restrict__ bs16,
+                                                   float* __restrict__ dt, int nsb, int m) {
     const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= n_blk) return;  // uniform per wave
     const int lane = threadIdx.x & 63;
@@ -82,6 +86,11 @@ __global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x,
             if (lane < 16) abs16[b * 16 + lane] = 0;
             if (lane == 0) ad[b] = 0.0f;
         }
+        if (a16) {
+            reinterpret_cast<uint2*>(a16 + b * 256)[lane] = make_uint2(0u, 0u);
+            if (lane < 16) bs16[b * 16 + lane] = 0;
+            if (lane == 0) dt[(b % nsb) * m + b / nsb] = 0.0f;
+        }
         return;
     }
     const float mx = __shfl(v[ai & 3], ai >> 2, AMV_WAVE);
@@ -108,6 +117,13 @@ __global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x,
         reinterpret_cast<int*>(aq + b * 256)[lane] = packed;
         if ((lane & 3) == 0) abs16[b * 16 + (lane >> 2)] = s;
         if (lane == 0) ad[b] = d;
+    }
+    if (a16) {
+        const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)q[0]), h1 = __builtin_bit_cast(uint16_t, (_Float16)q[1]);
+        const uint32_t h2 = __builtin_bit_cast(uint16_t, (_Float16)q[2]), h3 = __builtin_bit_cast(uint16_t, (_Float16)q[3]);
+        reinterpret_cast<uint2*>(a16 + b * 256)[lane] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+        if ((lane & 3) == 0) bs16[b * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)s);
+        if (lane == 0) dt[(b % nsb) * m + b / nsb] = d;
     }
 }
 
@@ -335,14 +351,25 @@ extern "C" int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, 
         int8_t* aq = y_act ? (int8_t*)y_act : nullptr;
         int2* ads = y_act ? (int2*)((uint8_t*)y_act + n) : nullptr;
         hipLaunchKernelGGL(k_quant_q8_0, grid_for(n, 256), 256, 0, st, x, n, rule, (uint8_t*)y_ggml, aq, ads);
-    } else if (type == AMV_T_Q8_K) {
+    } else if (type == AMV_T_Q8_K || type == AMV_ACT_Q8_K_MMA) {
         AMV_REQUIRE(k % 256 == 0, "amv_quantize_act: Q8_K needs k %% 256 == 0 (k = %lld)", (long long)k);
         AMV_REQUIRE(y_ggml == nullptr || ((uintptr_t)y_ggml & 3) == 0, "amv_quantize_act: y_ggml misaligned");
+        AMV_REQUIRE(type == AMV_T_Q8_K || y_act, "amv_quantize_act: AMV_ACT_Q8_K_MMA needs y_act");
+        AMV_REQUIRE(m * (k / 256) <= INT32_MAX, "amv_quantize_act: too many blocks");
         const int64_t n = m * k, nb = n / 256;
         int8_t* aq = y_act ? (int8_t*)y_act : nullptr;
         float* ad = y_act ? (float*)((uint8_t*)y_act + n) : nullptr;
         int32_t* abs16 = y_act ? (int32_t*)((uint8_t*)y_act + n + nb * 4) : nullptr;
-        hipLaunchKernelGGL(k_quant_q8_K, grid_for(nb, 4), 256, 0, st, x, nb, (uint8_t*)y_ggml, aq, ad, abs16);
+        uint16_t *a16 = nullptr, *bs16 = nullptr;
+        float* dt = nullptr;
+        if (type == AMV_ACT_Q8_K_MMA) {
+            const AmvQ8kMma L = amv_q8k_mma_layout(m, k);
+            a16 = (uint16_t*)((uint8_t*)y_act + L.a16);
+            bs16 = (uint16_t*)((uint8_t*)y_act + L.bs16);
+            dt = (float*)((uint8_t*)y_act + L.dt);
+        }
+        hipLaunchKernelGGL(k_quant_q8_K, grid_for(nb, 4), 256, 0, st, x, nb, (uint8_t*)y_ggml, aq, ad, abs16, a16,
+                           bs16, dt, (int)(k / 256), (int)m);
     } else {
         amv_set_error("amv_quantize_act: unsupported activation type %d", type);
         return AMV_ERR_UNSUPPORTED;

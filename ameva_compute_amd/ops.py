@@ -35,8 +35,15 @@ def _need_gpu(t: torch.Tensor, what: str, contiguous: bool = True) -> None:
         raise ValueError(f"{what}: tensor must be contiguous")
 
 
-def act_type(wtype: int) -> int:
-    """ggml vec_dot_type of a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants."""
+# Q8_K activations with the f16 copies the batched Q4_K MUL_MAT reads (include/ameva_hip.h AMV_ACT_Q8_K_MMA)
+Q8_K_MMA = 1015
+
+
+def act_type(wtype: int, m: int = 1) -> int:
+    """ggml vec_dot_type of a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants; for a batched Q4_K MUL_MAT
+    (m >= MMQ_MIN_M) the Q8_K layout extended for the matrix cores."""
+    if wtype == Q4_K and m >= MMQ_MIN_M:
+        return Q8_K_MMA
     return Q8_K if wtype in (Q4_K, Q6_K) else Q8_0
 
 
@@ -87,7 +94,8 @@ def quantize_act(x: torch.Tensor, atype: int = Q8_0, rule: int = Q8_X86, ggml: b
     if n < 0:
         raise ValueError(f"quantize_act: type {atype} cannot hold rows of {k}")
     act = torch.empty(n, dtype=torch.uint8, device=x.device)
-    g = torch.empty((m, ggml_row_bytes(atype, k)), dtype=torch.uint8, device=x.device) if ggml else None
+    gt = Q8_K if atype == Q8_K_MMA else atype
+    g = torch.empty((m, ggml_row_bytes(gt, k)), dtype=torch.uint8, device=x.device) if ggml else None
     check(lib().amv_quantize_act(atype, x2.data_ptr(), m, k, rule, _ptr(g), act.data_ptr(), _stream()),
           "amv_quantize_act")
     return act, g
@@ -105,13 +113,14 @@ def quantize_q4_0(x: torch.Tensor) -> torch.Tensor:
 
 # batch size from which MUL_MAT runs the int8-MFMA kernel (AMEVA_QGEMM_MIN_M of the reference, ggml-ameva.cpp:2486)
 MMQ_MIN_M = 8
-MMQ_TYPES = (Q4_0, Q8_0)
+MMQ_TYPES = (Q4_0, Q8_0, Q4_K)  # Q4_K: the activations must be Q8_K_MMA
 
 
 def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = None,
               kernel: str = "auto") -> torch.Tensor:
     """dst [m, n_rows] f32 from already quantized activations (amv_quantize_act layout of m rows).
-    kernel: "auto" (the reference's routing: MFMA GEMM for m >= MMQ_MIN_M where the type has one), "mmv", "mmq"."""
+    kernel: "auto" (the reference's routing: MFMA GEMM for m >= MMQ_MIN_M where the type has one), "mmv", "mmq".
+    Q4_K on "mmq" needs the activations quantized as Q8_K_MMA (act_type(Q4_K, m))."""
     _need_gpu(act, "mul_mat_q")
     if out is None:
         out = torch.empty((m, w.n_rows), dtype=torch.float32, device=act.device)
@@ -149,7 +158,7 @@ def mul_mat(w: QWeight, x: torch.Tensor, rule: int = Q8_X86) -> torch.Tensor:
     x2 = x.reshape(-1, x.shape[-1])
     if x2.shape[1] != w.k:
         raise ValueError(f"mul_mat: k mismatch {x2.shape[1]} != {w.k}")
-    act, _ = quantize_act(x2, act_type(w.type), rule)
+    act, _ = quantize_act(x2, act_type(w.type, x2.shape[0]), rule)
     return mul_mat_q(w, act, x2.shape[0])
 
 

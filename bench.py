@@ -200,6 +200,32 @@ def secondary_gemvs(ops, torch, dev):
     return res
 
 
+def bench_batched(ops, torch, dev):
+    """Q4_0 / Q8_0 / Q4_K MUL_MAT at the Llama-3-8B FFN shapes with token batches 16 and 512 (the
+    int8 / f16 matrix-core kernels), 2 M N K integer ops per call."""
+    res = {}
+    g = torch.Generator(device=dev)
+    for wname, wtype in (("q4_0", ops.Q4_0), ("q8_0", ops.Q8_0), ("q4_K", ops.Q4_K)):
+        for n, k in ((14336, 4096), (4096, 14336)):
+            w = make_weights(ops, torch, n, k, 1, 300 + n, dev, wtype)[0]
+            for m in (16, 512):
+                g.manual_seed(m + n)
+                x = torch.randn((m, k), generator=g, device=dev)
+                act, _ = ops.quantize_act(x, ops.act_type(wtype, m), ops.Q8_X86)
+                out = torch.empty((m, n), dtype=torch.float32, device=dev)
+                ms = time_steps_graph(torch, lambda i: ops.mul_mat_q(w, act, m, out), 50 if m == 512 else 200, 10,
+                                      per_graph=10)
+                tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+                key = f"{wname}_{n}x{k}_m{m}"
+                res[key + "_us"] = round(ms * 1e3, 2)
+                res[key + "_tops"] = round(tops, 1)
+                log(f"bench: {key} {ms * 1e3:.1f} us = {tops:.1f} TOPS ({tops / INT8_MFMA_PEAK_TOPS * 100:.1f}% of "
+                    f"int8 MFMA peak)")
+            del w
+            torch.cuda.empty_cache()
+    return res
+
+
 def bench_i2s(ops, torch, dev):
     """BitNet I2_S GEMV, batch 1, cold over 120 copies of each 4.4 MB weight."""
     res = {}
@@ -339,6 +365,7 @@ def main():
     ap.add_argument("--only-headline", action="store_true", help="skip the secondary figures (for profiling)")
     ap.add_argument("--only-layer", action="store_true", help="only the layer decode figure (for profiling)")
     ap.add_argument("--only-i2s", action="store_true", help="only the BitNet I2_S figures (for profiling)")
+    ap.add_argument("--only-batched", action="store_true", help="only the batched MUL_MAT figures (for profiling)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
@@ -359,6 +386,9 @@ def main():
         return
     if args.only_layer:
         print(json.dumps(bench_layer(torch, dev, args)), flush=True)
+        return
+    if args.only_batched:
+        print(json.dumps(bench_batched(ops, torch, dev)), flush=True)
         return
     if args.only_i2s:
         print(json.dumps(bench_i2s(ops, torch, dev)), flush=True)
@@ -400,6 +430,7 @@ def main():
         del ws
         torch.cuda.empty_cache()
         extra.update(secondary_gemvs(ops, torch, dev))
+        extra.update(bench_batched(ops, torch, dev))
         extra.update(bench_i2s(ops, torch, dev))
         extra.update(copy_ceiling(torch, dev, nbytes))
 

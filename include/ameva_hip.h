@@ -27,6 +27,7 @@ extern "C" {
  *   AMV_Q8_X86: d = amax/127, q = round-half-even(x * (127/amax))   -- ggml-cpu x86 quantize_row_q8_0 (default)
  *   AMV_Q8_ARM: d = amax/127, q = round-half-even(x * (1/d))        -- ggml-cpu ARM (ameva_quant_a8.comp:5)
  *   AMV_Q8_REF: d = amax/127, q = roundf(x * (1/d))                  -- quantize_row_q8_0_ref (weights, KV cache) */
+#define AMV_ACT_Q8_K_MMA 1015 /* Q8_K activations with the f16 copies the batched K-quant MUL_MAT reads */
 #define AMV_Q8_X86 0
 #define AMV_Q8_ARM 1
 #define AMV_Q8_REF 2
@@ -60,7 +61,11 @@ int amv_unrepack(int type, const void* src, void* dst_ggml, int64_t n_rows, int6
  *   y_act:  the kernels' activation layout, amv_act_bytes(type, m, k) bytes:
  *           Q8_0: qs int8[m][k] | {f32 d (fp16-rounded, as ggml uses it), i32 sum(qs)}[m][k/32]
  *           Q8_K: qs int8[m][k] | f32 d[m][k/256] | i32 sum(qs)[m][k/16]
- * type AMV_T Q8_0 (8) or Q8_K (15); rule applies to Q8_0 only.
+ *           AMV_ACT_Q8_K_MMA: the Q8_K layout, then (16-byte aligned) the same values as f16 [m][k] (exact), the
+ *           sums per 16 as f16 [m][k/16] and (16-byte aligned) the super-block scales transposed, f32 [k/256][m]:
+ *           the input of the batched Q4_K MUL_MAT (amv_mul_mat_q), which feeds the matrix cores in f16; its Q8_K
+ *           prefix is a plain Q8_K activation of the m rows (amv_mul_mat_vec reads it as such).
+ * type AMV_T Q8_0 (8), Q8_K (15) or AMV_ACT_Q8_K_MMA; rule applies to Q8_0 only.
  * ---------------------------------------------------------------------------------------------------------- */
 int64_t amv_act_bytes(int type, int64_t m, int64_t k);
 int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, int rule, void* y_ggml, void* y_act,

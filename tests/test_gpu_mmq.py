@@ -85,3 +85,37 @@ def test_routing_matches_reference_threshold(dev, ops, orc):
         y = ops.mul_mat(w, gpu(x, dev)).cpu().numpy()
         y_ref = orc.mul_mat(2, wg, n, k, orc.quantize_q8_0(x, orc.Q8_X86), m)
         assert rel_l2(y, y_ref) < TOL_F32
+
+
+def random_q4k(rng, n, k):
+    """Random bytes are valid Q4_K blocks once the fp16 d, dmin are small finite values (6-bit scales and mins and
+    nibbles then take every value, the worst case of the exact-sum bounds)."""
+    y = rng.integers(0, 256, (n, k // 256, 144), dtype=np.uint8)
+    for off in (0, 2):
+        v = rng.uniform(0.0, 0.002, (n, k // 256)).astype(np.float16)
+        y[:, :, off:off + 2] = v.view(np.uint8).reshape(n, k // 256, 2)
+    return y.reshape(n, -1)
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 64, 256), (16, 300, 1024), (70, 129, 512), (512, 256, 4096),
+                                   (512, 64, 14336), (130, 14336 // 8, 4096)])
+def test_mmq_q4k_block_sums_and_output(dev, ops, orc, m, n, k):
+    """Batched Q4_K on the f16 matrix cores: the per-super-block integers (sum sc * dot, sum m * bsum) bit-exact
+    against the oracle, f32 within 1e-3; the Q8_K prefix of the extended activations is the plain Q8_K layout."""
+    rng = np.random.default_rng(m + n + k)
+    wg = random_q4k(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0, :300] *= 40.0  # large activations: |q| = 127 across whole blocks
+    a_ref = orc.quantize_q8_K(x)
+    y_ref, s_ref = orc.mul_mat(ops.Q4_K, wg, n, k, a_ref, m, with_blocks=True)
+    w = ops.QWeight.from_ggml(ops.Q4_K, gpu(wg, dev), n, k)
+    act, ag = ops.quantize_act(gpu(x, dev), ops.Q8_K_MMA, ggml=True)
+    assert np.array_equal(ag.cpu().numpy(), a_ref)
+    plain, _ = ops.quantize_act(gpu(x, dev), ops.Q8_K)
+    assert torch.equal(act[: plain.numel()], plain)
+    sums = ops.block_sums(w, act, m, kernel="mmq").cpu().numpy()
+    assert np.array_equal(sums, s_ref)
+    y = ops.mul_mat_q(w, act, m, kernel="mmq").cpu().numpy()
+    assert rel_l2(y, y_ref) < TOL_F32
+    y_v = ops.mul_mat_q(w, act, m, kernel="mmv").cpu().numpy()  # the GEMV on the same buffer's Q8_K prefix
+    assert rel_l2(y, y_v) < 1e-5
