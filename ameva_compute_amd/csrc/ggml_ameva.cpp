@@ -11,7 +11,8 @@
 //     repack of ggml-ameva.cpp:5352-5373) and converted back by get_tensor, so other backends see ggml bytes;
 //   * MUL_MAT routes like enc_mul_mat (3607): int8-MFMA GEMM from 8 columns for Q4_0 / Q8_0, GEMV otherwise; the
 //     quantized activations of one src1 are reused by every MUL_MAT that reads it (the a8_src cache, 2738-2749);
-//   * RMS_NORM followed by a MUL by the norm weight runs as one kernel (ameva_find_fusion, 4345);
+//   * RMS_NORM followed by a MUL by the norm weight runs as one kernel (ameva_find_fusion, 4345), and a one-row
+//     MUL_MAT followed by ADD or GLU SWIGLU (split) by the GEMV's epilogue (the reference's MUL_MAT fusion pairs);
 //   * counters and failure injection as ggml-ameva.h:30-98.
 // On MI355X the Vulkan hazard tracking of the reference (ameva_record, 2174) is the in-order stream itself: each
 // kernel starts after the previous one has finished, so no barrier bookkeeping is needed.
@@ -469,10 +470,16 @@ struct Engine {
         return act;
     }
 
-    bool mul_mat(const ggml_tensor* n) {
+    // ep: the fused next node (ADD, or GLU SWIGLU split) of a one-row MUL_MAT, computed in the GEMV's epilogue
+    bool mul_mat(const ggml_tensor* n, const ggml_tensor* ep = nullptr) {
         const ggml_tensor *w = n->src[0], *x = n->src[1];
         const int64_t N = w->ne[1], K = w->ne[0], M = nrows(x);
-        const int atype = (w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K) ? GGML_TYPE_Q8_K : GGML_TYPE_Q8_0;
+        // batched (M >= 8) MUL_MATs run on the matrix cores for Q4_0 / Q8_0 / Q4_K (the reference's switch at
+        // AMEVA_QGEMM_MIN_M); batched Q4_K reads the Q8_K activations extended with their f16 copies
+        const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K);
+        const int atype = (w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K)
+                              ? (mmq && w->type == GGML_TYPE_Q4_K ? AMV_ACT_Q8_K_MMA : (int)GGML_TYPE_Q8_K)
+                              : (int)GGML_TYPE_Q8_0;
         // src0 in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized tensor of any
         // other buffer is repacked into scratch for this use
         const void* wp = w->data;
@@ -497,9 +504,21 @@ struct Engine {
         void* act = act_for(n, x, atype, M, K);
         if (!act) return false;
         if (g_fail.load() == AMEVA_FAIL_DISPATCH) return fail(n, "failure injection: dispatch");
-        const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0);
-        const int r = mmq ? amv_mul_mat_q(w->type, wp, N, K, act, M, (float*)n->data, N, st)
-                          : amv_mul_mat_vec(w->type, wp, N, K, act, M, (float*)n->data, N, st);
+        int r;
+        if (ep) {
+            const ggml_tensor* e = ep->src[0] == n ? ep->src[1] : ep->src[0];
+            int mode = AMV_EP_ADD;
+            if (ep->op == GGML_OP_GLU) {
+                const bool swapped = ep->op_params[1] != 0;  // swapped: silu(src1) * src0
+                const bool n_is_gate = (ep->src[0] == n) != swapped;
+                mode = n_is_gate ? AMV_EP_SILU_MUL : AMV_EP_MUL_SILU;
+            }
+            r = amv_mul_mat_vec_ep(w->type, wp, N, K, act, (float*)n->data, mode, (const float*)e->data,
+                                   (float*)ep->data, st);
+        } else {
+            r = mmq ? amv_mul_mat_q(w->type, wp, N, K, act, M, (float*)n->data, N, st)
+                    : amv_mul_mat_vec(w->type, wp, N, K, act, M, (float*)n->data, N, st);
+        }
         if (!rc(n, r)) return false;
         g_cnt.mul_mat++;
         g_cnt.qmv++;
@@ -596,7 +615,7 @@ struct Engine {
             const ggml_tensor* n = g->nodes[i];
             if (n->op == GGML_OP_MUL_MAT) {
                 s += (size_t)amv_act_bytes(GGML_TYPE_Q8_0, nrows(n->src[1]), n->src[1]->ne[0]) + 4096;
-                s += (size_t)amv_act_bytes(GGML_TYPE_Q8_K, nrows(n->src[1]), (n->src[1]->ne[0] + 255) / 256 * 256) + 4096;
+                s += (size_t)amv_act_bytes(AMV_ACT_Q8_K_MMA, nrows(n->src[1]), (n->src[1]->ne[0] + 255) / 256 * 256) + 4096;
                 if (n->src[0]->buffer->usage != GGML_BACKEND_BUFFER_USAGE_WEIGHTS) s += nbytes(n->src[0]) + 256;
             } else if (n->op == GGML_OP_FLASH_ATTN_EXT) {
                 const int64_t ws = amv_flash_attn_workspace_bytes(n->src[0]->ne[2], n->src[1]->ne[2], n->src[1]->ne[1], 128);
@@ -620,13 +639,49 @@ struct Engine {
         return m;
     }
 
+    // ADD or GLU SWIGLU (split form) right after a one-row GEMV MUL_MAT that consumes its result with a contiguous f32
+    // vector of N elements: computed in the GEMV's epilogue (ameva_find_fusion's MUL_MAT pairs); the MUL_MAT's own
+    // output is still written. The fused output must not overlap the activation row, the weight, the MUL_MAT output or
+    // the other operand.
+    static bool overlaps(const ggml_tensor* a, const ggml_tensor* b) {
+        const uint8_t *a0 = (const uint8_t*)a->data, *b0 = (const uint8_t*)b->data;
+        return a0 < b0 + nbytes(b) && b0 < a0 + nbytes(a);
+    }
+    static const ggml_tensor* fusable_epilogue(const ggml_cgraph* g, int i) {
+        const ggml_tensor* n = g->nodes[i];
+        if (i + 1 >= g->n_nodes || nrows(n->src[1]) != 1) return nullptr;
+        const ggml_type wt = n->src[0]->type;
+        if (wt != GGML_TYPE_Q4_0 && wt != GGML_TYPE_Q8_0 && wt != GGML_TYPE_Q4_K && wt != GGML_TYPE_Q6_K) return nullptr;
+        const ggml_tensor* e = g->nodes[i + 1];
+        if (e->op != GGML_OP_ADD && !(e->op == GGML_OP_GLU && e->src[1] && e->op_params[0] == GGML_GLU_OP_SWIGLU))
+            return nullptr;
+        const ggml_tensor* other = e->src[0] == n ? e->src[1] : (e->src[1] == n ? e->src[0] : nullptr);
+        const int64_t N = n->ne[0];
+        if (!other || other == n || other->type != GGML_TYPE_F32 || nelements(other) != N || !is_contiguous(other))
+            return nullptr;
+        if (e->type != GGML_TYPE_F32 || nelements(e) != N || !is_contiguous(e)) return nullptr;
+        if (overlaps(e, n->src[1]) || overlaps(e, n) || overlaps(e, other) || overlaps(e, n->src[0])) return nullptr;
+        return e;
+    }
+
     bool run(ggml_cgraph* g) {
         for (int i = 0; i < g->n_nodes; ++i) {
             const ggml_tensor* n = g->nodes[i];
             if (noop(n->op)) continue;
             bool ok = true;
             switch (n->op) {
-            case GGML_OP_MUL_MAT: ok = mul_mat(n); break;
+            case GGML_OP_MUL_MAT: {
+                const ggml_tensor* e = fusable_epilogue(g, i);
+                ok = mul_mat(n, e);
+                if (ok && e) {
+                    invalidate(n);
+                    g_cnt.gpu_op++;
+                    g_cnt.fused++;
+                    ++i;
+                    n = e;
+                }
+                break;
+            }
             case GGML_OP_RMS_NORM: {
                 const ggml_tensor* m = fusable_mul(g, i);
                 ok = rms_norm(n, m);

@@ -311,8 +311,9 @@ class Graph:
         return self._node(OP_FLASH_ATTN_EXT, F32, [v.ne[0], q.ne[2], q.ne[1], 1], [q, k, v, mask], name,
                           [scale, 0.0, 0.0])
 
-    def swiglu(self, g: Tensor, u: Tensor, name="swiglu") -> Tensor:
-        return self._node(OP_GLU, F32, list(g.ne), [g, u], name, [GLU_SWIGLU, 0])
+    def swiglu(self, g: Tensor, u: Tensor, name="swiglu", swapped: bool = False) -> Tensor:
+        """ggml_swiglu_split: silu(src0) * src1; swapped (op_params[1] = 1): silu(src1) * src0."""
+        return self._node(OP_GLU, F32, list(g.ne), [g, u], name, [GLU_SWIGLU, 1 if swapped else 0])
 
     def set_rows(self, dst: Tensor, src: Tensor, idx: Tensor, name="set_rows") -> Tensor:
         x = self._new(dst.type, list(dst.ne), "c", name, data=(dst.data, dst.buffer), nb=list(dst.nb))

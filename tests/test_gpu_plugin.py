@@ -68,7 +68,7 @@ def test_mul_mat_node(plugin, orc, wt, m):
         y = g.get(Y, np.float32, (m, n))
         assert rel_l2(y, orc.mul_mat(wt, wg, n, k, aq(x), m)) < 1e-3
         assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 1
-        assert gp.counter(plugin, "mmq_mul_mat_count") == (1 if m >= 8 and wt in (gp.Q4_0, gp.Q8_0) else 0)
+        assert gp.counter(plugin, "mmq_mul_mat_count") == (1 if m >= 8 and wt in (gp.Q4_0, gp.Q8_0, gp.Q4_K) else 0)
         assert gp.counter(plugin, "repacked_tensor_count") == rep0 + 1
         # the weight reads back in ggml layout, byte for byte
         assert np.array_equal(g.get(W, np.uint8), wg.reshape(-1))
@@ -106,6 +106,43 @@ def test_activation_reuse_and_norm_fusion(plugin, orc):
         assert gp.counter(plugin, "fused_pair_count") == 1
         assert gp.counter(plugin, "act_quant_reuse_count") == 1
         assert gp.counter(plugin, "gpu_op_count") == 4
+    finally:
+        g.free()
+
+
+@pytest.mark.parametrize("form", ["add", "gate", "up", "gate_swapped"])
+def test_mul_mat_epilogue_fusion(plugin, orc, form):
+    """A one-row MUL_MAT followed by ADD or GLU SWIGLU (split) runs as the GEMV's epilogue: the fused node's value and
+    the MUL_MAT's own output both match the unfused ops (ggml_swiglu_split(a, b) = silu(a) * b; swapped: silu(b) * a)."""
+    rng = np.random.default_rng(len(form))
+    k, n = 4096, 1024
+    wg = quantize(orc, gp.Q4_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    e = (rng.standard_normal((1, n)) * 2).astype(np.float32)
+    g = gp.Graph(wg.nbytes + 8192, 32 << 20)
+    try:
+        plugin.ggml_backend_ameva_reset_counters()
+        W, X, E = g.tensor(gp.Q4_0, [k, n], "w", "w"), g.tensor(gp.F32, [k, 1], "c", "x"), g.tensor(gp.F32, [n, 1], "c", "e")
+        for t, a in ((W, wg), (X, x), (E, e)):
+            g.set(t, a)
+        Y = g.mul_mat(W, X)
+        if form == "add":
+            Z = g.add(Y, E)
+        elif form == "gate":
+            Z = g.swiglu(Y, E)
+        elif form == "up":
+            Z = g.swiglu(E, Y)
+        else:
+            Z = g.swiglu(E, Y, swapped=True)  # silu(Y) * E with Y as src1
+        assert g.compute() == gp.STATUS_SUCCESS
+        y_ref = orc.mul_mat(gp.Q4_0, wg, n, k, orc.quantize_q8_0(x, orc.Q8_X86), 1).reshape(1, n)
+        y = g.get(Y, np.float32, (1, n))
+        assert rel_l2(y, y_ref) < 1e-3
+        z = g.get(Z, np.float32, (1, n))
+        ref = {"add": y + e, "gate": orc.swiglu(y, e), "up": orc.swiglu(e, y), "gate_swapped": orc.swiglu(y, e)}[form]
+        assert rel_l2(z, ref) < 1e-6
+        assert gp.counter(plugin, "fused_pair_count") == 1
+        assert gp.counter(plugin, "gpu_op_count") == 2
     finally:
         g.free()
 
@@ -231,7 +268,8 @@ def test_llama3_8b_decode_layer(plugin, orc):
         assert g.compute() == gp.STATUS_SUCCESS
         y = g.get(out, np.float32, (1, H))
         assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 7
-        assert gp.counter(plugin, "fused_pair_count") == 2
+        # RMS_NORM+MUL twice; the o and down projections + residual ADD, the up projection + SWIGLU as GEMV epilogues
+        assert gp.counter(plugin, "fused_pair_count") == 5
         assert gp.counter(plugin, "act_quant_reuse_count") == 3  # k, v share q's; up shares gate's
 
         # the oracle's chain of the same ops
