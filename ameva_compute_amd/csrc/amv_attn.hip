@@ -5,199 +5,303 @@
 // V load. ggml's CPU kernel rounds q to f16 before the dot with f16 K; so does this one. Scores, probabilities and
 // accumulators are f32.
 //
-// Pass 1 (k_fa_split): one workgroup of 256 per (key split, KV head). 16 lanes read one 256-byte K row (8 halves
-// each) and form the G partial dots, reduced over the 16 lanes; the split's scores go to LDS; per head the split
-// maximum m and l = sum exp(s - m); then each wave accumulates V rows (a lane owns 2 of the 128 dims) for its keys,
-// and the 4 waves' accumulators are summed in LDS. The partial (m, l, acc[D]) of every (head, split) goes to the
-// workspace. Pass 2 (k_fa_combine): per head M = max m_z, L = sum l_z e^(m_z - M), out = sum acc_z e^(m_z - M) / L.
+// Pass 1 (k_fa_split): one workgroup of 4 waves per (key split, KV head); each wave owns KPW consecutive keys and
+// works alone (16 lanes per 256-byte K/V row, G partial dots reduced over the 16 lanes, wave maximum, probabilities
+// and P V in registers); the 4 wave partials meet once in LDS and the workgroup's (m, l, acc[D]) per head goes to
+// the workspace. Pass 2 (fa_merge): per head M = max m_z, w_z = e^(m_z - M), L = sum l_z w_z,
+// out = sum w_z acc_z / L, with the quantization of the output for the next MUL_MAT fused. The merge runs either
+// as its own launch (k_fa_combine, one workgroup per head) or in the last workgroup of each KV head to finish its
+// split (one launch per decode step); both use the same code, so their outputs are identical. On MI355X the second
+// launch is the faster of the two at Llama shapes (a single merging workgroup per KV head sits on the critical path
+// after the arrival).
 #include "amv_common.h"
 
 #define FA_D 128
+#define FA_PS (FA_D + 4)        // floats per partial: m, l, 2 pad, acc[D] (16-byte aligned rows)
+#define FA_MAX_NSPLIT 1024      // splits per head (n_kv <= 128 K keys)
+
+// Merge of the split partials of the G heads of KV head hk by the 256 threads of a workgroup; sbuf holds at least
+// G * (8 * FA_D + FA_MAX_NSPLIT) + G floats of LDS.
+//   per head (one wave per head): M = max m_z, w_z = e^(m_z - M) (0 for an empty split), L = wave sum of l_z w_z;
+//   acc: thread (float4 column c4 = t % 32, split group zg = t / 32) sums w_z acc_z over z = zg, zg + 8, ... in
+//   order, the 8 groups are added in order through LDS; out = acc / L (0 when L = 0) and its activation blocks.
+// The loads of both phases for the first 64 splits of up to 4 heads are issued together (one memory round trip for
+// a context of up to 64 splits: 4096 keys).
+template <int G>
+__device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns, int hk, float* __restrict__ out,
+                                         const AmvActOut& act, float* sbuf) {
+    constexpr int GB = G < 4 ? G : 4;  // heads per batch of acc loads
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int c4 = tid & 31, zg = tid >> 5;
+    float* sAcc = sbuf;                    // [G][8][FA_D]
+    float* sw = sbuf + G * 8 * FA_D;       // [G][FA_MAX_NSPLIT]
+    float* sL = sw + G * FA_MAX_NSPLIT;    // [G]
+    const float* ph0 = part + (size_t)hk * G * n_split * FA_PS;
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (ns == 0) {  // no keys: zero outputs (every index below may assume a split 0)
+        for (int c = tid; c < G * (FA_D / 4); c += 256) {
+            const float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            *reinterpret_cast<float4*>(out + (size_t)hk * G * FA_D + 4 * c) = zero4;
+            if (act.type) amv_act_store4(act, hk * G * (FA_D / 4) + c, v);
+        }
+        return;
+    }
+    // Loads past the last split read split ns - 1 and get weight 0 (unconditional loads of valid addresses: a
+    // conditional load would be turned into a select of addresses with a stack zero, i.e. slow flat loads).
+    float4 va[GB][8];  // acc rows of splits zg + 8 i of heads 0 .. GB - 1
+#pragma unroll
+    for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int z = min(zg + 8 * i, ns - 1);
+            va[g][i] = *reinterpret_cast<const float4*>(ph0 + ((size_t)g * n_split + z) * FA_PS + 4 + 4 * c4);
+        }
+    for (int g = wv; g < G; g += 4) {
+        const float* ph = ph0 + (size_t)g * n_split * FA_PS;
+        const int z0 = min(lane, ns - 1);
+        const float m0r = ph[(size_t)z0 * FA_PS], l0 = ph[(size_t)z0 * FA_PS + 1];
+        const float m0 = lane < ns ? m0r : -INFINITY;
+        float m = m0;
+        for (int z = lane + 64; z < ns; z += 64) m = fmaxf(m, ph[(size_t)z * FA_PS]);
+        const float M = amv_wave_max(m);
+        float l = 0.0f;
+        if (lane < ns) {
+            const float w = (m0 == -INFINITY) ? 0.0f : expf(m0 - M);
+            sw[g * FA_MAX_NSPLIT + lane] = w;
+            l = fmaf(l0, w, l);
+        }
+        for (int z = lane + 64; z < ns; z += 64) {
+            const float mz = ph[(size_t)z * FA_PS];
+            const float w = (mz == -INFINITY) ? 0.0f : expf(mz - M);
+            sw[g * FA_MAX_NSPLIT + z] = w;
+            l = fmaf(ph[(size_t)z * FA_PS + 1], w, l);
+        }
+        l = amv_wave_sum(l);
+        if (lane == 0) sL[g] = l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g0 = 0; g0 < G; g0 += GB) {
+#pragma unroll
+        for (int gb = 0; gb < GB; ++gb) {
+            const int g = g0 + gb;
+            const float* pa = ph0 + (size_t)g * n_split * FA_PS + 4 + 4 * c4;
+            if (g0 > 0) {  // the second batch of heads (G = 8)
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    va[gb][i] = *reinterpret_cast<const float4*>(pa + (size_t)min(zg + 8 * i, ns - 1) * FA_PS);
+            }
+            float4 a = zero4;
+            for (int z0 = zg; z0 < ns; z0 += 64) {
+                float4 v[8];
+                float w[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int z = z0 + 8 * i;
+                    v[i] = z0 == zg ? va[gb][i] : *reinterpret_cast<const float4*>(pa + (size_t)min(z, ns - 1) * FA_PS);
+                    w[i] = z < ns ? sw[g * FA_MAX_NSPLIT + z] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    a.x = fmaf(w[i], v[i].x, a.x);
+                    a.y = fmaf(w[i], v[i].y, a.y);
+                    a.z = fmaf(w[i], v[i].z, a.z);
+                    a.w = fmaf(w[i], v[i].w, a.w);
+                }
+            }
+            *reinterpret_cast<float4*>(sAcc + (g * 8 + zg) * FA_D + 4 * c4) = a;
+        }
+    }
+    __syncthreads();
+    // thread c < G * 32 owns float4 chunk c of the G heads' outputs (the chunks of a Q8_0 or, with G even, a Q8_K
+    // block sit in consecutive lanes of one wave)
+    for (int c = tid; c < G * (FA_D / 4); c += 256) {
+        const int g = c / (FA_D / 4), d = 4 * (c % (FA_D / 4));
+        const float L = sL[g];
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float t = 0.0f;
+#pragma unroll
+            for (int z = 0; z < 8; ++z) t += sAcc[(g * 8 + z) * FA_D + d + e];
+            v[e] = L == 0.0f ? 0.0f : t / L;
+        }
+        *reinterpret_cast<float4*>(out + (size_t)(hk * G + g) * FA_D + d) = make_float4(v[0], v[1], v[2], v[3]);
+        if (act.type) amv_act_store4(act, hk * G * (FA_D / 4) + c, v);
+    }
+}
 
 // One workgroup per (split of 4 * KPW keys, KV head); each of its 4 waves owns KPW consecutive keys and works alone:
 // a 16-lane group owns keys 4 u + grp (u < KPW / 4) and reads 16 B of every K and V row of them (all K and V loads of
 // the wave are issued before the first is used); the G scores of a key are reduced over its 16 lanes; the wave's
 // maximum, probabilities, l and P V stay in registers. The 4 wave partials are merged once through LDS.
-template <int G, int KPW>
+// The key count is read from n_kv_dev when given (capped at the launch's n_kv); splits past it do nothing. FUSED: the
+// last workgroup of each KV head to arrive merges the head's splits (fa_merge).
+template <int G, int KPW, bool FUSED>
 __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, const uint16_t* __restrict__ k,
                                                  const uint16_t* __restrict__ v, const uint16_t* __restrict__ mask,
-                                                 float* __restrict__ part, int n_kv, int64_t k_row, int64_t k_head,
-                                                 int64_t v_row, int64_t v_head, int n_split, float scale) {
+                                                 float* part, int n_kv_max, const int* __restrict__ n_kv_dev,
+                                                 int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
+                                                 int n_split, float scale, unsigned int* counters,
+                                                 float* __restrict__ out, const AmvActOut act) {
     constexpr int U = KPW / 4;
-    __shared__ float sAcc[4][4][G][FA_D];  // [wave][lane group][head][dim]: partial P V of 4 keys per step
+    constexpr int SBUF = 4 * 4 * G * FA_D > G * (8 * FA_D + FA_MAX_NSPLIT + 1) ? 4 * 4 * G * FA_D
+                                                                              : G * (8 * FA_D + FA_MAX_NSPLIT + 1);
+    __shared__ __align__(16) float sbuf[SBUF];  // [wave][lane group][head][dim] partial P V; then the merge
     __shared__ float sM[4][G], sL[4][G];
     const int split = blockIdx.x, hk = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int grp = lane >> 4, d8 = 8 * (lane & 15);
-    const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
-    const uint16_t* kh = k + (size_t)hk * k_head;
-    const uint16_t* vh = v + (size_t)hk * v_head;
+    int n_kv = n_kv_max;
+    if (n_kv_dev) n_kv = max(0, min(*n_kv_dev, n_kv_max));
+    const int ns = (n_kv + 4 * KPW - 1) / (4 * KPW);  // splits holding keys
 
-    uint4 kr[U], vr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int i = min(kw0 + 4 * u + grp, n_kv - 1);
-        kr[u] = *reinterpret_cast<const uint4*>(kh + (size_t)i * k_row + d8);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int i = min(kw0 + 4 * u + grp, n_kv - 1);
-        vr[u] = *reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + d8);
-    }
-    // q of the G heads, 8 dims per lane, rounded to f16 as ggml does
-    float qv[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float4* qp = reinterpret_cast<const float4*>(q + (size_t)(hk * G + g) * FA_D + d8);
-        const float4 a = qp[0], b = qp[1];
-        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qv[g][e] = amv_round_f16(t[e]);
-    }
-    float s[U][G];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-        float kf[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            kf[2 * e] = amv_h2f(kw[e] & 0xFFFFu);
-            kf[2 * e + 1] = amv_h2f(kw[e] >> 16);
-        }
-        const int i = kw0 + 4 * u + grp;
-        const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float d = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
-            d = amv_row16_sum(d);
-            s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
-        }
-    }
-    float m[G], l[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float mm = s[0][g];
-#pragma unroll
-        for (int u = 1; u < U; ++u) mm = fmaxf(mm, s[u][g]);
-        mm = fmaxf(mm, __shfl_xor(mm, 16, AMV_WAVE));
-        mm = fmaxf(mm, __shfl_xor(mm, 32, AMV_WAVE));
-        m[g] = mm;
-        float ll = 0.0f;
+    if (split < ns) {
+        const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
+        const uint16_t* kh = k + (size_t)hk * k_head;
+        const uint16_t* vh = v + (size_t)hk * v_head;
+        uint4 kr[U], vr[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const float p = (mm == -INFINITY) ? 0.0f : expf(s[u][g] - mm);
-            s[u][g] = p;
-            ll += p;
+            const int i = min(kw0 + 4 * u + grp, n_kv - 1);
+            kr[u] = *reinterpret_cast<const uint4*>(kh + (size_t)i * k_row + d8);
         }
-        ll += __shfl_xor(ll, 16, AMV_WAVE);
-        ll += __shfl_xor(ll, 32, AMV_WAVE);
-        l[g] = ll;  // the 16 lanes of a group each counted their group's keys once: same total in every lane
-    }
-    float acc[G][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-        float vf[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
-            vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+        for (int u = 0; u < U; ++u) {
+            const int i = min(kw0 + 4 * u + grp, n_kv - 1);
+            vr[u] = *reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + d8);
         }
+        // q of the G heads, 8 dims per lane, rounded to f16 as ggml does
+        float qv[G][8];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float4* qp = reinterpret_cast<const float4*>(q + (size_t)(hk * G + g) * FA_D + d8);
+            const float4 a = qp[0], b = qp[1];
+            const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[g][e] = amv_round_f16(t[e]);
+        }
+        float s[U][G];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+            float kf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kf[2 * e] = amv_h2f(kw[e] & 0xFFFFu);
+                kf[2 * e + 1] = amv_h2f(kw[e] >> 16);
+            }
+            const int i = kw0 + 4 * u + grp;
+            const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
+                d = amv_row16_sum(d);
+                s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
+            }
+        }
+        float m[G], l[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float mm = s[0][g];
+#pragma unroll
+            for (int u = 1; u < U; ++u) mm = fmaxf(mm, s[u][g]);
+            mm = fmaxf(mm, __shfl_xor(mm, 16, AMV_WAVE));
+            mm = fmaxf(mm, __shfl_xor(mm, 32, AMV_WAVE));
+            m[g] = mm;
+            float ll = 0.0f;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float p = (mm == -INFINITY) ? 0.0f : expf(s[u][g] - mm);
+                s[u][g] = p;
+                ll += p;
+            }
+            ll += __shfl_xor(ll, 16, AMV_WAVE);
+            ll += __shfl_xor(ll, 32, AMV_WAVE);
+            l[g] = ll;  // the 16 lanes of a group each counted their group's keys once: same total in every lane
+        }
+        float acc[G][8];
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(s[u][g], vf[e], acc[g][e]);
-    }
-    // the 4 lane groups of a wave share the wave's maximum, so their accumulators add; the sum is taken in the merge
+            for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float4* dst = reinterpret_cast<float4*>(&sAcc[wv][grp][g][d8]);
-        dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-        dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-    }
-    if (lane == 0) {
+        for (int u = 0; u < U; ++u) {
+            const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+            float vf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
+                vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(s[u][g], vf[e], acc[g][e]);
+        }
+        // the 4 lane groups of a wave share the wave's maximum, so their accumulators add; the sum is taken below
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            sM[wv][g] = m[g];
-            sL[wv][g] = l[g];
+            float4* dst = reinterpret_cast<float4*>(sbuf + ((wv * 4 + grp) * G + g) * FA_D + d8);
+            dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+            dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                sM[wv][g] = m[g];
+                sL[wv][g] = l[g];
+            }
+        }
+        __syncthreads();
+        // merge the 4 wave partials of this workgroup
+        for (int e = tid; e < G * FA_D; e += 256) {
+            const int g = e / FA_D, d = e % FA_D;
+            const float M = fmaxf(fmaxf(sM[0][g], sM[1][g]), fmaxf(sM[2][g], sM[3][g]));
+            float a = 0.0f, L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = (sM[w][g] == -INFINITY) ? 0.0f : expf(sM[w][g] - M);
+                const float* sa = sbuf + ((w * 4) * G + g) * FA_D + d;
+                const float aw = (sa[0] + sa[G * FA_D]) + (sa[2 * G * FA_D] + sa[3 * G * FA_D]);
+                a = fmaf(aw, f, a);
+                L = fmaf(sL[w][g], f, L);
+            }
+            float* pp = part + ((size_t)(hk * G + g) * n_split + split) * FA_PS;
+            if constexpr (FUSED) {  // handed over to the merging workgroup within the launch
+                amv_store_coh(pp + 4 + d, a);
+                if (d == 0) {
+                    amv_store_coh(pp, M);
+                    amv_store_coh(pp + 1, L);
+                }
+            } else {
+                pp[4 + d] = a;
+                if (d == 0) {
+                    pp[0] = M;
+                    pp[1] = L;
+                }
+            }
         }
     }
-    __syncthreads();
-    // merge the 4 wave partials of this workgroup
-    for (int e = tid; e < G * FA_D; e += 256) {
-        const int g = e / FA_D, d = e % FA_D;
-        const float M = fmaxf(fmaxf(sM[0][g], sM[1][g]), fmaxf(sM[2][g], sM[3][g]));
-        float a = 0.0f, L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float f = (sM[w][g] == -INFINITY) ? 0.0f : expf(sM[w][g] - M);
-            const float aw = (sAcc[w][0][g][d] + sAcc[w][1][g][d]) + (sAcc[w][2][g][d] + sAcc[w][3][g][d]);
-            a = fmaf(aw, f, a);
-            L = fmaf(sL[w][g], f, L);
-        }
-        float* pp = part + ((size_t)(hk * G + g) * n_split + split) * (FA_D + 2);
-        pp[2 + d] = a;
-        if (d == 0) {
-            pp[0] = M;
-            pp[1] = L;
-        }
+    if constexpr (FUSED) {
+        if (!amv_arrive_last(counters + AMV_CNT_STRIDE * hk, gridDim.x)) return;
+        amv_acquire();
+        fa_merge<G>(part, n_split, ns, hk, out, act, sbuf);
     }
 }
 
-// Merge of the splits: workgroup (head h, 32-dim chunk c); thread (dim dl, split group zg of 8). With aq != NULL the
-// chunk (one 32-element block of the n_head x 128 output vector) is also quantized to Q8_0 for the next MUL_MAT.
-#define FA_MAX_NSPLIT 1024
+// The merge as its own launch: one workgroup per GH heads (GH = 1, or 2 for Q8_K output blocks of 256), the key
+// count from n_kv_dev when given, as in k_fa_split.
+template <int GH>
 __global__ __launch_bounds__(256) void k_fa_combine(const float* __restrict__ part, float* __restrict__ out,
-                                                   int n_split, int8_t* __restrict__ aq, int2* __restrict__ ameta,
-                                                   int rule) {
-    __shared__ float sw[FA_MAX_NSPLIT];
-    __shared__ float sRedM[4], sRedL[4];
-    __shared__ float sAcc[8][32];
-    const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const float* ph = part + (size_t)h * n_split * (FA_D + 2);
-    float m = -INFINITY;
-    for (int z = tid; z < n_split; z += 256) m = fmaxf(m, ph[(size_t)z * (FA_D + 2)]);
-    m = amv_wave_max(m);
-    if (lane == 0) sRedM[wv] = m;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(sRedM[0], sRedM[1]), fmaxf(sRedM[2], sRedM[3]));
-    float l = 0.0f;
-    for (int z = tid; z < n_split; z += 256) {
-        const float mz = ph[(size_t)z * (FA_D + 2)];
-        const float wz = (mz == -INFINITY) ? 0.0f : expf(mz - M);
-        sw[z] = wz;
-        l = fmaf(ph[(size_t)z * (FA_D + 2) + 1], wz, l);
-    }
-    l = amv_wave_sum(l);
-    if (lane == 0) sRedL[wv] = l;
-    __syncthreads();
-    const float L = (sRedL[0] + sRedL[1]) + (sRedL[2] + sRedL[3]);
-    const int dl = tid & 31, zg = tid >> 5;
-    const float* pa = ph + 2 + 32 * c + dl;
-    float a0 = 0.0f, a1 = 0.0f;
-    int z = zg;
-    for (; z + 8 < n_split; z += 16) {
-        a0 = fmaf(sw[z], pa[(size_t)z * (FA_D + 2)], a0);
-        a1 = fmaf(sw[z + 8], pa[(size_t)(z + 8) * (FA_D + 2)], a1);
-    }
-    if (z < n_split) a0 = fmaf(sw[z], pa[(size_t)z * (FA_D + 2)], a0);
-    sAcc[zg][dl] = a0 + a1;
-    __syncthreads();
-    if (tid < 32) {
-        float o = 0.0f;
-#pragma unroll
-        for (int g = 0; g < 8; ++g) o += sAcc[g][tid];
-        o = L == 0.0f ? 0.0f : o / L;
-        const size_t idx = (size_t)h * FA_D + 32 * c + tid;
-        out[idx] = o;
-        if (aq) amv_q8_0_lanes32(o, rule, tid, aq + (size_t)h * FA_D + 32 * c, ameta + (size_t)h * 4 + c);
-    }
+                                                   int n_split, int n_kv_max, const int* __restrict__ n_kv_dev,
+                                                   int split_len, const AmvActOut act) {
+    __shared__ __align__(16) float sbuf[GH * (8 * FA_D + FA_MAX_NSPLIT + 1)];
+    int ns = n_split;
+    if (n_kv_dev) ns = (max(0, min(*n_kv_dev, n_kv_max)) + split_len - 1) / split_len;
+    fa_merge<GH>(part, n_split, ns, blockIdx.x, out, act, sbuf);
 }
 
 // keys per wave: 16, or 32 when 16 would leave more than 4 workgroups per CU (long contexts)
@@ -207,43 +311,41 @@ extern "C" int64_t amv_flash_attn_workspace_bytes(int64_t n_head, int64_t n_head
     if (n_head <= 0 || n_head_kv <= 0 || n_kv <= 0 || D != FA_D) return -1;
     const int64_t sl = 4 * fa_kpw(n_kv, n_head_kv);
     const int64_t n_split = (n_kv + sl - 1) / sl;
-    return n_head * n_split * (D + 2) * 4;
+    return n_head * n_split * FA_PS * 4;
 }
 
-extern "C" int amv_flash_attn_decode(const float* q, const void* k, const void* v, const void* mask, float* out,
-                                     int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row,
-                                     int64_t k_head, int64_t v_row, int64_t v_head, float scale, void* workspace,
-                                     int64_t workspace_bytes, void* act, int rule, void* stream) {
-    AMV_REQUIRE(q && k && v && out && workspace, "amv_flash_attn_decode: null pointer");
-    AMV_REQUIRE(!act || ((uintptr_t)act & 15) == 0, "amv_flash_attn_decode: act must be 16-byte aligned");
-    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_flash_attn_decode: bad rule");
-    AMV_REQUIRE(D == FA_D, "amv_flash_attn_decode: head size %lld not supported (128 is)", (long long)D);
-    AMV_REQUIRE(n_head > 0 && n_head_kv > 0 && n_head % n_head_kv == 0, "amv_flash_attn_decode: bad head counts");
+static int fa_check(const char* fn, const float* q, const void* k, const void* v, const float* out, const void* ws,
+                    const void* act, int rule, int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D,
+                    int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int64_t workspace_bytes) {
+    AMV_REQUIRE(q && k && v && out && ws, "%s: null pointer", fn);
+    AMV_REQUIRE(!act || ((uintptr_t)act & 15) == 0, "%s: act must be 16-byte aligned", fn);
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "%s: bad rule", fn);
+    AMV_REQUIRE(D == FA_D, "%s: head size %lld not supported (128 is)", fn, (long long)D);
+    AMV_REQUIRE(n_head > 0 && n_head_kv > 0 && n_head % n_head_kv == 0, "%s: bad head counts", fn);
     const int64_t G = n_head / n_head_kv;
-    AMV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "amv_flash_attn_decode: GQA group %lld not supported", (long long)G);
-    AMV_REQUIRE(n_kv > 0 && n_kv <= 128LL * FA_MAX_NSPLIT, "amv_flash_attn_decode: n_kv %lld out of range",
-                (long long)n_kv);
-    AMV_REQUIRE(n_head_kv <= 65535, "amv_flash_attn_decode: too many KV heads");
+    AMV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "%s: GQA group %lld not supported", fn, (long long)G);
+    AMV_REQUIRE(n_kv > 0 && n_kv <= 128LL * FA_MAX_NSPLIT, "%s: n_kv %lld out of range", fn, (long long)n_kv);
+    AMV_REQUIRE(n_head_kv <= 65535, "%s: too many KV heads", fn);
     AMV_REQUIRE(k_row >= D && v_row >= D && k_row % 8 == 0 && v_row % 8 == 0 && k_head % 8 == 0 && v_head % 8 == 0 &&
                     k_head >= 0 && v_head >= 0,
-                "amv_flash_attn_decode: K/V strides must be >= D and multiples of 8 elements");
+                "%s: K/V strides must be >= D and multiples of 8 elements", fn);
     AMV_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 &&
-                    ((uintptr_t)workspace & 15) == 0,
-                "amv_flash_attn_decode: buffers must be 16-byte aligned");
+                    ((uintptr_t)ws & 15) == 0,
+                "%s: buffers must be 16-byte aligned", fn);
     const int64_t need = amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv, D);
-    AMV_REQUIRE(workspace_bytes >= need, "amv_flash_attn_decode: workspace %lld < %lld bytes", (long long)workspace_bytes,
+    AMV_REQUIRE(workspace_bytes >= need, "%s: workspace %lld < %lld bytes", fn, (long long)workspace_bytes,
                 (long long)need);
-    const int kpw = fa_kpw(n_kv, n_head_kv);
-    const int n_split = (int)((n_kv + 4 * kpw - 1) / (4 * kpw));
-    hipStream_t st = amv_stream(stream);
-    const dim3 grid(n_split, (unsigned)n_head_kv);
-    float* part = (float*)workspace;
-    const uint16_t* kk = (const uint16_t*)k;
-    const uint16_t* vv = (const uint16_t*)v;
-    const uint16_t* mm = (const uint16_t*)mask;
+    return AMV_OK;
+}
+
+template <bool FUSED>
+static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const float* q, const uint16_t* kk,
+                            const uint16_t* vv, const uint16_t* mm, float* part, int n_kv, const int* n_kv_dev,
+                            int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int n_split, float scale,
+                            unsigned int* counters, float* out, const AmvActOut& act) {
 #define FA_LAUNCH(GG, KK)                                                                                              \
-    hipLaunchKernelGGL((k_fa_split<GG, KK>), grid, dim3(256), 0, st, q, kk, vv, mm, part, (int)n_kv, k_row, k_head,   \
-                       v_row, v_head, n_split, scale)
+    hipLaunchKernelGGL((k_fa_split<GG, KK, FUSED>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev,      \
+                       k_row, k_head, v_row, v_head, n_split, scale, counters, out, act)
 #define FA_G(GG)                     \
     if (kpw == 16) FA_LAUNCH(GG, 16); \
     else FA_LAUNCH(GG, 32)
@@ -255,9 +357,56 @@ extern "C" int amv_flash_attn_decode(const float* q, const void* k, const void* 
     }
 #undef FA_G
 #undef FA_LAUNCH
-    int8_t* aq = act ? (int8_t*)act : nullptr;
-    int2* ameta = act ? (int2*)((uint8_t*)act + n_head * D) : nullptr;
-    hipLaunchKernelGGL(k_fa_combine, dim3((unsigned)n_head, FA_D / 32), dim3(256), 0, st, part, out, n_split, aq,
-                       ameta, rule);
-    return amv_check_launch("amv_flash_attn_decode");
+}
+
+// split + merge; counters == NULL: the merge as a second launch, else in the split launch's last workgroups
+static int fa_run(const char* fn, const float* q, const void* k, const void* v, const void* mask, float* out,
+                  int64_t n_head, int64_t n_head_kv, int64_t n_kv_max, const int32_t* n_kv_dev, int64_t D,
+                  int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, float scale, void* workspace,
+                  int64_t workspace_bytes, unsigned int* counters, void* act, int act_type, int rule, void* stream) {
+    int rc = fa_check(fn, q, k, v, out, workspace, act, rule, n_head, n_head_kv, n_kv_max, D, k_row, k_head, v_row,
+                      v_head, workspace_bytes);
+    if (rc) return rc;
+    const int G = (int)(n_head / n_head_kv);
+    AMV_REQUIRE(!act || act_type == AMV_T_Q8_0 || (act_type == AMV_T_Q8_K && G % 2 == 0),
+                "%s: act_type %d (Q8_0, or Q8_K with an even GQA group)", fn, act_type);
+    const int kpw = fa_kpw(n_kv_max, n_head_kv);
+    const int n_split = (int)((n_kv_max + 4 * kpw - 1) / (4 * kpw));
+    hipStream_t st = amv_stream(stream);
+    float* part = (float*)workspace;
+    const AmvActOut ao = amv_act_out(act, n_head * D, act ? act_type : 0, rule);
+    const dim3 grid(n_split, (unsigned)n_head_kv);
+    if (counters) {
+        fa_launch_split<true>(G, kpw, grid, st, q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)mask,
+                              part, (int)n_kv_max, n_kv_dev, k_row, k_head, v_row, v_head, n_split, scale, counters,
+                              out, ao);
+    } else {
+        fa_launch_split<false>(G, kpw, grid, st, q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)mask,
+                               part, (int)n_kv_max, n_kv_dev, k_row, k_head, v_row, v_head, n_split, scale, nullptr,
+                               nullptr, AmvActOut{});
+        if (ao.type == AMV_T_Q8_K)
+            hipLaunchKernelGGL(k_fa_combine<2>, dim3((unsigned)(n_head / 2)), dim3(256), 0, st, part, out, n_split,
+                               (int)n_kv_max, n_kv_dev, 4 * kpw, ao);
+        else
+            hipLaunchKernelGGL(k_fa_combine<1>, dim3((unsigned)n_head), dim3(256), 0, st, part, out, n_split,
+                               (int)n_kv_max, n_kv_dev, 4 * kpw, ao);
+    }
+    return amv_check_launch(fn);
+}
+
+extern "C" int amv_flash_attn_decode(const float* q, const void* k, const void* v, const void* mask, float* out,
+                                     int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row,
+                                     int64_t k_head, int64_t v_row, int64_t v_head, float scale, void* workspace,
+                                     int64_t workspace_bytes, void* act, int rule, void* stream) {
+    return fa_run("amv_flash_attn_decode", q, k, v, mask, out, n_head, n_head_kv, n_kv, nullptr, D, k_row, k_head,
+                  v_row, v_head, scale, workspace, workspace_bytes, nullptr, act, AMV_T_Q8_0, rule, stream);
+}
+
+extern "C" int amv_flash_attn_decode_ex(const float* q, const void* k, const void* v, const void* mask, float* out,
+                                        int64_t n_head, int64_t n_head_kv, int64_t n_kv_max, const int32_t* n_kv_dev,
+                                        int64_t D, int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
+                                        float scale, void* workspace, int64_t workspace_bytes, unsigned int* counters,
+                                        void* act, int act_type, int rule, void* stream) {
+    return fa_run("amv_flash_attn_decode_ex", q, k, v, mask, out, n_head, n_head_kv, n_kv_max, n_kv_dev, D, k_row,
+                  k_head, v_row, v_head, scale, workspace, workspace_bytes, counters, act, act_type, rule, stream);
 }

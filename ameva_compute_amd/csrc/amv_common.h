@@ -163,3 +163,273 @@ __device__ __forceinline__ void amv_q8_0_lanes32(float v, int rule, int j, int8_
     qs[j] = (int8_t)q;
     if (j == 0) *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
 }
+// Q8_0 quantization of one 32-element block spread over 8 consecutive lanes (4 elements each, lane j of the 8 holds
+// elements 4j .. 4j + 3): the rules of amv_quantize_act. All 8 lanes must call it; stores 4 int8 per lane.
+__device__ __forceinline__ void q8_block_lanes8(const float (&v)[4], int rule, int j, int8_t* __restrict__ qs,
+                                                int2* __restrict__ meta) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, AMV_WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, AMV_WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, AMV_WAVE));
+    const float d = amax / 127.0f;
+    float id;
+    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t packed = 0;
+    int s = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float t = v[e] * id;
+        float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+        qf = fminf(127.0f, fmaxf(-127.0f, qf));
+        const int q = (int)qf;
+        s += q;
+        packed |= (uint32_t)(q & 0xFF) << (8 * e);
+    }
+    s += __shfl_xor(s, 1, AMV_WAVE);
+    s += __shfl_xor(s, 2, AMV_WAVE);
+    s += __shfl_xor(s, 4, AMV_WAVE);
+    reinterpret_cast<uint32_t*>(qs)[j] = packed;
+    if (j == 0) *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q8_K quantization (ggml quantize_row_q8_K) of one 256-element block held by a whole wave, 4 consecutive elements
+// per lane: max = the element of largest magnitude (the first on ties), iscale = -127/max, q = min(127,
+// round-half-even(iscale * x)), d = 1/iscale; s16 = sum of q over the lane's group of 16 (lanes 4 i .. 4 i + 3), in
+// every lane of the group. An all-zero block gives q = 0, d = 0.
+struct AmvQ8K {
+    int q[4];
+    int s16;
+    float d;
+};
+__device__ __forceinline__ AmvQ8K amv_q8_K_lanes64(const float (&v)[4], int lane) {
+    AmvQ8K r;
+    float am = 0.0f;
+    int ai = 0x7FFFFFFF;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float a = fabsf(v[e]);
+        if (a > am) { am = a; ai = 4 * lane + e; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float om = __shfl_xor(am, o, AMV_WAVE);
+        const int oi = __shfl_xor(ai, o, AMV_WAVE);
+        if (om > am || (om == am && oi < ai)) { am = om; ai = oi; }
+    }
+    if (am == 0.0f) {
+        r.q[0] = r.q[1] = r.q[2] = r.q[3] = 0;
+        r.s16 = 0;
+        r.d = 0.0f;
+        return r;
+    }
+    const float mx = __shfl(v[ai & 3], ai >> 2, AMV_WAVE);
+    const float iscale = -127.0f / mx;
+    int s = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int t = (int)rintf(iscale * v[e]);
+        r.q[e] = t < 127 ? t : 127;
+        s += r.q[e];
+    }
+    s += __shfl_xor(s, 1, AMV_WAVE);
+    s += __shfl_xor(s, 2, AMV_WAVE);
+    r.s16 = s;
+    r.d = 1.0f / iscale;
+    return r;
+}
+__device__ __forceinline__ int amv_pack4(const int (&q)[4]) {
+    return (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | ((q[3] & 0xFF) << 24);
+}
+
+// Activation output of a fused quantization: one row in the amv_quantize_act layout of its type. Q8_0: qs [n], then
+// {f32 d, i32 sum q} per 32 at meta; Q8_K: qs [n], f32 d per 256 at meta, i32 sums per 16 at sums16.
+struct AmvActOut {
+    int8_t* qs;
+    void* meta;
+    int32_t* sums16;
+    int type;  // AMV_T_Q8_0 or AMV_T_Q8_K; 0: no output
+    int rule;  // Q8_0 rounding rule
+};
+// host: the descriptor of an activation of m rows of n values at act (amv_quantize_act layout); type 0 = none
+static inline AmvActOut amv_act_out(void* act, int64_t n, int type, int rule, int64_t m = 1) {
+    AmvActOut o{nullptr, nullptr, nullptr, 0, rule};
+    if (!act || !type) return o;
+    o.qs = (int8_t*)act;
+    o.meta = (uint8_t*)act + m * n;
+    o.sums16 = type == AMV_T_Q8_K ? (int32_t*)((uint8_t*)act + m * n + m * (n / 256) * 4) : nullptr;
+    o.type = type;
+    return o;
+}
+// the descriptor of row r of an m-row activation (amv_quantize_act layout: all rows' qs, then all rows' metadata)
+__host__ __device__ inline AmvActOut amv_act_row(const AmvActOut& a, int64_t r, int64_t n) {
+    AmvActOut o = a;
+    if (!a.type) return o;
+    o.qs = a.qs + r * n;
+    if (a.type == AMV_T_Q8_0) {
+        o.meta = reinterpret_cast<int2*>(a.meta) + r * (n / 32);
+    } else {
+        o.meta = reinterpret_cast<float*>(a.meta) + r * (n / 256);
+        o.sums16 = a.sums16 + r * (n / 16);
+    }
+    return o;
+}
+// Quantizes the 4 consecutive values of float4 chunk c of the row. Q8_0: the 8 chunks of a 32-block must be in 8
+// consecutive lanes; Q8_K: the 64 chunks of a 256-block must be the 64 lanes of one wave, in order.
+__device__ __forceinline__ void amv_act_store4(const AmvActOut& o, int c, const float (&v)[4]) {
+    if (o.type == AMV_T_Q8_0) {
+        q8_block_lanes8(v, o.rule, c & 7, o.qs + 32 * (c >> 3), reinterpret_cast<int2*>(o.meta) + (c >> 3));
+    } else if (o.type == AMV_T_Q8_K) {
+        const AmvQ8K r = amv_q8_K_lanes64(v, c & 63);
+        reinterpret_cast<int*>(o.qs)[c] = amv_pack4(r.q);
+        if ((c & 3) == 0) o.sums16[c >> 2] = r.s16;
+        if ((c & 63) == 0) reinterpret_cast<float*>(o.meta)[c >> 6] = r.d;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Data one workgroup hands to another inside a launch. The 8 XCDs of MI355X have private L2s; agent-scope fences
+// make ordinary stores visible by writing back and invalidating the whole L2 (tens of us when every wave does it),
+// so the handed-over values are instead stored and loaded with agent-scope relaxed atomics (sc1: coherent across
+// the XCDs without touching the rest of the cache), and amv_arrive_last orders them with a wait on the wave's own
+// memory counter.
+__device__ __forceinline__ void amv_store_coh(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float amv_load_coh(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 amv_load4_coh(const float* p) {
+    return make_float4(amv_load_coh(p), amv_load_coh(p + 1), amv_load_coh(p + 2), amv_load_coh(p + 3));
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// RMS_NORM of one row, shared by the norm kernel and the fused GEMV tail so that both produce the same bits. The
+// sum of squares is defined for 1024 virtual lanes: lane t sums the float4 chunks t, t + 1024, ... as f32 squares in
+// double, a 64-lane butterfly per virtual wave, then the 16 wave sums in order. A workgroup of NT threads (NT
+// divides 1024) plays V = 1024 / NT virtual lanes per thread (t = tid + NT v) and loads all V chunks of a round
+// before summing, so a row of up to 1024 chunks costs one memory round trip and its values stay in registers for
+// the second pass: y = x * scale, o = y * w, act = the quantized o (y without w). Any output may be NULL; the chunks
+// of a quantization block sit in consecutive lanes as amv_act_store4 needs (n % 32 == 0 with Q8_0, % 256 with
+// Q8_K).
+#define AMV_RMS_VLANES 1024
+__device__ __forceinline__ float amv_rms_scale(double tot, int n, float eps) {
+    const float mean = (float)(tot / (double)n);
+    return 1.0f / sqrtf(mean + eps);
+}
+__device__ __forceinline__ void amv_rms_chunk(int c, float4 v, float scale, const float* __restrict__ w,
+                                              float* __restrict__ y, float* __restrict__ o, const AmvActOut& act) {
+    const float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
+    if (y) reinterpret_cast<float4*>(y)[c] = yv;
+    float4 qv = yv;
+    if (w) {
+        const float4 wv = reinterpret_cast<const float4*>(w)[c];
+        qv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
+        if (o) reinterpret_cast<float4*>(o)[c] = qv;
+    }
+    if (act.type) {
+        const float vals[4] = {qv.x, qv.y, qv.z, qv.w};
+        amv_act_store4(act, c, vals);
+    }
+}
+template <int NT>
+__device__ __forceinline__ void amv_rms_row(const float4* __restrict__ x4, int n4, float eps,
+                                            const float* __restrict__ w, float* __restrict__ y,
+                                            float* __restrict__ o, const AmvActOut& act, double* sred) {
+    static_assert(AMV_RMS_VLANES % NT == 0 && NT % 64 == 0, "NT must divide 1024 in whole waves");
+    constexpr int V = AMV_RMS_VLANES / NT;
+    const int tid = threadIdx.x;
+    float4 xr[V];
+    double s[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) s[v] = 0.0;
+    for (int k0 = 0; k0 < n4; k0 += AMV_RMS_VLANES) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int c = k0 + tid + NT * v;
+            xr[v] = c < n4 ? x4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {  // absent chunks add exact zeros
+            s[v] += (double)(xr[v].x * xr[v].x);
+            s[v] += (double)(xr[v].y * xr[v].y);
+            s[v] += (double)(xr[v].z * xr[v].z);
+            s[v] += (double)(xr[v].w * xr[v].w);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        double t = s[v];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, AMV_WAVE);
+        if ((tid & 63) == 0) sred[(tid + NT * v) >> 6] = t;
+    }
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < AMV_RMS_VLANES / 64; ++i) tot += sred[i];
+    const float scale = amv_rms_scale(tot, 4 * n4, eps);
+    if (n4 <= AMV_RMS_VLANES) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int c = tid + NT * v;
+            if (c < n4) amv_rms_chunk(c, xr[v], scale, w, y, o, act);
+        }
+    } else {
+        for (int c = tid; c < n4; c += NT) amv_rms_chunk(c, x4[c], scale, w, y, o, act);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// ROPE of one pair (x0, x1) with pair index j at position p: the angle freq_scale * (p * theta_scale^j) built by
+// repeated f32 multiplication (ggml's rope f32, reference ameva_rope.comp:64-92). Shared by every ROPE kernel.
+__device__ __forceinline__ void amv_rope_cs(float p, int j, float theta_scale, float freq_scale, float attn_factor,
+                                            float& c, float& s) {
+    float theta = p;
+    for (int k = 0; k < j; ++k) theta *= theta_scale;
+    const float ang = freq_scale * theta;
+    c = cosf(ang) * attn_factor;
+    s = sinf(ang) * attn_factor;
+}
+__device__ __forceinline__ void amv_rope_apply(float c, float s, float x0, float x1, float& y0, float& y1) {
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+__device__ __forceinline__ void amv_rope_pair(float p, int j, float theta_scale, float freq_scale, float attn_factor,
+                                              float x0, float x1, float& y0, float& y1) {
+    float c, s;
+    amv_rope_cs(p, j, theta_scale, freq_scale, attn_factor, c, s);
+    amv_rope_apply(c, s, x0, x1, y0, y1);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Last-arrival test of a launch-wide (or group-wide) tail: each of `target` workgroups calls it once, with every
+// thread of the workgroup, after storing its handed-over values with amv_store_coh; it returns true in exactly one
+// of them, the last to arrive, which may then read all of them with amv_load_coh (or after amv_acquire). Each wave first waits until its
+// own stores have completed (s_waitcnt vmcnt(0)), so they are performed before the workgroup's arrival; the counter
+// is an atomicInc that wraps at target, so it is back to zero for the next launch without a reset.
+__device__ __forceinline__ bool amv_arrive_last(unsigned int* counter, unsigned int target) {
+    __shared__ unsigned int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicInc(counter, target - 1u) == target - 1u ? 1u : 0u;
+    __syncthreads();
+    return s_last != 0u;
+}
+// Arrivals on one counter serialize at the memory side (~12 ns each on MI355X: 512 workgroups add ~6 us), so each
+// counter sits in its own 128-byte line (AMV_CNT_STRIDE words) and a launch-wide tail meets in two levels: groups of
+// AMV_ARRIVE_GROUP workgroups on counters[(1 + group) * stride], the last of each group on counters[0]. Returns true
+// in the last workgroup of the launch.
+#define AMV_CNT_STRIDE 32
+#define AMV_ARRIVE_GROUP 16
+__device__ __forceinline__ bool amv_arrive_last_tree(unsigned int* counters) {
+    const unsigned int n = gridDim.x, gi = blockIdx.x / AMV_ARRIVE_GROUP;
+    const unsigned int n_groups = (n + AMV_ARRIVE_GROUP - 1) / AMV_ARRIVE_GROUP;
+    const unsigned int gsize = min((unsigned int)AMV_ARRIVE_GROUP, n - gi * AMV_ARRIVE_GROUP);
+    if (!amv_arrive_last(counters + AMV_CNT_STRIDE * (1 + gi), gsize)) return false;
+    return amv_arrive_last(counters, n_groups);
+}
+// Instead of amv_load_coh for a larger read: one agent-scope acquire (invalidates this XCD's L2 once), after which
+// ordinary (float4) loads see the handed-over values. For a workgroup that runs once per launch.
+__device__ __forceinline__ void amv_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }

@@ -22,23 +22,76 @@
 //   EP 4 (MI355X, one weight of stacked gate rows 0..F-1 and up rows F..2F-1): wave w computes rows w and F + w and
 //        eout[w] = v_w / (1 + exp(-v_w)) * v_{F+w}; the gate and up MUL_MATs read the same activations, so one
 //        launch streams both weights.
+// Launches that do more than their epilogue (MI355X decode fusions; each replaces one or two launches of small
+// kernels, which cost ~4 us apiece at bs1 whatever their size):
+//   EP 5 ROPE_KV:     q/k/v rows stacked (n_q q rows, n_k k rows, then v rows, heads of head_dim rows); ROPE NORMAL
+//                     on q and k (pair j = rows 2j, 2j + 1 of a head: exactly the two rows of a wave), dst gets the
+//                     rotated q/k and the v values, and the k and v rows are also stored as f16 at cache row
+//                     kv_idx[0] (k_rope_kv's arithmetic and skip/count rule)
+//   EP 6 ADD_NORM:    EP 1, then the last workgroup to finish applies RMS_NORM (+MUL by norm_w, +Q8_0) to the whole
+//                     eout vector (k_rms_norm's arithmetic, same bits)
+//   EP 7 SWIGLU_Q8:   EP 4, then the last workgroup of each 32 outputs quantizes them to Q8_0 (amv_quantize_act's
+//                     rules)
+#define MMV_EP_ROPE_KV 5
+#define MMV_EP_ADD_NORM 6
+#define MMV_EP_SWIGLU_Q8 7
+#define MMV_STACKED(EP) ((EP) == AMV_EP_SWIGLU_STACKED || (EP) == MMV_EP_SWIGLU_Q8)
+#define MMV_TAIL(EP) ((EP) == MMV_EP_ADD_NORM || (EP) == MMV_EP_SWIGLU_Q8)
+
+struct MmvPost {
+    const int32_t* pos;  // ROPE_KV: position of the token
+    float theta_scale, freq_scale, attn_factor;
+    int n_q, n_k, head_dim;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    int64_t cache_row;      // elements per cache row
+    const int64_t* kv_idx;  // cache row of the token
+    int64_t cache_rows;
+    unsigned int* bad;       // count of skipped k/v head stores (rows outside [0, cache_rows))
+    unsigned int* counters;  // tails: zero before the first launch, left at zero by every launch
+    const float* norm_w;     // ADD_NORM: MUL operand (NULL: none)
+    float eps;
+    float* norm_y;  // ADD_NORM outputs, each may be NULL: x * scale, then * norm_w
+    float* norm_o;
+    AmvActOut act;  // quantized output of the tail (Q8_0 or Q8_K activation row)
+};
+
 template <int EP>
 __device__ __forceinline__ int mmv_row(int wave, int r, int R, int n_rows) {
-    return EP == AMV_EP_SWIGLU_STACKED ? wave + r * (n_rows >> 1) : wave * R + r;
+    return MMV_STACKED(EP) ? wave + r * (n_rows >> 1) : wave * R + r;
 }
 template <int EP>
 __device__ __forceinline__ bool mmv_wave_live(int wave, int R, int n_rows) {
-    return EP == AMV_EP_SWIGLU_STACKED ? wave < (n_rows >> 1) : wave * R < n_rows;
+    return MMV_STACKED(EP) ? wave < (n_rows >> 1) : wave * R < n_rows;
 }
 __device__ __forceinline__ float mmv_silu(float x) { return x / (1.0f + expf(-x)); }
+
+// ROPE_KV: the token's cache row and the rotation of the wave's pair (a function of the position and the pair
+// index only), computed at the start of the kernel where they overlap the weight stream
+struct MmvRopeAt {
+    float c, s;
+    int64_t row;
+};
+template <int EP>
+__device__ __forceinline__ MmvRopeAt mmv_rope_at(const MmvPost& post, int wave) {
+    MmvRopeAt r{1.0f, 0.0f, 0};
+    if constexpr (EP == MMV_EP_ROPE_KV) {
+        r.row = post.kv_idx[0];
+        const int r0 = wave * 2;
+        if (r0 < post.n_q + post.n_k)
+            amv_rope_cs((float)post.pos[0], (r0 % post.head_dim) >> 1, post.theta_scale, post.freq_scale,
+                        post.attn_factor, r.c, r.s);
+    }
+    return r;
+}
 
 // End of a row group: wave sums of the R accumulators; with a split of K (S > 1 waves per row group) the S partial
 // sums meet in LDS and are added in the fixed order ks = 0 .. S-1 by the group's first wave; then the epilogue.
 template <int R, int EP, int S>
 __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int wi, int ks, bool live, int wave,
                                            int n_rows, float* __restrict__ dst, const float* __restrict__ epi,
-                                           float* __restrict__ eout) {
-    static_assert(EP != AMV_EP_SWIGLU_STACKED || R == 2, "the stacked SWIGLU pairs two rows per wave");
+                                           float* __restrict__ eout, const MmvPost& post, const MmvRopeAt& ra) {
+    static_assert((!MMV_STACKED(EP) && EP != MMV_EP_ROPE_KV) || R == 2, "stacked SWIGLU and ROPE pair two rows per wave");
     float t[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) t[r] = amv_wave_sum(acc[r]);
@@ -59,12 +112,35 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
         }
     }
     if (lane != 0) return;
-    if constexpr (EP == AMV_EP_SWIGLU_STACKED) {
+    if constexpr (EP == MMV_EP_ROPE_KV) {
+        const int r0 = wave * 2;
+        if (r0 >= n_rows) return;
+        const int nqk = post.n_q + post.n_k;
+        float y0 = t[0], y1 = t[1];
+        if (r0 < nqk) amv_rope_apply(ra.c, ra.s, t[0], t[1], y0, y1);
+        dst[r0] = y0;
+        dst[r0 + 1] = y1;
+        if (r0 >= post.n_q) {
+            const int64_t dr = ra.row;
+            const bool store = dr >= 0 && dr < post.cache_rows;
+            const int rr = r0 < nqk ? r0 - post.n_q : r0 - nqk;  // row within the k or v block
+            if (store) {
+                uint16_t* c = (r0 < nqk ? post.k_cache : post.v_cache) + dr * post.cache_row + rr;
+                c[0] = amv_f2h(y0);
+                c[1] = amv_f2h(y1);
+            } else if (rr % post.head_dim == 0 && post.bad) {
+                atomicAdd(post.bad, 1u);  // once per skipped head, as k_rope_kv counts
+            }
+        }
+        return;
+    }
+    if constexpr (MMV_STACKED(EP)) {
         if (dst) {
             dst[wave] = t[0];
             dst[wave + (n_rows >> 1)] = t[1];
         }
-        eout[wave] = mmv_silu(t[0]) * t[1];
+        if constexpr (EP == MMV_EP_SWIGLU_Q8) amv_store_coh(eout + wave, mmv_silu(t[0]) * t[1]);
+        else eout[wave] = mmv_silu(t[0]) * t[1];
         return;
     }
 #pragma unroll
@@ -73,8 +149,34 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
         if (row >= n_rows) continue;
         if (EP == AMV_EP_NONE || dst) dst[row] = t[r];
         if (EP == AMV_EP_ADD) eout[row] = t[r] + epi[row];
+        if (EP == MMV_EP_ADD_NORM) amv_store_coh(eout + row, t[r] + epi[row]);
         if (EP == AMV_EP_SILU_MUL) eout[row] = mmv_silu(t[r]) * epi[row];
         if (EP == AMV_EP_MUL_SILU) eout[row] = mmv_silu(epi[row]) * t[r];
+    }
+}
+
+// Tails of EP 6 and EP 7, run by every thread of the workgroup after the epilogue stores.
+template <int EP, int S>
+__device__ __forceinline__ void mmv_tail(const MmvPost& post, const float* eout, int n_rows) {
+    if constexpr (EP == MMV_EP_ADD_NORM) {
+        if (!amv_arrive_last_tree(post.counters)) return;
+        amv_acquire();
+        __shared__ double sred[AMV_RMS_VLANES / 64];
+        amv_rms_row<256>(reinterpret_cast<const float4*>(eout), n_rows / 4, post.eps, post.norm_w, post.norm_y,
+                         post.norm_o, post.act, sred);
+    } else {
+        // a workgroup's 4 / S outputs lie in one block of BS (the launcher checks that BS divides n_rows / 2); the
+        // first wave of the last workgroup quantizes it, 4 values per lane
+        constexpr int per_wg = 4 / S;
+        const int BS = post.act.type == AMV_T_Q8_K ? 256 : 32;
+        const int blk = (int)blockIdx.x * per_wg / BS;
+        if (!amv_arrive_last(post.counters + AMV_CNT_STRIDE * blk, BS / per_wg)) return;
+        const int lane = threadIdx.x;
+        if (lane < BS / 4) {
+            const float4 t = amv_load4_coh(eout + BS * blk + 4 * lane);
+            const float v[4] = {t.x, t.y, t.z, t.w};
+            amv_act_store4(post.act, BS / 4 * blk + lane, v);
+        }
     }
 }
 
@@ -86,12 +188,13 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
                                                  int n_rows, int nb, const int8_t* __restrict__ aq,
                                                  const int2* __restrict__ ads, float* __restrict__ dst,
                                                  int32_t* __restrict__ sums, const float* __restrict__ epi,
-                                                 float* __restrict__ eout) {
+                                                 float* __restrict__ eout, const MmvPost post) {
     static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
     const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
     const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
     const bool live = mmv_wave_live<EP>(wave, R, n_rows);
-    if (S == 1 && !live) return;  // uniform per wave
+    const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);  // ROPE_KV
+    if (S == 1 && !live && !MMV_TAIL(EP)) return;  // uniform per wave (tails need every wave)
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     const uint32_t* wd2 = reinterpret_cast<const uint32_t*>(wd);
     uint32_t rb[R], db[R];  // block index of (row, 0); scale index of (row, 0) minus the block offset factor
@@ -114,7 +217,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
 #pragma unroll
             for (int r = 0; r < R; ++r) w[u][r] = wq[rb[r] + j];
             if (BLOCK_SUMS) continue;
-            if constexpr (PAIRS && EP != AMV_EP_SWIGLU_STACKED && R % 2 == 0) {
+            if constexpr (PAIRS && !MMV_STACKED(EP) && R % 2 == 0) {
                 // the wave's rows 2p, 2p + 1 read both scales with one dword
 #pragma unroll
                 for (int r = 0; r < R; r += 2) {
@@ -159,7 +262,10 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
             }
         }
     }
-    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) {
+        mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ Q8_0 x Q8_0
@@ -168,12 +274,13 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
                                                  int n_rows, int nb, const int8_t* __restrict__ aq,
                                                  const int2* __restrict__ ads, float* __restrict__ dst,
                                                  int32_t* __restrict__ sums, const float* __restrict__ epi,
-                                                 float* __restrict__ eout) {
+                                                 float* __restrict__ eout, const MmvPost post) {
     static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
     const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
     const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
     const bool live = mmv_wave_live<EP>(wave, R, n_rows);
-    if (S == 1 && !live) return;  // uniform per wave
+    const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);  // ROPE_KV
+    if (S == 1 && !live && !MMV_TAIL(EP)) return;  // uniform per wave (tails need every wave)
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
 #pragma unroll
@@ -219,7 +326,10 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
             }
         }
     }
-    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) {
+        mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ K-quants
@@ -244,12 +354,13 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
                                                  int n_rows, int nsl, const int8_t* __restrict__ aq,
                                                  const float* __restrict__ ad, const int* __restrict__ abs16,
                                                  float* __restrict__ dst, int32_t* __restrict__ sums, const float* __restrict__ epi,
-                                                 float* __restrict__ eout) {
+                                                 float* __restrict__ eout, const MmvPost post) {
     static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
     const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
     const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
     const bool live = mmv_wave_live<EP>(wave, R, n_rows);
-    if (S == 1 && !live) return;  // uniform per wave
+    const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);  // ROPE_KV
+    if (S == 1 && !live && !MMV_TAIL(EP)) return;  // uniform per wave (tails need every wave)
     const int nsb = nsl >> 3;
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
@@ -295,7 +406,10 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
             }
         }
     }
-    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) {
+        mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+    }
 }
 
 template <int R, bool BLOCK_SUMS, int EP, int S>
@@ -304,12 +418,13 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
                                                  int n_rows, int nsl, const int8_t* __restrict__ aq,
                                                  const float* __restrict__ ad, const int* __restrict__ abs16,
                                                  float* __restrict__ dst, int32_t* __restrict__ sums, const float* __restrict__ epi,
-                                                 float* __restrict__ eout) {
+                                                 float* __restrict__ eout, const MmvPost post) {
     static_assert(!BLOCK_SUMS || S == 1, "block sums are written per block, without a split of K");
     const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, ks = wi % S;
     const int wave = blockIdx.x * (4 / S) + wi / S;  // row group; the S waves of a group split K
     const bool live = mmv_wave_live<EP>(wave, R, n_rows);
-    if (S == 1 && !live) return;  // uniform per wave
+    const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);  // ROPE_KV
+    if (S == 1 && !live && !MMV_TAIL(EP)) return;  // uniform per wave (tails need every wave)
     const int nsb = nsl >> 3;
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     float acc[R];
@@ -361,7 +476,10 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
             }
         }
     }
-    if constexpr (!BLOCK_SUMS) mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout);
+    if constexpr (!BLOCK_SUMS) {
+        mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
@@ -376,6 +494,7 @@ struct MmvArgs {
     int32_t* sums;
     const float* epi;      // epilogue operand
     float* eout;           // epilogue output
+    MmvPost post;          // EP 5..7
 };
 
 template <int R, int U, bool BS, int EP, int S>
@@ -386,18 +505,18 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 16);
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
-    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
-    const bool full = nb % (64 * U) == 0 && (EP == AMV_EP_SWIGLU_STACKED || a.n_rows % R == 0);
+    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const bool full = nb % (64 * U) == 0 && (MMV_STACKED(EP) || a.n_rows % R == 0);
     const dim3 grid((waves * S + 3) / 4);
     if (a.n_rows % 2 == 0 && full)
         hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, true, true>), grid, dim3(256), 0, st, wq, wd, a.n_rows, nb, aq,
-                           ads, a.dst, a.sums, a.epi, a.eout);
+                           ads, a.dst, a.sums, a.epi, a.eout, a.post);
     else if (a.n_rows % 2 == 0)
         hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, true, false>), grid, dim3(256), 0, st, wq, wd, a.n_rows, nb,
-                           aq, ads, a.dst, a.sums, a.epi, a.eout);
+                           aq, ads, a.dst, a.sums, a.epi, a.eout, a.post);
     else
         hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, false, false>), grid, dim3(256), 0, st, wq, wd, a.n_rows, nb,
-                           aq, ads, a.dst, a.sums, a.epi, a.eout);
+                           aq, ads, a.dst, a.sums, a.epi, a.eout, a.post);
 }
 
 template <int R, int U, bool BS, int EP, int S>
@@ -408,9 +527,9 @@ static void launch_q8_0(const MmvArgs& a, hipStream_t st) {
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 32);
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
-    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
     hipLaunchKernelGGL((k_mmv_q8_0<R, U, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
-                       a.dst, a.sums, a.epi, a.eout);
+                       a.dst, a.sums, a.epi, a.eout, a.post);
 }
 
 template <int R, bool BS, int EP, int S>
@@ -419,9 +538,9 @@ static void launch_q4_K(const MmvArgs& a, hipStream_t st) {
     const int64_t nblk = (int64_t)a.n_rows * nsb;
     const uint4* wq = reinterpret_cast<const uint4*>(a.w);
     const uint4* wh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
-    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
     hipLaunchKernelGGL((k_mmv_q4_K<R, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
-                       (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout);
+                       (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout, a.post);
 }
 
 template <int R, bool BS, int EP, int S>
@@ -432,9 +551,9 @@ static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
     const uint4* wqh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
     const uint4* wsc = reinterpret_cast<const uint4*>(a.w + nblk * 192);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 208);
-    const int waves = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
     hipLaunchKernelGGL((k_mmv_q6_K<R, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wl, wqh, wsc, wd, a.n_rows, nsl,
-                       a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout);
+                       a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout, a.post);
 }
 
 // Split of K over the S waves of a row group (S = 1, 2, 4) for launches of few row groups. Measured on MI355X
@@ -486,7 +605,7 @@ static void launch_q6_K_s(const MmvArgs& a, hipStream_t st, int S) {
 template <bool BS, int EP>
 static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
     const int nb = a.k / 32;
-    const int64_t groups2 = EP == AMV_EP_SWIGLU_STACKED ? a.n_rows / 2 : (a.n_rows + 1) / 2;  // R = 2 row groups
+    const int64_t groups2 = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + 1) / 2;  // R = 2 row groups
     const auto split = [&](int64_t groups, int64_t steps) { return BS ? 1 : mmv_split(groups, steps); };
     switch (a.wtype) {
     case AMV_T_Q4_0:
@@ -495,7 +614,7 @@ static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
         launch_q4_0_s<2, 1, BS, EP>(a, st, split(groups2, (nb + 63) / 64));
         return AMV_OK;
     case AMV_T_Q8_0:
-        if constexpr (EP != AMV_EP_SWIGLU_STACKED) {
+        if constexpr (!MMV_STACKED(EP) && EP != MMV_EP_ROPE_KV) {
             if (nb <= 64) {
                 launch_q8_0_s<4, 1, BS, EP>(a, st, 1);
                 return AMV_OK;
@@ -602,4 +721,99 @@ extern "C" int amv_mul_mat_block_sums(int wtype, const void* w, int64_t n_rows, 
         if (rc) return rc;
     }
     return amv_check_launch("amv_mul_mat_block_sums");
+}
+
+// ------------------------------------------------------------------------------------------------ fused decode GEMVs
+static int mmv_dispatch_fused(int ep, MmvArgs& a, const void* act, hipStream_t st) {
+    column_view(a, (const uint8_t*)act, 1, 0);
+    int rc;
+    switch (ep) {
+    case MMV_EP_ROPE_KV: rc = mmv_one_column<false, MMV_EP_ROPE_KV>(a, st); break;
+    case MMV_EP_ADD_NORM: rc = mmv_one_column<false, MMV_EP_ADD_NORM>(a, st); break;
+    default: rc = mmv_one_column<false, MMV_EP_SWIGLU_Q8>(a, st); break;
+    }
+    return rc;
+}
+
+extern "C" int amv_gemv_rope_kv(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* qkv,
+                                int64_t n_head, int64_t n_head_kv, int64_t D, const int32_t* pos, float freq_base,
+                                float freq_scale, float attn_factor, void* k_cache, void* v_cache, int64_t cache_row,
+                                const int64_t* kv_idx, int64_t cache_rows, unsigned int* bad, void* stream) {
+    int rc = check_common("amv_gemv_rope_kv", wtype, w, n_rows, k, act, 1);
+    if (rc) return rc;
+    AMV_REQUIRE(qkv && pos && k_cache && v_cache && kv_idx, "amv_gemv_rope_kv: null pointer");
+    AMV_REQUIRE(n_head > 0 && n_head_kv > 0 && D > 0 && D % 2 == 0 && n_rows == (n_head + 2 * n_head_kv) * D,
+                "amv_gemv_rope_kv: n_rows %lld != (n_head + 2 n_head_kv) * D", (long long)n_rows);
+    AMV_REQUIRE(cache_row >= n_head_kv * D && cache_rows > 0, "amv_gemv_rope_kv: cache row %lld < %lld",
+                (long long)cache_row, (long long)(n_head_kv * D));
+    MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, qkv, nullptr, nullptr, nullptr};
+    MmvPost& p = a.post;
+    p.pos = pos;
+    p.theta_scale = powf(freq_base, -2.0f / (float)D);  // amv_rope's expression with n_dims = D
+    p.freq_scale = freq_scale;
+    p.attn_factor = attn_factor;
+    p.n_q = (int)(n_head * D);
+    p.n_k = (int)(n_head_kv * D);
+    p.head_dim = (int)D;
+    p.k_cache = (uint16_t*)k_cache;
+    p.v_cache = (uint16_t*)v_cache;
+    p.cache_row = cache_row;
+    p.kv_idx = kv_idx;
+    p.cache_rows = cache_rows;
+    p.bad = bad;
+    rc = mmv_dispatch_fused(MMV_EP_ROPE_KV, a, act, amv_stream(stream));
+    if (rc) return rc;
+    return amv_check_launch("amv_gemv_rope_kv");
+}
+
+extern "C" int amv_gemv_add_rms_norm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst,
+                                     const float* e, float* eout, float eps, const float* norm_w, float* norm_y,
+                                     float* norm_o, void* act_out, int act_type, int rule, unsigned int* counters,
+                                     void* stream) {
+    int rc = check_common("amv_gemv_add_rms_norm", wtype, w, n_rows, k, act, 1);
+    if (rc) return rc;
+    AMV_REQUIRE(e && eout && counters, "amv_gemv_add_rms_norm: null pointer");
+    AMV_REQUIRE(norm_y || norm_o || act_out, "amv_gemv_add_rms_norm: no norm output requested");
+    AMV_REQUIRE(!norm_o || norm_w, "amv_gemv_add_rms_norm: norm_o needs norm_w");
+    AMV_REQUIRE(!act_out || act_type == AMV_T_Q8_0 || act_type == AMV_T_Q8_K,
+                "amv_gemv_add_rms_norm: act_type %d (Q8_0 or Q8_K)", act_type);
+    AMV_REQUIRE(n_rows % 4 == 0 && (!act_out || n_rows % (act_type == AMV_T_Q8_K ? 256 : 32) == 0),
+                "amv_gemv_add_rms_norm: n_rows must be a multiple of 4 (of the block size with the act output)");
+    AMV_REQUIRE(((uintptr_t)eout & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)norm_y & 15) == 0 &&
+                    ((uintptr_t)norm_o & 15) == 0 && ((uintptr_t)act_out & 15) == 0,
+                "amv_gemv_add_rms_norm: eout, norm buffers and act_out must be 16-byte aligned");
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_gemv_add_rms_norm: bad rule");
+    MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, dst, nullptr, e, eout};
+    MmvPost& p = a.post;
+    p.counters = counters;
+    p.norm_w = norm_w;
+    p.eps = eps;
+    p.norm_y = norm_y;
+    p.norm_o = norm_o;
+    p.act = amv_act_out(act_out, n_rows, act_out ? act_type : 0, rule);
+    rc = mmv_dispatch_fused(MMV_EP_ADD_NORM, a, act, amv_stream(stream));
+    if (rc) return rc;
+    return amv_check_launch("amv_gemv_add_rms_norm");
+}
+
+extern "C" int amv_gemv_swiglu_q8(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst,
+                                  float* eout, void* act_out, int act_type, int rule, unsigned int* counters,
+                                  void* stream) {
+    int rc = check_common("amv_gemv_swiglu_q8", wtype, w, n_rows, k, act, 1);
+    if (rc) return rc;
+    AMV_REQUIRE(eout && act_out && counters, "amv_gemv_swiglu_q8: null pointer");
+    AMV_REQUIRE(act_type == AMV_T_Q8_0 || act_type == AMV_T_Q8_K, "amv_gemv_swiglu_q8: act_type %d (Q8_0 or Q8_K)",
+                act_type);
+    AMV_REQUIRE(n_rows % (2 * (act_type == AMV_T_Q8_K ? 256 : 32)) == 0,
+                "amv_gemv_swiglu_q8: n_rows must be 2 x a multiple of the block size (gate rows, then up rows)");
+    AMV_REQUIRE(((uintptr_t)act_out & 15) == 0 && ((uintptr_t)eout & 15) == 0,
+                "amv_gemv_swiglu_q8: act_out and eout must be 16-byte aligned");
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_gemv_swiglu_q8: bad rule");
+    MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, dst, nullptr, nullptr, eout};
+    MmvPost& p = a.post;
+    p.counters = counters;
+    p.act = amv_act_out(act_out, n_rows / 2, act_type, rule);
+    rc = mmv_dispatch_fused(MMV_EP_SWIGLU_Q8, a, act, amv_stream(stream));
+    if (rc) return rc;
+    return amv_check_launch("amv_gemv_swiglu_q8");
 }

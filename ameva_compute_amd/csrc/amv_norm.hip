@@ -8,122 +8,19 @@
 // pair j is freq_scale * (p * theta_scale^j) built by the same repeated f32 multiplication as the CPU.
 #include "amv_common.h"
 
-// ---------------------------------------------------------------------------------------------------------------
-// Q8_0 quantization of one 32-element block held by one lane (the rules of amv_quantize_act)
-__device__ __forceinline__ void q8_block(const float (&v)[32], int rule, int8_t* __restrict__ qs, int2* __restrict__ meta) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    const float d = amax / 127.0f;
-    float id;
-    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    else id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t wq[8];
-    int s = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        uint32_t wv = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float t = v[4 * i + e] * id;
-            float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
-            qf = fminf(127.0f, fmaxf(-127.0f, qf));
-            const int q = (int)qf;
-            s += q;
-            wv |= (uint32_t)(q & 0xFF) << (8 * e);
-        }
-        wq[i] = wv;
-    }
-    reinterpret_cast<uint4*>(qs)[0] = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-    reinterpret_cast<uint4*>(qs)[1] = make_uint4(wq[4], wq[5], wq[6], wq[7]);
-    *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
-}
-
-// Q8_0 quantization of one 32-element block spread over 8 consecutive lanes (4 elements each, lane j of the 8 holds
-// elements 4j .. 4j + 3): the rules of amv_quantize_act. All 8 lanes must call it; stores 4 int8 per lane.
-__device__ __forceinline__ void q8_block_lanes8(const float (&v)[4], int rule, int j, int8_t* __restrict__ qs,
-                                                int2* __restrict__ meta) {
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, AMV_WAVE));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, AMV_WAVE));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, AMV_WAVE));
-    const float d = amax / 127.0f;
-    float id;
-    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    else id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t packed = 0;
-    int s = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float t = v[e] * id;
-        float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
-        qf = fminf(127.0f, fmaxf(-127.0f, qf));
-        const int q = (int)qf;
-        s += q;
-        packed |= (uint32_t)(q & 0xFF) << (8 * e);
-    }
-    s += __shfl_xor(s, 1, AMV_WAVE);
-    s += __shfl_xor(s, 2, AMV_WAVE);
-    s += __shfl_xor(s, 4, AMV_WAVE);
-    reinterpret_cast<uint32_t*>(qs)[j] = packed;
-    if (j == 0) *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
-}
-
-// One workgroup of 1024 per row; thread t owns the float4 chunks t, t + 1024, ... (its first chunk stays in registers
-// between the two passes). With the fused quantization the 8 lanes of a 32-element block quantize it together.
+// One workgroup of 1024 per row (amv_rms_row with one virtual lane per thread).
 #define RMS_THREADS 1024
 __global__ __launch_bounds__(RMS_THREADS) void k_rms_norm(const float* __restrict__ x, int n, float eps,
                                                          const float* __restrict__ w, float* __restrict__ y,
-                                                         float* __restrict__ o, int8_t* __restrict__ aq,
-                                                         int2* __restrict__ ameta, int rule) {
-    __shared__ double sred[RMS_THREADS / 64];
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const int n4 = n / 4;
-    const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)row * n);
-    const bool to_o = (w != nullptr && o != nullptr);
-    const float4 v0 = tid < n4 ? x4[tid] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const float4 w0 = (to_o && tid < n4) ? reinterpret_cast<const float4*>(w)[tid] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-    double s = (double)(v0.x * v0.x);
-    s += (double)(v0.y * v0.y);
-    s += (double)(v0.z * v0.z);
-    s += (double)(v0.w * v0.w);
-    for (int i = tid + RMS_THREADS; i < n4; i += RMS_THREADS) {
-        const float4 v = x4[i];
-        s += (double)(v.x * v.x);
-        s += (double)(v.y * v.y);
-        s += (double)(v.z * v.z);
-        s += (double)(v.w * v.w);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, AMV_WAVE);
-    if ((tid & 63) == 0) sred[tid >> 6] = s;
-    __syncthreads();
-    double tot = 0.0;
-#pragma unroll
-    for (int i = 0; i < RMS_THREADS / 64; ++i) tot += sred[i];
-    const float mean = (float)(tot / (double)n);
-    const float scale = 1.0f / sqrtf(mean + eps);
-    for (int i = tid; i < n4; i += RMS_THREADS) {
-        const float4 v = i == tid ? v0 : x4[i];
-        const float4 wv = !to_o ? make_float4(1.0f, 1.0f, 1.0f, 1.0f) : (i == tid ? w0 : reinterpret_cast<const float4*>(w)[i]);
-        const float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
-        if (y) reinterpret_cast<float4*>(y + (size_t)row * n)[i] = yv;
-        float4 qv = yv;
-        if (to_o) {
-            qv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
-            reinterpret_cast<float4*>(o + (size_t)row * n)[i] = qv;
-        }
-        if (aq) {
-            // n % 32 == 0 and the 8 chunks of a block are lanes 8 b .. 8 b + 7 of one wave (1024 is a multiple of 8)
-            const float vals[4] = {qv.x, qv.y, qv.z, qv.w};
-            q8_block_lanes8(vals, rule, i & 7, aq + (size_t)row * n + 32 * (i >> 3),
-                            ameta + (size_t)row * (n / 32) + (i >> 3));
-        }
-    }
+                                                         float* __restrict__ o, const AmvActOut act) {
+    __shared__ double sred[AMV_RMS_VLANES / 64];
+    const size_t row = blockIdx.x;
+    amv_rms_row<RMS_THREADS>(reinterpret_cast<const float4*>(x + row * n), n / 4, eps, w, y ? y + row * n : nullptr,
+                             o ? o + row * n : nullptr, amv_act_row(act, row, n), sred);
 }
 
-extern "C" int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y, float* o,
-                            void* act, int rule, void* stream) {
+extern "C" int amv_rms_norm_act(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y,
+                                float* o, void* act, int act_type, int rule, void* stream) {
     AMV_REQUIRE(x, "amv_rms_norm: null input");
     AMV_REQUIRE(n_rows > 0 && n > 0 && n_rows <= INT32_MAX && n <= INT32_MAX, "amv_rms_norm: bad shape");
     AMV_REQUIRE(n % 4 == 0, "amv_rms_norm: n %% 4 != 0");
@@ -132,20 +29,24 @@ extern "C" int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps
                 "amv_rms_norm: buffers must be 16-byte aligned");
     AMV_REQUIRE(!o || w, "amv_rms_norm: o needs the weight w");
     AMV_REQUIRE(y || o || act, "amv_rms_norm: no output requested");
-    AMV_REQUIRE(!act || n % 32 == 0, "amv_rms_norm: the fused Q8_0 output needs n %% 32 == 0");
+    AMV_REQUIRE(!act || act_type == AMV_T_Q8_0 || act_type == AMV_T_Q8_K, "amv_rms_norm: act_type %d (Q8_0 or Q8_K)",
+                act_type);
+    AMV_REQUIRE(!act || n % (act_type == AMV_T_Q8_K ? 256 : 32) == 0,
+                "amv_rms_norm: the fused quantization needs n %% block size == 0");
     AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_rms_norm: bad rule");
-    int8_t* aq = act ? (int8_t*)act : nullptr;
-    int2* ameta = act ? (int2*)((uint8_t*)act + n_rows * n) : nullptr;
     // the quantized output is of o when the weight is given, of y otherwise
-    const float* wq = w;
-    float* oo = o;
     if (act && w && !o) {
         amv_set_error("amv_rms_norm: the fused quantization of y * w needs o");
         return AMV_ERR_INVALID_ARG;
     }
-    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0, amv_stream(stream), x, (int)n, eps, wq,
-                       y, oo, aq, ameta, rule);
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0, amv_stream(stream), x, (int)n, eps, w,
+                       y, o, amv_act_out(act, n, act ? act_type : 0, rule, n_rows));
     return amv_check_launch("amv_rms_norm");
+}
+
+extern "C" int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y, float* o,
+                            void* act, int rule, void* stream) {
+    return amv_rms_norm_act(x, n_rows, n, eps, w, y, o, act, AMV_T_Q8_0, rule, stream);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -170,15 +71,12 @@ __global__ __launch_bounds__(256) void k_rope(const float* x, float* y,  // may 
         yr[2 * j + 1] = b;
         return;
     }
-    float theta = (float)pos[t];
-    for (int k = 0; k < j; ++k) theta *= theta_scale;
-    const float ang = freq_scale * theta;
-    const float c = cosf(ang) * attn_factor, s = sinf(ang) * attn_factor;
     const int e0 = neox ? j : 2 * j;
     const int e1 = neox ? j + n_dims / 2 : 2 * j + 1;
-    const float x0 = xr[e0], x1 = xr[e1];
-    yr[e0] = x0 * c - x1 * s;
-    yr[e1] = x0 * s + x1 * c;
+    float y0, y1;
+    amv_rope_pair((float)pos[t], j, theta_scale, freq_scale, attn_factor, xr[e0], xr[e1], y0, y1);
+    yr[e0] = y0;
+    yr[e1] = y1;
 }
 
 extern "C" int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_tok, int64_t n_head, int64_t ne0,
@@ -228,14 +126,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(float* __restrict__ qkv, const i
         const int e1 = 2 * j >= n_dims ? 2 * j + 1 : (neox ? j + n_dims / 2 : 2 * j + 1);
         const float x0 = xr[e0], x1 = xr[e1];
         float y0 = x0, y1 = x1;
-        if (2 * j < n_dims) {
-            float theta = p;
-            for (int k = 0; k < j; ++k) theta *= theta_scale;
-            const float ang = freq_scale * theta;
-            const float c = cosf(ang) * attn_factor, s = sinf(ang) * attn_factor;
-            y0 = x0 * c - x1 * s;
-            y1 = x0 * s + x1 * c;
-        }
+        if (2 * j < n_dims) amv_rope_pair(p, j, theta_scale, freq_scale, attn_factor, x0, x1, y0, y1);
         xr[e0] = y0;
         xr[e1] = y1;
         if (store) {

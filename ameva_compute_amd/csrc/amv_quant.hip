@@ -61,53 +61,12 @@ __global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x,
     const int lane = threadIdx.x & 63;
     const float4 v4 = reinterpret_cast<const float4*>(x + b * 256)[lane];
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    // (amax, index) with the smallest index on ties, then the signed value at that index
-    float am = 0.0f;
-    int ai = 0x7FFFFFFF;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float a = fabsf(v[e]);
-        if (a > am) { am = a; ai = 4 * lane + e; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float om = __shfl_xor(am, o, AMV_WAVE);
-        const int oi = __shfl_xor(ai, o, AMV_WAVE);
-        if (om > am || (om == am && oi < ai)) { am = om; ai = oi; }
-    }
+    const AmvQ8K r = amv_q8_K_lanes64(v, lane);
+    const int* q = r.q;
+    const int s = r.s16;
+    const float d = r.d;
+    const int packed = amv_pack4(r.q);
     uint8_t* yb = y_ggml ? y_ggml + b * 292 : nullptr;
-    if (am == 0.0f) {
-        int* yq = yb ? reinterpret_cast<int*>(yb) : nullptr;
-        if (yq) {
-            for (int w = lane; w < 73; w += 64) yq[w] = 0;
-        }
-        if (aq) {
-            reinterpret_cast<int*>(aq + b * 256)[lane] = 0;
-            if (lane < 16) abs16[b * 16 + lane] = 0;
-            if (lane == 0) ad[b] = 0.0f;
-        }
-        if (a16) {
-            reinterpret_cast<uint2*>(a16 + b * 256)[lane] = make_uint2(0u, 0u);
-            if (lane < 16) bs16[b * 16 + lane] = 0;
-            if (lane == 0) dt[(b % nsb) * m + b / nsb] = 0.0f;
-        }
-        return;
-    }
-    const float mx = __shfl(v[ai & 3], ai >> 2, AMV_WAVE);
-    const float iscale = -127.0f / mx;
-    int q[4];
-    int s = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int t = (int)rintf(iscale * v[e]);
-        q[e] = t < 127 ? t : 127;
-        s += q[e];
-    }
-    // sums over 16 elements = 4 lanes
-    s += __shfl_xor(s, 1, AMV_WAVE);
-    s += __shfl_xor(s, 2, AMV_WAVE);
-    const float d = 1.0f / iscale;
-    const int packed = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | ((q[3] & 0xFF) << 24);
     if (yb) {
         reinterpret_cast<int*>(yb + 4)[lane] = packed;
         if ((lane & 3) == 0) reinterpret_cast<int16_t*>(yb + 260)[lane >> 2] = (int16_t)s;

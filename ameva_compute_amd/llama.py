@@ -4,10 +4,11 @@ RMS_NORM+MUL, MUL_MAT q/k/v, ROPE, SET_ROWS into the KV cache, FLASH_ATTN_EXT, M
 MUL_MAT gate/up, SWIGLU, MUL_MAT down, ADD).
 
 MI355X-specific choices: q/k/v and gate/up are each one weight of stacked rows (one GEMV launch instead of three /
-two; the rows are independent, so the outputs equal the separate MUL_MATs), the Q8_0 quantization of each GEMV input
-is fused into the kernel that produces it (RMS_NORM, the attention combine), the residual ADDs and the SWIGLU are
-GEMV epilogues, and RoPE of q and k is one launch with the KV-cache stores. Every buffer is allocated up front, so a
-decode step launches kernels only and can be captured in a HIP graph.
+two; the rows are independent, so the outputs equal the separate MUL_MATs). The fused decode step is 8 launches:
+the GEMVs carry the small ops after them (ROPE + KV stores; ADD; SWIGLU + the activation quantization), the norms
+and the attention merge quantize their outputs for the next GEMV. Every buffer is allocated up front and the
+position and key count live in device memory, so a decode step launches kernels only and a captured HIP graph
+replays at any position.
 """
 from __future__ import annotations
 
@@ -46,13 +47,20 @@ class LlamaLayer:
         self.h = torch.empty(self.FF, **f32)
         self.down = torch.empty(self.H, **f32)
         u8 = dict(dtype=torch.uint8, device=dev)
-        self.act_h = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.H), **u8)
-        self.act_att = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.H), **u8)
-        self.act_h2 = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.H), **u8)
-        self.act_ff = torch.empty(lib().amv_act_bytes(ops.Q8_0, 1, self.FF), **u8)
-        self.fa_ws = torch.empty(lib().amv_flash_attn_workspace_bytes(n_head, n_head_kv, ctx, head_dim), **u8)
+        L = lib()
+        # activations of the GEMV inputs: Q8_0 for Q4_0 / Q8_0 weights, Q8_K for the K-quants
+        self.atype = ops.act_type(wq.type)
+        self.act_h = torch.empty(L.amv_act_bytes(self.atype, 1, self.H), **u8)
+        self.act_att = torch.empty(L.amv_act_bytes(self.atype, 1, self.H), **u8)
+        self.act_h2 = torch.empty(L.amv_act_bytes(self.atype, 1, self.H), **u8)
+        self.act_ff = torch.empty(L.amv_act_bytes(self.atype, 1, self.FF), **u8)
+        self.fa_ws = torch.empty(L.amv_flash_attn_workspace_bytes(n_head, n_head_kv, ctx, head_dim), **u8)
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.kv_idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.n_kv_dev = torch.ones(1, dtype=torch.int32, device=dev)
+        self.n_kv = 1
+        # arrival counters of the gate/up launch's quantization (self-resetting)
+        self.cnt = torch.zeros(ops.swiglu_counter_words(wgu.n_rows), dtype=torch.int32, device=dev)
 
     @staticmethod
     def stack_rows(*blocks: torch.Tensor) -> torch.Tensor:
@@ -60,97 +68,116 @@ class LlamaLayer:
         return torch.cat([b.reshape(b.shape[0], -1) for b in blocks], dim=0).contiguous()
 
     def set_position(self, pos: int) -> None:
-        """Position of the next decode step (written into device memory, so a captured graph picks it up)."""
+        """Position of the next decode step, written into device memory (a captured graph picks it up)."""
         self.pos.fill_(pos)
         self.kv_idx.fill_(pos)
+        self.n_kv_dev.fill_(pos + 1)
         self.n_kv = pos + 1
 
-    def decode(self, x: torch.Tensor, out: torch.Tensor, fused: bool = True) -> None:
-        """x f32 [H] -> out f32 [H] for the token at the position of set_position(); writes K/V into the cache.
-        The number of cached keys is fixed at n_kv for the launch (graph replays reuse it).
+    def _quant(self, x_ptr: int, n: int, act: torch.Tensor, st) -> None:
+        check(lib().amv_quantize_act(self.atype, x_ptr, 1, n, ops.Q8_X86, None, act.data_ptr(), st), "quantize")
 
-        fused=True runs 10 launches: RMS_NORM+MUL+Q8_0, q/k/v GEMV, ROPE+SET_ROWS, FA split, FA combine+Q8_0,
-        o GEMV+ADD, RMS_NORM+MUL+Q8_0, gate/up GEMV+SWIGLU, Q8_0, down GEMV+ADD. fused=False runs the same
-        arithmetic as one launch per graph node (16 launches); the results are identical."""
+    def decode(self, x: torch.Tensor, out: torch.Tensor, fused: bool = True, act_ready: bool = False,
+               next_layer: "LlamaLayer | None" = None) -> None:
+        """x f32 [H] -> out f32 [H] for the token at the position of set_position(); writes K/V into the cache.
+
+        fused=True, 8 launches: RMS_NORM + MUL + quantization of x (skipped with act_ready: the previous layer put it
+        in self.act_h); q/k/v GEMV + ROPE + KV stores; FA split; FA merge + quantization (key count from device
+        memory); o GEMV + ADD; FFN RMS_NORM + MUL + quantization; gate/up GEMV + SWIGLU + quantization; down GEMV +
+        ADD, then next_layer's attention RMS_NORM + quantization into next_layer.act_h when given (call
+        next_layer.decode with act_ready=True). The norms stay launches of their own: merged into the GEMV before
+        them (amv_gemv_add_rms_norm) they ran slower on MI355X.
+        fused=False: one launch per graph node (16 for Q4_0; the K-quant types quantize in separate launches and take
+        19), the key count from the host. Both give identical results."""
         L, st = lib(), torch.cuda.current_stream().cuda_stream
-        H, kv, D = self.H, self.kv, self.D
-        n_kv = self.n_kv
-        # attention block
-        check(L.amv_rms_norm(x.data_ptr(), 1, H, self.eps, self.attn_norm.data_ptr(), self.t_norm.data_ptr(),
-                             self.t_o.data_ptr(), self.act_h.data_ptr(), ops.Q8_X86, st), "rms_norm")
-        check(L.amv_mul_mat_vec(self.wqkv.type, self.wqkv.data.data_ptr(),
-                                self.wqkv.n_rows, H, self.act_h.data_ptr(), 1, self.qkv.data_ptr(), self.wqkv.n_rows,
-                                st), "qkv")
+        H, kv, D, FF, at = self.H, self.kv, self.D, self.FF, self.atype
+        q8 = at == ops.Q8_0
+        P = lambda t: t.data_ptr()  # noqa: E731
         if fused:
-            check(L.amv_rope_kv_store(self.qkv.data_ptr(), self.pos.data_ptr(), 1, self.n_head, self.n_head_kv, D, D,
-                                      0, self.base, 1.0, 1.0, self.k_cache.data_ptr(), self.v_cache.data_ptr(), kv,
-                                      self.kv_idx.data_ptr(), self.ctx, None, st), "rope + kv store")
-        else:
-            # RoPE of q and k: 40 contiguous heads of the qkv output, in place
-            check(L.amv_rope(self.qkv.data_ptr(), self.qkv.data_ptr(), self.pos.data_ptr(), 1,
-                             self.n_head + self.n_head_kv, D, D, 0, self.base, 1.0, 1.0, st), "rope")
-            kp = self.qkv.data_ptr() + H * 4
-            vp = kp + kv * 4
-            check(L.amv_set_rows_f16(kp, kv, self.k_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64,
-                                     self.ctx, None, st), "set_rows k")
-            check(L.amv_set_rows_f16(vp, kv, self.v_cache.data_ptr(), kv, 1, kv, self.kv_idx.data_ptr(), 64,
-                                     self.ctx, None, st), "set_rows v")
+            if not act_ready:
+                check(L.amv_rms_norm_act(P(x), 1, H, self.eps, P(self.attn_norm), None, P(self.t_o), P(self.act_h), at,
+                                         ops.Q8_X86, st), "rms_norm")
+            check(L.amv_gemv_rope_kv(self.wqkv.type, P(self.wqkv.data), self.wqkv.n_rows, H, P(self.act_h),
+                                     P(self.qkv), self.n_head, self.n_head_kv, D, P(self.pos), self.base, 1.0, 1.0,
+                                     P(self.k_cache), P(self.v_cache), kv, P(self.kv_idx), self.ctx, None, st),
+                  "qkv + rope + kv store")
+            cnt = P(self.cnt)
+            check(L.amv_flash_attn_decode_ex(P(self.qkv), P(self.k_cache), P(self.v_cache), None, P(self.att),
+                                             self.n_head, self.n_head_kv, self.ctx, P(self.n_kv_dev), D, kv, D, kv, D,
+                                             1.0 / (D ** 0.5), P(self.fa_ws), self.fa_ws.numel(), None,
+                                             P(self.act_att), at, ops.Q8_X86, st),
+                  "flash_attn (split, merge + quantization)")
+            check(L.amv_mul_mat_vec_ep(self.wo.type, P(self.wo.data), H, H, P(self.act_att), None, ops.EP_ADD, P(x),
+                                       P(self.x1), st), "wo + residual")
+            check(L.amv_rms_norm_act(P(self.x1), 1, H, self.eps, P(self.ffn_norm), None, P(self.t_o2), P(self.act_h2),
+                                     at, ops.Q8_X86, st), "ffn norm")
+            check(L.amv_gemv_swiglu_q8(self.wgu.type, P(self.wgu.data), self.wgu.n_rows, H, P(self.act_h2), None,
+                                       P(self.h), P(self.act_ff), at, ops.Q8_X86, cnt, st),
+                  "gate_up + swiglu + quantization")
+            check(L.amv_mul_mat_vec_ep(self.wdown.type, P(self.wdown.data), H, FF, P(self.act_ff), None,
+                                       ops.EP_ADD, P(self.x1), P(out), st), "down + residual")
+            if next_layer is not None:
+                nl = next_layer
+                check(L.amv_rms_norm_act(P(out), 1, H, nl.eps, P(nl.attn_norm), None, P(nl.t_o), P(nl.act_h),
+                                         nl.atype, ops.Q8_X86, st), "next attention norm")
+            return
+        # unfused: one launch per node
+        check(L.amv_rms_norm(P(x), 1, H, self.eps, P(self.attn_norm), P(self.t_norm), P(self.t_o),
+                             P(self.act_h) if q8 else None, ops.Q8_X86, st), "rms_norm")
+        if not q8:
+            self._quant(P(self.t_o), H, self.act_h, st)
+        check(L.amv_mul_mat_vec(self.wqkv.type, P(self.wqkv.data), self.wqkv.n_rows, H, P(self.act_h), 1,
+                                P(self.qkv), self.wqkv.n_rows, st), "qkv")
+        # RoPE of q and k: 40 contiguous heads of the qkv output, in place
+        check(L.amv_rope(P(self.qkv), P(self.qkv), P(self.pos), 1, self.n_head + self.n_head_kv, D, D, 0, self.base,
+                         1.0, 1.0, st), "rope")
+        kp = P(self.qkv) + H * 4
+        vp = kp + kv * 4
+        check(L.amv_set_rows_f16(kp, kv, P(self.k_cache), kv, 1, kv, P(self.kv_idx), 64, self.ctx, None, st),
+              "set_rows k")
+        check(L.amv_set_rows_f16(vp, kv, P(self.v_cache), kv, 1, kv, P(self.kv_idx), 64, self.ctx, None, st),
+              "set_rows v")
         ws = self.fa_ws.numel()
-        check(L.amv_flash_attn_decode(self.qkv.data_ptr(), self.k_cache.data_ptr(), self.v_cache.data_ptr(), None,
-                                      self.att.data_ptr(), self.n_head, self.n_head_kv, n_kv, D, kv, D, kv, D,
-                                      1.0 / (D ** 0.5), self.fa_ws.data_ptr(), ws, self.act_att.data_ptr(), ops.Q8_X86,
-                                      st), "flash_attn (+ Q8_0 of its output)")
-        if fused:
-            check(L.amv_mul_mat_vec_ep(self.wo.type, self.wo.data.data_ptr(), H, H, self.act_att.data_ptr(),
-                                       self.proj.data_ptr(), ops.EP_ADD, x.data_ptr(), self.x1.data_ptr(), st),
-                  "wo + residual")
-        else:
-            check(L.amv_mul_mat_vec(self.wo.type, self.wo.data.data_ptr(), H, H, self.act_att.data_ptr(), 1,
-                                    self.proj.data_ptr(), H, st), "wo")
-            check(L.amv_binary(0, self.proj.data_ptr(), x.data_ptr(), self.x1.data_ptr(), 1, H, 1, st), "residual 1")
-        # FFN block
-        check(L.amv_rms_norm(self.x1.data_ptr(), 1, H, self.eps, self.ffn_norm.data_ptr(), self.t_norm.data_ptr(),
-                             self.t_o2.data_ptr(), self.act_h2.data_ptr(), ops.Q8_X86, st), "ffn norm")
-        if fused:
-            check(L.amv_mul_mat_vec_ep(self.wgu.type, self.wgu.data.data_ptr(), self.wgu.n_rows, H,
-                                       self.act_h2.data_ptr(), self.gu.data_ptr(), ops.EP_SWIGLU_STACKED, None,
-                                       self.h.data_ptr(), st), "gate_up + swiglu")
-        else:
-            check(L.amv_mul_mat_vec(self.wgu.type, self.wgu.data.data_ptr(), self.wgu.n_rows, H,
-                                    self.act_h2.data_ptr(), 1, self.gu.data_ptr(), self.wgu.n_rows, st), "gate_up")
-            check(L.amv_swiglu(self.gu.data_ptr(), self.gu.data_ptr() + self.FF * 4, self.h.data_ptr(), self.FF, st),
-                  "swiglu")
-        check(L.amv_quantize_act(ops.Q8_0, self.h.data_ptr(), 1, self.FF, ops.Q8_X86, None, self.act_ff.data_ptr(),
-                                 st), "quant ffn")
-        if fused:
-            check(L.amv_mul_mat_vec_ep(self.wdown.type, self.wdown.data.data_ptr(), H, self.FF,
-                                       self.act_ff.data_ptr(), self.down.data_ptr(), ops.EP_ADD, self.x1.data_ptr(),
-                                       out.data_ptr(), st), "down + residual")
-        else:
-            check(L.amv_mul_mat_vec(self.wdown.type, self.wdown.data.data_ptr(), H, self.FF, self.act_ff.data_ptr(),
-                                    1, self.down.data_ptr(), H, st), "down")
-            check(L.amv_binary(0, self.down.data_ptr(), self.x1.data_ptr(), out.data_ptr(), 1, H, 1, st),
-                  "residual 2")
+        check(L.amv_flash_attn_decode(P(self.qkv), P(self.k_cache), P(self.v_cache), None, P(self.att), self.n_head,
+                                      self.n_head_kv, self.n_kv, D, kv, D, kv, D, 1.0 / (D ** 0.5), P(self.fa_ws), ws,
+                                      P(self.act_att) if q8 else None, ops.Q8_X86, st), "flash_attn")
+        if not q8:
+            self._quant(P(self.att), H, self.act_att, st)
+        check(L.amv_mul_mat_vec(self.wo.type, P(self.wo.data), H, H, P(self.act_att), 1, P(self.proj), H, st), "wo")
+        check(L.amv_binary(0, P(self.proj), P(x), P(self.x1), 1, H, 1, st), "residual 1")
+        check(L.amv_rms_norm(P(self.x1), 1, H, self.eps, P(self.ffn_norm), P(self.t_norm), P(self.t_o2),
+                             P(self.act_h2) if q8 else None, ops.Q8_X86, st), "ffn norm")
+        if not q8:
+            self._quant(P(self.t_o2), H, self.act_h2, st)
+        check(L.amv_mul_mat_vec(self.wgu.type, P(self.wgu.data), self.wgu.n_rows, H, P(self.act_h2), 1, P(self.gu),
+                                self.wgu.n_rows, st), "gate_up")
+        check(L.amv_swiglu(P(self.gu), P(self.gu) + FF * 4, P(self.h), FF, st), "swiglu")
+        self._quant(P(self.h), FF, self.act_ff, st)
+        check(L.amv_mul_mat_vec(self.wdown.type, P(self.wdown.data), H, FF, P(self.act_ff), 1, P(self.down), H, st),
+              "down")
+        check(L.amv_binary(0, P(self.down), P(self.x1), P(out), 1, H, 1, st), "residual 2")
 
     def _prefill_buffers(self, n_tok: int) -> dict:
         """Per-token-count buffers of prefill (allocated on first use; a captured graph must see them allocated)."""
         bufs = getattr(self, "_pf", None)
-        if bufs is not None and bufs["n"] >= n_tok:
+        if bufs is not None and bufs["n"] >= n_tok and bufs["at"] == ops.act_type(self.wqkv.type, n_tok):
             return bufs
         dev = self.attn_norm.device
         f32 = dict(dtype=torch.float32, device=dev)
         u8 = dict(dtype=torch.uint8, device=dev)
         L = lib()
         H, FF = self.H, self.FF
-        bufs = {"n": n_tok,
+        at = ops.act_type(self.wqkv.type, n_tok)
+        bufs = {"n": n_tok, "at": at,
                 "t_o": torch.empty((n_tok, H), **f32), "qkv": torch.empty((n_tok, self.wqkv.n_rows), **f32),
                 "att": torch.empty((n_tok, H), **f32), "proj": torch.empty((n_tok, H), **f32),
                 "x1": torch.empty((n_tok, H), **f32), "t_o2": torch.empty((n_tok, H), **f32),
                 "gu": torch.empty((n_tok, self.wgu.n_rows), **f32), "down": torch.empty((n_tok, H), **f32),
-                "act_h": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, H), **u8),
-                "act_att": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, H), **u8),
-                "act_h2": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, H), **u8),
-                "act_ff": torch.empty(L.amv_act_bytes(ops.Q8_0, n_tok, FF), **u8),
+                "act_h": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
+                "act_att": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
+                "act_h2": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
+                "act_ff": torch.empty(L.amv_act_bytes(at, n_tok, FF), **u8),
+                "h": torch.empty((n_tok, FF), **f32) if at != ops.Q8_0 else None,
                 "pos": torch.zeros(n_tok, dtype=torch.int32, device=dev),
                 "idx": torch.zeros(n_tok, dtype=torch.int64, device=dev)}
         self._pf = bufs
@@ -168,15 +195,24 @@ class LlamaLayer:
         """A prompt chunk through the layer: x f32 [n_tok, H] at positions set_prefill_position(pos0, n_tok) ->
         out f32 [n_tok, H]; writes the chunk's K/V rows into the cache and attends causally over keys
         0 .. pos0 + t. The MUL_MATs run on the int8 MFMA kernel (n_tok >= 8, the reference's crossover) and the
-        attention on the f16 MFMA prefill kernel; 12 launches."""
+        attention on the f16 MFMA prefill kernel; 12 launches (15 for the K-quants, whose activation
+        quantization is a launch of its own)."""
         L, st = lib(), torch.cuda.current_stream().cuda_stream
         n, pos0 = self.pf_n, self.pf_pos0
         b = self._prefill_buffers(n)
         H, kv, D, FF = self.H, self.kv, self.D, self.FF
-        mm = L.amv_mul_mat_q if n >= ops.MMQ_MIN_M else L.amv_mul_mat_vec
+        mm = L.amv_mul_mat_q if (n >= ops.MMQ_MIN_M and self.wqkv.type in ops.MMQ_TYPES) else L.amv_mul_mat_vec
         P = lambda t: t.data_ptr()  # noqa: E731
-        check(L.amv_rms_norm(P(x), n, H, self.eps, P(self.attn_norm), None, P(b["t_o"]), P(b["act_h"]), ops.Q8_X86,
-                             st), "rms_norm")
+        at = b["at"]
+        q8 = at == ops.Q8_0
+
+        def quant(src, k, act):
+            check(L.amv_quantize_act(at, src, n, k, ops.Q8_X86, None, P(act), st), "quantize")
+
+        check(L.amv_rms_norm(P(x), n, H, self.eps, P(self.attn_norm), None, P(b["t_o"]),
+                             P(b["act_h"]) if q8 else None, ops.Q8_X86, st), "rms_norm")
+        if not q8:
+            quant(P(b["t_o"]), H, b["act_h"])
         nq = self.wqkv.n_rows
         check(mm(self.wqkv.type, P(self.wqkv.data), nq, H, P(b["act_h"]), n, P(b["qkv"]), nq, st), "qkv")
         check(L.amv_rope_kv_store(P(b["qkv"]), P(b["pos"]), n, self.n_head, self.n_head_kv, D, D, 0, self.base, 1.0,
@@ -185,15 +221,22 @@ class LlamaLayer:
         check(L.amv_flash_attn_prefill(P(b["qkv"]), nq, D, P(self.k_cache), P(self.v_cache), None, 0, P(b["att"]), n,
                                        self.n_head, self.n_head_kv, pos0 + n, D, kv, D, kv, D, 1.0 / (D ** 0.5), pos0,
                                        st), "flash_attn prefill")
-        check(L.amv_quantize_act(ops.Q8_0, P(b["att"]), n, H, ops.Q8_X86, None, P(b["act_att"]), st), "quant att")
+        quant(P(b["att"]), H, b["act_att"])
         check(mm(self.wo.type, P(self.wo.data), H, H, P(b["act_att"]), n, P(b["proj"]), H, st), "wo")
         check(L.amv_binary(0, P(b["proj"]), P(x), P(b["x1"]), n, H, n, st), "residual 1")
-        check(L.amv_rms_norm(P(b["x1"]), n, H, self.eps, P(self.ffn_norm), None, P(b["t_o2"]), P(b["act_h2"]),
-                             ops.Q8_X86, st), "ffn norm")
+        check(L.amv_rms_norm(P(b["x1"]), n, H, self.eps, P(self.ffn_norm), None, P(b["t_o2"]),
+                             P(b["act_h2"]) if q8 else None, ops.Q8_X86, st), "ffn norm")
+        if not q8:
+            quant(P(b["t_o2"]), H, b["act_h2"])
         ng = self.wgu.n_rows
         check(mm(self.wgu.type, P(self.wgu.data), ng, H, P(b["act_h2"]), n, P(b["gu"]), ng, st), "gate_up")
-        check(L.amv_swiglu_rows(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, None, FF, n, FF, P(b["act_ff"]), ops.Q8_X86,
-                                st), "swiglu + quant")
+        if q8:
+            check(L.amv_swiglu_rows(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, None, FF, n, FF, P(b["act_ff"]),
+                                    ops.Q8_X86, st), "swiglu + quant")
+        else:
+            check(L.amv_swiglu_rows(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, P(b["h"]), FF, n, FF, None, ops.Q8_X86,
+                                    st), "swiglu")
+            quant(P(b["h"]), FF, b["act_ff"])
         check(mm(self.wdown.type, P(self.wdown.data), H, FF, P(b["act_ff"]), n, P(b["down"]), H, st), "down")
         check(L.amv_binary(0, P(b["down"]), P(b["x1"]), P(out), n, H, n, st), "residual 2")
 

@@ -153,6 +153,68 @@ def mul_mat_vec_ep(w: QWeight, act: torch.Tensor, ep_mode: int, e: torch.Tensor 
     return dst, (dst if eout is None else eout)
 
 
+def add_norm_counter_words(n_rows: int) -> int:
+    """Arrival-counter words of gemv_add_rms_norm (AMV_ADD_NORM_COUNTER_WORDS)."""
+    return 32 * (n_rows // 32 + 2)
+
+
+def swiglu_counter_words(n_rows: int) -> int:
+    """Arrival-counter words of gemv_swiglu_act for a stacked weight of n_rows rows (AMV_SWIGLU_COUNTER_WORDS)."""
+    return 32 * (n_rows // 64 + 1)
+
+
+def gemv_add_rms_norm(w: QWeight, act: torch.Tensor, e: torch.Tensor, eps: float, norm_w: torch.Tensor | None,
+                      act_t: int = Q8_0, rule: int = Q8_X86, counters: torch.Tensor | None = None):
+    """eout = W act + e, then RMS_NORM (+ MUL by norm_w) of eout and its activation row of type act_t, in one
+    launch. Returns (v = W act, eout, y = x * scale, o = y * norm_w or None, act_out)."""
+    _need_gpu(act, "gemv_add_rms_norm")
+    dev = act.device
+    n = w.n_rows
+    v = torch.empty(n, dtype=torch.float32, device=dev)
+    eout = torch.empty(n, dtype=torch.float32, device=dev)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    o = torch.empty(n, dtype=torch.float32, device=dev) if norm_w is not None else None
+    a = torch.empty(lib().amv_act_bytes(act_t, 1, n), dtype=torch.uint8, device=dev)
+    if counters is None:
+        counters = torch.zeros(add_norm_counter_words(n), dtype=torch.int32, device=dev)
+    check(lib().amv_gemv_add_rms_norm(w.type, w.data.data_ptr(), n, w.k, act.data_ptr(), v.data_ptr(), e.data_ptr(),
+                                      eout.data_ptr(), eps, _ptr(norm_w), y.data_ptr(), _ptr(o), a.data_ptr(), act_t,
+                                      rule, counters.data_ptr(), _stream()), "amv_gemv_add_rms_norm")
+    return v, eout, y, o, a
+
+
+def gemv_swiglu_act(w: QWeight, act: torch.Tensor, act_t: int = Q8_0, rule: int = Q8_X86,
+                    counters: torch.Tensor | None = None):
+    """Stacked gate/up GEMV + SWIGLU + the activation row of the result, one launch. Returns (v, h, act_out)."""
+    _need_gpu(act, "gemv_swiglu_act")
+    dev = act.device
+    F = w.n_rows // 2
+    v = torch.empty(w.n_rows, dtype=torch.float32, device=dev)
+    h = torch.empty(F, dtype=torch.float32, device=dev)
+    a = torch.empty(lib().amv_act_bytes(act_t, 1, F), dtype=torch.uint8, device=dev)
+    if counters is None:
+        counters = torch.zeros(swiglu_counter_words(w.n_rows), dtype=torch.int32, device=dev)
+    check(lib().amv_gemv_swiglu_q8(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), v.data_ptr(),
+                                   h.data_ptr(), a.data_ptr(), act_t, rule, counters.data_ptr(), _stream()),
+          "amv_gemv_swiglu_q8")
+    return v, h, a
+
+
+def gemv_rope_kv(w: QWeight, act: torch.Tensor, n_head: int, n_head_kv: int, pos: torch.Tensor,
+                 k_cache: torch.Tensor, v_cache: torch.Tensor, kv_idx: torch.Tensor, freq_base: float = 500000.0,
+                 freq_scale: float = 1.0, attn_factor: float = 1.0, bad: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k/v GEMV + ROPE NORMAL of q and k + f16 stores of k and v at cache row kv_idx[0]; returns qkv f32 [n_rows].
+    Caches f16 [rows, n_head_kv * D]; pos int32 [1], kv_idx int64 [1] on the device."""
+    _need_gpu(act, "gemv_rope_kv")
+    D = w.n_rows // (n_head + 2 * n_head_kv)
+    qkv = torch.empty(w.n_rows, dtype=torch.float32, device=act.device)
+    check(lib().amv_gemv_rope_kv(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), qkv.data_ptr(), n_head,
+                                 n_head_kv, D, pos.data_ptr(), freq_base, freq_scale, attn_factor,
+                                 k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), kv_idx.data_ptr(),
+                                 k_cache.shape[0], _ptr(bad), _stream()), "amv_gemv_rope_kv")
+    return qkv
+
+
 def mul_mat(w: QWeight, x: torch.Tensor, rule: int = Q8_X86) -> torch.Tensor:
     """ggml_mul_mat(src0 = w, src1 = x): x f32 [m, k] -> [m, n_rows]; activations quantized to vec_dot_type."""
     x2 = x.reshape(-1, x.shape[-1])
@@ -309,6 +371,36 @@ def flash_attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
     check(lib().amv_flash_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(mask), out.data_ptr(), n_head,
                                       n_head_kv, n_kv, D, k.stride(1), k.stride(0), v.stride(1), v.stride(0), scale,
                                       workspace.data_ptr(), need, _ptr(act), rule, _stream()), "amv_flash_attn_decode")
+    return out
+
+
+def flash_attn_decode_ex(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, n_kv_max: int,
+                         n_kv_dev: torch.Tensor | None = None, mask: torch.Tensor | None = None,
+                         act: torch.Tensor | None = None, act_t: int = Q8_0, rule: int = Q8_X86,
+                         counters: torch.Tensor | None = None, one_launch: bool = False,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """flash_attn_decode with the key count read from n_kv_dev (int32 [1] on the device) when given, capped at
+    n_kv_max. act: optional activation row of type act_t (Q8_0 or Q8_K) that also receives the output. one_launch:
+    the split merge runs in the split launch's last workgroups, on counters (int32 [>= 32 n_head_kv] zeros,
+    allocated when None)."""
+    _need_gpu(q, "flash_attn_decode_ex")
+    n_head, D = q.shape
+    n_head_kv = k.shape[0]
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("flash_attn_decode_ex: K/V rows must be contiguous")
+    need = lib().amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv_max, D)
+    if need < 0:
+        raise ValueError("flash_attn_decode_ex: unsupported shape")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if one_launch and counters is None:
+        counters = torch.zeros(32 * n_head_kv, dtype=torch.int32, device=q.device)
+    out = torch.empty_like(q)
+    check(lib().amv_flash_attn_decode_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(mask), out.data_ptr(),
+                                         n_head, n_head_kv, n_kv_max, _ptr(n_kv_dev), D, k.stride(1), k.stride(0),
+                                         v.stride(1), v.stride(0), scale, workspace.data_ptr(), need,
+                                         _ptr(counters if one_launch else None), _ptr(act), act_t, rule, _stream()),
+          "amv_flash_attn_decode_ex")
     return out
 
 

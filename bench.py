@@ -134,8 +134,10 @@ def bench_layer(torch, dev, args):
     xs = [torch.randn(4096, generator=g, device=dev)] + [torch.empty(4096, device=dev) for _ in range(layers_n)]
 
     def chain(fused=True):
+        # fused: each layer's down GEMV also computes the next layer's attention norm and activation row
         for i, lay in enumerate(layers):
-            lay.decode(xs[i], xs[i + 1], fused=fused)
+            nxt = layers[i + 1] if fused and i + 1 < layers_n else None
+            lay.decode(xs[i], xs[i + 1], fused=fused, act_ready=fused and i > 0, next_layer=nxt)
 
     def graph_ms(fused):
         s = torch.cuda.Stream()
@@ -157,8 +159,8 @@ def bench_layer(torch, dev, args):
     nbytes = layers[0].step_bytes(layers[0].ctx)
     gbs = nbytes / (ms * 1e-3) / 1e9
     pf = bench_prefill(torch, dev, layers[0], 512)
-    log(f"bench: layer decode {ms * 1e3:.2f} us/layer (graph, 10 launches), {ms_unfused * 1e3:.2f} us unfused "
-        f"(16 launches), {ms_eager * 1e3:.2f} us eager; {nbytes / 1e6:.1f} MB -> {gbs:.0f} GB/s")
+    log(f"bench: layer decode {ms * 1e3:.2f} us/layer (graph, 8 launches), {ms_unfused * 1e3:.2f} us "
+        f"unfused (16 launches), {ms_eager * 1e3:.2f} us eager; {nbytes / 1e6:.1f} MB -> {gbs:.0f} GB/s")
     del layers
     torch.cuda.empty_cache()
     return {"layer_decode_us": round(ms * 1e3, 3), "layer_decode_tok_s": round(1e3 / ms, 1),

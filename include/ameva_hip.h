@@ -105,6 +105,38 @@ int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t k, const v
 int amv_mul_mat_vec_ep(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst, int ep_mode,
                        const float* e, float* eout, void* stream);
 
+/* Decode GEMVs that carry the next small op of a Llama layer in the same launch (no counterpart kernel in the
+ * reference, whose graph runs these ops as separate nodes; each saves one ~4 us launch at bs1). One activation
+ * column (Q8_0 / Q8_K layout of amv_quantize_act), results identical to the unfused sequence.
+ * counters: device uint32 array, zero before the first call, left at zero by every call (self-resetting arrival
+ * counters, one per 128-byte line; calls that share one array must not run concurrently). Sizes in words:
+ * amv_gemv_add_rms_norm AMV_ADD_NORM_COUNTER_WORDS(n_rows), amv_gemv_swiglu_q8 AMV_SWIGLU_COUNTER_WORDS(n_rows). */
+#define AMV_ADD_NORM_COUNTER_WORDS(n_rows) (32 * ((n_rows) / 32 + 2))
+#define AMV_SWIGLU_COUNTER_WORDS(n_rows) (32 * ((n_rows) / 64 + 1))
+/*
+ *
+ * amv_gemv_rope_kv: w stacks n_head * D q rows, n_head_kv * D k rows, n_head_kv * D v rows (n_rows = their sum);
+ * qkv f32 [n_rows] gets q and k rotated by ROPE NORMAL (n_dims = D; amv_rope's arithmetic, positions from pos[0])
+ * and v as computed; k and v also go as f16 to row kv_idx[0] of the caches (amv_rope_kv_store's layout and skip
+ * rule: a row outside [0, cache_rows) is not stored and each skipped head adds 1 to *bad when bad is not NULL).
+ * = MUL_MAT + ROPE + ROPE + SET_ROWS + SET_ROWS. */
+int amv_gemv_rope_kv(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* qkv,
+                     int64_t n_head, int64_t n_head_kv, int64_t D, const int32_t* pos, float freq_base,
+                     float freq_scale, float attn_factor, void* k_cache, void* v_cache, int64_t cache_row,
+                     const int64_t* kv_idx, int64_t cache_rows, unsigned int* bad, void* stream);
+/* amv_gemv_add_rms_norm: eout = W act + e (dst = W act too when not NULL), then amv_rms_norm of eout (one row of
+ * n_rows) into norm_y / norm_o / act_out (any may be NULL; act_out is the activation row of act_type 8 = Q8_0, with
+ * `rule`, or 15 = Q8_K), done by the last workgroup of the launch.
+ * = MUL_MAT + ADD + RMS_NORM + MUL (+ the next activation quantization). */
+int amv_gemv_add_rms_norm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst,
+                          const float* e, float* eout, float eps, const float* norm_w, float* norm_y, float* norm_o,
+                          void* act_out, int act_type, int rule, unsigned int* counters, void* stream);
+/* amv_gemv_swiglu_q8: AMV_EP_SWIGLU_STACKED (w = F gate rows then F up rows; eout [F]) and the activation row of
+ * eout into act_out (act_type 8 = Q8_0 with `rule`, F % 32 == 0; 15 = Q8_K, F % 256 == 0), each block quantized by
+ * the last workgroup producing it. = MUL_MAT x 2 + SWIGLU + the next quantization. */
+int amv_gemv_swiglu_q8(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst, float* eout,
+                       void* act_out, int act_type, int rule, unsigned int* counters, void* stream);
+
 /* Parity instrumentation of the same kernels: the exact integer sums per weight block, int32
  * [m][n_rows][nblk * per] with nblk = k / block size, per = 2 for Q4_K (sum sc*dot, sum m*bsum) and 1 otherwise.
  * These are the per-block int32 sums of ggml's vec_dot (bit-exact contract). */
@@ -150,6 +182,10 @@ int amv_i2s_gemv_sums(const void* w, int64_t n_rows, int64_t k, const void* act,
  * ---------------------------------------------------------------------------------------------------------- */
 int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y, float* o, void* act,
                  int rule, void* stream);
+/* amv_rms_norm with the fused quantization into the activation type of the next GEMV: act_type 8 = Q8_0 (`rule`,
+ * n % 32 == 0) or 15 = Q8_K (n % 256 == 0); act has n_rows rows in the amv_quantize_act layout. */
+int amv_rms_norm_act(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y, float* o,
+                     void* act, int act_type, int rule, void* stream);
 
 /* ROPE (ggml_rope_ext f32, enc_rope ggml-ameva.cpp:3965, ameva_rope.comp): x, y [n_tok][n_head][ne0] contiguous
  * (in place allowed), pos int32 [n_tok]; mode 0 NORMAL or 2 NEOX; ext_factor 0, no frequency factors. */
@@ -191,6 +227,20 @@ int amv_flash_attn_decode(const float* q, const void* k, const void* v, const vo
                           int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row, int64_t k_head, int64_t v_row,
                           int64_t v_head, float scale, void* workspace, int64_t workspace_bytes, void* act, int rule,
                           void* stream);
+
+/* amv_flash_attn_decode with the key count in device memory and a choice of output quantization (no counterpart in
+ * the reference; for decode steps captured once in a HIP graph and replayed at growing positions). The key count is
+ * n_kv_dev[0] when n_kv_dev is not NULL, capped at n_kv_max, which sizes the launch and the workspace
+ * (amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv_max, D)). act (may be NULL): the output's activation row,
+ * act_type 8 = Q8_0 (`rule`) or 15 = Q8_K (even n_head / n_head_kv). counters == NULL: the split merge runs as a
+ * second launch; otherwise in the last workgroup of each KV head (one launch; counters: >= 32 * n_head_kv words,
+ * zero before the first call, left at zero). Results identical to amv_flash_attn_decode at the same key count
+ * whenever both pick the same key split (always when n_kv_max * n_head_kv <= 65536). */
+int amv_flash_attn_decode_ex(const float* q, const void* k, const void* v, const void* mask, float* out,
+                             int64_t n_head, int64_t n_head_kv, int64_t n_kv_max, const int32_t* n_kv_dev, int64_t D,
+                             int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, float scale,
+                             void* workspace, int64_t workspace_bytes, unsigned int* counters, void* act, int act_type,
+                             int rule, void* stream);
 
 /* FLASH_ATTN_EXT over n_tok query positions (prompt prefill; enc_flash_attn ggml-ameva.cpp:4204-4284 with
  * q->ne[1] > 1, ameva_flash_attn.comp), on the f16 matrix cores. D = 128, n_head / n_head_kv integral.

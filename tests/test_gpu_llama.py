@@ -161,3 +161,87 @@ def test_layer_prefill_matches_decode_steps(dev, n_tok, pos0):
     assert rel_l2(kp[rows].float().cpu().numpy(), layer.k_cache[rows].float().cpu().numpy()) < 1e-2
     assert rel_l2(vp[rows].float().cpu().numpy(), layer.v_cache[rows].float().cpu().numpy()) < 1e-2
     assert torch.equal(kp[:pos0], k0[:pos0]) and torch.equal(kp[pos0 + n_tok:], k0[pos0 + n_tok:])
+
+
+def _fill_caches(layer, dev, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    layer.k_cache.copy_(torch.randn(layer.k_cache.shape, generator=g, device=dev).half())
+    layer.v_cache.copy_(torch.randn(layer.v_cache.shape, generator=g, device=dev).half())
+    return g
+
+
+@pytest.mark.parametrize("wtype", [2, 12])
+def test_fused_chain_matches_unfused(dev, wtype):
+    """Two chained layers, fused (5 launches per layer: the first layer's down GEMV computes the second layer's
+    attention norm and its activation row) against one launch per node: identical outputs, K/V rows and activation
+    rows, for Q4_0 (Q8_0 activations) and Q4_K (Q8_K activations) weights."""
+    from ameva_compute_amd.llama import random_layer
+    layers = [random_layer(dev, seed=21 + i, ctx=512, wtype=wtype) for i in range(2)]
+    for i, lay in enumerate(layers):
+        _fill_caches(lay, dev, 40 + i)
+        lay.set_position(300)
+    k0 = [lay.k_cache.clone() for lay in layers]
+    v0 = [lay.v_cache.clone() for lay in layers]
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    x = torch.randn(layers[0].H, generator=g, device=dev)
+    mid, out = torch.empty_like(x), torch.empty_like(x)
+    layers[0].decode(x, mid, fused=False)
+    layers[1].decode(mid, out, fused=False)
+    torch.cuda.synchronize()
+    ref = (mid.clone(), out.clone(), [lay.k_cache.clone() for lay in layers], [lay.v_cache.clone() for lay in layers],
+           [lay.act_ff.clone() for lay in layers], layers[1].act_h.clone())
+    for i, lay in enumerate(layers):
+        lay.k_cache.copy_(k0[i])
+        lay.v_cache.copy_(v0[i])
+    layers[0].decode(x, mid, fused=True, next_layer=layers[1])
+    layers[1].decode(mid, out, fused=True, act_ready=True)
+    torch.cuda.synchronize()
+    assert torch.equal(mid, ref[0]) and torch.equal(out, ref[1])
+    for i, lay in enumerate(layers):
+        assert torch.equal(lay.k_cache, ref[2][i]) and torch.equal(lay.v_cache, ref[3][i])
+        assert torch.equal(lay.act_ff, ref[4][i])
+    assert torch.equal(layers[1].act_h, ref[5])
+
+
+def test_decode_graph_replays_at_growing_positions(dev):
+    """One fused decode step captured once and replayed at positions p .. p + 5 (position, cache row and key count
+    live in device memory): every replay equals the eager step at that position, K/V rows included."""
+    from ameva_compute_amd.llama import random_layer
+    layer = random_layer(dev, seed=5, ctx=1024)
+    g = _fill_caches(layer, dev, 8)
+    k0, v0 = layer.k_cache.clone(), layer.v_cache.clone()
+    xs = [torch.randn(layer.H, generator=g, device=dev) for _ in range(6)]
+    x, out = torch.empty(layer.H, device=dev), torch.empty(layer.H, device=dev)
+    p0 = 700
+    eager = []
+    for i in range(6):
+        layer.set_position(p0 + i)
+        x.copy_(xs[i])
+        layer.decode(x, out)
+        eager.append(out.clone())
+    torch.cuda.synchronize()
+    k_e, v_e = layer.k_cache.clone(), layer.v_cache.clone()
+    layer.k_cache.copy_(k0)
+    layer.v_cache.copy_(v0)
+    layer.set_position(p0)
+    x.copy_(xs[0])
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        layer.decode(x, out)  # warm-up on the capture stream (rewrites row p0 with the same values)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        layer.decode(x, out)
+    for i in range(6):
+        layer.set_position(p0 + i)
+        x.copy_(xs[i])
+        out.zero_()
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[i]), i
+    assert torch.equal(layer.k_cache, k_e) and torch.equal(layer.v_cache, v_e)
