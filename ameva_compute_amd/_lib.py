@@ -50,6 +50,7 @@ SIGNATURES = {
     "amv_binary": (I32, [I32, P, P, P, I64, I64, I64, P]),
     "amv_set_rows_f16": (I32, [P, I64, P, I64, I64, I64, P, I32, I64, P, P]),
     "amv_get_rows": (I32, [I32, P, I64, I64, P, I64, P, P, P]),
+    "amv_argmax": (I32, [P, I64, P, P, P, I64, P]),
 }
 
 _lib = None

@@ -1,5 +1,5 @@
 // Glue ops of the decoder graph: ADD / MUL with row broadcast (residuals, norm weights), f32 -> f16 copies and
-// SET_ROWS into an f16 KV cache, GET_ROWS (embedding lookup) from f32 / f16 / Q4_0 / Q8_0 / Q6_K rows.
+// SET_ROWS into an f16 KV cache, GET_ROWS (embedding lookup) from f32 / f16 / Q4_0 / Q8_0 / Q4_K / Q6_K rows.
 // Roles of ameva_binary.comp, ameva_cpy.comp, ameva_set_rows.comp and ameva_get_rows(_q).comp of the reference.
 #include "amv_common.h"
 
@@ -60,8 +60,8 @@ extern "C" int amv_set_rows_f16(const float* src, int64_t src_stride, void* dst,
     return amv_check_launch("amv_set_rows_f16");
 }
 
-// GET_ROWS: dst f32 [n_idx][n] = dequantized row idx[i] of src (type F32, F16, Q4_0, Q8_0: ggml blocks, row stride
-// in bytes). Dequantization as ggml's dequantize_row_* (ameva_get_rows_q.comp).
+// GET_ROWS: dst f32 [n_idx][n] = dequantized row idx[i] of src (type F32, F16, Q4_0, Q8_0, Q4_K, Q6_K: ggml blocks,
+// row stride in bytes). Dequantization as ggml's dequantize_row_* (ameva_get_rows_q.comp), the same f32 expressions.
 __global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ src, int64_t row_bytes, int type,
                                                  const int32_t* __restrict__ idx, int64_t n_idx, int64_t n,
                                                  int64_t src_rows, float* __restrict__ dst,
@@ -87,10 +87,38 @@ __global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ sr
         const float d = amv_h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
         const int nib = j < 16 ? (blk[2 + j] & 0xF) : (blk[2 + j - 16] >> 4);
         v = (float)(nib - 8) * d;
-    } else {  // Q8_0
+    } else if (type == AMV_T_Q8_0) {
         const uint8_t* blk = row + (c / 32) * 34;
         const float d = amv_h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
         v = (float)(int8_t)blk[2 + c % 32] * d;
+    } else if (type == AMV_T_Q4_K) {
+        // dequantize_row_q4_K: chunk of 64 = 32 low nibbles (sub-block 2 ch) then 32 high nibbles (2 ch + 1)
+        const uint8_t* blk = row + (c / 256) * 144;
+        const int e = (int)(c % 256), ch = e / 64, l = e % 64;
+        const int sub = 2 * ch + (l >= 32);
+        const uint8_t qb = blk[16 + 32 * ch + (l & 31)];
+        const int q = l < 32 ? (qb & 0xF) : (qb >> 4);
+        const uint8_t* sc = blk + 4;
+        int scl, mn;
+        if (sub < 4) {
+            scl = sc[sub] & 63;
+            mn = sc[sub + 4] & 63;
+        } else {
+            scl = (sc[sub + 4] & 0xF) | ((sc[sub - 4] >> 6) << 4);
+            mn = (sc[sub + 4] >> 4) | ((sc[sub] >> 6) << 4);
+        }
+        const float d = amv_h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const float dmin = amv_h2f((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+        v = (d * (float)scl) * (float)q - dmin * (float)mn;
+    } else {  // Q6_K (dequantize_row_q6_K): halves of 128, quarters of 32 take ql low/high nibbles and 2 qh bits
+        const uint8_t* blk = row + (c / 256) * 210;
+        const int e = (int)(c % 256), h = e / 128, r = e % 128, qt = r / 32, l = r % 32;
+        const uint8_t lb = blk[64 * h + l + 32 * (qt & 1)];
+        const int lo = qt < 2 ? (lb & 0xF) : (lb >> 4);
+        const int hi = (blk[128 + 32 * h + l] >> (2 * qt)) & 3;
+        const int q = (lo | (hi << 4)) - 32;
+        const float d = amv_h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+        v = d * (float)(int8_t)blk[192 + 8 * h + l / 16 + 2 * qt] * (float)q;
     }
     dst[i] = v;
 }
@@ -105,10 +133,73 @@ extern "C" int amv_get_rows(int type, const void* src, int64_t src_rows, int64_t
     case AMV_T_F16: rb = n * 2; break;
     case AMV_T_Q4_0: AMV_REQUIRE(n % 32 == 0, "amv_get_rows: n %% 32"); rb = n / 32 * 18; break;
     case AMV_T_Q8_0: AMV_REQUIRE(n % 32 == 0, "amv_get_rows: n %% 32"); rb = n / 32 * 34; break;
+    case AMV_T_Q4_K: AMV_REQUIRE(n % 256 == 0, "amv_get_rows: n %% 256"); rb = n / 256 * 144; break;
+    case AMV_T_Q6_K: AMV_REQUIRE(n % 256 == 0, "amv_get_rows: n %% 256"); rb = n / 256 * 210; break;
     default: amv_set_error("amv_get_rows: type %d not supported", type); return AMV_ERR_UNSUPPORTED;
     }
     const int64_t total = n_idx * n;
     hipLaunchKernelGGL(k_get_rows, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, amv_stream(stream),
                        (const uint8_t*)src, rb, type, idx, n_idx, n, src_rows, dst, bad);
     return amv_check_launch("amv_get_rows");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Greedy sampling: the index of the largest of x[0 .. n) (the first on ties; NaN never wins), written to token[0];
+// with history, also to history[step[0]] (when below history_len) and step[0] incremented, so a decode loop replayed
+// as a HIP graph keeps its token and its output on the device. One workgroup of 1024: float4 loads, then wave and
+// workgroup reductions with the same (value, index) order.
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, int32_t* __restrict__ token,
+                                                int32_t* __restrict__ history, int32_t* __restrict__ step,
+                                                int history_len) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    const int n4 = n / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (int i = tid; i < n4; i += 1024) {
+        const float4 v = x4[i];
+        argmax_take(bv, bi, v.x, 4 * i);
+        argmax_take(bv, bi, v.y, 4 * i + 1);
+        argmax_take(bv, bi, v.z, 4 * i + 2);
+        argmax_take(bv, bi, v.w, 4 * i + 3);
+    }
+    for (int i = 4 * n4 + tid; i < n; i += 1024) argmax_take(bv, bi, x[i], i);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) argmax_take(bv, bi, __shfl_xor(bv, o, AMV_WAVE), __shfl_xor(bi, o, AMV_WAVE));
+    if (lane == 0) {
+        sv[wv] = bv;
+        si[wv] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w) argmax_take(bv, bi, sv[w], si[w]);
+        const int t = bi == 0x7FFFFFFF ? 0 : bi;  // all NaN: token 0
+        token[0] = t;
+        if (history) {
+            const int s = step[0];
+            if (s >= 0 && s < history_len) history[s] = t;
+            step[0] = s + 1;
+        }
+    }
+}
+
+extern "C" int amv_argmax(const float* x, int64_t n, int32_t* token, int32_t* history, int32_t* step,
+                          int64_t history_len, void* stream) {
+    AMV_REQUIRE(x && token, "amv_argmax: null pointer");
+    AMV_REQUIRE(n > 0 && n <= INT32_MAX, "amv_argmax: bad length %lld", (long long)n);
+    AMV_REQUIRE(((uintptr_t)x & 15) == 0, "amv_argmax: x must be 16-byte aligned");
+    AMV_REQUIRE(!history || (step && history_len > 0 && history_len <= INT32_MAX),
+                "amv_argmax: history needs step and history_len");
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, amv_stream(stream), x, (int)n, token, history, step,
+                       (int)history_len);
+    return amv_check_launch("amv_argmax");
 }

@@ -458,9 +458,9 @@ def set_rows_f16(dst: torch.Tensor, src: torch.Tensor, idx: torch.Tensor | None 
 
 
 def get_rows(src: torch.Tensor, src_type: int, n: int, idx: torch.Tensor) -> torch.Tensor:
-    """ggml_get_rows: f32 [len(idx), n] from rows of src (F32 = 0, F16 = 1, Q4_0, Q8_0 in ggml layout)."""
+    """ggml_get_rows: f32 [len(idx), n] from rows of src (F32 = 0, F16 = 1, Q4_0, Q8_0, Q4_K, Q6_K in ggml layout)."""
     _need_gpu(idx, "get_rows")
-    rb = {0: n * 4, 1: n * 2, Q4_0: n // 32 * 18, Q8_0: n // 32 * 34}[src_type]
+    rb = 4 * n if src_type == 0 else 2 * n if src_type == 1 else ggml_row_bytes(src_type, n)
     rows = src.numel() * src.element_size() // rb
     out = torch.empty((idx.numel(), n), dtype=torch.float32, device=idx.device)
     bad = torch.zeros(1, dtype=torch.int32, device=idx.device)
@@ -469,3 +469,15 @@ def get_rows(src: torch.Tensor, src_type: int, n: int, idx: torch.Tensor) -> tor
     if int(bad.item()) != 0:
         raise IndexError("get_rows: row index out of range (FAIL-FAST)")
     return out
+
+
+def argmax(x: torch.Tensor, token: torch.Tensor | None = None, history: torch.Tensor | None = None,
+           step: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy sampling on the device: token int32 [1] = first index of the maximum of x (f32, contiguous); with
+    history (int32 [L]) and step (int32 [1]) also history[step] = token, step += 1."""
+    _need_gpu(x, "argmax")
+    if token is None:
+        token = torch.empty(1, dtype=torch.int32, device=x.device)
+    check(lib().amv_argmax(x.data_ptr(), x.numel(), token.data_ptr(), _ptr(history), _ptr(step),
+                           0 if history is None else history.numel(), _stream()), "amv_argmax")
+    return token

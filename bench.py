@@ -337,6 +337,72 @@ def bench_prefill(torch, dev, layer, n_tok):
             "layer_prefill_note": "one Llama-3-8B layer, Q4_0, 512-token prompt from position 0, HIP graph"}
 
 
+def bench_model(torch, dev, n_prompt: int = 512, n_new: int = 256) -> dict:
+    """the 32-layer Llama-3-8B-shape stack (Q4_K layers, Q6_K head of 128256 rows, Q4_K token
+    embedding), seeded random weights and prompt token ids. A 512-token prefill (the prompt as one chunk through
+    every layer, then the first token sampled), then 256 greedy decode steps, each one replay of a decode step
+    captured once in a HIP graph (token, position and key count live in device memory; context 513 .. 768)."""
+    from ameva_compute_amd.model import random_model
+    t0 = time.time()
+    m = random_model(dev, ctx=1024, max_new=n_new + 8)
+    torch.cuda.synchronize()
+    build_s = time.time() - t0
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    prompt = torch.randint(0, m.vocab, (n_prompt,), generator=g, device=dev, dtype=torch.int32)
+    m.reset()
+    m.prefill(prompt)  # allocates the prompt buffers
+    torch.cuda.synchronize()
+    reps = 3
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        m.reset()
+        m.prefill(prompt)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_pf = e0.elapsed_time(e1) / reps
+    first = int(m.token.item())
+    # decode: one step captured (after a warm-up step on the capture stream), state rewound, then n_new replays
+    m.set_position(n_prompt)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        m.decode_step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        m.decode_step()
+    m.set_position(n_prompt)
+    m.step.fill_(1)
+    m.token.fill_(first)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(n_new):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_dec = e0.elapsed_time(e1) / n_new
+    assert int(m.step.item()) == n_new + 1 and int(m.pos.item()) == n_prompt + n_new
+    toks = m.history[: n_new + 1].cpu().tolist()
+    nbytes = m.decode_bytes(n_prompt + n_new // 2)
+    ops_pf = m.prefill_ops(n_prompt)
+    log(f"bench: model (32 x Q4_K + Q6_K head) prefill {n_prompt} tokens {ms_pf:.1f} ms = "
+        f"{n_prompt / (ms_pf * 1e-3):.0f} tok/s ({ops_pf / (ms_pf * 1e-3) / 1e12:.1f} TOPS); decode {ms_dec * 1e3:.1f} "
+        f"us/token = {1e3 / ms_dec:.1f} tok/s, {nbytes / (ms_dec * 1e-3) / 1e9:.0f} GB/s; built in {build_s:.1f} s")
+    del gr, m
+    torch.cuda.empty_cache()
+    return {"model_prefill_512_ms": round(ms_pf, 3), "model_prefill_512_tok_s": round(n_prompt / (ms_pf * 1e-3), 1),
+            "model_prefill_512_tops": round(ops_pf / (ms_pf * 1e-3) / 1e12, 2),
+            "model_decode_ms_per_token": round(ms_dec, 4), "model_decode_tok_s": round(1e3 / ms_dec, 2),
+            "model_decode_bytes_per_token": nbytes, "model_decode_gbs": round(nbytes / (ms_dec * 1e-3) / 1e9, 1),
+            "model_tokens_head": toks[:8],
+            "model_note": "config 5: 32 Llama-3-8B layers Q4_K, Q6_K head 128256 x 4096, Q4_K embedding, random "
+                          "weights and prompt ids, 512-token prefill (one chunk) + 256 greedy decode steps (one HIP "
+                          "graph replayed per token)"}
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -368,6 +434,8 @@ def main():
     ap.add_argument("--only-layer", action="store_true", help="only the layer decode figure (for profiling)")
     ap.add_argument("--only-i2s", action="store_true", help="only the BitNet I2_S figures (for profiling)")
     ap.add_argument("--only-batched", action="store_true", help="only the batched MUL_MAT figures (for profiling)")
+    ap.add_argument("--only-model", action="store_true", help="only the 32-layer model figures (for profiling)")
+    ap.add_argument("--no-model", action="store_true", help="skip the 32-layer model figures")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
@@ -394,6 +462,9 @@ def main():
         return
     if args.only_i2s:
         print(json.dumps(bench_i2s(ops, torch, dev)), flush=True)
+        return
+    if args.only_model:
+        print(json.dumps(bench_model(torch, dev)), flush=True)
         return
 
     log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")
@@ -440,6 +511,8 @@ def main():
     if not args.only_headline:
         layer_info = bench_layer(torch, dev, args)
         extra.update(layer_info)
+        if not args.no_model:
+            extra.update(bench_model(torch, dev))
 
     result = {
         "metric": "Q4_0 GEMV GB/s (% HBM peak) + bs1 decode tok/s, Llama-8B-shape layer",

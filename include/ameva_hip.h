@@ -266,9 +266,17 @@ int amv_binary(int op, const float* a, const float* b, float* dst, int64_t n_row
  * r when idx is NULL; idx_bits 32 or 64. Out-of-range indices are skipped and counted in *bad (device, may be NULL). */
 int amv_set_rows_f16(const float* src, int64_t src_stride, void* dst, int64_t dst_stride, int64_t n_rows, int64_t n,
                      const void* idx, int idx_bits, int64_t dst_rows, unsigned int* bad, void* stream);
-/* GET_ROWS: dst f32 [n_idx][n] = row idx[i] of src (type F32, F16, Q4_0 or Q8_0 in ggml layout, src_rows rows). */
+/* GET_ROWS (enc_get_rows, ameva_get_rows_q.comp): dst f32 [n_idx][n] = row idx[i] of src (type F32, F16, Q4_0,
+ * Q8_0, Q4_K or Q6_K in ggml layout, src_rows rows), dequantized with ggml's dequantize_row_* expressions; rows
+ * outside [0, src_rows) give zeros and add 1 to *bad when bad is not NULL. */
 int amv_get_rows(int type, const void* src, int64_t src_rows, int64_t n, const int32_t* idx, int64_t n_idx, float* dst,
                  unsigned int* bad, void* stream);
+/* Greedy sampling of a decode step (the argmax of llama.cpp's greedy sampler; no GPU kernel in the reference, whose
+ * logits go back to the host): token[0] = index of the largest of x[0 .. n) (the first on ties; NaN never wins).
+ * history (may be NULL): history[step[0]] = token when step[0] < history_len, then step[0] += 1 -- a decode loop
+ * replayed as a HIP graph keeps its tokens on the device. x 16-byte aligned. */
+int amv_argmax(const float* x, int64_t n, int32_t* token, int32_t* history, int32_t* step, int64_t history_len,
+               void* stream);
 
 #ifdef __cplusplus
 }
