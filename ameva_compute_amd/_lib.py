@@ -32,6 +32,7 @@ SIGNATURES = {
     "amv_i2s_quantize_act": (I32, [P, I64, I64, P, P]),
     "amv_i2s_gemv": (I32, [P, I64, I64, P, I64, F32, P, I64, P]),
     "amv_i2s_gemv_sums": (I32, [P, I64, I64, P, I64, P, P]),
+    "amv_i2s_gemv_f32": (I32, [P, I64, I64, P, F32, P, P]),
     "amv_rms_norm_act": (I32, [P, I64, I64, F32, P, P, P, P, I32, I32, P]),
     "amv_rms_norm": (I32, [P, I64, I64, F32, P, P, P, P, I32, P]),
     "amv_rope": (I32, [P, P, P, I64, I64, I64, I32, I32, F32, F32, F32, P]),

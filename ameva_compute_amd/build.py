@@ -51,6 +51,7 @@ def build(verbose: bool = False) -> str:
     for o in objs:
         os.remove(o)
     build_plugin()
+    build_amuda()
     return LIB
 
 
@@ -76,6 +77,22 @@ def build_plugin() -> str:
         raise RuntimeError("hipcc failed on ggml_ameva.cpp")
     os.replace(tmp, PLUGIN)
     return PLUGIN
+
+
+AMUDA = os.path.join(HERE, "libamuda_hip.so")
+
+
+def build_amuda() -> str:
+    """libamuda_hip.so: the amuda / BitNet C ABI subset (include/amuda_hip.h) over libameva_hip.so (host code only)."""
+    src = os.path.join(CSRC, "amuda_hip.cpp")
+    tmp = AMUDA + ".tmp"
+    cmd = [HIPCC, *FLAGS, "-shared", "-o", tmp, src, "-L" + HERE, "-lameva_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed on amuda_hip.cpp")
+    os.replace(tmp, AMUDA)
+    return AMUDA
 
 
 if __name__ == "__main__":

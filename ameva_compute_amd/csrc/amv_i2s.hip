@@ -285,3 +285,57 @@ extern "C" int amv_i2s_gemv_sums(const void* w, int64_t n_rows, int64_t k, const
     AMV_REQUIRE(sums, "amv_i2s_gemv_sums: null output");
     return i2s_gemv_impl(w, n_rows, k, act, m, 0.0f, nullptr, 0, sums, stream);
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Ternary GEMV on f32 activations, the amuda entry's arithmetic (bitnet_gemv_i2_s_exact, reference
+// src/amuda/amuda_ops.c:91-121 and :299-352): y[r] = scale * sum_j map(c_rj) x_j with map = {-1, 0, +1, 0} for codes
+// 0..3 (code 3 contributes nothing, unlike the integer path's c - 1). One wave per row; lane l takes bytes
+// 16 l .. 16 l + 15 of each 1 KiB step of the row (one 16-byte load), i.e. half of a 32-byte block: weights
+// 128 b + 16 (l % 2) + i + 32 g for byte i and code group g. f32 products summed per lane, then a wave sum; the order
+// differs from the reference's sequential loop (the bar is f32 tolerance, as in its own test).
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_i2s_gemv_f32(const uint8_t* __restrict__ w, int n_rows, int k,
+                                                     const float* __restrict__ x, float scale,
+                                                     float* __restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n_rows) return;  // uniform per wave
+    const int rb = k / 4;       // bytes per row
+    const uint8_t* wr = w + (size_t)row * rb;
+    float acc = 0.0f;
+    for (int b0 = 16 * lane; b0 < rb; b0 += 1024) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wr + b0);
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+        const int blk = b0 >> 5, half = (b0 >> 4) & 1;
+        const float* xb = x + 128 * blk + 16 * half;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {  // code group g: bits 7-6, 5-4, 3-2, 1-0 of each byte
+            const float4* xg = reinterpret_cast<const float4*>(xb + 32 * g);
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 xv = xg[q4];
+                const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t c = (wd[q4] >> (8 * e + 6 - 2 * g)) & 3u;
+                    const float m = c == 0u ? -1.0f : (c == 2u ? 1.0f : 0.0f);
+                    acc = fmaf(m, xs[e], acc);
+                }
+            }
+        }
+    }
+    acc = amv_wave_sum(acc);
+    if (lane == 0) y[row] = acc * scale;
+}
+
+extern "C" int amv_i2s_gemv_f32(const void* w, int64_t n_rows, int64_t k, const float* x, float scale, float* y,
+                                void* stream) {
+    AMV_REQUIRE(w && x && y, "amv_i2s_gemv_f32: null pointer");
+    AMV_REQUIRE(n_rows > 0 && k > 0 && n_rows <= INT32_MAX && k <= INT32_MAX, "amv_i2s_gemv_f32: bad shape");
+    AMV_REQUIRE(k % 128 == 0, "amv_i2s_gemv_f32: k %% 128 != 0");
+    AMV_REQUIRE(k % 64 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0,
+                "amv_i2s_gemv_f32: w and x must be 16-byte aligned");
+    hipLaunchKernelGGL(k_i2s_gemv_f32, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0, amv_stream(stream),
+                       (const uint8_t*)w, (int)n_rows, (int)k, x, scale, y);
+    return amv_check_launch("amv_i2s_gemv_f32");
+}

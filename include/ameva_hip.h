@@ -173,6 +173,10 @@ int amv_i2s_gemv(const void* w, int64_t n_rows, int64_t k, const void* act, int6
 /* the exact integers sum_j (code_rj - 1) q_cj, int32 [m][n_rows] (bit-exact contract) */
 int amv_i2s_gemv_sums(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, int32_t* sums,
                       void* stream);
+/* Ternary GEMV on f32 activations with the amuda code map {-1, 0, +1, 0} (bitnet_gemv_i2_s_exact, amuda_ops.c:91-121):
+ * y f32 [n_rows] = scale * sum_j map(c_rj) x_j; w the BitNet packing above (k % 128 == 0), x f32 [k]. Backs
+ * ac_ops_bitnet_gemv_i2_s_exact of libamuda_hip.so. */
+int amv_i2s_gemv_f32(const void* w, int64_t n_rows, int64_t k, const float* x, float scale, float* y, void* stream);
 
 /* ------------------------------------------------------------------------------------------------------------
  * RMS_NORM (ggml_compute_forward_rms_norm_f32; enc_rms_norm ggml-ameva.cpp:3941 with the fused MUL of
