@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libameva_hip.so")
-SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_fa_prefill.hip", "amv_mmq.hip", "amv_elem.hip"]
+SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_fa_prefill.hip", "amv_mmq.hip", "amv_mmq16.hip", "amv_elem.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

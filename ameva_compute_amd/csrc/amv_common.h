@@ -32,6 +32,21 @@ static inline AmvQ8kMma amv_q8k_mma_layout(int64_t m, int64_t k) {
     return L;
 }
 
+// Offsets (bytes) of the AMV_ACT_Q8_0_MMA activation layout: after the Q8_0 layout (int8 [m][k], {f32 d, i32 sum}
+// [m][k/32]; rounded up to 16 bytes) come the int8 values as f16 [m][k] (exact) and the block scales transposed, f32
+// [k/32][m].
+struct AmvQ80Mma {
+    int64_t a16, dt, total;
+};
+static inline AmvQ80Mma amv_q8_0_mma_layout(int64_t m, int64_t k) {
+    AmvQ80Mma L;
+    const int64_t q80 = m * k + m * (k / 32) * 8;
+    L.a16 = (q80 + 15) & ~(int64_t)15;
+    L.dt = L.a16 + 2 * m * k;  // 2 m k is a multiple of 64 (k % 32 == 0)
+    L.total = L.dt + 4 * m * (k / 32);
+    return L;
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // host: error state (first message of the failing call, per thread)
 void amv_set_error(const char* fmt, ...);

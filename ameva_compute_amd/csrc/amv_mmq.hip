@@ -465,6 +465,44 @@ static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const v
     return amv_check_launch("amv_mul_mat_q");
 }
 
+// amv_mmq16.hip: Q4_0 / Q8_0 on the f16 matrix cores (AMV_ACT_Q8_0_MMA activations)
+int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
+              int64_t ldd, int32_t* sums, hipStream_t st);
+
+// Batches above this many tokens go to the f16 kernel (128-token tiles); smaller ones to the int8 kernel, which reads
+// the plain Q8_0 prefix of the same activation buffer.
+#define MMQ16_MIN_M 64
+
+static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
+                        int act_type, int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream) {
+    if (act_type == AMV_ACT_Q8_0_MMA && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0) && m > MMQ16_MIN_M) {
+        AMV_REQUIRE(w && act && (dst || sums), "%s: null pointer", fn);
+        AMV_REQUIRE(n_rows > 0 && k > 0 && k % 32 == 0, "%s: bad shape", fn);
+        AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 128 && m * k <= INT32_MAX && n_rows * (k / 32) <= INT32_MAX,
+                    "%s: too large", fn);
+        AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "%s: buffers must be 16-byte aligned", fn);
+        AMV_REQUIRE(!dst || ldd >= n_rows, "%s: ldd < n_rows", fn);
+        return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
+    }
+    const bool ok = (act_type == AMV_T_Q8_0 || act_type == AMV_ACT_Q8_0_MMA) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)
+                                                                             : (act_type == AMV_ACT_Q8_K_MMA && wtype == AMV_T_Q4_K);
+    AMV_REQUIRE(ok, "%s: activation type %d does not feed weight type %d", fn, act_type, wtype);
+    return mmq_impl(wtype, w, n_rows, k, act, m, dst, ldd, sums, stream);
+}
+
+extern "C" int amv_mul_mat_q_act(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type,
+                                 int64_t m, float* dst, int64_t ldd, void* stream) {
+    AMV_REQUIRE(dst, "amv_mul_mat_q_act: null dst");
+    return mmq_act_impl("amv_mul_mat_q_act", wtype, w, n_rows, k, act, act_type, m, dst, ldd, nullptr, stream);
+}
+
+extern "C" int amv_mul_mat_q_act_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
+                                            int act_type, int64_t m, int32_t* sums, void* stream) {
+    AMV_REQUIRE(sums, "amv_mul_mat_q_act_block_sums: null output");
+    return mmq_act_impl("amv_mul_mat_q_act_block_sums", wtype, w, n_rows, k, act, act_type, m, nullptr, 0, sums,
+                        stream);
+}
+
 extern "C" int amv_mul_mat_q(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m,
                              float* dst, int64_t ldd, void* stream) {
     AMV_REQUIRE(dst, "amv_mul_mat_q: null dst");

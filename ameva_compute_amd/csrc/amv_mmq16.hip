@@ -1,0 +1,273 @@
+// Prefill MUL_MAT for Q4_0 / Q8_0 weights on the f16 matrix cores of MI355X, with exact integer block sums.
+//
+// Role of ameva_mmq.comp / ameva_mmqb.comp (reference, enc_mul_mat_mmq ggml-ameva.cpp:2540-2647): dst[m][n] =
+// sum_b d_w[n][b] d_a[m][b] S[m][n][b], S the int32 dot of block b (ggml's vec_dot_q4_0_q8_0 / q8_0_q8_0 sumi).
+// The operands of S are small integers, exact in f16: the weight (q - 8 for Q4_0, q for Q8_0) and the activation
+// q_a (|q_a| <= 127); a block's 32 products sum to |S| <= 32 * 128 * 127 < 2^24, so v_mfma_f32_32x32x16_f16 (two per
+// block) returns S exactly in f32. The f32 epilogue per output and block is then two VALU operations,
+// t = S * d_w, acc = fma(t, d_a, acc), against three for int8 MFMA (convert, scale product, fma) -- on MI355X the
+// epilogue, not the matrix core, bounds a kernel with a scale per 32 products, and the f16 rate keeps pace with it.
+//
+// Workgroup of 4 waves (2 x 2) on a tile of 64 TN weight rows x 64 TM tokens; wave (wr, wc) owns rows
+// 32 TN wr .. + 32 TN and tokens 32 TM wc .. + 32 TM as TN x TM tiles of 32 x 32. Pipeline steps of 2 blocks (64 k): the
+// global loads of step s + 1 are issued before step s computes from LDS; at staging the weights are converted to f16
+// once per workgroup (shared by its 64 TM tokens) and the activations (already f16 copies, AMV_ACT_Q8_0_MMA) and both
+// scale vectors are copied. MFMA operand layout (32x32x16 f16): lane l supplies A row l % 32 and B column l % 32 with
+// 8 halves k = 8 (l / 32) .. + 7 of the 16-k step; it receives D column l % 32 (a token), rows
+// 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
+#include "amv_common.h"
+
+typedef _Float16 g16_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 g16_h2 __attribute__((ext_vector_type(2)));
+typedef float g16_f16v __attribute__((ext_vector_type(16)));
+
+#define G16_KS 64                // k per pipeline step (2 blocks)
+#define G16_LDK (G16_KS + 8)     // LDS row in halves, padded by 16 B against bank conflicts
+
+// 4 bytes of nibbles (low or high half already selected and masked) -> 4 halves (n - off) as two f16 pairs
+__device__ __forceinline__ uint2 g16_nib4(uint32_t x, g16_h2 off) {
+    const uint32_t m64 = 0x64646464u;
+    const g16_h2 p0 = __builtin_bit_cast(g16_h2, __builtin_amdgcn_perm(x, m64, 0x00050004u)) - off;
+    const g16_h2 p1 = __builtin_bit_cast(g16_h2, __builtin_amdgcn_perm(x, m64, 0x00070006u)) - off;
+    return make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+}
+
+// Registers of one staging step: thread t < 2 BN stages (row t / 2, block t % 2) of the weights (sw) and its scale
+// (sdw); every thread stages 64 bytes of one token's activations (token t / 2, block t % 2, sa) and one activation
+// scale (sda). Plain arrays (a struct of them was placed in scratch by the compiler).
+#define G16_NW(WT) ((WT) == AMV_T_Q4_0 ? 1 : 2)
+
+template <int WT, int TN, int TM>
+__device__ __forceinline__ void g16_load(uint4 (&sw)[G16_NW(WT)], float& sdw, uint4& sa0, uint4& sa1, uint4& sa2,
+                                         uint4& sa3, float& sda, int step, const uint8_t* __restrict__ wq,
+                                         const uint16_t* __restrict__ wd, int N, int nb, int n0,
+                                         const uint16_t* __restrict__ a16, const float* __restrict__ dT, int M, int m0,
+                                         int K) {
+    constexpr int BN = 64 * TN, BM = 64 * TM;
+    const int t = threadIdx.x;
+    const int blk = t & 1;
+    const int b = 2 * step + blk, bc = min(b, nb - 1);  // a block past the end reads the last one, scale 0
+    if (t < 2 * BN) {
+        const int row = min(n0 + (t >> 1), N - 1);
+        const size_t bi = (size_t)row * nb + bc;
+        if constexpr (WT == AMV_T_Q4_0) {
+            sw[0] = *reinterpret_cast<const uint4*>(wq + bi * 16);
+            sdw = b < nb ? amv_h2f(wd[amv_q4_0_didx(row, bc, nb, N)]) : 0.0f;
+        } else {
+            sw[0] = *reinterpret_cast<const uint4*>(wq + bi * 32);
+            sw[G16_NW(WT) - 1] = *reinterpret_cast<const uint4*>(wq + bi * 32 + 16);
+            sdw = b < nb ? amv_h2f(wd[bi]) : 0.0f;
+        }
+    }
+    if (t < 2 * BM) {
+        const int tok = min(m0 + (t >> 1), M - 1);
+        const uint4* ap = reinterpret_cast<const uint4*>(a16 + (size_t)tok * K + 32 * bc);
+        sa0 = ap[0];
+        sa1 = ap[1];
+        sa2 = ap[2];
+        sa3 = ap[3];
+        const int tb = t / BM;  // scale of (block 2 step + tb, token t % BM)
+        sda = dT[(size_t)min(2 * step + tb, nb - 1) * M + min(m0 + t % BM, M - 1)];
+    }
+}
+
+template <int WT, int TN, int TM>
+__device__ __forceinline__ void g16_store(const uint4 (&sw)[G16_NW(WT)], float sdw, uint4 sa0, uint4 sa1, uint4 sa2,
+                                          uint4 sa3, float sda, uint16_t* __restrict__ sA,
+                                          uint16_t* __restrict__ sB, float* __restrict__ sDw,
+                                          float* __restrict__ sDa) {
+    constexpr int BN = 64 * TN, BM = 64 * TM;
+    const int t = threadIdx.x;
+    const int blk = t & 1;
+    if (t < 2 * BN) {
+        uint4* dst = reinterpret_cast<uint4*>(sA + (t >> 1) * G16_LDK + 32 * blk);
+        if constexpr (WT == AMV_T_Q4_0) {
+            // element e < 16: low nibble of byte e; element 16 + e: high nibble of byte e; value q - 8
+            const g16_h2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
+            const uint32_t wv[4] = {sw[0].x, sw[0].y, sw[0].z, sw[0].w};
+            uint2 lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo[i] = g16_nib4(wv[i] & 0x0F0F0F0Fu, off);
+                hi[i] = g16_nib4((wv[i] >> 4) & 0x0F0F0F0Fu, off);
+            }
+            dst[0] = make_uint4(lo[0].x, lo[0].y, lo[1].x, lo[1].y);
+            dst[1] = make_uint4(lo[2].x, lo[2].y, lo[3].x, lo[3].y);
+            dst[2] = make_uint4(hi[0].x, hi[0].y, hi[1].x, hi[1].y);
+            dst[3] = make_uint4(hi[2].x, hi[2].y, hi[3].x, hi[3].y);
+        } else {
+            // int8 q -> f16: byte (q + 128) under the exponent of 1024, minus 1152
+            const g16_h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+            const uint4 w1 = sw[G16_NW(WT) - 1];
+            const uint32_t wv[8] = {sw[0].x, sw[0].y, sw[0].z, sw[0].w, w1.x, w1.y, w1.z, w1.w};
+            uint2 h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = g16_nib4(wv[i] ^ 0x80808080u, off);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = make_uint4(h[2 * i].x, h[2 * i].y, h[2 * i + 1].x, h[2 * i + 1].y);
+        }
+        sDw[blk * BN + (t >> 1)] = sdw;
+    }
+    if (t < 2 * BM) {
+        uint4* bd = reinterpret_cast<uint4*>(sB + (t >> 1) * G16_LDK + 32 * blk);
+        bd[0] = sa0;
+        bd[1] = sa1;
+        bd[2] = sa2;
+        bd[3] = sa3;
+        sDa[t] = sda;  // [block t / BM][token t % BM]
+    }
+}
+
+template <int WT, bool SUMS, int TN, int TM>
+__global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int N,
+                                              int nb, const uint16_t* __restrict__ a16, const float* __restrict__ dT,
+                                              int M, float* __restrict__ dst, int64_t ldd,
+                                              int32_t* __restrict__ sums, int vec_out) {
+    constexpr int BN = 64 * TN, BM = 64 * TM;
+    __shared__ __align__(16) uint16_t sA[2][BN * G16_LDK];
+    __shared__ __align__(16) uint16_t sB[2][BM * G16_LDK];
+    __shared__ __align__(16) float sDw[2][2 * BN];
+    __shared__ __align__(16) float sDa[2][2 * BM];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wr = w & 1, wc = w >> 1, c = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int K = nb * 32;
+    const int nsteps = (nb + 1) / 2;
+
+    g16_f16v acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    uint4 sw[G16_NW(WT)], sa0, sa1, sa2, sa3;
+    float sdw = 0.0f, sda = 0.0f;
+    g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, 0, wq, wd, N, nb, n0, a16, dT, M, m0, K);
+    g16_store<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, sA[0], sB[0], sDw[0], sDa[0]);
+    __syncthreads();
+    for (int step = 0; step < nsteps; ++step) {
+        const int buf = step & 1;
+        if (step + 1 < nsteps)
+            g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, step + 1, wq, wd, N, nb, n0, a16, dT, M, m0, K);
+#pragma unroll 1
+        for (int bl = 0; bl < 2; ++bl) {  // one block's accumulators live at a time
+            g16_f16v C[TN][TM];
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) C[i][j][r] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int kk = 32 * bl + 16 * ks + 8 * h;
+                g16_h8 A[TN], B[TM];
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+                    A[i] = *reinterpret_cast<const g16_h8*>(sA[buf] + (32 * (TN * wr + i) + c) * G16_LDK + kk);
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    B[j] = *reinterpret_cast<const g16_h8*>(sB[buf] + (32 * (TM * wc + j) + c) * G16_LDK + kk);
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) C[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[j], C[i][j], 0, 0, 0);
+            }
+            const int b = 2 * step + bl;
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int tl = 32 * (TM * wc + j) + c;  // token of this lane in the tile
+                if (SUMS) {
+                    const int m = m0 + tl;
+#pragma unroll
+                    for (int i = 0; i < TN; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int n = n0 + 32 * (TN * wr + i) + 8 * (r >> 2) + 4 * h + (r & 3);
+                            if (b < nb && m < M && n < N) sums[((size_t)m * N + n) * nb + b] = (int32_t)C[i][j][r];
+                        }
+                } else {
+                    const float da = sDa[buf][bl * BM + tl];
+#pragma unroll
+                    for (int i = 0; i < TN; ++i) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float4 dw4 = *reinterpret_cast<const float4*>(
+                                &sDw[buf][bl * BN + 32 * (TN * wr + i) + 8 * q + 4 * h]);
+                            const float dwv[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int r = 4 * q + e;
+                                acc[i][j][r] = fmaf(C[i][j][r] * dwv[e], da, acc[i][j][r]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        if (step + 1 < nsteps) {
+            g16_store<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, sA[buf ^ 1], sB[buf ^ 1], sDw[buf ^ 1], sDa[buf ^ 1]);
+            __syncthreads();
+        }
+    }
+    if constexpr (!SUMS) {
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            const int m = m0 + 32 * (TM * wc + j) + c;
+            if (m >= M) continue;
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int n = n0 + 32 * (TN * wr + i) + 8 * q + 4 * h;
+                    float* o = dst + (size_t)m * ldd + n;
+                    if (vec_out && n + 3 < N) {
+                        *reinterpret_cast<float4*>(o) =
+                            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < N) o[e] = acc[i][j][4 * q + e];
+                    }
+                }
+        }
+    }
+}
+
+// Q4_0 / Q8_0 weights (MI355X layout), activations AMV_ACT_Q8_0_MMA of m rows. Tile: 128 x 128, or 64 x 64 when
+// the big tiles would leave CUs idle.
+int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
+              int64_t ldd, int32_t* sums, hipStream_t st) {
+    const int nb = (int)(k / 32);
+    const int64_t nblk = n_rows * nb;
+    const uint8_t* wq = (const uint8_t*)w;
+    const uint16_t* wd = (const uint16_t*)(wq + nblk * (wtype == AMV_T_Q4_0 ? 16 : 32));
+    const AmvQ80Mma L = amv_q8_0_mma_layout(m, k);
+    const uint16_t* a16 = (const uint16_t*)((const uint8_t*)act + L.a16);
+    const float* dT = (const float*)((const uint8_t*)act + L.dt);
+    const int vec_out = ((uintptr_t)dst & 15) == 0 && (ldd & 3) == 0;  // float4 stores of 4 consecutive rows
+    const auto grid = [&](int tn, int tm) {
+        return dim3((unsigned)((n_rows + 64 * tn - 1) / (64 * tn)), (unsigned)((m + 64 * tm - 1) / (64 * tm)));
+    };
+    const auto wgs = [&](int tn, int tm) { const dim3 g = grid(tn, tm); return (int64_t)g.x * g.y; };
+    // measured on MI355X: 128 x 128 tiles win from ~1.5 workgroups per CU (14336 x 4096 at 512 tokens: 448 of them,
+    // 177 us against 207 us for 896 tiles of 64 x 128); below that 64 x 64 tiles (4096 x 14336: 241 us against 311)
+    const int cfg = wgs(2, 2) >= 384 ? 22 : 11;
+#define G16_LAUNCH(WT, S, TN, TM)                                                                                     \
+    hipLaunchKernelGGL((k_mmq16<WT, S, TN, TM>), grid(TN, TM), dim3(256), 0, st, wq, wd, (int)n_rows, nb, a16, dT,    \
+                       (int)m, dst, ldd, sums, vec_out)
+#define G16_CFG(WT, S)                          \
+    if (cfg == 22) G16_LAUNCH(WT, S, 2, 2);     \
+    else if (cfg == 12) G16_LAUNCH(WT, S, 1, 2); \
+    else G16_LAUNCH(WT, S, 1, 1)
+    if (wtype == AMV_T_Q4_0) {
+        if (sums) { G16_CFG(AMV_T_Q4_0, true); } else { G16_CFG(AMV_T_Q4_0, false); }
+    } else {
+        if (sums) { G16_CFG(AMV_T_Q8_0, true); } else { G16_CFG(AMV_T_Q8_0, false); }
+    }
+#undef G16_CFG
+#undef G16_LAUNCH
+    return amv_check_launch("amv_mul_mat_q_act");
+}

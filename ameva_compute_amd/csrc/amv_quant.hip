@@ -8,9 +8,12 @@
 // ggml quantize_row_q8_0 (x86: id = 127/amax, round half even; ARM: id = 1/d, round half even; ref: id = 1/d,
 // roundf) -- the rules of ameva_act_fq.comp:5,38-41 and ameva_quant_a8.comp:46-54; d = amax/127 stored fp16.
 // ---------------------------------------------------------------------------------------------------------------
+// With a16 (AMV_ACT_Q8_0_MMA) the values also go out as f16 and the block scale transposed (row t = b / nbr, block
+// j = b % nbr at dt[j * m + t]).
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x, int64_t n_elem, int rule,
                                                    uint8_t* __restrict__ y_ggml, int8_t* __restrict__ aq,
-                                                   int2* __restrict__ ads) {
+                                                   int2* __restrict__ ads, uint16_t* __restrict__ a16,
+                                                   float* __restrict__ dt, int nbr, int m) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const bool live = i < n_elem;
     const float v = live ? x[i] : 0.0f;
@@ -41,6 +44,10 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x,
     if (aq) {
         aq[i] = (int8_t)q;
         if (j == 0) ads[b] = make_int2(__float_as_int(amv_h2f(d16)), s);
+    }
+    if (a16) {
+        a16[i] = __builtin_bit_cast(uint16_t, (_Float16)q);
+        if (j == 0) dt[(b % nbr) * m + b / nbr] = amv_h2f(d16);
     }
 }
 
@@ -302,14 +309,24 @@ extern "C" int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, 
     AMV_REQUIRE(((uintptr_t)x & 15) == 0, "amv_quantize_act: input must be 16-byte aligned");
     AMV_REQUIRE(y_act == nullptr || ((uintptr_t)y_act & 15) == 0, "amv_quantize_act: y_act must be 16-byte aligned");
     hipStream_t st = amv_stream(stream);
-    if (type == AMV_T_Q8_0) {
+    if (type == AMV_T_Q8_0 || type == AMV_ACT_Q8_0_MMA) {
         AMV_REQUIRE(k % 32 == 0, "amv_quantize_act: Q8_0 needs k %% 32 == 0 (k = %lld)", (long long)k);
         AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_quantize_act: bad rule %d", rule);
         AMV_REQUIRE(y_ggml == nullptr || ((uintptr_t)y_ggml & 1) == 0, "amv_quantize_act: y_ggml misaligned");
+        AMV_REQUIRE(type == AMV_T_Q8_0 || y_act, "amv_quantize_act: AMV_ACT_Q8_0_MMA needs y_act");
+        AMV_REQUIRE(m <= INT32_MAX && k / 32 <= INT32_MAX, "amv_quantize_act: shape too large");
         const int64_t n = m * k;
         int8_t* aq = y_act ? (int8_t*)y_act : nullptr;
         int2* ads = y_act ? (int2*)((uint8_t*)y_act + n) : nullptr;
-        hipLaunchKernelGGL(k_quant_q8_0, grid_for(n, 256), 256, 0, st, x, n, rule, (uint8_t*)y_ggml, aq, ads);
+        uint16_t* a16 = nullptr;
+        float* dt = nullptr;
+        if (type == AMV_ACT_Q8_0_MMA) {
+            const AmvQ80Mma L = amv_q8_0_mma_layout(m, k);
+            a16 = (uint16_t*)((uint8_t*)y_act + L.a16);
+            dt = (float*)((uint8_t*)y_act + L.dt);
+        }
+        hipLaunchKernelGGL(k_quant_q8_0, grid_for(n, 256), 256, 0, st, x, n, rule, (uint8_t*)y_ggml, aq, ads, a16,
+                           dt, (int)(k / 32), (int)m);
     } else if (type == AMV_T_Q8_K || type == AMV_ACT_Q8_K_MMA) {
         AMV_REQUIRE(k % 256 == 0, "amv_quantize_act: Q8_K needs k %% 256 == 0 (k = %lld)", (long long)k);
         AMV_REQUIRE(y_ggml == nullptr || ((uintptr_t)y_ggml & 3) == 0, "amv_quantize_act: y_ggml misaligned");

@@ -201,9 +201,13 @@ class LlamaLayer:
         n, pos0 = self.pf_n, self.pf_pos0
         b = self._prefill_buffers(n)
         H, kv, D, FF = self.H, self.kv, self.D, self.FF
-        mm = L.amv_mul_mat_q if (n >= ops.MMQ_MIN_M and self.wqkv.type in ops.MMQ_TYPES) else L.amv_mul_mat_vec
         P = lambda t: t.data_ptr()  # noqa: E731
         at = b["at"]
+        if n >= ops.MMQ_MIN_M and self.wqkv.type in ops.MMQ_TYPES:
+            def mm(wt, w, nr, k, act, m, dst, ldd, s):
+                return L.amv_mul_mat_q_act(wt, w, nr, k, act, at, m, dst, ldd, s)
+        else:
+            mm = L.amv_mul_mat_vec
         q8 = at == ops.Q8_0
 
         def quant(src, k, act):

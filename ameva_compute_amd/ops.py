@@ -37,14 +37,27 @@ def _need_gpu(t: torch.Tensor, what: str, contiguous: bool = True) -> None:
 
 # Q8_K activations with the f16 copies the batched Q4_K MUL_MAT reads (include/ameva_hip.h AMV_ACT_Q8_K_MMA)
 Q8_K_MMA = 1015
+Q8_0_MMA = 1008
 
 
 def act_type(wtype: int, m: int = 1) -> int:
-    """ggml vec_dot_type of a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants; for a batched Q4_K MUL_MAT
-    (m >= MMQ_MIN_M) the Q8_K layout extended for the matrix cores."""
+    """ggml vec_dot_type of a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants; for a batched MUL_MAT
+    (m >= MMQ_MIN_M) of Q4_K / Q4_0 / Q8_0 the layout extended with the f16 copies the matrix-core kernels read."""
     if wtype == Q4_K and m >= MMQ_MIN_M:
         return Q8_K_MMA
+    if wtype in (Q4_0, Q8_0) and m >= MMQ_MIN_M:
+        return Q8_0_MMA
     return Q8_K if wtype in (Q4_K, Q6_K) else Q8_0
+
+
+def act_layout(wtype: int, act: torch.Tensor, m: int, k: int) -> int:
+    """The activation type a buffer of m rows of k holds, told apart by its size (the extended layouts are larger)."""
+    n = act.numel() * act.element_size()
+    base = Q8_K if wtype in (Q4_K, Q6_K) else Q8_0
+    for t in ((Q8_K_MMA,) if base == Q8_K else (Q8_0_MMA,)) + (base,):
+        if n >= lib().amv_act_bytes(t, m, k) and (t == base or n == lib().amv_act_bytes(t, m, k)):
+            return t
+    return base
 
 
 def ggml_row_bytes(t: int, k: int) -> int:
@@ -94,7 +107,7 @@ def quantize_act(x: torch.Tensor, atype: int = Q8_0, rule: int = Q8_X86, ggml: b
     if n < 0:
         raise ValueError(f"quantize_act: type {atype} cannot hold rows of {k}")
     act = torch.empty(n, dtype=torch.uint8, device=x.device)
-    gt = Q8_K if atype == Q8_K_MMA else atype
+    gt = Q8_K if atype == Q8_K_MMA else Q8_0 if atype == Q8_0_MMA else atype
     g = torch.empty((m, ggml_row_bytes(gt, k)), dtype=torch.uint8, device=x.device) if ggml else None
     check(lib().amv_quantize_act(atype, x2.data_ptr(), m, k, rule, _ptr(g), act.data_ptr(), _stream()),
           "amv_quantize_act")
@@ -125,9 +138,13 @@ def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = 
     if out is None:
         out = torch.empty((m, w.n_rows), dtype=torch.float32, device=act.device)
     use_mmq = kernel == "mmq" or (kernel == "auto" and m >= MMQ_MIN_M and w.type in MMQ_TYPES)
-    fn = lib().amv_mul_mat_q if use_mmq else lib().amv_mul_mat_vec
-    check(fn(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(), w.n_rows, _stream()),
-          "amv_mul_mat_q" if use_mmq else "amv_mul_mat_vec")
+    if use_mmq:
+        check(lib().amv_mul_mat_q_act(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(),
+                                      act_layout(w.type, act, m, w.k), m, out.data_ptr(), w.n_rows, _stream()),
+              "amv_mul_mat_q_act")
+    else:
+        check(lib().amv_mul_mat_vec(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(),
+                                    w.n_rows, _stream()), "amv_mul_mat_vec")
     return out
 
 
@@ -229,9 +246,13 @@ def block_sums(w: QWeight, act: torch.Tensor, m: int, kernel: str = "mmv") -> to
     be = BLOCK[w.type][0]
     per = 2 if w.type == Q4_K else 1
     out = torch.empty((m, w.n_rows, w.k // be * per), dtype=torch.int32, device=act.device)
-    fn = lib().amv_mul_mat_q_block_sums if kernel == "mmq" else lib().amv_mul_mat_block_sums
-    check(fn(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(), _stream()),
-          "amv_mul_mat_block_sums")
+    if kernel == "mmq":
+        check(lib().amv_mul_mat_q_act_block_sums(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(),
+                                                 act_layout(w.type, act, m, w.k), m, out.data_ptr(), _stream()),
+              "amv_mul_mat_q_act_block_sums")
+    else:
+        check(lib().amv_mul_mat_block_sums(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m,
+                                           out.data_ptr(), _stream()), "amv_mul_mat_block_sums")
     return out
 
 

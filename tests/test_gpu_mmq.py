@@ -38,16 +38,21 @@ def weights(orc, rng, wtype, n, k):
     return orc.quantize_q4_0(wf) if wtype == 2 else orc.quantize_q8_0(wf, orc.Q8_REF)
 
 
+@pytest.mark.parametrize("atype", [8, 1008])
 @pytest.mark.parametrize("wtype", [2, 8])
-@pytest.mark.parametrize("m,n,k", [(8, 16, 32), (40, 200, 1024), (17, 129, 96), (128, 256, 4096), (512, 64, 14336)])
-def test_mmq_block_sums_and_output(dev, ops, orc, wtype, m, n, k):
+@pytest.mark.parametrize("m,n,k", [(8, 16, 32), (40, 200, 1024), (17, 129, 96), (128, 256, 4096), (512, 64, 14336),
+                                   (65, 129, 96), (300, 200, 1056), (130, 64, 32), (512, 1000, 4096)])
+def test_mmq_block_sums_and_output(dev, ops, orc, wtype, m, n, k, atype):
+    """Both kernels (int8 MFMA on plain Q8_0 activations; f16 MFMA on AMV_ACT_Q8_0_MMA for m > 64): the per-block
+    integers bit for bit and the f32 output within the bar, ragged rows / tokens / odd block counts included."""
     rng = np.random.default_rng(m * 1000 + n + k + wtype)
     wg = weights(orc, rng, wtype, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     a_ref = orc.quantize_q8_0(x, orc.Q8_X86)
     y_ref, s_ref = orc.mul_mat(wtype, wg, n, k, a_ref, m, with_blocks=True)
     w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, k)
-    act, _ = ops.quantize_act(gpu(x, dev), ops.Q8_0)
+    act, ag = ops.quantize_act(gpu(x, dev), atype, ggml=True)
+    assert np.array_equal(ag.cpu().numpy(), a_ref)  # the MMA layout's quantization is ggml's, byte for byte
     sums = ops.block_sums(w, act, m, kernel="mmq").cpu().numpy()
     assert np.array_equal(sums, s_ref)
     y = ops.mul_mat_q(w, act, m, kernel="mmq").cpu().numpy()
@@ -66,10 +71,13 @@ def test_mmq_full_size(dev, ops, orc, wtype):
         _, wg = ops.quantize_act(wf, ops.Q8_0, ops.Q8_REF, ggml=True)
     w = ops.QWeight.from_ggml(wtype, wg, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    act, ag = ops.quantize_act(gpu(x, dev), ops.Q8_0, ggml=True)
-    y = ops.mul_mat_q(w, act, m, kernel="mmq")
-    y_mmv = ops.mul_mat_q(w, act, m, kernel="mmv")
+    act, ag = ops.quantize_act(gpu(x, dev), ops.Q8_0_MMA, ggml=True)
+    y = ops.mul_mat_q(w, act, m, kernel="mmq")                   # f16 MFMA kernel (m > 64)
+    y_mmv = ops.mul_mat_q(w, act, m, kernel="mmv")               # the GEMV on the layout's Q8_0 prefix
     assert rel_l2(y.cpu().numpy(), y_mmv.cpu().numpy()) < 1e-5
+    act8, _ = ops.quantize_act(gpu(x, dev), ops.Q8_0)
+    y8 = ops.mul_mat_q(w, act8, m, kernel="mmq")                 # int8 MFMA kernel
+    assert rel_l2(y.cpu().numpy(), y8.cpu().numpy()) < 1e-5
     y_ref = orc.mul_mat(wtype, wg.cpu().numpy(), n, k, ag.cpu().numpy(), m)
     assert rel_l2(y.cpu().numpy(), y_ref) < TOL_F32
 
