@@ -465,9 +465,12 @@ static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const v
     return amv_check_launch("amv_mul_mat_q");
 }
 
-// amv_mmq16.hip: Q4_0 / Q8_0 on the f16 matrix cores (AMV_ACT_Q8_0_MMA activations)
+// amv_mmq16.hip: Q4_0 / Q8_0 (AMV_ACT_Q8_0_MMA activations) and Q4_K (AMV_ACT_Q8_K_MMA) on the f16 matrix cores with
+// LDS-staged tiles
 int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
               int64_t ldd, int32_t* sums, hipStream_t st);
+int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
+                  int32_t* sums, hipStream_t st);
 
 // Batches above this many tokens go to the f16 kernel (128-token tiles); smaller ones to the int8 kernel, which reads
 // the plain Q8_0 prefix of the same activation buffer.
@@ -475,13 +478,19 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
 
 static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
                         int act_type, int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream) {
-    if (act_type == AMV_ACT_Q8_0_MMA && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0) && m > MMQ16_MIN_M) {
+    const bool tiled = m > MMQ16_MIN_M && ((act_type == AMV_ACT_Q8_0_MMA && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
+                                           (act_type == AMV_ACT_Q8_K_MMA && wtype == AMV_T_Q4_K));
+    if (tiled) {
         AMV_REQUIRE(w && act && (dst || sums), "%s: null pointer", fn);
         AMV_REQUIRE(n_rows > 0 && k > 0 && k % 32 == 0, "%s: bad shape", fn);
         AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 128 && m * k <= INT32_MAX && n_rows * (k / 32) <= INT32_MAX,
                     "%s: too large", fn);
         AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "%s: buffers must be 16-byte aligned", fn);
         AMV_REQUIRE(!dst || ldd >= n_rows, "%s: ldd < n_rows", fn);
+        if (wtype == AMV_T_Q4_K) {
+            AMV_REQUIRE(k % 256 == 0, "%s: Q4_K needs k %% 256 == 0", fn);
+            return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
+        }
         return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
     }
     const bool ok = (act_type == AMV_T_Q8_0 || act_type == AMV_ACT_Q8_0_MMA) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)

@@ -271,3 +271,263 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
 #undef G16_LAUNCH
     return amv_check_launch("amv_mul_mat_q_act");
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Q4_K on the same tiling (reference ameva_mmqb.comp:11-16 for the integer form): per super-block j of 256 weights
+// I1 = sum_u sc_u dot(q_u, q_a) and I2 = sum_u m_u bsum_u (exact integers), dst += d_a (d I1 - dmin I2). The weight
+// operand is sc_u * q (<= 945, exact in f16) and the activation q_a (exact); a half super-block's 128 products stay
+// below 2^24, so the accumulator is folded into the f32 sum after each half (d_a d C), and I2 is one more MFMA of the
+// units' mins against the activation sums per 16 (AMV_ACT_Q8_K_MMA's f16 copies). Pipeline steps of one 64-weight
+// chunk (units 2c, 2c + 1: the low and high nibbles of 32 bytes); the per-super-block values (d, dmin, the mins,
+// the activation 16-sums and d_a) are staged at its first chunk into a slot of their own, double-buffered by
+// super-block parity.
+struct G16K {
+    uint4 q, hd, a0, a1, a2, a3, bs;
+    float da;
+};
+
+template <int TN, int TM>
+__device__ __forceinline__ void g16k_load(G16K& s, int step, const uint4* __restrict__ wq, const uint4* __restrict__ wh,
+                                          int N, int nsb, int n0, const uint16_t* __restrict__ a16,
+                                          const uint16_t* __restrict__ bs16, const float* __restrict__ dT, int M, int m0,
+                                          int K) {
+    constexpr int BN = 64 * TN, BM = 64 * TM;
+    const int t = threadIdx.x, hf = t & 1;
+    const int j = step >> 2, c = step & 3;
+    if (t < 2 * BN) {
+        const int row = min(n0 + (t >> 1), N - 1);
+        const size_t sb = (size_t)row * nsb + j;
+        s.q = wq[sb * 8 + 2 * c + hf];  // bytes 16 hf .. + 15 of chunk c
+        s.hd = wh[sb];
+    }
+    if (t < 2 * BM) {
+        const int tok = min(m0 + (t >> 1), M - 1);
+        const uint4* ap = reinterpret_cast<const uint4*>(a16 + (size_t)tok * K + 256 * j + 64 * c + 32 * hf);
+        s.a0 = ap[0];
+        s.a1 = ap[1];
+        s.a2 = ap[2];
+        s.a3 = ap[3];
+        if (c == 0) {
+            s.bs = *reinterpret_cast<const uint4*>(bs16 + (size_t)tok * (K / 16) + 16 * j + 8 * hf);
+            s.da = dT[(size_t)j * M + tok];
+        }
+    }
+}
+
+template <int TN, int TM>
+__device__ __forceinline__ void g16k_store(const G16K& s, int step, uint16_t* __restrict__ sA, uint16_t* __restrict__ sB,
+                                           float* __restrict__ sD, float* __restrict__ sDm, uint16_t* __restrict__ sMn,
+                                           uint16_t* __restrict__ sBs, float* __restrict__ sDa) {
+    constexpr int BN = 64 * TN, BM = 64 * TM;
+    const int t = threadIdx.x, hf = t & 1, c = step & 3;
+    if (t < 2 * BN) {
+        const int rl = t >> 1;
+        int sc0, m0u, sc1, m1u;
+        k4_scale_min(2 * c, s.hd.y, s.hd.z, s.hd.w, sc0, m0u);
+        k4_scale_min(2 * c + 1, s.hd.y, s.hd.z, s.hd.w, sc1, m1u);
+        const g16_h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const g16_h2 f0 = {(_Float16)(float)sc0, (_Float16)(float)sc0}, f1 = {(_Float16)(float)sc1, (_Float16)(float)sc1};
+        const uint32_t wv[4] = {s.q.x, s.q.y, s.q.z, s.q.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // element 16 hf + 4 i + e of unit 2c (low nibble) and 2c + 1 (high nibble)
+            const uint2 l = g16_nib4(wv[i] & 0x0F0F0F0Fu, off), h = g16_nib4((wv[i] >> 4) & 0x0F0F0F0Fu, off);
+            lo[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, l.x) * f0);
+            lo[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, l.y) * f0);
+            hi[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, h.x) * f1);
+            hi[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, h.y) * f1);
+        }
+        uint4* dl = reinterpret_cast<uint4*>(sA + rl * G16_LDK + 16 * hf);
+        uint4* dh = reinterpret_cast<uint4*>(sA + rl * G16_LDK + 32 + 16 * hf);
+        dl[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        dl[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+        dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+        if (c == 0) {  // per super-block: d, dmin, and the mins of units 4 hf .. 4 hf + 3 on their 16-sum slots
+            if (hf == 0) {
+                sD[rl] = amv_h2f(s.hd.x);
+                sDm[rl] = amv_h2f(s.hd.x >> 16);
+            }
+            uint32_t mm[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                int scx, mx;
+                k4_scale_min(4 * hf + e, s.hd.y, s.hd.z, s.hd.w, scx, mx);
+                const uint32_t hb = __builtin_bit_cast(uint16_t, (_Float16)(float)mx);
+                mm[e] = hb | (hb << 16);  // slots 2 u, 2 u + 1 (the unit's two 16-sums)
+            }
+            *reinterpret_cast<uint4*>(sMn + rl * 16 + 8 * hf) = make_uint4(mm[0], mm[1], mm[2], mm[3]);
+        }
+    }
+    if (t < 2 * BM) {
+        const int tl = t >> 1;
+        uint4* bd = reinterpret_cast<uint4*>(sB + tl * G16_LDK + 32 * hf);
+        bd[0] = s.a0;
+        bd[1] = s.a1;
+        bd[2] = s.a2;
+        bd[3] = s.a3;
+        if (c == 0) {
+            *reinterpret_cast<uint4*>(sBs + tl * 16 + 8 * hf) = s.bs;
+            if (hf == 0) sDa[tl] = s.da;
+        }
+    }
+}
+
+template <bool SUMS, int TN, int TM>
+__global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
+                                                  int nsb, const uint16_t* __restrict__ a16,
+                                                  const uint16_t* __restrict__ bs16, const float* __restrict__ dT,
+                                                  int M, float* __restrict__ dst, int64_t ldd,
+                                                  int32_t* __restrict__ sums, int vec_out) {
+    constexpr int BN = 64 * TN, BM = 64 * TM;
+    __shared__ __align__(16) uint16_t sA[2][BN * G16_LDK];
+    __shared__ __align__(16) uint16_t sB[2][BM * G16_LDK];
+    __shared__ __align__(16) float sD[2][BN], sDm[2][BN], sDa[2][BM];
+    __shared__ __align__(16) uint16_t sMn[2][BN * 16], sBs[2][BM * 16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wr = w & 1, wc = w >> 1, c32 = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int K = nsb * 256;
+    const int nsteps = nsb * 4;
+
+    g16_f16v acc[TN][TM], C[TN][TM];
+    g16_f16v C0[TN][TM];  // SUMS: the first half's exact integers
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TM; ++jj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][jj][r] = C[i][jj][r] = C0[i][jj][r] = 0.0f;
+
+    G16K st;
+    g16k_load<TN, TM>(st, 0, wq, wh, N, nsb, n0, a16, bs16, dT, M, m0, K);
+    g16k_store<TN, TM>(st, 0, sA[0], sB[0], sD[0], sDm[0], sMn[0], sBs[0], sDa[0]);
+    __syncthreads();
+    for (int step = 0; step < nsteps; ++step) {
+        const int buf = step & 1, j = step >> 2, c = step & 3, jp = j & 1;
+        if (step + 1 < nsteps) g16k_load<TN, TM>(st, step + 1, wq, wh, N, nsb, n0, a16, bs16, dT, M, m0, K);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int kk = 16 * ks + 8 * h;
+            g16_h8 A[TN], B[TM];
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+                A[i] = *reinterpret_cast<const g16_h8*>(sA[buf] + (32 * (TN * wr + i) + c32) * G16_LDK + kk);
+#pragma unroll
+            for (int jj = 0; jj < TM; ++jj)
+                B[jj] = *reinterpret_cast<const g16_h8*>(sB[buf] + (32 * (TM * wc + jj) + c32) * G16_LDK + kk);
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int jj = 0; jj < TM; ++jj)
+                    C[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[jj], C[i][jj], 0, 0, 0);
+        }
+        if (c == 1 || c == 3) {
+            // fold the half super-block (and at its end I2, the mins against the activation 16-sums), tile by tile
+#pragma unroll
+            for (int jj = 0; jj < TM; ++jj) {
+                const int tl = 32 * (TM * wc + jj) + c32;
+                const float da = sDa[jp][tl];
+                const g16_h8 Bs = *reinterpret_cast<const g16_h8*>(sBs[jp] + tl * 16 + 8 * h);
+#pragma unroll
+                for (int i = 0; i < TN; ++i) {
+                    g16_f16v I2;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) I2[r] = 0.0f;
+                    if (c == 3) {
+                        const g16_h8 Am =
+                            *reinterpret_cast<const g16_h8*>(sMn[jp] + (32 * (TN * wr + i) + c32) * 16 + 8 * h);
+                        I2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(Am, Bs, I2, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int rl = 32 * (TN * wr + i) + 8 * q + 4 * h;
+                        const float4 d4 = *reinterpret_cast<const float4*>(&sD[jp][rl]);
+                        const float4 dm4 = *reinterpret_cast<const float4*>(&sDm[jp][rl]);
+                        const float dv[4] = {d4.x, d4.y, d4.z, d4.w}, dmv[4] = {dm4.x, dm4.y, dm4.z, dm4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = 4 * q + e;
+                            if constexpr (SUMS) {
+                                if (c == 1) {
+                                    C0[i][jj][r] = C[i][jj][r];
+                                } else {
+                                    const int m = m0 + tl, n = n0 + rl + e;
+                                    if (m < M && n < N) {
+                                        int32_t* o = sums + (((size_t)m * N + n) * nsb + j) * 2;
+                                        o[0] = (int)C0[i][jj][r] + (int)C[i][jj][r];
+                                        o[1] = (int)I2[r];
+                                    }
+                                }
+                            } else if (c == 1) {
+                                acc[i][jj][r] = fmaf(C[i][jj][r] * dv[e], da, acc[i][jj][r]);
+                            } else {
+                                acc[i][jj][r] = fmaf(fmaf(dv[e], C[i][jj][r], -dmv[e] * I2[r]), da, acc[i][jj][r]);
+                            }
+                            C[i][jj][r] = 0.0f;
+                        }
+                    }
+                }
+            }
+        }
+        if (step + 1 < nsteps) {
+            const int sp = ((step + 1) >> 2) & 1;  // per-super-block slot of the next step
+            g16k_store<TN, TM>(st, step + 1, sA[buf ^ 1], sB[buf ^ 1], sD[sp], sDm[sp], sMn[sp], sBs[sp], sDa[sp]);
+            __syncthreads();
+        }
+    }
+    if constexpr (!SUMS) {
+#pragma unroll
+        for (int jj = 0; jj < TM; ++jj) {
+            const int m = m0 + 32 * (TM * wc + jj) + c32;
+            if (m >= M) continue;
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int n = n0 + 32 * (TN * wr + i) + 8 * q + 4 * h;
+                    float* o = dst + (size_t)m * ldd + n;
+                    if (vec_out && n + 3 < N) {
+                        *reinterpret_cast<float4*>(o) = make_float4(acc[i][jj][4 * q], acc[i][jj][4 * q + 1],
+                                                                    acc[i][jj][4 * q + 2], acc[i][jj][4 * q + 3]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < N) o[e] = acc[i][jj][4 * q + e];
+                    }
+                }
+        }
+    }
+}
+
+// Q4_K weights (MI355X layout: qs [N][K/256][128] | head [N][K/256][16]), activations AMV_ACT_Q8_K_MMA of m rows
+int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
+                  int32_t* sums, hipStream_t st) {
+    const int nsb = (int)(k / 256);
+    const int64_t nblk = n_rows * nsb;
+    const uint4* wq = (const uint4*)w;
+    const uint4* wh = (const uint4*)((const uint8_t*)w + nblk * 128);
+    const AmvQ8kMma L = amv_q8k_mma_layout(m, k);
+    const uint16_t* a16 = (const uint16_t*)((const uint8_t*)act + L.a16);
+    const uint16_t* bs16 = (const uint16_t*)((const uint8_t*)act + L.bs16);
+    const float* dT = (const float*)((const uint8_t*)act + L.dt);
+    const int vec_out = ((uintptr_t)dst & 15) == 0 && (ldd & 3) == 0;
+    const auto grid = [&](int tn, int tm) {
+        return dim3((unsigned)((n_rows + 64 * tn - 1) / (64 * tn)), (unsigned)((m + 64 * tm - 1) / (64 * tm)));
+    };
+    // Tile by measurement on 28672/14336/6144/4096 x 4096 and 4096 x 14336 at m = 128, 512: the 64 x 128 tile
+    // (occupancy 2) wins once it fills 448 workgroups, else 64 x 64 (occupancy 3); the 128 x 128 tile holds 256 VGPRs
+    // + 123 AGPRs at occupancy 1 and lost to both everywhere.
+    const int cfg = (int64_t)grid(1, 2).x * grid(1, 2).y >= 448 ? 12 : 11;
+#define G16K_LAUNCH(S, TN, TM)                                                                                        \
+    hipLaunchKernelGGL((k_mmq16_q4k<S, TN, TM>), grid(TN, TM), dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, \
+                       dT, (int)m, dst, ldd, sums, vec_out)
+    if (sums) {  // instrumentation: the small tile (two accumulator sets fit its registers)
+        G16K_LAUNCH(true, 1, 1);
+    } else {
+        if (cfg == 12) G16K_LAUNCH(false, 1, 2);
+        else G16K_LAUNCH(false, 1, 1);
+    }
+#undef G16K_LAUNCH
+    return amv_check_launch("amv_mul_mat_q_act");
+}

@@ -106,7 +106,8 @@ def random_q4k(rng, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(8, 64, 256), (16, 300, 1024), (70, 129, 512), (512, 256, 4096),
-                                   (512, 64, 14336), (130, 14336 // 8, 4096)])
+                                   (512, 64, 14336), (130, 14336 // 8, 4096), (300, 200, 768), (65, 64, 256),
+                                   (512, 2048, 4096)])
 def test_mmq_q4k_block_sums_and_output(dev, ops, orc, m, n, k):
     """Batched Q4_K on the f16 matrix cores: the per-super-block integers (sum sc * dot, sum m * bsum) bit-exact
     against the oracle, f32 within 1e-3; the Q8_K prefix of the extended activations is the plain Q8_K layout."""
