@@ -475,11 +475,12 @@ struct Engine {
         const ggml_tensor *w = n->src[0], *x = n->src[1];
         const int64_t N = w->ne[1], K = w->ne[0], M = nrows(x);
         // batched (M >= 8) MUL_MATs run on the matrix cores for Q4_0 / Q8_0 / Q4_K (the reference's switch at
-        // AMEVA_QGEMM_MIN_M); batched Q4_K reads the Q8_K activations extended with their f16 copies
+        // AMEVA_QGEMM_MIN_M); they read the Q8_0 / Q8_K activations extended with the f16 copies the tiled kernels
+        // stage (the plain layout is the prefix of the extended one)
         const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K);
-        const int atype = (w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K)
-                              ? (mmq && w->type == GGML_TYPE_Q4_K ? AMV_ACT_Q8_K_MMA : (int)GGML_TYPE_Q8_K)
-                              : (int)GGML_TYPE_Q8_0;
+        const bool kq = w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K;
+        const int atype = kq ? (mmq ? AMV_ACT_Q8_K_MMA : (int)GGML_TYPE_Q8_K)
+                             : (mmq ? AMV_ACT_Q8_0_MMA : (int)GGML_TYPE_Q8_0);
         // src0 in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized tensor of any
         // other buffer is repacked into scratch for this use
         const void* wp = w->data;
@@ -516,7 +517,7 @@ struct Engine {
             r = amv_mul_mat_vec_ep(w->type, wp, N, K, act, (float*)n->data, mode, (const float*)e->data,
                                    (float*)ep->data, st);
         } else {
-            r = mmq ? amv_mul_mat_q(w->type, wp, N, K, act, M, (float*)n->data, N, st)
+            r = mmq ? amv_mul_mat_q_act(w->type, wp, N, K, act, atype, M, (float*)n->data, N, st)
                     : amv_mul_mat_vec(w->type, wp, N, K, act, M, (float*)n->data, N, st);
         }
         if (!rc(n, r)) return false;
@@ -614,7 +615,7 @@ struct Engine {
         for (int i = 0; i < g->n_nodes; ++i) {
             const ggml_tensor* n = g->nodes[i];
             if (n->op == GGML_OP_MUL_MAT) {
-                s += (size_t)amv_act_bytes(GGML_TYPE_Q8_0, nrows(n->src[1]), n->src[1]->ne[0]) + 4096;
+                s += (size_t)amv_act_bytes(AMV_ACT_Q8_0_MMA, nrows(n->src[1]), n->src[1]->ne[0]) + 4096;
                 s += (size_t)amv_act_bytes(AMV_ACT_Q8_K_MMA, nrows(n->src[1]), (n->src[1]->ne[0] + 255) / 256 * 256) + 4096;
                 if (n->src[0]->buffer->usage != GGML_BACKEND_BUFFER_USAGE_WEIGHTS) s += nbytes(n->src[0]) + 256;
             } else if (n->op == GGML_OP_FLASH_ATTN_EXT) {

@@ -44,7 +44,7 @@ def random_kquant(rng, t, n, k):
 
 
 @pytest.mark.parametrize("wt", [gp.Q4_0, gp.Q8_0, gp.Q4_K, gp.Q6_K])
-@pytest.mark.parametrize("m", [1, 16])
+@pytest.mark.parametrize("m", [1, 16, 100])
 def test_mul_mat_node(plugin, orc, wt, m):
     rng = np.random.default_rng(wt * 10 + m)
     n, k = 512, 4096
