@@ -52,6 +52,8 @@ def build(verbose: bool = False) -> str:
         os.remove(o)
     build_plugin()
     build_amuda()
+    build_runtime()
+    build_test_kernels()
     return LIB
 
 
@@ -93,6 +95,40 @@ def build_amuda() -> str:
         raise RuntimeError("hipcc failed on amuda_hip.cpp")
     os.replace(tmp, AMUDA)
     return AMUDA
+
+
+RUNTIME = os.path.join(HERE, "libac_runtime_hip.so")
+
+
+def build_runtime() -> str:
+    """libac_runtime_hip.so: the ac_runtime C ABI (include/ac_runtime_hip.h) on HIP (host code only)."""
+    src = os.path.join(CSRC, "ac_runtime_hip.cpp")
+    tmp = RUNTIME + ".tmp"
+    cmd = [HIPCC, *FLAGS, "-shared", "-o", tmp, src]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed on ac_runtime_hip.cpp")
+    os.replace(tmp, RUNTIME)
+    return RUNTIME
+
+
+TEST_KERNELS = os.path.join(os.path.dirname(HERE), "tests", "ac_kernels", "ac_test_kernels.hip")
+
+
+def build_test_kernels() -> str:
+    """The gfx950 code object the ac_runtime tests load (tests/ac_kernels/ac_test_kernels.hsaco)."""
+    out = TEST_KERNELS[:-4] + ".hsaco"
+    if not os.path.exists(TEST_KERNELS):  # a package installed without its tests
+        return ""
+    cmd = [HIPCC, "--genco", "--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-Xclang", "-target-feature",
+           "-Xclang", "-packed-fp32-ops", "-o", out + ".tmp", TEST_KERNELS]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc --genco failed on ac_test_kernels.hip")
+    os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":
