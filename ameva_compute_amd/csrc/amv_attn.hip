@@ -1,9 +1,12 @@
-// FLASH_ATTN_EXT for decode (one query position) over an f16 KV cache, split along the sequence (flash decoding).
+// FLASH_ATTN_EXT for decode (one query position) over an f16, Q8_0 or Q4_0 KV cache, split along the sequence
+// (flash decoding).
 //
 // Role of ameva_flash_attn.comp (split_keys > 0) + ameva_fa_combine.comp (reference): softmax(scale * q k^T + mask) v
 // per head; head h reads KV head h / G (G = n_head / n_head_kv), and the G query heads of a KV head share every K and
-// V load. ggml's CPU kernel rounds q to f16 before the dot with f16 K; so does this one. Scores, probabilities and
-// accumulators are f32.
+// V load. q meets K the way ggml's CPU kernel makes it: rounded to f16 for an f16 cache; for a Q8_0 / Q4_0 cache
+// quantized to Q8_0 (K's vec_dot_type, with the chosen rounding rule) and dotted in exact integers per 32-block,
+// score = sum_b float(isum_b) * (d_k * d_q) (vec_dot_q8_0_q8_0 / vec_dot_q4_0_q8_0). A quantized V row is dequantized
+// exactly (q * d). Scores, probabilities and accumulators are f32.
 //
 // Pass 1 (k_fa_split): one workgroup of 4 waves per (key split, KV head); each wave owns KPW consecutive keys and
 // works alone (16 lanes per 256-byte K/V row, G partial dots reduced over the 16 lanes, wave maximum, probabilities
@@ -137,12 +140,73 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
 // maximum, probabilities, l and P V stay in registers. The 4 wave partials are merged once through LDS.
 // The key count is read from n_kv_dev when given (capped at the launch's n_kv); splits past it do nothing. FUSED: the
 // last workgroup of each KV head to arrive merges the head's splits (fa_merge).
-template <int G, int KPW, bool FUSED>
-__global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, const uint16_t* __restrict__ k,
-                                                 const uint16_t* __restrict__ v, const uint16_t* __restrict__ mask,
+// cache element types of the split kernel
+#define FA_F16 0
+#define FA_Q8_0 1
+#define FA_Q4_0 2
+
+// The slice of one K / V row a lane works on: lane l16 (0..15 of its 16-lane group) owns elements 8 l16 .. 8 l16 + 7.
+// f16: those 16 bytes. Q8_0 / Q4_0 (ggml blocks of 34 / 18 bytes): element offset o = 8 (l16 & 3) in block l16 / 4;
+// .x, .y = the 8 int8 (Q8_0) or the 8 qs bytes whose low (o < 16) or high (o >= 16) nibbles are the elements (Q4_0),
+// .z = the block's fp16 d. Quantized rows need only 2-byte alignment (halfword loads).
+template <int KT>
+__device__ __forceinline__ uint4 fa_row(const uint8_t* __restrict__ row, int l16) {
+    if constexpr (KT == FA_F16) {
+        return *reinterpret_cast<const uint4*>(row + 16 * l16);
+    } else {
+        constexpr int BB = KT == FA_Q8_0 ? 34 : 18;
+        const int o = 8 * (l16 & 3);
+        const uint16_t* bp = reinterpret_cast<const uint16_t*>(row + BB * (l16 >> 2));
+        const int h = KT == FA_Q8_0 ? 1 + (o >> 1) : 1 + ((o & 15) >> 1);
+        const uint32_t b0 = bp[h], b1 = bp[h + 1], b2 = bp[h + 2], b3 = bp[h + 3];
+        return make_uint4(b0 | (b1 << 16), b2 | (b3 << 16), bp[0], 0u);
+    }
+}
+
+// The 8 elements of a quantized slice as signed bytes (Q4_0: the nibbles, not yet offset by -8).
+template <int KT>
+__device__ __forceinline__ uint2 fa_bytes(uint4 r, int lane) {
+    if constexpr (KT == FA_Q4_0) {
+        const int sh = (lane & 3) >= 2 ? 4 : 0;
+        return make_uint2((r.x >> sh) & 0x0F0F0F0Fu, (r.y >> sh) & 0x0F0F0F0Fu);
+    } else {
+        return make_uint2(r.x, r.y);
+    }
+}
+
+// Q8_0 of q for a quantized K: the 32-block of a lane's 8 elements spans the 4 lanes l16 = 4 b .. 4 b + 3; rules of
+// amv_quantize_act (ggml quantize_row_q8_0). qq: the lane's 8 int8, dq: the block's fp16-rounded d, qs: the sum of
+// the lane's 8 q.
+__device__ __forceinline__ void fa_quant_q(const float (&x)[8], int rule, uint32_t (&qq)[2], float& dq, int& qs) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, AMV_WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, AMV_WAVE));
+    const float d = amax / 127.0f;
+    float id;
+    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else id = d != 0.0f ? 1.0f / d : 0.0f;
+    qq[0] = qq[1] = 0u;
+    qs = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float t = x[e] * id;
+        float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+        qf = fminf(127.0f, fmaxf(-127.0f, qf));
+        const int qi = (int)qf;
+        qs += qi;
+        qq[e >> 2] |= (uint32_t)(qi & 0xFF) << (8 * (e & 3));
+    }
+    dq = amv_h2f(amv_f2h(d));
+}
+
+template <int G, int KPW, bool FUSED, int KT>
+__global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, const uint8_t* __restrict__ k,
+                                                 const uint8_t* __restrict__ v, const uint16_t* __restrict__ mask,
                                                  float* part, int n_kv_max, const int* __restrict__ n_kv_dev,
                                                  int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
-                                                 int n_split, float scale, unsigned int* counters,
+                                                 int n_split, float scale, int qrule, unsigned int* counters,
                                                  float* __restrict__ out, const AmvActOut act) {
     constexpr int U = KPW / 4;
     constexpr int SBUF = 4 * 4 * G * FA_D > G * (8 * FA_D + FA_MAX_NSPLIT + 1) ? 4 * 4 * G * FA_D
@@ -158,48 +222,70 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
 
     if (split < ns) {
         const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
-        const uint16_t* kh = k + (size_t)hk * k_head;
-        const uint16_t* vh = v + (size_t)hk * v_head;
+        const uint8_t* kh = k + (size_t)hk * k_head;
+        const uint8_t* vh = v + (size_t)hk * v_head;
         uint4 kr[U], vr[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = min(kw0 + 4 * u + grp, n_kv - 1);
-            kr[u] = *reinterpret_cast<const uint4*>(kh + (size_t)i * k_row + d8);
+            kr[u] = fa_row<KT>(kh + (size_t)i * k_row, lane & 15);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = min(kw0 + 4 * u + grp, n_kv - 1);
-            vr[u] = *reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + d8);
+            vr[u] = fa_row<KT>(vh + (size_t)i * v_row, lane & 15);
         }
-        // q of the G heads, 8 dims per lane, rounded to f16 as ggml does
+        // q of the G heads, 8 dims per lane: rounded to f16 for an f16 cache, else quantized to Q8_0 blocks
         float qv[G][8];
+        uint32_t qq[G][2];
+        float qd[G];
+        int qsum[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float4* qp = reinterpret_cast<const float4*>(q + (size_t)(hk * G + g) * FA_D + d8);
             const float4 a = qp[0], b = qp[1];
             const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qv[g][e] = amv_round_f16(t[e]);
+            for (int e = 0; e < 8; ++e) qv[g][e] = KT == FA_F16 ? amv_round_f16(t[e]) : t[e];
+            if constexpr (KT != FA_F16) fa_quant_q(qv[g], qrule, qq[g], qd[g], qsum[g]);
         }
         float s[U][G];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-            float kf[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kf[2 * e] = amv_h2f(kw[e] & 0xFFFFu);
-                kf[2 * e + 1] = amv_h2f(kw[e] >> 16);
-            }
             const int i = kw0 + 4 * u + grp;
             const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
+            if constexpr (KT == FA_F16) {
+                const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+                float kf[8];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float d = 0.0f;
+                for (int e = 0; e < 4; ++e) {
+                    kf[2 * e] = amv_h2f(kw[e] & 0xFFFFu);
+                    kf[2 * e + 1] = amv_h2f(kw[e] >> 16);
+                }
 #pragma unroll
-                for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
-                d = amv_row16_sum(d);
-                s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
+                for (int g = 0; g < G; ++g) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
+                    d = amv_row16_sum(d);
+                    s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
+                }
+            } else {
+                const uint2 kb = fa_bytes<KT>(kr[u], lane);
+                const float dk = amv_h2f((uint16_t)kr[u].z);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    int is = amv_dot4((int)kb.x, (int)qq[g][0], amv_dot4((int)kb.y, (int)qq[g][1], 0));
+                    if constexpr (KT == FA_Q4_0) is -= 8 * qsum[g];
+                    is += __shfl_xor(is, 1, AMV_WAVE);  // the block's exact integer sum in its 4 lanes
+                    is += __shfl_xor(is, 2, AMV_WAVE);
+                    // vec_dot_q8_0_q8_0: isum * (d_k * d_q); vec_dot_q4_0_q8_0: (isum * d_k) * d_q
+                    const float t = (lane & 3) != 0         ? 0.0f
+                                    : KT == FA_Q8_0 ? (float)is * (dk * qd[g])
+                                                    : ((float)is * dk) * qd[g];
+                    const float d = amv_row16_sum(t);
+                    s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
+                }
             }
         }
         float m[G], l[G];
@@ -229,12 +315,24 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
             for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
             float vf[8];
+            if constexpr (KT == FA_F16) {
+                const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
-                vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+                for (int e = 0; e < 4; ++e) {
+                    vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
+                    vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+                }
+            } else {  // ggml dequantize_row_q8_0 / q4_0: q * d, (nibble - 8) * d
+                const uint2 vb = fa_bytes<KT>(vr[u], lane);
+                const float dv = amv_h2f((uint16_t)vr[u].z);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int lo = KT == FA_Q8_0 ? (int)(int8_t)(vb.x >> (8 * e)) : (int)((vb.x >> (8 * e)) & 0xFF) - 8;
+                    const int hi = KT == FA_Q8_0 ? (int)(int8_t)(vb.y >> (8 * e)) : (int)((vb.y >> (8 * e)) & 0xFF) - 8;
+                    vf[e] = (float)lo * dv;
+                    vf[4 + e] = (float)hi * dv;
+                }
             }
 #pragma unroll
             for (int g = 0; g < G; ++g)
@@ -314,10 +412,12 @@ extern "C" int64_t amv_flash_attn_workspace_bytes(int64_t n_head, int64_t n_head
     return n_head * n_split * FA_PS * 4;
 }
 
-static int fa_check(const char* fn, const float* q, const void* k, const void* v, const float* out, const void* ws,
-                    const void* act, int rule, int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D,
-                    int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int64_t workspace_bytes) {
+// K / V strides in bytes; kv: AMV_T_F16, AMV_T_Q8_0 or AMV_T_Q4_0 (both caches)
+static int fa_check(const char* fn, int kv, const float* q, const void* k, const void* v, const float* out,
+                    const void* ws, const void* act, int rule, int64_t n_head, int64_t n_head_kv, int64_t n_kv,
+                    int64_t D, int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int64_t workspace_bytes) {
     AMV_REQUIRE(q && k && v && out && ws, "%s: null pointer", fn);
+    AMV_REQUIRE(kv == AMV_T_F16 || kv == AMV_T_Q8_0 || kv == AMV_T_Q4_0, "%s: KV type %d (F16, Q8_0 or Q4_0)", fn, kv);
     AMV_REQUIRE(!act || ((uintptr_t)act & 15) == 0, "%s: act must be 16-byte aligned", fn);
     AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "%s: bad rule", fn);
     AMV_REQUIRE(D == FA_D, "%s: head size %lld not supported (128 is)", fn, (long long)D);
@@ -326,26 +426,36 @@ static int fa_check(const char* fn, const float* q, const void* k, const void* v
     AMV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "%s: GQA group %lld not supported", fn, (long long)G);
     AMV_REQUIRE(n_kv > 0 && n_kv <= 128LL * FA_MAX_NSPLIT, "%s: n_kv %lld out of range", fn, (long long)n_kv);
     AMV_REQUIRE(n_head_kv <= 65535, "%s: too many KV heads", fn);
-    AMV_REQUIRE(k_row >= D && v_row >= D && k_row % 8 == 0 && v_row % 8 == 0 && k_head % 8 == 0 && v_head % 8 == 0 &&
-                    k_head >= 0 && v_head >= 0,
-                "%s: K/V strides must be >= D and multiples of 8 elements", fn);
-    AMV_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 &&
-                    ((uintptr_t)ws & 15) == 0,
-                "%s: buffers must be 16-byte aligned", fn);
+    AMV_REQUIRE(k_head >= 0 && v_head >= 0, "%s: negative head stride", fn);
+    if (kv == AMV_T_F16) {
+        AMV_REQUIRE(k_row >= 2 * D && v_row >= 2 * D && k_row % 16 == 0 && v_row % 16 == 0 && k_head % 16 == 0 &&
+                        v_head % 16 == 0,
+                    "%s: f16 K/V strides must be >= D and multiples of 8 elements", fn);
+        AMV_REQUIRE(((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0, "%s: f16 K/V must be 16-byte aligned", fn);
+    } else {
+        const int64_t rb = D / 32 * (kv == AMV_T_Q8_0 ? 34 : 18);
+        AMV_REQUIRE(k_row >= rb && v_row >= rb && k_row % 2 == 0 && v_row % 2 == 0 && k_head % 2 == 0 &&
+                        v_head % 2 == 0,
+                    "%s: quantized K/V rows must hold %lld bytes, even strides", fn, (long long)rb);
+        AMV_REQUIRE(((uintptr_t)k & 1) == 0 && ((uintptr_t)v & 1) == 0, "%s: quantized K/V must be 2-byte aligned",
+                    fn);
+    }
+    AMV_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)ws & 15) == 0, "%s: q and workspace must be 16-byte aligned",
+                fn);
     const int64_t need = amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv, D);
     AMV_REQUIRE(workspace_bytes >= need, "%s: workspace %lld < %lld bytes", fn, (long long)workspace_bytes,
                 (long long)need);
     return AMV_OK;
 }
 
-template <bool FUSED>
-static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const float* q, const uint16_t* kk,
-                            const uint16_t* vv, const uint16_t* mm, float* part, int n_kv, const int* n_kv_dev,
+template <bool FUSED, int KT>
+static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const float* q, const uint8_t* kk,
+                            const uint8_t* vv, const uint16_t* mm, float* part, int n_kv, const int* n_kv_dev,
                             int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int n_split, float scale,
-                            unsigned int* counters, float* out, const AmvActOut& act) {
+                            int rule, unsigned int* counters, float* out, const AmvActOut& act) {
 #define FA_LAUNCH(GG, KK)                                                                                              \
-    hipLaunchKernelGGL((k_fa_split<GG, KK, FUSED>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev,      \
-                       k_row, k_head, v_row, v_head, n_split, scale, counters, out, act)
+    hipLaunchKernelGGL((k_fa_split<GG, KK, FUSED, KT>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev, \
+                       k_row, k_head, v_row, v_head, n_split, scale, rule, counters, out, act)
 #define FA_G(GG)                     \
     if (kpw == 16) FA_LAUNCH(GG, 16); \
     else FA_LAUNCH(GG, 32)
@@ -359,13 +469,30 @@ static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const flo
 #undef FA_LAUNCH
 }
 
-// split + merge; counters == NULL: the merge as a second launch, else in the split launch's last workgroups
-static int fa_run(const char* fn, const float* q, const void* k, const void* v, const void* mask, float* out,
+template <bool FUSED>
+static void fa_launch_kv(int kv, int G, int kpw, dim3 grid, hipStream_t st, const float* q, const uint8_t* kk,
+                         const uint8_t* vv, const uint16_t* mm, float* part, int n_kv, const int* n_kv_dev,
+                         int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int n_split, float scale,
+                         int rule, unsigned int* counters, float* out, const AmvActOut& act) {
+    if (kv == AMV_T_Q8_0)
+        fa_launch_split<FUSED, FA_Q8_0>(G, kpw, grid, st, q, kk, vv, mm, part, n_kv, n_kv_dev, k_row, k_head, v_row,
+                                        v_head, n_split, scale, rule, counters, out, act);
+    else if (kv == AMV_T_Q4_0)
+        fa_launch_split<FUSED, FA_Q4_0>(G, kpw, grid, st, q, kk, vv, mm, part, n_kv, n_kv_dev, k_row, k_head, v_row,
+                                        v_head, n_split, scale, rule, counters, out, act);
+    else
+        fa_launch_split<FUSED, FA_F16>(G, kpw, grid, st, q, kk, vv, mm, part, n_kv, n_kv_dev, k_row, k_head, v_row,
+                                       v_head, n_split, scale, rule, counters, out, act);
+}
+
+// split + merge; counters == NULL: the merge as a second launch, else in the split launch's last workgroups.
+// K / V strides in bytes.
+static int fa_run(const char* fn, int kv, const float* q, const void* k, const void* v, const void* mask, float* out,
                   int64_t n_head, int64_t n_head_kv, int64_t n_kv_max, const int32_t* n_kv_dev, int64_t D,
                   int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, float scale, void* workspace,
                   int64_t workspace_bytes, unsigned int* counters, void* act, int act_type, int rule, void* stream) {
-    int rc = fa_check(fn, q, k, v, out, workspace, act, rule, n_head, n_head_kv, n_kv_max, D, k_row, k_head, v_row,
-                      v_head, workspace_bytes);
+    int rc = fa_check(fn, kv, q, k, v, out, workspace, act, rule, n_head, n_head_kv, n_kv_max, D, k_row, k_head,
+                      v_row, v_head, workspace_bytes);
     if (rc) return rc;
     const int G = (int)(n_head / n_head_kv);
     AMV_REQUIRE(!act || act_type == AMV_T_Q8_0 || (act_type == AMV_T_Q8_K && G % 2 == 0),
@@ -376,14 +503,14 @@ static int fa_run(const char* fn, const float* q, const void* k, const void* v, 
     float* part = (float*)workspace;
     const AmvActOut ao = amv_act_out(act, n_head * D, act ? act_type : 0, rule);
     const dim3 grid(n_split, (unsigned)n_head_kv);
+    const uint8_t* kk = (const uint8_t*)k;
+    const uint8_t* vv = (const uint8_t*)v;
     if (counters) {
-        fa_launch_split<true>(G, kpw, grid, st, q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)mask,
-                              part, (int)n_kv_max, n_kv_dev, k_row, k_head, v_row, v_head, n_split, scale, counters,
-                              out, ao);
+        fa_launch_kv<true>(kv, G, kpw, grid, st, q, kk, vv, (const uint16_t*)mask, part, (int)n_kv_max, n_kv_dev,
+                           k_row, k_head, v_row, v_head, n_split, scale, rule, counters, out, ao);
     } else {
-        fa_launch_split<false>(G, kpw, grid, st, q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)mask,
-                               part, (int)n_kv_max, n_kv_dev, k_row, k_head, v_row, v_head, n_split, scale, nullptr,
-                               nullptr, AmvActOut{});
+        fa_launch_kv<false>(kv, G, kpw, grid, st, q, kk, vv, (const uint16_t*)mask, part, (int)n_kv_max, n_kv_dev,
+                            k_row, k_head, v_row, v_head, n_split, scale, rule, nullptr, nullptr, AmvActOut{});
         if (ao.type == AMV_T_Q8_K)
             hipLaunchKernelGGL(k_fa_combine<2>, dim3((unsigned)(n_head / 2)), dim3(256), 0, st, part, out, n_split,
                                (int)n_kv_max, n_kv_dev, 4 * kpw, ao);
@@ -398,8 +525,9 @@ extern "C" int amv_flash_attn_decode(const float* q, const void* k, const void* 
                                      int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row,
                                      int64_t k_head, int64_t v_row, int64_t v_head, float scale, void* workspace,
                                      int64_t workspace_bytes, void* act, int rule, void* stream) {
-    return fa_run("amv_flash_attn_decode", q, k, v, mask, out, n_head, n_head_kv, n_kv, nullptr, D, k_row, k_head,
-                  v_row, v_head, scale, workspace, workspace_bytes, nullptr, act, AMV_T_Q8_0, rule, stream);
+    return fa_run("amv_flash_attn_decode", AMV_T_F16, q, k, v, mask, out, n_head, n_head_kv, n_kv, nullptr, D,
+                  2 * k_row, 2 * k_head, 2 * v_row, 2 * v_head, scale, workspace, workspace_bytes, nullptr, act,
+                  AMV_T_Q8_0, rule, stream);
 }
 
 extern "C" int amv_flash_attn_decode_ex(const float* q, const void* k, const void* v, const void* mask, float* out,
@@ -407,6 +535,18 @@ extern "C" int amv_flash_attn_decode_ex(const float* q, const void* k, const voi
                                         int64_t D, int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
                                         float scale, void* workspace, int64_t workspace_bytes, unsigned int* counters,
                                         void* act, int act_type, int rule, void* stream) {
-    return fa_run("amv_flash_attn_decode_ex", q, k, v, mask, out, n_head, n_head_kv, n_kv_max, n_kv_dev, D, k_row,
-                  k_head, v_row, v_head, scale, workspace, workspace_bytes, counters, act, act_type, rule, stream);
+    return fa_run("amv_flash_attn_decode_ex", AMV_T_F16, q, k, v, mask, out, n_head, n_head_kv, n_kv_max, n_kv_dev,
+                  D, 2 * k_row, 2 * k_head, 2 * v_row, 2 * v_head, scale, workspace, workspace_bytes, counters, act,
+                  act_type, rule, stream);
+}
+
+extern "C" int amv_flash_attn_decode_kv(int kv_type, const float* q, const void* k, const void* v, const void* mask,
+                                        float* out, int64_t n_head, int64_t n_head_kv, int64_t n_kv_max,
+                                        const int32_t* n_kv_dev, int64_t D, int64_t k_row_bytes, int64_t k_head_bytes,
+                                        int64_t v_row_bytes, int64_t v_head_bytes, float scale, void* workspace,
+                                        int64_t workspace_bytes, unsigned int* counters, void* act, int act_type,
+                                        int rule, void* stream) {
+    return fa_run("amv_flash_attn_decode_kv", kv_type, q, k, v, mask, out, n_head, n_head_kv, n_kv_max, n_kv_dev, D,
+                  k_row_bytes, k_head_bytes, v_row_bytes, v_head_bytes, scale, workspace, workspace_bytes, counters,
+                  act, act_type, rule, stream);
 }

@@ -96,20 +96,9 @@ __global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x,
 // ---------------------------------------------------------------------------------------------------------------
 // Q4_0 rows (ggml quantize_row_q4_0_ref; ameva_set_rows_q.comp:95-115): one lane per 32-element block.
 // ---------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_quant_q4_0(const float* __restrict__ x, int64_t n_blk,
-                                                   uint8_t* __restrict__ y) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= n_blk) return;
-    const float4* xp = reinterpret_cast<const float4*>(x + b * 32);
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 t = xp[i];
-        v[4 * i] = t.x;
-        v[4 * i + 1] = t.y;
-        v[4 * i + 2] = t.z;
-        v[4 * i + 3] = t.w;
-    }
+// One block as 9 halfwords: d (fp16), then byte j of qs = q[j] | q[j + 16] << 4. max = the first element of largest
+// magnitude, d = max / -8, id = 1/d, q = min(15, (int)(x * id + 8.5)).
+__device__ __forceinline__ void q4_0_block(const float (&v)[32], uint16_t (&h)[9]) {
     float amax = 0.0f, mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
@@ -117,7 +106,6 @@ __global__ __launch_bounds__(256) void k_quant_q4_0(const float* __restrict__ x,
     }
     const float d = mx / -8.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint16_t h[9];
     h[0] = amv_f2h(d);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -133,9 +121,118 @@ __global__ __launch_bounds__(256) void k_quant_q4_0(const float* __restrict__ x,
         }
         h[1 + k] = (uint16_t)pair;
     }
+}
+
+// One Q8_0 block as 17 halfwords (d fp16, then the 32 int8), with the rules of amv_quantize_act.
+__device__ __forceinline__ void q8_0_block(const float (&v)[32], int rule, uint16_t (&h)[17]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.0f;
+    float id;
+    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else id = d != 0.0f ? 1.0f / d : 0.0f;
+    h[0] = amv_f2h(d);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float t = v[2 * k + e] * id;
+            float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+            qf = fminf(127.0f, fmaxf(-127.0f, qf));
+            pair |= (uint32_t)((int)qf & 0xFF) << (8 * e);
+        }
+        h[1 + k] = (uint16_t)pair;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_quant_q4_0(const float* __restrict__ x, int64_t n_blk,
+                                                   uint8_t* __restrict__ y) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blk) return;
+    const float4* xp = reinterpret_cast<const float4*>(x + b * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = xp[i];
+        v[4 * i] = t.x;
+        v[4 * i + 1] = t.y;
+        v[4 * i + 2] = t.z;
+        v[4 * i + 3] = t.w;
+    }
+    uint16_t h[9];
+    q4_0_block(v, h);
     uint16_t* yb = reinterpret_cast<uint16_t*>(y + b * 18);
 #pragma unroll
     for (int k = 0; k < 9; ++k) yb[k] = h[k];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// SET_ROWS / CPY f32 -> Q8_0 or Q4_0 rows: ggml's from_float of the destination type (quantize_row_q8_0 with the
+// chosen rule, quantize_row_q4_0_ref; the reference's ameva_set_rows_q.comp:82-115). One lane per 32-element block of
+// a source row; row r goes to dst row idx[r] (or r), an index outside [0, dst_rows) is skipped and counted once.
+// ---------------------------------------------------------------------------------------------------------------
+template <int T>
+__global__ __launch_bounds__(256) void k_set_rows_q(const float* __restrict__ src, int64_t src_stride,
+                                                   uint8_t* __restrict__ dst, int64_t dst_stride, int64_t n_rows,
+                                                   int nb, const int64_t* __restrict__ idx64,
+                                                   const int32_t* __restrict__ idx32, int64_t dst_rows, int rule,
+                                                   unsigned int* __restrict__ bad) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_rows * nb) return;
+    const int64_t r = t / nb;
+    const int j = (int)(t - r * nb);
+    int64_t dr = r;
+    if (idx64) dr = idx64[r];
+    else if (idx32) dr = idx32[r];
+    if (dr < 0 || dr >= dst_rows) {
+        if (j == 0 && bad) atomicAdd(bad, 1u);
+        return;
+    }
+    const float* x = src + r * src_stride + 32 * j;
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = x[i];
+    constexpr int BB = T == AMV_T_Q8_0 ? 34 : 18;
+    uint16_t* yb = reinterpret_cast<uint16_t*>(dst + dr * dst_stride + (int64_t)BB * j);
+    if constexpr (T == AMV_T_Q8_0) {
+        uint16_t h[17];
+        q8_0_block(v, rule, h);
+#pragma unroll
+        for (int k = 0; k < 17; ++k) yb[k] = h[k];
+    } else {
+        uint16_t h[9];
+        q4_0_block(v, h);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) yb[k] = h[k];
+    }
+}
+
+extern "C" int amv_set_rows_q(int type, const float* src, int64_t src_stride, void* dst, int64_t dst_stride,
+                              int64_t n_rows, int64_t n, const void* idx, int idx_bits, int64_t dst_rows, int rule,
+                              unsigned int* bad, void* stream) {
+    AMV_REQUIRE(src && dst, "amv_set_rows_q: null pointer");
+    AMV_REQUIRE(type == AMV_T_Q8_0 || type == AMV_T_Q4_0, "amv_set_rows_q: type %d (Q8_0 or Q4_0)", type);
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_set_rows_q: bad rule");
+    AMV_REQUIRE(n_rows > 0 && n > 0 && n % 32 == 0 && src_stride >= n, "amv_set_rows_q: bad shape");
+    const int64_t nb = n / 32, bb = type == AMV_T_Q8_0 ? 34 : 18;
+    AMV_REQUIRE(dst_stride >= nb * bb && dst_stride % 2 == 0 && ((uintptr_t)dst & 1) == 0,
+                "amv_set_rows_q: dst rows must hold %lld bytes at even addresses", (long long)(nb * bb));
+    AMV_REQUIRE(nb <= INT32_MAX, "amv_set_rows_q: rows too long");
+    AMV_REQUIRE(idx == nullptr || idx_bits == 32 || idx_bits == 64, "amv_set_rows_q: index type must be i32 or i64");
+    AMV_REQUIRE(idx != nullptr || dst_rows >= n_rows, "amv_set_rows_q: dst too small");
+    const int64_t total = n_rows * nb;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    const int64_t* i64 = idx_bits == 64 ? (const int64_t*)idx : nullptr;
+    const int32_t* i32 = idx_bits == 32 ? (const int32_t*)idx : nullptr;
+    if (type == AMV_T_Q8_0)
+        hipLaunchKernelGGL(k_set_rows_q<AMV_T_Q8_0>, grid, dim3(256), 0, amv_stream(stream), src, src_stride,
+                           (uint8_t*)dst, dst_stride, n_rows, (int)nb, i64, i32, dst_rows, rule, bad);
+    else
+        hipLaunchKernelGGL(k_set_rows_q<AMV_T_Q4_0>, grid, dim3(256), 0, amv_stream(stream), src, src_stride,
+                           (uint8_t*)dst, dst_stride, n_rows, (int)nb, i64, i32, dst_rows, rule, bad);
+    return amv_check_launch("amv_set_rows_q");
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -365,13 +365,18 @@ const char* unsupported_reason(const ggml_tensor* n) {
     case GGML_OP_FLASH_ATTN_EXT: {
         const ggml_tensor *q = s0, *k = s1, *v = n->src[2], *m = n->src[3];
         if (n->src[4]) return "FLASH_ATTN_EXT sinks not supported";
-        if (q->type != GGML_TYPE_F32 || k->type != GGML_TYPE_F16 || v->type != GGML_TYPE_F16)
-            return "FLASH_ATTN_EXT needs F32 q and an F16 K/V cache";
-        if (q->ne[0] != 128 || v->ne[0] != 128) return "FLASH_ATTN_EXT head size must be 128";
+        const bool kvq = k->type == GGML_TYPE_Q8_0 || k->type == GGML_TYPE_Q4_0;  // a quantized cache
+        if (q->type != GGML_TYPE_F32 || (k->type != GGML_TYPE_F16 && !kvq) || v->type != k->type)
+            return "FLASH_ATTN_EXT needs F32 q and an F16, Q8_0 or Q4_0 K/V cache (K and V of one type)";
+        if (q->ne[0] != 128 || v->ne[0] != 128 || k->ne[0] != 128) return "FLASH_ATTN_EXT head size must be 128";
         if (q->ne[1] != 1 || q->ne[3] != 1 || k->ne[3] != 1) return "FLASH_ATTN_EXT decode (one query) only";
         if (q->nb[0] != 4 || q->nb[2] != 128 * 4 || !aligned16(q->data)) return "FLASH_ATTN_EXT q heads must be contiguous";
-        if (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 || v->nb[2] % 16)
-            return "FLASH_ATTN_EXT K/V rows must be 16-byte aligned";
+        if (!kvq && (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 ||
+                     v->nb[2] % 16 || !aligned16(k->data) || !aligned16(v->data)))
+            return "FLASH_ATTN_EXT f16 K/V rows must be 16-byte aligned";
+        if (kvq && (k->nb[0] != (size_t)type_size(k->type) || v->nb[0] != (size_t)type_size(v->type) || k->nb[1] % 2 ||
+                    k->nb[2] % 2 || v->nb[1] % 2 || v->nb[2] % 2 || ((uintptr_t)k->data & 1) || ((uintptr_t)v->data & 1)))
+            return "FLASH_ATTN_EXT quantized K/V rows must be dense blocks at even addresses";
         if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2]) return "FLASH_ATTN_EXT K/V shapes differ";
         const int64_t G = q->ne[2] / k->ne[2];
         if (q->ne[2] % k->ne[2] || (G != 1 && G != 2 && G != 4 && G != 8)) return "FLASH_ATTN_EXT GQA group not 1/2/4/8";
@@ -392,13 +397,18 @@ const char* unsupported_reason(const ggml_tensor* n) {
             return "GLU is contiguous F32 only";
         return nullptr;
     }
-    case GGML_OP_SET_ROWS:
-        if (s0->type != GGML_TYPE_F32 || n->type != GGML_TYPE_F16) return "SET_ROWS F32 -> F16 only";
+    case GGML_OP_SET_ROWS: {
+        const bool q = n->type == GGML_TYPE_Q8_0 || n->type == GGML_TYPE_Q4_0;  // a quantized KV cache
+        if (s0->type != GGML_TYPE_F32 || (n->type != GGML_TYPE_F16 && !q)) return "SET_ROWS F32 -> F16, Q8_0 or Q4_0 only";
         if (s1->type != GGML_TYPE_I64 && s1->type != GGML_TYPE_I32) return "SET_ROWS index must be I32 or I64";
         if (s0->ne[2] != 1 || s0->ne[3] != 1 || n->ne[2] != 1 || n->ne[3] != 1) return "SET_ROWS 2-D only";
-        if (s0->nb[0] != 4 || n->nb[0] != 2 || s1->nb[0] != (size_t)type_size(s1->type)) return "SET_ROWS rows must be dense";
+        if (s0->nb[0] != 4 || n->nb[0] != (size_t)type_size(n->type) || s1->nb[0] != (size_t)type_size(s1->type))
+            return "SET_ROWS rows must be dense";
+        if (q && (n->ne[0] % 32 || n->nb[1] % 2 || ((uintptr_t)n->data & 1)))
+            return "SET_ROWS quantized rows must be whole blocks at even addresses";
         if (s0->ne[0] != n->ne[0] || s1->ne[0] != s0->ne[1]) return "SET_ROWS shapes differ";
         return nullptr;
+    }
     case GGML_OP_CPY:
     case GGML_OP_CONT:
         if (s0->type != GGML_TYPE_F32 || (n->type != GGML_TYPE_F32 && n->type != GGML_TYPE_F16)) return "CPY F32 -> F32/F16 only";
@@ -555,10 +565,11 @@ struct Engine {
         const int64_t ws = amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv, D);
         void* work = dev->arena.take((size_t)ws);
         if (!work) return fail(n, "scratch exhausted");
-        return rc(n, amv_flash_attn_decode((const float*)q->data, k->data, v->data, m ? m->data : nullptr,
-                                           (float*)n->data, n_head, n_head_kv, n_kv, D, (int64_t)k->nb[1] / 2,
-                                           (int64_t)k->nb[2] / 2, (int64_t)v->nb[1] / 2, (int64_t)v->nb[2] / 2,
-                                           op_f32(n, 0), work, ws, nullptr, AMV_Q8_X86, st));
+        // K / V strides in bytes; a Q8_0 / Q4_0 cache meets q quantized to Q8_0 (x86 rule), as ggml's CPU kernel does
+        return rc(n, amv_flash_attn_decode_kv(k->type, (const float*)q->data, k->data, v->data, m ? m->data : nullptr,
+                                              (float*)n->data, n_head, n_head_kv, n_kv, nullptr, D, (int64_t)k->nb[1],
+                                              (int64_t)k->nb[2], (int64_t)v->nb[1], (int64_t)v->nb[2], op_f32(n, 0),
+                                              work, ws, nullptr, nullptr, (int)GGML_TYPE_Q8_0, AMV_Q8_X86, st));
     }
 
     bool glu(const ggml_tensor* n) {
@@ -577,6 +588,10 @@ struct Engine {
 
     bool set_rows(const ggml_tensor* n) {
         const ggml_tensor *src = n->src[0], *idx = n->src[1];
+        if (n->type != GGML_TYPE_F16)  // Q8_0 / Q4_0 cache rows: ggml's from_float of the type (Q8_0 x86 rule)
+            return rc(n, amv_set_rows_q(n->type, (const float*)src->data, (int64_t)src->nb[1] / 4, n->data,
+                                        (int64_t)n->nb[1], src->ne[1], src->ne[0], idx->data,
+                                        idx->type == GGML_TYPE_I64 ? 64 : 32, n->ne[1], AMV_Q8_X86, dev->status, st));
         return rc(n, amv_set_rows_f16((const float*)src->data, (int64_t)src->nb[1] / 4, n->data, (int64_t)n->nb[1] / 2,
                                       src->ne[1], src->ne[0], idx->data, idx->type == GGML_TYPE_I64 ? 64 : 32, n->ne[1],
                                       dev->status, st));

@@ -13,7 +13,7 @@ import torch
 from ._lib import check, lib
 
 # ggml_type values (reference include/ggml/ggml.h:394-437)
-Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, I2_S = 2, 8, 12, 14, 15, 36
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, I2_S = 0, 1, 2, 8, 12, 14, 15, 36
 # Q8_0 activation rounding rules (include/ameva_hip.h)
 Q8_X86, Q8_ARM, Q8_REF = 0, 1, 2
 
@@ -425,6 +425,36 @@ def flash_attn_decode_ex(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scal
     return out
 
 
+def flash_attn_decode_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_type: int, scale: float,
+                         n_kv_max: int | None = None, n_kv_dev: torch.Tensor | None = None,
+                         mask: torch.Tensor | None = None, act: torch.Tensor | None = None, act_t: int = Q8_0,
+                         rule: int = Q8_X86, one_launch: bool = False,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """FLASH_ATTN_EXT decode over an F16 (kv_type 1), Q8_0 (8) or Q4_0 (2) cache: k, v [n_head_kv, n_keys, row] views
+    (f16 elements, or the bytes of ggml blocks for the quantized types; any strides). A quantized K meets q quantized to
+    Q8_0 with `rule` (ggml's CPU kernel); otherwise as flash_attn_decode_ex."""
+    _need_gpu(q, "flash_attn_decode_kv")
+    n_head, D = q.shape
+    n_head_kv, n_keys = k.shape[0], k.shape[1]
+    n_kv_max = n_keys if n_kv_max is None else n_kv_max
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("flash_attn_decode_kv: K/V rows must be contiguous")
+    need = lib().amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv_max, D)
+    if need < 0:
+        raise ValueError("flash_attn_decode_kv: unsupported shape")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    counters = torch.zeros(32 * n_head_kv, dtype=torch.int32, device=q.device) if one_launch else None
+    ke, ve = k.element_size(), v.element_size()
+    out = torch.empty_like(q)
+    check(lib().amv_flash_attn_decode_kv(kv_type, q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(mask),
+                                         out.data_ptr(), n_head, n_head_kv, n_kv_max, _ptr(n_kv_dev), D,
+                                         k.stride(1) * ke, k.stride(0) * ke, v.stride(1) * ve, v.stride(0) * ve, scale,
+                                         workspace.data_ptr(), need, _ptr(counters), _ptr(act), act_t, rule,
+                                         _stream()), "amv_flash_attn_decode_kv")
+    return out
+
+
 def flash_attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, n_kv: int | None = None,
                        mask: torch.Tensor | None = None, causal_pos0: int = -1) -> torch.Tensor:
     """q f32 [n_tok, n_head, D] (any strides with contiguous rows); k, v f16 views [n_head_kv, n_keys, D] as in
@@ -476,6 +506,21 @@ def set_rows_f16(dst: torch.Tensor, src: torch.Tensor, idx: torch.Tensor | None 
                                  dst.shape[0], bad.data_ptr(), _stream()), "amv_set_rows_f16")
     if int(bad.item()) != 0:
         raise IndexError(f"set_rows_f16: {int(bad.item())} row indices out of range (FAIL-FAST)")
+
+
+def set_rows_q(dst: torch.Tensor, src: torch.Tensor, dst_type: int, idx: torch.Tensor | None = None,
+               rule: int = Q8_X86) -> None:
+    """Rows of src f32 [r, n] quantized (Q8_0 with `rule`, or Q4_0) into rows idx of dst (uint8 [rows, >= row bytes],
+    any row stride); raises on out-of-range indices."""
+    _need_gpu(src, "set_rows_q")
+    bad = torch.zeros(1, dtype=torch.int32, device=src.device)
+    r, n = src.shape
+    bits = 0 if idx is None else (64 if idx.dtype == torch.int64 else 32)
+    check(lib().amv_set_rows_q(dst_type, src.data_ptr(), src.stride(0), dst.data_ptr(),
+                               dst.stride(0) * dst.element_size(), r, n, _ptr(idx), bits, dst.shape[0], rule,
+                               bad.data_ptr(), _stream()), "amv_set_rows_q")
+    if int(bad.item()) != 0:
+        raise IndexError(f"set_rows_q: {int(bad.item())} row indices out of range (FAIL-FAST)")
 
 
 def get_rows(src: torch.Tensor, src_type: int, n: int, idx: torch.Tensor) -> torch.Tensor:

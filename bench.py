@@ -276,6 +276,44 @@ def bench_i2s(ops, torch, dev):
     return res
 
 
+def bench_kv_cache(ops, torch, dev):
+    """FLASH_ATTN_EXT decode at the Llama-3-8B layer shape (32 / 8 heads of 128, 4096 cached keys) over an F16, Q8_0
+    and Q4_0 KV cache in llama.cpp's layout (token rows of all KV heads), cold: the caches rotate over copies totalling
+    > 512 MiB. Algorithmic bytes: K + V rows read once."""
+    res = {}
+    NH, NKV, D, CTX = 32, 8, 128, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(4096)
+    q = torch.randn((NH, D), generator=g, device=dev)
+    for name, t in (("f16", ops.F16), ("q8_0", ops.Q8_0), ("q4_0", ops.Q4_0)):
+        rows = torch.randn((CTX, NKV * D), generator=g, device=dev)
+        if t == ops.F16:
+            base = [rows.half(), torch.randn((CTX, NKV * D), generator=g, device=dev).half()]
+            rb = 2 * D
+        else:
+            rb = D // 32 * (34 if t == ops.Q8_0 else 18)
+            base = []
+            for _ in range(2):
+                c = torch.empty((CTX, NKV * rb), dtype=torch.uint8, device=dev)
+                ops.set_rows_q(c, torch.randn((CTX, NKV * D), generator=g, device=dev), t)
+                base.append(c)
+        per = 2 * CTX * NKV * rb
+        copies = max(4, -(-(600 << 20) // per))
+        kv = [(base[0].clone(), base[1].clone()) for _ in range(copies)]
+        views = [(k.view(CTX, NKV, -1).permute(1, 0, 2), v.view(CTX, NKV, -1).permute(1, 0, 2)) for k, v in kv]
+        ws = torch.empty(max(1, ops.lib().amv_flash_attn_workspace_bytes(NH, NKV, CTX, D)), dtype=torch.uint8,
+                         device=dev)
+        ms = time_steps_graph(torch, lambda i: ops.flash_attn_decode_kv(q, views[i % copies][0], views[i % copies][1],
+                                                                       t, 0.0884, workspace=ws), 400, 40)
+        res[f"fa_decode_ctx4096_{name}_us"] = round(ms * 1e3, 2)
+        res[f"fa_decode_ctx4096_{name}_gbs"] = round(per / (ms * 1e-3) / 1e9, 1)
+        log(f"bench: FA decode ctx {CTX} {name} KV cache, cold: {ms * 1e3:.2f} us, {per / 2**20:.1f} MiB K+V -> "
+            f"{per / (ms * 1e-3) / 1e9:.0f} GB/s")
+        del kv, views, base
+        torch.cuda.empty_cache()
+    return res
+
+
 def copy_ceiling(torch, dev, nbytes):
     """Device-to-device copy of the headline's byte count (torch copy kernel), cold over 20 buffers: the HBM rate a
     single launch of a plain streaming kernel of that size reaches on this box, read + write bytes counted."""
@@ -505,6 +543,7 @@ def main():
         extra.update(secondary_gemvs(ops, torch, dev))
         extra.update(bench_batched(ops, torch, dev))
         extra.update(bench_i2s(ops, torch, dev))
+        extra.update(bench_kv_cache(ops, torch, dev))
         extra.update(copy_ceiling(torch, dev, nbytes))
 
     layer_info = None

@@ -258,6 +258,19 @@ int amv_flash_attn_decode_ex(const float* q, const void* k, const void* v, const
                              void* workspace, int64_t workspace_bytes, unsigned int* counters, void* act, int act_type,
                              int rule, void* stream);
 
+/* FLASH_ATTN_EXT decode over an f16, Q8_0 or Q4_0 KV cache (the reference's quantized-cache attention,
+ * ameva_flash_attn.comp:4-8 and 104-136; ggml_compute_forward_flash_attn_ext for the CPU semantics). kv_type: 1 = F16,
+ * 8 = Q8_0, 2 = Q4_0 (K and V both); strides in BYTES (ggml's nb[1], nb[2]); a quantized row of D = 128 elements is 4
+ * ggml blocks (136 bytes Q8_0, 72 bytes Q4_0) at a 2-byte-aligned address. For a quantized K, q is quantized to Q8_0
+ * with `rule` (K's vec_dot_type, as ggml's CPU kernel does) and each score is sum_b float(isum_b) * (d_k * d_q) over
+ * the exact integer block sums; V rows are dequantized exactly (q * d, (nibble - 8) * d); f16 caches behave as in
+ * amv_flash_attn_decode_ex. Other arguments as amv_flash_attn_decode_ex. */
+int amv_flash_attn_decode_kv(int kv_type, const float* q, const void* k, const void* v, const void* mask, float* out,
+                             int64_t n_head, int64_t n_head_kv, int64_t n_kv_max, const int32_t* n_kv_dev, int64_t D,
+                             int64_t k_row_bytes, int64_t k_head_bytes, int64_t v_row_bytes, int64_t v_head_bytes,
+                             float scale, void* workspace, int64_t workspace_bytes, unsigned int* counters, void* act,
+                             int act_type, int rule, void* stream);
+
 /* FLASH_ATTN_EXT over n_tok query positions (prompt prefill; enc_flash_attn ggml-ameva.cpp:4204-4284 with
  * q->ne[1] > 1, ameva_flash_attn.comp), on the f16 matrix cores. D = 128, n_head / n_head_kv integral.
  *   q f32: element d of head h of token t at q[t * q_tok_stride + h * q_head_stride + d] (strides in floats, multiples
@@ -282,6 +295,13 @@ int amv_binary(int op, const float* a, const float* b, float* dst, int64_t n_row
  * r when idx is NULL; idx_bits 32 or 64. Out-of-range indices are skipped and counted in *bad (device, may be NULL). */
 int amv_set_rows_f16(const float* src, int64_t src_stride, void* dst, int64_t dst_stride, int64_t n_rows, int64_t n,
                      const void* idx, int idx_bits, int64_t dst_rows, unsigned int* bad, void* stream);
+/* SET_ROWS / CPY f32 -> Q8_0 or Q4_0 (a quantized KV cache; ameva_set_rows_q.comp:82-115): row r of src (stride
+ * src_stride elements, n % 32 == 0) quantized with ggml's from_float of `type` (8 = Q8_0 with `rule`, 2 = Q4_0:
+ * quantize_row_q4_0_ref) into row idx[r] (or r) of dst, dst_stride in BYTES (even, >= n / 32 blocks); out-of-range
+ * indices are skipped and counted once per row in *bad. */
+int amv_set_rows_q(int type, const float* src, int64_t src_stride, void* dst, int64_t dst_stride, int64_t n_rows,
+                   int64_t n, const void* idx, int idx_bits, int64_t dst_rows, int rule, unsigned int* bad,
+                   void* stream);
 /* GET_ROWS (enc_get_rows, ameva_get_rows_q.comp): dst f32 [n_idx][n] = row idx[i] of src (type F32, F16, Q4_0,
  * Q8_0, Q4_K or Q6_K in ggml layout, src_rows rows), dequantized with ggml's dequantize_row_* expressions; rows
  * outside [0, src_rows) give zeros and add 1 to *bad when bad is not NULL. */

@@ -50,6 +50,8 @@ def lib() -> ctypes.CDLL:
             "orc_rope": (None, [P, P, P, I64, I64, I64, ctypes.c_int, ctypes.c_int, F, F, F]),
             "orc_swiglu": (None, [P, P, P, I64]),
             "orc_flash_attn_decode": (None, [P, P, P, P, P, I64, I64, I64, I64, F]),
+            "orc_flash_attn_decode_q": (ctypes.c_int, [ctypes.c_int, P, P, P, P, P, I64, I64, I64, I64, F,
+                                                       ctypes.c_int]),
             "orc_i2s_quantize_act": (F, [P, P, I64]),
             "orc_i2s_dot_row": (I64, [I64, P, P, P]),
             "orc_i2s_gemv": (None, [P, I64, I64, P, P, I64, F, P, P]),
@@ -193,6 +195,26 @@ def flash_attn_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
         mask = np.ascontiguousarray(mask, dtype=np.uint16)
         mp = _p(mask)
     lib().orc_flash_attn_decode(_p(q), _p(k), _p(v), mp, _p(out), n_head, n_head_kv, n_kv, D, scale)
+    return out
+
+
+def flash_attn_decode_q(kv_type: int, q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
+                        mask: np.ndarray | None = None, rule: int = Q8_X86):
+    """q f32 [n_head, D]; k, v uint8 [n_head_kv, n_kv, row bytes] of Q8_0 (kv_type 8) or Q4_0 (2) blocks; mask f16
+    bits [n_kv] or None."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.uint8)
+    v = np.ascontiguousarray(v, dtype=np.uint8)
+    n_head, D = q.shape
+    n_head_kv, n_kv, _ = k.shape
+    out = np.empty((n_head, D), dtype=np.float32)
+    mp = None
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.uint16)
+        mp = _p(mask)
+    rc = lib().orc_flash_attn_decode_q(kv_type, _p(q), _p(k), _p(v), mp, _p(out), n_head, n_head_kv, n_kv, D,
+                                       scale, rule)
+    assert rc == 0
     return out
 
 

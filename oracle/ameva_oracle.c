@@ -510,6 +510,55 @@ void orc_flash_attn_decode(const float *q, const uint16_t *k, const uint16_t *v,
 }
 
 /* ------------------------------------------------------------------------------------------------------------------
+ * Flash attention, decode, over a Q8_0 or Q4_0 K/V cache (the reference's quantized-cache attention,
+ * ameva_flash_attn.comp:4-8, 104-136; ggml's CPU kernel ggml_compute_forward_flash_attn_ext for what the build
+ * matches): q is converted with from_float of K's vec_dot_type (quantize_row_q8_0 with `rule`), each score is
+ * vec_dot_q8_0_q8_0 / vec_dot_q4_0_q8_0 of the K row and q in f32, then s * scale + mask in f32; V rows are
+ * dequantized (q * d, (nibble - 8) * d); the softmax and P V are evaluated exactly here (double), the value ggml's f32
+ * arithmetic approximates.
+ *   kv_type 8 (Q8_0) or 2 (Q4_0) for K and V; k, v [n_head_kv][n_kv] rows of D / 32 ggml blocks; q f32 [n_head][D];
+ *   mask f16 [n_kv] or NULL; out f32 [n_head][D]. Returns -1 for an unsupported type.
+ * ---------------------------------------------------------------------------------------------------------------- */
+int orc_flash_attn_decode_q(int kv_type, const float *q, const uint8_t *k, const uint8_t *v, const uint16_t *mask,
+                            float *out, int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D, float scale,
+                            int rule) {
+    if (kv_type != 8 && kv_type != 2) return -1;
+    const int64_t bs = kv_type == 8 ? BS_Q8_0 : BS_Q4_0, rb = D / 32 * bs, G = n_head / n_head_kv;
+#pragma omp parallel for schedule(static)
+    for (int64_t h = 0; h < n_head; ++h) {
+        const int64_t hk = h / G;
+        uint8_t *qq = (uint8_t *)malloc((size_t)(D / 32 * BS_Q8_0));
+        double *s = (double *)malloc(sizeof(double) * (size_t)n_kv);
+        double *acc = (double *)calloc((size_t)D, sizeof(double));
+        float *vr = (float *)malloc(sizeof(float) * (size_t)D);
+        orc_quantize_q8_0(q + h * D, qq, 1, D, rule);
+        double mx = -INFINITY;
+        for (int64_t j = 0; j < n_kv; ++j) {
+            const uint8_t *kr = k + (hk * n_kv + j) * rb;
+            float x = kv_type == 8 ? orc_vec_dot_q8_0_q8_0(D, kr, qq, NULL) : orc_vec_dot_q4_0_q8_0(D, kr, qq, NULL);
+            x = x * scale;
+            if (mask) x += orc_fp16_to_fp32(mask[j]);
+            s[j] = (double)x;
+            if (s[j] > mx) mx = s[j];
+        }
+        double l = 0.0;
+        for (int64_t j = 0; j < n_kv; ++j) {
+            if (s[j] == -INFINITY) continue;
+            const double p = exp(s[j] - mx);
+            l += p;
+            orc_dequantize(kv_type, v + (hk * n_kv + j) * rb, vr, D);
+            for (int64_t d = 0; d < D; ++d) acc[d] += p * (double)vr[d];
+        }
+        for (int64_t d = 0; d < D; ++d) out[h * D + d] = l > 0.0 ? (float)(acc[d] / l) : 0.0f;
+        free(qq);
+        free(s);
+        free(acc);
+        free(vr);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------------------------
  * BitNet I2_S
  * ---------------------------------------------------------------------------------------------------------------- */
 

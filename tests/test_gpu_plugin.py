@@ -209,6 +209,59 @@ def test_failure_injection_and_contract_fail_fast(plugin):
         g.free()
 
 
+@pytest.mark.parametrize("t", [gp.Q8_0, gp.Q4_0])
+def test_quantized_kv_cache_nodes(plugin, orc, t):
+    """SET_ROWS of a token's K and V rows into a Q8_0 / Q4_0 cache, then FLASH_ATTN_EXT over llama.cpp's views of that
+    cache (the reference's quantized-cache path, ameva_set_rows_q.comp + ameva_flash_attn.comp:104-136): the written
+    rows equal the oracle's quantizer bytes, and the attention equals the oracle's restatement of ggml's CPU kernel."""
+    rng = np.random.default_rng(77 + t)
+    NH, NKV, D, CTX, pos_t = 32, 8, 128, 512, 300
+    bs = 34 if t == gp.Q8_0 else 18
+    rb = D // 32 * bs                                     # one head row
+    quant = (lambda a: orc.quantize_q8_0(a, orc.Q8_X86)) if t == gp.Q8_0 else orc.quantize_q4_0
+    kf = rng.standard_normal((CTX, NKV * D)).astype(np.float32)
+    vf = rng.standard_normal((CTX, NKV * D)).astype(np.float32)
+    kc, vc = quant(kf), quant(vf)                         # [CTX, NKV * rb]
+    knew = rng.standard_normal((1, NKV * D)).astype(np.float32)
+    vnew = rng.standard_normal((1, NKV * D)).astype(np.float32)
+    q = rng.standard_normal((NH, D)).astype(np.float32)
+    mask = np.zeros(CTX, np.float16)
+    mask[pos_t + 1:] = -np.inf
+    g = gp.Graph(4096, 32 << 20)
+    try:
+        KC, VC = g.tensor(t, [NKV * D, CTX], "c", "k_cache"), g.tensor(t, [NKV * D, CTX], "c", "v_cache")
+        g.set(KC, kc)
+        g.set(VC, vc)
+        KN, VN = g.tensor(gp.F32, [NKV * D, 1], "c", "k_new"), g.tensor(gp.F32, [NKV * D, 1], "c", "v_new")
+        g.set(KN, knew)
+        g.set(VN, vnew)
+        IDX = g.tensor(gp.I64, [1], "c", "kv_idx")
+        g.set(IDX, np.array([pos_t], np.int64))
+        Q = g.tensor(gp.F32, [D, NH, 1], "c", "q")
+        g.set(Q, q)
+        MASK = g.tensor(gp.F16, [CTX, 1], "c", "mask")
+        g.set(MASK, mask)
+        g.set_rows(KC, KN, IDX)
+        g.set_rows(VC, VN, IDX)
+        kv_nb = [bs, NKV * rb, rb, NKV * rb * CTX]
+        kview = g.view_nd(KC, gp.OP_VIEW, [D, CTX, NKV], kv_nb)
+        vview = g.view_nd(VC, gp.OP_VIEW, [D, CTX, NKV], kv_nb)
+        qp = g.view_nd(Q, gp.OP_PERMUTE, [D, 1, NH], [4, D * NH * 4, D * 4, D * NH * 4])
+        att = g.flash_attn_ext(qp, kview, vview, MASK, 1.0 / np.sqrt(D))
+        assert g.compute() == gp.STATUS_SUCCESS
+        got = g.get(att, np.float32, (NH, D))
+        kc2, vc2 = kc.copy(), vc.copy()
+        kc2[pos_t], vc2[pos_t] = quant(knew)[0], quant(vnew)[0]
+        assert np.array_equal(g.get(KC, np.uint8, kc.shape), kc2)
+        assert np.array_equal(g.get(VC, np.uint8, vc.shape), vc2)
+        kh = np.ascontiguousarray(kc2.reshape(CTX, NKV, rb).transpose(1, 0, 2))
+        vh = np.ascontiguousarray(vc2.reshape(CTX, NKV, rb).transpose(1, 0, 2))
+        want = orc.flash_attn_decode_q(t, q, kh, vh, 1.0 / np.sqrt(D), mask.view(np.uint16))
+        assert rel_l2(got, want) < 1e-4
+    finally:
+        g.free()
+
+
 def test_llama3_8b_decode_layer(plugin, orc):
     """One decoder layer of Llama-3-8B shape, bs1 decode at position 4095 with 4095 cached tokens."""
     rng = np.random.default_rng(2024)

@@ -315,6 +315,58 @@ def test_flash_attn_decode_closed_form(orc):
     assert rel_l2(out, want) < 1e-6
 
 
+def exact_cache(rng, kv, n_rows, D):
+    """Q8_0 / Q4_0 rows of D with d a power of two (2^-7, 2^-4): every dequantized value is exact in f16."""
+    nb = D // 32
+    if kv == 8:
+        blk = np.zeros((n_rows, nb, 34), np.uint8)
+        blk[:, :, 0:2] = np.array([2.0 ** -7], np.float16).view(np.uint8)
+        blk[:, :, 2:] = rng.integers(-127, 128, (n_rows, nb, 32)).astype(np.int8).view(np.uint8)
+    else:
+        blk = np.zeros((n_rows, nb, 18), np.uint8)
+        blk[:, :, 0:2] = np.array([2.0 ** -4], np.float16).view(np.uint8)
+        blk[:, :, 2:] = rng.integers(0, 256, (n_rows, nb, 16)).astype(np.uint8)
+    return blk.reshape(n_rows, -1)
+
+
+@pytest.mark.parametrize("kv", [8, 2])
+def test_flash_attn_decode_quantized_cache(orc, kv):
+    """The quantized-cache oracle against (a) float64 from the pinned dequantizer and the pinned Q8_0 of q (the scores
+    are exact integers times d_k d_q) and (b) the f16-cache oracle where Q8_0 of q is exact and the cache values are
+    exact in f16: a swapped nibble, a wrong block or head index or a dropped d breaks one of them."""
+    rng = np.random.default_rng(40 + kv)
+    n_head, n_head_kv, n_kv, D = 8, 2, 300, 128
+    scale = 1.0 / np.sqrt(D)
+    mask = np.zeros(n_kv, np.float16)
+    mask[250:] = -np.inf
+    quant = (lambda x: orc.quantize_q8_0(x, orc.Q8_X86)) if kv == 8 else orc.quantize_q4_0
+    q = rng.standard_normal((n_head, D)).astype(np.float32)
+    kq = quant(rng.standard_normal((n_head_kv * n_kv, D)).astype(np.float32)).reshape(n_head_kv, n_kv, -1)
+    vq = quant(rng.standard_normal((n_head_kv * n_kv, D)).astype(np.float32)).reshape(n_head_kv, n_kv, -1)
+    out = orc.flash_attn_decode_q(kv, q, kq, vq, scale, mask.view(np.uint16))
+    kd = orc.dequantize(kv, kq, D).reshape(n_head_kv, n_kv, D).astype(np.float64)
+    vd = orc.dequantize(kv, vq, D).reshape(n_head_kv, n_kv, D).astype(np.float64)
+    qd = orc.dequantize(8, orc.quantize_q8_0(q, orc.Q8_X86), D).astype(np.float64)
+    want = np.empty((n_head, D))
+    G = n_head // n_head_kv
+    for h in range(n_head):
+        sc = kd[h // G, :250] @ qd[h] * scale
+        p = np.exp(sc - sc.max())
+        want[h] = p @ vd[h // G, :250] / p.sum()
+    assert rel_l2(out, want) < 1e-5
+    # exact regime: q = n 2^-6 with a +-127 in every block (Q8_0 of q is exact), cache values exact in f16
+    n = rng.integers(-127, 128, (n_head, D))
+    n[:, ::32] = 127 * rng.choice([-1, 1], (n_head, D // 32))
+    qx = (n * 2.0 ** -6).astype(np.float32)
+    kx = exact_cache(rng, kv, n_head_kv * n_kv, D).reshape(n_head_kv, n_kv, -1)
+    vx = exact_cache(rng, kv, n_head_kv * n_kv, D).reshape(n_head_kv, n_kv, -1)
+    k16 = orc.dequantize(kv, kx, D).reshape(n_head_kv, n_kv, D).astype(np.float16)
+    v16 = orc.dequantize(kv, vx, D).reshape(n_head_kv, n_kv, D).astype(np.float16)
+    a = orc.flash_attn_decode_q(kv, qx, kx, vx, scale, mask.view(np.uint16))
+    b = orc.flash_attn_decode(qx, k16.view(np.uint16), v16.view(np.uint16), scale, mask.view(np.uint16))
+    assert rel_l2(a, b) < 1e-6
+
+
 # ------------------------------------------------------------------------------------------------------ SwiGLU
 def test_swiglu_closed_form(orc):
     rng = np.random.default_rng(23)
