@@ -152,12 +152,13 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
 template <int KT>
 __device__ __forceinline__ uint4 fa_row(const uint8_t* __restrict__ row, int l16) {
     if constexpr (KT == FA_F16) {
-        return *reinterpret_cast<const uint4*>(row + 16 * l16);
+        return amv_ld_stream(reinterpret_cast<const uint4*>(row + 16 * l16));
     } else {
         constexpr int BB = KT == FA_Q8_0 ? 34 : 18;
         const int o = 8 * (l16 & 3);
         const uint16_t* bp = reinterpret_cast<const uint16_t*>(row + BB * (l16 >> 2));
         const int h = KT == FA_Q8_0 ? 1 + (o >> 1) : 1 + ((o & 15) >> 1);
+        // halfword pieces of lines the 16 lanes share: ordinary (cached) loads
         const uint32_t b0 = bp[h], b1 = bp[h + 1], b2 = bp[h + 2], b3 = bp[h + 3];
         return make_uint4(b0 | (b1 << 16), b2 | (b3 << 16), bp[0], 0u);
     }

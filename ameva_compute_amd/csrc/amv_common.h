@@ -94,6 +94,18 @@ __device__ __forceinline__ uint16_t amv_f2h(float f) {
 // f32 -> fp16 -> f32 rounding of a value loaded from memory (v_cvt_f16_f32, round to nearest even): one instruction,
 // for rounding points of a computation (ggml's f16 q in flash attention); the stored scales above use amv_f2h.
 __device__ __forceinline__ float amv_round_f16(float x) { return (float)(_Float16)x; }
+// Streaming loads for data read once per launch (GEMV weights, KV rows): non-temporal, so the lines do not displace
+// what is reused (activations) in L2 and the Infinity Cache. Measured on MI355X: a cold 33 MB read runs ~7 % faster.
+// Only for loads whose wave instruction covers whole lines: a line that a later instruction reads again is fetched
+// twice when the first read was non-temporal.
+typedef unsigned int amv_v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 amv_ld_stream(const uint4* p) {
+    const amv_v4u v = __builtin_nontemporal_load(reinterpret_cast<const amv_v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t amv_ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint16_t amv_ld_stream(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+
 __device__ __forceinline__ float amv_h2f(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
 }

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void k_i2s_gemv(const uint4* __restrict__ w, i
         const int jj = min(j, nsl - 1);
         uint4 c[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) c[r] = w[(size_t)min(row0 + r, n_rows - 1) * nsl + jj];
+        for (int r = 0; r < R; ++r) c[r] = amv_ld_stream(w + (size_t)min(row0 + r, n_rows - 1) * nsl + jj);
         if (j < nsl) {
             const int b = jj >> 1, p = jj & 1;
             int4 a[4];
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(256) void k_i2s_gemv_f32(const uint8_t* __restrict_
     const uint8_t* wr = w + (size_t)row * rb;
     float acc = 0.0f;
     for (int b0 = 16 * lane; b0 < rb; b0 += 1024) {
-        const uint4 v = *reinterpret_cast<const uint4*>(wr + b0);
+        const uint4 v = amv_ld_stream(reinterpret_cast<const uint4*>(wr + b0));
         const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
         const int blk = b0 >> 5, half = (b0 >> 4) & 1;
         const float* xb = x + 128 * blk + 16 * half;

@@ -215,23 +215,23 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
         for (int u = 0; u < U; ++u) {
             const int j = FULL ? j0 + 64 * u + lane : min(j0 + 64 * u + lane, nb - 1);
 #pragma unroll
-            for (int r = 0; r < R; ++r) w[u][r] = wq[rb[r] + j];
+            for (int r = 0; r < R; ++r) w[u][r] = amv_ld_stream(wq + rb[r] + j);
             if (BLOCK_SUMS) continue;
             if constexpr (PAIRS && !MMV_STACKED(EP) && R % 2 == 0) {
                 // the wave's rows 2p, 2p + 1 read both scales with one dword
 #pragma unroll
                 for (int r = 0; r < R; r += 2) {
-                    const uint32_t d2 = wd2[(db[r] >> 1) + j];
+                    const uint32_t d2 = amv_ld_stream(wd2 + (db[r] >> 1) + j);
                     dw[u][r] = d2 & 0xFFFFu;
                     dw[u][r + 1] = d2 >> 16;
                 }
             } else if constexpr (PAIRS) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) dw[u][r] = wd[db[r] + 2 * j];
+                for (int r = 0; r < R; ++r) dw[u][r] = amv_ld_stream(wd + db[r] + 2 * j);
             } else {
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    dw[u][r] = wd[amv_q4_0_didx(min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1), j, nb, n_rows)];
+                    dw[u][r] = amv_ld_stream(wd + amv_q4_0_didx(min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1), j, nb, n_rows));
             }
         }
 #pragma unroll
@@ -295,9 +295,11 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const size_t bi = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1) * nb + j;
+                // each lane reads its block's 32 bytes in two halves: a line a wave touches twice must stay in L2,
+                // so these loads are not streaming (measured: 14.2 us against 12.1 us at 14336 x 4096)
                 w0[u][r] = wq[2 * bi];
                 w1[u][r] = wq[2 * bi + 1];
-                dw[u][r] = wd[bi];
+                dw[u][r] = amv_ld_stream(wd + bi);
             }
         }
 #pragma unroll
@@ -373,8 +375,8 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const size_t row = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
-            q[r] = wq[row * nsl + j];
-            hd[r] = wh[row * nsb + sb];
+            q[r] = amv_ld_stream(wq + row * nsl + j);
+            hd[r] = amv_ld_stream(wh + row * nsb + sb);
         }
         const int4 alo = a4[sb * 16 + 4 * c + h], ahi = a4[sb * 16 + 4 * c + 2 + h];
         const float da = ad[sb];
@@ -441,10 +443,10 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
         for (int r = 0; r < R; ++r) {
             const size_t rw = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
             const size_t rb = rw * nsb + sb;
-            ql[r] = wl[rw * nsl + j];
-            qh[r] = wqh[rb * 4 + 2 * hh + (lq >> 4)];
-            sc[r] = wsc[rb];
-            dd[r] = wd[rb];
+            ql[r] = amv_ld_stream(wl + rw * nsl + j);
+            qh[r] = amv_ld_stream(wqh + rb * 4 + 2 * hh + (lq >> 4));
+            sc[r] = amv_ld_stream(wsc + rb);
+            dd[r] = amv_ld_stream(wd + rb);
         }
         const int elo = 128 * hh + 32 * slo + lq;  // element offset in the super-block
         const int4 alo = a4[(sb * 256 + elo) >> 4], ahi = a4[(sb * 256 + elo + 64) >> 4];
@@ -556,13 +558,14 @@ static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
                        a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout, a.post);
 }
 
-// Split of K over the S waves of a row group (S = 1, 2, 4) for launches of few row groups. Measured on MI355X
-// (cold, one launch): from 2048 row groups up (the 4096-row projections) the split does not pay (4096 x 14336:
-// 8.0 us with S = 4 against 7.9 us without), so only matrices of at most 2048 rows are split, S doubling while the
-// launch stays within 4096 waves and each wave keeps a whole 64-unit step.
+// Split of K over the S waves of a row group (S = 1, 2, 4). Measured on MI355X (cold, one launch, streaming
+// weight loads): matrices of at most 1024 row groups are split, S doubling while the launch stays within 2048 waves
+// and each wave keeps a whole 64-unit step; a long K (>= 4 steps per row group, the 4096 x 14336 down projection:
+// 7.25 us with S = 2 against 7.68 us) takes S = 2 at any row count; 4096 x 4096 and 14336 x 4096 run best unsplit.
 static int mmv_split(int64_t groups, int64_t steps) {
     int S = 1;
     while (S < 4 && groups * S * 2 <= 2048 && S * 2 <= steps) S *= 2;
+    if (S == 1 && steps >= 4) S = 2;
     return S;
 }
 
@@ -622,7 +625,27 @@ static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
         }
         launch_q8_0_s<2, 2, BS, EP>(a, st, split(groups2, (nb + 127) / 128));
         return AMV_OK;
-    case AMV_T_Q4_K: launch_q4_K_s<2, BS, EP>(a, st, split(groups2, (nb + 63) / 64)); return AMV_OK;
+    case AMV_T_Q4_K: {
+        // from the MI355X sweep (cold, streaming loads): long rows split K in four (4096 x 14336: 8.5 us against 9.1 us
+        // with S = 2); 8192 .. 16383 rows split K in two (14336 x 4096: 7.9 us with 4 rows per wave against 8.8 us
+        // for R = 2 unsplit); taller launches (the stacked 28672 x 4096 gate/up) stay unsplit, where the SWIGLU
+        // epilogue's per-block arrivals would double. S depends on the launch shape only, so a fused epilogue sums
+        // each row in the order of the plain GEMV of the same weight (bit-identical results); R, which does not change
+        // a row's sums, is 4 wherever the epilogue allows it (28672 x 4096 plain: 13.4 us against 14.5 us).
+        const int64_t steps = (nb + 63) / 64;
+        const int S = BS ? 1
+                      : steps >= 4                                           ? 4
+                      : (a.n_rows >= 8192 && a.n_rows < 16384 && steps >= 2) ? 2
+                                                                             : split(groups2, steps);
+        if constexpr (!BS && !MMV_STACKED(EP) && EP != MMV_EP_ROPE_KV && !MMV_TAIL(EP)) {
+            if (a.n_rows >= 8192 && a.n_rows % 4 == 0 && steps < 4) {
+                launch_q4_K_s<4, BS, EP>(a, st, S);
+                return AMV_OK;
+            }
+        }
+        launch_q4_K_s<2, BS, EP>(a, st, S);
+        return AMV_OK;
+    }
     case AMV_T_Q6_K: launch_q6_K_s<2, BS, EP>(a, st, split(groups2, (nb + 63) / 64)); return AMV_OK;
     default: amv_set_error("amv_mul_mat_vec: weight type %d not supported", a.wtype); return AMV_ERR_UNSUPPORTED;
     }
