@@ -52,6 +52,10 @@ SIGNATURES = {
                                      I64, P]),
     "amv_binary": (I32, [I32, P, P, P, I64, I64, I64, P]),
     "amv_set_rows_f16": (I32, [P, I64, P, I64, I64, I64, P, I32, I64, P, P]),
+    "amv_i2s_gemv_acc": (I32, [P, I64, I64, P, F32, P, P]),
+    "amv_bitnet_norm_q8": (I32, [P, P, P, I64, F32, I32, I32, P, P, P]),
+    "amv_bitnet_rope_kv": (I32, [P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
+    "amv_gemv_f16": (I32, [P, I64, I64, P, P, P]),
     "amv_set_rows_q": (I32, [I32, P, I64, P, I64, I64, I64, P, I32, I64, I32, P, P]),
     "amv_flash_attn_decode_kv": (I32, [I32, P, P, P, P, P, I64, I64, I64, P, I64, I64, I64, I64, I64, F32, P, I64, P,
                                        P, I32, I32, P]),

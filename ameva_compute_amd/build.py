@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libameva_hip.so")
-SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_fa_prefill.hip", "amv_mmq.hip", "amv_mmq16.hip", "amv_elem.hip"]
+SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_fa_prefill.hip", "amv_mmq.hip", "amv_mmq16.hip", "amv_elem.hip", "amv_bitnet.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -53,6 +53,7 @@ def build(verbose: bool = False) -> str:
     build_plugin()
     build_amuda()
     build_runtime()
+    build_bitnet()
     build_test_kernels()
     return LIB
 
@@ -111,6 +112,22 @@ def build_runtime() -> str:
         raise RuntimeError("hipcc failed on ac_runtime_hip.cpp")
     os.replace(tmp, RUNTIME)
     return RUNTIME
+
+
+BITNET = os.path.join(HERE, "libac_bitnet_hip.so")
+
+
+def build_bitnet() -> str:
+    """libac_bitnet_hip.so: the BitNet per-token engine (include/ac_bitnet_engine_hip.h) over libameva_hip.so."""
+    src = os.path.join(CSRC, "ac_bitnet_engine.cpp")
+    tmp = BITNET + ".tmp"
+    cmd = [HIPCC, *FLAGS, "-shared", "-o", tmp, src, "-L" + HERE, "-lameva_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed on ac_bitnet_engine.cpp")
+    os.replace(tmp, BITNET)
+    return BITNET
 
 
 TEST_KERNELS = os.path.join(os.path.dirname(HERE), "tests", "ac_kernels", "ac_test_kernels.hip")

@@ -144,15 +144,24 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
 #define FA_F16 0
 #define FA_Q8_0 1
 #define FA_Q4_0 2
+#define FA_F32 3  // the BitNet engine's cache (llama_bitnet_core.cpp:1022-1082): f32 q . k, no rounding of q
+
+// A lane's slice of a K / V row: .a (and .b for an f32 row, whose 8 elements are 32 bytes).
+struct FaRow {
+    uint4 a, b;
+};
 
 // The slice of one K / V row a lane works on: lane l16 (0..15 of its 16-lane group) owns elements 8 l16 .. 8 l16 + 7.
-// f16: those 16 bytes. Q8_0 / Q4_0 (ggml blocks of 34 / 18 bytes): element offset o = 8 (l16 & 3) in block l16 / 4;
+// f32: those 32 bytes (.a, .b). f16: those 16 bytes. Q8_0 / Q4_0 (ggml blocks of 34 / 18 bytes): element offset o = 8 (l16 & 3) in block l16 / 4;
 // .x, .y = the 8 int8 (Q8_0) or the 8 qs bytes whose low (o < 16) or high (o >= 16) nibbles are the elements (Q4_0),
 // .z = the block's fp16 d. Quantized rows need only 2-byte alignment (halfword loads).
 template <int KT>
-__device__ __forceinline__ uint4 fa_row(const uint8_t* __restrict__ row, int l16) {
-    if constexpr (KT == FA_F16) {
-        return amv_ld_stream(reinterpret_cast<const uint4*>(row + 16 * l16));
+__device__ __forceinline__ FaRow fa_row(const uint8_t* __restrict__ row, int l16) {
+    if constexpr (KT == FA_F32) {
+        const uint4* p = reinterpret_cast<const uint4*>(row + 32 * l16);
+        return FaRow{amv_ld_stream(p), amv_ld_stream(p + 1)};
+    } else if constexpr (KT == FA_F16) {
+        return FaRow{amv_ld_stream(reinterpret_cast<const uint4*>(row + 16 * l16)), make_uint4(0u, 0u, 0u, 0u)};
     } else {
         constexpr int BB = KT == FA_Q8_0 ? 34 : 18;
         const int o = 8 * (l16 & 3);
@@ -160,13 +169,13 @@ __device__ __forceinline__ uint4 fa_row(const uint8_t* __restrict__ row, int l16
         const int h = KT == FA_Q8_0 ? 1 + (o >> 1) : 1 + ((o & 15) >> 1);
         // halfword pieces of lines the 16 lanes share: ordinary (cached) loads
         const uint32_t b0 = bp[h], b1 = bp[h + 1], b2 = bp[h + 2], b3 = bp[h + 3];
-        return make_uint4(b0 | (b1 << 16), b2 | (b3 << 16), bp[0], 0u);
+        return FaRow{make_uint4(b0 | (b1 << 16), b2 | (b3 << 16), bp[0], 0u), make_uint4(0u, 0u, 0u, 0u)};
     }
 }
 
 // The 8 elements of a quantized slice as signed bytes (Q4_0: the nibbles, not yet offset by -8).
 template <int KT>
-__device__ __forceinline__ uint2 fa_bytes(uint4 r, int lane) {
+__device__ __forceinline__ uint2 fa_bytes(const uint4& r, int lane) {
     if constexpr (KT == FA_Q4_0) {
         const int sh = (lane & 3) >= 2 ? 4 : 0;
         return make_uint2((r.x >> sh) & 0x0F0F0F0Fu, (r.y >> sh) & 0x0F0F0F0Fu);
@@ -225,7 +234,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
         const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
         const uint8_t* kh = k + (size_t)hk * k_head;
         const uint8_t* vh = v + (size_t)hk * v_head;
-        uint4 kr[U], vr[U];
+        FaRow kr[U], vr[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = min(kw0 + 4 * u + grp, n_kv - 1);
@@ -248,20 +257,27 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
             const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) qv[g][e] = KT == FA_F16 ? amv_round_f16(t[e]) : t[e];
-            if constexpr (KT != FA_F16) fa_quant_q(qv[g], qrule, qq[g], qd[g], qsum[g]);
+            if constexpr (KT == FA_Q8_0 || KT == FA_Q4_0) fa_quant_q(qv[g], qrule, qq[g], qd[g], qsum[g]);
         }
         float s[U][G];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = kw0 + 4 * u + grp;
             const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
-            if constexpr (KT == FA_F16) {
-                const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+            if constexpr (KT == FA_F16 || KT == FA_F32) {
                 float kf[8];
+                if constexpr (KT == FA_F32) {
+                    const uint4 x0 = kr[u].a, x1 = kr[u].b;
+                    const uint32_t kw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    kf[2 * e] = amv_h2f(kw[e] & 0xFFFFu);
-                    kf[2 * e + 1] = amv_h2f(kw[e] >> 16);
+                    for (int e = 0; e < 8; ++e) kf[e] = __uint_as_float(kw[e]);
+                } else {
+                    const uint32_t kw[4] = {kr[u].a.x, kr[u].a.y, kr[u].a.z, kr[u].a.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kf[2 * e] = amv_h2f(kw[e] & 0xFFFFu);
+                        kf[2 * e + 1] = amv_h2f(kw[e] >> 16);
+                    }
                 }
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
@@ -272,8 +288,8 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
                     s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
                 }
             } else {
-                const uint2 kb = fa_bytes<KT>(kr[u], lane);
-                const float dk = amv_h2f((uint16_t)kr[u].z);
+                const uint2 kb = fa_bytes<KT>(kr[u].a, lane);
+                const float dk = amv_h2f((uint16_t)kr[u].a.z);
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
                     int is = amv_dot4((int)kb.x, (int)qq[g][0], amv_dot4((int)kb.y, (int)qq[g][1], 0));
@@ -317,16 +333,21 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float vf[8];
-            if constexpr (KT == FA_F16) {
-                const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+            if constexpr (KT == FA_F32) {
+                const uint4 x0 = vr[u].a, x1 = vr[u].b;
+                const uint32_t vw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vf[e] = __uint_as_float(vw[e]);
+            } else if constexpr (KT == FA_F16) {
+                const uint32_t vw[4] = {vr[u].a.x, vr[u].a.y, vr[u].a.z, vr[u].a.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
                     vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
                 }
             } else {  // ggml dequantize_row_q8_0 / q4_0: q * d, (nibble - 8) * d
-                const uint2 vb = fa_bytes<KT>(vr[u], lane);
-                const float dv = amv_h2f((uint16_t)vr[u].z);
+                const uint2 vb = fa_bytes<KT>(vr[u].a, lane);
+                const float dv = amv_h2f((uint16_t)vr[u].a.z);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int lo = KT == FA_Q8_0 ? (int)(int8_t)(vb.x >> (8 * e)) : (int)((vb.x >> (8 * e)) & 0xFF) - 8;
@@ -418,7 +439,8 @@ static int fa_check(const char* fn, int kv, const float* q, const void* k, const
                     const void* ws, const void* act, int rule, int64_t n_head, int64_t n_head_kv, int64_t n_kv,
                     int64_t D, int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int64_t workspace_bytes) {
     AMV_REQUIRE(q && k && v && out && ws, "%s: null pointer", fn);
-    AMV_REQUIRE(kv == AMV_T_F16 || kv == AMV_T_Q8_0 || kv == AMV_T_Q4_0, "%s: KV type %d (F16, Q8_0 or Q4_0)", fn, kv);
+    AMV_REQUIRE(kv == AMV_T_F32 || kv == AMV_T_F16 || kv == AMV_T_Q8_0 || kv == AMV_T_Q4_0,
+                "%s: KV type %d (F32, F16, Q8_0 or Q4_0)", fn, kv);
     AMV_REQUIRE(!act || ((uintptr_t)act & 15) == 0, "%s: act must be 16-byte aligned", fn);
     AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "%s: bad rule", fn);
     AMV_REQUIRE(D == FA_D, "%s: head size %lld not supported (128 is)", fn, (long long)D);
@@ -428,7 +450,11 @@ static int fa_check(const char* fn, int kv, const float* q, const void* k, const
     AMV_REQUIRE(n_kv > 0 && n_kv <= 128LL * FA_MAX_NSPLIT, "%s: n_kv %lld out of range", fn, (long long)n_kv);
     AMV_REQUIRE(n_head_kv <= 65535, "%s: too many KV heads", fn);
     AMV_REQUIRE(k_head >= 0 && v_head >= 0, "%s: negative head stride", fn);
-    if (kv == AMV_T_F16) {
+    if (kv == AMV_T_F32) {
+        AMV_REQUIRE(k_row >= 4 * D && v_row >= 4 * D && k_row % 16 == 0 && v_row % 16 == 0 && k_head % 16 == 0 &&
+                        v_head % 16 == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0,
+                    "%s: f32 K/V rows must be 16-byte aligned", fn);
+    } else if (kv == AMV_T_F16) {
         AMV_REQUIRE(k_row >= 2 * D && v_row >= 2 * D && k_row % 16 == 0 && v_row % 16 == 0 && k_head % 16 == 0 &&
                         v_head % 16 == 0,
                     "%s: f16 K/V strides must be >= D and multiples of 8 elements", fn);
@@ -475,7 +501,10 @@ static void fa_launch_kv(int kv, int G, int kpw, dim3 grid, hipStream_t st, cons
                          const uint8_t* vv, const uint16_t* mm, float* part, int n_kv, const int* n_kv_dev,
                          int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head, int n_split, float scale,
                          int rule, unsigned int* counters, float* out, const AmvActOut& act) {
-    if (kv == AMV_T_Q8_0)
+    if (kv == AMV_T_F32)
+        fa_launch_split<FUSED, FA_F32>(G, kpw, grid, st, q, kk, vv, mm, part, n_kv, n_kv_dev, k_row, k_head, v_row,
+                                       v_head, n_split, scale, rule, counters, out, act);
+    else if (kv == AMV_T_Q8_0)
         fa_launch_split<FUSED, FA_Q8_0>(G, kpw, grid, st, q, kk, vv, mm, part, n_kv, n_kv_dev, k_row, k_head, v_row,
                                         v_head, n_split, scale, rule, counters, out, act);
     else if (kv == AMV_T_Q4_0)

@@ -42,9 +42,10 @@ __global__ __launch_bounds__(256) void k_i2s_quant(const float* __restrict__ x, 
 
 // ---------------------------------------------------------------------------------------------------------------
 // GEMV: a wave owns R rows; the k/64 16-byte slices of a row go to the lanes (slice j: block j/2, bytes
-// 16 (j%2) .. +15, i.e. weights 16 (j%2) + i + 32 g of the block). OUT_SUMS writes the exact integer per row.
+// 16 (j%2) .. +15, i.e. weights 16 (j%2) + i + 32 g of the block). OUT_SUMS writes the exact integer per row; ACC adds
+// the result to dst (the residual add of the BitNet layer, x += W q: llama_bitnet_core.cpp:1244, 1264).
 // ---------------------------------------------------------------------------------------------------------------
-template <int R, bool OUT_SUMS>
+template <int R, bool OUT_SUMS, bool ACC = false>
 __global__ __launch_bounds__(256) void k_i2s_gemv(const uint4* __restrict__ w, int n_rows, int nsl,
                                                  const int8_t* __restrict__ q, const int2* __restrict__ meta,
                                                  float wscale, float* __restrict__ dst, int32_t* __restrict__ isums) {
@@ -88,6 +89,7 @@ __global__ __launch_bounds__(256) void k_i2s_gemv(const uint4* __restrict__ w, i
         const int t = amv_wave_sum_i(acc[r]) - m.y;
         if (lane == 0 && row0 + r < n_rows) {
             if (OUT_SUMS) isums[row0 + r] = t;
+            else if (ACC) dst[row0 + r] = dst[row0 + r] + (float)t * total_scale;
             else dst[row0 + r] = (float)t * total_scale;
         }
     }
@@ -278,6 +280,20 @@ extern "C" int amv_i2s_gemv(const void* w, int64_t n_rows, int64_t k, const void
                             float* dst, int64_t ldd, void* stream) {
     AMV_REQUIRE(dst, "amv_i2s_gemv: null dst");
     return i2s_gemv_impl(w, n_rows, k, act, m, weight_scale, dst, ldd, nullptr, stream);
+}
+
+// dst[r] += float(isum_r) * (act_dequant * weight_scale) for one activation row (the residual add fused)
+extern "C" int amv_i2s_gemv_acc(const void* w, int64_t n_rows, int64_t k, const void* act, float weight_scale,
+                                float* dst, void* stream) {
+    AMV_REQUIRE(w && act && dst, "amv_i2s_gemv_acc: null pointer");
+    AMV_REQUIRE(n_rows > 0 && k > 0 && n_rows <= INT32_MAX && k % 128 == 0, "amv_i2s_gemv_acc: bad shape");
+    AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "amv_i2s_gemv_acc: buffers must be 16-byte aligned");
+    const int waves = (int)((n_rows + 1) / 2);
+    const int8_t* q = (const int8_t*)act;
+    const int2* meta = (const int2*)((const uint8_t*)act + k);
+    hipLaunchKernelGGL((k_i2s_gemv<2, false, true>), dim3((waves + 3) / 4), dim3(256), 0, amv_stream(stream),
+                       (const uint4*)w, (int)n_rows, (int)(k / 64), q, meta, weight_scale, dst, nullptr);
+    return amv_check_launch("amv_i2s_gemv_acc");
 }
 
 extern "C" int amv_i2s_gemv_sums(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m,

@@ -441,6 +441,68 @@ def bench_model(torch, dev, n_prompt: int = 512, n_new: int = 256) -> dict:
                           "graph replayed per token)"}
 
 
+def bench_bitnet(n_tok: int = 128) -> dict:
+    """BitNet b1.58 2B decode through the per-token engine (libac_bitnet_hip.so, the reference's AcBitNetEngine):
+    30 layers of 2560 / 6912 (20 / 5 heads of 128, ReLU^2 FFN with sub norms, RoPE theta 500000), random ternary I2_S
+    weights (P = 1/3 each) and an f16 LM head of 128256 x 2560 (random rows). n_tok tokens from position 0, each one
+    EvalToken call (x in from host memory, x out and all logits back), timed by the host clock around the calls, so
+    the figure includes the two small copies and the graph launch. Bytes per token: every I2_S weight byte, the LM
+    head, and the f32 K / V rows read by the attention (at the mean position)."""
+    import numpy as np
+    from ameva_compute_amd.bitnet_engine import BitNetEngine
+    E, F, H, KVH, HD, NL, V, CTX = 2560, 6912, 20, 5, 128, 30, 128256, 4096
+    rng = np.random.default_rng(2025)
+    # every byte of 4 codes in {0, 1, 2} (code 1 = weight 0): 81 byte values
+    c = np.array([(a << 6) | (b << 4) | (d << 2) | e for a in range(3) for b in range(3) for d in range(3)
+                  for e in range(3)], np.uint8)
+    t0 = time.time()
+    eng = BitNetEngine()
+    eng.configure(E, F, H, KVH, HD, CTX, NL, 1e-5, 500000.0, True)
+    kv = KVH * HD
+    nrm = lambda n: (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)  # noqa: E731
+    w = lambda r, k: c[rng.integers(0, 81, (r, k // 4))]  # noqa: E731
+    wbytes = 0
+    for i in range(NL):
+        lay = dict(attn_norm=nrm(E), attn_sub_norm=nrm(E), ffn_norm=nrm(E), ffn_sub_norm=nrm(F), wq=w(E, E),
+                   wk=w(kv, E), wv=w(kv, E), wo=w(E, E), w_gate=w(F, E), w_up=w(F, E), w_down=w(E, F),
+                   scale_wq=1.2, scale_wk=1.1, scale_wv=0.9, scale_wo=0.03, scale_w_gate=0.8, scale_w_up=0.7,
+                   scale_w_down=0.01)
+        wbytes += sum(lay[n].nbytes for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"))
+        eng.upload_layer(i, lay)
+    block = (rng.standard_normal((1024, E)) * 0.02).astype(np.float16).view(np.uint16)
+    head = np.empty((V, E), np.uint16)
+    for r0 in range(0, V, 1024):
+        head[r0:r0 + 1024] = block[: min(1024, V - r0)]
+    eng.upload_output(nrm(E), head)
+    del head
+    build_s = time.time() - t0
+    x = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    xo = np.empty(E, np.float32)
+    lg = np.empty(V, np.float32)
+    for p in range(4):  # the first call captures the step graph
+        eng.eval_token(p, x, xo, lg)
+    res = {}
+    for name, want_logits in (("with_logits", True), ("no_logits", False)):
+        t0 = time.perf_counter()
+        for p in range(n_tok):
+            eng.eval_token(p, x, xo, lg if want_logits else None)
+        s = (time.perf_counter() - t0) / n_tok
+        kv_bytes = 2 * NL * (n_tok // 2) * kv * 4
+        nbytes = wbytes + kv_bytes + (V * E * 2 if want_logits else 0)
+        res[f"bitnet2b_decode_{name}_ms_per_token"] = round(s * 1e3, 4)
+        res[f"bitnet2b_decode_{name}_tok_s"] = round(1 / s, 1)
+        res[f"bitnet2b_decode_{name}_gbs"] = round(nbytes / s / 1e9, 1)
+        log(f"bench: BitNet 2B decode ({name}) {s * 1e3:.3f} ms/token = {1 / s:.0f} tok/s, "
+            f"{nbytes / 2**20:.0f} MiB/token -> {nbytes / s / 1e9:.0f} GB/s")
+    assert np.isfinite(xo).all() and np.isfinite(lg).all()
+    eng.close()
+    res["bitnet2b_i2s_weight_bytes"] = wbytes
+    res["bitnet2b_note"] = (f"30 BitNet b1.58 2B layers (I2_S) + f16 LM head {V} x {E}, random weights, {n_tok} tokens "
+                            f"from position 0 through AcBitNetEngine::EvalToken (one HIP graph per token), host clock; "
+                            f"built in {build_s:.1f} s")
+    return res
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -474,6 +536,7 @@ def main():
     ap.add_argument("--only-batched", action="store_true", help="only the batched MUL_MAT figures (for profiling)")
     ap.add_argument("--only-model", action="store_true", help="only the 32-layer model figures (for profiling)")
     ap.add_argument("--no-model", action="store_true", help="skip the 32-layer model figures")
+    ap.add_argument("--only-bitnet", action="store_true", help="only the BitNet 2B engine decode figures")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
@@ -503,6 +566,9 @@ def main():
         return
     if args.only_model:
         print(json.dumps(bench_model(torch, dev)), flush=True)
+        return
+    if args.only_bitnet:
+        print(json.dumps(bench_bitnet()), flush=True)
         return
 
     log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")
@@ -552,6 +618,7 @@ def main():
         extra.update(layer_info)
         if not args.no_model:
             extra.update(bench_model(torch, dev))
+            extra.update(bench_bitnet())
 
     result = {
         "metric": "Q4_0 GEMV GB/s (% HBM peak) + bs1 decode tok/s, Llama-8B-shape layer",

@@ -188,6 +188,25 @@ int amv_i2s_gemv_sums(const void* w, int64_t n_rows, int64_t k, const void* act,
 /* Ternary GEMV on f32 activations with the amuda code map {-1, 0, +1, 0} (bitnet_gemv_i2_s_exact, amuda_ops.c:91-121):
  * y f32 [n_rows] = scale * sum_j map(c_rj) x_j; w the BitNet packing above (k % 128 == 0), x f32 [k]. Backs
  * ac_ops_bitnet_gemv_i2_s_exact of libamuda_hip.so. */
+/* dst[r] += float(isum_r) * (act_dequant * weight_scale) for one activation row (I2_S GEMV with the residual add of
+ * the BitNet layer fused: llama_bitnet_core.cpp:1244, 1264). */
+int amv_i2s_gemv_acc(const void* w, int64_t n_rows, int64_t k, const void* act, float weight_scale, float* dst,
+                     void* stream);
+
+/* The BitNet token step's other kernels (the reference engine ac_bitnet_engine.cpp:246-351 over the CPU arithmetic of
+ * llama_bitnet_core.cpp:886-1117):
+ *   amv_bitnet_norm_q8: x = a (mode 0), relu(a)^2 * b (1) or silu(a) * b (2); when do_norm, x = x / sqrt(mean x^2 + eps)
+ *     times w (w may be NULL); y (may be NULL) receives x, act (may be NULL) its int8 activation in the
+ *     amv_i2s_quantize_act layout (quantize_activation_int8). One row of n <= 16384 (n % 16 == 0 with act).
+ *   amv_bitnet_rope_kv: RoPE (pairs i, i + hd/2) of q [n_head][hd] in place and of k [n_head_kv][hd] into row pos[0] of
+ *     k_cache, v into row pos[0] of v_cache (rows of n_head_kv * hd floats), from cs = [cos 0..hd/2-1, sin 0..hd/2-1].
+ *   amv_gemv_f16: y[r] = sum_c f16(w[r][c]) * x[c] (the f16 LM head), k % 8 == 0, 16-byte aligned w and x. */
+int amv_bitnet_norm_q8(const float* a, const float* b, const float* w, int64_t n, float eps, int mode, int do_norm,
+                       float* y, void* act, void* stream);
+int amv_bitnet_rope_kv(float* q, const float* k, const float* v, const float* cs, float* k_cache, float* v_cache,
+                       const int32_t* pos, int64_t n_head, int64_t n_head_kv, int64_t hd, int64_t n_ctx, void* stream);
+int amv_gemv_f16(const void* w, int64_t n_rows, int64_t k, const float* x, float* y, void* stream);
+
 int amv_i2s_gemv_f32(const void* w, int64_t n_rows, int64_t k, const float* x, float scale, float* y, void* stream);
 
 /* ------------------------------------------------------------------------------------------------------------
@@ -258,9 +277,10 @@ int amv_flash_attn_decode_ex(const float* q, const void* k, const void* v, const
                              void* workspace, int64_t workspace_bytes, unsigned int* counters, void* act, int act_type,
                              int rule, void* stream);
 
-/* FLASH_ATTN_EXT decode over an f16, Q8_0 or Q4_0 KV cache (the reference's quantized-cache attention,
- * ameva_flash_attn.comp:4-8 and 104-136; ggml_compute_forward_flash_attn_ext for the CPU semantics). kv_type: 1 = F16,
- * 8 = Q8_0, 2 = Q4_0 (K and V both); strides in BYTES (ggml's nb[1], nb[2]); a quantized row of D = 128 elements is 4
+/* FLASH_ATTN_EXT decode over an f32, f16, Q8_0 or Q4_0 KV cache (the reference's quantized-cache attention,
+ * ameva_flash_attn.comp:4-8 and 104-136; ggml_compute_forward_flash_attn_ext for the CPU semantics; the f32 cache is
+ * the BitNet engine's, llama_bitnet_core.cpp:1033-1082, with q . k in f32). kv_type: 0 = F32, 1 = F16, 8 = Q8_0,
+ * 2 = Q4_0 (K and V both); strides in BYTES (ggml's nb[1], nb[2]); a quantized row of D = 128 elements is 4
  * ggml blocks (136 bytes Q8_0, 72 bytes Q4_0) at a 2-byte-aligned address. For a quantized K, q is quantized to Q8_0
  * with `rule` (K's vec_dot_type, as ggml's CPU kernel does) and each score is sum_b float(isum_b) * (d_k * d_q) over
  * the exact integer block sums; V rows are dequantized exactly (q * d, (nibble - 8) * d); f16 caches behave as in

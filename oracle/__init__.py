@@ -53,6 +53,11 @@ def lib() -> ctypes.CDLL:
             "orc_flash_attn_decode_q": (ctypes.c_int, [ctypes.c_int, P, P, P, P, P, I64, I64, I64, I64, F,
                                                        ctypes.c_int]),
             "orc_i2s_quantize_act": (F, [P, P, I64]),
+            "orc_bitnet_rms_norm": (None, [P, P, P, I64, F]),
+            "orc_bitnet_gemv_f16": (None, [P, P, P, I64, I64]),
+            "orc_bitnet_attention": (None, [P, P, P, P, I64, I64, I64, I64]),
+            "orc_bitnet_token": (None, [P, I64, I64, I64, I64, I64, I64, I64, F, F, ctypes.c_int, P, P, I64, P, P,
+                                        P, I64, P]),
             "orc_i2s_dot_row": (I64, [I64, P, P, P]),
             "orc_i2s_gemv": (None, [P, I64, I64, P, P, I64, F, P, P]),
             "orc_i2s_dequantize": (None, [P, F, I64, P]),
@@ -295,3 +300,73 @@ class RefI2S:
         s = np.empty(n_rows, dtype=np.float32)
         self.fn(k, _p(s), 1, _p(w), k, _p(q), k, n_rows, 0)
         return s
+
+
+class BitnetLayer(ctypes.Structure):
+    """OrcBitnetLayer: one BitNet layer on the host (F32 norms, sub norms may be NULL; I2_S projections; scales)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm", "wq", "wk",
+                                               "wv", "wo", "w_gate", "w_up", "w_down")] + \
+               [(n, ctypes.c_float) for n in ("scale_wq", "scale_wk", "scale_wv", "scale_wo", "scale_w_gate",
+                                              "scale_w_up", "scale_w_down")]
+
+
+def bitnet_rms_norm(x: np.ndarray, w, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    wp = None if w is None else _p(np.ascontiguousarray(w, dtype=np.float32))
+    lib().orc_bitnet_rms_norm(_p(out), _p(x), wp, x.size, eps)
+    return out
+
+
+def bitnet_gemv_f16(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(w.shape[0], np.float32)
+    lib().orc_bitnet_gemv_f16(_p(out), _p(w), _p(x), w.shape[1], w.shape[0])
+    return out
+
+
+def bitnet_attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos: int, n_kv_heads: int) -> np.ndarray:
+    """q [n_heads, hd]; kc, vc [n_ctx, n_kv_heads * hd] of one layer; keys 0 .. pos."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kc, dtype=np.float32)
+    vc = np.ascontiguousarray(vc, dtype=np.float32)
+    out = np.empty_like(q)
+    lib().orc_bitnet_attention(_p(out), _p(q), _p(kc), _p(vc), pos, q.shape[0], n_kv_heads, q.shape[1])
+    return out
+
+
+class BitnetModel:
+    """A BitNet model on the host for orc_bitnet_token: layers (list of dicts of numpy arrays and scales), caches
+    [n_layers, n_ctx, kv] kept here between tokens."""
+
+    def __init__(self, cfg: dict, layers: list, out_norm: np.ndarray, lm_head: np.ndarray):
+        self.cfg = cfg
+        self.keep = []
+        arr = (BitnetLayer * len(layers))()
+        for i, L in enumerate(layers):
+            for n in ("attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm", "wq", "wk", "wv", "wo", "w_gate",
+                      "w_up", "w_down"):
+                a = L.get(n)
+                if a is not None:
+                    a = np.ascontiguousarray(a)
+                    self.keep.append(a)
+                    setattr(arr[i], n, a.ctypes.data)
+            for n in ("scale_wq", "scale_wk", "scale_wv", "scale_wo", "scale_w_gate", "scale_w_up", "scale_w_down"):
+                setattr(arr[i], n, float(L.get(n, 1.0)))
+        self.layers = arr
+        self.out_norm = np.ascontiguousarray(out_norm, dtype=np.float32)
+        self.lm_head = np.ascontiguousarray(lm_head, dtype=np.uint16)
+        kv = cfg["n_kv_heads"] * cfg["head_dim"]
+        self.kc = np.zeros((len(layers), cfg["n_ctx"], kv), np.float32)
+        self.vc = np.zeros_like(self.kc)
+
+    def token(self, pos: int, x: np.ndarray, logits: bool = True):
+        c = self.cfg
+        x = np.array(x, dtype=np.float32)
+        lg = np.empty(self.lm_head.shape[0], np.float32) if logits else None
+        lib().orc_bitnet_token(self.layers, len(self.layers), c["n_embd"], c["n_ffn"], c["n_heads"], c["n_kv_heads"],
+                               c["head_dim"], c["n_ctx"], c["norm_eps"], c["rope_theta"], int(c["relu2"]),
+                               _p(self.kc), _p(self.vc), pos, _p(x), _p(self.out_norm), _p(self.lm_head),
+                               self.lm_head.shape[0], None if lg is None else _p(lg))
+        return x, lg

@@ -632,3 +632,146 @@ float orc_i2s_trailer_scale(const uint8_t *tensor, int64_t n_rows, int64_t k) {
     memcpy(&s, tensor + n_rows * (k / 4), 4);
     return s;
 }
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * BitNet b1.58 token step of the CPU path (llama_bitnet_core.cpp:1186-1300), the arithmetic the reference's GPU
+ * engine (ac_bitnet_engine.cpp) and this build's engine follow. Non-NEON branches: sums are sequential f32.
+ * ---------------------------------------------------------------------------------------------------------------- */
+
+/* rms_norm (:886-912), F32 weight or none: scale = 1 / sqrt(sum x^2 / dim + eps), out = x * scale * w. */
+void orc_bitnet_rms_norm(float *out, const float *x, const float *w, int64_t dim, float eps) {
+    float sum_sq = 0.0f;
+    for (int64_t i = 0; i < dim; ++i) sum_sq += x[i] * x[i];
+    const float scale = 1.0f / sqrtf(sum_sq / (float)dim + eps);
+    for (int64_t i = 0; i < dim; ++i) out[i] = w ? x[i] * scale * w[i] : x[i] * scale;
+}
+
+/* bitnet_gemv for an I2_S weight (:928-940): out[r] = float(isum_r) * (dequant * weight_scale). */
+static void bitnet_i2s_gemv(float *out, const uint8_t *w, const int8_t *q, float dequant, int64_t in_dim,
+                            int64_t out_dim, float weight_scale) {
+    const float total = dequant * weight_scale;
+    for (int64_t r = 0; r < out_dim; ++r) out[r] = (float)orc_i2s_dot_row(in_dim, w + r * (in_dim / 4), q, NULL) * total;
+}
+
+/* bitnet_gemv for an F16 weight, scalar branch (:992-995): out[r] = sum_c f16(w[r][c]) * x[c], sequential f32. */
+void orc_bitnet_gemv_f16(float *out, const uint16_t *w, const float *x, int64_t in_dim, int64_t out_dim) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < out_dim; ++r) {
+        float sum = 0.0f;
+        const uint16_t *row = w + r * in_dim;
+        for (int64_t c = 0; c < in_dim; ++c) sum += orc_fp16_to_fp32(row[c]) * x[c];
+        out[r] = sum;
+    }
+}
+
+/* apply_rope (:1006-1020): pairs (i, i + head_dim / 2), theta = pos / theta_base^(2i / head_dim). */
+static void bitnet_rope(float *vec, int64_t pos, int64_t n_heads, int64_t head_dim, float theta_base) {
+    const int64_t half = head_dim / 2;
+    for (int64_t h = 0; h < n_heads; ++h) {
+        float *hp = vec + h * head_dim;
+        for (int64_t i = 0; i < half; ++i) {
+            const float theta = (float)pos / powf(theta_base, (float)(2 * i) / (float)head_dim);
+            const float c = cosf(theta), s = sinf(theta);
+            const float v0 = hp[i], v1 = hp[i + half];
+            hp[i] = v0 * c - v1 * s;
+            hp[i + half] = v1 * c + v0 * s;
+        }
+    }
+}
+
+/* multi_head_attention (:1033-1082) over cache rows [n_ctx][n_kv_heads * head_dim] of one layer, keys 0 .. pos. */
+void orc_bitnet_attention(float *out, const float *q, const float *kc, const float *vc, int64_t pos, int64_t n_heads,
+                          int64_t n_kv_heads, int64_t head_dim) {
+    const float inv_sqrt = 1.0f / sqrtf((float)head_dim);
+    const int64_t G = n_heads / n_kv_heads, kv = n_kv_heads * head_dim;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)(pos + 1));
+    for (int64_t h = 0; h < n_heads; ++h) {
+        const int64_t kh = h / G;
+        const float *qh = q + h * head_dim;
+        float max_score = -1e9f;
+        for (int64_t p = 0; p <= pos; ++p) {
+            const float *k = kc + p * kv + kh * head_dim;
+            float dot = 0.0f;
+            for (int64_t d = 0; d < head_dim; ++d) dot += qh[d] * k[d];
+            scores[p] = dot * inv_sqrt;
+            if (scores[p] > max_score) max_score = scores[p];
+        }
+        float sum_exp = 0.0f;
+        for (int64_t p = 0; p <= pos; ++p) {
+            scores[p] = expf(scores[p] - max_score);
+            sum_exp += scores[p];
+        }
+        const float inv_sum = 1.0f / (sum_exp + 1e-9f);
+        float *oh = out + h * head_dim;
+        for (int64_t d = 0; d < head_dim; ++d) oh[d] = 0.0f;
+        for (int64_t p = 0; p <= pos; ++p) {
+            const float wgt = scores[p] * inv_sum;
+            const float *v = vc + p * kv + kh * head_dim;
+            for (int64_t d = 0; d < head_dim; ++d) oh[d] += wgt * v[d];
+        }
+    }
+    free(scores);
+}
+
+/* One layer's tensors on the host (BitNetLayerWeights of the CPU path): F32 norms (sub norms may be NULL), I2_S
+ * projections (out_rows * in_dim / 4 bytes) and their scales. */
+typedef struct {
+    const float *attn_norm, *attn_sub_norm, *ffn_norm, *ffn_sub_norm;
+    const uint8_t *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down;
+    float scale_wq, scale_wk, scale_wv, scale_wo, scale_w_gate, scale_w_up, scale_w_down;
+} OrcBitnetLayer;
+
+/* bitnet_eval for one token at pos (:1186-1300): x [n_embd] in and out (the residual stream after the last layer);
+ * caches [n_layers][n_ctx][n_kv_heads * head_dim] (row pos written here); logits (may be NULL): the final norm and
+ * the F16 LM head [n_vocab][n_embd]. relu2: relu(g)^2 * u with ffn_sub_norm, else silu(g) * u. */
+void orc_bitnet_token(const OrcBitnetLayer *layers, int64_t n_layers, int64_t n_embd, int64_t n_ffn, int64_t n_heads,
+                      int64_t n_kv_heads, int64_t head_dim, int64_t n_ctx, float norm_eps, float rope_theta, int relu2,
+                      float *k_cache, float *v_cache, int64_t pos, float *x, const float *out_norm,
+                      const uint16_t *lm_head, int64_t n_vocab, float *logits) {
+    const int64_t E = n_embd, F = n_ffn, kv = n_kv_heads * head_dim;
+    const int64_t vmax = E > F ? E : F;
+    float *xn = (float *)malloc(sizeof(float) * (size_t)vmax), *q = (float *)malloc(sizeof(float) * (size_t)E);
+    float *k = (float *)malloc(sizeof(float) * (size_t)kv), *v = (float *)malloc(sizeof(float) * (size_t)kv);
+    float *att = (float *)malloc(sizeof(float) * (size_t)E), *o = (float *)malloc(sizeof(float) * (size_t)E);
+    float *g = (float *)malloc(sizeof(float) * (size_t)F), *u = (float *)malloc(sizeof(float) * (size_t)F);
+    int8_t *q8 = (int8_t *)malloc((size_t)vmax);
+    for (int64_t l = 0; l < n_layers; ++l) {
+        const OrcBitnetLayer *L = layers + l;
+        float *kc = k_cache + l * n_ctx * kv, *vc = v_cache + l * n_ctx * kv;
+        orc_bitnet_rms_norm(xn, x, L->attn_norm, E, norm_eps);
+        float dq = orc_i2s_quantize_act(xn, q8, E);
+        bitnet_i2s_gemv(q, L->wq, q8, dq, E, E, L->scale_wq);
+        bitnet_i2s_gemv(k, L->wk, q8, dq, E, kv, L->scale_wk);
+        bitnet_i2s_gemv(v, L->wv, q8, dq, E, kv, L->scale_wv);
+        bitnet_rope(q, pos, n_heads, head_dim, rope_theta);
+        bitnet_rope(k, pos, n_kv_heads, head_dim, rope_theta);
+        memcpy(kc + pos * kv, k, sizeof(float) * (size_t)kv);
+        memcpy(vc + pos * kv, v, sizeof(float) * (size_t)kv);
+        orc_bitnet_attention(att, q, kc, vc, pos, n_heads, n_kv_heads, head_dim);
+        if (L->attn_sub_norm) orc_bitnet_rms_norm(att, att, L->attn_sub_norm, E, norm_eps);
+        dq = orc_i2s_quantize_act(att, q8, E);
+        bitnet_i2s_gemv(o, L->wo, q8, dq, E, E, L->scale_wo);
+        for (int64_t i = 0; i < E; ++i) x[i] += o[i];
+        orc_bitnet_rms_norm(xn, x, L->ffn_norm, E, norm_eps);
+        dq = orc_i2s_quantize_act(xn, q8, E);
+        bitnet_i2s_gemv(g, L->w_gate, q8, dq, E, F, L->scale_w_gate);
+        bitnet_i2s_gemv(u, L->w_up, q8, dq, E, F, L->scale_w_up);
+        for (int64_t i = 0; i < F; ++i) {
+            if (relu2) {
+                const float r = g[i] > 0.0f ? g[i] : 0.0f;
+                g[i] = (r * r) * u[i];
+            } else {
+                g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+            }
+        }
+        if (L->ffn_sub_norm) orc_bitnet_rms_norm(g, g, L->ffn_sub_norm, F, norm_eps);
+        dq = orc_i2s_quantize_act(g, q8, F);
+        bitnet_i2s_gemv(o, L->w_down, q8, dq, F, E, L->scale_w_down);
+        for (int64_t i = 0; i < E; ++i) x[i] += o[i];
+    }
+    if (logits) {
+        orc_bitnet_rms_norm(xn, x, out_norm, E, norm_eps);
+        orc_bitnet_gemv_f16(logits, lm_head, xn, E, n_vocab);
+    }
+    free(xn); free(q); free(k); free(v); free(att); free(o); free(g); free(u); free(q8);
+}
