@@ -67,9 +67,8 @@ struct AcBitNetEngine::Impl {
     BitNetGpuConfig cfg;
     std::vector<Layer> layers;
     // scratch
-    float *x = nullptr, *y = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *gate = nullptr,
-          *up = nullptr, *cs = nullptr, *logits = nullptr, *out_norm = nullptr;
-    uint8_t* act = nullptr;
+    float *x = nullptr, *y = nullptr, *q = nullptr, *att = nullptr, *gate = nullptr, *up = nullptr, *cs = nullptr,
+          *logits = nullptr, *out_norm = nullptr;
     int32_t* pos_dev = nullptr;  // [pos, n_kv]
     void* fa_ws = nullptr;
     int64_t fa_ws_bytes = 0;
@@ -119,37 +118,47 @@ struct AcBitNetEngine::Impl {
             if (t) t->mark(n);
         };
         mark("start");
+        const float eps = cfg.norm_eps;
         for (const Layer& L : layers) {
-            amv_check(amv_bitnet_norm_q8(x, nullptr, L.attn_norm, E, cfg.norm_eps, 0, 1, nullptr, act, st), "attn_norm + q8");
-            mark("norm_q8");
-            amv_check(amv_i2s_gemv(L.wq, H * hd, E, act, 1, L.s_q, q, H * hd, st), "attn_q");
-            amv_check(amv_i2s_gemv(L.wk, kv, E, act, 1, L.s_k, k, kv, st), "attn_k");
-            amv_check(amv_i2s_gemv(L.wv, kv, E, act, 1, L.s_v, v, kv, st), "attn_v");
-            mark("gemv_i2s");
-            amv_check(amv_bitnet_rope_kv(q, k, v, cs, L.kc, L.vc, pos_dev, H, KVH, hd, cfg.n_ctx, st), "rope + kv");
-            mark("rope_kv");
+            // attn_norm + int8 -> Q | K | V -> RoPE -> k, v into the cache row of the position: one launch
+            const void* w_qkv[3] = {L.wq, L.wk, L.wv};
+            const int64_t r_qkv[3] = {(int64_t)H * hd, kv, kv};
+            const float s_qkv[3] = {L.s_q, L.s_k, L.s_v};
+            float* d_qkv[3] = {q, L.kc, L.vc};
+            amv_check(amv_bitnet_gemv_fused(x, nullptr, L.attn_norm, E, eps, 0, 1, 3, w_qkv, r_qkv, s_qkv, d_qkv, 0, cs,
+                                            pos_dev, cfg.n_ctx, st),
+                      "attn_norm + q8 + attn_q/k/v + rope");
+            mark("norm_qkv_rope");
             amv_check(amv_flash_attn_decode_kv(0, q, L.kc, L.vc, nullptr, att, H, KVH, cfg.n_ctx, pos_dev + 1, hd,
                                                (int64_t)kv * 4, (int64_t)hd * 4, (int64_t)kv * 4, (int64_t)hd * 4,
                                                inv_sqrt, fa_ws, fa_ws_bytes, nullptr, nullptr, 8, 0, st),
                       "attention");
             mark("attention");
-            amv_check(amv_bitnet_norm_q8(att, nullptr, L.attn_sub_norm, E, cfg.norm_eps, 0, L.has_attn_sub ? 1 : 0,
-                                         nullptr, act, st),
-                      "attn_sub_norm + q8");
-            mark("norm_q8");
-            amv_check(amv_i2s_gemv_acc(L.wo, E, E, act, L.s_o, x, st), "attn_output + residual");
-            mark("gemv_i2s");
-            amv_check(amv_bitnet_norm_q8(x, nullptr, L.ffn_norm, E, cfg.norm_eps, 0, 1, nullptr, act, st), "ffn_norm + q8");
-            mark("norm_q8");
-            amv_check(amv_i2s_gemv(L.wg, F, E, act, 1, L.s_g, gate, F, st), "ffn_gate");
-            amv_check(amv_i2s_gemv(L.wu, F, E, act, 1, L.s_u, up, F, st), "ffn_up");
-            mark("gemv_i2s");
-            amv_check(amv_bitnet_norm_q8(gate, up, L.ffn_sub_norm, F, cfg.norm_eps, cfg.relu2_ffn ? 1 : 2,
-                                         L.has_ffn_sub ? 1 : 0, nullptr, act, st),
-                      "ffn activation + ffn_sub_norm + q8");
-            mark("norm_q8");
-            amv_check(amv_i2s_gemv_acc(L.wd, E, F, act, L.s_d, x, st), "ffn_down + residual");
-            mark("gemv_i2s");
+            // attn_sub_norm (when present) + int8 -> output projection added to x
+            const void* w_o[1] = {L.wo};
+            const int64_t r_e[1] = {E};
+            const float s_o[1] = {L.s_o};
+            float* d_x[1] = {x};
+            amv_check(amv_bitnet_gemv_fused(att, nullptr, L.attn_sub_norm, E, eps, 0, L.has_attn_sub ? 1 : 0, 1, w_o,
+                                            r_e, s_o, d_x, 1, nullptr, nullptr, 0, st),
+                      "attn_sub_norm + q8 + attn_output + residual");
+            mark("norm_o");
+            // ffn_norm + int8 -> gate | up
+            const void* w_gu[2] = {L.wg, L.wu};
+            const int64_t r_gu[2] = {F, F};
+            const float s_gu[2] = {L.s_g, L.s_u};
+            float* d_gu[2] = {gate, up};
+            amv_check(amv_bitnet_gemv_fused(x, nullptr, L.ffn_norm, E, eps, 0, 1, 2, w_gu, r_gu, s_gu, d_gu, 0, nullptr,
+                                            nullptr, 0, st),
+                      "ffn_norm + q8 + ffn_gate/up");
+            mark("norm_gate_up");
+            // relu(gate)^2 * up or silu(gate) * up -> ffn_sub_norm (when present) + int8 -> down projection added to x
+            const void* w_d[1] = {L.wd};
+            const float s_d[1] = {L.s_d};
+            amv_check(amv_bitnet_gemv_fused(gate, up, L.ffn_sub_norm, F, eps, cfg.relu2_ffn ? 1 : 2,
+                                            L.has_ffn_sub ? 1 : 0, 1, w_d, r_e, s_d, d_x, 1, nullptr, nullptr, 0, st),
+                      "ffn activation + ffn_sub_norm + q8 + ffn_down + residual");
+            mark("act_norm_down");
         }
         if (with_head) {
             amv_check(amv_bitnet_norm_q8(x, nullptr, out_norm, E, cfg.norm_eps, 0, 1, y, nullptr, st), "output_norm");
@@ -320,17 +329,13 @@ void AcBitNetEngine::Configure(const BitNetGpuConfig& cfg) {
         hip_check(hipMemsetAsync(L.vc, 0, kvb, m.st), "clear V cache");
         m.kv_bytes += 2 * kvb;
     }
-    const uint32_t vmax = std::max(E, F);
     m.x = (float*)m.dev_alloc(4ull * E, "x");
     m.y = (float*)m.dev_alloc(4ull * E, "x normalized");
     m.q = (float*)m.dev_alloc(4ull * qd, "q");
-    m.k = (float*)m.dev_alloc(4ull * kv, "k");
-    m.v = (float*)m.dev_alloc(4ull * kv, "v");
     m.att = (float*)m.dev_alloc(4ull * qd, "attention");
     m.gate = (float*)m.dev_alloc(4ull * F, "gate");
     m.up = (float*)m.dev_alloc(4ull * F, "up");
     m.cs = (float*)m.dev_alloc(4ull * hd, "rope table");
-    m.act = (uint8_t*)m.dev_alloc(vmax + 16, "int8 activation");
     m.pos_dev = (int32_t*)m.dev_alloc(8, "position");
     m.fa_ws_bytes = amv_flash_attn_workspace_bytes(cfg.n_heads, cfg.n_kv_heads, cfg.n_ctx, hd);
     if (m.fa_ws_bytes <= 0) throw AcBitNetError("attention workspace", (int)AC_ERR_INVALID_ARGUMENT);

@@ -203,3 +203,305 @@ extern "C" int amv_gemv_f16(const void* w, int64_t n_rows, int64_t k, const floa
                        (const uint4*)w, (int)n_rows, (int)(k / 8), (const float4*)x, y);
     return amv_check_launch("amv_gemv_f16");
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// One launch per projection group of the BitNet token step: the activation of the group's input vector (FFN
+// activation, RMS_NORM, quantize_activation_int8 exactly as k_bitnet_norm_q8) is computed by EVERY workgroup into its
+// own LDS, then the workgroup's rows of up to three stacked I2_S matrices (Q | K | V, or gate | up) are dotted against
+// it from LDS. The input vector is a few KB and sits in L2, so recomputing it per workgroup costs less than the
+// launch and the global round trip it replaces; the weight rows of the wave are requested right after the prologue's
+// own loads and arrive while it runs. Epilogue per row: float(isum - sum q) * (dequant * scale_of_its_matrix), written
+// or added (the residual add). ROPE: the wave's rows are pairs (i, i + 64) of one 128-row head (rows of every matrix
+// are a multiple of 128), so the rotation of apply_rope is done in registers with the position's cos / sin table, q is
+// written rotated, k rotated and v as is into the f32 cache rows of the position read from device memory (the
+// separate k_bitnet_rope_kv path computes the same values).
+// NT threads (NT / 64 waves, R rows per wave), V4 float4 of the input per thread: k <= 4 * NT * V4. Reductions are
+// DPP within rows plus readlanes (no LDS round trips), and every load before the first barrier is unconditional.
+// ---------------------------------------------------------------------------------------------------------------
+
+struct BnSegs {
+    const uint4* w[3];  // rows of matrix s: [end[s - 1], end[s]), each k / 4 bytes
+    float* dst[3];
+    float wscale[3];
+    int end[3];
+};
+
+__device__ __forceinline__ int bn_seg(const BnSegs& sg, int r) { return r < sg.end[0] ? 0 : (r < sg.end[1] ? 1 : 2); }
+// field s of the segment table by selects over constant indices: an indexed read of the kernel-argument struct
+// becomes a vector load from memory with a full wait in front of the weight loads
+template <typename T>
+__device__ __forceinline__ T bn_pick(int s, T v0, T v1, T v2) { return s == 0 ? v0 : (s == 1 ? v1 : v2); }
+__device__ __forceinline__ int bn_beg(const BnSegs& sg, int s) { return bn_pick(s, 0, sg.end[0], sg.end[1]); }
+
+template <int MODE>
+__device__ __forceinline__ float bn_act_t(float x, float y) {
+    if constexpr (MODE == 1) {
+        const float r = x > 0.0f ? x : 0.0f;
+        return (r * r) * y;
+    } else if constexpr (MODE == 2) {
+        return (x / (1.0f + expf(-x))) * y;
+    } else {
+        return x;
+    }
+}
+
+template <int NT, int V4, bool ROPE, int MODE, int R>
+__global__ __launch_bounds__(NT) void k_bitnet_qgemv(const float4* __restrict__ a, const float4* __restrict__ b,
+                                                    const float4* __restrict__ nw, int k, float eps, int do_norm, const BnSegs sg, int n_seg, int accumulate,
+                                                    const float* __restrict__ cs, const int* __restrict__ pos,
+                                                    int n_ctx) {
+    constexpr int NW = NT / 64, NIT = (NT * V4 + 1023) / 1024;  // k <= 4 NT V4: 16-byte weight slices <= 64 NIT
+    __shared__ __align__(16) int sq[NT * V4];  // the int8 activation, 4 per int
+    __shared__ double sd[NW];
+    __shared__ float sf[NW];
+    __shared__ int si[NW];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n_rows = sg.end[n_seg - 1];
+    const int wave = blockIdx.x * NW + wv;
+    // rows of the wave: R consecutive rows, or with ROPE R / 2 pairs (i, i + 64) of one 128-row head
+    int rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (ROPE) {
+            constexpr int PW = 64 / (R / 2);  // waves per head
+            const int i = (wave % PW) + PW * (r >> 1);
+            rows[r] = (wave / PW) * 128 + i + 64 * (r & 1);
+        } else {
+            rows[r] = R * wave + r;
+        }
+    }
+    const bool active = rows[0] < n_rows;  // uniform per wave; every wave takes part in the prologue
+    const int nsl = k >> 6;                // 16-byte slices per weight row
+    // prologue: x = act(a, b); v = RMS_NORM(x) (* w); q = int8(v). Its loads are issued first and the weight rows
+    // of the wave right after them: loads complete in order, so the prologue waits only for its own data while the
+    // weights stream in.
+    const int n4 = k >> 2;
+    // every load is unconditional (an absent norm_w reads a instead; rows past the end read the last row): a load
+    // under a branch makes the wait at the join conservative, i.e. a wait for the weights before the prologue
+    const float4* wp = nw ? nw : a;
+    float4 xv[V4], bv[V4], wn[V4];
+#pragma unroll
+    for (int u = 0; u < V4; ++u) xv[u] = a[min(tid + NT * u, n4 - 1)];
+    if constexpr (MODE != 0) {
+#pragma unroll
+        for (int u = 0; u < V4; ++u) bv[u] = b[min(tid + NT * u, n4 - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < V4; ++u) wn[u] = wp[min(tid + NT * u, n4 - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep the weight loads behind the prologue's
+    uint4 c[R][NIT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(rows[r], n_rows - 1);
+        const int s = bn_seg(sg, row);
+        const uint4* wr = bn_pick(s, sg.w[0], sg.w[1], sg.w[2]) + (size_t)(row - bn_beg(sg, s)) * nsl;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) c[r][it] = amv_ld_stream(wr + min(it * 64 + lane, nsl - 1));
+    }
+    // branch-free from here to the first barrier (a branch would let the compiler sink the prologue loads behind
+    // the weight loads): scale 1 without the norm and weight 1 without norm_w (x * 1 = x)
+#pragma unroll
+    for (int u = 0; u < V4; ++u) {
+        const bool in = tid + NT * u < n4;
+        if constexpr (MODE != 0) {
+            xv[u].x = bn_act_t<MODE>(xv[u].x, bv[u].x);
+            xv[u].y = bn_act_t<MODE>(xv[u].y, bv[u].y);
+            xv[u].z = bn_act_t<MODE>(xv[u].z, bv[u].z);
+            xv[u].w = bn_act_t<MODE>(xv[u].w, bv[u].w);
+        }
+        if (!in) xv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int u = 0; u < V4; ++u)
+        ss += (double)xv[u].x * xv[u].x + (double)xv[u].y * xv[u].y + (double)xv[u].z * xv[u].z +
+              (double)xv[u].w * xv[u].w;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, AMV_WAVE);
+    if (lane == 0) sd[wv] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) tot += sd[i];
+    const float scale = do_norm ? 1.0f / sqrtf((float)tot / (float)k + eps) : 1.0f;
+    const bool use_w = do_norm && nw;
+#pragma unroll
+    for (int u = 0; u < V4; ++u) {
+        xv[u].x = (xv[u].x * scale) * (use_w ? wn[u].x : 1.0f);
+        xv[u].y = (xv[u].y * scale) * (use_w ? wn[u].y : 1.0f);
+        xv[u].z = (xv[u].z * scale) * (use_w ? wn[u].z : 1.0f);
+        xv[u].w = (xv[u].w * scale) * (use_w ? wn[u].w : 1.0f);
+    }
+    float amax = 1e-7f;
+#pragma unroll
+    for (int u = 0; u < V4; ++u)
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xv[u].x), fabsf(xv[u].y)), fmaxf(fabsf(xv[u].z), fabsf(xv[u].w))));
+    amax = amv_wave_max_u(amax);
+    if (lane == 0) sf[wv] = amax;
+    __syncthreads();
+    amax = sf[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) amax = fmaxf(amax, sf[i]);
+    const float qs = 127.0f / amax;
+    int isum = 0;
+#pragma unroll
+    for (int u = 0; u < V4; ++u) {
+        const int i = tid + NT * u;
+        if (i < n4) {
+            const float t[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+            uint32_t packed = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int qi = (int)fminf(127.0f, fmaxf(-127.0f, roundf(t[e] * qs)));
+                isum += qi;
+                packed |= (uint32_t)(qi & 0xFF) << (8 * e);
+            }
+            sq[i] = (int)packed;
+        }
+    }
+    isum = amv_wave_sum_i_u(isum);
+    if (lane == 0) si[wv] = isum;
+    __syncthreads();
+    int qsum = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) qsum += si[i];
+    if (!active) return;
+    // the ternary dots from LDS (lane j: 16 weight bytes = 64 weights of 128-block j / 2, half j % 2)
+    const int4* aq = reinterpret_cast<const int4*>(sq);
+    int acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int j = it * 64 + lane;
+        if (j < nsl) {
+            const int bb = j >> 1, p = j & 1;
+            int4 av[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) av[g] = aq[bb * 8 + 2 * g + p];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                int s = acc[r];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int sh = 6 - 2 * g;
+                    s = amv_dot4((int)((c[r][it].x >> sh) & 0x03030303u), av[g].x, s);
+                    s = amv_dot4((int)((c[r][it].y >> sh) & 0x03030303u), av[g].y, s);
+                    s = amv_dot4((int)((c[r][it].z >> sh) & 0x03030303u), av[g].z, s);
+                    s = amv_dot4((int)((c[r][it].w >> sh) & 0x03030303u), av[g].w, s);
+                }
+                acc[r] = s;
+            }
+        }
+    }
+    const float dq = 1.0f / qs;
+    int t[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) t[r] = amv_wave_sum_i_u(acc[r]) - qsum;
+    if (lane != 0) return;
+    if (ROPE) {
+        const int s = bn_seg(sg, rows[0]);  // every row of the wave is in one matrix (128-row heads)
+        const int beg = bn_beg(sg, s);
+        const float ts = dq * bn_pick(s, sg.wscale[0], sg.wscale[1], sg.wscale[2]);
+        const int width = sg.end[1] - sg.end[0];     // K and V rows are equal (checked on the host)
+        const int p = min(max(*pos, 0), n_ctx - 1);  // the host checks the position; clamped for memory safety
+#pragma unroll
+        for (int h = 0; h < R / 2; ++h) {
+            const int r0 = rows[2 * h], r1 = rows[2 * h + 1];
+            const float v0 = (float)t[2 * h] * ts, v1 = (float)t[2 * h + 1] * ts;
+            const int i = r0 & 127, local = r0 - beg;
+            if (s == 0) {
+                const float cc = cs[i], sn = cs[64 + i];
+                sg.dst[0][r0] = v0 * cc - v1 * sn;
+                sg.dst[0][r1] = v1 * cc + v0 * sn;
+            } else {
+                float* row = (s == 1 ? sg.dst[1] : sg.dst[2]) + (size_t)p * width + local;
+                if (s == 1) {
+                    const float cc = cs[i], sn = cs[64 + i];
+                    row[0] = v0 * cc - v1 * sn;
+                    row[64] = v1 * cc + v0 * sn;
+                } else {
+                    row[0] = v0;
+                    row[64] = v1;
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = rows[r];
+        if (row >= n_rows) break;
+        const int s = bn_seg(sg, row);
+        const float out = (float)t[r] * (dq * bn_pick(s, sg.wscale[0], sg.wscale[1], sg.wscale[2]));
+        float* d = bn_pick(s, sg.dst[0], sg.dst[1], sg.dst[2]) + (row - bn_beg(sg, s));
+        if (accumulate) *d = *d + out;
+        else *d = out;
+    }
+}
+
+extern "C" int amv_bitnet_gemv_fused(const float* a, const float* b, const float* norm_w, int64_t k, float eps,
+                                     int mode, int do_norm, int n_seg, const void* const* w, const int64_t* rows,
+                                     const float* wscale, float* const* dst, int accumulate, const float* rope_cs,
+                                     const int32_t* pos, int64_t n_ctx, void* stream) {
+    AMV_REQUIRE(a && w && rows && wscale && dst, "amv_bitnet_gemv_fused: null pointer");
+    AMV_REQUIRE(mode >= 0 && mode <= 2 && (mode == 0 || b), "amv_bitnet_gemv_fused: mode %d (0 plain, 1 relu2, 2 silu) "
+                "needs the second operand for 1 and 2", mode);
+    AMV_REQUIRE(k > 0 && k % 128 == 0 && k <= 16384, "amv_bitnet_gemv_fused: k %lld (a multiple of 128, <= 16384)",
+                (long long)k);
+    AMV_REQUIRE(n_seg >= 1 && n_seg <= 3, "amv_bitnet_gemv_fused: n_seg %d (1..3)", n_seg);
+    AMV_REQUIRE((((uintptr_t)a | (uintptr_t)b | (uintptr_t)norm_w) & 15) == 0,
+                "amv_bitnet_gemv_fused: a, b and norm_w must be 16-byte aligned");
+    BnSegs sg{};
+    int64_t total = 0;
+    for (int s = 0; s < 3; ++s) {
+        if (s < n_seg) {
+            AMV_REQUIRE(w[s] && dst[s] && rows[s] > 0, "amv_bitnet_gemv_fused: matrix %d: null pointer or no rows", s);
+            AMV_REQUIRE(((uintptr_t)w[s] & 15) == 0, "amv_bitnet_gemv_fused: weights must be 16-byte aligned");
+            total += rows[s];
+            AMV_REQUIRE(total <= (1 << 24), "amv_bitnet_gemv_fused: too many rows");
+            sg.w[s] = (const uint4*)w[s];
+            sg.dst[s] = dst[s];
+            sg.wscale[s] = wscale[s];
+        }
+        sg.end[s] = (int)total;
+    }
+    const bool rope = rope_cs != nullptr;
+    if (rope) {
+        AMV_REQUIRE(mode == 0 && n_seg == 3 && rows[0] % 128 == 0 && rows[1] % 128 == 0 && rows[2] == rows[1] &&
+                        !accumulate && pos && n_ctx > 0,
+                    "amv_bitnet_gemv_fused: RoPE needs Q | K | V (head_dim 128, K and V of equal rows, mode 0), the "
+                    "position and the context length, and no accumulation");
+    }
+    // Launch shape (measured on MI355X, cold weights): 2 rows per wave, 4 from 8192 rows on (the per-wave fixed
+    // work of the prologue then counts half as often: gate | up 13824 x 2560 8.3 -> 7.4 us, while 2560- and 3840-row
+    // launches lose ~1 us with 4); 512 threads per workgroup (against 256 / 1024: 4.1 / 4.5-5.9 us for Q | K | V),
+    // 1024 when k > 8192 so the input fits 4 float4 per thread.
+    const int R = total >= 8192 ? 4 : 2;
+    const int64_t waves = (total + R - 1) / R;
+    hipStream_t st = amv_stream(stream);
+    const float4 *a4 = (const float4*)a, *b4 = (const float4*)b, *w4 = (const float4*)norm_w;
+#define BN_QG_LAUNCH(NT, V4, ROPE, MODE, RR, CS, POS, CTX)                                                       \
+    hipLaunchKernelGGL((k_bitnet_qgemv<NT, V4, ROPE, MODE, RR>),                                                   \
+                       dim3((unsigned)((waves + NT / 64 - 1) / (NT / 64))), dim3(NT), 0, st, a4, b4, w4, (int)k, eps,  \
+                       do_norm, sg, n_seg, accumulate, CS, POS, CTX)
+#define BN_QG_R(NT, V4, RR)                                                                                        \
+    do {                                                                                                           \
+        if (rope) BN_QG_LAUNCH(NT, V4, true, 0, RR, rope_cs, pos, (int)n_ctx);                                     \
+        else if (mode == 1) BN_QG_LAUNCH(NT, V4, false, 1, RR, nullptr, nullptr, 0);                               \
+        else if (mode == 2) BN_QG_LAUNCH(NT, V4, false, 2, RR, nullptr, nullptr, 0);                               \
+        else BN_QG_LAUNCH(NT, V4, false, 0, RR, nullptr, nullptr, 0);                                              \
+    } while (0)
+#define BN_QG(NT, V4)                                                                                              \
+    do {                                                                                                           \
+        if (R == 4) BN_QG_R(NT, V4, 4);                                                                            \
+        else BN_QG_R(NT, V4, 2);                                                                                   \
+    } while (0)
+    if (k > 8192) BN_QG(1024, 4);
+    else if (k > 4096) BN_QG(512, 4);
+    else if (k > 2048) BN_QG(512, 2);
+    else BN_QG(512, 1);
+#undef BN_QG
+#undef BN_QG_R
+#undef BN_QG_LAUNCH
+    return amv_check_launch("amv_bitnet_gemv_fused");
+}

@@ -168,6 +168,45 @@ __device__ __forceinline__ float amv_wave_max(float v) {
     return v;
 }
 
+// Wave-uniform reductions without LDS round trips: DPP within each 16-lane row, then the four row results read into
+// scalar registers (rows summed in the order 0, 1, 2, 3). The result is the same in every lane.
+template <int CTRL>
+__device__ __forceinline__ int amv_dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ double amv_dpp_d(double v) {
+    const int lo = amv_dpp_i<CTRL>(__double2loint(v)), hi = amv_dpp_i<CTRL>(__double2hiint(v));
+    return __hiloint2double(hi, lo);
+}
+__device__ __forceinline__ int amv_wave_sum_i_u(int v) {
+    v += amv_dpp_i<0xB1>(v);
+    v += amv_dpp_i<0x4E>(v);
+    v += amv_dpp_i<0x141>(v);
+    v += amv_dpp_i<0x140>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
+}
+__device__ __forceinline__ float amv_wave_max_u(float v) {
+    v = fmaxf(v, __int_as_float(amv_dpp_i<0xB1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(amv_dpp_i<0x4E>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(amv_dpp_i<0x141>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(amv_dpp_i<0x140>(__float_as_int(v))));
+    const int i = __float_as_int(v);
+    return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(i, 0)), __int_as_float(__builtin_amdgcn_readlane(i, 16))),
+                 fmaxf(__int_as_float(__builtin_amdgcn_readlane(i, 32)), __int_as_float(__builtin_amdgcn_readlane(i, 48))));
+}
+__device__ __forceinline__ double amv_wave_sum_d_u(double v) {
+    v += amv_dpp_d<0xB1>(v);
+    v += amv_dpp_d<0x4E>(v);
+    v += amv_dpp_d<0x141>(v);
+    v += amv_dpp_d<0x140>(v);
+    const int lo = __double2loint(v), hi = __double2hiint(v);
+    double t = __hiloint2double(__builtin_amdgcn_readlane(hi, 0), __builtin_amdgcn_readlane(lo, 0));
+#pragma unroll
+    for (int r = 16; r < 64; r += 16)
+        t += __hiloint2double(__builtin_amdgcn_readlane(hi, r), __builtin_amdgcn_readlane(lo, r));
+    return t;
+}
+
 // Q8_0 quantization of one 32-element block held one element per lane by 32 consecutive lanes of a wave (lane j of
 // the block holds element j): the rules of amv_quantize_act (ggml quantize_row_q8_0 x86 / ARM / ref). Every lane of
 // the 32 must call it. Writes the int8 of its element to qs[j]; lane j == 0 writes {fp16-rounded d, sum q} to *meta.

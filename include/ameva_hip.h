@@ -206,6 +206,17 @@ int amv_bitnet_norm_q8(const float* a, const float* b, const float* w, int64_t n
 int amv_bitnet_rope_kv(float* q, const float* k, const float* v, const float* cs, float* k_cache, float* v_cache,
                        const int32_t* pos, int64_t n_head, int64_t n_head_kv, int64_t hd, int64_t n_ctx, void* stream);
 int amv_gemv_f16(const void* w, int64_t n_rows, int64_t k, const float* x, float* y, void* stream);
+/* One launch per projection group of the BitNet token step (the reference engine's RecordNormQ8 + RecordGemv pairs,
+ * ac_bitnet_engine.cpp:268-341): the input's activation as amv_bitnet_norm_q8 (mode, do_norm, norm_w) computed by
+ * every workgroup into LDS, then n_seg (1..3) stacked I2_S matrices: matrix s has rows[s] rows of k / 4 bytes at w[s],
+ * its outputs dst[s][r] = float(isum_r) * (dequant * wscale[s]) (added to dst[s][r] when accumulate). With rope_cs
+ * (= [cos 0..63, sin 0..63] of the position, head_dim 128): matrices Q | K | V, q written rotated to dst[0], k rotated
+ * and v as is into row pos[0] (clamped to n_ctx - 1) of the f32 caches dst[1], dst[2] (rows of rows[1] floats): the
+ * values amv_i2s_gemv + amv_bitnet_rope_kv produce. k % 128 == 0, k <= 16384, 16-byte aligned pointers. */
+int amv_bitnet_gemv_fused(const float* a, const float* b, const float* norm_w, int64_t k, float eps, int mode,
+                          int do_norm, int n_seg, const void* const* w, const int64_t* rows, const float* wscale,
+                          float* const* dst, int accumulate, const float* rope_cs, const int32_t* pos, int64_t n_ctx,
+                          void* stream);
 
 int amv_i2s_gemv_f32(const void* w, int64_t n_rows, int64_t k, const float* x, float scale, float* y, void* stream);
 

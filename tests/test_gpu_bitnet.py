@@ -180,6 +180,87 @@ def test_i2s_gemv_residual_add(dev):
     assert torch.equal(acc, g(r, dev) + plain)
 
 
+def fused(a, b, nw, k, mode, do_norm, ws, rows, scales, dsts, acc, cs=None, pos=None, n_ctx=0):
+    n = len(ws)
+    W = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in ws])
+    Rw = (ctypes.c_int64 * 3)(*rows)
+    S = (ctypes.c_float * 3)(*scales)
+    D = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in dsts])
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    return L().amv_bitnet_gemv_fused(p(a), p(b), p(nw), k, 1e-5, mode, do_norm, n, W, Rw, S, D, acc, p(cs), p(pos),
+                                     n_ctx, stream())
+
+
+def unfused_act(dev, a, b, nw, k, mode, do_norm):
+    act = torch.empty(k + 16, dtype=torch.uint8, device=dev)
+    assert L().amv_bitnet_norm_q8(a.data_ptr(), None if b is None else b.data_ptr(),
+                                  None if nw is None else nw.data_ptr(), k, 1e-5, mode, do_norm, None, act.data_ptr(),
+                                  stream()) == 0
+    return act
+
+
+@pytest.mark.parametrize("k,rows,mode,do_norm,with_w,acc", [
+    (2560, (2560,), 0, 1, True, 1), (2560, (2560,), 0, 0, False, 1), (2560, (6912, 6912), 0, 1, True, 0),
+    (6912, (2560,), 1, 1, True, 1), (6912, (2560,), 2, 0, False, 1), (6912, (2560,), 1, 1, False, 0),
+    (12288, (999,), 0, 1, True, 0), (256, (3, 5, 7), 2, 1, True, 1), (4096, (130, 1), 1, 1, True, 0)])
+def test_fused_norm_gemv_equals_the_separate_kernels(dev, k, rows, mode, do_norm, with_w, acc):
+    """One launch (the activation per workgroup in LDS, stacked matrices) = amv_bitnet_norm_q8 then one amv_i2s_gemv
+    (or _acc) per matrix, bit for bit."""
+    rng = np.random.default_rng(k + sum(rows) + 10 * mode + do_norm)
+    a = g(rng.standard_normal(k).astype(np.float32), dev)
+    b = g(rng.standard_normal(k).astype(np.float32), dev) if mode else None
+    nw = g((1 + 0.1 * rng.standard_normal(k)).astype(np.float32), dev) if with_w else None
+    ws = [g(i2s_pack(rng.integers(0, 3, (r, k)).astype(np.uint8)), dev) for r in rows]
+    scales = [0.5 + 0.25 * i for i in range(len(rows))]
+    base = [g(rng.standard_normal(r).astype(np.float32), dev) for r in rows]
+    got = [t.clone() for t in base]
+    assert fused(a, b, nw, k, mode, do_norm, ws, rows, scales, got, acc) == 0
+    act = unfused_act(dev, a, b, nw, k, mode, do_norm)
+    for w, r, sc, t0, t1 in zip(ws, rows, scales, base, got):
+        want = t0.clone()
+        if acc:
+            assert L().amv_i2s_gemv_acc(w.data_ptr(), r, k, act.data_ptr(), sc, want.data_ptr(), stream()) == 0
+        else:
+            assert L().amv_i2s_gemv(w.data_ptr(), r, k, act.data_ptr(), 1, sc, want.data_ptr(), r, stream()) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(t1, want)
+
+
+@pytest.mark.parametrize("E,H,KVH,pos", [(2560, 20, 5, 17), (256, 2, 1, 0), (1024, 8, 8, 39), (8192, 64, 8, 5)])
+def test_fused_qkv_rope_equals_the_separate_kernels(dev, E, H, KVH, pos):
+    rng = np.random.default_rng(E + pos)
+    hd, ctx, kv = 128, 40, KVH * 128
+    x = g(rng.standard_normal(E).astype(np.float32), dev)
+    nw = g((1 + 0.1 * rng.standard_normal(E)).astype(np.float32), dev)
+    ws = [g(i2s_pack(rng.integers(0, 3, (r, E)).astype(np.uint8)), dev) for r in (H * hd, kv, kv)]
+    sc = [1.3, 0.9, 1.1]
+    th = np.float32(pos) / np.power(np.float32(10000.0), (2 * np.arange(64, dtype=np.float32)) / np.float32(hd))
+    cs = g(np.concatenate([np.cos(th), np.sin(th)]).astype(np.float32), dev)
+    p = torch.tensor([pos], dtype=torch.int32, device=dev)
+    q1 = torch.empty(H * hd, dtype=torch.float32, device=dev)
+    kc1, vc1 = torch.zeros((ctx, kv), device=dev), torch.zeros((ctx, kv), device=dev)
+    assert fused(x, None, nw, E, 0, 1, ws, (H * hd, kv, kv), sc, [q1, kc1, vc1], 0, cs, p, ctx) == 0
+    act = unfused_act(dev, x, None, nw, E, 0, 1)
+    q2, k2, v2 = (torch.empty(r, dtype=torch.float32, device=dev) for r in (H * hd, kv, kv))
+    for w, r, s_, o in zip(ws, (H * hd, kv, kv), sc, (q2, k2, v2)):
+        assert L().amv_i2s_gemv(w.data_ptr(), r, E, act.data_ptr(), 1, s_, o.data_ptr(), r, stream()) == 0
+    kc2, vc2 = torch.zeros((ctx, kv), device=dev), torch.zeros((ctx, kv), device=dev)
+    assert L().amv_bitnet_rope_kv(q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), cs.data_ptr(), kc2.data_ptr(),
+                                  vc2.data_ptr(), p.data_ptr(), H, KVH, hd, ctx, stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert kc1[pos].abs().sum() > 0 and not torch.cat([kc1[:pos], kc1[pos + 1:]]).any()
+
+
+def test_fused_argument_errors(dev):
+    t = torch.zeros(1024, device=dev)
+    w = torch.zeros(1024, dtype=torch.uint8, device=dev)
+    assert fused(t, None, None, 100, 0, 1, [w], (4,), [1.0], [t], 0) != 0          # k % 128
+    assert fused(t, None, None, 128, 1, 1, [w], (4,), [1.0], [t], 0) != 0          # relu2 without b
+    assert fused(t, None, None, 256, 0, 1, [w, w], (4, 4), [1.0, 1.0], [t, t], 0, cs=t, pos=t, n_ctx=4) != 0  # rope: 3
+    assert b"RoPE" in L().amv_last_error()
+
+
 def random_model(rng, cfg, n_layers, n_vocab, relu2=True):
     E, F, kv = cfg["n_embd"], cfg["n_ffn"], cfg["n_kv_heads"] * cfg["head_dim"]
     r = lambda a, b: i2s_pack(rng.integers(0, 3, (a, b)).astype(np.uint8))  # noqa: E731
