@@ -13,8 +13,10 @@
  * (relu2_ffn) or silu(gate) * up -> RMS_NORM(., ffn_sub_norm) when present -> int8 -> down projection added to x;
  * then, when logits are asked for, RMS_NORM(x, output_norm) and the f16 LM head.
  *
- * On MI355X: all state lives in HBM; the token step (every layer, and the head) is one HIP graph captured at the
- * first call and replayed, the position and key count being read from device memory; chunk_layers is accepted and
+ * On MI355X: all state lives in HBM; each layer is 6 launches (each norm + int8 step runs inside the projection that
+ * consumes it, Q|K|V and gate|up are one launch each, RoPE and the cache stores ride in the Q|K|V epilogue); the
+ * token step (every layer, and the head) is one HIP graph captured at the first call and replayed, the position and
+ * key count being read from device memory; chunk_layers is accepted and
  * has no effect (there is no submission-length limit to bound). Shapes: head_dim 128, n_heads / n_kv_heads in
  * {1, 2, 4, 8}, n_embd and n_ffn multiples of 128 up to 16384 (BitNet b1.58 2B: 2560 / 6912, 20 / 5 heads).
  * AC_BITNET_PROFILE=1 runs the step eagerly and prints the GPU time per kernel to stderr; AC_BITNET_GEMV must be
