@@ -314,6 +314,45 @@ def bench_kv_cache(ops, torch, dev):
     return res
 
 
+def bench_load_path(ops, torch, dev):
+    """The weight load path (the reference's set_tensor repack, ggml-ameva-buffer.cpp:509-561): amv_repack (ggml blocks
+    -> the MI355X layout) and amv_unrepack (back, as get_tensor does) of a 14336 x 4096 weight per type, cold over
+    rotating sources > 512 MiB (the bytes are shuffled, not interpreted, so random bytes serve), read + write bytes
+    counted; and the pinned host -> HBM copy of the same bytes, the step a load cannot avoid."""
+    from ameva_compute_amd._lib import lib as _lib
+    res = {}
+    n, k = 14336, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    for name, wtype in (("q4_0", ops.Q4_0), ("q8_0", ops.Q8_0), ("q4_K", ops.Q4_K), ("q6_K", ops.Q6_K)):
+        nb = _lib().amv_weight_bytes(wtype, n, k)
+        copies = max(4, -(-(600 << 20) // nb))
+        srcs = [torch.randint(0, 256, (nb,), generator=g, device=dev, dtype=torch.uint8) for _ in range(copies)]
+        dst = torch.empty(nb, dtype=torch.uint8, device=dev)
+        st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+        ms_r = time_steps_graph(torch, lambda i: _lib().amv_repack(wtype, srcs[i % copies].data_ptr(), dst.data_ptr(),
+                                                                   n, k, st()), 200, 20, per_graph=copies)
+        ms_u = time_steps_graph(torch, lambda i: _lib().amv_unrepack(wtype, srcs[i % copies].data_ptr(),
+                                                                     dst.data_ptr(), n, k, st()), 200, 20,
+                                per_graph=copies)
+        res[f"repack_{name}_14336x4096_us"] = round(ms_r * 1e3, 2)
+        res[f"repack_{name}_gbs"] = round(2 * nb / (ms_r * 1e-3) / 1e9, 1)
+        res[f"unrepack_{name}_14336x4096_us"] = round(ms_u * 1e3, 2)
+        log(f"bench: repack {name} 14336x4096 ({nb / 2**20:.1f} MiB) {ms_r * 1e3:.1f} us = "
+            f"{2 * nb / (ms_r * 1e-3) / 1e9:.0f} GB/s read+write; unrepack {ms_u * 1e3:.1f} us")
+        del srcs, dst
+    nb = _lib().amv_weight_bytes(ops.Q4_0, n, k)
+    host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(nb, dtype=torch.uint8, device=dev)
+    ms_h = time_steps(torch, lambda i: dst.copy_(host, non_blocking=True), 50, 5)
+    res["h2d_pinned_33MB_gbs"] = round(nb / (ms_h * 1e-3) / 1e9, 1)
+    log(f"bench: pinned host -> HBM copy of {nb / 2**20:.1f} MiB: {ms_h * 1e3:.0f} us = "
+        f"{nb / (ms_h * 1e-3) / 1e9:.1f} GB/s")
+    del host, dst
+    torch.cuda.empty_cache()
+    return res
+
+
 def copy_ceiling(torch, dev, nbytes):
     """Device-to-device copy of the headline's byte count (torch copy kernel), cold over 20 buffers: the HBM rate a
     single launch of a plain streaming kernel of that size reaches on this box, read + write bytes counted."""
@@ -537,6 +576,7 @@ def main():
     ap.add_argument("--only-model", action="store_true", help="only the 32-layer model figures (for profiling)")
     ap.add_argument("--no-model", action="store_true", help="skip the 32-layer model figures")
     ap.add_argument("--only-bitnet", action="store_true", help="only the BitNet 2B engine decode figures")
+    ap.add_argument("--only-load", action="store_true", help="only the weight load path figures (repack, upload)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
@@ -569,6 +609,9 @@ def main():
         return
     if args.only_bitnet:
         print(json.dumps(bench_bitnet()), flush=True)
+        return
+    if args.only_load:
+        print(json.dumps(bench_load_path(ops, torch, dev)), flush=True)
         return
 
     log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")
@@ -610,6 +653,7 @@ def main():
         extra.update(bench_batched(ops, torch, dev))
         extra.update(bench_i2s(ops, torch, dev))
         extra.update(bench_kv_cache(ops, torch, dev))
+        extra.update(bench_load_path(ops, torch, dev))
         extra.update(copy_ceiling(torch, dev, nbytes))
 
     layer_info = None
