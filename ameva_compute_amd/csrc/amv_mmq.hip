@@ -468,9 +468,9 @@ static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const v
 // amv_mmq16.hip: Q4_0 / Q8_0 (AMV_ACT_Q8_0_MMA activations) and Q4_K (AMV_ACT_Q8_K_MMA) on the f16 matrix cores with
 // LDS-staged tiles
 int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
-              int64_t ldd, int32_t* sums, hipStream_t st);
+              int64_t ldd, int32_t* sums, int deq, hipStream_t st);
 int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
-                  int32_t* sums, hipStream_t st);
+                  int32_t* sums, int deq, hipStream_t st);
 
 // Batches above this many tokens go to the f16 kernel (128-token tiles); smaller ones to the int8 kernel, which reads
 // the plain Q8_0 prefix of the same activation buffer.
@@ -478,10 +478,15 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
 
 static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
                         int act_type, int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream) {
-    const bool tiled = m > MMQ16_MIN_M && ((act_type == AMV_ACT_Q8_0_MMA && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
-                                           (act_type == AMV_ACT_Q8_K_MMA && wtype == AMV_T_Q4_K));
+    const bool deq = act_type == AMV_ACT_Q8_0_DEQ || act_type == AMV_ACT_Q8_K_DEQ;
+    const bool q80x = act_type == AMV_ACT_Q8_0_MMA || act_type == AMV_ACT_Q8_0_DEQ;
+    const bool q8kx = act_type == AMV_ACT_Q8_K_MMA || act_type == AMV_ACT_Q8_K_DEQ;
+    const bool tiled = m > MMQ16_MIN_M && ((q80x && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
+                                           (q8kx && wtype == AMV_T_Q4_K));
     if (tiled) {
         AMV_REQUIRE(w && act && (dst || sums), "%s: null pointer", fn);
+        AMV_REQUIRE(!(deq && sums), "%s: block sums need the exact layout (AMV_ACT_Q8_0_MMA / AMV_ACT_Q8_K_MMA), not "
+                    "the scaled one", fn);
         AMV_REQUIRE(n_rows > 0 && k > 0 && k % 32 == 0, "%s: bad shape", fn);
         AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 128 && m * k <= INT32_MAX && n_rows * (k / 32) <= INT32_MAX,
                     "%s: too large", fn);
@@ -489,13 +494,16 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
         AMV_REQUIRE(!dst || ldd >= n_rows, "%s: ldd < n_rows", fn);
         if (wtype == AMV_T_Q4_K) {
             AMV_REQUIRE(k % 256 == 0, "%s: Q4_K needs k %% 256 == 0", fn);
-            return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
+            return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, sums, deq ? 1 : 0, amv_stream(stream));
         }
-        return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
+        return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, deq ? 1 : 0, amv_stream(stream));
     }
-    const bool ok = (act_type == AMV_T_Q8_0 || act_type == AMV_ACT_Q8_0_MMA) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)
-                                                                             : (act_type == AMV_ACT_Q8_K_MMA && wtype == AMV_T_Q4_K);
+    const bool ok = (act_type == AMV_T_Q8_0 || q80x) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)
+                                                     : (q8kx && wtype == AMV_T_Q4_K);
     AMV_REQUIRE(ok, "%s: activation type %d does not feed weight type %d", fn, act_type, wtype);
+    // the small-batch Q4_K kernel reads the f16 copies as exact integers
+    AMV_REQUIRE(!(deq && wtype == AMV_T_Q4_K), "%s: Q4_K batches of m <= %d need the exact layout AMV_ACT_Q8_K_MMA",
+                fn, MMQ16_MIN_M);
     return mmq_impl(wtype, w, n_rows, k, act, m, dst, ldd, sums, stream);
 }
 

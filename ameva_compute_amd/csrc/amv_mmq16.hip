@@ -8,6 +8,10 @@
 // t = S * d_w, acc = fma(t, d_a, acc), against three for int8 MFMA (convert, scale product, fma) -- on MI355X the
 // epilogue, not the matrix core, bounds a kernel with a scale per 32 products, and the f16 rate keeps pace with it.
 //
+// DEQ variant (activations AMV_ACT_Q8_0_DEQ): the weights are staged as f16 (q - 8) d_w (Q4_0) or q d_w (Q8_0) and the
+// activations arrive as f16 q_a d_a, so the matrix core accumulates across all of k with no per-block epilogue. Each
+// operand is rounded to f16 once (relative 2^-11), so the f32 result is within ~3e-4 relative L2 of the exact-sum
+// form instead of bit-identical to it; the block sums (SUMS) always use the exact form.
 // Workgroup of 4 waves (2 x 2) on a tile of 64 TN weight rows x 64 TM tokens; wave (wr, wc) owns rows
 // 32 TN wr .. + 32 TN and tokens 32 TM wc .. + 32 TM as TN x TM tiles of 32 x 32. Pipeline steps of 2 blocks (64 k): the
 // global loads of step s + 1 are issued before step s computes from LDS; at staging the weights are converted to f16
@@ -30,6 +34,12 @@ __device__ __forceinline__ uint2 g16_nib4(uint32_t x, g16_h2 off) {
     const g16_h2 p0 = __builtin_bit_cast(g16_h2, __builtin_amdgcn_perm(x, m64, 0x00050004u)) - off;
     const g16_h2 p1 = __builtin_bit_cast(g16_h2, __builtin_amdgcn_perm(x, m64, 0x00070006u)) - off;
     return make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+}
+
+// the two f16 pairs of v scaled by s (one rounding each)
+__device__ __forceinline__ uint2 g16_scale2(uint2 v, g16_h2 sc) {
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, v.x) * sc),
+                      __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, v.y) * sc));
 }
 
 // Registers of one staging step: thread t < 2 BN stages (row t / 2, block t % 2) of the weights (sw) and its scale
@@ -71,7 +81,7 @@ __device__ __forceinline__ void g16_load(uint4 (&sw)[G16_NW(WT)], float& sdw, ui
     }
 }
 
-template <int WT, int TN, int TM>
+template <int WT, int TN, int TM, bool DEQ>
 __device__ __forceinline__ void g16_store(const uint4 (&sw)[G16_NW(WT)], float sdw, uint4 sa0, uint4 sa1, uint4 sa2,
                                           uint4 sa3, float sda, uint16_t* __restrict__ sA,
                                           uint16_t* __restrict__ sB, float* __restrict__ sDw,
@@ -81,6 +91,7 @@ __device__ __forceinline__ void g16_store(const uint4 (&sw)[G16_NW(WT)], float s
     const int blk = t & 1;
     if (t < 2 * BN) {
         uint4* dst = reinterpret_cast<uint4*>(sA + (t >> 1) * G16_LDK + 32 * blk);
+        const g16_h2 dw2 = {(_Float16)sdw, (_Float16)sdw};  // DEQ: the block scale (an f16 value, exact)
         if constexpr (WT == AMV_T_Q4_0) {
             // element e < 16: low nibble of byte e; element 16 + e: high nibble of byte e; value q - 8
             const g16_h2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
@@ -90,6 +101,10 @@ __device__ __forceinline__ void g16_store(const uint4 (&sw)[G16_NW(WT)], float s
             for (int i = 0; i < 4; ++i) {
                 lo[i] = g16_nib4(wv[i] & 0x0F0F0F0Fu, off);
                 hi[i] = g16_nib4((wv[i] >> 4) & 0x0F0F0F0Fu, off);
+                if constexpr (DEQ) {
+                    lo[i] = g16_scale2(lo[i], dw2);
+                    hi[i] = g16_scale2(hi[i], dw2);
+                }
             }
             dst[0] = make_uint4(lo[0].x, lo[0].y, lo[1].x, lo[1].y);
             dst[1] = make_uint4(lo[2].x, lo[2].y, lo[3].x, lo[3].y);
@@ -102,11 +117,14 @@ __device__ __forceinline__ void g16_store(const uint4 (&sw)[G16_NW(WT)], float s
             const uint32_t wv[8] = {sw[0].x, sw[0].y, sw[0].z, sw[0].w, w1.x, w1.y, w1.z, w1.w};
             uint2 h[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) h[i] = g16_nib4(wv[i] ^ 0x80808080u, off);
+            for (int i = 0; i < 8; ++i) {
+                h[i] = g16_nib4(wv[i] ^ 0x80808080u, off);
+                if constexpr (DEQ) h[i] = g16_scale2(h[i], dw2);
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) dst[i] = make_uint4(h[2 * i].x, h[2 * i].y, h[2 * i + 1].x, h[2 * i + 1].y);
         }
-        sDw[blk * BN + (t >> 1)] = sdw;
+        if constexpr (!DEQ) sDw[blk * BN + (t >> 1)] = sdw;
     }
     if (t < 2 * BM) {
         uint4* bd = reinterpret_cast<uint4*>(sB + (t >> 1) * G16_LDK + 32 * blk);
@@ -114,11 +132,11 @@ __device__ __forceinline__ void g16_store(const uint4 (&sw)[G16_NW(WT)], float s
         bd[1] = sa1;
         bd[2] = sa2;
         bd[3] = sa3;
-        sDa[t] = sda;  // [block t / BM][token t % BM]
+        if constexpr (!DEQ) sDa[t] = sda;  // [block t / BM][token t % BM]
     }
 }
 
-template <int WT, bool SUMS, int TN, int TM>
+template <int WT, bool SUMS, int TN, int TM, bool DEQ>
 __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int N,
                                               int nb, const uint16_t* __restrict__ a16, const float* __restrict__ dT,
                                               int M, float* __restrict__ dst, int64_t ldd,
@@ -145,14 +163,32 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
     uint4 sw[G16_NW(WT)], sa0, sa1, sa2, sa3;
     float sdw = 0.0f, sda = 0.0f;
     g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, 0, wq, wd, N, nb, n0, a16, dT, M, m0, K);
-    g16_store<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, sA[0], sB[0], sDw[0], sDa[0]);
+    g16_store<WT, TN, TM, DEQ>(sw, sdw, sa0, sa1, sa2, sa3, sda, sA[0], sB[0], sDw[0], sDa[0]);
     __syncthreads();
     for (int step = 0; step < nsteps; ++step) {
         const int buf = step & 1;
         if (step + 1 < nsteps)
             g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, step + 1, wq, wd, N, nb, n0, a16, dT, M, m0, K);
+        if constexpr (DEQ) {  // scaled operands: accumulate across the whole step
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int kk = 16 * ks + 8 * h;
+                g16_h8 A[TN], B[TM];
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+                    A[i] = *reinterpret_cast<const g16_h8*>(sA[buf] + (32 * (TN * wr + i) + c) * G16_LDK + kk);
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    B[j] = *reinterpret_cast<const g16_h8*>(sB[buf] + (32 * (TM * wc + j) + c) * G16_LDK + kk);
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[j], acc[i][j], 0, 0, 0);
+            }
+        }
 #pragma unroll 1
-        for (int bl = 0; bl < 2; ++bl) {  // one block's accumulators live at a time
+        for (int bl = 0; bl < (DEQ ? 0 : 2); ++bl) {  // one block's accumulators live at a time
             g16_f16v C[TN][TM];
 #pragma unroll
             for (int i = 0; i < TN; ++i)
@@ -208,7 +244,8 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
             }
         }
         if (step + 1 < nsteps) {
-            g16_store<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, sA[buf ^ 1], sB[buf ^ 1], sDw[buf ^ 1], sDa[buf ^ 1]);
+            g16_store<WT, TN, TM, DEQ>(sw, sdw, sa0, sa1, sa2, sa3, sda, sA[buf ^ 1], sB[buf ^ 1], sDw[buf ^ 1],
+                                       sDa[buf ^ 1]);
             __syncthreads();
         }
     }
@@ -239,7 +276,7 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
 // Q4_0 / Q8_0 weights (MI355X layout), activations AMV_ACT_Q8_0_MMA of m rows. Tile: 128 x 128, or 64 x 64 when
 // the big tiles would leave CUs idle.
 int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
-              int64_t ldd, int32_t* sums, hipStream_t st) {
+              int64_t ldd, int32_t* sums, int deq, hipStream_t st) {
     const int nb = (int)(k / 32);
     const int64_t nblk = n_rows * nb;
     const uint8_t* wq = (const uint8_t*)w;
@@ -252,20 +289,28 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
         return dim3((unsigned)((n_rows + 64 * tn - 1) / (64 * tn)), (unsigned)((m + 64 * tm - 1) / (64 * tm)));
     };
     const auto wgs = [&](int tn, int tm) { const dim3 g = grid(tn, tm); return (int64_t)g.x * g.y; };
-    // measured on MI355X: 128 x 128 tiles win from ~1.5 workgroups per CU (14336 x 4096 at 512 tokens: 448 of them,
-    // 177 us against 207 us for 896 tiles of 64 x 128); below that 64 x 64 tiles (4096 x 14336: 241 us against 311)
-    const int cfg = wgs(2, 2) >= 384 ? 22 : 11;
-#define G16_LAUNCH(WT, S, TN, TM)                                                                                     \
-    hipLaunchKernelGGL((k_mmq16<WT, S, TN, TM>), grid(TN, TM), dim3(256), 0, st, wq, wd, (int)n_rows, nb, a16, dT,    \
+    // exact form, measured on MI355X: 128 x 128 tiles win from ~1.5 workgroups per CU (14336 x 4096 at 512 tokens: 448
+    // of them, 177 us against 207 us for 896 tiles of 64 x 128); below that 64 x 64 tiles (4096 x 14336: 241 us
+    // against 311)
+    // scaled form (DEQ), swept over 4096 / 6144 / 14336 / 28672 x 4096 and 4096 x 14336 at m = 128, 512 for Q4_0,
+    // Q8_0, Q4_K: 128 x 128 from 224 workgroups (14336 x 4096 at 512: 83 us against 131 for 64 x 64), else 64 x 64
+    const int cfg = deq ? (wgs(2, 2) >= 224 ? 22 : 11) : (wgs(2, 2) >= 384 ? 22 : 11);
+#define G16_LAUNCH(WT, S, TN, TM, D)                                                                                  \
+    hipLaunchKernelGGL((k_mmq16<WT, S, TN, TM, D>), grid(TN, TM), dim3(256), 0, st, wq, wd, (int)n_rows, nb, a16, dT, \
                        (int)m, dst, ldd, sums, vec_out)
-#define G16_CFG(WT, S)                          \
-    if (cfg == 22) G16_LAUNCH(WT, S, 2, 2);     \
-    else if (cfg == 12) G16_LAUNCH(WT, S, 1, 2); \
-    else G16_LAUNCH(WT, S, 1, 1)
+#define G16_CFG(WT, S, D)                          \
+    if (cfg == 22) G16_LAUNCH(WT, S, 2, 2, D);     \
+    else if (cfg == 12) G16_LAUNCH(WT, S, 1, 2, D); \
+    else if (cfg == 21) G16_LAUNCH(WT, S, 2, 1, D); \
+    else G16_LAUNCH(WT, S, 1, 1, D)
     if (wtype == AMV_T_Q4_0) {
-        if (sums) { G16_CFG(AMV_T_Q4_0, true); } else { G16_CFG(AMV_T_Q4_0, false); }
+        if (sums) { G16_CFG(AMV_T_Q4_0, true, false); }
+        else if (deq) { G16_CFG(AMV_T_Q4_0, false, true); }
+        else { G16_CFG(AMV_T_Q4_0, false, false); }
     } else {
-        if (sums) { G16_CFG(AMV_T_Q8_0, true); } else { G16_CFG(AMV_T_Q8_0, false); }
+        if (sums) { G16_CFG(AMV_T_Q8_0, true, false); }
+        else if (deq) { G16_CFG(AMV_T_Q8_0, false, true); }
+        else { G16_CFG(AMV_T_Q8_0, false, false); }
     }
 #undef G16_CFG
 #undef G16_LAUNCH
@@ -281,6 +326,9 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
 // chunk (units 2c, 2c + 1: the low and high nibbles of 32 bytes); the per-super-block values (d, dmin, the mins,
 // the activation 16-sums and d_a) are staged at its first chunk into a slot of their own, double-buffered by
 // super-block parity.
+// DEQ variant (activations AMV_ACT_Q8_K_DEQ, f16 q_a d_a): each weight is staged as f16 of (d sc) q - dmin m (the
+// two products rounded to f16, then one f16 fma), so the matrix core accumulates across all of k; no mins MFMA, no
+// fold (the same ~3e-4 relative L2 as the Q4_0 / Q8_0 DEQ form).
 struct G16K {
     uint4 q, hd, a0, a1, a2, a3, bs;
     float da;
@@ -314,7 +362,7 @@ __device__ __forceinline__ void g16k_load(G16K& s, int step, const uint4* __rest
     }
 }
 
-template <int TN, int TM>
+template <int TN, int TM, bool DEQ>
 __device__ __forceinline__ void g16k_store(const G16K& s, int step, uint16_t* __restrict__ sA, uint16_t* __restrict__ sB,
                                            float* __restrict__ sD, float* __restrict__ sDm, uint16_t* __restrict__ sMn,
                                            uint16_t* __restrict__ sBs, float* __restrict__ sDa) {
@@ -326,16 +374,35 @@ __device__ __forceinline__ void g16k_store(const G16K& s, int step, uint16_t* __
         k4_scale_min(2 * c, s.hd.y, s.hd.z, s.hd.w, sc0, m0u);
         k4_scale_min(2 * c + 1, s.hd.y, s.hd.z, s.hd.w, sc1, m1u);
         const g16_h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
-        const g16_h2 f0 = {(_Float16)(float)sc0, (_Float16)(float)sc0}, f1 = {(_Float16)(float)sc1, (_Float16)(float)sc1};
+        g16_h2 f0, f1, n0v = {(_Float16)0.0f, (_Float16)0.0f}, n1v = n0v;
+        if constexpr (DEQ) {  // (d sc) and -(dmin m) of the two units, rounded to f16
+            const float d = amv_h2f(s.hd.x), dmin = amv_h2f(s.hd.x >> 16);
+            const _Float16 a0 = (_Float16)(d * (float)sc0), a1 = (_Float16)(d * (float)sc1);
+            const _Float16 b0 = (_Float16)(-(dmin * (float)m0u)), b1 = (_Float16)(-(dmin * (float)m1u));
+            f0 = {a0, a0};
+            f1 = {a1, a1};
+            n0v = {b0, b0};
+            n1v = {b1, b1};
+        } else {
+            f0 = {(_Float16)(float)sc0, (_Float16)(float)sc0};
+            f1 = {(_Float16)(float)sc1, (_Float16)(float)sc1};
+        }
         const uint32_t wv[4] = {s.q.x, s.q.y, s.q.z, s.q.w};
         uint32_t lo[8], hi[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // element 16 hf + 4 i + e of unit 2c (low nibble) and 2c + 1 (high nibble)
             const uint2 l = g16_nib4(wv[i] & 0x0F0F0F0Fu, off), h = g16_nib4((wv[i] >> 4) & 0x0F0F0F0Fu, off);
-            lo[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, l.x) * f0);
-            lo[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, l.y) * f0);
-            hi[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, h.x) * f1);
-            hi[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, h.y) * f1);
+            if constexpr (DEQ) {
+                lo[2 * i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(g16_h2, l.x), f0, n0v));
+                lo[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(g16_h2, l.y), f0, n0v));
+                hi[2 * i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(g16_h2, h.x), f1, n1v));
+                hi[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(g16_h2, h.y), f1, n1v));
+            } else {
+                lo[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, l.x) * f0);
+                lo[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, l.y) * f0);
+                hi[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, h.x) * f1);
+                hi[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(g16_h2, h.y) * f1);
+            }
         }
         uint4* dl = reinterpret_cast<uint4*>(sA + rl * G16_LDK + 16 * hf);
         uint4* dh = reinterpret_cast<uint4*>(sA + rl * G16_LDK + 32 + 16 * hf);
@@ -343,7 +410,7 @@ __device__ __forceinline__ void g16k_store(const G16K& s, int step, uint16_t* __
         dl[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
         dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-        if (c == 0) {  // per super-block: d, dmin, and the mins of units 4 hf .. 4 hf + 3 on their 16-sum slots
+        if (!DEQ && c == 0) {  // per super-block: d, dmin, and the mins of units 4 hf .. 4 hf + 3 on their 16-sum slots
             if (hf == 0) {
                 sD[rl] = amv_h2f(s.hd.x);
                 sDm[rl] = amv_h2f(s.hd.x >> 16);
@@ -366,14 +433,14 @@ __device__ __forceinline__ void g16k_store(const G16K& s, int step, uint16_t* __
         bd[1] = s.a1;
         bd[2] = s.a2;
         bd[3] = s.a3;
-        if (c == 0) {
+        if (!DEQ && c == 0) {
             *reinterpret_cast<uint4*>(sBs + tl * 16 + 8 * hf) = s.bs;
             if (hf == 0) sDa[tl] = s.da;
         }
     }
 }
 
-template <bool SUMS, int TN, int TM>
+template <bool SUMS, int TN, int TM, bool DEQ>
 __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
                                                   int nsb, const uint16_t* __restrict__ a16,
                                                   const uint16_t* __restrict__ bs16, const float* __restrict__ dT,
@@ -401,7 +468,7 @@ __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq,
 
     G16K st;
     g16k_load<TN, TM>(st, 0, wq, wh, N, nsb, n0, a16, bs16, dT, M, m0, K);
-    g16k_store<TN, TM>(st, 0, sA[0], sB[0], sD[0], sDm[0], sMn[0], sBs[0], sDa[0]);
+    g16k_store<TN, TM, DEQ>(st, 0, sA[0], sB[0], sD[0], sDm[0], sMn[0], sBs[0], sDa[0]);
     __syncthreads();
     for (int step = 0; step < nsteps; ++step) {
         const int buf = step & 1, j = step >> 2, c = step & 3, jp = j & 1;
@@ -419,10 +486,12 @@ __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq,
 #pragma unroll
             for (int i = 0; i < TN; ++i)
 #pragma unroll
-                for (int jj = 0; jj < TM; ++jj)
-                    C[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[jj], C[i][jj], 0, 0, 0);
+                for (int jj = 0; jj < TM; ++jj) {
+                    if constexpr (DEQ) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[jj], acc[i][jj], 0, 0, 0);
+                    else C[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[jj], C[i][jj], 0, 0, 0);
+                }
         }
-        if (c == 1 || c == 3) {
+        if (!DEQ && (c == 1 || c == 3)) {
             // fold the half super-block (and at its end I2, the mins against the activation 16-sums), tile by tile
 #pragma unroll
             for (int jj = 0; jj < TM; ++jj) {
@@ -472,7 +541,7 @@ __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq,
         }
         if (step + 1 < nsteps) {
             const int sp = ((step + 1) >> 2) & 1;  // per-super-block slot of the next step
-            g16k_store<TN, TM>(st, step + 1, sA[buf ^ 1], sB[buf ^ 1], sD[sp], sDm[sp], sMn[sp], sBs[sp], sDa[sp]);
+            g16k_store<TN, TM, DEQ>(st, step + 1, sA[buf ^ 1], sB[buf ^ 1], sD[sp], sDm[sp], sMn[sp], sBs[sp], sDa[sp]);
             __syncthreads();
         }
     }
@@ -502,7 +571,7 @@ __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq,
 
 // Q4_K weights (MI355X layout: qs [N][K/256][128] | head [N][K/256][16]), activations AMV_ACT_Q8_K_MMA of m rows
 int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
-                  int32_t* sums, hipStream_t st) {
+                  int32_t* sums, int deq, hipStream_t st) {
     const int nsb = (int)(k / 256);
     const int64_t nblk = n_rows * nsb;
     const uint4* wq = (const uint4*)w;
@@ -515,18 +584,24 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
     const auto grid = [&](int tn, int tm) {
         return dim3((unsigned)((n_rows + 64 * tn - 1) / (64 * tn)), (unsigned)((m + 64 * tm - 1) / (64 * tm)));
     };
-    // Tile by measurement on 28672/14336/6144/4096 x 4096 and 4096 x 14336 at m = 128, 512: the 64 x 128 tile
-    // (occupancy 2) wins once it fills 448 workgroups, else 64 x 64 (occupancy 3); the 128 x 128 tile holds 256 VGPRs
-    // + 123 AGPRs at occupancy 1 and lost to both everywhere.
-    const int cfg = (int64_t)grid(1, 2).x * grid(1, 2).y >= 448 ? 12 : 11;
-#define G16K_LAUNCH(S, TN, TM)                                                                                        \
-    hipLaunchKernelGGL((k_mmq16_q4k<S, TN, TM>), grid(TN, TM), dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, \
-                       dT, (int)m, dst, ldd, sums, vec_out)
+    const auto wgs = [&](int tn, int tm) { const dim3 g = grid(tn, tm); return (int64_t)g.x * g.y; };
+    // Exact form, tile by measurement on 28672/14336/6144/4096 x 4096 and 4096 x 14336 at m = 128, 512: the 64 x 128
+    // tile (occupancy 2) wins once it fills 448 workgroups, else 64 x 64 (occupancy 3); the 128 x 128 tile holds 256
+    // VGPRs + 123 AGPRs at occupancy 1 and lost to both everywhere.
+    const int cfg = deq ? (wgs(2, 2) >= 224 ? 22 : 11) : (wgs(1, 2) >= 448 ? 12 : 11);  // DEQ: the Q4_0 sweep's rule
+#define G16K_LAUNCH(S, TN, TM, D)                                                                                     \
+    hipLaunchKernelGGL((k_mmq16_q4k<S, TN, TM, D>), grid(TN, TM), dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16,     \
+                       bs16, dT, (int)m, dst, ldd, sums, vec_out)
     if (sums) {  // instrumentation: the small tile (two accumulator sets fit its registers)
-        G16K_LAUNCH(true, 1, 1);
+        G16K_LAUNCH(true, 1, 1, false);
+    } else if (deq) {
+        if (cfg == 22) G16K_LAUNCH(false, 2, 2, true);
+        else if (cfg == 12) G16K_LAUNCH(false, 1, 2, true);
+        else if (cfg == 21) G16K_LAUNCH(false, 2, 1, true);
+        else G16K_LAUNCH(false, 1, 1, true);
     } else {
-        if (cfg == 12) G16K_LAUNCH(false, 1, 2);
-        else G16K_LAUNCH(false, 1, 1);
+        if (cfg == 12) G16K_LAUNCH(false, 1, 2, false);
+        else G16K_LAUNCH(false, 1, 1, false);
     }
 #undef G16K_LAUNCH
     return amv_check_launch("amv_mul_mat_q_act");

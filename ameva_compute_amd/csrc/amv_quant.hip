@@ -9,11 +9,11 @@
 // roundf) -- the rules of ameva_act_fq.comp:5,38-41 and ameva_quant_a8.comp:46-54; d = amax/127 stored fp16.
 // ---------------------------------------------------------------------------------------------------------------
 // With a16 (AMV_ACT_Q8_0_MMA) the values also go out as f16 and the block scale transposed (row t = b / nbr, block
-// j = b % nbr at dt[j * m + t]).
+// j = b % nbr at dt[j * m + t]); with deq (AMV_ACT_Q8_0_DEQ) the f16 copies are q * d (one rounding) instead of q.
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x, int64_t n_elem, int rule,
                                                    uint8_t* __restrict__ y_ggml, int8_t* __restrict__ aq,
                                                    int2* __restrict__ ads, uint16_t* __restrict__ a16,
-                                                   float* __restrict__ dt, int nbr, int m) {
+                                                   float* __restrict__ dt, int nbr, int m, int deq) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const bool live = i < n_elem;
     const float v = live ? x[i] : 0.0f;
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x,
         if (j == 0) ads[b] = make_int2(__float_as_int(amv_h2f(d16)), s);
     }
     if (a16) {
-        a16[i] = __builtin_bit_cast(uint16_t, (_Float16)q);
+        a16[i] = __builtin_bit_cast(uint16_t, deq ? (_Float16)((float)q * amv_h2f(d16)) : (_Float16)q);
         if (j == 0) dt[(b % nbr) * m + b / nbr] = amv_h2f(d16);
     }
 }
@@ -57,12 +57,12 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x,
 // iscale * x)), d = 1/iscale, bsums = sums of q over 16 elements.
 // ---------------------------------------------------------------------------------------------------------------
 // With a16 (AMV_ACT_Q8_K_MMA) the block's values also go out as f16, its sums per 16 as f16 and its scale transposed
-// (token t = b / nsb, super-block j = b % nsb at dt[j * m + t]).
+// (token t = b / nsb, super-block j = b % nsb at dt[j * m + t]); with deq (AMV_ACT_Q8_K_DEQ) the f16 copies are q * d.
 __global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x, int64_t n_blk,
                                                    uint8_t* __restrict__ y_ggml, int8_t* __restrict__ aq,
                                                    float* __restrict__ ad, int32_t* __restrict__ abs16,
                                                    uint16_t* __restrict__ a16, uint16_t* __restrict__ bs16,
-                                                   float* __restrict__ dt, int nsb, int m) {
+                                                   float* __restrict__ dt, int nsb, int m, int deq) {
     const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= n_blk) return;  // uniform per wave
     const int lane = threadIdx.x & 63;
@@ -85,8 +85,11 @@ __global__ __launch_bounds__(256) void k_quant_q8_K(const float* __restrict__ x,
         if (lane == 0) ad[b] = d;
     }
     if (a16) {
-        const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)q[0]), h1 = __builtin_bit_cast(uint16_t, (_Float16)q[1]);
-        const uint32_t h2 = __builtin_bit_cast(uint16_t, (_Float16)q[2]), h3 = __builtin_bit_cast(uint16_t, (_Float16)q[3]);
+        const float sc = deq ? d : 1.0f;  // q * 1 = q exactly
+        const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)((float)q[0] * sc));
+        const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)((float)q[1] * sc));
+        const uint32_t h2 = __builtin_bit_cast(uint16_t, (_Float16)((float)q[2] * sc));
+        const uint32_t h3 = __builtin_bit_cast(uint16_t, (_Float16)((float)q[3] * sc));
         reinterpret_cast<uint2*>(a16 + b * 256)[lane] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
         if ((lane & 3) == 0) bs16[b * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)s);
         if (lane == 0) dt[(b % nsb) * m + b / nsb] = d;
@@ -406,6 +409,9 @@ extern "C" int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, 
     AMV_REQUIRE(((uintptr_t)x & 15) == 0, "amv_quantize_act: input must be 16-byte aligned");
     AMV_REQUIRE(y_act == nullptr || ((uintptr_t)y_act & 15) == 0, "amv_quantize_act: y_act must be 16-byte aligned");
     hipStream_t st = amv_stream(stream);
+    const int deq = type == AMV_ACT_Q8_0_DEQ || type == AMV_ACT_Q8_K_DEQ;
+    if (type == AMV_ACT_Q8_0_DEQ) type = AMV_ACT_Q8_0_MMA;  // same layout, scaled f16 copies
+    if (type == AMV_ACT_Q8_K_DEQ) type = AMV_ACT_Q8_K_MMA;
     if (type == AMV_T_Q8_0 || type == AMV_ACT_Q8_0_MMA) {
         AMV_REQUIRE(k % 32 == 0, "amv_quantize_act: Q8_0 needs k %% 32 == 0 (k = %lld)", (long long)k);
         AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_quantize_act: bad rule %d", rule);
@@ -423,7 +429,7 @@ extern "C" int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, 
             dt = (float*)((uint8_t*)y_act + L.dt);
         }
         hipLaunchKernelGGL(k_quant_q8_0, grid_for(n, 256), 256, 0, st, x, n, rule, (uint8_t*)y_ggml, aq, ads, a16,
-                           dt, (int)(k / 32), (int)m);
+                           dt, (int)(k / 32), (int)m, deq);
     } else if (type == AMV_T_Q8_K || type == AMV_ACT_Q8_K_MMA) {
         AMV_REQUIRE(k % 256 == 0, "amv_quantize_act: Q8_K needs k %% 256 == 0 (k = %lld)", (long long)k);
         AMV_REQUIRE(y_ggml == nullptr || ((uintptr_t)y_ggml & 3) == 0, "amv_quantize_act: y_ggml misaligned");
@@ -442,7 +448,7 @@ extern "C" int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, 
             dt = (float*)((uint8_t*)y_act + L.dt);
         }
         hipLaunchKernelGGL(k_quant_q8_K, grid_for(nb, 4), 256, 0, st, x, nb, (uint8_t*)y_ggml, aq, ad, abs16, a16,
-                           bs16, dt, (int)(k / 256), (int)m);
+                           bs16, dt, (int)(k / 256), (int)m, deq);
     } else {
         amv_set_error("amv_quantize_act: unsupported activation type %d", type);
         return AMV_ERR_UNSUPPORTED;

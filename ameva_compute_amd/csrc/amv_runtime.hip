@@ -58,7 +58,7 @@ extern "C" int64_t amv_act_bytes(int type, int64_t m, int64_t k) {
     if (m < 0) return -1;
     if (type == AMV_T_Q8_0 && k % 32 == 0) return m * k + m * (k / 32) * 8;
     if (type == AMV_T_Q8_K && k % 256 == 0) return m * k + m * (k / 256) * 4 + m * (k / 16) * 4;
-    if (type == AMV_ACT_Q8_K_MMA && k % 256 == 0) return amv_q8k_mma_layout(m, k).total;
-    if (type == AMV_ACT_Q8_0_MMA && k % 32 == 0) return amv_q8_0_mma_layout(m, k).total;
+    if ((type == AMV_ACT_Q8_K_MMA || type == AMV_ACT_Q8_K_DEQ) && k % 256 == 0) return amv_q8k_mma_layout(m, k).total;
+    if ((type == AMV_ACT_Q8_0_MMA || type == AMV_ACT_Q8_0_DEQ) && k % 32 == 0) return amv_q8_0_mma_layout(m, k).total;
     return -1;
 }

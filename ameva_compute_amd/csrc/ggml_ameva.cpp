@@ -489,8 +489,11 @@ struct Engine {
         // stage (the plain layout is the prefix of the extended one)
         const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K);
         const bool kq = w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K;
-        const int atype = kq ? (mmq ? AMV_ACT_Q8_K_MMA : (int)GGML_TYPE_Q8_K)
-                             : (mmq ? AMV_ACT_Q8_0_MMA : (int)GGML_TYPE_Q8_0);
+        // batched: above 64 tokens the scaled layout (f16 q * d), whose tiled MFMA GEMM accumulates across k without
+        // a per-block epilogue; 8 .. 64 tokens the exact layout (the small-batch kernels read exact f16 integers)
+        const bool deq = M > 64;
+        const int atype = kq ? (mmq ? (deq ? AMV_ACT_Q8_K_DEQ : AMV_ACT_Q8_K_MMA) : (int)GGML_TYPE_Q8_K)
+                             : (mmq ? (deq ? AMV_ACT_Q8_0_DEQ : AMV_ACT_Q8_0_MMA) : (int)GGML_TYPE_Q8_0);
         // src0 in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized tensor of any
         // other buffer is repacked into scratch for this use
         const void* wp = w->data;

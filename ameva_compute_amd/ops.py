@@ -38,15 +38,20 @@ def _need_gpu(t: torch.Tensor, what: str, contiguous: bool = True) -> None:
 # Q8_K activations with the f16 copies the batched Q4_K MUL_MAT reads (include/ameva_hip.h AMV_ACT_Q8_K_MMA)
 Q8_K_MMA = 1015
 Q8_0_MMA = 1008
+# the same layouts with f16 q * d in place of f16 q: the scaled batched MUL_MAT (AMV_ACT_Q8_K_DEQ / AMV_ACT_Q8_0_DEQ)
+Q8_K_DEQ = 1115
+Q8_0_DEQ = 1108
 
 
-def act_type(wtype: int, m: int = 1) -> int:
+def act_type(wtype: int, m: int = 1, exact: bool = False) -> int:
     """ggml vec_dot_type of a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants; for a batched MUL_MAT
-    (m >= MMQ_MIN_M) of Q4_K / Q4_0 / Q8_0 the layout extended with the f16 copies the matrix-core kernels read."""
+    (m >= MMQ_MIN_M) of Q4_K / Q4_0 / Q8_0 the layout extended with the f16 copies the matrix-core kernels read:
+    above MMQ16_MIN_M tokens scaled (DEQ, the fast tiled form) unless exact, else the exact-integer form (MMA)."""
+    deq = m > MMQ16_MIN_M and not exact
     if wtype == Q4_K and m >= MMQ_MIN_M:
-        return Q8_K_MMA
+        return Q8_K_DEQ if deq else Q8_K_MMA
     if wtype in (Q4_0, Q8_0) and m >= MMQ_MIN_M:
-        return Q8_0_MMA
+        return Q8_0_DEQ if deq else Q8_0_MMA
     return Q8_K if wtype in (Q4_K, Q6_K) else Q8_0
 
 
@@ -107,7 +112,7 @@ def quantize_act(x: torch.Tensor, atype: int = Q8_0, rule: int = Q8_X86, ggml: b
     if n < 0:
         raise ValueError(f"quantize_act: type {atype} cannot hold rows of {k}")
     act = torch.empty(n, dtype=torch.uint8, device=x.device)
-    gt = Q8_K if atype == Q8_K_MMA else Q8_0 if atype == Q8_0_MMA else atype
+    gt = Q8_K if atype in (Q8_K_MMA, Q8_K_DEQ) else Q8_0 if atype in (Q8_0_MMA, Q8_0_DEQ) else atype
     g = torch.empty((m, ggml_row_bytes(gt, k)), dtype=torch.uint8, device=x.device) if ggml else None
     check(lib().amv_quantize_act(atype, x2.data_ptr(), m, k, rule, _ptr(g), act.data_ptr(), _stream()),
           "amv_quantize_act")
@@ -126,22 +131,24 @@ def quantize_q4_0(x: torch.Tensor) -> torch.Tensor:
 
 # batch size from which MUL_MAT runs the int8-MFMA kernel (AMEVA_QGEMM_MIN_M of the reference, ggml-ameva.cpp:2486)
 MMQ_MIN_M = 8
+MMQ16_MIN_M = 64  # above this many tokens the tiled f16 kernels run (amv_mmq.hip MMQ16_MIN_M)
 MMQ_TYPES = (Q4_0, Q8_0, Q4_K)  # Q4_K: the activations must be Q8_K_MMA
 
 
 def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = None,
-              kernel: str = "auto") -> torch.Tensor:
+              kernel: str = "auto", act_t: int | None = None) -> torch.Tensor:
     """dst [m, n_rows] f32 from already quantized activations (amv_quantize_act layout of m rows).
     kernel: "auto" (the reference's routing: MFMA GEMM for m >= MMQ_MIN_M where the type has one), "mmv", "mmq".
-    Q4_K on "mmq" needs the activations quantized as Q8_K_MMA (act_type(Q4_K, m))."""
+    Q4_K on "mmq" needs the activations quantized as Q8_K_MMA or Q8_K_DEQ. act_t: the activation layout (the DEQ
+    layouts have the MMA sizes, so they must be named; None: told apart by size, i.e. plain or MMA)."""
     _need_gpu(act, "mul_mat_q")
     if out is None:
         out = torch.empty((m, w.n_rows), dtype=torch.float32, device=act.device)
     use_mmq = kernel == "mmq" or (kernel == "auto" and m >= MMQ_MIN_M and w.type in MMQ_TYPES)
     if use_mmq:
-        check(lib().amv_mul_mat_q_act(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(),
-                                      act_layout(w.type, act, m, w.k), m, out.data_ptr(), w.n_rows, _stream()),
-              "amv_mul_mat_q_act")
+        at = act_layout(w.type, act, m, w.k) if act_t is None else act_t
+        check(lib().amv_mul_mat_q_act(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), at, m,
+                                      out.data_ptr(), w.n_rows, _stream()), "amv_mul_mat_q_act")
     else:
         check(lib().amv_mul_mat_vec(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), m, out.data_ptr(),
                                     w.n_rows, _stream()), "amv_mul_mat_vec")
@@ -237,8 +244,9 @@ def mul_mat(w: QWeight, x: torch.Tensor, rule: int = Q8_X86) -> torch.Tensor:
     x2 = x.reshape(-1, x.shape[-1])
     if x2.shape[1] != w.k:
         raise ValueError(f"mul_mat: k mismatch {x2.shape[1]} != {w.k}")
-    act, _ = quantize_act(x2, act_type(w.type, x2.shape[0]), rule)
-    return mul_mat_q(w, act, x2.shape[0])
+    at = act_type(w.type, x2.shape[0])
+    act, _ = quantize_act(x2, at, rule)
+    return mul_mat_q(w, act, x2.shape[0], act_t=at)
 
 
 def block_sums(w: QWeight, act: torch.Tensor, m: int, kernel: str = "mmv") -> torch.Tensor:

@@ -29,6 +29,8 @@ extern "C" {
  *   AMV_Q8_REF: d = amax/127, q = roundf(x * (1/d))                  -- quantize_row_q8_0_ref (weights, KV cache) */
 #define AMV_ACT_Q8_K_MMA 1015 /* Q8_K activations with the f16 copies the batched K-quant MUL_MAT reads */
 #define AMV_ACT_Q8_0_MMA 1008 /* Q8_0 activations with the f16 copies the batched Q4_0 / Q8_0 MUL_MAT reads */
+#define AMV_ACT_Q8_K_DEQ 1115 /* AMV_ACT_Q8_K_MMA's layout with f16 q * d in place of f16 q (the scaled batched form) */
+#define AMV_ACT_Q8_0_DEQ 1108 /* AMV_ACT_Q8_0_MMA's layout with f16 q * d in place of f16 q (the scaled batched form) */
 #define AMV_Q8_X86 0
 #define AMV_Q8_ARM 1
 #define AMV_Q8_REF 2
@@ -69,7 +71,10 @@ int amv_unrepack(int type, const void* src, void* dst_ggml, int64_t n_rows, int6
  *           AMV_ACT_Q8_0_MMA: the Q8_0 layout, then (16-byte aligned) the same values as f16 [m][k] and the block
  *           scales transposed, f32 [k/32][m]: the input of the batched Q4_0 / Q8_0 MUL_MAT on the f16 matrix cores
  *           (amv_mul_mat_q_act); its prefix is a plain Q8_0 activation of the m rows.
- * type AMV_T Q8_0 (8), Q8_K (15), AMV_ACT_Q8_K_MMA or AMV_ACT_Q8_0_MMA; rule applies to Q8_0 only.
+ *           AMV_ACT_Q8_0_DEQ / AMV_ACT_Q8_K_DEQ: the same layouts (and sizes) with f16 of q * d (one rounding) in
+ *           place of the f16 copies of q: the input of the scaled batched MUL_MAT.
+ * type AMV_T Q8_0 (8), Q8_K (15), AMV_ACT_Q8_K_MMA, AMV_ACT_Q8_0_MMA, AMV_ACT_Q8_K_DEQ or AMV_ACT_Q8_0_DEQ; rule
+ * applies to the Q8_0 forms only.
  * ---------------------------------------------------------------------------------------------------------- */
 int64_t amv_act_bytes(int type, int64_t m, int64_t k);
 int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, int rule, void* y_ggml, void* y_act,
@@ -155,10 +160,13 @@ int amv_mul_mat_q(int wtype, const void* w, int64_t n_rows, int64_t k, const voi
                   int64_t ldd, void* stream);
 int amv_mul_mat_q_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m,
                              int32_t* sums, void* stream);
-/* amv_mul_mat_q with the activation layout named: act_type AMV_T_Q8_0 or AMV_ACT_Q8_0_MMA for Q4_0 / Q8_0 weights,
- * AMV_ACT_Q8_K_MMA for Q4_K. With AMV_ACT_Q8_0_MMA and m > 64 the product runs on the f16 matrix cores
- * (v_mfma_f32_32x32x16_f16 on the exact integers q - 8 / q and q_a: each block's int32 sum comes out exact, then
- * acc += S d_w d_a); smaller batches run the int8 kernel on the layout's Q8_0 prefix. Same result contract. */
+/* amv_mul_mat_q with the activation layout named: act_type AMV_T_Q8_0, AMV_ACT_Q8_0_MMA or AMV_ACT_Q8_0_DEQ for
+ * Q4_0 / Q8_0 weights, AMV_ACT_Q8_K_MMA or AMV_ACT_Q8_K_DEQ for Q4_K. With the MMA layouts and m > 64 the product runs
+ * on the f16 matrix cores on exact integers (v_mfma_f32_32x32x16_f16 on q - 8 / q and q_a: each block's int32 sum
+ * comes out exact, then acc += S d_w d_a); with the DEQ layouts and m > 64 the weights are staged as f16 (q - 8) d_w
+ * (Q4_K: (d sc) q - dmin m) against the activations' f16 q_a d_a and the matrix cores accumulate across all of k (no
+ * per-block epilogue; within ~3e-4 relative L2 of the exact form, the DEQ rounding of both operands to f16 aside).
+ * Smaller batches run the int8 kernel on the layout's plain prefix. Block sums need an MMA layout. */
 int amv_mul_mat_q_act(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type, int64_t m,
                       float* dst, int64_t ldd, void* stream);
 int amv_mul_mat_q_act_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type,

@@ -128,3 +128,58 @@ def test_mmq_q4k_block_sums_and_output(dev, ops, orc, m, n, k):
     assert rel_l2(y, y_ref) < TOL_F32
     y_v = ops.mul_mat_q(w, act, m, kernel="mmv").cpu().numpy()  # the GEMV on the same buffer's Q8_K prefix
     assert rel_l2(y, y_v) < 1e-5
+
+
+def deq_f16_region(act, m, k, q4k):
+    """The f16 region of a DEQ (or MMA) activation buffer, [m, k] halves (offsets of amv_q8k_mma_layout /
+    amv_q8_0_mma_layout)."""
+    base = m * k + (m * (k // 256) * 4 + m * (k // 16) * 4 if q4k else m * (k // 32) * 8)
+    off = (base + 15) // 16 * 16
+    return act[off: off + 2 * m * k].cpu().numpy().view(np.float16).reshape(m, k)
+
+
+@pytest.mark.parametrize("wtype", [2, 8, 12])
+@pytest.mark.parametrize("m,n,k", [(65, 129, 256), (130, 64, 512), (300, 200, 1024), (512, 1000, 4096),
+                                   (200, 4096, 14336 // 256 * 256)])
+def test_scaled_gemm_matches_oracle_and_exact_form(dev, ops, orc, wtype, m, n, k):
+    """The scaled batched MUL_MAT (DEQ layouts: f16 (q - 8) d_w / (d sc) q - dmin m against f16 q_a d_a, one MFMA
+    accumulation across k): the activation's f16 copies are exactly f16(q * d) of its own plain prefix, the plain
+    prefix is ggml's quantization, and the f32 result is within 1e-3 relative L2 of the oracle and of the exact-sum
+    form; block sums are refused on the scaled layout."""
+    q4k = wtype == ops.Q4_K
+    rng = np.random.default_rng(m + n + k + wtype)
+    wg = random_q4k(rng, n, k) if q4k else weights(orc, rng, wtype, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0, :100] *= 30.0
+    a_ref = orc.quantize_q8_K(x) if q4k else orc.quantize_q8_0(x, orc.Q8_X86)
+    y_ref = orc.mul_mat(wtype, wg, n, k, a_ref, m)
+    w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, k)
+    deq_t, mma_t = (ops.Q8_K_DEQ, ops.Q8_K_MMA) if q4k else (ops.Q8_0_DEQ, ops.Q8_0_MMA)
+    act_d, ag = ops.quantize_act(gpu(x, dev), deq_t, ggml=True)
+    assert np.array_equal(ag.cpu().numpy(), a_ref)
+    act_e, _ = ops.quantize_act(gpu(x, dev), mma_t)
+    plain_n = m * k + (m * (k // 256) * 4 + m * (k // 16) * 4 if q4k else m * (k // 32) * 8)
+    assert torch.equal(act_d[:plain_n], act_e[:plain_n])
+    q = act_d[: m * k].cpu().numpy().view(np.int8).reshape(m, k).astype(np.float32)
+    if q4k:
+        d = act_d[m * k: m * k + m * (k // 256) * 4].cpu().numpy().view(np.float32).reshape(m, k // 256)
+        d = np.repeat(d, 256, axis=1)
+    else:
+        meta = act_d[m * k: m * k + m * (k // 32) * 8].cpu().numpy().view(np.float32).reshape(m, k // 32, 2)
+        d = np.repeat(meta[:, :, 0], 32, axis=1)
+    # q * d rounded to f16 once (the exact product), or through f32 first (the compiler may fuse the product and the
+    # conversion into one mixed-precision fma); for Q8_0 the f32 product is exact and both agree
+    # (compared as values: q = 0 times a negative Q8_K scale is -0 on the CPU, +0 from the fused form)
+    once = (q.astype(np.float64) * d.astype(np.float64)).astype(np.float16)
+    twice = (q * d).astype(np.float16)
+    got = deq_f16_region(act_d, m, k, q4k)
+    assert np.all((got == once) | (got == twice))
+    y_d = ops.mul_mat_q(w, act_d, m, kernel="mmq", act_t=deq_t).cpu().numpy()
+    y_e = ops.mul_mat_q(w, act_e, m, kernel="mmq", act_t=mma_t).cpu().numpy()
+    e_ref, e_ex = rel_l2(y_d, y_ref), rel_l2(y_d, y_e)
+    print(f"scaled form: rel L2 {e_ref:.2e} against the oracle, {e_ex:.2e} against the exact form")
+    assert e_ref < TOL_F32 and e_ex < TOL_F32
+    sums = torch.empty(m * n * (k // 256 * 2 if q4k else k // 32), dtype=torch.int32, device=dev)
+    rc = ops.lib().amv_mul_mat_q_act_block_sums(wtype, w.data.data_ptr(), n, k, act_d.data_ptr(), deq_t, m,
+                                                sums.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc != 0 and b"exact layout" in ops.lib().amv_last_error()
