@@ -21,6 +21,11 @@
 // 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
 #include "amv_common.h"
 
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
 typedef _Float16 g16_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 g16_h2 __attribute__((ext_vector_type(2)));
 typedef float g16_f16v __attribute__((ext_vector_type(16)));
@@ -52,21 +57,22 @@ __device__ __forceinline__ void g16_load(uint4 (&sw)[G16_NW(WT)], float& sdw, ui
                                          uint4& sa3, float& sda, int step, const uint8_t* __restrict__ wq,
                                          const uint16_t* __restrict__ wd, int N, int nb, int n0,
                                          const uint16_t* __restrict__ a16, const float* __restrict__ dT, int M, int m0,
-                                         int K) {
+                                         int K, int b0, int b_end) {
     constexpr int BN = 64 * TN, BM = 64 * TM;
     const int t = threadIdx.x;
     const int blk = t & 1;
-    const int b = 2 * step + blk, bc = min(b, nb - 1);  // a block past the end reads the last one, scale 0
+    // blocks b0 .. b_end - 1 of the row (a split of k); a block past the end reads the last one, scale 0
+    const int b = b0 + 2 * step + blk, bc = min(b, b_end - 1);
     if (t < 2 * BN) {
         const int row = min(n0 + (t >> 1), N - 1);
         const size_t bi = (size_t)row * nb + bc;
         if constexpr (WT == AMV_T_Q4_0) {
             sw[0] = *reinterpret_cast<const uint4*>(wq + bi * 16);
-            sdw = b < nb ? amv_h2f(wd[amv_q4_0_didx(row, bc, nb, N)]) : 0.0f;
+            sdw = b < b_end ? amv_h2f(wd[amv_q4_0_didx(row, bc, nb, N)]) : 0.0f;
         } else {
             sw[0] = *reinterpret_cast<const uint4*>(wq + bi * 32);
             sw[G16_NW(WT) - 1] = *reinterpret_cast<const uint4*>(wq + bi * 32 + 16);
-            sdw = b < nb ? amv_h2f(wd[bi]) : 0.0f;
+            sdw = b < b_end ? amv_h2f(wd[bi]) : 0.0f;
         }
     }
     if (t < 2 * BM) {
@@ -77,7 +83,7 @@ __device__ __forceinline__ void g16_load(uint4 (&sw)[G16_NW(WT)], float& sdw, ui
         sa2 = ap[2];
         sa3 = ap[3];
         const int tb = t / BM;  // scale of (block 2 step + tb, token t % BM)
-        sda = dT[(size_t)min(2 * step + tb, nb - 1) * M + min(m0 + t % BM, M - 1)];
+        sda = dT[(size_t)min(b0 + 2 * step + tb, b_end - 1) * M + min(m0 + t % BM, M - 1)];
     }
 }
 
@@ -140,7 +146,7 @@ template <int WT, bool SUMS, int TN, int TM, bool DEQ>
 __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int N,
                                               int nb, const uint16_t* __restrict__ a16, const float* __restrict__ dT,
                                               int M, float* __restrict__ dst, int64_t ldd,
-                                              int32_t* __restrict__ sums, int vec_out) {
+                                              int32_t* __restrict__ sums, int vec_out, int kb_per, int64_t zstride) {
     constexpr int BN = 64 * TN, BM = 64 * TM;
     __shared__ __align__(16) uint16_t sA[2][BN * G16_LDK];
     __shared__ __align__(16) uint16_t sB[2][BM * G16_LDK];
@@ -150,7 +156,10 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
     const int wr = w & 1, wc = w >> 1, c = lane & 31, h = lane >> 5;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int K = nb * 32;
-    const int nsteps = (nb + 1) / 2;
+    // split of k (grid z): blocks b0 .. b_end - 1, output at dst + z * zstride (a partial when split)
+    const int b0 = blockIdx.z * kb_per, b_end = min(nb, b0 + kb_per);
+    const int nsteps = (b_end - b0 + 1) / 2;
+    dst += (size_t)blockIdx.z * zstride;
 
     g16_f16v acc[TN][TM];
 #pragma unroll
@@ -162,13 +171,14 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
 
     uint4 sw[G16_NW(WT)], sa0, sa1, sa2, sa3;
     float sdw = 0.0f, sda = 0.0f;
-    g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, 0, wq, wd, N, nb, n0, a16, dT, M, m0, K);
+    g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, 0, wq, wd, N, nb, n0, a16, dT, M, m0, K, b0, b_end);
     g16_store<WT, TN, TM, DEQ>(sw, sdw, sa0, sa1, sa2, sa3, sda, sA[0], sB[0], sDw[0], sDa[0]);
     __syncthreads();
     for (int step = 0; step < nsteps; ++step) {
         const int buf = step & 1;
         if (step + 1 < nsteps)
-            g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, step + 1, wq, wd, N, nb, n0, a16, dT, M, m0, K);
+            g16_load<WT, TN, TM>(sw, sdw, sa0, sa1, sa2, sa3, sda, step + 1, wq, wd, N, nb, n0, a16, dT, M, m0, K, b0,
+                                 b_end);
         if constexpr (DEQ) {  // scaled operands: accumulate across the whole step
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
 #pragma unroll
                     for (int j = 0; j < TM; ++j) C[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[j], C[i][j], 0, 0, 0);
             }
-            const int b = 2 * step + bl;
+            const int b = b0 + 2 * step + bl;
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const int tl = 32 * (TM * wc + j) + c;  // token of this lane in the tile
@@ -222,7 +232,7 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int n = n0 + 32 * (TN * wr + i) + 8 * (r >> 2) + 4 * h + (r & 3);
-                            if (b < nb && m < M && n < N) sums[((size_t)m * N + n) * nb + b] = (int32_t)C[i][j][r];
+                            if (b < b_end && m < M && n < N) sums[((size_t)m * N + n) * nb + b] = (int32_t)C[i][j][r];
                         }
                 } else {
                     const float da = sDa[buf][bl * BM + tl];
@@ -275,6 +285,92 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
 
 // Q4_0 / Q8_0 weights (MI355X layout), activations AMV_ACT_Q8_0_MMA of m rows. Tile: 128 x 128, or 64 x 64 when
 // the big tiles would leave CUs idle.
+// ---------------------------------------------------------------------------------------------------------------
+// Split of k for the scaled (DEQ) form when the output tiles alone leave the CUs idle (the 4096-row, k = 14336 down
+// projection): split z writes its partial tile to a workspace and k_splitk_sum adds the S partials in order z = 0 ..
+// S - 1 (deterministic) into dst. The workspace is this library's, one per device, grown outside graph capture and
+// never freed (a captured graph keeps the address it recorded); a call under capture that would need more than the
+// device's workspace runs unsplit. Calls that split k share it: two on different streams must not overlap in time
+// (calls on one stream are ordered).
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ part, int S, int64_t zstride, int m,
+                                                   int n, float* __restrict__ dst, int64_t ldd, int vec) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (vec) {  // 4 consecutive outputs (n % 4 == 0, 16-byte aligned rows)
+        const int n4 = n >> 2;
+        if (i >= (int64_t)m * n4) return;
+        const int r = (int)(i / n4), c = (int)(i % n4) * 4;
+        float4 a = *reinterpret_cast<const float4*>(part + (size_t)r * n + c);
+        for (int z = 1; z < S; ++z) {
+            const float4 b = *reinterpret_cast<const float4*>(part + z * zstride + (size_t)r * n + c);
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        *reinterpret_cast<float4*>(dst + (size_t)r * ldd + c) = a;
+    } else {
+        if (i >= (int64_t)m * n) return;
+        const int r = (int)(i / n), c = (int)(i % n);
+        float a = part[(size_t)r * n + c];
+        for (int z = 1; z < S; ++z) a += part[z * zstride + (size_t)r * n + c];
+        dst[(size_t)r * ldd + c] = a;
+    }
+}
+
+namespace {
+std::mutex g_splitk_mu;
+std::map<int, std::pair<float*, size_t>> g_splitk_ws;  // device -> (buffer, bytes)
+}  // namespace
+
+static float* splitk_workspace(size_t bytes, hipStream_t st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_splitk_mu);
+    auto& w = g_splitk_ws[dev];
+    if (w.second >= bytes) return w.first;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    const size_t want = std::max(bytes, 2 * w.second);
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    w = {(float*)p, want};  // the previous buffer stays allocated: a captured graph may still write it
+    return w.first;
+}
+
+// splits of k for `tiles` output tiles over `steps` pipeline steps (64 of k each): only for k >= 64 SPLITK_MIN_TOTAL
+// (the partials' extra traffic, (S + 1) m n 4 bytes, must stay small beside the product), doubled while the launch has
+// fewer than SPLITK_TARGET workgroups and each split keeps >= SPLITK_MIN_STEPS steps (up to 8)
+#ifndef SPLITK_TARGET
+#define SPLITK_TARGET 1024
+#endif
+#ifndef SPLITK_MIN_STEPS
+#define SPLITK_MIN_STEPS 24
+#endif
+#ifndef SPLITK_MIN_TOTAL
+#define SPLITK_MIN_TOTAL 96
+#endif
+static int splitk_count(int64_t tiles, int steps) {
+    int S = 1;
+    if (steps < SPLITK_MIN_TOTAL) return 1;
+    while (S < 8 && tiles * S < SPLITK_TARGET && steps / (2 * S) >= SPLITK_MIN_STEPS) S *= 2;
+    return S;
+}
+
+static void splitk_reduce(const float* part, int S, int64_t zstride, int64_t m, int64_t n, float* dst, int64_t ldd,
+                          hipStream_t st) {
+    const int vec = n % 4 == 0 && ldd % 4 == 0 && ((uintptr_t)dst & 15) == 0;
+    const int64_t items = vec ? m * (n / 4) : m * n;
+    hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, part, S, zstride, (int)m,
+                       (int)n, dst, ldd, vec);
+}
+
 int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
               int64_t ldd, int32_t* sums, int deq, hipStream_t st) {
     const int nb = (int)(k / 32);
@@ -295,9 +391,32 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
     // scaled form (DEQ), swept over 4096 / 6144 / 14336 / 28672 x 4096 and 4096 x 14336 at m = 128, 512 for Q4_0,
     // Q8_0, Q4_K: 128 x 128 from 224 workgroups (14336 x 4096 at 512: 83 us against 131 for 64 x 64), else 64 x 64
     const int cfg = deq ? (wgs(2, 2) >= 224 ? 22 : 11) : (wgs(2, 2) >= 384 ? 22 : 11);
-#define G16_LAUNCH(WT, S, TN, TM, D)                                                                                  \
-    hipLaunchKernelGGL((k_mmq16<WT, S, TN, TM, D>), grid(TN, TM), dim3(256), 0, st, wq, wd, (int)n_rows, nb, a16, dT, \
-                       (int)m, dst, ldd, sums, vec_out)
+    // DEQ: split of k when the tiles leave CUs idle
+    int nz = 1, kb_per = nb;
+    float* out = dst;
+    int64_t ldo = ldd, zstride = 0;
+    int vo = vec_out;
+    if (deq && !sums) {
+        const int S = splitk_count(cfg == 22 ? wgs(2, 2) : wgs(1, 1), (nb + 1) / 2);
+        if (S > 1) {
+            kb_per = ((nb + S - 1) / S + 1) & ~1;  // whole pipeline steps
+            nz = (nb + kb_per - 1) / kb_per;
+            float* ws = nz > 1 ? splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
+            if (ws) {
+                out = ws;
+                ldo = n_rows;
+                zstride = m * n_rows;
+                vo = n_rows % 4 == 0;
+            } else {
+                nz = 1;
+                kb_per = nb;
+            }
+        }
+    }
+    const auto gridz = [&](int tn, int tm) { dim3 g = grid(tn, tm); g.z = (unsigned)nz; return g; };
+#define G16_LAUNCH(WT, S, TN, TM, D)                                                                                 \
+    hipLaunchKernelGGL((k_mmq16<WT, S, TN, TM, D>), gridz(TN, TM), dim3(256), 0, st, wq, wd, (int)n_rows, nb, a16, \
+                       dT, (int)m, out, ldo, sums, vo, kb_per, zstride)
 #define G16_CFG(WT, S, D)                          \
     if (cfg == 22) G16_LAUNCH(WT, S, 2, 2, D);     \
     else if (cfg == 12) G16_LAUNCH(WT, S, 1, 2, D); \
@@ -314,6 +433,7 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
     }
 #undef G16_CFG
 #undef G16_LAUNCH
+    if (nz > 1) splitk_reduce(out, nz, zstride, m, n_rows, dst, ldd, st);
     return amv_check_launch("amv_mul_mat_q_act");
 }
 
@@ -338,10 +458,10 @@ template <int TN, int TM>
 __device__ __forceinline__ void g16k_load(G16K& s, int step, const uint4* __restrict__ wq, const uint4* __restrict__ wh,
                                           int N, int nsb, int n0, const uint16_t* __restrict__ a16,
                                           const uint16_t* __restrict__ bs16, const float* __restrict__ dT, int M, int m0,
-                                          int K) {
+                                          int K, int sb0) {
     constexpr int BN = 64 * TN, BM = 64 * TM;
     const int t = threadIdx.x, hf = t & 1;
-    const int j = step >> 2, c = step & 3;
+    const int j = sb0 + (step >> 2), c = step & 3;  // super-block j (of a split starting at sb0), chunk c
     if (t < 2 * BN) {
         const int row = min(n0 + (t >> 1), N - 1);
         const size_t sb = (size_t)row * nsb + j;
@@ -445,7 +565,8 @@ __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq,
                                                   int nsb, const uint16_t* __restrict__ a16,
                                                   const uint16_t* __restrict__ bs16, const float* __restrict__ dT,
                                                   int M, float* __restrict__ dst, int64_t ldd,
-                                                  int32_t* __restrict__ sums, int vec_out) {
+                                                  int32_t* __restrict__ sums, int vec_out, int sb_per,
+                                                  int64_t zstride) {
     constexpr int BN = 64 * TN, BM = 64 * TM;
     __shared__ __align__(16) uint16_t sA[2][BN * G16_LDK];
     __shared__ __align__(16) uint16_t sB[2][BM * G16_LDK];
@@ -455,7 +576,10 @@ __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq,
     const int wr = w & 1, wc = w >> 1, c32 = lane & 31, h = lane >> 5;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int K = nsb * 256;
-    const int nsteps = nsb * 4;
+    // split of k (grid z): super-blocks sb0 .. sb_end - 1, output at dst + z * zstride (a partial when split)
+    const int sb0 = blockIdx.z * sb_per, sb_end = min(nsb, sb0 + sb_per);
+    const int nsteps = (sb_end - sb0) * 4;
+    dst += (size_t)blockIdx.z * zstride;
 
     g16_f16v acc[TN][TM], C[TN][TM];
     g16_f16v C0[TN][TM];  // SUMS: the first half's exact integers
@@ -467,12 +591,12 @@ __global__ __launch_bounds__(256) void k_mmq16_q4k(const uint4* __restrict__ wq,
             for (int r = 0; r < 16; ++r) acc[i][jj][r] = C[i][jj][r] = C0[i][jj][r] = 0.0f;
 
     G16K st;
-    g16k_load<TN, TM>(st, 0, wq, wh, N, nsb, n0, a16, bs16, dT, M, m0, K);
+    g16k_load<TN, TM>(st, 0, wq, wh, N, nsb, n0, a16, bs16, dT, M, m0, K, sb0);
     g16k_store<TN, TM, DEQ>(st, 0, sA[0], sB[0], sD[0], sDm[0], sMn[0], sBs[0], sDa[0]);
     __syncthreads();
     for (int step = 0; step < nsteps; ++step) {
-        const int buf = step & 1, j = step >> 2, c = step & 3, jp = j & 1;
-        if (step + 1 < nsteps) g16k_load<TN, TM>(st, step + 1, wq, wh, N, nsb, n0, a16, bs16, dT, M, m0, K);
+        const int buf = step & 1, j = sb0 + (step >> 2), c = step & 3, jp = (step >> 2) & 1;
+        if (step + 1 < nsteps) g16k_load<TN, TM>(st, step + 1, wq, wh, N, nsb, n0, a16, bs16, dT, M, m0, K, sb0);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int kk = 16 * ks + 8 * h;
@@ -589,9 +713,31 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
     // tile (occupancy 2) wins once it fills 448 workgroups, else 64 x 64 (occupancy 3); the 128 x 128 tile holds 256
     // VGPRs + 123 AGPRs at occupancy 1 and lost to both everywhere.
     const int cfg = deq ? (wgs(2, 2) >= 224 ? 22 : 11) : (wgs(1, 2) >= 448 ? 12 : 11);  // DEQ: the Q4_0 sweep's rule
-#define G16K_LAUNCH(S, TN, TM, D)                                                                                     \
-    hipLaunchKernelGGL((k_mmq16_q4k<S, TN, TM, D>), grid(TN, TM), dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16,     \
-                       bs16, dT, (int)m, dst, ldd, sums, vec_out)
+    int nz = 1, sb_per = nsb;
+    float* out = dst;
+    int64_t ldo = ldd, zstride = 0;
+    int vo = vec_out;
+    if (deq && !sums) {  // split of k when the tiles leave CUs idle (4 pipeline steps per super-block)
+        const int S = splitk_count(cfg == 22 ? wgs(2, 2) : wgs(1, 1), 4 * nsb);
+        if (S > 1) {
+            sb_per = (nsb + S - 1) / S;
+            nz = (nsb + sb_per - 1) / sb_per;
+            float* ws = nz > 1 ? splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
+            if (ws) {
+                out = ws;
+                ldo = n_rows;
+                zstride = m * n_rows;
+                vo = n_rows % 4 == 0;
+            } else {
+                nz = 1;
+                sb_per = nsb;
+            }
+        }
+    }
+    const auto gridz = [&](int tn, int tm) { dim3 g = grid(tn, tm); g.z = (unsigned)nz; return g; };
+#define G16K_LAUNCH(S, TN, TM, D)                                                                                    \
+    hipLaunchKernelGGL((k_mmq16_q4k<S, TN, TM, D>), gridz(TN, TM), dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16,  \
+                       bs16, dT, (int)m, out, ldo, sums, vo, sb_per, zstride)
     if (sums) {  // instrumentation: the small tile (two accumulator sets fit its registers)
         G16K_LAUNCH(true, 1, 1, false);
     } else if (deq) {
@@ -604,5 +750,6 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
         else G16K_LAUNCH(false, 1, 1, false);
     }
 #undef G16K_LAUNCH
+    if (nz > 1) splitk_reduce(out, nz, zstride, m, n_rows, dst, ldd, st);
     return amv_check_launch("amv_mul_mat_q_act");
 }
