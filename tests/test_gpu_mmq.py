@@ -183,3 +183,39 @@ def test_scaled_gemm_matches_oracle_and_exact_form(dev, ops, orc, wtype, m, n, k
     rc = ops.lib().amv_mul_mat_q_act_block_sums(wtype, w.data.data_ptr(), n, k, act_d.data_ptr(), deq_t, m,
                                                 sums.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert rc != 0 and b"exact layout" in ops.lib().amv_last_error()
+
+
+def test_split_k_under_graph_capture(dev, ops, orc):
+    """The scaled GEMM split over k (4096 x 14336 at 200 tokens) inside a captured graph: every replay equals the
+    eager result bit for bit (the partials are summed in a fixed order), also after eager calls that grow the
+    library's workspace between the replays (the graph keeps the buffer it recorded, which stays allocated)."""
+    rng = np.random.default_rng(77)
+    n, k, m = 4096, 14336, 200
+    wg = weights(orc, rng, ops.Q4_0, n, k)
+    w = ops.QWeight.from_ggml(ops.Q4_0, gpu(wg, dev), n, k)
+    x = gpu(rng.standard_normal((m, k)).astype(np.float32), dev)
+    act, _ = ops.quantize_act(x, ops.Q8_0_DEQ)
+    y_eager = ops.mul_mat_q(w, act, m, kernel="mmq", act_t=ops.Q8_0_DEQ)
+    out = torch.empty_like(y_eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.mul_mat_q(w, act, m, out, kernel="mmq", act_t=ops.Q8_0_DEQ)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.mul_mat_q(w, act, m, out, kernel="mmq", act_t=ops.Q8_0_DEQ)
+    big_m = 512
+    xb = gpu(rng.standard_normal((big_m, k)).astype(np.float32), dev)
+    actb, _ = ops.quantize_act(xb, ops.Q8_0_DEQ)
+    for rep in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y_eager), rep
+        # eager work between the replays, the larger batch asking for a larger workspace
+        yb = ops.mul_mat_q(w, actb, big_m, kernel="mmq", act_t=ops.Q8_0_DEQ)
+        torch.cuda.synchronize()
+        assert torch.isfinite(yb).all()
+    assert torch.equal(ops.mul_mat_q(w, act, m, kernel="mmq", act_t=ops.Q8_0_DEQ), y_eager)
