@@ -393,6 +393,27 @@ def pmc_probe(ops, torch, dev):
                       "copy_dispatches": 50, "copy_bytes_each_way": n * 4}), flush=True)
 
 
+def pmc_gemm(ops, torch, dev):
+    """Dispatches for the matrix-core counters: the scaled batched Q4_K MUL_MAT at M = 512 on the Llama-3-8B FFN
+    shapes (14336 x 4096, then 4096 x 14336, whose k is split: its launch is followed by k_splitk_sum), 20 eager
+    launches each over one weight."""
+    res = {}
+    g = torch.Generator(device=dev)
+    for n, k in ((14336, 4096), (4096, 14336)):
+        w = make_weights(ops, torch, n, k, 1, 300 + n, dev, ops.Q4_K)[0]
+        g.manual_seed(512 + n)
+        x = torch.randn((512, k), generator=g, device=dev)
+        at = ops.act_type(ops.Q4_K, 512)
+        act, _ = ops.quantize_act(x, at, ops.Q8_X86)
+        out = torch.empty((512, n), dtype=torch.float32, device=dev)
+        for _ in range(20):
+            ops.mul_mat_q(w, act, 512, out, act_t=at)
+        torch.cuda.synchronize()
+        res[f"q4_K_{n}x{k}_m512"] = {"dispatches": 20, "ops_each": 2 * 512 * n * k}
+        del w
+    print(json.dumps(res), flush=True)
+
+
 INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix peak (5.0 POPS)
 
 
@@ -579,6 +600,8 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the 32-layer model figures")
     ap.add_argument("--only-bitnet", action="store_true", help="only the BitNet 2B engine decode figures")
     ap.add_argument("--only-load", action="store_true", help="only the weight load path figures (repack, upload)")
+    ap.add_argument("--pmc-gemm", action="store_true",
+                    help="for rocprofv3 --pmc: 20 eager scaled Q4_K MUL_MATs at M = 512 on each FFN shape")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
@@ -596,6 +619,9 @@ def main():
 
     if args.pmc_probe:
         pmc_probe(ops, torch, dev)
+        return
+    if args.pmc_gemm:
+        pmc_gemm(ops, torch, dev)
         return
     if args.only_layer:
         print(json.dumps(bench_layer(torch, dev, args)), flush=True)
