@@ -73,6 +73,9 @@ def test_quantize_q8_K_bytes(dev, ops, orc):
     x[2, 256:512] = 3.0          # ties for the max: the first element wins
     x[2, 300] = -3.0
     x[3] *= 1e-4
+    x[4, :256] = 0.0  # exact ties (iscale = 1): round half to even, as the oracle's known answers pin
+    x[4, 0] = -127.0
+    x[4, 1:11] = [2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 126.5, -126.5, 64.5]
     _, g = ops.quantize_act(gpu(x, dev), ops.Q8_K, ggml=True)
     want = orc.quantize_q8_K(x)
     assert np.array_equal(g.cpu().numpy(), want)

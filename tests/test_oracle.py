@@ -156,6 +156,27 @@ def test_q8_K_invariants(orc):
     assert not z.any()
 
 
+def test_q8_K_ties_round_half_even(orc):
+    """Known answers at exact ties: a block whose largest element is -127 (or +127) has iscale = -127/max = +1 (-1)
+    exactly, so half-integer inputs land on ties, which ggml's nearest_int (the 1.5 * 2^23 addition in the default
+    rounding mode) resolves to the even neighbour, as numpy's rint does; d = 1 / iscale."""
+    ties = np.array([2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 126.5, -126.5, 64.5], np.float32)
+    for lead, sign in ((-127.0, 1.0), (127.0, -1.0)):
+        x = np.zeros((1, 256), np.float32)
+        x[0, 0] = lead
+        x[0, 1:1 + ties.size] = ties
+        x[0, 100] = 3.25  # not a tie: nearest
+        y = orc.quantize_q8_K(x).reshape(292)
+        assert y[:4].copy().view(np.float32)[0] == sign
+        q = y[4:260].view(np.int8).astype(np.int32)
+        want = np.zeros(256, np.int32)
+        want[0] = -127
+        want[1:1 + ties.size] = (sign * np.array([2, 4, -2, -4, 0, 2, 0, 126, -126, 64])).astype(np.int32)
+        want[100] = int(sign * 3)
+        assert np.array_equal(q, want)
+        assert np.array_equal(np.rint(sign * x[0]).astype(np.int32), want)
+
+
 # ------------------------------------------------------------------------------------------- K-quant layouts
 def _pack_k4_scales(sc, mn):
     """ggml's documented 12-byte packing of 8 six-bit scales and mins (the inverse of get_scale_min_k4)."""
