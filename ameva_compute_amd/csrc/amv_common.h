@@ -375,8 +375,8 @@ __device__ __forceinline__ float4 amv_load4_coh(const float* p) {
 // sum of squares is defined for 1024 virtual lanes: lane t sums the float4 chunks t, t + 1024, ... as f32 squares in
 // double, a 64-lane butterfly per virtual wave, then the 16 wave sums in order. A workgroup of NT threads (NT
 // divides 1024) plays V = 1024 / NT virtual lanes per thread (t = tid + NT v) and loads all V chunks of a round
-// before summing, so a row of up to 1024 chunks costs one memory round trip and its values stay in registers for
-// the second pass: y = x * scale, o = y * w, act = the quantized o (y without w). Any output may be NULL; the chunks
+// before summing, so a row of up to 1024 chunks costs one memory round trip (its w chunks load in the same one) and
+// its values stay in registers for the second pass: y = x * scale, o = y * w, act = the quantized o (y without w). Any output may be NULL; the chunks
 // of a quantization block sit in consecutive lanes as amv_act_store4 needs (n % 32 == 0 with Q8_0, % 256 with
 // Q8_K).
 #define AMV_RMS_VLANES 1024
@@ -384,13 +384,13 @@ __device__ __forceinline__ float amv_rms_scale(double tot, int n, float eps) {
     const float mean = (float)(tot / (double)n);
     return 1.0f / sqrtf(mean + eps);
 }
-__device__ __forceinline__ void amv_rms_chunk(int c, float4 v, float scale, const float* __restrict__ w,
+// chunk c of the second pass; wv = chunk c of w when has_w
+__device__ __forceinline__ void amv_rms_chunk(int c, float4 v, float scale, bool has_w, float4 wv,
                                               float* __restrict__ y, float* __restrict__ o, const AmvActOut& act) {
     const float4 yv = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
     if (y) reinterpret_cast<float4*>(y)[c] = yv;
     float4 qv = yv;
-    if (w) {
-        const float4 wv = reinterpret_cast<const float4*>(w)[c];
+    if (has_w) {
         qv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
         if (o) reinterpret_cast<float4*>(o)[c] = qv;
     }
@@ -406,7 +406,8 @@ __device__ __forceinline__ void amv_rms_row(const float4* __restrict__ x4, int n
     static_assert(AMV_RMS_VLANES % NT == 0 && NT % 64 == 0, "NT must divide 1024 in whole waves");
     constexpr int V = AMV_RMS_VLANES / NT;
     const int tid = threadIdx.x;
-    float4 xr[V];
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 xr[V], wr[V];
     double s[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) s[v] = 0.0;
@@ -415,6 +416,8 @@ __device__ __forceinline__ void amv_rms_row(const float4* __restrict__ x4, int n
         for (int v = 0; v < V; ++v) {
             const int c = k0 + tid + NT * v;
             xr[v] = c < n4 ? x4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            // a row of one round: its w chunks load with x (one memory round trip for both)
+            wr[v] = c < n4 && w && n4 <= AMV_RMS_VLANES ? w4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
 #pragma unroll
         for (int v = 0; v < V; ++v) {  // absent chunks add exact zeros
@@ -440,10 +443,11 @@ __device__ __forceinline__ void amv_rms_row(const float4* __restrict__ x4, int n
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             const int c = tid + NT * v;
-            if (c < n4) amv_rms_chunk(c, xr[v], scale, w, y, o, act);
+            if (c < n4) amv_rms_chunk(c, xr[v], scale, w != nullptr, wr[v], y, o, act);
         }
     } else {
-        for (int c = tid; c < n4; c += NT) amv_rms_chunk(c, x4[c], scale, w, y, o, act);
+        for (int c = tid; c < n4; c += NT)
+            amv_rms_chunk(c, x4[c], scale, w != nullptr, w ? w4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f), y, o, act);
     }
 }
 
