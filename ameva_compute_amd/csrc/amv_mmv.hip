@@ -56,13 +56,16 @@ struct MmvPost {
     AmvActOut act;  // quantized output of the tail (Q8_0 or Q8_K activation row)
 };
 
+// Stacked SWIGLU: a wave owns the R / 2 consecutive outputs o = (R / 2) wave + i, i.e. gate rows o (r = i) and up
+// rows F + o (r = R / 2 + i), F = n_rows / 2.
 template <int EP>
 __device__ __forceinline__ int mmv_row(int wave, int r, int R, int n_rows) {
-    return MMV_STACKED(EP) ? wave + r * (n_rows >> 1) : wave * R + r;
+    const int P = R >> 1;
+    return MMV_STACKED(EP) ? P * wave + r % P + (r / P) * (n_rows >> 1) : wave * R + r;
 }
 template <int EP>
 __device__ __forceinline__ bool mmv_wave_live(int wave, int R, int n_rows) {
-    return MMV_STACKED(EP) ? wave < (n_rows >> 1) : wave * R < n_rows;
+    return MMV_STACKED(EP) ? (R >> 1) * wave < (n_rows >> 1) : wave * R < n_rows;
 }
 __device__ __forceinline__ float mmv_silu(float x) { return x / (1.0f + expf(-x)); }
 
@@ -91,7 +94,8 @@ template <int R, int EP, int S>
 __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int wi, int ks, bool live, int wave,
                                            int n_rows, float* __restrict__ dst, const float* __restrict__ epi,
                                            float* __restrict__ eout, const MmvPost& post, const MmvRopeAt& ra) {
-    static_assert((!MMV_STACKED(EP) && EP != MMV_EP_ROPE_KV) || R == 2, "stacked SWIGLU and ROPE pair two rows per wave");
+    static_assert(EP != MMV_EP_ROPE_KV || R == 2, "ROPE pairs the two rows of a wave");
+    static_assert(!MMV_STACKED(EP) || R == 2 || R == 4, "stacked SWIGLU takes 1 or 2 outputs per wave");
     float t[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) t[r] = amv_wave_sum(acc[r]);
@@ -135,12 +139,19 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
         return;
     }
     if constexpr (MMV_STACKED(EP)) {
-        if (dst) {
-            dst[wave] = t[0];
-            dst[wave + (n_rows >> 1)] = t[1];
+        constexpr int P = R / 2;
+        const int F = n_rows >> 1;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int o = P * wave + i;
+            if (o >= F) break;
+            if (dst) {
+                dst[o] = t[i];
+                dst[o + F] = t[P + i];
+            }
+            if constexpr (EP == MMV_EP_SWIGLU_Q8) amv_store_coh(eout + o, mmv_silu(t[i]) * t[P + i]);
+            else eout[o] = mmv_silu(t[i]) * t[P + i];
         }
-        if constexpr (EP == MMV_EP_SWIGLU_Q8) amv_store_coh(eout + wave, mmv_silu(t[0]) * t[1]);
-        else eout[wave] = mmv_silu(t[0]) * t[1];
         return;
     }
 #pragma unroll
@@ -156,7 +167,7 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
 }
 
 // Tails of EP 6 and EP 7, run by every thread of the workgroup after the epilogue stores.
-template <int EP, int S>
+template <int EP, int S, int R>
 __device__ __forceinline__ void mmv_tail(const MmvPost& post, const float* eout, int n_rows) {
     if constexpr (EP == MMV_EP_ADD_NORM) {
         if (!amv_arrive_last_tree(post.counters)) return;
@@ -165,9 +176,9 @@ __device__ __forceinline__ void mmv_tail(const MmvPost& post, const float* eout,
         amv_rms_row<256>(reinterpret_cast<const float4*>(eout), n_rows / 4, post.eps, post.norm_w, post.norm_y,
                          post.norm_o, post.act, sred);
     } else {
-        // a workgroup's 4 / S outputs lie in one block of BS (the launcher checks that BS divides n_rows / 2); the
-        // first wave of the last workgroup quantizes it, 4 values per lane
-        constexpr int per_wg = 4 / S;
+        // a workgroup's (4 / S) (R / 2) outputs lie in one block of BS (the launcher checks that BS divides
+        // n_rows / 2); the first wave of the last workgroup quantizes it, 4 values per lane
+        constexpr int per_wg = 4 / S * (R / 2);
         const int BS = post.act.type == AMV_T_Q8_K ? 256 : 32;
         const int blk = (int)blockIdx.x * per_wg / BS;
         if (!amv_arrive_last(post.counters + AMV_CNT_STRIDE * blk, BS / per_wg)) return;
@@ -264,7 +275,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
     }
     if constexpr (!BLOCK_SUMS) {
         mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
-        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S, R>(post, eout, n_rows);
     }
 }
 
@@ -330,7 +341,7 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, 
     }
     if constexpr (!BLOCK_SUMS) {
         mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
-        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S, R>(post, eout, n_rows);
     }
 }
 
@@ -410,7 +421,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
     }
     if constexpr (!BLOCK_SUMS) {
         mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
-        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S, R>(post, eout, n_rows);
     }
 }
 
@@ -480,7 +491,7 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
     }
     if constexpr (!BLOCK_SUMS) {
         mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
-        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S>(post, eout, n_rows);
+        if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S, R>(post, eout, n_rows);
     }
 }
 
@@ -507,7 +518,7 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 16);
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
-    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const int waves = MMV_STACKED(EP) ? a.n_rows / R : (a.n_rows + R - 1) / R;
     const bool full = nb % (64 * U) == 0 && (MMV_STACKED(EP) || a.n_rows % R == 0);
     const dim3 grid((waves * S + 3) / 4);
     if (a.n_rows % 2 == 0 && full)
@@ -529,7 +540,7 @@ static void launch_q8_0(const MmvArgs& a, hipStream_t st) {
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 32);
     const int2* ads = reinterpret_cast<const int2*>(a.ameta0);
     const int8_t* aq = a.aq;
-    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const int waves = MMV_STACKED(EP) ? a.n_rows / R : (a.n_rows + R - 1) / R;
     hipLaunchKernelGGL((k_mmv_q8_0<R, U, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wq, wd, a.n_rows, nb, aq, ads,
                        a.dst, a.sums, a.epi, a.eout, a.post);
 }
@@ -540,7 +551,7 @@ static void launch_q4_K(const MmvArgs& a, hipStream_t st) {
     const int64_t nblk = (int64_t)a.n_rows * nsb;
     const uint4* wq = reinterpret_cast<const uint4*>(a.w);
     const uint4* wh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
-    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const int waves = MMV_STACKED(EP) ? a.n_rows / R : (a.n_rows + R - 1) / R;
     hipLaunchKernelGGL((k_mmv_q4_K<R, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
                        (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout, a.post);
 }
@@ -553,7 +564,7 @@ static void launch_q6_K(const MmvArgs& a, hipStream_t st) {
     const uint4* wqh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
     const uint4* wsc = reinterpret_cast<const uint4*>(a.w + nblk * 192);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(a.w + nblk * 208);
-    const int waves = MMV_STACKED(EP) ? a.n_rows / 2 : (a.n_rows + R - 1) / R;
+    const int waves = MMV_STACKED(EP) ? a.n_rows / R : (a.n_rows + R - 1) / R;
     hipLaunchKernelGGL((k_mmv_q6_K<R, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wl, wqh, wsc, wd, a.n_rows, nsl,
                        a.aq, (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout, a.post);
 }
@@ -603,7 +614,8 @@ static void launch_q6_K_s(const MmvArgs& a, hipStream_t st, int S) {
 }
 
 // Kernel variant (rows per wave R, blocks-per-lane unroll U) chosen from the block count of a row; the table is the
-// result of the launch-shape sweep on MI355X. The stacked SWIGLU epilogue pairs rows w and F + w, so it runs R = 2.
+// result of the launch-shape sweep on MI355X. The stacked SWIGLU epilogue pairs gate row o with up row F + o: R = 2 (one output per wave), or for the Q4_K
+// gate/up of 16384+ rows R = 4 (two outputs per wave, 1904 -> 1877 us per 32-layer model token).
 // The block-sum instrumentation runs without a split (S = 1).
 template <bool BS, int EP>
 static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
@@ -639,6 +651,14 @@ static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
                                                                              : split(groups2, steps);
         if constexpr (!BS && !MMV_STACKED(EP) && EP != MMV_EP_ROPE_KV && !MMV_TAIL(EP)) {
             if (a.n_rows >= 8192 && a.n_rows % 4 == 0 && steps < 4) {
+                launch_q4_K_s<4, BS, EP>(a, st, S);
+                return AMV_OK;
+            }
+        }
+        if constexpr (!BS && MMV_STACKED(EP)) {
+            // the stacked gate/up of 16384+ rows unsplit: two outputs per wave (rows o, o + 1 and F + o, F + o + 1),
+            // as the plain GEMV's 4 rows per wave
+            if (a.n_rows >= 16384 && a.n_rows % 4 == 0 && S == 1) {
                 launch_q4_K_s<4, BS, EP>(a, st, S);
                 return AMV_OK;
             }

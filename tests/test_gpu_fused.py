@@ -76,13 +76,15 @@ def test_gemv_add_rms_norm(dev, ops, orc, wtype, n, k, act_t):
 
 @pytest.mark.parametrize("wtype,F,k,act_t", [(2, 14336, 4096, 8), (12, 14336, 4096, 15), (8, 64, 256, 8),
                                              (14, 256, 512, 15), (2, 32, 64, 8), (12, 512, 256, 15),
-                                             (2, 64, 8192, 8), (12, 256, 8192, 15)])
+                                             (2, 64, 8192, 8), (12, 256, 8192, 15), (12, 8192, 256, 15)])
 def test_gemv_swiglu_act(dev, ops, orc, wtype, F, k, act_t):
     rng = np.random.default_rng(F + k + wtype)
     n = 2 * F
     w = ops.QWeight.from_ggml(wtype, gpu(weight(rng, orc, wtype, n, k), dev), n, k)
     act = act_of(ops, gpu(rng.standard_normal(k).astype(np.float32), dev), ops.act_type(wtype))
     v_ref, h_ref = ops.mul_mat_vec_ep(w, act, ops.EP_SWIGLU_STACKED)
+    # the stacked launches (1 or, from 16384 rows, 2 outputs per wave) sum every row as the plain GEMV does
+    assert torch.equal(v_ref, ops.mul_mat_q(w, act, 1, kernel="mmv").reshape(-1))
     a_ref = act_of(ops, h_ref, act_t)
     cnt = torch.zeros(ops.swiglu_counter_words(n), dtype=torch.int32, device=dev)
     for _ in range(2):
