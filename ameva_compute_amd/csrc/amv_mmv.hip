@@ -614,8 +614,9 @@ static void launch_q6_K_s(const MmvArgs& a, hipStream_t st, int S) {
 }
 
 // Kernel variant (rows per wave R, blocks-per-lane unroll U) chosen from the block count of a row; the table is the
-// result of the launch-shape sweep on MI355X. The stacked SWIGLU epilogue pairs gate row o with up row F + o: R = 2 (one output per wave), or for the Q4_K
-// gate/up of 16384+ rows R = 4 (two outputs per wave, 1904 -> 1877 us per 32-layer model token).
+// result of the launch-shape sweep on MI355X. The stacked SWIGLU epilogue pairs gate row o with up row F + o: R = 2
+// (one output per wave), or for the Q4_K gate/up of 16384+ rows R = 4 (two outputs per wave, 1904 -> 1877 us per
+// 32-layer model token).
 // The block-sum instrumentation runs without a split (S = 1).
 template <bool BS, int EP>
 static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
