@@ -615,8 +615,8 @@ static void launch_q6_K_s(const MmvArgs& a, hipStream_t st, int S) {
 
 // Kernel variant (rows per wave R, blocks-per-lane unroll U) chosen from the block count of a row; the table is the
 // result of the launch-shape sweep on MI355X. The stacked SWIGLU epilogue pairs gate row o with up row F + o: R = 2
-// (one output per wave), or for the Q4_K gate/up of 16384+ rows R = 4 (two outputs per wave, 1904 -> 1877 us per
-// 32-layer model token).
+// (one output per wave), or for an unsplit Q4_0 / Q4_K gate/up of 16384+ rows R = 4 (two outputs per wave: Q4_0
+// layer 54.5 -> 53.2 us, Q4_K 32-layer model token 1904 -> 1877 us).
 // The block-sum instrumentation runs without a split (S = 1).
 template <bool BS, int EP>
 static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
@@ -627,6 +627,12 @@ static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
     case AMV_T_Q4_0:
         // R = 2 rows per wave, one 64-block step at a time: the fastest shape of the MI355X sweep at K = 4096
         // (7.44 us cold for 14336 x 4096 against 8.5 us for R = 4, 11.2 us for R = 8)
+        if constexpr (!BS && MMV_STACKED(EP)) {
+            if (a.n_rows >= 16384 && a.n_rows % 4 == 0 && split(groups2, (nb + 63) / 64) == 1) {
+                launch_q4_0_s<4, 1, BS, EP>(a, st, 1);
+                return AMV_OK;
+            }
+        }
         launch_q4_0_s<2, 1, BS, EP>(a, st, split(groups2, (nb + 63) / 64));
         return AMV_OK;
     case AMV_T_Q8_0:
