@@ -18,7 +18,9 @@
 // kernel starts after the previous one has finished, so no barrier bookkeeping is needed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -42,6 +44,72 @@ struct Counters {
 };
 Counters g_cnt;
 std::atomic<int> g_fail{AMEVA_FAIL_NONE};
+
+// AMEVA_PROFILE (ggml-ameva.cpp:104-114 of the reference): 1 = totals per graph (host encode, wait, launches),
+// 2 = also the GPU time of each node kind, from a HIP event recorded after every node on the graph's stream.
+// AMEVA_TRACE=1: one stderr line per graph before its launches and one after completion.
+int env_level(const char* name) {
+    const char* e = std::getenv(name);
+    return e && (e[0] == '1' || e[0] == '2') && e[1] == 0 ? e[0] - '0' : 0;
+}
+int profile_level() {
+    static const int level = env_level("AMEVA_PROFILE");
+    return level;
+}
+bool trace_on() {
+    static const bool on = env_level("AMEVA_TRACE") == 1;
+    return on;
+}
+struct Profile {
+    std::mutex mu;
+    int64_t graphs = 0, nodes = 0, launches = 0, gpu_samples = 0;
+    double encode_ms = 0, wait_ms = 0, gpu_ms = 0;
+    struct Kind {
+        double ms = 0;
+        int64_t n = 0;
+    };
+    std::vector<std::pair<std::string, Kind>> kinds;  // in order of first appearance
+    void add_kind(const std::string& k, double ms) {
+        for (auto& e : kinds)
+            if (e.first == k) {
+                e.second.ms += ms;
+                e.second.n++;
+                return;
+            }
+        kinds.push_back({k, Kind{ms, 1}});
+    }
+};
+Profile g_prof;
+double now_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+const char* op_name(int op) {
+    switch (op) {
+    case GGML_OP_ADD: return "ADD";
+    case GGML_OP_MUL: return "MUL";
+    case GGML_OP_RMS_NORM: return "RMS_NORM";
+    case GGML_OP_MUL_MAT: return "MUL_MAT";
+    case GGML_OP_CPY: return "CPY";
+    case GGML_OP_CONT: return "CONT";
+    case GGML_OP_GET_ROWS: return "GET_ROWS";
+    case GGML_OP_SET_ROWS: return "SET_ROWS";
+    case GGML_OP_ROPE: return "ROPE";
+    case GGML_OP_FLASH_ATTN_EXT: return "FLASH_ATTN_EXT";
+    case GGML_OP_GLU: return "GLU";
+    default: return "OTHER";
+    }
+}
+const char* type_name(int t) {
+    switch (t) {
+    case GGML_TYPE_F32: return "f32";
+    case GGML_TYPE_F16: return "f16";
+    case GGML_TYPE_Q4_0: return "q4_0";
+    case GGML_TYPE_Q8_0: return "q8_0";
+    case GGML_TYPE_Q4_K: return "q4_K";
+    case GGML_TYPE_Q6_K: return "q6_K";
+    default: return "other";
+    }
+}
 
 void log_line(const char* fmt, ...) {
     va_list ap;
@@ -174,7 +242,16 @@ struct Device {
     hipStream_t stream = nullptr;
     Arena arena;
     unsigned int* status = nullptr;  // bad-index counter of SET_ROWS / GET_ROWS
+    std::vector<hipEvent_t> events;  // AMEVA_PROFILE=2: one after every node of a graph (grows, reused)
     bool inited = false;
+    hipEvent_t event(size_t i) {
+        while (events.size() <= i) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreate(&e) != hipSuccess) return nullptr;
+            events.push_back(e);
+        }
+        return events[i];
+    }
     bool init() {
         if (inited) return true;
         if (hipSetDevice(0) != hipSuccess) return false;
@@ -206,9 +283,7 @@ void buf_free(ggml_backend_buffer_t b) {
     g_cnt.buf_destroy++;
 }
 void* buf_get_base(ggml_backend_buffer_t b) { return ((BufCtx*)b->context)->dev; }
-void buf_memset(ggml_backend_buffer_t, ggml_tensor* t, uint8_t v, size_t off, size_t size) {
-    (void)hipMemset((uint8_t*)t->data + off, v, size);
-}
+void buf_memset(ggml_backend_buffer_t b, ggml_tensor* t, uint8_t v, size_t off, size_t size);
 
 // converts a quantized tensor between ggml blocks and the MI355X layout in place (through a temporary copy)
 bool convert_in_place(ggml_tensor* t, bool to_repacked) {
@@ -240,6 +315,14 @@ bool ensure_raw(BufCtx* c, ggml_tensor* t) {
     g_cnt.repacked_tensors--;
     g_cnt.repacked_bytes -= (int64_t)nbytes(t);
     return true;
+}
+
+// a partial write of a tensor held repacked first returns it to the ggml layout (the write is in ggml bytes)
+void buf_memset(ggml_backend_buffer_t b, ggml_tensor* t, uint8_t v, size_t off, size_t size) {
+    BufCtx* c = (BufCtx*)b->context;
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (!ensure_raw(c, t)) log_line("memset_tensor %s: could not restore the ggml layout (FAIL-FAST)", t->name);
+    if (hipMemset((uint8_t*)t->data + off, v, size) != hipSuccess) log_line("memset_tensor %s: failed", t->name);
 }
 
 void buf_set_tensor(ggml_backend_buffer_t b, ggml_tensor* t, const void* data, size_t off, size_t size) {
@@ -431,6 +514,7 @@ struct ActEntry {
     const void* data;
     size_t bytes;
     int atype;
+    int64_t m, k;  // the rows and row length it was quantized as (a reshaped view of the same bytes differs)
     void* act;
 };
 
@@ -440,6 +524,8 @@ struct Engine {
     std::vector<ActEntry> acts;  // quantized activations valid at this point of the graph
     bool failed = false;
     std::string why;
+    std::vector<std::string> labels;  // AMEVA_PROFILE=2: the kind of each timed node (events 0 .. n)
+    int64_t encoded = 0;              // nodes encoded (a fused pair counts once)
 
     bool fail(const ggml_tensor* n, const char* what) {
         failed = true;
@@ -463,7 +549,7 @@ struct Engine {
 
     void* act_for(const ggml_tensor* n, const ggml_tensor* x, int atype, int64_t m, int64_t k) {
         for (auto& e : acts)
-            if (e.data == x->data && e.atype == atype && e.bytes == nbytes(x)) {
+            if (e.data == x->data && e.atype == atype && e.bytes == nbytes(x) && e.m == m && e.k == k) {
                 g_cnt.act_reuse++;
                 return e.act;
             }
@@ -476,7 +562,7 @@ struct Engine {
             fail(n, amv_last_error());
             return nullptr;
         }
-        acts.push_back({x->data, nbytes(x), atype, act});
+        acts.push_back({x->data, nbytes(x), atype, m, k, act});
         return act;
     }
 
@@ -683,10 +769,26 @@ struct Engine {
         return e;
     }
 
+    // the kind a node's GPU time is booked under: op, and for MUL_MAT the weight type, kernel family and fusion
+    static std::string kind_of(const ggml_tensor* n, const ggml_tensor* fused) {
+        std::string k = op_name(n->op);
+        if (n->op == GGML_OP_MUL_MAT) {
+            k += std::string(" ") + type_name(n->src[0]->type) + (nrows(n->src[1]) >= 8 ? " batched" : " gemv");
+        }
+        if (fused) k += std::string("+") + op_name(fused->op);
+        return k;
+    }
+
     bool run(ggml_cgraph* g) {
+        const bool prof = profile_level() >= 2;
+        if (prof) {
+            hipEvent_t e0 = dev->event(0);
+            if (!e0 || hipEventRecord(e0, st) != hipSuccess) return fail(nullptr, "profile event");
+        }
         for (int i = 0; i < g->n_nodes; ++i) {
             const ggml_tensor* n = g->nodes[i];
             if (noop(n->op)) continue;
+            const ggml_tensor* first = n;
             bool ok = true;
             switch (n->op) {
             case GGML_OP_MUL_MAT: {
@@ -728,6 +830,12 @@ struct Engine {
             if (!ok) return false;
             invalidate(n);
             g_cnt.gpu_op++;
+            encoded++;
+            if (prof) {
+                labels.push_back(kind_of(first, n != first ? n : nullptr));
+                hipEvent_t e = dev->event(labels.size());
+                if (!e || hipEventRecord(e, st) != hipSuccess) return fail(n, "profile event");
+            }
         }
         return true;
     }
@@ -754,9 +862,42 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
     }
     d->arena.used = 0;
     if (hipMemsetAsync(d->status, 0, 256, d->stream) != hipSuccess) return GGML_STATUS_FAILED;
-    Engine e{d, d->stream, {}, false, {}};
+    const int prof = profile_level();
+    const double t0 = prof || trace_on() ? now_ms() : 0.0;
+    Engine e{d, d->stream, {}, false, {}, {}, 0};
     const bool ok = e.run(g);
+    const double t1 = prof || trace_on() ? now_ms() : 0.0;
+    int64_t graph_no = 0;
+    if (trace_on()) {
+        std::lock_guard<std::mutex> pl(g_prof.mu);
+        graph_no = g_prof.graphs;
+        std::fprintf(stderr, "AMEVA_TRACE graph=%lld nodes=%d encoded=%lld encode_ms=%.3f\n", (long long)graph_no,
+                     g->n_nodes, (long long)e.encoded, t1 - t0);
+    }
     const hipError_t se = hipStreamSynchronize(d->stream);
+    if (prof) {
+        const double t2 = now_ms();
+        std::lock_guard<std::mutex> pl(g_prof.mu);
+        g_prof.graphs++;
+        g_prof.nodes += g->n_nodes;
+        g_prof.launches += e.encoded;
+        g_prof.encode_ms += t1 - t0;
+        g_prof.wait_ms += t2 - t1;
+        if (ok && se == hipSuccess && prof >= 2 && !e.labels.empty()) {
+            double total = 0;
+            for (size_t i = 0; i < e.labels.size(); ++i) {
+                float ms = 0.0f;
+                if (hipEventElapsedTime(&ms, d->events[i], d->events[i + 1]) != hipSuccess) continue;
+                g_prof.add_kind(e.labels[i], ms);
+                total += ms;
+            }
+            g_prof.gpu_ms += total;
+            g_prof.gpu_samples++;
+        }
+    }
+    if (trace_on())
+        std::fprintf(stderr, "AMEVA_TRACE graph=%lld done status=%s\n", (long long)graph_no,
+                     ok && se == hipSuccess ? "ok" : "failed");
     if (!ok) {
         log_line("%s (FAIL-FAST)", e.why.c_str());
         return GGML_STATUS_FAILED;
@@ -917,6 +1058,13 @@ int64_t ggml_backend_ameva_get_mmq_mul_mat_count(void) { return g_cnt.mmq; }
 int64_t ggml_backend_ameva_get_mmqb_mul_mat_count(void) { return 0; }
 int64_t ggml_backend_ameva_get_fused_pair_count(void) { return g_cnt.fused; }
 int64_t ggml_backend_ameva_get_act_quant_reuse_count(void) { return g_cnt.act_reuse; }
+// the convolution / group-norm / windowed-node counters of the reference (ggml-ameva.h:70-78): this plugin runs none
+// of those ops (it declines them in supports_op), so they stay 0 and the f16 convolution decoder is "not determined"
+int64_t ggml_backend_ameva_get_conv_count(void) { return 0; }
+int ggml_backend_ameva_get_conv_f16_decoder(void) { return -1; }
+int64_t ggml_backend_ameva_get_conv_bias_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_group_norm_count(void) { return 0; }
+int64_t ggml_backend_ameva_get_window_node_count(void) { return 0; }
 const char* ggml_backend_ameva_get_build_commit(void) {
 #ifdef AMEVA_BUILD_COMMIT
     return AMEVA_BUILD_COMMIT;
@@ -936,10 +1084,34 @@ void ggml_backend_ameva_reset_counters(void) {
     g_cnt.act_reuse = 0;
 }
 void ggml_backend_ameva_profile_report(void) {
-    log_line("counters: gpu_op %lld mul_mat %lld mmq %lld fused %lld act_reuse %lld repacked %lld (%lld bytes)",
-             (long long)g_cnt.gpu_op.load(), (long long)g_cnt.mul_mat.load(), (long long)g_cnt.mmq.load(),
-             (long long)g_cnt.fused.load(), (long long)g_cnt.act_reuse.load(), (long long)g_cnt.repacked_tensors.load(),
-             (long long)g_cnt.repacked_bytes.load());
+    std::lock_guard<std::mutex> pl(g_prof.mu);
+    const double gr = g_prof.graphs ? (double)g_prof.graphs : 1.0;
+    if (profile_level() >= 2) {
+        std::vector<size_t> order(g_prof.kinds.size());
+        double total = 0;
+        for (size_t i = 0; i < order.size(); ++i) {
+            order[i] = i;
+            total += g_prof.kinds[i].second.ms;
+        }
+        std::sort(order.begin(), order.end(),
+                  [](size_t a, size_t b) { return g_prof.kinds[a].second.ms > g_prof.kinds[b].second.ms; });
+        for (size_t i : order) {
+            const auto& k = g_prof.kinds[i];
+            std::fprintf(stderr, "AMEVA_PROFILE kind=\"%s\" nodes=%lld gpu_ms=%.3f share=%.1f%% per_node_us=%.2f\n",
+                         k.first.c_str(), (long long)k.second.n, k.second.ms, total > 0 ? 100.0 * k.second.ms / total : 0.0,
+                         k.second.n ? 1e3 * k.second.ms / (double)k.second.n : 0.0);
+        }
+    }
+    std::fprintf(stderr, "AMEVA_PROFILE graphs=%lld nodes=%lld encoded=%lld mul_mat=%lld mmq_mul_mat=%lld fused_pairs=%lld "
+                         "act_quant_reuse=%lld\n",
+                 (long long)g_prof.graphs, (long long)g_prof.nodes, (long long)g_prof.launches,
+                 (long long)g_cnt.mul_mat.load(), (long long)g_cnt.mmq.load(), (long long)g_cnt.fused.load(),
+                 (long long)g_cnt.act_reuse.load());
+    std::fprintf(stderr, "AMEVA_PROFILE per_graph_ms encode=%.3f wait=%.3f gpu=%.3f (gpu samples %lld)\n",
+                 g_prof.encode_ms / gr, g_prof.wait_ms / gr,
+                 g_prof.gpu_samples ? g_prof.gpu_ms / (double)g_prof.gpu_samples : 0.0, (long long)g_prof.gpu_samples);
+    std::fprintf(stderr, "AMEVA_PROFILE repacked_tensors=%lld repacked_mib=%.1f\n",
+                 (long long)g_cnt.repacked_tensors.load(), (double)g_cnt.repacked_bytes.load() / 1048576.0);
 }
 void ggml_backend_ameva_set_failure_injection(AmevaFailureInjectionPoint p) { g_fail = (int)p; }
 AmevaFailureInjectionPoint ggml_backend_ameva_get_failure_injection(void) { return (AmevaFailureInjectionPoint)g_fail.load(); }

@@ -71,9 +71,19 @@ int64_t ggml_backend_ameva_get_mmq_mul_mat_count(void);
 int64_t ggml_backend_ameva_get_mmqb_mul_mat_count(void);
 int64_t ggml_backend_ameva_get_fused_pair_count(void);
 int64_t ggml_backend_ameva_get_act_quant_reuse_count(void);
+/* Convolution, group-norm and windowed-node counters (ggml-ameva.h:70-78). This plugin declines CONV_2D and
+ * GROUP_NORM in supports_op, so the counts stay 0 and conv_f16_decoder stays -1 ("not determined"). */
+int64_t ggml_backend_ameva_get_conv_count(void);
+int ggml_backend_ameva_get_conv_f16_decoder(void);
+int64_t ggml_backend_ameva_get_conv_bias_count(void);
+int64_t ggml_backend_ameva_get_group_norm_count(void);
+int64_t ggml_backend_ameva_get_window_node_count(void);
 const char* ggml_backend_ameva_get_build_commit(void);
 void ggml_backend_ameva_reset_counters(void);
-/* Prints the AMEVA_PROFILE per-op GPU time table now (ggml-ameva.h profile_report). */
+/* Prints the AMEVA_PROFILE report now (ggml-ameva.h profile_report; ggml-ameva.cpp:208-277): with AMEVA_PROFILE=1
+ * the per-graph totals (graphs, nodes, encoded launches, host encode and wait ms), with AMEVA_PROFILE=2 also the GPU
+ * time per node kind (op, weight type, GEMV or batched kernel, fused partner) from a HIP event after every node.
+ * AMEVA_TRACE=1 prints one line per graph before its launches and one after completion (ggml-ameva.cpp:5526). */
 void ggml_backend_ameva_profile_report(void);
 
 /* Failure injection (ggml-ameva.h:83-98): forces a failure from the host at the named point so the FAIL-FAST paths

@@ -114,6 +114,34 @@ def test_q8_0_rules_known_answers(orc):
         assert (q[1], q[2]) == want, rule
 
 
+def test_q8_0_x86_and_arm_rules_differ(orc):
+    """Blocks where 127/amax and 1/(amax/127) are different f32 values and one element lands on opposite sides of
+    a rounding boundary: rule 0 must give the x86 result (x * (127/amax)), rule 1 the ARM one (x * (1/d)). The
+    expected integers are fixed constants, and numpy's IEEE single-precision arithmetic recomputes both rules."""
+    f = np.float32
+    cases = [  # (amax bits, x bits, q under x86, q under ARM)
+        (1081376603, 1064977893, 32, 33),
+        (1073587831, 1058916430, 40, 39),
+        (1074107746, 1073866479, 123, 124),
+        (1072994361, 1049022689, 18, 17),
+        (1067132384, 1058743776, 63, 64),  # x = amax / 2 exactly: a real tie at 63.5
+    ]
+    x = np.zeros((len(cases), 32), np.float32)
+    for i, (ab, xb, _, _) in enumerate(cases):
+        x[i, 0] = np.array(ab, np.uint32).view(np.float32)
+        x[i, 7] = np.array(xb, np.uint32).view(np.float32)
+    y86 = orc.quantize_q8_0(x, orc.Q8_X86).reshape(len(cases), 34)
+    yarm = orc.quantize_q8_0(x, orc.Q8_ARM).reshape(len(cases), 34)
+    for i, (_, _, q86, qarm) in enumerate(cases):
+        amax, xv = x[i, 0], x[i, 7]
+        id86, idarm = f(127) / amax, f(1) / (amax / f(127))
+        assert id86 != idarm
+        assert np.rint(xv * id86) == q86 and np.rint(xv * idarm) == qarm
+        assert int(y86[i, 2 + 7].view(np.int8)) == q86, i
+        assert int(yarm[i, 2 + 7].view(np.int8)) == qarm, i
+        assert int(y86[i, 2].view(np.int8)) == 127 and int(yarm[i, 2].view(np.int8)) == 127
+
+
 def test_q8_0_invariants(orc):
     rng = np.random.default_rng(3)
     x = rng.standard_normal((16, 4096)).astype(np.float32)

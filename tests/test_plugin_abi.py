@@ -61,6 +61,18 @@ def test_public_header_symbols_exported(libs):
         assert hasattr(plugin, n), n
 
 
+def test_conv_and_window_counters(libs):
+    """The reference's convolution / group-norm / window counters (ggml-ameva.h:70-78) link and read as nothing run:
+    its tests/ameva_window_check.cpp binds them."""
+    _, plugin = libs
+    for n in ("conv_count", "conv_bias_count", "group_norm_count", "window_node_count"):
+        f = getattr(plugin, "ggml_backend_ameva_get_" + n)
+        f.restype = ctypes.c_int64
+        assert f() == 0, n
+    plugin.ggml_backend_ameva_get_conv_f16_decoder.restype = ctypes.c_int
+    assert plugin.ggml_backend_ameva_get_conv_f16_decoder() == -1
+
+
 class FakeHost:
     """Tensors whose buffer struct names the AMEVA buffer type, with made-up aligned device addresses."""
 
