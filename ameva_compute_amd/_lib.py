@@ -60,6 +60,9 @@ SIGNATURES = {
     "amv_set_rows_q": (I32, [I32, P, I64, P, I64, I64, I64, P, I32, I64, I32, P, P]),
     "amv_flash_attn_decode_kv": (I32, [I32, P, P, P, P, P, I64, I64, I64, P, I64, I64, I64, I64, I64, F32, P, I64, P,
                                        P, I32, I32, P]),
+    "amv_flash_attn_noalloc_max_bytes": (I64, []),
+    "amv_flash_attn_decode_noalloc": (I32, [I32, P, P, P, P, P, I64, I64, I64, P, I64, I64, I64, I64, I64, F32, P,
+                                            I32, I32, P]),
     "amv_get_rows": (I32, [I32, P, I64, I64, P, I64, P, P, P]),
     "amv_argmax": (I32, [P, I64, P, P, P, I64, P]),
 }

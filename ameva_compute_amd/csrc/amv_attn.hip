@@ -19,6 +19,9 @@
 // after the arrival).
 #include "amv_common.h"
 
+#include <map>
+#include <mutex>
+
 #define FA_D 128
 #define FA_PS (FA_D + 4)        // floats per partial: m, l, 2 pad, acc[D] (16-byte aligned rows)
 #define FA_MAX_NSPLIT 1024      // splits per head (n_kv <= 128 K keys)
@@ -579,4 +582,64 @@ extern "C" int amv_flash_attn_decode_kv(int kv_type, const float* q, const void*
     return fa_run("amv_flash_attn_decode_kv", kv_type, q, k, v, mask, out, n_head, n_head_kv, n_kv_max, n_kv_dev, D,
                   k_row_bytes, k_head_bytes, v_row_bytes, v_head_bytes, scale, workspace, workspace_bytes, counters,
                   act, act_type, rule, stream);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// The decode attention without a workspace argument and without any allocation (for callers that cannot allocate:
+// code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). The split partials live in
+// `scratch`, a file-scope device array of AMV_FA_SCRATCH_BYTES that every GPU the library runs on holds until the
+// process ends. Host code never uses the array's name as a device address: its address on each device is looked up
+// once with hipGetSymbolAddress (with that device current, at the first call on it) and kept per device. The
+// partials are written before they are read within one call (pass 1 writes every split that holds keys, the merge
+// reads only those), so nothing needs clearing; calls that overlap in time on one device race on the array.
+// ---------------------------------------------------------------------------------------------------------------
+#define AMV_FA_SCRATCH_BYTES (8u << 20)
+static __device__ __align__(256) uint8_t scratch[AMV_FA_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_ptr;  // device -> address of `scratch` on that device
+}  // namespace
+
+static void* fa_scratch(const char* fn) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        amv_set_error("%s: hipGetDevice failed", fn);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_ptr.find(dev);
+    if (it != g_scratch_ptr.end()) return it->second;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        amv_set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev, hipGetErrorString(e));
+        return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+    return ptr;
+}
+
+extern "C" int64_t amv_flash_attn_noalloc_max_bytes(void) { return AMV_FA_SCRATCH_BYTES; }
+
+extern "C" int amv_flash_attn_decode_noalloc(int kv_type, const float* q, const void* k, const void* v,
+                                             const void* mask, float* out, int64_t n_head, int64_t n_head_kv,
+                                             int64_t n_kv_max, const int32_t* n_kv_dev, int64_t D,
+                                             int64_t k_row_bytes, int64_t k_head_bytes, int64_t v_row_bytes,
+                                             int64_t v_head_bytes, float scale, void* act, int act_type, int rule,
+                                             void* stream) {
+    const char* fn = "amv_flash_attn_decode_noalloc";
+    const int64_t need = amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv_max, D);
+    AMV_REQUIRE(need > 0, "%s: unsupported shape (n_head %lld, n_head_kv %lld, n_kv_max %lld, D %lld)", fn,
+                (long long)n_head, (long long)n_head_kv, (long long)n_kv_max, (long long)D);
+    AMV_REQUIRE(need <= (int64_t)AMV_FA_SCRATCH_BYTES,
+                "%s: the split partials need %lld bytes, above the %u-byte scratch of this entry point (use "
+                "amv_flash_attn_decode_kv with a workspace)", fn, (long long)need, AMV_FA_SCRATCH_BYTES);
+    void* ws = fa_scratch(fn);
+    if (!ws) return AMV_ERR_HIP;
+    return fa_run(fn, kv_type, q, k, v, mask, out, n_head, n_head_kv, n_kv_max, n_kv_dev, D, k_row_bytes,
+                  k_head_bytes, v_row_bytes, v_head_bytes, scale, ws, (int64_t)AMV_FA_SCRATCH_BYTES, nullptr, act,
+                  act_type, rule, stream);
 }

@@ -310,6 +310,21 @@ int amv_flash_attn_decode_kv(int kv_type, const float* q, const void* k, const v
                              float scale, void* workspace, int64_t workspace_bytes, unsigned int* counters, void* act,
                              int act_type, int rule, void* stream);
 
+/* amv_flash_attn_decode_kv without a workspace or counters argument and without any allocation. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The split partials live in a library-owned device array of
+ * amv_flash_attn_noalloc_max_bytes() bytes (8 MiB) that each GPU the library runs on holds until the process ends;
+ * shapes whose partials need more (amv_flash_attn_workspace_bytes) are rejected with AMV_ERR_INVALID_ARG. The first
+ * call on a device looks the array's address up (no allocation; make that call outside graph capture). Calls that
+ * overlap in time on one device share the array and race; the merge always runs as a second launch. Results are
+ * identical to amv_flash_attn_decode_kv with counters == NULL. */
+int64_t amv_flash_attn_noalloc_max_bytes(void);
+int amv_flash_attn_decode_noalloc(int kv_type, const float* q, const void* k, const void* v, const void* mask,
+                                  float* out, int64_t n_head, int64_t n_head_kv, int64_t n_kv_max,
+                                  const int32_t* n_kv_dev, int64_t D, int64_t k_row_bytes, int64_t k_head_bytes,
+                                  int64_t v_row_bytes, int64_t v_head_bytes, float scale, void* act, int act_type,
+                                  int rule, void* stream);
+
 /* FLASH_ATTN_EXT over n_tok query positions (prompt prefill; enc_flash_attn ggml-ameva.cpp:4204-4284 with
  * q->ne[1] > 1, ameva_flash_attn.comp), on the f16 matrix cores. D = 128, n_head / n_head_kv integral.
  *   q f32: element d of head h of token t at q[t * q_tok_stride + h * q_head_stride + d] (strides in floats, multiples
