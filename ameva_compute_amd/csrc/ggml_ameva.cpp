@@ -56,6 +56,15 @@ int profile_level() {
     static const int level = env_level("AMEVA_PROFILE");
     return level;
 }
+// AMEVA_MMQ_FORM=scaled: batched MUL_MATs above 64 tokens on operands rounded to f16 once (~3e-4 relative L2 from
+// the exact form); anything else (the default): exact integer block sums
+bool mmq_scaled() {
+    static const bool on = [] {
+        const char* e = std::getenv("AMEVA_MMQ_FORM");
+        return e && std::strcmp(e, "scaled") == 0;
+    }();
+    return on;
+}
 bool trace_on() {
     static const bool on = env_level("AMEVA_TRACE") == 1;
     return on;
@@ -409,8 +418,16 @@ const char* unsupported_reason(const ggml_tensor* n) {
     case GGML_OP_MUL_MAT: {
         if (!quant_weight_type(s0->type)) return "MUL_MAT src0 type is not Q4_0, Q8_0, Q4_K or Q6_K";
         if (s0->ne[2] != 1 || s0->ne[3] != 1) return "MUL_MAT src0 must be a 2-D weight";
-        if (!is_contiguous(s0) || s0->view_src) return "MUL_MAT src0 must be a whole contiguous tensor";
-        if (!aligned16(s0->data)) return "MUL_MAT src0 must be 16-byte aligned";
+        if (!is_contiguous(s0)) return "MUL_MAT src0 rows must be contiguous";
+        if (s0->view_src) {  // a view of whole rows of a 2-D weight (ggml_view_2d at a row offset)
+            const ggml_tensor* p = s0->view_src;
+            if (p->type != s0->type || p->ne[0] != s0->ne[0] || p->ne[2] != 1 || p->ne[3] != 1 || p->view_src ||
+                !is_contiguous(p) || s0->nb[1] != p->nb[1] || s0->view_offs % p->nb[1] != 0 ||
+                s0->view_offs + nbytes(s0) > nbytes(p) || !aligned16(p->data))
+                return "MUL_MAT src0 view must be whole rows of a 2-D quantized weight";
+        } else if (!aligned16(s0->data)) {
+            return "MUL_MAT src0 must be 16-byte aligned";
+        }
         if (s1->type != GGML_TYPE_F32 || !is_contiguous(s1)) return "MUL_MAT src1 must be contiguous F32";
         if (s1->ne[0] != s0->ne[0]) return "MUL_MAT inner dimensions differ";
         if (n->type != GGML_TYPE_F32 || !is_contiguous(n)) return "MUL_MAT dst must be contiguous F32";
@@ -575,16 +592,32 @@ struct Engine {
         // stage (the plain layout is the prefix of the extended one)
         const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K);
         const bool kq = w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K;
-        // batched: above 64 tokens the scaled layout (f16 q * d), whose tiled MFMA GEMM accumulates across k without
-        // a per-block epilogue; 8 .. 64 tokens the exact layout (the small-batch kernels read exact f16 integers)
-        const bool deq = M > 64;
+        // batched: the exact layout (exact per-block integer sums, ggml's f32 epilogue: the reference's MMQ
+        // arithmetic); AMEVA_MMQ_FORM=scaled selects the scaled layout (f16 q * d) above 64 tokens
+        const bool deq = M > 64 && mmq_scaled();
         const int atype = kq ? (mmq ? (deq ? AMV_ACT_Q8_K_DEQ : AMV_ACT_Q8_K_MMA) : (int)GGML_TYPE_Q8_K)
                              : (mmq ? (deq ? AMV_ACT_Q8_0_DEQ : AMV_ACT_Q8_0_MMA) : (int)GGML_TYPE_Q8_0);
         // src0 in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized tensor of any
         // other buffer is repacked into scratch for this use
         const void* wp = w->data;
         BufCtx* bc = (BufCtx*)w->buffer->context;
-        {
+        if (w->view_src) {
+            // rows of another weight: their ggml bytes (from a layout copy of the parent when the parent is held
+            // repacked) are repacked into scratch for this use
+            const ggml_tensor* p = w->view_src;
+            std::lock_guard<std::mutex> lk(bc->mu);
+            const uint8_t* src = (const uint8_t*)w->data;
+            if (bc->repacked.count(p->data)) {
+                uint8_t* raw = (uint8_t*)dev->arena.take(nbytes(p));
+                if (!raw) return fail(n, "scratch exhausted");
+                if (!rc(n, amv_unrepack(p->type, p->data, raw, p->ne[1], p->ne[0], st))) return false;
+                src = raw + w->view_offs;
+            }
+            void* tmp = dev->arena.take(nbytes(w));
+            if (!tmp) return fail(n, "scratch exhausted");
+            if (!rc(n, amv_repack(w->type, src, tmp, N, K, st))) return false;
+            wp = tmp;
+        } else {
             std::lock_guard<std::mutex> lk(bc->mu);
             if (!bc->repacked.count(w->data)) {
                 if (w->buffer->usage == GGML_BACKEND_BUFFER_USAGE_WEIGHTS && repackable(w)) {
@@ -721,7 +754,8 @@ struct Engine {
             if (n->op == GGML_OP_MUL_MAT) {
                 s += (size_t)amv_act_bytes(AMV_ACT_Q8_0_MMA, nrows(n->src[1]), n->src[1]->ne[0]) + 4096;
                 s += (size_t)amv_act_bytes(AMV_ACT_Q8_K_MMA, nrows(n->src[1]), (n->src[1]->ne[0] + 255) / 256 * 256) + 4096;
-                if (n->src[0]->buffer->usage != GGML_BACKEND_BUFFER_USAGE_WEIGHTS) s += nbytes(n->src[0]) + 256;
+                if (n->src[0]->view_src) s += nbytes(n->src[0]->view_src) + nbytes(n->src[0]) + 512;
+                else if (n->src[0]->buffer->usage != GGML_BACKEND_BUFFER_USAGE_WEIGHTS) s += nbytes(n->src[0]) + 256;
             } else if (n->op == GGML_OP_FLASH_ATTN_EXT) {
                 const int64_t ws = amv_flash_attn_workspace_bytes(n->src[0]->ne[2], n->src[1]->ne[2], n->src[1]->ne[1], 128);
                 s += (size_t)(ws > 0 ? ws : 0) + 256;

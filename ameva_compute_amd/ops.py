@@ -8,6 +8,8 @@ there is no CPU path.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from ._lib import check, lib
@@ -43,10 +45,20 @@ Q8_K_DEQ = 1115
 Q8_0_DEQ = 1108
 
 
-def act_type(wtype: int, m: int = 1, exact: bool = False) -> int:
+# The batched MUL_MAT's arithmetic above MMQ16_MIN_M tokens: "exact" (the default: exact per-block integer sums and
+# ggml's f32 epilogue, the reference's MMQ arithmetic) or "scaled" (operands rounded to f16 once, ~3e-4 relative L2
+# from the exact value), chosen with AMEVA_MMQ_FORM.
+MMQ_FORM = os.environ.get("AMEVA_MMQ_FORM", "exact")
+if MMQ_FORM not in ("exact", "scaled"):
+    raise ValueError(f"AMEVA_MMQ_FORM={MMQ_FORM!r}: exact or scaled")
+
+
+def act_type(wtype: int, m: int = 1, exact: bool | None = None) -> int:
     """ggml vec_dot_type of a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants; for a batched MUL_MAT
-    (m >= MMQ_MIN_M) of Q4_K / Q4_0 / Q8_0 the layout extended with the f16 copies the matrix-core kernels read:
-    above MMQ16_MIN_M tokens scaled (DEQ, the fast tiled form) unless exact, else the exact-integer form (MMA)."""
+    (m >= MMQ_MIN_M) the layout extended with the f16 copies the matrix-core kernels read: the exact-integer form
+    (MMA), or above MMQ16_MIN_M tokens the scaled form (DEQ) when exact is False (None: MMQ_FORM decides)."""
+    if exact is None:
+        exact = MMQ_FORM == "exact"
     deq = m > MMQ16_MIN_M and not exact
     if wtype == Q4_K and m >= MMQ_MIN_M:
         return Q8_K_DEQ if deq else Q8_K_MMA

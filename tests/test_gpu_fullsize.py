@@ -1,0 +1,355 @@
+"""BASELINE configs 2 and 5 at their full sizes on the GPU, against the CPU oracle where it finishes in seconds.
+
+* Config 2: Q4_0 / Q8_0 / Q4_K batched MUL_MAT at Llama-3-8B FFN shapes (14336 x 4096 gate/up, 4096 x 14336 down)
+  for 16 and 512 tokens, both activation layouts of the tiled kernels (exact integer block sums, and the scaled
+  f16 form): the f32 result of every token on a sample of weight rows against the oracle (rows are independent, so
+  the sample is exact at the full shape), the Q8_0 / Q8_K activation bytes over the whole batch, and the per-block
+  int32 sums of the exact form on a 256-row slice of the weight at the full k and batch.
+* Config 5 pieces at 8B size: the Q6_K output head GEMV (128256 x 4096, block sums bit-exact, f32 within 1e-3), the
+  Q4_K token-embedding GET_ROWS (bit-exact rows), one Q4_K Llama-3-8B decoder layer stage by stage against the
+  oracle (as tests/test_gpu_llama.py does for Q4_0), and the full 32-layer model: a 512-token prefill and greedy
+  steps, with graph replay equal to eager steps, the prompt's logits equal to token-by-token decoding within the
+  chain bar, and the head of the last step against the oracle's GEMV of the same hidden state."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, Q6_K, Q8_K = 2, 8, 12, 14, 15
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from ameva_compute_amd import ops
+    return ops
+
+
+def weights(ops, orc, dev, wt, n, k, seed):
+    """ggml blocks of N(0, 0.02) rows: Q4_0 / Q8_0 by the oracle's quantizers (ggml's _ref rules), the K-quants by
+    this library's GPU quantizer. Returns (ggml bytes on the host, QWeight on the device)."""
+    if wt in (Q4_0, Q8_0):
+        rng = np.random.default_rng(seed)
+        w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+        wg = orc.quantize_q4_0(w) if wt == Q4_0 else orc.quantize_q8_0(w, orc.Q8_REF)
+        wg = wg.reshape(n, -1)
+        dg = torch.from_numpy(wg).to(dev)
+    else:
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        dg = ops.quantize_k(torch.randn((n, k), generator=g, device=dev) * 0.02, wt)
+        wg = dg.cpu().numpy()
+    return wg, ops.QWeight.from_ggml(wt, dg, n, k)
+
+
+def sample_rows(n, count, seed):
+    rng = np.random.default_rng(seed)
+    r = np.unique(np.concatenate([[0, 1, n // 2, n - 2, n - 1], rng.choice(n, count, replace=False)]))
+    return r.astype(np.int64)
+
+
+@pytest.mark.parametrize("m", [16, 512])
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("wt", [Q4_0, Q8_0, Q4_K])
+def test_config2_batched_full_shape(dev, ops, orc, wt, shape, m):
+    n, k = shape
+    seed = wt * 1000 + n // 1024 + m
+    wg, wq = weights(ops, orc, dev, wt, n, k, seed)
+    x = np.random.default_rng(seed + 1).standard_normal((m, k), dtype=np.float32)
+    xd = torch.from_numpy(x).to(dev)
+    base = Q8_K if wt == Q4_K else Q8_0
+    forms = [(ops.act_type(wt, m, exact=True), "exact")]
+    if m > ops.MMQ16_MIN_M:
+        forms.append((ops.act_type(wt, m, exact=False), "scaled"))
+    # activation bytes: the GPU quantizer's ggml blocks equal the oracle's over the whole batch
+    a_ref = orc.quantize_q8_K(x) if base == Q8_K else orc.quantize_q8_0(x, orc.Q8_X86)
+    rows = sample_rows(n, 192, seed + 2)
+    y_ref = orc.mul_mat(wt, np.ascontiguousarray(wg[rows]), len(rows), k, a_ref, m)  # [m, rows]
+    for at, name in forms:
+        act, ag = ops.quantize_act(xd, at, ops.Q8_X86, ggml=True)
+        assert np.array_equal(ag.cpu().numpy().reshape(-1), a_ref.reshape(-1)), name
+        y = ops.mul_mat_q(wq, act, m, act_t=at)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()[:, rows]
+        e = rel_l2(got, y_ref)
+        worst = max(rel_l2(got[:, j], y_ref[:, j]) for j in range(0, len(rows), 7))
+        print(f"{name}: wt {wt} {n}x{k} m {m}: rel L2 {e:.2e}, worst sampled row {worst:.2e}")
+        assert e < 1e-3, (name, e)
+        assert np.isfinite(got).all()
+    # exact form: the per-block integers of a 256-row slice at the full k and batch, bit for bit
+    sl = rows[:256] if len(rows) >= 256 else rows
+    wsl = np.ascontiguousarray(wg[sl])
+    qs = ops.QWeight.from_ggml(wt, torch.from_numpy(wsl).to(dev), len(sl), k)
+    act, _ = ops.quantize_act(xd, ops.act_type(wt, m, exact=True), ops.Q8_X86)
+    s = ops.block_sums(qs, act, m, kernel="mmq").cpu().numpy()
+    _, s_ref = orc.mul_mat(wt, wsl, len(sl), k, a_ref, m, with_blocks=True)
+    assert np.array_equal(s.reshape(-1), np.asarray(s_ref).reshape(-1))
+
+
+def test_q6k_output_head_full(dev, ops, orc):
+    """The config-5 output head: Q6_K 128256 x 4096 GEMV of one Q8_K activation row."""
+    n, k = 128256, 4096
+    wg, wq = weights(ops, orc, dev, Q6_K, n, k, 6)
+    x = np.random.default_rng(7).standard_normal((1, k), dtype=np.float32)
+    act, ag = ops.quantize_act(torch.from_numpy(x).to(dev), Q8_K, ops.Q8_X86, ggml=True)
+    a_ref = orc.quantize_q8_K(x)
+    assert np.array_equal(ag.cpu().numpy().reshape(-1), a_ref.reshape(-1))
+    y = ops.mul_mat_q(wq, act, 1).cpu().numpy().reshape(-1)
+    s = ops.block_sums(wq, act, 1).cpu().numpy().reshape(-1)
+    y_ref, s_ref = orc.mul_mat(Q6_K, wg, n, k, a_ref, 1, with_blocks=True)
+    assert np.array_equal(s, np.asarray(s_ref).reshape(-1))
+    e = rel_l2(y, y_ref.reshape(-1))
+    print(f"Q6_K head 128256x4096: rel L2 {e:.2e}")
+    assert e < 1e-3
+    assert int(np.argmax(y)) == int(np.argmax(y_ref))
+
+
+def test_q4k_token_embedding_get_rows_full(dev, ops, orc):
+    n_vocab, H = 128256, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    tab = torch.empty((n_vocab, H // 256 * 144), dtype=torch.uint8, device=dev)
+    for r0 in range(0, n_vocab, 32768):
+        r1 = min(n_vocab, r0 + 32768)
+        tab[r0:r1] = ops.quantize_k(torch.randn((r1 - r0, H), generator=g, device=dev) * 0.02, Q4_K)
+    ids = np.array([0, n_vocab - 1, 128000, 5, 5, 77777, 1, 64000] + list(range(300, 340)), np.int32)
+    got = ops.get_rows(tab, Q4_K, H, torch.from_numpy(ids).to(dev)).cpu().numpy()
+    rows = tab[torch.from_numpy(ids.astype(np.int64)).to(dev)].cpu().numpy()
+    ref = orc.dequantize(Q4_K, rows, H)
+    assert np.array_equal(got.view(np.uint32), ref.reshape(got.shape).view(np.uint32))
+
+
+def test_q4k_layer_decode_vs_oracle(dev, ops, orc):
+    """One Llama-3-8B layer on Q4_K weights (Q8_K activations), fused decode at position 3000 of a 4096 cache: each
+    stage against the oracle fed the GPU's own input to that stage, and the whole chain against the oracle's."""
+    from ameva_compute_amd.llama import LlamaLayer
+    H, NH, NKV, D, FF, CTX = 4096, 32, 8, 128, 14336, 4096
+    eps, base = 1e-5, 500000.0
+    w = {}
+    qw = {}
+    for i, (name, n, k) in enumerate((("q", NH * D, H), ("k", NKV * D, H), ("v", NKV * D, H), ("o", H, H),
+                                      ("gate", FF, H), ("up", FF, H), ("down", H, FF))):
+        w[name], qw[name] = weights(ops, orc, dev, Q4_K, n, k, 500 + i)
+    rng = np.random.default_rng(77)
+    an = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    fn = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    g = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    st = LlamaLayer.stack_rows
+    layer = LlamaLayer(ops.QWeight.from_ggml(Q4_K, st(g(w["q"]), g(w["k"]), g(w["v"])), H + 2 * NKV * D, H),
+                       qw["o"], ops.QWeight.from_ggml(Q4_K, st(g(w["gate"]), g(w["up"])), 2 * FF, H), qw["down"],
+                       g(an), g(fn), ctx=CTX)
+    kc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    vc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    layer.k_cache.copy_(g(kc))
+    layer.v_cache.copy_(g(vc))
+    pos = 3000
+    layer.set_position(pos)
+    x = rng.standard_normal(H).astype(np.float32)
+    xg, out = g(x), torch.empty(H, dtype=torch.float32, device=dev)
+    layer.decode(xg, out)
+    torch.cuda.synchronize()
+    y = out.cpu().numpy()
+    out_u = torch.empty_like(out)
+    layer.decode(xg, out_u, fused=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_u, out)
+
+    def mm(name, a):
+        n_, k_ = w[name].shape[0], w[name].shape[1] * 256 // 144
+        return orc.mul_mat(Q4_K, w[name], n_, k_, orc.quantize_q8_K(a.reshape(1, -1)), 1).reshape(-1)
+    cpu = lambda t: t.float().cpu().numpy().reshape(-1)  # noqa: E731
+    p = np.array([pos], np.int32)
+    _, c = orc.rms_norm(x.reshape(1, H), eps, an)
+    assert rel_l2(cpu(layer.t_o), c) < 1e-6
+    qkv_g = cpu(layer.qkv)
+    q_in = np.concatenate([mm("q", cpu(layer.t_o)), mm("k", cpu(layer.t_o))])
+    qk_ref = orc.rope(q_in.reshape(1, NH + NKV, D), p, D, 0, base).reshape(-1)
+    assert rel_l2(qkv_g[: H + NKV * D], qk_ref) < 1e-3
+    assert rel_l2(qkv_g[H + NKV * D:], mm("v", cpu(layer.t_o))) < 1e-3
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[pos] = qkv_g[H:H + NKV * D].astype(np.float16)
+    vc2[pos] = qkv_g[H + NKV * D:].astype(np.float16)
+    assert np.array_equal(layer.k_cache[pos].cpu().numpy(), kc2[pos])
+    assert np.array_equal(layer.v_cache[pos].cpu().numpy(), vc2[pos])
+    kh = np.ascontiguousarray(kc2[: pos + 1].reshape(pos + 1, NKV, D).transpose(1, 0, 2))
+    vh = np.ascontiguousarray(vc2[: pos + 1].reshape(pos + 1, NKV, D).transpose(1, 0, 2))
+    att_ref = orc.flash_attn_decode(qkv_g[:H].reshape(NH, D), kh.view(np.uint16), vh.view(np.uint16),
+                                    1.0 / np.sqrt(D)).reshape(-1)
+    assert rel_l2(cpu(layer.att), att_ref) < 2e-3
+    assert rel_l2(cpu(layer.x1), mm("o", cpu(layer.att)) + x) < 1e-3
+    _, c2 = orc.rms_norm(cpu(layer.x1).reshape(1, H), eps, fn)
+    assert rel_l2(cpu(layer.t_o2), c2) < 1e-6
+    gu_ref = np.concatenate([mm("gate", cpu(layer.t_o2)), mm("up", cpu(layer.t_o2))])
+    assert rel_l2(cpu(layer.gu), gu_ref) < 1e-3
+    assert rel_l2(cpu(layer.h), orc.swiglu(cpu(layer.gu)[:FF], cpu(layer.gu)[FF:])) < 1e-6
+    assert rel_l2(y, mm("down", cpu(layer.h)) + cpu(layer.x1)) < 1e-3
+    # the whole chain on the oracle
+    _, c = orc.rms_norm(x.reshape(1, H), eps, an)
+    qr = orc.rope(mm("q", c).reshape(1, NH, D), p, D, 0, base).reshape(NH, D)
+    kr = orc.rope(mm("k", c).reshape(1, NKV, D), p, D, 0, base).reshape(-1)
+    ko, vo = kc.copy(), vc.copy()
+    ko[pos], vo[pos] = kr.astype(np.float16), mm("v", c).astype(np.float16)
+    kh = np.ascontiguousarray(ko[: pos + 1].reshape(pos + 1, NKV, D).transpose(1, 0, 2))
+    vh = np.ascontiguousarray(vo[: pos + 1].reshape(pos + 1, NKV, D).transpose(1, 0, 2))
+    att = orc.flash_attn_decode(qr, kh.view(np.uint16), vh.view(np.uint16), 1.0 / np.sqrt(D)).reshape(-1)
+    x1 = mm("o", att) + x
+    _, c2 = orc.rms_norm(x1.reshape(1, H), eps, fn)
+    y_ref = mm("down", orc.swiglu(mm("gate", c2), mm("up", c2))) + x1
+    err = rel_l2(y, y_ref)
+    print(f"Q4_K layer end-to-end rel L2 {err:.2e}")
+    assert err < 1e-2, err
+
+
+@pytest.fixture(scope="module")
+def model(dev):
+    from ameva_compute_amd.model import random_model
+    m = random_model(dev, ctx=1024, seed=5, max_new=64)
+    torch.cuda.synchronize()
+    return m
+
+
+def _clear(m):
+    for lay in m.layers:
+        lay.k_cache.zero_()
+        lay.v_cache.zero_()
+    m.reset()
+
+
+def test_full_model_prefill_and_greedy_graph_replay(dev, model, ops, orc):
+    """Config 5 at full size: 32 Q4_K layers, Q6_K head of 128256 rows, Q4_K embedding. A 512-token prefill, then
+    greedy steps captured once in a HIP graph and replayed: tokens and logits equal the eager steps; every token is
+    the argmax of the logits before it; the last step's head equals the oracle's Q6_K GEMV of the same normed
+    hidden state."""
+    m = model
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    prompt = torch.randint(0, m.vocab, (512,), generator=g, device=dev, dtype=torch.int32)
+    steps = 6
+
+    def run(graph):
+        _clear(m)
+        m.prefill(prompt)
+        m.set_position(prompt.numel())
+        logits = [m.logits.clone()]
+        if graph:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                m.decode_step(True)
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            logits.append(m.logits.clone())
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                m.decode_step(True)
+            for _ in range(steps - 1):
+                gr.replay()
+                torch.cuda.synchronize()
+                logits.append(m.logits.clone())
+        else:
+            for _ in range(steps):
+                m.decode_step(True)
+                logits.append(m.logits.clone())
+        torch.cuda.synchronize()
+        return m.history[: steps + 1].cpu().tolist(), torch.stack(logits)
+
+    h_e, l_e = run(False)
+    assert torch.isfinite(l_e).all()
+    h_g, l_g = run(True)
+    assert h_g == h_e and torch.equal(l_g, l_e)
+    assert [int(torch.argmax(lv).item()) for lv in l_e] == h_e
+    # the head of the last step against the oracle, from the normed hidden state the GPU fed it
+    t = m.t_out.cpu().numpy().reshape(1, -1)
+    a = orc.quantize_q8_K(t)
+    head = m.head.to_ggml().cpu().numpy()
+    y_ref = orc.mul_mat(Q6_K, head, m.vocab, m.H, a, 1).reshape(-1)
+    e = rel_l2(m.logits.cpu().numpy(), y_ref)
+    print(f"32-layer model: tokens {h_e}; head vs oracle rel L2 {e:.2e}")
+    assert e < 1e-3
+
+
+def _prefill_by_layer(m, prompt):
+    """The model's prefill run layer by layer: returns each layer's input and output rows of the last token."""
+    n = prompt.numel()
+    st = torch.cuda.current_stream().cuda_stream
+    shared = m.layers[0]._prefill_buffers(n)
+    for lay in m.layers:
+        lay._pf = shared
+    a = torch.empty((n, m.H), device=prompt.device)
+    b = torch.empty_like(a)
+    m._embed(prompt, a, n, st)
+    m.layers[0].set_prefill_position(0, n)
+    ins, outs, atts = [], [], []
+    for lay in m.layers:
+        lay.pf_pos0, lay.pf_n = 0, n
+        ins.append(a[n - 1].clone())
+        lay.prefill(a, b)
+        outs.append(b[n - 1].clone())
+        atts.append(shared["att"][n - 1].clone())
+        a, b = b, a
+    return ins, outs, atts
+
+
+def test_full_model_prefill_matches_token_by_token(dev, model):
+    """The 512-token prompt as one prefill chunk against the same prompt decoded one token at a time (the prompt's
+    tokens forced into 512 decode steps).
+
+    The two paths differ by design in one place: prefill attention runs on the f16 matrix cores with f16
+    probabilities, decode attention in f32 (1e-4 relative on a layer's attention output). Every Q8_K requantization
+    after it (attention output, FFN norm, SWIGLU output) turns that into whole-quantum flips of the elements near a
+    rounding boundary and grows it ~5-10x, so one layer's output differs by ~1.5e-2 and 32 random layers accumulate
+    ~1e-1 on the logits. Checked: (1) per layer, decode of the last token fed the prefill's own input to that layer
+    (layers 0, 16, 31): attention within the 2e-3 bar and the layer output within 3e-2; (2) end to end: the same
+    greedy token, and a KL divergence of the next-token distributions below 5e-2."""
+    m = model
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    n = 512
+    prompt = torch.randint(0, m.vocab, (n,), generator=g, device=dev, dtype=torch.int32)
+    _clear(m)
+    ins, outs, atts = _prefill_by_layer(m, prompt)
+    st = torch.cuda.current_stream().cuda_stream
+    m._head(outs[-1], st)
+    torch.cuda.synchronize()
+    lp = m.logits.cpu().numpy().copy()
+    # (1) per layer, on the caches the prefill wrote (the decode rewrites key n - 1 with its own, nearly equal row)
+    y = torch.empty(m.H, device=dev)
+    for li in (0, 16, 31):
+        lay = m.layers[li]
+        lay.set_position(n - 1)
+        lay.decode(ins[li].contiguous(), y, fused=False)
+        torch.cuda.synchronize()
+        ea, eo = rel_l2(lay.att.cpu().numpy(), atts[li].cpu().numpy()), rel_l2(y.cpu().numpy(), outs[li].cpu().numpy())
+        print(f"layer {li}: attention rel L2 {ea:.2e}, layer output rel L2 {eo:.2e}")
+        assert ea < 2e-3 and eo < 3e-2, (li, ea, eo)
+    # (2) end to end
+    _clear(m)
+    for i in range(n):
+        m.set_position(i)
+        m.token.copy_(prompt[i:i + 1])
+        m.decode_step(True)
+    torch.cuda.synchronize()
+    ld = m.logits.cpu().numpy()
+    e = rel_l2(ld, lp)
+    pp = np.exp(lp.astype(np.float64) - lp.max())
+    pp /= pp.sum()
+    pd = np.exp(ld.astype(np.float64) - ld.max())
+    pd /= pd.sum()
+    kld = float(np.sum(pp * (np.log(pp + 1e-300) - np.log(pd + 1e-300))))
+    print(f"32-layer prefill(512) vs token-by-token: logits rel L2 {e:.2e}, KLD {kld:.2e}, top-1 "
+          f"{int(np.argmax(lp))} / {int(np.argmax(ld))}")
+    assert kld < 5e-2, kld
+    assert int(np.argmax(ld)) == int(np.argmax(lp))

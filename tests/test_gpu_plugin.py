@@ -79,6 +79,111 @@ def test_mul_mat_node(plugin, orc, wt, m):
         g.free()
 
 
+# The reference's placement matrix (tests/ameva_qmm_check.cpp:46-48, 103-166, 240-246): the weight in a compute
+# buffer ("resident", repacked into scratch per use), in a WEIGHTS buffer ("weights", repacked in place once), in a
+# WEIGHTS buffer written by two partial set_tensor calls that end inside a row ("split"), and a view of rows
+# [3, 3 + N) of a weight of N + 5 rows ("view"); its shapes: one-column GEMVs, small batches below and above the
+# MFMA crossover (M = 8), odd N and partial tiles, long rows, and K = 544 (17 blocks of 32, not whole K-quant
+# super-blocks).
+MMQ_PLUGIN_TYPES = (gp.Q4_0, gp.Q8_0, gp.Q4_K)  # weight types with a batched (M >= 8) matrix-core kernel
+QMM_SHAPES = [(1, 37, 256), (5, 64, 512), (8, 16, 256), (13, 33, 768), (1, 70, 2560), (3, 19, 4096), (40, 70, 512),
+              (33, 130, 256), (1, 21, 544)]
+
+
+@pytest.mark.parametrize("place", ["resident", "weights", "split", "view"])
+@pytest.mark.parametrize("wt", [gp.Q4_0, gp.Q8_0, gp.Q4_K, gp.Q6_K])
+def test_mul_mat_placement_matrix(plugin, orc, wt, place):
+    be = gp.BLOCK[wt][0]
+    ran = 0
+    for M, N, K in QMM_SHAPES:
+        if K % be:
+            continue
+        rng = np.random.default_rng(wt * 7919 + M * 131 + N * 17 + K)
+        NW = N + 5 if place == "view" else N
+        if wt in (gp.Q4_0, gp.Q8_0):
+            wg = quantize(orc, wt, (rng.standard_normal((NW, K)) * 0.02).astype(np.float32))
+            aq = lambda x: orc.quantize_q8_0(x, orc.Q8_X86)  # noqa: E731
+        else:
+            wg = random_kquant(rng, wt, NW, K)
+            aq = orc.quantize_q8_K
+        wg = wg.reshape(NW, -1)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        g = gp.Graph(wg.nbytes + 4096, 16 << 20)
+        try:
+            plugin.ggml_backend_ameva_reset_counters()
+            W = g.tensor(wt, [K, NW], "c" if place == "resident" else "w", "w")
+            X = g.tensor(gp.F32, [K, M], "c", "x")
+            if place == "split":  # the first write ends inside a row and is not the whole tensor
+                raw = np.ascontiguousarray(wg).reshape(-1)
+                cut = raw.nbytes // 3 + 1
+                buf = gp.ctypes.cast(W.buffer, gp.POINTER(gp.Buffer)).contents
+                buf.iface.set_tensor(W.buffer, gp.ctypes.addressof(W), raw.ctypes.data, 0, cut)
+                buf.iface.set_tensor(W.buffer, gp.ctypes.addressof(W), raw.ctypes.data + cut, cut, raw.nbytes - cut)
+            else:
+                g.set(W, wg)
+            g.set(X, x)
+            rb = wg.shape[1]
+            src0 = g.view(W, wt, [K, N], [W.nb[0], rb, rb * N, rb * N], 3 * rb, "w_rows") if place == "view" else W
+            Y = g.mul_mat(src0, X)
+            assert not g.reason(Y), (M, N, K, g.reason(Y))
+            rep0 = gp.counter(plugin, "repacked_tensor_count")
+            assert g.compute() == gp.STATUS_SUCCESS, (M, N, K)
+            y = g.get(Y, np.float32, (M, N))
+            r0 = 3 if place == "view" else 0
+            want = orc.mul_mat(wt, np.ascontiguousarray(wg[r0:r0 + N]), N, K, aq(x), M)
+            assert rel_l2(y, want) < 1e-3, (M, N, K, rel_l2(y, want))
+            repacked = place in ("weights", "split")
+            assert gp.counter(plugin, "repacked_tensor_count") == rep0 + (1 if repacked else 0), (M, N, K)
+            assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 1
+            batched = M >= 8 and wt in MMQ_PLUGIN_TYPES
+            assert gp.counter(plugin, "mmq_mul_mat_count") == (1 if batched else 0), (M, N, K)
+            # the buffer interface returns the uploaded ggml bytes, whole and from inside a row to inside a row
+            assert np.array_equal(g.get(W, np.uint8), wg.reshape(-1)), (M, N, K)
+            o, cnt = rb // 2 + 1, wg.nbytes - rb
+            part = np.empty(cnt, np.uint8)
+            buf = gp.ctypes.cast(W.buffer, gp.POINTER(gp.Buffer)).contents
+            buf.iface.get_tensor(W.buffer, gp.ctypes.addressof(W), part.ctypes.data, o, cnt)
+            assert np.array_equal(part, wg.reshape(-1)[o:o + cnt]), (M, N, K)
+            ran += 1
+        finally:
+            g.free()
+    assert ran >= 7
+
+
+@pytest.mark.parametrize("wt", [gp.Q4_0, gp.Q4_K])
+def test_mul_mat_view_of_repacked_weight(plugin, orc, wt):
+    """A graph that reads a weight whole (which repacks it in place) and then rows [3, 3 + N) of it through a view:
+    the view's rows come from a ggml-layout copy of the repacked parent, and both products match the oracle."""
+    rng = np.random.default_rng(wt)
+    NW, N, K, M = 133, 64, 512, 12
+    if wt == gp.Q4_0:
+        wg = quantize(orc, wt, (rng.standard_normal((NW, K)) * 0.02).astype(np.float32)).reshape(NW, -1)
+        aq = lambda x: orc.quantize_q8_0(x, orc.Q8_X86)  # noqa: E731
+    else:
+        wg = random_kquant(rng, wt, NW, K)
+        aq = orc.quantize_q8_K
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    g = gp.Graph(wg.nbytes + 4096, 16 << 20)
+    try:
+        W = g.tensor(wt, [K, NW], "w", "w")
+        X = g.tensor(gp.F32, [K, M], "c", "x")
+        g.set(W, wg)
+        g.set(X, x)
+        rb = wg.shape[1]
+        V = g.view(W, wt, [K, N], [W.nb[0], rb, rb * N, rb * N], 3 * rb, "w_rows")
+        YW = g.mul_mat(W, X, "whole")
+        YV = g.mul_mat(V, X, "rows")
+        rep0 = gp.counter(plugin, "repacked_tensor_count")
+        assert g.compute() == gp.STATUS_SUCCESS
+        assert gp.counter(plugin, "repacked_tensor_count") == rep0 + 1
+        a = aq(x)
+        assert rel_l2(g.get(YW, np.float32, (M, NW)), orc.mul_mat(wt, wg, NW, K, a, M)) < 1e-3
+        assert rel_l2(g.get(YV, np.float32, (M, N)), orc.mul_mat(wt, np.ascontiguousarray(wg[3:3 + N]), N, K, a, M)) < 1e-3
+        assert np.array_equal(g.get(W, np.uint8), wg.reshape(-1))
+    finally:
+        g.free()
+
+
 def test_activation_reuse_and_norm_fusion(plugin, orc):
     rng = np.random.default_rng(3)
     k, n = 4096, 256
