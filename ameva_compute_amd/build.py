@@ -3,7 +3,10 @@
 Flags that carry meaning:
   -ffp-contract=off and -fhip-fp32-correctly-rounded-divide-sqrt: the quantizers must round x * id, 1/d and
       127/amax exactly as the CPU does (bit-exact Q8_0 / Q4_0 bytes);
-  -Xclang -target-feature -Xclang -packed-fp32-ops: keep hipcc from emitting packed-FP32 VALU ops.
+  -Xclang -target-feature -Xclang -packed-fp32-ops: keep hipcc from emitting packed-FP32 VALU ops;
+  -mllvm -amdgpu-mfma-vgpr-form: matrix-core results in VGPRs (the epilogues read them with VALU ops; in AGPRs every
+      value costs a v_accvgpr_read first: 64 more VALU ops per 32x32 block of four tiles);
+  -mllvm -disable-promote-alloca-to-lds: keep per-thread staging structs in registers, not in LDS slices.
 """
 from __future__ import annotations
 
@@ -14,13 +17,14 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libameva_hip.so")
-SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_fa_prefill.hip", "amv_mmq.hip", "amv_mmq16.hip", "amv_elem.hip", "amv_bitnet.hip"]
+SOURCES = ["amv_runtime.hip", "amv_quant.hip", "amv_mmv.hip", "amv_i2s.hip", "amv_norm.hip", "amv_attn.hip", "amv_fa_prefill.hip", "amv_mmq.hip", "amv_mmq16.hip", "amv_qgemm.hip", "amv_elem.hip", "amv_bitnet.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-disable-promote-alloca-to-lds",
     "-Wall", "-Wno-unused-function",
 ]
 

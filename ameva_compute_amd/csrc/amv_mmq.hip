@@ -438,6 +438,15 @@ static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, in
     return amv_check_launch("amv_mul_mat_q");
 }
 
+// amv_qgemm.hip: Q4_0 / Q8_0 / Q4_K on the int8 matrix cores with exact block integers, plain activation layouts
+int amv_qgemm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
+              int64_t ldd, int32_t* sums, hipStream_t st);
+
+// Batches above this many tokens go to the tiled kernels (amv_qgemm for the exact layouts and the plain ones, the f16
+// kernels for the scaled DEQ layouts); smaller ones to the k_mmq kernels of this file, which read the plain Q8_0
+// prefix (Q4_0 / Q8_0) or the f16 copies of AMV_ACT_Q8_K_MMA (Q4_K).
+#define MMQ16_MIN_M 64
+
 static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                     int64_t ldd, int32_t* sums, void* stream) {
     AMV_REQUIRE(w && act && (dst || sums), "amv_mul_mat_q: null pointer");
@@ -447,6 +456,11 @@ static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const v
     AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 32 && n_rows * (k / 32) <= INT32_MAX, "amv_mul_mat_q: too large");
     AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "amv_mul_mat_q: buffers must be 16-byte aligned");
     AMV_REQUIRE(!dst || ldd >= n_rows, "amv_mul_mat_q: ldd < n_rows");
+    if (m > MMQ16_MIN_M) {  // the tiled int8 kernel reads the plain prefix of any of the activation layouts
+        AMV_REQUIRE(wtype != AMV_T_Q4_K || k % 256 == 0, "amv_mul_mat_q: Q4_K needs k %% 256 == 0");
+        AMV_REQUIRE(m * k <= INT32_MAX && m <= 65535LL * 128, "amv_mul_mat_q: too large");
+        return amv_qgemm(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
+    }
     if (wtype == AMV_T_Q4_K) return mmq_q4k(w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
     const int nb = (int)(k / 32);
     const int64_t nblk = n_rows * nb;
@@ -472,17 +486,14 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
 int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
                   int32_t* sums, int deq, hipStream_t st);
 
-// Batches above this many tokens go to the f16 kernel (128-token tiles); smaller ones to the int8 kernel, which reads
-// the plain Q8_0 prefix of the same activation buffer.
-#define MMQ16_MIN_M 64
 
 static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
                         int act_type, int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream) {
     const bool deq = act_type == AMV_ACT_Q8_0_DEQ || act_type == AMV_ACT_Q8_K_DEQ;
     const bool q80x = act_type == AMV_ACT_Q8_0_MMA || act_type == AMV_ACT_Q8_0_DEQ;
     const bool q8kx = act_type == AMV_ACT_Q8_K_MMA || act_type == AMV_ACT_Q8_K_DEQ;
-    const bool tiled = m > MMQ16_MIN_M && ((q80x && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
-                                           (q8kx && wtype == AMV_T_Q4_K));
+    const bool tiled = m > MMQ16_MIN_M && (((q80x || act_type == AMV_T_Q8_0) && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
+                                           ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q4_K));
     if (tiled) {
         AMV_REQUIRE(w && act && (dst || sums), "%s: null pointer", fn);
         AMV_REQUIRE(!(deq && sums), "%s: block sums need the exact layout (AMV_ACT_Q8_0_MMA / AMV_ACT_Q8_K_MMA), not "
@@ -492,11 +503,10 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
                     "%s: too large", fn);
         AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "%s: buffers must be 16-byte aligned", fn);
         AMV_REQUIRE(!dst || ldd >= n_rows, "%s: ldd < n_rows", fn);
-        if (wtype == AMV_T_Q4_K) {
-            AMV_REQUIRE(k % 256 == 0, "%s: Q4_K needs k %% 256 == 0", fn);
-            return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, sums, deq ? 1 : 0, amv_stream(stream));
-        }
-        return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, deq ? 1 : 0, amv_stream(stream));
+        if (wtype == AMV_T_Q4_K) AMV_REQUIRE(k % 256 == 0, "%s: Q4_K needs k %% 256 == 0", fn);
+        if (!deq) return amv_qgemm(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
+        if (wtype == AMV_T_Q4_K) return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, sums, 1, amv_stream(stream));
+        return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, 1, amv_stream(stream));
     }
     const bool ok = (act_type == AMV_T_Q8_0 || q80x) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)
                                                      : (q8kx && wtype == AMV_T_Q4_K);

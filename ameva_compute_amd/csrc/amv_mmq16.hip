@@ -323,7 +323,7 @@ std::mutex g_splitk_mu;
 std::map<int, std::pair<float*, size_t>> g_splitk_ws;  // device -> (buffer, bytes)
 }  // namespace
 
-static float* splitk_workspace(size_t bytes, hipStream_t st) {
+float* amv_splitk_workspace(size_t bytes, hipStream_t st) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_splitk_mu);
@@ -356,15 +356,15 @@ static float* splitk_workspace(size_t bytes, hipStream_t st) {
 #ifndef SPLITK_MIN_TOTAL
 #define SPLITK_MIN_TOTAL 96
 #endif
-static int splitk_count(int64_t tiles, int steps) {
+int amv_splitk_count(int64_t tiles, int steps) {
     int S = 1;
     if (steps < SPLITK_MIN_TOTAL) return 1;
     while (S < 8 && tiles * S < SPLITK_TARGET && steps / (2 * S) >= SPLITK_MIN_STEPS) S *= 2;
     return S;
 }
 
-static void splitk_reduce(const float* part, int S, int64_t zstride, int64_t m, int64_t n, float* dst, int64_t ldd,
-                          hipStream_t st) {
+void amv_splitk_reduce(const float* part, int S, int64_t zstride, int64_t m, int64_t n, float* dst, int64_t ldd,
+                       hipStream_t st) {
     const int vec = n % 4 == 0 && ldd % 4 == 0 && ((uintptr_t)dst & 15) == 0;
     const int64_t items = vec ? m * (n / 4) : m * n;
     hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, part, S, zstride, (int)m,
@@ -397,11 +397,11 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
     int64_t ldo = ldd, zstride = 0;
     int vo = vec_out;
     if (deq && !sums) {
-        const int S = splitk_count(cfg == 22 ? wgs(2, 2) : wgs(1, 1), (nb + 1) / 2);
+        const int S = amv_splitk_count(cfg == 22 ? wgs(2, 2) : wgs(1, 1), (nb + 1) / 2);
         if (S > 1) {
             kb_per = ((nb + S - 1) / S + 1) & ~1;  // whole pipeline steps
             nz = (nb + kb_per - 1) / kb_per;
-            float* ws = nz > 1 ? splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
+            float* ws = nz > 1 ? amv_splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
             if (ws) {
                 out = ws;
                 ldo = n_rows;
@@ -433,7 +433,7 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
     }
 #undef G16_CFG
 #undef G16_LAUNCH
-    if (nz > 1) splitk_reduce(out, nz, zstride, m, n_rows, dst, ldd, st);
+    if (nz > 1) amv_splitk_reduce(out, nz, zstride, m, n_rows, dst, ldd, st);
     return amv_check_launch("amv_mul_mat_q_act");
 }
 
@@ -718,11 +718,11 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
     int64_t ldo = ldd, zstride = 0;
     int vo = vec_out;
     if (deq && !sums) {  // split of k when the tiles leave CUs idle (4 pipeline steps per super-block)
-        const int S = splitk_count(cfg == 22 ? wgs(2, 2) : wgs(1, 1), 4 * nsb);
+        const int S = amv_splitk_count(cfg == 22 ? wgs(2, 2) : wgs(1, 1), 4 * nsb);
         if (S > 1) {
             sb_per = (nsb + S - 1) / S;
             nz = (nsb + sb_per - 1) / sb_per;
-            float* ws = nz > 1 ? splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
+            float* ws = nz > 1 ? amv_splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
             if (ws) {
                 out = ws;
                 ldo = n_rows;
@@ -750,6 +750,6 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
         else G16K_LAUNCH(false, 1, 1, false);
     }
 #undef G16K_LAUNCH
-    if (nz > 1) splitk_reduce(out, nz, zstride, m, n_rows, dst, ldd, st);
+    if (nz > 1) amv_splitk_reduce(out, nz, zstride, m, n_rows, dst, ldd, st);
     return amv_check_launch("amv_mul_mat_q_act");
 }

@@ -54,16 +54,16 @@ if MMQ_FORM not in ("exact", "scaled"):
 
 
 def act_type(wtype: int, m: int = 1, exact: bool | None = None) -> int:
-    """ggml vec_dot_type of a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants; for a batched MUL_MAT
-    (m >= MMQ_MIN_M) the layout extended with the f16 copies the matrix-core kernels read: the exact-integer form
-    (MMA), or above MMQ16_MIN_M tokens the scaled form (DEQ) when exact is False (None: MMQ_FORM decides)."""
+    """The activation layout a MUL_MAT of m tokens reads: ggml's vec_dot_type (Q8_0 for Q4_0/Q8_0, Q8_K for the
+    K-quants) in the plain layout, except for batched Q4_K of MMQ_MIN_M..MMQ16_MIN_M tokens (the small-batch kernel
+    reads the f16 copies of Q8_K_MMA) and for the scaled form above MMQ16_MIN_M tokens when exact is False (DEQ;
+    None: MMQ_FORM decides). The exact tiled kernel above MMQ16_MIN_M tokens reads the plain layout."""
     if exact is None:
         exact = MMQ_FORM == "exact"
-    deq = m > MMQ16_MIN_M and not exact
-    if wtype == Q4_K and m >= MMQ_MIN_M:
-        return Q8_K_DEQ if deq else Q8_K_MMA
-    if wtype in (Q4_0, Q8_0) and m >= MMQ_MIN_M:
-        return Q8_0_DEQ if deq else Q8_0_MMA
+    if wtype in (Q4_0, Q8_0, Q4_K) and m > MMQ16_MIN_M and not exact:
+        return Q8_K_DEQ if wtype == Q4_K else Q8_0_DEQ
+    if wtype == Q4_K and MMQ_MIN_M <= m <= MMQ16_MIN_M:
+        return Q8_K_MMA
     return Q8_K if wtype in (Q4_K, Q6_K) else Q8_0
 
 
@@ -143,15 +143,15 @@ def quantize_q4_0(x: torch.Tensor) -> torch.Tensor:
 
 # batch size from which MUL_MAT runs the int8-MFMA kernel (AMEVA_QGEMM_MIN_M of the reference, ggml-ameva.cpp:2486)
 MMQ_MIN_M = 8
-MMQ16_MIN_M = 64  # above this many tokens the tiled f16 kernels run (amv_mmq.hip MMQ16_MIN_M)
-MMQ_TYPES = (Q4_0, Q8_0, Q4_K)  # Q4_K: the activations must be Q8_K_MMA
+MMQ16_MIN_M = 64  # above this many tokens the tiled kernels run (amv_mmq.hip MMQ16_MIN_M)
+MMQ_TYPES = (Q4_0, Q8_0, Q4_K)  # Q4_K of MMQ_MIN_M..MMQ16_MIN_M tokens: the activations must be Q8_K_MMA
 
 
 def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = None,
               kernel: str = "auto", act_t: int | None = None) -> torch.Tensor:
     """dst [m, n_rows] f32 from already quantized activations (amv_quantize_act layout of m rows).
     kernel: "auto" (the reference's routing: MFMA GEMM for m >= MMQ_MIN_M where the type has one), "mmv", "mmq".
-    Q4_K on "mmq" needs the activations quantized as Q8_K_MMA or Q8_K_DEQ. act_t: the activation layout (the DEQ
+    Q4_K on "mmq" needs Q8_K_MMA activations up to MMQ16_MIN_M tokens. act_t: the activation layout (the DEQ
     layouts have the MMA sizes, so they must be named; None: told apart by size, i.e. plain or MMA)."""
     _need_gpu(act, "mul_mat_q")
     if out is None:
