@@ -150,12 +150,12 @@ __device__ __forceinline__ float amv_row16_sum(float v) {
     return v;
 }
 
-// wave64 sum: every lane ends with the total (DPP within rows, then two cross-row exchanges)
+// wave64 sum: every lane ends with the total, (row 0 + row 1) + (row 2 + row 3) of the DPP row sums, the four row
+// totals read with v_readlane (no LDS round trip)
 __device__ __forceinline__ float amv_wave_sum(float v) {
-    v = amv_row16_sum(v);
-    v += __shfl_xor(v, 16, AMV_WAVE);
-    v += __shfl_xor(v, 32, AMV_WAVE);
-    return v;
+    const int i = __float_as_int(amv_row16_sum(v));
+    return (__int_as_float(__builtin_amdgcn_readlane(i, 0)) + __int_as_float(__builtin_amdgcn_readlane(i, 16))) +
+           (__int_as_float(__builtin_amdgcn_readlane(i, 32)) + __int_as_float(__builtin_amdgcn_readlane(i, 48)));
 }
 __device__ __forceinline__ int amv_wave_sum_i(int v) {
 #pragma unroll
