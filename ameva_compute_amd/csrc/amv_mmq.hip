@@ -438,7 +438,8 @@ static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, in
     return amv_check_launch("amv_mul_mat_q");
 }
 
-// amv_qgemm.hip: Q4_0 / Q8_0 / Q4_K on the int8 matrix cores with exact block integers, plain activation layouts
+// amv_qgemm.hip: Q4_0 / Q8_0 / Q4_K / Q6_K on the int8 matrix cores with exact block integers, plain activation
+// layouts
 int amv_qgemm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
               int64_t ldd, int32_t* sums, hipStream_t st);
 
@@ -450,14 +451,15 @@ int amv_qgemm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
 static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                     int64_t ldd, int32_t* sums, void* stream) {
     AMV_REQUIRE(w && act && (dst || sums), "amv_mul_mat_q: null pointer");
-    AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0 || wtype == AMV_T_Q4_K,
-                "amv_mul_mat_q: weight type %d not supported (Q4_0, Q8_0, Q4_K)", wtype);
+    AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0 || wtype == AMV_T_Q4_K || wtype == AMV_T_Q6_K,
+                "amv_mul_mat_q: weight type %d not supported (Q4_0, Q8_0, Q4_K, Q6_K)", wtype);
     AMV_REQUIRE(n_rows > 0 && m > 0 && k > 0 && k % 32 == 0, "amv_mul_mat_q: bad shape");
     AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 32 && n_rows * (k / 32) <= INT32_MAX, "amv_mul_mat_q: too large");
     AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "amv_mul_mat_q: buffers must be 16-byte aligned");
     AMV_REQUIRE(!dst || ldd >= n_rows, "amv_mul_mat_q: ldd < n_rows");
-    if (m > MMQ16_MIN_M) {  // the tiled int8 kernel reads the plain prefix of any of the activation layouts
-        AMV_REQUIRE(wtype != AMV_T_Q4_K || k % 256 == 0, "amv_mul_mat_q: Q4_K needs k %% 256 == 0");
+    if (m > MMQ16_MIN_M || wtype == AMV_T_Q6_K) {  // the tiled int8 kernel reads the plain prefix of any layout
+        AMV_REQUIRE((wtype != AMV_T_Q4_K && wtype != AMV_T_Q6_K) || k % 256 == 0,
+                    "amv_mul_mat_q: K-quants need k %% 256 == 0");
         AMV_REQUIRE(m * k <= INT32_MAX && m <= 65535LL * 128, "amv_mul_mat_q: too large");
         return amv_qgemm(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
     }
@@ -492,8 +494,10 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
     const bool deq = act_type == AMV_ACT_Q8_0_DEQ || act_type == AMV_ACT_Q8_K_DEQ;
     const bool q80x = act_type == AMV_ACT_Q8_0_MMA || act_type == AMV_ACT_Q8_0_DEQ;
     const bool q8kx = act_type == AMV_ACT_Q8_K_MMA || act_type == AMV_ACT_Q8_K_DEQ;
-    const bool tiled = m > MMQ16_MIN_M && (((q80x || act_type == AMV_T_Q8_0) && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
-                                           ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q4_K));
+    // Q6_K batches of any size run the tiled int8 kernel (there is no small-batch Q6_K kernel)
+    const bool tiled = (m > MMQ16_MIN_M && (((q80x || act_type == AMV_T_Q8_0) && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
+                                            ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q4_K))) ||
+                       ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q6_K);
     if (tiled) {
         AMV_REQUIRE(w && act && (dst || sums), "%s: null pointer", fn);
         AMV_REQUIRE(!(deq && sums), "%s: block sums need the exact layout (AMV_ACT_Q8_0_MMA / AMV_ACT_Q8_K_MMA), not "
@@ -503,7 +507,8 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
                     "%s: too large", fn);
         AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "%s: buffers must be 16-byte aligned", fn);
         AMV_REQUIRE(!dst || ldd >= n_rows, "%s: ldd < n_rows", fn);
-        if (wtype == AMV_T_Q4_K) AMV_REQUIRE(k % 256 == 0, "%s: Q4_K needs k %% 256 == 0", fn);
+        if (wtype == AMV_T_Q4_K || wtype == AMV_T_Q6_K) AMV_REQUIRE(k % 256 == 0, "%s: K-quants need k %% 256 == 0", fn);
+        AMV_REQUIRE(!(deq && wtype == AMV_T_Q6_K), "%s: Q6_K has no scaled form (use Q8_K or AMV_ACT_Q8_K_MMA)", fn);
         if (!deq) return amv_qgemm(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
         if (wtype == AMV_T_Q4_K) return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, sums, 1, amv_stream(stream));
         return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, 1, amv_stream(stream));

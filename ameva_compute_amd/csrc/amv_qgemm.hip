@@ -455,6 +455,222 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Q6_K x Q8_K (reference vec_dot_q6_K_q8_K; ameva_qdecode.glsl:246-258 for the element layout). A super-block of 256
+// is 16 sub-blocks of 16 consecutive elements with int8 scales sc_s and one f16 d: I = sum_s sc_s sum_k q_k a_k with
+// q = (4 low bits from ql | 2 high bits from qh) - 32, dst += d_a d I. The sub-blocks are 16 long, so the matrix core
+// runs v_mfma_i32_32x32x16_i8 (lane half h supplies 8 of the 16 bytes) and I accumulates sc_s C_s in integers. Step =
+// one 128-element half n of the super-block: ql bytes 64 n .. + 63 and qh bytes 32 n .. + 31 give elements
+// 128 n + {l, 32 + l, 64 + l, 96 + l} (l < 32) from ql[l] low / ql[32 + l] low / ql[l] high / ql[32 + l] high nibbles
+// and qh[l] bits 0-1 / 2-3 / 4-5 / 6-7.
+// ---------------------------------------------------------------------------------------------------------------
+typedef long qg_i64;
+
+#define QG6_LD (128 + 16)  // LDS row stride (bytes) of the 128-element steps
+
+struct QgQ6Regs {
+    uint4 l0, l1, qh;  // ql[16 hf ..], ql[32 + 16 hf ..], qh[16 hf ..] of the half (row t / 2, hf = t % 2)
+    uint4 a0, a1, a2, a3;  // 64 activation int8 (token t / 2, elements 128 c + 64 hf ..)
+    uint4 sc;          // at half 0: the row's 16 scales
+    uint32_t d;        // at half 0: f16 d
+    float da;          // at half 0: the token's d
+};
+
+template <int TT, int TW>
+__device__ __forceinline__ void qg6_load(QgQ6Regs& s, int step, const uint4* __restrict__ wl,
+                                         const uint4* __restrict__ wqh, const uint4* __restrict__ wsc,
+                                         const uint16_t* __restrict__ wd, int N, int nsb, int n0,
+                                         const int8_t* __restrict__ aq, const float* __restrict__ ad, int M, int m0,
+                                         int K, int sb0) {
+    constexpr int BN = 64 * TW, BM = 64 * TT;
+    const int t = threadIdx.x, hf = t & 1;
+    const int j = sb0 + (step >> 1), c = step & 1;
+    if (t < 2 * BN) {
+        const int row = min(n0 + (t >> 1), N - 1);
+        const size_t sb = (size_t)row * nsb + j;
+        s.l0 = wl[sb * 8 + 4 * c + hf];      // ql bytes 64 c + 16 hf
+        s.l1 = wl[sb * 8 + 4 * c + 2 + hf];  // ql bytes 64 c + 32 + 16 hf
+        s.qh = wqh[sb * 4 + 2 * c + hf];     // qh bytes 32 c + 16 hf
+        if (c == 0) {
+            s.sc = wsc[sb];
+            s.d = wd[sb];
+        }
+    }
+    if (t < 2 * BM) {
+        const int tok = min(m0 + (t >> 1), M - 1);
+        const uint4* p = reinterpret_cast<const uint4*>(aq + (size_t)tok * K + 256 * j + 128 * c + 64 * hf);
+        s.a0 = p[0];
+        s.a1 = p[1];
+        s.a2 = p[2];
+        s.a3 = p[3];
+        if (c == 0) s.da = ad[(size_t)tok * nsb + j];
+    }
+}
+
+// 4 bytes of ql nibbles n (already selected) and their 2 high bits hb (already at bit 4..5): n | hb - 32 per byte
+__device__ __forceinline__ uint32_t qg6_q(uint32_t n, uint32_t hb) { return ((n | hb) + 0x60606060u) ^ 0x80808080u; }
+
+template <int TT, int TW>
+__device__ __forceinline__ void qg6_store(const QgQ6Regs& s, int step, int8_t* __restrict__ sW,
+                                          int8_t* __restrict__ sA, int8_t* __restrict__ sSc, float* __restrict__ sD,
+                                          float* __restrict__ sDa) {
+    constexpr int BN = 64 * TW, BM = 64 * TT;
+    const int t = threadIdx.x, hf = t & 1, c = step & 1;
+    if (t < 2 * BN) {
+        const int rl = t >> 1;
+        uint4* d = reinterpret_cast<uint4*>(sW + rl * QG6_LD);
+        const uint32_t L0[4] = {s.l0.x, s.l0.y, s.l0.z, s.l0.w}, L1[4] = {s.l1.x, s.l1.y, s.l1.z, s.l1.w};
+        const uint32_t H[4] = {s.qh.x, s.qh.y, s.qh.z, s.qh.w};
+        uint32_t q1[4], q2[4], q3[4], q4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q1[i] = qg6_q(L0[i] & 0x0F0F0F0Fu, (H[i] & 0x03030303u) << 4);
+            q2[i] = qg6_q(L1[i] & 0x0F0F0F0Fu, (H[i] & 0x0C0C0C0Cu) << 2);
+            q3[i] = qg6_q((L0[i] >> 4) & 0x0F0F0F0Fu, H[i] & 0x30303030u);
+            q4[i] = qg6_q((L1[i] >> 4) & 0x0F0F0F0Fu, (H[i] >> 2) & 0x30303030u);
+        }
+        d[hf] = make_uint4(q1[0], q1[1], q1[2], q1[3]);      // elements 16 hf ..
+        d[2 + hf] = make_uint4(q2[0], q2[1], q2[2], q2[3]);  // 32 + 16 hf ..
+        d[4 + hf] = make_uint4(q3[0], q3[1], q3[2], q3[3]);  // 64 + 16 hf ..
+        d[6 + hf] = make_uint4(q4[0], q4[1], q4[2], q4[3]);  // 96 + 16 hf ..
+        if (c == 0) {  // scales of sub-blocks 8 hf .. 8 hf + 7 (bytes), d
+            const uint32_t sw[2] = {hf ? s.sc.z : s.sc.x, hf ? s.sc.w : s.sc.y};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sSc[(8 * hf + e) * BN + rl] = (int8_t)((sw[e >> 2] >> (8 * (e & 3))) & 0xFFu);
+            if (hf == 0) sD[rl] = amv_h2f(s.d);
+        }
+    }
+    if (t < 2 * BM) {
+        const int tl = t >> 1;
+        uint4* d = reinterpret_cast<uint4*>(sA + tl * QG6_LD + 64 * hf);
+        d[0] = s.a0;
+        d[1] = s.a1;
+        d[2] = s.a2;
+        d[3] = s.a3;
+        if (c == 0 && hf == 0) sDa[tl] = s.da;
+    }
+}
+
+template <bool SUMS, int TT, int TW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm_q6k(
+    const uint4* __restrict__ wl, const uint4* __restrict__ wqh, const uint4* __restrict__ wsc,
+    const uint16_t* __restrict__ wd, int N, int nsb, const int8_t* __restrict__ aq, const float* __restrict__ ad, int M,
+    float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ sums, int sb_per, int64_t zstride, int n_tw, int n_tt,
+    int n_z) {
+    constexpr int BN = 64 * TW, BM = 64 * TT;
+    __shared__ __align__(16) int8_t sW[2][BN * QG6_LD];
+    __shared__ __align__(16) int8_t sA[2][BM * QG6_LD];
+    __shared__ __align__(16) int8_t sSc[2][16 * BN];
+    __shared__ __align__(16) float sD[2][BN], sDa[2][BM];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wt = w & 1, ww = w >> 1, c32 = lane & 31, h = lane >> 5;
+    const int T = qg_tile(blockIdx.x, n_tw * n_z * n_tt);
+    const int tt = T % n_tt, z = (T / n_tt) % n_z, tw = T / (n_tt * n_z);
+    const int n0 = tw * BN, m0 = tt * BM;
+    const int K = nsb * 256;
+    const int sb0 = z * sb_per, sb_end = min(nsb, sb0 + sb_per);
+    const int nsteps = (sb_end - sb0) * 2;
+    dst += (size_t)z * zstride;
+
+    qg_f16v acc[TT][TW];
+    qg_v16i I[TT][TW];
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int j = 0; j < TW; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[i][j][r] = 0.0f;
+                I[i][j][r] = 0;
+            }
+
+    QgQ6Regs st;
+    qg6_load<TT, TW>(st, 0, wl, wqh, wsc, wd, N, nsb, n0, aq, ad, M, m0, K, sb0);
+    qg6_store<TT, TW>(st, 0, sW[0], sA[0], sSc[0], sD[0], sDa[0]);
+    __syncthreads();
+    for (int step = 0; step < nsteps; ++step) {
+        const int buf = step & 1, j = sb0 + (step >> 1), c = step & 1, jp = (step >> 1) & 1;
+        if (step + 1 < nsteps) qg6_load<TT, TW>(st, step + 1, wl, wqh, wsc, wd, N, nsb, n0, aq, ad, M, m0, K, sb0);
+#pragma unroll 2
+        for (int u = 0; u < 8; ++u) {  // sub-block 8 c + u
+            qg_i64 A[TT], B[TW];
+            int sc[TW];
+#pragma unroll
+            for (int i = 0; i < TT; ++i)
+                A[i] = *reinterpret_cast<const qg_i64*>(sA[buf] + (32 * (TT * wt + i) + c32) * QG6_LD + 16 * u + 8 * h);
+#pragma unroll
+            for (int jj = 0; jj < TW; ++jj) {
+                const int rl = 32 * (TW * ww + jj) + c32;
+                B[jj] = *reinterpret_cast<const qg_i64*>(sW[buf] + rl * QG6_LD + 16 * u + 8 * h);
+                sc[jj] = sSc[jp][(8 * c + u) * BN + rl];
+            }
+#pragma unroll
+            for (int i = 0; i < TT; ++i)
+#pragma unroll
+                for (int jj = 0; jj < TW; ++jj) {
+                    const qg_v16i zero = {};
+                    const qg_v16i C = __builtin_amdgcn_mfma_i32_32x32x16_i8(A[i], B[jj], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) I[i][jj][r] += __mul24(C[r], sc[jj]);
+                }
+        }
+        if (c == 1) {  // end of super-block j
+#pragma unroll
+            for (int i = 0; i < TT; ++i) {
+                const int tl = 32 * (TT * wt + i) + 4 * h;
+                float da[16];
+                if constexpr (!SUMS) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 v = *reinterpret_cast<const float4*>(&sDa[jp][tl + 8 * q]);
+                        da[4 * q] = v.x;
+                        da[4 * q + 1] = v.y;
+                        da[4 * q + 2] = v.z;
+                        da[4 * q + 3] = v.w;
+                    }
+                }
+#pragma unroll
+                for (int jj = 0; jj < TW; ++jj) {
+                    const int rl = 32 * (TW * ww + jj) + c32;
+                    if constexpr (SUMS) {
+                        const int n = n0 + rl;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int m = m0 + tl + 8 * (r >> 2) + (r & 3);
+                            if (m < M && n < N) sums[((size_t)m * N + n) * nsb + j] = I[i][jj][r];
+                        }
+                    } else {
+                        const float d = sD[jp][rl];
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][jj][r] = fmaf(d * da[r], (float)I[i][jj][r], acc[i][jj][r]);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) I[i][jj][r] = 0;
+                }
+            }
+        }
+        if (step + 1 < nsteps) {
+            const int sp = ((step + 1) >> 1) & 1;
+            qg6_store<TT, TW>(st, step + 1, sW[buf ^ 1], sA[buf ^ 1], sSc[sp], sD[sp], sDa[sp]);
+            __syncthreads();
+        }
+    }
+    if constexpr (!SUMS) {
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const int n = n0 + 32 * (TW * ww + jj) + c32;
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < TT; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + 32 * (TT * wt + i) + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < M) dst[(size_t)m * ldd + n] = acc[i][jj][r];
+                }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------------------------------------------
 // split of k shared with the f16 kernels (amv_mmq16.hip): workspace per device and the in-order partial sum
@@ -470,17 +686,17 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
     const int8_t* aq = (const int8_t*)act;
     const int n_tw = (int)((n_rows + BN - 1) / BN), n_tt = (int)((m + BM - 1) / BM);
     const int64_t tiles = (int64_t)n_tw * n_tt;
-    const bool q4k = wtype == AMV_T_Q4_K;
+    const bool q4k = wtype == AMV_T_Q4_K, q6k = wtype == AMV_T_Q6_K, kq = q4k || q6k;
     const int nb = (int)(k / 32), nsb = (int)(k / 256);
-    const int steps = q4k ? 4 * nsb : (nb + 1) / 2;
+    const int steps = q4k ? 4 * nsb : q6k ? 4 * nsb : (nb + 1) / 2;  // in units of 64 k
     // split of k when the tiles leave CUs idle (partials in the library's workspace, summed in order of k)
     int S = sums ? 1 : amv_splitk_count(tiles, steps);
-    int per = q4k ? nsb : nb;
+    int per = kq ? nsb : nb;
     float* out = dst;
     int64_t ldo = ldd, zstride = 0;
     if (S > 1) {
-        per = q4k ? (nsb + S - 1) / S : (((nb + S - 1) / S + 1) & ~1);
-        S = q4k ? (nsb + per - 1) / per : (nb + per - 1) / per;
+        per = kq ? (nsb + S - 1) / S : (((nb + S - 1) / S + 1) & ~1);
+        S = kq ? (nsb + per - 1) / per : (nb + per - 1) / per;
         float* ws = S > 1 ? amv_splitk_workspace((size_t)S * m * n_rows * 4, st) : nullptr;
         if (ws) {
             out = ws;
@@ -488,11 +704,25 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
             zstride = m * n_rows;
         } else {
             S = 1;
-            per = q4k ? nsb : nb;
+            per = kq ? nsb : nb;
         }
     }
     const dim3 grid((unsigned)(tiles * S));
-    if (q4k) {
+    if (q6k) {  // ql [n][nsb][128] | qh [n][nsb][64] | scales [n][nsb][16] | d [n][nsb]
+        const int64_t nblk = n_rows * nsb;
+        const uint8_t* base = (const uint8_t*)w;
+        const uint4* wl = (const uint4*)base;
+        const uint4* wqh = (const uint4*)(base + nblk * 128);
+        const uint4* wsc = (const uint4*)(base + nblk * 192);
+        const uint16_t* wd = (const uint16_t*)(base + nblk * 208);
+        const float* ad = (const float*)(aq + m * k);
+        if (sums)
+            hipLaunchKernelGGL((k_qgemm_q6k<true, TT, TW>), grid, dim3(256), 0, st, wl, wqh, wsc, wd, (int)n_rows, nsb,
+                               aq, ad, (int)m, out, ldo, sums, per, zstride, n_tw, n_tt, S);
+        else
+            hipLaunchKernelGGL((k_qgemm_q6k<false, TT, TW>), grid, dim3(256), 0, st, wl, wqh, wsc, wd, (int)n_rows,
+                               nsb, aq, ad, (int)m, out, ldo, sums, per, zstride, n_tw, n_tt, S);
+    } else if (q4k) {
         const int64_t nblk = n_rows * nsb;
         const uint4* wq = (const uint4*)w;
         const uint4* wh = (const uint4*)((const uint8_t*)w + nblk * 128);

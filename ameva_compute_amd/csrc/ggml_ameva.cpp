@@ -587,15 +587,16 @@ struct Engine {
     bool mul_mat(const ggml_tensor* n, const ggml_tensor* ep = nullptr) {
         const ggml_tensor *w = n->src[0], *x = n->src[1];
         const int64_t N = w->ne[1], K = w->ne[0], M = nrows(x);
-        // batched (M >= 8) MUL_MATs run on the matrix cores for Q4_0 / Q8_0 / Q4_K (the reference's switch at
+        // batched (M >= 8) MUL_MATs run on the matrix cores for Q4_0 / Q8_0 / Q4_K / Q6_K (the reference's switch at
         // AMEVA_QGEMM_MIN_M). Above 64 tokens the exact form (exact per-block integer sums, ggml's f32 epilogue: the
         // reference's MMQ arithmetic) reads the plain Q8_0 / Q8_K layout; Q4_K batches of 8..64 tokens read the f16
         // copies of AMV_ACT_Q8_K_MMA; AMEVA_MMQ_FORM=scaled selects the scaled layouts (f16 q * d) above 64 tokens
-        const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K);
+        const bool mmq = M >= 8 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K ||
+                                    w->type == GGML_TYPE_Q6_K);
         const bool kq = w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K;
-        const bool deq = mmq && M > 64 && mmq_scaled();
+        const bool deq = mmq && M > 64 && mmq_scaled() && w->type != GGML_TYPE_Q6_K;  // Q6_K: exact form only
         const int atype = deq ? (kq ? AMV_ACT_Q8_K_DEQ : AMV_ACT_Q8_0_DEQ)
-                        : (mmq && kq && M <= 64) ? AMV_ACT_Q8_K_MMA
+                        : (mmq && w->type == GGML_TYPE_Q4_K && M <= 64) ? AMV_ACT_Q8_K_MMA
                         : kq ? (int)GGML_TYPE_Q8_K : (int)GGML_TYPE_Q8_0;
         // src0 in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized tensor of any
         // other buffer is repacked into scratch for this use

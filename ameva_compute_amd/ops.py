@@ -144,7 +144,7 @@ def quantize_q4_0(x: torch.Tensor) -> torch.Tensor:
 # batch size from which MUL_MAT runs the int8-MFMA kernel (AMEVA_QGEMM_MIN_M of the reference, ggml-ameva.cpp:2486)
 MMQ_MIN_M = 8
 MMQ16_MIN_M = 64  # above this many tokens the tiled kernels run (amv_mmq.hip MMQ16_MIN_M)
-MMQ_TYPES = (Q4_0, Q8_0, Q4_K)  # Q4_K of MMQ_MIN_M..MMQ16_MIN_M tokens: the activations must be Q8_K_MMA
+MMQ_TYPES = (Q4_0, Q8_0, Q4_K, Q6_K)  # Q4_K of MMQ_MIN_M..MMQ16_MIN_M tokens: the activations must be Q8_K_MMA
 
 
 def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = None,

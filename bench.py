@@ -203,15 +203,16 @@ def secondary_gemvs(ops, torch, dev):
 
 
 def bench_batched(ops, torch, dev):
-    """Q4_0 / Q8_0 / Q4_K MUL_MAT at the Llama-3-8B FFN shapes with token batches 16 and 512 (the
-    int8 / f16 matrix-core kernels; at 512 the scaled form, the default, and the exact-integer-sum form), 2 M N K
-    ops per call."""
+    """Q4_0 / Q8_0 / Q4_K MUL_MAT at the Llama-3-8B FFN shapes with token batches 16 and 512, and
+    Q6_K (ffn_down / attn_v of Q4_K_M files): the exact form (exact per-block integers on the int8 matrix cores, the
+    default) and, at 512 tokens, the scaled f16 form (AMEVA_MMQ_FORM=scaled; not for Q6_K); 2 M N K ops per call."""
     res = {}
     g = torch.Generator(device=dev)
-    for wname, wtype in (("q4_0", ops.Q4_0), ("q8_0", ops.Q8_0), ("q4_K", ops.Q4_K)):
+    for wname, wtype in (("q4_0", ops.Q4_0), ("q8_0", ops.Q8_0), ("q4_K", ops.Q4_K), ("q6_K", ops.Q6_K)):
         for n, k in ((14336, 4096), (4096, 14336)):
             w = make_weights(ops, torch, n, k, 1, 300 + n, dev, wtype)[0]
-            for m, exact in ((16, False), (512, False), (512, True)):
+            forms = ((16, True), (512, True)) + (((512, False),) if wtype != ops.Q6_K else ())
+            for m, exact in forms:
                 g.manual_seed(m + n)
                 x = torch.randn((m, k), generator=g, device=dev)
                 at = ops.act_type(wtype, m, exact=exact)
@@ -220,7 +221,7 @@ def bench_batched(ops, torch, dev):
                 ms = time_steps_graph(torch, lambda i: ops.mul_mat_q(w, act, m, out, act_t=at),
                                       50 if m == 512 else 200, 10, per_graph=10)
                 tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-                key = f"{wname}_{n}x{k}_m{m}" + ("_exact" if exact else "")
+                key = f"{wname}_{n}x{k}_m{m}" + ("" if exact else "_scaled")
                 res[key + "_us"] = round(ms * 1e3, 2)
                 res[key + "_tops"] = round(tops, 1)
                 log(f"bench: {key} {ms * 1e3:.1f} us = {tops:.1f} TOPS ({tops / INT8_MFMA_PEAK_TOPS * 100:.1f}% of "

@@ -2,8 +2,8 @@
 
 * Config 2: Q4_0 / Q8_0 / Q4_K batched MUL_MAT at Llama-3-8B FFN shapes (14336 x 4096 gate/up, 4096 x 14336 down)
   for 16 and 512 tokens, both activation layouts of the tiled kernels (exact integer block sums, and the scaled
-  f16 form): the f32 result of every token on a sample of weight rows against the oracle (rows are independent, so
-  the sample is exact at the full shape), the Q8_0 / Q8_K activation bytes over the whole batch, and the per-block
+  f16 form), and Q6_K (the ffn_down / attn_v type of Q4_K_M files; exact form only): the f32 result of every token
+  on a sample of weight rows against the oracle (rows are independent, so the sample is exact at the full shape), the Q8_0 / Q8_K activation bytes over the whole batch, and the per-block
   int32 sums of the exact form on a 256-row slice of the weight at the full k and batch.
 * Config 5 pieces at 8B size: the Q6_K output head GEMV (128256 x 4096, block sums bit-exact, f32 within 1e-3), the
   Q4_K token-embedding GET_ROWS (bit-exact rows), one Q4_K Llama-3-8B decoder layer stage by stage against the
@@ -63,16 +63,16 @@ def sample_rows(n, count, seed):
 
 @pytest.mark.parametrize("m", [16, 512])
 @pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336)])
-@pytest.mark.parametrize("wt", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("wt", [Q4_0, Q8_0, Q4_K, Q6_K])
 def test_config2_batched_full_shape(dev, ops, orc, wt, shape, m):
     n, k = shape
     seed = wt * 1000 + n // 1024 + m
     wg, wq = weights(ops, orc, dev, wt, n, k, seed)
     x = np.random.default_rng(seed + 1).standard_normal((m, k), dtype=np.float32)
     xd = torch.from_numpy(x).to(dev)
-    base = Q8_K if wt == Q4_K else Q8_0
+    base = Q8_K if wt in (Q4_K, Q6_K) else Q8_0
     forms = [(ops.act_type(wt, m, exact=True), "exact")]
-    if m > ops.MMQ16_MIN_M:
+    if m > ops.MMQ16_MIN_M and wt != Q6_K:
         forms.append((ops.act_type(wt, m, exact=False), "scaled"))
     # activation bytes: the GPU quantizer's ggml blocks equal the oracle's over the whole batch
     a_ref = orc.quantize_q8_K(x) if base == Q8_K else orc.quantize_q8_0(x, orc.Q8_X86)

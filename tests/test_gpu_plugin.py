@@ -68,7 +68,7 @@ def test_mul_mat_node(plugin, orc, wt, m):
         y = g.get(Y, np.float32, (m, n))
         assert rel_l2(y, orc.mul_mat(wt, wg, n, k, aq(x), m)) < 1e-3
         assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 1
-        assert gp.counter(plugin, "mmq_mul_mat_count") == (1 if m >= 8 and wt in (gp.Q4_0, gp.Q8_0, gp.Q4_K) else 0)
+        assert gp.counter(plugin, "mmq_mul_mat_count") == (1 if m >= 8 else 0)
         assert gp.counter(plugin, "repacked_tensor_count") == rep0 + 1
         # the weight reads back in ggml layout, byte for byte
         assert np.array_equal(g.get(W, np.uint8), wg.reshape(-1))
@@ -85,7 +85,7 @@ def test_mul_mat_node(plugin, orc, wt, m):
 # [3, 3 + N) of a weight of N + 5 rows ("view"); its shapes: one-column GEMVs, small batches below and above the
 # MFMA crossover (M = 8), odd N and partial tiles, long rows, and K = 544 (17 blocks of 32, not whole K-quant
 # super-blocks).
-MMQ_PLUGIN_TYPES = (gp.Q4_0, gp.Q8_0, gp.Q4_K)  # weight types with a batched (M >= 8) matrix-core kernel
+MMQ_PLUGIN_TYPES = (gp.Q4_0, gp.Q8_0, gp.Q4_K, gp.Q6_K)  # weight types with a batched (M >= 8) matrix-core kernel
 QMM_SHAPES = [(1, 37, 256), (5, 64, 512), (8, 16, 256), (13, 33, 768), (1, 70, 2560), (3, 19, 4096), (40, 70, 512),
               (33, 130, 256), (1, 21, 544)]
 
