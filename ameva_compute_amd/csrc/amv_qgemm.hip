@@ -239,59 +239,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 // unit 2c + 1. Per super-block values (unit scales and mins, d, dmin, the activation sums per 16 and d_a) are staged
 // at its chunk 0 into a slot of their own, double-buffered by super-block parity.
 // ---------------------------------------------------------------------------------------------------------------
-// Per-step registers (weights and activations of one chunk) and per-super-block registers (head, activation sums,
-// d_a): the step registers run two steps ahead of the compute, the super-block registers one super-block ahead.
-struct QgKStep {
+struct QgKRegs {
     uint4 q;       // weight bytes 16 hf .. + 15 of the chunk (row t / 2, hf = t % 2)
+    uint4 hd;      // the row's 16-byte head (d, dmin, 12 scale bytes), at chunk 0
     uint4 a0, a1;  // 32 activation int8 (token t / 2, k 64 c + 32 hf ..)
-};
-struct QgKSb {
-    uint4 hd;   // the row's 16-byte head (d, dmin, 12 scale bytes)
-    int s[8];   // the token's sums per 16, 8 hf .. 8 hf + 7
-    float da;   // the token's super-block scale
+    int s[8];      // at chunk 0: the token's sums per 16, 8 hf .. 8 hf + 7
+    float da;      // at chunk 0: the token's super-block scale
 };
 
 template <int TT, int TW>
-__device__ __forceinline__ QgKStep qgk_load_step(int step, const uint4* __restrict__ wq, int N, int nsb, int n0,
-                                                 const int8_t* __restrict__ aq, int M, int m0, int K, int sb0) {
+__device__ __forceinline__ void qgk_load(QgKRegs& s, int step, const uint4* __restrict__ wq,
+                                         const uint4* __restrict__ wh, int N, int nsb, int n0,
+                                         const int8_t* __restrict__ aq, const float* __restrict__ ad,
+                                         const int32_t* __restrict__ as16, int M, int m0, int K, int sb0) {
     constexpr int BN = 64 * TW, BM = 64 * TT;
     const int t = threadIdx.x, hf = t & 1;
     const int j = sb0 + (step >> 2), c = step & 3;
-    QgKStep s;
-    s.q = s.a0 = s.a1 = make_uint4(0, 0, 0, 0);
-    if (wq && t < 2 * BN) {
+    if (t < 2 * BN) {
         const int row = min(n0 + (t >> 1), N - 1);
-        s.q = wq[((size_t)row * nsb + j) * 8 + 2 * c + hf];
+        const size_t sb = (size_t)row * nsb + j;
+        s.q = wq[sb * 8 + 2 * c + hf];
+        if (c == 0) s.hd = wh[sb];
     }
-    if (aq && t < 2 * BM) {
+    if (t < 2 * BM) {
         const int tok = min(m0 + (t >> 1), M - 1);
         const uint4* p = reinterpret_cast<const uint4*>(aq + (size_t)tok * K + 256 * j + 64 * c + 32 * hf);
         s.a0 = p[0];
         s.a1 = p[1];
-    }
-    return s;
-}
-
-template <int TT, int TW>
-__device__ __forceinline__ QgKSb qgk_load_sb(int j, const uint4* __restrict__ wh, int N, int nsb, int n0,
-                                             const float* __restrict__ ad, const int32_t* __restrict__ as16, int M,
-                                             int m0, int K) {
-    constexpr int BN = 64 * TW, BM = 64 * TT;
-    const int t = threadIdx.x, hf = t & 1;
-    QgKSb s;
-    s.hd = make_uint4(0, 0, 0, 0);
+        if (c == 0) {
+            const int32_t* q = as16 + (size_t)tok * (K / 16) + 16 * j + 8 * hf;  // 4-byte aligned only
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s.s[e] = 0;
-    s.da = 0.0f;
-    if (t < 2 * BN) s.hd = wh[(size_t)min(n0 + (t >> 1), N - 1) * nsb + j];
-    if (t < 2 * BM) {
-        const int tok = min(m0 + (t >> 1), M - 1);
-        const int32_t* q = as16 + (size_t)tok * (K / 16) + 16 * j + 8 * hf;  // 4-byte aligned only
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s.s[e] = q[e];
-        s.da = ad[(size_t)tok * nsb + j];
+            for (int e = 0; e < 8; ++e) s.s[e] = q[e];
+            s.da = ad[(size_t)tok * nsb + j];
+        }
     }
-    return s;
 }
 
 __device__ __forceinline__ uint32_t qg_h2(int a, int b) {
@@ -300,50 +281,45 @@ __device__ __forceinline__ uint32_t qg_h2(int a, int b) {
 }
 
 template <int TT, int TW>
-__device__ __forceinline__ void qgk_store_step(const QgKStep& s, int8_t* __restrict__ sW, int8_t* __restrict__ sA) {
+__device__ __forceinline__ void qgk_store(const QgKRegs& s, int step, int8_t* __restrict__ sW,
+                                          int8_t* __restrict__ sA, uint8_t* __restrict__ sSc,
+                                          float* __restrict__ sD, float* __restrict__ sDm, uint16_t* __restrict__ sMn,
+                                          uint16_t* __restrict__ sBs, float* __restrict__ sDa) {
     constexpr int BN = 64 * TW, BM = 64 * TT;
-    const int t = threadIdx.x, hf = t & 1;
+    const int t = threadIdx.x, hf = t & 1, c = step & 3;
     if (t < 2 * BN) {
-        uint4* d = reinterpret_cast<uint4*>(sW + (t >> 1) * QG_LD);
+        const int rl = t >> 1;
+        uint4* d = reinterpret_cast<uint4*>(sW + rl * QG_LD);
         const uint4 x = s.q;  // unit 2c: low nibbles (elements 16 hf ..), unit 2c + 1: high nibbles
         d[hf] = make_uint4(x.x & 0x0F0F0F0Fu, x.y & 0x0F0F0F0Fu, x.z & 0x0F0F0F0Fu, x.w & 0x0F0F0F0Fu);
         d[2 + hf] = make_uint4((x.x >> 4) & 0x0F0F0F0Fu, (x.y >> 4) & 0x0F0F0F0Fu, (x.z >> 4) & 0x0F0F0F0Fu,
                                (x.w >> 4) & 0x0F0F0F0Fu);
+        if (c == 0) {  // units 4 hf .. 4 hf + 3: scales (bytes) and mins (f16, on the two 16-sum slots of each unit)
+            uint32_t mm[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                int sc, mn;
+                k4_scale_min(4 * hf + e, s.hd.y, s.hd.z, s.hd.w, sc, mn);
+                sSc[(4 * hf + e) * BN + rl] = (uint8_t)sc;
+                mm[e] = qg_h2(mn, mn);
+            }
+            *reinterpret_cast<uint4*>(sMn + rl * 16 + 8 * hf) = make_uint4(mm[0], mm[1], mm[2], mm[3]);
+            if (hf == 0) {
+                sD[rl] = amv_h2f(s.hd.x);
+                sDm[rl] = amv_h2f(s.hd.x >> 16);
+            }
+        }
     }
     if (t < 2 * BM) {
-        uint4* d = reinterpret_cast<uint4*>(sA + (t >> 1) * QG_LD + 32 * hf);
+        const int tl = t >> 1;
+        uint4* d = reinterpret_cast<uint4*>(sA + tl * QG_LD + 32 * hf);
         d[0] = s.a0;
         d[1] = s.a1;
-    }
-}
-
-template <int TT, int TW>
-__device__ __forceinline__ void qgk_store_sb(const QgKSb& s, uint8_t* __restrict__ sSc, float* __restrict__ sD,
-                                             float* __restrict__ sDm, uint16_t* __restrict__ sMn,
-                                             uint16_t* __restrict__ sBs, float* __restrict__ sDa) {
-    constexpr int BN = 64 * TW, BM = 64 * TT;
-    const int t = threadIdx.x, hf = t & 1;
-    if (t < 2 * BN) {  // units 4 hf .. 4 hf + 3: scales (bytes) and mins (f16, on the two 16-sum slots of each unit)
-        const int rl = t >> 1;
-        uint32_t mm[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            int sc, mn;
-            k4_scale_min(4 * hf + e, s.hd.y, s.hd.z, s.hd.w, sc, mn);
-            sSc[(4 * hf + e) * BN + rl] = (uint8_t)sc;
-            mm[e] = qg_h2(mn, mn);
+        if (c == 0) {  // the 16-sums as f16 (|sum| <= 2032: exact)
+            *reinterpret_cast<uint4*>(sBs + tl * 16 + 8 * hf) =
+                make_uint4(qg_h2(s.s[0], s.s[1]), qg_h2(s.s[2], s.s[3]), qg_h2(s.s[4], s.s[5]), qg_h2(s.s[6], s.s[7]));
+            if (hf == 0) sDa[tl] = s.da;
         }
-        *reinterpret_cast<uint4*>(sMn + rl * 16 + 8 * hf) = make_uint4(mm[0], mm[1], mm[2], mm[3]);
-        if (hf == 0) {
-            sD[rl] = amv_h2f(s.hd.x);
-            sDm[rl] = amv_h2f(s.hd.x >> 16);
-        }
-    }
-    if (t < 2 * BM) {  // the 16-sums as f16 (|sum| <= 2032: exact)
-        const int tl = t >> 1;
-        *reinterpret_cast<uint4*>(sBs + tl * 16 + 8 * hf) =
-            make_uint4(qg_h2(s.s[0], s.s[1]), qg_h2(s.s[2], s.s[3]), qg_h2(s.s[4], s.s[5]), qg_h2(s.s[6], s.s[7]));
-        if (hf == 0) sDa[tl] = s.da;
     }
 }
 
@@ -366,7 +342,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int n0 = tw * BN, m0 = tt * BM;
     const int K = nsb * 256;
     const int sb0 = z * sb_per, sb_end = min(nsb, sb0 + sb_per);
-    const int nsbl = sb_end - sb0, nsteps = nsbl * 4;
+    const int nsteps = (sb_end - sb0) * 4;
     dst += (size_t)z * zstride;
 
     qg_f16v acc[TT][TW];
@@ -381,10 +357,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 I1[i][j][r] = 0;
             }
 
-    // units 2c, 2c + 1 of the chunk in LDS buffer buf; at c == 3 the super-block's fold (per-super-block slot jp)
-    const auto compute = [&](int buf, int c, int jp, int j) {
+    QgKRegs st;
+    qgk_load<TT, TW>(st, 0, wq, wh, N, nsb, n0, aq, ad, as16, M, m0, K, sb0);
+    qgk_store<TT, TW>(st, 0, sW[0], sA[0], sSc[0], sD[0], sDm[0], sMn[0], sBs[0], sDa[0]);
+    __syncthreads();
+    for (int step = 0; step < nsteps; ++step) {
+        const int buf = step & 1, j = sb0 + (step >> 2), c = step & 3, jp = (step >> 2) & 1;
+        if (step + 1 < nsteps) qgk_load<TT, TW>(st, step + 1, wq, wh, N, nsb, n0, aq, ad, as16, M, m0, K, sb0);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < 2; ++u) {  // unit 2c + u
             qg_v4i A[TT], B[TW];
             int sc[TW];
 #pragma unroll
@@ -450,35 +431,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 }
             }
         }
-    };
-
-    // the weight chunk (from HBM) two steps ahead, the activations (L2 hits) one step ahead
-    QgKStep rs = qgk_load_step<TT, TW>(0, wq, N, nsb, n0, aq, M, m0, K, sb0);
-    QgKSb sbr = qgk_load_sb<TT, TW>(sb0, wh, N, nsb, n0, ad, as16, M, m0, K);
-    qgk_store_step<TT, TW>(rs, sW[0], sA[0]);
-    qgk_store_sb<TT, TW>(sbr, sSc[0], sD[0], sDm[0], sMn[0], sBs[0], sDa[0]);
-    uint4 wn = make_uint4(0, 0, 0, 0);  // weight bytes of step + 2
-    if (nsteps > 1) rs.q = qgk_load_step<TT, TW>(1, wq, N, nsb, n0, nullptr, M, m0, K, sb0).q;
-    __syncthreads();
-#pragma unroll 1
-    for (int step = 0; step < nsteps; ++step) {
-        const int buf = step & 1, p = step >> 2, c = step & 3, j = sb0 + p, jp = p & 1;
-        // the super-block after this one: its head and activation sums, at its last step
-        if (c == 3 && p + 1 < nsbl) sbr = qgk_load_sb<TT, TW>(j + 1, wh, N, nsb, n0, ad, as16, M, m0, K);
-        if (step + 2 < nsteps) wn = qgk_load_step<TT, TW>(step + 2, wq, N, nsb, n0, nullptr, M, m0, K, sb0).q;
         if (step + 1 < nsteps) {
-            const QgKStep a = qgk_load_step<TT, TW>(step + 1, nullptr, N, nsb, n0, aq, M, m0, K, sb0);
-            rs.a0 = a.a0;
-            rs.a1 = a.a1;
-        }
-        compute(buf, c, jp, j);
-        if (step + 1 < nsteps) {
-            qgk_store_step<TT, TW>(rs, sW[buf ^ 1], sA[buf ^ 1]);
-            if (c == 3)
-                qgk_store_sb<TT, TW>(sbr, sSc[jp ^ 1], sD[jp ^ 1], sDm[jp ^ 1], sMn[jp ^ 1], sBs[jp ^ 1], sDa[jp ^ 1]);
+            const int sp = ((step + 1) >> 2) & 1;
+            qgk_store<TT, TW>(st, step + 1, sW[buf ^ 1], sA[buf ^ 1], sSc[sp], sD[sp], sDm[sp], sMn[sp], sBs[sp],
+                              sDa[sp]);
             __syncthreads();
         }
-        rs.q = wn;
     }
     if constexpr (!SUMS) {
 #pragma unroll
