@@ -5,167 +5,261 @@
 // before the dot with the f16 K; so does this one. Scores, softmax and accumulators are f32; the probabilities enter
 // the P V product as f16 (the CPU accumulates V in f16 instead).
 //
-// One workgroup of 4 waves per (head, 64 consecutive queries); wave w owns queries 16 w .. 16 w + 15 of the tile and
-// runs flash attention over blocks of 64 keys with v_mfma_f32_16x16x16f16:
-//   S^T (16 keys x 16 queries) = K (16 keys x 128) . Q^T, accumulated over 8 steps of 16 dims. The reduction order
-//   of the dims is free, so lane group g takes dims 32 j + 8 g .. + 7 of both K and Q for steps 2 j, 2 j + 1: every
-//   lane reads 16 contiguous bytes of its K row. In the result lane (g, c) holds S[query c][keys 4 g .. 4 g + 3].
-//   O^T (16 dims x 16 queries) += V^T (16 dims x 16 keys) . P^T: the P^T operand is exactly the S^T result layout,
-//   so the probabilities never move between lanes; V^T comes from LDS, where the workgroup stages the key block's
-//   V rows transposed ([dim][key]).
-// Online softmax per query: the block maximum over the lane's 16 scores and the 4 lanes of the query (xor 16, 32),
-// rescale of l and O by exp(m_old - m_new). Causal tiles stop at the last key their last query may see.
+// One workgroup of 4 waves per (head, 32 consecutive queries); the waves split the tile's blocks of 32 keys (wave w
+// takes blocks w, w + 4, ...: the last tile of a 512-token causal prompt runs 4 blocks per wave, not 16 in a row)
+// and merge their (m, l, O) through LDS at the end. Per block, each wave with v_mfma_f32_32x32x16_f16 (the full-rate
+// f16 shape of gfx950):
+//   S^T (32 keys x 32 queries) = K (32 keys x 128) . Q^T, 8 steps of 16 dims: lane l reads 16 contiguous bytes of
+//   key l % 32 from the wave's K rows in LDS, Q^T is held in registers as f16 for the whole kernel. In the result lane
+//   (c, h = l / 32) holds query c and keys 8 (r / 4) + 4 h + r % 4, r = 0..15.
+//   O^T (128 dims x 32 queries) += V^T . P^T, per 32-dim tile 2 steps of 16 keys. The k slots of a step are assigned
+//   so that P^T is exactly the lane's own S values (slots 0..3 = keys 16 s + 4 h + 0..3, slots 4..7 = keys
+//   16 s + 8 + 4 h + 0..3: r = 8 s .. 8 s + 7), and the V^T operand comes from the row-major V block in LDS through
+//   ds_read_b64_tr_b16: in each group of 16 lanes lane i receives element (4 e + i / 4, i % 4) of the 16 x 4 block the
+//   group addressed, so lanes pointing at (key k0 + j / 4, dims d0 + 4 (j % 4) .. + 3) give lane i dim d0 + i of keys
+//   k0 .. k0 + 3: two such reads are one operand, no transposed staging.
+// Each wave stages its own K and V rows: 16 lanes per 256-byte row, 4 rows per load instruction (the loads that
+// gather 16 or 32 bytes from 32 rows per instruction took half as long again), one block ahead of the one in use.
+// Online softmax per query over the 16 scores of the lane and of its partner lane l ^ 32; causal tiles stop at the
+// last key their last query may see, and the tiles with the most keys are launched first.
 #include "amv_common.h"
 
-#define FP_D 128
-#define FP_KB 64                 // keys per block
-#define FP_VT (FP_KB + 8)        // LDS row of V^T in halves (padded against bank conflicts)
+#define FQ_D 128
+#define FQ_KB 32            // keys per block
+#define FQ_LOG2E 1.4426950408889634f
+#define FQ_KLD (FQ_D + 8)   // K row stride in halves (272 bytes: the 16-byte fragment reads of 16 rows hit distinct banks)
+#define FQ_VLD (FQ_D + 16)  // V row stride in halves (288 bytes: the transposing reads of 4 rows hit distinct banks)
 
-typedef _Float16 fp_h4 __attribute__((ext_vector_type(4)));
-typedef float fp_f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 fq_h8 __attribute__((ext_vector_type(8)));
+typedef short fq_s4 __attribute__((ext_vector_type(4)));
+typedef float fq_f16v __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) fq_s4 fq_lds_s4;
 
-__device__ __forceinline__ fp_h4 fp_h4_of(uint32_t lo, uint32_t hi) {
-    const uint2 u = make_uint2(lo, hi);
-    return __builtin_bit_cast(fp_h4, u);
+// 8 halves for the V^T operand: dims d0 + i of keys k0 .. k0 + 3 and k0 + 8 .. k0 + 11 (lane i of its 16-lane group)
+__device__ __forceinline__ fq_h8 fq_vt(const uint16_t* vb, int k0, int d0, int j) {
+    const uint16_t* p = vb + (k0 + (j >> 2)) * FQ_VLD + d0 + 4 * (j & 3);
+    const fq_s4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fq_lds_s4*)(__attribute__((address_space(3))) uint16_t*)p);
+    const fq_s4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (fq_lds_s4*)(__attribute__((address_space(3))) uint16_t*)(p + 8 * FQ_VLD));
+    typedef short fq_s8 __attribute__((ext_vector_type(8)));
+    const fq_s8 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(fq_h8, ab);
 }
 
+// the value of lane l ^ 32 beside the lane's own (v_permlane32_swap: the upper half of the wave trades places with
+// the lower half of the copy), combined by max or sum: the same result in both lanes
+__device__ __forceinline__ float fq_max32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float fq_sum32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// orders one wave's LDS accesses at this point (no instruction: a wave's LDS operations already run in order)
+__device__ __forceinline__ void fq_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// rows key0 + 4 i (i = 0..7, clamped to the last key), 16 bytes from half col of each
+typedef unsigned int fq_u4 __attribute__((ext_vector_type(4)));
+struct FqRows {
+    fq_u4 r[8];
+};
+__device__ __forceinline__ FqRows fq_load_rows(const uint16_t* __restrict__ base, int64_t row, int key0, int col,
+                                               int n_kv) {
+    FqRows t;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        t.r[i] = *reinterpret_cast<const fq_u4*>(base + (int64_t)min(key0 + 4 * i, n_kv - 1) * row + col);
+    return t;
+}
+
+template <bool MASK>
 __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q, int64_t q_ts, int64_t q_hs,
                                                    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                    const uint16_t* __restrict__ mask, int64_t mask_stride,
                                                    float* __restrict__ out, int n_tok, int n_head, int G, int n_kv,
                                                    int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
                                                    float scale, int64_t pos0) {
-    __shared__ uint16_t vt[FP_D * FP_VT];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
-    const int h = blockIdx.y, hk = h / G;
-    const int qi = blockIdx.x * 64 + 16 * w + c;  // this lane's query (column of S^T and O^T)
-    const int qc = min(qi, n_tok - 1);
+    // per wave: the K and V rows of the block it works on; after the key loop sV holds the partials of the merge
+    __shared__ __align__(16) uint16_t sK[4][FQ_KB * FQ_KLD];
+    __shared__ __align__(16) uint16_t sV[4][FQ_KB * FQ_VLD];
+    const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wave (uniform: block loop and tests run scalar)
+    const int n_tiles = (int)gridDim.x;
+    const int q0 = (n_tiles - 1 - (int)blockIdx.x) * 32;  // the tiles with the most keys first
+    const int hq = (int)blockIdx.y, hk = hq / G;
+    const int qi = q0 + c, qc = min(qi, n_tok - 1);
 
-    // Q^T operand, f16: qb[2 j + e] = q[qi][32 j + 8 g + 4 e .. + 3]
-    fp_h4 qb[8];
+    // Q^T operand, f16: qb[s] = q[qi][16 s + 8 h .. + 7]
+    fq_h8 qb[8];
     {
-        const float* qr = q + (int64_t)qc * q_ts + (int64_t)h * q_hs;
+        const float* qr = q + (int64_t)qc * q_ts + (int64_t)hq * q_hs + 8 * h;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const float4 a = *reinterpret_cast<const float4*>(qr + 32 * j + 8 * g + 4 * e);
-                fp_h4 t;
-                t.x = (_Float16)a.x;
-                t.y = (_Float16)a.y;
-                t.z = (_Float16)a.z;
-                t.w = (_Float16)a.w;
-                qb[2 * j + e] = t;
-            }
+        for (int s = 0; s < 8; ++s) {
+            const float4 a = *reinterpret_cast<const float4*>(qr + 16 * s);
+            const float4 b = *reinterpret_cast<const float4*>(qr + 16 * s + 4);
+            qb[s] = fq_h8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                          (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
         }
     }
-    // keys this tile needs: up to the last key its last query may see
+    // keys this tile needs: up to the last key its last query may see; wave w takes blocks w, w + 4, ...
     int kend = n_kv;
-    if (pos0 >= 0) kend = (int)min((int64_t)kend, pos0 + min(blockIdx.x * 64 + 63, n_tok - 1) + 1);
-    const int nblk = (kend + FP_KB - 1) / FP_KB;
-    const int64_t qlim = pos0 >= 0 ? pos0 + qi : (int64_t)n_kv;  // last key this query may see (causal)
+    if (pos0 >= 0) kend = (int)min((int64_t)kend, pos0 + min(q0 + 31, n_tok - 1) + 1);
+    const int nblk = (kend + FQ_KB - 1) / FQ_KB;
+    // last key this query may see (causal limit and n_kv); keys below klim0 are visible to every query of the tile
+    const int qlim = (int)min(pos0 >= 0 ? pos0 + qi : (int64_t)n_kv, (int64_t)n_kv - 1);
+    const int klim0 = (int)min(pos0 >= 0 ? pos0 + q0 + 1 : (int64_t)n_kv, (int64_t)n_kv);
+    const float sl2 = scale * FQ_LOG2E;
 
     const uint16_t* kh = k + (int64_t)hk * k_head;
     const uint16_t* vh = v + (int64_t)hk * v_head;
-    float m = -INFINITY, l = 0.0f;
-    fp_f4 o[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] = fp_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint16_t* kb = sK[w];
+    uint16_t* vb = sV[w];
+    // K / V staging of a block by the wave alone: lane l moves rows l / 16 + 4 i (i = 0..7), dims 8 (l % 16) ..
+    const int srow = lane >> 4, scol = 8 * (lane & 15);
+    FqRows rk, rv;
 
-    for (int b = 0; b < nblk; ++b) {
-        const int kb0 = b * FP_KB;
-        // K rows of the block for the S^T operand (issued before the V staging)
-        uint4 kr[4][4];
+    float m = -INFINITY, l = 0.0f;
+    fq_f16v o[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint16_t* row = kh + (int64_t)min(kb0 + 16 * t + c, n_kv - 1) * k_row;
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) kr[t][j] = *reinterpret_cast<const uint4*>(row + 32 * j + 8 * g);
+        for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
+
+    const int j16 = lane & 15, g16 = lane >> 4;  // the transposing reads: lane index in its 16-lane group, the group
+    // The wave's next block is in flight while it works on the current one, loaded unconditionally (the last block
+    // again at the end: the addresses stay in bounds, the values go unused), so the loads of one iteration retire in
+    // issue order and no wait covers a prefetch.
+    const int kmax = n_kv - 1;
+    if (w < nblk) {
+        rk = fq_load_rows(kh, k_row, FQ_KB * w + srow, scol, n_kv);
+        rv = fq_load_rows(vh, v_row, FQ_KB * w + srow, scol, n_kv);
+    }
+    for (int b = w; b < nblk; b += 4) {
+        const int kb0 = FQ_KB * b, bn = min(b + 4, nblk - 1);
+        // this block's K and V rows into the wave's LDS, the K fragments back out (lane: key c, dims 16 st + 8 h ..)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            *reinterpret_cast<fq_u4*>(&kb[(srow + 4 * i) * FQ_KLD + scol]) = rk.r[i];
+            *reinterpret_cast<fq_u4*>(&vb[(srow + 4 * i) * FQ_VLD + scol]) = rv.r[i];
         }
-        // stage V^T of the block: thread (key kk = tid % 64, dims 8 s .. 8 s + 7), s = 4 it + tid / 64
-        __syncthreads();  // the previous block's readers are done
+        fq_wave_sync();
+        fq_h8 kf[8];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int kk = tid & 63, s8 = 8 * (4 * it + (tid >> 6));
-            const int key = kb0 + kk;
-            uint4 val = make_uint4(0u, 0u, 0u, 0u);
-            if (key < n_kv) val = *reinterpret_cast<const uint4*>(vh + (int64_t)key * v_row + s8);
-            const uint32_t wv[4] = {val.x, val.y, val.z, val.w};
+        for (int st = 0; st < 8; ++st) kf[st] = *reinterpret_cast<const fq_h8*>(&kb[c * FQ_KLD + 16 * st + 8 * h]);
+        float mk[16];
+        if (MASK) {
+            const uint16_t* mr = mask + (int64_t)qc * mask_stride;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vt[(s8 + 2 * e) * FP_VT + kk] = (uint16_t)(wv[e] & 0xFFFFu);
-                vt[(s8 + 2 * e + 1) * FP_VT + kk] = (uint16_t)(wv[e] >> 16);
-            }
+            for (int r = 0; r < 16; ++r) mk[r] = amv_h2f(mr[min(kb0 + 8 * (r >> 2) + 4 * h + (r & 3), kmax)]);
         }
-        // S^T = K Q^T for the 4 tiles of 16 keys
-        fp_f4 s[4];
+        rk = fq_load_rows(kh, k_row, FQ_KB * bn + srow, scol, n_kv);
+        rv = fq_load_rows(vh, v_row, FQ_KB * bn + srow, scol, n_kv);
+        // S^T = K Q^T
+        fq_f16v s;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            fp_f4 acc = fp_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(fp_h4_of(kr[t][j].x, kr[t][j].y), qb[2 * j], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(fp_h4_of(kr[t][j].z, kr[t][j].w), qb[2 * j + 1], acc, 0,
-                                                            0, 0);
-            }
-            s[t] = acc;  // s[t][i] = S[query qi][key kb0 + 16 t + 4 g + i]
-        }
-        // scale, mask, causal limit; block maximum per query
+        for (int st = 0; st < 8; ++st) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[st], qb[st], s, 0, 0, 0);
+        // scores in log2 units (scale * log2 e folded in), the mask added, keys past the causal limit or n_kv at
+        // -inf; blocks wholly inside every query's limit (most blocks of a causal prompt) skip the key tests
+        const bool full = kb0 + FQ_KB <= klim0;
         float mx = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kb0 + 16 * t + 4 * g + i;
-                float x = s[t][i] * scale;
-                if (mask) x += amv_h2f(mask[(int64_t)qc * mask_stride + min(key, n_kv - 1)]);
-                if (key >= n_kv || key > qlim) x = -INFINITY;
-                s[t][i] = x;
-                mx = fmaxf(mx, x);
+        for (int r = 0; r < 16; ++r) {
+            float x = MASK ? (s[r] * scale + mk[r]) * FQ_LOG2E : s[r] * sl2;
+            if (!full) {
+                const int key = kb0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (key > qlim) x = -INFINITY;
             }
+            s[r] = x;
+            mx = fmaxf(mx, x);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, AMV_WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, AMV_WAVE));
-        const float m_new = fmaxf(m, mx);
-        const bool none = m_new == -INFINITY;  // nothing visible yet for this query
-        const float alpha = none ? 1.0f : expf(m - m_new);
+        mx = fq_max32(mx);  // the query's maximum over the block's 32 keys
+        // The running maximum moves only when a block exceeds it by more than 8 (a factor 256): until then the
+        // exponentials stay below 256 (exact enough in f16 for P, the sums are f32) and the accumulators need no
+        // rescaling, which most blocks then skip as a whole wave.
+        const bool grow = mx > m + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float alpha = grow ? (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mx)) : 1.0f;
+            if (grow) m = mx;
+            l *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        }
+        const float mref = m == -INFINITY ? 0.0f : m;  // nothing visible yet: every score is -inf, every weight 0
         float rs = 0.0f;
-        fp_h4 p[4];
+        fq_h8 p0, p1;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            fp_h4 pt;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float e = none ? 0.0f : expf(s[t][i] - m_new);
-                rs += e;
-                pt[i] = (_Float16)e;
-            }
-            p[t] = pt;
+        for (int r = 0; r < 16; ++r) {
+            const float e = __builtin_amdgcn_exp2f(s[r] - mref);
+            rs += e;
+            if (r < 8) p0[r] = (_Float16)e;
+            else p1[r - 8] = (_Float16)e;
         }
-        rs += __shfl_xor(rs, 16, AMV_WAVE);
-        rs += __shfl_xor(rs, 32, AMV_WAVE);
-        l = l * alpha + rs;
-        m = m_new;
+        l += fq_sum32(rs);
+        // O^T += V^T P^T (the V rows were written by this wave before the fence: LDS operations of one wave complete in
+        // order)
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-        __syncthreads();  // V^T staged
-        // O^T += V^T P^T
+        for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const fp_h4 a = *reinterpret_cast<const fp_h4*>(vt + (16 * dt + c) * FP_VT + 16 * t + 4 * g);
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, p[t], o[dt], 0, 0, 0);
+            for (int ks = 0; ks < 2; ++ks) {
+                const fq_h8 a = fq_vt(vb, 16 * ks + 4 * (g16 >> 1), 32 * dt + 16 * (g16 & 1), j16);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ks ? p1 : p0, o[dt], 0, 0, 0);
             }
         }
+        fq_wave_sync();  // the K / V reads stay before the next block's writes
     }
-    if (qi < n_tok) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float* orow = out + ((int64_t)qi * n_head + h) * FP_D;
+    // merge the four waves' partials (m, l, O^T; lane for lane the same query and dims): waves 2, 3 into 0, 1, then
+    // 1 into 0, through the LDS of the V blocks
+    float* mg = reinterpret_cast<float*>(&sV[0][0]);  // [2][66][64]: O^T values, m, l of one wave per slot
+    const auto put = [&](int slot) {
+        float* d = mg + slot * 66 * 64 + lane;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *reinterpret_cast<float4*>(orow + 16 * dt + 4 * g) =
-                make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) d[(16 * dt + r) * 64] = o[dt][r];
+        d[64 * 64] = m;
+        d[65 * 64] = l;
+    };
+    const auto take = [&](int slot) {
+        const float* d = mg + slot * 66 * 64 + lane;
+        const float mb = d[64 * 64], lb = d[65 * 64];
+        const float M = fmaxf(m, mb);
+        if (M == -INFINITY) return;
+        const float fa = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M),
+                    fb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - M);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * fa + d[(16 * dt + r) * 64] * fb;
+        l = l * fa + lb * fb;
+        m = M;
+    };
+    __syncthreads();  // every wave is done with its K / V rows
+    if (w >= 2) put(w - 2);
+    __syncthreads();
+    if (w < 2) take(w);
+    __syncthreads();
+    if (w == 1) put(0);
+    __syncthreads();
+    if (w == 0) {
+        take(0);
+        if (qi < n_tok) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            float* orow = out + ((int64_t)qi * n_head + hq) * FQ_D;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                    *reinterpret_cast<float4*>(orow + 32 * dt + 8 * q4 + 4 * h) =
+                        make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv, o[dt][4 * q4 + 2] * inv,
+                                    o[dt][4 * q4 + 3] * inv);
+        }
     }
 }
 
@@ -175,7 +269,7 @@ extern "C" int amv_flash_attn_prefill(const float* q, int64_t q_tok_stride, int6
                                       int64_t k_head, int64_t v_row, int64_t v_head, float scale, int64_t causal_pos0,
                                       void* stream) {
     AMV_REQUIRE(q && k && v && out, "amv_flash_attn_prefill: null pointer");
-    AMV_REQUIRE(D == FP_D, "amv_flash_attn_prefill: head size %lld not supported (128 is)", (long long)D);
+    AMV_REQUIRE(D == FQ_D, "amv_flash_attn_prefill: head size %lld not supported (128 is)", (long long)D);
     AMV_REQUIRE(n_tok > 0 && n_kv > 0 && n_head > 0 && n_head_kv > 0 && n_head % n_head_kv == 0,
                 "amv_flash_attn_prefill: bad shape");
     AMV_REQUIRE(n_tok <= (int64_t)1 << 24 && n_kv <= (int64_t)1 << 24 && n_head <= 65535,
@@ -188,8 +282,8 @@ extern "C" int amv_flash_attn_prefill(const float* q, int64_t q_tok_stride, int6
     AMV_REQUIRE(((uintptr_t)out & 15) == 0, "amv_flash_attn_prefill: out must be 16-byte aligned");
     AMV_REQUIRE(mask == nullptr || mask_stride >= n_kv, "amv_flash_attn_prefill: mask stride %lld < n_kv",
                 (long long)mask_stride);
-    const dim3 grid((unsigned)((n_tok + 63) / 64), (unsigned)n_head);
-    hipLaunchKernelGGL(k_fa_prefill, grid, dim3(256), 0, amv_stream(stream), q, q_tok_stride, q_head_stride,
+    const dim3 grid((unsigned)((n_tok + 31) / 32), (unsigned)n_head);
+    hipLaunchKernelGGL(mask ? k_fa_prefill<true> : k_fa_prefill<false>, grid, dim3(256), 0, amv_stream(stream), q, q_tok_stride, q_head_stride,
                        (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)mask, mask_stride, out, (int)n_tok,
                        (int)n_head, (int)(n_head / n_head_kv), (int)n_kv, k_row, k_head, v_row, v_head, scale,
                        causal_pos0);

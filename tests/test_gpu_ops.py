@@ -371,6 +371,7 @@ def test_rope_kv_store_bad_index(dev, ops):
     (100, 8, 2, 300, 200, "token"),     # chunk of a longer prompt (tail tile, keys before the chunk)
     (64, 8, 1, 1000, -1, "head"),       # no causal limit, GQA 8, head-major cache
     (1, 4, 4, 1, 0, "head"),            # one token
+    (45, 8, 4, 45, 0, "token"),         # GQA 2 (waves past the group's heads idle), partial tiles
 ])
 def test_flash_attn_prefill(dev, ops, orc, n_tok, n_head, n_head_kv, n_kv, pos0, layout):
     rng = np.random.default_rng(n_tok + n_kv)
