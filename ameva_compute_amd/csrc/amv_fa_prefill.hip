@@ -33,6 +33,7 @@
 typedef _Float16 fq_h8 __attribute__((ext_vector_type(8)));
 typedef short fq_s4 __attribute__((ext_vector_type(4)));
 typedef float fq_f16v __attribute__((ext_vector_type(16)));
+typedef float fq_f4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) fq_s4 fq_lds_s4;
 
 // 8 halves for the V^T operand: dims d0 + i of keys k0 .. k0 + 3 and k0 + 8 .. k0 + 11 (lane i of its 16-lane group)
@@ -84,9 +85,8 @@ __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q,
                                                    float* __restrict__ out, int n_tok, int n_head, int G, int n_kv,
                                                    int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
                                                    float scale, int64_t pos0) {
-    // per wave: the K and V rows of the block it works on; after the key loop sV holds the partials of the merge
-    __shared__ __align__(16) uint16_t sK[4][FQ_KB * FQ_KLD];
-    __shared__ __align__(16) uint16_t sV[4][FQ_KB * FQ_VLD];
+    // per wave the K and V rows of the block it works on; after the key loop the partials of the merge
+    __shared__ __align__(16) uint16_t lds[4 * FQ_KB * (FQ_KLD + FQ_VLD)];
     const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wave (uniform: block loop and tests run scalar)
     const int n_tiles = (int)gridDim.x;
@@ -94,16 +94,14 @@ __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q,
     const int hq = (int)blockIdx.y, hk = hq / G;
     const int qi = q0 + c, qc = min(qi, n_tok - 1);
 
-    // Q^T operand, f16: qb[s] = q[qi][16 s + 8 h .. + 7]
-    fq_h8 qb[8];
+    // the query rows: loads first, converted to the f16 Q^T operand once the first K / V block is in flight
+    fq_f4 qa[16];  // q[qi][16 s + 8 h .. + 7] = qa[2 s], qa[2 s + 1]
     {
         const float* qr = q + (int64_t)qc * q_ts + (int64_t)hq * q_hs + 8 * h;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const float4 a = *reinterpret_cast<const float4*>(qr + 16 * s);
-            const float4 b = *reinterpret_cast<const float4*>(qr + 16 * s + 4);
-            qb[s] = fq_h8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
-                          (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+            qa[2 * s] = *reinterpret_cast<const fq_f4*>(qr + 16 * s);
+            qa[2 * s + 1] = *reinterpret_cast<const fq_f4*>(qr + 16 * s + 4);
         }
     }
     // keys this tile needs: up to the last key its last query may see; wave w takes blocks w, w + 4, ...
@@ -117,8 +115,8 @@ __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q,
 
     const uint16_t* kh = k + (int64_t)hk * k_head;
     const uint16_t* vh = v + (int64_t)hk * v_head;
-    uint16_t* kb = sK[w];
-    uint16_t* vb = sV[w];
+    uint16_t* kb = lds + w * FQ_KB * (FQ_KLD + FQ_VLD);
+    uint16_t* vb = kb + FQ_KB * FQ_KLD;
     // K / V staging of a block by the wave alone: lane l moves rows l / 16 + 4 i (i = 0..7), dims 8 (l % 16) ..
     const int srow = lane >> 4, scol = 8 * (lane & 15);
     FqRows rk, rv;
@@ -138,6 +136,13 @@ __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q,
     if (w < nblk) {
         rk = fq_load_rows(kh, k_row, FQ_KB * w + srow, scol, n_kv);
         rv = fq_load_rows(vh, v_row, FQ_KB * w + srow, scol, n_kv);
+    }
+    fq_h8 qb[8];  // Q^T operand: qb[s] = q[qi][16 s + 8 h .. + 7] as f16
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const fq_f4 a = qa[2 * s], b = qa[2 * s + 1];
+        qb[s] = fq_h8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                      (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
     }
     for (int b = w; b < nblk; b += 4) {
         const int kb0 = FQ_KB * b, bn = min(b + 4, nblk - 1);
@@ -214,52 +219,40 @@ __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q,
         }
         fq_wave_sync();  // the K / V reads stay before the next block's writes
     }
-    // merge the four waves' partials (m, l, O^T; lane for lane the same query and dims): waves 2, 3 into 0, 1, then
-    // 1 into 0, through the LDS of the V blocks
-    float* mg = reinterpret_cast<float*>(&sV[0][0]);  // [2][66][64]: O^T values, m, l of one wave per slot
-    const auto put = [&](int slot) {
-        float* d = mg + slot * 66 * 64 + lane;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) d[(16 * dt + r) * 64] = o[dt][r];
-        d[64 * 64] = m;
-        d[65 * 64] = l;
-    };
-    const auto take = [&](int slot) {
-        const float* d = mg + slot * 66 * 64 + lane;
-        const float mb = d[64 * 64], lb = d[65 * 64];
-        const float M = fmaxf(m, mb);
-        if (M == -INFINITY) return;
-        const float fa = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M),
-                    fb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - M);
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * fa + d[(16 * dt + r) * 64] * fb;
-        l = l * fa + lb * fb;
-        m = M;
-    };
+    // merge: every wave leaves its (m, l, O^T) in LDS, then wave w combines dims 32 w .. 32 w + 31 of the tile's
+    // queries over the four waves (lane for lane the same query and dims) and writes them
     __syncthreads();  // every wave is done with its K / V rows
-    if (w >= 2) put(w - 2);
-    __syncthreads();
-    if (w < 2) take(w);
-    __syncthreads();
-    if (w == 1) put(0);
-    __syncthreads();
-    if (w == 0) {
-        take(0);
-        if (qi < n_tok) {
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            float* orow = out + ((int64_t)qi * n_head + hq) * FQ_D;
+    fq_f4* mo = reinterpret_cast<fq_f4*>(lds);          // [wave][dt][q4][lane]: o[dt][4 q4 .. 4 q4 + 3]
+    float* mml = reinterpret_cast<float*>(lds) + 16384;  // [wave][m, l][lane]
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4)
-                    *reinterpret_cast<float4*>(orow + 32 * dt + 8 * q4 + 4 * h) =
-                        make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv, o[dt][4 * q4 + 2] * inv,
-                                    o[dt][4 * q4 + 3] * inv);
-        }
+        for (int q4 = 0; q4 < 4; ++q4)
+            mo[((w * 4 + dt) * 4 + q4) * 64 + lane] =
+                fq_f4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+    mml[2 * w * 64 + lane] = m;
+    mml[(2 * w + 1) * 64 + lane] = l;
+    __syncthreads();
+    float mj[4], M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        mj[j] = mml[2 * j * 64 + lane];
+        M = fmaxf(M, mj[j]);
+    }
+    float L = 0.0f;
+    fq_f4 acc[4] = {};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float f = mj[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj[j] - M);
+        L += mml[(2 * j + 1) * 64 + lane] * f;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) acc[q4] += mo[((j * 4 + w) * 4 + q4) * 64 + lane] * f;
+    }
+    if (qi < n_tok) {
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        float* orow = out + ((int64_t)qi * n_head + hq) * FQ_D + 32 * w + 4 * h;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) *reinterpret_cast<fq_f4*>(orow + 8 * q4) = acc[q4] * inv;
     }
 }
 
