@@ -72,13 +72,13 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
         const float M = amv_wave_max(m);
         float l = 0.0f;
         if (lane < ns) {
-            const float w = (m0 == -INFINITY) ? 0.0f : expf(m0 - M);
+            const float w = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
             sw[g * FA_MAX_NSPLIT + lane] = w;
             l = fmaf(l0, w, l);
         }
         for (int z = lane + 64; z < ns; z += 64) {
             const float mz = ph[(size_t)z * FA_PS];
-            const float w = (mz == -INFINITY) ? 0.0f : expf(mz - M);
+            const float w = (mz == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mz - M);
             sw[g * FA_MAX_NSPLIT + z] = w;
             l = fmaf(ph[(size_t)z * FA_PS + 1], w, l);
         }
@@ -253,6 +253,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
         uint32_t qq[G][2];
         float qd[G];
         int qsum[G];
+        amv_h2 qh[G][4];  // f16 cache: q as f16 pairs
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float4* qp = reinterpret_cast<const float4*>(q + (size_t)(hk * G + g) * FA_D + d8);
@@ -261,34 +262,39 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
 #pragma unroll
             for (int e = 0; e < 8; ++e) qv[g][e] = KT == FA_F16 ? amv_round_f16(t[e]) : t[e];
             if constexpr (KT == FA_Q8_0 || KT == FA_Q4_0) fa_quant_q(qv[g], qrule, qq[g], qd[g], qsum[g]);
+            if constexpr (KT == FA_F16)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qh[g][e] = amv_h2{(_Float16)qv[g][2 * e], (_Float16)qv[g][2 * e + 1]};
         }
         float s[U][G];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = kw0 + 4 * u + grp;
             const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
-            if constexpr (KT == FA_F16 || KT == FA_F32) {
-                float kf[8];
-                if constexpr (KT == FA_F32) {
-                    const uint4 x0 = kr[u].a, x1 = kr[u].b;
-                    const uint32_t kw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            if constexpr (KT == FA_F16) {
+                // q (rounded to f16) . k as 4 v_dot2_f32_f16 per head: the f16 products are exact in f32
+                const uint32_t kw[4] = {kr[u].a.x, kr[u].a.y, kr[u].a.z, kr[u].a.w};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) kf[e] = __uint_as_float(kw[e]);
-                } else {
-                    const uint32_t kw[4] = {kr[u].a.x, kr[u].a.y, kr[u].a.z, kr[u].a.w};
+                for (int g = 0; g < G; ++g) {
+                    float d = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kf[2 * e] = amv_h2f(kw[e] & 0xFFFFu);
-                        kf[2 * e + 1] = amv_h2f(kw[e] >> 16);
-                    }
+                    for (int e = 0; e < 4; ++e) d = __builtin_amdgcn_fdot2(__builtin_bit_cast(amv_h2, kw[e]), qh[g][e], d, false);
+                    d = amv_row16_sum(d);
+                    s[u][g] = (mk == -INFINITY) ? -INFINITY : (d * scale + mk) * AMV_LOG2E;
                 }
+            } else if constexpr (KT == FA_F32) {
+                float kf[8];
+                const uint4 x0 = kr[u].a, x1 = kr[u].b;
+                const uint32_t kw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) kf[e] = __uint_as_float(kw[e]);
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
                     float d = 0.0f;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
                     d = amv_row16_sum(d);
-                    s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
+                    s[u][g] = (mk == -INFINITY) ? -INFINITY : (d * scale + mk) * AMV_LOG2E;
                 }
             } else {
                 const uint2 kb = fa_bytes<KT>(kr[u].a, lane);
@@ -304,7 +310,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
                                     : KT == FA_Q8_0 ? (float)is * (dk * qd[g])
                                                     : ((float)is * dk) * qd[g];
                     const float d = amv_row16_sum(t);
-                    s[u][g] = (mk == -INFINITY) ? -INFINITY : d * scale + mk;
+                    s[u][g] = (mk == -INFINITY) ? -INFINITY : (d * scale + mk) * AMV_LOG2E;
                 }
             }
         }
@@ -314,18 +320,16 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
             float mm = s[0][g];
 #pragma unroll
             for (int u = 1; u < U; ++u) mm = fmaxf(mm, s[u][g]);
-            mm = fmaxf(mm, __shfl_xor(mm, 16, AMV_WAVE));
-            mm = fmaxf(mm, __shfl_xor(mm, 32, AMV_WAVE));
+            mm = amv_max_x32(amv_max_x16(mm));
             m[g] = mm;
             float ll = 0.0f;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const float p = (mm == -INFINITY) ? 0.0f : expf(s[u][g] - mm);
+                const float p = __builtin_amdgcn_exp2f(s[u][g] - (mm == -INFINITY ? 0.0f : mm));
                 s[u][g] = p;
                 ll += p;
             }
-            ll += __shfl_xor(ll, 16, AMV_WAVE);
-            ll += __shfl_xor(ll, 32, AMV_WAVE);
+            ll = amv_sum_x32(amv_sum_x16(ll));
             l[g] = ll;  // the 16 lanes of a group each counted their group's keys once: same total in every lane
         }
         float acc[G][8];
@@ -386,7 +390,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
             float a = 0.0f, L = 0.0f;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const float f = (sM[w][g] == -INFINITY) ? 0.0f : expf(sM[w][g] - M);
+                const float f = (sM[w][g] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sM[w][g] - M);
                 const float* sa = sbuf + ((w * 4) * G + g) * FA_D + d;
                 const float aw = (sa[0] + sa[G * FA_D]) + (sa[2 * G * FA_D] + sa[3 * G * FA_D]);
                 a = fmaf(aw, f, a);

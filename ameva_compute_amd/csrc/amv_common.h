@@ -162,6 +162,28 @@ __device__ __forceinline__ int amv_wave_sum_i(int v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, AMV_WAVE);
     return v;
 }
+#define AMV_LOG2E 1.4426950408889634f
+typedef _Float16 amv_h2 __attribute__((ext_vector_type(2)));  // scores kept in log2 units meet v_exp_f32 (2^x) directly
+
+// Reductions over the lane pairs l, l ^ 16 and l, l ^ 32 without LDS (v_permlane16_swap / v_permlane32_swap trade
+// the odd 16-lane rows / the upper half of the wave with the other copy): the same result in both lanes.
+__device__ __forceinline__ float amv_max_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float amv_sum_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float amv_max_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float amv_sum_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float amv_wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, AMV_WAVE));

@@ -47,17 +47,6 @@ __device__ __forceinline__ fq_h8 fq_vt(const uint16_t* vb, int k0, int d0, int j
     return __builtin_bit_cast(fq_h8, ab);
 }
 
-// the value of lane l ^ 32 beside the lane's own (v_permlane32_swap: the upper half of the wave trades places with
-// the lower half of the copy), combined by max or sum: the same result in both lanes
-__device__ __forceinline__ float fq_max32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float fq_sum32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // orders one wave's LDS accesses at this point (no instruction: a wave's LDS operations already run in order)
 __device__ __forceinline__ void fq_wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -184,7 +173,7 @@ __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q,
             s[r] = x;
             mx = fmaxf(mx, x);
         }
-        mx = fq_max32(mx);  // the query's maximum over the block's 32 keys
+        mx = amv_max_x32(mx);  // the query's maximum over the block's 32 keys
         // The running maximum moves only when a block exceeds it by more than 8 (a factor 256): until then the
         // exponentials stay below 256 (exact enough in f16 for P, the sums are f32) and the accumulators need no
         // rescaling, which most blocks then skip as a whole wave.
@@ -206,7 +195,7 @@ __global__ __launch_bounds__(256) void k_fa_prefill(const float* __restrict__ q,
             if (r < 8) p0[r] = (_Float16)e;
             else p1[r - 8] = (_Float16)e;
         }
-        l += fq_sum32(rs);
+        l += amv_sum_x32(rs);
         // O^T += V^T P^T (the V rows were written by this wave before the fence: LDS operations of one wave complete in
         // order)
 #pragma unroll

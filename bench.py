@@ -601,6 +601,7 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the 32-layer model figures")
     ap.add_argument("--only-bitnet", action="store_true", help="only the BitNet 2B engine decode figures")
     ap.add_argument("--only-load", action="store_true", help="only the weight load path figures (repack, upload)")
+    ap.add_argument("--only-kv", action="store_true", help="only the FA decode figures over the three KV caches")
     ap.add_argument("--pmc-gemm", action="store_true",
                     help="for rocprofv3 --pmc: 20 eager scaled Q4_K MUL_MATs at M = 512 on each FFN shape")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -641,6 +642,9 @@ def main():
         return
     if args.only_load:
         print(json.dumps(bench_load_path(ops, torch, dev)), flush=True)
+        return
+    if args.only_kv:
+        print(json.dumps(bench_kv_cache(ops, torch, dev)), flush=True)
         return
 
     log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")
