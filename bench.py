@@ -395,9 +395,9 @@ def pmc_probe(ops, torch, dev):
 
 
 def pmc_gemm(ops, torch, dev):
-    """Dispatches for the matrix-core counters: the scaled batched Q4_K MUL_MAT at M = 512 on the Llama-3-8B FFN
-    shapes (14336 x 4096, then 4096 x 14336, whose k is split: its launch is followed by k_splitk_sum), 20 eager
-    launches each over one weight."""
+    """Dispatches for the matrix-core counters: the default (exact, int8 MFMA) batched Q4_K MUL_MAT at M = 512 on the
+    Llama-3-8B FFN shapes (14336 x 4096, then 4096 x 14336, whose k is split: its launch is followed by
+    k_splitk_sum), 20 eager launches each over one weight."""
     res = {}
     g = torch.Generator(device=dev)
     for n, k in ((14336, 4096), (4096, 14336)):
@@ -603,7 +603,7 @@ def main():
     ap.add_argument("--only-load", action="store_true", help="only the weight load path figures (repack, upload)")
     ap.add_argument("--only-kv", action="store_true", help="only the FA decode figures over the three KV caches")
     ap.add_argument("--pmc-gemm", action="store_true",
-                    help="for rocprofv3 --pmc: 20 eager scaled Q4_K MUL_MATs at M = 512 on each FFN shape")
+                    help="for rocprofv3 --pmc: 20 eager exact Q4_K MUL_MATs at M = 512 on each FFN shape")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
