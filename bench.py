@@ -69,9 +69,11 @@ def time_steps(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps  # ms per step
 
 
-def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS):
+def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS, info=None):
     """fn(i) for i in 0..per_graph-1 captured once in a HIP graph; the graph is replayed so that K >= steps steps
-    run back to back with no host launch cost between kernels. Returns ms per step."""
+    run back to back with no host launch cost between kernels. Returns ms per step; info (a dict), when given,
+    receives the step counts that actually ran: 'timed' (replays x per_graph) and 'warmup' (the eager pass before
+    the capture plus the untimed replays)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -85,6 +87,9 @@ def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS):
             fn(i)
     reps = max(1, (steps + per_graph - 1) // per_graph)
     wreps = max(1, warmup // per_graph)
+    if info is not None:
+        info["timed"] = reps * per_graph
+        info["warmup"] = (1 + wreps) * per_graph
     ms = time_steps(torch, lambda i: graph.replay(), reps, wreps)
     del graph
     return ms / per_graph
@@ -661,7 +666,8 @@ def main():
     def step_hot(i):
         ops.mul_mat_q(ws[0], act, 1, out)
 
-    ms_cold = time_steps_graph(torch, step_cold, args.steps, args.warmup)
+    ran = {}
+    ms_cold = time_steps_graph(torch, step_cold, args.steps, args.warmup, info=ran)
     nbytes = gemv_bytes(N_ROWS, K)
     gbs = nbytes / (ms_cold * 1e-3) / 1e9
     log(f"bench: cold {ms_cold * 1e3:.2f} us/GEMV = {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
@@ -702,8 +708,8 @@ def main():
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": ran["timed"],
+        "warmup": ran["warmup"],
         "ms_per_step": round(ms_cold, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -712,7 +718,9 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights quantized on the GPU (ggml Q4_0 rule), N(0,1) activation",
         "config": {"workload": "Q4_0 GEMV 14336x4096 M=1 (Llama-3-8B FFN gate/up), Q8_0 activation, cold: "
                                f"{COPIES} rotating weight copies ({COPIES * N_ROWS * K * 18 // 32 / 2**20:.0f} MiB)",
-                   "n_rows": N_ROWS, "k": K, "m": 1, "weight_copies": COPIES, "timing": f"HIP graph of {GRAPH_STEPS} GEMV launches, replayed"},
+                   "n_rows": N_ROWS, "k": K, "m": 1, "weight_copies": COPIES, "timing": f"HIP graph of {GRAPH_STEPS} GEMV launches replayed {ran['timed'] // GRAPH_STEPS} times "
+                             f"(steps = GEMVs timed); warmup = {GRAPH_STEPS} eager GEMVs + "
+                             f"{ran['warmup'] // GRAPH_STEPS - 1} untimed replays"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic()},
         "extra": extra,
