@@ -95,32 +95,109 @@ def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS, info=None)
     return ms / per_graph
 
 
+def _cpu_q4_0_weights(rng, n, k):
+    """Random Q4_0 blocks (random nibbles, d = 0.01) of an n x k weight: the CPU baseline's timing does not depend on
+    the values, and random bytes avoid quantizing a 900 MB f32 matrix on the host."""
+    import numpy as np
+    w = np.frombuffer(rng.bytes(n * (k // 32) * 18), np.uint8).reshape(n, k // 32, 18).copy()
+    w[:, :, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+    return w.reshape(n, -1)
+
+
+def _timed(fn, seconds, min_runs=3):
+    import time as _t
+    fn()  # warm-up
+    n, t0 = 0, _t.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = _t.perf_counter() - t0
+        if el >= seconds and n >= min_runs:
+            return el / n, n, el
+
+
+def cpu_layer_decode(oracle, rng, seconds):
+    """One bs1 decode step of the Llama-3-8B Q4_0 layer at 4096 cached keys on the host cores: the GEMVs and the
+    attention on the AVX2 baseline kernels (oracle/cpu_simd.c), the O(4096)-element steps (RMS norm, Q8_0
+    quantization, RoPE, SwiGLU) on the oracle's C. Returns (s per token, steps, seconds)."""
+    import numpy as np
+    H, F, NH, NKV, D, CTX = 4096, 14336, 32, 8, 128, 4096
+    wqkv = _cpu_q4_0_weights(rng, (NH + 2 * NKV) * D, H)
+    wo = _cpu_q4_0_weights(rng, H, NH * D)
+    wgu = _cpu_q4_0_weights(rng, 2 * F, H)
+    wd = _cpu_q4_0_weights(rng, H, F)
+    kc = rng.standard_normal((CTX, NKV, D)).astype(np.float16)
+    vc = rng.standard_normal((CTX, NKV, D)).astype(np.float16)
+    nw = np.ones(H, np.float32)
+    x0 = rng.standard_normal(H).astype(np.float32)
+    pos = np.array([CTX - 1], np.int32)
+
+    def step():
+        y, o = oracle.rms_norm(x0[None, :], 1e-5, nw)
+        a = oracle.quantize_q8_0(o, oracle.Q8_X86)
+        qkv = oracle.simd_mul_mat_q4_0(wqkv, wqkv.shape[0], H, a, 1)[0]
+        q = oracle.rope(qkv[:NH * D].reshape(1, NH, D), pos, D)
+        k = oracle.rope(qkv[NH * D:(NH + NKV) * D].reshape(1, NKV, D), pos, D)
+        kc[CTX - 1] = k[0].astype(np.float16)
+        vc[CTX - 1] = qkv[(NH + NKV) * D:].reshape(NKV, D).astype(np.float16)
+        att = oracle.simd_flash_attn_decode(q[0], kc, vc, 1.0 / np.sqrt(D))
+        x1 = x0 + oracle.simd_mul_mat_q4_0(wo, H, NH * D, oracle.quantize_q8_0(att.reshape(1, -1), oracle.Q8_X86), 1)[0]
+        y, o = oracle.rms_norm(x1[None, :], 1e-5, nw)
+        gu = oracle.simd_mul_mat_q4_0(wgu, 2 * F, H, oracle.quantize_q8_0(o, oracle.Q8_X86), 1)[0]
+        h = oracle.swiglu(gu[:F], gu[F:])
+        return x1 + oracle.simd_mul_mat_q4_0(wd, H, F, oracle.quantize_q8_0(h[None, :], oracle.Q8_X86), 1)[0]
+
+    return _timed(step, seconds)
+
+
 def cpu_baseline(seconds: float = 10.0):
+    """The headline GEMV on the host cores (plus, beside it, the M = 512 GEMM and the layer decode step): ggml's AVX2
+    vec_dot_q4_0_q8_0 algorithm (oracle/cpu_simd.c, OpenMP) where the CPU has AVX2 / FMA / F16C, else the oracle's
+    scalar C. Each figure is timed for a bounded sample (about `seconds` of CPU work for the GEMV, a third of it for
+    each of the other two)."""
     import numpy as np
     import oracle
     rng = np.random.default_rng(1234)
-    w = (rng.standard_normal((N_ROWS, K)) * 0.02).astype(np.float32)
-    wq = oracle.quantize_q4_0(w)
-    del w
+    simd = oracle.cpu_simd() is not None
     x = rng.standard_normal((1, K)).astype(np.float32)
     aq = oracle.quantize_q8_0(x, oracle.Q8_X86)
-    oracle.mul_mat(oracle.Q4_0, wq, N_ROWS, K, aq, 1)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        oracle.mul_mat(oracle.Q4_0, wq, N_ROWS, K, aq, 1)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 3:
-            break
-    per = el / n
-    return {
+    if simd:
+        wq = _cpu_q4_0_weights(rng, N_ROWS, K)
+        out = np.empty((1, N_ROWS), np.float32)
+        per, n, el = _timed(lambda: oracle.simd_mul_mat_q4_0(wq, N_ROWS, K, aq, 1, out), seconds)
+        threads = oracle.cpu_simd().cpu_num_threads()
+        how = "ggml's AVX2 vec_dot_q4_0_q8_0 algorithm (oracle/cpu_simd.c, OpenMP)"
+    else:
+        w = (rng.standard_normal((N_ROWS, K)) * 0.02).astype(np.float32)
+        wq = oracle.quantize_q4_0(w)
+        del w
+        per, n, el = _timed(lambda: oracle.mul_mat(oracle.Q4_0, wq, N_ROWS, K, aq, 1), seconds)
+        threads = oracle.num_threads()
+        how = "oracle vec_dot_q4_0_q8_0 (scalar C, OpenMP; this CPU lacks AVX2 / FMA / F16C)"
+    res = {
         "value": round(gemv_bytes(N_ROWS, K) / per / 1e9, 3),
         "unit": "GB/s",
-        "cores": oracle.num_threads(),
+        "cores": threads,
         "kind": "port",
-        "sample": f"{n} Q4_0 GEMVs 14336x4096 (M=1) in {el:.1f} s, oracle vec_dot_q4_0_q8_0 (C, OpenMP), "
-                  f"{per * 1e3:.2f} ms each; host CPU: {cpu_model()}",
+        "sample": f"{n} Q4_0 GEMVs 14336x4096 (M=1) in {el:.1f} s, {how}, {per * 1e3:.3f} ms each; "
+                  f"host CPU: {cpu_model()}",
     }
+    if simd:
+        rows, m = 1792, 512  # a row slice of the 14336 x 4096 GEMM at 512 tokens
+        a5 = oracle.quantize_q8_0(rng.standard_normal((m, K)).astype(np.float32), oracle.Q8_X86)
+        w5 = np.ascontiguousarray(wq[:rows])
+        o5 = np.empty((m, rows), np.float32)
+        per5, n5, el5 = _timed(lambda: oracle.simd_mul_mat_q4_0(w5, rows, K, a5, m, o5), seconds / 3)
+        res["gemm_m512_gops"] = round(2.0 * rows * K * m / per5 / 1e9, 1)
+        res["gemm_sample"] = (f"{n5} Q4_0 x Q8_0 GEMMs of {rows} of the 14336 rows x 4096 x 512 tokens in {el5:.1f} s "
+                              f"({per5 * 1e3:.1f} ms each; the full 14336-row GEMM scales by 8)")
+        del wq, w5, a5, o5
+        perl, nl, ell = cpu_layer_decode(oracle, rng, seconds / 3)
+        res["layer_decode_tok_s"] = round(1.0 / perl, 2)
+        res["layer_decode_sample"] = (f"{nl} bs1 decode steps of one Llama-3-8B Q4_0 layer at 4096 cached keys in "
+                                      f"{ell:.1f} s ({perl * 1e3:.2f} ms each): GEMVs and attention on "
+                                      f"oracle/cpu_simd.c, norms / quantization / RoPE / SwiGLU on the oracle's C")
+    return res
 
 
 def bench_layer(torch, dev, args):

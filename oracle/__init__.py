@@ -15,6 +15,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libameva_oracle.so")
 REF_I2S_PATH = os.path.join(HERE, "_ref", "libbitnet_mad_ref.so")
+SIMD_PATH = os.path.join(HERE, "libameva_cpu_simd.so")
 
 # ggml_type values (include/ggml/ggml.h:394-437)
 Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, I2_S = 2, 8, 12, 14, 15, 36
@@ -68,6 +69,55 @@ def lib() -> ctypes.CDLL:
             fn.restype = res
             fn.argtypes = args
     return _lib
+
+
+_simd = None
+
+
+def cpu_simd():
+    """The CPU baseline kernels (cpu_simd.c, AVX2 / FMA / F16C), or None when this CPU lacks those extensions. Used by
+    bench.py's cpu_baseline leg only; the parity checker is lib()."""
+    global _simd
+    if _simd is None:
+        try:
+            with open("/proc/cpuinfo") as f:
+                flags = next((ln.split(":", 1)[1].split() for ln in f if ln.startswith("flags")), [])
+        except OSError:
+            flags = []
+        if not all(x in flags for x in ("avx2", "fma", "f16c")):
+            return None
+        if not os.path.exists(SIMD_PATH):
+            build()
+        _simd = ctypes.CDLL(SIMD_PATH)
+        P, I64, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float
+        _simd.cpu_mul_mat_q4_0.restype = None
+        _simd.cpu_mul_mat_q4_0.argtypes = [P, I64, I64, P, I64, P]
+        _simd.cpu_flash_attn_decode_f16.restype = None
+        _simd.cpu_flash_attn_decode_f16.argtypes = [P, P, P, P, I64, I64, I64, I64, F]
+        _simd.cpu_num_threads.restype = ctypes.c_int
+        _simd.cpu_num_threads.argtypes = []
+    return _simd
+
+
+def simd_mul_mat_q4_0(w: np.ndarray, n_rows: int, k: int, a_q: np.ndarray, m: int, out: np.ndarray | None = None):
+    """CPU baseline Q4_0 x Q8_0 MUL_MAT (ggml's AVX2 vec_dot algorithm): [m][n_rows] f32."""
+    if out is None:
+        out = np.empty((m, n_rows), np.float32)
+    cpu_simd().cpu_mul_mat_q4_0(_p(w), n_rows, k, _p(a_q), m, _p(out))
+    return out
+
+
+def simd_flash_attn_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """CPU baseline decode attention: q f32 [n_head][D], k / v f16 [n_kv][n_head_kv][D] -> [n_head][D]."""
+    n_head, D = q.shape
+    n_kv, n_head_kv, _ = k.shape
+    assert D % 8 == 0 and D <= 256 and n_head % n_head_kv == 0
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float16)
+    v = np.ascontiguousarray(v, np.float16)
+    out = np.empty((n_head, D), np.float32)
+    cpu_simd().cpu_flash_attn_decode_f16(_p(q), _p(k), _p(v), _p(out), n_head, n_head_kv, n_kv, D, scale)
+    return out
 
 
 def _p(a: np.ndarray):
