@@ -44,6 +44,9 @@ struct Counters {
 };
 Counters g_cnt;
 std::atomic<int> g_fail{AMEVA_FAIL_NONE};
+// bumped whenever device memory a captured graph may read changes meaning outside a graph: a weight changing layout
+// (repacked at first use, or returned to ggml bytes by a write), a buffer allocated, freed or cleared
+std::atomic<int64_t> g_layout_gen{0};
 
 // AMEVA_PROFILE (ggml-ameva.cpp:104-114 of the reference): 1 = totals per graph (host encode, wait, launches),
 // 2 = also the GPU time of each node kind, from a HIP event recorded after every node on the graph's stream.
@@ -246,11 +249,30 @@ struct Arena {
     }
 };
 
+// The last graph computed, as a signature of everything its launches bake in (per node and source: op, type, shape,
+// strides, data address, view offset, op parameters), and its capture as a HIP graph with the counter increments
+// one run of it makes.
+struct Replay {
+    std::vector<int64_t> sig;
+    int64_t gen = -1;                  // g_layout_gen when sig was computed
+    hipGraphExec_t exec = nullptr;     // captured on the second computation of an identical graph
+    const void* arena_base = nullptr;  // the scratch the capture addresses
+    bool uncapturable = false;         // capture of this signature failed once: eager from now on
+    int64_t d_gpu_op = 0, d_mul_mat = 0, d_qmv = 0, d_mmq = 0, d_fused = 0, d_act_reuse = 0, encoded = 0;
+    void drop() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        exec = nullptr;
+        uncapturable = false;
+    }
+};
+
 struct Device {
     std::mutex compute_mu;
     hipStream_t stream = nullptr;
     Arena arena;
-    unsigned int* status = nullptr;  // bad-index counter of SET_ROWS / GET_ROWS
+    Replay replay;
+    unsigned int* status = nullptr;       // bad-index counter of SET_ROWS / GET_ROWS
+    unsigned int* status_host = nullptr;  // pinned copy of it, written by the graph's last copy
     std::vector<hipEvent_t> events;  // AMEVA_PROFILE=2: one after every node of a graph (grows, reused)
     bool inited = false;
     hipEvent_t event(size_t i) {
@@ -266,6 +288,7 @@ struct Device {
         if (hipSetDevice(0) != hipSuccess) return false;
         if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess) return false;
         if (hipMalloc(&status, 256) != hipSuccess) return false;
+        if (hipHostMalloc((void**)&status_host, 256, hipHostMallocDefault) != hipSuccess) return false;
         inited = true;
         g_cnt.ctx_create++;
         return true;
@@ -279,6 +302,7 @@ Device* device() {
 
 // ------------------------------------------------------------------------------------------------ buffers
 void buf_free(ggml_backend_buffer_t b) {
+    g_layout_gen++;
     BufCtx* c = (BufCtx*)b->context;
     if (c) {
         std::lock_guard<std::mutex> lk(c->mu);
@@ -296,6 +320,7 @@ void buf_memset(ggml_backend_buffer_t b, ggml_tensor* t, uint8_t v, size_t off, 
 
 // converts a quantized tensor between ggml blocks and the MI355X layout in place (through a temporary copy)
 bool convert_in_place(ggml_tensor* t, bool to_repacked) {
+    g_layout_gen++;
     const size_t n = nbytes(t);
     void* tmp = nullptr;
     if (hipMalloc(&tmp, n) != hipSuccess) return false;
@@ -378,6 +403,7 @@ bool buf_cpy_tensor(ggml_backend_buffer_t b, const ggml_tensor* src, ggml_tensor
 }
 
 void buf_clear(ggml_backend_buffer_t b, uint8_t v) {
+    g_layout_gen++;
     BufCtx* c = (BufCtx*)b->context;
     std::lock_guard<std::mutex> lk(c->mu);
     g_cnt.repacked_tensors -= (int64_t)c->repacked.size();
@@ -394,6 +420,7 @@ ggml_backend_buffer_t buft_alloc_buffer(ggml_backend_buffer_type_t buft, size_t 
         log_line("no HIP device (FAIL-FAST)");
         return nullptr;
     }
+    g_layout_gen++;
     BufCtx* c = new BufCtx;
     c->size = size;
     if (hipMalloc(&c->dev, size ? size : 256) != hipSuccess) {
@@ -536,9 +563,10 @@ struct ActEntry {
 };
 
 struct Engine {
-    Device* dev;
-    hipStream_t st;
+    Device* dev = nullptr;
+    hipStream_t st = nullptr;
     std::vector<ActEntry> acts;  // quantized activations valid at this point of the graph
+    ActEntry pending_act{};      // one written by the node being encoded (registered after its own invalidation)
     bool failed = false;
     std::string why;
     std::vector<std::string> labels;  // AMEVA_PROFILE=2: the kind of each timed node (events 0 .. n)
@@ -666,12 +694,46 @@ struct Engine {
                                 nrows(b), st));
     }
 
-    bool rms_norm(const ggml_tensor* n, const ggml_tensor* mul) {
+    // The activation type (Q8_0 or Q8_K) the first later one-row GEMV MUL_MAT reading `out` (the same bytes: out
+    // itself or a view of it) quantizes it to, or 0: the producer of `out` can then write that activation row in the
+    // same pass (act_for finds it in the cache); rows = k = elements of out.
+    const ggml_cgraph* graph = nullptr;
+    int gemv_act_type(int from, const ggml_tensor* out) const {
+        for (int i = from; graph && i < graph->n_nodes; ++i) {
+            const ggml_tensor* c = graph->nodes[i];
+            if (c->op != GGML_OP_MUL_MAT || c->src[1]->data != out->data || nbytes(c->src[1]) != nbytes(out)) continue;
+            const ggml_tensor* w = c->src[0];
+            if (nrows(c->src[1]) != 1 || c->src[1]->type != GGML_TYPE_F32 || w->ne[0] != nelements(out)) return 0;
+            if (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0) return w->ne[0] % 32 == 0 ? (int)GGML_TYPE_Q8_0 : 0;
+            if (w->type == GGML_TYPE_Q4_K || w->type == GGML_TYPE_Q6_K) return w->ne[0] % 256 == 0 ? (int)GGML_TYPE_Q8_K : 0;
+            return 0;
+        }
+        return 0;
+    }
+    void* fused_act(const ggml_tensor* n, const ggml_tensor* out, int atype) {
+        void* act = dev->arena.take((size_t)amv_act_bytes(atype, 1, nelements(out)));
+        if (!act) fail(n, "scratch exhausted");
+        return act;
+    }
+
+    bool rms_norm(int i, const ggml_tensor* n, const ggml_tensor* mul) {
         const ggml_tensor* x = n->src[0];
         const float eps = op_f32(n, 0);
+        const ggml_tensor* out = mul ? mul : n;
+        const int atype = nrows(x) == 1 && aligned16(out->data) ? gemv_act_type(i + (mul ? 2 : 1), out) : 0;
+        const ggml_tensor* w = mul ? (mul->src[0] == n ? mul->src[1] : mul->src[0]) : nullptr;
+        if (atype) {  // the next GEMV's activation row in the same pass
+            void* act = fused_act(n, out, atype);
+            if (!act) return false;
+            if (!rc(n, amv_rms_norm_act((const float*)x->data, 1, x->ne[0], eps, w ? (const float*)w->data : nullptr,
+                                        (float*)n->data, mul ? (float*)mul->data : nullptr, act, atype, AMV_Q8_X86,
+                                        st)))
+                return false;
+            pending_act = {out->data, nbytes(out), atype, 1, nelements(out), act};
+            return true;
+        }
         if (!mul) return rc(n, amv_rms_norm((const float*)x->data, nrows(x), x->ne[0], eps, nullptr, (float*)n->data,
                                             nullptr, nullptr, AMV_Q8_X86, st));
-        const ggml_tensor* w = mul->src[0] == n ? mul->src[1] : mul->src[0];
         return rc(n, amv_rms_norm((const float*)x->data, nrows(x), x->ne[0], eps, (const float*)w->data,
                                   (float*)n->data, (float*)mul->data, nullptr, AMV_Q8_X86, st));
     }
@@ -682,17 +744,26 @@ struct Engine {
                               x->ne[0], n->op_params[1], n->op_params[2], op_f32(n, 5), op_f32(n, 6), op_f32(n, 8), st));
     }
 
-    bool flash_attn(const ggml_tensor* n) {
+    bool flash_attn(int i, const ggml_tensor* n) {
         const ggml_tensor *q = n->src[0], *k = n->src[1], *v = n->src[2], *m = n->src[3];
         const int64_t n_head = q->ne[2], n_head_kv = k->ne[2], n_kv = k->ne[1], D = q->ne[0];
         const int64_t ws = amv_flash_attn_workspace_bytes(n_head, n_head_kv, n_kv, D);
         void* work = dev->arena.take((size_t)ws);
         if (!work) return fail(n, "scratch exhausted");
+        // the o projection's activation row written by the split merge (Q8_K needs an even GQA group)
+        int atype = q->ne[1] == 1 && aligned16(n->data) ? gemv_act_type(i + 1, n) : 0;
+        if (atype == (int)GGML_TYPE_Q8_K && (n_head / n_head_kv) % 2 != 0) atype = 0;
+        void* act = atype ? fused_act(n, n, atype) : nullptr;
+        if (atype && !act) return false;
         // K / V strides in bytes; a Q8_0 / Q4_0 cache meets q quantized to Q8_0 (x86 rule), as ggml's CPU kernel does
-        return rc(n, amv_flash_attn_decode_kv(k->type, (const float*)q->data, k->data, v->data, m ? m->data : nullptr,
-                                              (float*)n->data, n_head, n_head_kv, n_kv, nullptr, D, (int64_t)k->nb[1],
-                                              (int64_t)k->nb[2], (int64_t)v->nb[1], (int64_t)v->nb[2], op_f32(n, 0),
-                                              work, ws, nullptr, nullptr, (int)GGML_TYPE_Q8_0, AMV_Q8_X86, st));
+        if (!rc(n, amv_flash_attn_decode_kv(k->type, (const float*)q->data, k->data, v->data, m ? m->data : nullptr,
+                                            (float*)n->data, n_head, n_head_kv, n_kv, nullptr, D, (int64_t)k->nb[1],
+                                            (int64_t)k->nb[2], (int64_t)v->nb[1], (int64_t)v->nb[2], op_f32(n, 0),
+                                            work, ws, nullptr, act, atype ? atype : (int)GGML_TYPE_Q8_0, AMV_Q8_X86,
+                                            st)))
+            return false;
+        if (act) pending_act = {n->data, nbytes(n), atype, 1, nelements(n), act};
+        return true;
     }
 
     bool glu(const ggml_tensor* n) {
@@ -815,6 +886,7 @@ struct Engine {
     }
 
     bool run(ggml_cgraph* g) {
+        graph = g;
         const bool prof = profile_level() >= 2;
         if (prof) {
             hipEvent_t e0 = dev->event(0);
@@ -840,7 +912,7 @@ struct Engine {
             }
             case GGML_OP_RMS_NORM: {
                 const ggml_tensor* m = fusable_mul(g, i);
-                ok = rms_norm(n, m);
+                ok = rms_norm(i, n, m);
                 if (ok && m) {
                     invalidate(n);
                     invalidate(m);
@@ -854,7 +926,7 @@ struct Engine {
             case GGML_OP_ADD: ok = binary(n, 0); break;
             case GGML_OP_MUL: ok = binary(n, 1); break;
             case GGML_OP_ROPE: ok = rope(n); break;
-            case GGML_OP_FLASH_ATTN_EXT: ok = flash_attn(n); break;
+            case GGML_OP_FLASH_ATTN_EXT: ok = flash_attn(i, n); break;
             case GGML_OP_GLU: ok = glu(n); break;
             case GGML_OP_SET_ROWS: ok = set_rows(n); break;
             case GGML_OP_CPY:
@@ -864,6 +936,10 @@ struct Engine {
             }
             if (!ok) return false;
             invalidate(n);
+            if (pending_act.act) {  // an activation row written with the node's output: valid from here on
+                acts.push_back(pending_act);
+                pending_act = {};
+            }
             g_cnt.gpu_op++;
             encoded++;
             if (prof) {
@@ -875,6 +951,48 @@ struct Engine {
         return true;
     }
 };
+
+// the status word cleared by a kernel, not a memset node, so that a captured graph clears it on every replay
+__global__ void k_clear_status(unsigned int* s) { s[threadIdx.x] = 0u; }
+
+void sig_tensor(std::vector<int64_t>& s, const ggml_tensor* t) {
+    s.push_back((int64_t)(uintptr_t)t->data);
+    s.push_back((int64_t)t->type);
+    s.push_back((int64_t)t->op);
+    for (int i = 0; i < 4; ++i) {
+        s.push_back(t->ne[i]);
+        s.push_back((int64_t)t->nb[i]);
+    }
+    s.push_back((int64_t)t->view_offs);
+    s.push_back((int64_t)(uintptr_t)t->buffer);
+    for (int i = 0; i < 16; ++i) s.push_back(t->op_params[i]);
+}
+
+std::vector<int64_t> graph_signature(const ggml_cgraph* g) {
+    std::vector<int64_t> s;
+    s.reserve((size_t)g->n_nodes * 8 * 30);
+    s.push_back(g->n_nodes);
+    for (int i = 0; i < g->n_nodes; ++i) {
+        const ggml_tensor* n = g->nodes[i];
+        sig_tensor(s, n);
+        for (int j = 0; j < GGML_MAX_SRC; ++j) {
+            if (n->src[j]) sig_tensor(s, n->src[j]);
+            else s.push_back(-1);
+        }
+    }
+    return s;
+}
+
+// AMEVA_GRAPH=0: every graph runs eagerly (no capture, no replay)
+bool graph_replay_on() {
+    static const bool on = [] {
+        const char* e = std::getenv("AMEVA_GRAPH");
+        return !(e && e[0] == '0' && e[1] == 0);
+    }();
+    return on;
+}
+
+enum ggml_status finish_graph(Device* d, bool ok, const std::string& why);
 
 enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
     Device* d = device();
@@ -896,11 +1014,85 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         return GGML_STATUS_FAILED;
     }
     d->arena.used = 0;
-    if (hipMemsetAsync(d->status, 0, 256, d->stream) != hipSuccess) return GGML_STATUS_FAILED;
     const int prof = profile_level();
+    // A graph identical to the last one (same signature, no layout change since) is replayed from its HIP graph,
+    // captured on its second computation; the first runs eagerly (it repacks weights on first use).
+    Replay& rp = d->replay;
+    const bool can_graph = graph_replay_on() && !prof && g_fail.load() == AMEVA_FAIL_NONE;
+    std::vector<int64_t> sig;
+    bool same = false;
+    if (can_graph) {
+        sig = graph_signature(g);
+        same = sig == rp.sig && rp.gen == g_layout_gen.load();
+        if (same && rp.exec && rp.arena_base != d->arena.base) rp.drop();  // the scratch moved: capture again
+    }
+    if (same && rp.exec) {
+        if (trace_on()) std::fprintf(stderr, "AMEVA_TRACE graph replay nodes=%d\n", g->n_nodes);
+        const bool ok = hipGraphLaunch(rp.exec, d->stream) == hipSuccess;
+        if (ok) {
+            g_cnt.gpu_op += rp.d_gpu_op;
+            g_cnt.mul_mat += rp.d_mul_mat;
+            g_cnt.qmv += rp.d_qmv;
+            g_cnt.mmq += rp.d_mmq;
+            g_cnt.fused += rp.d_fused;
+            g_cnt.act_reuse += rp.d_act_reuse;
+        }
+        return finish_graph(d, ok, ok ? std::string() : std::string("graph replay failed"));
+    }
+    if (!same || !can_graph) {
+        rp.drop();
+        rp.sig = std::move(sig);  // empty when graphs are off: never equal to a real signature
+    }
+    if (same && !rp.exec && !rp.uncapturable) {
+        // second computation: capture, then launch the capture (the captured work has not run yet)
+        const int64_t c0[6] = {g_cnt.gpu_op, g_cnt.mul_mat, g_cnt.qmv, g_cnt.mmq, g_cnt.fused, g_cnt.act_reuse};
+        Engine e;
+        e.dev = d;
+        e.st = d->stream;
+        hipGraph_t graph = nullptr;
+        bool ok = hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal) == hipSuccess;
+        if (ok) {
+            hipLaunchKernelGGL(k_clear_status, dim3(1), dim3(64), 0, d->stream, d->status);
+            ok = e.run(g) && hipMemcpyAsync(d->status_host, d->status, sizeof(unsigned int), hipMemcpyDeviceToHost,
+                                            d->stream) == hipSuccess;
+            const bool ended = hipStreamEndCapture(d->stream, &graph) == hipSuccess;
+            ok = ok && ended && graph &&
+                 hipGraphInstantiate(&rp.exec, graph, nullptr, nullptr, 0) == hipSuccess;
+            if (graph) (void)hipGraphDestroy(graph);
+        }
+        (void)hipGetLastError();
+        if (ok) {
+            rp.arena_base = d->arena.base;
+            rp.d_gpu_op = g_cnt.gpu_op - c0[0];
+            rp.d_mul_mat = g_cnt.mul_mat - c0[1];
+            rp.d_qmv = g_cnt.qmv - c0[2];
+            rp.d_mmq = g_cnt.mmq - c0[3];
+            rp.d_fused = g_cnt.fused - c0[4];
+            rp.d_act_reuse = g_cnt.act_reuse - c0[5];
+            rp.encoded = e.encoded;
+            if (trace_on()) std::fprintf(stderr, "AMEVA_TRACE graph captured nodes=%d\n", g->n_nodes);
+            const bool launched = hipGraphLaunch(rp.exec, d->stream) == hipSuccess;
+            return finish_graph(d, launched, launched ? std::string() : std::string("graph launch failed"));
+        }
+        // not capturable (a step needed something a capture cannot hold): undo the counts, run eagerly below
+        if (rp.exec) (void)hipGraphExecDestroy(rp.exec);
+        rp.exec = nullptr;
+        rp.uncapturable = true;
+        g_cnt.gpu_op = c0[0];
+        g_cnt.mul_mat = c0[1];
+        g_cnt.qmv = c0[2];
+        g_cnt.mmq = c0[3];
+        g_cnt.fused = c0[4];
+        g_cnt.act_reuse = c0[5];
+        d->arena.used = 0;
+    }
+    hipLaunchKernelGGL(k_clear_status, dim3(1), dim3(64), 0, d->stream, d->status);
     const double t0 = prof || trace_on() ? now_ms() : 0.0;
-    Engine e{d, d->stream, {}, false, {}, {}, 0};
-    const bool ok = e.run(g);
+    Engine e;
+    e.dev = d;
+    e.st = d->stream;
+    const bool ok = e.run(g) && hipMemcpyAsync(d->status_host, d->status, sizeof(unsigned int),
+                                               hipMemcpyDeviceToHost, d->stream) == hipSuccess;
     const double t1 = prof || trace_on() ? now_ms() : 0.0;
     int64_t graph_no = 0;
     if (trace_on()) {
@@ -937,6 +1129,17 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         log_line("%s (FAIL-FAST)", e.why.c_str());
         return GGML_STATUS_FAILED;
     }
+    rp.gen = g_layout_gen.load();  // the layout this run left (its first use repacked the weights)
+    return finish_graph(d, se == hipSuccess, se == hipSuccess ? std::string() : std::string(hipGetErrorString(se)));
+}
+
+// after the graph's work is queued (eager) or launched (replay): wait, then the status word
+enum ggml_status finish_graph(Device* d, bool ok, const std::string& why) {
+    const hipError_t se = ok ? hipStreamSynchronize(d->stream) : hipSuccess;
+    if (!ok) {
+        log_line("%s (FAIL-FAST)", why.c_str());
+        return GGML_STATUS_FAILED;
+    }
     if (g_fail.load() == AMEVA_FAIL_WAIT_TIMEOUT) {
         log_line("failure injection: wait timeout (FAIL-FAST)");
         return GGML_STATUS_FAILED;
@@ -945,8 +1148,7 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         log_line("graph execution failed: %s (FAIL-FAST)", hipGetErrorString(se));
         return GGML_STATUS_FAILED;
     }
-    unsigned int bad = 0;
-    (void)hipMemcpy(&bad, d->status, sizeof(bad), hipMemcpyDeviceToHost);
+    const unsigned int bad = *(volatile unsigned int*)d->status_host;  // copied by the graph's last step
     if (bad != 0 || g_fail.load() == AMEVA_FAIL_INVALIDATE_DST) {
         log_line("%u row indices out of range (FAIL-FAST)", bad);
         return GGML_STATUS_FAILED;
@@ -1040,7 +1242,11 @@ void ggml_backend_ameva_teardown(void) {
         (void)hipStreamSynchronize(d->stream);
         if (d->arena.base) (void)hipFree(d->arena.base);
         d->arena = Arena{};
+        d->replay.drop();
+        d->replay.sig.clear();
         (void)hipFree(d->status);
+        (void)hipHostFree(d->status_host);
+        d->status_host = nullptr;
         (void)hipStreamDestroy(d->stream);
         d->inited = false;
     }

@@ -252,6 +252,83 @@ def bench_layer(torch, dev, args):
             "layer_decode_note": "Llama-3-8B layer, Q4_0, bs1, 4096 cached keys, 4 chained cold layers in one HIP graph"}
 
 
+def bench_plugin_layer(torch, dev):
+    """bs1 decode of the Llama-3-8B-shape Q4_0 layer at 4096 cached keys through the drop-in boundary: the ggml graph
+    llama.cpp builds for one layer (RMS_NORM, MUL, q/k/v MUL_MATs, ROPE, SET_ROWS into the f16 cache, FLASH_ATTN_EXT,
+    o MUL_MAT + ADD, RMS_NORM, MUL, gate/up MUL_MATs, SWIGLU, down MUL_MAT + ADD) handed to libggml-ameva.so's
+    graph_compute, which runs it eagerly on its stream and returns after the stream completes (as the reference's
+    ggml_backend_graph_compute does, adapters/llama/ameva_backend_bench.cpp:38-79). The ggml host side is the
+    stand-in the plugin tests use (tests/ggml_plugin.py: ggml's structs and the buffer calls the plugin binds to).
+    Weights: random Q4_0 blocks (d = 0.01). Reported per layer: wall time of one graph_compute call."""
+    import ctypes
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import ggml_plugin as gp
+    rng = np.random.default_rng(2024)
+    H, NH, NKV, D, FF, CTX = 4096, 32, 8, 128, 14336, 4096
+    pos_t = CTX - 1
+
+    def wq4(n, k):
+        w = np.frombuffer(rng.bytes(n * (k // 32) * 18), np.uint8).reshape(n, k // 32, 18).copy()
+        w[:, :, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+        return w.reshape(n, -1)
+    w = {"q": wq4(NH * D, H), "k": wq4(NKV * D, H), "v": wq4(NKV * D, H), "o": wq4(H, NH * D),
+         "gate": wq4(FF, H), "up": wq4(FF, H), "down": wq4(H, FF)}
+    g = gp.Graph(sum(a.nbytes for a in w.values()) + 16 * 4096, 96 << 20)
+    try:
+        T = {k_: g.tensor(gp.Q4_0, [a.shape[1] * 32 // 18, a.shape[0]], "w", k_) for k_, a in w.items()}
+        for k_, a in w.items():
+            g.set(T[k_], a)
+        AN, FN = g.tensor(gp.F32, [H], "w", "attn_norm"), g.tensor(gp.F32, [H], "w", "ffn_norm")
+        g.set(AN, (1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+        g.set(FN, (1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+        KC, VC = g.tensor(gp.F16, [NKV * D, CTX], "c", "k_cache"), g.tensor(gp.F16, [NKV * D, CTX], "c", "v_cache")
+        g.set(KC, rng.standard_normal((CTX, NKV * D)).astype(np.float16))
+        g.set(VC, rng.standard_normal((CTX, NKV * D)).astype(np.float16))
+        X = g.tensor(gp.F32, [H, 1], "c", "inp")
+        g.set(X, rng.standard_normal((1, H)).astype(np.float32))
+        POS = g.tensor(gp.I32, [1], "c", "pos")
+        g.set(POS, np.array([pos_t], np.int32))
+        IDX = g.tensor(gp.I64, [1], "c", "kv_idx")
+        g.set(IDX, np.array([pos_t], np.int64))
+        MASK = g.tensor(gp.F16, [CTX, 1], "c", "mask")
+        g.set(MASK, np.zeros(CTX, np.float16))
+        cur = g.mul(g.rms_norm(X, 1e-5), AN)
+        q = g.rope(g.reshape_3d(g.mul_mat(T["q"], cur), D, NH, 1), POS, D, 0, 500000.0)
+        k = g.rope(g.reshape_3d(g.mul_mat(T["k"], cur), D, NKV, 1), POS, D, 0, 500000.0)
+        v = g.mul_mat(T["v"], cur)
+        g.set_rows(KC, g.view_nd(k, gp.OP_RESHAPE, [NKV * D, 1], [4, NKV * D * 4, NKV * D * 4, NKV * D * 4]), IDX)
+        g.set_rows(VC, v, IDX)
+        kv_nb = [2, NKV * D * 2, D * 2, NKV * D * 2 * CTX]
+        att = g.flash_attn_ext(g.view_nd(q, gp.OP_PERMUTE, [D, 1, NH], [4, D * NH * 4, D * 4, D * NH * 4]),
+                               g.view_nd(KC, gp.OP_VIEW, [D, CTX, NKV], kv_nb),
+                               g.view_nd(VC, gp.OP_VIEW, [D, CTX, NKV], kv_nb), MASK, 1.0 / np.sqrt(D))
+        ffn_inp = g.add(g.mul_mat(T["o"], g.view_nd(att, gp.OP_RESHAPE, [H, 1], [4, H * 4, H * 4, H * 4])), X)
+        cur = g.mul(g.rms_norm(ffn_inp, 1e-5), FN)
+        ff = g.swiglu(g.mul_mat(T["gate"], cur), g.mul_mat(T["up"], cur))
+        g.add(g.mul_mat(T["down"], ff), ffn_inp)
+        for _ in range(5):  # the first call repacks the weights in place
+            assert g.compute() == gp.STATUS_SUCCESS
+        g.plugin.ggml_backend_ameva_reset_counters()
+        # the cgraph of the last call, handed over again as a host would (no Python rebuilding per call)
+        compute, be, cg = g.backend.iface.graph_compute, g.backend_ptr, ctypes.addressof(g._keep[1])
+        n = 200
+        t0 = time.perf_counter()
+        for _ in range(n):
+            compute(be, cg)
+        el = (time.perf_counter() - t0) / n
+        nodes = len(g.nodes)
+        fused = gp.counter(g.plugin, "fused_pair_count") // n
+    finally:
+        g.free()
+    log(f"bench: plugin layer decode (graph_compute, {nodes} ggml nodes, {fused} fused pairs) {el * 1e6:.2f} us/layer")
+    return {"plugin_layer_decode_us": round(el * 1e6, 2), "plugin_layer_decode_tok_s": round(1.0 / el, 1),
+            "plugin_layer_decode_nodes": nodes, "plugin_layer_decode_fused_pairs": fused,
+            "plugin_layer_decode_note": "one Llama-3-8B Q4_0 layer graph, bs1, 4096 cached keys, through "
+                                        "libggml-ameva.so graph_compute (synchronous per call; the unchanged graph "
+                                        "replays its HIP-graph capture)"}
+
+
 BLOCK_BYTES = {2: 18, 8: 34, 12: 144 * 32 // 256, 14: 210 * 32 // 256}  # bytes per 32 weights
 
 
@@ -684,6 +761,8 @@ def main():
     ap.add_argument("--only-bitnet", action="store_true", help="only the BitNet 2B engine decode figures")
     ap.add_argument("--only-load", action="store_true", help="only the weight load path figures (repack, upload)")
     ap.add_argument("--only-kv", action="store_true", help="only the FA decode figures over the three KV caches")
+    ap.add_argument("--only-plugin", action="store_true",
+                    help="only the layer decode through libggml-ameva.so graph_compute")
     ap.add_argument("--pmc-gemm", action="store_true",
                     help="for rocprofv3 --pmc: 20 eager exact Q4_K MUL_MATs at M = 512 on each FFN shape")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -727,6 +806,9 @@ def main():
         return
     if args.only_kv:
         print(json.dumps(bench_kv_cache(ops, torch, dev)), flush=True)
+        return
+    if args.only_plugin:
+        print(json.dumps(bench_plugin_layer(torch, dev)), flush=True)
         return
 
     log(f"bench: Q4_0 GEMV {N_ROWS}x{K}, {COPIES} weight copies, steps={args.steps} warmup={args.warmup}")
@@ -776,6 +858,7 @@ def main():
     if not args.only_headline:
         layer_info = bench_layer(torch, dev, args)
         extra.update(layer_info)
+        extra.update(bench_plugin_layer(torch, dev))
         if not args.no_model:
             extra.update(bench_model(torch, dev))
             extra.update(bench_bitnet())
