@@ -41,6 +41,9 @@ SIGNATURES = {
     "amv_gemv_rope_kv": (I32, [I32, P, I64, I64, P, P, I64, I64, I64, P, F32, F32, F32, P, P, I64, P, I64, P, P]),
     "amv_gemv_add_rms_norm": (I32, [I32, P, I64, I64, P, P, P, P, F32, P, P, P, P, I32, I32, P, P]),
     "amv_gemv_swiglu_q8": (I32, [I32, P, I64, I64, P, P, P, P, I32, I32, P, P]),
+    "amv_gemv_rope_kv_seg": (I32, [I32, P, P, P, I64, P, P, P, P, I64, I64, I64, P, F32, F32, F32, P, P, I64, P, I64,
+                                   P, P]),
+    "amv_gemv_swiglu_q8_seg": (I32, [I32, P, P, I64, I64, P, P, P, I32, I32, P, P]),
     "amv_flash_attn_decode_ex": (I32, [P, P, P, P, P, I64, I64, I64, P, I64, I64, I64, I64, I64, F32, P, I64, P, P,
                                           I32, I32, P]),
     "amv_rope_kv_store": (I32, [P, P, I64, I64, I64, I64, I32, I32, F32, F32, F32, P, P, I64, P, I64, P, P]),

@@ -54,7 +54,21 @@ struct MmvPost {
     float* norm_y;  // ADD_NORM outputs, each may be NULL: x * scale, then * norm_w
     float* norm_o;
     AmvActOut act;  // quantized output of the tail (Q8_0 or Q8_K activation row)
+    // Segmented weights (EP 5 and 7 over separate matrices, SEG kernels): rows seg_row[s] .. seg_row[s + 1] - 1 of
+    // the stacked row space are the rows of matrix s, held at w_seg[s] in its own layout; EP 5 writes them to
+    // dst_seg[s]. n_seg = 0: one matrix; else seg_row[n_seg .. 3] are INT32_MAX.
+    int n_seg;
+    int seg_row[4];
+    const uint8_t* w_seg[3];
+    float* dst_seg[3];
 };
+
+// the segment of stacked row `row` and its row within that matrix
+__device__ __forceinline__ int mmv_seg(const MmvPost& p, int row, int& local) {
+    const int s = (row >= p.seg_row[1]) + (row >= p.seg_row[2]);
+    local = row - p.seg_row[s];
+    return s;
+}
 
 // Stacked SWIGLU: a wave owns the R / 2 consecutive outputs o = (R / 2) wave + i, i.e. gate rows o (r = i) and up
 // rows F + o (r = R / 2 + i), F = n_rows / 2.
@@ -90,7 +104,7 @@ __device__ __forceinline__ MmvRopeAt mmv_rope_at(const MmvPost& post, int wave) 
 
 // End of a row group: wave sums of the R accumulators; with a split of K (S > 1 waves per row group) the S partial
 // sums meet in LDS and are added in the fixed order ks = 0 .. S-1 by the group's first wave; then the epilogue.
-template <int R, int EP, int S>
+template <int R, int EP, int S, bool SEG = false>
 __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int wi, int ks, bool live, int wave,
                                            int n_rows, float* __restrict__ dst, const float* __restrict__ epi,
                                            float* __restrict__ eout, const MmvPost& post, const MmvRopeAt& ra) {
@@ -122,8 +136,15 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
         const int nqk = post.n_q + post.n_k;
         float y0 = t[0], y1 = t[1];
         if (r0 < nqk) amv_rope_apply(ra.c, ra.s, t[0], t[1], y0, y1);
-        dst[r0] = y0;
-        dst[r0 + 1] = y1;
+        if constexpr (SEG) {
+            int lr;
+            const int sg = mmv_seg(post, r0, lr);
+            post.dst_seg[sg][lr] = y0;
+            post.dst_seg[sg][lr + 1] = y1;
+        } else {
+            dst[r0] = y0;
+            dst[r0 + 1] = y1;
+        }
         if (r0 >= post.n_q) {
             const int64_t dr = ra.row;
             const bool store = dr >= 0 && dr < post.cache_rows;
@@ -196,7 +217,7 @@ __device__ __forceinline__ void mmv_tail(const MmvPost& post, const float* eout,
 // indices are 32-bit (the launcher checks n_rows * nb < 2^31). PAIRS: n_rows is even, every scale sits in a pair.
 // NBT: the block count of a row as a compile-time constant (128: K = 4096, the hidden size of most Llama GEMVs) or 0
 // (the nb argument): with a constant the row offsets are shifts and the one-step loop has no test.
-template <int R, int U, bool BLOCK_SUMS, int EP, int S, bool PAIRS, bool FULL, int NBT = 0>
+template <int R, int U, bool BLOCK_SUMS, int EP, int S, bool PAIRS, bool FULL, int NBT = 0, bool SEG = false>
 __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                  int n_rows, int nb_arg, const int8_t* __restrict__ aq,
                                                  const int2* __restrict__ ads, float* __restrict__ dst,
@@ -214,9 +235,21 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
     const int4* a4 = reinterpret_cast<const int4*>(aq);
     const uint32_t* wd2 = reinterpret_cast<const uint32_t*>(wd);
     uint32_t rb[R], db[R];  // block index of (row, 0); scale index of (row, 0) minus the block offset factor
+    const uint4* wqr[R];    // SEG: the row's matrix (its rows are indexed within it)
+    const uint16_t* wdr[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int row = min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
+        int row = min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
+        wqr[r] = wq;
+        wdr[r] = wd;
+        if constexpr (SEG) {
+            int lr;
+            const int sg = mmv_seg(post, row, lr);
+            const uint32_t rows_s = (uint32_t)(post.seg_row[sg + 1] - post.seg_row[sg]);
+            wqr[r] = reinterpret_cast<const uint4*>(post.w_seg[sg]);
+            wdr[r] = reinterpret_cast<const uint16_t*>(post.w_seg[sg] + (size_t)rows_s * nb * 16);
+            row = lr;
+        }
         rb[r] = (uint32_t)row * (uint32_t)nb;
         db[r] = (uint32_t)(row >> 1) * (uint32_t)nb * 2u + (uint32_t)(row & 1);  // PAIRS: + 2 j
     }
@@ -236,9 +269,12 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
         for (int u = 0; u < U; ++u) {
             const int j = FULL ? j0 + 64 * u + lane : min(j0 + 64 * u + lane, nb - 1);
 #pragma unroll
-            for (int r = 0; r < R; ++r) w[u][r] = amv_ld_stream(wq + rb[r] + j);
+            for (int r = 0; r < R; ++r) w[u][r] = amv_ld_stream((SEG ? wqr[r] : wq) + rb[r] + j);
             if (BLOCK_SUMS) continue;
-            if constexpr (PAIRS && !MMV_STACKED(EP) && R % 2 == 0) {
+            if constexpr (SEG) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) dw[u][r] = amv_ld_stream(wdr[r] + db[r] + 2 * j);
+            } else if constexpr (PAIRS && !MMV_STACKED(EP) && R % 2 == 0) {
                 // the wave's rows 2p, 2p + 1 read both scales with one dword
 #pragma unroll
                 for (int r = 0; r < R; r += 2) {
@@ -293,7 +329,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
         }
     } while ((j0 += 64 * U * S) < nb);
     if constexpr (!BLOCK_SUMS) {
-        mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
+        mmv_finish<R, EP, S, SEG>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
         if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S, R>(post, eout, n_rows);
     }
 }
@@ -433,7 +469,7 @@ __device__ __forceinline__ int dot16(uint4 w, int4 a, int acc) {
     return amv_dot4((int)w.w, a.w, acc);
 }
 
-template <int R, bool BLOCK_SUMS, int EP, int S>
+template <int R, bool BLOCK_SUMS, int EP, int S, bool SEG = false>
 __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, const uint4* __restrict__ wh,
                                                  int n_rows, int nsl, const int8_t* __restrict__ aq,
                                                  const float* __restrict__ ad, const int* __restrict__ abs16,
@@ -456,9 +492,18 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
         uint4 q[R], hd[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const size_t row = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
-            q[r] = amv_ld_stream(wq + row * nsl + j);
-            hd[r] = amv_ld_stream(wh + row * nsb + sb);
+            int row = min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
+            const uint4* wqs = wq;
+            const uint4* whs = wh;
+            if constexpr (SEG) {  // the row's matrix: qs of its rows, then their 16-byte heads
+                int lr;
+                const int sg = mmv_seg(post, row, lr);
+                wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
+                whs = wqs + (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]) * nsl;
+                row = lr;
+            }
+            q[r] = amv_ld_stream(wqs + (size_t)row * nsl + j);
+            hd[r] = amv_ld_stream(whs + (size_t)row * nsb + sb);
         }
         const int4 alo = a4[sb * 16 + 4 * c + h], ahi = a4[sb * 16 + 4 * c + 2 + h];
         const float da = ad[sb];
@@ -491,7 +536,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
         }
     }
     if constexpr (!BLOCK_SUMS) {
-        mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
+        mmv_finish<R, EP, S, SEG>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
         if constexpr (MMV_TAIL(EP)) mmv_tail<EP, S, R>(post, eout, n_rows);
     }
 }
@@ -592,6 +637,18 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const int waves = MMV_STACKED(EP) ? a.n_rows / R : (a.n_rows + R - 1) / R;
     const bool full = nb % (64 * U) == 0 && (MMV_STACKED(EP) || a.n_rows % R == 0);
     const dim3 grid((waves * S + 3) / 4);
+    if constexpr (!BS && (EP == MMV_EP_ROPE_KV || EP == MMV_EP_SWIGLU_Q8)) {
+        if (a.post.n_seg > 0) {  // separate matrices (the launcher checked whole steps and even rows per matrix)
+            const uint4* w0 = reinterpret_cast<const uint4*>(a.post.w_seg[0]);
+            if (nb == 128 && U == 2)
+                hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, true, true, 128, true>), grid, dim3(256), 0, st, w0,
+                                   nullptr, a.n_rows, nb, aq, ads, a.dst, a.sums, a.epi, a.eout, a.post);
+            else
+                hipLaunchKernelGGL((k_mmv_q4_0<R, U, BS, EP, S, true, true, 0, true>), grid, dim3(256), 0, st, w0,
+                                   nullptr, a.n_rows, nb, aq, ads, a.dst, a.sums, a.epi, a.eout, a.post);
+            return;
+        }
+    }
     if (!BS && EP == AMV_EP_NONE && S == 1 && R == 2 && a.n_rows % 2 == 0 && nb == 128)
         hipLaunchKernelGGL(k_mmv_q4_0_k4096, grid, dim3(256), 0, st, wq, reinterpret_cast<const uint32_t*>(wd),
                            a.n_rows, reinterpret_cast<const int4*>(aq), ads, a.dst);
@@ -629,6 +686,14 @@ static void launch_q4_K(const MmvArgs& a, hipStream_t st) {
     const uint4* wq = reinterpret_cast<const uint4*>(a.w);
     const uint4* wh = reinterpret_cast<const uint4*>(a.w + nblk * 128);
     const int waves = MMV_STACKED(EP) ? a.n_rows / R : (a.n_rows + R - 1) / R;
+    if constexpr (!BS && (EP == MMV_EP_ROPE_KV || EP == MMV_EP_SWIGLU_Q8)) {
+        if (a.post.n_seg > 0) {  // separate matrices
+            hipLaunchKernelGGL((k_mmv_q4_K<R, BS, EP, S, true>), dim3((waves * S + 3) / 4), dim3(256), 0, st,
+                               reinterpret_cast<const uint4*>(a.post.w_seg[0]), nullptr, a.n_rows, nsl, a.aq,
+                               (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout, a.post);
+            return;
+        }
+    }
     hipLaunchKernelGGL((k_mmv_q4_K<R, BS, EP, S>), dim3((waves * S + 3) / 4), dim3(256), 0, st, wq, wh, a.n_rows, nsl, a.aq,
                        (const float*)a.ameta0, (const int*)a.ameta1, a.dst, a.sums, a.epi, a.eout, a.post);
 }
@@ -892,6 +957,92 @@ extern "C" int amv_gemv_rope_kv(int wtype, const void* w, int64_t n_rows, int64_
     rc = mmv_dispatch_fused(MMV_EP_ROPE_KV, a, act, amv_stream(stream));
     if (rc) return rc;
     return amv_check_launch("amv_gemv_rope_kv");
+}
+
+// Segment table of separate matrices stacked by rows (their repacked layouts stay their own).
+static int mmv_segments(const char* fn, MmvPost& p, int n, const void* const* w, const int64_t* rows, int wtype,
+                        int64_t k) {
+    p.n_seg = n;
+    int64_t r0 = 0;
+    for (int s = 0; s < 4; ++s) p.seg_row[s] = INT32_MAX;
+    for (int s = 0; s < n; ++s) {
+        AMV_REQUIRE(w[s] && ((uintptr_t)w[s] & 15) == 0, "%s: matrix %d null or not 16-byte aligned", fn, s);
+        AMV_REQUIRE(rows[s] > 0 && rows[s] % 2 == 0, "%s: matrix %d rows %lld (even, > 0)", fn, s, (long long)rows[s]);
+        p.seg_row[s] = (int)r0;
+        p.w_seg[s] = (const uint8_t*)w[s];
+        r0 += rows[s];
+    }
+    p.seg_row[n] = (int)r0;
+    AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q4_K, "%s: weight type %d (Q4_0 or Q4_K)", fn, wtype);
+    AMV_REQUIRE(wtype != AMV_T_Q4_0 || k % (64 * 2 * 32) == 0, "%s: Q4_0 k %% 4096 != 0", fn);
+    return AMV_OK;
+}
+
+extern "C" int amv_gemv_rope_kv_seg(int wtype, const void* wq, const void* wk, const void* wv, int64_t k,
+                                    const void* act, float* q_out, float* k_out, float* v_out, int64_t n_head,
+                                    int64_t n_head_kv, int64_t D, const int32_t* pos, float freq_base, float freq_scale,
+                                    float attn_factor, void* k_cache, void* v_cache, int64_t cache_row,
+                                    const int64_t* kv_idx, int64_t cache_rows, unsigned int* bad, void* stream) {
+    const int64_t n_rows = (n_head + 2 * n_head_kv) * D;
+    int rc = check_common("amv_gemv_rope_kv_seg", wtype, wq, n_rows, k, act, 1);
+    if (rc) return rc;
+    AMV_REQUIRE(q_out && k_out && v_out && pos && k_cache && v_cache && kv_idx, "amv_gemv_rope_kv_seg: null pointer");
+    AMV_REQUIRE(n_head > 0 && n_head_kv > 0 && D > 0 && D % 2 == 0, "amv_gemv_rope_kv_seg: bad heads");
+    AMV_REQUIRE(cache_row >= n_head_kv * D && cache_rows > 0, "amv_gemv_rope_kv_seg: cache row %lld < %lld",
+                (long long)cache_row, (long long)(n_head_kv * D));
+    MmvArgs a{wtype, (const uint8_t*)wq, (int)n_rows, (int)k, nullptr, nullptr, nullptr, q_out, nullptr, nullptr,
+              nullptr};
+    MmvPost& p = a.post;
+    const void* ws[3] = {wq, wk, wv};
+    const int64_t rows[3] = {n_head * D, n_head_kv * D, n_head_kv * D};
+    rc = mmv_segments("amv_gemv_rope_kv_seg", p, 3, ws, rows, wtype, k);
+    if (rc) return rc;
+    p.dst_seg[0] = q_out;
+    p.dst_seg[1] = k_out;
+    p.dst_seg[2] = v_out;
+    p.pos = pos;
+    p.theta_scale = powf(freq_base, -2.0f / (float)D);  // amv_rope's expression with n_dims = D
+    p.freq_scale = freq_scale;
+    p.attn_factor = attn_factor;
+    p.n_q = (int)(n_head * D);
+    p.n_k = (int)(n_head_kv * D);
+    p.head_dim = (int)D;
+    p.k_cache = (uint16_t*)k_cache;
+    p.v_cache = (uint16_t*)v_cache;
+    p.cache_row = cache_row;
+    p.kv_idx = kv_idx;
+    p.cache_rows = cache_rows;
+    p.bad = bad;
+    rc = mmv_dispatch_fused(MMV_EP_ROPE_KV, a, act, amv_stream(stream));
+    if (rc) return rc;
+    return amv_check_launch("amv_gemv_rope_kv_seg");
+}
+
+extern "C" int amv_gemv_swiglu_q8_seg(int wtype, const void* w_gate, const void* w_up, int64_t F, int64_t k,
+                                      const void* act, float* eout, void* act_out, int act_type, int rule,
+                                      unsigned int* counters, void* stream) {
+    int rc = check_common("amv_gemv_swiglu_q8_seg", wtype, w_gate, 2 * F, k, act, 1);
+    if (rc) return rc;
+    AMV_REQUIRE(eout && act_out && counters, "amv_gemv_swiglu_q8_seg: null pointer");
+    AMV_REQUIRE(act_type == AMV_T_Q8_0 || act_type == AMV_T_Q8_K,
+                "amv_gemv_swiglu_q8_seg: act_type %d (Q8_0 or Q8_K)", act_type);
+    AMV_REQUIRE(F > 0 && F % (act_type == AMV_T_Q8_K ? 256 : 32) == 0,
+                "amv_gemv_swiglu_q8_seg: F must be a multiple of the block size");
+    AMV_REQUIRE(((uintptr_t)act_out & 15) == 0 && ((uintptr_t)eout & 15) == 0,
+                "amv_gemv_swiglu_q8_seg: act_out and eout must be 16-byte aligned");
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_gemv_swiglu_q8_seg: bad rule");
+    MmvArgs a{wtype, (const uint8_t*)w_gate, (int)(2 * F), (int)k, nullptr, nullptr, nullptr, nullptr, nullptr,
+              nullptr, eout};
+    MmvPost& p = a.post;
+    const void* ws[2] = {w_gate, w_up};
+    const int64_t rows[2] = {F, F};
+    rc = mmv_segments("amv_gemv_swiglu_q8_seg", p, 2, ws, rows, wtype, k);
+    if (rc) return rc;
+    p.counters = counters;
+    p.act = amv_act_out(act_out, F, act_type, rule);
+    rc = mmv_dispatch_fused(MMV_EP_SWIGLU_Q8, a, act, amv_stream(stream));
+    if (rc) return rc;
+    return amv_check_launch("amv_gemv_swiglu_q8_seg");
 }
 
 extern "C" int amv_gemv_add_rms_norm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst,

@@ -266,12 +266,16 @@ struct Replay {
     }
 };
 
+// arrival counters for gate/up GEMVs of up to 2 x 65536 rows (AMV_SWIGLU_COUNTER_WORDS)
+#define AMEVA_COUNTER_WORDS AMV_SWIGLU_COUNTER_WORDS(2 * 65536)
+
 struct Device {
     std::mutex compute_mu;
     hipStream_t stream = nullptr;
     Arena arena;
     Replay replay;
     unsigned int* status = nullptr;       // bad-index counter of SET_ROWS / GET_ROWS
+    unsigned int* counters = nullptr;     // arrival counters of the fused gate/up GEMV's tail (zero between calls)
     unsigned int* status_host = nullptr;  // pinned copy of it, written by the graph's last copy
     std::vector<hipEvent_t> events;  // AMEVA_PROFILE=2: one after every node of a graph (grows, reused)
     bool inited = false;
@@ -289,6 +293,9 @@ struct Device {
         if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess) return false;
         if (hipMalloc(&status, 256) != hipSuccess) return false;
         if (hipHostMalloc((void**)&status_host, 256, hipHostMallocDefault) != hipSuccess) return false;
+        if (hipMalloc(&counters, AMEVA_COUNTER_WORDS * 4) != hipSuccess ||
+            hipMemset(counters, 0, AMEVA_COUNTER_WORDS * 4) != hipSuccess)
+            return false;
         inited = true;
         g_cnt.ctx_create++;
         return true;
@@ -614,7 +621,7 @@ struct Engine {
     // ep: the fused next node (ADD, or GLU SWIGLU split) of a one-row MUL_MAT, computed in the GEMV's epilogue
     bool mul_mat(const ggml_tensor* n, const ggml_tensor* ep = nullptr) {
         const ggml_tensor *w = n->src[0], *x = n->src[1];
-        const int64_t N = w->ne[1], K = w->ne[0], M = nrows(x);
+        const int64_t K = w->ne[0], M = nrows(x);
         // batched (M >= 8) MUL_MATs run on the matrix cores for Q4_0 / Q8_0 / Q4_K / Q6_K (the reference's switch at
         // AMEVA_QGEMM_MIN_M). Above 64 tokens the exact form (exact per-block integer sums, ggml's f32 epilogue: the
         // reference's MMQ arithmetic) reads the plain Q8_0 / Q8_K layout; Q4_K batches of 8..64 tokens read the f16
@@ -626,8 +633,20 @@ struct Engine {
         const int atype = deq ? (kq ? AMV_ACT_Q8_K_DEQ : AMV_ACT_Q8_0_DEQ)
                         : (mmq && w->type == GGML_TYPE_Q4_K && M <= 64) ? AMV_ACT_Q8_K_MMA
                         : kq ? (int)GGML_TYPE_Q8_K : (int)GGML_TYPE_Q8_0;
-        // src0 in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized tensor of any
-        // other buffer is repacked into scratch for this use
+        const void* wp = weight_ptr(n);
+        if (!wp) return false;
+        if (g_fail.load() == AMEVA_FAIL_MAP_SRC1) return fail(n, "failure injection: src1");
+        void* act = act_for(n, x, atype, M, K);
+        if (!act) return false;
+        if (g_fail.load() == AMEVA_FAIL_DISPATCH) return fail(n, "failure injection: dispatch");
+        return mul_mat_run(n, ep, wp, act, atype, M, mmq);
+    }
+
+    // src0 of a MUL_MAT in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized
+    // tensor of any other buffer is repacked into scratch for this use. NULL (and the engine failed) on error.
+    const void* weight_ptr(const ggml_tensor* n) {
+        const ggml_tensor* w = n->src[0];
+        const int64_t N = w->ne[1], K = w->ne[0];
         const void* wp = w->data;
         BufCtx* bc = (BufCtx*)w->buffer->context;
         if (w->view_src) {
@@ -638,34 +657,37 @@ struct Engine {
             const uint8_t* src = (const uint8_t*)w->data;
             if (bc->repacked.count(p->data)) {
                 uint8_t* raw = (uint8_t*)dev->arena.take(nbytes(p));
-                if (!raw) return fail(n, "scratch exhausted");
-                if (!rc(n, amv_unrepack(p->type, p->data, raw, p->ne[1], p->ne[0], st))) return false;
+                if (!raw) return fail(n, "scratch exhausted"), nullptr;
+                if (!rc(n, amv_unrepack(p->type, p->data, raw, p->ne[1], p->ne[0], st))) return nullptr;
                 src = raw + w->view_offs;
             }
             void* tmp = dev->arena.take(nbytes(w));
-            if (!tmp) return fail(n, "scratch exhausted");
-            if (!rc(n, amv_repack(w->type, src, tmp, N, K, st))) return false;
+            if (!tmp) return fail(n, "scratch exhausted"), nullptr;
+            if (!rc(n, amv_repack(w->type, src, tmp, N, K, st))) return nullptr;
             wp = tmp;
         } else {
             std::lock_guard<std::mutex> lk(bc->mu);
             if (!bc->repacked.count(w->data)) {
                 if (w->buffer->usage == GGML_BACKEND_BUFFER_USAGE_WEIGHTS && repackable(w)) {
-                    if (!convert_in_place(const_cast<ggml_tensor*>(w), true)) return fail(n, "weight repack failed");
+                    if (!convert_in_place(const_cast<ggml_tensor*>(w), true)) return fail(n, "weight repack failed"), nullptr;
                     bc->repacked[w->data] = w->type;
                     g_cnt.repacked_tensors++;
                     g_cnt.repacked_bytes += (int64_t)nbytes(w);
                 } else {
                     void* tmp = dev->arena.take(nbytes(w));
-                    if (!tmp) return fail(n, "scratch exhausted");
-                    if (!rc(n, amv_repack(w->type, w->data, tmp, N, K, st))) return false;
+                    if (!tmp) return fail(n, "scratch exhausted"), nullptr;
+                    if (!rc(n, amv_repack(w->type, w->data, tmp, N, K, st))) return nullptr;
                     wp = tmp;
                 }
             }
         }
-        if (g_fail.load() == AMEVA_FAIL_MAP_SRC1) return fail(n, "failure injection: src1");
-        void* act = act_for(n, x, atype, M, K);
-        if (!act) return false;
-        if (g_fail.load() == AMEVA_FAIL_DISPATCH) return fail(n, "failure injection: dispatch");
+        return wp;
+    }
+
+    bool mul_mat_run(const ggml_tensor* n, const ggml_tensor* ep, const void* wp, void* act, int atype, int64_t M,
+                     bool mmq) {
+        const ggml_tensor *w = n->src[0];
+        const int64_t N = w->ne[1], K = w->ne[0];
         int r;
         if (ep) {
             const ggml_tensor* e = ep->src[0] == n ? ep->src[1] : ep->src[0];
@@ -885,6 +907,174 @@ struct Engine {
         return k;
     }
 
+    // ---- node groups of llama.cpp's decode layer that run as one launch (recognised at their first node)
+    static const ggml_tensor* root(const ggml_tensor* t) { return t->view_src ? t->view_src : t; }
+    // a node outside `group` (graph indices) computes from t or a view of it
+    bool read_outside(const ggml_tensor* t, const std::vector<int>& group) const {
+        for (int i = 0; i < graph->n_nodes; ++i) {
+            const ggml_tensor* c = graph->nodes[i];
+            if (noop(c->op) || std::find(group.begin(), group.end(), i) != group.end()) continue;
+            for (int j = 0; j < GGML_MAX_SRC; ++j)
+                if (c->src[j] && root(c->src[j]) == t) return true;
+        }
+        return false;
+    }
+    static bool gemv_q4(const ggml_tensor* c, const ggml_tensor* x) {  // one-row Q4_0 / Q4_K MUL_MAT of x
+        const ggml_tensor* w = c->src[0];
+        if (c->op != GGML_OP_MUL_MAT || c->src[1]->data != x->data || nbytes(c->src[1]) != nbytes(x) ||
+            nrows(c->src[1]) != 1 || c->src[1]->type != GGML_TYPE_F32 || w->view_src || w->ne[1] % 2 != 0)
+            return false;
+        if (w->type == GGML_TYPE_Q4_0) return w->ne[0] % 4096 == 0;
+        return w->type == GGML_TYPE_Q4_K && w->ne[0] % 256 == 0;
+    }
+
+    // q, k, v MUL_MATs of one activation row, ROPE NORMAL of q and k over whole heads at one position, SET_ROWS of
+    // k (roped) and v into f16 caches at one row, nothing else in between: amv_gemv_rope_kv_seg
+    struct QkvGroup {
+        const ggml_tensor *mq, *mk, *mv, *rq, *rk, *sk, *sv;
+        int last;
+    };
+    bool match_qkv(int i, QkvGroup& f) const {
+        const ggml_tensor* n0 = graph->nodes[i];
+        const ggml_tensor* x = n0->src[1];
+        if (!gemv_q4(n0, x)) return false;
+        const ggml_tensor *mm[3], *ro[2], *sr[2];
+        int nm = 0, nr = 0, ns = 0;
+        std::vector<int> group;
+        for (int j = i; j < graph->n_nodes && j < i + 32 && !(nm == 3 && nr == 2 && ns == 2); ++j) {
+            const ggml_tensor* c = graph->nodes[j];
+            if (!noop(c->op)) {
+                if (nm < 3 && gemv_q4(c, x) && c->src[0]->type == n0->src[0]->type && c->src[0]->ne[0] == n0->src[0]->ne[0])
+                    mm[nm++] = c;
+                else if (nr < 2 && c->op == GGML_OP_ROPE)
+                    ro[nr++] = c;
+                else if (ns < 2 && c->op == GGML_OP_SET_ROWS)
+                    sr[ns++] = c;
+                else
+                    return false;
+            }
+            group.push_back(j);
+            f.last = j;
+        }
+        if (!(nm == 3 && nr == 2 && ns == 2)) return false;
+        f.rk = f.rq = f.sk = f.sv = nullptr;
+        for (int a = 0; a < 2; ++a)
+            for (int b = 0; b < 2; ++b)
+                if (root(sr[b]->src[0]) == ro[a]) {
+                    f.rk = ro[a], f.rq = ro[1 - a], f.sk = sr[b], f.sv = sr[1 - b];
+                }
+        if (!f.rk) return false;
+        f.mq = f.mk = f.mv = nullptr;
+        for (int a = 0; a < 3; ++a) {
+            if (root(f.rq->src[0]) == mm[a]) f.mq = mm[a];
+            else if (root(f.rk->src[0]) == mm[a]) f.mk = mm[a];
+            else if (root(f.sv->src[0]) == mm[a]) f.mv = mm[a];
+        }
+        if (!f.mq || !f.mk || !f.mv) return false;
+        const ggml_tensor *qi = f.rq->src[0], *ki = f.rk->src[0], *pos = f.rq->src[1], *idx = f.sk->src[1];
+        const int64_t D = qi->ne[0], nh = qi->ne[1], nkv = ki->ne[1];
+        if (ki->ne[0] != D || qi->ne[2] != 1 || ki->ne[2] != 1 || D % 2 != 0) return false;
+        for (const ggml_tensor* r : {f.rq, f.rk})
+            if (r->op_params[2] != 0 || r->op_params[1] != D || r->type != GGML_TYPE_F32 || !is_contiguous(r) ||
+                !is_contiguous(r->src[0]))
+                return false;
+        if (f.rk->src[1] != pos || pos->type != GGML_TYPE_I32 || nelements(pos) != 1) return false;
+        for (int p : {5, 6, 8})
+            if (op_f32(f.rq, p) != op_f32(f.rk, p)) return false;
+        if (f.mq->ne[0] != nh * D || f.mk->ne[0] != nkv * D || f.mv->ne[0] != nkv * D) return false;
+        if (f.sv->src[1] != idx || idx->type != GGML_TYPE_I64 || nelements(idx) != 1) return false;
+        for (const ggml_tensor* c : {f.sk, f.sv})
+            if (c->type != GGML_TYPE_F16 || c->ne[0] != nkv * D || c->nb[0] != 2 || nrows(c->src[0]) != 1 ||
+                c->src[0]->type != GGML_TYPE_F32 || !is_contiguous(c->src[0]))
+                return false;
+        if (f.sk->nb[1] != f.sv->nb[1] || f.sk->ne[1] != f.sv->ne[1] || f.sk->nb[1] % 2 != 0) return false;
+        if (!is_contiguous(f.mv)) return false;
+        // the un-rotated q and k exist only inside the launch
+        return !read_outside(f.mq, group) && !read_outside(f.mk, group);
+    }
+    bool run_qkv(const QkvGroup& f) {
+        const ggml_tensor* x = f.mq->src[1];
+        const int wt = f.mq->src[0]->type;
+        const int64_t K = f.mq->src[0]->ne[0];
+        const ggml_tensor *qi = f.rq->src[0], *ki = f.rk->src[0];
+        const void* wq = weight_ptr(f.mq);
+        const void* wk = wq ? weight_ptr(f.mk) : nullptr;
+        const void* wv = wk ? weight_ptr(f.mv) : nullptr;
+        if (!wv) return false;
+        const int atype = wt == GGML_TYPE_Q4_K ? (int)GGML_TYPE_Q8_K : (int)GGML_TYPE_Q8_0;
+        void* act = act_for(f.mq, x, atype, 1, K);
+        if (!act) return false;
+        if (!rc(f.mq, amv_gemv_rope_kv_seg(wt, wq, wk, wv, K, act, (float*)f.rq->data, (float*)f.rk->data,
+                                           (float*)f.mv->data, qi->ne[1], ki->ne[1], qi->ne[0],
+                                           (const int32_t*)f.rq->src[1]->data, op_f32(f.rq, 5), op_f32(f.rq, 6),
+                                           op_f32(f.rq, 8), f.sk->data, f.sv->data, (int64_t)f.sk->nb[1] / 2,
+                                           (const int64_t*)f.sk->src[1]->data, f.sk->ne[1], dev->status, st)))
+            return false;
+        g_cnt.mul_mat += 3;
+        g_cnt.qmv += 3;
+        g_cnt.fused += 6;  // k, v, both ROPEs and both SET_ROWS ride on the q launch
+        return true;
+    }
+
+    // gate and up MUL_MATs of one activation row and the GLU SWIGLU of their results, the product read by a later
+    // one-row GEMV: amv_gemv_swiglu_q8_seg, which also writes that GEMV's activation row
+    struct GateUp {
+        const ggml_tensor *gate, *up, *glu;
+        int last, atype;
+    };
+    bool match_gate_up(int i, GateUp& f) const {
+        const ggml_tensor* n0 = graph->nodes[i];
+        const ggml_tensor* x = n0->src[1];
+        if (!gemv_q4(n0, x)) return false;
+        std::vector<int> group{i};
+        int j = i + 1;
+        while (j < graph->n_nodes && noop(graph->nodes[j]->op)) group.push_back(j++);
+        if (j >= graph->n_nodes) return false;
+        const ggml_tensor* n1 = graph->nodes[j];
+        if (!gemv_q4(n1, x) || n1->src[0]->type != n0->src[0]->type || n1->src[0]->ne[0] != n0->src[0]->ne[0] ||
+            n1->src[0]->ne[1] != n0->src[0]->ne[1])
+            return false;
+        group.push_back(j++);
+        while (j < graph->n_nodes && noop(graph->nodes[j]->op)) group.push_back(j++);
+        if (j >= graph->n_nodes) return false;
+        const ggml_tensor* e = graph->nodes[j];
+        if (e->op != GGML_OP_GLU || !e->src[1] || e->op_params[0] != GGML_GLU_OP_SWIGLU) return false;
+        if (!((e->src[0] == n0 && e->src[1] == n1) || (e->src[0] == n1 && e->src[1] == n0))) return false;
+        group.push_back(j);
+        const int64_t F = n0->src[0]->ne[1];
+        if (F > 65536 || e->type != GGML_TYPE_F32 || nelements(e) != F || !is_contiguous(e) || !aligned16(e->data))
+            return false;
+        const bool swapped = e->op_params[1] != 0;  // swapped: silu(src1) * src0
+        f.gate = swapped ? e->src[1] : e->src[0];
+        f.up = swapped ? e->src[0] : e->src[1];
+        f.glu = e;
+        f.last = j;
+        f.atype = gemv_act_type(j + 1, e);
+        if (!f.atype || F % (f.atype == (int)GGML_TYPE_Q8_K ? 256 : 32) != 0) return false;
+        return !read_outside(n0, group) && !read_outside(n1, group);
+    }
+    bool run_gate_up(const GateUp& f) {
+        const ggml_tensor* x = f.gate->src[1];
+        const int wt = f.gate->src[0]->type;
+        const int64_t K = f.gate->src[0]->ne[0], F = f.gate->src[0]->ne[1];
+        const void* wg = weight_ptr(f.gate);
+        const void* wu = wg ? weight_ptr(f.up) : nullptr;
+        if (!wu) return false;
+        const int atype = wt == GGML_TYPE_Q4_K ? (int)GGML_TYPE_Q8_K : (int)GGML_TYPE_Q8_0;
+        void* act = act_for(f.gate, x, atype, 1, K);
+        if (!act) return false;
+        void* act_out = fused_act(f.glu, f.glu, f.atype);
+        if (!act_out) return false;
+        if (!rc(f.gate, amv_gemv_swiglu_q8_seg(wt, wg, wu, F, K, act, (float*)f.glu->data, act_out, f.atype,
+                                               AMV_Q8_X86, dev->counters, st)))
+            return false;
+        pending_act = {f.glu->data, nbytes(f.glu), f.atype, 1, F, act_out};
+        g_cnt.mul_mat += 2;
+        g_cnt.qmv += 2;
+        g_cnt.fused += 2;  // up and SWIGLU ride on the gate launch
+        return true;
+    }
+
     bool run(ggml_cgraph* g) {
         graph = g;
         const bool prof = profile_level() >= 2;
@@ -897,6 +1087,35 @@ struct Engine {
             if (noop(n->op)) continue;
             const ggml_tensor* first = n;
             bool ok = true;
+            if (n->op == GGML_OP_MUL_MAT && g_fail.load() == AMEVA_FAIL_NONE) {
+                QkvGroup qg;
+                GateUp gu;
+                int last = -1;
+                if (match_qkv(i, qg)) {
+                    ok = run_qkv(qg);
+                    last = qg.last;
+                } else if (match_gate_up(i, gu)) {
+                    ok = run_gate_up(gu);
+                    last = gu.last;
+                }
+                if (last >= 0) {
+                    if (!ok) return false;
+                    for (int j = i; j <= last; ++j) invalidate(g->nodes[j]);
+                    if (pending_act.act) {
+                        acts.push_back(pending_act);
+                        pending_act = {};
+                    }
+                    g_cnt.gpu_op++;
+                    encoded++;
+                    if (prof) {
+                        labels.push_back(kind_of(first, g->nodes[last]));
+                        hipEvent_t ev = dev->event(labels.size());
+                        if (!ev || hipEventRecord(ev, st) != hipSuccess) return fail(n, "profile event");
+                    }
+                    i = last;
+                    continue;
+                }
+            }
             switch (n->op) {
             case GGML_OP_MUL_MAT: {
                 const ggml_tensor* e = fusable_epilogue(g, i);
@@ -1245,6 +1464,8 @@ void ggml_backend_ameva_teardown(void) {
         d->replay.drop();
         d->replay.sig.clear();
         (void)hipFree(d->status);
+        (void)hipFree(d->counters);
+        d->counters = nullptr;
         (void)hipHostFree(d->status_host);
         d->status_host = nullptr;
         (void)hipStreamDestroy(d->stream);

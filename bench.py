@@ -252,14 +252,16 @@ def bench_layer(torch, dev, args):
             "layer_decode_note": "Llama-3-8B layer, Q4_0, bs1, 4096 cached keys, 4 chained cold layers in one HIP graph"}
 
 
-def bench_plugin_layer(torch, dev):
-    """bs1 decode of the Llama-3-8B-shape Q4_0 layer at 4096 cached keys through the drop-in boundary: the ggml graph
-    llama.cpp builds for one layer (RMS_NORM, MUL, q/k/v MUL_MATs, ROPE, SET_ROWS into the f16 cache, FLASH_ATTN_EXT,
-    o MUL_MAT + ADD, RMS_NORM, MUL, gate/up MUL_MATs, SWIGLU, down MUL_MAT + ADD) handed to libggml-ameva.so's
-    graph_compute, which runs it eagerly on its stream and returns after the stream completes (as the reference's
-    ggml_backend_graph_compute does, adapters/llama/ameva_backend_bench.cpp:38-79). The ggml host side is the
-    stand-in the plugin tests use (tests/ggml_plugin.py: ggml's structs and the buffer calls the plugin binds to).
-    Weights: random Q4_0 blocks (d = 0.01). Reported per layer: wall time of one graph_compute call."""
+def bench_plugin_layer(torch, dev, layers=4):
+    """bs1 decode of Llama-3-8B-shape Q4_0 layers at 4096 cached keys through the drop-in boundary: the ggml graph
+    llama.cpp builds per layer (RMS_NORM, MUL, q/k/v MUL_MATs, ROPE, SET_ROWS into the f16 cache, FLASH_ATTN_EXT,
+    o MUL_MAT + ADD, RMS_NORM, MUL, gate/up MUL_MATs, SWIGLU, down MUL_MAT + ADD), `layers` of them chained in one
+    graph (each with its own weights and KV cache: 4 x 140 MB, more than the 256 MB Infinity Cache, so the weights
+    stream from HBM as in a whole model), handed to libggml-ameva.so's graph_compute, which runs it on its stream and
+    returns after the stream completes (as the reference's ggml_backend_graph_compute does,
+    adapters/llama/ameva_backend_bench.cpp:38-79). The ggml host side is the stand-in the plugin tests use
+    (tests/ggml_plugin.py: ggml's structs and the buffer calls the plugin binds to). Weights: random Q4_0 blocks
+    (d = 0.01). Reported: wall time of one graph_compute call, and that time per layer."""
     import ctypes
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -272,19 +274,11 @@ def bench_plugin_layer(torch, dev):
         w = np.frombuffer(rng.bytes(n * (k // 32) * 18), np.uint8).reshape(n, k // 32, 18).copy()
         w[:, :, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
         return w.reshape(n, -1)
-    w = {"q": wq4(NH * D, H), "k": wq4(NKV * D, H), "v": wq4(NKV * D, H), "o": wq4(H, NH * D),
-         "gate": wq4(FF, H), "up": wq4(FF, H), "down": wq4(H, FF)}
-    g = gp.Graph(sum(a.nbytes for a in w.values()) + 16 * 4096, 96 << 20)
+    shapes = {"q": (NH * D, H), "k": (NKV * D, H), "v": (NKV * D, H), "o": (H, NH * D), "gate": (FF, H),
+              "up": (FF, H), "down": (H, FF)}
+    wbytes = sum(n * (k // 32) * 18 for n, k in shapes.values())
+    g = gp.Graph(layers * (wbytes + 16 * 4096), (64 << 20) + layers * (32 << 20))
     try:
-        T = {k_: g.tensor(gp.Q4_0, [a.shape[1] * 32 // 18, a.shape[0]], "w", k_) for k_, a in w.items()}
-        for k_, a in w.items():
-            g.set(T[k_], a)
-        AN, FN = g.tensor(gp.F32, [H], "w", "attn_norm"), g.tensor(gp.F32, [H], "w", "ffn_norm")
-        g.set(AN, (1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
-        g.set(FN, (1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
-        KC, VC = g.tensor(gp.F16, [NKV * D, CTX], "c", "k_cache"), g.tensor(gp.F16, [NKV * D, CTX], "c", "v_cache")
-        g.set(KC, rng.standard_normal((CTX, NKV * D)).astype(np.float16))
-        g.set(VC, rng.standard_normal((CTX, NKV * D)).astype(np.float16))
         X = g.tensor(gp.F32, [H, 1], "c", "inp")
         g.set(X, rng.standard_normal((1, H)).astype(np.float32))
         POS = g.tensor(gp.I32, [1], "c", "pos")
@@ -293,21 +287,35 @@ def bench_plugin_layer(torch, dev):
         g.set(IDX, np.array([pos_t], np.int64))
         MASK = g.tensor(gp.F16, [CTX, 1], "c", "mask")
         g.set(MASK, np.zeros(CTX, np.float16))
-        cur = g.mul(g.rms_norm(X, 1e-5), AN)
-        q = g.rope(g.reshape_3d(g.mul_mat(T["q"], cur), D, NH, 1), POS, D, 0, 500000.0)
-        k = g.rope(g.reshape_3d(g.mul_mat(T["k"], cur), D, NKV, 1), POS, D, 0, 500000.0)
-        v = g.mul_mat(T["v"], cur)
-        g.set_rows(KC, g.view_nd(k, gp.OP_RESHAPE, [NKV * D, 1], [4, NKV * D * 4, NKV * D * 4, NKV * D * 4]), IDX)
-        g.set_rows(VC, v, IDX)
-        kv_nb = [2, NKV * D * 2, D * 2, NKV * D * 2 * CTX]
-        att = g.flash_attn_ext(g.view_nd(q, gp.OP_PERMUTE, [D, 1, NH], [4, D * NH * 4, D * 4, D * NH * 4]),
-                               g.view_nd(KC, gp.OP_VIEW, [D, CTX, NKV], kv_nb),
-                               g.view_nd(VC, gp.OP_VIEW, [D, CTX, NKV], kv_nb), MASK, 1.0 / np.sqrt(D))
-        ffn_inp = g.add(g.mul_mat(T["o"], g.view_nd(att, gp.OP_RESHAPE, [H, 1], [4, H * 4, H * 4, H * 4])), X)
-        cur = g.mul(g.rms_norm(ffn_inp, 1e-5), FN)
-        ff = g.swiglu(g.mul_mat(T["gate"], cur), g.mul_mat(T["up"], cur))
-        g.add(g.mul_mat(T["down"], ff), ffn_inp)
-        for _ in range(5):  # the first call repacks the weights in place
+        x = X
+        for _ in range(layers):
+            T = {}
+            for k_, (n, k) in shapes.items():
+                T[k_] = g.tensor(gp.Q4_0, [k, n], "w", k_)
+                g.set(T[k_], wq4(n, k))
+            AN, FN = g.tensor(gp.F32, [H], "w", "attn_norm"), g.tensor(gp.F32, [H], "w", "ffn_norm")
+            g.set(AN, (1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+            g.set(FN, (1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+            KC = g.tensor(gp.F16, [NKV * D, CTX], "c", "k_cache")
+            VC = g.tensor(gp.F16, [NKV * D, CTX], "c", "v_cache")
+            g.set(KC, rng.standard_normal((CTX, NKV * D)).astype(np.float16))
+            g.set(VC, rng.standard_normal((CTX, NKV * D)).astype(np.float16))
+            cur = g.mul(g.rms_norm(x, 1e-5), AN)
+            q = g.rope(g.reshape_3d(g.mul_mat(T["q"], cur), D, NH, 1), POS, D, 0, 500000.0)
+            k = g.rope(g.reshape_3d(g.mul_mat(T["k"], cur), D, NKV, 1), POS, D, 0, 500000.0)
+            v = g.mul_mat(T["v"], cur)
+            g.set_rows(KC, g.view_nd(k, gp.OP_RESHAPE, [NKV * D, 1], [4, NKV * D * 4, NKV * D * 4, NKV * D * 4]),
+                       IDX)
+            g.set_rows(VC, v, IDX)
+            kv_nb = [2, NKV * D * 2, D * 2, NKV * D * 2 * CTX]
+            att = g.flash_attn_ext(g.view_nd(q, gp.OP_PERMUTE, [D, 1, NH], [4, D * NH * 4, D * 4, D * NH * 4]),
+                                   g.view_nd(KC, gp.OP_VIEW, [D, CTX, NKV], kv_nb),
+                                   g.view_nd(VC, gp.OP_VIEW, [D, CTX, NKV], kv_nb), MASK, 1.0 / np.sqrt(D))
+            ffn_inp = g.add(g.mul_mat(T["o"], g.view_nd(att, gp.OP_RESHAPE, [H, 1], [4, H * 4, H * 4, H * 4])), x)
+            cur = g.mul(g.rms_norm(ffn_inp, 1e-5), FN)
+            ff = g.swiglu(g.mul_mat(T["gate"], cur), g.mul_mat(T["up"], cur))
+            x = g.add(g.mul_mat(T["down"], ff), ffn_inp)
+        for _ in range(5):  # the first call repacks the weights in place, the second captures the HIP graph
             assert g.compute() == gp.STATUS_SUCCESS
         g.plugin.ggml_backend_ameva_reset_counters()
         # the cgraph of the last call, handed over again as a host would (no Python rebuilding per call)
@@ -321,12 +329,16 @@ def bench_plugin_layer(torch, dev):
         fused = gp.counter(g.plugin, "fused_pair_count") // n
     finally:
         g.free()
-    log(f"bench: plugin layer decode (graph_compute, {nodes} ggml nodes, {fused} fused pairs) {el * 1e6:.2f} us/layer")
-    return {"plugin_layer_decode_us": round(el * 1e6, 2), "plugin_layer_decode_tok_s": round(1.0 / el, 1),
-            "plugin_layer_decode_nodes": nodes, "plugin_layer_decode_fused_pairs": fused,
-            "plugin_layer_decode_note": "one Llama-3-8B Q4_0 layer graph, bs1, 4096 cached keys, through "
-                                        "libggml-ameva.so graph_compute (synchronous per call; the unchanged graph "
-                                        "replays its HIP-graph capture)"}
+    per = el / layers
+    log(f"bench: plugin decode, {layers} layers in one graph_compute ({nodes} ggml nodes, {fused} fused) "
+        f"{el * 1e6:.2f} us/call = {per * 1e6:.2f} us/layer")
+    return {"plugin_layer_decode_us": round(per * 1e6, 2), "plugin_layer_decode_tok_s": round(1.0 / per, 1),
+            "plugin_graph_compute_us": round(el * 1e6, 2), "plugin_graph_layers": layers,
+            "plugin_graph_nodes": nodes, "plugin_graph_fused_nodes": fused,
+            "plugin_layer_decode_note": f"{layers} chained Llama-3-8B Q4_0 layers (cold weights) in one ggml graph, "
+                                        "bs1, 4096 cached keys, through libggml-ameva.so graph_compute (synchronous "
+                                        "per call; the unchanged graph replays its HIP-graph capture); per layer = "
+                                        "call time / layers"}
 
 
 BLOCK_BYTES = {2: 18, 8: 34, 12: 144 * 32 // 256, 14: 210 * 32 // 256}  # bytes per 32 weights

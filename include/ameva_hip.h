@@ -145,6 +145,19 @@ int amv_gemv_add_rms_norm(int wtype, const void* w, int64_t n_rows, int64_t k, c
  * the last workgroup producing it. = MUL_MAT x 2 + SWIGLU + the next quantization. */
 int amv_gemv_swiglu_q8(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, float* dst, float* eout,
                        void* act_out, int act_type, int rule, unsigned int* counters, void* stream);
+/* The same two fused GEMVs over separate weights (no counterpart in the reference; for the ggml plugin, whose q, k,
+ * v and gate, up weights are separate ggml tensors, each in its own repacked layout): Q4_0 (k % 4096 == 0) or Q4_K,
+ * every matrix with an even row count. amv_gemv_rope_kv_seg: wq / wk / wv with n_head * D, n_head_kv * D and
+ * n_head_kv * D rows; the rotated q and k and the v values go to q_out / k_out / v_out (the cache rows as in
+ * amv_gemv_rope_kv). amv_gemv_swiglu_q8_seg: w_gate and w_up of F rows each (counters as amv_gemv_swiglu_q8 with
+ * n_rows = 2 F); no dst. Results are those of the stacked calls over the concatenated rows, bit for bit. */
+int amv_gemv_rope_kv_seg(int wtype, const void* wq, const void* wk, const void* wv, int64_t k, const void* act,
+                         float* q_out, float* k_out, float* v_out, int64_t n_head, int64_t n_head_kv, int64_t D,
+                         const int32_t* pos, float freq_base, float freq_scale, float attn_factor, void* k_cache,
+                         void* v_cache, int64_t cache_row, const int64_t* kv_idx, int64_t cache_rows,
+                         unsigned int* bad, void* stream);
+int amv_gemv_swiglu_q8_seg(int wtype, const void* w_gate, const void* w_up, int64_t F, int64_t k, const void* act,
+                           float* eout, void* act_out, int act_type, int rule, unsigned int* counters, void* stream);
 
 /* Parity instrumentation of the same kernels: the exact integer sums per weight block, int32
  * [m][n_rows][nblk * per] with nblk = k / block size, per = 2 for Q4_K (sum sc*dot, sum m*bsum) and 1 otherwise.

@@ -158,3 +158,62 @@ def test_flash_attn_decode_ex(dev, ops, orc, n_head, n_head_kv, n_kv_max, n_kv, 
     # without n_kv_dev the launch's n_kv_max keys are used
     full = ops.flash_attn_decode_ex(q, kh, vh, scale, n_kv_max, None)
     assert torch.equal(full, ops.flash_attn_decode(q, kh, vh, scale, n_kv=n_kv_max))
+
+
+@pytest.mark.parametrize("wtype", [2, 12])
+@pytest.mark.parametrize("n_head,n_head_kv,D", [(32, 8, 128), (8, 2, 64)])
+def test_gemv_rope_kv_seg(dev, ops, orc, wtype, n_head, n_head_kv, D):
+    """q, k, v as three matrices (each repacked on its own, as the plugin holds separate ggml weights): the same bits
+    as the stacked launch over their rows, in the three outputs and both cache rows."""
+    rng = np.random.default_rng(n_head * 3 + D + wtype)
+    H = 4096 if wtype == 2 else 512
+    n = (n_head + 2 * n_head_kv) * D
+    nq, kv = n_head * D, n_head_kv * D
+    wg = weight(rng, orc, wtype, n, H)
+    w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, H)
+    parts = [ops.QWeight.from_ggml(wtype, gpu(np.ascontiguousarray(wg[a:b]), dev), b - a, H)
+             for a, b in ((0, nq), (nq, nq + kv), (nq + kv, n))]
+    act = act_of(ops, gpu(rng.standard_normal(H).astype(np.float32), dev), ops.act_type(wtype))
+    CTX = 40
+    kc = gpu(rng.standard_normal((CTX, kv)).astype(np.float16), dev)
+    vc = gpu(rng.standard_normal((CTX, kv)).astype(np.float16), dev)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    pos = torch.tensor([777], dtype=torch.int32, device=dev)
+    idx = torch.tensor([5], dtype=torch.int64, device=dev)
+    qkv_ref = ops.gemv_rope_kv(w, act, n_head, n_head_kv, pos, kc_ref, vc_ref, idx)
+    outs = [torch.empty(p.n_rows, dtype=torch.float32, device=dev) for p in parts]
+    lib = ops.lib()
+    rc = lib.amv_gemv_rope_kv_seg(wtype, parts[0].data.data_ptr(), parts[1].data.data_ptr(), parts[2].data.data_ptr(),
+                                  H, act.data_ptr(), outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(),
+                                  n_head, n_head_kv, D, pos.data_ptr(), 500000.0, 1.0, 1.0, kc.data_ptr(),
+                                  vc.data_ptr(), kv, idx.data_ptr(), CTX, None, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.amv_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat(outs), qkv_ref)
+    assert torch.equal(kc.view(torch.int16), kc_ref.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), vc_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("wtype,F,k,act_t", [(2, 14336, 4096, 8), (12, 14336, 4096, 15), (2, 64, 4096, 8),
+                                             (12, 512, 256, 15)])
+def test_gemv_swiglu_act_seg(dev, ops, orc, wtype, F, k, act_t):
+    """gate and up as two matrices: the same SWIGLU values and activation row as the stacked launch."""
+    rng = np.random.default_rng(F + k + wtype + 1)
+    wg = weight(rng, orc, wtype, 2 * F, k)
+    w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), 2 * F, k)
+    wgate = ops.QWeight.from_ggml(wtype, gpu(np.ascontiguousarray(wg[:F]), dev), F, k)
+    wup = ops.QWeight.from_ggml(wtype, gpu(np.ascontiguousarray(wg[F:]), dev), F, k)
+    act = act_of(ops, gpu(rng.standard_normal(k).astype(np.float32), dev), ops.act_type(wtype))
+    _, h_ref, a_ref = ops.gemv_swiglu_act(w, act, act_t)
+    h = torch.empty(F, dtype=torch.float32, device=dev)
+    a = torch.empty(ops.lib().amv_act_bytes(act_t, 1, F), dtype=torch.uint8, device=dev)
+    cnt = torch.zeros(ops.swiglu_counter_words(2 * F), dtype=torch.int32, device=dev)
+    lib = ops.lib()
+    for _ in range(2):
+        rc = lib.amv_gemv_swiglu_q8_seg(wtype, wgate.data.data_ptr(), wup.data.data_ptr(), F, k, act.data_ptr(),
+                                        h.data_ptr(), a.data_ptr(), act_t, 0, cnt.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.amv_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(h, h_ref) and torch.equal(a, a_ref)
+        assert not cnt.any()

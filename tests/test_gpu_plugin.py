@@ -427,10 +427,12 @@ def test_llama3_8b_decode_layer(plugin, orc):
         assert g.compute() == gp.STATUS_SUCCESS
         y = g.get(out, np.float32, (1, H))
         assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 7
-        # RMS_NORM+MUL twice; the o and down projections + residual ADD, the up projection + SWIGLU as GEMV epilogues
-        assert gp.counter(plugin, "fused_pair_count") == 5
-        # q, k, v and gate, up read the rows the two RMS_NORM + MUL write; o reads the one the attention merge writes
-        assert gp.counter(plugin, "act_quant_reuse_count") == 6
+        # nodes run inside another node's launch: the MUL of both RMS_NORM + MUL (2); k, v, both ROPEs and both
+        # SET_ROWS in the q launch (6); up and SWIGLU in the gate launch (2); the residual ADDs of o and down (2)
+        assert gp.counter(plugin, "fused_pair_count") == 12
+        # the q/k/v and gate/up launches read the rows the two RMS_NORM + MUL write, o the one the attention merge
+        # writes, down the one the gate/up launch writes
+        assert gp.counter(plugin, "act_quant_reuse_count") == 4
 
         # the oracle's chain of the same ops
         q8 = lambda a: orc.quantize_q8_0(a, orc.Q8_X86)  # noqa: E731
