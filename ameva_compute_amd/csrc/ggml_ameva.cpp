@@ -276,7 +276,9 @@ struct Device {
     Replay replay;
     unsigned int* status = nullptr;       // bad-index counter of SET_ROWS / GET_ROWS
     unsigned int* counters = nullptr;     // arrival counters of the fused gate/up GEMV's tail (zero between calls)
-    unsigned int* status_host = nullptr;  // pinned copy of it, written by the graph's last copy
+    unsigned int* status_host = nullptr;  // pinned copy of it, written by the graph's last kernel
+    unsigned int* status_host_dev = nullptr;  // the same pinned word as the device addresses it
+    bool status_clean = false;            // status holds zeros (the last run ended with k_status_out)
     std::vector<hipEvent_t> events;  // AMEVA_PROFILE=2: one after every node of a graph (grows, reused)
     bool inited = false;
     hipEvent_t event(size_t i) {
@@ -293,6 +295,9 @@ struct Device {
         if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess) return false;
         if (hipMalloc(&status, 256) != hipSuccess) return false;
         if (hipHostMalloc((void**)&status_host, 256, hipHostMallocDefault) != hipSuccess) return false;
+        if (hipHostGetDevicePointer((void**)&status_host_dev, status_host, 0) != hipSuccess) return false;
+        if (hipMemset(status, 0, 256) != hipSuccess) return false;
+        status_clean = true;
         if (hipMalloc(&counters, AMEVA_COUNTER_WORDS * 4) != hipSuccess ||
             hipMemset(counters, 0, AMEVA_COUNTER_WORDS * 4) != hipSuccess)
             return false;
@@ -1171,8 +1176,15 @@ struct Engine {
     }
 };
 
-// the status word cleared by a kernel, not a memset node, so that a captured graph clears it on every replay
+// The status words are cleared by kernels, not memset nodes: the last kernel of every run (eager or captured) copies
+// the bad-index count to pinned host memory and clears the words for the next run; a run that stopped early leaves
+// them for k_clear_status before the next one.
 __global__ void k_clear_status(unsigned int* s) { s[threadIdx.x] = 0u; }
+__global__ void k_status_out(unsigned int* s, unsigned int* host) {
+    const unsigned int v = s[0];
+    if (threadIdx.x == 0) host[0] = v;
+    s[threadIdx.x] = 0u;
+}
 
 void sig_tensor(std::vector<int64_t>& s, const ggml_tensor* t) {
     s.push_back((int64_t)(uintptr_t)t->data);
@@ -1245,6 +1257,8 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         same = sig == rp.sig && rp.gen == g_layout_gen.load();
         if (same && rp.exec && rp.arena_base != d->arena.base) rp.drop();  // the scratch moved: capture again
     }
+    if (!d->status_clean) hipLaunchKernelGGL(k_clear_status, dim3(1), dim3(64), 0, d->stream, d->status);
+    d->status_clean = false;  // until a run completes through k_status_out
     if (same && rp.exec) {
         if (trace_on()) std::fprintf(stderr, "AMEVA_TRACE graph replay nodes=%d\n", g->n_nodes);
         const bool ok = hipGraphLaunch(rp.exec, d->stream) == hipSuccess;
@@ -1271,9 +1285,8 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         hipGraph_t graph = nullptr;
         bool ok = hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal) == hipSuccess;
         if (ok) {
-            hipLaunchKernelGGL(k_clear_status, dim3(1), dim3(64), 0, d->stream, d->status);
-            ok = e.run(g) && hipMemcpyAsync(d->status_host, d->status, sizeof(unsigned int), hipMemcpyDeviceToHost,
-                                            d->stream) == hipSuccess;
+            ok = e.run(g);
+            if (ok) hipLaunchKernelGGL(k_status_out, dim3(1), dim3(64), 0, d->stream, d->status, d->status_host_dev);
             const bool ended = hipStreamEndCapture(d->stream, &graph) == hipSuccess;
             ok = ok && ended && graph &&
                  hipGraphInstantiate(&rp.exec, graph, nullptr, nullptr, 0) == hipSuccess;
@@ -1305,13 +1318,12 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         g_cnt.act_reuse = c0[5];
         d->arena.used = 0;
     }
-    hipLaunchKernelGGL(k_clear_status, dim3(1), dim3(64), 0, d->stream, d->status);
     const double t0 = prof || trace_on() ? now_ms() : 0.0;
     Engine e;
     e.dev = d;
     e.st = d->stream;
-    const bool ok = e.run(g) && hipMemcpyAsync(d->status_host, d->status, sizeof(unsigned int),
-                                               hipMemcpyDeviceToHost, d->stream) == hipSuccess;
+    const bool ok = e.run(g);
+    if (ok) hipLaunchKernelGGL(k_status_out, dim3(1), dim3(64), 0, d->stream, d->status, d->status_host_dev);
     const double t1 = prof || trace_on() ? now_ms() : 0.0;
     int64_t graph_no = 0;
     if (trace_on()) {
@@ -1367,7 +1379,8 @@ enum ggml_status finish_graph(Device* d, bool ok, const std::string& why) {
         log_line("graph execution failed: %s (FAIL-FAST)", hipGetErrorString(se));
         return GGML_STATUS_FAILED;
     }
-    const unsigned int bad = *(volatile unsigned int*)d->status_host;  // copied by the graph's last step
+    d->status_clean = true;  // k_status_out ran last
+    const unsigned int bad = *(volatile unsigned int*)d->status_host;  // copied by the graph's last kernel
     if (bad != 0 || g_fail.load() == AMEVA_FAIL_INVALIDATE_DST) {
         log_line("%u row indices out of range (FAIL-FAST)", bad);
         return GGML_STATUS_FAILED;
