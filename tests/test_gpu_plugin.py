@@ -368,14 +368,24 @@ def test_quantized_kv_cache_nodes(plugin, orc, t):
         g.free()
 
 
-def test_llama3_8b_decode_layer(plugin, orc):
-    """One decoder layer of Llama-3-8B shape, bs1 decode at position 4095 with 4095 cached tokens."""
+@pytest.mark.parametrize("wt", [gp.Q4_0, gp.Q4_K])
+def test_llama3_8b_decode_layer(plugin, orc, wt):
+    """One decoder layer of Llama-3-8B shape, bs1 decode at position 4095 with 4095 cached tokens, Q4_0 weights (Q8_0
+    activations) or Q4_K weights (Q8_K activations): the plugin runs it as 8 launches (RMS_NORM + MUL, q/k/v with ROPE
+    and both SET_ROWS, the attention split and merge, o + ADD, RMS_NORM + MUL, gate/up + SWIGLU, down + ADD)."""
     rng = np.random.default_rng(2024)
     H, NH, NKV, D, FF, CTX = 4096, 32, 8, 128, 14336, 4096
     pos_t = CTX - 1
     eps, base = 1e-5, 500000.0
     def wq4(n, k):
+        if wt == gp.Q4_K:  # random K-quant blocks, d and dmin in [0, 2e-4): weights of magnitude ~0.1
+            y = random_kquant(rng, gp.Q4_K, n, k)
+            for off in (0, 2):
+                v = rng.uniform(0.0, 2e-4, (n, k // 256)).astype(np.float16)
+                y.reshape(n, k // 256, 144)[:, :, off:off + 2] = v.view(np.uint8).reshape(n, k // 256, 2)
+            return y
         return orc.quantize_q4_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    bpw = {gp.Q4_0: (32, 18), gp.Q4_K: (256, 144)}[wt]  # weights per block, bytes per block
     w = {"q": wq4(NH * D, H), "k": wq4(NKV * D, H), "v": wq4(NKV * D, H), "o": wq4(H, NH * D),
          "gate": wq4(FF, H), "up": wq4(FF, H), "down": wq4(H, FF)}
     attn_norm = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
@@ -387,7 +397,7 @@ def test_llama3_8b_decode_layer(plugin, orc):
     g = gp.Graph(wbytes, 96 << 20)
     try:
         plugin.ggml_backend_ameva_reset_counters()
-        T = {k_: g.tensor(gp.Q4_0, [a.shape[1] * 32 // 18, a.shape[0]], "w", k_) for k_, a in w.items()}
+        T = {k_: g.tensor(wt, [a.shape[1] * bpw[0] // bpw[1], a.shape[0]], "w", k_) for k_, a in w.items()}
         for k_, a in w.items():
             g.set(T[k_], a)
         AN, FN = g.tensor(gp.F32, [H], "w", "attn_norm"), g.tensor(gp.F32, [H], "w", "ffn_norm")
@@ -435,10 +445,11 @@ def test_llama3_8b_decode_layer(plugin, orc):
         assert gp.counter(plugin, "act_quant_reuse_count") == 4
 
         # the oracle's chain of the same ops
-        q8 = lambda a: orc.quantize_q8_0(a, orc.Q8_X86)  # noqa: E731
+        def q8(a):
+            return orc.quantize_q8_K(a) if wt == gp.Q4_K else orc.quantize_q8_0(a, orc.Q8_X86)
         def mm(name, a):
-            n_, kk_ = w[name].shape[0], w[name].shape[1] * 32 // 18
-            return orc.mul_mat(gp.Q4_0, w[name], n_, kk_, q8(a), 1)
+            n_, kk_ = w[name].shape[0], w[name].shape[1] * bpw[0] // bpw[1]
+            return orc.mul_mat(wt, w[name], n_, kk_, q8(a), 1)
         _, c = orc.rms_norm(x, eps, attn_norm)
         qr = orc.rope(mm("q", c).reshape(1, NH, D), np.array([pos_t], np.int32), D, 0, base)
         kr = orc.rope(mm("k", c).reshape(1, NKV, D), np.array([pos_t], np.int32), D, 0, base)
