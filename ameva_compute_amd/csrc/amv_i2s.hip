@@ -9,6 +9,8 @@
 // sum_j c_rj q_j - sum_j q_j with v_dot4_i32_i8 (codes 0..3 are valid signed bytes).
 #include "amv_common.h"
 
+#include <algorithm>
+
 // ---------------------------------------------------------------------------------------------------------------
 // quantize_activation_int8: one workgroup of 256 per row. max_abs starts at 1e-7, scale = 127 / max_abs,
 // q = clamp(roundf(x * scale), -127, 127) (round half away from zero), dequant = 1 / scale, plus sum(q).
@@ -209,6 +211,153 @@ __global__ __launch_bounds__(64 * NW) void k_i2s_mmq(const uint8_t* __restrict__
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Batched I2_S with the k range split over workgroups (k_i2s_mmq_s), for shapes that give k_i2s_mmq too few
+// workgroups: a workgroup computes a 128-row x 64-token tile over its share of the k blocks, so that a BitNet-2B shape
+// at batch 128 (2560 x 6912: 40 tiles) still spreads over the CUs. Per chunk of up to I2S_KMAX blocks every global load is issued before the first LDS store: the 64 tokens'
+// 128 activation bytes per block go through LDS (8 KB: eight lanes per token row, whole 128-byte lines; a token row
+// takes I2S_ALD = 144 bytes, which keeps a ds_read_b128 group on distinct banks), the weights straight into the MFMA
+// operand registers (lane (c, h) of wave w: 16 bytes of row 32 w + c); the first half of the chunk is multiplied while
+// the second half arrives. Wave w multiplies rows 32 w .. 32 w + 31 against both 32-token tiles
+// (v_mfma_i32_32x32x32_i8 with the k-slot assignment of k_i2s_mmq, exact integers). The tile's integers go through
+// LDS to row-contiguous stores: the final values (one split), or per-split partials [S][m][n_rows] in the library
+// workspace that k_i2s_split_sum adds (measured: handing them to the tile's last split with agent-scope loads and
+// stores inside the launch was 2.5x slower). Measured on MI355X (eager, batch 128): the staged weights and a store loop
+// that waited on each LDS read cost 2560 x 6912 11.8 -> 9.7 us (4 splits, weights cache-resident).
+// ---------------------------------------------------------------------------------------------------------------
+#define I2S_KMAX 8
+#define I2S_ALD 144
+#define I2S_OUT_F32 0
+#define I2S_OUT_SUMS 1
+
+template <int OUT, bool SPLIT>
+__global__ __launch_bounds__(256) void k_i2s_mmq_s(const uint8_t* __restrict__ w, int n_rows, int kb,
+                                                  const int8_t* __restrict__ q, const int2* __restrict__ meta, int m,
+                                                  int kb_per, float wscale, float* __restrict__ dst, int64_t ldd,
+                                                  int32_t* __restrict__ iout, int32_t* __restrict__ part) {
+    __shared__ __align__(16) uint8_t sa[I2S_KMAX][64 * I2S_ALD];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, h = lane >> 5;
+    const int row0 = blockIdx.x * 128, tok0 = blockIdx.y * 64, sp = blockIdx.z;
+    const int b0 = sp * kb_per, nblk = min(kb_per, kb - b0);  // >= 1 (the launcher's split)
+    const size_t k = (size_t)kb * 128;
+    // loads: the lane's weight half (row 32 wv + c, half h); activation chunks tid and tid + 256 = (token, 16-byte part)
+    const int atok = tid >> 3, apart = tid & 7;
+    const i2s_v4i* wsrc = reinterpret_cast<const i2s_v4i*>(w + (size_t)min(row0 + 32 * wv + c, n_rows - 1) * kb * 32) + h;
+    const i2s_v4i* asrc0 = reinterpret_cast<const i2s_v4i*>(q + (size_t)min(tok0 + atok, m - 1) * k) + apart;
+    const i2s_v4i* asrc1 = reinterpret_cast<const i2s_v4i*>(q + (size_t)min(tok0 + 32 + atok, m - 1) * k) + apart;
+    const int aofs = atok * I2S_ALD + 16 * apart;
+    i2s_v16i acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0;
+    constexpr int HALF = I2S_KMAX / 2;
+    for (int c0 = 0; c0 < nblk; c0 += I2S_KMAX) {  // chunks of I2S_KMAX blocks (one chunk for a split launch)
+        const int nc = min(I2S_KMAX, nblk - c0);
+        i2s_v4i rw[I2S_KMAX], ra0[I2S_KMAX], ra1[I2S_KMAX];
+#pragma unroll
+        for (int i = 0; i < I2S_KMAX; ++i) {  // unconditional: blocks past the chunk reload its last block (unused)
+            const int b = b0 + c0 + min(i, nc - 1);
+            rw[i] = __builtin_nontemporal_load(wsrc + 2 * b);
+            ra0[i] = asrc0[8 * b];
+            ra1[i] = asrc1[8 * b];
+        }
+        if (c0 > 0) __syncthreads();  // every wave is done with the previous chunk's blocks
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+#pragma unroll
+            for (int i = part * HALF; i < (part + 1) * HALF; ++i) {
+                *reinterpret_cast<i2s_v4i*>(&sa[i][aofs]) = ra0[i];
+                *reinterpret_cast<i2s_v4i*>(&sa[i][aofs + 32 * I2S_ALD]) = ra1[i];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = part * HALF; i < (part + 1) * HALF; ++i) {
+                if (i >= nc) break;  // uniform
+                const i2s_v4i wa = rw[i];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int sh = 6 - 2 * t;
+                    const i2s_v4i A = (wa >> sh) & 0x03030303;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const i2s_v4i B =
+                            *reinterpret_cast<const i2s_v4i*>(&sa[i][(32 * j + c) * I2S_ALD + 32 * t + 16 * h]);
+                        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, acc[j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // the wave's 32 rows x 64 tokens through LDS, [token][row] (33 words per token row), then row-contiguous stores
+    __syncthreads();  // every wave is done with the staged blocks
+    int32_t* st = reinterpret_cast<int32_t*>(&sa[0][0]) + wv * 64 * 33;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[(32 * j + c) * 33 + 8 * (r >> 2) + 4 * h + (r & 3)] = acc[j][r];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int rr = lane & 31, th = lane >> 5;  // lane: row rr of the wave's 32, tokens th, th + 2, ...
+    const int row = row0 + 32 * wv + rr;
+    int32_t vv[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) vv[i] = st[(th + 2 * i) * 33 + rr];  // every read issued before the first store
+    if constexpr (SPLIT) {  // this split's integers, [S][m][n_rows], added by k_i2s_split_sum
+        int32_t* pp = part + ((size_t)sp * m + tok0 + th) * n_rows + row;
+        if (row < n_rows) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (tok0 + th + 2 * i < m) pp[(size_t)2 * i * n_rows] = vv[i];
+        }
+        return;
+    }
+    if (row < n_rows) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int tok = tok0 + th + 2 * i;
+            if (tok >= m) break;
+            const int2 mt = meta[tok];
+            const int32_t t = vv[i] - mt.y;
+            if constexpr (OUT == I2S_OUT_SUMS) iout[(size_t)tok * n_rows + row] = t;
+            else dst[(size_t)tok * ldd + row] = (float)t * (__int_as_float(mt.x) * wscale);
+        }
+    }
+}
+
+// Sum of the S split partials (integers: exact in any order), minus sum q, scaled. Thread (x, y): rows 4 x .. 4 x + 3
+// of token y; VEC: n_rows % 4 == 0 (16-byte partial rows).
+template <bool OUT_SUMS, bool VEC>
+__global__ __launch_bounds__(256) void k_i2s_split_sum(const int32_t* __restrict__ part, int S, int n_rows, int m,
+                                                      const int2* __restrict__ meta, float wscale,
+                                                      float* __restrict__ dst, int64_t ldd,
+                                                      int32_t* __restrict__ isums) {
+    const int tok = blockIdx.y, r0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (r0 >= n_rows) return;
+    const size_t plane = (size_t)m * n_rows, base = (size_t)tok * n_rows + r0;
+    const int nr = min(4, n_rows - r0);
+    int t[4] = {0, 0, 0, 0};
+    for (int s2 = 0; s2 < S; ++s2) {
+        if constexpr (VEC) {
+            const int4 v = *reinterpret_cast<const int4*>(part + s2 * plane + base);
+            t[0] += v.x;
+            t[1] += v.y;
+            t[2] += v.z;
+            t[3] += v.w;
+        } else {
+            for (int e = 0; e < nr; ++e) t[e] += part[s2 * plane + base + e];
+        }
+    }
+    const int2 mt = meta[tok];
+    const float sc = __int_as_float(mt.x) * wscale;
+    for (int e = 0; e < nr; ++e) {
+        if (OUT_SUMS) isums[base + e] = t[e] - mt.y;
+        else dst[(size_t)tok * ldd + r0 + e] = (float)(t[e] - mt.y) * sc;
+    }
+}
+
+float* amv_splitk_workspace(size_t bytes, hipStream_t st);
+
 extern "C" int64_t amv_i2s_act_bytes(int64_t m, int64_t k) { return (m < 0 || k < 0) ? -1 : m * k + m * 8; }
 
 extern "C" int amv_i2s_quantize_act(const float* x, int64_t m, int64_t k, void* act, void* stream) {
@@ -228,6 +377,52 @@ extern "C" int amv_i2s_quantize_act(const float* x, int64_t m, int64_t k, void* 
 #define I2S_MMQ_WAVES 4
 #endif
 
+// The batched launch for shapes whose k_i2s_mmq grid (64 x 64 tiles) would leave most CUs idle: k split over S
+// workgroups per 128 x 64 tile, S ~ 256 / tiles (at most 8). Measured on MI355X at batch 128, cold weights, graph
+// replays: 2560 x 6912 (k_i2s_mmq: 80 workgroups) 23.6 us -> 17.3 us with 6 splits (18.5 with 4, 19.7 with 9);
+// 6912 x 2560 (216 workgroups) stays on k_i2s_mmq (13.5 us; the split kernel's best, 2 splits, 18.7 us).
+// False (nothing launched) when k_i2s_mmq fills the GPU, or when the partials need a workspace that cannot be
+// allocated now (under stream capture).
+static bool i2s_mmq_split(const void* w, int64_t n_rows, int kb, const void* act, int64_t m, float wscale, float* dst,
+                          int64_t ldd, int32_t* sums, hipStream_t st) {
+    if (((n_rows + 63) / 64) * ((m + 63) / 64) >= 160) return false;
+    const int64_t tiles = ((n_rows + 127) / 128) * ((m + 63) / 64);
+    int S = (int)std::min<int64_t>({(int64_t)kb, (int64_t)8, std::max<int64_t>(1, (256 + tiles / 2) / tiles)});
+    const int kb_per = (kb + S - 1) / S;
+    S = (kb + kb_per - 1) / kb_per;
+    const int8_t* q = (const int8_t*)act;
+    const int2* meta = (const int2*)((const uint8_t*)act + m * (int64_t)kb * 128);
+    const uint8_t* wp = (const uint8_t*)w;
+    const dim3 grid((unsigned)((n_rows + 127) / 128), (unsigned)((m + 63) / 64), (unsigned)S);
+    int32_t* part = nullptr;
+    if (S > 1) {
+        part = reinterpret_cast<int32_t*>(amv_splitk_workspace((size_t)S * m * n_rows * 4, st));
+        if (!part) return false;
+    }
+#define I2S_S(OUT, SPLIT, D, L, IO) hipLaunchKernelGGL((k_i2s_mmq_s<OUT, SPLIT>), grid, dim3(256), 0, st, wp, (int)n_rows, \
+                                                       kb, q, meta, (int)m, kb_per, wscale, D, L, IO, part)
+    if (S == 1) {
+        if (sums) I2S_S(I2S_OUT_SUMS, false, nullptr, (int64_t)0, sums);
+        else I2S_S(I2S_OUT_F32, false, dst, ldd, nullptr);
+        return true;
+    }
+    I2S_S(I2S_OUT_F32, true, nullptr, (int64_t)0, nullptr);
+    const dim3 g2((unsigned)((n_rows + 1023) / 1024), (unsigned)m);
+    const bool vec = n_rows % 4 == 0;
+#define I2S_SUM(SU, V) hipLaunchKernelGGL((k_i2s_split_sum<SU, V>), g2, dim3(256), 0, st, part, S, (int)n_rows, (int)m, \
+                                          meta, wscale, dst, ldd, sums)
+    if (sums) {
+        if (vec) I2S_SUM(true, true);
+        else I2S_SUM(true, false);
+    } else {
+        if (vec) I2S_SUM(false, true);
+        else I2S_SUM(false, false);
+    }
+#undef I2S_SUM
+#undef I2S_S
+    return true;
+}
+
 static int i2s_gemv_impl(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float wscale,
                          float* dst, int64_t ldd, int32_t* sums, void* stream) {
     AMV_REQUIRE(w && act && (dst || sums), "amv_i2s_gemv: null pointer");
@@ -239,6 +434,7 @@ static int i2s_gemv_impl(const void* w, int64_t n_rows, int64_t k, const void* a
     hipStream_t st = amv_stream(stream);
     if (m >= I2S_MMQ_MIN_M) {
         const int kb = (int)(k / 128);
+        if (i2s_mmq_split(w, n_rows, kb, act, m, wscale, dst, ldd, sums, st)) return amv_check_launch("amv_i2s_gemv");
         const int8_t* q = (const int8_t*)act;
         const int2* meta = (const int2*)((const uint8_t*)act + m * k);
         const int64_t tok_tiles = (m + 63) / 64;
