@@ -481,12 +481,12 @@ static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const v
     return amv_check_launch("amv_mul_mat_q");
 }
 
-// amv_mmq16.hip: Q4_0 / Q8_0 (AMV_ACT_Q8_0_MMA activations) and Q4_K (AMV_ACT_Q8_K_MMA) on the f16 matrix cores with
-// LDS-staged tiles
+// amv_mmq16.hip: the scaled form of Q4_0 / Q8_0 (AMV_ACT_Q8_0_DEQ activations) and Q4_K (AMV_ACT_Q8_K_DEQ) on the f16
+// matrix cores with LDS-staged tiles
 int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
-              int64_t ldd, int32_t* sums, int deq, hipStream_t st);
+              int64_t ldd, hipStream_t st);
 int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
-                  int32_t* sums, int deq, hipStream_t st);
+                  hipStream_t st);
 
 
 static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
@@ -510,8 +510,8 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
         if (wtype == AMV_T_Q4_K || wtype == AMV_T_Q6_K) AMV_REQUIRE(k % 256 == 0, "%s: K-quants need k %% 256 == 0", fn);
         AMV_REQUIRE(!(deq && wtype == AMV_T_Q6_K), "%s: Q6_K has no scaled form (use Q8_K or AMV_ACT_Q8_K_MMA)", fn);
         if (!deq) return amv_qgemm(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
-        if (wtype == AMV_T_Q4_K) return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, sums, 1, amv_stream(stream));
-        return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, sums, 1, amv_stream(stream));
+        if (wtype == AMV_T_Q4_K) return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, amv_stream(stream));
+        return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, amv_stream(stream));
     }
     const bool ok = (act_type == AMV_T_Q8_0 || q80x) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)
                                                      : (q8kx && wtype == AMV_T_Q4_K);
