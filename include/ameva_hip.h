@@ -66,11 +66,11 @@ int amv_unrepack(int type, const void* src, void* dst_ggml, int64_t n_rows, int6
  *           Q8_K: qs int8[m][k] | f32 d[m][k/256] | i32 sum(qs)[m][k/16]
  *           AMV_ACT_Q8_K_MMA: the Q8_K layout, then (16-byte aligned) the same values as f16 [m][k] (exact), the
  *           sums per 16 as f16 [m][k/16] and (16-byte aligned) the super-block scales transposed, f32 [k/256][m]:
- *           the input of the batched Q4_K MUL_MAT (amv_mul_mat_q), which feeds the matrix cores in f16; its Q8_K
- *           prefix is a plain Q8_K activation of the m rows (amv_mul_mat_vec reads it as such).
+ *           the batched Q4_K MUL_MAT of 8..64 tokens reads the f16 copies; its Q8_K prefix is a plain Q8_K
+ *           activation of the m rows (amv_mul_mat_vec and the larger batches read it as such).
  *           AMV_ACT_Q8_0_MMA: the Q8_0 layout, then (16-byte aligned) the same values as f16 [m][k] and the block
- *           scales transposed, f32 [k/32][m]: the input of the batched Q4_0 / Q8_0 MUL_MAT on the f16 matrix cores
- *           (amv_mul_mat_q_act); its prefix is a plain Q8_0 activation of the m rows.
+ *           scales transposed, f32 [k/32][m]; its prefix is a plain Q8_0 activation of the m rows, which is what
+ *           the batched Q4_0 / Q8_0 MUL_MAT reads.
  *           AMV_ACT_Q8_0_DEQ / AMV_ACT_Q8_K_DEQ: the same layouts (and sizes) with f16 of q * d (one rounding) in
  *           place of the f16 copies of q: the input of the scaled batched MUL_MAT.
  * type AMV_T Q8_0 (8), Q8_K (15), AMV_ACT_Q8_K_MMA, AMV_ACT_Q8_0_MMA, AMV_ACT_Q8_K_DEQ or AMV_ACT_Q8_0_DEQ; rule
@@ -174,12 +174,13 @@ int amv_mul_mat_q(int wtype, const void* w, int64_t n_rows, int64_t k, const voi
 int amv_mul_mat_q_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m,
                              int32_t* sums, void* stream);
 /* amv_mul_mat_q with the activation layout named: act_type AMV_T_Q8_0, AMV_ACT_Q8_0_MMA or AMV_ACT_Q8_0_DEQ for
- * Q4_0 / Q8_0 weights, AMV_ACT_Q8_K_MMA or AMV_ACT_Q8_K_DEQ for Q4_K. With the MMA layouts and m > 64 the product runs
- * on the f16 matrix cores on exact integers (v_mfma_f32_32x32x16_f16 on q - 8 / q and q_a: each block's int32 sum
- * comes out exact, then acc += S d_w d_a); with the DEQ layouts and m > 64 the weights are staged as f16 (q - 8) d_w
- * (Q4_K: (d sc) q - dmin m) against the activations' f16 q_a d_a and the matrix cores accumulate across all of k (no
- * per-block epilogue; within ~3e-4 relative L2 of the exact form, the DEQ rounding of both operands to f16 aside).
- * Smaller batches run the int8 kernel on the layout's plain prefix. Block sums need an MMA layout. */
+ * Q4_0 / Q8_0 weights, AMV_T_Q8_K, AMV_ACT_Q8_K_MMA or AMV_ACT_Q8_K_DEQ for Q4_K (Q6_K: AMV_T_Q8_K or
+ * AMV_ACT_Q8_K_MMA). With the plain or MMA layouts and m > 64 the product is the exact form on the int8 matrix cores
+ * (one v_mfma_i32_32x32x32_i8 per 32-block: each block's ggml integer comes out exact, then ggml's f32 epilogue);
+ * with the DEQ layouts and m > 64 the weights are staged as f16 (q - 8) d_w (Q4_K: (d sc) q - dmin m) against the
+ * activations' f16 q_a d_a and the matrix cores accumulate across all of k (no per-block epilogue; within ~3e-4
+ * relative L2 of the exact form). 8..64 tokens run the small-batch kernels (Q4_K on the MMA layout's f16 copies).
+ * Block sums need a plain or MMA layout. */
 int amv_mul_mat_q_act(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type, int64_t m,
                       float* dst, int64_t ldd, void* stream);
 int amv_mul_mat_q_act_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type,
