@@ -512,3 +512,78 @@ def test_graph_replay(plugin, orc):
             assert rel_l2(g.get(Y, np.float32, (1, n)), want) < 1e-3
     finally:
         g.free()
+
+
+@pytest.mark.parametrize("extra_reads", [False, True])
+def test_node_groups_and_their_guards(plugin, orc, extra_reads):
+    """The q/k/v (+ ROPE + SET_ROWS) and gate/up (+ SWIGLU) node groups run as one launch each, and only when nothing
+    else reads their intermediate values: with a later MUL reading the un-rotated q and another reading the raw gate,
+    the plugin runs the nodes one by one. Both graphs match the oracle's chain."""
+    rng = np.random.default_rng(99)
+    H, NH, NKV, D, FF, CTX, pos_t = 4096, 4, 2, 128, 1024, 64, 37
+    def wq4(n, k):
+        return orc.quantize_q4_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    w = {"q": wq4(NH * D, H), "k": wq4(NKV * D, H), "v": wq4(NKV * D, H), "gate": wq4(FF, H), "up": wq4(FF, H),
+         "down": wq4(H, FF)}
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    e_q = rng.standard_normal((1, NH * D)).astype(np.float32)
+    e_g = rng.standard_normal((1, FF)).astype(np.float32)
+    kc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    vc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    g = gp.Graph(sum(a.nbytes for a in w.values()) + 8 * 4096, 16 << 20)
+    try:
+        T = {k_: g.tensor(gp.Q4_0, [a.shape[1] * 32 // 18, a.shape[0]], "w", k_) for k_, a in w.items()}
+        for k_, a in w.items():
+            g.set(T[k_], a)
+        X = g.tensor(gp.F32, [H, 1], "c", "x")
+        g.set(X, x)
+        EQ, EG = g.tensor(gp.F32, [NH * D, 1], "c", "eq"), g.tensor(gp.F32, [FF, 1], "c", "eg")
+        g.set(EQ, e_q)
+        g.set(EG, e_g)
+        POS, IDX = g.tensor(gp.I32, [1], "c", "pos"), g.tensor(gp.I64, [1], "c", "idx")
+        g.set(POS, np.array([pos_t], np.int32))
+        g.set(IDX, np.array([pos_t], np.int64))
+        KC, VC = g.tensor(gp.F16, [NKV * D, CTX], "c", "kc"), g.tensor(gp.F16, [NKV * D, CTX], "c", "vc")
+        g.set(KC, kc)
+        g.set(VC, vc)
+        q_raw = g.mul_mat(T["q"], X)
+        q = g.rope(g.reshape_3d(q_raw, D, NH, 1), POS, D, 0, 500000.0)
+        k = g.rope(g.reshape_3d(g.mul_mat(T["k"], X), D, NKV, 1), POS, D, 0, 500000.0)
+        v = g.mul_mat(T["v"], X)
+        g.set_rows(KC, g.view_nd(k, gp.OP_RESHAPE, [NKV * D, 1], [4, NKV * D * 4, NKV * D * 4, NKV * D * 4]), IDX)
+        g.set_rows(VC, v, IDX)
+        gate = g.mul_mat(T["gate"], X)
+        ff = g.swiglu(gate, g.mul_mat(T["up"], X))
+        y = g.mul_mat(T["down"], ff)
+        if extra_reads:
+            yq, yg = g.mul(q_raw, EQ), g.mul(gate, EG)
+        plugin.ggml_backend_ameva_reset_counters()
+        assert g.compute() == gp.STATUS_SUCCESS
+        fused = gp.counter(plugin, "fused_pair_count")
+        assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 6
+        if extra_reads:
+            assert fused < 8
+        else:
+            assert fused == 8  # k, v, both ROPEs and both SET_ROWS in the q launch; up and SWIGLU in the gate launch
+
+        q8 = lambda a: orc.quantize_q8_0(a, orc.Q8_X86)  # noqa: E731
+        def mm(name, a):
+            n_, kk_ = w[name].shape[0], w[name].shape[1] * 32 // 18
+            return orc.mul_mat(gp.Q4_0, w[name], n_, kk_, q8(a), 1)
+        qm, km, gm = mm("q", x), mm("k", x), mm("gate", x)
+        qr = orc.rope(qm.reshape(1, NH, D), np.array([pos_t], np.int32), D, 0, 500000.0)
+        kr = orc.rope(km.reshape(1, NKV, D), np.array([pos_t], np.int32), D, 0, 500000.0)
+        assert rel_l2(g.get(q, np.float32, (1, NH, D)), qr) < 1e-3
+        assert rel_l2(g.get(v, np.float32, (1, NKV * D)), mm("v", x)) < 1e-3
+        kc_out = g.get(KC, np.float16, (CTX, NKV * D))
+        assert np.array_equal(np.delete(kc_out, pos_t, axis=0).view(np.uint16), np.delete(kc, pos_t, axis=0).view(np.uint16))
+        assert rel_l2(kc_out[pos_t], kr.reshape(-1).astype(np.float16)) < 1e-3
+        assert rel_l2(g.get(VC, np.float16, (CTX, NKV * D))[pos_t], mm("v", x).reshape(-1).astype(np.float16)) < 1e-3
+        h = orc.swiglu(gm, mm("up", x))
+        assert rel_l2(g.get(ff, np.float32, (1, FF)), h) < 1e-3
+        assert rel_l2(g.get(y, np.float32, (1, H)), mm("down", h)) < 2e-3
+        if extra_reads:
+            assert rel_l2(g.get(yq, np.float32, (1, NH * D)), qm * e_q) < 1e-3
+            assert rel_l2(g.get(yg, np.float32, (1, FF)), gm * e_g) < 1e-3
+    finally:
+        g.free()
