@@ -203,6 +203,239 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ wq, con
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Small batches (m <= 32) of Q4_0 / Q8_0, streamed like the GEMV (k_mmq_sb). A wave owns 16 weight rows and all the
+// tokens (one or two 16-token tiles); the 4 waves of a workgroup take every fourth group of 4 blocks of those rows
+// and add their f32 partials in LDS in wave order. Per group each lane issues whole 16-byte loads: block 4 q + g of
+// its row (lane group g = l / 16), of its token's activation row and of the scale runs of 4 blocks; a 4 x 4 transpose
+// of dwords across the lane groups (v_permlane32_swap, then v_permlane16_swap) hands lane group g dword g of every
+// block, i.e. the MFMA operands of one v_mfma_i32_16x16x32_i8 per block: lane group g supplies the k slots 8 g .. 8 g
+// + 7 as weights 4 g .. 4 g + 3 (Q4_0: the low nibbles of bytes 4 g .. 4 g + 3; Q8_0: those bytes) and weights
+// 16 + 4 g .. 16 + 4 g + 3 (high nibbles; bytes 16 + 4 g ..), the activations in the same slots. Each block's exact
+// integer comes out of its MFMA, then the f32 epilogue acc += S * (d_w * d_a). The loads of the next group are in
+// flight while a group computes. Needs nb % 4 == 0 (16-byte scale runs) and, for Q4_0, an even row count (paired
+// scales).
+// ---------------------------------------------------------------------------------------------------------------
+typedef unsigned int sb_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int sb_v2u __attribute__((ext_vector_type(2)));
+
+// lane group g of (x0, x1, x2, x3) ends up with dword g of the values lane groups 0..3 held: x_j <- x_g of group j
+__device__ __forceinline__ void sb_transpose4(uint32_t& x0, uint32_t& x1, uint32_t& x2, uint32_t& x3) {
+    const auto a = __builtin_amdgcn_permlane32_swap(x0, x2, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(x1, x3, false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    x0 = c[0];
+    x1 = c[1];
+    x2 = d[0];
+    x3 = d[1];
+}
+__device__ __forceinline__ void sb_transpose4(sb_v4u& v) {
+    uint32_t x0 = v.x, x1 = v.y, x2 = v.z, x3 = v.w;
+    sb_transpose4(x0, x1, x2, x3);
+    v = sb_v4u{x0, x1, x2, x3};
+}
+
+template <int WT, int TI, int TJ, int NW, bool SUMS>
+__global__ __launch_bounds__(64 * NW) void k_mmq_sb(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int N,
+                                               int nb, const int8_t* __restrict__ aq, const int2* __restrict__ ameta,
+                                               int M, float* __restrict__ dst, int64_t ldd,
+                                               int32_t* __restrict__ sums) {
+    constexpr int QW = WT == AMV_T_Q4_0 ? 1 : 2;  // 16-byte chunks per weight block
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16 * TI;
+    const size_t K = (size_t)nb * 32;
+    const int ngrp = nb >> 2;
+    const sb_v4u* wr[TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+        wr[i] = reinterpret_cast<const sb_v4u*>(wq) + (size_t)min(n0 + 16 * i + r16, N - 1) * nb * QW;
+    const sb_v4u* ar[TJ];
+    const int2* mr[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int t = min(16 * j + r16, M - 1);
+        ar[j] = reinterpret_cast<const sb_v4u*>(aq + t * K);
+        mr[j] = ameta + (size_t)t * nb;
+    }
+    // scale runs of the lane's 4 output rows 16 i + 4 g .. + 3 of each tile: Q4_0 two row pairs, Q8_0 four rows
+    const sb_v4u* sp[TI][2];
+    const sb_v2u* sq[TI][4];
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        if constexpr (WT == AMV_T_Q4_0) {
+            const int pmax = N / 2 - 1, pb = ((n0 + 16 * i) >> 1) + 2 * g;
+            sp[i][0] = reinterpret_cast<const sb_v4u*>(wd) + (size_t)min(pb, pmax) * (nb >> 2);
+            sp[i][1] = reinterpret_cast<const sb_v4u*>(wd) + (size_t)min(pb + 1, pmax) * (nb >> 2);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                sq[i][e] = reinterpret_cast<const sb_v2u*>(wd) + (size_t)min(n0 + 16 * i + 4 * g + e, N - 1) * (nb >> 2);
+        }
+    }
+    float acc[TI][TJ][4];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
+
+    // one group's loads: lane group g takes block 4 q + g of its rows and tokens (with that block's activation scale)
+    // and the scale runs of blocks 4 q .. 4 q + 3 of its output rows
+    sb_v4u lw[2][TI][QW], la[2][TJ][2], ls[2][TI][2];
+    sb_v2u lq[2][TI][4];
+    float lm[2][TJ];
+    const auto load = [&](int s, int q) {
+        const size_t b = (size_t)4 * q + g;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int c = 0; c < QW; ++c) lw[s][i][c] = __builtin_nontemporal_load(wr[i] + b * QW + c);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            la[s][j][0] = ar[j][2 * b];
+            la[s][j][1] = ar[j][2 * b + 1];
+            lm[s][j] = __int_as_float(mr[j][b].x);
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            if constexpr (WT == AMV_T_Q4_0) {
+                ls[s][i][0] = sp[i][0][q];
+                ls[s][i][1] = sp[i][1][q];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) lq[s][i][e] = sq[i][e][q];
+            }
+        }
+    };
+    const auto compute = [&](int s, int q) {
+        // operands: dword g of each block of the group; the activation scales of all 4 blocks
+        sb_v4u wv[TI][QW], av[TJ][2];
+        uint32_t da[TJ][4];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int c = 0; c < QW; ++c) {
+                wv[i][c] = lw[s][i][c];
+                sb_transpose4(wv[i][c]);
+            }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            av[j][0] = la[s][j][0];
+            av[j][1] = la[s][j][1];
+            sb_transpose4(av[j][0]);
+            sb_transpose4(av[j][1]);
+            const uint32_t d = __float_as_uint(lm[s][j]);
+            da[j][0] = da[j][1] = da[j][2] = da[j][3] = d;
+            sb_transpose4(da[j][0], da[j][1], da[j][2], da[j][3]);  // da[j][jb]: the scale of block 4 q + jb
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            long A[TI];
+            float dw[TI][4];
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                uint32_t lo, hi;
+                if constexpr (WT == AMV_T_Q4_0) {
+                    const uint32_t x = wv[i][0][jb];
+                    lo = ((x & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;  // (nibble - 8) as a signed byte
+                    hi = (((x >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+                    dw[i][0] = amv_h2f(ls[s][i][0][jb]);
+                    dw[i][1] = amv_h2f(ls[s][i][0][jb] >> 16);
+                    dw[i][2] = amv_h2f(ls[s][i][1][jb]);
+                    dw[i][3] = amv_h2f(ls[s][i][1][jb] >> 16);
+                } else {
+                    lo = wv[i][0][jb];
+                    hi = wv[i][1][jb];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dw[i][e] = amv_h2f(lq[s][i][e][jb >> 1] >> (16 * (jb & 1)));
+                }
+                A[i] = (long)(((uint64_t)hi << 32) | lo);
+            }
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const long B = (long)(((uint64_t)av[j][1][jb] << 32) | av[j][0][jb]);
+                const float dav = __uint_as_float(da[j][jb]);
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const v4i zero = {0, 0, 0, 0};
+                    const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[i], B, zero, 0, 0, 0);
+                    if constexpr (SUMS) {
+                        const int m = 16 * j + r16;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int n = n0 + 16 * i + 4 * g + e;
+                            if (m < M && n < N) sums[((size_t)m * N + n) * nb + 4 * q + jb] = C[e];
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf((float)C[e], dw[i][e] * dav, acc[i][j][e]);
+                    }
+                }
+            }
+        }
+    };
+    int q = w;
+    if (q < ngrp) load(0, q);
+    for (; q < ngrp; q += 2 * NW) {
+        if (q + NW < ngrp) load(1, q + NW);
+        compute(0, q);
+        if (q + NW >= ngrp) break;
+        if (q + 2 * NW < ngrp) load(0, q + 2 * NW);
+        compute(1, q + NW);
+    }
+    if constexpr (!SUMS) {
+        __shared__ float red[NW - 1][TI * TJ * 4][64];
+        if (w > 0) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) red[w - 1][(i * TJ + j) * 4 + e][lane] = acc[i][j][e];
+        }
+        __syncthreads();
+        if (w > 0) return;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int m = 16 * j + r16;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int x = (i * TJ + j) * 4 + e;
+                    float v = acc[i][j][e];
+#pragma unroll
+                    for (int o = 0; o < NW - 1; ++o) v += red[o][x][lane];  // wave order
+                    const int n = n0 + 16 * i + 4 * g + e;
+                    if (m < M && n < N) dst[(size_t)m * ldd + n] = v;
+                }
+            }
+    }
+}
+
+// the streamed small-batch kernel where it applies: two 16-row tiles per wave (sharing the activation operands) and
+// 4 waves per workgroup while that leaves >= 256 workgroups, else one tile per wave and 8 waves splitting k
+template <int WT, bool SUMS>
+static bool mmq_sb_launch(const uint8_t* wq, const uint16_t* wd, int N, int nb, const int8_t* aq, const int2* ameta,
+                          int M, float* dst, int64_t ldd, int32_t* sums, hipStream_t st) {
+    if (M > 32 || nb % 4 != 0 || (WT == AMV_T_Q4_0 && N % 2 != 0)) return false;
+    const bool two = (N + 31) / 32 >= 256;
+    const dim3 grid((unsigned)(two ? (N + 31) / 32 : (N + 15) / 16));
+#define SB(TI, TJ, NW) hipLaunchKernelGGL((k_mmq_sb<WT, TI, TJ, NW, SUMS>), grid, dim3(64 * NW), 0, st, wq, wd, N, nb, \
+                                          aq, ameta, M, dst, ldd, sums)
+    if (M <= 16) {
+        if (two) SB(2, 1, 4);
+        else SB(1, 1, 8);
+    } else {
+        if (two) SB(2, 2, 4);
+        else SB(1, 2, 8);
+    }
+#undef SB
+    return true;
+}
+
 template <int WT, bool SUMS, int TI, int TJ, int U, int WR = 2, int KS = 1>
 static void mmq_launch(const uint8_t* wq, const uint16_t* wd, int N, int nb, const int8_t* aq, const int2* ameta,
                        int M, float* dst, int64_t ldd, int32_t* sums, hipStream_t st) {
@@ -224,6 +457,7 @@ template <int WT, bool SUMS>
 static void mmq_dispatch(const uint8_t* wq, const uint16_t* wd, int N, int nb, const int8_t* aq, const int2* ameta,
                          int M, float* dst, int64_t ldd, int32_t* sums, hipStream_t st) {
     const int64_t row_tiles = (N + 127) / 128;
+    if (mmq_sb_launch<WT, SUMS>(wq, wd, N, nb, aq, ameta, M, dst, ldd, sums, st)) return;
     if (M <= 32) {
         // small batches: one 16 TI x 16 TJ tile per workgroup, its 4 waves splitting k; the largest row tile that
         // still gives >= 224 workgroups (M = 16: 14336 x 4096 28 us with TI = 4, 4096 x 14336 41 us with TI = 1)

@@ -41,10 +41,12 @@ def weights(orc, rng, wtype, n, k):
 @pytest.mark.parametrize("atype", [8, 1008])
 @pytest.mark.parametrize("wtype", [2, 8])
 @pytest.mark.parametrize("m,n,k", [(8, 16, 32), (40, 200, 1024), (17, 129, 96), (128, 256, 4096), (512, 64, 14336),
-                                   (65, 129, 96), (300, 200, 1056), (130, 64, 32), (512, 1000, 4096)])
+                                   (65, 129, 96), (300, 200, 1056), (130, 64, 32), (512, 1000, 4096),
+                                   (8, 64, 128), (16, 300, 1024), (32, 130, 4096), (17, 129, 1024), (24, 48, 512)])
 def test_mmq_block_sums_and_output(dev, ops, orc, wtype, m, n, k, atype):
-    """Both kernels (int8 MFMA on plain Q8_0 activations; f16 MFMA on AMV_ACT_Q8_0_MMA for m > 64): the per-block
-    integers bit for bit and the f32 output within the bar, ragged rows / tokens / odd block counts included."""
+    """The batched kernels on both activation layouts: the streamed small-batch kernel (m <= 32, k % 128 == 0; Q4_0
+    with an even row count), the tiled int8 kernels, the exact form above 64 tokens: the per-block integers bit for
+    bit and the f32 output within the bar, ragged rows / tokens / odd block counts included."""
     rng = np.random.default_rng(m * 1000 + n + k + wtype)
     wg = weights(orc, rng, wtype, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
