@@ -508,13 +508,13 @@ __device__ __forceinline__ k4_h8 k4_nib_f16(uint32_t x0, uint32_t x1, k4_h2 sc2)
 // KS = 4 (small batches): the 4 waves share one 32 x 32 TT tile and split the super-blocks (wave w takes j = w,
 // w + 4, ...); their f32 partials are added in LDS in wave order.
 template <bool SUMS, int TT, int KS>
-__global__ __launch_bounds__(256) void k_mmq_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
+__global__ __launch_bounds__(KS > 1 ? 64 * KS : 256) void k_mmq_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
                                                 int nsb, const uint16_t* __restrict__ a16,
                                                 const uint16_t* __restrict__ bs16, const float* __restrict__ dt, int M,
                                                 float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ sums) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = lane & 31, h = lane >> 5;
-    const int row0 = KS == 4 ? blockIdx.x * 32 : blockIdx.x * 64 + 32 * (w & 1);
-    const int tok0 = KS == 4 ? blockIdx.y * (32 * TT) : blockIdx.y * (64 * TT) + 32 * TT * (w >> 1);
+    const int row0 = KS > 1 ? blockIdx.x * 32 : blockIdx.x * 64 + 32 * (w & 1);
+    const int tok0 = KS > 1 ? blockIdx.y * (32 * TT) : blockIdx.y * (64 * TT) + 32 * TT * (w >> 1);
     const int K = nsb * 256;
     const int row = min(row0 + c, N - 1);
     const uint4* qrow = wq + (size_t)row * nsb * 8 + 4 * h;  // 8 uint4 of qs per super-block; this half's 4
@@ -533,11 +533,23 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(const uint4* __restrict__ wq, c
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
-    for (int j = KS == 4 ? w : 0; j < nsb; j += KS) {
+    // the weights of the wave's next super-block are loaded while this one computes
+    const int j_first = KS > 1 ? w : 0;
+    uint4 nq4[4], nhd = make_uint4(0, 0, 0, 0);
+    if (j_first < nsb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nq4[i] = qrow[(size_t)j_first * 8 + i];
+        nhd = hrow[j_first];
+    }
+    for (int j = j_first; j < nsb; j += KS) {
         uint4 q4[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q4[i] = qrow[(size_t)j * 8 + i];
-        const uint4 hd = hrow[j];
+        for (int i = 0; i < 4; ++i) q4[i] = nq4[i];
+        const uint4 hd = nhd;
+        const int jn = min(j + KS, nsb - 1);  // the last super-block reloads itself (unused)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nq4[i] = qrow[(size_t)jn * 8 + i];
+        nhd = hrow[jn];
         // scales and mins of units 4 h .. 4 h + 3 (get_scale_min_k4 on the 12 packed bytes)
         int scv[4], mv[4];
 #pragma unroll
@@ -611,8 +623,8 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(const uint4* __restrict__ wq, c
             }
         }
     }
-    if constexpr (KS == 4 && !SUMS) {
-        __shared__ float red[3][TT * 16][64];
+    if constexpr (KS > 1 && !SUMS) {
+        __shared__ float red[KS - 1][TT * 16][64];
         if (w > 0) {
 #pragma unroll
             for (int t = 0; t < TT; ++t)
@@ -625,7 +637,8 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(const uint4* __restrict__ wq, c
         for (int t = 0; t < TT; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                acc[t][r] = ((acc[t][r] + red[0][t * 16 + r][lane]) + red[1][t * 16 + r][lane]) + red[2][t * 16 + r][lane];
+#pragma unroll
+                for (int o = 0; o < KS - 1; ++o) acc[t][r] += red[o][t * 16 + r][lane];  // wave order
     }
     if (!SUMS) {
         const int n = row0 + c;
@@ -655,14 +668,18 @@ static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, in
     const unsigned gx = (unsigned)((n_rows + 63) / 64);
 #define Q4K_LAUNCH(TT, KS, G) \
     do { \
-        if (sums) hipLaunchKernelGGL((k_mmq_q4k<true, TT, KS>), G, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, \
+        const dim3 B(KS > 1 ? 64 * KS : 256); \
+        if (sums) hipLaunchKernelGGL((k_mmq_q4k<true, TT, KS>), G, B, 0, st, wq, wh, (int)n_rows, nsb, a16, \
                                      bs16, dt, (int)m, dst, ldd, sums); \
-        else hipLaunchKernelGGL((k_mmq_q4k<false, TT, KS>), G, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, \
+        else hipLaunchKernelGGL((k_mmq_q4k<false, TT, KS>), G, B, 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, \
                                 dt, (int)m, dst, ldd, sums); \
     } while (0)
     if (m <= 32) {
-        // small batches: one 32-row x 32-token tile per workgroup, the 4 waves splitting the super-blocks
-        Q4K_LAUNCH(1, 4, dim3((unsigned)((n_rows + 31) / 32), (unsigned)((m + 31) / 32)));
+        // small batches: one 32-row x 32-token tile per workgroup, its waves splitting the super-blocks: 4, or 8 when
+        // the row tiles alone leave CUs idle (4096 x 14336: 128 tiles)
+        const dim3 G((unsigned)((n_rows + 31) / 32), (unsigned)((m + 31) / 32));
+        if ((int64_t)G.x * G.y >= 256) Q4K_LAUNCH(1, 4, G);
+        else Q4K_LAUNCH(1, 8, G);
     } else if (m <= 64) {
         Q4K_LAUNCH(1, 1, dim3(gx, (unsigned)((m + 63) / 64)));
     } else {
