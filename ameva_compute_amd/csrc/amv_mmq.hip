@@ -492,6 +492,8 @@ static void mmq_dispatch(const uint8_t* wq, const uint16_t* wd, int N, int nb, c
 typedef _Float16 k4_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 k4_h2 __attribute__((ext_vector_type(2)));
 typedef float k4_f16v __attribute__((ext_vector_type(16)));
+typedef _Float16 k4_h4 __attribute__((ext_vector_type(4)));
+typedef float k4_f16v4 __attribute__((ext_vector_type(4)));
 
 // 8 nibbles (bytes of x0, x1 after the nibble select) -> 8 f16 values nib * sc (exact)
 __device__ __forceinline__ k4_h8 k4_nib_f16(uint32_t x0, uint32_t x1, k4_h2 sc2) {
@@ -654,6 +656,162 @@ __global__ __launch_bounds__(KS > 1 ? 64 * KS : 256) void k_mmq_q4k(const uint4*
     }
 }
 
+// Small batches (m <= 32) of Q4_K, streamed like k_mmq_sb (k_mmq_q4k_sb). A wave owns TI 16-row weight tiles and
+// every token (TJ 16-token tiles); the waves of a workgroup take every NW-th super-block. Roles: A = activations (the
+// f16 copies of AMV_ACT_Q8_K_MMA, token l % 16), B = weights (row l % 16), so a lane's 4 outputs are one weight row
+// (its own d, dmin and scales) and tokens 4 g .. 4 g + 3. k slots of unit u (one v_mfma_f32_16x16x32_f16 per unit):
+// lane group g supplies weights 8 g .. 8 g + 7 of the unit, i.e. the nibbles (low for even u, high for odd u) of bytes
+// 8 g .. 8 g + 7 of chunk u / 2; each lane loads chunk g of its row's super-block (32 bytes) and a 4 x 4 transpose of
+// the even and of the odd dwords across the lane groups hands it bytes 8 g .. 8 g + 7 of every chunk. The weight
+// operand is sc_u * q (<= 945, exact in f16), so each half super-block's f32 sum (<= 15.4 M) is ggml's integer exactly;
+// I2 = sum_u m_u bsum_u is one v_mfma_f32_16x16x16_f16 of the activation 16-sums against the mins; then
+// acc += d_a (d I1 - dmin I2). The loads of the next super-block are in flight while one computes.
+template <int TI, int TJ, int NW, bool SUMS>
+__global__ __launch_bounds__(64 * NW) void k_mmq_q4k_sb(const uint4* __restrict__ wq, const uint4* __restrict__ wh,
+                                                       int N, int nsb, const uint16_t* __restrict__ a16,
+                                                       const uint16_t* __restrict__ bs16, const float* __restrict__ dt,
+                                                       int M, float* __restrict__ dst, int64_t ldd,
+                                                       int32_t* __restrict__ sums) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16 * TI;
+    const size_t K = (size_t)nsb * 256;
+    const sb_v4u* qr[TI];
+    const sb_v4u* hr[TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const size_t row = (size_t)min(n0 + 16 * i + r16, N - 1);
+        qr[i] = reinterpret_cast<const sb_v4u*>(wq) + row * nsb * 8 + 2 * g;  // chunk g: 2 x 16 bytes of 8 per super-block
+        hr[i] = reinterpret_cast<const sb_v4u*>(wh) + row * nsb;
+    }
+    const uint16_t* ar[TJ];
+    const uint16_t* br[TJ];
+    int tk[TJ][4];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const size_t t = (size_t)min(16 * j + r16, M - 1);
+        ar[j] = a16 + t * K + 8 * g;
+        br[j] = bs16 + t * (K / 16) + 4 * g;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tk[j][e] = min(16 * j + 4 * g + e, M - 1);
+    }
+    float acc[TI][TJ][4];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
+
+    sb_v4u lq[2][TI][2], lh[2][TI], la[2][TJ][8];
+    sb_v2u lb[2][TJ];
+    float ld[2][TJ][4];
+    const auto load = [&](int s, int sb) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            lq[s][i][0] = __builtin_nontemporal_load(qr[i] + (size_t)sb * 8);
+            lq[s][i][1] = __builtin_nontemporal_load(qr[i] + (size_t)sb * 8 + 1);
+            lh[s][i] = __builtin_nontemporal_load(hr[i] + sb);
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) la[s][j][u] = *reinterpret_cast<const sb_v4u*>(ar[j] + (size_t)sb * 256 + 32 * u);
+            lb[s][j] = *reinterpret_cast<const sb_v2u*>(br[j] + (size_t)sb * 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ld[s][j][e] = dt[(size_t)sb * M + tk[j][e]];
+        }
+    };
+    const auto compute = [&](int s, int sb) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            // bytes 8 g .. 8 g + 7 of chunk c: dwords 2 g, 2 g + 1 -> ev[c], od[c]
+            uint32_t ev[4] = {lq[s][i][0].x, lq[s][i][0].z, lq[s][i][1].x, lq[s][i][1].z};
+            uint32_t od[4] = {lq[s][i][0].y, lq[s][i][0].w, lq[s][i][1].y, lq[s][i][1].w};
+            sb_transpose4(ev[0], ev[1], ev[2], ev[3]);
+            sb_transpose4(od[0], od[1], od[2], od[3]);
+            const sb_v4u hd = lh[s][i];
+            int scv[8], mlo, mhi, dummy;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) k4_scale_min(u, hd.y, hd.z, hd.w, scv[u], dummy);
+            k4_scale_min(2 * g, hd.y, hd.z, hd.w, dummy, mlo);  // the mins of units 2 g, 2 g + 1 (the I2 k slots)
+            k4_scale_min(2 * g + 1, hd.y, hd.z, hd.w, dummy, mhi);
+            k4_f16v4 C0[TJ], C1[TJ], I2[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) C0[j][e] = C1[j][e] = I2[j][e] = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = u >> 1, sh = 4 * (u & 1);
+                const _Float16 scf = (_Float16)(float)scv[u];
+                const k4_h8 B = k4_nib_f16((ev[c] >> sh) & 0x0F0F0F0Fu, (od[c] >> sh) & 0x0F0F0F0Fu, k4_h2{scf, scf});
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const k4_h8 A = __builtin_bit_cast(k4_h8, la[s][j][u]);
+                    if (u < 4) C0[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, C0[j], 0, 0, 0);
+                    else C1[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, C1[j], 0, 0, 0);
+                }
+            }
+            // I2: k slot 4 g + e <-> 16-sum 4 g + e of the super-block <-> unit 2 g + e / 2
+            const k4_h4 Bm = {(_Float16)(float)mlo, (_Float16)(float)mlo, (_Float16)(float)mhi, (_Float16)(float)mhi};
+            const float d = amv_h2f(hd.x), dmin = amv_h2f(hd.x >> 16);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const k4_h4 Am = __builtin_bit_cast(k4_h4, lb[s][j]);
+                I2[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(Am, Bm, I2[j], 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (SUMS) {
+                        const int tok = 16 * j + 4 * g + e, n = n0 + 16 * i + r16;
+                        if (tok < M && n < N) {
+                            int32_t* o = sums + (((size_t)tok * N + n) * nsb + sb) * 2;
+                            o[0] = (int)C0[j][e] + (int)C1[j][e];
+                            o[1] = (int)I2[j][e];
+                        }
+                    } else {
+                        acc[i][j][e] = fmaf(ld[s][j][e], fmaf(d, C0[j][e] + C1[j][e], -dmin * I2[j][e]), acc[i][j][e]);
+                    }
+                }
+            }
+        }
+    };
+    int sb = w;
+    if (sb < nsb) load(0, sb);
+    for (; sb < nsb; sb += 2 * NW) {
+        if (sb + NW < nsb) load(1, sb + NW);
+        compute(0, sb);
+        if (sb + NW >= nsb) break;
+        if (sb + 2 * NW < nsb) load(0, sb + 2 * NW);
+        compute(1, sb + NW);
+    }
+    if constexpr (!SUMS) {
+        __shared__ float red[NW - 1][TI * TJ * 4][64];
+        if (w > 0) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) red[w - 1][(i * TJ + j) * 4 + e][lane] = acc[i][j][e];
+        }
+        __syncthreads();
+        if (w > 0) return;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int x = (i * TJ + j) * 4 + e;
+                    float v = acc[i][j][e];
+#pragma unroll
+                    for (int o = 0; o < NW - 1; ++o) v += red[o][x][lane];  // wave order
+                    const int tok = 16 * j + 4 * g + e, n = n0 + 16 * i + r16;
+                    if (tok < M && n < N) dst[(size_t)tok * ldd + n] = v;
+                }
+    }
+}
+
 static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
                    int32_t* sums, hipStream_t st) {
     AMV_REQUIRE(k % 256 == 0, "amv_mul_mat_q: Q4_K needs k %% 256 == 0");
@@ -675,11 +833,25 @@ static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, in
                                 dt, (int)m, dst, ldd, sums); \
     } while (0)
     if (m <= 32) {
-        // small batches: one 32-row x 32-token tile per workgroup, its waves splitting the super-blocks: 4, or 8 when
-        // the row tiles alone leave CUs idle (4096 x 14336: 128 tiles)
-        const dim3 G((unsigned)((n_rows + 31) / 32), (unsigned)((m + 31) / 32));
-        if ((int64_t)G.x * G.y >= 256) Q4K_LAUNCH(1, 4, G);
-        else Q4K_LAUNCH(1, 8, G);
+        // small batches, streamed: two 16-row tiles per wave and 4 waves while that leaves >= 256 workgroups, else one
+        // tile and 8 waves splitting the super-blocks (4 for two token tiles)
+        const bool two = (n_rows + 31) / 32 >= 256;
+        const dim3 G((unsigned)(two ? (n_rows + 31) / 32 : (n_rows + 15) / 16));
+#define Q4K_SB(TI, TJ, NW)                                                                                           \
+    do {                                                                                                              \
+        if (sums) hipLaunchKernelGGL((k_mmq_q4k_sb<TI, TJ, NW, true>), G, dim3(64 * NW), 0, st, wq, wh, (int)n_rows, \
+                                     nsb, a16, bs16, dt, (int)m, dst, ldd, sums);                                     \
+        else hipLaunchKernelGGL((k_mmq_q4k_sb<TI, TJ, NW, false>), G, dim3(64 * NW), 0, st, wq, wh, (int)n_rows, nsb, \
+                                a16, bs16, dt, (int)m, dst, ldd, sums);                                               \
+    } while (0)
+        if (m <= 16) {
+            if (two) Q4K_SB(2, 1, 4);
+            else Q4K_SB(1, 1, 8);
+        } else {
+            if (two) Q4K_SB(2, 2, 4);
+            else Q4K_SB(1, 2, 4);  // 8 waves of this tile would spill registers
+        }
+#undef Q4K_SB
     } else if (m <= 64) {
         Q4K_LAUNCH(1, 1, dim3(gx, (unsigned)((m + 63) / 64)));
     } else {
