@@ -507,16 +507,16 @@ __device__ __forceinline__ k4_h8 k4_nib_f16(uint32_t x0, uint32_t x1, k4_h2 sc2)
     return k4_h8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
 }
 
-// KS = 4 (small batches): the 4 waves share one 32 x 32 TT tile and split the super-blocks (wave w takes j = w,
-// w + 4, ...); their f32 partials are added in LDS in wave order.
-template <bool SUMS, int TT, int KS>
-__global__ __launch_bounds__(KS > 1 ? 64 * KS : 256) void k_mmq_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
+// 33..64 tokens: a workgroup of 2 x 2 waves on 64 rows x 64 TT tokens, each wave one 32 x 32 TT tile over all the
+// super-blocks (smaller batches run k_mmq_q4k_sb).
+template <bool SUMS, int TT>
+__global__ __launch_bounds__(256) void k_mmq_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
                                                 int nsb, const uint16_t* __restrict__ a16,
                                                 const uint16_t* __restrict__ bs16, const float* __restrict__ dt, int M,
                                                 float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ sums) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = lane & 31, h = lane >> 5;
-    const int row0 = KS > 1 ? blockIdx.x * 32 : blockIdx.x * 64 + 32 * (w & 1);
-    const int tok0 = KS > 1 ? blockIdx.y * (32 * TT) : blockIdx.y * (64 * TT) + 32 * TT * (w >> 1);
+    const int row0 = blockIdx.x * 64 + 32 * (w & 1);
+    const int tok0 = blockIdx.y * (64 * TT) + 32 * TT * (w >> 1);
     const int K = nsb * 256;
     const int row = min(row0 + c, N - 1);
     const uint4* qrow = wq + (size_t)row * nsb * 8 + 4 * h;  // 8 uint4 of qs per super-block; this half's 4
@@ -535,20 +535,17 @@ __global__ __launch_bounds__(KS > 1 ? 64 * KS : 256) void k_mmq_q4k(const uint4*
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
-    // the weights of the wave's next super-block are loaded while this one computes
-    const int j_first = KS > 1 ? w : 0;
-    uint4 nq4[4], nhd = make_uint4(0, 0, 0, 0);
-    if (j_first < nsb) {
+    // the weights of the next super-block are loaded while this one computes
+    uint4 nq4[4], nhd;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) nq4[i] = qrow[(size_t)j_first * 8 + i];
-        nhd = hrow[j_first];
-    }
-    for (int j = j_first; j < nsb; j += KS) {
+    for (int i = 0; i < 4; ++i) nq4[i] = qrow[i];
+    nhd = hrow[0];
+    for (int j = 0; j < nsb; ++j) {
         uint4 q4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) q4[i] = nq4[i];
         const uint4 hd = nhd;
-        const int jn = min(j + KS, nsb - 1);  // the last super-block reloads itself (unused)
+        const int jn = min(j + 1, nsb - 1);  // the last super-block reloads itself (unused)
 #pragma unroll
         for (int i = 0; i < 4; ++i) nq4[i] = qrow[(size_t)jn * 8 + i];
         nhd = hrow[jn];
@@ -624,23 +621,6 @@ __global__ __launch_bounds__(KS > 1 ? 64 * KS : 256) void k_mmq_q4k(const uint4*
                 }
             }
         }
-    }
-    if constexpr (KS > 1 && !SUMS) {
-        __shared__ float red[KS - 1][TT * 16][64];
-        if (w > 0) {
-#pragma unroll
-            for (int t = 0; t < TT; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) red[w - 1][t * 16 + r][lane] = acc[t][r];
-        }
-        __syncthreads();
-        if (w > 0) return;
-#pragma unroll
-        for (int t = 0; t < TT; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-#pragma unroll
-                for (int o = 0; o < KS - 1; ++o) acc[t][r] += red[o][t * 16 + r][lane];  // wave order
     }
     if (!SUMS) {
         const int n = row0 + c;
@@ -824,14 +804,6 @@ static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, in
     const uint16_t* bs16 = (const uint16_t*)((const uint8_t*)act + L.bs16);
     const float* dt = (const float*)((const uint8_t*)act + L.dt);
     const unsigned gx = (unsigned)((n_rows + 63) / 64);
-#define Q4K_LAUNCH(TT, KS, G) \
-    do { \
-        const dim3 B(KS > 1 ? 64 * KS : 256); \
-        if (sums) hipLaunchKernelGGL((k_mmq_q4k<true, TT, KS>), G, B, 0, st, wq, wh, (int)n_rows, nsb, a16, \
-                                     bs16, dt, (int)m, dst, ldd, sums); \
-        else hipLaunchKernelGGL((k_mmq_q4k<false, TT, KS>), G, B, 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, \
-                                dt, (int)m, dst, ldd, sums); \
-    } while (0)
     if (m <= 32) {
         // small batches, streamed: two 16-row tiles per wave and 4 waves while that leaves >= 256 workgroups, else one
         // tile and 8 waves splitting the super-blocks (4 for two token tiles)
@@ -852,12 +824,13 @@ static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, in
             else Q4K_SB(1, 2, 4);  // 8 waves of this tile would spill registers
         }
 #undef Q4K_SB
-    } else if (m <= 64) {
-        Q4K_LAUNCH(1, 1, dim3(gx, (unsigned)((m + 63) / 64)));
-    } else {
-        Q4K_LAUNCH(2, 1, dim3(gx, (unsigned)((m + 127) / 128)));
+    } else {  // 33..64 tokens: 64-row x 64-token tiles of 2 x 2 waves
+        const dim3 G(gx, (unsigned)((m + 63) / 64));
+        if (sums) hipLaunchKernelGGL((k_mmq_q4k<true, 1>), G, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, dt,
+                                     (int)m, dst, ldd, sums);
+        else hipLaunchKernelGGL((k_mmq_q4k<false, 1>), G, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, a16, bs16, dt,
+                                (int)m, dst, ldd, sums);
     }
-#undef Q4K_LAUNCH
     return amv_check_launch("amv_mul_mat_q");
 }
 
