@@ -134,6 +134,21 @@ __device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, ui
     }
 }
 
+// Scales and mins of the unit pair 2c, 2c + 1 (c = 0..3, may vary per lane) without branches: byte pair c & 1 of each
+// scale dword; for c >= 2 the 6-bit values are the low (scale) / high (min) nibbles of bytes 8..11 with the top two
+// bits from bytes 0..3 (scales) / 4..7 (mins), as get_scale_min_k4.
+__device__ __forceinline__ void k4_scale_min_pair(int c, uint32_t s0, uint32_t s1, uint32_t s2, int& sl, int& ml,
+                                                  int& sh, int& mh) {
+    const int sh16 = 16 * (c & 1);
+    const uint32_t A = s0 >> sh16, B = s1 >> sh16, C = s2 >> sh16;
+    const uint32_t scp = c < 2 ? (A & 0x3F3Fu) : ((C & 0x0F0Fu) | ((A >> 2) & 0x3030u));
+    const uint32_t mp = c < 2 ? (B & 0x3F3Fu) : (((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u));
+    sl = (int)(scp & 0xFFu);
+    sh = (int)((scp >> 8) & 0xFFu);
+    ml = (int)(mp & 0xFFu);
+    mh = (int)((mp >> 8) & 0xFFu);
+}
+
 // signed 4x8-bit dot product with 32-bit accumulate (v_dot4_i32_i8)
 __device__ __forceinline__ int amv_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

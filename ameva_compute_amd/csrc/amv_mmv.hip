@@ -503,7 +503,14 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
                 row = lr;
             }
             q[r] = amv_ld_stream(wqs + (size_t)row * nsl + j);
-            hd[r] = amv_ld_stream(whs + (size_t)row * nsb + sb);
+            // the super-block's 16-byte head: each lane of a quad loads one dword (the quad shares the super-block:
+            // groups of 8 lanes do, clamped lanes included), then DPP hands every lane all four
+            const uint32_t hv =
+                amv_ld_stream(reinterpret_cast<const uint32_t*>(whs + (size_t)row * nsb + sb) + (lane & 3));
+            hd[r] = make_uint4(__builtin_amdgcn_mov_dpp(hv, 0x00, 0xF, 0xF, false),   // quad_perm [0,0,0,0]
+                               __builtin_amdgcn_mov_dpp(hv, 0x55, 0xF, 0xF, false),   // [1,1,1,1]
+                               __builtin_amdgcn_mov_dpp(hv, 0xAA, 0xF, 0xF, false),   // [2,2,2,2]
+                               __builtin_amdgcn_mov_dpp(hv, 0xFF, 0xF, 0xF, false));  // [3,3,3,3]
         }
         const int4 alo = a4[sb * 16 + 4 * c + h], ahi = a4[sb * 16 + 4 * c + 2 + h];
         const float da = ad[sb];
@@ -511,8 +518,7 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             int sl, ml, sh, mh;
-            k4_scale_min(2 * c, hd[r].y, hd[r].z, hd[r].w, sl, ml);
-            k4_scale_min(2 * c + 1, hd[r].y, hd[r].z, hd[r].w, sh, mh);
+            k4_scale_min_pair(c, hd[r].y, hd[r].z, hd[r].w, sl, ml, sh, mh);
             const uint4 lo = make_uint4(q[r].x & M4, q[r].y & M4, q[r].z & M4, q[r].w & M4);
             const uint4 hi = make_uint4((q[r].x >> 4) & M4, (q[r].y >> 4) & M4, (q[r].z >> 4) & M4, (q[r].w >> 4) & M4);
             int isum = sl * dot16(lo, alo, 0) + sh * dot16(hi, ahi, 0);
@@ -789,30 +795,12 @@ static int mmv_one_column(const MmvArgs& a, hipStream_t st) {
         return AMV_OK;
     case AMV_T_Q4_K: {
         // from the MI355X sweep (cold, streaming loads): long rows split K in four (4096 x 14336: 8.5 us against 9.1 us
-        // with S = 2); 8192 .. 16383 rows split K in two (14336 x 4096: 7.9 us with 4 rows per wave against 8.8 us
-        // for R = 2 unsplit); taller launches (the stacked 28672 x 4096 gate/up) stay unsplit, where the SWIGLU
-        // epilogue's per-block arrivals would double. S depends on the launch shape only, so a fused epilogue sums
-        // each row in the order of the plain GEMV of the same weight (bit-identical results); R, which does not change
-        // a row's sums, is 4 wherever the epilogue allows it (28672 x 4096 plain: 13.4 us against 14.5 us).
+        // with S = 2); K = 4096 unsplit with 2 rows per wave (14336 x 4096 7.6 us, the stacked 28672 x 4096 12.6 us,
+        // against 8.1 / 12.7 us for 4 rows per wave split in two, since the head arrives as one dword per lane and
+        // the unit scales decode without branches). S depends on the launch shape only, so a fused epilogue sums
+        // each row in the order of the plain GEMV of the same weight (bit-identical results).
         const int64_t steps = (nb + 63) / 64;
-        const int S = BS ? 1
-                      : steps >= 4                                           ? 4
-                      : (a.n_rows >= 8192 && a.n_rows < 16384 && steps >= 2) ? 2
-                                                                             : split(groups2, steps);
-        if constexpr (!BS && !MMV_STACKED(EP) && EP != MMV_EP_ROPE_KV && !MMV_TAIL(EP)) {
-            if (a.n_rows >= 8192 && a.n_rows % 4 == 0 && steps < 4) {
-                launch_q4_K_s<4, BS, EP>(a, st, S);
-                return AMV_OK;
-            }
-        }
-        if constexpr (!BS && MMV_STACKED(EP)) {
-            // the stacked gate/up of 16384+ rows unsplit: two outputs per wave (rows o, o + 1 and F + o, F + o + 1),
-            // as the plain GEMV's 4 rows per wave
-            if (a.n_rows >= 16384 && a.n_rows % 4 == 0 && S == 1) {
-                launch_q4_K_s<4, BS, EP>(a, st, S);
-                return AMV_OK;
-            }
-        }
+        const int S = BS ? 1 : steps >= 4 ? 4 : split(groups2, steps);
         launch_q4_K_s<2, BS, EP>(a, st, S);
         return AMV_OK;
     }
