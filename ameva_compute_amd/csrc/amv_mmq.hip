@@ -844,8 +844,10 @@ int amv_qgemm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
 // prefix (Q4_0 / Q8_0) or the f16 copies of AMV_ACT_Q8_K_MMA (Q4_K).
 #define MMQ16_MIN_M 64
 
+// q4k_mma: act is AMV_ACT_Q8_K_MMA (the small-batch Q4_K kernels read its f16 copies); with a plain Q8_K act every
+// Q4_K batch runs the tiled int8 kernel
 static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
-                    int64_t ldd, int32_t* sums, void* stream) {
+                    int64_t ldd, int32_t* sums, void* stream, bool q4k_mma = false) {
     AMV_REQUIRE(w && act && (dst || sums), "amv_mul_mat_q: null pointer");
     AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0 || wtype == AMV_T_Q4_K || wtype == AMV_T_Q6_K,
                 "amv_mul_mat_q: weight type %d not supported (Q4_0, Q8_0, Q4_K, Q6_K)", wtype);
@@ -853,7 +855,8 @@ static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const v
     AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 32 && n_rows * (k / 32) <= INT32_MAX, "amv_mul_mat_q: too large");
     AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "amv_mul_mat_q: buffers must be 16-byte aligned");
     AMV_REQUIRE(!dst || ldd >= n_rows, "amv_mul_mat_q: ldd < n_rows");
-    if (m > MMQ16_MIN_M || wtype == AMV_T_Q6_K) {  // the tiled int8 kernel reads the plain prefix of any layout
+    // the tiled int8 kernel reads the plain prefix of any layout
+    if (m > MMQ16_MIN_M || wtype == AMV_T_Q6_K || (wtype == AMV_T_Q4_K && !q4k_mma)) {
         AMV_REQUIRE((wtype != AMV_T_Q4_K && wtype != AMV_T_Q6_K) || k % 256 == 0,
                     "amv_mul_mat_q: K-quants need k %% 256 == 0");
         AMV_REQUIRE(m * k <= INT32_MAX && m <= 65535LL * 128, "amv_mul_mat_q: too large");
@@ -915,7 +918,7 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
     // the small-batch Q4_K kernel reads the f16 copies as exact integers
     AMV_REQUIRE(!(deq && wtype == AMV_T_Q4_K), "%s: Q4_K batches of m <= %d need the exact layout AMV_ACT_Q8_K_MMA",
                 fn, MMQ16_MIN_M);
-    return mmq_impl(wtype, w, n_rows, k, act, m, dst, ldd, sums, stream);
+    return mmq_impl(wtype, w, n_rows, k, act, m, dst, ldd, sums, stream, q8kx);
 }
 
 extern "C" int amv_mul_mat_q_act(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type,

@@ -166,9 +166,10 @@ int amv_mul_mat_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, 
                            int32_t* sums, void* stream);
 
 /* Prefill MUL_MAT with int8 MFMA (enc_mul_mat_mmq ggml-ameva.cpp:2540-2647, ameva_mmq.comp): same operands and
- * result as amv_mul_mat_vec, for Q4_0 / Q8_0 weights and many activation columns (the reference switches at
- * M >= AMEVA_QGEMM_MIN_M = 8, ggml-ameva.cpp:2486-2505). The _block_sums form writes the MFMA's exact per-block
- * integers, int32 [m][n_rows][k/32], for the bit-exact check. */
+ * result as amv_mul_mat_vec (plain Q8_0 activations for Q4_0 / Q8_0, plain Q8_K for Q4_K / Q6_K) and many activation
+ * columns (the reference switches at M >= AMEVA_QGEMM_MIN_M = 8, ggml-ameva.cpp:2486-2505). The _block_sums form
+ * writes the MFMA's exact per-block integers, int32 [m][n_rows][k/32] (Q4_K: [..][k/256][2]), for the bit-exact
+ * check. */
 int amv_mul_mat_q(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                   int64_t ldd, void* stream);
 int amv_mul_mat_q_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m,

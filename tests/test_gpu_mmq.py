@@ -221,3 +221,21 @@ def test_split_k_under_graph_capture(dev, ops, orc):
         torch.cuda.synchronize()
         assert torch.isfinite(yb).all()
     assert torch.equal(ops.mul_mat_q(w, act, m, kernel="mmq", act_t=ops.Q8_0_DEQ), y_eager)
+
+
+@pytest.mark.parametrize("m", [8, 16, 40])
+def test_mul_mat_q_plain_q8k_for_q4k(dev, ops, orc, m):
+    """amv_mul_mat_q with a plain Q8_K activation (no f16 copies) for Q4_K weights: small batches go to the tiled
+    int8 kernel, which reads only the plain layout (the small-batch kernels need AMV_ACT_Q8_K_MMA)."""
+    from ameva_compute_amd._lib import lib
+    rng = np.random.default_rng(300 + m)
+    n, k = 96, 1024
+    wg = random_q4k(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y_ref = orc.mul_mat(ops.Q4_K, wg, n, k, orc.quantize_q8_K(x), m)
+    w = ops.QWeight.from_ggml(ops.Q4_K, gpu(wg, dev), n, k)
+    plain, _ = ops.quantize_act(gpu(x, dev), ops.Q8_K)
+    out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    assert lib().amv_mul_mat_q(ops.Q4_K, w.data.data_ptr(), n, k, plain.data_ptr(), m, out.data_ptr(), n,
+                               torch.cuda.current_stream().cuda_stream) == 0
+    assert rel_l2(out.cpu().numpy(), y_ref) < TOL_F32
