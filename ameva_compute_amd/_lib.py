@@ -49,6 +49,7 @@ SIGNATURES = {
     "amv_rope_kv_store": (I32, [P, P, I64, I64, I64, I64, I32, I32, F32, F32, F32, P, P, I64, P, I64, P, P]),
     "amv_swiglu": (I32, [P, P, P, I64, P]),
     "amv_swiglu_rows": (I32, [P, I64, P, I64, P, I64, I64, I64, P, I32, P]),
+    "amv_swiglu_rows_act": (I32, [P, I64, P, I64, P, I64, I64, I64, P, I32, I32, P]),
     "amv_flash_attn_workspace_bytes": (I64, [I64, I64, I64, I64]),
     "amv_flash_attn_decode": (I32, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I64, F32, P, I64, P, I32, P]),
     "amv_flash_attn_prefill": (I32, [P, I64, I64, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64, F32,

@@ -8,6 +8,8 @@
 // pair j is freq_scale * (p * theta_scale^j) built by the same repeated f32 multiplication as the CPU.
 #include "amv_common.h"
 
+#include <algorithm>
+
 // One workgroup of 1024 per row (amv_rms_row with one virtual lane per thread).
 #define RMS_THREADS 1024
 __global__ __launch_bounds__(RMS_THREADS) void k_rms_norm(const float* __restrict__ x, int n, float eps,
@@ -94,44 +96,73 @@ extern "C" int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// ROPE of q and k + SET_ROWS of k and v into the f16 cache, one launch per decode step. Token t's row of qkv holds
-// n_head q heads, n_head_kv k heads and n_head_kv v heads of D floats. Block (head, t), one wave: q and k heads are
-// rotated in place (k_rope's arithmetic, so the values equal ROPE's), k and v heads are also stored as f16 (amv_f2h,
-// round to nearest even as the CPU's fp32 -> fp16) at row kv_idx[t] of the caches; rows outside [0, cache_rows) are
-// skipped and counted in *bad.
+// ROPE of q and k + SET_ROWS of k and v into the f16 cache. Token t's row of qkv holds n_head q heads, n_head_kv k
+// heads and n_head_kv v heads of D floats. q and k heads are rotated in place (k_rope's arithmetic, so the values equal
+// ROPE's), k and v heads are also stored as f16 (amv_f2h, round to nearest even as the CPU's fp32 -> fp16) at row
+// kv_idx[t] of the caches; rows outside [0, cache_rows) are skipped and counted in *bad (once per k / v head).
+// Workgroup (token t, group of HPW heads): the cos / sin of the token's pairs are computed once into LDS (the angle
+// loop and sincos are the costly part of a pair), then thread i handles pair i % (D / 2) of head i / (D / 2), so a
+// wave's loads and stores cover consecutive pairs (NORMAL: one 8-byte load, one 8-byte store and one 4-byte f16 pair
+// store per pair).
 // ---------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void k_rope_kv(float* __restrict__ qkv, const int32_t* __restrict__ pos, int n_head,
-                                                int n_head_kv, int D, int n_dims, int neox, float theta_scale,
+#define ROPE_MAX_PAIRS 256  // D <= 512
+template <bool NEOX>
+__global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ qkv, const int32_t* __restrict__ pos, int n_head,
+                                                int n_head_kv, int D, int n_dims, int hpw, float theta_scale,
                                                 float freq_scale, float attn_factor, uint16_t* __restrict__ kc,
                                                 uint16_t* __restrict__ vc, int64_t cache_row,
                                                 const int64_t* __restrict__ kv_idx, int64_t cache_rows,
-                                                unsigned int* __restrict__ bad) {
-    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-    const int n_all = n_head + 2 * n_head_kv;
-    float* xr = qkv + ((int64_t)t * n_all + h) * D;
-    const bool is_q = h < n_head, is_v = h >= n_head + n_head_kv;
-    const int64_t dr = is_q ? 0 : kv_idx[t];
-    const bool store = !is_q && dr >= 0 && dr < cache_rows;
-    if (!is_q && !store && lane == 0 && bad) atomicAdd(bad, 1u);
-    uint16_t* cr = nullptr;
-    if (store) cr = (is_v ? vc + (int64_t)(h - n_head - n_head_kv) * D : kc + (int64_t)(h - n_head) * D) + dr * cache_row;
-    if (is_v) {
-        if (store)
-            for (int e = lane; e < D; e += 64) cr[e] = amv_f2h(xr[e]);
-        return;
-    }
+                                                unsigned int* __restrict__ bad, bool pair_stores) {
+    __shared__ float s_c[ROPE_MAX_PAIRS], s_s[ROPE_MAX_PAIRS];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int half = D / 2, n_all = n_head + 2 * n_head_kv;
+    const int h0 = blockIdx.y * hpw, h1 = min(n_all, h0 + hpw);
     const float p = (float)pos[t];
-    for (int j = lane; j < D / 2; j += 64) {
-        const int e0 = 2 * j >= n_dims ? 2 * j : (neox ? j : 2 * j);
-        const int e1 = 2 * j >= n_dims ? 2 * j + 1 : (neox ? j + n_dims / 2 : 2 * j + 1);
-        const float x0 = xr[e0], x1 = xr[e1];
-        float y0 = x0, y1 = x1;
-        if (2 * j < n_dims) amv_rope_pair(p, j, theta_scale, freq_scale, attn_factor, x0, x1, y0, y1);
-        xr[e0] = y0;
-        xr[e1] = y1;
-        if (store) {
-            cr[e0] = amv_f2h(y0);
-            cr[e1] = amv_f2h(y1);
+    for (int j = tid; 2 * j < n_dims; j += 256) {
+        float c, sn;
+        amv_rope_cs(p, j, theta_scale, freq_scale, attn_factor, c, sn);
+        s_c[j] = c;
+        s_s[j] = sn;
+    }
+    const int64_t dr = kv_idx[t];
+    const bool store = dr >= 0 && dr < cache_rows;
+    if (!store && bad) {  // one count per k / v head of this group
+        const int nkv = max(0, h1 - max(h0, n_head));
+        if (tid == 0 && nkv > 0) atomicAdd(bad, (unsigned)nkv);
+    }
+    __syncthreads();
+    float* xt = qkv + (int64_t)t * n_all * D;
+    for (int i = h0 * half + tid; i < h1 * half; i += 256) {
+        const int h = i / half, j = i - h * half;
+        float* xr = xt + (int64_t)h * D;
+        const bool is_q = h < n_head, is_v = h >= n_head + n_head_kv;
+        const bool rot = !is_v && 2 * j < n_dims;
+        uint16_t* cr = nullptr;
+        if (!is_q && store)
+            cr = (is_v ? vc + (int64_t)(h - n_head - n_head_kv) * D : kc + (int64_t)(h - n_head) * D) + dr * cache_row;
+        if (NEOX && rot) {
+            const int e0 = j, e1 = j + n_dims / 2;
+            float y0, y1;
+            amv_rope_apply(s_c[j], s_s[j], xr[e0], xr[e1], y0, y1);
+            xr[e0] = y0;
+            xr[e1] = y1;
+            if (cr) {
+                cr[e0] = amv_f2h(y0);
+                cr[e1] = amv_f2h(y1);
+            }
+        } else {
+            const float2 x = *reinterpret_cast<const float2*>(xr + 2 * j);
+            float2 y = x;
+            if (rot) amv_rope_apply(s_c[j], s_s[j], x.x, x.y, y.x, y.y);
+            if (!is_v) *reinterpret_cast<float2*>(xr + 2 * j) = y;
+            if (cr) {
+                if (pair_stores) {
+                    *reinterpret_cast<uint32_t*>(cr + 2 * j) = (uint32_t)amv_f2h(y.x) | ((uint32_t)amv_f2h(y.y) << 16);
+                } else {
+                    cr[2 * j] = amv_f2h(y.x);
+                    cr[2 * j + 1] = amv_f2h(y.y);
+                }
+            }
         }
     }
 }
@@ -141,17 +172,29 @@ extern "C" int amv_rope_kv_store(float* qkv, const int32_t* pos, int64_t n_tok, 
                                  void* k_cache, void* v_cache, int64_t cache_row, const int64_t* kv_idx,
                                  int64_t cache_rows, unsigned int* bad, void* stream) {
     AMV_REQUIRE(qkv && pos && k_cache && v_cache && kv_idx, "amv_rope_kv_store: null pointer");
-    AMV_REQUIRE(n_tok > 0 && n_tok <= 65535 && n_head > 0 && n_head_kv > 0 && D > 0 && D % 2 == 0,
+    AMV_REQUIRE(n_tok > 0 && n_tok <= INT32_MAX && n_head > 0 && n_head_kv > 0 && D > 0 && D % 2 == 0 &&
+                    D <= 2 * ROPE_MAX_PAIRS && n_head + 2 * n_head_kv <= 65535,
                 "amv_rope_kv_store: bad shape");
+    AMV_REQUIRE(((uintptr_t)qkv & 7) == 0, "amv_rope_kv_store: qkv must be 8-byte aligned");
     AMV_REQUIRE(n_dims > 0 && n_dims <= D && n_dims % 2 == 0, "amv_rope_kv_store: bad n_dims %d", n_dims);
     AMV_REQUIRE(mode == 0 || mode == 2, "amv_rope_kv_store: mode %d not supported (NORMAL 0 and NEOX 2 are)", mode);
     AMV_REQUIRE(cache_row >= n_head_kv * D && cache_rows > 0, "amv_rope_kv_store: cache row %lld < %lld",
                 (long long)cache_row, (long long)(n_head_kv * D));
     const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
-    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)(n_head + 2 * n_head_kv), (unsigned)n_tok), dim3(64), 0,
-                       amv_stream(stream), qkv, pos, (int)n_head, (int)n_head_kv, (int)D, n_dims, mode == 2 ? 1 : 0,
-                       theta_scale, freq_scale, attn_factor, (uint16_t*)k_cache, (uint16_t*)v_cache, cache_row,
-                       kv_idx, cache_rows, bad);
+    // heads per workgroup: all of a token's heads when there are enough tokens to fill the GPU, else fewer
+    const int n_all = (int)(n_head + 2 * n_head_kv);
+    const int hpw = (int)std::max<int64_t>(1, std::min<int64_t>(n_all, (int64_t)n_all * n_tok / 512));
+    const dim3 grid((unsigned)n_tok, (unsigned)((n_all + hpw - 1) / hpw));
+    // f16 pairs as one 4-byte store when every pair starts 4-byte aligned
+    const bool pairs = cache_row % 2 == 0 && ((uintptr_t)k_cache & 3) == 0 && ((uintptr_t)v_cache & 3) == 0;
+    if (mode == 2)
+        hipLaunchKernelGGL(k_rope_kv<true>, grid, dim3(256), 0, amv_stream(stream), qkv, pos, (int)n_head,
+                           (int)n_head_kv, (int)D, n_dims, hpw, theta_scale, freq_scale, attn_factor,
+                           (uint16_t*)k_cache, (uint16_t*)v_cache, cache_row, kv_idx, cache_rows, bad, pairs);
+    else
+        hipLaunchKernelGGL(k_rope_kv<false>, grid, dim3(256), 0, amv_stream(stream), qkv, pos, (int)n_head,
+                           (int)n_head_kv, (int)D, n_dims, hpw, theta_scale, freq_scale, attn_factor,
+                           (uint16_t*)k_cache, (uint16_t*)v_cache, cache_row, kv_idx, cache_rows, bad, pairs);
     return amv_check_launch("amv_rope_kv_store");
 }
 
@@ -186,17 +229,56 @@ __global__ __launch_bounds__(256) void k_swiglu_q8(const float* __restrict__ g, 
     if (aq) amv_q8_0_lanes32(h, rule, (int)(c & 31), aq + r * n + (c & ~(int64_t)31), am + r * (n / 32) + c / 32);
 }
 
-extern "C" int amv_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* y,
-                               int64_t y_stride, int64_t n_rows, int64_t n, void* act, int rule, void* stream) {
+// The same SWIGLU four elements per thread (float4 chunk i of the concatenated rows), with the quantization of each
+// output row to Q8_0 or Q8_K fused (amv_act_store4: a Q8_0 block is 8 consecutive lanes, a Q8_K block one wave); the
+// values and bytes equal k_swiglu_q8's and amv_quantize_act's.
+__device__ __forceinline__ float amv_swiglu1(float a, float b) { return (a / (1.0f + expf(-a))) * b; }
+__global__ __launch_bounds__(256) void k_swiglu_act(const float* __restrict__ g, int64_t gs,
+                                                   const float* __restrict__ u, int64_t us, float* __restrict__ y,
+                                                   int64_t ys, int total4, int n4, const AmvActOut act) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= total4) return;  // rows hold whole quantization blocks, so blocks leave together
+    const int r = i / n4, c = i - r * n4;
+    const float4 a = *reinterpret_cast<const float4*>(g + r * gs + 4 * c);
+    const float4 b = *reinterpret_cast<const float4*>(u + r * us + 4 * c);
+    const float h[4] = {amv_swiglu1(a.x, b.x), amv_swiglu1(a.y, b.y), amv_swiglu1(a.z, b.z), amv_swiglu1(a.w, b.w)};
+    if (y) *reinterpret_cast<float4*>(y + r * ys + 4 * c) = make_float4(h[0], h[1], h[2], h[3]);
+    if (act.type) amv_act_store4(amv_act_row(act, r, 4 * (int64_t)n4), c, h);
+}
+
+extern "C" int amv_swiglu_rows_act(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* y,
+                                   int64_t y_stride, int64_t n_rows, int64_t n, void* act, int act_type, int rule,
+                                   void* stream) {
     AMV_REQUIRE(g && u && (y || act) && n_rows > 0 && n > 0, "amv_swiglu_rows: bad arguments");
     AMV_REQUIRE(g_stride >= n && u_stride >= n && (!y || y_stride >= n), "amv_swiglu_rows: row stride < n");
-    AMV_REQUIRE(!act || n % 32 == 0, "amv_swiglu_rows: the Q8_0 output needs n %% 32 == 0");
+    AMV_REQUIRE(!act || act_type == AMV_T_Q8_0 || act_type == AMV_T_Q8_K,
+                "amv_swiglu_rows: act_type %d (Q8_0 or Q8_K)", act_type);
+    const int bs = act_type == AMV_T_Q8_K ? 256 : 32;
+    AMV_REQUIRE(!act || n % bs == 0, "amv_swiglu_rows: the quantized output needs n %% %d == 0", bs);
     AMV_REQUIRE(!act || ((uintptr_t)act & 7) == 0, "amv_swiglu_rows: act must be 8-byte aligned");
     AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_swiglu_rows: unknown rule %d", rule);
-    int8_t* aq = (int8_t*)act;
-    int2* am = act ? reinterpret_cast<int2*>(aq + n_rows * n) : nullptr;
-    const int64_t total = n_rows * n;
-    hipLaunchKernelGGL(k_swiglu_q8, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, amv_stream(stream), g,
-                       g_stride, u, u_stride, y, y_stride, n_rows, n, rule, aq, am);
+    const bool vec = n % 4 == 0 && g_stride % 4 == 0 && u_stride % 4 == 0 && (!y || y_stride % 4 == 0) &&
+                     ((uintptr_t)g & 15) == 0 && ((uintptr_t)u & 15) == 0 && ((uintptr_t)y & 15) == 0 &&
+                     n_rows * std::max(std::max(g_stride, u_stride), y ? y_stride : 0) <= INT32_MAX;
+    hipStream_t st = amv_stream(stream);
+    if (vec) {
+        const int64_t total4 = n_rows * (n / 4);
+        hipLaunchKernelGGL(k_swiglu_act, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0, st, g, g_stride, u,
+                           u_stride, y, y_stride, (int)total4, (int)(n / 4),
+                           amv_act_out(act, n, act ? act_type : 0, rule, n_rows));
+    } else {
+        AMV_REQUIRE(!act || act_type == AMV_T_Q8_0,
+                    "amv_swiglu_rows: the Q8_K output needs 16-byte aligned rows of whole float4s");
+        int8_t* aq = (int8_t*)act;
+        int2* am = act ? reinterpret_cast<int2*>(aq + n_rows * n) : nullptr;
+        const int64_t total = n_rows * n;
+        hipLaunchKernelGGL(k_swiglu_q8, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, g, g_stride, u,
+                           u_stride, y, y_stride, n_rows, n, rule, aq, am);
+    }
     return amv_check_launch("amv_swiglu_rows");
+}
+
+extern "C" int amv_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* y,
+                               int64_t y_stride, int64_t n_rows, int64_t n, void* act, int rule, void* stream) {
+    return amv_swiglu_rows_act(g, g_stride, u, u_stride, y, y_stride, n_rows, n, act, AMV_T_Q8_0, rule, stream);
 }

@@ -177,7 +177,7 @@ class LlamaLayer:
                 "act_att": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
                 "act_h2": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
                 "act_ff": torch.empty(L.amv_act_bytes(at, n_tok, FF), **u8),
-                "h": torch.empty((n_tok, FF), **f32) if at != ops.Q8_0 else None,
+                "h": torch.empty((n_tok, FF), **f32) if at not in (ops.Q8_0, ops.Q8_K) else None,
                 "pos": torch.zeros(n_tok, dtype=torch.int32, device=dev),
                 "idx": torch.zeros(n_tok, dtype=torch.int64, device=dev)}
         self._pf = bufs
@@ -195,8 +195,8 @@ class LlamaLayer:
         """A prompt chunk through the layer: x f32 [n_tok, H] at positions set_prefill_position(pos0, n_tok) ->
         out f32 [n_tok, H]; writes the chunk's K/V rows into the cache and attends causally over keys
         0 .. pos0 + t. The MUL_MATs run on the int8 MFMA kernel (n_tok >= 8, the reference's crossover) and the
-        attention on the f16 MFMA prefill kernel; 12 launches (15 for the K-quants, whose activation
-        quantization is a launch of its own)."""
+        attention on the f16 MFMA prefill kernel; 12 launches (15 where the activation layout is an extended one,
+        whose quantization is a launch of its own)."""
         L, st = lib(), torch.cuda.current_stream().cuda_stream
         n, pos0 = self.pf_n, self.pf_pos0
         b = self._prefill_buffers(n)
@@ -208,13 +208,13 @@ class LlamaLayer:
                 return L.amv_mul_mat_q_act(wt, w, nr, k, act, at, m, dst, ldd, s)
         else:
             mm = L.amv_mul_mat_vec
-        q8 = at == ops.Q8_0
+        q8 = at in (ops.Q8_0, ops.Q8_K)  # plain layouts: the norms and SWIGLU write them directly
 
         def quant(src, k, act):
             check(L.amv_quantize_act(at, src, n, k, ops.Q8_X86, None, P(act), st), "quantize")
 
-        check(L.amv_rms_norm(P(x), n, H, self.eps, P(self.attn_norm), None, P(b["t_o"]),
-                             P(b["act_h"]) if q8 else None, ops.Q8_X86, st), "rms_norm")
+        check(L.amv_rms_norm_act(P(x), n, H, self.eps, P(self.attn_norm), None, P(b["t_o"]),
+                                 P(b["act_h"]) if q8 else None, at, ops.Q8_X86, st), "rms_norm")
         if not q8:
             quant(P(b["t_o"]), H, b["act_h"])
         nq = self.wqkv.n_rows
@@ -228,15 +228,15 @@ class LlamaLayer:
         quant(P(b["att"]), H, b["act_att"])
         check(mm(self.wo.type, P(self.wo.data), H, H, P(b["act_att"]), n, P(b["proj"]), H, st), "wo")
         check(L.amv_binary(0, P(b["proj"]), P(x), P(b["x1"]), n, H, n, st), "residual 1")
-        check(L.amv_rms_norm(P(b["x1"]), n, H, self.eps, P(self.ffn_norm), None, P(b["t_o2"]),
-                             P(b["act_h2"]) if q8 else None, ops.Q8_X86, st), "ffn norm")
+        check(L.amv_rms_norm_act(P(b["x1"]), n, H, self.eps, P(self.ffn_norm), None, P(b["t_o2"]),
+                                 P(b["act_h2"]) if q8 else None, at, ops.Q8_X86, st), "ffn norm")
         if not q8:
             quant(P(b["t_o2"]), H, b["act_h2"])
         ng = self.wgu.n_rows
         check(mm(self.wgu.type, P(self.wgu.data), ng, H, P(b["act_h2"]), n, P(b["gu"]), ng, st), "gate_up")
         if q8:
-            check(L.amv_swiglu_rows(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, None, FF, n, FF, P(b["act_ff"]),
-                                    ops.Q8_X86, st), "swiglu + quant")
+            check(L.amv_swiglu_rows_act(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, None, FF, n, FF, P(b["act_ff"]),
+                                        at, ops.Q8_X86, st), "swiglu + quant")
         else:
             check(L.amv_swiglu_rows(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, P(b["h"]), FF, n, FF, None, ops.Q8_X86,
                                     st), "swiglu")

@@ -374,9 +374,9 @@ def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     return y
 
 
-def swiglu_rows(g: torch.Tensor, u: torch.Tensor, quantize: bool = False, rule: int = Q8_X86):
-    """SWIGLU of row views g, u [n_rows, n] (contiguous rows, any row stride). Returns y, or (y, act) with the Q8_0
-    activation buffer of y (amv_quantize_act layout) when quantize."""
+def swiglu_rows(g: torch.Tensor, u: torch.Tensor, quantize: bool = False, rule: int = Q8_X86, act_type: int = Q8_0):
+    """SWIGLU of row views g, u [n_rows, n] (contiguous rows, any row stride). Returns y, or (y, act) with the
+    activation buffer of y (amv_quantize_act layout, act_type Q8_0 or Q8_K) when quantize."""
     _need_gpu(g, "swiglu_rows", contiguous=False)
     n_rows, n = g.shape
     if g.stride(1) != 1 or u.stride(1) != 1 or u.shape != g.shape:
@@ -384,9 +384,9 @@ def swiglu_rows(g: torch.Tensor, u: torch.Tensor, quantize: bool = False, rule: 
     y = torch.empty((n_rows, n), dtype=torch.float32, device=g.device)
     act = None
     if quantize:
-        act = torch.empty(lib().amv_act_bytes(Q8_0, n_rows, n), dtype=torch.uint8, device=g.device)
-    check(lib().amv_swiglu_rows(g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), y.data_ptr(), n, n_rows, n,
-                                _ptr(act), rule, _stream()), "amv_swiglu_rows")
+        act = torch.empty(lib().amv_act_bytes(act_type, n_rows, n), dtype=torch.uint8, device=g.device)
+    check(lib().amv_swiglu_rows_act(g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), y.data_ptr(), n, n_rows, n,
+                                    _ptr(act), act_type, rule, _stream()), "amv_swiglu_rows")
     return (y, act) if quantize else y
 
 

@@ -279,6 +279,10 @@ int amv_swiglu(const float* g, const float* u, float* y, int64_t n, void* stream
  * NULL when act is given). The act bytes equal amv_quantize_act of y. */
 int amv_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* y, int64_t y_stride,
                     int64_t n_rows, int64_t n, void* act, int rule, void* stream);
+/* amv_swiglu_rows with the fused quantization into the activation type of the next MUL_MAT: act_type 8 = Q8_0
+ * (`rule`, n % 32 == 0) or 15 = Q8_K (n % 256 == 0; g, u, y 16-byte aligned with strides and n multiples of 4). */
+int amv_swiglu_rows_act(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* y,
+                        int64_t y_stride, int64_t n_rows, int64_t n, void* act, int act_type, int rule, void* stream);
 
 /* ------------------------------------------------------------------------------------------------------------
  * FLASH_ATTN_EXT, decode (one query position), f16 K/V cache (enc_flash_attn ggml-ameva.cpp:4204-4284 with the key

@@ -194,6 +194,23 @@ def test_swiglu(dev, ops, orc):
     assert rel_l2(y, orc.swiglu(g, u)) < 1e-6
 
 
+@pytest.mark.parametrize("n_rows,F,act_type,offset", [(512, 14336, "Q8_0", 0), (512, 14336, "Q8_K", 0),
+                                                       (7, 512, "Q8_K", 0), (9, 96, "Q8_0", 0), (5, 96, "Q8_0", 1)])
+def test_swiglu_rows_quantized(dev, ops, orc, n_rows, F, act_type, offset):
+    """SWIGLU over the two halves of a stacked gate|up output with the activation of the next MUL_MAT fused: y within
+    1e-6 of the oracle, the Q8_0 / Q8_K bytes equal amv_quantize_act of y (offset 1: rows not 16-byte aligned, the
+    one-element-per-thread kernel)."""
+    at = getattr(ops, act_type)
+    rng = np.random.default_rng(n_rows + F + offset)
+    gu = (rng.standard_normal((n_rows, 2 * F + offset)) * 3).astype(np.float32)
+    t = gpu(gu, dev)
+    g, u = t[:, offset:offset + F], t[:, offset + F:]
+    y, act = ops.swiglu_rows(g, u, quantize=True, act_type=at)
+    assert rel_l2(y.cpu().numpy(), orc.swiglu(gu[:, offset:offset + F], gu[:, offset + F:])) < 1e-6
+    ref, _ = ops.quantize_act(y, at, ops.Q8_X86)
+    assert torch.equal(act, ref)
+
+
 # ---------------------------------------------------------------------------------------------- FA decode
 @pytest.mark.parametrize("n_head,n_head_kv,n_kv,stride", [(32, 8, 4096, 4096), (32, 8, 1000, 4096), (8, 8, 17, 64),
                                                           (16, 8, 300, 300), (8, 1, 1, 8), (32, 4, 2049, 2100)])
@@ -323,11 +340,13 @@ def test_gemv_epilogue_errors(dev, ops, orc):
 
 # ---------------------------------------------------------------------------------------------- ROPE + KV store
 @pytest.mark.parametrize("mode", [0, 2])
-@pytest.mark.parametrize("n_head,n_head_kv,D,n_tok", [(32, 8, 128, 1), (32, 8, 128, 5), (8, 2, 64, 3)])
+@pytest.mark.parametrize("n_head,n_head_kv,D,n_tok", [(32, 8, 128, 1), (32, 8, 128, 5), (8, 2, 64, 3),
+                                                      (32, 8, 128, 512), (4, 1, 256, 40)])
 def test_rope_kv_store(dev, ops, orc, mode, n_head, n_head_kv, D, n_tok):
-    """Equals amv_rope followed by the two SET_ROWS bit for bit, and the oracle's rope within 1e-5."""
+    """Equals amv_rope followed by the two SET_ROWS bit for bit, and the oracle's rope within 1e-5 (512 tokens: a
+    prefill chunk, every head of a token in one workgroup)."""
     rng = np.random.default_rng(n_head + D + n_tok + mode)
-    CTX = 64
+    CTX = max(64, n_tok)
     n_all = n_head + 2 * n_head_kv
     kvw = n_head_kv * D
     pos = rng.integers(0, 100000, n_tok).astype(np.int32)
@@ -353,6 +372,29 @@ def test_rope_kv_store(dev, ops, orc, mode, n_head, n_head_kv, D, n_tok):
     assert rel_l2(qkv[:, :n_head + n_head_kv].cpu().numpy(), ref) < 1e-5
     untouched = np.setdiff1d(np.arange(CTX), idx)
     assert np.array_equal(kc.cpu().numpy()[untouched].view(np.uint16), kc0[untouched].view(np.uint16))
+
+
+@pytest.mark.parametrize("n_dims", [128, 64])
+def test_rope_kv_store_strided_cache(dev, ops, n_dims):
+    """A cache of odd row stride (f16 pairs stored as halfwords) and partial rotation (n_dims < D) give the same
+    values as a contiguous cache."""
+    n_head, n_head_kv, D, n_tok, CTX = 8, 2, 128, 9, 16
+    kvw = n_head_kv * D
+    x = torch.randn((n_tok, n_head + 2 * n_head_kv, D), device=dev)
+    pos = torch.arange(100, 100 + n_tok, dtype=torch.int32, device=dev)
+    idx = torch.arange(n_tok, dtype=torch.int64, device=dev) + 3
+    kc = torch.zeros((CTX, kvw), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    q1 = x.clone()
+    ops.rope_kv_store(q1, pos, n_head, n_head_kv, kc, vc, idx, n_dims, 0, 500000.0)
+    kb = torch.zeros((CTX, kvw + 1), dtype=torch.float16, device=dev)
+    vb = torch.zeros_like(kb)
+    q2 = x.clone()
+    ops.rope_kv_store(q2, pos, n_head, n_head_kv, kb[:, :kvw], vb[:, :kvw], idx, n_dims, 0, 500000.0)
+    assert torch.equal(q1, q2)
+    assert torch.equal(kb[:, :kvw], kc) and torch.equal(vb[:, :kvw], vc) and not kb[:, kvw].any()
+    if n_dims < D:  # elements past n_dims are not rotated
+        assert torch.equal(q1[:, :n_head + n_head_kv, n_dims:], x[:, :n_head + n_head_kv, n_dims:])
 
 
 def test_rope_kv_store_bad_index(dev, ops):
