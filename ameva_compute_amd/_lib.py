@@ -29,6 +29,7 @@ SIGNATURES = {
     "amv_mul_mat_q": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
     "amv_mul_mat_q_block_sums": (I32, [I32, P, I64, I64, P, I64, P, P]),
     "amv_mul_mat_q_act": (I32, [I32, P, I64, I64, P, I32, I64, P, I64, P]),
+    "amv_mul_mat_q_act_add": (I32, [I32, P, I64, I64, P, I32, I64, P, I64, P, P]),
     "amv_mul_mat_q_act_block_sums": (I32, [I32, P, I64, I64, P, I32, I64, P, P]),
     "amv_i2s_act_bytes": (I64, [I64, I64]),
     "amv_i2s_quantize_act": (I32, [P, I64, I64, P, P]),

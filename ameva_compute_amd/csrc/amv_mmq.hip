@@ -837,7 +837,7 @@ static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, in
 // amv_qgemm.hip: Q4_0 / Q8_0 / Q4_K / Q6_K on the int8 matrix cores with exact block integers, plain activation
 // layouts
 int amv_qgemm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
-              int64_t ldd, int32_t* sums, hipStream_t st);
+              int64_t ldd, int32_t* sums, hipStream_t st, const float* add = nullptr);
 
 // Batches above this many tokens go to the tiled kernels (amv_qgemm for the exact layouts and the plain ones, the f16
 // kernels for the scaled DEQ layouts); smaller ones to the k_mmq kernels of this file, which read the plain Q8_0
@@ -888,8 +888,18 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
                   hipStream_t st);
 
 
+// dst[t][n] += add[t][n] (row stride ldd): the residual of a fused ADD for the kernels that do not take it
+__global__ __launch_bounds__(256) void k_add_rows(float* __restrict__ dst, const float* __restrict__ add, int64_t ldd,
+                                                 int m, int n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)m * n) return;
+    const int64_t o = (i / n) * ldd + i % n;
+    dst[o] = dst[o] + add[o];
+}
+
 static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
-                        int act_type, int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream) {
+                        int act_type, int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream,
+                        const float* add = nullptr) {
     const bool deq = act_type == AMV_ACT_Q8_0_DEQ || act_type == AMV_ACT_Q8_K_DEQ;
     const bool q80x = act_type == AMV_ACT_Q8_0_MMA || act_type == AMV_ACT_Q8_0_DEQ;
     const bool q8kx = act_type == AMV_ACT_Q8_K_MMA || act_type == AMV_ACT_Q8_K_DEQ;
@@ -897,6 +907,14 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
     const bool tiled = (m > MMQ16_MIN_M && (((q80x || act_type == AMV_T_Q8_0) && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
                                             ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q4_K))) ||
                        ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q6_K);
+    if (add && !(tiled && !deq)) {  // only the exact tiled kernels add the residual in their epilogue
+        int rc = mmq_act_impl(fn, wtype, w, n_rows, k, act, act_type, m, dst, ldd, nullptr, stream);
+        if (rc) return rc;
+        const int64_t total = m * n_rows;
+        hipLaunchKernelGGL(k_add_rows, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, amv_stream(stream), dst,
+                           add, ldd, (int)m, (int)n_rows);
+        return amv_check_launch(fn);
+    }
     if (tiled) {
         AMV_REQUIRE(w && act && (dst || sums), "%s: null pointer", fn);
         AMV_REQUIRE(!(deq && sums), "%s: block sums need the exact layout (AMV_ACT_Q8_0_MMA / AMV_ACT_Q8_K_MMA), not "
@@ -908,7 +926,7 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
         AMV_REQUIRE(!dst || ldd >= n_rows, "%s: ldd < n_rows", fn);
         if (wtype == AMV_T_Q4_K || wtype == AMV_T_Q6_K) AMV_REQUIRE(k % 256 == 0, "%s: K-quants need k %% 256 == 0", fn);
         AMV_REQUIRE(!(deq && wtype == AMV_T_Q6_K), "%s: Q6_K has no scaled form (use Q8_K or AMV_ACT_Q8_K_MMA)", fn);
-        if (!deq) return amv_qgemm(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
+        if (!deq) return amv_qgemm(wtype, w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream), add);
         if (wtype == AMV_T_Q4_K) return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, amv_stream(stream));
         return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, amv_stream(stream));
     }
@@ -925,6 +943,15 @@ extern "C" int amv_mul_mat_q_act(int wtype, const void* w, int64_t n_rows, int64
                                  int64_t m, float* dst, int64_t ldd, void* stream) {
     AMV_REQUIRE(dst, "amv_mul_mat_q_act: null dst");
     return mmq_act_impl("amv_mul_mat_q_act", wtype, w, n_rows, k, act, act_type, m, dst, ldd, nullptr, stream);
+}
+
+extern "C" int amv_mul_mat_q_act_add(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,
+                                     int act_type, int64_t m, float* dst, int64_t ldd, const float* add, void* stream) {
+    AMV_REQUIRE(dst && add, "amv_mul_mat_q_act_add: null dst or add");
+    AMV_REQUIRE(add + (m - 1) * ldd + n_rows <= dst || dst + (m - 1) * ldd + n_rows <= add,
+                "amv_mul_mat_q_act_add: add overlaps dst");
+    return mmq_act_impl("amv_mul_mat_q_act_add", wtype, w, n_rows, k, act, act_type, m, dst, ldd, nullptr, stream,
+                        add);
 }
 
 extern "C" int amv_mul_mat_q_act_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act,

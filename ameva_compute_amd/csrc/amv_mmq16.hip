@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void k_mmq16(const uint8_t* __restrict__ wq, c
 // (calls on one stream are ordered).
 // ---------------------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ part, int S, int64_t zstride, int m,
-                                                   int n, float* __restrict__ dst, int64_t ldd, int vec) {
+                                                   int n, float* dst, int64_t ldd, const float* add, int vec) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (vec) {  // 4 consecutive outputs (n % 4 == 0, 16-byte aligned rows)
         const int n4 = n >> 2;
@@ -229,12 +229,20 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ pa
             a.z += b.z;
             a.w += b.w;
         }
+        if (add) {  // the residual of a fused ADD, after the partials (add may be dst)
+            const float4 b = *reinterpret_cast<const float4*>(add + (size_t)r * ldd + c);
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
         *reinterpret_cast<float4*>(dst + (size_t)r * ldd + c) = a;
     } else {
         if (i >= (int64_t)m * n) return;
         const int r = (int)(i / n), c = (int)(i % n);
         float a = part[(size_t)r * n + c];
         for (int z = 1; z < S; ++z) a += part[z * zstride + (size_t)r * n + c];
+        if (add) a += add[(size_t)r * ldd + c];
         dst[(size_t)r * ldd + c] = a;
     }
 }
@@ -285,11 +293,11 @@ int amv_splitk_count(int64_t tiles, int steps) {
 }
 
 void amv_splitk_reduce(const float* part, int S, int64_t zstride, int64_t m, int64_t n, float* dst, int64_t ldd,
-                       hipStream_t st) {
-    const int vec = n % 4 == 0 && ldd % 4 == 0 && ((uintptr_t)dst & 15) == 0;
+                       hipStream_t st, const float* add = nullptr) {
+    const int vec = n % 4 == 0 && ldd % 4 == 0 && ((uintptr_t)dst & 15) == 0 && ((uintptr_t)add & 15) == 0;
     const int64_t items = vec ? m * (n / 4) : m * n;
     hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, part, S, zstride, (int)m,
-                       (int)n, dst, ldd, vec);
+                       (int)n, dst, ldd, add, vec);
 }
 
 // Q4_0 / Q8_0 weights (MI355X layout), activations AMV_ACT_Q8_0_DEQ of m rows, the scaled form

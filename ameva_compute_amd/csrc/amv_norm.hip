@@ -36,11 +36,7 @@ extern "C" int amv_rms_norm_act(const float* x, int64_t n_rows, int64_t n, float
     AMV_REQUIRE(!act || n % (act_type == AMV_T_Q8_K ? 256 : 32) == 0,
                 "amv_rms_norm: the fused quantization needs n %% block size == 0");
     AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "amv_rms_norm: bad rule");
-    // the quantized output is of o when the weight is given, of y otherwise
-    if (act && w && !o) {
-        amv_set_error("amv_rms_norm: the fused quantization of y * w needs o");
-        return AMV_ERR_INVALID_ARG;
-    }
+    // the quantized output is of y * w when the weight is given (o may then be NULL), of y otherwise
     hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0, amv_stream(stream), x, (int)n, eps, w,
                        y, o, amv_act_out(act, n, act ? act_type : 0, rule, n_rows));
     return amv_check_launch("amv_rms_norm");

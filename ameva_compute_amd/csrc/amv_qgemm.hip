@@ -120,11 +120,11 @@ __device__ __forceinline__ void qg_store(const QgRegs<WT>& s, int8_t* __restrict
     }
 }
 
-template <int WT, bool SUMS, int TT, int TW>
+template <int WT, bool SUMS, int TT, int TW, bool ADD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                               int N, int nb, const int8_t* __restrict__ aq,
                                               const int2* __restrict__ am, int M, float* __restrict__ dst,
-                                              int64_t ldd, int32_t* __restrict__ sums, int kb_per,
+                                              int64_t ldd, const float* add, int32_t* __restrict__ sums, int kb_per,
                                               int64_t zstride, int n_tw, int n_tt, int n_z) {
     constexpr int BN = 64 * TW, BM = 64 * TT;
     __shared__ __align__(16) int8_t sW[2][BN * QG_LD];
@@ -228,7 +228,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int m = m0 + 32 * (TT * wt + i) + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < M) dst[(size_t)m * ldd + n] = acc[i][j][r];
+                    if (m < M) {
+                        const size_t o = (size_t)m * ldd + n;
+                        if constexpr (ADD) dst[o] = acc[i][j][r] + add[o];
+                        else dst[o] = acc[i][j][r];
+                    }
                 }
         }
     }
@@ -323,11 +327,11 @@ __device__ __forceinline__ void qgk_store(const QgKRegs& s, int step, int8_t* __
     }
 }
 
-template <bool SUMS, int TT, int TW>
+template <bool SUMS, int TT, int TW, bool ADD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm_q4k(const uint4* __restrict__ wq, const uint4* __restrict__ wh, int N,
                                                   int nsb, const int8_t* __restrict__ aq, const float* __restrict__ ad,
                                                   const int32_t* __restrict__ as16, int M, float* __restrict__ dst,
-                                                  int64_t ldd, int32_t* __restrict__ sums, int sb_per,
+                                                  int64_t ldd, const float* add, int32_t* __restrict__ sums, int sb_per,
                                                   int64_t zstride, int n_tw, int n_tt, int n_z) {
     constexpr int BN = 64 * TW, BM = 64 * TT;
     __shared__ __align__(16) int8_t sW[2][BN * QG_LD];
@@ -448,7 +452,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int m = m0 + 32 * (TT * wt + i) + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < M) dst[(size_t)m * ldd + n] = acc[i][jj][r];
+                    if (m < M) {
+                        const size_t o = (size_t)m * ldd + n;
+                        if constexpr (ADD) dst[o] = acc[i][jj][r] + add[o];
+                        else dst[o] = acc[i][jj][r];
+                    }
                 }
         }
     }
@@ -550,11 +558,11 @@ __device__ __forceinline__ void qg6_store(const QgQ6Regs& s, int step, int8_t* _
     }
 }
 
-template <bool SUMS, int TT, int TW>
+template <bool SUMS, int TT, int TW, bool ADD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm_q6k(
     const uint4* __restrict__ wl, const uint4* __restrict__ wqh, const uint4* __restrict__ wsc,
     const uint16_t* __restrict__ wd, int N, int nsb, const int8_t* __restrict__ aq, const float* __restrict__ ad, int M,
-    float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ sums, int sb_per, int64_t zstride, int n_tw, int n_tt,
+    float* __restrict__ dst, int64_t ldd, const float* add, int32_t* __restrict__ sums, int sb_per, int64_t zstride, int n_tw, int n_tt,
     int n_z) {
     constexpr int BN = 64 * TW, BM = 64 * TT;
     __shared__ __align__(16) int8_t sW[2][BN * QG6_LD];
@@ -664,7 +672,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int m = m0 + 32 * (TT * wt + i) + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < M) dst[(size_t)m * ldd + n] = acc[i][jj][r];
+                    if (m < M) {
+                        const size_t o = (size_t)m * ldd + n;
+                        if constexpr (ADD) dst[o] = acc[i][jj][r] + add[o];
+                        else dst[o] = acc[i][jj][r];
+                    }
                 }
         }
     }
@@ -677,11 +689,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 float* amv_splitk_workspace(size_t bytes, hipStream_t st);
 int amv_splitk_count(int64_t tiles, int steps);
 void amv_splitk_reduce(const float* part, int S, int64_t zstride, int64_t m, int64_t n, float* dst, int64_t ldd,
-                       hipStream_t st);
+                       hipStream_t st, const float* add = nullptr);
 
 template <int TT, int TW>
 static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
-                         int64_t ldd, int32_t* sums, hipStream_t st) {
+                         int64_t ldd, int32_t* sums, hipStream_t st, const float* add) {
     constexpr int BM = 64 * TT, BN = 64 * TW;
     const int8_t* aq = (const int8_t*)act;
     const int n_tw = (int)((n_rows + BN - 1) / BN), n_tt = (int)((m + BM - 1) / BM);
@@ -708,6 +720,7 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
         }
     }
     const dim3 grid((unsigned)(tiles * S));
+    const float* kadd = S > 1 ? nullptr : add;  // with a split of k the residual joins in the sum of the partials
     if (q6k) {  // ql [n][nsb][128] | qh [n][nsb][64] | scales [n][nsb][16] | d [n][nsb]
         const int64_t nblk = n_rows * nsb;
         const uint8_t* base = (const uint8_t*)w;
@@ -718,10 +731,13 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
         const float* ad = (const float*)(aq + m * k);
         if (sums)
             hipLaunchKernelGGL((k_qgemm_q6k<true, TT, TW>), grid, dim3(256), 0, st, wl, wqh, wsc, wd, (int)n_rows, nsb,
-                               aq, ad, (int)m, out, ldo, sums, per, zstride, n_tw, n_tt, S);
+                               aq, ad, (int)m, out, ldo, kadd, sums, per, zstride, n_tw, n_tt, S);
+        else if (kadd)
+            hipLaunchKernelGGL((k_qgemm_q6k<false, TT, TW, true>), grid, dim3(256), 0, st, wl, wqh, wsc, wd,
+                               (int)n_rows, nsb, aq, ad, (int)m, out, ldo, kadd, sums, per, zstride, n_tw, n_tt, S);
         else
             hipLaunchKernelGGL((k_qgemm_q6k<false, TT, TW>), grid, dim3(256), 0, st, wl, wqh, wsc, wd, (int)n_rows,
-                               nsb, aq, ad, (int)m, out, ldo, sums, per, zstride, n_tw, n_tt, S);
+                               nsb, aq, ad, (int)m, out, ldo, kadd, sums, per, zstride, n_tw, n_tt, S);
     } else if (q4k) {
         const int64_t nblk = n_rows * nsb;
         const uint4* wq = (const uint4*)w;
@@ -730,28 +746,33 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
         const int32_t* as16 = (const int32_t*)(aq + m * k + m * nsb * 4);
         if (sums)
             hipLaunchKernelGGL((k_qgemm_q4k<true, TT, TW>), grid, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, aq, ad,
-                               as16, (int)m, out, ldo, sums, per, zstride, n_tw, n_tt, S);
+                               as16, (int)m, out, ldo, kadd, sums, per, zstride, n_tw, n_tt, S);
+        else if (kadd)
+            hipLaunchKernelGGL((k_qgemm_q4k<false, TT, TW, true>), grid, dim3(256), 0, st, wq, wh, (int)n_rows, nsb,
+                               aq, ad, as16, (int)m, out, ldo, kadd, sums, per, zstride, n_tw, n_tt, S);
         else
             hipLaunchKernelGGL((k_qgemm_q4k<false, TT, TW>), grid, dim3(256), 0, st, wq, wh, (int)n_rows, nsb, aq, ad,
-                               as16, (int)m, out, ldo, sums, per, zstride, n_tw, n_tt, S);
+                               as16, (int)m, out, ldo, kadd, sums, per, zstride, n_tw, n_tt, S);
     } else {
         const int64_t nblk = n_rows * nb;
         const uint8_t* wq = (const uint8_t*)w;
         const uint16_t* wd = (const uint16_t*)(wq + nblk * (wtype == AMV_T_Q4_0 ? 16 : 32));
         const int2* am = (const int2*)(aq + m * k);
-#define QG_LAUNCH(WT, SU)                                                                                        \
-    hipLaunchKernelGGL((k_qgemm<WT, SU, TT, TW>), grid, dim3(256), 0, st, wq, wd, (int)n_rows, nb, aq, am, (int)m, \
-                       out, ldo, sums, per, zstride, n_tw, n_tt, S)
+#define QG_LAUNCH(WT, SU, AD)                                                                                     \
+    hipLaunchKernelGGL((k_qgemm<WT, SU, TT, TW, AD>), grid, dim3(256), 0, st, wq, wd, (int)n_rows, nb, aq, am, (int)m, \
+                       out, ldo, kadd, sums, per, zstride, n_tw, n_tt, S)
         if (wtype == AMV_T_Q4_0) {
-            if (sums) QG_LAUNCH(AMV_T_Q4_0, true);
-            else QG_LAUNCH(AMV_T_Q4_0, false);
+            if (sums) QG_LAUNCH(AMV_T_Q4_0, true, false);
+            else if (kadd) QG_LAUNCH(AMV_T_Q4_0, false, true);
+            else QG_LAUNCH(AMV_T_Q4_0, false, false);
         } else {
-            if (sums) QG_LAUNCH(AMV_T_Q8_0, true);
-            else QG_LAUNCH(AMV_T_Q8_0, false);
+            if (sums) QG_LAUNCH(AMV_T_Q8_0, true, false);
+            else if (kadd) QG_LAUNCH(AMV_T_Q8_0, false, true);
+            else QG_LAUNCH(AMV_T_Q8_0, false, false);
         }
 #undef QG_LAUNCH
     }
-    if (S > 1) amv_splitk_reduce(out, S, zstride, m, n_rows, dst, ldd, st);
+    if (S > 1) amv_splitk_reduce(out, S, zstride, m, n_rows, dst, ldd, st, add);
 }
 
 // Q4_0 / Q8_0 weights with plain Q8_0 activations (int8 [m][k], {f32 d, i32 sum} [m][k/32]); Q4_K weights with plain
@@ -761,9 +782,9 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
 // tokens 104 us with 128 x 128 against 115 us with 64 x 64; 6144 x 4096 at 512 tokens 55 us with 64 x 64 against
 // 65 us (64 x 128) and 76 us (128 x 128); 14336 x 4096 at 128 tokens 47 us with 64 x 64 against 52 and 75 us.
 int amv_qgemm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
-              int64_t ldd, int32_t* sums, hipStream_t st) {
+              int64_t ldd, int32_t* sums, hipStream_t st, const float* add) {
     const auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n_rows + bn - 1) / bn); };
-    if (tiles(128, 128) >= 384) qgemm_launch<2, 2>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st);
-    else qgemm_launch<1, 1>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st);
+    if (tiles(128, 128) >= 384) qgemm_launch<2, 2>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st, add);
+    else qgemm_launch<1, 1>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st, add);
     return amv_check_launch("amv_mul_mat_q_act");
 }

@@ -51,6 +51,17 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x,
     }
 }
 
+// The plain layout alone (no ggml blocks, no f16 copies), four elements per lane and a block per 8 lanes
+// (q8_block_lanes8: the same rules, the same bytes).
+__global__ __launch_bounds__(256) void k_quant_q8_0_x4(const float4* __restrict__ x, int n4, int rule,
+                                                      int8_t* __restrict__ aq, int2* __restrict__ ads) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;  // n4 % 8 == 0: the 8 lanes of a block leave together
+    const float4 v4 = x[i];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    q8_block_lanes8(v, rule, i & 7, aq + 32 * (int64_t)(i >> 3), ads + (i >> 3));
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Q8_K activations (ggml quantize_row_q8_K_ref): one wave per 256-element block, 4 elements per lane.
 // max = the element of largest magnitude (the first on ties), iscale = -127/max, q = min(127, round-half-even(
@@ -428,8 +439,12 @@ extern "C" int amv_quantize_act(int type, const float* x, int64_t m, int64_t k, 
             a16 = (uint16_t*)((uint8_t*)y_act + L.a16);
             dt = (float*)((uint8_t*)y_act + L.dt);
         }
-        hipLaunchKernelGGL(k_quant_q8_0, grid_for(n, 256), 256, 0, st, x, n, rule, (uint8_t*)y_ggml, aq, ads, a16,
-                           dt, (int)(k / 32), (int)m, deq);
+        if (!y_ggml && !a16 && n / 4 <= INT32_MAX)
+            hipLaunchKernelGGL(k_quant_q8_0_x4, grid_for(n / 4, 256), 256, 0, st, reinterpret_cast<const float4*>(x),
+                               (int)(n / 4), rule, aq, ads);
+        else
+            hipLaunchKernelGGL(k_quant_q8_0, grid_for(n, 256), 256, 0, st, x, n, rule, (uint8_t*)y_ggml, aq, ads, a16,
+                               dt, (int)(k / 32), (int)m, deq);
     } else if (type == AMV_T_Q8_K || type == AMV_ACT_Q8_K_MMA) {
         AMV_REQUIRE(k % 256 == 0, "amv_quantize_act: Q8_K needs k %% 256 == 0 (k = %lld)", (long long)k);
         AMV_REQUIRE(y_ggml == nullptr || ((uintptr_t)y_ggml & 3) == 0, "amv_quantize_act: y_ggml misaligned");

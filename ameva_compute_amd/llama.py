@@ -170,9 +170,9 @@ class LlamaLayer:
         at = ops.act_type(self.wqkv.type, n_tok)
         bufs = {"n": n_tok, "at": at,
                 "t_o": torch.empty((n_tok, H), **f32), "qkv": torch.empty((n_tok, self.wqkv.n_rows), **f32),
-                "att": torch.empty((n_tok, H), **f32), "proj": torch.empty((n_tok, H), **f32),
+                "att": torch.empty((n_tok, H), **f32),
                 "x1": torch.empty((n_tok, H), **f32), "t_o2": torch.empty((n_tok, H), **f32),
-                "gu": torch.empty((n_tok, self.wgu.n_rows), **f32), "down": torch.empty((n_tok, H), **f32),
+                "gu": torch.empty((n_tok, self.wgu.n_rows), **f32),
                 "act_h": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
                 "act_att": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
                 "act_h2": torch.empty(L.amv_act_bytes(at, n_tok, H), **u8),
@@ -195,8 +195,8 @@ class LlamaLayer:
         """A prompt chunk through the layer: x f32 [n_tok, H] at positions set_prefill_position(pos0, n_tok) ->
         out f32 [n_tok, H]; writes the chunk's K/V rows into the cache and attends causally over keys
         0 .. pos0 + t. The MUL_MATs run on the int8 MFMA kernel (n_tok >= 8, the reference's crossover) and the
-        attention on the f16 MFMA prefill kernel; 12 launches (15 where the activation layout is an extended one,
-        whose quantization is a launch of its own)."""
+        attention on the f16 MFMA prefill kernel; the residual ADDs in the epilogues of the o and down GEMMs:
+        10 launches (13 where the activation layout is an extended one, whose quantization is a launch of its own)."""
         L, st = lib(), torch.cuda.current_stream().cuda_stream
         n, pos0 = self.pf_n, self.pf_pos0
         b = self._prefill_buffers(n)
@@ -206,14 +206,21 @@ class LlamaLayer:
         if n >= ops.MMQ_MIN_M and self.wqkv.type in ops.MMQ_TYPES:
             def mm(wt, w, nr, k, act, m, dst, ldd, s):
                 return L.amv_mul_mat_q_act(wt, w, nr, k, act, at, m, dst, ldd, s)
+
+            def mm_add(wt, w, nr, k, act, m, dst, ldd, add, what):  # the residual ADD in the GEMM's epilogue
+                check(L.amv_mul_mat_q_act_add(wt, w, nr, k, act, at, m, dst, ldd, add, st), what)
         else:
             mm = L.amv_mul_mat_vec
+
+            def mm_add(wt, w, nr, k, act, m, dst, ldd, add, what):
+                check(mm(wt, w, nr, k, act, m, dst, ldd, st), what)
+                check(L.amv_binary(0, dst, add, dst, m, nr, m, st), what + " residual")
         q8 = at in (ops.Q8_0, ops.Q8_K)  # plain layouts: the norms and SWIGLU write them directly
 
         def quant(src, k, act):
             check(L.amv_quantize_act(at, src, n, k, ops.Q8_X86, None, P(act), st), "quantize")
 
-        check(L.amv_rms_norm_act(P(x), n, H, self.eps, P(self.attn_norm), None, P(b["t_o"]),
+        check(L.amv_rms_norm_act(P(x), n, H, self.eps, P(self.attn_norm), None, None if q8 else P(b["t_o"]),
                                  P(b["act_h"]) if q8 else None, at, ops.Q8_X86, st), "rms_norm")
         if not q8:
             quant(P(b["t_o"]), H, b["act_h"])
@@ -226,9 +233,8 @@ class LlamaLayer:
                                        self.n_head, self.n_head_kv, pos0 + n, D, kv, D, kv, D, 1.0 / (D ** 0.5), pos0,
                                        st), "flash_attn prefill")
         quant(P(b["att"]), H, b["act_att"])
-        check(mm(self.wo.type, P(self.wo.data), H, H, P(b["act_att"]), n, P(b["proj"]), H, st), "wo")
-        check(L.amv_binary(0, P(b["proj"]), P(x), P(b["x1"]), n, H, n, st), "residual 1")
-        check(L.amv_rms_norm_act(P(b["x1"]), n, H, self.eps, P(self.ffn_norm), None, P(b["t_o2"]),
+        mm_add(self.wo.type, P(self.wo.data), H, H, P(b["act_att"]), n, P(b["x1"]), H, P(x), "wo + residual")
+        check(L.amv_rms_norm_act(P(b["x1"]), n, H, self.eps, P(self.ffn_norm), None, None if q8 else P(b["t_o2"]),
                                  P(b["act_h2"]) if q8 else None, at, ops.Q8_X86, st), "ffn norm")
         if not q8:
             quant(P(b["t_o2"]), H, b["act_h2"])
@@ -241,8 +247,7 @@ class LlamaLayer:
             check(L.amv_swiglu_rows(P(b["gu"]), ng, P(b["gu"]) + FF * 4, ng, P(b["h"]), FF, n, FF, None, ops.Q8_X86,
                                     st), "swiglu")
             quant(P(b["h"]), FF, b["act_ff"])
-        check(mm(self.wdown.type, P(self.wdown.data), H, FF, P(b["act_ff"]), n, P(b["down"]), H, st), "down")
-        check(L.amv_binary(0, P(b["down"]), P(b["x1"]), P(out), n, H, n, st), "residual 2")
+        mm_add(self.wdown.type, P(self.wdown.data), H, FF, P(b["act_ff"]), n, P(out), H, P(b["x1"]), "down + residual")
 
     def prefill_ops(self, n_tok: int, n_kv: int) -> int:
         """Multiply-adds x 2 of one prefill chunk: the four weight products and the attention (causal half)."""

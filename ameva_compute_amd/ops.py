@@ -147,6 +147,20 @@ MMQ16_MIN_M = 64  # above this many tokens the tiled kernels run (amv_mmq.hip MM
 MMQ_TYPES = (Q4_0, Q8_0, Q4_K, Q6_K)  # Q4_K of MMQ_MIN_M..MMQ16_MIN_M tokens: the activations must be Q8_K_MMA
 
 
+def mul_mat_q_add(w: QWeight, act: torch.Tensor, m: int, add: torch.Tensor, act_t: int | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """mul_mat_q on the batched kernels followed by ADD of add f32 [m, n_rows] (amv_mul_mat_q_act_add)."""
+    _need_gpu(act, "mul_mat_q_add")
+    if add.shape != (m, w.n_rows) or add.dtype != torch.float32 or not add.is_contiguous():
+        raise ValueError("mul_mat_q_add: add must be contiguous f32 [m, n_rows]")
+    if out is None:
+        out = torch.empty((m, w.n_rows), dtype=torch.float32, device=act.device)
+    at = act_layout(w.type, act, m, w.k) if act_t is None else act_t
+    check(lib().amv_mul_mat_q_act_add(w.type, w.data.data_ptr(), w.n_rows, w.k, act.data_ptr(), at, m, out.data_ptr(),
+                                      w.n_rows, add.data_ptr(), _stream()), "amv_mul_mat_q_act_add")
+    return out
+
+
 def mul_mat_q(w: QWeight, act: torch.Tensor, m: int, out: torch.Tensor | None = None,
               kernel: str = "auto", act_t: int | None = None) -> torch.Tensor:
     """dst [m, n_rows] f32 from already quantized activations (amv_quantize_act layout of m rows).

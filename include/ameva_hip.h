@@ -186,6 +186,12 @@ int amv_mul_mat_q_act(int wtype, const void* w, int64_t n_rows, int64_t k, const
                       float* dst, int64_t ldd, void* stream);
 int amv_mul_mat_q_act_block_sums(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type,
                                  int64_t m, int32_t* sums, void* stream);
+/* amv_mul_mat_q_act followed by ADD (the residual after a projection: ggml's ADD of a MUL_MAT's output,
+ * enc_binary ggml-ameva.cpp:3806; no fused counterpart in the reference): dst[t][n] = (W act)[t][n] + add[t][n],
+ * add f32 with row stride ldd, not overlapping dst. The exact tiled kernels add it in their epilogue (after the
+ * k-split partials), the other paths in a second launch; the values equal the two ops' bit for bit. */
+int amv_mul_mat_q_act_add(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int act_type,
+                          int64_t m, float* dst, int64_t ldd, const float* add, void* stream);
 
 /* Q4_K / Q6_K weights from f32 rows (ggml blocks), with this library's own deterministic rule: ggml's
  * make_qkx2_quants search (quantize_row_q4_K_ref / q6_K_ref) is not reproduced, so these weight bytes are not a
@@ -246,8 +252,9 @@ int amv_i2s_gemv_f32(const void* w, int64_t n_rows, int64_t k, const float* x, f
 /* ------------------------------------------------------------------------------------------------------------
  * RMS_NORM (ggml_compute_forward_rms_norm_f32; enc_rms_norm ggml-ameva.cpp:3941 with the fused MUL of
  * ameva_find_fusion 4348-4357, ameva_rms_norm.comp): x f32 [n_rows][n]; y = x / sqrt(mean(x^2) + eps) (may be NULL),
- * o = y * w (w f32 [n]; NULL for none), act (may be NULL): the Q8_0 activation layout of amv_quantize_act, of o when
- * w is given and of y otherwise, quantized with `rule` -- the input of the next MUL_MAT in one pass.
+ * o = y * w (w f32 [n]; NULL for none), act (may be NULL): the Q8_0 activation layout of amv_quantize_act, of y * w
+ * when w is given (o may then be NULL) and of y otherwise, quantized with `rule` -- the input of the next MUL_MAT in
+ * one pass.
  * ---------------------------------------------------------------------------------------------------------- */
 int amv_rms_norm(const float* x, int64_t n_rows, int64_t n, float eps, const float* w, float* y, float* o, void* act,
                  int rule, void* stream);

@@ -239,3 +239,29 @@ def test_mul_mat_q_plain_q8k_for_q4k(dev, ops, orc, m):
     assert lib().amv_mul_mat_q(ops.Q4_K, w.data.data_ptr(), n, k, plain.data_ptr(), m, out.data_ptr(), n,
                                torch.cuda.current_stream().cuda_stream) == 0
     assert rel_l2(out.cpu().numpy(), y_ref) < TOL_F32
+
+
+@pytest.mark.parametrize("wtype,atype,m,n,k", [
+    (2, "Q8_0", 512, 4096, 14336),     # exact tiled, k split: the residual joins in the sum of the partials
+    (2, "Q8_0", 130, 256, 4096),       # exact tiled, one k range: the residual in the epilogue
+    (12, "Q8_K", 512, 1024, 4096),     # exact Q4_K tiled
+    (12, "Q8_K_MMA", 16, 512, 1024),   # small-batch Q4_K kernel + a second launch
+    (2, "Q8_0", 16, 256, 1024),        # streamed small-batch kernel + a second launch
+    (2, "Q8_0_DEQ", 130, 256, 4096),   # scaled form + a second launch
+])
+def test_mul_mat_q_add(dev, ops, orc, wtype, atype, m, n, k):
+    """amv_mul_mat_q_act_add equals amv_mul_mat_q_act followed by the ADD, bit for bit, on every path."""
+    rng = np.random.default_rng(m + n + k + wtype)
+    if wtype == 2:
+        wg = orc.quantize_q4_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    else:
+        wg = random_q4k(rng, n, k)
+    w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, k)
+    at = getattr(ops, atype)
+    act, _ = ops.quantize_act(gpu(rng.standard_normal((m, k)).astype(np.float32), dev), at)
+    res = gpu(rng.standard_normal((m, n)).astype(np.float32), dev)
+    y = ops.mul_mat_q(w, act, m, kernel="mmq", act_t=at)
+    got = ops.mul_mat_q_add(w, act, m, res, act_t=at)
+    assert torch.equal(got, y + res)
+    with pytest.raises(Exception, match="overlaps"):
+        ops.mul_mat_q_add(w, act, m, got, act_t=at, out=got)

@@ -64,6 +64,9 @@ def test_quantize_q8_0_bytes(dev, ops, orc, rule):
         d16 = orc.fp16_to_fp32(wb[:, :, 0].astype(np.uint16) | (wb[:, :, 1].astype(np.uint16) << 8))
         assert np.array_equal(meta[:, :, 0].view(np.float32), d16)
         assert np.array_equal(meta[:, :, 1], qs.astype(np.int32).sum(axis=2))
+        # without the ggml blocks the plain layout comes from the four-elements-per-lane kernel: the same bytes
+        act2, _ = ops.quantize_act(gpu(x, dev), ops.Q8_0, rule)
+        assert torch.equal(act2, act)
 
 
 def test_quantize_q8_K_bytes(dev, ops, orc):

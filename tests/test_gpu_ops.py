@@ -168,6 +168,17 @@ def test_rms_norm_fused(dev, ops, orc, m, n):
     assert np.array_equal(meta[:, :, 0].view(np.float32), d16)
     y2 = ops.rms_norm(gpu(x, dev), 1e-5).cpu().numpy()
     assert np.array_equal(y2, y)
+    # the quantized y * w alone (no y, no o stored), Q8_0 and Q8_K: the same bytes as quantizing the stored o
+    from ameva_compute_amd._lib import lib
+    for at, bs in ((ops.Q8_0, 32), (ops.Q8_K, 256)):
+        if n % bs:
+            continue
+        act2 = torch.empty(lib().amv_act_bytes(at, m, n), dtype=torch.uint8, device=dev)
+        xg, wg = gpu(x, dev), gpu(w, dev)
+        assert lib().amv_rms_norm_act(xg.data_ptr(), m, n, 1e-5, wg.data_ptr(), None, None, act2.data_ptr(), at,
+                                      ops.Q8_X86, ops._stream()) == 0
+        ref, _ = ops.quantize_act(gpu(o, dev), at, ops.Q8_X86)
+        assert torch.equal(act2, ref)
 
 
 # ---------------------------------------------------------------------------------------------- ROPE
