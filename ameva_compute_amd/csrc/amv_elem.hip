@@ -165,12 +165,22 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
     int bi = 0x7FFFFFFF;
     const int n4 = n / 4;
     const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (int i = tid; i < n4; i += 1024) {
-        const float4 v = x4[i];
-        argmax_take(bv, bi, v.x, 4 * i);
-        argmax_take(bv, bi, v.y, 4 * i + 1);
-        argmax_take(bv, bi, v.z, 4 * i + 2);
-        argmax_take(bv, bi, v.w, 4 * i + 3);
+    // eight float4 loads of a thread in flight per round (a 128256-entry row: 4 rounds instead of 32 dependent
+    // ones); the selection is order-free (larger value, then smaller index), so the rounds may take any order
+    for (int i0 = tid; i0 < n4; i0 += 8 * 1024) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = x4[min(i0 + 1024 * u, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + 1024 * u;
+            if (i < n4) {
+                argmax_take(bv, bi, v[u].x, 4 * i);
+                argmax_take(bv, bi, v[u].y, 4 * i + 1);
+                argmax_take(bv, bi, v[u].z, 4 * i + 2);
+                argmax_take(bv, bi, v[u].w, 4 * i + 3);
+            }
+        }
     }
     for (int i = 4 * n4 + tid; i < n; i += 1024) argmax_take(bv, bi, x[i], i);
 #pragma unroll

@@ -57,6 +57,10 @@ def test_argmax(dev, ops):
         x = rng.standard_normal(n).astype(np.float32)
         tok = ops.argmax(torch.from_numpy(x).to(dev))
         assert int(tok.item()) == int(np.argmax(x)), n
+    for where in ([100000, 40000, 5], [128255], [40963, 32768 + 4]):  # ties across rounds and threads, the last entry
+        x = np.zeros(128257, np.float32)
+        x[where] = 2.0
+        assert int(ops.argmax(torch.from_numpy(x).to(dev)).item()) == min(where)
     x = np.zeros(5000, np.float32)
     x[[10, 4000, 4999]] = 3.0          # ties: the first index
     x[[1, 2]] = np.nan                 # NaN never wins
