@@ -102,6 +102,7 @@ extern "C" int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_
 // store per pair).
 // ---------------------------------------------------------------------------------------------------------------
 #define ROPE_MAX_PAIRS 256  // D <= 512
+#define ROPE_RB 12          // pairs per thread and round (a 48-head token of D = 128: one round)
 template <bool NEOX>
 __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ qkv, const int32_t* __restrict__ pos, int n_head,
                                                 int n_head_kv, int D, int n_dims, int hpw, float theta_scale,
@@ -113,6 +114,23 @@ __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ qkv, const 
     const int t = blockIdx.x, tid = threadIdx.x;
     const int half = D / 2, n_all = n_head + 2 * n_head_kv;
     const int h0 = blockIdx.y * hpw, h1 = min(n_all, h0 + hpw);
+    float* xt = qkv + (int64_t)t * n_all * D;
+    // rounds of ROPE_RB pairs per thread: every load of a round is issued before its stores (the stores go to the
+    // same rows, so the compiler would otherwise keep each pair's load behind the previous pair's store); the first
+    // round's loads are in flight while the cos / sin are computed
+    float2 x[ROPE_RB];
+    const auto load_round = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < ROPE_RB; ++u) {
+            const int i = min(i0 + 256 * u, h1 * half - 1);  // past the end: re-read the last pair, not stored
+            const int h = i / half, j = i - h * half;
+            const float* xr = xt + (int64_t)h * D;
+            if (NEOX && h < n_head + n_head_kv && 2 * j < n_dims) x[u] = make_float2(xr[j], xr[j + n_dims / 2]);
+            else x[u] = *reinterpret_cast<const float2*>(xr + 2 * j);
+        }
+    };
+    const int first = h0 * half + tid;
+    load_round(first);
     const float p = (float)pos[t];
     for (int j = tid; 2 * j < n_dims; j += 256) {
         float c, sn;
@@ -127,36 +145,38 @@ __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ qkv, const 
         if (tid == 0 && nkv > 0) atomicAdd(bad, (unsigned)nkv);
     }
     __syncthreads();
-    float* xt = qkv + (int64_t)t * n_all * D;
-    for (int i = h0 * half + tid; i < h1 * half; i += 256) {
-        const int h = i / half, j = i - h * half;
-        float* xr = xt + (int64_t)h * D;
-        const bool is_q = h < n_head, is_v = h >= n_head + n_head_kv;
-        const bool rot = !is_v && 2 * j < n_dims;
-        uint16_t* cr = nullptr;
-        if (!is_q && store)
-            cr = (is_v ? vc + (int64_t)(h - n_head - n_head_kv) * D : kc + (int64_t)(h - n_head) * D) + dr * cache_row;
-        if (NEOX && rot) {
-            const int e0 = j, e1 = j + n_dims / 2;
-            float y0, y1;
-            amv_rope_apply(s_c[j], s_s[j], xr[e0], xr[e1], y0, y1);
-            xr[e0] = y0;
-            xr[e1] = y1;
-            if (cr) {
-                cr[e0] = amv_f2h(y0);
-                cr[e1] = amv_f2h(y1);
+    for (int i0 = first; i0 < h1 * half; i0 += 256 * ROPE_RB) {
+        if (i0 != first) load_round(i0);
+#pragma unroll
+        for (int u = 0; u < ROPE_RB; ++u) {
+            const int i = i0 + 256 * u;
+            if (i >= h1 * half) break;
+            const int h = i / half, j = i - h * half;
+            float* xr = xt + (int64_t)h * D;
+            const bool is_q = h < n_head, is_v = h >= n_head + n_head_kv;
+            const bool rot = !is_v && 2 * j < n_dims;
+            uint16_t* cr = nullptr;
+            if (!is_q && store)
+                cr = (is_v ? vc + (int64_t)(h - n_head - n_head_kv) * D : kc + (int64_t)(h - n_head) * D) +
+                     dr * cache_row;
+            float2 y = x[u];
+            if (rot) amv_rope_apply(s_c[j], s_s[j], x[u].x, x[u].y, y.x, y.y);
+            // element indices of the pair: NEOX rotates j with j + n_dims / 2, else 2 j with 2 j + 1
+            const int e0 = NEOX && rot ? j : 2 * j, e1 = NEOX && rot ? j + n_dims / 2 : 2 * j + 1;
+            if (!is_v) {
+                if (NEOX && rot) {
+                    xr[e0] = y.x;
+                    xr[e1] = y.y;
+                } else {
+                    *reinterpret_cast<float2*>(xr + 2 * j) = y;
+                }
             }
-        } else {
-            const float2 x = *reinterpret_cast<const float2*>(xr + 2 * j);
-            float2 y = x;
-            if (rot) amv_rope_apply(s_c[j], s_s[j], x.x, x.y, y.x, y.y);
-            if (!is_v) *reinterpret_cast<float2*>(xr + 2 * j) = y;
             if (cr) {
-                if (pair_stores) {
+                if (!(NEOX && rot) && pair_stores) {
                     *reinterpret_cast<uint32_t*>(cr + 2 * j) = (uint32_t)amv_f2h(y.x) | ((uint32_t)amv_f2h(y.y) << 16);
                 } else {
-                    cr[2 * j] = amv_f2h(y.x);
-                    cr[2 * j + 1] = amv_f2h(y.y);
+                    cr[e0] = amv_f2h(y.x);
+                    cr[e1] = amv_f2h(y.y);
                 }
             }
         }
