@@ -103,7 +103,7 @@ extern "C" int amv_rope(const float* x, float* y, const int32_t* pos, int64_t n_
 // ---------------------------------------------------------------------------------------------------------------
 #define ROPE_MAX_PAIRS 256  // D <= 512
 #define ROPE_RB 12          // pairs per thread and round (a 48-head token of D = 128: one round)
-template <bool NEOX>
+template <bool NEOX, int HALF>  // HALF: D / 2 known at compile time (0: read from D)
 __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ qkv, const int32_t* __restrict__ pos, int n_head,
                                                 int n_head_kv, int D, int n_dims, int hpw, float theta_scale,
                                                 float freq_scale, float attn_factor, uint16_t* __restrict__ kc,
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ qkv, const 
                                                 unsigned int* __restrict__ bad, bool pair_stores) {
     __shared__ float s_c[ROPE_MAX_PAIRS], s_s[ROPE_MAX_PAIRS];
     const int t = blockIdx.x, tid = threadIdx.x;
-    const int half = D / 2, n_all = n_head + 2 * n_head_kv;
+    const int half = HALF ? HALF : D / 2, n_all = n_head + 2 * n_head_kv;
     const int h0 = blockIdx.y * hpw, h1 = min(n_all, h0 + hpw);
     float* xt = qkv + (int64_t)t * n_all * D;
     // rounds of ROPE_RB pairs per thread: every load of a round is issued before its stores (the stores go to the
@@ -203,14 +203,19 @@ extern "C" int amv_rope_kv_store(float* qkv, const int32_t* pos, int64_t n_tok, 
     const dim3 grid((unsigned)n_tok, (unsigned)((n_all + hpw - 1) / hpw));
     // f16 pairs as one 4-byte store when every pair starts 4-byte aligned
     const bool pairs = cache_row % 2 == 0 && ((uintptr_t)k_cache & 3) == 0 && ((uintptr_t)v_cache & 3) == 0;
-    if (mode == 2)
-        hipLaunchKernelGGL(k_rope_kv<true>, grid, dim3(256), 0, amv_stream(stream), qkv, pos, (int)n_head,
-                           (int)n_head_kv, (int)D, n_dims, hpw, theta_scale, freq_scale, attn_factor,
-                           (uint16_t*)k_cache, (uint16_t*)v_cache, cache_row, kv_idx, cache_rows, bad, pairs);
-    else
-        hipLaunchKernelGGL(k_rope_kv<false>, grid, dim3(256), 0, amv_stream(stream), qkv, pos, (int)n_head,
-                           (int)n_head_kv, (int)D, n_dims, hpw, theta_scale, freq_scale, attn_factor,
-                           (uint16_t*)k_cache, (uint16_t*)v_cache, cache_row, kv_idx, cache_rows, bad, pairs);
+    // D = 128 (every Llama head): the (head, pair) of an item by shifts instead of a division by a run-time D / 2
+#define ROPE_LAUNCH(NX, HF)                                                                                         \
+    hipLaunchKernelGGL((k_rope_kv<NX, HF>), grid, dim3(256), 0, amv_stream(stream), qkv, pos, (int)n_head,          \
+                       (int)n_head_kv, (int)D, n_dims, hpw, theta_scale, freq_scale, attn_factor, (uint16_t*)k_cache, \
+                       (uint16_t*)v_cache, cache_row, kv_idx, cache_rows, bad, pairs)
+    if (mode == 2) {
+        if (D == 128) ROPE_LAUNCH(true, 64);
+        else ROPE_LAUNCH(true, 0);
+    } else {
+        if (D == 128) ROPE_LAUNCH(false, 64);
+        else ROPE_LAUNCH(false, 0);
+    }
+#undef ROPE_LAUNCH
     return amv_check_launch("amv_rope_kv_store");
 }
 
