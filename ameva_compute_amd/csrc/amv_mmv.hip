@@ -274,8 +274,10 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
             if constexpr (SEG) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) dw[u][r] = amv_ld_stream(wdr[r] + db[r] + 2 * j);
-            } else if constexpr (PAIRS && !MMV_STACKED(EP) && R % 2 == 0) {
-                // the wave's rows 2p, 2p + 1 read both scales with one dword
+            } else if constexpr (PAIRS && R % 2 == 0 && (!MMV_STACKED(EP) || (EP == MMV_EP_SWIGLU_Q8 && R == 4))) {
+                // the wave's rows 2p, 2p + 1 read both scales with one dword (stacked gate/up with two outputs per
+                // wave: rows o, o + 1 and F + o, F + o + 1, pairs since o and F = n_rows / 2 are even: the launcher
+                // makes the quantization block size divide F)
 #pragma unroll
                 for (int r = 0; r < R; r += 2) {
                     const uint32_t d2 = amv_ld_stream(wd2 + (db[r] >> 1) + j);
