@@ -271,7 +271,15 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
 #pragma unroll
             for (int r = 0; r < R; ++r) w[u][r] = amv_ld_stream((SEG ? wqr[r] : wq) + rb[r] + j);
             if (BLOCK_SUMS) continue;
-            if constexpr (SEG) {
+            if constexpr (SEG && PAIRS && R % 2 == 0 && (!MMV_STACKED(EP) || R == 4)) {
+                // rows 2p, 2p + 1 of one matrix (each matrix holds an even row count): both scales in one dword
+#pragma unroll
+                for (int r = 0; r < R; r += 2) {
+                    const uint32_t d2 = amv_ld_stream(reinterpret_cast<const uint32_t*>(wdr[r]) + (db[r] >> 1) + j);
+                    dw[u][r] = d2 & 0xFFFFu;
+                    dw[u][r + 1] = d2 >> 16;
+                }
+            } else if constexpr (SEG) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) dw[u][r] = amv_ld_stream(wdr[r] + db[r] + 2 * j);
             } else if constexpr (PAIRS && R % 2 == 0 && (!MMV_STACKED(EP) || (EP == MMV_EP_SWIGLU_Q8 && R == 4))) {
