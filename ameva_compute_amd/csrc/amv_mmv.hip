@@ -396,6 +396,64 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096(const uint4* __restrict_
     if (live && lane < 2) dst[row0 + lane] = lane ? t1 : t0;
 }
 
+// The stacked gate|up GEMV at K = 4096 with SWIGLU and the Q8 tail (EP 7) in the same lean form: two outputs per
+// wave, rows o, o + 1 (gate) and F + o, F + o + 1 (up) with o = 2 wave, the scales of each row pair in one dword, every
+// load of the wave issued before its arithmetic; the per-lane sums in the order of k_mmv_q4_0 (same bits). Measured on
+// MI355X at 28672 x 4096 against the generic stacked kernel: see the launcher.
+__global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_swiglu(const uint4* __restrict__ wq,
+                                                               const uint32_t* __restrict__ wd2, int n_rows,
+                                                               const int4* __restrict__ a4,
+                                                               const int2* __restrict__ ads, float* __restrict__ dst,
+                                                               float* __restrict__ eout, const MmvPost post) {
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6;
+    const int wave = blockIdx.x * 4 + wi;
+    const int F = n_rows >> 1;
+    const bool live = 2 * wave < F;
+    const int o = min(2 * wave, F - 2);  // a wave past the end re-reads the last pair and stores nothing
+    const int rows[4] = {o, o + 1, F + o, F + o + 1};
+    uint4 w[2][4];
+    uint32_t dw[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = 64 * u + lane;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[u][r] = amv_ld_stream(wq + (size_t)rows[r] * 128 + j);
+        dw[u][0] = amv_ld_stream(wd2 + (size_t)(o >> 1) * 128 + j);
+        dw[u][1] = amv_ld_stream(wd2 + (size_t)((F + o) >> 1) * 128 + j);
+    }
+    int4 a0[2], a1[2];
+    int2 ds[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = 64 * u + lane;
+        a0[u] = a4[2 * j];
+        a1[u] = a4[2 * j + 1];
+        ds[u] = ads[j];
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float da = __int_as_float(ds[u].x);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint4 q = w[u][r];
+            int s = amv_dot4((int)(q.x & M4), a0[u].x, 0);
+            s = amv_dot4((int)(q.y & M4), a0[u].y, s);
+            s = amv_dot4((int)(q.z & M4), a0[u].z, s);
+            s = amv_dot4((int)(q.w & M4), a0[u].w, s);
+            s = amv_dot4((int)((q.x >> 4) & M4), a1[u].x, s);
+            s = amv_dot4((int)((q.y >> 4) & M4), a1[u].y, s);
+            s = amv_dot4((int)((q.z >> 4) & M4), a1[u].z, s);
+            s = amv_dot4((int)((q.w >> 4) & M4), a1[u].w, s);
+            s -= 8 * ds[u].y;
+            const uint32_t d2 = dw[u][r >> 1];
+            acc[r] = fmaf((float)s, amv_h2f((r & 1) ? d2 >> 16 : d2) * da, acc[r]);
+        }
+    }
+    mmv_finish<4, MMV_EP_SWIGLU_Q8, 1>(acc, lane, wi, 0, live, wave, n_rows, dst, nullptr, eout, post, MmvRopeAt{});
+    mmv_tail<MMV_EP_SWIGLU_Q8, 1, 4>(post, eout, n_rows);
+}
+
 // ------------------------------------------------------------------------------------------------ Q8_0 x Q8_0
 template <int R, int U, bool BLOCK_SUMS, int EP, int S>
 __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, const uint16_t* __restrict__ wd,
@@ -653,6 +711,14 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const int waves = MMV_STACKED(EP) ? a.n_rows / R : (a.n_rows + R - 1) / R;
     const bool full = nb % (64 * U) == 0 && (MMV_STACKED(EP) || a.n_rows % R == 0);
     const dim3 grid((waves * S + 3) / 4);
+    if constexpr (!BS && EP == MMV_EP_SWIGLU_Q8 && R == 4 && S == 1 && U == 2) {
+        // the stacked weight at K = 4096: the lean kernel
+        if (a.post.n_seg == 0 && nb == 128) {
+            hipLaunchKernelGGL(k_mmv_q4_0_k4096_swiglu, grid, dim3(256), 0, st, wq, reinterpret_cast<const uint32_t*>(wd),
+                               a.n_rows, reinterpret_cast<const int4*>(aq), ads, a.dst, a.eout, a.post);
+            return;
+        }
+    }
     if constexpr (!BS && (EP == MMV_EP_ROPE_KV || EP == MMV_EP_SWIGLU_Q8)) {
         if (a.post.n_seg > 0) {  // separate matrices (the launcher checked whole steps and even rows per matrix)
             const uint4* w0 = reinterpret_cast<const uint4*>(a.post.w_seg[0]);
