@@ -400,6 +400,9 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096(const uint4* __restrict_
 // wave, rows o, o + 1 (gate) and F + o, F + o + 1 (up) with o = 2 wave, the scales of each row pair in one dword, every
 // load of the wave issued before its arithmetic; the per-lane sums in the order of k_mmv_q4_0 (same bits). Measured on
 // MI355X at 28672 x 4096 against the generic stacked kernel: see the launcher.
+// SEG: gate and up are two matrices of F rows each (w_seg[0], w_seg[1] in their own layouts: llama.cpp's separate
+// ffn_gate / ffn_up), the wave's rows o, o + 1 of both.
+template <bool SEG>
 __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_swiglu(const uint4* __restrict__ wq,
                                                                const uint32_t* __restrict__ wd2, int n_rows,
                                                                const int4* __restrict__ a4,
@@ -410,16 +413,30 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_swiglu(const uint4* __re
     const int F = n_rows >> 1;
     const bool live = 2 * wave < F;
     const int o = min(2 * wave, F - 2);  // a wave past the end re-reads the last pair and stores nothing
-    const int rows[4] = {o, o + 1, F + o, F + o + 1};
+    // gate rows o, o + 1 at wg / dg, up rows at wu / du (row ou, ou + 1 of that matrix)
+    const uint4* wg = wq;
+    const uint4* wu = wq;
+    const uint32_t* dg = wd2;
+    const uint32_t* du = wd2;
+    int ou = F + o;
+    if constexpr (SEG) {
+        wg = reinterpret_cast<const uint4*>(post.w_seg[0]);
+        wu = reinterpret_cast<const uint4*>(post.w_seg[1]);
+        dg = reinterpret_cast<const uint32_t*>(post.w_seg[0] + (size_t)F * 128 * 16);
+        du = reinterpret_cast<const uint32_t*>(post.w_seg[1] + (size_t)F * 128 * 16);
+        ou = o;
+    }
     uint4 w[2][4];
     uint32_t dw[2][2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int j = 64 * u + lane;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) w[u][r] = amv_ld_stream(wq + (size_t)rows[r] * 128 + j);
-        dw[u][0] = amv_ld_stream(wd2 + (size_t)(o >> 1) * 128 + j);
-        dw[u][1] = amv_ld_stream(wd2 + (size_t)((F + o) >> 1) * 128 + j);
+        w[u][0] = amv_ld_stream(wg + (size_t)o * 128 + j);
+        w[u][1] = amv_ld_stream(wg + (size_t)(o + 1) * 128 + j);
+        w[u][2] = amv_ld_stream(wu + (size_t)ou * 128 + j);
+        w[u][3] = amv_ld_stream(wu + (size_t)(ou + 1) * 128 + j);
+        dw[u][0] = amv_ld_stream(dg + (size_t)(o >> 1) * 128 + j);
+        dw[u][1] = amv_ld_stream(du + (size_t)(ou >> 1) * 128 + j);
     }
     int4 a0[2], a1[2];
     int2 ds[2];
@@ -712,11 +729,16 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const bool full = nb % (64 * U) == 0 && (MMV_STACKED(EP) || a.n_rows % R == 0);
     const dim3 grid((waves * S + 3) / 4);
     if constexpr (!BS && EP == MMV_EP_SWIGLU_Q8 && R == 4 && S == 1 && U == 2) {
-        // the stacked weight at K = 4096: the lean kernel
-        if (a.post.n_seg == 0 && nb == 128) {
-            hipLaunchKernelGGL(k_mmv_q4_0_k4096_swiglu, grid, dim3(256), 0, st, wq, reinterpret_cast<const uint32_t*>(wd),
-                               a.n_rows, reinterpret_cast<const int4*>(aq), ads, a.dst, a.eout, a.post);
-            return;
+        // K = 4096: the lean kernel, stacked or over the two matrices (each of n_rows / 2 rows)
+        if (nb == 128) {
+            if (a.post.n_seg == 2)
+                hipLaunchKernelGGL(k_mmv_q4_0_k4096_swiglu<true>, grid, dim3(256), 0, st, nullptr, nullptr, a.n_rows,
+                                   reinterpret_cast<const int4*>(aq), ads, a.dst, a.eout, a.post);
+            else if (a.post.n_seg == 0)
+                hipLaunchKernelGGL(k_mmv_q4_0_k4096_swiglu<false>, grid, dim3(256), 0, st, wq,
+                                   reinterpret_cast<const uint32_t*>(wd), a.n_rows, reinterpret_cast<const int4*>(aq),
+                                   ads, a.dst, a.eout, a.post);
+            if (a.post.n_seg == 2 || a.post.n_seg == 0) return;
         }
     }
     if constexpr (!BS && (EP == MMV_EP_ROPE_KV || EP == MMV_EP_SWIGLU_Q8)) {
