@@ -471,6 +471,70 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_swiglu(const uint4* __re
     mmv_tail<MMV_EP_SWIGLU_Q8, 1, 4>(post, eout, n_rows);
 }
 
+// The K = 4096 GEMV with the ADD (o projection + residual) or ROPE_KV (q/k/v + RoPE + cache rows) epilogue in the same
+// lean form, two rows per wave; SEG: the rows' matrix from the segment table (each holds an even row count, so a
+// wave's pair lies in one). Same sums as k_mmv_q4_0<2, 2, ...>.
+template <int EP, bool SEG>
+__global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_ep(const uint4* __restrict__ wq,
+                                                           const uint32_t* __restrict__ wd2, int n_rows,
+                                                           const int4* __restrict__ a4, const int2* __restrict__ ads,
+                                                           float* __restrict__ dst, const float* __restrict__ epi,
+                                                           float* __restrict__ eout, const MmvPost post) {
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6;
+    const int wave = blockIdx.x * 4 + wi;
+    const bool live = 2 * wave < n_rows;
+    const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);
+    int row0 = min(2 * wave, n_rows - 2);  // a wave past the end re-reads the last pair and stores nothing
+    const uint4* wqs = wq;
+    const uint32_t* wds = wd2;
+    if constexpr (SEG) {
+        int lr;
+        const int sg = mmv_seg(post, row0, lr);
+        const size_t rows_s = (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]);
+        wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
+        wds = reinterpret_cast<const uint32_t*>(post.w_seg[sg] + rows_s * 128 * 16);
+        row0 = lr;
+    }
+    uint4 w[2][2];
+    uint32_t dw[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = 64 * u + lane;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) w[u][r] = amv_ld_stream(wqs + (size_t)(row0 + r) * 128 + j);
+        dw[u] = amv_ld_stream(wds + (size_t)(row0 >> 1) * 128 + j);
+    }
+    int4 a0[2], a1[2];
+    int2 ds[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = 64 * u + lane;
+        a0[u] = a4[2 * j];
+        a1[u] = a4[2 * j + 1];
+        ds[u] = ads[j];
+    }
+    float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float da = __int_as_float(ds[u].x);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const uint4 q = w[u][r];
+            int s = amv_dot4((int)(q.x & M4), a0[u].x, 0);
+            s = amv_dot4((int)(q.y & M4), a0[u].y, s);
+            s = amv_dot4((int)(q.z & M4), a0[u].z, s);
+            s = amv_dot4((int)(q.w & M4), a0[u].w, s);
+            s = amv_dot4((int)((q.x >> 4) & M4), a1[u].x, s);
+            s = amv_dot4((int)((q.y >> 4) & M4), a1[u].y, s);
+            s = amv_dot4((int)((q.z >> 4) & M4), a1[u].z, s);
+            s = amv_dot4((int)((q.w >> 4) & M4), a1[u].w, s);
+            s -= 8 * ds[u].y;
+            acc[r] = fmaf((float)s, amv_h2f(r ? dw[u] >> 16 : dw[u]) * da, acc[r]);
+        }
+    }
+    mmv_finish<2, EP, 1, SEG>(acc, lane, wi, 0, live, wave, n_rows, dst, epi, eout, post, ra);
+}
+
 // ------------------------------------------------------------------------------------------------ Q8_0 x Q8_0
 template <int R, int U, bool BLOCK_SUMS, int EP, int S>
 __global__ __launch_bounds__(256) void k_mmv_q8_0(const uint4* __restrict__ wq, const uint16_t* __restrict__ wd,
@@ -739,6 +803,19 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
                                    reinterpret_cast<const uint32_t*>(wd), a.n_rows, reinterpret_cast<const int4*>(aq),
                                    ads, a.dst, a.eout, a.post);
             if (a.post.n_seg == 2 || a.post.n_seg == 0) return;
+        }
+    }
+    if constexpr (!BS && (EP == MMV_EP_ROPE_KV || EP == AMV_EP_ADD) && R == 2 && S == 1 && U == 2) {
+        // K = 4096: the lean kernel (stacked or segmented q/k/v; o projection + residual)
+        if (nb == 128 && a.n_rows % 2 == 0) {
+            if (a.post.n_seg > 0)
+                hipLaunchKernelGGL((k_mmv_q4_0_k4096_ep<EP, true>), grid, dim3(256), 0, st, nullptr, nullptr, a.n_rows,
+                                   reinterpret_cast<const int4*>(aq), ads, a.dst, a.epi, a.eout, a.post);
+            else
+                hipLaunchKernelGGL((k_mmv_q4_0_k4096_ep<EP, false>), grid, dim3(256), 0, st, wq,
+                                   reinterpret_cast<const uint32_t*>(wd), a.n_rows, reinterpret_cast<const int4*>(aq),
+                                   ads, a.dst, a.epi, a.eout, a.post);
+            return;
         }
     }
     if constexpr (!BS && (EP == MMV_EP_ROPE_KV || EP == MMV_EP_SWIGLU_Q8)) {
