@@ -33,18 +33,27 @@ def sources() -> list[str]:
     return [os.path.join(CSRC, s) for s in SOURCES]
 
 
+def _jobs() -> int:
+    return max(1, min(8, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+
+
 def build(verbose: bool = False) -> str:
-    objs = []
-    for src in sources():
+    from concurrent.futures import ThreadPoolExecutor
+
+    def compile_one(src):
         obj = os.path.join(CSRC, os.path.basename(src) + ".o")
-        cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
-        r = subprocess.run(cmd, capture_output=True, text=True)
-        if r.returncode != 0:
-            sys.stderr.write(r.stdout + r.stderr)
-            raise RuntimeError(f"hipcc failed on {src}")
-        if verbose:
-            sys.stderr.write(r.stderr)
-        objs.append(obj)
+        r = subprocess.run([HIPCC, *FLAGS, "-c", src, "-o", obj], capture_output=True, text=True)
+        return src, obj, r
+
+    objs = []
+    with ThreadPoolExecutor(_jobs()) as ex:
+        for src, obj, r in ex.map(compile_one, sources()):
+            if r.returncode != 0:
+                sys.stderr.write(r.stdout + r.stderr)
+                raise RuntimeError(f"hipcc failed on {src}")
+            if verbose:
+                sys.stderr.write(r.stderr)
+            objs.append(obj)
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -54,11 +63,10 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     for o in objs:
         os.remove(o)
-    build_plugin()
-    build_amuda()
-    build_runtime()
-    build_bitnet()
-    build_test_kernels()
+    # the libraries over libameva_hip.so and the test code object are independent of each other
+    with ThreadPoolExecutor(_jobs()) as ex:
+        for f in [ex.submit(fn) for fn in (build_plugin, build_amuda, build_runtime, build_bitnet, build_test_kernels)]:
+            f.result()
     return LIB
 
 

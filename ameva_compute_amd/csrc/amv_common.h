@@ -62,6 +62,9 @@ int amv_check_launch(const char* what);
 
 static inline hipStream_t amv_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// the per-device split-k workspace of the batched kernels (amv_splitk_workspace): fixed, never grown
+#define AMV_SPLITK_WS_BYTES ((size_t)128 << 20)
+
 // ---------------------------------------------------------------------------------------------------------------
 // device: fp16 <-> f32
 // f32 -> fp16 for stored quantization scales: IEEE round to nearest even done in integers, with ggml's NaN (0x7E00)

@@ -930,8 +930,10 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
         if (wtype == AMV_T_Q4_K) return amv_mmq16_q4k(w, n_rows, k, act, m, dst, ldd, amv_stream(stream));
         return amv_mmq16(wtype, w, n_rows, k, act, m, dst, ldd, amv_stream(stream));
     }
+    // a plain Q8_K activation of a Q4_K batch this small goes to the tiled int8 kernel (mmq_impl with q4k_mma false):
+    // the small-batch Q4_K kernels read the f16 copies that only AMV_ACT_Q8_K_MMA holds
     const bool ok = (act_type == AMV_T_Q8_0 || q80x) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)
-                                                     : (q8kx && wtype == AMV_T_Q4_K);
+                                                     : ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q4_K);
     AMV_REQUIRE(ok, "%s: activation type %d does not feed weight type %d", fn, act_type, wtype);
     // the small-batch Q4_K kernel reads the f16 copies as exact integers
     AMV_REQUIRE(!(deq && wtype == AMV_T_Q4_K), "%s: Q4_K batches of m <= %d need the exact layout AMV_ACT_Q8_K_MMA",

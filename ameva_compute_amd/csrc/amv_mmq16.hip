@@ -249,28 +249,43 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ pa
 
 namespace {
 std::mutex g_splitk_mu;
-std::map<int, std::pair<float*, size_t>> g_splitk_ws;  // device -> (buffer, bytes)
+std::map<int, float*> g_splitk_ws;  // device -> the workspace (AMV_SPLITK_WS_BYTES)
 }  // namespace
 
+// The split-k partials of every batched kernel live in one per-device workspace of a fixed size, allocated by the
+// first call that splits k and held until the process ends: a split count S is only chosen while the launch has
+// fewer than SPLITK_TARGET (1024) workgroups, so S x tiles < 2 x 1024 and S x m x n x 4 bytes stay below
+// 2048 x (128 x 128) x 4 = 128 MiB. The workspace never grows, so a captured graph's pointer stays valid. Under
+// stream capture no allocation is possible: a call that splits k before any uncaptured call did fails (it never
+// falls back to an unsplit launch, whose f32 summation order would differ from the same call outside capture).
 float* amv_splitk_workspace(size_t bytes, hipStream_t st) {
+    if (bytes > AMV_SPLITK_WS_BYTES) {
+        amv_set_error("split-k workspace: %zu bytes asked, %zu available", bytes, (size_t)AMV_SPLITK_WS_BYTES);
+        return nullptr;
+    }
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        amv_set_error("split-k workspace: no current device");
+        return nullptr;
+    }
     std::lock_guard<std::mutex> lk(g_splitk_mu);
-    auto& w = g_splitk_ws[dev];
-    if (w.second >= bytes) return w.first;
+    float*& w = g_splitk_ws[dev];
+    if (w) return w;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
         (void)hipGetLastError();
+        amv_set_error("split-k workspace: first needed under stream capture; run a batched MUL_MAT that splits k "
+                      "(k >= 6144 with fewer than 1024 tiles) once before capturing");
         return nullptr;
     }
-    const size_t want = std::max(bytes, 2 * w.second);
     void* p = nullptr;
-    if (hipMalloc(&p, want) != hipSuccess) {
+    if (hipMalloc(&p, AMV_SPLITK_WS_BYTES) != hipSuccess) {
         (void)hipGetLastError();
+        amv_set_error("split-k workspace: hipMalloc of %zu bytes failed", (size_t)AMV_SPLITK_WS_BYTES);
         return nullptr;
     }
-    w = {(float*)p, want};  // the previous buffer stays allocated: a captured graph may still write it
-    return w.first;
+    w = (float*)p;
+    return w;
 }
 
 // splits of k for `tiles` output tiles over `steps` pipeline steps (64 of k each): only for k >= 64 SPLITK_MIN_TOTAL
@@ -327,6 +342,7 @@ int amv_mmq16(int wtype, const void* w, int64_t n_rows, int64_t k, const void* a
         kb_per = ((nb + S - 1) / S + 1) & ~1;  // whole pipeline steps
         nz = (nb + kb_per - 1) / kb_per;
         float* ws = nz > 1 ? amv_splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
+        if (nz > 1 && !ws) return AMV_ERR_HIP;  // never unsplit: the summation order would change
         if (ws) {
             out = ws;
             ldo = n_rows;
@@ -507,6 +523,7 @@ int amv_mmq16_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int
         sb_per = (nsb + S - 1) / S;
         nz = (nsb + sb_per - 1) / sb_per;
         float* ws = nz > 1 ? amv_splitk_workspace((size_t)nz * m * n_rows * 4, st) : nullptr;
+        if (nz > 1 && !ws) return AMV_ERR_HIP;  // never unsplit: the summation order would change
         if (ws) {
             out = ws;
             ldo = n_rows;

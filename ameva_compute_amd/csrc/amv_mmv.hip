@@ -11,6 +11,8 @@
 // The BLOCK_SUMS instantiation stores the int32 block sums instead (parity instrumentation of the same code).
 #include "amv_common.h"
 
+#include <atomic>
+
 #define M4 0x0F0F0F0Fu
 
 // Epilogues of the one-column GEMV, the reference's ameva_qmv / ameva_mmvq ep_mode (ameva_qmv.comp:233-246,
@@ -781,8 +783,16 @@ struct MmvArgs {
     MmvPost post;          // EP 5..7
 };
 
+// Parity instrumentation (amv_debug_gemv_generic): while set, the Q4_0 launches skip the lean K = 4096 kernels and run
+// the generic k_mmv_q4_0 of the same rows per wave, split and epilogue, whose BLOCK_SUMS instantiation gives the
+// block integers the tests compare with the oracle; the lean kernels keep that kernel's arithmetic and summation
+// order, so the two f32 results must be equal bit for bit.
+static std::atomic<int> g_mmv_generic{0};
+extern "C" int amv_debug_gemv_generic(int on) { return g_mmv_generic.exchange(on ? 1 : 0); }
+
 template <int R, int U, bool BS, int EP, int S>
 static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
+    const bool lean = g_mmv_generic.load(std::memory_order_relaxed) == 0;
     const int nb = a.k / 32;
     const int64_t nblk = (int64_t)a.n_rows * nb;
     const uint4* wq = reinterpret_cast<const uint4*>(a.w);
@@ -794,7 +804,7 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     const dim3 grid((waves * S + 3) / 4);
     if constexpr (!BS && EP == MMV_EP_SWIGLU_Q8 && R == 4 && S == 1 && U == 2) {
         // K = 4096: the lean kernel, stacked or over the two matrices (each of n_rows / 2 rows)
-        if (nb == 128) {
+        if (nb == 128 && lean) {
             if (a.post.n_seg == 2)
                 hipLaunchKernelGGL(k_mmv_q4_0_k4096_swiglu<true>, grid, dim3(256), 0, st, nullptr, nullptr, a.n_rows,
                                    reinterpret_cast<const int4*>(aq), ads, a.dst, a.eout, a.post);
@@ -807,7 +817,7 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
     }
     if constexpr (!BS && (EP == MMV_EP_ROPE_KV || EP == AMV_EP_ADD) && R == 2 && S == 1 && U == 2) {
         // K = 4096: the lean kernel (stacked or segmented q/k/v; o projection + residual)
-        if (nb == 128 && a.n_rows % 2 == 0) {
+        if (nb == 128 && a.n_rows % 2 == 0 && lean) {
             if (a.post.n_seg > 0)
                 hipLaunchKernelGGL((k_mmv_q4_0_k4096_ep<EP, true>), grid, dim3(256), 0, st, nullptr, nullptr, a.n_rows,
                                    reinterpret_cast<const int4*>(aq), ads, a.dst, a.epi, a.eout, a.post);
@@ -830,7 +840,7 @@ static void launch_q4_0(const MmvArgs& a, hipStream_t st) {
             return;
         }
     }
-    if (!BS && EP == AMV_EP_NONE && S == 1 && R == 2 && a.n_rows % 2 == 0 && nb == 128)
+    if (!BS && EP == AMV_EP_NONE && S == 1 && R == 2 && a.n_rows % 2 == 0 && nb == 128 && lean)
         hipLaunchKernelGGL(k_mmv_q4_0_k4096, grid, dim3(256), 0, st, wq, reinterpret_cast<const uint32_t*>(wd),
                            a.n_rows, reinterpret_cast<const int4*>(aq), ads, a.dst);
     else if (a.n_rows % 2 == 0 && full && nb == 128 && U == 2)

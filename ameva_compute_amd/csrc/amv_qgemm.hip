@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                     } else {
                         const float dw = sDw[buf][bl * BN + rl];
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf((float)C[r] * da[r], dw, acc[i][j][r]);
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf((float)C[r], dw * da[r], acc[i][j][r]);
                     }
                 }
             }
@@ -692,7 +692,7 @@ void amv_splitk_reduce(const float* part, int S, int64_t zstride, int64_t m, int
                        hipStream_t st, const float* add = nullptr);
 
 template <int TT, int TW>
-static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
+static int qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                          int64_t ldd, int32_t* sums, hipStream_t st, const float* add) {
     constexpr int BM = 64 * TT, BN = 64 * TW;
     const int8_t* aq = (const int8_t*)act;
@@ -710,6 +710,7 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
         per = kq ? (nsb + S - 1) / S : (((nb + S - 1) / S + 1) & ~1);
         S = kq ? (nsb + per - 1) / per : (nb + per - 1) / per;
         float* ws = S > 1 ? amv_splitk_workspace((size_t)S * m * n_rows * 4, st) : nullptr;
+        if (S > 1 && !ws) return AMV_ERR_HIP;  // never unsplit: the summation order would change
         if (ws) {
             out = ws;
             ldo = n_rows;
@@ -773,6 +774,7 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
 #undef QG_LAUNCH
     }
     if (S > 1) amv_splitk_reduce(out, S, zstride, m, n_rows, dst, ldd, st, add);
+    return AMV_OK;
 }
 
 // Q4_0 / Q8_0 weights with plain Q8_0 activations (int8 [m][k], {f32 d, i32 sum} [m][k/32]); Q4_K weights with plain
@@ -784,7 +786,8 @@ static void qgemm_launch(int wtype, const void* w, int64_t n_rows, int64_t k, co
 int amv_qgemm(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
               int64_t ldd, int32_t* sums, hipStream_t st, const float* add) {
     const auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n_rows + bn - 1) / bn); };
-    if (tiles(128, 128) >= 384) qgemm_launch<2, 2>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st, add);
-    else qgemm_launch<1, 1>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st, add);
+    const int rc = tiles(128, 128) >= 384 ? qgemm_launch<2, 2>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st, add)
+                                          : qgemm_launch<1, 1>(wtype, w, n_rows, k, act, m, dst, ldd, sums, st, add);
+    if (rc) return rc;
     return amv_check_launch("amv_mul_mat_q_act");
 }

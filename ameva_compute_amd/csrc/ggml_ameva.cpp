@@ -16,6 +16,7 @@
 //   * counters and failure injection as ggml-ameva.h:30-98.
 // On MI355X the Vulkan hazard tracking of the reference (ameva_record, 2174) is the in-order stream itself: each
 // kernel starts after the previous one has finished, so no barrier bookkeeping is needed.
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -27,6 +28,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -280,6 +282,7 @@ struct Device {
     unsigned int* status_host_dev = nullptr;  // the same pinned word as the device addresses it
     bool status_clean = false;            // status holds zeros (the last run ended with k_status_out)
     std::vector<hipEvent_t> events;  // AMEVA_PROFILE=2: one after every node of a graph (grows, reused)
+    hipEvent_t done = nullptr;       // recorded after a graph's last kernel: the bounded completion wait polls it
     bool inited = false;
     hipEvent_t event(size_t i) {
         while (events.size() <= i) {
@@ -301,6 +304,7 @@ struct Device {
         if (hipMalloc(&counters, AMEVA_COUNTER_WORDS * 4) != hipSuccess ||
             hipMemset(counters, 0, AMEVA_COUNTER_WORDS * 4) != hipSuccess)
             return false;
+        if (hipEventCreateWithFlags(&done, hipEventDisableTiming) != hipSuccess) return false;
         inited = true;
         g_cnt.ctx_create++;
         return true;
@@ -363,18 +367,41 @@ bool ensure_raw(BufCtx* c, ggml_tensor* t) {
     return true;
 }
 
-// a partial write of a tensor held repacked first returns it to the ggml layout (the write is in ggml bytes)
+// A write of a tensor held repacked first returns it to the ggml layout (the write is in ggml bytes). When that
+// fails, a partial write stops there (its bytes would land in a layout the kernels read differently); a write of
+// the whole tensor replaces every byte, so the tensor is marked as held in ggml layout and written.
+void forget_repacked(BufCtx* c, const ggml_tensor* t) {
+    auto it = c->repacked.find(t->data);
+    if (it == c->repacked.end()) return;
+    c->repacked.erase(it);
+    g_cnt.repacked_tensors--;
+    g_cnt.repacked_bytes -= (int64_t)nbytes(t);
+    g_layout_gen++;
+}
+
 void buf_memset(ggml_backend_buffer_t b, ggml_tensor* t, uint8_t v, size_t off, size_t size) {
     BufCtx* c = (BufCtx*)b->context;
     std::lock_guard<std::mutex> lk(c->mu);
-    if (!ensure_raw(c, t)) log_line("memset_tensor %s: could not restore the ggml layout (FAIL-FAST)", t->name);
+    if (!ensure_raw(c, t)) {
+        if (off != 0 || size != nbytes(t)) {
+            log_line("memset_tensor %s: could not restore the ggml layout; nothing written (FAIL-FAST)", t->name);
+            return;
+        }
+        forget_repacked(c, t);
+    }
     if (hipMemset((uint8_t*)t->data + off, v, size) != hipSuccess) log_line("memset_tensor %s: failed", t->name);
 }
 
 void buf_set_tensor(ggml_backend_buffer_t b, ggml_tensor* t, const void* data, size_t off, size_t size) {
     BufCtx* c = (BufCtx*)b->context;
     std::lock_guard<std::mutex> lk(c->mu);
-    if (!ensure_raw(c, t)) log_line("set_tensor %s: could not restore the ggml layout (FAIL-FAST)", t->name);
+    if (!ensure_raw(c, t)) {
+        if (off != 0 || size != nbytes(t)) {
+            log_line("set_tensor %s: could not restore the ggml layout; nothing written (FAIL-FAST)", t->name);
+            return;
+        }
+        forget_repacked(c, t);
+    }
     if (hipMemcpy((uint8_t*)t->data + off, data, size, hipMemcpyHostToDevice) != hipSuccess)
         log_line("set_tensor %s: copy failed", t->name);
 }
@@ -994,6 +1021,16 @@ struct Engine {
                 return false;
         if (f.sk->nb[1] != f.sv->nb[1] || f.sk->ne[1] != f.sv->ne[1] || f.sk->nb[1] % 2 != 0) return false;
         if (!is_contiguous(f.mv)) return false;
+        // The launch writes q, k, v and both cache rows at once and reads the position and the row index while it
+        // writes. ggml-alloc may place a node's output in the memory of a tensor that is dead by then in the graph's
+        // own node order (k in q's memory after the q ROPE, say), which is safe node by node but not in one launch:
+        // the group is taken only when all of these are disjoint.
+        const ggml_tensor* outs[5] = {f.rq, f.rk, f.mv, f.sk, f.sv};
+        for (int a = 0; a < 5; ++a) {
+            if (overlaps(outs[a], pos) || overlaps(outs[a], idx)) return false;
+            for (int b = a + 1; b < 5; ++b)
+                if (overlaps(outs[a], outs[b])) return false;
+        }
         // the un-rotated q and k exist only inside the launch
         return !read_outside(f.mq, group) && !read_outside(f.mk, group);
     }
@@ -1223,7 +1260,64 @@ bool graph_replay_on() {
     return on;
 }
 
-enum ggml_status finish_graph(Device* d, bool ok, const std::string& why);
+// Bounded completion wait (ggml-ameva.cpp:5545-5561): a graph gets 30 s plus its multiply-accumulates at 0.05e9 per
+// second (at most two hours; AMEVA_WAIT_TIMEOUT_S = 1..86400 seconds replaces that, any other value aborts), then it
+// fails with GGML_STATUS_FAILED instead of blocking the caller for ever. The wait polls an event recorded after the
+// graph's last kernel: spinning for the first 2 ms (a decode graph completes in a fraction of that), then sleeping
+// 50 us between polls. Failure injection point 7 (AMEVA_FAIL_WAIT_TIMEOUT) gives a limit of zero.
+double graph_macs(const ggml_cgraph* g) {
+    double macs = 0.0;
+    for (int i = 0; i < g->n_nodes; ++i) {
+        const ggml_tensor* n = g->nodes[i];
+        if (n->op == GGML_OP_MUL_MAT) macs += (double)nelements(n) * (double)n->src[0]->ne[0];
+        else if (n->op == GGML_OP_FLASH_ATTN_EXT)  // q.k and p.v over every key of every query head
+            macs += 2.0 * (double)n->src[0]->ne[0] * (double)n->src[1]->ne[1] * (double)n->src[0]->ne[2] *
+                    (double)n->src[0]->ne[1];
+        else macs += (double)nelements(n);
+    }
+    return macs;
+}
+uint64_t wait_limit_ns(double macs) {
+    static const uint64_t override_s = [] {
+        const char* e = std::getenv("AMEVA_WAIT_TIMEOUT_S");
+        if (!e || !*e) return (uint64_t)0;
+        char* end = nullptr;
+        const unsigned long long v = std::strtoull(e, &end, 10);
+        if (!end || *end || v < 1 || v > 86400) {
+            log_line("AMEVA_WAIT_TIMEOUT_S must be 1..86400 (got \"%s\")", e);
+            std::abort();
+        }
+        return (uint64_t)v;
+    }();
+    if (g_fail.load() == AMEVA_FAIL_WAIT_TIMEOUT) return 0;
+    const uint64_t work_s = (uint64_t)std::min(7170.0, macs / 0.05e9);
+    return (override_s ? override_s : 30 + work_s) * 1000000000ull;
+}
+struct WaitResult {
+    hipError_t se = hipSuccess;
+    bool timed_out = false;
+};
+WaitResult bounded_wait(Device* d, uint64_t limit_ns) {
+    WaitResult w;
+    if ((w.se = hipEventRecord(d->done, d->stream)) != hipSuccess) return w;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint64_t polls = 0;; ++polls) {
+        const uint64_t el = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                std::chrono::steady_clock::now() - t0).count();
+        if (el >= limit_ns) {
+            w.timed_out = true;
+            return w;
+        }
+        const hipError_t q = hipEventQuery(d->done);
+        if (q == hipSuccess) return w;
+        if (q != hipErrorNotReady) {
+            w.se = q;
+            return w;
+        }
+        if (el > 2000000) std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+}
+enum ggml_status finish_graph(Device* d, bool ok, const std::string& why, const WaitResult& w);
 
 enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
     Device* d = device();
@@ -1246,6 +1340,7 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
     }
     d->arena.used = 0;
     const int prof = profile_level();
+    const uint64_t limit_ns = wait_limit_ns(graph_macs(g));
     // A graph identical to the last one (same signature, no layout change since) is replayed from its HIP graph,
     // captured on its second computation; the first runs eagerly (it repacks weights on first use).
     Replay& rp = d->replay;
@@ -1270,7 +1365,8 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
             g_cnt.fused += rp.d_fused;
             g_cnt.act_reuse += rp.d_act_reuse;
         }
-        return finish_graph(d, ok, ok ? std::string() : std::string("graph replay failed"));
+        return finish_graph(d, ok, ok ? std::string() : std::string("graph replay failed"),
+                            ok ? bounded_wait(d, limit_ns) : WaitResult{});
     }
     if (!same || !can_graph) {
         rp.drop();
@@ -1304,7 +1400,8 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
             rp.encoded = e.encoded;
             if (trace_on()) std::fprintf(stderr, "AMEVA_TRACE graph captured nodes=%d\n", g->n_nodes);
             const bool launched = hipGraphLaunch(rp.exec, d->stream) == hipSuccess;
-            return finish_graph(d, launched, launched ? std::string() : std::string("graph launch failed"));
+            return finish_graph(d, launched, launched ? std::string() : std::string("graph launch failed"),
+                                launched ? bounded_wait(d, limit_ns) : WaitResult{});
         }
         // not capturable (a step needed something a capture cannot hold): undo the counts, run eagerly below
         if (rp.exec) (void)hipGraphExecDestroy(rp.exec);
@@ -1332,7 +1429,8 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         std::fprintf(stderr, "AMEVA_TRACE graph=%lld nodes=%d encoded=%lld encode_ms=%.3f\n", (long long)graph_no,
                      g->n_nodes, (long long)e.encoded, t1 - t0);
     }
-    const hipError_t se = hipStreamSynchronize(d->stream);
+    const WaitResult w = bounded_wait(d, limit_ns);  // also after a failed encode: what was queued completes
+    const hipError_t se = w.timed_out ? hipErrorNotReady : w.se;
     if (prof) {
         const double t2 = now_ms();
         std::lock_guard<std::mutex> pl(g_prof.mu);
@@ -1361,20 +1459,22 @@ enum ggml_status graph_compute(ggml_backend_t, ggml_cgraph* g) {
         return GGML_STATUS_FAILED;
     }
     rp.gen = g_layout_gen.load();  // the layout this run left (its first use repacked the weights)
-    return finish_graph(d, se == hipSuccess, se == hipSuccess ? std::string() : std::string(hipGetErrorString(se)));
+    return finish_graph(d, true, std::string(), w);
 }
 
 // after the graph's work is queued (eager) or launched (replay): wait, then the status word
-enum ggml_status finish_graph(Device* d, bool ok, const std::string& why) {
-    const hipError_t se = ok ? hipStreamSynchronize(d->stream) : hipSuccess;
+enum ggml_status finish_graph(Device* d, bool ok, const std::string& why, const WaitResult& w) {
     if (!ok) {
         log_line("%s (FAIL-FAST)", why.c_str());
         return GGML_STATUS_FAILED;
     }
-    if (g_fail.load() == AMEVA_FAIL_WAIT_TIMEOUT) {
-        log_line("failure injection: wait timeout (FAIL-FAST)");
+    if (w.timed_out) {
+        // the graph may still run: the status words are cleared before the next one
+        log_line("graph did not complete within the wait limit%s (FAIL-FAST)",
+                 g_fail.load() == AMEVA_FAIL_WAIT_TIMEOUT ? " (failure injection: wait timeout)" : "");
         return GGML_STATUS_FAILED;
     }
+    const hipError_t se = w.se;
     if (se != hipSuccess) {
         log_line("graph execution failed: %s (FAIL-FAST)", hipGetErrorString(se));
         return GGML_STATUS_FAILED;
@@ -1457,6 +1557,124 @@ void setup_registry() {
     });
 }
 
+// ---- load-time check of the host's ggml ABI (the reference's ameva_abi_check, ggml-ameva-device.cpp:415-495)
+// ggml-backend-impl.h carries no ABI version: a libggml-base built from other headers (another member count in a
+// vtable, another GGML_MAX_NAME) reads this plugin's structs at shifted offsets. Before the registry reaches the
+// host, objects laid out by ggml_abi.h are read back through the host's own accessors, and every op and type value
+// the engine dispatches on is named by the host. The accessors are looked up in the library that provides
+// ggml_backend_buffer_init (the plugin's one link-time host symbol), else in the global scope.
+struct abi_init_params {  // struct ggml_init_params (ggml.h)
+    size_t mem_size;
+    void* mem_buffer;
+    bool no_alloc;
+};
+struct ggml_context;
+
+const char* abi_check() {
+    static std::once_flag once;
+    static char msg[448];
+    static const char* result = nullptr;
+    std::call_once(once, [] {
+        void* lib = nullptr;
+        Dl_info info{};
+        if (dladdr((void*)&ggml_backend_buffer_init, &info) && info.dli_fname)
+            lib = dlopen(info.dli_fname, RTLD_LAZY | RTLD_NOLOAD);
+        const char* missing = nullptr;
+        auto sym = [&](const char* name) -> void* {
+            void* p = lib ? dlsym(lib, name) : nullptr;
+            if (!p) p = dlsym(RTLD_DEFAULT, name);
+            if (!p && !missing) missing = name;
+            return p;
+        };
+        auto get_device = (ggml_backend_dev_t(*)(ggml_backend_t))sym("ggml_backend_get_device");
+        auto buf_size = (size_t(*)(ggml_backend_buffer_t))sym("ggml_backend_buffer_get_size");
+        auto buf_type = (ggml_backend_buffer_type_t(*)(ggml_backend_buffer_t))sym("ggml_backend_buffer_get_type");
+        auto buft_device = (ggml_backend_dev_t(*)(ggml_backend_buffer_type_t))sym("ggml_backend_buft_get_device");
+        auto dev_reg = (ggml_backend_reg_t(*)(ggml_backend_dev_t))sym("ggml_backend_dev_backend_reg");
+        auto op_nm = (const char* (*)(int))sym("ggml_op_name");
+        auto type_nm = (const char* (*)(int))sym("ggml_type_name");
+        auto overhead = (size_t(*)(void))sym("ggml_tensor_overhead");
+        auto init = (ggml_context * (*)(abi_init_params))sym("ggml_init");
+        auto free_ctx = (void (*)(ggml_context*))sym("ggml_free");
+        auto new_2d = (ggml_tensor * (*)(ggml_context*, int, int64_t, int64_t))sym("ggml_new_tensor_2d");
+        auto mul_mat = (ggml_tensor * (*)(ggml_context*, ggml_tensor*, ggml_tensor*))sym("ggml_mul_mat");
+        auto nbytes_fn = (size_t(*)(const ggml_tensor*))sym("ggml_nbytes");
+        auto set_name = (ggml_tensor * (*)(ggml_tensor*, const char*))sym("ggml_set_name");
+        auto get_name = (const char* (*)(const ggml_tensor*))sym("ggml_get_name");
+        if (lib) dlclose(lib);
+        if (missing) {
+            std::snprintf(msg, sizeof(msg), "the host's libggml-base does not export %s: its ABI cannot be checked",
+                          missing);
+            result = msg;
+            return;
+        }
+        const char* what = nullptr;
+        ggml_backend pb{};
+        pb.device = &g_device;
+        ggml_backend_buffer_type pbt{};
+        pbt.device = &g_device;
+        ggml_backend_buffer pbuf{};
+        pbuf.buft = &pbt;
+        pbuf.size = 0x5A17;
+        ggml_backend_device pd{};
+        pd.reg = &g_reg;
+        if (get_device(&pb) != &g_device) what = "struct ggml_backend (ggml_backend_i member count)";
+        else if (buf_size(&pbuf) != 0x5A17 || buf_type(&pbuf) != &pbt)
+            what = "struct ggml_backend_buffer (ggml_backend_buffer_i member count)";
+        else if (buft_device(&pbt) != &g_device) what = "struct ggml_backend_buffer_type";
+        else if (dev_reg(&pd) != &g_reg) what = "struct ggml_backend_device";
+        // every op and type value graph_compute and supports_op switch on
+        static const struct { int v; const char* name; } ops[] = {
+            {GGML_OP_NONE, "NONE"},         {GGML_OP_ADD, "ADD"},         {GGML_OP_MUL, "MUL"},
+            {GGML_OP_RMS_NORM, "RMS_NORM"}, {GGML_OP_MUL_MAT, "MUL_MAT"}, {GGML_OP_CPY, "CPY"},
+            {GGML_OP_CONT, "CONT"},         {GGML_OP_RESHAPE, "RESHAPE"}, {GGML_OP_VIEW, "VIEW"},
+            {GGML_OP_PERMUTE, "PERMUTE"},   {GGML_OP_TRANSPOSE, "TRANSPOSE"}, {GGML_OP_GET_ROWS, "GET_ROWS"},
+            {GGML_OP_SET_ROWS, "SET_ROWS"}, {GGML_OP_SOFT_MAX, "SOFT_MAX"}, {GGML_OP_ROPE, "ROPE"},
+            {GGML_OP_FLASH_ATTN_EXT, "FLASH_ATTN_EXT"}, {GGML_OP_UNARY, "UNARY"}, {GGML_OP_GLU, "GLU"}};
+        static const struct { int v; const char* name; } types[] = {
+            {GGML_TYPE_F32, "f32"},   {GGML_TYPE_F16, "f16"},   {GGML_TYPE_Q4_0, "q4_0"}, {GGML_TYPE_Q8_0, "q8_0"},
+            {GGML_TYPE_Q4_K, "q4_K"}, {GGML_TYPE_Q6_K, "q6_K"}, {GGML_TYPE_I32, "i32"},   {GGML_TYPE_I64, "i64"}};
+        for (const auto& o : ops) {
+            const char* s = what ? nullptr : op_nm(o.v);
+            if (!what && (!s || std::strcmp(s, o.name) != 0)) what = "enum ggml_op";
+        }
+        for (const auto& t : types) {
+            const char* s = what ? nullptr : type_nm(t.v);
+            if (!what && (!s || std::strcmp(s, t.name) != 0)) what = "enum ggml_type";
+        }
+        if (!what) {
+            // struct ggml_tensor: a MUL_MAT node built by the host, read with this plugin's layout
+            ggml_context* ctx = init(abi_init_params{8 * overhead(), nullptr, true});
+            if (!ctx) {
+                what = "ggml_init for the tensor layout probe";
+            } else {
+                ggml_tensor* a = new_2d(ctx, GGML_TYPE_F32, 8, 3);
+                ggml_tensor* b = new_2d(ctx, GGML_TYPE_F32, 8, 2);
+                ggml_tensor* c = a && b ? mul_mat(ctx, a, b) : nullptr;
+                if (!c || c->op != GGML_OP_MUL_MAT || c->src[0] != a || c->src[1] != b || c->type != GGML_TYPE_F32 ||
+                    c->ne[0] != 3 || c->ne[1] != 2 || a->nb[1] != 32 || nbytes_fn(c) != 24 || c->data != nullptr)
+                    what = "struct ggml_tensor";
+                // the host cuts a name to its own GGML_MAX_NAME - 1 characters; extra sits behind name[]
+                char probe[512];
+                std::memset(probe, 'n', sizeof(probe) - 1);
+                probe[sizeof(probe) - 1] = 0;
+                if (!what && std::strlen(get_name(set_name(c, probe))) != sizeof(c->name) - 1)
+                    what = "struct ggml_tensor (GGML_MAX_NAME)";
+                free_ctx(ctx);
+            }
+        }
+        if (what) {
+            std::snprintf(msg, sizeof(msg),
+                          "ABI mismatch with the loaded libggml-base: %s differs from the ggml 0.9.8 layout "
+                          "libggml-ameva.so was built with (offsetof(ggml_backend, device) = %zu); rebuild it against "
+                          "the host's ggml headers",
+                          what, offsetof(ggml_backend, device));
+            result = msg;
+        }
+    });
+    return result;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------------ exports
@@ -1466,7 +1684,13 @@ ggml_backend_reg_t ggml_backend_ameva_reg(void) {
     setup_registry();
     return &g_reg;
 }
-void ggml_backend_ameva_register(void) { setup_registry(); }
+void ggml_backend_ameva_register(void) {
+    if (const char* why = abi_check()) {
+        log_line("not registering the AMEVA backend: %s", why);
+        return;
+    }
+    setup_registry();
+}
 void ggml_backend_ameva_teardown(void) {
     Device* d = device();
     std::lock_guard<std::mutex> lk(d->compute_mu);
@@ -1485,12 +1709,26 @@ void ggml_backend_ameva_teardown(void) {
         d->inited = false;
     }
 }
-ggml_backend_reg_t ggml_backend_init(void) { return ggml_backend_ameva_reg(); }
+// the dynamic loader's entry (ggml-ameva.cpp:5693-5702): NULL when the host's ggml ABI differs, so the loader
+// reports the backend as failed instead of reading this plugin's structs at the wrong offsets
+ggml_backend_reg_t ggml_backend_init(void) {
+    if (const char* why = abi_check()) {
+        log_line("refusing to load: %s", why);
+        return nullptr;
+    }
+    return ggml_backend_ameva_reg();
+}
+// the reason ggml_backend_init refuses, or NULL when the host's ABI matches
+const char* ggml_backend_ameva_abi_check(void) { return abi_check(); }
 int ggml_backend_score(void) { return 100; }
 
 ggml_backend_t ggml_backend_ameva_init(size_t dev_num) {
     if (dev_num != 0) {
         log_line("device %zu does not exist (AMEVA0 only)", dev_num);
+        return nullptr;
+    }
+    if (const char* why = abi_check()) {
+        log_line("cannot create the AMEVA backend: %s", why);
         return nullptr;
     }
     setup_registry();

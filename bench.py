@@ -69,11 +69,12 @@ def time_steps(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps  # ms per step
 
 
-def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS, info=None):
+def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS, info=None, min_reps=1, median=False):
     """fn(i) for i in 0..per_graph-1 captured once in a HIP graph; the graph is replayed so that K >= steps steps
-    run back to back with no host launch cost between kernels. Returns ms per step; info (a dict), when given,
-    receives the step counts that actually ran: 'timed' (replays x per_graph) and 'warmup' (the eager pass before
-    the capture plus the untimed replays)."""
+    (and at least min_reps replays) run back to back with no host launch cost between kernels. Returns ms per step:
+    the mean over all replays, or with median=True the median of the replays, each timed by its own pair of events
+    on the replay stream. info (a dict), when given, receives the step counts that actually ran: 'timed' (replays x
+    per_graph), 'warmup' (the eager pass before the capture plus the untimed replays) and 'replays'."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -85,12 +86,26 @@ def time_steps_graph(torch, fn, steps, warmup, per_graph=GRAPH_STEPS, info=None)
     with torch.cuda.graph(graph):
         for i in range(per_graph):
             fn(i)
-    reps = max(1, (steps + per_graph - 1) // per_graph)
+    reps = max(min_reps, (steps + per_graph - 1) // per_graph)
     wreps = max(1, warmup // per_graph)
     if info is not None:
         info["timed"] = reps * per_graph
         info["warmup"] = (1 + wreps) * per_graph
-    ms = time_steps(torch, lambda i: graph.replay(), reps, wreps)
+        info["replays"] = reps
+    if median:
+        for _ in range(wreps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        ev[0].record()
+        for r in range(reps):
+            graph.replay()
+            ev[r + 1].record()
+        torch.cuda.synchronize()
+        per = sorted(ev[r].elapsed_time(ev[r + 1]) for r in range(reps))
+        ms = per[reps // 2] if reps % 2 else 0.5 * (per[reps // 2 - 1] + per[reps // 2])
+    else:
+        ms = time_steps(torch, lambda i: graph.replay(), reps, wreps)
     del graph
     return ms / per_graph
 
@@ -150,6 +165,9 @@ def cpu_layer_decode(oracle, rng, seconds):
     return _timed(step, seconds)
 
 
+CPU_COPIES = 12
+
+
 def cpu_baseline(seconds: float = 10.0):
     """The headline GEMV on the host cores (plus, beside it, the M = 512 GEMM and the layer decode step): ggml's AVX2
     vec_dot_q4_0_q8_0 algorithm (oracle/cpu_simd.c, OpenMP) where the CPU has AVX2 / FMA / F16C, else the oracle's
@@ -162,11 +180,19 @@ def cpu_baseline(seconds: float = 10.0):
     x = rng.standard_normal((1, K)).astype(np.float32)
     aq = oracle.quantize_q8_0(x, oracle.Q8_X86)
     if simd:
-        wq = _cpu_q4_0_weights(rng, N_ROWS, K)
+        # cold like the GPU figure: CPU_COPIES rotating weight copies (~400 MB, beyond the host's L3)
+        wqs = [_cpu_q4_0_weights(rng, N_ROWS, K) for _ in range(CPU_COPIES)]
+        wq = wqs[0]
         out = np.empty((1, N_ROWS), np.float32)
-        per, n, el = _timed(lambda: oracle.simd_mul_mat_q4_0(wq, N_ROWS, K, aq, 1, out), seconds)
+        turn = [0]
+
+        def gemv_cold():
+            oracle.simd_mul_mat_q4_0(wqs[turn[0] % CPU_COPIES], N_ROWS, K, aq, 1, out)
+            turn[0] += 1
+        per, n, el = _timed(gemv_cold, seconds)
         threads = oracle.cpu_simd().cpu_num_threads()
-        how = "ggml's AVX2 vec_dot_q4_0_q8_0 algorithm (oracle/cpu_simd.c, OpenMP)"
+        how = (f"ggml's AVX2 vec_dot_q4_0_q8_0 algorithm (oracle/cpu_simd.c, OpenMP), cold: {CPU_COPIES} rotating "
+               f"weight copies ({CPU_COPIES * N_ROWS * K * 18 // 32 / 1e6:.0f} MB, beyond the host's L3)")
     else:
         w = (rng.standard_normal((N_ROWS, K)) * 0.02).astype(np.float32)
         wq = oracle.quantize_q4_0(w)
@@ -191,7 +217,7 @@ def cpu_baseline(seconds: float = 10.0):
         res["gemm_m512_gops"] = round(2.0 * rows * K * m / per5 / 1e9, 1)
         res["gemm_sample"] = (f"{n5} Q4_0 x Q8_0 GEMMs of {rows} of the 14336 rows x 4096 x 512 tokens in {el5:.1f} s "
                               f"({per5 * 1e3:.1f} ms each; the full 14336-row GEMM scales by 8)")
-        del wq, w5, a5, o5
+        del wq, wqs, w5, a5, o5
         perl, nl, ell = cpu_layer_decode(oracle, rng, seconds / 3)
         res["layer_decode_tok_s"] = round(1.0 / perl, 2)
         res["layer_decode_sample"] = (f"{nl} bs1 decode steps of one Llama-3-8B Q4_0 layer at 4096 cached keys in "
@@ -838,7 +864,7 @@ def main():
         ops.mul_mat_q(ws[0], act, 1, out)
 
     ran = {}
-    ms_cold = time_steps_graph(torch, step_cold, args.steps, args.warmup, info=ran)
+    ms_cold = time_steps_graph(torch, step_cold, args.steps, args.warmup, info=ran, min_reps=10, median=True)
     nbytes = gemv_bytes(N_ROWS, K)
     gbs = nbytes / (ms_cold * 1e-3) / 1e9
     log(f"bench: cold {ms_cold * 1e3:.2f} us/GEMV = {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
@@ -890,8 +916,9 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights quantized on the GPU (ggml Q4_0 rule), N(0,1) activation",
         "config": {"workload": "Q4_0 GEMV 14336x4096 M=1 (Llama-3-8B FFN gate/up), Q8_0 activation, cold: "
                                f"{COPIES} rotating weight copies ({COPIES * N_ROWS * K * 18 // 32 / 2**20:.0f} MiB)",
-                   "n_rows": N_ROWS, "k": K, "m": 1, "weight_copies": COPIES, "timing": f"HIP graph of {GRAPH_STEPS} GEMV launches replayed {ran['timed'] // GRAPH_STEPS} times "
-                             f"(steps = GEMVs timed); warmup = {GRAPH_STEPS} eager GEMVs + "
+                   "n_rows": N_ROWS, "k": K, "m": 1, "weight_copies": COPIES, "timing": f"HIP graph of {GRAPH_STEPS} GEMV launches replayed {ran['replays']} times, each "
+                             f"replay timed by its own events, median replay / {GRAPH_STEPS} (steps = GEMVs timed, "
+                             f"at least 10 replays whatever --steps says); warmup = {GRAPH_STEPS} eager GEMVs + "
                              f"{ran['warmup'] // GRAPH_STEPS - 1} untimed replays"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic()},

@@ -94,6 +94,12 @@ int amv_quantize_q4_0(const float* x, int64_t n_rows, int64_t k, void* y_ggml, v
  * ---------------------------------------------------------------------------------------------------------- */
 int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                     int64_t ldd, void* stream);
+/* Parity instrumentation (no counterpart in the reference; for tests): while on != 0, the Q4_0 GEMV launches of this
+ * process skip the dedicated K = 4096 kernels and run the generic one-column kernel of the same rows per wave, split
+ * and epilogue, whose block-sum instantiation is the one amv_mul_mat_block_sums reads; the dedicated kernels keep
+ * that kernel's arithmetic and summation order, so a test compares their f32 results bit for bit. Returns the
+ * previous setting. Not for production calls: the generic kernels are slower. */
+int amv_debug_gemv_generic(int on);
 
 /* One-column GEMV with the fused epilogue of the next graph node: the reference's ameva_qmv / ameva_mmvq ep_mode
  * (ameva_qmv.comp:233-246) chosen by ameva_find_fusion (ggml-ameva.cpp:4280-4285, 4355-4375). v[n] is the dot

@@ -79,6 +79,12 @@ int64_t ggml_backend_ameva_get_conv_bias_count(void);
 int64_t ggml_backend_ameva_get_group_norm_count(void);
 int64_t ggml_backend_ameva_get_window_node_count(void);
 const char* ggml_backend_ameva_get_build_commit(void);
+/* The host ABI check that ggml_backend_init, ggml_backend_ameva_register and ggml_backend_ameva_init run before
+ * anything of the plugin reaches libggml-base (the reference's internal ameva_abi_check, ggml-ameva-device.cpp:415-495;
+ * exported here, with no counterpart in the reference's header, so a host or test can read the reason): NULL when the
+ * loaded libggml-base reads the plugin's ggml_backend, buffer, buffer type, device and tensor structs at the offsets
+ * this build uses and names every op and type value it dispatches on the same; else the mismatch. */
+const char* ggml_backend_ameva_abi_check(void);
 void ggml_backend_ameva_reset_counters(void);
 /* Prints the AMEVA_PROFILE report now (ggml-ameva.h profile_report; ggml-ameva.cpp:208-277): with AMEVA_PROFILE=1
  * the per-graph totals (graphs, nodes, encoded launches, host encode and wait ms), with AMEVA_PROFILE=2 also the GPU

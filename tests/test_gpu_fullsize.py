@@ -13,6 +13,8 @@
 import numpy as np
 import pytest
 
+from parity import TOL_F16_OPERANDS, dequant_act, per_output_gate
+
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
@@ -78,6 +80,7 @@ def test_config2_batched_full_shape(dev, ops, orc, wt, shape, m):
     a_ref = orc.quantize_q8_K(x) if base == Q8_K else orc.quantize_q8_0(x, orc.Q8_X86)
     rows = sample_rows(n, 192, seed + 2)
     y_ref = orc.mul_mat(wt, np.ascontiguousarray(wg[rows]), len(rows), k, a_ref, m)  # [m, rows]
+    w_deq, a_deq = orc.dequantize(wt, np.ascontiguousarray(wg[rows]), k), dequant_act(a_ref, base, k)
     for at, name in forms:
         act, ag = ops.quantize_act(xd, at, ops.Q8_X86, ggml=True)
         assert np.array_equal(ag.cpu().numpy().reshape(-1), a_ref.reshape(-1)), name
@@ -89,6 +92,10 @@ def test_config2_batched_full_shape(dev, ops, orc, wt, shape, m):
         print(f"{name}: wt {wt} {n}x{k} m {m}: rel L2 {e:.2e}, worst sampled row {worst:.2e}")
         assert e < 1e-3, (name, e)
         assert np.isfinite(got).all()
+        # output by output: the reference's gate for the exact form, the f16 rounding bound for the scaled one
+        g = per_output_gate(got, w_deq, a_deq, tol=TOL_F16_OPERANDS if name == "scaled" else 1e-5,
+                            what=f"{name} wt {wt} {n}x{k} m {m}")
+        print(f"{name}: worst per-output error {g:.2e} of sum |w a|")
     # exact form: the per-block integers of a 256-row slice at the full k and batch, bit for bit
     sl = rows[:256] if len(rows) >= 256 else rows
     wsl = np.ascontiguousarray(wg[sl])
@@ -114,6 +121,7 @@ def test_q6k_output_head_full(dev, ops, orc):
     e = rel_l2(y, y_ref.reshape(-1))
     print(f"Q6_K head 128256x4096: rel L2 {e:.2e}")
     assert e < 1e-3
+    per_output_gate(y, orc.dequantize(Q6_K, wg, k), dequant_act(a_ref, Q8_K, k), what="Q6_K head")
     assert int(np.argmax(y)) == int(np.argmax(y_ref))
 
 

@@ -4,6 +4,8 @@ MFMA path agrees with the decode GEMV column by column."""
 import numpy as np
 import pytest
 
+from parity import TOL_F16_OPERANDS, dequant_act, per_output_gate
+
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
@@ -59,6 +61,7 @@ def test_mmq_block_sums_and_output(dev, ops, orc, wtype, m, n, k, atype):
     assert np.array_equal(sums, s_ref)
     y = ops.mul_mat_q(w, act, m, kernel="mmq").cpu().numpy()
     assert rel_l2(y, y_ref) < TOL_F32
+    per_output_gate(y, orc.dequantize(wtype, wg, k), dequant_act(a_ref, 8, k), what=f"mmq {wtype} {m}x{n}x{k}")
 
 
 @pytest.mark.parametrize("wtype", [2, 8])
@@ -82,6 +85,10 @@ def test_mmq_full_size(dev, ops, orc, wtype):
     assert rel_l2(y.cpu().numpy(), y8.cpu().numpy()) < 1e-5
     y_ref = orc.mul_mat(wtype, wg.cpu().numpy(), n, k, ag.cpu().numpy(), m)
     assert rel_l2(y.cpu().numpy(), y_ref) < TOL_F32
+    # output by output, the batched product and the GEMV of the same rows are both within the reference's gate
+    w_deq, a_deq = orc.dequantize(wtype, wg.cpu().numpy(), k), dequant_act(ag.cpu().numpy(), 8, k)
+    per_output_gate(y.cpu().numpy(), w_deq, a_deq, what="mmq M=512")
+    per_output_gate(y_mmv.cpu().numpy(), w_deq, a_deq, what="GEMV columns M=512")
 
 
 def test_routing_matches_reference_threshold(dev, ops, orc):
@@ -130,6 +137,9 @@ def test_mmq_q4k_block_sums_and_output(dev, ops, orc, m, n, k):
     assert rel_l2(y, y_ref) < TOL_F32
     y_v = ops.mul_mat_q(w, act, m, kernel="mmv").cpu().numpy()  # the GEMV on the same buffer's Q8_K prefix
     assert rel_l2(y, y_v) < 1e-5
+    w_deq, a_deq = orc.dequantize(ops.Q4_K, wg, k), dequant_act(a_ref, 15, k)
+    per_output_gate(y, w_deq, a_deq, what=f"mmq Q4_K {m}x{n}x{k}")
+    per_output_gate(y_v, w_deq, a_deq, what=f"GEMV Q4_K columns {m}x{n}x{k}")
 
 
 def deq_f16_region(act, m, k, q4k):
@@ -181,6 +191,10 @@ def test_scaled_gemm_matches_oracle_and_exact_form(dev, ops, orc, wtype, m, n, k
     e_ref, e_ex = rel_l2(y_d, y_ref), rel_l2(y_d, y_e)
     print(f"scaled form: rel L2 {e_ref:.2e} against the oracle, {e_ex:.2e} against the exact form")
     assert e_ref < TOL_F32 and e_ex < TOL_F32
+    # each operand rounded once to f16: per output within 2^-10 sum |w a| (the exact form within 1e-5)
+    w_deq, a_deq = orc.dequantize(wtype, wg, k), dequant_act(a_ref, 15 if q4k else 8, k)
+    per_output_gate(y_d, w_deq, a_deq, tol=TOL_F16_OPERANDS, what="scaled form")
+    per_output_gate(y_e, w_deq, a_deq, what="exact form")
     sums = torch.empty(m * n * (k // 256 * 2 if q4k else k // 32), dtype=torch.int32, device=dev)
     rc = ops.lib().amv_mul_mat_q_act_block_sums(wtype, w.data.data_ptr(), n, k, act_d.data_ptr(), deq_t, m,
                                                 sums.data_ptr(), torch.cuda.current_stream().cuda_stream)
@@ -189,8 +203,9 @@ def test_scaled_gemm_matches_oracle_and_exact_form(dev, ops, orc, wtype, m, n, k
 
 def test_split_k_under_graph_capture(dev, ops, orc):
     """The scaled GEMM split over k (4096 x 14336 at 200 tokens) inside a captured graph: every replay equals the
-    eager result bit for bit (the partials are summed in a fixed order), also after eager calls that grow the
-    library's workspace between the replays (the graph keeps the buffer it recorded, which stays allocated)."""
+    eager result bit for bit (the partials are summed in a fixed order), also with eager calls of a larger batch
+    between the replays (the library's split-k workspace has a fixed size, allocated by the first uncaptured call
+    that splits k, and never moves)."""
     rng = np.random.default_rng(77)
     n, k, m = 4096, 14336, 200
     wg = weights(orc, rng, ops.Q4_0, n, k)
@@ -225,8 +240,9 @@ def test_split_k_under_graph_capture(dev, ops, orc):
 
 @pytest.mark.parametrize("m", [8, 16, 40])
 def test_mul_mat_q_plain_q8k_for_q4k(dev, ops, orc, m):
-    """amv_mul_mat_q with a plain Q8_K activation (no f16 copies) for Q4_K weights: small batches go to the tiled
-    int8 kernel, which reads only the plain layout (the small-batch kernels need AMV_ACT_Q8_K_MMA)."""
+    """amv_mul_mat_q, and amv_mul_mat_q_act with act_type AMV_T_Q8_K, on a plain Q8_K activation (no f16 copies) for
+    Q4_K weights: small batches go to the tiled int8 kernel, which reads only the plain layout (the small-batch
+    kernels need AMV_ACT_Q8_K_MMA); both equal, within the per-output gate of the oracle."""
     from ameva_compute_amd._lib import lib
     rng = np.random.default_rng(300 + m)
     n, k = 96, 1024
@@ -236,9 +252,16 @@ def test_mul_mat_q_plain_q8k_for_q4k(dev, ops, orc, m):
     w = ops.QWeight.from_ggml(ops.Q4_K, gpu(wg, dev), n, k)
     plain, _ = ops.quantize_act(gpu(x, dev), ops.Q8_K)
     out = torch.empty((m, n), dtype=torch.float32, device=dev)
-    assert lib().amv_mul_mat_q(ops.Q4_K, w.data.data_ptr(), n, k, plain.data_ptr(), m, out.data_ptr(), n,
-                               torch.cuda.current_stream().cuda_stream) == 0
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib().amv_mul_mat_q(ops.Q4_K, w.data.data_ptr(), n, k, plain.data_ptr(), m, out.data_ptr(), n, st) == 0
     assert rel_l2(out.cpu().numpy(), y_ref) < TOL_F32
+    out2 = torch.empty_like(out)
+    rc = lib().amv_mul_mat_q_act(ops.Q4_K, w.data.data_ptr(), n, k, plain.data_ptr(), ops.Q8_K, m, out2.data_ptr(), n,
+                                 st)
+    assert rc == 0, lib().amv_last_error()
+    assert torch.equal(out2, out)
+    per_output_gate(out.cpu().numpy(), orc.dequantize(ops.Q4_K, wg, k), dequant_act(orc.quantize_q8_K(x), 15, k),
+                    what=f"Q4_K plain Q8_K m={m}")
 
 
 @pytest.mark.parametrize("wtype,atype,m,n,k", [

@@ -1,10 +1,13 @@
 """GPU parity of the quantizers, the weight repack and the decode GEMV against the CPU oracle, through the C ABI.
 
 Bars: Q8_0 / Q4_0 / Q8_K bytes and per-block int32 sums bit-exact; f32 GEMV output within 1e-3 relative L2 of the
-oracle (the observed error is ~1e-7: only the f32 summation order differs).
+oracle (the observed error is ~1e-7: only the f32 summation order differs) and, output by output, within the
+reference's gate |got - ref| <= 1e-5 sum |w a| (tests/parity.py).
 """
 import numpy as np
 import pytest
+
+from parity import dequant_act, per_output_gate
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -152,6 +155,7 @@ def test_gemv_parity(dev, ops, orc, wtype, n, k):
     sums = ops.block_sums(w, act, 1).cpu().numpy()
     assert np.array_equal(sums, s_ref)
     assert rel_l2(y, y_ref) < TOL_F32
+    per_output_gate(y, orc.dequantize(wtype, wg, k), dequant_act(a_ref, 8, k), what=f"GEMV {wtype} {n}x{k}")
 
 
 @pytest.mark.parametrize("wtype", [2, 8])
@@ -168,6 +172,7 @@ def test_gemv_multi_column(dev, ops, orc, wtype):
     sums = ops.block_sums(w, act, m).cpu().numpy()
     assert np.array_equal(sums, s_ref)
     assert rel_l2(y, y_ref) < TOL_F32
+    per_output_gate(y, orc.dequantize(wtype, wg, k), dequant_act(a_ref, 8, k), what="GEMV m=5")
 
 
 def test_gemv_full_size_linearity(dev, ops):

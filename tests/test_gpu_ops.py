@@ -7,6 +7,8 @@ outputs within 1e-3 relative L2 of the oracle; attention with the f16 KV cache w
 import numpy as np
 import pytest
 
+from parity import dequant_act, per_output_gate
+
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
@@ -70,6 +72,7 @@ def test_kquant_gemv_parity(dev, ops, orc, wtype, n, k):
     sums = ops.block_sums(w, act, 1).cpu().numpy()
     assert np.array_equal(sums, s_ref)
     assert rel_l2(y, y_ref) < TOL_F32
+    per_output_gate(y, orc.dequantize(wtype, wg, k), dequant_act(a_ref, 15, k), what=f"GEMV {wtype} {n}x{k}")
 
 
 @pytest.mark.parametrize("wtype", [12, 14])

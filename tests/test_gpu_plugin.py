@@ -10,6 +10,7 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 import ggml_plugin as gp  # noqa: E402
+from parity import dequant_act, per_output_gate  # noqa: E402
 
 
 def rel_l2(a, b):
@@ -67,6 +68,8 @@ def test_mul_mat_node(plugin, orc, wt, m):
         assert g.compute() == gp.STATUS_SUCCESS
         y = g.get(Y, np.float32, (m, n))
         assert rel_l2(y, orc.mul_mat(wt, wg, n, k, aq(x), m)) < 1e-3
+        per_output_gate(y, orc.dequantize(wt, wg, k), dequant_act(aq(x), 15 if wt in (gp.Q4_K, gp.Q6_K) else 8, k),
+                        what=f"plugin MUL_MAT {wt} m={m}")
         assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 1
         assert gp.counter(plugin, "mmq_mul_mat_count") == (1 if m >= 8 else 0)
         assert gp.counter(plugin, "repacked_tensor_count") == rep0 + 1
@@ -132,6 +135,9 @@ def test_mul_mat_placement_matrix(plugin, orc, wt, place):
             r0 = 3 if place == "view" else 0
             want = orc.mul_mat(wt, np.ascontiguousarray(wg[r0:r0 + N]), N, K, aq(x), M)
             assert rel_l2(y, want) < 1e-3, (M, N, K, rel_l2(y, want))
+            per_output_gate(y, orc.dequantize(wt, np.ascontiguousarray(wg[r0:r0 + N]), K),
+                            dequant_act(aq(x), 15 if wt in (gp.Q4_K, gp.Q6_K) else 8, K),
+                            what=f"placement {place} {wt} {(M, N, K)}")
             repacked = place in ("weights", "split")
             assert gp.counter(plugin, "repacked_tensor_count") == rep0 + (1 if repacked else 0), (M, N, K)
             assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 1
@@ -585,5 +591,59 @@ def test_node_groups_and_their_guards(plugin, orc, extra_reads):
         if extra_reads:
             assert rel_l2(g.get(yq, np.float32, (1, NH * D)), qm * e_q) < 1e-3
             assert rel_l2(g.get(yg, np.float32, (1, FF)), gm * e_g) < 1e-3
+    finally:
+        g.free()
+
+
+def test_qkv_group_declined_when_outputs_share_memory(plugin, orc):
+    """ggml-alloc places a node's output in the memory of a tensor that is dead by then in the graph's node order. With
+    the nodes ordered k MUL_MAT, k ROPE, k SET_ROWS, q MUL_MAT, q ROPE, v MUL_MAT, v SET_ROWS, the roped q may take the
+    memory of the roped k, which SET_ROWS has consumed: correct node by node, but one launch writing q and k at once
+    would lose one of them. The plugin then declines the q/k/v node group and runs the nodes one by one: the q values,
+    both cache rows and v match the oracle."""
+    rng = np.random.default_rng(123)
+    H, NH, NKV, D, CTX, pos_t = 4096, 2, 2, 128, 48, 29
+    def wq4(n, k):
+        return orc.quantize_q4_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    w = {"q": wq4(NH * D, H), "k": wq4(NKV * D, H), "v": wq4(NKV * D, H)}
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    kc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    vc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    g = gp.Graph(sum(a.nbytes for a in w.values()) + 4 * 4096, 8 << 20)
+    try:
+        T = {k_: g.tensor(gp.Q4_0, [H, a.shape[0]], "w", k_) for k_, a in w.items()}
+        for k_, a in w.items():
+            g.set(T[k_], a)
+        X = g.tensor(gp.F32, [H, 1], "c", "x")
+        g.set(X, x)
+        POS, IDX = g.tensor(gp.I32, [1], "c", "pos"), g.tensor(gp.I64, [1], "c", "idx")
+        g.set(POS, np.array([pos_t], np.int32))
+        g.set(IDX, np.array([pos_t], np.int64))
+        KC, VC = g.tensor(gp.F16, [NKV * D, CTX], "c", "kc"), g.tensor(gp.F16, [NKV * D, CTX], "c", "vc")
+        g.set(KC, kc)
+        g.set(VC, vc)
+        k = g.rope(g.reshape_3d(g.mul_mat(T["k"], X), D, NKV, 1), POS, D, 0, 500000.0)
+        g.set_rows(KC, g.view_nd(k, gp.OP_RESHAPE, [NKV * D, 1], [4, NKV * D * 4, NKV * D * 4, NKV * D * 4]), IDX)
+        q = g.rope(g.reshape_3d(g.mul_mat(T["q"], X), D, NH, 1), POS, D, 0, 500000.0)
+        q.data = k.data  # the roped k is dead after its SET_ROWS: gallocr may hand its memory to the roped q
+        v = g.mul_mat(T["v"], X)
+        g.set_rows(VC, v, IDX)
+        plugin.ggml_backend_ameva_reset_counters()
+        assert g.compute() == gp.STATUS_SUCCESS
+        assert gp.counter(plugin, "fused_pair_count") == 0  # no group: q would overwrite k inside one launch
+        assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 3
+
+        def mm(name):
+            return orc.mul_mat(gp.Q4_0, w[name], w[name].shape[0], H, orc.quantize_q8_0(x, orc.Q8_X86), 1)
+        p = np.array([pos_t], np.int32)
+        qr = orc.rope(mm("q").reshape(1, NH, D), p, D, 0, 500000.0)
+        kr = orc.rope(mm("k").reshape(1, NKV, D), p, D, 0, 500000.0)
+        assert rel_l2(g.get(q, np.float32, (1, NH, D)), qr) < 1e-3
+        assert rel_l2(g.get(v, np.float32, (1, NKV * D)), mm("v")) < 1e-3
+        kc_out = g.get(KC, np.float16, (CTX, NKV * D))
+        assert rel_l2(kc_out[pos_t], kr.reshape(-1).astype(np.float16)) < 1e-3
+        assert np.array_equal(np.delete(kc_out, pos_t, axis=0).view(np.uint16),
+                              np.delete(kc, pos_t, axis=0).view(np.uint16))
+        assert rel_l2(g.get(VC, np.float16, (CTX, NKV * D))[pos_t], mm("v").reshape(-1).astype(np.float16)) < 1e-3
     finally:
         g.free()

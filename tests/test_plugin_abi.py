@@ -189,3 +189,44 @@ def test_failure_injection_rejects_from_the_host(libs):
     finally:
         plugin.ggml_backend_ameva_set_failure_injection(0)
     assert h.reason(n) is None
+
+
+def test_host_abi_check_passes_on_a_matching_host(libs):
+    """ggml_backend_init, ggml_backend_ameva_register and ggml_backend_ameva_init check the host's ggml ABI first
+    (ameva_abi_check, ggml-ameva-device.cpp:415-495): on a host whose accessors read the plugin's structs as it lays
+    them out, the check passes and the registry is returned."""
+    _, plugin = libs
+    plugin.ggml_backend_ameva_abi_check.restype = ctypes.c_char_p
+    assert plugin.ggml_backend_ameva_abi_check() is None
+    assert plugin.ggml_backend_init()
+
+
+_SKEWED_LOAD = r"""
+import ctypes, sys
+host = ctypes.CDLL(sys.argv[1], mode=ctypes.RTLD_GLOBAL)
+plugin = ctypes.CDLL(sys.argv[2])
+plugin.ggml_backend_init.restype = ctypes.c_void_p
+plugin.ggml_backend_ameva_abi_check.restype = ctypes.c_char_p
+plugin.ggml_backend_ameva_reg.restype = ctypes.c_void_p
+print("init", plugin.ggml_backend_init() or 0)
+print("why", plugin.ggml_backend_ameva_abi_check().decode())
+"""
+
+
+@pytest.mark.parametrize("skew,what", [(1, "struct ggml_backend"), (2, "GGML_MAX_NAME")])
+def test_host_abi_check_refuses_a_skewed_host(tmp_path, skew, what):
+    """A host built from other ggml headers: one whose ggml_backend_i has one member fewer (it reads the device one
+    slot early), and one built with GGML_MAX_NAME 128. ggml_backend_init returns NULL (llama.cpp's loader then reports
+    the backend as failed) and the reason names the struct. Each host is loaded in a process of its own."""
+    import subprocess
+    import sys
+    so = tmp_path / f"libggml_testhost_skew{skew}.so"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-shared", f"-DGGML_TESTHOST_SKEW={skew}", "-o", str(so), gp.HOST_SRC],
+                   check=True)
+    r = subprocess.run([sys.executable, "-c", _SKEWED_LOAD, str(so), gp.PLUGIN_LIB], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = dict(line.split(" ", 1) for line in r.stdout.splitlines())
+    assert out["init"] == "0"
+    assert "ABI mismatch" in out["why"] and what in out["why"], out["why"]
+    assert "refusing to load" in r.stderr
