@@ -71,6 +71,7 @@ SIGNATURES = {
                                             I32, I32, P]),
     "amv_get_rows": (I32, [I32, P, I64, I64, P, I64, P, P, P]),
     "amv_argmax": (I32, [P, I64, P, P, P, I64, P]),
+    "amv_argmax_ex": (I32, [P, I64, P, P, P, I64, P, P, P, P, P]),
 }
 
 _lib = None

@@ -3,6 +3,8 @@
 // Roles of ameva_binary.comp, ameva_cpy.comp, ameva_set_rows.comp and ameva_get_rows(_q).comp of the reference.
 #include "amv_common.h"
 
+#include <algorithm>
+
 // dst[r][i] = a[r][i] op b[r % b_rows][i]   (op 0 add, 1 mul); n = elements per row
 __global__ __launch_bounds__(256) void k_binary(const float* __restrict__ a, const float* __restrict__ b,
                                                float* __restrict__ dst, int64_t n_rows, int64_t n, int64_t b_rows,
@@ -200,6 +202,88 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
             step[0] = s + 1;
         }
     }
+}
+
+// The argmax spread over the GPU: workgroup b of 256 threads takes float4 chunks [2048 b, 2048 b + 2048) of x (eight
+// loads per thread in flight, one round), reduces them with argmax_take's order, and offers its best as one 64-bit
+// key to an atomic maximum: the high word is the value mapped to an unsigned order (x >= 0: bits | 2^31, x < 0: ~bits;
+// -0 as +0, so equal values meet on equal keys), the low word 2^32 - 1 - index (the smaller index wins a tie); a
+// workgroup with no candidate (NaN only) offers 0. Each workgroup then arrives on a counter (atomicInc wrapping at
+// the grid size, after its maximum has completed); the last to arrive takes the key with an exchange that leaves 0,
+// so ws holds zeros again for the next call, and writes the token (0 when no value was a candidate), the history
+// and, when given, the decode position advanced by one (pos, kv_idx and n_kv each + 1).
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    if (i == 0x7FFFFFFF) return 0ull;
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
+}
+__global__ __launch_bounds__(256) void k_argmax_mw(const float* __restrict__ x, int n, int32_t* __restrict__ token,
+                                                  int32_t* __restrict__ history, int32_t* __restrict__ step,
+                                                  int history_len, int32_t* pos, int64_t* kv_idx, int32_t* n_kv,
+                                                  unsigned long long* ws) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n4 = n / 4, c0 = blockIdx.x * 2048;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = x4[min(c0 + 256 * u + tid, n4 - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int i = c0 + 256 * u + tid;
+        if (i < n4) {
+            argmax_take(bv, bi, v[u].x, 4 * i);
+            argmax_take(bv, bi, v[u].y, 4 * i + 1);
+            argmax_take(bv, bi, v[u].z, 4 * i + 2);
+            argmax_take(bv, bi, v[u].w, 4 * i + 3);
+        }
+    }
+    if (blockIdx.x == gridDim.x - 1)
+        for (int i = 4 * n4 + tid; i < n; i += 256) argmax_take(bv, bi, x[i], i);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) argmax_take(bv, bi, __shfl_xor(bv, o, AMV_WAVE), __shfl_xor(bi, o, AMV_WAVE));
+    if (lane == 0) {
+        sv[wv] = bv;
+        si[wv] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w) argmax_take(bv, bi, sv[w], si[w]);
+        atomicMax(ws, argmax_key(bv, bi));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned int* cnt = reinterpret_cast<unsigned int*>(ws + 1);
+        if (atomicInc(cnt, gridDim.x - 1u) == gridDim.x - 1u) {
+            const unsigned long long k = atomicExch(ws, 0ull);
+            const int t = k == 0ull ? 0 : (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+            token[0] = t;
+            if (history) {
+                const int s = step[0];
+                if (s >= 0 && s < history_len) history[s] = t;
+                step[0] = s + 1;
+            }
+            if (pos) pos[0] += 1;
+            if (kv_idx) kv_idx[0] += 1;
+            if (n_kv) n_kv[0] += 1;
+        }
+    }
+}
+
+extern "C" int amv_argmax_ex(const float* x, int64_t n, int32_t* token, int32_t* history, int32_t* step,
+                             int64_t history_len, int32_t* pos, int64_t* kv_idx, int32_t* n_kv, void* ws,
+                             void* stream) {
+    AMV_REQUIRE(x && token && ws, "amv_argmax_ex: null pointer");
+    AMV_REQUIRE(n > 0 && n <= INT32_MAX - 8192, "amv_argmax_ex: bad length %lld", (long long)n);
+    AMV_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)ws & 15) == 0, "amv_argmax_ex: x and ws must be 16-byte aligned");
+    AMV_REQUIRE(!history || (step && history_len > 0 && history_len <= INT32_MAX),
+                "amv_argmax_ex: history needs step and history_len");
+    const int64_t blocks = std::max<int64_t>(1, (n / 4 + 2047) / 2048);
+    hipLaunchKernelGGL(k_argmax_mw, dim3((unsigned)blocks), dim3(256), 0, amv_stream(stream), x, (int)n, token, history,
+                       step, (int)history_len, pos, kv_idx, n_kv, reinterpret_cast<unsigned long long*>(ws));
+    return amv_check_launch("amv_argmax_ex");
 }
 
 extern "C" int amv_argmax(const float* x, int64_t n, int32_t* token, int32_t* history, int32_t* step,

@@ -44,6 +44,7 @@ class LlamaModel:
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.history = torch.zeros(max_new, dtype=torch.int32, device=dev)
         self.step = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.argmax_ws = torch.zeros(2, dtype=torch.int64, device=dev)  # amv_argmax_ex's 16 bytes, left zero
         self._pf = None
 
     # ---------------------------------------------------------------------------------------------- helpers
@@ -51,16 +52,19 @@ class LlamaModel:
         check(lib().amv_get_rows(self.embd_type, self.tok_embd.data_ptr(), self.vocab, self.H, idx.data_ptr(), n,
                                  out.data_ptr(), None, st), "get_rows (token embedding)")
 
-    def _head(self, x_last: torch.Tensor, st) -> None:
-        """RMS_NORM + MUL of the last hidden state, the head MUL_MAT, the argmax into token / history / step."""
+    def _head(self, x_last: torch.Tensor, st, advance: bool = False) -> None:
+        """RMS_NORM + MUL of the last hidden state, the head MUL_MAT, the argmax into token / history / step; with
+        advance, the same launch moves the decode position (pos, cache row, key count) on by one."""
         L = lib()
         check(L.amv_rms_norm_act(x_last.data_ptr(), 1, self.H, self.eps, self.output_norm.data_ptr(), None,
                                  self.t_out.data_ptr(), self.act_head.data_ptr(), self.hatype, ops.Q8_X86, st),
               "output norm")
         check(L.amv_mul_mat_vec(self.head.type, self.head.data.data_ptr(), self.vocab, self.H,
                                 self.act_head.data_ptr(), 1, self.logits.data_ptr(), self.vocab, st), "output head")
-        check(L.amv_argmax(self.logits.data_ptr(), self.vocab, self.token.data_ptr(), self.history.data_ptr(),
-                           self.step.data_ptr(), self.history.numel(), st), "argmax")
+        adv = (self.pos.data_ptr(), self.kv_idx.data_ptr(), self.n_kv_dev.data_ptr()) if advance else (None,) * 3
+        check(L.amv_argmax_ex(self.logits.data_ptr(), self.vocab, self.token.data_ptr(), self.history.data_ptr(),
+                              self.step.data_ptr(), self.history.numel(), *adv, self.argmax_ws.data_ptr(), st),
+              "argmax")
 
     def set_position(self, pos: int) -> None:
         self.pos.fill_(pos)
@@ -103,8 +107,8 @@ class LlamaModel:
     # ---------------------------------------------------------------------------------------------- decode
     def decode_step(self, fused: bool = True) -> None:
         """One generated token: embeds `token` (the previous sample), runs the layers at the current position,
-        samples the next token into token / history[step], advances the position. Launches only, on the current
-        stream, so it can be captured once and replayed."""
+        samples the next token into token / history[step] and advances the position (in the argmax launch). Launches
+        only, on the current stream, so it can be captured once and replayed."""
         st = torch.cuda.current_stream().cuda_stream
         x, y = self.x
         self._embed(self.token, x, 1, st)
@@ -113,10 +117,7 @@ class LlamaModel:
             nxt = self.layers[i + 1] if fused and i + 1 < nl else None
             lay.decode(x, y, fused=fused, act_ready=fused and i > 0, next_layer=nxt)
             x, y = y, x
-        self._head(x, st)
-        self.pos.add_(1)
-        self.kv_idx.add_(1)
-        self.n_kv_dev.add_(1)
+        self._head(x, st, advance=True)
 
     def decode_bytes(self, n_kv: int) -> int:
         """Algorithmic HBM bytes of one decode step at n_kv cached keys: every weight once, the KV rows, the

@@ -399,6 +399,13 @@ int amv_get_rows(int type, const void* src, int64_t src_rows, int64_t n, const i
  * replayed as a HIP graph keeps its tokens on the device. x 16-byte aligned. */
 int amv_argmax(const float* x, int64_t n, int32_t* token, int32_t* history, int32_t* step, int64_t history_len,
                void* stream);
+/* amv_argmax over the whole GPU (workgroups of 2048 float4 of x; an atomic maximum of (value, index) keys and the last
+ * workgroup to arrive writes the result), and, when pos / kv_idx / n_kv are not NULL, the decode position advanced:
+ * pos[0] += 1, kv_idx[0] += 1, n_kv[0] += 1 -- the end of a decode step in one launch (no counterpart in the
+ * reference, whose sampler runs on the host). ws: 16 bytes, 16-byte aligned, zero before the first call; every call
+ * leaves them zero. Calls that overlap on one ws race. Same token as amv_argmax. */
+int amv_argmax_ex(const float* x, int64_t n, int32_t* token, int32_t* history, int32_t* step, int64_t history_len,
+                  int32_t* pos, int64_t* kv_idx, int32_t* n_kv, void* ws, void* stream);
 
 #ifdef __cplusplus
 }

@@ -72,6 +72,56 @@ def test_argmax(dev, ops):
     assert hist.tolist() == [10, 10, 10] and int(step.item()) == 4
 
 
+def test_argmax_ex_matches_argmax_and_advances(dev, ops):
+    """amv_argmax_ex (every workgroup offers a (value, index) key to an atomic maximum, the last to arrive writes the
+    token) gives amv_argmax's token: random rows, ties within and across workgroups (the first index), NaN never
+    winning, -0 tied with +0, all-NaN and all -inf rows (token 0), lengths not a multiple of 4 or of a workgroup's
+    8192 floats; the decode position (pos, kv_idx, n_kv) moves on by one per call, and ws is left zero."""
+    lib = ops.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    ws = torch.zeros(2, dtype=torch.int64, device=dev)
+    pos = torch.tensor([7], dtype=torch.int32, device=dev)
+    kv = torch.tensor([7], dtype=torch.int64, device=dev)
+    nkv = torch.tensor([8], dtype=torch.int32, device=dev)
+    rng = np.random.default_rng(44)
+    cases = [rng.standard_normal(n).astype(np.float32) for n in (1, 3, 7, 1000, 8191, 8192, 8193, 128256, 128257)]
+    for where in ([100000, 40000, 5], [128255], [40963, 32768 + 4], [8191, 8192], [16383, 16384, 0]):
+        x = np.zeros(128257, np.float32)
+        x[where] = 2.0
+        cases.append(x)
+    x = np.full(20000, -1.0, np.float32)
+    x[[9000, 17000]] = -0.0
+    x[[12000, 3]] = 0.0                # +0 and -0 tie: the first index of either
+    cases.append(x)
+    x = np.zeros(30000, np.float32)
+    x[:] = np.nan
+    x[29999] = -5.0                    # NaN never wins: the only number does
+    cases.append(x)
+    cases.append(np.full(20001, np.nan, np.float32))
+    cases.append(np.full(9000, -np.inf, np.float32))
+    for i, x in enumerate(cases):
+        xg = torch.from_numpy(x).to(dev)
+        want = int(ops.argmax(xg).item())
+        tok = torch.full((1,), -1, dtype=torch.int32, device=dev)
+        rc = lib.amv_argmax_ex(xg.data_ptr(), x.size, tok.data_ptr(), None, None, 0, pos.data_ptr(), kv.data_ptr(),
+                               nkv.data_ptr(), ws.data_ptr(), st)
+        assert rc == 0, lib.amv_last_error()
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want, (i, x.size)
+        assert not ws.any()
+    n = len(cases)
+    assert int(pos.item()) == 7 + n and int(kv.item()) == 7 + n and int(nkv.item()) == 8 + n
+    # history and step as amv_argmax, without the position (NULL pointers)
+    hist = torch.full((2,), -1, dtype=torch.int32, device=dev)
+    step = torch.zeros(1, dtype=torch.int32, device=dev)
+    xg = torch.from_numpy(cases[7]).to(dev)
+    for _ in range(3):
+        assert lib.amv_argmax_ex(xg.data_ptr(), xg.numel(), tok.data_ptr(), hist.data_ptr(), step.data_ptr(), 2, None,
+                                 None, None, ws.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert hist.tolist() == [int(np.argmax(cases[7]))] * 2 and int(step.item()) == 3
+
+
 def tiny_model(dev):
     from ameva_compute_amd.model import random_model
     return random_model(dev, n_layers=2, H=256, n_head=2, n_head_kv=1, D=128, FF=512, vocab=1000, ctx=64, seed=3,
