@@ -792,6 +792,208 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q4k_sb(const uint4* __restrict_
     }
 }
 
+// Small batches (m <= 32) of Q6_K, streamed like k_mmq_sb (k_mmq_q6k_sb): the exact integers of ggml's
+// vec_dot_q6_K_q8_K, I = sum over the 16 sub-blocks s of a super-block of sc_s sum_k q_k a_k (q = 6-bit code - 32,
+// sc_s int8), then dst += (d * d_a) I. A wave owns TI 16-row weight tiles and every token (TJ 16-token tiles); the NW
+// waves of a workgroup take every NW-th super-block and add their f32 partials in LDS in wave order. Roles: A =
+// activations (token l % 16), B = weights (row l % 16), so a lane's 4 outputs are its own weight row (its own scales
+// and d) and tokens 4 g .. 4 g + 3. A v_mfma_i32_16x16x32_i8 covers 32 consecutive elements 32 p .. 32 p + 31 (k slots
+// 8 g .. 8 g + 7 from lane group g): sub-block 2 p in the slots of groups 0 and 1, sub-block 2 p + 1 in those of
+// groups 2 and 3; two MFMAs per pair, each with the other sub-block's activation slots set to zero, give the two
+// sub-block sums apart. Element 32 p + 8 g + b of the super-block is, in ggml's Q6_K layout (half h = p / 4, quarter
+// t = p % 4), the low (t < 2) or high (t >= 2) nibble of ql byte 64 h + 32 (t % 2) + 8 g + b with bits 2 t, 2 t + 1 of qh
+// byte 32 h + 8 g + b above it: each lane loads those 8-byte runs (4 of ql, 2 of qh per super-block) and the 8-byte
+// runs of its token's activation row, and builds q - 32 as signed bytes (flip bit 5 of the 6-bit code, copy it into
+// bits 6 and 7). The loads of the next super-block are in flight while one computes. Reads the plain Q8_K layout (the
+// prefix of AMV_ACT_Q8_K_MMA too).
+template <int TI, int TJ, int NW, bool SUMS>
+__global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restrict__ wl, const uint8_t* __restrict__ wqh,
+                                                       const sb_v4u* __restrict__ wsc, const uint16_t* __restrict__ wd,
+                                                       int N, int nsb, const int8_t* __restrict__ aq,
+                                                       const float* __restrict__ ad, int M, float* __restrict__ dst,
+                                                       int64_t ldd, int32_t* __restrict__ sums) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16 * TI;
+    const size_t K = (size_t)nsb * 256;
+    const uint8_t* lr[TI];
+    const uint8_t* hr[TI];
+    size_t rb[TI];  // row * nsb
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const size_t row = (size_t)min(n0 + 16 * i + r16, N - 1);
+        rb[i] = row * nsb;
+        lr[i] = wl + rb[i] * 128 + 8 * g;
+        hr[i] = wqh + rb[i] * 64 + 8 * g;
+    }
+    const int8_t* ar[TJ];
+    const float* dr[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const size_t t = (size_t)min(16 * j + r16, M - 1);
+        ar[j] = aq + t * K + 8 * g;
+        dr[j] = ad + t * nsb;
+    }
+    float acc[TI][TJ][4];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
+
+    sb_v2u lq[2][TI][4], lh[2][TI][2], la[2][TJ][8];
+    sb_v4u ls[2][TI];
+    uint32_t ldw[2][TI];
+    float lda[2][TJ];
+    const auto load = [&](int s, int sb) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                lq[s][i][c] = __builtin_nontemporal_load(reinterpret_cast<const sb_v2u*>(lr[i] + (size_t)sb * 128 + 32 * c));
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                lh[s][i][c] = __builtin_nontemporal_load(reinterpret_cast<const sb_v2u*>(hr[i] + (size_t)sb * 64 + 32 * c));
+            ls[s][i] = wsc[rb[i] + sb];
+            ldw[s][i] = wd[rb[i] + sb];
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p) la[s][j][p] = *reinterpret_cast<const sb_v2u*>(ar[j] + (size_t)sb * 256 + 32 * p);
+            lda[s][j] = dr[j][sb];
+        }
+    };
+    const auto compute = [&](int s, int sb) {
+        // the activation scales of the lane's output tokens 16 j + 4 g + e, held by lanes 4 g + e (token r16's)
+        float da[TJ][4];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) da[j][e] = __shfl(lda[s][j], 4 * g + e, AMV_WAVE);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            int I[TJ][4];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) I[j][e] = 0;
+            const uint32_t scw[4] = {ls[s][i].x, ls[s][i].y, ls[s][i].z, ls[s][i].w};
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const int h = p >> 2, t = p & 3;
+                const sb_v2u qlv = lq[s][i][2 * h + (t & 1)], qhv = lh[s][i][h];
+                uint32_t x[2];
+#pragma unroll
+                for (int d2 = 0; d2 < 2; ++d2) {
+                    const uint32_t lo = ((t >= 2 ? qlv[d2] >> 4 : qlv[d2]) & 0x0F0F0F0Fu) |
+                                        (((qhv[d2] >> (2 * t)) & 0x03030303u) << 4);
+                    const uint32_t f = lo ^ 0x20202020u;  // 6-bit code - 32: bit 5 flipped, then copied up
+                    const uint32_t m5 = f & 0x20202020u;
+                    x[d2] = f | (m5 << 2) | (m5 << 1);
+                }
+                const long B = (long)(((uint64_t)x[1] << 32) | x[0]);
+                const int sa = (int)(int8_t)(scw[p >> 1] >> (16 * (p & 1)));       // sc[2 p]
+                const int sb2 = (int)(int8_t)(scw[p >> 1] >> (16 * (p & 1) + 8));  // sc[2 p + 1]
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const long A = (long)(((uint64_t)la[s][j][p][1] << 32) | la[s][j][p][0]);
+                    const long Aa = g < 2 ? A : 0L, Ab = g < 2 ? 0L : A;
+                    const v4i zero = {0, 0, 0, 0};
+                    const v4i Ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(Aa, B, zero, 0, 0, 0);
+                    const v4i Cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(Ab, B, zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) I[j][e] += sa * Ca[e] + sb2 * Cb[e];
+                }
+            }
+            const float d = amv_h2f((uint16_t)ldw[s][i]);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (SUMS) {
+                        const int tok = 16 * j + 4 * g + e, n = n0 + 16 * i + r16;
+                        if (tok < M && n < N) sums[((size_t)tok * N + n) * nsb + sb] = I[j][e];
+                    } else {
+                        acc[i][j][e] = fmaf(d * da[j][e], (float)I[j][e], acc[i][j][e]);
+                    }
+                }
+        }
+    };
+    int sb = w;
+    if (sb < nsb) load(0, sb);
+    for (; sb < nsb; sb += 2 * NW) {
+        if (sb + NW < nsb) load(1, sb + NW);
+        compute(0, sb);
+        if (sb + NW >= nsb) break;
+        if (sb + 2 * NW < nsb) load(0, sb + 2 * NW);
+        compute(1, sb + NW);
+    }
+    if constexpr (!SUMS) {
+        __shared__ float red[NW - 1][TI * TJ * 4][64];
+        if (w > 0) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) red[w - 1][(i * TJ + j) * 4 + e][lane] = acc[i][j][e];
+        }
+        __syncthreads();
+        if (w > 0) return;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int x = (i * TJ + j) * 4 + e;
+                    float v = acc[i][j][e];
+#pragma unroll
+                    for (int o = 0; o < NW - 1; ++o) v += red[o][x][lane];  // wave order
+                    const int tok = 16 * j + 4 * g + e, n = n0 + 16 * i + r16;
+                    if (tok < M && n < N) dst[(size_t)tok * ldd + n] = v;
+                }
+    }
+}
+
+// Q6_K batches of m <= 32 tokens (plain Q8_K activations or the Q8_K prefix of AMV_ACT_Q8_K_MMA): two 16-row tiles
+// per wave and 4 waves while that leaves >= 256 workgroups, else one tile and 8 waves splitting the super-blocks
+static int mmq_q6k_sb(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
+                      int32_t* sums, hipStream_t st) {
+    AMV_REQUIRE(k % 256 == 0, "amv_mul_mat_q: Q6_K needs k %% 256 == 0");
+    AMV_REQUIRE(m >= 1 && m <= 32, "amv_mul_mat_q: the small-batch Q6_K kernel takes 1..32 tokens");
+    const int nsb = (int)(k / 256);
+    const int64_t nblk = n_rows * nsb;
+    const uint8_t* base = (const uint8_t*)w;
+    const uint8_t* wl = base;
+    const uint8_t* wqh = base + nblk * 128;
+    const sb_v4u* wsc = (const sb_v4u*)(base + nblk * 192);
+    const uint16_t* wd = (const uint16_t*)(base + nblk * 208);
+    const int8_t* aq = (const int8_t*)act;
+    const float* ad = (const float*)((const uint8_t*)act + m * k);
+    const bool two = (n_rows + 31) / 32 >= 256;
+#define Q6K_SB(TI, TJ, NW)                                                                                          \
+    do {                                                                                                             \
+        const dim3 G((unsigned)((n_rows + 16 * TI - 1) / (16 * TI)));                                              \
+        if (sums) hipLaunchKernelGGL((k_mmq_q6k_sb<TI, TJ, NW, true>), G, dim3(64 * NW), 0, st, wl, wqh, wsc, wd,   \
+                                     (int)n_rows, nsb, aq, ad, (int)m, dst, ldd, sums);                              \
+        else hipLaunchKernelGGL((k_mmq_q6k_sb<TI, TJ, NW, false>), G, dim3(64 * NW), 0, st, wl, wqh, wsc, wd,       \
+                                (int)n_rows, nsb, aq, ad, (int)m, dst, ldd, sums);                                   \
+    } while (0)
+    // measured on MI355X (14336 x 4096 and 4096 x 14336 at 16 and 32 tokens): 8 or 16 waves per workgroup, or one
+    // tile per wave where two fit, were all slower (M = 16: 32-56 against 29.5-31.8 us)
+    if (m <= 16) {
+        if (two) Q6K_SB(2, 1, 4);
+        else Q6K_SB(1, 1, 8);
+    } else {
+        if (two) Q6K_SB(2, 2, 4);
+        else Q6K_SB(1, 2, 4);  // 8 waves of this tile would spill registers
+    }
+#undef Q6K_SB
+    return amv_check_launch("amv_mul_mat_q");
+}
+
 static int mmq_q4k(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
                    int32_t* sums, hipStream_t st) {
     AMV_REQUIRE(k % 256 == 0, "amv_mul_mat_q: Q4_K needs k %% 256 == 0");
@@ -855,6 +1057,8 @@ static int mmq_impl(int wtype, const void* w, int64_t n_rows, int64_t k, const v
     AMV_REQUIRE(n_rows <= INT32_MAX && m <= 65535LL * 32 && n_rows * (k / 32) <= INT32_MAX, "amv_mul_mat_q: too large");
     AMV_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)act & 15) == 0, "amv_mul_mat_q: buffers must be 16-byte aligned");
     AMV_REQUIRE(!dst || ldd >= n_rows, "amv_mul_mat_q: ldd < n_rows");
+    // Q6_K up to 32 tokens: the streamed small-batch kernel (the plain Q8_K prefix of either layout)
+    if (wtype == AMV_T_Q6_K && m <= 32) return mmq_q6k_sb(w, n_rows, k, act, m, dst, ldd, sums, amv_stream(stream));
     // the tiled int8 kernel reads the plain prefix of any layout
     if (m > MMQ16_MIN_M || wtype == AMV_T_Q6_K || (wtype == AMV_T_Q4_K && !q4k_mma)) {
         AMV_REQUIRE((wtype != AMV_T_Q4_K && wtype != AMV_T_Q6_K) || k % 256 == 0,
@@ -903,10 +1107,10 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
     const bool deq = act_type == AMV_ACT_Q8_0_DEQ || act_type == AMV_ACT_Q8_K_DEQ;
     const bool q80x = act_type == AMV_ACT_Q8_0_MMA || act_type == AMV_ACT_Q8_0_DEQ;
     const bool q8kx = act_type == AMV_ACT_Q8_K_MMA || act_type == AMV_ACT_Q8_K_DEQ;
-    // Q6_K batches of any size run the tiled int8 kernel (there is no small-batch Q6_K kernel)
+    // Q6_K batches above 32 tokens run the tiled int8 kernel (up to 32 the streamed k_mmq_q6k_sb)
     const bool tiled = (m > MMQ16_MIN_M && (((q80x || act_type == AMV_T_Q8_0) && (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)) ||
                                             ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q4_K))) ||
-                       ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q6_K);
+                       ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q6_K && m > 32);
     if (add && !(tiled && !deq)) {  // only the exact tiled kernels add the residual in their epilogue
         int rc = mmq_act_impl(fn, wtype, w, n_rows, k, act, act_type, m, dst, ldd, nullptr, stream);
         if (rc) return rc;
@@ -933,8 +1137,10 @@ static int mmq_act_impl(const char* fn, int wtype, const void* w, int64_t n_rows
     // a plain Q8_K activation of a Q4_K batch this small goes to the tiled int8 kernel (mmq_impl with q4k_mma false):
     // the small-batch Q4_K kernels read the f16 copies that only AMV_ACT_Q8_K_MMA holds
     const bool ok = (act_type == AMV_T_Q8_0 || q80x) ? (wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0)
-                                                     : ((q8kx || act_type == AMV_T_Q8_K) && wtype == AMV_T_Q4_K);
+                                                     : ((q8kx || act_type == AMV_T_Q8_K) &&
+                                                        (wtype == AMV_T_Q4_K || wtype == AMV_T_Q6_K));
     AMV_REQUIRE(ok, "%s: activation type %d does not feed weight type %d", fn, act_type, wtype);
+    AMV_REQUIRE(!(deq && wtype == AMV_T_Q6_K), "%s: Q6_K has no scaled form (use Q8_K or AMV_ACT_Q8_K_MMA)", fn);
     // the small-batch Q4_K kernel reads the f16 copies as exact integers
     AMV_REQUIRE(!(deq && wtype == AMV_T_Q4_K), "%s: Q4_K batches of m <= %d need the exact layout AMV_ACT_Q8_K_MMA",
                 fn, MMQ16_MIN_M);

@@ -288,3 +288,42 @@ def test_mul_mat_q_add(dev, ops, orc, wtype, atype, m, n, k):
     assert torch.equal(got, y + res)
     with pytest.raises(Exception, match="overlaps"):
         ops.mul_mat_q_add(w, act, m, got, act_t=at, out=got)
+
+
+def random_q6k(rng, n, k):
+    """Random bytes are valid Q6_K blocks once the fp16 d is a small finite value (codes, int8 sub-block scales and
+    high bits then take every value)."""
+    y = rng.integers(0, 256, (n, k // 256, 210), dtype=np.uint8)
+    v = rng.uniform(0.0, 0.002, (n, k // 256)).astype(np.float16)
+    y[:, :, 208:210] = v.view(np.uint8).reshape(n, k // 256, 2)
+    return y.reshape(n, -1)
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 64, 256), (16, 300, 1024), (17, 129, 512), (32, 512, 4096), (24, 33, 256),
+                                   (1, 70, 512), (16, 8192, 1024), (32, 100, 2048)])
+@pytest.mark.parametrize("atype", ["Q8_K", "Q8_K_MMA"])
+def test_mmq_q6k_small_batch(dev, ops, orc, m, n, k, atype):
+    """The streamed small-batch Q6_K kernel (k_mmq_q6k_sb, m <= 32; sub-block sums from v_mfma_i32_16x16x32_i8 with
+    the other sub-block's activation slots zeroed): each super-block's integer I = sum_s sc_s sum q a bit-exact against
+    the oracle, every output within the per-output gate, on both activation layouts; ragged rows and tokens, one or
+    two 16-row tiles per wave, one or two token tiles."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    wg = random_q6k(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0, :100] *= 30.0  # |q| = 127 in whole sub-blocks
+    a_ref = orc.quantize_q8_K(x)
+    y_ref, s_ref = orc.mul_mat(ops.Q6_K, wg, n, k, a_ref, m, with_blocks=True)
+    w = ops.QWeight.from_ggml(ops.Q6_K, gpu(wg, dev), n, k)
+    at = getattr(ops, atype)
+    act, ag = ops.quantize_act(gpu(x, dev), at, ggml=True)
+    assert np.array_equal(ag.cpu().numpy(), a_ref)
+    sums = torch.empty(m * n * (k // 256), dtype=torch.int32, device=dev)
+    rc = ops.lib().amv_mul_mat_q_act_block_sums(ops.Q6_K, w.data.data_ptr(), n, k, act.data_ptr(), at, m,
+                                                sums.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ops.lib().amv_last_error()
+    assert np.array_equal(sums.cpu().numpy().reshape(s_ref.shape), s_ref)
+    y = ops.mul_mat_q(w, act, m, kernel="mmq", act_t=at).cpu().numpy()
+    assert rel_l2(y, y_ref) < TOL_F32
+    per_output_gate(y, orc.dequantize(ops.Q6_K, wg, k), dequant_act(a_ref, 15, k), what=f"Q6_K m={m} {n}x{k}")
+    res = gpu(rng.standard_normal((m, n)).astype(np.float32), dev)  # the residual form: a second launch adds it
+    assert torch.equal(ops.mul_mat_q_add(w, act, m, res, act_t=at), torch.from_numpy(y).to(dev) + res)
