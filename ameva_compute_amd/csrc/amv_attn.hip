@@ -419,6 +419,166 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
     }
 }
 
+// Pass 1 for an f16 cache with q . k on the matrix cores (16 keys per wave, as k_fa_split<G, 16, FUSED, FA_F16>, same
+// splits and partials): S = K q^T of the wave's 16 keys and the G heads is four v_mfma_f32_16x16x32_f16 over the 128
+// dims (A: key l % 16, dims 32 kk + 8 (l / 16) .. + 7 of its row, loaded as 16 bytes; B: q of head l % 16 rounded to
+// f16, zero columns from G on), so the f16 products are exact and summed in f32 as the dot2 form sums them (in another
+// order). The result gives lane l the scores of keys 4 (l / 16) + e of head l % 16: the maximum and the sum over the
+// 16 keys of a head are over its 4 values and the lane pairs l ^ 16, l ^ 32. The probabilities reach the P V layout
+// of k_fa_split (lane group g: keys 4 u + g, 8 dims per lane) through 16 x G floats of LDS per wave; P V, the merge of
+// the 4 wave partials and the split merge are k_fa_split's.
+typedef _Float16 fa_h8 __attribute__((ext_vector_type(8)));
+typedef float fa_f4 __attribute__((ext_vector_type(4)));
+
+template <int G, bool FUSED>
+__global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q, const uint8_t* __restrict__ k,
+                                                    const uint8_t* __restrict__ v, const uint16_t* __restrict__ mask,
+                                                    float* part, int n_kv_max, const int* __restrict__ n_kv_dev,
+                                                    int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
+                                                    int n_split, float scale, unsigned int* counters,
+                                                    float* __restrict__ out, const AmvActOut act) {
+    constexpr int KPW = 16, U = 4;
+    constexpr int SBUF = 4 * 4 * G * FA_D > G * (8 * FA_D + FA_MAX_NSPLIT + 1) ? 4 * 4 * G * FA_D
+                                                                              : G * (8 * FA_D + FA_MAX_NSPLIT + 1);
+    __shared__ __align__(16) float sbuf[SBUF];  // [wave][lane group][head][dim] partial P V; then the merge
+    __shared__ float sM[4][G], sL[4][G];
+    __shared__ float sP[4][KPW][G];  // per wave: probability of key, head
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int grp = lane >> 4, c16 = lane & 15, d8 = 8 * c16;
+    int n_kv = n_kv_max;
+    if (n_kv_dev) n_kv = max(0, min(*n_kv_dev, n_kv_max));
+    const int ns = (n_kv + 4 * KPW - 1) / (4 * KPW);  // splits holding keys
+
+    if (split < ns) {
+        const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
+        const uint8_t* kh = k + (size_t)hk * k_head;
+        const uint8_t* vh = v + (size_t)hk * v_head;
+        // K as the A operand: lane (grp, c16) takes key kw0 + c16, bytes 64 kk + 16 grp (an instruction covers half of
+        // each of 16 rows' lines: ordinary loads, so the second half meets the line in L2)
+        uint4 kr[4];
+        const int ik = min(kw0 + c16, n_kv - 1);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            kr[kk] = *reinterpret_cast<const uint4*>(kh + (size_t)ik * k_row + 64 * kk + 16 * grp);
+        // V in k_fa_split's layout: lane (grp, c16) takes key kw0 + 4 u + grp, dims 8 c16 .. + 7 (whole 256-byte rows
+        // per 16 lanes: streamed)
+        uint4 vr[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = min(kw0 + 4 * u + grp, n_kv - 1);
+            vr[u] = amv_ld_stream(reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + 16 * c16));
+        }
+        // q as the B operand: head c16 (columns from G on are zero), dims 32 kk + 8 grp .. + 7, rounded to f16
+        fa_h8 qb[4];
+        {
+            const float* qp = q + (size_t)(hk * G + min(c16, G - 1)) * FA_D + 8 * grp;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float4 a = *reinterpret_cast<const float4*>(qp + 32 * kk);
+                const float4 b = *reinterpret_cast<const float4*>(qp + 32 * kk + 4);
+                const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qb[kk][e] = c16 < G ? (_Float16)t[e] : (_Float16)0.0f;
+            }
+        }
+        fa_f4 S = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) S = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(fa_h8, kr[kk]),
+                                                                                 qb[kk], S, 0, 0, 0);
+        // lane (grp, c16): keys kw0 + 4 grp + e of head c16, in log2 units
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = kw0 + 4 * grp + e;
+            const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
+            sc[e] = (mk == -INFINITY) ? -INFINITY : (S[e] * scale + mk) * AMV_LOG2E;
+        }
+        float mm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mm = amv_max_x32(amv_max_x16(mm));
+        float ll = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sc[e] = __builtin_amdgcn_exp2f(sc[e] - (mm == -INFINITY ? 0.0f : mm));
+            ll += sc[e];
+        }
+        ll = amv_sum_x32(amv_sum_x16(ll));
+        if (c16 < G) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sP[wv][4 * grp + e][c16] = sc[e];
+            if (grp == 0) {
+                sM[wv][c16] = mm;
+                sL[wv][c16] = ll;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float acc[G][8];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float vf[8];
+            const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
+                vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = sP[wv][4 * u + grp][g];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+            }
+        }
+        // the 4 lane groups of a wave share the wave's maximum, so their accumulators add; the sum is taken below
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float4* dst = reinterpret_cast<float4*>(sbuf + ((wv * 4 + grp) * G + g) * FA_D + d8);
+            dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+            dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+        }
+        __syncthreads();
+        // merge the 4 wave partials of this workgroup
+        for (int e = tid; e < G * FA_D; e += 256) {
+            const int g = e / FA_D, d = e % FA_D;
+            const float M = fmaxf(fmaxf(sM[0][g], sM[1][g]), fmaxf(sM[2][g], sM[3][g]));
+            float a = 0.0f, L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = (sM[w][g] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sM[w][g] - M);
+                const float* sa = sbuf + ((w * 4) * G + g) * FA_D + d;
+                const float aw = (sa[0] + sa[G * FA_D]) + (sa[2 * G * FA_D] + sa[3 * G * FA_D]);
+                a = fmaf(aw, f, a);
+                L = fmaf(sL[w][g], f, L);
+            }
+            float* pp = part + ((size_t)(hk * G + g) * n_split + split) * FA_PS;
+            if constexpr (FUSED) {  // handed over to the merging workgroup within the launch
+                amv_store_coh(pp + 4 + d, a);
+                if (d == 0) {
+                    amv_store_coh(pp, M);
+                    amv_store_coh(pp + 1, L);
+                }
+            } else {
+                pp[4 + d] = a;
+                if (d == 0) {
+                    pp[0] = M;
+                    pp[1] = L;
+                }
+            }
+        }
+    }
+    if constexpr (FUSED) {
+        if (!amv_arrive_last(counters + AMV_CNT_STRIDE * hk, gridDim.x)) return;
+        amv_acquire();
+        fa_merge<G>(part, n_split, ns, hk, out, act, sbuf);
+    }
+}
+
 // The merge as its own launch: one workgroup per GH heads (GH = 1, or 2 for Q8_K output blocks of 256), the key
 // count from n_kv_dev when given, as in k_fa_split.
 template <int GH>
@@ -490,8 +650,12 @@ static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const flo
 #define FA_LAUNCH(GG, KK)                                                                                              \
     hipLaunchKernelGGL((k_fa_split<GG, KK, FUSED, KT>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev, \
                        k_row, k_head, v_row, v_head, n_split, scale, rule, counters, out, act)
-#define FA_G(GG)                     \
-    if (kpw == 16) FA_LAUNCH(GG, 16); \
+#define FA_MF(GG)                                                                                                   \
+    hipLaunchKernelGGL((k_fa_split_mf<GG, FUSED>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev, k_row, \
+                       k_head, v_row, v_head, n_split, scale, counters, out, act)
+#define FA_G(GG)                                  \
+    if (KT == FA_F16 && kpw == 16) FA_MF(GG);      \
+    else if (kpw == 16) FA_LAUNCH(GG, 16);         \
     else FA_LAUNCH(GG, 32)
     switch (G) {
     case 1: FA_G(1); break;
@@ -500,6 +664,7 @@ static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const flo
     default: FA_G(8); break;
     }
 #undef FA_G
+#undef FA_MF
 #undef FA_LAUNCH
 }
 
