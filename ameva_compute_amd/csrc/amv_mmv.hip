@@ -398,6 +398,61 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096(const uint4* __restrict_
     if (live && lane < 2) dst[row0 + lane] = lane ? t1 : t0;
 }
 
+// Measurement instrumentation (amv_debug_gemv_read_probe): k_mmv_q4_0_k4096's grid, wave-to-row mapping and weight /
+// scale loads (non-temporal, all issued first), without the activation loads and the dot products: each wave folds
+// its weight bits with XOR and writes one word per row, so no load is dropped. The time of this kernel is the read
+// ceiling of the mapping the headline GEMV streams with. LOAD = false keeps the grid and the stores and drops the
+// loads: the fixed cost of launching and draining that grid.
+template <bool LOAD>
+__global__ __launch_bounds__(256) void k_gemv_read_probe(const uint4* __restrict__ wq, const uint32_t* __restrict__ wd2,
+                                                        int n_rows, uint32_t* __restrict__ dst) {
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6;
+    const int row0 = min((int)(blockIdx.x * 4 + wi) * 2, n_rows - 2);
+    const bool live = (int)(blockIdx.x * 4 + wi) * 2 < n_rows;
+    if constexpr (!LOAD) {
+        if (live && lane < 2) dst[row0 + lane] = (uint32_t)(row0 + lane);
+        return;
+    }
+    uint4 w[2][2];
+    uint32_t dw[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = 64 * u + lane;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) w[u][r] = amv_ld_stream(wq + (size_t)(row0 + r) * 128 + j);
+        dw[u] = amv_ld_stream(wd2 + (size_t)(row0 >> 1) * 128 + j);
+    }
+    uint32_t x[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        x[r] = dw[0] ^ dw[1];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) x[r] ^= w[u][r].x ^ w[u][r].y ^ w[u][r].z ^ w[u][r].w;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x[r] ^= (uint32_t)__shfl_xor((int)x[r], o, AMV_WAVE);
+    }
+    if (live && lane < 2) dst[row0 + lane] = lane ? x[1] : x[0];
+}
+
+extern "C" int amv_debug_gemv_read_probe(const void* w, int64_t n_rows, int64_t k, uint32_t* dst, int loads,
+                                         void* stream) {
+    AMV_REQUIRE(w && dst, "amv_debug_gemv_read_probe: null pointer");
+    AMV_REQUIRE(loads == 0 || loads == 1, "amv_debug_gemv_read_probe: loads must be 0 or 1");
+    AMV_REQUIRE(k == 4096 && n_rows >= 2 && n_rows % 2 == 0 && n_rows <= (1 << 24),
+                "amv_debug_gemv_read_probe: the headline kernel's shapes (k = 4096, even n_rows)");
+    AMV_REQUIRE(((uintptr_t)w & 15) == 0, "amv_debug_gemv_read_probe: w must be 16-byte aligned");
+    const uint4* wq = reinterpret_cast<const uint4*>(w);
+    const uint32_t* wd2 = reinterpret_cast<const uint32_t*>((const uint8_t*)w + (size_t)n_rows * 128 * 16);
+    const int waves = (int)(n_rows / 2);
+    if (loads)
+        hipLaunchKernelGGL(k_gemv_read_probe<true>, dim3((waves + 3) / 4), dim3(256), 0, amv_stream(stream), wq, wd2,
+                           (int)n_rows, dst);
+    else
+        hipLaunchKernelGGL(k_gemv_read_probe<false>, dim3((waves + 3) / 4), dim3(256), 0, amv_stream(stream), wq, wd2,
+                           (int)n_rows, dst);
+    return amv_check_launch("amv_debug_gemv_read_probe");
+}
+
 // The stacked gate|up GEMV at K = 4096 with SWIGLU and the Q8 tail (EP 7) in the same lean form: two outputs per
 // wave, rows o, o + 1 (gate) and F + o, F + o + 1 (up) with o = 2 wave, the scales of each row pair in one dword, every
 // load of the wave issued before its arithmetic; the per-lane sums in the order of k_mmv_q4_0 (same bits). Measured on

@@ -567,8 +567,9 @@ def copy_ceiling(torch, dev, nbytes):
 
 def pmc_probe(ops, torch, dev):
     """Dispatches for the HBM-traffic counters: the headline GEMV, eager (one dispatch each) over the rotating cold
-    weights, and torch's copy kernel moving a float32 tensor of the GEMV's weight byte count, whose FETCH_SIZE and
-    WRITE_SIZE must read that byte count (the scale of the counters)."""
+    weights, the read-only probe of its mapping over the same weights, and torch's copy kernel moving a float32
+    tensor of the GEMV's weight byte count, whose FETCH_SIZE and WRITE_SIZE must read that byte count (the scale of
+    the counters)."""
     ws = make_weights(ops, torch, N_ROWS, K, COPIES, 42, dev, ops.Q4_0)
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -577,6 +578,12 @@ def pmc_probe(ops, torch, dev):
     out = torch.empty((1, N_ROWS), dtype=torch.float32, device=dev)
     for i in range(50):
         ops.mul_mat_q(ws[i % COPIES], act, 1, out)
+    torch.cuda.synchronize()
+    from ameva_compute_amd._lib import check, lib as _lib
+    probe_out = torch.empty(N_ROWS, dtype=torch.int32, device=dev)
+    for i in range(50):  # the read-only probe of the same mapping (k_gemv_read_probe<true>)
+        check(_lib().amv_debug_gemv_read_probe(ws[i % COPIES].data.data_ptr(), N_ROWS, K, probe_out.data_ptr(), 1,
+                                               torch.cuda.current_stream().cuda_stream), "read probe")
     torch.cuda.synchronize()
     wbytes = ws[0].nbytes
     del ws
@@ -587,14 +594,14 @@ def pmc_probe(ops, torch, dev):
     for i in range(50):
         dst.copy_(srcs[i % COPIES])
     torch.cuda.synchronize()
-    print(json.dumps({"gemv_dispatches": 50, "gemv_algorithmic_bytes": gemv_bytes(N_ROWS, K),
+    print(json.dumps({"gemv_dispatches": 50, "gemv_algorithmic_bytes": gemv_bytes(N_ROWS, K), "probe_dispatches": 50,
                       "copy_dispatches": 50, "copy_bytes_each_way": n * 4}), flush=True)
 
 
 def pmc_gemm(ops, torch, dev):
     """Dispatches for the matrix-core counters: the default (exact, int8 MFMA) batched Q4_K MUL_MAT at M = 512 on the
     Llama-3-8B FFN shapes (14336 x 4096, then 4096 x 14336, whose k is split: its launch is followed by
-    k_splitk_sum), 20 eager launches each over one weight."""
+    k_splitk_sum), 20 eager launches each over one weight, then 20 plain copies of known size (the counters' scale)."""
     res = {}
     g = torch.Generator(device=dev)
     for n, k in ((14336, 4096), (4096, 14336)):
@@ -609,6 +616,13 @@ def pmc_gemm(ops, torch, dev):
         torch.cuda.synchronize()
         res[f"q4_K_{n}x{k}_m512"] = {"dispatches": 20, "ops_each": 2 * 512 * n * k}
         del w
+    # the scale of FETCH_SIZE / WRITE_SIZE: 20 plain copies of a float32 tensor of the Q4_K weight's byte count
+    n_f = 14336 * 4096 // 256 * 144 // 4
+    src, dst = torch.randn(n_f, device=dev), torch.empty(n_f, device=dev)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    res["copy"] = {"dispatches": 20, "bytes_each_way": n_f * 4}
     print(json.dumps(res), flush=True)
 
 
@@ -869,6 +883,33 @@ def main():
     gbs = nbytes / (ms_cold * 1e-3) / 1e9
     log(f"bench: cold {ms_cold * 1e3:.2f} us/GEMV = {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
     extra = {}
+    # the read ceiling of the headline kernel's mapping: the same grid and weight / scale loads over the same cold
+    # copies, without the activation and the arithmetic (amv_debug_gemv_read_probe)
+    from ameva_compute_amd._lib import check, lib as _lib
+    probe_out = torch.empty(N_ROWS, dtype=torch.int32, device=dev)
+
+    def probe(w_ptr, n_rows, loads):
+        check(_lib().amv_debug_gemv_read_probe(w_ptr, n_rows, K, probe_out.data_ptr(), loads,
+                                               torch.cuda.current_stream().cuda_stream), "read probe")
+    ms_probe = time_steps_graph(torch, lambda i: probe(ws[i % COPIES].data.data_ptr(), N_ROWS, 1), args.steps,
+                                args.warmup, min_reps=10, median=True)
+    ms_floor = time_steps_graph(torch, lambda i: probe(ws[i % COPIES].data.data_ptr(), N_ROWS, 0), args.steps,
+                                args.warmup, min_reps=10, median=True)
+    extra["gemv_read_probe_cold_us"] = round(ms_probe * 1e3, 3)
+    extra["gemv_read_probe_cold_gbs"] = round(ws[0].nbytes / (ms_probe * 1e-3) / 1e9, 1)
+    extra["gemv_grid_launch_floor_us"] = round(ms_floor * 1e3, 3)
+    # the same mapping over 2 GiB (932,066 rows of 2304 bytes): its streaming rate with the fixed cost amortised
+    big_rows = (2 << 30) // 2304 // 2 * 2
+    big = torch.empty(big_rows * 2304, dtype=torch.uint8, device=dev)
+    big_out = torch.empty(big_rows, dtype=torch.int32, device=dev)
+    ms_big = time_steps_graph(torch, lambda i: check(_lib().amv_debug_gemv_read_probe(
+        big.data_ptr(), big_rows, K, big_out.data_ptr(), 1, torch.cuda.current_stream().cuda_stream), "read probe"),
+        20, 3, min_reps=10, median=True)
+    extra["gemv_read_probe_2gib_gbs"] = round(big.numel() / (ms_big * 1e-3) / 1e9, 1)
+    del big, big_out
+    log(f"bench: read probe of the same mapping {ms_probe * 1e3:.2f} us (weights only: "
+        f"{ws[0].nbytes / (ms_probe * 1e-3) / 1e9:.0f} GB/s); the grid without loads {ms_floor * 1e3:.2f} us; "
+        f"the mapping over 2 GiB {extra['gemv_read_probe_2gib_gbs']:.0f} GB/s")
     if not args.only_headline:
         ms_hot = time_steps_graph(torch, step_hot, args.steps, args.warmup)
         extra["hot_gbs"] = round(nbytes / (ms_hot * 1e-3) / 1e9, 1)
@@ -877,7 +918,6 @@ def main():
         extra["cold_eager_launch_us"] = round(ms_eager * 1e3, 3)
 
         act2 = torch.empty_like(act)
-        from ameva_compute_amd._lib import lib as _lib
 
         def step_quant(i):
             _lib().amv_quantize_act(ops.Q8_0, x.data_ptr(), 1, K, ops.Q8_X86, None, act2.data_ptr(),

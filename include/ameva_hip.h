@@ -100,6 +100,12 @@ int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t k, const v
  * that kernel's arithmetic and summation order, so a test compares their f32 results bit for bit. Returns the
  * previous setting. Not for production calls: the generic kernels are slower. */
 int amv_debug_gemv_generic(int on);
+/* Measurement instrumentation (no counterpart in the reference; for bench.py and profiles): the headline kernel's grid,
+ * row mapping and weight / scale loads for a Q4_0 weight of n_rows x 4096 (n_rows even), without the activation and
+ * the arithmetic; dst gets one XOR fold of the weight words per row. Its time is the read ceiling of that mapping.
+ * loads = 0 launches the same grid without the loads (dst[r] = r): the fixed cost of launching and draining it. w
+ * needs n_rows x 2304 readable bytes; its contents do not matter. */
+int amv_debug_gemv_read_probe(const void* w, int64_t n_rows, int64_t k, uint32_t* dst, int loads, void* stream);
 
 /* One-column GEMV with the fused epilogue of the next graph node: the reference's ameva_qmv / ameva_mmvq ep_mode
  * (ameva_qmv.comp:233-246) chosen by ameva_find_fusion (ggml-ameva.cpp:4280-4285, 4355-4375). v[n] is the dot

@@ -162,3 +162,24 @@ def test_rope_kv_kernels_equal_generic(dev, ops, orc):
         assert torch.equal(k1.view(torch.int16), k2.view(torch.int16))
         assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
     assert torch.equal(lean[0][0], lean[1][0])
+
+
+@pytest.mark.parametrize("n", [1024, 2, 14336])
+def test_read_probe_reads_every_weight_word(dev, ops, n):
+    """amv_debug_gemv_read_probe (the bench's read ceiling of the headline mapping) folds every quant word of a row
+    and every scale word of its row pair; with loads = 0 it writes the row index and reads nothing."""
+    rng = np.random.default_rng(n + 17)
+    raw = rng.integers(0, 2**32, size=n * 2304 // 4, dtype=np.uint32)
+    words = raw[: n * 512].reshape(n, 512)
+    scales = raw[n * 512:].reshape(n // 2, 128)
+    want = np.bitwise_xor.reduce(words, axis=1) ^ np.repeat(np.bitwise_xor.reduce(scales, axis=1), 2)
+    w = gpu(raw.view(np.uint8), dev)
+    out = torch.full((n,), -1, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    assert ops.lib().amv_debug_gemv_read_probe(w.data_ptr(), n, 4096, out.data_ptr(), 1, s) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want)
+    assert ops.lib().amv_debug_gemv_read_probe(w.data_ptr(), n, 4096, out.data_ptr(), 0, s) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), np.arange(n, dtype=np.int32))
+    assert ops.lib().amv_debug_gemv_read_probe(w.data_ptr(), n + 1, 4096, out.data_ptr(), 1, s) != 0
