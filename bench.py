@@ -626,6 +626,56 @@ def pmc_gemm(ops, torch, dev):
     print(json.dumps(res), flush=True)
 
 
+def pmc_i2s(ops, torch, dev):
+    """Dispatches for the counters of the BitNet I2_S batch-128 MUL_MAT (BASELINE config 3 shapes, int8 MFMA): 20
+    eager launches on each of 2560 x 6912 and 6912 x 2560 over one random ternary weight, then 20 plain copies of the
+    first weight's byte count (the FETCH_SIZE scale)."""
+    from ameva_compute_amd._lib import check, lib as _lib
+    res = {}
+    g = torch.Generator(device=dev)
+    for n, k in ((2560, 6912), (6912, 2560)):
+        g.manual_seed(500 + n)
+        cb = torch.randint(0, 3, (n, k // 128, 4, 32), generator=g, device=dev, dtype=torch.int32)
+        w = ((cb[:, :, 0] << 6) | (cb[:, :, 1] << 4) | (cb[:, :, 2] << 2) | cb[:, :, 3]).to(torch.uint8)
+        w = w.reshape(n, k // 4).contiguous()
+        x = torch.randn((128, k), generator=g, device=dev)
+        act = ops.i2s_quantize_act(x)
+        out = torch.empty((128, n), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            check(_lib().amv_i2s_gemv(w.data_ptr(), n, k, act.data_ptr(), 128, 1.5, out.data_ptr(), n,
+                                      torch.cuda.current_stream().cuda_stream), "amv_i2s_gemv")
+        torch.cuda.synchronize()
+        res[f"i2s_{n}x{k}_b128"] = {"dispatches": 20, "ops_each": 2 * 128 * n * k, "weight_bytes": n * k // 4,
+                                    "act_bytes": 128 * k + 128 * 4}
+    n_f = 2560 * 6912 // 4 // 4
+    src, dst = torch.randn(n_f, device=dev), torch.empty(n_f, device=dev)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    res["copy"] = {"dispatches": 20, "bytes_each_way": n_f * 4}
+    print(json.dumps(res), flush=True)
+
+
+def pmc_fa(ops, torch, dev):
+    """Dispatches for the counters of FLASH_ATTN_EXT decode at the Llama-3-8B layer shape (32 / 8 heads of 128, 4096
+    cached keys, F16 cache in llama.cpp's layout): 20 eager split + merge launches, each over its own cold copy of
+    the K and V rows (20 x 16.8 MB)."""
+    NH, NKV, D, CTX = 32, 8, 128, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(4096)
+    q = torch.randn((NH, D), generator=g, device=dev)
+    kv = [(torch.randn((CTX, NKV * D), generator=g, device=dev).half(),
+           torch.randn((CTX, NKV * D), generator=g, device=dev).half()) for _ in range(20)]
+    views = [(k.view(CTX, NKV, -1).permute(1, 0, 2), v.view(CTX, NKV, -1).permute(1, 0, 2)) for k, v in kv]
+    ws = torch.empty(max(1, ops.lib().amv_flash_attn_workspace_bytes(NH, NKV, CTX, D)), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    for i in range(20):
+        ops.flash_attn_decode_kv(q, views[i][0], views[i][1], ops.F16, 0.0884, workspace=ws)
+    torch.cuda.synchronize()
+    print(json.dumps({"fa_dispatches": 20, "kv_bytes_each": 2 * CTX * NKV * D * 2}), flush=True)
+
+
 INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix peak (5.0 POPS)
 
 
@@ -820,6 +870,10 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
+    ap.add_argument("--pmc-i2s", action="store_true",
+                    help="for rocprofv3 --pmc: 20 eager I2_S batch-128 MUL_MATs on each BitNet 2B shape")
+    ap.add_argument("--pmc-fa", action="store_true",
+                    help="for rocprofv3 --pmc: 20 eager cold FA decodes at 4096 keys over an F16 cache")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -837,6 +891,12 @@ def main():
         return
     if args.pmc_gemm:
         pmc_gemm(ops, torch, dev)
+        return
+    if args.pmc_i2s:
+        pmc_i2s(ops, torch, dev)
+        return
+    if args.pmc_fa:
+        pmc_fa(ops, torch, dev)
         return
     if args.only_layer:
         print(json.dumps(bench_layer(torch, dev, args)), flush=True)
