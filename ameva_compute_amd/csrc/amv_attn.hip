@@ -443,7 +443,9 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
     __shared__ __align__(16) float sbuf[SBUF];  // [wave][lane group][head][dim] partial P V; then the merge
     __shared__ float sM[4][G], sL[4][G];
     __shared__ float sP[4][KPW][G];  // per wave: probability of key, head
-    const int split = blockIdx.x, hk = blockIdx.y;
+    // grid (KV heads, splits): the workgroups reading the KV heads' slices of the same token rows are dispatched
+    // together
+    const int split = blockIdx.y, hk = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int grp = lane >> 4, c16 = lane & 15, d8 = 8 * c16;
     int n_kv = n_kv_max;
@@ -573,7 +575,7 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
         }
     }
     if constexpr (FUSED) {
-        if (!amv_arrive_last(counters + AMV_CNT_STRIDE * hk, gridDim.x)) return;
+        if (!amv_arrive_last(counters + AMV_CNT_STRIDE * hk, gridDim.y)) return;
         amv_acquire();
         fa_merge<G>(part, n_split, ns, hk, out, act, sbuf);
     }
@@ -651,8 +653,8 @@ static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const flo
     hipLaunchKernelGGL((k_fa_split<GG, KK, FUSED, KT>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev, \
                        k_row, k_head, v_row, v_head, n_split, scale, rule, counters, out, act)
 #define FA_MF(GG)                                                                                                   \
-    hipLaunchKernelGGL((k_fa_split_mf<GG, FUSED>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev, k_row, \
-                       k_head, v_row, v_head, n_split, scale, counters, out, act)
+    hipLaunchKernelGGL((k_fa_split_mf<GG, FUSED>), dim3(grid.y, grid.x), dim3(256), 0, st, q, kk, vv, mm, part, n_kv, \
+                       n_kv_dev, k_row, k_head, v_row, v_head, n_split, scale, counters, out, act)
 #define FA_G(GG)                                  \
     if (KT == FA_F16 && kpw == 16) FA_MF(GG);      \
     else if (kpw == 16) FA_LAUNCH(GG, 16);         \
