@@ -598,17 +598,18 @@ def pmc_probe(ops, torch, dev):
                       "copy_dispatches": 50, "copy_bytes_each_way": n * 4}), flush=True)
 
 
-def pmc_gemm(ops, torch, dev):
+def pmc_gemm(ops, torch, dev, exact=True):
     """Dispatches for the matrix-core counters: the default (exact, int8 MFMA) batched Q4_K MUL_MAT at M = 512 on the
     Llama-3-8B FFN shapes (14336 x 4096, then 4096 x 14336, whose k is split: its launch is followed by
-    k_splitk_sum), 20 eager launches each over one weight, then 20 plain copies of known size (the counters' scale)."""
+    k_splitk_sum), 20 eager launches each over one weight, then 20 plain copies of known size (the counters' scale).
+    exact=False runs the scaled f16-MFMA form instead (Q8_K_DEQ activations)."""
     res = {}
     g = torch.Generator(device=dev)
     for n, k in ((14336, 4096), (4096, 14336)):
         w = make_weights(ops, torch, n, k, 1, 300 + n, dev, ops.Q4_K)[0]
         g.manual_seed(512 + n)
         x = torch.randn((512, k), generator=g, device=dev)
-        at = ops.act_type(ops.Q4_K, 512)
+        at = ops.act_type(ops.Q4_K, 512, exact=exact)
         act, _ = ops.quantize_act(x, at, ops.Q8_X86)
         out = torch.empty((512, n), dtype=torch.float32, device=dev)
         for _ in range(20):
@@ -870,6 +871,8 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: 50 eager cold headline GEMVs and 50 plain copies of the same byte "
                          "count (the counter scale reference); prints a JSON line of what ran")
+    ap.add_argument("--pmc-gemm-scaled", action="store_true",
+                    help="as --pmc-gemm, with the scaled f16-MFMA form (Q8_K_DEQ activations)")
     ap.add_argument("--pmc-i2s", action="store_true",
                     help="for rocprofv3 --pmc: 20 eager I2_S batch-128 MUL_MATs on each BitNet 2B shape")
     ap.add_argument("--pmc-fa", action="store_true",
@@ -889,8 +892,8 @@ def main():
     if args.pmc_probe:
         pmc_probe(ops, torch, dev)
         return
-    if args.pmc_gemm:
-        pmc_gemm(ops, torch, dev)
+    if args.pmc_gemm or args.pmc_gemm_scaled:
+        pmc_gemm(ops, torch, dev, exact=not args.pmc_gemm_scaled)
         return
     if args.pmc_i2s:
         pmc_i2s(ops, torch, dev)
