@@ -102,6 +102,14 @@ __device__ __forceinline__ float amv_round_f16(float x) { return (float)(_Float1
 // Only for loads whose wave instruction covers whole lines: a line that a later instruction reads again is fetched
 // twice when the first read was non-temporal.
 typedef unsigned int amv_v4u __attribute__((ext_vector_type(4)));
+// Workgroup index -> tile index for a one-dimensional grid: MI355X hands workgroup i to XCD i % 8 and each XCD has its
+// own L2, so consecutive tile indices (tiles that share an operand, ordered by the caller) go to one XCD: XCD x runs
+// tiles x * g8 .. x * g8 + g8 - 1 (g8 = total / 8); the last total % 8 workgroups keep their index.
+__device__ __forceinline__ int amv_xcd_tile(int id, int total) {
+    const int g8 = total >> 3;
+    return id < 8 * g8 ? (id & 7) * g8 + (id >> 3) : id;
+}
+
 __device__ __forceinline__ uint4 amv_ld_stream(const uint4* p) {
     const amv_v4u v = __builtin_nontemporal_load(reinterpret_cast<const amv_v4u*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);

@@ -105,23 +105,79 @@ __global__ __launch_bounds__(256) void k_i2s_gemv(const uint4* __restrict__ w, i
 // MFMA k slots may be assigned to weights in any order A and B share: in block b, step t (0..3), lane half h
 // (lanes 32 h .. 32 h + 31) supplies the 16 weights 32 t + 16 h + s (s = 0..15), i.e. the 2-bit field t (shift
 // 6 - 2 t) of block bytes 16 h .. 16 h + 15, and the activations q[128 b + 32 t + 16 h + s]: one 16-byte load each.
-// Workgroup: 64 weight rows x 64 tokens (2 x 2 MFMA tiles of 32 x 32 per wave); its NW waves split the k blocks
-// (wave w takes blocks w, w + NW, ...) and the integer partials meet in LDS through integer atomics (exact). Lane l of
-// a 32 x 32 tile holds token column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
+// Lane l of a 32 x 32 tile holds token column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
 // ---------------------------------------------------------------------------------------------------------------
 typedef int i2s_v4i __attribute__((ext_vector_type(4)));
 typedef int i2s_v16i __attribute__((ext_vector_type(16)));
 
-template <bool OUT_SUMS, int NW>
-__global__ __launch_bounds__(64 * NW) void k_i2s_mmq(const uint8_t* __restrict__ w, int n_rows, int kb,
-                                                    const int8_t* __restrict__ q, const int2* __restrict__ meta, int m,
-                                                    float wscale, float* __restrict__ dst, int64_t ldd,
-                                                    int32_t* __restrict__ isums) {
-    __shared__ int part[2][2][16][64];  // integer sum of the wave partials: [row tile][token tile][r][lane]
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 31, h = lane >> 5;
-    const int row0 = blockIdx.x * 64, tok0 = blockIdx.y * 64;
-    const int k = kb * 128;
-    for (int i = threadIdx.x; i < 2 * 2 * 16 * 64; i += 64 * NW) (&part[0][0][0][0])[i] = 0;
+#define I2S_OUT_F32 0
+#define I2S_OUT_SUMS 1
+
+// Sum of the S split partials (integers: exact in any order), minus sum q, scaled. Thread (x, y): rows 4 x .. 4 x + 3
+// of token y; VEC: n_rows % 4 == 0 (16-byte partial rows), the S loads of a thread issued before its first add.
+template <bool OUT_SUMS, bool VEC>
+__global__ __launch_bounds__(256) void k_i2s_split_sum(const int32_t* __restrict__ part, int S, int n_rows, int m,
+                                                      const int2* __restrict__ meta, float wscale,
+                                                      float* __restrict__ dst, int64_t ldd,
+                                                      int32_t* __restrict__ isums) {
+    const int tok = blockIdx.y, r0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (r0 >= n_rows) return;
+    const size_t plane = (size_t)m * n_rows, base = (size_t)tok * n_rows + r0;
+    const int nr = min(4, n_rows - r0);
+    int t[4] = {0, 0, 0, 0};
+    if constexpr (VEC) {
+        for (int s0 = 0; s0 < S; s0 += 8) {
+            int4 v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (s0 + e < S) v[e] = *reinterpret_cast<const int4*>(part + (s0 + e) * plane + base);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (s0 + e < S) {
+                    t[0] += v[e].x;
+                    t[1] += v[e].y;
+                    t[2] += v[e].z;
+                    t[3] += v[e].w;
+                }
+            }
+        }
+    } else {
+        for (int s2 = 0; s2 < S; ++s2)
+            for (int e = 0; e < nr; ++e) t[e] += part[s2 * plane + base + e];
+    }
+    const int2 mt = meta[tok];
+    const float sc = __int_as_float(mt.x) * wscale;
+    for (int e = 0; e < nr; ++e) {
+        if (OUT_SUMS) isums[base + e] = t[e] - mt.y;
+        else dst[(size_t)tok * ldd + r0 + e] = (float)(t[e] - mt.y) * sc;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Batched I2_S (k_i2s_mmq_p): a workgroup computes a 64-row x 64-token tile over the k blocks of its split; wave w takes
+// the split's blocks w, w + 4, ... in chunks of PB blocks whose global loads (the two row tiles' weight halves
+// straight into the A operands, the two token tiles' activations into the B operands: one 16-byte load each, the
+// k-slot assignment above) are all issued before the chunk's first MFMA, so a wave waits for memory once per chunk
+// rather than once per block. The four waves' integer tiles are added in LDS in a fixed order (exact), then
+// stored row-contiguous: the final values (one split) or this split's partial plane [S][m][n_rows] for
+// k_i2s_split_sum. One-dimensional grid: the token tiles of a row tile, then the row tiles, then the splits, dealt
+// to the XCDs in consecutive runs (amv_xcd_tile), so the workgroups sharing a weight tile share an L2.
+// LDS: the four waves' tiles [wave][tile][r][lane] with the lane index XOR-swizzled by r + 16 (row tile) so that both
+// the wave-wide stores (one r) and the row-wise sums (64 rows of one token) meet distinct banks: 64 KB.
+// ---------------------------------------------------------------------------------------------------------------
+template <int OUT, bool SPLIT, int PB>
+__global__ __launch_bounds__(256) void k_i2s_mmq_p(const uint8_t* __restrict__ w, int n_rows, int kb,
+                                                  const int8_t* __restrict__ q, const int2* __restrict__ meta, int m,
+                                                  int kb_per, int n_rt, int n_tt, int n_sp, float wscale,
+                                                  float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ iout,
+                                                  int32_t* __restrict__ part) {
+    __shared__ int32_t red[4][4][16][64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, h = lane >> 5;
+    const int T = amv_xcd_tile(blockIdx.x, n_tt * n_rt * n_sp);
+    const int tt = T % n_tt, rt = (T / n_tt) % n_rt, sp = T / (n_tt * n_rt);
+    const int row0 = rt * 64, tok0 = tt * 64;
+    const int b0 = sp * kb_per, nblk = min(kb_per, kb - b0);  // >= 1 (the launcher's split)
+    const size_t k = (size_t)kb * 128;
     const uint4* wr[2];
     const int4* qa[2];
 #pragma unroll
@@ -137,222 +193,73 @@ __global__ __launch_bounds__(64 * NW) void k_i2s_mmq(const uint8_t* __restrict__
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-    uint4 wb[2];
-    int4 ab[2][4];
-    int b = wv;
-    if (b < kb) {
+    const int nbw = nblk > wv ? (nblk - wv + 3) / 4 : 0;  // this wave's blocks: b0 + wv + 4 i, i < nbw
+    for (int c0 = 0; c0 < nbw; c0 += PB) {
+        uint4 wb[PB][2];
+        int4 ab[PB][2][4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) wb[i] = wr[i][2 * b];
+        for (int i = 0; i < PB; ++i) {
+            if (c0 + i < nbw) {  // uniform
+                const int b = b0 + wv + 4 * (c0 + i);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+                for (int ii = 0; ii < 2; ++ii) wb[i][ii] = wr[ii][2 * b];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) ab[j][t] = qa[j][8 * b + 2 * t];
-    }
-    for (; b < kb; b += NW) {
-        const int bn = b + NW < kb ? b + NW : b;  // next block of this wave (reloads b at the end: harmless)
-        uint4 nwb[2];
-        int4 nab[2][4];
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) nwb[i] = wr[i][2 * bn];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) nab[j][t] = qa[j][8 * bn + 2 * t];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int sh = 6 - 2 * t;
-            i2s_v4i A[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                A[i] = i2s_v4i{(int)((wb[i].x >> sh) & 0x03030303u), (int)((wb[i].y >> sh) & 0x03030303u),
-                               (int)((wb[i].z >> sh) & 0x03030303u), (int)((wb[i].w >> sh) & 0x03030303u)};
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int4 v = ab[j][t];
-                    const i2s_v4i B = {v.x, v.y, v.z, v.w};
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B, acc[i][j], 0, 0, 0);
-                }
+                    for (int t = 0; t < 4; ++t) ab[i][j][t] = qa[j][8 * b + 2 * t];
+            }
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) wb[i] = nwb[i];
+        for (int i = 0; i < PB; ++i) {
+            if (c0 + i >= nbw) break;  // uniform
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int t = 0; t < 4; ++t) {
+                const int sh = 6 - 2 * t;
+                i2s_v4i A[2];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) ab[j][t] = nab[j][t];
+                for (int ii = 0; ii < 2; ++ii)
+                    A[ii] = i2s_v4i{(int)((wb[i][ii].x >> sh) & 0x03030303u), (int)((wb[i][ii].y >> sh) & 0x03030303u),
+                                    (int)((wb[i][ii].z >> sh) & 0x03030303u), (int)((wb[i][ii].w >> sh) & 0x03030303u)};
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int4 v = ab[i][j][t];
+                        acc[ii][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[ii], i2s_v4i{v.x, v.y, v.z, v.w},
+                                                                           acc[ii][j], 0, 0, 0);
+                    }
+            }
+        }
     }
-    __syncthreads();  // part zeroed
+    // lane l of tile (i, j) holds token 32 j + l % 32 and rows 32 i + 8 (r / 4) + 4 (l / 32) + r % 4
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) atomicAdd(&part[i][j][r][lane], acc[i][j][r]);
+            for (int r = 0; r < 16; ++r) red[wv][2 * i + j][r][lane ^ (r + 16 * i)] = acc[i][j][r];
     __syncthreads();
-    if (wv != 0) return;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int tok = tok0 + 32 * j + c;
-        if (tok >= m) continue;
-        const int2 mt = meta[tok];
-        const float ts = __int_as_float(mt.x) * wscale;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = row0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row >= n_rows) continue;
-                const int t = part[i][j][r][lane] - mt.y;
-                if (OUT_SUMS) isums[(size_t)tok * n_rows + row] = t;
-                else dst[(size_t)tok * ldd + row] = (float)t * ts;
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// Batched I2_S with the k range split over workgroups (k_i2s_mmq_s), for shapes that give k_i2s_mmq too few
-// workgroups: a workgroup computes a 128-row x 64-token tile over its share of the k blocks, so that a BitNet-2B shape
-// at batch 128 (2560 x 6912: 40 tiles) still spreads over the CUs. Per chunk of up to I2S_KMAX blocks every global load is issued before the first LDS store: the 64 tokens'
-// 128 activation bytes per block go through LDS (8 KB: eight lanes per token row, whole 128-byte lines; a token row
-// takes I2S_ALD = 144 bytes, which keeps a ds_read_b128 group on distinct banks), the weights straight into the MFMA
-// operand registers (lane (c, h) of wave w: 16 bytes of row 32 w + c); the first half of the chunk is multiplied while
-// the second half arrives. Wave w multiplies rows 32 w .. 32 w + 31 against both 32-token tiles
-// (v_mfma_i32_32x32x32_i8 with the k-slot assignment of k_i2s_mmq, exact integers). The tile's integers go through
-// LDS to row-contiguous stores: the final values (one split), or per-split partials [S][m][n_rows] in the library
-// workspace that k_i2s_split_sum adds (measured: handing them to the tile's last split with agent-scope loads and
-// stores inside the launch was 2.5x slower). Measured on MI355X (eager, batch 128): the staged weights and a store loop
-// that waited on each LDS read cost 2560 x 6912 11.8 -> 9.7 us (4 splits, weights cache-resident).
-// ---------------------------------------------------------------------------------------------------------------
-#define I2S_KMAX 8
-#define I2S_ALD 144
-#define I2S_OUT_F32 0
-#define I2S_OUT_SUMS 1
-
-template <int OUT, bool SPLIT>
-__global__ __launch_bounds__(256) void k_i2s_mmq_s(const uint8_t* __restrict__ w, int n_rows, int kb,
-                                                  const int8_t* __restrict__ q, const int2* __restrict__ meta, int m,
-                                                  int kb_per, float wscale, float* __restrict__ dst, int64_t ldd,
-                                                  int32_t* __restrict__ iout, int32_t* __restrict__ part) {
-    __shared__ __align__(16) uint8_t sa[I2S_KMAX][64 * I2S_ALD];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, h = lane >> 5;
-    const int row0 = blockIdx.x * 128, tok0 = blockIdx.y * 64, sp = blockIdx.z;
-    const int b0 = sp * kb_per, nblk = min(kb_per, kb - b0);  // >= 1 (the launcher's split)
-    const size_t k = (size_t)kb * 128;
-    // loads: the lane's weight half (row 32 wv + c, half h); activation chunks tid and tid + 256 = (token, 16-byte part)
-    const int atok = tid >> 3, apart = tid & 7;
-    const i2s_v4i* wsrc = reinterpret_cast<const i2s_v4i*>(w + (size_t)min(row0 + 32 * wv + c, n_rows - 1) * kb * 32) + h;
-    const i2s_v4i* asrc0 = reinterpret_cast<const i2s_v4i*>(q + (size_t)min(tok0 + atok, m - 1) * k) + apart;
-    const i2s_v4i* asrc1 = reinterpret_cast<const i2s_v4i*>(q + (size_t)min(tok0 + 32 + atok, m - 1) * k) + apart;
-    const int aofs = atok * I2S_ALD + 16 * apart;
-    i2s_v16i acc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0;
-    constexpr int HALF = I2S_KMAX / 2;
-    for (int c0 = 0; c0 < nblk; c0 += I2S_KMAX) {  // chunks of I2S_KMAX blocks (one chunk for a split launch)
-        const int nc = min(I2S_KMAX, nblk - c0);
-        i2s_v4i rw[I2S_KMAX], ra0[I2S_KMAX], ra1[I2S_KMAX];
-#pragma unroll
-        for (int i = 0; i < I2S_KMAX; ++i) {  // unconditional: blocks past the chunk reload its last block (unused)
-            const int b = b0 + c0 + min(i, nc - 1);
-            rw[i] = __builtin_nontemporal_load(wsrc + 2 * b);
-            ra0[i] = asrc0[8 * b];
-            ra1[i] = asrc1[8 * b];
-        }
-        if (c0 > 0) __syncthreads();  // every wave is done with the previous chunk's blocks
-#pragma unroll
-        for (int part = 0; part < 2; ++part) {
-#pragma unroll
-            for (int i = part * HALF; i < (part + 1) * HALF; ++i) {
-                *reinterpret_cast<i2s_v4i*>(&sa[i][aofs]) = ra0[i];
-                *reinterpret_cast<i2s_v4i*>(&sa[i][aofs + 32 * I2S_ALD]) = ra1[i];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i = part * HALF; i < (part + 1) * HALF; ++i) {
-                if (i >= nc) break;  // uniform
-                const i2s_v4i wa = rw[i];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int sh = 6 - 2 * t;
-                    const i2s_v4i A = (wa >> sh) & 0x03030303;
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const i2s_v4i B =
-                            *reinterpret_cast<const i2s_v4i*>(&sa[i][(32 * j + c) * I2S_ALD + 32 * t + 16 * h]);
-                        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, acc[j], 0, 0, 0);
-                    }
-                }
-            }
-        }
-    }
-    // the wave's 32 rows x 64 tokens through LDS, [token][row] (33 words per token row), then row-contiguous stores
-    __syncthreads();  // every wave is done with the staged blocks
-    int32_t* st = reinterpret_cast<int32_t*>(&sa[0][0]) + wv * 64 * 33;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) st[(32 * j + c) * 33 + 8 * (r >> 2) + 4 * h + (r & 3)] = acc[j][r];
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const int rr = lane & 31, th = lane >> 5;  // lane: row rr of the wave's 32, tokens th, th + 2, ...
-    const int row = row0 + 32 * wv + rr;
-    int32_t vv[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) vv[i] = st[(th + 2 * i) * 33 + rr];  // every read issued before the first store
-    if constexpr (SPLIT) {  // this split's integers, [S][m][n_rows], added by k_i2s_split_sum
-        int32_t* pp = part + ((size_t)sp * m + tok0 + th) * n_rows + row;
-        if (row < n_rows) {
-#pragma unroll
-            for (int i = 0; i < 32; ++i)
-                if (tok0 + th + 2 * i < m) pp[(size_t)2 * i * n_rows] = vv[i];
-        }
-        return;
-    }
-    if (row < n_rows) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int tok = tok0 + th + 2 * i;
-            if (tok >= m) break;
+    // thread: tile row rr (64 consecutive threads = 64 consecutive rows), tokens 16 (tid / 64) .. + 15
+    const int rr = tid & 63, i = rr >> 5, r32 = rr & 31;
+    const int r = 4 * (r32 >> 3) + (r32 & 3), hh = (r32 >> 2) & 1;
+    const int row = row0 + rr;
+    if (row >= n_rows) return;  // after the only barrier
+#pragma unroll 4
+    for (int e = 0; e < 16; ++e) {
+        const int tk = 16 * (tid >> 6) + e, j = tk >> 5;
+        const int tok = tok0 + tk;
+        if (tok >= m) break;
+        const int ln = ((tk & 31) + 32 * hh) ^ (r + 16 * i);
+        const int32_t v = ((red[0][2 * i + j][r][ln] + red[1][2 * i + j][r][ln]) + red[2][2 * i + j][r][ln]) +
+                          red[3][2 * i + j][r][ln];
+        if constexpr (SPLIT) {
+            part[((size_t)sp * m + tok) * n_rows + row] = v;
+        } else {
             const int2 mt = meta[tok];
-            const int32_t t = vv[i] - mt.y;
+            const int32_t t = v - mt.y;
             if constexpr (OUT == I2S_OUT_SUMS) iout[(size_t)tok * n_rows + row] = t;
             else dst[(size_t)tok * ldd + row] = (float)t * (__int_as_float(mt.x) * wscale);
         }
-    }
-}
-
-// Sum of the S split partials (integers: exact in any order), minus sum q, scaled. Thread (x, y): rows 4 x .. 4 x + 3
-// of token y; VEC: n_rows % 4 == 0 (16-byte partial rows).
-template <bool OUT_SUMS, bool VEC>
-__global__ __launch_bounds__(256) void k_i2s_split_sum(const int32_t* __restrict__ part, int S, int n_rows, int m,
-                                                      const int2* __restrict__ meta, float wscale,
-                                                      float* __restrict__ dst, int64_t ldd,
-                                                      int32_t* __restrict__ isums) {
-    const int tok = blockIdx.y, r0 = 4 * (blockIdx.x * 256 + threadIdx.x);
-    if (r0 >= n_rows) return;
-    const size_t plane = (size_t)m * n_rows, base = (size_t)tok * n_rows + r0;
-    const int nr = min(4, n_rows - r0);
-    int t[4] = {0, 0, 0, 0};
-    for (int s2 = 0; s2 < S; ++s2) {
-        if constexpr (VEC) {
-            const int4 v = *reinterpret_cast<const int4*>(part + s2 * plane + base);
-            t[0] += v.x;
-            t[1] += v.y;
-            t[2] += v.z;
-            t[3] += v.w;
-        } else {
-            for (int e = 0; e < nr; ++e) t[e] += part[s2 * plane + base + e];
-        }
-    }
-    const int2 mt = meta[tok];
-    const float sc = __int_as_float(mt.x) * wscale;
-    for (int e = 0; e < nr; ++e) {
-        if (OUT_SUMS) isums[base + e] = t[e] - mt.y;
-        else dst[(size_t)tok * ldd + r0 + e] = (float)(t[e] - mt.y) * sc;
     }
 }
 
@@ -373,40 +280,50 @@ extern "C" int amv_i2s_quantize_act(const float* x, int64_t m, int64_t k, void* 
 
 // batch from which the MFMA kernel runs (as the Q4_0 / Q8_0 MUL_MAT, AMEVA_QGEMM_MIN_M = 8)
 #define I2S_MMQ_MIN_M 8
-#ifndef I2S_MMQ_WAVES
-#define I2S_MMQ_WAVES 4
-#endif
-
-// The batched launch for shapes whose k_i2s_mmq grid (64 x 64 tiles) would leave most CUs idle: k split over S
-// workgroups per 128 x 64 tile, S ~ 256 / tiles (at most 8). Measured on MI355X at batch 128, cold weights, graph
-// replays: 2560 x 6912 (k_i2s_mmq: 80 workgroups) 23.6 us -> 17.3 us with 6 splits (18.5 with 4, 19.7 with 9);
-// 6912 x 2560 (216 workgroups) stays on k_i2s_mmq (13.5 us; the split kernel's best, 2 splits, 18.7 us).
-// False (nothing launched) when k_i2s_mmq fills the GPU, or when the partials need a workspace that cannot be
-// allocated now (under stream capture).
-static bool i2s_mmq_split(const void* w, int64_t n_rows, int kb, const void* act, int64_t m, float wscale, float* dst,
-                          int64_t ldd, int32_t* sums, hipStream_t st) {
-    if (((n_rows + 63) / 64) * ((m + 63) / 64) >= 160) return false;
-    const int64_t tiles = ((n_rows + 127) / 128) * ((m + 63) / 64);
-    int S = (int)std::min<int64_t>({(int64_t)kb, (int64_t)8, std::max<int64_t>(1, (256 + tiles / 2) / tiles)});
-    const int kb_per = (kb + S - 1) / S;
+// The batched launch (k_i2s_mmq_p): 64 x 64 tiles, k split over S workgroups when the tiles alone leave CUs idle (about
+// one workgroup per CU: the four-block prefetch keeps a wave's 250 VGPRs, one wave per SIMD), the partials added by
+// k_i2s_split_sum. The integers do not depend on S (exact in any order): without the workspace (first needed under
+// capture) the launch runs unsplit. Measured on MI355X at batch 128, cold weights, graph replays (bench.py
+// --only-i2s): 2560 x 6912 (80 tiles, 3 splits) 15.1 us (2, 4, 6 splits: 17.2, 18.4, 17.7; the former 128 x 64-tile
+// split kernel 17.3); 6912 x 2560 (216 tiles, unsplit) 12.6 us (2 splits 18.0; the former 64 x 64 kernel with
+// one block of lookahead 13.4). Prefetching all of a wave's blocks (up to 8) measured the same as 4.
+static void i2s_mmq_p(const void* w, int64_t n_rows, int kb, const void* act, int64_t m, float wscale, float* dst,
+                      int64_t ldd, int32_t* sums, hipStream_t st) {
+    const int64_t n_rt = (n_rows + 63) / 64, n_tt = (m + 63) / 64, tiles = n_rt * n_tt;
+    int S = (int)std::min<int64_t>({(int64_t)kb, (int64_t)16, std::max<int64_t>(1, 256 / tiles)});
+    int kb_per = (kb + S - 1) / S;
     S = (kb + kb_per - 1) / kb_per;
+    int32_t* part = nullptr;
+    if (S > 1) {
+        const size_t bytes = (size_t)S * m * n_rows * 4;
+        part = bytes <= AMV_SPLITK_WS_BYTES ? reinterpret_cast<int32_t*>(amv_splitk_workspace(bytes, st)) : nullptr;
+        if (!part) {
+            S = 1;
+            kb_per = kb;
+        }
+    }
     const int8_t* q = (const int8_t*)act;
     const int2* meta = (const int2*)((const uint8_t*)act + m * (int64_t)kb * 128);
     const uint8_t* wp = (const uint8_t*)w;
-    const dim3 grid((unsigned)((n_rows + 127) / 128), (unsigned)((m + 63) / 64), (unsigned)S);
-    int32_t* part = nullptr;
-    if (S > 1) {
-        part = reinterpret_cast<int32_t*>(amv_splitk_workspace((size_t)S * m * n_rows * 4, st));
-        if (!part) return false;
-    }
-#define I2S_S(OUT, SPLIT, D, L, IO) hipLaunchKernelGGL((k_i2s_mmq_s<OUT, SPLIT>), grid, dim3(256), 0, st, wp, (int)n_rows, \
-                                                       kb, q, meta, (int)m, kb_per, wscale, D, L, IO, part)
+    const int nbw = (kb_per + 3) / 4;  // blocks of the busiest wave
+    const unsigned n_wg = (unsigned)(tiles * S);
+#define I2S_P(OUT, SPLIT, PB, D, L, IO)                                                                               \
+    hipLaunchKernelGGL((k_i2s_mmq_p<OUT, SPLIT, PB>), dim3(n_wg), dim3(256), 0, st, wp, (int)n_rows, kb, q, meta,     \
+                       (int)m, kb_per, (int)n_rt, (int)n_tt, S, wscale, D, L, IO, part)
+#define I2S_PB(OUT, SPLIT, D, L, IO)          \
+    if (nbw <= 2) I2S_P(OUT, SPLIT, 2, D, L, IO); \
+    else I2S_P(OUT, SPLIT, 4, D, L, IO)
     if (S == 1) {
-        if (sums) I2S_S(I2S_OUT_SUMS, false, nullptr, (int64_t)0, sums);
-        else I2S_S(I2S_OUT_F32, false, dst, ldd, nullptr);
-        return true;
+        if (sums) {
+            I2S_PB(I2S_OUT_SUMS, false, nullptr, (int64_t)0, sums);
+        } else {
+            I2S_PB(I2S_OUT_F32, false, dst, ldd, nullptr);
+        }
+        return;
     }
-    I2S_S(I2S_OUT_F32, true, nullptr, (int64_t)0, nullptr);
+    I2S_PB(I2S_OUT_F32, true, nullptr, (int64_t)0, nullptr);
+#undef I2S_PB
+#undef I2S_P
     const dim3 g2((unsigned)((n_rows + 1023) / 1024), (unsigned)m);
     const bool vec = n_rows % 4 == 0;
 #define I2S_SUM(SU, V) hipLaunchKernelGGL((k_i2s_split_sum<SU, V>), g2, dim3(256), 0, st, part, S, (int)n_rows, (int)m, \
@@ -419,8 +336,6 @@ static bool i2s_mmq_split(const void* w, int64_t n_rows, int kb, const void* act
         else I2S_SUM(false, false);
     }
 #undef I2S_SUM
-#undef I2S_S
-    return true;
 }
 
 static int i2s_gemv_impl(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float wscale,
@@ -433,26 +348,7 @@ static int i2s_gemv_impl(const void* w, int64_t n_rows, int64_t k, const void* a
     AMV_REQUIRE(!dst || ldd >= n_rows, "amv_i2s_gemv: ldd < n_rows");
     hipStream_t st = amv_stream(stream);
     if (m >= I2S_MMQ_MIN_M) {
-        const int kb = (int)(k / 128);
-        if (i2s_mmq_split(w, n_rows, kb, act, m, wscale, dst, ldd, sums, st)) return amv_check_launch("amv_i2s_gemv");
-        const int8_t* q = (const int8_t*)act;
-        const int2* meta = (const int2*)((const uint8_t*)act + m * k);
-        const int64_t tok_tiles = (m + 63) / 64;
-        const dim3 grid((unsigned)((n_rows + 63) / 64), (unsigned)tok_tiles);
-        const uint8_t* wp = (const uint8_t*)w;
-        const int nw = I2S_MMQ_WAVES;
-#define I2S_MMQ(S, NWV, D, L, IS) hipLaunchKernelGGL((k_i2s_mmq<S, NWV>), grid, dim3(64 * NWV), 0, st, wp, \
-                                                     (int)n_rows, kb, q, meta, (int)m, wscale, D, L, IS)
-        if (sums) {
-            if (nw == 16) I2S_MMQ(true, 16, nullptr, (int64_t)0, sums);
-            else if (nw == 8) I2S_MMQ(true, 8, nullptr, (int64_t)0, sums);
-            else I2S_MMQ(true, 4, nullptr, (int64_t)0, sums);
-        } else {
-            if (nw == 16) I2S_MMQ(false, 16, dst, ldd, nullptr);
-            else if (nw == 8) I2S_MMQ(false, 8, dst, ldd, nullptr);
-            else I2S_MMQ(false, 4, dst, ldd, nullptr);
-        }
-#undef I2S_MMQ
+        i2s_mmq_p(w, n_rows, (int)(k / 128), act, m, wscale, dst, ldd, sums, st);
         return amv_check_launch("amv_i2s_gemv");
     }
     const int nsl = (int)(k / 64);

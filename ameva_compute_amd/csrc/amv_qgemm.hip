@@ -44,12 +44,6 @@ typedef float qg_f16v __attribute__((ext_vector_type(16)));
 // byte-wise n - 8 of nibbles n in 0..15 (no carry crosses a byte: n + 0x78 <= 0x87)
 __device__ __forceinline__ uint32_t qg_m8(uint32_t v) { return (v + 0x78787878u) ^ 0x80808080u; }
 
-// workgroup index -> tile index: consecutive tile indices (the token tiles of one weight tile, then the next weight
-// tile; the k range slowest) go to one XCD; the last total % 8 workgroups keep their index
-__device__ __forceinline__ int qg_tile(int id, int total) {
-    const int g8 = total >> 3;
-    return id < 8 * g8 ? (id & 7) * g8 + (id >> 3) : id;
-}
 
 // ---------------------------------------------------------------------------------------------------------------
 // Q4_0 / Q8_0
@@ -136,7 +130,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wt = w & 1, ww = w >> 1, c = lane & 31, h = lane >> 5;
     // tile index: token tile fastest, then the split of k, then the weight tile
-    const int T = qg_tile(blockIdx.x, n_tw * n_z * n_tt);
+    const int T = amv_xcd_tile(blockIdx.x, n_tw * n_z * n_tt);  // token tiles, weight tiles, k ranges
     const int tt = T % n_tt, tw = (T / n_tt) % n_tw, z = T / (n_tt * n_tw);
     const int n0 = tw * BN, m0 = tt * BM;
     const int K = nb * 32;
@@ -343,7 +337,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     __shared__ __align__(16) uint16_t sMn[2][BN * 16], sBs[2][BM * 16];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wt = w & 1, ww = w >> 1, c32 = lane & 31, h = lane >> 5;
-    const int T = qg_tile(blockIdx.x, n_tw * n_z * n_tt);
+    const int T = amv_xcd_tile(blockIdx.x, n_tw * n_z * n_tt);  // token tiles, weight tiles, k ranges
     const int tt = T % n_tt, tw = (T / n_tt) % n_tw, z = T / (n_tt * n_tw);
     const int n0 = tw * BN, m0 = tt * BM;
     const int K = nsb * 256;
@@ -573,7 +567,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     __shared__ __align__(16) float sD[2][BN], sDa[2][BM];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wt = w & 1, ww = w >> 1, c32 = lane & 31, h = lane >> 5;
-    const int T = qg_tile(blockIdx.x, n_tw * n_z * n_tt);
+    const int T = amv_xcd_tile(blockIdx.x, n_tw * n_z * n_tt);  // token tiles, weight tiles, k ranges
     const int tt = T % n_tt, tw = (T / n_tt) % n_tw, z = T / (n_tt * n_tw);
     const int n0 = tw * BN, m0 = tt * BM;
     const int K = nsb * 256;

@@ -105,11 +105,11 @@ def pack_i2s(codes):
 @pytest.mark.parametrize("n,k,m", [(6912, 2560, 1), (2560, 6912, 1), (6912, 2560, 128), (2560, 6912, 128), (3, 128, 2),
                                    (129, 256, 5), (100, 384, 70), (64, 128, 8), (1000, 1280, 2000)])
 def test_i2s_parity(dev, ops, orc, n, k, m):
-    """m < 8: the GEMV; m >= 8: the int8-MFMA kernels (BASELINE config 3 batch 128): 64 x 64 tiles with the k blocks
-    split over the waves (6912 x 2560, 1000 x 1280 at m = 2000 with ragged row and token tiles), or for grids of fewer
-    than 160 such tiles 128 x 64 tiles with k split over workgroups and the partials added in a second launch (2560 x
-    6912: 6 splits of 9 blocks, staged in two chunks; the small shapes). Integer outputs bit-exact and the f32 outputs
-    bit-exact too (the same f32 operations as the CPU on the same integer)."""
+    """m < 8: the GEMV; m >= 8: the int8-MFMA kernel k_i2s_mmq_p (BASELINE config 3 batch 128): 64 x 64 tiles whose
+    k blocks the 4 waves share, unsplit when the tiles fill the GPU (6912 x 2560: 5 blocks per wave in two chunks;
+    1000 x 1280 at m = 2000 with ragged row and token tiles) or with k split over workgroups and the partials added
+    in a second launch (2560 x 6912: 3 splits of 18 blocks; the small shapes). Integer outputs bit-exact and the f32
+    outputs bit-exact too (the same f32 operations as the CPU on the same integer)."""
     rng = np.random.default_rng(n * 3 + k + m)
     codes = rng.integers(0, 3, (n, k))
     w = pack_i2s(codes)
