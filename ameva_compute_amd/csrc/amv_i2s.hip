@@ -286,7 +286,10 @@ extern "C" int amv_i2s_quantize_act(const float* x, int64_t m, int64_t k, void* 
 // capture) the launch runs unsplit. Measured on MI355X at batch 128, cold weights, graph replays (bench.py
 // --only-i2s): 2560 x 6912 (80 tiles, 3 splits) 15.1 us (2, 4, 6 splits: 17.2, 18.4, 17.7; the former 128 x 64-tile
 // split kernel 17.3); 6912 x 2560 (216 tiles, unsplit) 12.6 us (2 splits 18.0; the former 64 x 64 kernel with
-// one block of lookahead 13.4). Prefetching all of a wave's blocks (up to 8) measured the same as 4.
+// one block of lookahead 13.4). Prefetching all of a wave's blocks (up to 8) measured the same as 4. Staging the
+// activations through LDS with whole-line loads (8 lanes per 128-byte token row, XOR-swizzled slots, conflict-free
+// operand reads) measured 1.7-1.8x slower (23.0 / 25.8 us): the scattered direct operand loads are not what bounds
+// these launches.
 static void i2s_mmq_p(const void* w, int64_t n_rows, int kb, const void* act, int64_t m, float wscale, float* dst,
                       int64_t ldd, int32_t* sums, hipStream_t st) {
     const int64_t n_rt = (n_rows + 63) / 64, n_tt = (m + 63) / 64, tiles = n_rt * n_tt;
