@@ -627,6 +627,28 @@ def pmc_gemm(ops, torch, dev, exact=True):
     print(json.dumps(res), flush=True)
 
 
+def pmc_small(ops, torch, dev):
+    """Dispatches for the counters of the small-batch (M = 16) MUL_MATs on the FFN gate/up shape 14336 x 4096: 20 eager
+    launches each for Q4_K and Q6_K over 20 rotating cold weight copies."""
+    res = {}
+    g = torch.Generator(device=dev)
+    for name, wtype in (("q4_K", ops.Q4_K), ("q6_K", ops.Q6_K)):
+        ws = make_weights(ops, torch, 14336, 4096, 20, 700 + wtype, dev, wtype)
+        g.manual_seed(16 + wtype)
+        x = torch.randn((16, 4096), generator=g, device=dev)
+        at = ops.act_type(wtype, 16)
+        act, _ = ops.quantize_act(x, at, ops.Q8_X86)
+        out = torch.empty((16, 14336), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for i in range(20):
+            ops.mul_mat_q(ws[i], act, 16, out, act_t=at)
+        torch.cuda.synchronize()
+        res[f"{name}_14336x4096_m16"] = {"dispatches": 20, "weight_bytes": ws[0].nbytes}
+        del ws
+        torch.cuda.empty_cache()
+    print(json.dumps(res), flush=True)
+
+
 def pmc_i2s(ops, torch, dev):
     """Dispatches for the counters of the BitNet I2_S batch-128 MUL_MAT (BASELINE config 3 shapes, int8 MFMA): 20
     eager launches on each of 2560 x 6912 and 6912 x 2560 over one random ternary weight, then 20 plain copies of the
@@ -873,6 +895,8 @@ def main():
                          "count (the counter scale reference); prints a JSON line of what ran")
     ap.add_argument("--pmc-gemm-scaled", action="store_true",
                     help="as --pmc-gemm, with the scaled f16-MFMA form (Q8_K_DEQ activations)")
+    ap.add_argument("--pmc-small", action="store_true",
+                    help="for rocprofv3 --pmc: 20 eager cold Q4_K and Q6_K MUL_MATs at M = 16 (14336 x 4096)")
     ap.add_argument("--pmc-i2s", action="store_true",
                     help="for rocprofv3 --pmc: 20 eager I2_S batch-128 MUL_MATs on each BitNet 2B shape")
     ap.add_argument("--pmc-fa", action="store_true",
@@ -897,6 +921,9 @@ def main():
         return
     if args.pmc_i2s:
         pmc_i2s(ops, torch, dev)
+        return
+    if args.pmc_small:
+        pmc_small(ops, torch, dev)
         return
     if args.pmc_fa:
         pmc_fa(ops, torch, dev)
