@@ -24,6 +24,7 @@ SIGNATURES = {
     "amv_quantize_q4_0": (I32, [P, I64, I64, P, P]),
     "amv_mul_mat_vec": (I32, [I32, P, I64, I64, P, I64, P, I64, P]),
     "amv_debug_gemv_generic": (I32, [I32]),
+    "amv_mul_mat_vec_raw": (I32, [I32, P, I64, I64, I64, P, I64, P, I64, P, P]),
     "amv_debug_gemv_read_probe": (I32, [P, I64, I64, P, I32, P]),
     "amv_mul_mat_vec_ep": (I32, [I32, P, I64, I64, P, P, I32, P, P, P]),
     "amv_mul_mat_block_sums": (I32, [I32, P, I64, I64, P, I64, P, P]),

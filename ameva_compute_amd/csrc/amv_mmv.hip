@@ -1144,6 +1144,129 @@ extern "C" int amv_mul_mat_block_sums(int wtype, const void* w, int64_t n_rows, 
     return amv_check_launch("amv_mul_mat_block_sums");
 }
 
+// ------------------------------------------------------------------------------------------------ raw ggml blocks
+// MUL_MAT of one to eight activation columns on Q4_0 / Q8_0 weights still in ggml's block layout: the reference's
+// raw-layout path (ameva_qmm.comp:315-372) for a quantized tensor outside a WEIGHTS buffer or a row view of one, read
+// in place instead of repacked per use. A block is 18 / 34 bytes, so a pair of blocks is 36 / 68 bytes and dword
+// aligned whenever a row starts on a dword (k % 64 == 0, a dword-aligned row stride). A wave owns two rows; lane l takes
+// block pairs l, l + 64, ... of both: each pair loads whole (two / four dword-aligned 16-byte loads and one dword, the
+// 64 lanes covering 2.3 / 4.4 KB of the row contiguously), the first block's quants are realigned by two bytes
+// (v_alignbyte_b32), and ggml's exact block integers come from v_dot4 as in the repacked GEMV (Q4_0: low nibbles
+// against elements 0..15, high against 16..31, minus 8 sum(q_a)). f32 = sum over the lane's blocks in order of
+// d_w d_a s, then the wave sum. SUMS writes the block integers [m][n_rows][k / 32] instead.
+#define RAW_MAXM 8
+template <int WT, bool SUMS, int MAXM>
+__global__ __launch_bounds__(256) void k_mmv_raw(const uint8_t* __restrict__ w, int64_t row_bytes, int n_rows, int k,
+                                                 const int8_t* __restrict__ aq, const int2* __restrict__ ameta, int m,
+                                                 float* __restrict__ dst, int64_t ldd, int32_t* __restrict__ sums) {
+    constexpr int PW = WT == AMV_T_Q4_0 ? 9 : 17;  // dwords of a block pair
+    constexpr int NQ = WT == AMV_T_Q4_0 ? 4 : 8;   // quant dwords of a block
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
+    if (row0 >= n_rows) return;  // whole waves; the kernel has no barrier
+    const int nr = min(2, n_rows - row0);
+    const int npair = k / 64, nblk = k / 32;
+    float acc[MAXM][2];
+#pragma unroll
+    for (int c = 0; c < MAXM; ++c) acc[c][0] = acc[c][1] = 0.0f;
+    for (int p = lane; p < npair; p += 64) {
+        uint32_t D[2][PW];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(
+                __builtin_assume_aligned(w + (size_t)(row0 + min(r, nr - 1)) * row_bytes + (size_t)p * 4 * PW, 4));
+#pragma unroll
+            for (int i = 0; i < PW; ++i) D[r][i] = src[i];
+        }
+#pragma unroll
+        for (int c = 0; c < MAXM; ++c) {
+            if (c >= m) break;  // uniform
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {  // block 2 p + b
+                const int j = 2 * p + b;
+                const int4* a4 = reinterpret_cast<const int4*>(aq + (size_t)c * k + 32 * j);
+                const int4 a0 = a4[0], a1 = a4[1];
+                const int2 ds = ameta[(size_t)c * nblk + j];
+                const float da = __int_as_float(ds.x);
+                const int av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    // block b of the pair: f16 d at byte 0 (b = 0) or at dword NQ + 0's high half (b = 1), quants after
+                    uint32_t q[NQ];
+                    uint16_t dh;
+                    if (b == 0) {
+                        dh = (uint16_t)(D[r][0] & 0xFFFFu);
+#pragma unroll
+                        for (int i = 0; i < NQ; ++i) q[i] = __builtin_amdgcn_alignbyte(D[r][i + 1], D[r][i], 2);
+                    } else {
+                        dh = (uint16_t)(D[r][NQ] >> 16);
+#pragma unroll
+                        for (int i = 0; i < NQ; ++i) q[i] = D[r][NQ + 1 + i];
+                    }
+                    int sacc = 0;
+                    if constexpr (WT == AMV_T_Q4_0) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) sacc = amv_dot4((int)(q[i] & M4), av[i], sacc);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) sacc = amv_dot4((int)((q[i] >> 4) & M4), av[4 + i], sacc);
+                        sacc -= 8 * ds.y;
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) sacc = amv_dot4((int)q[i], av[i], sacc);
+                    }
+                    if constexpr (SUMS) {
+                        if (r < nr) sums[((size_t)c * n_rows + row0 + r) * nblk + j] = sacc;
+                    } else {
+                        acc[c][r] = fmaf((float)sacc, amv_h2f(dh) * da, acc[c][r]);
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (!SUMS) {
+#pragma unroll
+        for (int c = 0; c < MAXM; ++c) {
+            if (c >= m) break;
+            const float t0 = amv_wave_sum(acc[c][0]), t1 = amv_wave_sum(acc[c][1]);
+            if (lane < nr) dst[(size_t)c * ldd + row0 + lane] = lane ? t1 : t0;
+        }
+    }
+}
+
+extern "C" int amv_mul_mat_vec_raw(int wtype, const void* w, int64_t row_bytes, int64_t n_rows, int64_t k,
+                                   const void* act, int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream) {
+    AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q8_0, "amv_mul_mat_vec_raw: type %d (Q4_0 or Q8_0)", wtype);
+    AMV_REQUIRE(w && act && (dst || sums), "amv_mul_mat_vec_raw: null pointer");
+    AMV_REQUIRE(n_rows > 0 && n_rows <= INT32_MAX && k > 0 && k % 64 == 0 && k <= INT32_MAX,
+                "amv_mul_mat_vec_raw: k %lld (a positive multiple of 64)", (long long)k);
+    AMV_REQUIRE(m >= 1 && m <= RAW_MAXM, "amv_mul_mat_vec_raw: m %lld (1..%d columns)", (long long)m, RAW_MAXM);
+    const int64_t blk = wtype == AMV_T_Q4_0 ? 18 : 34;
+    AMV_REQUIRE(row_bytes >= k / 32 * blk && row_bytes % 4 == 0 && ((uintptr_t)w & 3) == 0,
+                "amv_mul_mat_vec_raw: rows of %lld bytes (>= %lld, dword-aligned rows needed)", (long long)row_bytes,
+                (long long)(k / 32 * blk));
+    AMV_REQUIRE(((uintptr_t)act & 15) == 0, "amv_mul_mat_vec_raw: act must be 16-byte aligned");
+    AMV_REQUIRE(!dst || ldd >= n_rows, "amv_mul_mat_vec_raw: ldd < n_rows");
+    const int8_t* aq = (const int8_t*)act;
+    const int2* meta = (const int2*)((const uint8_t*)act + m * k);
+    const int waves = (int)((n_rows + 1) / 2);
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    hipStream_t st = amv_stream(stream);
+#define RAW_L(WTT, SU, MM) hipLaunchKernelGGL((k_mmv_raw<WTT, SU, MM>), grid, dim3(256), 0, st, (const uint8_t*)w, \
+                                              row_bytes, (int)n_rows, (int)k, aq, meta, (int)m, dst, ldd, sums)
+    // one column (decode) in its own instantiation: the eight-column one holds eight accumulator pairs
+    if (wtype == AMV_T_Q4_0) {
+        if (sums) RAW_L(AMV_T_Q4_0, true, RAW_MAXM);
+        else if (m == 1) RAW_L(AMV_T_Q4_0, false, 1);
+        else RAW_L(AMV_T_Q4_0, false, RAW_MAXM);
+    } else {
+        if (sums) RAW_L(AMV_T_Q8_0, true, RAW_MAXM);
+        else if (m == 1) RAW_L(AMV_T_Q8_0, false, 1);
+        else RAW_L(AMV_T_Q8_0, false, RAW_MAXM);
+    }
+#undef RAW_L
+    return amv_check_launch("amv_mul_mat_vec_raw");
+}
+
 // ------------------------------------------------------------------------------------------------ fused decode GEMVs
 static int mmv_dispatch_fused(int ep, MmvArgs& a, const void* act, hipStream_t st) {
     column_view(a, (const uint8_t*)act, 1, 0);

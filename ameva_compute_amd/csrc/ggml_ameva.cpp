@@ -665,6 +665,7 @@ struct Engine {
         const int atype = deq ? (kq ? AMV_ACT_Q8_K_DEQ : AMV_ACT_Q8_0_DEQ)
                         : (mmq && w->type == GGML_TYPE_Q4_K && M <= 64) ? AMV_ACT_Q8_K_MMA
                         : kq ? (int)GGML_TYPE_Q8_K : (int)GGML_TYPE_Q8_0;
+        if (!mmq && !ep && raw_readable(w)) return mul_mat_raw(n, atype);
         const void* wp = weight_ptr(n);
         if (!wp) return false;
         if (g_fail.load() == AMEVA_FAIL_MAP_SRC1) return fail(n, "failure injection: src1");
@@ -672,6 +673,35 @@ struct Engine {
         if (!act) return false;
         if (g_fail.load() == AMEVA_FAIL_DISPATCH) return fail(n, "failure injection: dispatch");
         return mul_mat_run(n, ep, wp, act, atype, M, mmq);
+    }
+
+    // A Q4_0 / Q8_0 weight that stays in ggml's block layout for this read: outside a WEIGHTS buffer (or a row view of
+    // a tensor) and not held repacked. The GEMV reads its blocks in place (the reference's raw-layout MUL_MAT,
+    // ameva_qmm.comp:315-372) instead of repacking a copy into scratch on every use; WEIGHTS tensors are still
+    // repacked in place once, which later reads amortise.
+    bool raw_readable(const ggml_tensor* w) {
+        if (w->type != GGML_TYPE_Q4_0 && w->type != GGML_TYPE_Q8_0) return false;
+        if (w->ne[0] % 64 != 0 || ((uintptr_t)w->data & 3) != 0 || w->nb[1] % 4 != 0) return false;
+        BufCtx* bc = (BufCtx*)w->buffer->context;
+        const ggml_tensor* base = w->view_src ? w->view_src : w;
+        std::lock_guard<std::mutex> lk(bc->mu);
+        if (bc->repacked.count(base->data)) return false;
+        return w->view_src || w->buffer->usage != GGML_BACKEND_BUFFER_USAGE_WEIGHTS || !repackable(w);
+    }
+
+    bool mul_mat_raw(const ggml_tensor* n, int atype) {
+        const ggml_tensor *w = n->src[0], *x = n->src[1];
+        const int64_t N = w->ne[1], K = w->ne[0], M = nrows(x);
+        if (g_fail.load() == AMEVA_FAIL_MAP_SRC1) return fail(n, "failure injection: src1");
+        void* act = act_for(n, x, atype, M, K);
+        if (!act) return false;
+        if (g_fail.load() == AMEVA_FAIL_DISPATCH) return fail(n, "failure injection: dispatch");
+        if (!rc(n, amv_mul_mat_vec_raw(w->type, w->data, (int64_t)w->nb[1], N, K, act, M, (float*)n->data, N, nullptr,
+                                       st)))
+            return false;
+        g_cnt.mul_mat++;
+        g_cnt.qmv++;
+        return true;
     }
 
     // src0 of a MUL_MAT in the MI355X layout: weights are repacked in place once (WEIGHTS buffers); a quantized

@@ -518,7 +518,8 @@ def bench_load_path(ops, torch, dev):
     """The weight load path (the reference's set_tensor repack, ggml-ameva-buffer.cpp:509-561): amv_repack (ggml blocks
     -> the MI355X layout) and amv_unrepack (back, as get_tensor does) of a 14336 x 4096 weight per type, cold over
     rotating sources > 512 MiB (the bytes are shuffled, not interpreted, so random bytes serve), read + write bytes
-    counted; and the pinned host -> HBM copy of the same bytes, the step a load cannot avoid."""
+    counted; the raw-layout GEMV (ggml blocks read in place, amv_mul_mat_vec_raw) against a repack per use; and the
+    pinned host -> HBM copy of the same bytes, the step a load cannot avoid."""
     from ameva_compute_amd._lib import lib as _lib
     res = {}
     n, k = 14336, 4096
@@ -541,6 +542,34 @@ def bench_load_path(ops, torch, dev):
         log(f"bench: repack {name} 14336x4096 ({nb / 2**20:.1f} MiB) {ms_r * 1e3:.1f} us = "
             f"{2 * nb / (ms_r * 1e-3) / 1e9:.0f} GB/s read+write; unrepack {ms_u * 1e3:.1f} us")
         del srcs, dst
+    # the raw-layout MUL_MAT (a quantized src0 outside a WEIGHTS buffer, M = 1): the GEMV on ggml's blocks in place,
+    # against a repack into scratch per use followed by the repacked GEMV; cold over rotating copies of random blocks
+    # whose f16 scales are kept finite
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    for name, wtype, blk in (("q4_0", ops.Q4_0, 18), ("q8_0", ops.Q8_0, 34)):
+        nb = n * k // 32 * blk
+        copies = max(4, -(-(600 << 20) // nb))
+        raws = [torch.randint(0, 256, (nb,), generator=g, device=dev, dtype=torch.uint8) for _ in range(copies)]
+        for r in raws:
+            r.view(n * k // 32, blk)[:, 1] = 0x20
+        x = torch.randn((1, k), generator=g, device=dev)
+        act, _ = ops.quantize_act(x, ops.Q8_0, ops.Q8_X86)
+        y = torch.empty((1, n), dtype=torch.float32, device=dev)
+        tmp = torch.empty(nb, dtype=torch.uint8, device=dev)
+        ms_raw = time_steps_graph(torch, lambda i: _lib().amv_mul_mat_vec_raw(
+            wtype, raws[i % copies].data_ptr(), k // 32 * blk, n, k, act.data_ptr(), 1, y.data_ptr(), n, None, st()),
+            1000, 100, min_reps=10, median=True)
+
+        def per_use(i):
+            _lib().amv_repack(wtype, raws[i % copies].data_ptr(), tmp.data_ptr(), n, k, st())
+            _lib().amv_mul_mat_vec(wtype, tmp.data_ptr(), n, k, act.data_ptr(), 1, y.data_ptr(), n, st())
+        ms_pu = time_steps_graph(torch, per_use, 500, 50, min_reps=10, median=True)
+        res[f"gemv_raw_{name}_14336x4096_us"] = round(ms_raw * 1e3, 3)
+        res[f"gemv_raw_{name}_gbs"] = round(nb / (ms_raw * 1e-3) / 1e9, 1)
+        res[f"gemv_repack_per_use_{name}_14336x4096_us"] = round(ms_pu * 1e3, 3)
+        log(f"bench: raw-layout GEMV {name} 14336x4096 cold {ms_raw * 1e3:.2f} us = "
+            f"{nb / (ms_raw * 1e-3) / 1e9:.0f} GB/s; repack per use + GEMV {ms_pu * 1e3:.2f} us")
+        del raws, tmp
     nb = _lib().amv_weight_bytes(ops.Q4_0, n, k)
     host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
     dst = torch.empty(nb, dtype=torch.uint8, device=dev)

@@ -94,6 +94,14 @@ int amv_quantize_q4_0(const float* x, int64_t n_rows, int64_t k, void* y_ggml, v
  * ---------------------------------------------------------------------------------------------------------- */
 int amv_mul_mat_vec(int wtype, const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst,
                     int64_t ldd, void* stream);
+/* MUL_MAT of m (1..8) activation columns on Q4_0 / Q8_0 weights still in ggml's block layout, read in place: the
+ * reference's raw-layout path (ameva_qmm.comp:315-372, reached from enc_mul_mat for a quantized src0 outside a WEIGHTS
+ * buffer, ggml-ameva.cpp:3607-3804). Row r of the weight starts at w + r * row_bytes (a row view keeps its parent's
+ * stride); k % 64 == 0, w and row_bytes dword-aligned. act: the plain Q8_0 activation of amv_quantize_act (m rows of
+ * k). dst[c * ldd + r] as amv_mul_mat_vec; with sums != NULL the exact block integers sums[(c * n_rows + r) * k/32 + b]
+ * are written instead (dst may then be NULL). */
+int amv_mul_mat_vec_raw(int wtype, const void* w, int64_t row_bytes, int64_t n_rows, int64_t k, const void* act,
+                        int64_t m, float* dst, int64_t ldd, int32_t* sums, void* stream);
 /* Parity instrumentation (no counterpart in the reference; for tests): while on != 0, the Q4_0 GEMV launches of this
  * process skip the dedicated K = 4096 kernels and run the generic one-column kernel of the same rows per wave, split
  * and epilogue, whose block-sum instantiation is the one amv_mul_mat_block_sums reads; the dedicated kernels keep

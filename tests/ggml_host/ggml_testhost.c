@@ -8,6 +8,7 @@
  * Built with -DGGML_TESTHOST_SKEW=1 it reads struct ggml_backend as a host whose ggml_backend_i has one member fewer
  * (device one slot earlier); with -DGGML_TESTHOST_SKEW=2 it cuts tensor names as a host built with GGML_MAX_NAME 128:
  * hosts the plugin must refuse. */
+#include <stddef.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -161,9 +162,12 @@ struct ggml_tensor* ggml_set_name(struct ggml_tensor* t, const char* name) {
 #else
     const size_t cap = sizeof(t->name);
 #endif
+    /* through a pointer into the whole allocation (new_tensor leaves 256 bytes behind the struct), not through the
+     * name[] array: indexing name[] past its 64 bytes would be undefined, and the optimiser exploits it */
+    char* dst = (char*)t + offsetof(struct ggml_tensor, name);
     size_t i = 0;
-    for (; i + 1 < cap && name[i]; ++i) t->name[i] = name[i];
-    t->name[i] = 0;
+    for (; i + 1 < cap && name[i]; ++i) dst[i] = name[i];
+    dst[i] = 0;
     return t;
 }
 

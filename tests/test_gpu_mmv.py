@@ -186,3 +186,48 @@ def test_gemv_full_size_linearity(dev, ops):
     y1 = ops.mul_mat(w, x)
     y2 = ops.mul_mat(w, x * 2)
     assert torch.equal(y2, y1 * 2)
+
+
+@pytest.mark.parametrize("wtype", [2, 8])
+@pytest.mark.parametrize("n,k,m,pad", [(14336, 4096, 1, 0), (4096, 14336, 1, 0), (3, 64, 1, 0), (257, 640, 3, 0),
+                                       (129, 2048, 8, 36), (64, 128, 2, 4)])
+def test_gemv_raw_blocks(dev, ops, orc, wtype, n, k, m, pad):
+    """amv_mul_mat_vec_raw: ggml's blocks read in place (the raw-layout MUL_MAT), rows of k/32 blocks plus `pad` bytes
+    (a row view of a wider tensor keeps its parent's stride): block integers bit-exact, f32 within the gates."""
+    rng = np.random.default_rng(n + k + m + pad + wtype)
+    wg = _q4_0_case(orc, rng, n, k) if wtype == 2 else _q8_0_case(orc, rng, n, k)
+    rb = wg.shape[1] + pad
+    rows = np.zeros((n, rb), np.uint8)
+    rows[:, : wg.shape[1]] = wg
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    a_ref = orc.quantize_q8_0(x, orc.Q8_X86)
+    y_ref, s_ref = orc.mul_mat(wtype, wg, n, k, a_ref, m, with_blocks=True)
+    wd = gpu(rows.reshape(-1), dev)
+    act, _ = ops.quantize_act(gpu(x, dev), ops.Q8_0, ops.Q8_X86)
+    s = torch.cuda.current_stream().cuda_stream
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    sums = torch.empty((m, n, k // 32), dtype=torch.int32, device=dev)
+    L = ops.lib()
+    assert L.amv_mul_mat_vec_raw(wtype, wd.data_ptr(), rb, n, k, act.data_ptr(), m, y.data_ptr(), n, None, s) == 0
+    assert L.amv_mul_mat_vec_raw(wtype, wd.data_ptr(), rb, n, k, act.data_ptr(), m, None, n, sums.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(sums.cpu().numpy(), s_ref)
+    y = y.cpu().numpy()
+    assert rel_l2(y, y_ref) < TOL_F32
+    per_output_gate(y, orc.dequantize(wtype, wg, k), dequant_act(a_ref, 8, k), what=f"raw {wtype} {n}x{k} m={m}")
+    # the repacked GEMV of the same weight agrees within the same gates
+    w = ops.QWeight.from_ggml(wtype, gpu(wg, dev), n, k)
+    y2 = ops.mul_mat_q(w, act, m).cpu().numpy()
+    assert rel_l2(y, y2) < 1e-6
+
+
+def test_gemv_raw_blocks_refuses_bad_shapes(dev, ops):
+    L = ops.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    w = torch.zeros(64 * 1024, dtype=torch.uint8, device=dev)
+    a = torch.zeros(64 * 1024, dtype=torch.uint8, device=dev)
+    y = torch.zeros(1024, dtype=torch.float32, device=dev)
+    assert L.amv_mul_mat_vec_raw(2, w.data_ptr(), 36, 4, 96, a.data_ptr(), 1, y.data_ptr(), 4, None, s) != 0  # k % 64
+    assert L.amv_mul_mat_vec_raw(2, w.data_ptr(), 36, 4, 64, a.data_ptr(), 9, y.data_ptr(), 4, None, s) != 0  # m > 8
+    assert L.amv_mul_mat_vec_raw(2, w.data_ptr(), 38, 4, 64, a.data_ptr(), 1, y.data_ptr(), 4, None, s) != 0  # stride
+    assert L.amv_mul_mat_vec_raw(12, w.data_ptr(), 144, 4, 256, a.data_ptr(), 1, y.data_ptr(), 4, None, s) != 0  # Q4_K
