@@ -278,33 +278,44 @@ __device__ __forceinline__ void amv_q8_0_lanes32(float v, int rule, int j, int8_
     if (j == 0) *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
 }
 // Q8_0 quantization of one 32-element block spread over 8 consecutive lanes (4 elements each, lane j of the 8 holds
-// elements 4j .. 4j + 3): the rules of amv_quantize_act. All 8 lanes must call it; stores 4 int8 per lane.
-__device__ __forceinline__ void q8_block_lanes8(const float (&v)[4], int rule, int j, int8_t* __restrict__ qs,
-                                                int2* __restrict__ meta) {
+// elements 4j .. 4j + 3): the rules of amv_quantize_act. All 8 lanes must call it; stores 4 int8 per lane. The rule
+// is uniform, so it is a branch to one of three instantiations rather than both roundings and both reciprocals in
+// every lane.
+template <int RULE>
+__device__ __forceinline__ void q8_block_lanes8_r(const float (&v)[4], int j, int8_t* __restrict__ qs,
+                                                  int2* __restrict__ meta) {
+    // the 8 lanes' max and sum by DPP within the lane octet (xor 1, xor 2, mirror of the half row): exact, so the
+    // order does not matter
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, AMV_WAVE));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, AMV_WAVE));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, AMV_WAVE));
+    amax = fmaxf(amax, __int_as_float(amv_dpp_i<0xB1>(__float_as_int(amax))));
+    amax = fmaxf(amax, __int_as_float(amv_dpp_i<0x4E>(__float_as_int(amax))));
+    amax = fmaxf(amax, __int_as_float(amv_dpp_i<0x141>(__float_as_int(amax))));
     const float d = amax / 127.0f;
     float id;
-    if (rule == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    if constexpr (RULE == AMV_Q8_X86) id = amax != 0.0f ? 127.0f / amax : 0.0f;
     else id = d != 0.0f ? 1.0f / d : 0.0f;
     uint32_t packed = 0;
     int s = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float t = v[e] * id;
-        float qf = rule == AMV_Q8_REF ? roundf(t) : rintf(t);
+        float qf = RULE == AMV_Q8_REF ? roundf(t) : rintf(t);
         qf = fminf(127.0f, fmaxf(-127.0f, qf));
         const int q = (int)qf;
         s += q;
         packed |= (uint32_t)(q & 0xFF) << (8 * e);
     }
-    s += __shfl_xor(s, 1, AMV_WAVE);
-    s += __shfl_xor(s, 2, AMV_WAVE);
-    s += __shfl_xor(s, 4, AMV_WAVE);
+    s += amv_dpp_i<0xB1>(s);
+    s += amv_dpp_i<0x4E>(s);
+    s += amv_dpp_i<0x141>(s);
     reinterpret_cast<uint32_t*>(qs)[j] = packed;
     if (j == 0) *meta = make_int2(__float_as_int(amv_h2f(amv_f2h(d))), s);
+}
+__device__ __forceinline__ void q8_block_lanes8(const float (&v)[4], int rule, int j, int8_t* __restrict__ qs,
+                                                int2* __restrict__ meta) {
+    if (rule == AMV_Q8_X86) q8_block_lanes8_r<AMV_Q8_X86>(v, j, qs, meta);
+    else if (rule == AMV_Q8_ARM) q8_block_lanes8_r<AMV_Q8_ARM>(v, j, qs, meta);
+    else q8_block_lanes8_r<AMV_Q8_REF>(v, j, qs, meta);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -421,13 +432,26 @@ __device__ __forceinline__ float4 amv_load4_coh(const float* p) {
 // ---------------------------------------------------------------------------------------------------------------
 // RMS_NORM of one row, shared by the norm kernel and the fused GEMV tail so that both produce the same bits. The
 // sum of squares is defined for 1024 virtual lanes: lane t sums the float4 chunks t, t + 1024, ... as f32 squares in
-// double, a 64-lane butterfly per virtual wave, then the 16 wave sums in order. A workgroup of NT threads (NT
+// double, amv_wave_sum_d_u per virtual wave (DPP within each row of 16 lanes, then the four row sums in order), then
+// the 16 wave sums by amv_rms_total. A workgroup of NT threads (NT
 // divides 1024) plays V = 1024 / NT virtual lanes per thread (t = tid + NT v) and loads all V chunks of a round
 // before summing, so a row of up to 1024 chunks costs one memory round trip (its w chunks load in the same one) and
 // its values stay in registers for the second pass: y = x * scale, o = y * w, act = the quantized o (y without w). Any output may be NULL; the chunks
 // of a quantization block sit in consecutive lanes as amv_act_store4 needs (n % 32 == 0 with Q8_0, % 256 with
 // Q8_K).
 #define AMV_RMS_VLANES 1024
+// the 16 virtual-wave sums in a fixed order: lanes 0..15 of each row hold sred[0..15], DPP within the row (xor 1,
+// xor 2, half-row mirror, row mirror), then lane 0's value, uniform over the wave. Every lane of the wave must call it.
+__device__ __forceinline__ double amv_rms_total(const double* sred) {
+    static_assert(AMV_RMS_VLANES / 64 == 16, "one row of 16 lanes holds the virtual-wave sums");
+    double v = sred[threadIdx.x & 15];
+    v += amv_dpp_d<0xB1>(v);
+    v += amv_dpp_d<0x4E>(v);
+    v += amv_dpp_d<0x141>(v);
+    v += amv_dpp_d<0x140>(v);
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), 0),
+                            __builtin_amdgcn_readlane(__double2loint(v), 0));
+}
 __device__ __forceinline__ float amv_rms_scale(double tot, int n, float eps) {
     const float mean = (float)(tot / (double)n);
     return 1.0f / sqrtf(mean + eps);
@@ -477,16 +501,11 @@ __device__ __forceinline__ void amv_rms_row(const float4* __restrict__ x4, int n
     }
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        double t = s[v];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, AMV_WAVE);
+        const double t = amv_wave_sum_d_u(s[v]);
         if ((tid & 63) == 0) sred[(tid + NT * v) >> 6] = t;
     }
     __syncthreads();
-    double tot = 0.0;
-#pragma unroll
-    for (int i = 0; i < AMV_RMS_VLANES / 64; ++i) tot += sred[i];
-    const float scale = amv_rms_scale(tot, 4 * n4, eps);
+    const float scale = amv_rms_scale(amv_rms_total(sred), 4 * n4, eps);
     if (n4 <= AMV_RMS_VLANES) {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
@@ -497,6 +516,46 @@ __device__ __forceinline__ void amv_rms_row(const float4* __restrict__ x4, int n
         for (int c = tid; c < n4; c += NT)
             amv_rms_chunk(c, x4[c], scale, w != nullptr, w ? w4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f), y, o, act);
     }
+}
+
+// amv_rms_row for a row of exactly 1024 float4 chunks (4096 values) with the MUL weight, in two parts so that a
+// kernel can issue other loads between them: amv_rms1024_load issues the row's x and w loads (before anything else,
+// so that waiting for them never waits for later loads), amv_rms1024_quant sums, meets in sred and writes the
+// quantized row to act (any AmvActOut, one pointing to LDS included). Same arithmetic and order as amv_rms_row, so
+// the same bytes.
+template <int NT>
+struct AmvRms1024 {
+    static constexpr int V = AMV_RMS_VLANES / NT;
+    float4 x[V], w[V];
+};
+template <int NT>
+__device__ __forceinline__ void amv_rms1024_load(const float4* __restrict__ x4, const float4* __restrict__ w4,
+                                                 AmvRms1024<NT>& r) {
+#pragma unroll
+    for (int v = 0; v < AmvRms1024<NT>::V; ++v) {
+        r.x[v] = x4[threadIdx.x + NT * v];
+        r.w[v] = w4[threadIdx.x + NT * v];
+    }
+}
+template <int NT>
+__device__ __forceinline__ void amv_rms1024_quant(const AmvRms1024<NT>& r, float eps, const AmvActOut& act,
+                                                  double* sred) {
+    constexpr int V = AmvRms1024<NT>::V;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        double t = 0.0;
+        t += (double)(r.x[v].x * r.x[v].x);
+        t += (double)(r.x[v].y * r.x[v].y);
+        t += (double)(r.x[v].z * r.x[v].z);
+        t += (double)(r.x[v].w * r.x[v].w);
+        t = amv_wave_sum_d_u(t);
+        if ((tid & 63) == 0) sred[(tid + NT * v) >> 6] = t;
+    }
+    __syncthreads();
+    const float scale = amv_rms_scale(amv_rms_total(sred), 4096, eps);
+#pragma unroll
+    for (int v = 0; v < V; ++v) amv_rms_chunk(tid + NT * v, r.x[v], scale, true, r.w[v], nullptr, nullptr, act);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

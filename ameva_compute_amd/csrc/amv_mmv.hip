@@ -111,7 +111,7 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
                                            int n_rows, float* __restrict__ dst, const float* __restrict__ epi,
                                            float* __restrict__ eout, const MmvPost& post, const MmvRopeAt& ra) {
     static_assert(EP != MMV_EP_ROPE_KV || R == 2, "ROPE pairs the two rows of a wave");
-    static_assert(!MMV_STACKED(EP) || R == 2 || R == 4, "stacked SWIGLU takes 1 or 2 outputs per wave");
+    static_assert(!MMV_STACKED(EP) || R == 2 || R == 4 || R == 8, "stacked SWIGLU takes 1, 2 or 4 outputs per wave");
     float t[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) t[r] = amv_wave_sum(acc[r]);
@@ -189,8 +189,8 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
     }
 }
 
-// Tails of EP 6 and EP 7, run by every thread of the workgroup after the epilogue stores.
-template <int EP, int S, int R>
+// Tails of EP 6 and EP 7, run by every thread of the workgroup (NW waves) after the epilogue stores.
+template <int EP, int S, int R, int NW = 4>
 __device__ __forceinline__ void mmv_tail(const MmvPost& post, const float* eout, int n_rows) {
     if constexpr (EP == MMV_EP_ADD_NORM) {
         if (!amv_arrive_last_tree(post.counters)) return;
@@ -199,9 +199,9 @@ __device__ __forceinline__ void mmv_tail(const MmvPost& post, const float* eout,
         amv_rms_row<256>(reinterpret_cast<const float4*>(eout), n_rows / 4, post.eps, post.norm_w, post.norm_y,
                          post.norm_o, post.act, sred);
     } else {
-        // a workgroup's (4 / S) (R / 2) outputs lie in one block of BS (the launcher checks that BS divides
+        // a workgroup's (NW / S) (R / 2) outputs lie in one block of BS (the launcher checks that BS divides
         // n_rows / 2); the first wave of the last workgroup quantizes it, 4 values per lane
-        constexpr int per_wg = 4 / S * (R / 2);
+        constexpr int per_wg = NW / S * (R / 2);
         const int BS = post.act.type == AMV_T_Q8_K ? 256 : 32;
         const int blk = (int)blockIdx.x * per_wg / BS;
         if (!amv_arrive_last(post.counters + AMV_CNT_STRIDE * blk, BS / per_wg)) return;
@@ -590,6 +590,167 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_ep(const uint4* __restri
         }
     }
     mmv_finish<2, EP, 1, SEG>(acc, lane, wi, 0, live, wave, n_rows, dst, epi, eout, post, ra);
+}
+
+// The lean K = 4096 GEMVs with the RMS_NORM before them folded in: every workgroup of NT threads computes
+// RMS_NORM(x) * norm_w and its Q8_0 quantization into LDS (amv_rms1024_*: k_rms_norm's arithmetic, the same bytes
+// as the activation that launch writes) instead of reading an activation written by a launch of its own, while its
+// weight rows stream in; then the dot products of k_mmv_q4_0_k4096_swiglu (EP 7: stacked gate|up + SWIGLU + Q8_0 of
+// the result, P outputs per wave) or k_mmv_q4_0_k4096_ep (EP 5: q/k/v + ROPE + cache rows, two rows per wave) with the
+// activation read from LDS: the same sums in the same order, so the same bits as the norm launch followed by the
+// plain lean kernel. Every wave issues its share of the row before any wave of the workgroup issues a weight load
+// (a barrier between them): a CU's vector memory returns its loads in order, so a row load queued behind weight
+// loads would wait for the weights (measured with per-wave timestamps: ~2 us at p90) and the norm would run after
+// them instead of under them. Sized for one workgroup per CU (NT = 1024; 192 and 224 workgroups for the Llama-3-8B
+// q/k/v and gate/up). EP 7 with NW P a multiple of 32: each workgroup owns whole Q8_0 blocks of the SWIGLU output and
+// quantizes them from LDS after a barrier, no arrival counters (k_mmv_q4_0_k4096_swiglu's values and rules).
+template <int NT, int EP, bool SEG, int P = 2>
+__global__ __launch_bounds__(NT) void k_mmv_q4_0_k4096_norm(const float4* __restrict__ x4,
+                                                            const float4* __restrict__ nw4, float eps, int rule,
+                                                            const uint4* __restrict__ wq,
+                                                            const uint32_t* __restrict__ wd2, int n_rows,
+                                                            float* __restrict__ dst, float* __restrict__ eout,
+                                                            const MmvPost post) {
+    constexpr int NW = NT / 64;
+    constexpr bool SW = EP == MMV_EP_SWIGLU_Q8;
+    constexpr int R = SW ? 2 * P : 2;
+    constexpr bool WG_TAIL = SW && (NW * P) % 32 == 0;
+    static_assert(SW || EP == MMV_EP_ROPE_KV, "EP 5 or EP 7");
+    static_assert(!SW || ((P == 2 || P == 4) && (WG_TAIL || 32 % (NW * P) == 0)),
+                  "a workgroup's outputs are whole Q8_0 blocks or lie in one");
+    __shared__ __align__(16) int8_t s_q[4096];
+    __shared__ __align__(16) int2 s_m[128];
+    __shared__ double sred[AMV_RMS_VLANES / 64];
+    __shared__ __align__(16) float s_h[WG_TAIL ? NW * P : 4];
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6;
+    const int wave = blockIdx.x * NW + wi;
+    AmvRms1024<NT> nr;
+    amv_rms1024_load<NT>(x4, nw4, nr);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();  // issue order only: no wait for the loads
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 w[2][R];
+    uint32_t dw[2][R / 2];
+    bool live;
+    if constexpr (SW) {
+        // gate rows o .. o + P - 1 and the same up rows; their scales in P / 2 row-pair dwords per matrix
+        const int F = n_rows >> 1;
+        live = P * wave < F;
+        const int o = min(P * wave, F - P);  // a wave past the end re-reads the last rows and stores nothing
+        const uint4* wg = wq;
+        const uint4* wu = wq;
+        const uint32_t* dg = wd2;
+        const uint32_t* du = wd2;
+        int ou = F + o;
+        if constexpr (SEG) {
+            wg = reinterpret_cast<const uint4*>(post.w_seg[0]);
+            wu = reinterpret_cast<const uint4*>(post.w_seg[1]);
+            dg = reinterpret_cast<const uint32_t*>(post.w_seg[0] + (size_t)F * 128 * 16);
+            du = reinterpret_cast<const uint32_t*>(post.w_seg[1] + (size_t)F * 128 * 16);
+            ou = o;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int j = 64 * u + lane;
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                w[u][i] = amv_ld_stream(wg + (size_t)(o + i) * 128 + j);
+                w[u][P + i] = amv_ld_stream(wu + (size_t)(ou + i) * 128 + j);
+            }
+#pragma unroll
+            for (int q = 0; q < P / 2; ++q) {
+                dw[u][q] = amv_ld_stream(dg + (size_t)((o >> 1) + q) * 128 + j);
+                dw[u][P / 2 + q] = amv_ld_stream(du + (size_t)((ou >> 1) + q) * 128 + j);
+            }
+        }
+    } else {
+        live = 2 * wave < n_rows;
+        int row0 = min(2 * wave, n_rows - 2);
+        const uint4* wqs = wq;
+        const uint32_t* wds = wd2;
+        if constexpr (SEG) {
+            int lr;
+            const int sg = mmv_seg(post, row0, lr);
+            const size_t rows_s = (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]);
+            wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
+            wds = reinterpret_cast<const uint32_t*>(post.w_seg[sg] + rows_s * 128 * 16);
+            row0 = lr;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int j = 64 * u + lane;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) w[u][r] = amv_ld_stream(wqs + (size_t)(row0 + r) * 128 + j);
+            dw[u][0] = amv_ld_stream(wds + (size_t)(row0 >> 1) * 128 + j);
+        }
+    }
+    // the norm's arithmetic waits for the row only; everything after it for the weights too
+    __builtin_amdgcn_sched_barrier(0);
+    const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);
+    amv_rms1024_quant<NT>(nr, eps, AmvActOut{s_q, s_m, nullptr, AMV_T_Q8_0, rule}, sred);
+    __syncthreads();
+    int4 a0[2], a1[2];
+    int2 ds[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = 64 * u + lane;
+        a0[u] = reinterpret_cast<const int4*>(s_q)[2 * j];
+        a1[u] = reinterpret_cast<const int4*>(s_q)[2 * j + 1];
+        ds[u] = s_m[j];
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float da = __int_as_float(ds[u].x);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint4 q = w[u][r];
+            int s = amv_dot4((int)(q.x & M4), a0[u].x, 0);
+            s = amv_dot4((int)(q.y & M4), a0[u].y, s);
+            s = amv_dot4((int)(q.z & M4), a0[u].z, s);
+            s = amv_dot4((int)(q.w & M4), a0[u].w, s);
+            s = amv_dot4((int)((q.x >> 4) & M4), a1[u].x, s);
+            s = amv_dot4((int)((q.y >> 4) & M4), a1[u].y, s);
+            s = amv_dot4((int)((q.z >> 4) & M4), a1[u].z, s);
+            s = amv_dot4((int)((q.w >> 4) & M4), a1[u].w, s);
+            s -= 8 * ds[u].y;
+            const uint32_t d2 = dw[u][r >> 1];
+            acc[r] = fmaf((float)s, amv_h2f((r & 1) ? d2 >> 16 : d2) * da, acc[r]);
+        }
+    }
+    if constexpr (WG_TAIL) {
+        const int F = n_rows >> 1;
+        float t[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) t[r] = amv_wave_sum(acc[r]);
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                const int o = P * wave + i;
+                if (o >= F) break;
+                if (dst) {
+                    dst[o] = t[i];
+                    dst[o + F] = t[P + i];
+                }
+                const float h = mmv_silu(t[i]) * t[P + i];
+                eout[o] = h;
+                s_h[P * wi + i] = h;
+            }
+        }
+        __syncthreads();
+        constexpr int NQ = NW * P / 4;  // chunks of 4 outputs in the workgroup: whole 8-lane Q8_0 blocks
+        const int c = (int)blockIdx.x * NQ + (int)threadIdx.x;
+        if (threadIdx.x < NQ && 4 * c < F) {  // whole blocks only (F % 32 == 0)
+            const float4 v4 = reinterpret_cast<const float4*>(s_h)[threadIdx.x];
+            const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+            amv_act_store4(post.act, c, v);
+        }
+    } else {
+        mmv_finish<R, EP, 1, SEG>(acc, lane, wi, 0, live, wave, n_rows, dst, nullptr, eout, post, ra);
+        if constexpr (SW) mmv_tail<EP, 1, R, NW>(post, eout, n_rows);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ Q8_0 x Q8_0
@@ -1446,4 +1607,99 @@ extern "C" int amv_gemv_swiglu_q8(int wtype, const void* w, int64_t n_rows, int6
     rc = mmv_dispatch_fused(MMV_EP_SWIGLU_Q8, a, act, amv_stream(stream));
     if (rc) return rc;
     return amv_check_launch("amv_gemv_swiglu_q8");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// RMS_NORM (* norm_w, Q8_0) folded into the Q4_0 K = 4096 decode GEMV after it (k_mmv_q4_0_k4096_norm).
+static std::atomic<int> g_norm_nt{0};
+extern "C" void amv_debug_norm_gemv_threads(int nt) { g_norm_nt.store(nt, std::memory_order_relaxed); }
+
+template <int EP, bool SEG, int P = 2>
+static void launch_norm_gemv(int nt, int waves, const float* x, const float* nw, float eps, int rule, const MmvArgs& a,
+                             hipStream_t st) {
+    const int64_t nblk = (int64_t)a.n_rows * 128;
+    const uint4* wq = SEG ? nullptr : reinterpret_cast<const uint4*>(a.w);
+    const uint32_t* wd = SEG ? nullptr : reinterpret_cast<const uint32_t*>(a.w + nblk * 16);
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* w4 = reinterpret_cast<const float4*>(nw);
+#define AMV_NORM_LAUNCH(NT)                                                                                        \
+    hipLaunchKernelGGL((k_mmv_q4_0_k4096_norm<NT, EP, SEG, P>),                                                 \
+                       dim3((unsigned)((waves + NT / 64 - 1) / (NT / 64))), dim3(NT), 0, st, x4, w4, eps, rule, wq, wd, \
+                       a.n_rows, a.dst, a.eout, a.post)
+    if (nt == 256) AMV_NORM_LAUNCH(256);
+    else if (nt == 512) AMV_NORM_LAUNCH(512);
+    else AMV_NORM_LAUNCH(1024);
+#undef AMV_NORM_LAUNCH
+}
+
+static int norm_gemv_checks(const char* fn, const float* x, const float* nw, int rule, int wtype, const void* w,
+                            int64_t n_rows, int64_t k) {
+    AMV_REQUIRE(x && nw && w, "%s: null pointer", fn);
+    AMV_REQUIRE(wtype == AMV_T_Q4_0, "%s: weight type %d (Q4_0)", fn, wtype);
+    AMV_REQUIRE(k == 4096, "%s: k %lld (the folded norm takes rows of 4096)", fn, (long long)k);
+    AMV_REQUIRE(n_rows > 0 && n_rows % 2 == 0 && n_rows <= (1 << 24), "%s: n_rows %lld (even)", fn,
+                (long long)n_rows);
+    AMV_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)nw & 15) == 0 && ((uintptr_t)w & 15) == 0,
+                "%s: x, norm_w and w must be 16-byte aligned", fn);
+    AMV_REQUIRE(rule >= AMV_Q8_X86 && rule <= AMV_Q8_REF, "%s: bad rule", fn);
+    return AMV_OK;
+}
+
+extern "C" int amv_rms_norm_gemv_rope_kv(const float* x, const float* norm_w, float eps, int rule, int wtype,
+                                         const void* w, int64_t n_rows, int64_t k, float* qkv, int64_t n_head,
+                                         int64_t n_head_kv, int64_t D, const int32_t* pos, float freq_base,
+                                         float freq_scale, float attn_factor, void* k_cache, void* v_cache,
+                                         int64_t cache_row, const int64_t* kv_idx, int64_t cache_rows,
+                                         unsigned int* bad, void* stream) {
+    const char* fn = "amv_rms_norm_gemv_rope_kv";
+    int rc = norm_gemv_checks(fn, x, norm_w, rule, wtype, w, n_rows, k);
+    if (rc) return rc;
+    AMV_REQUIRE(qkv && pos && k_cache && v_cache && kv_idx, "%s: null pointer", fn);
+    AMV_REQUIRE(n_head > 0 && n_head_kv > 0 && D > 0 && D % 2 == 0 && n_rows == (n_head + 2 * n_head_kv) * D,
+                "%s: n_rows %lld != (n_head + 2 n_head_kv) * D", fn, (long long)n_rows);
+    AMV_REQUIRE(cache_row >= n_head_kv * D && cache_rows > 0, "%s: cache row %lld < %lld", fn, (long long)cache_row,
+                (long long)(n_head_kv * D));
+    MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, qkv, nullptr, nullptr, nullptr};
+    MmvPost& p = a.post;
+    p.pos = pos;
+    p.theta_scale = powf(freq_base, -2.0f / (float)D);  // amv_rope's expression with n_dims = D
+    p.freq_scale = freq_scale;
+    p.attn_factor = attn_factor;
+    p.n_q = (int)(n_head * D);
+    p.n_k = (int)(n_head_kv * D);
+    p.head_dim = (int)D;
+    p.k_cache = (uint16_t*)k_cache;
+    p.v_cache = (uint16_t*)v_cache;
+    p.cache_row = cache_row;
+    p.kv_idx = kv_idx;
+    p.cache_rows = cache_rows;
+    p.bad = bad;
+    const int nt = g_norm_nt.load(std::memory_order_relaxed);
+    launch_norm_gemv<MMV_EP_ROPE_KV, false>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, rule, a,
+                                            amv_stream(stream));
+    return amv_check_launch(fn);
+}
+
+extern "C" int amv_rms_norm_gemv_swiglu_q8(const float* x, const float* norm_w, float eps, int rule, int wtype,
+                                           const void* w, int64_t n_rows, int64_t k, float* dst, float* eout,
+                                           void* act_out, unsigned int* counters, void* stream) {
+    const char* fn = "amv_rms_norm_gemv_swiglu_q8";
+    int rc = norm_gemv_checks(fn, x, norm_w, rule, wtype, w, n_rows, k);
+    if (rc) return rc;
+    AMV_REQUIRE(eout && act_out && counters, "%s: null pointer", fn);
+    AMV_REQUIRE(n_rows % 64 == 0, "%s: n_rows must be 2 x a multiple of 32 (gate rows, then up rows)", fn);
+    AMV_REQUIRE(((uintptr_t)act_out & 15) == 0 && ((uintptr_t)eout & 15) == 0,
+                "%s: act_out and eout must be 16-byte aligned", fn);
+    MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, dst, nullptr, nullptr, eout};
+    MmvPost& p = a.post;
+    p.counters = counters;
+    p.act = amv_act_out(act_out, n_rows / 2, AMV_T_Q8_0, rule);
+    const int nt = g_norm_nt.load(std::memory_order_relaxed);
+    if (nt < 0)  // instrumentation: -NT threads, four outputs per wave
+        launch_norm_gemv<MMV_EP_SWIGLU_Q8, false, 4>(-nt, (int)(n_rows / 8), x, norm_w, eps, rule, a,
+                                                     amv_stream(stream));
+    else  // two outputs per wave, 1024 threads by default
+        launch_norm_gemv<MMV_EP_SWIGLU_Q8, false>(nt ? nt : 1024, (int)(n_rows / 4), x, norm_w, eps, rule, a,
+                                                  amv_stream(stream));
+    return amv_check_launch(fn);
 }

@@ -179,6 +179,24 @@ int amv_gemv_rope_kv_seg(int wtype, const void* wq, const void* wk, const void* 
 int amv_gemv_swiglu_q8_seg(int wtype, const void* w_gate, const void* w_up, int64_t F, int64_t k, const void* act,
                            float* eout, void* act_out, int act_type, int rule, unsigned int* counters, void* stream);
 
+/* The RMS_NORM node before a decode GEMV folded into it (the reference runs RMS_NORM + MUL and the MUL_MAT as graph
+ * nodes, ggml-ameva.cpp:3607-3804 / ameva_rms_norm.comp:39-91; no single counterpart): the GEMV takes the f32 row x
+ * (4096 values), RMS_NORM(x, eps) * norm_w and its Q8_0 quantization with `rule` are computed inside (amv_rms_norm_act's
+ * arithmetic, the same bytes), and the rest is amv_gemv_rope_kv / amv_gemv_swiglu_q8 (act_type Q8_0, the same
+ * `rule`) over that activation, bit for bit. Q4_0 weights of k = 4096, even row counts; x and norm_w 16-byte aligned.
+ * No activation buffer is written for the norm. */
+int amv_rms_norm_gemv_rope_kv(const float* x, const float* norm_w, float eps, int rule, int wtype, const void* w,
+                              int64_t n_rows, int64_t k, float* qkv, int64_t n_head, int64_t n_head_kv, int64_t D,
+                              const int32_t* pos, float freq_base, float freq_scale, float attn_factor, void* k_cache,
+                              void* v_cache, int64_t cache_row, const int64_t* kv_idx, int64_t cache_rows,
+                              unsigned int* bad, void* stream);
+int amv_rms_norm_gemv_swiglu_q8(const float* x, const float* norm_w, float eps, int rule, int wtype, const void* w,
+                                int64_t n_rows, int64_t k, float* dst, float* eout, void* act_out,
+                                unsigned int* counters, void* stream);
+/* Measurement instrumentation (no counterpart in the reference): threads per workgroup of the folded-norm GEMVs
+ * (256, 512 or 1024; 0 = the default). */
+void amv_debug_norm_gemv_threads(int nt);
+
 /* Parity instrumentation of the same kernels: the exact integer sums per weight block, int32
  * [m][n_rows][nblk * per] with nblk = k / block size, per = 2 for Q4_K (sum sc*dot, sum m*bsum) and 1 otherwise.
  * These are the per-block int32 sums of ggml's vec_dot (bit-exact contract). */

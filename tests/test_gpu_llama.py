@@ -173,9 +173,10 @@ def _fill_caches(layer, dev, seed):
 
 @pytest.mark.parametrize("wtype", [2, 12])
 def test_fused_chain_matches_unfused(dev, wtype):
-    """Two chained layers, fused (5 launches per layer: the first layer's down GEMV computes the second layer's
-    attention norm and its activation row) against one launch per node: identical outputs, K/V rows and activation
-    rows, for Q4_0 (Q8_0 activations) and Q4_K (Q8_K activations) weights."""
+    """Two chained layers, fused (Q4_0: 6 launches per layer, each RMS_NORM folded into the GEMV after it; Q4_K: 8,
+    the first layer's step ending with the second layer's attention norm and its activation row) against one launch
+    per node: identical outputs, K/V rows and activation rows, for Q4_0 (Q8_0 activations) and Q4_K (Q8_K
+    activations) weights."""
     from ameva_compute_amd.llama import random_layer
     layers = [random_layer(dev, seed=21 + i, ctx=512, wtype=wtype) for i in range(2)]
     for i, lay in enumerate(layers):
@@ -202,7 +203,8 @@ def test_fused_chain_matches_unfused(dev, wtype):
     for i, lay in enumerate(layers):
         assert torch.equal(lay.k_cache, ref[2][i]) and torch.equal(lay.v_cache, ref[3][i])
         assert torch.equal(lay.act_ff, ref[4][i])
-    assert torch.equal(layers[1].act_h, ref[5])
+    if not layers[1].fold_norm:  # a folded norm keeps its activation row in LDS
+        assert torch.equal(layers[1].act_h, ref[5])
 
 
 def test_decode_graph_replays_at_growing_positions(dev):
