@@ -51,6 +51,9 @@ SIGNATURES = {
     "amv_rms_norm_gemv_rope_kv": (I32, [P, P, F32, I32, I32, P, I64, I64, P, I64, I64, I64, P, F32, F32, F32, P, P,
                                         I64, P, I64, P, P]),
     "amv_rms_norm_gemv_swiglu_q8": (I32, [P, P, F32, I32, I32, P, I64, I64, P, P, P, P, P]),
+    "amv_rms_norm_gemv_rope_kv_seg": (I32, [P, P, F32, I32, I32, P, P, P, I64, P, P, P, I64, I64, I64, P, F32, F32,
+                                            F32, P, P, I64, P, I64, P, P]),
+    "amv_rms_norm_gemv_swiglu_q8_seg": (I32, [P, P, F32, I32, I32, P, P, I64, I64, P, P, P, P]),
     "amv_debug_norm_gemv_threads": (None, [I32]),
     "amv_flash_attn_decode_ex": (I32, [P, P, P, P, P, I64, I64, I64, P, I64, I64, I64, I64, I64, F32, P, I64, P, P,
                                           I32, I32, P]),

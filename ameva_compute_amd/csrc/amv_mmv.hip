@@ -1703,3 +1703,75 @@ extern "C" int amv_rms_norm_gemv_swiglu_q8(const float* x, const float* norm_w, 
                                                   amv_stream(stream));
     return amv_check_launch(fn);
 }
+
+extern "C" int amv_rms_norm_gemv_rope_kv_seg(const float* x, const float* norm_w, float eps, int rule, int wtype,
+                                             const void* wq, const void* wk, const void* wv, int64_t k, float* q_out,
+                                             float* k_out, float* v_out, int64_t n_head, int64_t n_head_kv, int64_t D,
+                                             const int32_t* pos, float freq_base, float freq_scale,
+                                             float attn_factor, void* k_cache, void* v_cache, int64_t cache_row,
+                                             const int64_t* kv_idx, int64_t cache_rows, unsigned int* bad,
+                                             void* stream) {
+    const char* fn = "amv_rms_norm_gemv_rope_kv_seg";
+    AMV_REQUIRE(n_head > 0 && n_head_kv > 0 && D > 0 && D % 2 == 0, "%s: bad heads", fn);
+    const int64_t n_rows = (n_head + 2 * n_head_kv) * D;
+    int rc = norm_gemv_checks(fn, x, norm_w, rule, wtype, wq, n_rows, k);
+    if (rc) return rc;
+    AMV_REQUIRE(q_out && k_out && v_out && pos && k_cache && v_cache && kv_idx, "%s: null pointer", fn);
+    AMV_REQUIRE(cache_row >= n_head_kv * D && cache_rows > 0, "%s: cache row %lld < %lld", fn, (long long)cache_row,
+                (long long)(n_head_kv * D));
+    MmvArgs a{wtype, (const uint8_t*)wq, (int)n_rows, (int)k, nullptr, nullptr, nullptr, q_out, nullptr, nullptr,
+              nullptr};
+    MmvPost& p = a.post;
+    const void* ws[3] = {wq, wk, wv};
+    const int64_t rows[3] = {n_head * D, n_head_kv * D, n_head_kv * D};
+    rc = mmv_segments(fn, p, 3, ws, rows, wtype, k);
+    if (rc) return rc;
+    p.dst_seg[0] = q_out;
+    p.dst_seg[1] = k_out;
+    p.dst_seg[2] = v_out;
+    p.pos = pos;
+    p.theta_scale = powf(freq_base, -2.0f / (float)D);  // amv_rope's expression with n_dims = D
+    p.freq_scale = freq_scale;
+    p.attn_factor = attn_factor;
+    p.n_q = (int)(n_head * D);
+    p.n_k = (int)(n_head_kv * D);
+    p.head_dim = (int)D;
+    p.k_cache = (uint16_t*)k_cache;
+    p.v_cache = (uint16_t*)v_cache;
+    p.cache_row = cache_row;
+    p.kv_idx = kv_idx;
+    p.cache_rows = cache_rows;
+    p.bad = bad;
+    const int nt = g_norm_nt.load(std::memory_order_relaxed);
+    launch_norm_gemv<MMV_EP_ROPE_KV, true>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, rule, a,
+                                           amv_stream(stream));
+    return amv_check_launch(fn);
+}
+
+extern "C" int amv_rms_norm_gemv_swiglu_q8_seg(const float* x, const float* norm_w, float eps, int rule, int wtype,
+                                               const void* w_gate, const void* w_up, int64_t F, int64_t k,
+                                               float* eout, void* act_out, unsigned int* counters, void* stream) {
+    const char* fn = "amv_rms_norm_gemv_swiglu_q8_seg";
+    int rc = norm_gemv_checks(fn, x, norm_w, rule, wtype, w_gate, 2 * F, k);
+    if (rc) return rc;
+    AMV_REQUIRE(eout && act_out && counters, "%s: null pointer", fn);
+    AMV_REQUIRE(F > 0 && F % 32 == 0, "%s: F must be a multiple of 32", fn);
+    AMV_REQUIRE(((uintptr_t)act_out & 15) == 0 && ((uintptr_t)eout & 15) == 0,
+                "%s: act_out and eout must be 16-byte aligned", fn);
+    MmvArgs a{wtype, (const uint8_t*)w_gate, (int)(2 * F), (int)k, nullptr, nullptr, nullptr, nullptr, nullptr,
+              nullptr, eout};
+    MmvPost& p = a.post;
+    const void* ws[2] = {w_gate, w_up};
+    const int64_t rows[2] = {F, F};
+    rc = mmv_segments(fn, p, 2, ws, rows, wtype, k);
+    if (rc) return rc;
+    p.counters = counters;
+    p.act = amv_act_out(act_out, F, AMV_T_Q8_0, rule);
+    const int nt = g_norm_nt.load(std::memory_order_relaxed);
+    if (nt < 0)
+        launch_norm_gemv<MMV_EP_SWIGLU_Q8, true, 4>(-nt, (int)(F / 4), x, norm_w, eps, rule, a, amv_stream(stream));
+    else
+        launch_norm_gemv<MMV_EP_SWIGLU_Q8, true>(nt ? nt : 1024, (int)(F / 2), x, norm_w, eps, rule, a,
+                                                 amv_stream(stream));
+    return amv_check_launch(fn);
+}

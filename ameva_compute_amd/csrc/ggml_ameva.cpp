@@ -13,6 +13,8 @@
 //     quantized activations of one src1 are reused by every MUL_MAT that reads it (the a8_src cache, 2738-2749);
 //   * RMS_NORM followed by a MUL by the norm weight runs as one kernel (ameva_find_fusion, 4345), and a one-row
 //     MUL_MAT followed by ADD or GLU SWIGLU (split) by the GEMV's epilogue (the reference's MUL_MAT fusion pairs);
+//     llama.cpp's q/k/v (+ ROPE, SET_ROWS) and gate/up (+ SWIGLU) node groups run as one launch each, and for Q4_0
+//     weights at K = 4096 the RMS_NORM + MUL before such a group is computed inside it (no launch of its own);
 //   * counters and failure injection as ggml-ameva.h:30-98.
 // On MI355X the Vulkan hazard tracking of the reference (ameva_record, 2174) is the in-order stream itself: each
 // kernel starts after the previous one has finished, so no barrier bookkeeping is needed.
@@ -1147,6 +1149,96 @@ struct Engine {
         return true;
     }
 
+    // RMS_NORM + MUL by a one-row norm weight whose product feeds only the q/k/v group or the gate/up group right
+    // after them: the norm is computed inside that group's launch (amv_rms_norm_gemv_*_seg: per workgroup, into LDS,
+    // the bytes the norm launch would write) for Q4_0 weights at K = 4096. Neither the RMS_NORM nor the MUL output is
+    // written, so both must be read by nothing else and not be graph outputs; the norm's input is read by every
+    // workgroup during the launch, so no output of the group may overlap it.
+    struct NormFold {
+        const ggml_tensor *norm, *mul;
+        QkvGroup qg;
+        GateUp gu;
+        bool qkv;
+        int last;
+    };
+    bool match_norm_fold(int i, NormFold& f) const {
+        const ggml_tensor* n = graph->nodes[i];
+        const ggml_tensor* m = fusable_mul(graph, i);
+        if (!m) return false;
+        const ggml_tensor* x = n->src[0];
+        if (x->type != GGML_TYPE_F32 || nrows(x) != 1 || x->ne[0] != 4096 || !is_contiguous(x) || !aligned16(x->data))
+            return false;
+        constexpr int32_t FLAG_OUTPUT = 2;  // GGML_TENSOR_FLAG_OUTPUT
+        if ((n->flags | m->flags) & FLAG_OUTPUT) return false;
+        int j = i + 2;
+        while (j < graph->n_nodes && noop(graph->nodes[j]->op)) ++j;
+        if (j >= graph->n_nodes) return false;
+        const ggml_tensor* c = graph->nodes[j];
+        if (c->op != GGML_OP_MUL_MAT || c->src[1]->data != m->data || c->src[0]->type != GGML_TYPE_Q4_0 ||
+            c->src[0]->ne[0] != 4096)
+            return false;
+        f.norm = n;
+        f.mul = m;
+        if (match_qkv(j, f.qg)) {
+            f.qkv = true;
+            f.last = f.qg.last;
+            for (const ggml_tensor* o : {f.qg.rq, f.qg.rk, f.qg.mv, f.qg.sk, f.qg.sv})
+                if (overlaps(o, x)) return false;
+        } else if (match_gate_up(j, f.gu) && f.gu.atype == (int)GGML_TYPE_Q8_0) {
+            f.qkv = false;
+            f.last = f.gu.last;
+            if (overlaps(f.gu.glu, x)) return false;
+        } else {
+            return false;
+        }
+        std::vector<int> group;
+        for (int g = i; g <= f.last; ++g) group.push_back(g);
+        return !read_outside(n, group) && !read_outside(m, group);
+    }
+    bool run_norm_fold(const NormFold& f) {
+        const ggml_tensor* x = f.norm->src[0];
+        const ggml_tensor* w = f.mul->src[0] == f.norm ? f.mul->src[1] : f.mul->src[0];
+        const float eps = op_f32(f.norm, 0);
+        if (f.qkv) {
+            const QkvGroup& q = f.qg;
+            const int wt = q.mq->src[0]->type;
+            const int64_t K = q.mq->src[0]->ne[0];
+            const ggml_tensor *qi = q.rq->src[0], *ki = q.rk->src[0];
+            const void* wq = weight_ptr(q.mq);
+            const void* wk = wq ? weight_ptr(q.mk) : nullptr;
+            const void* wv = wk ? weight_ptr(q.mv) : nullptr;
+            if (!wv) return false;
+            if (!rc(q.mq, amv_rms_norm_gemv_rope_kv_seg(
+                              (const float*)x->data, (const float*)w->data, eps, AMV_Q8_X86, wt, wq, wk, wv, K,
+                              (float*)q.rq->data, (float*)q.rk->data, (float*)q.mv->data, qi->ne[1], ki->ne[1],
+                              qi->ne[0], (const int32_t*)q.rq->src[1]->data, op_f32(q.rq, 5), op_f32(q.rq, 6),
+                              op_f32(q.rq, 8), q.sk->data, q.sv->data, (int64_t)q.sk->nb[1] / 2,
+                              (const int64_t*)q.sk->src[1]->data, q.sk->ne[1], dev->status, st)))
+                return false;
+            g_cnt.mul_mat += 3;
+            g_cnt.qmv += 3;
+            g_cnt.fused += 8;  // the norm, its MUL, k, v, both ROPEs and both SET_ROWS ride on the q launch
+            return true;
+        }
+        const GateUp& u = f.gu;
+        const int wt = u.gate->src[0]->type;
+        const int64_t K = u.gate->src[0]->ne[0], F = u.gate->src[0]->ne[1];
+        const void* wg = weight_ptr(u.gate);
+        const void* wu = wg ? weight_ptr(u.up) : nullptr;
+        if (!wu) return false;
+        void* act_out = fused_act(u.glu, u.glu, u.atype);
+        if (!act_out) return false;
+        if (!rc(u.gate, amv_rms_norm_gemv_swiglu_q8_seg((const float*)x->data, (const float*)w->data, eps, AMV_Q8_X86,
+                                                        wt, wg, wu, F, K, (float*)u.glu->data, act_out, dev->counters,
+                                                        st)))
+            return false;
+        pending_act = {u.glu->data, nbytes(u.glu), u.atype, 1, F, act_out};
+        g_cnt.mul_mat += 2;
+        g_cnt.qmv += 2;
+        g_cnt.fused += 4;  // the norm, its MUL, up and SWIGLU ride on the gate launch
+        return true;
+    }
+
     bool run(ggml_cgraph* g) {
         graph = g;
         const bool prof = profile_level() >= 2;
@@ -1159,11 +1251,17 @@ struct Engine {
             if (noop(n->op)) continue;
             const ggml_tensor* first = n;
             bool ok = true;
-            if (n->op == GGML_OP_MUL_MAT && g_fail.load() == AMEVA_FAIL_NONE) {
+            if ((n->op == GGML_OP_MUL_MAT || n->op == GGML_OP_RMS_NORM) && g_fail.load() == AMEVA_FAIL_NONE) {
                 QkvGroup qg;
                 GateUp gu;
+                NormFold nf;
                 int last = -1;
-                if (match_qkv(i, qg)) {
+                if (n->op == GGML_OP_RMS_NORM) {
+                    if (match_norm_fold(i, nf)) {
+                        ok = run_norm_fold(nf);
+                        last = nf.last;
+                    }
+                } else if (match_qkv(i, qg)) {
                     ok = run_qkv(qg);
                     last = qg.last;
                 } else if (match_gate_up(i, gu)) {

@@ -193,8 +193,18 @@ int amv_rms_norm_gemv_rope_kv(const float* x, const float* norm_w, float eps, in
 int amv_rms_norm_gemv_swiglu_q8(const float* x, const float* norm_w, float eps, int rule, int wtype, const void* w,
                                 int64_t n_rows, int64_t k, float* dst, float* eout, void* act_out,
                                 unsigned int* counters, void* stream);
+/* The same over separate matrices (llama.cpp's q, k, v and gate, up tensors; the segment rules of
+ * amv_gemv_rope_kv_seg / amv_gemv_swiglu_q8_seg), bit for bit the stacked calls. */
+int amv_rms_norm_gemv_rope_kv_seg(const float* x, const float* norm_w, float eps, int rule, int wtype, const void* wq,
+                                  const void* wk, const void* wv, int64_t k, float* q_out, float* k_out, float* v_out,
+                                  int64_t n_head, int64_t n_head_kv, int64_t D, const int32_t* pos, float freq_base,
+                                  float freq_scale, float attn_factor, void* k_cache, void* v_cache, int64_t cache_row,
+                                  const int64_t* kv_idx, int64_t cache_rows, unsigned int* bad, void* stream);
+int amv_rms_norm_gemv_swiglu_q8_seg(const float* x, const float* norm_w, float eps, int rule, int wtype,
+                                    const void* w_gate, const void* w_up, int64_t F, int64_t k, float* eout,
+                                    void* act_out, unsigned int* counters, void* stream);
 /* Measurement instrumentation (no counterpart in the reference): threads per workgroup of the folded-norm GEMVs
- * (256, 512 or 1024; 0 = the default). */
+ * (256, 512 or 1024; a negative value -NT: the gate/up launches with four outputs per wave; 0 = the default). */
 void amv_debug_norm_gemv_threads(int nt);
 
 /* Parity instrumentation of the same kernels: the exact integer sums per weight block, int32

@@ -378,7 +378,8 @@ def test_quantized_kv_cache_nodes(plugin, orc, t):
 def test_llama3_8b_decode_layer(plugin, orc, wt):
     """One decoder layer of Llama-3-8B shape, bs1 decode at position 4095 with 4095 cached tokens, Q4_0 weights (Q8_0
     activations) or Q4_K weights (Q8_K activations): the plugin runs it as 8 launches (RMS_NORM + MUL, q/k/v with ROPE
-    and both SET_ROWS, the attention split and merge, o + ADD, RMS_NORM + MUL, gate/up + SWIGLU, down + ADD)."""
+    and both SET_ROWS, the attention split and merge, o + ADD, RMS_NORM + MUL, gate/up + SWIGLU, down + ADD), Q4_0 as 6
+    (each RMS_NORM + MUL computed inside the q/k/v and gate/up launches)."""
     rng = np.random.default_rng(2024)
     H, NH, NKV, D, FF, CTX = 4096, 32, 8, 128, 14336, 4096
     pos_t = CTX - 1
@@ -443,12 +444,13 @@ def test_llama3_8b_decode_layer(plugin, orc, wt):
         assert g.compute() == gp.STATUS_SUCCESS
         y = g.get(out, np.float32, (1, H))
         assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 7
-        # nodes run inside another node's launch: the MUL of both RMS_NORM + MUL (2); k, v, both ROPEs and both
-        # SET_ROWS in the q launch (6); up and SWIGLU in the gate launch (2); the residual ADDs of o and down (2)
-        assert gp.counter(plugin, "fused_pair_count") == 12
-        # the q/k/v and gate/up launches read the rows the two RMS_NORM + MUL write, o the one the attention merge
-        # writes, down the one the gate/up launch writes
-        assert gp.counter(plugin, "act_quant_reuse_count") == 4
+        # nodes run inside another node's launch: the MUL of both RMS_NORM + MUL (2; Q4_0: both nodes of each, 4);
+        # k, v, both ROPEs and both SET_ROWS in the q launch (6); up and SWIGLU in the gate launch (2); the residual
+        # ADDs of o and down (2)
+        assert gp.counter(plugin, "fused_pair_count") == (14 if wt == gp.Q4_0 else 12)
+        # o reads the row the attention merge writes, down the one the gate/up launch writes; Q4_K: the q/k/v and
+        # gate/up launches also read the rows the two RMS_NORM + MUL write (Q4_0 computes them inside)
+        assert gp.counter(plugin, "act_quant_reuse_count") == (2 if wt == gp.Q4_0 else 4)
 
         # the oracle's chain of the same ops
         def q8(a):
@@ -645,5 +647,87 @@ def test_qkv_group_declined_when_outputs_share_memory(plugin, orc):
         assert np.array_equal(np.delete(kc_out, pos_t, axis=0).view(np.uint16),
                               np.delete(kc, pos_t, axis=0).view(np.uint16))
         assert rel_l2(g.get(VC, np.float16, (CTX, NKV * D))[pos_t], mm("v").reshape(-1).astype(np.float16)) < 1e-3
+    finally:
+        g.free()
+
+
+@pytest.mark.parametrize("guard", ["none", "extra_read", "output_flag", "x_shared"])
+def test_norm_fold_and_its_guards(plugin, orc, guard):
+    """RMS_NORM + MUL before a Q4_0 q/k/v or gate/up node group at K = 4096 runs inside that group's launch, and only
+    when its product is read by nothing else, is not a graph output and no output of the group shares the norm
+    input's memory: a later MUL reading the normed row, the OUTPUT flag on it, or the SWIGLU output placed over the
+    FFN input each make the plugin run the norm as a launch of its own. Every graph matches the oracle's chain."""
+    rng = np.random.default_rng(321)
+    H, NH, NKV, D, FF, CTX, pos_t = 4096, 4, 2, 128, 1024, 64, 41
+    eps, base = 1e-5, 500000.0
+    def wq4(n, k):
+        return orc.quantize_q4_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    w = {"q": wq4(NH * D, H), "k": wq4(NKV * D, H), "v": wq4(NKV * D, H), "gate": wq4(FF, H), "up": wq4(FF, H),
+         "down": wq4(H, FF)}
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    x2 = rng.standard_normal((1, H)).astype(np.float32)
+    an = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    fn = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    e = rng.standard_normal((1, H)).astype(np.float32)
+    kc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    vc = rng.standard_normal((CTX, NKV * D)).astype(np.float16)
+    g = gp.Graph(sum(a.nbytes for a in w.values()) + 16 * 4096, 16 << 20)
+    try:
+        T = {k_: g.tensor(gp.Q4_0, [a.shape[1] * 32 // 18, a.shape[0]], "w", k_) for k_, a in w.items()}
+        for k_, a in w.items():
+            g.set(T[k_], a)
+        AN, FN = g.tensor(gp.F32, [H], "w", "an"), g.tensor(gp.F32, [H], "w", "fn")
+        g.set(AN, an)
+        g.set(FN, fn)
+        X, X2, E = g.tensor(gp.F32, [H, 1], "c", "x"), g.tensor(gp.F32, [H, 1], "c", "x2"), g.tensor(gp.F32, [H, 1], "c", "e")
+        g.set(X, x)
+        g.set(X2, x2)
+        g.set(E, e)
+        POS, IDX = g.tensor(gp.I32, [1], "c", "pos"), g.tensor(gp.I64, [1], "c", "idx")
+        g.set(POS, np.array([pos_t], np.int32))
+        g.set(IDX, np.array([pos_t], np.int64))
+        KC, VC = g.tensor(gp.F16, [NKV * D, CTX], "c", "kc"), g.tensor(gp.F16, [NKV * D, CTX], "c", "vc")
+        g.set(KC, kc)
+        g.set(VC, vc)
+        cur = g.mul(g.rms_norm(X, eps), AN)
+        q = g.rope(g.reshape_3d(g.mul_mat(T["q"], cur), D, NH, 1), POS, D, 0, base)
+        k = g.rope(g.reshape_3d(g.mul_mat(T["k"], cur), D, NKV, 1), POS, D, 0, base)
+        v = g.mul_mat(T["v"], cur)
+        g.set_rows(KC, g.view_nd(k, gp.OP_RESHAPE, [NKV * D, 1], [4, NKV * D * 4, NKV * D * 4, NKV * D * 4]), IDX)
+        g.set_rows(VC, v, IDX)
+        cur2 = g.mul(g.rms_norm(X2, eps), FN)
+        ff = g.swiglu(g.mul_mat(T["gate"], cur2), g.mul_mat(T["up"], cur2))
+        y = g.mul_mat(T["down"], ff)  # the one-row GEMV the gate/up group writes the activation row for
+        if guard == "extra_read":
+            ye = g.mul(cur, E)
+        elif guard == "output_flag":
+            cur2.flags = 2  # GGML_TENSOR_FLAG_OUTPUT
+        elif guard == "x_shared":
+            ff.data = X2.data  # the SWIGLU output over the FFN norm's input (dead after the norm in node order)
+        plugin.ggml_backend_ameva_reset_counters()
+        assert g.compute() == gp.STATUS_SUCCESS
+        fused = gp.counter(plugin, "fused_pair_count")
+        # folded: the norm, its MUL, k, v, both ROPEs and both SET_ROWS in the q launch (8); the norm, its MUL, up and
+        # SWIGLU in the gate launch (4); a declined fold keeps the RMS_NORM + MUL pair (1) before its group
+        assert fused == {"none": 12, "extra_read": 7 + 4, "output_flag": 8 + 3, "x_shared": 8 + 3}[guard]
+
+        q8 = lambda a: orc.quantize_q8_0(a, orc.Q8_X86)  # noqa: E731
+        def mm(name, a):
+            return orc.mul_mat(gp.Q4_0, w[name], w[name].shape[0], H, q8(a), 1)
+        _, c = orc.rms_norm(x, eps, an)
+        _, c2 = orc.rms_norm(x2, eps, fn)
+        p = np.array([pos_t], np.int32)
+        qr = orc.rope(mm("q", c).reshape(1, NH, D), p, D, 0, base)
+        kr = orc.rope(mm("k", c).reshape(1, NKV, D), p, D, 0, base)
+        assert rel_l2(g.get(q, np.float32, (1, NH, D)), qr) < 1e-3
+        assert rel_l2(g.get(KC, np.float16, (CTX, NKV * D))[pos_t], kr.reshape(-1).astype(np.float16)) < 1e-3
+        assert rel_l2(g.get(VC, np.float16, (CTX, NKV * D))[pos_t], mm("v", c).reshape(-1).astype(np.float16)) < 1e-3
+        h = orc.swiglu(mm("gate", c2), mm("up", c2))
+        assert rel_l2(g.get(ff, np.float32, (1, FF)), h) < 1e-3
+        assert rel_l2(g.get(y, np.float32, (1, H)), orc.mul_mat(gp.Q4_0, w["down"], H, FF, q8(h), 1)) < 2e-3
+        if guard == "extra_read":
+            assert rel_l2(g.get(ye, np.float32, (1, H)), c * e) < 1e-6
+        if guard == "output_flag":
+            assert rel_l2(g.get(cur2, np.float32, (1, H)), c2) < 1e-6
     finally:
         g.free()
