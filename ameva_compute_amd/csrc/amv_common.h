@@ -337,11 +337,27 @@ __device__ __forceinline__ AmvQ8K amv_q8_K_lanes64(const float (&v)[4], int lane
         const float a = fabsf(v[e]);
         if (a > am) { am = a; ai = 4 * lane + e; }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float om = __shfl_xor(am, o, AMV_WAVE);
-        const int oi = __shfl_xor(ai, o, AMV_WAVE);
+    // (largest magnitude, then smallest index) is an exact, order-free choice: DPP within each row of 16 lanes (xor
+    // 1, xor 2, half-row mirror, row mirror), then the four rows' picks through scalar registers
+    const auto pick = [&](float om, int oi) {
         if (om > am || (om == am && oi < ai)) { am = om; ai = oi; }
+    };
+    pick(__int_as_float(amv_dpp_i<0xB1>(__float_as_int(am))), amv_dpp_i<0xB1>(ai));
+    pick(__int_as_float(amv_dpp_i<0x4E>(__float_as_int(am))), amv_dpp_i<0x4E>(ai));
+    pick(__int_as_float(amv_dpp_i<0x141>(__float_as_int(am))), amv_dpp_i<0x141>(ai));
+    pick(__int_as_float(amv_dpp_i<0x140>(__float_as_int(am))), amv_dpp_i<0x140>(ai));
+    {
+        const int ab = __float_as_int(am);
+        float bm = __int_as_float(__builtin_amdgcn_readlane(ab, 0));
+        int bi = __builtin_amdgcn_readlane(ai, 0);
+#pragma unroll
+        for (int row = 16; row < 64; row += 16) {
+            const float om = __int_as_float(__builtin_amdgcn_readlane(ab, row));
+            const int oi = __builtin_amdgcn_readlane(ai, row);
+            if (om > bm || (om == bm && oi < bi)) { bm = om; bi = oi; }
+        }
+        am = bm;
+        ai = bi;
     }
     if (am == 0.0f) {
         r.q[0] = r.q[1] = r.q[2] = r.q[3] = 0;
@@ -349,7 +365,8 @@ __device__ __forceinline__ AmvQ8K amv_q8_K_lanes64(const float (&v)[4], int lane
         r.d = 0.0f;
         return r;
     }
-    const float mx = __shfl(v[ai & 3], ai >> 2, AMV_WAVE);
+    const float vsel = (ai & 3) == 0 ? v[0] : ((ai & 3) == 1 ? v[1] : ((ai & 3) == 2 ? v[2] : v[3]));
+    const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vsel), ai >> 2));
     const float iscale = -127.0f / mx;
     int s = 0;
 #pragma unroll
@@ -358,8 +375,8 @@ __device__ __forceinline__ AmvQ8K amv_q8_K_lanes64(const float (&v)[4], int lane
         r.q[e] = t < 127 ? t : 127;
         s += r.q[e];
     }
-    s += __shfl_xor(s, 1, AMV_WAVE);
-    s += __shfl_xor(s, 2, AMV_WAVE);
+    s += amv_dpp_i<0xB1>(s);
+    s += amv_dpp_i<0x4E>(s);
     r.s16 = s;
     r.d = 1.0f / iscale;
     return r;

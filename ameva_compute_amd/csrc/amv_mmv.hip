@@ -914,6 +914,92 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
     }
 }
 
+// k_mmv_q4_K at K = 4096 (S = 1) with the RMS_NORM before it folded in, as k_mmv_q4_0_k4096_norm: every workgroup
+// of NT threads issues its share of the row x and the norm weight, then (after a barrier, so that no row load waits
+// behind a weight load of the CU) every weight slice and super-block head of its waves (both 64-slice steps), then
+// computes RMS_NORM(x) * norm_w and its Q8_K quantization into LDS (amv_rms1024_*: k_rms_norm's bytes) while the
+// weights stream in, and dots them in k_mmv_q4_K's order: the same bits as the norm launch followed by that kernel.
+// EP 5 (q/k/v + ROPE + cache rows) or EP 7 (stacked gate|up + SWIGLU + Q8_K tail, one output per wave with R = 2).
+template <int NT, int EP, bool SEG, int R = 2>
+__global__ __launch_bounds__(NT) void k_mmv_q4_K_norm(const float4* __restrict__ x4, const float4* __restrict__ nw4,
+                                                      float eps, const uint4* __restrict__ wq,
+                                                      const uint4* __restrict__ wh, int n_rows,
+                                                      float* __restrict__ dst, float* __restrict__ eout,
+                                                      const MmvPost post) {
+    constexpr int NW = NT / 64, NSL = 128, NSB = 16;  // K = 4096: 16-byte weight slices and super-blocks per row
+    static_assert(EP == MMV_EP_ROPE_KV || EP == MMV_EP_SWIGLU_Q8, "EP 5 or EP 7");
+    __shared__ __align__(16) int8_t s_q[4096];
+    __shared__ __align__(16) float s_d[NSB];
+    __shared__ __align__(16) int32_t s_s16[256];
+    __shared__ double sred[AMV_RMS_VLANES / 64];
+    const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6;
+    const int wave = blockIdx.x * NW + wi;
+    const bool live = mmv_wave_live<EP>(wave, R, n_rows);
+    AmvRms1024<NT> nr;
+    amv_rms1024_load<NT>(x4, nw4, nr);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();  // issue order only: no wait for the loads
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 q[2][R];
+    uint32_t hv[2][R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int row = min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
+        const uint4* wqs = wq;
+        const uint4* whs = wh;
+        if constexpr (SEG) {  // the row's matrix: qs of its rows, then their 16-byte heads
+            int lr;
+            const int sg = mmv_seg(post, row, lr);
+            wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
+            whs = wqs + (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]) * NSL;
+            row = lr;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int j = 64 * u + lane, sb = j >> 3;
+            q[u][r] = amv_ld_stream(wqs + (size_t)row * NSL + j);
+            hv[u][r] = amv_ld_stream(reinterpret_cast<const uint32_t*>(whs + (size_t)row * NSB + sb) + (lane & 3));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);
+    amv_rms1024_quant<NT>(nr, eps, AmvActOut{s_q, s_d, s_s16, AMV_T_Q8_K, 0}, sred);
+    __syncthreads();
+    const int4* a4 = reinterpret_cast<const int4*>(s_q);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = 64 * u + lane;
+        const int sb = j >> 3, t = j & 7, c = t >> 1, h = t & 1;
+        const int4 alo = a4[sb * 16 + 4 * c + h], ahi = a4[sb * 16 + 4 * c + 2 + h];
+        const float da = s_d[sb];
+        const int bslo = s_s16[sb * 16 + 4 * c + h], bshi = s_s16[sb * 16 + 4 * c + 2 + h];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            // the super-block head: lane l of each quad loaded dword l, DPP hands every lane all four
+            const uint32_t h0 = hv[u][r];
+            const uint4 hd = make_uint4(__builtin_amdgcn_mov_dpp(h0, 0x00, 0xF, 0xF, false),
+                                        __builtin_amdgcn_mov_dpp(h0, 0x55, 0xF, 0xF, false),
+                                        __builtin_amdgcn_mov_dpp(h0, 0xAA, 0xF, 0xF, false),
+                                        __builtin_amdgcn_mov_dpp(h0, 0xFF, 0xF, 0xF, false));
+            int sl, ml, sh, mh;
+            k4_scale_min_pair(c, hd.y, hd.z, hd.w, sl, ml, sh, mh);
+            const uint4 w = q[u][r];
+            const uint4 lo = make_uint4(w.x & M4, w.y & M4, w.z & M4, w.w & M4);
+            const uint4 hi = make_uint4((w.x >> 4) & M4, (w.y >> 4) & M4, (w.z >> 4) & M4, (w.w >> 4) & M4);
+            const int isum = sl * dot16(lo, alo, 0) + sh * dot16(hi, ahi, 0);
+            const int msum = ml * bslo + mh * bshi;
+            const float d = amv_h2f(hd.x) * da, dmin = amv_h2f(hd.x >> 16) * da;
+            acc[r] = fmaf(d, (float)isum, acc[r]);
+            acc[r] = fmaf(-dmin, (float)msum, acc[r]);
+        }
+    }
+    mmv_finish<R, EP, 1, SEG>(acc, lane, wi, 0, live, wave, n_rows, dst, nullptr, eout, post, ra);
+    if constexpr (EP == MMV_EP_SWIGLU_Q8) mmv_tail<EP, 1, R, NW>(post, eout, n_rows);
+}
+
 template <int R, bool BLOCK_SUMS, int EP, int S>
 __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, const uint4* __restrict__ wqh,
                                                  const uint4* __restrict__ wsc, const uint16_t* __restrict__ wd,
@@ -1632,10 +1718,26 @@ static void launch_norm_gemv(int nt, int waves, const float* x, const float* nw,
 #undef AMV_NORM_LAUNCH
 }
 
+template <int EP, bool SEG>
+static void launch_norm_gemv_q4k(int nt, int waves, const float* x, const float* nw, float eps, const MmvArgs& a,
+                                 hipStream_t st) {
+    const uint4* wq = SEG ? nullptr : reinterpret_cast<const uint4*>(a.w);
+    const uint4* wh = SEG ? nullptr : reinterpret_cast<const uint4*>(a.w + (size_t)a.n_rows * 16 * 128);
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* w4 = reinterpret_cast<const float4*>(nw);
+#define AMV_NORM_K_LAUNCH(NT)                                                                                      \
+    hipLaunchKernelGGL((k_mmv_q4_K_norm<NT, EP, SEG>), dim3((unsigned)((waves + NT / 64 - 1) / (NT / 64))),       \
+                       dim3(NT), 0, st, x4, w4, eps, wq, wh, a.n_rows, a.dst, a.eout, a.post)
+    if (nt == 256) AMV_NORM_K_LAUNCH(256);
+    else if (nt == 512) AMV_NORM_K_LAUNCH(512);
+    else AMV_NORM_K_LAUNCH(1024);
+#undef AMV_NORM_K_LAUNCH
+}
+
 static int norm_gemv_checks(const char* fn, const float* x, const float* nw, int rule, int wtype, const void* w,
                             int64_t n_rows, int64_t k) {
     AMV_REQUIRE(x && nw && w, "%s: null pointer", fn);
-    AMV_REQUIRE(wtype == AMV_T_Q4_0, "%s: weight type %d (Q4_0)", fn, wtype);
+    AMV_REQUIRE(wtype == AMV_T_Q4_0 || wtype == AMV_T_Q4_K, "%s: weight type %d (Q4_0 or Q4_K)", fn, wtype);
     AMV_REQUIRE(k == 4096, "%s: k %lld (the folded norm takes rows of 4096)", fn, (long long)k);
     AMV_REQUIRE(n_rows > 0 && n_rows % 2 == 0 && n_rows <= (1 << 24), "%s: n_rows %lld (even)", fn,
                 (long long)n_rows);
@@ -1675,8 +1777,12 @@ extern "C" int amv_rms_norm_gemv_rope_kv(const float* x, const float* norm_w, fl
     p.cache_rows = cache_rows;
     p.bad = bad;
     const int nt = g_norm_nt.load(std::memory_order_relaxed);
-    launch_norm_gemv<MMV_EP_ROPE_KV, false>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, rule, a,
-                                            amv_stream(stream));
+    if (wtype == AMV_T_Q4_K)
+        launch_norm_gemv_q4k<MMV_EP_ROPE_KV, false>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, a,
+                                                    amv_stream(stream));
+    else
+        launch_norm_gemv<MMV_EP_ROPE_KV, false>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, rule, a,
+                                                amv_stream(stream));
     return amv_check_launch(fn);
 }
 
@@ -1687,15 +1793,19 @@ extern "C" int amv_rms_norm_gemv_swiglu_q8(const float* x, const float* norm_w, 
     int rc = norm_gemv_checks(fn, x, norm_w, rule, wtype, w, n_rows, k);
     if (rc) return rc;
     AMV_REQUIRE(eout && act_out && counters, "%s: null pointer", fn);
-    AMV_REQUIRE(n_rows % 64 == 0, "%s: n_rows must be 2 x a multiple of 32 (gate rows, then up rows)", fn);
+    const int bs = wtype == AMV_T_Q4_K ? 256 : 32;  // the output activation: Q8_K for Q4_K, Q8_0 for Q4_0
+    AMV_REQUIRE(n_rows % (2 * bs) == 0, "%s: n_rows must be 2 x a multiple of %d (gate rows, then up rows)", fn, bs);
     AMV_REQUIRE(((uintptr_t)act_out & 15) == 0 && ((uintptr_t)eout & 15) == 0,
                 "%s: act_out and eout must be 16-byte aligned", fn);
     MmvArgs a{wtype, (const uint8_t*)w, (int)n_rows, (int)k, nullptr, nullptr, nullptr, dst, nullptr, nullptr, eout};
     MmvPost& p = a.post;
     p.counters = counters;
-    p.act = amv_act_out(act_out, n_rows / 2, AMV_T_Q8_0, rule);
+    p.act = amv_act_out(act_out, n_rows / 2, wtype == AMV_T_Q4_K ? AMV_T_Q8_K : AMV_T_Q8_0, rule);
     const int nt = g_norm_nt.load(std::memory_order_relaxed);
-    if (nt < 0)  // instrumentation: -NT threads, four outputs per wave
+    if (wtype == AMV_T_Q4_K)
+        launch_norm_gemv_q4k<MMV_EP_SWIGLU_Q8, false>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, a,
+                                                      amv_stream(stream));
+    else if (nt < 0)  // instrumentation: -NT threads, four outputs per wave
         launch_norm_gemv<MMV_EP_SWIGLU_Q8, false, 4>(-nt, (int)(n_rows / 8), x, norm_w, eps, rule, a,
                                                      amv_stream(stream));
     else  // two outputs per wave, 1024 threads by default
@@ -1743,8 +1853,12 @@ extern "C" int amv_rms_norm_gemv_rope_kv_seg(const float* x, const float* norm_w
     p.cache_rows = cache_rows;
     p.bad = bad;
     const int nt = g_norm_nt.load(std::memory_order_relaxed);
-    launch_norm_gemv<MMV_EP_ROPE_KV, true>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, rule, a,
-                                           amv_stream(stream));
+    if (wtype == AMV_T_Q4_K)
+        launch_norm_gemv_q4k<MMV_EP_ROPE_KV, true>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, a,
+                                                   amv_stream(stream));
+    else
+        launch_norm_gemv<MMV_EP_ROPE_KV, true>(nt > 0 ? nt : 1024, (int)(n_rows / 2), x, norm_w, eps, rule, a,
+                                               amv_stream(stream));
     return amv_check_launch(fn);
 }
 
@@ -1755,7 +1869,8 @@ extern "C" int amv_rms_norm_gemv_swiglu_q8_seg(const float* x, const float* norm
     int rc = norm_gemv_checks(fn, x, norm_w, rule, wtype, w_gate, 2 * F, k);
     if (rc) return rc;
     AMV_REQUIRE(eout && act_out && counters, "%s: null pointer", fn);
-    AMV_REQUIRE(F > 0 && F % 32 == 0, "%s: F must be a multiple of 32", fn);
+    const int bs = wtype == AMV_T_Q4_K ? 256 : 32;  // the output activation: Q8_K for Q4_K, Q8_0 for Q4_0
+    AMV_REQUIRE(F > 0 && F % bs == 0, "%s: F must be a multiple of %d", fn, bs);
     AMV_REQUIRE(((uintptr_t)act_out & 15) == 0 && ((uintptr_t)eout & 15) == 0,
                 "%s: act_out and eout must be 16-byte aligned", fn);
     MmvArgs a{wtype, (const uint8_t*)w_gate, (int)(2 * F), (int)k, nullptr, nullptr, nullptr, nullptr, nullptr,
@@ -1766,9 +1881,12 @@ extern "C" int amv_rms_norm_gemv_swiglu_q8_seg(const float* x, const float* norm
     rc = mmv_segments(fn, p, 2, ws, rows, wtype, k);
     if (rc) return rc;
     p.counters = counters;
-    p.act = amv_act_out(act_out, F, AMV_T_Q8_0, rule);
+    p.act = amv_act_out(act_out, F, wtype == AMV_T_Q4_K ? AMV_T_Q8_K : AMV_T_Q8_0, rule);
     const int nt = g_norm_nt.load(std::memory_order_relaxed);
-    if (nt < 0)
+    if (wtype == AMV_T_Q4_K)
+        launch_norm_gemv_q4k<MMV_EP_SWIGLU_Q8, true>(nt > 0 ? nt : 1024, (int)F, x, norm_w, eps, a,
+                                                     amv_stream(stream));
+    else if (nt < 0)
         launch_norm_gemv<MMV_EP_SWIGLU_Q8, true, 4>(-nt, (int)(F / 4), x, norm_w, eps, rule, a, amv_stream(stream));
     else
         launch_norm_gemv<MMV_EP_SWIGLU_Q8, true>(nt ? nt : 1024, (int)(F / 2), x, norm_w, eps, rule, a,

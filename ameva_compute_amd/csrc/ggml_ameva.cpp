@@ -13,8 +13,8 @@
 //     quantized activations of one src1 are reused by every MUL_MAT that reads it (the a8_src cache, 2738-2749);
 //   * RMS_NORM followed by a MUL by the norm weight runs as one kernel (ameva_find_fusion, 4345), and a one-row
 //     MUL_MAT followed by ADD or GLU SWIGLU (split) by the GEMV's epilogue (the reference's MUL_MAT fusion pairs);
-//     llama.cpp's q/k/v (+ ROPE, SET_ROWS) and gate/up (+ SWIGLU) node groups run as one launch each, and for Q4_0
-//     weights at K = 4096 the RMS_NORM + MUL before such a group is computed inside it (no launch of its own);
+//     llama.cpp's q/k/v (+ ROPE, SET_ROWS) and gate/up (+ SWIGLU) node groups run as one launch each, and at K = 4096
+//     the RMS_NORM + MUL before a Q4_0 group or a Q4_K q/k/v group is computed inside it (no launch of its own);
 //   * counters and failure injection as ggml-ameva.h:30-98.
 // On MI355X the Vulkan hazard tracking of the reference (ameva_record, 2174) is the in-order stream itself: each
 // kernel starts after the previous one has finished, so no barrier bookkeeping is needed.
@@ -1151,7 +1151,8 @@ struct Engine {
 
     // RMS_NORM + MUL by a one-row norm weight whose product feeds only the q/k/v group or the gate/up group right
     // after them: the norm is computed inside that group's launch (amv_rms_norm_gemv_*_seg: per workgroup, into LDS,
-    // the bytes the norm launch would write) for Q4_0 weights at K = 4096. Neither the RMS_NORM nor the MUL output is
+    // the bytes the norm launch would write) at K = 4096: q/k/v groups of Q4_0 or Q4_K weights, gate/up groups of
+    // Q4_0 weights whose SWIGLU row feeds a Q8_0 GEMV. Neither the RMS_NORM nor the MUL output is
     // written, so both must be read by nothing else and not be graph outputs; the norm's input is read by every
     // workgroup during the launch, so no output of the group may overlap it.
     struct NormFold {
@@ -1174,9 +1175,11 @@ struct Engine {
         while (j < graph->n_nodes && noop(graph->nodes[j]->op)) ++j;
         if (j >= graph->n_nodes) return false;
         const ggml_tensor* c = graph->nodes[j];
-        if (c->op != GGML_OP_MUL_MAT || c->src[1]->data != m->data || c->src[0]->type != GGML_TYPE_Q4_0 ||
+        const ggml_type wt = c->src[0]->type;
+        if (c->op != GGML_OP_MUL_MAT || c->src[1]->data != m->data || (wt != GGML_TYPE_Q4_0 && wt != GGML_TYPE_Q4_K) ||
             c->src[0]->ne[0] != 4096)
             return false;
+        const int out_act = wt == GGML_TYPE_Q4_K ? (int)GGML_TYPE_Q8_K : (int)GGML_TYPE_Q8_0;
         f.norm = n;
         f.mul = m;
         if (match_qkv(j, f.qg)) {
@@ -1184,7 +1187,8 @@ struct Engine {
             f.last = f.qg.last;
             for (const ggml_tensor* o : {f.qg.rq, f.qg.rk, f.qg.mv, f.qg.sk, f.qg.sv})
                 if (overlaps(o, x)) return false;
-        } else if (match_gate_up(j, f.gu) && f.gu.atype == (int)GGML_TYPE_Q8_0) {
+        } else if (wt == GGML_TYPE_Q4_0 && match_gate_up(j, f.gu) && f.gu.atype == out_act) {
+            // (Q4_K keeps its FFN norm launch: that fold measured slower on the 32-layer model)
             f.qkv = false;
             f.last = f.gu.last;
             if (overlaps(f.gu.glu, x)) return false;

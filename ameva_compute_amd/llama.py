@@ -61,10 +61,14 @@ class LlamaLayer:
         self.n_kv = 1
         # arrival counters of the gate/up launch's quantization (self-resetting)
         self.cnt = torch.zeros(ops.swiglu_counter_words(wgu.n_rows), dtype=torch.int32, device=dev)
-        # Q4_0 weights at H = 4096: the fused step folds both RMS_NORMs into the GEMV after them
+        # Q4_0 / Q4_K weights at H = 4096: the fused step folds both RMS_NORMs into the GEMV after them
         # (amv_rms_norm_gemv_rope_kv / amv_rms_norm_gemv_swiglu_q8, the same bytes as the norm launch)
-        self.fold_norm = (wq.type == ops.Q4_0 and wgu.type == ops.Q4_0 and self.H == 4096
-                          and wgu.n_rows % 64 == 0)
+        self.fold_norm = (wq.type in (ops.Q4_0, ops.Q4_K) and wgu.type == wq.type and self.H == 4096
+                          and self.FF % (256 if wq.type == ops.Q4_K else 32) == 0)
+        # measured on the 32-layer Q4_K model: the FFN fold of Q4_K costs more than its norm launch (1688 against
+        # 1677 us per token with the attention fold alone), so Q4_K folds the attention norm only
+        self.fold_attn = self.fold_norm
+        self.fold_ffn = self.fold_norm and wq.type == ops.Q4_0
 
     @staticmethod
     def stack_rows(*blocks: torch.Tensor) -> torch.Tensor:
@@ -89,9 +93,10 @@ class LlamaLayer:
         in self.act_h); q/k/v GEMV + ROPE + KV stores; FA split; FA merge + quantization (key count from device
         memory); o GEMV + ADD; FFN RMS_NORM + MUL + quantization; gate/up GEMV + SWIGLU + quantization; down GEMV +
         ADD, then next_layer's attention RMS_NORM + quantization into next_layer.act_h when given (call
-        next_layer.decode with act_ready=True). With fold_norm (Q4_0, H = 4096) 6 launches: each RMS_NORM is computed
-        inside the GEMV after it, per workgroup while its weights stream in (act_h, act_h2, t_o and t_o2 are then not
-        written, act_ready is ignored and next_layer gets no norm launch when it folds its own). Merged into the GEMV
+        next_layer.decode with act_ready=True). With fold_attn / fold_ffn (Q4_0 at H = 4096: both, 6 launches; Q4_K: the
+        attention norm, 7) an RMS_NORM is computed inside the GEMV after it, per workgroup while its weights stream in
+        (act_h / t_o or act_h2 / t_o2 are then not written, act_ready is ignored and next_layer gets no norm launch
+        when it folds its own). Merged into the GEMV
         before them (amv_gemv_add_rms_norm) the norms ran slower on MI355X.
         fused=False: one launch per graph node (16 for Q4_0; the K-quant types quantize in separate launches and take
         19), the key count from the host. Both give identical results."""
@@ -100,7 +105,7 @@ class LlamaLayer:
         q8 = at == ops.Q8_0
         P = lambda t: t.data_ptr()  # noqa: E731
         if fused:
-            if self.fold_norm:
+            if self.fold_attn:
                 check(L.amv_rms_norm_gemv_rope_kv(P(x), P(self.attn_norm), self.eps, ops.Q8_X86, self.wqkv.type,
                                                   P(self.wqkv.data), self.wqkv.n_rows, H, P(self.qkv), self.n_head,
                                                   self.n_head_kv, D, P(self.pos), self.base, 1.0, 1.0,
@@ -122,7 +127,7 @@ class LlamaLayer:
                   "flash_attn (split, merge + quantization)")
             check(L.amv_mul_mat_vec_ep(self.wo.type, P(self.wo.data), H, H, P(self.act_att), None, ops.EP_ADD, P(x),
                                        P(self.x1), st), "wo + residual")
-            if self.fold_norm:
+            if self.fold_ffn:
                 check(L.amv_rms_norm_gemv_swiglu_q8(P(self.x1), P(self.ffn_norm), self.eps, ops.Q8_X86, self.wgu.type,
                                                     P(self.wgu.data), self.wgu.n_rows, H, None, P(self.h),
                                                     P(self.act_ff), cnt, st), "ffn norm + gate_up + swiglu + quant")
@@ -134,7 +139,7 @@ class LlamaLayer:
                       "gate_up + swiglu + quantization")
             check(L.amv_mul_mat_vec_ep(self.wdown.type, P(self.wdown.data), H, FF, P(self.act_ff), None,
                                        ops.EP_ADD, P(self.x1), P(out), st), "down + residual")
-            if next_layer is not None and not next_layer.fold_norm:
+            if next_layer is not None and not next_layer.fold_attn:
                 nl = next_layer
                 check(L.amv_rms_norm_act(P(out), 1, H, nl.eps, P(nl.attn_norm), None, P(nl.t_o), P(nl.act_h),
                                          nl.atype, ops.Q8_X86, st), "next attention norm")

@@ -182,9 +182,9 @@ int amv_gemv_swiglu_q8_seg(int wtype, const void* w_gate, const void* w_up, int6
 /* The RMS_NORM node before a decode GEMV folded into it (the reference runs RMS_NORM + MUL and the MUL_MAT as graph
  * nodes, ggml-ameva.cpp:3607-3804 / ameva_rms_norm.comp:39-91; no single counterpart): the GEMV takes the f32 row x
  * (4096 values), RMS_NORM(x, eps) * norm_w and its Q8_0 quantization with `rule` are computed inside (amv_rms_norm_act's
- * arithmetic, the same bytes), and the rest is amv_gemv_rope_kv / amv_gemv_swiglu_q8 (act_type Q8_0, the same
- * `rule`) over that activation, bit for bit. Q4_0 weights of k = 4096, even row counts; x and norm_w 16-byte aligned.
- * No activation buffer is written for the norm. */
+ * arithmetic, the same bytes), and the rest is amv_gemv_rope_kv / amv_gemv_swiglu_q8 over that activation, bit for
+ * bit. Q4_0 weights (Q8_0 activations with `rule`; act_out Q8_0) or Q4_K weights (Q8_K; act_out Q8_K) of k = 4096,
+ * even row counts; x and norm_w 16-byte aligned. No activation buffer is written for the norm. */
 int amv_rms_norm_gemv_rope_kv(const float* x, const float* norm_w, float eps, int rule, int wtype, const void* w,
                               int64_t n_rows, int64_t k, float* qkv, int64_t n_head, int64_t n_head_kv, int64_t D,
                               const int32_t* pos, float freq_base, float freq_scale, float attn_factor, void* k_cache,

@@ -203,7 +203,7 @@ def test_fused_chain_matches_unfused(dev, wtype):
     for i, lay in enumerate(layers):
         assert torch.equal(lay.k_cache, ref[2][i]) and torch.equal(lay.v_cache, ref[3][i])
         assert torch.equal(lay.act_ff, ref[4][i])
-    if not layers[1].fold_norm:  # a folded norm keeps its activation row in LDS
+    if not layers[1].fold_attn:  # a folded norm keeps its activation row in LDS
         assert torch.equal(layers[1].act_h, ref[5])
 
 

@@ -377,9 +377,9 @@ def test_quantized_kv_cache_nodes(plugin, orc, t):
 @pytest.mark.parametrize("wt", [gp.Q4_0, gp.Q4_K])
 def test_llama3_8b_decode_layer(plugin, orc, wt):
     """One decoder layer of Llama-3-8B shape, bs1 decode at position 4095 with 4095 cached tokens, Q4_0 weights (Q8_0
-    activations) or Q4_K weights (Q8_K activations): the plugin runs it as 8 launches (RMS_NORM + MUL, q/k/v with ROPE
-    and both SET_ROWS, the attention split and merge, o + ADD, RMS_NORM + MUL, gate/up + SWIGLU, down + ADD), Q4_0 as 6
-    (each RMS_NORM + MUL computed inside the q/k/v and gate/up launches)."""
+    activations) or Q4_K weights (Q8_K activations): the plugin runs it as 6 launches for Q4_0 (q/k/v with the
+    RMS_NORM + MUL before it, ROPE and both SET_ROWS; the attention split and merge; o + ADD; gate/up with the
+    RMS_NORM + MUL before it and SWIGLU; down + ADD), as 7 for Q4_K (the FFN RMS_NORM + MUL a launch of its own)."""
     rng = np.random.default_rng(2024)
     H, NH, NKV, D, FF, CTX = 4096, 32, 8, 128, 14336, 4096
     pos_t = CTX - 1
@@ -444,13 +444,14 @@ def test_llama3_8b_decode_layer(plugin, orc, wt):
         assert g.compute() == gp.STATUS_SUCCESS
         y = g.get(out, np.float32, (1, H))
         assert gp.counter(plugin, "f32_gpu_sgemm_dispatch_count") == 7
-        # nodes run inside another node's launch: the MUL of both RMS_NORM + MUL (2; Q4_0: both nodes of each, 4);
+        # nodes run inside another node's launch: both RMS_NORM + MUL pairs (4; Q4_K: the attention pair and the
+        # FFN norm's MUL, 3);
         # k, v, both ROPEs and both SET_ROWS in the q launch (6); up and SWIGLU in the gate launch (2); the residual
         # ADDs of o and down (2)
-        assert gp.counter(plugin, "fused_pair_count") == (14 if wt == gp.Q4_0 else 12)
-        # o reads the row the attention merge writes, down the one the gate/up launch writes; Q4_K: the q/k/v and
-        # gate/up launches also read the rows the two RMS_NORM + MUL write (Q4_0 computes them inside)
-        assert gp.counter(plugin, "act_quant_reuse_count") == (2 if wt == gp.Q4_0 else 4)
+        assert gp.counter(plugin, "fused_pair_count") == (14 if wt == gp.Q4_0 else 13)
+        # o reads the row the attention merge writes, down the one the gate/up launch writes (the q/k/v launch and,
+        # for Q4_0, the gate/up launch compute theirs inside; Q4_K's gate/up reads the one its norm launch writes)
+        assert gp.counter(plugin, "act_quant_reuse_count") == (2 if wt == gp.Q4_0 else 3)
 
         # the oracle's chain of the same ops
         def q8(a):
