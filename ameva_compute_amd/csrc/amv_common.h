@@ -575,6 +575,43 @@ __device__ __forceinline__ void amv_rms1024_quant(const AmvRms1024<NT>& r, float
     for (int v = 0; v < V; ++v) amv_rms_chunk(tid + NT * v, r.x[v], scale, true, r.w[v], nullptr, nullptr, act);
 }
 
+// amv_rms1024_quant with the activation type and the Q8_0 rule fixed at compile time (AT = AMV_T_Q8_0 with RULE, or
+// AMV_T_Q8_K): the same arithmetic and bytes, without the code of the other types and rules in the kernel.
+template <int NT, int AT, int RULE>
+__device__ __forceinline__ void amv_rms1024_quant_t(const AmvRms1024<NT>& r, float eps, int8_t* __restrict__ qs,
+                                                    void* __restrict__ meta, int32_t* __restrict__ sums16,
+                                                    double* sred) {
+    constexpr int V = AmvRms1024<NT>::V;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        double t = 0.0;
+        t += (double)(r.x[v].x * r.x[v].x);
+        t += (double)(r.x[v].y * r.x[v].y);
+        t += (double)(r.x[v].z * r.x[v].z);
+        t += (double)(r.x[v].w * r.x[v].w);
+        t = amv_wave_sum_d_u(t);
+        if ((tid & 63) == 0) sred[(tid + NT * v) >> 6] = t;
+    }
+    __syncthreads();
+    const float scale = amv_rms_scale(amv_rms_total(sred), 4096, eps);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int c = tid + NT * v;
+        const float4 x = r.x[v], w = r.w[v];
+        const float4 yv = make_float4(x.x * scale, x.y * scale, x.z * scale, x.w * scale);
+        const float vals[4] = {yv.x * w.x, yv.y * w.y, yv.z * w.z, yv.w * w.w};
+        if constexpr (AT == AMV_T_Q8_0) {
+            q8_block_lanes8_r<RULE>(vals, c & 7, qs + 32 * (c >> 3), reinterpret_cast<int2*>(meta) + (c >> 3));
+        } else {
+            const AmvQ8K q = amv_q8_K_lanes64(vals, c & 63);
+            reinterpret_cast<int*>(qs)[c] = amv_pack4(q.q);
+            if ((c & 3) == 0) sums16[c >> 2] = q.s16;
+            if ((c & 63) == 0) reinterpret_cast<float*>(meta)[c >> 6] = q.d;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // ROPE of one pair (x0, x1) with pair index j at position p: the angle freq_scale * (p * theta_scale^j) built by
 // repeated f32 multiplication (ggml's rope f32, reference ameva_rope.comp:64-92). Shared by every ROPE kernel.

@@ -604,9 +604,9 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_ep(const uint4* __restri
 // them instead of under them. Sized for one workgroup per CU (NT = 1024; 192 and 224 workgroups for the Llama-3-8B
 // q/k/v and gate/up). EP 7 with NW P a multiple of 32: each workgroup owns whole Q8_0 blocks of the SWIGLU output and
 // quantizes them from LDS after a barrier, no arrival counters (k_mmv_q4_0_k4096_swiglu's values and rules).
-template <int NT, int EP, bool SEG, int P = 2>
+template <int NT, int EP, bool SEG, int P, int RULE>
 __global__ __launch_bounds__(NT) void k_mmv_q4_0_k4096_norm(const float4* __restrict__ x4,
-                                                            const float4* __restrict__ nw4, float eps, int rule,
+                                                            const float4* __restrict__ nw4, float eps,
                                                             const uint4* __restrict__ wq,
                                                             const uint32_t* __restrict__ wd2, int n_rows,
                                                             float* __restrict__ dst, float* __restrict__ eout,
@@ -687,7 +687,7 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_0_k4096_norm(const float4* __rest
     // the norm's arithmetic waits for the row only; everything after it for the weights too
     __builtin_amdgcn_sched_barrier(0);
     const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);
-    amv_rms1024_quant<NT>(nr, eps, AmvActOut{s_q, s_m, nullptr, AMV_T_Q8_0, rule}, sred);
+    amv_rms1024_quant_t<NT, AMV_T_Q8_0, RULE>(nr, eps, s_q, s_m, nullptr, sred);
     __syncthreads();
     int4 a0[2], a1[2];
     int2 ds[2];
@@ -745,7 +745,8 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_0_k4096_norm(const float4* __rest
         if (threadIdx.x < NQ && 4 * c < F) {  // whole blocks only (F % 32 == 0)
             const float4 v4 = reinterpret_cast<const float4*>(s_h)[threadIdx.x];
             const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-            amv_act_store4(post.act, c, v);
+            q8_block_lanes8_r<RULE>(v, c & 7, post.act.qs + 32 * (c >> 3),
+                                    reinterpret_cast<int2*>(post.act.meta) + (c >> 3));
         }
     } else {
         mmv_finish<R, EP, 1, SEG>(acc, lane, wi, 0, live, wave, n_rows, dst, nullptr, eout, post, ra);
@@ -963,7 +964,7 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_K_norm(const float4* __restrict__
     }
     __builtin_amdgcn_sched_barrier(0);
     const MmvRopeAt ra = mmv_rope_at<EP>(post, wave);
-    amv_rms1024_quant<NT>(nr, eps, AmvActOut{s_q, s_d, s_s16, AMV_T_Q8_K, 0}, sred);
+    amv_rms1024_quant_t<NT, AMV_T_Q8_K, 0>(nr, eps, s_q, s_d, s_s16, sred);
     __syncthreads();
     const int4* a4 = reinterpret_cast<const int4*>(s_q);
     float acc[R];
@@ -1700,22 +1701,30 @@ extern "C" int amv_gemv_swiglu_q8(int wtype, const void* w, int64_t n_rows, int6
 static std::atomic<int> g_norm_nt{0};
 extern "C" void amv_debug_norm_gemv_threads(int nt) { g_norm_nt.store(nt, std::memory_order_relaxed); }
 
-template <int EP, bool SEG, int P = 2>
-static void launch_norm_gemv(int nt, int waves, const float* x, const float* nw, float eps, int rule, const MmvArgs& a,
-                             hipStream_t st) {
+template <int EP, bool SEG, int P, int RULE>
+static void launch_norm_gemv_r(int nt, int waves, const float* x, const float* nw, float eps, const MmvArgs& a,
+                               hipStream_t st) {
     const int64_t nblk = (int64_t)a.n_rows * 128;
     const uint4* wq = SEG ? nullptr : reinterpret_cast<const uint4*>(a.w);
     const uint32_t* wd = SEG ? nullptr : reinterpret_cast<const uint32_t*>(a.w + nblk * 16);
     const float4* x4 = reinterpret_cast<const float4*>(x);
     const float4* w4 = reinterpret_cast<const float4*>(nw);
 #define AMV_NORM_LAUNCH(NT)                                                                                        \
-    hipLaunchKernelGGL((k_mmv_q4_0_k4096_norm<NT, EP, SEG, P>),                                                 \
-                       dim3((unsigned)((waves + NT / 64 - 1) / (NT / 64))), dim3(NT), 0, st, x4, w4, eps, rule, wq, wd, \
+    hipLaunchKernelGGL((k_mmv_q4_0_k4096_norm<NT, EP, SEG, P, RULE>),                                           \
+                       dim3((unsigned)((waves + NT / 64 - 1) / (NT / 64))), dim3(NT), 0, st, x4, w4, eps, wq, wd,       \
                        a.n_rows, a.dst, a.eout, a.post)
     if (nt == 256) AMV_NORM_LAUNCH(256);
     else if (nt == 512) AMV_NORM_LAUNCH(512);
     else AMV_NORM_LAUNCH(1024);
 #undef AMV_NORM_LAUNCH
+}
+// the Q8_0 rule as a template argument: each kernel holds the code of one rule only
+template <int EP, bool SEG, int P = 2>
+static void launch_norm_gemv(int nt, int waves, const float* x, const float* nw, float eps, int rule, const MmvArgs& a,
+                             hipStream_t st) {
+    if (rule == AMV_Q8_X86) launch_norm_gemv_r<EP, SEG, P, AMV_Q8_X86>(nt, waves, x, nw, eps, a, st);
+    else if (rule == AMV_Q8_ARM) launch_norm_gemv_r<EP, SEG, P, AMV_Q8_ARM>(nt, waves, x, nw, eps, a, st);
+    else launch_norm_gemv_r<EP, SEG, P, AMV_Q8_REF>(nt, waves, x, nw, eps, a, st);
 }
 
 template <int EP, bool SEG>
