@@ -376,14 +376,31 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_sb(const uint8_t* __restrict__ 
             }
         }
     };
-    int q = w;
-    if (q < ngrp) load(0, q);
-    for (; q < ngrp; q += 2 * NW) {
-        if (q + NW < ngrp) load(1, q + NW);
-        compute(0, q);
-        if (q + NW >= ngrp) break;
-        if (q + 2 * NW < ngrp) load(0, q + 2 * NW);
-        compute(1, q + NW);
+    // the wave's groups w, w + NW, ..., two buffers; no load sits behind a branch inside an iteration, so the
+    // wait before each compute covers exactly the loads it reads (a conditional load made the compiler wait for the
+    // prefetch as well)
+    const int nit = (ngrp - w + NW - 1) / NW;
+    if (nit > 0) {
+        load(0, w);
+        int k = 0;
+        for (; k + 2 < nit; k += 2) {
+            load(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);  // each prefetch goes out before the compute that follows it
+            compute(0, w + k * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            load(0, w + (k + 2) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (nit - k == 2) {
+            load(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(0, w + k * NW);
+            compute(1, w + (k + 1) * NW);
+        } else {
+            compute(0, w + k * NW);
+        }
     }
     if constexpr (!SUMS) {
         __shared__ float red[NW - 1][TI * TJ * 4][64];
@@ -755,14 +772,31 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q4k_sb(const uint4* __restrict_
             }
         }
     };
-    int sb = w;
-    if (sb < nsb) load(0, sb);
-    for (; sb < nsb; sb += 2 * NW) {
-        if (sb + NW < nsb) load(1, sb + NW);
-        compute(0, sb);
-        if (sb + NW >= nsb) break;
-        if (sb + 2 * NW < nsb) load(0, sb + 2 * NW);
-        compute(1, sb + NW);
+    // the wave's super-blocks w, w + NW, ..., two buffers; no load sits behind a branch inside an iteration, so the
+    // wait before each compute covers exactly the loads it reads (a conditional load made the compiler wait for the
+    // prefetch as well)
+    const int nit = (nsb - w + NW - 1) / NW;
+    if (nit > 0) {
+        load(0, w);
+        int k = 0;
+        for (; k + 2 < nit; k += 2) {
+            load(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);  // each prefetch goes out before the compute that follows it
+            compute(0, w + k * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            load(0, w + (k + 2) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (nit - k == 2) {
+            load(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(0, w + k * NW);
+            compute(1, w + (k + 1) * NW);
+        } else {
+            compute(0, w + k * NW);
+        }
     }
     if constexpr (!SUMS) {
         __shared__ float red[NW - 1][TI * TJ * 4][64];
@@ -797,22 +831,29 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q4k_sb(const uint4* __restrict_
 // sc_s int8), then dst += (d * d_a) I. A wave owns TI 16-row weight tiles and every token (TJ 16-token tiles); the NW
 // waves of a workgroup take every NW-th super-block and add their f32 partials in LDS in wave order. Roles: A =
 // activations (token l % 16), B = weights (row l % 16), so a lane's 4 outputs are its own weight row (its own scales
-// and d) and tokens 4 g .. 4 g + 3. A v_mfma_i32_16x16x32_i8 covers 32 consecutive elements 32 p .. 32 p + 31 (k slots
-// 8 g .. 8 g + 7 from lane group g): sub-block 2 p in the slots of groups 0 and 1, sub-block 2 p + 1 in those of
-// groups 2 and 3; two MFMAs per pair, each with the other sub-block's activation slots set to zero, give the two
-// sub-block sums apart. Element 32 p + 8 g + b of the super-block is, in ggml's Q6_K layout (half h = p / 4, quarter
-// t = p % 4), the low (t < 2) or high (t >= 2) nibble of ql byte 64 h + 32 (t % 2) + 8 g + b with bits 2 t, 2 t + 1 of qh
-// byte 32 h + 8 g + b above it: each lane loads those 8-byte runs (4 of ql, 2 of qh per super-block) and the 8-byte
-// runs of its token's activation row, and builds q - 32 as signed bytes (flip bit 5 of the 6-bit code, copy it into
-// bits 6 and 7). The loads of the next super-block are in flight while one computes. Reads the plain Q8_K layout (the
-// prefix of AMV_ACT_Q8_K_MMA too).
+// and d) and tokens 4 g .. 4 g + 3 (lane group g = l / 16).
+// Loads: 16 bytes per lane with consecutive lanes on consecutive bytes (lane 4 r + c: row or token r, 16-byte chunk
+// c), so each quad of lanes reads 64 contiguous bytes of a row; ds_bpermute then moves chunk g of row r to lane
+// 16 g + r, the MFMA operand layout. Chunks: ql bytes 64 h + 16 c (half h = 0, 1), qh bytes 16 c, the activation
+// bytes 64 q + 16 c (q = 0..3), the scale dword c. In ggml's Q6_K layout ql byte 64 h + 16 g + i holds in its low
+// nibble element 128 h + 16 g + i (sub-block 8 h + g) and in its high nibble element 128 h + 64 + 16 g + i (sub-block
+// 8 h + 4 + g), with bits 2 t, 2 t + 1 of qh byte 32 h + 16 (g & 1) + i above them (quarter t = g >> 1, + 2 for the
+// high nibble); the qh chunk of half h sits in lane group 2 h + (g & 1) and v_permlane32_swap hands it over. So for
+// q = 2 h + hi lane group g holds sub-block 4 q + g whole (16 signed bytes q - 32), and so does the activation lane
+// of the same group. A dot product does not depend on the order of k, so each operand is rearranged the same way
+// across lane groups: v_permlane16_swap of (bytes 0..7, bytes 8..15) gives X = sub-block 4 q in groups 0 and 1,
+// 4 q + 2 in groups 2 and 3, and Y = 4 q + 1 | 4 q + 3. Two v_mfma_i32_16x16x32_i8 per operand, each with the other
+// sub-block's activation slots set to zero, give the two sub-block sums apart. The loads of the next super-block are
+// in flight while one computes. Reads the plain Q8_K layout (the prefix of AMV_ACT_Q8_K_MMA too).
 template <int TI, int TJ, int NW, bool SUMS>
 __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restrict__ wl, const uint8_t* __restrict__ wqh,
-                                                       const sb_v4u* __restrict__ wsc, const uint16_t* __restrict__ wd,
+                                                       const uint32_t* __restrict__ wsc, const uint16_t* __restrict__ wd,
                                                        int N, int nsb, const int8_t* __restrict__ aq,
                                                        const float* __restrict__ ad, int M, float* __restrict__ dst,
                                                        int64_t ldd, int32_t* __restrict__ sums) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g = lane >> 4;
+    const int lr4 = lane >> 2, lc = lane & 3;  // load layout: row / token lr4, chunk lc
+    const int perm = 4 * (4 * r16 + g);        // ds_bpermute address: the load lane holding chunk g of row r16
     const int n0 = blockIdx.x * 16 * TI;
     const size_t K = (size_t)nsb * 256;
     const uint8_t* lr[TI];
@@ -820,17 +861,17 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
     size_t rb[TI];  // row * nsb
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
-        const size_t row = (size_t)min(n0 + 16 * i + r16, N - 1);
+        const size_t row = (size_t)min(n0 + 16 * i + lr4, N - 1);
         rb[i] = row * nsb;
-        lr[i] = wl + rb[i] * 128 + 8 * g;
-        hr[i] = wqh + rb[i] * 64 + 8 * g;
+        lr[i] = wl + rb[i] * 128 + 16 * lc;
+        hr[i] = wqh + rb[i] * 64 + 16 * lc;
     }
     const int8_t* ar[TJ];
     const float* dr[TJ];
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
-        const size_t t = (size_t)min(16 * j + r16, M - 1);
-        ar[j] = aq + t * K + 8 * g;
+        const size_t t = (size_t)min(16 * j + lr4, M - 1);
+        ar[j] = aq + t * K + 16 * lc;
         dr[j] = ad + t * nsb;
     }
     float acc[TI][TJ][4];
@@ -841,36 +882,58 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
 
-    sb_v2u lq[2][TI][4], lh[2][TI][2], la[2][TJ][8];
-    sb_v4u ls[2][TI];
-    uint32_t ldw[2][TI];
+    sb_v4u lq[2][TI][2], lh[2][TI], la[2][TJ][4];
+    uint32_t ls[2][TI], ldw[2][TI];
     float lda[2][TJ];
     const auto load = [&](int s, int sb) {
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                lq[s][i][c] = __builtin_nontemporal_load(reinterpret_cast<const sb_v2u*>(lr[i] + (size_t)sb * 128 + 32 * c));
-#pragma unroll
-            for (int c = 0; c < 2; ++c)
-                lh[s][i][c] = __builtin_nontemporal_load(reinterpret_cast<const sb_v2u*>(hr[i] + (size_t)sb * 64 + 32 * c));
-            ls[s][i] = wsc[rb[i] + sb];
+            for (int h = 0; h < 2; ++h)
+                lq[s][i][h] = __builtin_nontemporal_load(reinterpret_cast<const sb_v4u*>(lr[i] + (size_t)sb * 128 + 64 * h));
+            lh[s][i] = __builtin_nontemporal_load(reinterpret_cast<const sb_v4u*>(hr[i] + (size_t)sb * 64));
+            ls[s][i] = wsc[(rb[i] + sb) * 4 + lc];
             ldw[s][i] = wd[rb[i] + sb];
         }
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
 #pragma unroll
-            for (int p = 0; p < 8; ++p) la[s][j][p] = *reinterpret_cast<const sb_v2u*>(ar[j] + (size_t)sb * 256 + 32 * p);
+            for (int c = 0; c < 4; ++c) la[s][j][c] = *reinterpret_cast<const sb_v4u*>(ar[j] + (size_t)sb * 256 + 64 * c);
             lda[s][j] = dr[j][sb];
         }
     };
+    const auto bperm = [&](uint32_t v) { return (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v); };
+    const auto bperm4 = [&](const sb_v4u& v, uint32_t (&o)[4]) {
+        o[0] = bperm(v.x);
+        o[1] = bperm(v.y);
+        o[2] = bperm(v.z);
+        o[3] = bperm(v.w);
+    };
+    // (bytes 0..7, bytes 8..15) of the 4 lane groups' sub-blocks -> X = groups (0: 0..7 of group 0's, 1: 8..15 of
+    // group 0's, 2: 0..7 of group 2's, 3: 8..15 of group 2's), Y the same of groups 1 and 3
+    const auto pair = [](const uint32_t (&v)[4], long& X, long& Y) {
+        const auto p0 = __builtin_amdgcn_permlane16_swap(v[0], v[2], false, false);
+        const auto p1 = __builtin_amdgcn_permlane16_swap(v[1], v[3], false, false);
+        X = (long)(((uint64_t)p1[0] << 32) | p0[0]);
+        Y = (long)(((uint64_t)p1[1] << 32) | p0[1]);
+    };
     const auto compute = [&](int s, int sb) {
-        // the activation scales of the lane's output tokens 16 j + 4 g + e, held by lanes 4 g + e (token r16's)
+        // the activation scales of the lane's output tokens 16 j + 4 g + e, loaded by lanes 4 (4 g + e) + c
         float da[TJ][4];
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) da[j][e] = __shfl(lda[s][j], 4 * g + e, AMV_WAVE);
+            for (int e = 0; e < 4; ++e) da[j][e] = __shfl(lda[s][j], 16 * g + 4 * e, AMV_WAVE);
+        // activation operands of the 4 quarters c (sub-blocks 4 c .. 4 c + 3)
+        long AX[TJ][4], AY[TJ][4];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint32_t v[4];
+                bperm4(la[s][j][c], v);
+                pair(v, AX[j][c], AY[j][c]);
+            }
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
             int I[TJ][4];
@@ -878,35 +941,58 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
             for (int j = 0; j < TJ; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) I[j][e] = 0;
-            const uint32_t scw[4] = {ls[s][i].x, ls[s][i].y, ls[s][i].z, ls[s][i].w};
+            // the 4 scale dwords and d of row r16: loaded by lanes 4 r16 + c
+            uint32_t scw[4];
 #pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                const int h = p >> 2, t = p & 3;
-                const sb_v2u qlv = lq[s][i][2 * h + (t & 1)], qhv = lh[s][i][h];
-                uint32_t x[2];
+            for (int c = 0; c < 4; ++c) scw[c] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * r16 + c), (int)ls[s][i]);
+            const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(16 * r16, (int)ldw[s][i]);
+            // the qh run of half h for this lane group: lane group 2 h + (g & 1) holds it
+            uint32_t qh[2][4];
+            {
+                uint32_t hv[4];
+                bperm4(lh[s][i], hv);
 #pragma unroll
-                for (int d2 = 0; d2 < 2; ++d2) {
-                    const uint32_t lo = ((t >= 2 ? qlv[d2] >> 4 : qlv[d2]) & 0x0F0F0F0Fu) |
-                                        (((qhv[d2] >> (2 * t)) & 0x03030303u) << 4);
-                    const uint32_t f = lo ^ 0x20202020u;  // 6-bit code - 32: bit 5 flipped, then copied up
-                    const uint32_t m5 = f & 0x20202020u;
-                    x[d2] = f | (m5 << 2) | (m5 << 1);
-                }
-                const long B = (long)(((uint64_t)x[1] << 32) | x[0]);
-                const int sa = (int)(int8_t)(scw[p >> 1] >> (16 * (p & 1)));       // sc[2 p]
-                const int sb2 = (int)(int8_t)(scw[p >> 1] >> (16 * (p & 1) + 8));  // sc[2 p + 1]
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) {
-                    const long A = (long)(((uint64_t)la[s][j][p][1] << 32) | la[s][j][p][0]);
-                    const long Aa = g < 2 ? A : 0L, Ab = g < 2 ? 0L : A;
-                    const v4i zero = {0, 0, 0, 0};
-                    const v4i Ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(Aa, B, zero, 0, 0, 0);
-                    const v4i Cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(Ab, B, zero, 0, 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) I[j][e] += sa * Ca[e] + sb2 * Cb[e];
+                for (int d = 0; d < 4; ++d) {
+                    const auto r = __builtin_amdgcn_permlane32_swap(hv[d], hv[d], false, false);
+                    qh[0][d] = r[0];
+                    qh[1][d] = r[1];
                 }
             }
-            const float d = amv_h2f((uint16_t)ldw[s][i]);
+            uint32_t qlw[2][4];  // ql chunk g of each half
+            bperm4(lq[s][i][0], qlw[0]);
+            bperm4(lq[s][i][1], qlw[1]);
+            const int sh = 2 * (g >> 1);  // qh bit pair of the low nibble's quarter (+ 4 for the high nibble)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int h = c >> 1, hi = c & 1;
+                uint32_t x[4];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t lo = ((hi ? qlw[h][d] >> 4 : qlw[h][d]) & 0x0F0F0F0Fu) |
+                                        (((qh[h][d] >> (sh + 4 * hi)) & 0x03030303u) << 4);
+                    const uint32_t f = lo ^ 0x20202020u;  // 6-bit code - 32: bit 5 flipped, then copied up
+                    const uint32_t m5 = f & 0x20202020u;
+                    x[d] = f | (m5 << 2) | (m5 << 1);
+                }
+                long BX, BY;
+                pair(x, BX, BY);
+                // sc bytes 4 c .. 4 c + 3: X holds sub-blocks 4 c | 4 c + 2, Y 4 c + 1 | 4 c + 3
+                const int s0 = (int)(int8_t)scw[c], s1 = (int)(int8_t)(scw[c] >> 8);
+                const int s2 = (int)(int8_t)(scw[c] >> 16), s3 = (int)(int8_t)(scw[c] >> 24);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const v4i zero = {0, 0, 0, 0};
+                    const long AXa = g < 2 ? AX[j][c] : 0L, AXb = g < 2 ? 0L : AX[j][c];
+                    const long AYa = g < 2 ? AY[j][c] : 0L, AYb = g < 2 ? 0L : AY[j][c];
+                    const v4i C0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(AXa, BX, zero, 0, 0, 0);
+                    const v4i C2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(AXb, BX, zero, 0, 0, 0);
+                    const v4i C1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(AYa, BY, zero, 0, 0, 0);
+                    const v4i C3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(AYb, BY, zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) I[j][e] += s0 * C0[e] + s2 * C2[e] + s1 * C1[e] + s3 * C3[e];
+                }
+            }
+            const float d = amv_h2f((uint16_t)dw);
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
 #pragma unroll
@@ -920,14 +1006,31 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
                 }
         }
     };
-    int sb = w;
-    if (sb < nsb) load(0, sb);
-    for (; sb < nsb; sb += 2 * NW) {
-        if (sb + NW < nsb) load(1, sb + NW);
-        compute(0, sb);
-        if (sb + NW >= nsb) break;
-        if (sb + 2 * NW < nsb) load(0, sb + 2 * NW);
-        compute(1, sb + NW);
+    // the wave's super-blocks w, w + NW, ..., two buffers; no load sits behind a branch inside an iteration, so the
+    // wait before each compute covers exactly the loads it reads (a conditional load made the compiler wait for the
+    // prefetch as well)
+    const int nit = (nsb - w + NW - 1) / NW;
+    if (nit > 0) {
+        load(0, w);
+        int k = 0;
+        for (; k + 2 < nit; k += 2) {
+            load(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);  // each prefetch goes out before the compute that follows it
+            compute(0, w + k * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            load(0, w + (k + 2) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (nit - k == 2) {
+            load(1, w + (k + 1) * NW);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(0, w + k * NW);
+            compute(1, w + (k + 1) * NW);
+        } else {
+            compute(0, w + k * NW);
+        }
     }
     if constexpr (!SUMS) {
         __shared__ float red[NW - 1][TI * TJ * 4][64];
@@ -957,8 +1060,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
     }
 }
 
-// Q6_K batches of m <= 32 tokens (plain Q8_K activations or the Q8_K prefix of AMV_ACT_Q8_K_MMA): two 16-row tiles
-// per wave and 4 waves while that leaves >= 256 workgroups, else one tile and 8 waves splitting the super-blocks
+// Q6_K batches of m <= 32 tokens (plain Q8_K activations or the Q8_K prefix of AMV_ACT_Q8_K_MMA)
 static int mmq_q6k_sb(const void* w, int64_t n_rows, int64_t k, const void* act, int64_t m, float* dst, int64_t ldd,
                       int32_t* sums, hipStream_t st) {
     AMV_REQUIRE(k % 256 == 0, "amv_mul_mat_q: Q6_K needs k %% 256 == 0");
@@ -968,11 +1070,10 @@ static int mmq_q6k_sb(const void* w, int64_t n_rows, int64_t k, const void* act,
     const uint8_t* base = (const uint8_t*)w;
     const uint8_t* wl = base;
     const uint8_t* wqh = base + nblk * 128;
-    const sb_v4u* wsc = (const sb_v4u*)(base + nblk * 192);
+    const uint32_t* wsc = (const uint32_t*)(base + nblk * 192);
     const uint16_t* wd = (const uint16_t*)(base + nblk * 208);
     const int8_t* aq = (const int8_t*)act;
     const float* ad = (const float*)((const uint8_t*)act + m * k);
-    const bool two = (n_rows + 31) / 32 >= 256;
 #define Q6K_SB(TI, TJ, NW)                                                                                          \
     do {                                                                                                             \
         const dim3 G((unsigned)((n_rows + 16 * TI - 1) / (16 * TI)));                                              \
@@ -981,14 +1082,17 @@ static int mmq_q6k_sb(const void* w, int64_t n_rows, int64_t k, const void* act,
         else hipLaunchKernelGGL((k_mmq_q6k_sb<TI, TJ, NW, false>), G, dim3(64 * NW), 0, st, wl, wqh, wsc, wd,       \
                                 (int)n_rows, nsb, aq, ad, (int)m, dst, ldd, sums);                                   \
     } while (0)
-    // measured on MI355X (14336 x 4096 and 4096 x 14336 at 16 and 32 tokens): 8 or 16 waves per workgroup, or one
-    // tile per wave where two fit, were all slower (M = 16: 32-56 against 29.5-31.8 us)
+    // one 16-row tile per wave; 2 waves per workgroup when there are >= 512 tiles (14336 rows), else 4. Measured on
+    // MI355X at 14336 x 4096 / 4096 x 14336 (us, hot weights): M = 16 17.6 / 17.2 against 18.5 / 18.4 for two tiles
+    // per wave and 4 / 8 waves, and 19-58 for 8 or 16 waves or two tiles with 2 waves; M = 32 28.5 / 26.0 against
+    // 33.9 / 26.0 (two tiles per wave with 2 waves 28.4 / 74.8)
+    const bool wide = (n_rows + 15) / 16 >= 512;
     if (m <= 16) {
-        if (two) Q6K_SB(2, 1, 4);
-        else Q6K_SB(1, 1, 8);
+        if (wide) Q6K_SB(1, 1, 2);
+        else Q6K_SB(1, 1, 4);
     } else {
-        if (two) Q6K_SB(2, 2, 4);
-        else Q6K_SB(1, 2, 4);  // 8 waves of this tile would spill registers
+        if (wide) Q6K_SB(1, 2, 2);
+        else Q6K_SB(1, 2, 4);
     }
 #undef Q6K_SB
     return amv_check_launch("amv_mul_mat_q");
