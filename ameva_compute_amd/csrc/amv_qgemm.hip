@@ -52,7 +52,9 @@ template <int WT>
 struct QgRegs {  // one thread's share of a step: weight block (row t / 2, block t % 2), activation block (token t / 2)
     uint4 w0, w1;  // Q4_0: w0 = the 16 nibble bytes; Q8_0: the 32 bytes
     uint4 a0, a1;  // 32 int8 of the token's block
-    float dw, da;
+    uint32_t dw;   // the weight block's f16 scale bits
+    float da;
+    bool past;     // a block past the split's end: weight scale 0
 };
 
 template <int WT, int TT, int TW>
@@ -63,23 +65,24 @@ __device__ __forceinline__ QgRegs<WT> qg_load(int step, const uint8_t* __restric
     constexpr int BN = 64 * TW, BM = 64 * TT;
     const int t = threadIdx.x, blk = t & 1;
     const int b = b0 + 2 * step + blk, bc = min(b, b_end - 1);  // a block past the split's end: weight scale 0
+    // the loaded values stay untouched until qg_store (any arithmetic on them here makes the compiler wait for the
+    // whole prefetch at the load); the fields of a role the thread does not have are not read
     QgRegs<WT> s;
-    s.w0 = s.w1 = s.a0 = s.a1 = make_uint4(0, 0, 0, 0);
-    s.dw = s.da = 0.0f;
-    if (t < 2 * BN) {
+    s.past = b >= b_end;
+    if (2 * BN >= 256 || t < 2 * BN) {  // (every thread of the 256 when BN = 128)
         const int row = min(n0 + (t >> 1), N - 1);
         const size_t bi = (size_t)row * nb + bc;
         if constexpr (WT == AMV_T_Q4_0) {
             s.w0 = *reinterpret_cast<const uint4*>(wq + bi * 16);
-            s.dw = b < b_end ? amv_h2f(wd[amv_q4_0_didx(row, bc, nb, N)]) : 0.0f;
+            s.dw = wd[amv_q4_0_didx(row, bc, nb, N)];
         } else {
             const uint4* p = reinterpret_cast<const uint4*>(wq + bi * 32);
             s.w0 = p[0];
             s.w1 = p[1];
-            s.dw = b < b_end ? amv_h2f(wd[bi]) : 0.0f;
+            s.dw = wd[bi];
         }
     }
-    if (t < 2 * BM) {
+    if (2 * BM >= 256 || t < 2 * BM) {
         const int tok = min(m0 + (t >> 1), M - 1);
         const uint4* p = reinterpret_cast<const uint4*>(aq + (size_t)tok * K + 32 * bc);
         s.a0 = p[0];
@@ -106,7 +109,7 @@ __device__ __forceinline__ void qg_store(const QgRegs<WT>& s, int8_t* __restrict
             d[0] = s.w0;
             d[1] = s.w1;
         }
-        sDw[blk * BN + (t >> 1)] = s.dw;
+        sDw[blk * BN + (t >> 1)] = s.past ? 0.0f : amv_h2f((uint16_t)s.dw);
     }
     if (t < 2 * BM) {
         uint4* d = reinterpret_cast<uint4*>(sA + (t >> 1) * QG_LD + 32 * blk);
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     QgRegs<WT> st0, st1;
     st0 = qg_load<WT, TT, TW>(0, wq, wd, N, nb, n0, aq, am, M, m0, K, b0, b_end);
     qg_store<WT, TT, TW>(st0, sW[0], sA[0], sDw[0], sDa[0]);
-    if (1 < nsteps) st1 = qg_load<WT, TT, TW>(1, wq, wd, N, nb, n0, aq, am, M, m0, K, b0, b_end);
+    st1 = qg_load<WT, TT, TW>(min(1, nsteps - 1), wq, wd, N, nb, n0, aq, am, M, m0, K, b0, b_end);
     __syncthreads();
     const auto compute = [&](int step) {
         const int buf = step & 1;
@@ -200,13 +203,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
     };
+    // the prefetches are unconditional (past the last step they read the last step again) so that the wait before
+    // each store covers only the registers it stores, not the prefetch issued after them
     for (int step = 0; step < nsteps; step += 2) {
-        if (step + 2 < nsteps) st0 = qg_load<WT, TT, TW>(step + 2, wq, wd, N, nb, n0, aq, am, M, m0, K, b0, b_end);
+        st0 = qg_load<WT, TT, TW>(min(step + 2, nsteps - 1), wq, wd, N, nb, n0, aq, am, M, m0, K, b0, b_end);
         compute(step);
         if (step + 1 >= nsteps) break;
         qg_store<WT, TT, TW>(st1, sW[1], sA[1], sDw[1], sDa[1]);
         __syncthreads();
-        if (step + 3 < nsteps) st1 = qg_load<WT, TT, TW>(step + 3, wq, wd, N, nb, n0, aq, am, M, m0, K, b0, b_end);
+        st1 = qg_load<WT, TT, TW>(min(step + 3, nsteps - 1), wq, wd, N, nb, n0, aq, am, M, m0, K, b0, b_end);
         compute(step + 1);
         if (step + 2 >= nsteps) break;
         qg_store<WT, TT, TW>(st0, sW[0], sA[0], sDw[0], sDa[0]);
