@@ -854,10 +854,26 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int j0 = live ? 64 * ks : nsl; j0 < nsl; j0 += 64 * S) {
+    // two 64-slice steps per pass, both steps' loads issued before either step's arithmetic (a wave's step-2 loads
+    // would otherwise wait for its step-1 compute: two memory round trips in a row). A lane past the row's end
+    // loads slice nsl - 1 and adds nothing; the steps add into acc in order, as one step per pass would.
+    struct Step {
+        uint4 q[R];
+        uint32_t hv[R];  // dword lane & 3 of the super-block's 16-byte head (spread over the quad in compute)
+        int4 alo, ahi;
+        float da;
+        int bslo, bshi;
+        int j, sb, c, t;
+        bool valid;
+    };
+    const auto load = [&](int j0, Step& st) {
+        st.valid = j0 + lane < nsl;
         const int j = min(j0 + lane, nsl - 1);  // nsl is a multiple of 8: clamped lanes fill whole groups of 8
         const int sb = j >> 3, t = j & 7, c = t >> 1, h = t & 1;
-        uint4 q[R], hd[R];
+        st.j = j;
+        st.sb = sb;
+        st.c = c;
+        st.t = t;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             int row = min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
@@ -870,27 +886,34 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
                 whs = wqs + (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]) * nsl;
                 row = lr;
             }
-            q[r] = amv_ld_stream(wqs + (size_t)row * nsl + j);
+            st.q[r] = amv_ld_stream(wqs + (size_t)row * nsl + j);
             // the super-block's 16-byte head: each lane of a quad loads one dword (the quad shares the super-block:
-            // groups of 8 lanes do, clamped lanes included), then DPP hands every lane all four
-            const uint32_t hv =
-                amv_ld_stream(reinterpret_cast<const uint32_t*>(whs + (size_t)row * nsb + sb) + (lane & 3));
-            hd[r] = make_uint4(__builtin_amdgcn_mov_dpp(hv, 0x00, 0xF, 0xF, false),   // quad_perm [0,0,0,0]
-                               __builtin_amdgcn_mov_dpp(hv, 0x55, 0xF, 0xF, false),   // [1,1,1,1]
-                               __builtin_amdgcn_mov_dpp(hv, 0xAA, 0xF, 0xF, false),   // [2,2,2,2]
-                               __builtin_amdgcn_mov_dpp(hv, 0xFF, 0xF, 0xF, false));  // [3,3,3,3]
+            // groups of 8 lanes do, clamped lanes included); compute hands every lane all four by DPP (no arithmetic
+            // on a loaded value here, or the compiler waits for the loads at this point)
+            st.hv[r] = amv_ld_stream(reinterpret_cast<const uint32_t*>(whs + (size_t)row * nsb + sb) + (lane & 3));
         }
-        const int4 alo = a4[sb * 16 + 4 * c + h], ahi = a4[sb * 16 + 4 * c + 2 + h];
-        const float da = ad[sb];
-        const int bslo = abs16[sb * 16 + 4 * c + h], bshi = abs16[sb * 16 + 4 * c + 2 + h];
+        st.alo = a4[sb * 16 + 4 * c + h];
+        st.ahi = a4[sb * 16 + 4 * c + 2 + h];
+        st.da = ad[sb];
+        st.bslo = abs16[sb * 16 + 4 * c + h];
+        st.bshi = abs16[sb * 16 + 4 * c + 2 + h];
+    };
+    const auto compute = [&](const Step& st) {
+        const int sb = st.sb, c = st.c, t = st.t;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
+            const uint32_t hv = st.hv[r];
+            const uint4 hd = make_uint4(__builtin_amdgcn_mov_dpp(hv, 0x00, 0xF, 0xF, false),   // quad_perm [0,0,0,0]
+                                        __builtin_amdgcn_mov_dpp(hv, 0x55, 0xF, 0xF, false),   // [1,1,1,1]
+                                        __builtin_amdgcn_mov_dpp(hv, 0xAA, 0xF, 0xF, false),   // [2,2,2,2]
+                                        __builtin_amdgcn_mov_dpp(hv, 0xFF, 0xF, 0xF, false));  // [3,3,3,3]
             int sl, ml, sh, mh;
-            k4_scale_min_pair(c, hd[r].y, hd[r].z, hd[r].w, sl, ml, sh, mh);
-            const uint4 lo = make_uint4(q[r].x & M4, q[r].y & M4, q[r].z & M4, q[r].w & M4);
-            const uint4 hi = make_uint4((q[r].x >> 4) & M4, (q[r].y >> 4) & M4, (q[r].z >> 4) & M4, (q[r].w >> 4) & M4);
-            int isum = sl * dot16(lo, alo, 0) + sh * dot16(hi, ahi, 0);
-            int msum = ml * bslo + mh * bshi;
+            k4_scale_min_pair(c, hd.y, hd.z, hd.w, sl, ml, sh, mh);
+            const uint4 q = st.q[r];
+            const uint4 lo = make_uint4(q.x & M4, q.y & M4, q.z & M4, q.w & M4);
+            const uint4 hi = make_uint4((q.x >> 4) & M4, (q.y >> 4) & M4, (q.z >> 4) & M4, (q.w >> 4) & M4);
+            int isum = sl * dot16(lo, st.alo, 0) + sh * dot16(hi, st.ahi, 0);
+            int msum = ml * st.bslo + mh * st.bshi;
             if (BLOCK_SUMS) {
 #pragma unroll
                 for (int o = 1; o < 8; o <<= 1) {
@@ -898,16 +921,23 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
                     msum += __shfl_xor(msum, o, AMV_WAVE);
                 }
                 const int rr = mmv_row<EP>(wave, r, R, n_rows);
-                if (t == 0 && j0 + lane < nsl && rr < n_rows) {
+                if (t == 0 && st.valid && rr < n_rows) {
                     sums[((size_t)rr * nsb + sb) * 2] = isum;
                     sums[((size_t)rr * nsb + sb) * 2 + 1] = msum;
                 }
-            } else if (j0 + lane < nsl) {
-                const float d = amv_h2f(hd[r].x) * da, dmin = amv_h2f(hd[r].x >> 16) * da;
+            } else if (st.valid) {
+                const float d = amv_h2f(hd.x) * st.da, dmin = amv_h2f(hd.x >> 16) * st.da;
                 acc[r] = fmaf(d, (float)isum, acc[r]);
                 acc[r] = fmaf(-dmin, (float)msum, acc[r]);
             }
         }
+    };
+    for (int j0 = live ? 64 * ks : nsl; j0 < nsl; j0 += 128 * S) {
+        Step s0, s1;
+        load(j0, s0);
+        load(j0 + 64 * S, s1);
+        compute(s0);
+        compute(s1);
     }
     if constexpr (!BLOCK_SUMS) {
         mmv_finish<R, EP, S, SEG>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
@@ -1019,31 +1049,49 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int j0 = live ? 64 * ks : nsl; j0 < nsl; j0 += 64 * S) {
+    // two 64-slice steps per pass, both steps' loads issued before either step's arithmetic (as k_mmv_q4_K)
+    struct Step {
+        uint4 ql[R], qh[R], sc[R];
+        uint16_t dd[R];
+        int4 alo, ahi;
+        float da;
+        int blo, bhi;
+        int sb, t, slo, glo;
+        bool valid;
+    };
+    const auto load = [&](int j0, Step& st) {
+        st.valid = j0 + lane < nsl;
         const int j = min(j0 + lane, nsl - 1);
         const int sb = j >> 3, t = j & 7;
         const int hh = t >> 2, l0 = 16 * (t & 3);  // ql byte offset 64 hh + l0
         const int slo = l0 >> 5, lq = l0 & 31;      // weights 128 hh + 32 s + lq + i, s in {slo, slo + 2}
-        uint4 ql[R], qh[R], sc[R];
-        uint16_t dd[R];
+        st.sb = sb;
+        st.t = t;
+        st.slo = slo;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const size_t rw = (size_t)min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
             const size_t rb = rw * nsb + sb;
-            ql[r] = amv_ld_stream(wl + rw * nsl + j);
-            qh[r] = amv_ld_stream(wqh + rb * 4 + 2 * hh + (lq >> 4));
-            sc[r] = amv_ld_stream(wsc + rb);
-            dd[r] = amv_ld_stream(wd + rb);
+            st.ql[r] = amv_ld_stream(wl + rw * nsl + j);
+            st.qh[r] = amv_ld_stream(wqh + rb * 4 + 2 * hh + (lq >> 4));
+            st.sc[r] = amv_ld_stream(wsc + rb);
+            st.dd[r] = amv_ld_stream(wd + rb);
         }
         const int elo = 128 * hh + 32 * slo + lq;  // element offset in the super-block
-        const int4 alo = a4[(sb * 256 + elo) >> 4], ahi = a4[(sb * 256 + elo + 64) >> 4];
-        const float da = ad[sb];
+        st.alo = a4[(sb * 256 + elo) >> 4];
+        st.ahi = a4[(sb * 256 + elo + 64) >> 4];
+        st.da = ad[sb];
         const int glo = elo >> 4, ghi = glo + 4;
-        const int blo = abs16[sb * 16 + glo], bhi = abs16[sb * 16 + ghi];
-        const int shlo = 2 * slo, shhi = 2 * slo + 4;
+        st.glo = glo;
+        st.blo = abs16[sb * 16 + glo];
+        st.bhi = abs16[sb * 16 + ghi];
+    };
+    const auto compute = [&](const Step& st) {
+        const int sb = st.sb, t = st.t, glo = st.glo, ghi = glo + 4;
+        const int shlo = 2 * st.slo, shhi = 2 * st.slo + 4;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint4 L = ql[r], H = qh[r];
+            const uint4 L = st.ql[r], H = st.qh[r];
             const uint4 vlo = make_uint4((L.x & M4) | (((H.x >> shlo) & 0x03030303u) << 4),
                                          (L.y & M4) | (((H.y >> shlo) & 0x03030303u) << 4),
                                          (L.z & M4) | (((H.z >> shlo) & 0x03030303u) << 4),
@@ -1052,18 +1100,25 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
                                          ((L.y >> 4) & M4) | (((H.y >> shhi) & 0x03030303u) << 4),
                                          ((L.z >> 4) & M4) | (((H.z >> shhi) & 0x03030303u) << 4),
                                          ((L.w >> 4) & M4) | (((H.w >> shhi) & 0x03030303u) << 4));
-            const uint32_t scw[4] = {sc[r].x, sc[r].y, sc[r].z, sc[r].w};
+            const uint32_t scw[4] = {st.sc[r].x, st.sc[r].y, st.sc[r].z, st.sc[r].w};
             const int sclo = (int)(int8_t)((scw[glo >> 2] >> (8 * (glo & 3))) & 0xFFu);
             const int schi = (int)(int8_t)((scw[ghi >> 2] >> (8 * (ghi & 3))) & 0xFFu);
-            int isum = sclo * (dot16(vlo, alo, 0) - 32 * blo) + schi * (dot16(vhi, ahi, 0) - 32 * bhi);
+            int isum = sclo * (dot16(vlo, st.alo, 0) - 32 * st.blo) + schi * (dot16(vhi, st.ahi, 0) - 32 * st.bhi);
             if (BLOCK_SUMS) {
 #pragma unroll
                 for (int o = 1; o < 8; o <<= 1) isum += __shfl_xor(isum, o, AMV_WAVE);
-                if (t == 0 && j0 + lane < nsl && mmv_row<EP>(wave, r, R, n_rows) < n_rows) sums[(size_t)mmv_row<EP>(wave, r, R, n_rows) * nsb + sb] = isum;
-            } else if (j0 + lane < nsl) {
-                acc[r] = fmaf(amv_h2f(dd[r]) * da, (float)isum, acc[r]);
+                if (t == 0 && st.valid && mmv_row<EP>(wave, r, R, n_rows) < n_rows) sums[(size_t)mmv_row<EP>(wave, r, R, n_rows) * nsb + sb] = isum;
+            } else if (st.valid) {
+                acc[r] = fmaf(amv_h2f(st.dd[r]) * st.da, (float)isum, acc[r]);
             }
         }
+    };
+    for (int j0 = live ? 64 * ks : nsl; j0 < nsl; j0 += 128 * S) {
+        Step s0, s1;
+        load(j0, s0);
+        load(j0 + 64 * S, s1);
+        compute(s0);
+        compute(s1);
     }
     if constexpr (!BLOCK_SUMS) {
         mmv_finish<R, EP, S>(acc, lane, wi, ks, live, wave, n_rows, dst, epi, eout, post, ra);
