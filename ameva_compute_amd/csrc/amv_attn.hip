@@ -248,6 +248,15 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
             const int i = min(kw0 + 4 * u + grp, n_kv - 1);
             vr[u] = fa_row<KT>(vh + (size_t)i * v_row, lane & 15);
         }
+        // the mask values of the lane's keys, loaded with the rest and converted where they are used (a load behind
+        // a branch, or converted here, makes the compiler wait for every load issued so far); without a mask the
+        // lanes read element 0 of q and ignore it
+        uint16_t mraw[U];
+        {
+            const uint16_t* mp = mask ? mask : reinterpret_cast<const uint16_t*>(q);
+#pragma unroll
+            for (int u = 0; u < U; ++u) mraw[u] = mp[mask ? min(kw0 + 4 * u + grp, n_kv - 1) : 0];
+        }
         // q of the G heads, 8 dims per lane: rounded to f16 for an f16 cache, else quantized to Q8_0 blocks
         float qv[G][8];
         uint32_t qq[G][2];
@@ -270,7 +279,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = kw0 + 4 * u + grp;
-            const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
+            const float mk = (i < n_kv) ? (mask ? amv_h2f(mraw[u]) : 0.0f) : -INFINITY;
             if constexpr (KT == FA_F16) {
                 // q (rounded to f16) . k as 4 v_dot2_f32_f16 per head: the f16 products are exact in f32
                 const uint32_t kw[4] = {kr[u].a.x, kr[u].a.y, kr[u].a.z, kr[u].a.w};
@@ -471,6 +480,15 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
             const int i = min(kw0 + 4 * u + grp, n_kv - 1);
             vr[u] = amv_ld_stream(reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + 16 * c16));
         }
+        // the mask values of the lane's score keys kw0 + 4 grp + e, loaded with the rest and converted where they are
+        // used (a load behind a branch, or converted here, makes the compiler wait for every load issued so far);
+        // without a mask the lanes read element 0 of q and ignore it
+        uint16_t mraw[4];
+        {
+            const uint16_t* mp = mask ? mask : reinterpret_cast<const uint16_t*>(q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mraw[e] = mp[mask ? min(kw0 + 4 * grp + e, n_kv - 1) : 0];
+        }
         // q as the B operand: head c16 (columns from G on are zero), dims 32 kk + 8 grp .. + 7, rounded to f16
         fa_h8 qb[4];
         {
@@ -493,7 +511,7 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = kw0 + 4 * grp + e;
-            const float mk = (i < n_kv) ? (mask ? amv_h2f(mask[i]) : 0.0f) : -INFINITY;
+            const float mk = (i < n_kv) ? (mask ? amv_h2f(mraw[e]) : 0.0f) : -INFINITY;
             sc[e] = (mk == -INFINITY) ? -INFINITY : (S[e] * scale + mk) * AMV_LOG2E;
         }
         float mm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
