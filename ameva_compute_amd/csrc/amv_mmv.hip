@@ -66,9 +66,28 @@ struct MmvPost {
 };
 
 // the segment of stacked row `row` and its row within that matrix
+// The fields of segment s are read by constant index and selected: a run-time index into the by-value kernel argument
+// makes the compiler read it with vector loads from the argument segment, and every weight address then waits for
+// them (a memory round trip before the weight stream).
+__device__ __forceinline__ int mmv_seg_first(const MmvPost& p, int s) {
+    const int r0 = p.seg_row[0], r1 = p.seg_row[1], r2 = p.seg_row[2], r3 = p.seg_row[3];
+    return s == 0 ? r0 : s == 1 ? r1 : s == 2 ? r2 : r3;
+}
+__device__ __forceinline__ const uint8_t* mmv_seg_w(const MmvPost& p, int s) {
+    const uint8_t* w0 = p.w_seg[0];
+    const uint8_t* w1 = p.w_seg[1];
+    const uint8_t* w2 = p.w_seg[2];
+    return s == 0 ? w0 : s == 1 ? w1 : w2;
+}
+__device__ __forceinline__ float* mmv_seg_dst(const MmvPost& p, int s) {
+    float* d0 = p.dst_seg[0];
+    float* d1 = p.dst_seg[1];
+    float* d2 = p.dst_seg[2];
+    return s == 0 ? d0 : s == 1 ? d1 : d2;
+}
 __device__ __forceinline__ int mmv_seg(const MmvPost& p, int row, int& local) {
     const int s = (row >= p.seg_row[1]) + (row >= p.seg_row[2]);
-    local = row - p.seg_row[s];
+    local = row - mmv_seg_first(p, s);
     return s;
 }
 
@@ -141,8 +160,8 @@ __device__ __forceinline__ void mmv_finish(const float (&acc)[R], int lane, int 
         if constexpr (SEG) {
             int lr;
             const int sg = mmv_seg(post, r0, lr);
-            post.dst_seg[sg][lr] = y0;
-            post.dst_seg[sg][lr + 1] = y1;
+            mmv_seg_dst(post, sg)[lr] = y0;
+            mmv_seg_dst(post, sg)[lr + 1] = y1;
         } else {
             dst[r0] = y0;
             dst[r0 + 1] = y1;
@@ -247,9 +266,9 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0(const uint4* __restrict__ wq, 
         if constexpr (SEG) {
             int lr;
             const int sg = mmv_seg(post, row, lr);
-            const uint32_t rows_s = (uint32_t)(post.seg_row[sg + 1] - post.seg_row[sg]);
-            wqr[r] = reinterpret_cast<const uint4*>(post.w_seg[sg]);
-            wdr[r] = reinterpret_cast<const uint16_t*>(post.w_seg[sg] + (size_t)rows_s * nb * 16);
+            const uint32_t rows_s = (uint32_t)(mmv_seg_first(post, sg + 1) - mmv_seg_first(post, sg));
+            wqr[r] = reinterpret_cast<const uint4*>(mmv_seg_w(post, sg));
+            wdr[r] = reinterpret_cast<const uint16_t*>(mmv_seg_w(post, sg) + (size_t)rows_s * nb * 16);
             row = lr;
         }
         rb[r] = (uint32_t)row * (uint32_t)nb;
@@ -547,9 +566,9 @@ __global__ __launch_bounds__(256) void k_mmv_q4_0_k4096_ep(const uint4* __restri
     if constexpr (SEG) {
         int lr;
         const int sg = mmv_seg(post, row0, lr);
-        const size_t rows_s = (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]);
-        wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
-        wds = reinterpret_cast<const uint32_t*>(post.w_seg[sg] + rows_s * 128 * 16);
+        const size_t rows_s = (size_t)(mmv_seg_first(post, sg + 1) - mmv_seg_first(post, sg));
+        wqs = reinterpret_cast<const uint4*>(mmv_seg_w(post, sg));
+        wds = reinterpret_cast<const uint32_t*>(mmv_seg_w(post, sg) + rows_s * 128 * 16);
         row0 = lr;
     }
     uint4 w[2][2];
@@ -624,24 +643,22 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_0_k4096_norm(const float4* __rest
     __shared__ __align__(16) float s_h[WG_TAIL ? NW * P : 4];
     const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6;
     const int wave = blockIdx.x * NW + wi;
-    AmvRms1024<NT> nr;
-    amv_rms1024_load<NT>(x4, nw4, nr);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();  // issue order only: no wait for the loads
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 w[2][R];
-    uint32_t dw[2][R / 2];
+    // the weight rows' addresses first (no memory access): the segment selects branch, and control flow between the
+    // row loads and the barrier below lets the compiler move the barrier above the row loads
     bool live;
+    const uint4* wg = wq;  // SW: gate rows o .. o + P - 1 and the same up rows; their scales in P / 2 row-pair dwords
+    const uint4* wu = wq;
+    const uint32_t* dg = wd2;
+    const uint32_t* du = wd2;
+    int o = 0, ou = 0;
+    const uint4* wqs = wq;  // EP 5: rows row0, row0 + 1
+    const uint32_t* wds = wd2;
+    int row0 = 0;
     if constexpr (SW) {
-        // gate rows o .. o + P - 1 and the same up rows; their scales in P / 2 row-pair dwords per matrix
         const int F = n_rows >> 1;
         live = P * wave < F;
-        const int o = min(P * wave, F - P);  // a wave past the end re-reads the last rows and stores nothing
-        const uint4* wg = wq;
-        const uint4* wu = wq;
-        const uint32_t* dg = wd2;
-        const uint32_t* du = wd2;
-        int ou = F + o;
+        o = min(P * wave, F - P);  // a wave past the end re-reads the last rows and stores nothing
+        ou = F + o;
         if constexpr (SEG) {
             wg = reinterpret_cast<const uint4*>(post.w_seg[0]);
             wu = reinterpret_cast<const uint4*>(post.w_seg[1]);
@@ -649,6 +666,26 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_0_k4096_norm(const float4* __rest
             du = reinterpret_cast<const uint32_t*>(post.w_seg[1] + (size_t)F * 128 * 16);
             ou = o;
         }
+    } else {
+        live = 2 * wave < n_rows;
+        row0 = min(2 * wave, n_rows - 2);
+        if constexpr (SEG) {
+            int lr;
+            const int sg = mmv_seg(post, row0, lr);
+            const size_t rows_s = (size_t)(mmv_seg_first(post, sg + 1) - mmv_seg_first(post, sg));
+            wqs = reinterpret_cast<const uint4*>(mmv_seg_w(post, sg));
+            wds = reinterpret_cast<const uint32_t*>(mmv_seg_w(post, sg) + rows_s * 128 * 16);
+            row0 = lr;
+        }
+    }
+    AmvRms1024<NT> nr;
+    amv_rms1024_load<NT>(x4, nw4, nr);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();  // issue order only: no wait for the loads
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 w[2][R];
+    uint32_t dw[2][R / 2];
+    if constexpr (SW) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int j = 64 * u + lane;
@@ -664,18 +701,6 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_0_k4096_norm(const float4* __rest
             }
         }
     } else {
-        live = 2 * wave < n_rows;
-        int row0 = min(2 * wave, n_rows - 2);
-        const uint4* wqs = wq;
-        const uint32_t* wds = wd2;
-        if constexpr (SEG) {
-            int lr;
-            const int sg = mmv_seg(post, row0, lr);
-            const size_t rows_s = (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]);
-            wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
-            wds = reinterpret_cast<const uint32_t*>(post.w_seg[sg] + rows_s * 128 * 16);
-            row0 = lr;
-        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int j = 64 * u + lane;
@@ -882,8 +907,8 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const uint4* __restrict__ wq, 
             if constexpr (SEG) {  // the row's matrix: qs of its rows, then their 16-byte heads
                 int lr;
                 const int sg = mmv_seg(post, row, lr);
-                wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
-                whs = wqs + (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]) * nsl;
+                wqs = reinterpret_cast<const uint4*>(mmv_seg_w(post, sg));
+                whs = wqs + (size_t)(mmv_seg_first(post, sg + 1) - mmv_seg_first(post, sg)) * nsl;
                 row = lr;
             }
             st.q[r] = amv_ld_stream(wqs + (size_t)row * nsl + j);
@@ -966,6 +991,24 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_K_norm(const float4* __restrict__
     const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6;
     const int wave = blockIdx.x * NW + wi;
     const bool live = mmv_wave_live<EP>(wave, R, n_rows);
+    // the weight rows' addresses first (no memory access): the segment selects branch, and control flow between the
+    // row loads and the barrier below lets the compiler move the barrier above the row loads
+    int rows[R];
+    const uint4* wqs[R];
+    const uint4* whs[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rows[r] = min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
+        wqs[r] = wq;
+        whs[r] = wh;
+        if constexpr (SEG) {  // the row's matrix: qs of its rows, then their 16-byte heads
+            int lr;
+            const int sg = mmv_seg(post, rows[r], lr);
+            wqs[r] = reinterpret_cast<const uint4*>(mmv_seg_w(post, sg));
+            whs[r] = wqs[r] + (size_t)(mmv_seg_first(post, sg + 1) - mmv_seg_first(post, sg)) * NSL;
+            rows[r] = lr;
+        }
+    }
     AmvRms1024<NT> nr;
     amv_rms1024_load<NT>(x4, nw4, nr);
     __builtin_amdgcn_sched_barrier(0);
@@ -975,21 +1018,12 @@ __global__ __launch_bounds__(NT) void k_mmv_q4_K_norm(const float4* __restrict__
     uint32_t hv[2][R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        int row = min(mmv_row<EP>(wave, r, R, n_rows), n_rows - 1);
-        const uint4* wqs = wq;
-        const uint4* whs = wh;
-        if constexpr (SEG) {  // the row's matrix: qs of its rows, then their 16-byte heads
-            int lr;
-            const int sg = mmv_seg(post, row, lr);
-            wqs = reinterpret_cast<const uint4*>(post.w_seg[sg]);
-            whs = wqs + (size_t)(post.seg_row[sg + 1] - post.seg_row[sg]) * NSL;
-            row = lr;
-        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int j = 64 * u + lane, sb = j >> 3;
-            q[u][r] = amv_ld_stream(wqs + (size_t)row * NSL + j);
-            hv[u][r] = amv_ld_stream(reinterpret_cast<const uint32_t*>(whs + (size_t)row * NSB + sb) + (lane & 3));
+            q[u][r] = amv_ld_stream(wqs[r] + (size_t)rows[r] * NSL + j);
+            hv[u][r] =
+                amv_ld_stream(reinterpret_cast<const uint32_t*>(whs[r] + (size_t)rows[r] * NSB + sb) + (lane & 3));
         }
     }
     __builtin_amdgcn_sched_barrier(0);
