@@ -428,25 +428,27 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
     }
 }
 
-// Pass 1 for an f16 cache with q . k on the matrix cores (16 keys per wave, as k_fa_split<G, 16, FUSED, FA_F16>, same
-// splits and partials): S = K q^T of the wave's 16 keys and the G heads is four v_mfma_f32_16x16x32_f16 over the 128
-// dims (A: key l % 16, dims 32 kk + 8 (l / 16) .. + 7 of its row, loaded as 16 bytes; B: q of head l % 16 rounded to
-// f16, zero columns from G on), so the f16 products are exact and summed in f32 as the dot2 form sums them (in another
-// order). The result gives lane l the scores of keys 4 (l / 16) + e of head l % 16: the maximum and the sum over the
-// 16 keys of a head are over its 4 values and the lane pairs l ^ 16, l ^ 32. The probabilities reach the P V layout
-// of k_fa_split (lane group g: keys 4 u + g, 8 dims per lane) through 16 x G floats of LDS per wave; P V, the merge of
-// the 4 wave partials and the split merge are k_fa_split's.
+// Pass 1 for an f16 cache with q . k on the matrix cores (KPW = 16 or 32 keys per wave, as k_fa_split<G, KPW, FUSED,
+// FA_F16>, same splits and partials; 32 at long contexts: 16384 / 32768 keys 18.7 / 30.5 us against 20.0 / 32.4 us
+// for the VALU form): per 16-key chunk, S = K q^T of its 16 keys and the G heads is four v_mfma_f32_16x16x32_f16
+// over the 128 dims (A: key l % 16, dims 32 kk + 8 (l / 16) .. + 7 of its row, loaded as 16 bytes; B: q of head
+// l % 16 rounded to f16, zero columns from G on), so the f16 products are exact and summed in f32 as the dot2 form
+// sums them (in another order). The result gives lane l the scores of keys 4 (l / 16) + e of head l % 16 in each
+// chunk: the maximum and the sum over a head's keys are over the lane's values and the lane pairs l ^ 16, l ^ 32.
+// The probabilities reach the P V layout of k_fa_split (lane group g: keys 16 c + 4 u + g, 8 dims per lane) through
+// KPW x G floats of LDS per wave; P V, the merge of the 4 wave partials and the split merge are k_fa_split's.
 typedef _Float16 fa_h8 __attribute__((ext_vector_type(8)));
 typedef float fa_f4 __attribute__((ext_vector_type(4)));
 
-template <int G, bool FUSED>
+template <int G, bool FUSED, int KPW>
 __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q, const uint8_t* __restrict__ k,
                                                     const uint8_t* __restrict__ v, const uint16_t* __restrict__ mask,
                                                     float* part, int n_kv_max, const int* __restrict__ n_kv_dev,
                                                     int64_t k_row, int64_t k_head, int64_t v_row, int64_t v_head,
                                                     int n_split, float scale, unsigned int* counters,
                                                     float* __restrict__ out, const AmvActOut act) {
-    constexpr int KPW = 16, U = 4;
+    constexpr int NC = KPW / 16, U = 4;  // 16-key chunks per wave
+    static_assert(KPW == 16 || KPW == 32, "16 or 32 keys per wave");
     constexpr int SBUF = 4 * 4 * G * FA_D > G * (8 * FA_D + FA_MAX_NSPLIT + 1) ? 4 * 4 * G * FA_D
                                                                               : G * (8 * FA_D + FA_MAX_NSPLIT + 1);
     __shared__ __align__(16) float sbuf[SBUF];  // [wave][lane group][head][dim] partial P V; then the merge
@@ -465,29 +467,37 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
         const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
         const uint8_t* kh = k + (size_t)hk * k_head;
         const uint8_t* vh = v + (size_t)hk * v_head;
-        // K as the A operand: lane (grp, c16) takes key kw0 + c16, bytes 64 kk + 16 grp (an instruction covers half of
-        // each of 16 rows' lines: ordinary loads, so the second half meets the line in L2)
-        uint4 kr[4];
-        const int ik = min(kw0 + c16, n_kv - 1);
+        // per 16-key chunk c (keys kw0 + 16 c ..): K as the A operand: lane (grp, c16) takes key kw0 + 16 c + c16,
+        // bytes 64 kk + 16 grp (an instruction covers half of each of 16 rows' lines: ordinary loads, so the second
+        // half meets the line in L2)
+        uint4 kr[NC][4];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-            kr[kk] = *reinterpret_cast<const uint4*>(kh + (size_t)ik * k_row + 64 * kk + 16 * grp);
-        // V in k_fa_split's layout: lane (grp, c16) takes key kw0 + 4 u + grp, dims 8 c16 .. + 7 (whole 256-byte rows
-        // per 16 lanes: streamed)
-        uint4 vr[U];
+        for (int c = 0; c < NC; ++c) {
+            const int ik = min(kw0 + 16 * c + c16, n_kv - 1);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = min(kw0 + 4 * u + grp, n_kv - 1);
-            vr[u] = amv_ld_stream(reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + 16 * c16));
+            for (int kk = 0; kk < 4; ++kk)
+                kr[c][kk] = *reinterpret_cast<const uint4*>(kh + (size_t)ik * k_row + 64 * kk + 16 * grp);
         }
-        // the mask values of the lane's score keys kw0 + 4 grp + e, loaded with the rest and converted where they are
-        // used (a load behind a branch, or converted here, makes the compiler wait for every load issued so far);
-        // without a mask the lanes read element 0 of q and ignore it
-        uint16_t mraw[4];
+        // V in k_fa_split's layout: lane (grp, c16) takes key kw0 + 16 c + 4 u + grp, dims 8 c16 .. + 7 (whole
+        // 256-byte rows per 16 lanes: streamed)
+        uint4 vr[NC][U];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int i = min(kw0 + 16 * c + 4 * u + grp, n_kv - 1);
+                vr[c][u] = amv_ld_stream(reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + 16 * c16));
+            }
+        // the mask values of the lane's score keys kw0 + 16 c + 4 grp + e, loaded with the rest and converted where
+        // they are used (a load behind a branch, or converted here, makes the compiler wait for every load issued so
+        // far); without a mask the lanes read element 0 of q and ignore it
+        uint16_t mraw[NC][4];
         {
             const uint16_t* mp = mask ? mask : reinterpret_cast<const uint16_t*>(q);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) mraw[e] = mp[mask ? min(kw0 + 4 * grp + e, n_kv - 1) : 0];
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mraw[c][e] = mp[mask ? min(kw0 + 16 * c + 4 * grp + e, n_kv - 1) : 0];
         }
         // q as the B operand: head c16 (columns from G on are zero), dims 32 kk + 8 grp .. + 7, rounded to f16
         fa_h8 qb[4];
@@ -502,30 +512,39 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
                 for (int e = 0; e < 8; ++e) qb[kk][e] = c16 < G ? (_Float16)t[e] : (_Float16)0.0f;
             }
         }
-        fa_f4 S = {0.0f, 0.0f, 0.0f, 0.0f};
+        // lane (grp, c16): keys kw0 + 16 c + 4 grp + e of head c16, in log2 units
+        float sc[NC][4];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) S = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(fa_h8, kr[kk]),
-                                                                                 qb[kk], S, 0, 0, 0);
-        // lane (grp, c16): keys kw0 + 4 grp + e of head c16, in log2 units
-        float sc[4];
+        for (int c = 0; c < NC; ++c) {
+            fa_f4 S = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = kw0 + 4 * grp + e;
-            const float mk = (i < n_kv) ? (mask ? amv_h2f(mraw[e]) : 0.0f) : -INFINITY;
-            sc[e] = (mk == -INFINITY) ? -INFINITY : (S[e] * scale + mk) * AMV_LOG2E;
+            for (int kk = 0; kk < 4; ++kk)
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(fa_h8, kr[c][kk]), qb[kk], S, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = kw0 + 16 * c + 4 * grp + e;
+                const float mk = (i < n_kv) ? (mask ? amv_h2f(mraw[c][e]) : 0.0f) : -INFINITY;
+                sc[c][e] = (mk == -INFINITY) ? -INFINITY : (S[e] * scale + mk) * AMV_LOG2E;
+            }
         }
-        float mm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        float mm = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) mm = fmaxf(mm, fmaxf(fmaxf(sc[c][0], sc[c][1]), fmaxf(sc[c][2], sc[c][3])));
         mm = amv_max_x32(amv_max_x16(mm));
         float ll = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            sc[e] = __builtin_amdgcn_exp2f(sc[e] - (mm == -INFINITY ? 0.0f : mm));
-            ll += sc[e];
-        }
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sc[c][e] = __builtin_amdgcn_exp2f(sc[c][e] - (mm == -INFINITY ? 0.0f : mm));
+                ll += sc[c][e];
+            }
         ll = amv_sum_x32(amv_sum_x16(ll));
         if (c16 < G) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sP[wv][4 * grp + e][c16] = sc[e];
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sP[wv][16 * c + 4 * grp + e][c16] = sc[c][e];
             if (grp == 0) {
                 sM[wv][c16] = mm;
                 sL[wv][c16] = ll;
@@ -540,21 +559,23 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float vf[8];
-            const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+        for (int c = 0; c < NC; ++c)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
-                vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+            for (int u = 0; u < U; ++u) {
+                float vf[8];
+                const uint32_t vw[4] = {vr[c][u].x, vr[c][u].y, vr[c][u].z, vr[c][u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
+                    vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+                }
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float p = sP[wv][16 * c + 4 * u + grp][g];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+                }
             }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float p = sP[wv][4 * u + grp][g];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
-            }
-        }
         // the 4 lane groups of a wave share the wave's maximum, so their accumulators add; the sum is taken below
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -612,6 +633,7 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float* __restrict__ pa
 }
 
 // keys per wave: 16, or 32 when 16 would leave more than 4 workgroups per CU (long contexts)
+// (measured on MI355X, f16 cache, 8 KV heads: 32 keys per wave at 4096 keys 9.97 against 9.85 us for 16)
 static int fa_kpw(int64_t n_kv, int64_t n_head_kv) { return (n_kv * n_head_kv) / (4 * 16) > 1024 ? 32 : 16; }
 
 extern "C" int64_t amv_flash_attn_workspace_bytes(int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D) {
@@ -670,11 +692,12 @@ static void fa_launch_split(int G, int kpw, dim3 grid, hipStream_t st, const flo
 #define FA_LAUNCH(GG, KK)                                                                                              \
     hipLaunchKernelGGL((k_fa_split<GG, KK, FUSED, KT>), grid, dim3(256), 0, st, q, kk, vv, mm, part, n_kv, n_kv_dev, \
                        k_row, k_head, v_row, v_head, n_split, scale, rule, counters, out, act)
-#define FA_MF(GG)                                                                                                   \
-    hipLaunchKernelGGL((k_fa_split_mf<GG, FUSED>), dim3(grid.y, grid.x), dim3(256), 0, st, q, kk, vv, mm, part, n_kv, \
-                       n_kv_dev, k_row, k_head, v_row, v_head, n_split, scale, counters, out, act)
+#define FA_MF(GG, KK)                                                                                            \
+    hipLaunchKernelGGL((k_fa_split_mf<GG, FUSED, KK>), dim3(grid.y, grid.x), dim3(256), 0, st, q, kk, vv, mm, part, \
+                       n_kv, n_kv_dev, k_row, k_head, v_row, v_head, n_split, scale, counters, out, act)
 #define FA_G(GG)                                  \
-    if (KT == FA_F16 && kpw == 16) FA_MF(GG);      \
+    if (KT == FA_F16 && kpw == 16) FA_MF(GG, 16);  \
+    else if (KT == FA_F16) FA_MF(GG, 32);          \
     else if (kpw == 16) FA_LAUNCH(GG, 16);         \
     else FA_LAUNCH(GG, 32)
     switch (G) {

@@ -847,7 +847,8 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q4k_sb(const uint4* __restrict_
 // in flight while one computes. Reads the plain Q8_K layout (the prefix of AMV_ACT_Q8_K_MMA too).
 template <int TI, int TJ, int NW, bool SUMS>
 __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restrict__ wl, const uint8_t* __restrict__ wqh,
-                                                       const uint32_t* __restrict__ wsc, const uint16_t* __restrict__ wd,
+                                                       const uint32_t* __restrict__ wsc,
+                                                       const uint16_t* __restrict__ wd,
                                                        int N, int nsb, const int8_t* __restrict__ aq,
                                                        const float* __restrict__ ad, int M, float* __restrict__ dst,
                                                        int64_t ldd, int32_t* __restrict__ sums) {
@@ -890,7 +891,8 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
         for (int i = 0; i < TI; ++i) {
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                lq[s][i][h] = __builtin_nontemporal_load(reinterpret_cast<const sb_v4u*>(lr[i] + (size_t)sb * 128 + 64 * h));
+                lq[s][i][h] =
+                    __builtin_nontemporal_load(reinterpret_cast<const sb_v4u*>(lr[i] + (size_t)sb * 128 + 64 * h));
             lh[s][i] = __builtin_nontemporal_load(reinterpret_cast<const sb_v4u*>(hr[i] + (size_t)sb * 64));
             ls[s][i] = wsc[(rb[i] + sb) * 4 + lc];
             ldw[s][i] = wd[rb[i] + sb];
@@ -898,7 +900,8 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) la[s][j][c] = *reinterpret_cast<const sb_v4u*>(ar[j] + (size_t)sb * 256 + 64 * c);
+            for (int c = 0; c < 4; ++c)
+                la[s][j][c] = *reinterpret_cast<const sb_v4u*>(ar[j] + (size_t)sb * 256 + 64 * c);
             lda[s][j] = dr[j][sb];
         }
     };
@@ -944,7 +947,8 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_q6k_sb(const uint8_t* __restric
             // the 4 scale dwords and d of row r16: loaded by lanes 4 r16 + c
             uint32_t scw[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) scw[c] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * r16 + c), (int)ls[s][i]);
+            for (int c = 0; c < 4; ++c)
+                scw[c] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * r16 + c), (int)ls[s][i]);
             const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(16 * r16, (int)ldw[s][i]);
             // the qh run of half h for this lane group: lane group 2 h + (g & 1) holds it
             uint32_t qh[2][4];

@@ -1141,7 +1141,8 @@ __global__ __launch_bounds__(256) void k_mmv_q6_K(const uint4* __restrict__ wl, 
             if (BLOCK_SUMS) {
 #pragma unroll
                 for (int o = 1; o < 8; o <<= 1) isum += __shfl_xor(isum, o, AMV_WAVE);
-                if (t == 0 && st.valid && mmv_row<EP>(wave, r, R, n_rows) < n_rows) sums[(size_t)mmv_row<EP>(wave, r, R, n_rows) * nsb + sb] = isum;
+                const int rr = mmv_row<EP>(wave, r, R, n_rows);
+                if (t == 0 && st.valid && rr < n_rows) sums[(size_t)rr * nsb + sb] = isum;
             } else if (st.valid) {
                 acc[r] = fmaf(amv_h2f(st.dd[r]) * st.da, (float)isum, acc[r]);
             }
