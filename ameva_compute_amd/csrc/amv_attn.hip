@@ -35,7 +35,8 @@
 // a context of up to 64 splits: 4096 keys).
 template <int G>
 __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns, int hk, float* __restrict__ out,
-                                         const AmvActOut& act, float* sbuf) {
+                                         const AmvActOut& act, float* sbuf, const int* n_kv_dev = nullptr,
+                                         int n_kv_max = 0, int split_len = 1) {
     constexpr int GB = G < 4 ? G : 4;  // heads per batch of acc loads
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int c4 = tid & 31, zg = tid >> 5;
@@ -44,7 +45,28 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
     float* sL = sw + G * FA_MAX_NSPLIT;    // [G]
     const float* ph0 = part + (size_t)hk * G * n_split * FA_PS;
     const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (ns == 0) {  // no keys: zero outputs (every index below may assume a split 0)
+    // The first loads do not depend on ns (which a caller may take from a key count in device memory): they read
+    // the launch's splits up to n_split - 1, and a split past ns (whose partial this launch did not write) is
+    // selected away, never multiplied. Unconditional loads of valid addresses: a conditional load would be turned
+    // into a select of addresses with a stack zero, i.e. slow flat loads.
+    float4 va[GB][8];  // acc rows of splits zg + 8 i of heads 0 .. GB - 1
+#pragma unroll
+    for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int z = min(zg + 8 * i, n_split - 1);
+            va[g][i] = *reinterpret_cast<const float4*>(ph0 + ((size_t)g * n_split + z) * FA_PS + 4 + 4 * c4);
+        }
+    float2 ml0[(G + 3) / 4];  // (m, l) of split lane of head wv + 4 j
+#pragma unroll
+    for (int j = 0; j < (G + 3) / 4; ++j) {
+        const int g = min(wv + 4 * j, G - 1);
+        ml0[j] = *reinterpret_cast<const float2*>(ph0 + ((size_t)g * n_split + min(lane, n_split - 1)) * FA_PS);
+    }
+    // with n_kv_dev, ns comes from the key count in device memory, read only now that the loads above are issued
+    asm volatile("" ::: "memory");
+    if (n_kv_dev) ns = (max(0, min(*n_kv_dev, n_kv_max)) + split_len - 1) / split_len;
+    if (ns == 0) {  // no keys: zero outputs
         for (int c = tid; c < G * (FA_D / 4); c += 256) {
             const float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             *reinterpret_cast<float4*>(out + (size_t)hk * G * FA_D + 4 * c) = zero4;
@@ -52,20 +74,12 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
         }
         return;
     }
-    // Loads past the last split read split ns - 1 and get weight 0 (unconditional loads of valid addresses: a
-    // conditional load would be turned into a select of addresses with a stack zero, i.e. slow flat loads).
-    float4 va[GB][8];  // acc rows of splits zg + 8 i of heads 0 .. GB - 1
 #pragma unroll
-    for (int g = 0; g < GB; ++g)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int z = min(zg + 8 * i, ns - 1);
-            va[g][i] = *reinterpret_cast<const float4*>(ph0 + ((size_t)g * n_split + z) * FA_PS + 4 + 4 * c4);
-        }
-    for (int g = wv; g < G; g += 4) {
+    for (int j = 0; j < (G + 3) / 4; ++j) {
+        const int g = wv + 4 * j;
+        if (g >= G) break;  // uniform per wave
         const float* ph = ph0 + (size_t)g * n_split * FA_PS;
-        const int z0 = min(lane, ns - 1);
-        const float m0r = ph[(size_t)z0 * FA_PS], l0 = ph[(size_t)z0 * FA_PS + 1];
+        const float m0r = ml0[j].x, l0 = ml0[j].y;
         const float m0 = lane < ns ? m0r : -INFINITY;
         float m = m0;
         for (int z = lane + 64; z < ns; z += 64) m = fmaxf(m, ph[(size_t)z * FA_PS]);
@@ -105,6 +119,13 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
                 for (int i = 0; i < 8; ++i) {
                     const int z = z0 + 8 * i;
                     v[i] = z0 == zg ? va[gb][i] : *reinterpret_cast<const float4*>(pa + (size_t)min(z, ns - 1) * FA_PS);
+                    // a split this launch did not write: its bits masked to zero (an integer mask, not a select of
+                    // values, which the compiler would turn into a select of addresses with a stack zero)
+                    const uint32_t km = z < ns ? 0xFFFFFFFFu : 0u;
+                    v[i] = make_float4(__uint_as_float(__float_as_uint(v[i].x) & km),
+                                       __uint_as_float(__float_as_uint(v[i].y) & km),
+                                       __uint_as_float(__float_as_uint(v[i].z) & km),
+                                       __uint_as_float(__float_as_uint(v[i].w) & km));
                     w[i] = z < ns ? sw[g * FA_MAX_NSPLIT + z] : 0.0f;
                 }
 #pragma unroll
@@ -459,12 +480,13 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
     const int split = blockIdx.y, hk = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int grp = lane >> 4, c16 = lane & 15, d8 = 8 * c16;
-    int n_kv = n_kv_max;
-    if (n_kv_dev) n_kv = max(0, min(*n_kv_dev, n_kv_max));
-    const int ns = (n_kv + 4 * KPW - 1) / (4 * KPW);  // splits holding keys
-
-    if (split < ns) {
-        const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
+    // Every load below is addressed within the launch's n_kv_max keys and issued before the key count in device
+    // memory is read; keys from n_kv on are selected away (score -inf, V values 0), and a workgroup past the last
+    // split holding keys drops its loads.
+    int n_kv = n_kv_max, ns = 0;                 // ns: splits holding keys
+    const int kw0 = split * 4 * KPW + wv * KPW;  // first key of this wave
+    const int klast = n_kv_max - 1;
+    {
         const uint8_t* kh = k + (size_t)hk * k_head;
         const uint8_t* vh = v + (size_t)hk * v_head;
         // per 16-key chunk c (keys kw0 + 16 c ..): K as the A operand: lane (grp, c16) takes key kw0 + 16 c + c16,
@@ -473,7 +495,7 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
         uint4 kr[NC][4];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int ik = min(kw0 + 16 * c + c16, n_kv - 1);
+            const int ik = min(kw0 + 16 * c + c16, klast);
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
                 kr[c][kk] = *reinterpret_cast<const uint4*>(kh + (size_t)ik * k_row + 64 * kk + 16 * grp);
@@ -485,7 +507,7 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
         for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int i = min(kw0 + 16 * c + 4 * u + grp, n_kv - 1);
+                const int i = min(kw0 + 16 * c + 4 * u + grp, klast);
                 vr[c][u] = amv_ld_stream(reinterpret_cast<const uint4*>(vh + (size_t)i * v_row + 16 * c16));
             }
         // the mask values of the lane's score keys kw0 + 16 c + 4 grp + e, loaded with the rest and converted where
@@ -497,7 +519,7 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
 #pragma unroll
             for (int c = 0; c < NC; ++c)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) mraw[c][e] = mp[mask ? min(kw0 + 16 * c + 4 * grp + e, n_kv - 1) : 0];
+                for (int e = 0; e < 4; ++e) mraw[c][e] = mp[mask ? min(kw0 + 16 * c + 4 * grp + e, klast) : 0];
         }
         // q as the B operand: head c16 (columns from G on are zero), dims 32 kk + 8 grp .. + 7, rounded to f16
         fa_h8 qb[4];
@@ -512,6 +534,10 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
                 for (int e = 0; e < 8; ++e) qb[kk][e] = c16 < G ? (_Float16)t[e] : (_Float16)0.0f;
             }
         }
+        asm volatile("" ::: "memory");  // the key count is read after the loads above are issued
+        if (n_kv_dev) n_kv = max(0, min(*n_kv_dev, n_kv_max));
+        ns = (n_kv + 4 * KPW - 1) / (4 * KPW);
+        if (split < ns) {  // uniform per workgroup
         // lane (grp, c16): keys kw0 + 16 c + 4 grp + e of head c16, in log2 units
         float sc[NC][4];
 #pragma unroll
@@ -564,10 +590,11 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
             for (int u = 0; u < U; ++u) {
                 float vf[8];
                 const uint32_t vw[4] = {vr[c][u].x, vr[c][u].y, vr[c][u].z, vr[c][u].w};
+                const bool live = kw0 + 16 * c + 4 * u + grp < n_kv;  // a row past the keys may hold anything
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    vf[2 * e] = amv_h2f(vw[e] & 0xFFFFu);
-                    vf[2 * e + 1] = amv_h2f(vw[e] >> 16);
+                    vf[2 * e] = live ? amv_h2f(vw[e] & 0xFFFFu) : 0.0f;
+                    vf[2 * e + 1] = live ? amv_h2f(vw[e] >> 16) : 0.0f;
                 }
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
@@ -612,6 +639,7 @@ __global__ __launch_bounds__(256) void k_fa_split_mf(const float* __restrict__ q
                 }
             }
         }
+        }
     }
     if constexpr (FUSED) {
         if (!amv_arrive_last(counters + AMV_CNT_STRIDE * hk, gridDim.y)) return;
@@ -627,9 +655,7 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float* __restrict__ pa
                                                    int n_split, int n_kv_max, const int* __restrict__ n_kv_dev,
                                                    int split_len, const AmvActOut act) {
     __shared__ __align__(16) float sbuf[GH * (8 * FA_D + FA_MAX_NSPLIT + 1)];
-    int ns = n_split;
-    if (n_kv_dev) ns = (max(0, min(*n_kv_dev, n_kv_max)) + split_len - 1) / split_len;
-    fa_merge<GH>(part, n_split, ns, blockIdx.x, out, act, sbuf);
+    fa_merge<GH>(part, n_split, n_split, blockIdx.x, out, act, sbuf, n_kv_dev, n_kv_max, split_len);
 }
 
 // keys per wave: 16, or 32 when 16 would leave more than 4 workgroups per CU (long contexts)
