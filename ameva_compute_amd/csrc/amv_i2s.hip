@@ -58,31 +58,52 @@ __global__ __launch_bounds__(256) void k_i2s_gemv(const uint4* __restrict__ w, i
     int acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0;
-    for (int j0 = 0; j0 < nsl; j0 += 64) {
+    // two 64-slice steps per pass, every load of both issued before either step's arithmetic and none behind a
+    // lane branch (a lane past the row's end reads slice nsl - 1 and adds nothing): one memory round trip per pass
+    struct Step {
+        uint4 c[R];
+        int4 a[4];
+        bool valid;
+    };
+    const auto load = [&](int j0, Step& st) {
         const int j = j0 + lane;
         const int jj = min(j, nsl - 1);
-        uint4 c[R];
+        st.valid = j < nsl;
 #pragma unroll
-        for (int r = 0; r < R; ++r) c[r] = amv_ld_stream(w + (size_t)min(row0 + r, n_rows - 1) * nsl + jj);
-        if (j < nsl) {
-            const int b = jj >> 1, p = jj & 1;
-            int4 a[4];
+        for (int r = 0; r < R; ++r) st.c[r] = amv_ld_stream(w + (size_t)min(row0 + r, n_rows - 1) * nsl + jj);
+        const int b = jj >> 1, p = jj & 1;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) a[g] = a4[b * 8 + 2 * g + p];
+        for (int g = 0; g < 4; ++g) st.a[g] = a4[b * 8 + 2 * g + p];
+    };
+    const auto compute = [&](const Step& st) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                int s = acc[r];
+        for (int r = 0; r < R; ++r) {
+            int s = acc[r];
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int sh = 6 - 2 * g;
-                    s = amv_dot4((int)((c[r].x >> sh) & 0x03030303u), a[g].x, s);
-                    s = amv_dot4((int)((c[r].y >> sh) & 0x03030303u), a[g].y, s);
-                    s = amv_dot4((int)((c[r].z >> sh) & 0x03030303u), a[g].z, s);
-                    s = amv_dot4((int)((c[r].w >> sh) & 0x03030303u), a[g].w, s);
-                }
-                acc[r] = s;
+            for (int g = 0; g < 4; ++g) {
+                const int sh = 6 - 2 * g;
+                s = amv_dot4((int)((st.c[r].x >> sh) & 0x03030303u), st.a[g].x, s);
+                s = amv_dot4((int)((st.c[r].y >> sh) & 0x03030303u), st.a[g].y, s);
+                s = amv_dot4((int)((st.c[r].z >> sh) & 0x03030303u), st.a[g].z, s);
+                s = amv_dot4((int)((st.c[r].w >> sh) & 0x03030303u), st.a[g].w, s);
             }
+            acc[r] = st.valid ? s : acc[r];
         }
+    };
+    // a row of at most 64 slices (K <= 4096) takes the single step after the loop, no pass of clamped reads
+    int j0 = 0;
+    for (; j0 + 64 < nsl; j0 += 128) {
+        Step s0, s1;
+        load(j0, s0);
+        load(j0 + 64, s1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(s0);
+        compute(s1);
+    }
+    if (j0 < nsl) {
+        Step s0;
+        load(j0, s0);
+        compute(s0);
     }
     const int2 m = meta[0];
     const float total_scale = __int_as_float(m.x) * wscale;
