@@ -45,7 +45,7 @@ __global__ __launch_bounds__(BN_THREADS) void k_bitnet_norm_q8(const float* __re
         double s = 0.0;
 #pragma unroll
         for (int e = 0; e < BN_MAX_PER_THREAD; ++e) s += (double)v[e] * (double)v[e];
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, AMV_WAVE);
+        s = amv_wave_sum_d_u(s);  // DPP within rows, readlane across them: no LDS round trip per step
         if (lane == 0) sd[wv] = s;
         __syncthreads();
         double tot = 0.0;
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(NT) void k_bitnet_qgemv(const float4* __restrict__ 
     for (int u = 0; u < V4; ++u)
         ss += (double)xv[u].x * xv[u].x + (double)xv[u].y * xv[u].y + (double)xv[u].z * xv[u].z +
               (double)xv[u].w * xv[u].w;
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, AMV_WAVE);
+    ss = amv_wave_sum_d_u(ss);  // DPP within rows, readlane across them: no LDS round trip per step
     if (lane == 0) sd[wv] = ss;
     __syncthreads();
     double tot = 0.0;
