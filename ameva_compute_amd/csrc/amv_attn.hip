@@ -83,7 +83,7 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
         const float m0 = lane < ns ? m0r : -INFINITY;
         float m = m0;
         for (int z = lane + 64; z < ns; z += 64) m = fmaxf(m, ph[(size_t)z * FA_PS]);
-        const float M = amv_wave_max(m);
+        const float M = amv_wave_max_u(m);
         float l = 0.0f;
         if (lane < ns) {
             const float w = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);

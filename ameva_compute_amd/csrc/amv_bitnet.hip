@@ -70,7 +70,7 @@ __global__ __launch_bounds__(BN_THREADS) void k_bitnet_norm_q8(const float* __re
 #pragma unroll
     for (int e = 0; e < BN_MAX_PER_THREAD; ++e)
         if (tid + e * BN_THREADS < n) amax = fmaxf(amax, fabsf(v[e]));
-    amax = amv_wave_max(amax);
+    amax = amv_wave_max_u(amax);
     if (lane == 0) sf[wv] = amax;
     __syncthreads();
     amax = sf[0];
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(BN_THREADS) void k_bitnet_norm_q8(const float* __re
             s += (int)t;
         }
     }
-    s = amv_wave_sum_i(s);
+    s = amv_wave_sum_i_u(s);
     if (lane == 0) si[wv] = s;
     __syncthreads();
     if (tid == 0) {

@@ -183,11 +183,6 @@ __device__ __forceinline__ float amv_wave_sum(float v) {
     return (__int_as_float(__builtin_amdgcn_readlane(i, 0)) + __int_as_float(__builtin_amdgcn_readlane(i, 16))) +
            (__int_as_float(__builtin_amdgcn_readlane(i, 32)) + __int_as_float(__builtin_amdgcn_readlane(i, 48)));
 }
-__device__ __forceinline__ int amv_wave_sum_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, AMV_WAVE);
-    return v;
-}
 #define AMV_LOG2E 1.4426950408889634f
 typedef _Float16 amv_h2 __attribute__((ext_vector_type(2)));  // scores kept in log2 units meet v_exp_f32 (2^x) directly
 
@@ -208,12 +203,6 @@ __device__ __forceinline__ float amv_max_x32(float v) {
 __device__ __forceinline__ float amv_sum_x32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-__device__ __forceinline__ float amv_wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, AMV_WAVE));
-    return v;
 }
 
 // Wave-uniform reductions without LDS round trips: DPP within each 16-lane row, then the four row results read into

@@ -24,7 +24,7 @@ __global__ __launch_bounds__(256) void k_i2s_quant(const float* __restrict__ x, 
     const float* xr = x + (size_t)row * k;
     float amax = 1e-7f;
     for (int i = tid; i < k; i += 256) amax = fmaxf(amax, fabsf(xr[i]));
-    amax = amv_wave_max(amax);
+    amax = amv_wave_max_u(amax);
     if (lane == 0) smax[w] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void k_i2s_quant(const float* __restrict__ x, 
         q[(size_t)row * k + i] = (int8_t)(int)v;
         s += (int)v;
     }
-    s = amv_wave_sum_i(s);
+    s = amv_wave_sum_i_u(s);
     if (lane == 0) ssum[w] = s;
     __syncthreads();
     if (tid == 0) meta[row] = make_int2(__float_as_int(1.0f / scale), ssum[0] + ssum[1] + ssum[2] + ssum[3]);
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void k_i2s_gemv(const uint4* __restrict__ w, i
     const float total_scale = __int_as_float(m.x) * wscale;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int t = amv_wave_sum_i(acc[r]) - m.y;
+        const int t = amv_wave_sum_i_u(acc[r]) - m.y;
         if (lane == 0 && row0 + r < n_rows) {
             if (OUT_SUMS) isums[row0 + r] = t;
             else if (ACC) dst[row0 + r] = dst[row0 + r] + (float)t * total_scale;
