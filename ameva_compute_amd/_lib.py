@@ -72,7 +72,10 @@ SIGNATURES = {
     "amv_bitnet_rope_kv": (I32, [P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
     "amv_gemv_f16": (I32, [P, I64, I64, P, P, P]),
     "amv_bitnet_gemv_fused": (I32, [P, P, P, I64, F32, I32, I32, I32, P, P, P, P, I32, P, P, I64, P]),
+    "amv_bitnet_gemv_fa_merge": (I32, [P, I32, I32, I64, P, P, I64, F32, I32, P, I64, F32, P, I32, P]),
     "amv_set_rows_q": (I32, [I32, P, I64, P, I64, I64, I64, P, I32, I64, I32, P, P]),
+    "amv_flash_attn_split_kv": (I32, [I32, P, P, P, P, I64, I64, I64, P, I64, I64, I64, I64, I64, F32, P, I64, I32, P,
+                                      P, P]),
     "amv_flash_attn_decode_kv": (I32, [I32, P, P, P, P, P, I64, I64, I64, P, I64, I64, I64, I64, I64, F32, P, I64, P,
                                        P, I32, I32, P]),
     "amv_flash_attn_noalloc_max_bytes": (I64, []),

@@ -77,7 +77,20 @@ struct AcBitNetEngine::Impl {
     // pinned staging of what one step reads from the host: x (n_embd), the RoPE table (head_dim), pos and n_kv
     float* h_stage = nullptr;
     size_t stage_floats = 0;
-    hipGraphExec_t graph[2] = {nullptr, nullptr};  // [0] layers, [1] layers + head
+    // [short context][0 layers, 1 layers + head]. At a context of at most kFoldKeys keys (4 key splits) the
+    // attention's split merge runs inside the output projection's prologue (amv_bitnet_gemv_fa_merge, bit-identical
+    // to the merge launch it replaces): one launch fewer per layer; the environment variable
+    // AMV_BITNET_FOLD_MERGE=0 keeps the merge launch at every position.
+    static constexpr uint32_t kFoldKeys = 256;
+    hipGraphExec_t graph[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+    bool fold_merge = true, short_ctx = false;
+    void drop_graphs() {
+        for (auto& gs : graph)
+            for (auto& g : gs) {
+                if (g) (void)hipGraphExecDestroy(g);
+                g = nullptr;
+            }
+    }
     uint64_t weight_bytes = 0, lm_head_bytes = 0, kv_bytes = 0;
     std::vector<void*> allocs;
 
@@ -129,20 +142,36 @@ struct AcBitNetEngine::Impl {
                                             pos_dev, cfg.n_ctx, st),
                       "attn_norm + q8 + attn_q/k/v + rope");
             mark("norm_qkv_rope");
-            amv_check(amv_flash_attn_decode_kv(0, q, L.kc, L.vc, nullptr, att, H, KVH, cfg.n_ctx, pos_dev + 1, hd,
-                                               (int64_t)kv * 4, (int64_t)hd * 4, (int64_t)kv * 4, (int64_t)hd * 4,
-                                               inv_sqrt, fa_ws, fa_ws_bytes, nullptr, nullptr, 8, 0, st),
-                      "attention");
-            mark("attention");
-            // attn_sub_norm (when present) + int8 -> output projection added to x
-            const void* w_o[1] = {L.wo};
             const int64_t r_e[1] = {E};
-            const float s_o[1] = {L.s_o};
             float* d_x[1] = {x};
-            amv_check(amv_bitnet_gemv_fused(att, nullptr, L.attn_sub_norm, E, eps, 0, L.has_attn_sub ? 1 : 0, 1, w_o,
-                                            r_e, s_o, d_x, 1, nullptr, nullptr, 0, st),
-                      "attn_sub_norm + q8 + attn_output + residual");
-            mark("norm_o");
+            if (short_ctx) {
+                // the splits only; their merge + attn_sub_norm + int8 -> output projection added to x
+                const int64_t nk = std::min<int64_t>(cfg.n_ctx, kFoldKeys);
+                int32_t n_split = 0, split_len = 0;
+                amv_check(amv_flash_attn_split_kv(0, q, L.kc, L.vc, nullptr, H, KVH, nk, pos_dev + 1, hd,
+                                                  (int64_t)kv * 4, (int64_t)hd * 4, (int64_t)kv * 4, (int64_t)hd * 4,
+                                                  inv_sqrt, fa_ws, fa_ws_bytes, 0, &n_split, &split_len, st),
+                          "attention splits");
+                mark("attention");
+                amv_check(amv_bitnet_gemv_fa_merge((const float*)fa_ws, n_split, split_len, nk, pos_dev + 1,
+                                                   L.attn_sub_norm, E, eps, L.has_attn_sub ? 1 : 0, L.wo, E, L.s_o, x,
+                                                   1, st),
+                          "attention merge + attn_sub_norm + q8 + attn_output + residual");
+                mark("norm_o");
+            } else {
+                amv_check(amv_flash_attn_decode_kv(0, q, L.kc, L.vc, nullptr, att, H, KVH, cfg.n_ctx, pos_dev + 1, hd,
+                                                   (int64_t)kv * 4, (int64_t)hd * 4, (int64_t)kv * 4, (int64_t)hd * 4,
+                                                   inv_sqrt, fa_ws, fa_ws_bytes, nullptr, nullptr, 8, 0, st),
+                          "attention");
+                mark("attention");
+                // attn_sub_norm (when present) + int8 -> output projection added to x
+                const void* w_o[1] = {L.wo};
+                const float s_o[1] = {L.s_o};
+                amv_check(amv_bitnet_gemv_fused(att, nullptr, L.attn_sub_norm, E, eps, 0, L.has_attn_sub ? 1 : 0, 1,
+                                                w_o, r_e, s_o, d_x, 1, nullptr, nullptr, 0, st),
+                          "attn_sub_norm + q8 + attn_output + residual");
+                mark("norm_o");
+            }
             // ffn_norm + int8 -> gate | up
             const void* w_gu[2] = {L.wg, L.wu};
             const int64_t r_gu[2] = {F, F};
@@ -179,6 +208,7 @@ struct AcBitNetEngine::Impl {
         }
         if (x_in) std::memcpy(h_stage, x_in, (size_t)E * 4);
         int32_t* pp = reinterpret_cast<int32_t*>(h_stage + E + hd);
+        short_ctx = fold_merge && pos + 1 <= std::min<uint32_t>(cfg.n_ctx, kFoldKeys);
         pp[0] = (int32_t)pos;
         pp[1] = (int32_t)pos + 1;
         if (x_in) hip_check(hipMemcpyAsync(x, h_stage, (size_t)E * 4, hipMemcpyHostToDevice, st), "upload x");
@@ -207,7 +237,7 @@ struct AcBitNetEngine::Impl {
             for (auto& m : t.marks) (void)hipEventDestroy(m.second);
             return;
         }
-        hipGraphExec_t& g = graph[with_head ? 1 : 0];
+        hipGraphExec_t& g = graph[short_ctx ? 1 : 0][with_head ? 1 : 0];
         if (!g) {
             hipGraph_t gr = nullptr;
             hip_check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
@@ -229,10 +259,7 @@ struct AcBitNetEngine::Impl {
 
     void release() {
         if (st) (void)hipStreamSynchronize(st);
-        for (auto& g : graph) {
-            if (g) (void)hipGraphExecDestroy(g);
-            g = nullptr;
-        }
+        drop_graphs();
         for (void* p : allocs) (void)hipFree(p);
         allocs.clear();
         if (h_stage) (void)hipHostFree(h_stage);
@@ -268,6 +295,12 @@ void AcBitNetEngine::Initialize() {
         if (strcmp(e, "1") == 0) m.profile = true;
         else if (*e && strcmp(e, "0") != 0)
             throw AcBitNetError(std::string("AC_BITNET_PROFILE must be 0 or 1, got ") + e, (int)AC_ERR_INVALID_ARGUMENT);
+    }
+    if (const char* e = getenv("AMV_BITNET_FOLD_MERGE")) {
+        if (strcmp(e, "0") == 0) m.fold_merge = false;
+        else if (*e && strcmp(e, "1") != 0)
+            throw AcBitNetError(std::string("AMV_BITNET_FOLD_MERGE must be 0 or 1, got ") + e,
+                                (int)AC_ERR_INVALID_ARGUMENT);
     }
     hip_check(hipStreamCreateWithFlags(&m.st, hipStreamNonBlocking), "hipStreamCreate");
     fprintf(stderr, "[ac_bitnet] %s: i2_s GEMV through v_dot4 (exact integers), token step in one HIP graph\n",
@@ -387,10 +420,7 @@ void AcBitNetEngine::UploadLayer(uint32_t l, const BitNetGpuLayerHost& lay) {
     L.s_d = lay.scale_w_down;
     L.uploaded = true;
     // the captured steps hold the norm pointers of this layer: capture again
-    for (auto& g : m.graph) {
-        if (g) (void)hipGraphExecDestroy(g);
-        g = nullptr;
-    }
+    m.drop_graphs();
 }
 
 void AcBitNetEngine::UploadOutput(const float* output_norm, const uint16_t* lm_head_f16, uint32_t n_vocab) {

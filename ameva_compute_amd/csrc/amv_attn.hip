@@ -792,6 +792,32 @@ static int fa_run(const char* fn, int kv, const float* q, const void* k, const v
     return amv_check_launch(fn);
 }
 
+// The split pass alone: the partials for a consumer that merges them itself (the BitNet engine's output projection,
+// amv_bitnet_gemv_fa_merge). The launch, its split count and its keys per split are those of amv_flash_attn_decode_kv
+// at the same n_kv_max; head h, split z at workspace + (h * n_split + z) * FA_PS floats: m, l, two pad, acc[D].
+extern "C" int amv_flash_attn_split_kv(int kv_type, const float* q, const void* k, const void* v, const void* mask,
+                                       int64_t n_head, int64_t n_head_kv, int64_t n_kv_max, const int32_t* n_kv_dev,
+                                       int64_t D, int64_t k_row_bytes, int64_t k_head_bytes, int64_t v_row_bytes,
+                                       int64_t v_head_bytes, float scale, void* workspace, int64_t workspace_bytes,
+                                       int rule, int32_t* n_split_out, int32_t* split_len_out, void* stream) {
+    const char* fn = "amv_flash_attn_split_kv";
+    // the split pass writes no output row: the workspace stands in for `out` in the argument check
+    int rc = fa_check(fn, kv_type, q, k, v, (const float*)workspace, workspace, nullptr, rule, n_head, n_head_kv,
+                      n_kv_max, D, k_row_bytes, k_head_bytes, v_row_bytes, v_head_bytes, workspace_bytes);
+    if (rc) return rc;
+    AMV_REQUIRE(n_split_out && split_len_out, "%s: null pointer", fn);
+    const int G = (int)(n_head / n_head_kv);
+    const int kpw = fa_kpw(n_kv_max, n_head_kv);
+    const int n_split = (int)((n_kv_max + 4 * kpw - 1) / (4 * kpw));
+    fa_launch_kv<false>(kv_type, G, kpw, dim3(n_split, (unsigned)n_head_kv), amv_stream(stream), q,
+                        (const uint8_t*)k, (const uint8_t*)v, (const uint16_t*)mask, (float*)workspace, (int)n_kv_max,
+                        n_kv_dev, k_row_bytes, k_head_bytes, v_row_bytes, v_head_bytes, n_split, scale, rule, nullptr,
+                        nullptr, AmvActOut{});
+    *n_split_out = n_split;
+    *split_len_out = 4 * kpw;
+    return amv_check_launch(fn);
+}
+
 extern "C" int amv_flash_attn_decode(const float* q, const void* k, const void* v, const void* mask, float* out,
                                      int64_t n_head, int64_t n_head_kv, int64_t n_kv, int64_t D, int64_t k_row,
                                      int64_t k_head, int64_t v_row, int64_t v_head, float scale, void* workspace,

@@ -9,6 +9,8 @@
 // The attention over the f32 cache is the split kernel of amv_attn.hip (cache type F32).
 #include "amv_common.h"
 
+#include <algorithm>
+
 #define BN_THREADS 1024
 #define BN_MAX_PER_THREAD 16  // rows up to 16384 elements
 
@@ -233,6 +235,17 @@ template <typename T>
 __device__ __forceinline__ T bn_pick(int s, T v0, T v1, T v2) { return s == 0 ? v0 : (s == 1 ? v1 : v2); }
 __device__ __forceinline__ int bn_beg(const BnSegs& sg, int s) { return bn_pick(s, 0, sg.end[0], sg.end[1]); }
 
+// MODE 3 input: the flash-attention split partials of amv_flash_attn_split_kv (per head h and split z, BN_FA_PS
+// floats at part + (h * n_split + z) * BN_FA_PS: m, l, two pad, acc[128]), merged per element in the prologue; the
+// key count from n_kv[0] (capped at n_kv_max) gives the splits holding keys, at most BN_FA_ZM
+#define BN_FA_PS 132
+#define BN_FA_ZM 4
+struct BnFa {
+    const float* part;
+    const int* n_kv;
+    int n_split, split_len, n_kv_max;
+};
+
 template <int MODE>
 __device__ __forceinline__ float bn_act_t(float x, float y) {
     if constexpr (MODE == 1) {
@@ -249,7 +262,7 @@ template <int NT, int V4, bool ROPE, int MODE, int R>
 __global__ __launch_bounds__(NT) void k_bitnet_qgemv(const float4* __restrict__ a, const float4* __restrict__ b,
                                                     const float4* __restrict__ nw, int k, float eps, int do_norm, const BnSegs sg, int n_seg, int accumulate,
                                                     const float* __restrict__ cs, const int* __restrict__ pos,
-                                                    int n_ctx) {
+                                                    int n_ctx, const BnFa fa) {
     constexpr int NW = NT / 64, NIT = (NT * V4 + 1023) / 1024;  // k <= 4 NT V4: 16-byte weight slices <= 64 NIT
     __shared__ __align__(16) int sq[NT * V4];  // the int8 activation, 4 per int
     __shared__ double sd[NW];
@@ -280,9 +293,28 @@ __global__ __launch_bounds__(NT) void k_bitnet_qgemv(const float4* __restrict__ 
     // under a branch makes the wait at the join conservative, i.e. a wait for the weights before the prologue
     const float4* wp = nw ? nw : a;
     float4 xv[V4], bv[V4], wn[V4];
+    constexpr int VP = MODE == 3 ? V4 : 1;
+    float4 pv[VP][BN_FA_ZM];  // MODE 3: acc of splits 0 .. BN_FA_ZM - 1 of the thread's float4s (head i4 / 32)
+    float2 pml[VP][BN_FA_ZM];  // and their (m, l)
+    // MODE 3: the key count first, a scalar load whose wait does not cover the vector loads below
+    const int fa_nkv = MODE == 3 ? *fa.n_kv : 0;
+    if constexpr (MODE == 3) {
 #pragma unroll
-    for (int u = 0; u < V4; ++u) xv[u] = a[min(tid + NT * u, n4 - 1)];
-    if constexpr (MODE != 0) {
+        for (int u = 0; u < V4; ++u) {
+            const int i4 = min(tid + NT * u, n4 - 1);
+            const float* ph = fa.part + (size_t)(i4 >> 5) * fa.n_split * BN_FA_PS;
+#pragma unroll
+            for (int z = 0; z < BN_FA_ZM; ++z) {
+                const float* pz = ph + (size_t)min(z, fa.n_split - 1) * BN_FA_PS;
+                pv[u][z] = *reinterpret_cast<const float4*>(pz + 4 + 4 * (i4 & 31));
+                pml[u][z] = *reinterpret_cast<const float2*>(pz);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < V4; ++u) xv[u] = a[min(tid + NT * u, n4 - 1)];
+    }
+    if constexpr (MODE == 1 || MODE == 2) {
 #pragma unroll
         for (int u = 0; u < V4; ++u) bv[u] = b[min(tid + NT * u, n4 - 1)];
     }
@@ -298,12 +330,54 @@ __global__ __launch_bounds__(NT) void k_bitnet_qgemv(const float4* __restrict__ 
 #pragma unroll
         for (int it = 0; it < NIT; ++it) c[r][it] = amv_ld_stream(wr + min(it * 64 + lane, nsl - 1));
     }
+    if constexpr (MODE == 3) {
+        // the split merge of k_fa_combine, per element and in its order, so the result is bit-identical to the
+        // merged attention row: M = max m_z, w_z = 2^(m_z - M) (0 for an empty split), L = (l_0 w_0 + l_1 w_1) +
+        // (l_2 w_2 + l_3 w_3) (the wave sum's DPP order over splits in lanes 0..3), t = sum over the 8 split groups
+        // in order of fma(w_z, acc_z, 0), x = t / L (0 when L = 0). Splits past the count are masked with integer
+        // masks, never selected as loaded values.
+        const int nkv = max(0, min(fa_nkv, fa.n_kv_max));
+        const int ns = (nkv + fa.split_len - 1) / fa.split_len;
+#pragma unroll
+        for (int u = 0; u < V4; ++u) {
+            float mz[BN_FA_ZM], w[BN_FA_ZM], lw[BN_FA_ZM];
+            uint32_t km[BN_FA_ZM];
+            float M = -INFINITY;
+#pragma unroll
+            for (int z = 0; z < BN_FA_ZM; ++z) {
+                km[z] = z < ns ? 0xFFFFFFFFu : 0u;
+                mz[z] = __uint_as_float((__float_as_uint(pml[u][z].x) & km[z]) | (0xFF800000u & ~km[z]));
+                M = fmaxf(M, mz[z]);
+            }
+#pragma unroll
+            for (int z = 0; z < BN_FA_ZM; ++z) {
+                w[z] = mz[z] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mz[z] - M);
+                lw[z] = fmaf(__uint_as_float(__float_as_uint(pml[u][z].y) & km[z]), w[z], 0.0f);
+            }
+            const float L = (lw[0] + lw[1]) + (lw[2] + lw[3]);
+            float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int z = 0; z < BN_FA_ZM; ++z) {
+                const float4 v = pv[u][z];
+                t[0] += fmaf(w[z], __uint_as_float(__float_as_uint(v.x) & km[z]), 0.0f);
+                t[1] += fmaf(w[z], __uint_as_float(__float_as_uint(v.y) & km[z]), 0.0f);
+                t[2] += fmaf(w[z], __uint_as_float(__float_as_uint(v.z) & km[z]), 0.0f);
+                t[3] += fmaf(w[z], __uint_as_float(__float_as_uint(v.w) & km[z]), 0.0f);
+            }
+#pragma unroll
+            for (int z = BN_FA_ZM; z < 8; ++z)  // the empty split groups add +0 (turning a -0 sum into +0)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[e] += 0.0f;
+            xv[u] = L == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                              : make_float4(t[0] / L, t[1] / L, t[2] / L, t[3] / L);
+        }
+    }
     // branch-free from here to the first barrier (a branch would let the compiler sink the prologue loads behind
     // the weight loads): scale 1 without the norm and weight 1 without norm_w (x * 1 = x)
 #pragma unroll
     for (int u = 0; u < V4; ++u) {
         const bool in = tid + NT * u < n4;
-        if constexpr (MODE != 0) {
+        if constexpr (MODE == 1 || MODE == 2) {
             xv[u].x = bn_act_t<MODE>(xv[u].x, bv[u].x);
             xv[u].y = bn_act_t<MODE>(xv[u].y, bv[u].y);
             xv[u].z = bn_act_t<MODE>(xv[u].z, bv[u].z);
@@ -483,7 +557,7 @@ extern "C" int amv_bitnet_gemv_fused(const float* a, const float* b, const float
 #define BN_QG_LAUNCH(NT, V4, ROPE, MODE, RR, CS, POS, CTX)                                                       \
     hipLaunchKernelGGL((k_bitnet_qgemv<NT, V4, ROPE, MODE, RR>),                                                   \
                        dim3((unsigned)((waves + NT / 64 - 1) / (NT / 64))), dim3(NT), 0, st, a4, b4, w4, (int)k, eps,  \
-                       do_norm, sg, n_seg, accumulate, CS, POS, CTX)
+                       do_norm, sg, n_seg, accumulate, CS, POS, CTX, BnFa{})
 #define BN_QG_R(NT, V4, RR)                                                                                        \
     do {                                                                                                           \
         if (rope) BN_QG_LAUNCH(NT, V4, true, 0, RR, rope_cs, pos, (int)n_ctx);                                     \
@@ -504,4 +578,46 @@ extern "C" int amv_bitnet_gemv_fused(const float* a, const float* b, const float
 #undef BN_QG_R
 #undef BN_QG_LAUNCH
     return amv_check_launch("amv_bitnet_gemv_fused");
+}
+
+extern "C" int amv_bitnet_gemv_fa_merge(const float* part, int n_split, int split_len, int64_t n_kv_max,
+                                        const int32_t* n_kv_dev, const float* norm_w, int64_t k, float eps,
+                                        int do_norm, const void* w, int64_t rows, float wscale, float* dst,
+                                        int accumulate, void* stream) {
+    AMV_REQUIRE(part && n_kv_dev && w && dst, "amv_bitnet_gemv_fa_merge: null pointer");
+    AMV_REQUIRE(k > 0 && k % 128 == 0 && k <= 16384, "amv_bitnet_gemv_fa_merge: k %lld (heads of 128, <= 16384)",
+                (long long)k);
+    AMV_REQUIRE(n_split >= 1 && split_len >= 1 && n_kv_max >= 1 &&
+                    (n_kv_max + split_len - 1) / split_len <= std::min(n_split, BN_FA_ZM),
+                "amv_bitnet_gemv_fa_merge: %lld keys in splits of %d need more than min(%d, %d) splits",
+                (long long)n_kv_max, split_len, n_split, BN_FA_ZM);
+    AMV_REQUIRE(rows > 0 && rows <= (1 << 24), "amv_bitnet_gemv_fa_merge: rows %lld", (long long)rows);
+    AMV_REQUIRE((((uintptr_t)part | (uintptr_t)norm_w | (uintptr_t)w) & 15) == 0,
+                "amv_bitnet_gemv_fa_merge: part, norm_w and the weights must be 16-byte aligned");
+    BnSegs sg{};
+    sg.w[0] = (const uint4*)w;
+    sg.dst[0] = dst;
+    sg.wscale[0] = wscale;
+    sg.end[0] = sg.end[1] = sg.end[2] = (int)rows;
+    const BnFa fa{part, n_kv_dev, n_split, split_len, (int)n_kv_max};
+    const int R = rows >= 8192 ? 4 : 2;  // the launch shape of amv_bitnet_gemv_fused
+    const int64_t waves = (rows + R - 1) / R;
+    hipStream_t st = amv_stream(stream);
+    const float4 *a4 = (const float4*)part, *w4 = (const float4*)norm_w;
+#define BN_FM_LAUNCH(NT, V4, RR)                                                                                  \
+    hipLaunchKernelGGL((k_bitnet_qgemv<NT, V4, false, 3, RR>), dim3((unsigned)((waves + NT / 64 - 1) / (NT / 64))), \
+                       dim3(NT), 0, st, a4, nullptr, w4, (int)k, eps, do_norm, sg, 1, accumulate, nullptr, nullptr,  \
+                       0, fa)
+#define BN_FM(NT, V4)                          \
+    do {                                       \
+        if (R == 4) BN_FM_LAUNCH(NT, V4, 4);   \
+        else BN_FM_LAUNCH(NT, V4, 2);          \
+    } while (0)
+    if (k > 8192) BN_FM(1024, 4);
+    else if (k > 4096) BN_FM(512, 4);
+    else if (k > 2048) BN_FM(512, 2);
+    else BN_FM(512, 1);
+#undef BN_FM
+#undef BN_FM_LAUNCH
+    return amv_check_launch("amv_bitnet_gemv_fa_merge");
 }

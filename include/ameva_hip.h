@@ -294,6 +294,16 @@ int amv_bitnet_gemv_fused(const float* a, const float* b, const float* norm_w, i
                           int do_norm, int n_seg, const void* const* w, const int64_t* rows, const float* wscale,
                           float* const* dst, int accumulate, const float* rope_cs, const int32_t* pos, int64_t n_ctx,
                           void* stream);
+/* The output projection group of the BitNet token step with the attention's split merge in its prologue (no
+ * counterpart in the reference, whose engine runs attention as one dispatch; for the HIP engine at short contexts,
+ * where the merge launch is a memory round trip the projection's prologue already pays): every workgroup merges the
+ * partials of amv_flash_attn_split_kv (part, n_split splits of split_len keys, the key count n_kv_dev[0] capped at
+ * n_kv_max; k / 128 heads of 128) exactly as amv_flash_attn_decode_kv's merge does, then runs
+ * amv_bitnet_gemv_fused(att, NULL, norm_w, k, eps, 0, do_norm, 1, {w}, {rows}, {wscale}, {dst}, accumulate):
+ * bit-identical to the split + merge + projection launches. n_kv_max may span at most min(n_split, 4) splits. */
+int amv_bitnet_gemv_fa_merge(const float* part, int n_split, int split_len, int64_t n_kv_max, const int32_t* n_kv_dev,
+                             const float* norm_w, int64_t k, float eps, int do_norm, const void* w, int64_t rows,
+                             float wscale, float* dst, int accumulate, void* stream);
 
 int amv_i2s_gemv_f32(const void* w, int64_t n_rows, int64_t k, const float* x, float scale, float* y, void* stream);
 
@@ -383,6 +393,17 @@ int amv_flash_attn_decode_kv(int kv_type, const float* q, const void* k, const v
                              int64_t k_row_bytes, int64_t k_head_bytes, int64_t v_row_bytes, int64_t v_head_bytes,
                              float scale, void* workspace, int64_t workspace_bytes, unsigned int* counters, void* act,
                              int act_type, int rule, void* stream);
+
+/* The split pass of amv_flash_attn_decode_kv alone, for a consumer that merges the partials itself
+ * (amv_bitnet_gemv_fa_merge; no counterpart in the reference). Same launch, arguments and workspace as
+ * amv_flash_attn_decode_kv with counters == NULL and no output; writes the launch's split count and keys per split to
+ * *n_split and *split_len. Head h, split z: (m, l, pad, pad, acc[D]) at workspace + (h * n_split + z) * (D + 4) floats
+ * for the splits that hold keys. */
+int amv_flash_attn_split_kv(int kv_type, const float* q, const void* k, const void* v, const void* mask, int64_t n_head,
+                            int64_t n_head_kv, int64_t n_kv_max, const int32_t* n_kv_dev, int64_t D,
+                            int64_t k_row_bytes, int64_t k_head_bytes, int64_t v_row_bytes, int64_t v_head_bytes,
+                            float scale, void* workspace, int64_t workspace_bytes, int rule, int32_t* n_split,
+                            int32_t* split_len, void* stream);
 
 /* amv_flash_attn_decode_kv without a workspace or counters argument and without any allocation. No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving

@@ -366,3 +366,74 @@ def test_engine_error_rules(dev, eng):
         assert eng.ac_bitnet_engine_eval_token(h, 0, x.ctypes.data, None, None, 0) == -106  # layer not uploaded
     finally:
         eng.ac_bitnet_engine_destroy(h)
+
+
+@pytest.mark.parametrize("do_norm,acc", [(1, 1), (0, 1), (1, 0)])
+def test_fa_merge_fold_equals_the_merge_launch(dev, do_norm, acc):
+    """The BitNet engine's short-context output projection: the attention splits alone (amv_flash_attn_split_kv) and
+    their merge in the projection's prologue (amv_bitnet_gemv_fa_merge) = split + merge (amv_flash_attn_decode_kv)
+    + amv_bitnet_gemv_fused on the merged row, bit for bit, over an f32 cache with the key count in device memory.
+    Counts run downward, so the splits past each count hold an earlier call's partials (masked, never read)."""
+    rng = np.random.default_rng(31 + do_norm + 2 * acc)
+    H, KVH, hd, nk = 20, 5, 128, 256
+    E, kv = H * hd, KVH * hd
+    scale = 1.0 / float(np.sqrt(np.float32(hd)))
+    q = g(rng.standard_normal((H, hd)).astype(np.float32), dev)
+    kc = g(rng.standard_normal((nk, kv)).astype(np.float32), dev)
+    vc = g(rng.standard_normal((nk, kv)).astype(np.float32), dev)
+    nw = g((1 + 0.1 * rng.standard_normal(E)).astype(np.float32), dev) if do_norm else None
+    w = g(i2s_pack(rng.integers(0, 3, (E, E)).astype(np.uint8)), dev)
+    base = g(rng.standard_normal(E).astype(np.float32), dev)
+    wsb = L().amv_flash_attn_workspace_bytes(H, KVH, nk, hd)
+    ws = torch.empty(wsb // 4, dtype=torch.float32, device=dev)
+    att = torch.empty(E, dtype=torch.float32, device=dev)
+    nkv = torch.zeros(1, dtype=torch.int32, device=dev)
+    ns, sl = ctypes.c_int32(0), ctypes.c_int32(0)
+    st = stream()
+    for n in (256, 200, 129, 128, 65, 64, 37, 2, 1):
+        nkv.fill_(n)
+        want = base.clone()
+        assert L().amv_flash_attn_decode_kv(0, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), None, att.data_ptr(), H, KVH,
+                                            nk, nkv.data_ptr(), hd, kv * 4, hd * 4, kv * 4, hd * 4, scale,
+                                            ws.data_ptr(), wsb, None, None, 8, 0, st) == 0
+        assert fused(att, None, nw, E, 0, do_norm, [w], (E,), (0.05,), [want], acc) == 0
+        got = base.clone()
+        assert L().amv_flash_attn_split_kv(0, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), None, H, KVH, nk,
+                                           nkv.data_ptr(), hd, kv * 4, hd * 4, kv * 4, hd * 4, scale, ws.data_ptr(),
+                                           wsb, 0, ctypes.byref(ns), ctypes.byref(sl), st) == 0
+        assert (ns.value, sl.value) == (4, 64)
+        assert L().amv_bitnet_gemv_fa_merge(ws.data_ptr(), ns.value, sl.value, nk, nkv.data_ptr(),
+                                            None if nw is None else nw.data_ptr(), E, 1e-5, do_norm, w.data_ptr(), E,
+                                            0.05, got.data_ptr(), acc, st) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), n
+    # more keys than 4 splits hold is refused
+    assert L().amv_bitnet_gemv_fa_merge(ws.data_ptr(), 8, 64, 300, nkv.data_ptr(), None, E, 1e-5, 0, w.data_ptr(), E,
+                                        0.05, base.data_ptr(), 1, st) != 0
+
+
+def test_engine_fold_merge_equals_merge_launch(dev, eng, monkeypatch):
+    """The engine at short contexts (the merge folded into the output projection) against the same engine with the
+    merge launch kept (AMV_BITNET_FOLD_MERGE=0): every token's x and logits bit-identical, at positions on both
+    sides of the fold's 256-key limit."""
+    rng = np.random.default_rng(12)
+    cfg = dict(n_embd=256, n_ffn=512, n_heads=2, n_kv_heads=1, head_dim=128, n_ctx=300, norm_eps=1e-5,
+               rope_theta=10000.0, relu2=True)
+    layers, out_norm, head = random_model(rng, cfg, 2, 1000)
+    h = make_engine(eng, cfg, layers, out_norm, head)
+    monkeypatch.setenv("AMV_BITNET_FOLD_MERGE", "0")
+    h2 = make_engine(eng, cfg, layers, out_norm, head)
+    try:
+        E = cfg["n_embd"]
+        for pos in range(258):  # consecutive positions: each token reads the cache rows the earlier ones wrote
+            x = (rng.standard_normal(E) * 0.5).astype(np.float32)
+            out = []
+            for hh in (h, h2):
+                xo = np.empty(E, np.float32)
+                lo = np.empty(1000, np.float32)
+                assert eng.ac_bitnet_engine_eval_token(hh, pos, x.ctypes.data, xo.ctypes.data, lo.ctypes.data, 0) == 0
+                out.append((xo, lo))
+            assert np.array_equal(out[0][0], out[1][0]) and np.array_equal(out[0][1], out[1][1]), pos
+    finally:
+        eng.ac_bitnet_engine_destroy(h)
+        eng.ac_bitnet_engine_destroy(h2)
