@@ -49,6 +49,13 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
     // the launch's splits up to n_split - 1, and a split past ns (whose partial this launch did not write) is
     // selected away, never multiplied. Unconditional loads of valid addresses: a conditional load would be turned
     // into a select of addresses with a stack zero, i.e. slow flat loads.
+    // (m, l) first: loads complete in order, so the weights and L are computed while the acc rows still arrive
+    float2 ml0[(G + 3) / 4];  // (m, l) of split lane of head wv + 4 j
+#pragma unroll
+    for (int j = 0; j < (G + 3) / 4; ++j) {
+        const int g = min(wv + 4 * j, G - 1);
+        ml0[j] = *reinterpret_cast<const float2*>(ph0 + ((size_t)g * n_split + min(lane, n_split - 1)) * FA_PS);
+    }
     float4 va[GB][8];  // acc rows of splits zg + 8 i of heads 0 .. GB - 1
 #pragma unroll
     for (int g = 0; g < GB; ++g)
@@ -57,12 +64,6 @@ __device__ __forceinline__ void fa_merge(const float* part, int n_split, int ns,
             const int z = min(zg + 8 * i, n_split - 1);
             va[g][i] = *reinterpret_cast<const float4*>(ph0 + ((size_t)g * n_split + z) * FA_PS + 4 + 4 * c4);
         }
-    float2 ml0[(G + 3) / 4];  // (m, l) of split lane of head wv + 4 j
-#pragma unroll
-    for (int j = 0; j < (G + 3) / 4; ++j) {
-        const int g = min(wv + 4 * j, G - 1);
-        ml0[j] = *reinterpret_cast<const float2*>(ph0 + ((size_t)g * n_split + min(lane, n_split - 1)) * FA_PS);
-    }
     // with n_kv_dev, ns comes from the key count in device memory, read only now that the loads above are issued
     asm volatile("" ::: "memory");
     if (n_kv_dev) ns = (max(0, min(*n_kv_dev, n_kv_max)) + split_len - 1) / split_len;
